@@ -1,0 +1,853 @@
+/*
+ * engine.c -- host side of the MI355X DPUF engine (C11).
+ *
+ * Implements the dpuf_engine_* ABI of include/dpuf_kernels.h over the thin
+ * HIP layer of hip_layer.h.  The structure follows the reference engine
+ * (dpuf_engine.c in dulePan/dpuf): create copies the config and layer
+ * descriptors (dpuf_engine.c:1208-1354), forward runs embed -> L x [norm,
+ * QKV, rope+KV, attention, O, norm, gate/up, SwiGLU, down] -> norm -> LM head
+ * (dpuf_engine.c:1625-2147).  What changes is where the work happens: every
+ * weight payload is validated and uploaded to HBM once at create, and each
+ * step of the loop is one HIP kernel launch on the engine's stream.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "../../include/dpuf_amd.h"
+#include "../../include/dpuf_kernels.h"
+#include "hip_layer.h"
+
+#define N_SLOTS 8
+#define N_PREFIX 8
+#define N_KINDS 8
+#define MAX_EVENTS 8192
+
+enum { K_GU = 0, K_DOWN, K_QKV, K_O, K_LM, K_ATTN, K_PREP, K_CALL };
+enum { W_Q = 0, W_K, W_V, W_O, W_GATE, W_UP, W_DOWN };
+
+typedef struct {
+    const uint8_t* host_base;
+    void* d_tiles;
+    void* d_offs;
+    void* d_sign;
+    uint64_t bytes;
+} Upload;
+
+typedef struct {
+    DpufModelConfig cfg;
+    int32_t L, H, I, nq, nkv, hd, qd, kvd, V, max_seq;
+    DpufDevW* lw;        /* [L][7] */
+    float** d_norm;      /* [L][4]: attn, q, k, ffn */
+    DpufDevW tok, lm;
+    float* d_out_norm;
+    float* d_cos;
+    float* d_sin;
+    float* kc[N_SLOTS];
+    float* vc[N_SLOTS];
+    int32_t active;
+    float* pk[N_PREFIX];
+    float* pv[N_PREFIX];
+    int32_t plen[N_PREFIX], pcap[N_PREFIX], pvalid[N_PREFIX];
+    /* scratch for up to DPUF_AMD_MAX_BATCH rows */
+    float *h, *hn, *q, *k, *v, *ao, *gate, *up, *logits, *scores, *embeds, *capture;
+    int32_t capture_cap;
+    DpufPrep prep[3];
+    int32_t *d_ids, *d_pos0, *d_flag, *d_tok;
+    int32_t* h_pinned;   /* host staging: [0] pos0, [1] flag, [2] token, [8..] ids */
+    uint8_t* q_idx;      /* per layer: prep index of q,k,v (3 bytes) and gate/up (2 bytes) */
+    float deadzone;
+    void* stream;
+    Upload* ups;
+    int32_t n_ups;
+    uint64_t weight_bytes;
+    int64_t early_exits;
+    /* timing */
+    int32_t timing;
+    void* ev[MAX_EVENTS];
+    int32_t ev_kind[MAX_EVENTS / 2];
+    double ev_bytes[MAX_EVENTS / 2];
+    int32_t n_ev;
+    double t_ms[N_KINDS];
+    int64_t t_cnt[N_KINDS];
+    double t_bytes[N_KINDS];
+    /* decode graph */
+    void* graph;
+    int32_t graph_key[5];
+} Engine;
+
+/* ------------------------------------------------------------------------- */
+
+static int env_int(const char* name, int* out) {
+    const char* s = getenv(name);
+    if (!s) return 0;
+    *out = atoi(s);
+    return 1;
+}
+
+static void tm_begin(Engine* e, int kind, double bytes) {
+    if (!e->timing || e->n_ev + 2 > MAX_EVENTS) return;
+    if (!e->ev[e->n_ev]) e->ev[e->n_ev] = dpuf_hip_event_create();
+    if (!e->ev[e->n_ev + 1]) e->ev[e->n_ev + 1] = dpuf_hip_event_create();
+    e->ev_kind[e->n_ev / 2] = kind;
+    e->ev_bytes[e->n_ev / 2] = bytes;
+    dpuf_hip_event_record(e->ev[e->n_ev], e->stream);
+}
+
+static void tm_end(Engine* e) {
+    if (!e->timing || e->n_ev + 2 > MAX_EVENTS) return;
+    dpuf_hip_event_record(e->ev[e->n_ev + 1], e->stream);
+    e->n_ev += 2;
+}
+
+static void tm_collect(Engine* e) {
+    if (!e->timing) return;
+    for (int32_t i = 0; i < e->n_ev; i += 2) {
+        int k = e->ev_kind[i / 2];
+        e->t_ms[k] += dpuf_hip_event_elapsed_ms(e->ev[i], e->ev[i + 1]);
+        e->t_cnt[k] += 1;
+        e->t_bytes[k] += e->ev_bytes[i / 2];
+    }
+    e->n_ev = 0;
+}
+
+/* Checks that every tile of a mode 12 descriptor lies inside its payload and
+ * that row counts are consistent, so that no kernel can read out of bounds. */
+static int validate_desc(const DpufWeightDesc* d) {
+    if (!d || d->mode != DPUF_MODE_QR_HAD4_PACKED) return 0;
+    if (d->rows <= 0 || d->cols <= 0 || (d->cols % 64) != 0 || d->n_tiles != (d->rows + 15) / 16) return 0;
+    if (!d->tensor_base || !d->tile_offsets) return 0;
+    const uint64_t total = d->tile_offsets[d->n_tiles];
+    const uint64_t grp = (uint64_t)(d->cols / 32) * 144u;
+    for (int32_t t = 0; t < d->n_tiles; t++) {
+        uint64_t o = d->tile_offsets[t];
+        if (o % 16 != 0 || o + 16 > total) return 0;
+        DpufQrTileHdr th;
+        memcpy(&th, d->tensor_base + o, sizeof th);
+        int32_t want = (t * 16 + 16 <= d->rows) ? 16 : d->rows - t * 16;
+        if (th.n_rows != want) return 0;
+        if (o + 16 + (uint64_t)((th.n_rows + 7) / 8) * grp > total) return 0;
+    }
+    return 1;
+}
+
+static int upload_desc(Engine* e, const DpufWeightDesc* d, DpufDevW* out) {
+    if (!validate_desc(d)) return 0;
+    for (int32_t i = 0; i < e->n_ups; i++) {
+        if (e->ups[i].host_base == d->tensor_base) {
+            out->tiles = (const uint8_t*)e->ups[i].d_tiles;
+            out->offs = (const uint64_t*)e->ups[i].d_offs;
+            out->sign = (const uint8_t*)e->ups[i].d_sign;
+            out->rows = d->rows;
+            out->cols = d->cols;
+            out->n_tiles = d->n_tiles;
+            return 1;
+        }
+    }
+    Upload u;
+    memset(&u, 0, sizeof u);
+    u.host_base = d->tensor_base;
+    u.bytes = d->tile_offsets[d->n_tiles];
+    u.d_tiles = dpuf_hip_malloc((size_t)u.bytes);
+    u.d_offs = dpuf_hip_malloc(((size_t)d->n_tiles + 1) * 8u);
+    if (d->sign_bits) u.d_sign = dpuf_hip_malloc((size_t)d->cols / 8u);
+    if (!u.d_tiles || !u.d_offs || (d->sign_bits && !u.d_sign)) {
+        dpuf_hip_free(u.d_tiles); dpuf_hip_free(u.d_offs); dpuf_hip_free(u.d_sign);
+        return 0;
+    }
+    dpuf_hip_h2d(u.d_tiles, d->tensor_base, (size_t)u.bytes, e->stream);
+    dpuf_hip_h2d(u.d_offs, d->tile_offsets, ((size_t)d->n_tiles + 1) * 8u, e->stream);
+    if (d->sign_bits) dpuf_hip_h2d(u.d_sign, d->sign_bits, (size_t)d->cols / 8u, e->stream);
+    /* synchronous upload: the caller's pageable buffers may be released later */
+    if (dpuf_hip_sync(e->stream) != 0) return 0;
+    e->ups = (Upload*)realloc(e->ups, (size_t)(e->n_ups + 1) * sizeof(Upload));
+    e->ups[e->n_ups++] = u;
+    out->tiles = (const uint8_t*)u.d_tiles;
+    out->offs = (const uint64_t*)u.d_offs;
+    out->sign = (const uint8_t*)u.d_sign;
+    out->rows = d->rows;
+    out->cols = d->cols;
+    out->n_tiles = d->n_tiles;
+    return 1;
+}
+
+static float* upload_floats(Engine* e, const float* src, size_t n) {
+    if (!src) return NULL;
+    float* d = (float*)dpuf_hip_malloc(n * sizeof(float));
+    if (!d) return NULL;
+    dpuf_hip_h2d(d, src, n * sizeof(float), e->stream);
+    return d;
+}
+
+static int same_signs(const DpufWeightDesc* a, const DpufWeightDesc* b) {
+    if (a->cols != b->cols) return 0;
+    if (!a->sign_bits || !b->sign_bits) return a->sign_bits == b->sign_bits;
+    return memcmp(a->sign_bits, b->sign_bits, (size_t)a->cols / 8u) == 0;
+}
+
+/* RoPE tables on the host with the C library, exactly as the reference's
+ * precompute_rope (dpuf_engine.c:183-223), then uploaded. */
+static int rope_tables(Engine* e) {
+    const int32_t half = e->hd >> 1;
+    const DpufModelConfig* c = &e->cfg;
+    float* inv_freq = (float*)malloc((size_t)half * sizeof(float));
+    float* ct = (float*)malloc((size_t)e->max_seq * half * sizeof(float));
+    float* st = (float*)malloc((size_t)e->max_seq * half * sizeof(float));
+    if (!inv_freq || !ct || !st) { free(inv_freq); free(ct); free(st); return 0; }
+    for (int32_t j = 0; j < half; j++) {
+        float freq = 1.0f / powf(c->rope_theta, (float)(2 * j) / (float)e->hd);
+        if (c->use_llama3_rope) {
+            float factor = c->rope_factor, low_f = c->rope_low_freq, high_f = c->rope_high_freq;
+            float orig_max = (float)c->rope_orig_max_pos;
+            float wavelen = (2.0f * 3.14159265358979323846f) / freq;
+            float low_wavelen = orig_max / low_f, high_wavelen = orig_max / high_f;
+            if (wavelen > low_wavelen) {
+                freq /= factor;
+            } else if (wavelen >= high_wavelen) {
+                float smooth = (orig_max / wavelen - low_f) / (high_f - low_f);
+                freq = (1.0f - smooth) * (freq / factor) + smooth * freq;
+            }
+        }
+        inv_freq[j] = freq;
+    }
+    for (int32_t p = 0; p < e->max_seq; p++)
+        for (int32_t j = 0; j < half; j++) {
+            float ang = (float)p * inv_freq[j];
+            ct[(size_t)p * half + j] = cosf(ang);
+            st[(size_t)p * half + j] = sinf(ang);
+        }
+    e->d_cos = upload_floats(e, ct, (size_t)e->max_seq * half);
+    e->d_sin = upload_floats(e, st, (size_t)e->max_seq * half);
+    int ok = e->d_cos && e->d_sin && dpuf_hip_sync(e->stream) == 0;
+    free(inv_freq); free(ct); free(st);
+    return ok;
+}
+
+static size_t kv_floats(const Engine* e) {
+    return (size_t)e->L * (size_t)e->nkv * (size_t)e->max_seq * (size_t)e->hd;
+}
+
+static int slot_alloc(Engine* e, int32_t s) {
+    if (e->kc[s]) return 1;
+    size_t n = kv_floats(e);
+    e->kc[s] = (float*)dpuf_hip_malloc(n * sizeof(float));
+    e->vc[s] = (float*)dpuf_hip_malloc(n * sizeof(float));
+    if (!e->kc[s] || !e->vc[s]) {
+        dpuf_hip_free(e->kc[s]); dpuf_hip_free(e->vc[s]);
+        e->kc[s] = e->vc[s] = NULL;
+        return 0;
+    }
+    dpuf_hip_fill_zero(e->kc[s], n * sizeof(float), e->stream);
+    dpuf_hip_fill_zero(e->vc[s], n * sizeof(float), e->stream);
+    return dpuf_hip_sync(e->stream) == 0;
+}
+
+static void engine_free(Engine* e) {
+    if (!e) return;
+    if (e->stream) dpuf_hip_sync(e->stream);
+    dpuf_hip_graph_destroy(e->graph);
+    for (int32_t i = 0; i < e->n_ups; i++) {
+        dpuf_hip_free(e->ups[i].d_tiles); dpuf_hip_free(e->ups[i].d_offs); dpuf_hip_free(e->ups[i].d_sign);
+    }
+    free(e->ups);
+    if (e->d_norm) {
+        for (int32_t i = 0; i < 4 * e->L; i++) dpuf_hip_free(e->d_norm[i]);
+        free(e->d_norm);
+    }
+    free(e->lw);
+    free(e->q_idx);
+    dpuf_hip_free(e->d_out_norm); dpuf_hip_free(e->d_cos); dpuf_hip_free(e->d_sin);
+    for (int s = 0; s < N_SLOTS; s++) { dpuf_hip_free(e->kc[s]); dpuf_hip_free(e->vc[s]); }
+    for (int p = 0; p < N_PREFIX; p++) { dpuf_hip_free(e->pk[p]); dpuf_hip_free(e->pv[p]); }
+    float* bufs[] = {e->h, e->hn, e->q, e->k, e->v, e->ao, e->gate, e->up, e->logits, e->scores, e->embeds, e->capture};
+    for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++) dpuf_hip_free(bufs[i]);
+    for (int i = 0; i < 3; i++) { dpuf_hip_free(e->prep[i].q); dpuf_hip_free(e->prep[i].s); dpuf_hip_free(e->prep[i].m); }
+    dpuf_hip_free(e->d_ids);
+    dpuf_hip_host_free(e->h_pinned);
+    for (int i = 0; i < MAX_EVENTS; i++) if (e->ev[i]) dpuf_hip_event_destroy(e->ev[i]);
+    if (e->stream) dpuf_hip_stream_destroy(e->stream);
+    free(e);
+}
+
+DPUF_EXPORT int32_t dpuf_amd_device_ok(void) { return dpuf_hip_device_count() > 0; }
+DPUF_EXPORT const char* dpuf_amd_last_error(void) { return dpuf_hip_error_string(); }
+
+DPUF_EXPORT void* dpuf_engine_create(const DpufModelConfig* cfg, const DpufLayerWeights* layers,
+                                     const DpufWeightDesc* w_tok_embd, const DpufWeightDesc* w_lm_head,
+                                     const float* output_norm) {
+    if (!cfg || !layers || !w_tok_embd || !w_lm_head || !output_norm) return NULL;
+    if (cfg->num_layers < 0 || cfg->hidden_size <= 0 || cfg->head_dim <= 0 || (cfg->head_dim % 64) != 0 ||
+        cfg->head_dim > 256 || cfg->num_kv_heads <= 0 || cfg->num_q_heads <= 0 ||
+        (cfg->num_q_heads % cfg->num_kv_heads) != 0 || cfg->max_seq_len <= 0 || cfg->vocab_size <= 0 ||
+        cfg->kv_type != DPUF_KV_F32 || cfg->has_mrope || (cfg->hidden_size % 64) != 0 ||
+        (cfg->intermediate_size % 64) != 0)
+        return NULL;
+    if (dpuf_hip_device_count() <= 0) return NULL;
+    Engine* e = (Engine*)calloc(1, sizeof(Engine));
+    if (!e) return NULL;
+    e->cfg = *cfg;
+    e->L = cfg->num_layers;
+    e->H = cfg->hidden_size;
+    e->I = cfg->intermediate_size;
+    e->nq = cfg->num_q_heads;
+    e->nkv = cfg->num_kv_heads;
+    e->hd = cfg->head_dim;
+    e->qd = e->nq * e->hd;
+    e->kvd = e->nkv * e->hd;
+    e->V = cfg->vocab_size;
+    e->max_seq = cfg->max_seq_len;
+    const char* dz = getenv("DPUF_SWIGLU_DEADZONE");
+    e->deadzone = dz ? (float)atof(dz) : 0.005f;
+    e->stream = dpuf_hip_stream_create();
+    if (!e->stream) goto fail;
+
+    /* weights: descriptors must match the config's shapes */
+    e->lw = (DpufDevW*)calloc((size_t)(e->L > 0 ? e->L : 1) * 7u, sizeof(DpufDevW));
+    e->d_norm = (float**)calloc((size_t)(e->L > 0 ? e->L : 1) * 4u, sizeof(float*));
+    e->q_idx = (uint8_t*)calloc((size_t)(e->L > 0 ? e->L : 1) * 5u, 1);
+    if (!e->lw || !e->d_norm || !e->q_idx) goto fail;
+    if (w_tok_embd->rows != e->V || w_tok_embd->cols != e->H || w_lm_head->rows != e->V || w_lm_head->cols != e->H)
+        goto fail;
+    if (!upload_desc(e, w_tok_embd, &e->tok) || !upload_desc(e, w_lm_head, &e->lm)) goto fail;
+    for (int32_t l = 0; l < e->L; l++) {
+        const DpufLayerWeights* lw = &layers[l];
+        const DpufWeightDesc* ds[7] = {&lw->w_q, &lw->w_k, &lw->w_v, &lw->w_o, &lw->w_gate, &lw->w_up, &lw->w_down};
+        const int32_t want_r[7] = {e->qd, e->kvd, e->kvd, e->H, e->I, e->I, e->H};
+        const int32_t want_c[7] = {e->H, e->H, e->H, e->qd, e->H, e->H, e->I};
+        for (int k = 0; k < 7; k++) {
+            if (ds[k]->rows != want_r[k] || ds[k]->cols != want_c[k]) goto fail;
+            if (!upload_desc(e, ds[k], &e->lw[(size_t)l * 7 + k])) goto fail;
+        }
+        if (!lw->attn_norm || !lw->ffn_norm) goto fail;
+        e->d_norm[4 * l + 0] = upload_floats(e, lw->attn_norm, (size_t)e->H);
+        if (cfg->has_qk_norm && lw->attn_q_norm) e->d_norm[4 * l + 1] = upload_floats(e, lw->attn_q_norm, (size_t)e->hd);
+        if (cfg->has_qk_norm && lw->attn_k_norm) e->d_norm[4 * l + 2] = upload_floats(e, lw->attn_k_norm, (size_t)e->hd);
+        e->d_norm[4 * l + 3] = upload_floats(e, lw->ffn_norm, (size_t)e->H);
+        if (!e->d_norm[4 * l + 0] || !e->d_norm[4 * l + 3]) goto fail;
+        /* shared activation prep when sign vectors agree (dpuf_engine.c:887-897) */
+        /* qi[0..2]: prep index of Q, K, V; qi[3]: distinct preps; qi[4]: up's */
+        uint8_t* qi = e->q_idx + 5 * (size_t)l;
+        const DpufWeightDesc* qkv[3] = {&lw->w_q, &lw->w_k, &lw->w_v};
+        int rep[3], n = 0;
+        for (int k = 0; k < 3; k++) {
+            int found = -1;
+            for (int j = 0; j < n && found < 0; j++)
+                if (same_signs(qkv[rep[j]], qkv[k])) found = j;
+            if (found < 0) { rep[n] = k; found = n++; }
+            qi[k] = (uint8_t)found;
+        }
+        qi[3] = (uint8_t)n;
+        qi[4] = same_signs(&lw->w_gate, &lw->w_up) ? 0 : 1;
+    }
+    e->d_out_norm = upload_floats(e, output_norm, (size_t)e->H);
+    if (!e->d_out_norm || !rope_tables(e)) goto fail;
+    for (int32_t i = 0; i < e->n_ups; i++) e->weight_bytes += e->ups[i].bytes;
+
+    /* scratch */
+    {
+        const size_t B = DPUF_AMD_MAX_BATCH;
+        int32_t maxd = e->H > e->I ? e->H : e->I;
+        if (e->qd > maxd) maxd = e->qd;
+        e->h = (float*)dpuf_hip_malloc(B * e->H * 4);
+        e->hn = (float*)dpuf_hip_malloc(B * e->H * 4);
+        e->q = (float*)dpuf_hip_malloc(B * e->qd * 4);
+        e->k = (float*)dpuf_hip_malloc(B * e->kvd * 4);
+        e->v = (float*)dpuf_hip_malloc(B * e->kvd * 4);
+        e->ao = (float*)dpuf_hip_malloc(B * e->qd * 4);
+        e->gate = (float*)dpuf_hip_malloc(B * e->I * 4);
+        e->up = (float*)dpuf_hip_malloc(B * e->I * 4);
+        e->logits = (float*)dpuf_hip_malloc(B * (size_t)e->V * 4);
+        e->scores = (float*)dpuf_hip_malloc(B * (size_t)e->nq * e->max_seq * 4);
+        e->embeds = (float*)dpuf_hip_malloc(B * e->H * 4);
+        for (int i = 0; i < 3; i++) {
+            e->prep[i].q = (int8_t*)dpuf_hip_malloc(B * maxd);
+            e->prep[i].s = (float*)dpuf_hip_malloc(B * (maxd / 32) * 4);
+            e->prep[i].m = (int32_t*)dpuf_hip_malloc(B * (maxd / 32) * 4);
+            if (!e->prep[i].q || !e->prep[i].s || !e->prep[i].m) goto fail;
+        }
+        e->d_ids = (int32_t*)dpuf_hip_malloc((B + 64) * 4);
+        e->h_pinned = (int32_t*)dpuf_hip_host_alloc((B + 64) * 4);
+        if (!e->h || !e->hn || !e->q || !e->k || !e->v || !e->ao || !e->gate || !e->up || !e->logits ||
+            !e->scores || !e->embeds || !e->d_ids || !e->h_pinned)
+            goto fail;
+        e->d_pos0 = e->d_ids + B;
+        e->d_flag = e->d_ids + B + 1;
+        e->d_tok = e->d_ids + B + 2;
+        dpuf_hip_fill_zero(e->d_ids, (B + 64) * 4, e->stream);
+        dpuf_hip_fill_zero(e->hn, B * e->H * 4, e->stream);
+    }
+    if (!slot_alloc(e, 0)) goto fail;
+    if (dpuf_hip_sync(e->stream) != 0) goto fail;
+    return e;
+fail:
+    engine_free(e);
+    return NULL;
+}
+
+DPUF_EXPORT void dpuf_engine_destroy(void* handle) { engine_free((Engine*)handle); }
+
+DPUF_EXPORT int32_t dpuf_engine_set_slot(void* handle, int32_t slot_id) {
+    Engine* e = (Engine*)handle;
+    if (!e || slot_id < 0 || slot_id >= N_SLOTS) return -1;
+    if (!slot_alloc(e, slot_id)) return -2;
+    e->active = slot_id;
+    return 0;
+}
+
+DPUF_EXPORT int32_t dpuf_engine_get_slot(void* handle) {
+    Engine* e = (Engine*)handle;
+    return e ? e->active : 0;
+}
+
+DPUF_EXPORT int32_t dpuf_engine_num_slots(void* handle) { return handle ? N_SLOTS : 1; }
+
+DPUF_EXPORT void dpuf_engine_reset_slot(void* handle, int32_t slot_id) {
+    Engine* e = (Engine*)handle;
+    if (!e || slot_id < 0 || slot_id >= N_SLOTS || !e->kc[slot_id]) return;
+    size_t n = kv_floats(e) * sizeof(float);
+    dpuf_hip_fill_zero(e->kc[slot_id], n, e->stream);
+    dpuf_hip_fill_zero(e->vc[slot_id], n, e->stream);
+    dpuf_hip_sync(e->stream);
+}
+
+DPUF_EXPORT void dpuf_engine_reset_cache(void* handle) {
+    Engine* e = (Engine*)handle;
+    if (!e) return;
+    dpuf_engine_reset_slot(handle, e->active);
+}
+
+DPUF_EXPORT size_t dpuf_engine_slot_memory(void* handle) {
+    Engine* e = (Engine*)handle;
+    if (!e) return 0;
+    return 2 * kv_floats(e) * sizeof(float);
+}
+
+/* Prefix caches are [L][kv head][len][hd] (dpuf_engine.c:1471-1600). */
+DPUF_EXPORT int32_t dpuf_engine_freeze_prefix(void* handle, int32_t pfx_id, int32_t prefix_len) {
+    Engine* e = (Engine*)handle;
+    if (!e || pfx_id < 0 || pfx_id >= N_PREFIX || prefix_len <= 0 || prefix_len > e->max_seq) return 0;
+    if (e->pcap[pfx_id] < prefix_len || !e->pk[pfx_id]) {
+        dpuf_hip_free(e->pk[pfx_id]); dpuf_hip_free(e->pv[pfx_id]);
+        size_t n = (size_t)e->L * e->nkv * (size_t)prefix_len * e->hd * sizeof(float);
+        e->pk[pfx_id] = (float*)dpuf_hip_malloc(n);
+        e->pv[pfx_id] = (float*)dpuf_hip_malloc(n);
+        e->pvalid[pfx_id] = 0;
+        e->pcap[pfx_id] = 0;
+        if (!e->pk[pfx_id] || !e->pv[pfx_id]) {
+            dpuf_hip_free(e->pk[pfx_id]); dpuf_hip_free(e->pv[pfx_id]);
+            e->pk[pfx_id] = e->pv[pfx_id] = NULL;
+            return 0;
+        }
+        e->pcap[pfx_id] = prefix_len;
+    }
+    if (!e->kc[e->active]) return 0;
+    const size_t hd = (size_t)e->hd, chunk = (size_t)prefix_len * hd * sizeof(float);
+    for (int32_t l = 0; l < e->L; l++)
+        for (int32_t h = 0; h < e->nkv; h++) {
+            size_t po = ((size_t)l * e->nkv + h) * (size_t)prefix_len * hd;
+            size_t so = ((size_t)l * e->nkv + h) * (size_t)e->max_seq * hd;
+            dpuf_hip_d2d(e->pk[pfx_id] + po, e->kc[e->active] + so, chunk, e->stream);
+            dpuf_hip_d2d(e->pv[pfx_id] + po, e->vc[e->active] + so, chunk, e->stream);
+        }
+    if (dpuf_hip_sync(e->stream) != 0) return 0;
+    e->plen[pfx_id] = prefix_len;
+    e->pvalid[pfx_id] = 1;
+    return 1;
+}
+
+DPUF_EXPORT int32_t dpuf_engine_apply_prefix(void* handle, int32_t slot_id, int32_t pfx_id) {
+    Engine* e = (Engine*)handle;
+    if (!e || slot_id < 0 || slot_id >= N_SLOTS || pfx_id < 0 || pfx_id >= N_PREFIX) return 0;
+    if (!e->pvalid[pfx_id] || e->plen[pfx_id] <= 0) return 0;
+    if (!slot_alloc(e, slot_id)) return 0;
+    const int32_t len = e->plen[pfx_id];
+    const size_t hd = (size_t)e->hd, chunk = (size_t)len * hd * sizeof(float);
+    for (int32_t l = 0; l < e->L; l++)
+        for (int32_t h = 0; h < e->nkv; h++) {
+            size_t po = ((size_t)l * e->nkv + h) * (size_t)len * hd;
+            size_t so = ((size_t)l * e->nkv + h) * (size_t)e->max_seq * hd;
+            dpuf_hip_d2d(e->kc[slot_id] + so, e->pk[pfx_id] + po, chunk, e->stream);
+            dpuf_hip_d2d(e->vc[slot_id] + so, e->pv[pfx_id] + po, chunk, e->stream);
+        }
+    if (dpuf_hip_sync(e->stream) != 0) return 0;
+    return len;
+}
+
+DPUF_EXPORT int32_t dpuf_engine_get_prefix_len(void* handle, int32_t pfx_id) {
+    Engine* e = (Engine*)handle;
+    if (!e || pfx_id < 0 || pfx_id >= N_PREFIX) return 0;
+    return e->pvalid[pfx_id] ? e->plen[pfx_id] : 0;
+}
+
+/* ------------------------------------------------------------------------- */
+/* Forward                                                                    */
+/* ------------------------------------------------------------------------- */
+
+static double gemv_bytes(const DpufDevW* w, int32_t t0, int32_t t1, int32_t M) {
+    const double rows = (double)((t1 * 16 < w->rows ? t1 * 16 : w->rows) - t0 * 16);
+    const double n_blk = (double)(w->cols / 32);
+    return rows / 8.0 * n_blk * 144.0 + (double)M * (w->cols + n_blk * 8.0 + rows * 4.0);
+}
+
+static DpufGemvJob job(const DpufDevW* w, int32_t t0, int32_t t1, DpufPrep p, float* out, int32_t ldo) {
+    DpufGemvJob j;
+    j.w = *w;
+    j.t0 = t0;
+    j.t1 = t1;
+    j.p = p;
+    j.out = out;
+    j.ldo = ldo;
+    return j;
+}
+
+/* Enqueues one forward step (ids/embeds/pos0 already on the device). */
+static void enqueue_forward(Engine* e, int32_t M, int32_t use_embeds, int32_t only_last, int32_t keep_tiles,
+                            int32_t early_tiles, float early_margin, int32_t want_argmax) {
+    void* s = e->stream;
+    const int32_t H = e->H, I = e->I;
+    const float eps = e->cfg.rms_eps;
+    const float scale = 1.0f / sqrtf((float)e->hd);
+
+    dpuf_hip_embed(s, e->tok, e->d_ids, M, use_embeds ? e->embeds : NULL, e->h);
+    for (int32_t l = 0; l < e->L; l++) {
+        const DpufDevW* W = e->lw + (size_t)l * 7;
+        const uint8_t* qi = e->q_idx + (size_t)l * 5;
+        float* kc = e->kc[e->active] + (size_t)l * e->nkv * e->max_seq * e->hd;
+        float* vc = e->vc[e->active] + (size_t)l * e->nkv * e->max_seq * e->hd;
+
+        /* (1) [h += down] + attn RMSNorm + prep of the Q/K/V input */
+        {
+            const uint8_t* signs[3] = {W[W_Q].sign, W[W_K].sign, W[W_V].sign};
+            const int32_t np = qi[3];
+            const uint8_t* ps[3] = {NULL, NULL, NULL};
+            for (int k = 2; k >= 0; k--) ps[qi[k]] = signs[k];
+            tm_begin(e, K_PREP, 0);
+            dpuf_hip_resnorm_prep(s, M, H, e->h, l > 0 ? e->hn : NULL, e->d_norm[4 * l], eps, np, ps, e->prep, NULL);
+            tm_end(e);
+        }
+        /* (2) Q, K, V in one launch */
+        {
+            DpufGemvJob js[3] = {
+                job(&W[W_Q], 0, W[W_Q].n_tiles, e->prep[qi[0]], e->q, e->qd),
+                job(&W[W_K], 0, W[W_K].n_tiles, e->prep[qi[1]], e->k, e->kvd),
+                job(&W[W_V], 0, W[W_V].n_tiles, e->prep[qi[2]], e->v, e->kvd),
+            };
+            double b = gemv_bytes(&W[W_Q], 0, W[W_Q].n_tiles, M) + gemv_bytes(&W[W_K], 0, W[W_K].n_tiles, M) +
+                       gemv_bytes(&W[W_V], 0, W[W_V].n_tiles, M);
+            tm_begin(e, K_QKV, b);
+            dpuf_hip_gemv(s, M, 3, js, NULL, 0.0f);
+            tm_end(e);
+        }
+        /* (3) QK-norm + RoPE + KV store, (4) attention */
+        tm_begin(e, K_ATTN, 0);
+        dpuf_hip_qk_rope_kv(s, M, e->q, e->k, e->v, e->d_norm[4 * l + 1], e->d_norm[4 * l + 2], eps, e->d_cos,
+                            e->d_sin, kc, vc, e->d_pos0, e->nq, e->nkv, e->hd, e->max_seq);
+        dpuf_hip_attn(s, M, e->q, kc, vc, e->ao, e->scores, e->d_pos0, e->nq, e->nkv, e->hd, e->max_seq, scale);
+        tm_end(e);
+        /* (5) O projection into hn */
+        tm_begin(e, K_PREP, 0);
+        dpuf_hip_prep(s, M, e->qd, e->ao, W[W_O].sign, e->prep[0]);
+        tm_end(e);
+        {
+            DpufGemvJob j = job(&W[W_O], 0, W[W_O].n_tiles, e->prep[0], e->hn, H);
+            tm_begin(e, K_O, gemv_bytes(&W[W_O], 0, W[W_O].n_tiles, M));
+            dpuf_hip_gemv(s, M, 1, &j, NULL, 0.0f);
+            tm_end(e);
+        }
+        /* (6) h += O; FFN RMSNorm; prep of gate/up input */
+        {
+            int32_t np = qi[4] ? 2 : 1;
+            const uint8_t* ps[2] = {W[W_GATE].sign, W[W_UP].sign};
+            tm_begin(e, K_PREP, 0);
+            dpuf_hip_resnorm_prep(s, M, H, e->h, e->hn, e->d_norm[4 * l + 3], eps, np, ps, e->prep, NULL);
+            tm_end(e);
+        }
+        /* (7) gate + up in one launch */
+        {
+            DpufGemvJob js[2] = {
+                job(&W[W_GATE], 0, W[W_GATE].n_tiles, e->prep[0], e->gate, I),
+                job(&W[W_UP], 0, W[W_UP].n_tiles, e->prep[qi[4]], e->up, I),
+            };
+            double b = gemv_bytes(&W[W_GATE], 0, W[W_GATE].n_tiles, M) + gemv_bytes(&W[W_UP], 0, W[W_UP].n_tiles, M);
+            tm_begin(e, K_GU, b);
+            dpuf_hip_gemv(s, M, 2, js, NULL, 0.0f);
+            tm_end(e);
+        }
+        /* (8) SwiGLU + dead zone + prep of the down input */
+        tm_begin(e, K_PREP, 0);
+        dpuf_hip_swiglu_prep(s, M, I, e->gate, e->up, e->deadzone, W[W_DOWN].sign, e->prep[0]);
+        tm_end(e);
+        /* (9) down projection, pruned to keep_tiles with the rest zeroed
+         * (dpuf_engine.c:2018-2044) */
+        {
+            int32_t nt = W[W_DOWN].n_tiles;
+            int32_t kt = (keep_tiles > 0 && keep_tiles < nt) ? keep_tiles : nt;
+            DpufGemvJob j = job(&W[W_DOWN], 0, kt, e->prep[0], e->hn, H);
+            tm_begin(e, K_DOWN, gemv_bytes(&W[W_DOWN], 0, kt, M));
+            dpuf_hip_gemv(s, M, 1, &j, NULL, 0.0f);
+            tm_end(e);
+            if (kt < nt) dpuf_hip_zero_rows(s, M, e->hn, H, kt * 16, W[W_DOWN].rows);
+        }
+        if (e->capture && M <= e->capture_cap)
+            dpuf_hip_capture(s, M, H, e->h, e->hn, e->capture + (size_t)l * e->capture_cap * H);
+    }
+
+    if (only_last == 2) return;
+    const int32_t lm0 = only_last ? M - 1 : 0, lmM = M - lm0;
+    {
+        const uint8_t* ps[1] = {e->lm.sign};
+        tm_begin(e, K_PREP, 0);
+        dpuf_hip_resnorm_prep(s, lmM, H, e->h + (size_t)lm0 * H, e->L > 0 ? e->hn + (size_t)lm0 * H : NULL,
+                              e->d_out_norm, eps, 1, ps, e->prep, NULL);
+        tm_end(e);
+    }
+    const int32_t nt = e->lm.n_tiles;
+    if (early_tiles > 0 && lmM == 1 && nt > 2048) {
+        /* Zone-A early exit (dpuf_engine.c:2091-2136): zone tiles, top-2
+         * margin test on the device, then either the -1e9 fill or the
+         * remaining tiles, decided by a device flag (no host round trip). */
+        int32_t za = early_tiles < 256 ? 256 : early_tiles;
+        if (za > nt) za = nt;
+        int32_t nz = za * 16 < e->V ? za * 16 : e->V;
+        DpufGemvJob j0 = job(&e->lm, 0, za, e->prep[0], e->logits, e->V);
+        tm_begin(e, K_LM, gemv_bytes(&e->lm, 0, za, 1));
+        dpuf_hip_gemv(s, 1, 1, &j0, NULL, 0.0f);
+        dpuf_hip_topcheck(s, e->logits, nz, early_margin, e->d_flag);
+        if (za < nt) {
+            DpufGemvJob j1 = job(&e->lm, za, nt, e->prep[0], e->logits, e->V);
+            dpuf_hip_gemv(s, 1, 1, &j1, e->d_flag, -1e9f);
+        }
+        tm_end(e);
+    } else {
+        DpufGemvJob j = job(&e->lm, 0, nt, e->prep[0], e->logits, e->V);
+        tm_begin(e, K_LM, gemv_bytes(&e->lm, 0, nt, lmM));
+        dpuf_hip_gemv(s, lmM, 1, &j, NULL, 0.0f);
+        tm_end(e);
+        dpuf_hip_fill_zero(e->d_flag, 4, s);
+    }
+    if (want_argmax) dpuf_hip_argmax(s, e->logits + (size_t)(lmM - 1) * e->V, e->V, e->d_tok);
+}
+
+static int32_t forward_common(Engine* e, int32_t n_tokens, const int32_t* token_ids, int32_t pos0,
+                              const float* embeds_in, const int32_t* pos_t, const int32_t* pos_h,
+                              const int32_t* pos_w, const float* const* deepstack_in, int32_t only_last,
+                              float* logits_out, int32_t* token_out, int32_t use_graph) {
+    if (!e || (!token_ids && !embeds_in) || (!logits_out && !token_out && only_last != 2)) return -1;
+    if (n_tokens <= 0 || n_tokens > DPUF_AMD_MAX_BATCH) return -2;
+    if (pos0 < 0 || pos0 + n_tokens > e->max_seq) return -3;
+    if (deepstack_in) return -5;
+    if (pos_t || pos_h || pos_w) {
+        for (int32_t m = 0; m < n_tokens; m++) {
+            int32_t p = pos0 + m;
+            if ((pos_t && pos_t[m] != p) || (pos_h && pos_h[m] != p) || (pos_w && pos_w[m] != p)) return -5;
+        }
+    }
+    for (int32_t m = 0; m < n_tokens; m++) {
+        int32_t id = token_ids ? token_ids[m] : -1;
+        if (id >= e->V || (id < 0 && !embeds_in)) return -4;
+    }
+    const int32_t M = n_tokens;
+    int32_t keep = 0, early = 0;
+    env_int(M > 1 ? "DPUF_PREFILL_KEEP_TILES" : "DPUF_GEN_KEEP_TILES", &keep);
+    int32_t has_early = env_int("DPUF_EARLY_TILES", &early);
+    const char* em = getenv("DPUF_EARLY_MARGIN");
+    float margin = em ? (float)atof(em) : 1.25f;
+    if (!has_early) early = 0;
+    else if (early <= 0) early = 1; /* env set: the zone is at least 256 tiles */
+
+    int32_t* hp = e->h_pinned;
+    hp[0] = pos0;
+    for (int32_t m = 0; m < M; m++) hp[8 + m] = token_ids ? token_ids[m] : -1;
+    dpuf_hip_h2d(e->d_ids, hp + 8, (size_t)M * 4, e->stream);
+    dpuf_hip_h2d(e->d_pos0, hp, 4, e->stream);
+    if (embeds_in) dpuf_hip_h2d(e->embeds, embeds_in, (size_t)M * e->H * 4, e->stream);
+
+    tm_begin(e, K_CALL, (double)e->weight_bytes);
+    const int graphable = use_graph && M == 1 && !e->timing && !embeds_in && !e->capture;
+    if (graphable) {
+        int32_t key[5] = {only_last, keep, early, e->active, 0};
+        memcpy(&key[4], &margin, 4);
+        if (e->graph && memcmp(key, e->graph_key, sizeof key) != 0) {
+            dpuf_hip_graph_destroy(e->graph);
+            e->graph = NULL;
+        }
+        if (!e->graph) {
+            if (dpuf_hip_capture_begin(e->stream) == 0) {
+                enqueue_forward(e, 1, 0, only_last, keep, early, margin, 1);
+                e->graph = dpuf_hip_capture_end(e->stream);
+                memcpy(e->graph_key, key, sizeof key);
+            }
+        }
+        if (e->graph) dpuf_hip_graph_launch(e->graph, e->stream);
+        else enqueue_forward(e, M, embeds_in != NULL, only_last, keep, early, margin, token_out != NULL);
+    } else {
+        enqueue_forward(e, M, embeds_in != NULL, only_last, keep, early, margin, token_out != NULL);
+    }
+    tm_end(e);
+    if (only_last != 2) {
+        const int32_t rows = only_last ? 1 : M;
+        if (logits_out) dpuf_hip_d2h(logits_out, e->logits, (size_t)rows * e->V * 4, e->stream);
+        dpuf_hip_d2h(hp + 1, e->d_flag, 8, e->stream); /* flag and token */
+    }
+    if (dpuf_hip_sync(e->stream) != 0) return -6;
+    tm_collect(e);
+    if (only_last != 2) {
+        if (hp[1]) e->early_exits++;
+        if (token_out) *token_out = hp[2];
+    }
+    return dpuf_hip_ok() ? 0 : -6;
+}
+
+DPUF_EXPORT int32_t dpuf_engine_forward_batch_ex(void* handle, int32_t n_tokens, const int32_t* token_ids,
+                                                 int32_t pos0, const float* embeds_in, const int32_t* pos_t,
+                                                 const int32_t* pos_h, const int32_t* pos_w,
+                                                 const float* const* deepstack_in, int32_t only_last_logits,
+                                                 float* logits_out) {
+    Engine* e = (Engine*)handle;
+    if (!e || (!logits_out && only_last_logits != 2)) return -1;
+    return forward_common(e, n_tokens, token_ids, pos0, embeds_in, pos_t, pos_h, pos_w, deepstack_in,
+                          only_last_logits, logits_out, NULL, 0);
+}
+
+DPUF_EXPORT int32_t dpuf_engine_forward_batch(void* handle, int32_t n_tokens, const int32_t* token_ids, int32_t pos0,
+                                              int32_t only_last_logits, float* logits_out) {
+    return dpuf_engine_forward_batch_ex(handle, n_tokens, token_ids, pos0, NULL, NULL, NULL, NULL, NULL,
+                                        only_last_logits, logits_out);
+}
+
+DPUF_EXPORT int32_t dpuf_engine_forward_token(void* handle, int32_t token_id, int32_t pos, float* logits_out) {
+    int32_t t = token_id;
+    return dpuf_engine_forward_batch(handle, 1, &t, pos, 1, logits_out);
+}
+
+DPUF_EXPORT int32_t dpuf_amd_engine_forward_argmax(void* handle, int32_t n_tokens, const int32_t* token_ids,
+                                                   int32_t pos0, const float* embeds_in, int32_t use_graph,
+                                                   int32_t* token_out, float* logits_out) {
+    Engine* e = (Engine*)handle;
+    if (!e || !token_out) return -1;
+    return forward_common(e, n_tokens, token_ids, pos0, embeds_in, NULL, NULL, NULL, NULL, 1, logits_out, token_out,
+                          use_graph);
+}
+
+/* ------------------------------------------------------------------------- */
+/* Test and measurement hooks (include/dpuf_amd.h)                            */
+/* ------------------------------------------------------------------------- */
+
+DPUF_EXPORT int32_t dpuf_amd_engine_set_kv(void* handle, int32_t layer, int32_t kvh, int32_t pos0, int32_t n,
+                                           const float* k, const float* v) {
+    Engine* e = (Engine*)handle;
+    if (!e || layer < 0 || layer >= e->L || kvh < 0 || kvh >= e->nkv || pos0 < 0 || n < 0 || pos0 + n > e->max_seq ||
+        !k || !v)
+        return -1;
+    size_t off = (((size_t)layer * e->nkv + kvh) * (size_t)e->max_seq + pos0) * e->hd;
+    dpuf_hip_h2d(e->kc[e->active] + off, k, (size_t)n * e->hd * 4, e->stream);
+    dpuf_hip_h2d(e->vc[e->active] + off, v, (size_t)n * e->hd * 4, e->stream);
+    return dpuf_hip_sync(e->stream);
+}
+
+DPUF_EXPORT int32_t dpuf_amd_engine_get_kv(void* handle, int32_t layer, int32_t kvh, int32_t pos0, int32_t n,
+                                           float* k, float* v) {
+    Engine* e = (Engine*)handle;
+    if (!e || layer < 0 || layer >= e->L || kvh < 0 || kvh >= e->nkv || pos0 < 0 || n < 0 || pos0 + n > e->max_seq ||
+        !k || !v)
+        return -1;
+    size_t off = (((size_t)layer * e->nkv + kvh) * (size_t)e->max_seq + pos0) * e->hd;
+    dpuf_hip_d2h(k, e->kc[e->active] + off, (size_t)n * e->hd * 4, e->stream);
+    dpuf_hip_d2h(v, e->vc[e->active] + off, (size_t)n * e->hd * 4, e->stream);
+    return dpuf_hip_sync(e->stream);
+}
+
+DPUF_EXPORT int32_t dpuf_amd_engine_set_capture(void* handle, int32_t max_tokens) {
+    Engine* e = (Engine*)handle;
+    if (!e || max_tokens < 0 || max_tokens > DPUF_AMD_MAX_BATCH) return -1;
+    dpuf_hip_free(e->capture);
+    e->capture = NULL;
+    e->capture_cap = 0;
+    if (max_tokens == 0 || e->L == 0) return 0;
+    e->capture = (float*)dpuf_hip_malloc((size_t)e->L * max_tokens * e->H * 4);
+    if (!e->capture) return -1;
+    e->capture_cap = max_tokens;
+    dpuf_hip_fill_zero(e->capture, (size_t)e->L * max_tokens * e->H * 4, e->stream);
+    return dpuf_hip_sync(e->stream);
+}
+
+DPUF_EXPORT int32_t dpuf_amd_engine_get_capture(void* handle, float* out, size_t n_floats) {
+    Engine* e = (Engine*)handle;
+    if (!e || !e->capture || !out) return -1;
+    size_t total = (size_t)e->L * e->capture_cap * e->H;
+    if (n_floats > total) n_floats = total;
+    dpuf_hip_d2h(out, e->capture, n_floats * 4, e->stream);
+    return dpuf_hip_sync(e->stream);
+}
+
+DPUF_EXPORT void dpuf_amd_engine_set_timing(void* handle, int32_t enable) {
+    Engine* e = (Engine*)handle;
+    if (!e) return;
+    e->timing = enable ? 1 : 0;
+    e->n_ev = 0;
+    memset(e->t_ms, 0, sizeof e->t_ms);
+    memset(e->t_cnt, 0, sizeof e->t_cnt);
+    memset(e->t_bytes, 0, sizeof e->t_bytes);
+}
+
+DPUF_EXPORT int32_t dpuf_amd_engine_get_timing(void* handle, int32_t kind, double* total_ms, int64_t* count,
+                                               double* bytes) {
+    Engine* e = (Engine*)handle;
+    if (!e || kind < 0 || kind >= N_KINDS) return -1;
+    if (total_ms) *total_ms = e->t_ms[kind];
+    if (count) *count = e->t_cnt[kind];
+    if (bytes) *bytes = e->t_bytes[kind];
+    return 0;
+}
+
+DPUF_EXPORT uint64_t dpuf_amd_engine_weight_bytes(void* handle) {
+    Engine* e = (Engine*)handle;
+    return e ? e->weight_bytes : 0;
+}
+
+DPUF_EXPORT int64_t dpuf_amd_engine_early_exit_count(void* handle) {
+    Engine* e = (Engine*)handle;
+    return e ? e->early_exits : 0;
+}
+
+DPUF_EXPORT double dpuf_amd_gemv_bench(void* handle, int32_t which, int32_t M, int32_t iters, int32_t start_layer,
+                                       double* bytes) {
+    Engine* e = (Engine*)handle;
+    if (!e || which < 0 || which > 7 || M < 1 || M > DPUF_AMD_MAX_BATCH || iters < 1) return -1.0;
+    if (which < 7 && (e->L == 0 || start_layer < 0 || start_layer >= e->L)) return -1.0;
+    const DpufDevW* w0 = which == 7 ? &e->lm : &e->lw[(size_t)start_layer * 7 + which];
+    const int32_t K = w0->cols;
+    /* activations: the prep of a fixed, non-trivial vector per row */
+    float* x = (float*)malloc((size_t)M * K * 4);
+    if (!x) return -1.0;
+    uint32_t st = 12345u;
+    for (size_t i = 0; i < (size_t)M * K; i++) {
+        st = st * 1664525u + 1013904223u;
+        x[i] = ((float)(st >> 8) / 16777216.0f) * 2.0f - 1.0f;
+    }
+    dpuf_hip_h2d(e->gate, x, (size_t)M * K * 4, e->stream);
+    dpuf_hip_prep(e->stream, M, K, e->gate, w0->sign, e->prep[0]);
+    dpuf_hip_sync(e->stream);
+    free(x);
+    void* a = dpuf_hip_event_create();
+    void* b = dpuf_hip_event_create();
+    float* out = which == 7 ? e->logits : e->up;
+    const int32_t nl = which == 7 ? 1 : e->L - start_layer;
+    /* warm-up launch */
+    DpufGemvJob j = job(w0, 0, w0->n_tiles, e->prep[0], out, w0->rows);
+    dpuf_hip_gemv(e->stream, M, 1, &j, NULL, 0.0f);
+    dpuf_hip_event_record(a, e->stream);
+    for (int32_t i = 0; i < iters; i++) {
+        const DpufDevW* w = which == 7 ? &e->lm : &e->lw[(size_t)(start_layer + (i % nl)) * 7 + which];
+        j = job(w, 0, w->n_tiles, e->prep[0], out, w->rows);
+        dpuf_hip_gemv(e->stream, M, 1, &j, NULL, 0.0f);
+    }
+    dpuf_hip_event_record(b, e->stream);
+    float ms = dpuf_hip_event_elapsed_ms(a, b);
+    dpuf_hip_event_destroy(a);
+    dpuf_hip_event_destroy(b);
+    if (bytes) *bytes = gemv_bytes(w0, 0, w0->n_tiles, M);
+    if (!dpuf_hip_ok()) return -1.0;
+    return (double)ms / iters;
+}

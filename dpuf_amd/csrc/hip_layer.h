@@ -1,0 +1,103 @@
+/*
+ * hip_layer.h -- the thin C ABI between the C host engine (engine.c) and the
+ * gfx950 HIP code (kernels.hip).  Plain pointers and sizes only; every
+ * function that launches work takes the engine's stream as an opaque handle.
+ */
+#ifndef DPUF_HIP_LAYER_H
+#define DPUF_HIP_LAYER_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* One mode 12 matrix resident in HBM: the tile region exactly as stored in
+ * the .dpuf blob (tile t at tiles + offs[t]) and its tile offset table. */
+typedef struct {
+    const uint8_t*  tiles;
+    const uint64_t* offs;
+    const uint8_t*  sign;
+    int32_t rows, cols, n_tiles;
+} DpufDevW;
+
+/* Prepped activations of M rows: q int8 [M][K], s f32 [M][K/32], m i32 [M][K/32]. */
+typedef struct {
+    int8_t*  q;
+    float*   s;
+    int32_t* m;
+} DpufPrep;
+
+/* One matrix of a fused GEMV launch: tiles [t0, t1) of w, reading prep p,
+ * writing out[m * ldo + row]. */
+typedef struct {
+    DpufDevW w;
+    int32_t t0, t1;
+    DpufPrep p;
+    float* out;
+    int32_t ldo;
+} DpufGemvJob;
+
+int32_t dpuf_hip_device_count(void);
+const char* dpuf_hip_error_string(void);
+int32_t dpuf_hip_ok(void);          /* 1 if no HIP error has been recorded */
+void dpuf_hip_clear_error(void);
+
+void* dpuf_hip_malloc(size_t bytes);
+void  dpuf_hip_free(void* p);
+void* dpuf_hip_host_alloc(size_t bytes);   /* pinned */
+void  dpuf_hip_host_free(void* p);
+void* dpuf_hip_stream_create(void);
+void  dpuf_hip_stream_destroy(void* s);
+int32_t dpuf_hip_sync(void* s);
+void dpuf_hip_h2d(void* dst, const void* src, size_t n, void* s);
+void dpuf_hip_d2h(void* dst, const void* src, size_t n, void* s);
+void dpuf_hip_d2d(void* dst, const void* src, size_t n, void* s);
+void dpuf_hip_fill_zero(void* dst, size_t n, void* s);   /* kernel fill, graph-safe */
+void dpuf_hip_fill_f32(float* dst, size_t n, float v, void* s);
+
+void* dpuf_hip_event_create(void);
+void  dpuf_hip_event_destroy(void* e);
+void  dpuf_hip_event_record(void* e, void* s);
+float dpuf_hip_event_elapsed_ms(void* a, void* b);   /* synchronises on b */
+
+/* Graph capture of a stream into a replayable executable graph. */
+int32_t dpuf_hip_capture_begin(void* s);
+void* dpuf_hip_capture_end(void* s);                 /* returns exec graph or NULL */
+int32_t dpuf_hip_graph_launch(void* g, void* s);
+void dpuf_hip_graph_destroy(void* g);
+
+/* Kernels.  pos0 is read from device memory so a captured step replays at
+ * any position. */
+void dpuf_hip_embed(void* s, DpufDevW w, const int32_t* ids, int32_t M, const float* embeds,
+                    float* out);
+void dpuf_hip_resnorm_prep(void* s, int32_t M, int32_t H, float* h, const float* res,
+                           const float* w, float eps, int32_t n_prep, const uint8_t* const* signs,
+                           const DpufPrep* preps, float* xn_out);
+void dpuf_hip_prep(void* s, int32_t M, int32_t K, const float* x, const uint8_t* sign, DpufPrep p);
+void dpuf_hip_swiglu_prep(void* s, int32_t M, int32_t I, const float* gate, const float* up,
+                          float dz, const uint8_t* sign, DpufPrep p);
+void dpuf_hip_gemv(void* s, int32_t M, int32_t n_jobs, const DpufGemvJob* jobs,
+                   const int32_t* skip_flag, float fill);
+void dpuf_hip_qk_rope_kv(void* s, int32_t M, float* q, float* k, const float* v,
+                         const float* q_norm, const float* k_norm, float eps,
+                         const float* cos_tab, const float* sin_tab, float* kc, float* vc,
+                         const int32_t* pos0, int32_t n_q, int32_t n_kv, int32_t hd, int32_t max_seq);
+void dpuf_hip_attn(void* s, int32_t M, const float* q, const float* kc, const float* vc, float* out,
+                   float* scores, const int32_t* pos0, int32_t n_q, int32_t n_kv, int32_t hd,
+                   int32_t max_seq, float scale);
+void dpuf_hip_zero_rows(void* s, int32_t M, float* out, int32_t ld, int32_t r0, int32_t r1);
+void dpuf_hip_capture(void* s, int32_t M, int32_t H, const float* h, const float* hn, float* cap);
+void dpuf_hip_topcheck(void* s, const float* logits, int32_t n, float thr, int32_t* flag);
+void dpuf_hip_argmax(void* s, const float* logits, int32_t V, int32_t* out);
+void dpuf_hip_fwht_sign(void* s, int32_t M, int32_t K, const float* x, const uint8_t* sign, float* out);
+void dpuf_hip_slab_pack(void* s, int32_t mc, int32_t K, DpufPrep rows, int32_t* sq, float* ss, int32_t* sm);
+void dpuf_hip_slab_unpack(void* s, int32_t M, int32_t K, const int32_t* sq, const float* ss, const int32_t* sm,
+                          DpufPrep rows);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

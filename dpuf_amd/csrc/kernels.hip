@@ -1,0 +1,1079 @@
+// kernels.hip -- gfx950 (CDNA4, wave64) kernels of the DPUF Mode 12 token loop
+// and the thin extern "C" layer that launches them (hip_layer.h).
+//
+// Numerics contract: every kernel reproduces the fp32 operation order of the
+// reference CPU path (dpuf_avx2.c / dpuf_engine.c in dulePan/dpuf) so that
+// results are bit-identical, not merely close:
+//   * integer parts (nibble x int8 dots) are exact in any order, so they are
+//     spread over lanes and reduced with DPP;
+//   * every floating-point reduction whose order the reference fixes (the
+//     per-row FMA chain over 32-blocks, RMSNorm's 8 FMA lanes + hsum tree,
+//     attention's hadd tree, softmax sums, the P.V chain) runs in that order;
+//   * build with -ffp-contract=off; fused multiply-adds are explicit fmaf.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "hip_layer.h"
+
+#define DEV __device__ __forceinline__
+
+// ---------------------------------------------------------------------------
+// Error bookkeeping
+// ---------------------------------------------------------------------------
+static hipError_t g_err = hipSuccess;
+static char g_err_msg[256];
+
+static void note(hipError_t e, const char* what) {
+    if (e != hipSuccess && g_err == hipSuccess) {
+        g_err = e;
+        snprintf(g_err_msg, sizeof g_err_msg, "%s: %s", what, hipGetErrorString(e));
+    }
+}
+#define CK(x) note((x), #x)
+#define LAUNCHED(name) note(hipGetLastError(), name)
+
+// ---------------------------------------------------------------------------
+// Scalar helpers
+// ---------------------------------------------------------------------------
+DEV float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+
+// 8-lane sum in the order of the reference's eng_hsum256_ps
+// (dpuf_engine.c:37-46): ((a0+a4)+(a1+a5)) + ((a2+a6)+(a3+a7)).
+DEV float hsum8(const float* a) {
+    float s0 = a[0] + a[4], s1 = a[1] + a[5], s2 = a[2] + a[6], s3 = a[3] + a[7];
+    return (s0 + s1) + (s2 + s3);
+}
+
+// 8-lane sum as hsum4_256_ps's hadd tree leaves it (dpuf_engine.c:318-323):
+// ((a0+a1)+(a2+a3)) + ((a4+a5)+(a6+a7)).
+DEV float hsum8_hadd(const float* a) {
+    float lo = (a[0] + a[1]) + (a[2] + a[3]);
+    float hi = (a[4] + a[5]) + (a[6] + a[7]);
+    return lo + hi;
+}
+
+// The reference's own 8-wide exp polynomial (dpuf_engine.c:297-316), per lane.
+DEV float exp_poly(float x) {
+    x = fmaxf(-45.0f, fminf(x, 45.0f));
+    float fx = rintf(x * 1.44269504088896341f);
+    float r = fmaf(-fx, 0.693359375f, x);
+    r = fmaf(-fx, -2.12194440e-4f, r);
+    float p = 1.9875691500e-4f;
+    p = fmaf(p, r, 1.3981999507e-3f);
+    p = fmaf(p, r, 8.3334519073e-3f);
+    p = fmaf(p, r, 4.1665795894e-2f);
+    p = fmaf(p, r, 1.6666665459e-1f);
+    p = fmaf(p, r, 5.0000001201e-1f);
+    float r2 = r * r;
+    float er = fmaf(p, r2, r) + 1.0f;
+    int n = (int)fx;
+    return er * __int_as_float((n + 127) << 23);
+}
+
+// exp for x <= 0 with the results of the host C library's expf, which the
+// reference calls on the scalar tail of its softmax (dpuf_engine.c:423-426).
+// Method: exp(x) = 2^(k/32) * 2^(r/32), k = round(x*32/ln2), with a 32-entry
+// table of 2^(i/32) and a cubic polynomial evaluated in double precision,
+// rounded once to float (the exp2f-table method of Szabolcs Nagy used by
+// glibc's expf).  The table holds bits(2^(i/32)) - (i << 47), i.e. the
+// correctly rounded doubles 2^(i/32) with the exponent contribution removed.
+// Checked bit-for-bit against glibc expf over every float in [-104, 0].
+__constant__ uint64_t c_exp2_tab[32] = {
+    0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
+    0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
+    0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
+    0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
+    0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
+    0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
+    0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
+    0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull,
+};
+
+DEV float expf_libc(float x) {
+    if (x < -0x1.9fe368p6f) return 0.0f;  // below log(2^-150): rounds to +0
+    const double inv_ln2_n = 0x1.71547652b82fep+0 * 32.0;
+    const double shift = 0x1.8p+52;
+    const double c0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
+    const double c1 = 0x1.ebfce50fac4f3p-3 / 32.0 / 32.0;
+    const double c2 = 0x1.62e42ff0c52d6p-1 / 32.0;
+    double xd = (double)x;
+    double kd = fma(inv_ln2_n, xd, shift);
+    uint64_t ki = (uint64_t)__double_as_longlong(kd);
+    kd -= shift;
+    double r = fma(inv_ln2_n, xd, -kd);
+    uint64_t t = c_exp2_tab[ki & 31u] + (ki << 47);
+    double sc = __longlong_as_double((long long)t);
+    double z = fma(c0, r, c1);
+    double r2 = r * r;
+    double y = fma(c2, r, 1.0);
+    y = fma(z, r2, y);
+    y = y * sc;
+    return (float)y;
+}
+
+// In-register FWHT-64: radix-2 butterflies with strides 1..32, then x 1/8
+// (reference fwht64_block_f32, dpuf_avx2.c:724-772).
+DEV void fwht64(float* y) {
+#pragma unroll
+    for (int h = 1; h < 64; h <<= 1) {
+#pragma unroll
+        for (int i = 0; i < 64; i += 2 * h) {
+#pragma unroll
+            for (int j = i; j < i + h; j++) {
+                float a = y[j], b = y[j + h];
+                y[j] = a + b;
+                y[j + h] = a - b;
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 64; i++) y[i] = y[i] * 0.125f;
+}
+
+// Quantises 32 FWHT'd values like dpuf_prep_had4_packed_slab
+// (dpuf_avx2.c:2400-2446): returns the scale, writes 8 packed int8 words and
+// 8 * sum(q).
+DEV float quant32(const float* f, uint32_t* qw, int32_t* sum8) {
+    float amax = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 32; k++) {
+        float a = fabsf(f[k]);
+        amax = a > amax ? a : amax;
+    }
+    if (amax <= 1e-4f) {
+#pragma unroll
+        for (int g = 0; g < 8; g++) qw[g] = 0u;
+        *sum8 = 0;
+        return 0.0f;
+    }
+    float d = amax / 127.0f;
+    float inv = (amax > 1e-12f) ? (127.0f / amax) : 0.0f;
+    int32_t s = 0;
+#pragma unroll
+    for (int g = 0; g < 8; g++) {
+        uint32_t w = 0;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            float v = f[4 * g + k] * inv;
+            int32_t qi;
+            if (!(v > -2147483648.0f && v < 2147483648.0f)) qi = -127;  // cvtps -> INT_MIN -> -127
+            else qi = (int32_t)rintf(v);
+            qi = qi > 127 ? 127 : qi;
+            qi = qi < -127 ? -127 : qi;
+            s += qi;
+            w |= ((uint32_t)(qi & 0xFF)) << (8 * k);
+        }
+        qw[g] = w;
+    }
+    *sum8 = s * 8;
+    return d;
+}
+
+// sign (.) x then FWHT-64 then quantisation of the two 32-blocks of one
+// 64-column block `blk` (reference dpuf_prep_had4_packed_slab).
+DEV void prep_block64(const float* x, const uint8_t* sign, int blk, int8_t* q, float* s, int32_t* m) {
+    float v[64];
+    const float4* x4 = (const float4*)(x + 64 * blk);
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        float4 t = x4[i];
+        v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
+    }
+    if (sign) {
+#pragma unroll
+        for (int bb = 0; bb < 8; bb++) {
+            uint32_t sb = sign[8 * blk + bb];
+#pragma unroll
+            for (int k = 0; k < 8; k++)
+                if ((sb >> k) & 1u) v[8 * bb + k] = -v[8 * bb + k];
+        }
+    }
+    fwht64(v);
+#pragma unroll
+    for (int hb = 0; hb < 2; hb++) {
+        uint32_t qw[8];
+        int32_t sum8;
+        float d = quant32(v + 32 * hb, qw, &sum8);
+        uint4* qo = (uint4*)(q + 64 * blk + 32 * hb);
+        qo[0] = make_uint4(qw[0], qw[1], qw[2], qw[3]);
+        qo[1] = make_uint4(qw[4], qw[5], qw[6], qw[7]);
+        s[2 * blk + hb] = d;
+        m[2 * blk + hb] = sum8;
+    }
+}
+
+// DPP quad permutations: xor 1 = (1,0,3,2), xor 2 = (2,3,0,1).
+DEV int dpp_xor1(int v) { return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false); }
+DEV int dpp_xor2(int v) { return __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false); }
+
+// ---------------------------------------------------------------------------
+// Embedding (reference dpuf_embed_qr_hadamard4_packed_f32, dpuf_avx2.c:2738-2783)
+// grid: M rows; thread per 64-column block.
+// ---------------------------------------------------------------------------
+__global__ void k_embed(DpufDevW w, const int32_t* __restrict__ ids, const float* __restrict__ embeds,
+                        float* __restrict__ out) {
+    const int m = blockIdx.x;
+    const int H = w.cols, n_blk = H >> 5;
+    float* dst = out + (size_t)m * H;
+    const int id = ids ? ids[m] : -1;
+    if (embeds && id < 0) {
+        for (int i = threadIdx.x; i < H; i += blockDim.x) dst[i] = embeds[(size_t)m * H + i];
+        return;
+    }
+    const int t = id >> 4, lr = id & 15, rg = lr >> 3, ri = lr & 7;
+    const uint8_t* grp = w.tiles + w.offs[t] + 16 + (size_t)rg * n_blk * 144;
+    const uint16_t* sc = (const uint16_t*)grp;
+    const uint8_t* qg = grp + (size_t)n_blk * 16;
+    for (int blk = threadIdx.x; blk < (H >> 6); blk += blockDim.x) {
+        float v[64];
+#pragma unroll
+        for (int hb = 0; hb < 2; hb++) {
+            const int b = 2 * blk + hb;
+            const float ws = h2f(sc[b * 8 + ri]);
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const uint32_t word = *(const uint32_t*)(qg + (size_t)b * 128 + c * 32 + ri * 4);
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const uint32_t by = (word >> (8 * k)) & 0xFFu;
+                    v[32 * hb + 8 * c + k] = (float)((int)(by & 15u) - 8) * ws;
+                    v[32 * hb + 8 * c + 4 + k] = (float)((int)(by >> 4) - 8) * ws;
+                }
+            }
+        }
+        fwht64(v);
+        if (w.sign) {
+#pragma unroll
+            for (int bb = 0; bb < 8; bb++) {
+                const uint32_t sb = w.sign[8 * blk + bb];
+#pragma unroll
+                for (int k = 0; k < 8; k++)
+                    if ((sb >> k) & 1u) v[8 * bb + k] = -v[8 * bb + k];
+            }
+        }
+        float4* d4 = (float4*)(dst + 64 * blk);
+#pragma unroll
+        for (int i = 0; i < 16; i++) d4[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Residual add + RMSNorm + activation prep for up to three sign vectors
+// (reference add_and_rms_norm_f32 dpuf_engine.c:243-272 and
+// dpuf_prep_had4_packed_slab).  grid: M rows, 256 threads, LDS = H floats.
+// ---------------------------------------------------------------------------
+struct PrepSet {
+    const uint8_t* sign[3];
+    DpufPrep p[3];
+    int n;
+};
+
+__global__ __launch_bounds__(256) void k_resnorm_prep(int H, float* __restrict__ h, const float* __restrict__ res,
+                                                      const float* __restrict__ w, float eps, PrepSet ps,
+                                                      float* __restrict__ xn_out) {
+    extern __shared__ float sx[];
+    __shared__ float part[8];
+    __shared__ float inv_sh;
+    const int m = blockIdx.x;
+    float* hr = h + (size_t)m * H;
+    for (int i = threadIdx.x; i < H; i += blockDim.x) {
+        float v = hr[i];
+        if (res) {
+            v = v + res[(size_t)m * H + i];
+            hr[i] = v;
+        }
+        sx[i] = v;
+    }
+    __syncthreads();
+    if (threadIdx.x < 8) {
+        // lane j of the reference's 8-wide FMA accumulator: elements j, j+8, ...
+        float a = 0.0f;
+        for (int i = threadIdx.x; i < H; i += 8) a = fmaf(sx[i], sx[i], a);
+        part[threadIdx.x] = a;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float ss = hsum8(part);
+        inv_sh = 1.0f / sqrtf(ss / (float)H + eps);
+    }
+    __syncthreads();
+    const float inv = inv_sh;
+    for (int i = threadIdx.x; i < H; i += blockDim.x) {
+        float v = (sx[i] * inv) * w[i];
+        sx[i] = v;
+        if (xn_out) xn_out[(size_t)m * H + i] = v;
+    }
+    __syncthreads();
+    const int nb = H >> 5;
+    for (int p = 0; p < ps.n; p++) {
+        for (int blk = threadIdx.x; blk < (H >> 6); blk += blockDim.x)
+            prep_block64(sx, ps.sign[p], blk, ps.p[p].q + (size_t)m * H, ps.p[p].s + (size_t)m * nb,
+                         ps.p[p].m + (size_t)m * nb);
+    }
+}
+
+// Plain activation prep of M rows of x [M][K].
+__global__ void k_prep(int K, const float* __restrict__ x, const uint8_t* __restrict__ sign, DpufPrep p) {
+    const int m = blockIdx.x, nb = K >> 5;
+    for (int blk = threadIdx.x; blk < (K >> 6); blk += blockDim.x)
+        prep_block64(x + (size_t)m * K, sign, blk, p.q + (size_t)m * K, p.s + (size_t)m * nb, p.m + (size_t)m * nb);
+}
+
+// SwiGLU with dead zone (reference swiglu_range_avx2, 8-wide path,
+// dpuf_engine.c:976-989) fused with the prep of the down projection's input.
+__global__ void k_swiglu_prep(int I, const float* __restrict__ gate, const float* __restrict__ up, float dz,
+                              const uint8_t* __restrict__ sign, DpufPrep p) {
+    const int m = blockIdx.x, nb = I >> 5;
+    for (int blk = threadIdx.x; blk < (I >> 6); blk += blockDim.x) {
+        float v[64];
+        const float4* g4 = (const float4*)(gate + (size_t)m * I + 64 * blk);
+        const float4* u4 = (const float4*)(up + (size_t)m * I + 64 * blk);
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const float4 g = g4[i], u = u4[i];
+            const float gg[4] = {g.x, g.y, g.z, g.w}, uu[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                float ng = fmaxf(-40.0f, fminf(0.0f - gg[k], 40.0f));
+                float silu = gg[k] / (1.0f + exp_poly(ng));
+                float r = silu * uu[k];
+                if (dz > 0.0f && !(fabsf(r) >= dz)) r = 0.0f;
+                v[4 * i + k] = r;
+            }
+        }
+        if (sign) {
+#pragma unroll
+            for (int bb = 0; bb < 8; bb++) {
+                const uint32_t sb = sign[8 * blk + bb];
+#pragma unroll
+                for (int k = 0; k < 8; k++)
+                    if ((sb >> k) & 1u) v[8 * bb + k] = -v[8 * bb + k];
+            }
+        }
+        fwht64(v);
+#pragma unroll
+        for (int hb = 0; hb < 2; hb++) {
+            uint32_t qw[8];
+            int32_t sum8;
+            float d = quant32(v + 32 * hb, qw, &sum8);
+            uint4* qo = (uint4*)(p.q + (size_t)m * I + 64 * blk + 32 * hb);
+            qo[0] = make_uint4(qw[0], qw[1], qw[2], qw[3]);
+            qo[1] = make_uint4(qw[4], qw[5], qw[6], qw[7]);
+            p.s[(size_t)m * nb + 2 * blk + hb] = d;
+            p.m[(size_t)m * nb + 2 * blk + hb] = sum8;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Mode 12 GEMV / GEMM.
+//
+// One wave (64 lanes) owns one 8-row group of a tile.  The group is stored as
+// [n_blk x 8 fp16 scales][n_blk x 128 B nibbles]; in 32-byte chunk c of block
+// b, byte ri*4+k holds row ri, column 32b+8c+k (low nibble) and 32b+8c+4+k
+// (high nibble) (reference layout, dpuf_avx2.c:2347-2353).
+//
+// Per step the wave streams 8 blocks = 1 KB of nibbles with one coalesced
+// 16-byte load per lane: lane = bi*8 + h*4 + c holds chunk c of block b0+bi,
+// rows 4h..4h+3.  Each lane forms 4 exact int32 row dots with sdot4, the
+// quad (c = 0..3) is reduced with two DPP adds, and lane (bi, h, c) keeps
+// row 4h+c.  The per-row fp32 chain acc = fma(float(D - sum8), ws * xs, acc)
+// must run over blocks in ascending order (dpuf_avx2.c:2633-2635), so the
+// (D, ws*xs) pairs go through LDS to the chain lanes.
+//
+// k_gemv1: M == 1, blocks with xs <= 0 are skipped (dpuf_avx2.c:2621-2622).
+// k_gemm8: up to 8 tokens per wave, every block accumulated (slab path,
+//          dpuf_avx2.c:2643-2676); the 64 lanes then run 8 rows x 8 tokens
+//          chains.
+// ---------------------------------------------------------------------------
+struct GemvBatch {
+    DpufGemvJob j[3];
+    int g_begin[4];
+    int n;
+};
+
+DEV int find_job(const GemvBatch& B, int g) {
+    int j = 0;
+    if (B.n > 1 && g >= B.g_begin[1]) j = 1;
+    if (B.n > 2 && g >= B.g_begin[2]) j = 2;
+    return j;
+}
+
+
+// Locates group g of a job: tile pointer, first row, rows in the group.
+// Returns false when the group does not exist (second group of a short tile).
+DEV bool group_of(const DpufGemvJob& J, int g, const uint8_t*& grp, int& r0, int& n8) {
+    const int t = J.t0 + (g >> 1), rg = g & 1;
+    const uint8_t* tp = J.w.tiles + J.w.offs[t];
+    const int n_r = *(const uint16_t*)(tp + 4);
+    if (rg * 8 >= n_r) return false;
+    const int n_blk = J.w.cols >> 5;
+    grp = tp + 16 + (size_t)rg * n_blk * 144;
+    r0 = t * 16 + rg * 8;
+    n8 = n_r - rg * 8 < 8 ? n_r - rg * 8 : 8;
+    return true;
+}
+
+// Integer part for one lane: 4 row dots (rows 4h..4h+3) of one chunk against
+// 8 int8 activations, quad-reduced; returns the dot of row 4h+c.
+DEV int lane_row_dot(uint4 wq, int2 xw, int c) {
+    int d0 = __builtin_amdgcn_sdot4((int)(wq.x & 0x0F0F0F0Fu), xw.x, 0, false);
+    int d1 = __builtin_amdgcn_sdot4((int)(wq.y & 0x0F0F0F0Fu), xw.x, 0, false);
+    int d2 = __builtin_amdgcn_sdot4((int)(wq.z & 0x0F0F0F0Fu), xw.x, 0, false);
+    int d3 = __builtin_amdgcn_sdot4((int)(wq.w & 0x0F0F0F0Fu), xw.x, 0, false);
+    d0 = __builtin_amdgcn_sdot4((int)((wq.x >> 4) & 0x0F0F0F0Fu), xw.y, d0, false);
+    d1 = __builtin_amdgcn_sdot4((int)((wq.y >> 4) & 0x0F0F0F0Fu), xw.y, d1, false);
+    d2 = __builtin_amdgcn_sdot4((int)((wq.z >> 4) & 0x0F0F0F0Fu), xw.y, d2, false);
+    d3 = __builtin_amdgcn_sdot4((int)((wq.w >> 4) & 0x0F0F0F0Fu), xw.y, d3, false);
+    d0 += dpp_xor1(d0); d1 += dpp_xor1(d1); d2 += dpp_xor1(d2); d3 += dpp_xor1(d3);
+    d0 += dpp_xor2(d0); d1 += dpp_xor2(d1); d2 += dpp_xor2(d2); d3 += dpp_xor2(d3);
+    return c == 0 ? d0 : (c == 1 ? d1 : (c == 2 ? d2 : d3));
+}
+
+__global__ __launch_bounds__(64) void k_gemv1(GemvBatch B, const int32_t* __restrict__ skip_flag, float fill) {
+    __shared__ float2 st[8][8];
+    const int ji = find_job(B, blockIdx.x);
+    const DpufGemvJob& J = B.j[ji];
+    const uint8_t* grp;
+    int r0, n8;
+    if (!group_of(J, blockIdx.x - B.g_begin[ji], grp, r0, n8)) return;
+    const int lane = threadIdx.x;
+    if (skip_flag && *skip_flag) {
+        if (lane < n8) J.out[r0 + lane] = fill;
+        return;
+    }
+    const int n_blk = J.w.cols >> 5;
+    const uint16_t* sc = (const uint16_t*)grp;
+    const uint8_t* qg = grp + (size_t)n_blk * 16;
+    const int bi = lane >> 3, h = (lane >> 2) & 1, c = lane & 3, rr = 4 * h + c;
+    float acc = 0.0f;
+    for (int b0 = 0; b0 < n_blk; b0 += 8) {
+        const int b = b0 + bi;
+        float dcf = 0.0f, sp = 0.0f;
+        if (b < n_blk) {
+            const uint4 wq = *(const uint4*)(qg + (size_t)b * 128 + c * 32 + h * 16);
+            const int2 xw = *(const int2*)(J.p.q + b * 32 + c * 8);
+            const int dot = lane_row_dot(wq, xw, c);
+            const float bs = J.p.s[b];
+            if (bs > 0.0f) {
+                dcf = (float)(dot - J.p.m[b]);
+                sp = h2f(sc[b * 8 + rr]) * bs;
+            }
+        }
+        st[rr][bi] = make_float2(dcf, sp);
+        __syncthreads();
+        if (lane < 8) {
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const float2 e = st[lane][k];
+                if (b0 + k < n_blk) acc = fmaf(e.x, e.y, acc);
+            }
+        }
+        __syncthreads();
+    }
+    if (lane < n8) J.out[r0 + lane] = acc;
+}
+
+__global__ __launch_bounds__(64) void k_gemm8(GemvBatch B, int M) {
+    __shared__ float2 st[8][8][8];  // [token][row][block]
+    const int ji = find_job(B, blockIdx.x);
+    const DpufGemvJob& J = B.j[ji];
+    const uint8_t* grp;
+    int r0, n8;
+    if (!group_of(J, blockIdx.x - B.g_begin[ji], grp, r0, n8)) return;
+    const int m0 = blockIdx.y * 8;
+    const int mt = M - m0 < 8 ? M - m0 : 8;
+    const int K = J.w.cols, n_blk = K >> 5;
+    const uint16_t* sc = (const uint16_t*)grp;
+    const uint8_t* qg = grp + (size_t)n_blk * 16;
+    const int lane = threadIdx.x;
+    const int bi = lane >> 3, h = (lane >> 2) & 1, c = lane & 3, rr = 4 * h + c;
+    const int cm = lane >> 3, cr = lane & 7;  // chain lane: token cm, row cr
+    float acc = 0.0f;
+    for (int b0 = 0; b0 < n_blk; b0 += 8) {
+        const int b = b0 + bi;
+        uint4 wq = make_uint4(0, 0, 0, 0);
+        float ws = 0.0f;
+        if (b < n_blk) {
+            wq = *(const uint4*)(qg + (size_t)b * 128 + c * 32 + h * 16);
+            ws = h2f(sc[b * 8 + rr]);
+        }
+        for (int mi = 0; mi < mt; mi++) {
+            const int m = m0 + mi;
+            float dcf = 0.0f, sp = 0.0f;
+            if (b < n_blk) {
+                const int2 xw = *(const int2*)(J.p.q + (size_t)m * K + b * 32 + c * 8);
+                const int dot = lane_row_dot(wq, xw, c);
+                dcf = (float)(dot - J.p.m[(size_t)m * n_blk + b]);
+                sp = ws * J.p.s[(size_t)m * n_blk + b];
+            }
+            st[mi][rr][bi] = make_float2(dcf, sp);
+        }
+        __syncthreads();
+        if (cm < mt) {
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const float2 e = st[cm][cr][k];
+                if (b0 + k < n_blk) acc = fmaf(e.x, e.y, acc);
+            }
+        }
+        __syncthreads();
+    }
+    if (cm < mt && cr < n8) J.out[(size_t)(m0 + cm) * J.ldo + r0 + cr] = acc;
+}
+
+// ---------------------------------------------------------------------------
+// QK-norm + NeoX RoPE + KV-cache store (reference dpuf_engine.c:1791-1817,
+// 1841-1879).  grid: (M, n_q + n_kv); block: hd threads.
+// ---------------------------------------------------------------------------
+__global__ void k_qk_rope_kv(float* __restrict__ q, float* __restrict__ k, const float* __restrict__ v,
+                             const float* __restrict__ qn, const float* __restrict__ kn, float eps,
+                             const float* __restrict__ cos_tab, const float* __restrict__ sin_tab,
+                             float* __restrict__ kc, float* __restrict__ vc, const int32_t* __restrict__ pos0p,
+                             int n_q, int n_kv, int hd, int max_seq) {
+    extern __shared__ float sv[];
+    __shared__ float part[8];
+    __shared__ float inv_sh;
+    const int m = blockIdx.x, head = blockIdx.y, tid = threadIdx.x;
+    const int pos = *pos0p + m;
+    const bool is_k = head >= n_q;
+    const int hh = is_k ? head - n_q : head;
+    float* vec = is_k ? (k + ((size_t)m * n_kv + hh) * hd) : (q + ((size_t)m * n_q + hh) * hd);
+    const float* nw = is_k ? kn : qn;
+    sv[tid] = vec[tid];
+    __syncthreads();
+    if (nw) {
+        if (tid < 8) {
+            float a = 0.0f;
+            for (int i = tid; i < hd; i += 8) a = fmaf(sv[i], sv[i], a);
+            part[tid] = a;
+        }
+        __syncthreads();
+        if (tid == 0) inv_sh = 1.0f / sqrtf(hsum8(part) / (float)hd + eps);
+        __syncthreads();
+        const float x = (sv[tid] * inv_sh) * nw[tid];
+        __syncthreads();
+        sv[tid] = x;
+        __syncthreads();
+    }
+    const int half = hd >> 1;
+    float o;
+    if (tid < half) {
+        const float c = cos_tab[(size_t)pos * half + tid], s = sin_tab[(size_t)pos * half + tid];
+        o = fmaf(sv[tid], c, -(sv[tid + half] * s));
+    } else {
+        const int j = tid - half;
+        const float c = cos_tab[(size_t)pos * half + j], s = sin_tab[(size_t)pos * half + j];
+        o = fmaf(sv[tid], c, sv[j] * s);
+    }
+    vec[tid] = o;
+    if (is_k) {
+        const size_t off = ((size_t)hh * max_seq + pos) * hd + tid;
+        kc[off] = o;
+        vc[off] = v[((size_t)m * n_kv + hh) * hd + tid];
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Causal GQA attention over the fp32 cache, one query head pair per block
+// (reference gqa_attn_head_pair_f32, dpuf_engine.c:341-577).
+// grid: (M, n_kv, ceil(groups/2)); block 256.
+// ---------------------------------------------------------------------------
+DEV float score_hadd(const float* q, const float* kp, int hd) {
+    float a[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int i = 0; i < hd; i += 8) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) a[j] = fmaf(q[i + j], kp[i + j], a[j]);
+    }
+    return hsum8_hadd(a);
+}
+DEV float score_hsum(const float* q, const float* kp, int hd) {
+    float a[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int i = 0; i < hd; i += 8) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) a[j] = fmaf(q[i + j], kp[i + j], a[j]);
+    }
+    return hsum8(a);
+}
+// dot_f32_avx2 (dpuf_engine.c:325-339) for the single-head tail.
+DEV float score_dot2(const float* q, const float* kp, int hd) {
+    float a0[8] = {0, 0, 0, 0, 0, 0, 0, 0}, a1[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    int i = 0;
+    for (; i + 15 < hd; i += 16) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            a0[j] = fmaf(q[i + j], kp[i + j], a0[j]);
+            a1[j] = fmaf(q[i + 8 + j], kp[i + 8 + j], a1[j]);
+        }
+    }
+    for (; i + 7 < hd; i += 8) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) a0[j] = fmaf(q[i + j], kp[i + j], a0[j]);
+    }
+    float cc[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) cc[j] = a0[j] + a1[j];
+    return hsum8(cc);
+}
+
+__global__ __launch_bounds__(256) void k_attn(const float* __restrict__ q, const float* __restrict__ kc,
+                                              const float* __restrict__ vc, float* __restrict__ out,
+                                              float* __restrict__ scores, const int32_t* __restrict__ pos0p,
+                                              int n_q, int n_kv, int hd, int max_seq, float scale) {
+    extern __shared__ float qs[];  // 2 * hd
+    __shared__ float red[2][256];
+    __shared__ float vs8[2][8];
+    __shared__ float inv_sh[2];
+    const int m = blockIdx.x, kvh = blockIdx.y, gp = blockIdx.z, tid = threadIdx.x;
+    const int groups = n_q / n_kv;
+    const int g0 = 2 * gp;
+    const bool pair = (g0 + 1 < groups);
+    const int nh = pair ? 2 : 1;
+    const int qh0 = kvh * groups + g0;
+    const int kv_len = *pos0p + m + 1;
+    const float* K = kc + (size_t)kvh * max_seq * hd;
+    const float* V = vc + (size_t)kvh * max_seq * hd;
+    for (int i = tid; i < nh * hd; i += blockDim.x) qs[i] = q[((size_t)m * n_q + qh0) * hd + i];
+    __syncthreads();
+    float* sc0 = scores + ((size_t)m * n_q + qh0) * max_seq;
+    float* sc1 = sc0 + max_seq;
+    const int n4 = kv_len & ~3;
+    float mx0 = -1e30f, mx1 = -1e30f;
+    for (int t = tid; t < kv_len; t += blockDim.x) {
+        const float* kp = K + (size_t)t * hd;
+        float s0, s1 = 0.0f;
+        if (t < n4) {
+            s0 = score_hadd(qs, kp, hd) * scale;
+            if (pair) s1 = score_hadd(qs + hd, kp, hd) * scale;
+        } else if (pair) {
+            s0 = score_hsum(qs, kp, hd) * scale;
+            s1 = score_hsum(qs + hd, kp, hd) * scale;
+        } else {
+            s0 = score_dot2(qs, kp, hd) * scale;
+        }
+        sc0[t] = s0;
+        mx0 = s0 > mx0 ? s0 : mx0;
+        if (pair) {
+            sc1[t] = s1;
+            mx1 = s1 > mx1 ? s1 : mx1;
+        }
+    }
+    red[0][tid] = mx0;
+    red[1][tid] = mx1;
+    __syncthreads();
+    for (int w = blockDim.x / 2; w > 0; w >>= 1) {
+        if (tid < w) {
+            red[0][tid] = fmaxf(red[0][tid], red[0][tid + w]);
+            red[1][tid] = fmaxf(red[1][tid], red[1][tid + w]);
+        }
+        __syncthreads();
+    }
+    const float M0 = red[0][0], M1 = red[1][0];
+    const int n8 = kv_len & ~7;
+    for (int t = tid; t < kv_len; t += blockDim.x) {
+        sc0[t] = t < n8 ? exp_poly(sc0[t] - M0) : expf_libc(sc0[t] - M0);
+        if (pair) sc1[t] = t < n8 ? exp_poly(sc1[t] - M1) : expf_libc(sc1[t] - M1);
+    }
+    __syncthreads();
+    if (tid < 16) {
+        const int hsel = tid >> 3, j = tid & 7;
+        if (hsel < nh) {
+            const float* sc = hsel ? sc1 : sc0;
+            float a = 0.0f;
+            for (int t = j; t < n8; t += 8) a = a + sc[t];
+            vs8[hsel][j] = a;
+        }
+    }
+    __syncthreads();
+    if (tid < nh) {
+        const float* sc = tid ? sc1 : sc0;
+        float sp = hsum8(vs8[tid]);
+        for (int t = n8; t < kv_len; t++) sp += sc[t];
+        inv_sh[tid] = 1.0f / (sp + 1e-12f);
+    }
+    __syncthreads();
+    for (int t = tid; t < kv_len; t += blockDim.x) {
+        sc0[t] = sc0[t] * inv_sh[0];
+        if (pair) sc1[t] = sc1[t] * inv_sh[1];
+    }
+    __syncthreads();
+    for (int o = tid; o < nh * hd; o += blockDim.x) {
+        const int hsel = o / hd, d = o % hd;
+        const float* p = hsel ? sc1 : sc0;
+        float a = 0.0f;
+        if (pair) {
+            for (int t = 0; t < kv_len; t++) a = fmaf(p[t], V[(size_t)t * hd + d], a);
+        } else if ((hd & 63) == 0) {
+            int t = 0;
+            for (; t + 1 < kv_len; t += 2)
+                a = fmaf(p[t], V[(size_t)t * hd + d], fmaf(p[t + 1], V[(size_t)(t + 1) * hd + d], a));
+            if (t < kv_len) a = fmaf(p[t], V[(size_t)t * hd + d], a);
+        } else {
+            for (int t = 0; t < kv_len; t++) a = fmaf(p[t], V[(size_t)t * hd + d], a);
+        }
+        out[((size_t)m * n_q + qh0 + hsel) * hd + d] = a;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Small utility kernels
+// ---------------------------------------------------------------------------
+__global__ void k_fill_f32(float* p, size_t n, float v) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) p[i] = v;
+}
+__global__ void k_fill_zero_u32(uint32_t* p, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) p[i] = 0u;
+}
+__global__ void k_fill_zero_u8(uint8_t* p, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) p[i] = 0u;
+}
+__global__ void k_zero_rows(float* out, int ld, int r0, int r1) {
+    const int m = blockIdx.x;
+    for (int r = r0 + threadIdx.x; r < r1; r += blockDim.x) out[(size_t)m * ld + r] = 0.0f;
+}
+__global__ void k_capture(int H, const float* h, const float* hn, float* cap) {
+    const int m = blockIdx.x;
+    for (int i = threadIdx.x; i < H; i += blockDim.x) cap[(size_t)m * H + i] = h[(size_t)m * H + i] + hn[(size_t)m * H + i];
+}
+
+// Top-2 over logits [0, n) with multiplicity (the reference's sequential
+// b1/b2 scan, dpuf_engine.c:2101-2110, is order independent), then the
+// early-exit decision b1 - b2 >= thr (thr > 0).  One block of 1024.
+__global__ __launch_bounds__(1024) void k_topcheck(const float* __restrict__ x, int n, float thr, int32_t* flag) {
+    __shared__ float s1[1024], s2[1024];
+    float b1 = -1e30f, b2 = -1e30f;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const float v = x[i];
+        if (v > b1) { b2 = b1; b1 = v; }
+        else if (v > b2) { b2 = v; }
+    }
+    s1[threadIdx.x] = b1;
+    s2[threadIdx.x] = b2;
+    __syncthreads();
+    for (int w = blockDim.x / 2; w > 0; w >>= 1) {
+        if (threadIdx.x < w) {
+            const float a1 = s1[threadIdx.x], a2 = s2[threadIdx.x];
+            const float c1 = s1[threadIdx.x + w], c2 = s2[threadIdx.x + w];
+            float n1, n2;
+            if (a1 >= c1) { n1 = a1; n2 = fmaxf(a2, c1); }
+            else { n1 = c1; n2 = fmaxf(c2, a1); }
+            s1[threadIdx.x] = n1;
+            s2[threadIdx.x] = n2;
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) *flag = (thr > 0.0f && (s1[0] - s2[0]) >= thr) ? 1 : 0;
+}
+
+// First index of the maximum under strict '>' (dpuf-cli.c:1997-2004).
+__global__ __launch_bounds__(1024) void k_argmax(const float* __restrict__ x, int n, int32_t* out) {
+    __shared__ float sv[1024];
+    __shared__ int si[1024];
+    float bv = x[0];
+    int bi = 0;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const float v = x[i];
+        if (v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
+    }
+    sv[threadIdx.x] = bv;
+    si[threadIdx.x] = bi;
+    __syncthreads();
+    for (int w = blockDim.x / 2; w > 0; w >>= 1) {
+        if (threadIdx.x < w) {
+            const float v = sv[threadIdx.x + w];
+            const int i = si[threadIdx.x + w];
+            if (v > sv[threadIdx.x] || (v == sv[threadIdx.x] && i < si[threadIdx.x])) {
+                sv[threadIdx.x] = v;
+                si[threadIdx.x] = i;
+            }
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) *out = si[0];
+}
+
+
+// ---------------------------------------------------------------------------
+// Standalone-entry helpers: FWHT-only transform and slab (re)packing of the
+// reference's multi-token activation layout ([n_blk][8 words][6 tokens] per
+// 6-token slab, dpuf_avx2.c:2390-2447).
+// ---------------------------------------------------------------------------
+__global__ void k_fwht_sign(int K, const float* __restrict__ x, const uint8_t* __restrict__ sign, float* __restrict__ out) {
+    const int m = blockIdx.x;
+    for (int blk = threadIdx.x; blk < (K >> 6); blk += blockDim.x) {
+        float v[64];
+        const float* src = x + (size_t)m * K + 64 * blk;
+#pragma unroll
+        for (int i = 0; i < 64; i++) v[i] = src[i];
+        if (sign) {
+#pragma unroll
+            for (int bb = 0; bb < 8; bb++) {
+                const uint32_t sb = sign[8 * blk + bb];
+#pragma unroll
+                for (int k = 0; k < 8; k++)
+                    if ((sb >> k) & 1u) v[8 * bb + k] = -v[8 * bb + k];
+            }
+        }
+        fwht64(v);
+        float* dst = out + (size_t)m * K + 64 * blk;
+#pragma unroll
+        for (int i = 0; i < 64; i++) dst[i] = v[i];
+    }
+}
+
+// rows [mc][K] -> one slab; only token lanes j < mc are written.
+__global__ void k_slab_pack(int mc, int K, DpufPrep rows, int32_t* __restrict__ sq, float* __restrict__ ss,
+                            int32_t* __restrict__ sm) {
+    const int nb = K >> 5;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < nb * 8 * mc; i += gridDim.x * blockDim.x) {
+        const int j = i % mc, g = (i / mc) % 8, b = i / (8 * mc);
+        sq[b * 48 + g * 6 + j] = *(const int32_t*)(rows.q + (size_t)j * K + b * 32 + g * 4);
+        if (g == 0) {
+            ss[b * 6 + j] = rows.s[(size_t)j * nb + b];
+            sm[b * 6 + j] = rows.m[(size_t)j * nb + b];
+        }
+    }
+}
+
+// slabs of M tokens -> rows [M][K].
+__global__ void k_slab_unpack(int M, int K, const int32_t* __restrict__ sq, const float* __restrict__ ss,
+                              const int32_t* __restrict__ sm, DpufPrep rows) {
+    const int nb = K >> 5;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < M * nb * 8; i += gridDim.x * blockDim.x) {
+        const int g = i % 8, b = (i / 8) % nb, m = i / (8 * nb);
+        const int slab = m / 6, j = m % 6;
+        const size_t base = (size_t)slab * nb;
+        *(int32_t*)(rows.q + (size_t)m * K + b * 32 + g * 4) = sq[(base + b) * 48 + g * 6 + j];
+        if (g == 0) {
+            rows.s[(size_t)m * nb + b] = ss[(base + b) * 6 + j];
+            rows.m[(size_t)m * nb + b] = sm[(base + b) * 6 + j];
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// extern "C" layer
+// ---------------------------------------------------------------------------
+#define ST(s) ((hipStream_t)(s))
+
+extern "C" {
+
+int32_t dpuf_hip_device_count(void) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+    return n;
+}
+const char* dpuf_hip_error_string(void) { return g_err == hipSuccess ? "" : g_err_msg; }
+int32_t dpuf_hip_ok(void) { return g_err == hipSuccess; }
+void dpuf_hip_clear_error(void) { g_err = hipSuccess; g_err_msg[0] = 0; }
+
+void* dpuf_hip_malloc(size_t bytes) {
+    void* p = nullptr;
+    hipError_t e = hipMalloc(&p, bytes ? bytes : 256);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    return p;
+}
+void dpuf_hip_free(void* p) { if (p) CK(hipFree(p)); }
+void* dpuf_hip_host_alloc(size_t bytes) {
+    void* p = nullptr;
+    if (hipHostMalloc(&p, bytes ? bytes : 64, hipHostMallocDefault) != hipSuccess) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    return p;
+}
+void dpuf_hip_host_free(void* p) { if (p) CK(hipHostFree(p)); }
+void* dpuf_hip_stream_create(void) {
+    hipStream_t s = nullptr;
+    CK(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+    return (void*)s;
+}
+void dpuf_hip_stream_destroy(void* s) { if (s) CK(hipStreamDestroy(ST(s))); }
+int32_t dpuf_hip_sync(void* s) {
+    CK(hipStreamSynchronize(ST(s)));
+    return g_err == hipSuccess ? 0 : -1;
+}
+void dpuf_hip_h2d(void* dst, const void* src, size_t n, void* s) {
+    if (n) CK(hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, ST(s)));
+}
+void dpuf_hip_d2h(void* dst, const void* src, size_t n, void* s) {
+    if (n) CK(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, ST(s)));
+}
+void dpuf_hip_d2d(void* dst, const void* src, size_t n, void* s) {
+    if (n) CK(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToDevice, ST(s)));
+}
+void dpuf_hip_fill_zero(void* dst, size_t n, void* s) {
+    if (!n) return;
+    if ((n & 3) == 0 && ((uintptr_t)dst & 3) == 0) {
+        size_t w = n / 4;
+        int blocks = (int)((w + 255) / 256 < 4096 ? (w + 255) / 256 : 4096);
+        hipLaunchKernelGGL(k_fill_zero_u32, dim3(blocks), dim3(256), 0, ST(s), (uint32_t*)dst, w);
+    } else {
+        int blocks = (int)((n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096);
+        hipLaunchKernelGGL(k_fill_zero_u8, dim3(blocks), dim3(256), 0, ST(s), (uint8_t*)dst, n);
+    }
+    LAUNCHED("k_fill_zero");
+}
+void dpuf_hip_fill_f32(float* dst, size_t n, float v, void* s) {
+    if (!n) return;
+    int blocks = (int)((n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096);
+    hipLaunchKernelGGL(k_fill_f32, dim3(blocks), dim3(256), 0, ST(s), dst, n, v);
+    LAUNCHED("k_fill_f32");
+}
+
+void* dpuf_hip_event_create(void) {
+    hipEvent_t e = nullptr;
+    CK(hipEventCreate(&e));
+    return (void*)e;
+}
+void dpuf_hip_event_destroy(void* e) { if (e) CK(hipEventDestroy((hipEvent_t)e)); }
+void dpuf_hip_event_record(void* e, void* s) { CK(hipEventRecord((hipEvent_t)e, ST(s))); }
+float dpuf_hip_event_elapsed_ms(void* a, void* b) {
+    float ms = 0.0f;
+    CK(hipEventSynchronize((hipEvent_t)b));
+    CK(hipEventElapsedTime(&ms, (hipEvent_t)a, (hipEvent_t)b));
+    return ms;
+}
+
+int32_t dpuf_hip_capture_begin(void* s) {
+    hipError_t e = hipStreamBeginCapture(ST(s), hipStreamCaptureModeThreadLocal);
+    note(e, "hipStreamBeginCapture");
+    return e == hipSuccess ? 0 : -1;
+}
+void* dpuf_hip_capture_end(void* s) {
+    hipGraph_t g = nullptr;
+    hipGraphExec_t ge = nullptr;
+    hipError_t e = hipStreamEndCapture(ST(s), &g);
+    note(e, "hipStreamEndCapture");
+    if (e != hipSuccess || !g) return nullptr;
+    e = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+    note(e, "hipGraphInstantiate");
+    (void)hipGraphDestroy(g);
+    return e == hipSuccess ? (void*)ge : nullptr;
+}
+int32_t dpuf_hip_graph_launch(void* g, void* s) {
+    hipError_t e = hipGraphLaunch((hipGraphExec_t)g, ST(s));
+    note(e, "hipGraphLaunch");
+    return e == hipSuccess ? 0 : -1;
+}
+void dpuf_hip_graph_destroy(void* g) { if (g) (void)hipGraphExecDestroy((hipGraphExec_t)g); }
+
+void dpuf_hip_embed(void* s, DpufDevW w, const int32_t* ids, int32_t M, const float* embeds, float* out) {
+    int threads = (w.cols >> 6) < 256 ? (w.cols >> 6) : 256;
+    threads = (threads + 63) & ~63;
+    hipLaunchKernelGGL(k_embed, dim3(M), dim3(threads), 0, ST(s), w, ids, embeds, out);
+    LAUNCHED("k_embed");
+}
+
+void dpuf_hip_resnorm_prep(void* s, int32_t M, int32_t H, float* h, const float* res, const float* w, float eps,
+                           int32_t n_prep, const uint8_t* const* signs, const DpufPrep* preps, float* xn_out) {
+    PrepSet ps;
+    memset(&ps, 0, sizeof ps);
+    ps.n = n_prep;
+    for (int i = 0; i < n_prep; i++) {
+        ps.sign[i] = signs[i];
+        ps.p[i] = preps[i];
+    }
+    hipLaunchKernelGGL(k_resnorm_prep, dim3(M), dim3(256), (size_t)H * sizeof(float), ST(s), H, h, res, w, eps, ps,
+                       xn_out);
+    LAUNCHED("k_resnorm_prep");
+}
+
+void dpuf_hip_prep(void* s, int32_t M, int32_t K, const float* x, const uint8_t* sign, DpufPrep p) {
+    int threads = (K >> 6) < 256 ? (K >> 6) : 256;
+    threads = (threads + 63) & ~63;
+    hipLaunchKernelGGL(k_prep, dim3(M), dim3(threads), 0, ST(s), K, x, sign, p);
+    LAUNCHED("k_prep");
+}
+
+void dpuf_hip_swiglu_prep(void* s, int32_t M, int32_t I, const float* gate, const float* up, float dz,
+                          const uint8_t* sign, DpufPrep p) {
+    int threads = (I >> 6) < 256 ? (I >> 6) : 256;
+    threads = (threads + 63) & ~63;
+    hipLaunchKernelGGL(k_swiglu_prep, dim3(M), dim3(threads), 0, ST(s), I, gate, up, dz, sign, p);
+    LAUNCHED("k_swiglu_prep");
+}
+
+void dpuf_hip_gemv(void* s, int32_t M, int32_t n_jobs, const DpufGemvJob* jobs, const int32_t* skip_flag,
+                   float fill) {
+    GemvBatch B;
+    memset(&B, 0, sizeof B);
+    int g = 0;
+    B.n = n_jobs;
+    for (int i = 0; i < n_jobs; i++) {
+        B.j[i] = jobs[i];
+        B.g_begin[i] = g;
+        g += 2 * (jobs[i].t1 - jobs[i].t0);
+    }
+    B.g_begin[n_jobs] = g;
+    if (g <= 0) return;
+    if (M == 1) {
+        hipLaunchKernelGGL(k_gemv1, dim3(g), dim3(64), 0, ST(s), B, skip_flag, fill);
+        LAUNCHED("k_gemv1");
+    } else {
+        hipLaunchKernelGGL(k_gemm8, dim3(g, (M + 7) / 8), dim3(64), 0, ST(s), B, M);
+        LAUNCHED("k_gemm8");
+    }
+}
+
+void dpuf_hip_qk_rope_kv(void* s, int32_t M, float* q, float* k, const float* v, const float* q_norm,
+                         const float* k_norm, float eps, const float* cos_tab, const float* sin_tab, float* kc,
+                         float* vc, const int32_t* pos0, int32_t n_q, int32_t n_kv, int32_t hd, int32_t max_seq) {
+    hipLaunchKernelGGL(k_qk_rope_kv, dim3(M, n_q + n_kv), dim3(hd), (size_t)hd * sizeof(float), ST(s), q, k, v,
+                       q_norm, k_norm, eps, cos_tab, sin_tab, kc, vc, pos0, n_q, n_kv, hd, max_seq);
+    LAUNCHED("k_qk_rope_kv");
+}
+
+void dpuf_hip_attn(void* s, int32_t M, const float* q, const float* kc, const float* vc, float* out, float* scores,
+                   const int32_t* pos0, int32_t n_q, int32_t n_kv, int32_t hd, int32_t max_seq, float scale) {
+    const int groups = n_q / n_kv;
+    hipLaunchKernelGGL(k_attn, dim3(M, n_kv, (groups + 1) / 2), dim3(256), (size_t)2 * hd * sizeof(float), ST(s), q,
+                       kc, vc, out, scores, pos0, n_q, n_kv, hd, max_seq, scale);
+    LAUNCHED("k_attn");
+}
+
+void dpuf_hip_zero_rows(void* s, int32_t M, float* out, int32_t ld, int32_t r0, int32_t r1) {
+    if (r1 <= r0) return;
+    hipLaunchKernelGGL(k_zero_rows, dim3(M), dim3(256), 0, ST(s), out, ld, r0, r1);
+    LAUNCHED("k_zero_rows");
+}
+
+void dpuf_hip_capture(void* s, int32_t M, int32_t H, const float* h, const float* hn, float* cap) {
+    hipLaunchKernelGGL(k_capture, dim3(M), dim3(256), 0, ST(s), H, h, hn, cap);
+    LAUNCHED("k_capture");
+}
+
+void dpuf_hip_topcheck(void* s, const float* logits, int32_t n, float thr, int32_t* flag) {
+    hipLaunchKernelGGL(k_topcheck, dim3(1), dim3(1024), 0, ST(s), logits, n, thr, flag);
+    LAUNCHED("k_topcheck");
+}
+
+void dpuf_hip_argmax(void* s, const float* logits, int32_t V, int32_t* out) {
+    hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, ST(s), logits, V, out);
+    LAUNCHED("k_argmax");
+}
+
+void dpuf_hip_fwht_sign(void* s, int32_t M, int32_t K, const float* x, const uint8_t* sign, float* out) {
+    int threads = (K >> 6) < 256 ? (K >> 6) : 256;
+    threads = (threads + 63) & ~63;
+    hipLaunchKernelGGL(k_fwht_sign, dim3(M), dim3(threads), 0, ST(s), K, x, sign, out);
+    LAUNCHED("k_fwht_sign");
+}
+
+void dpuf_hip_slab_pack(void* s, int32_t mc, int32_t K, DpufPrep rows, int32_t* sq, float* ss, int32_t* sm) {
+    hipLaunchKernelGGL(k_slab_pack, dim3(64), dim3(256), 0, ST(s), mc, K, rows, sq, ss, sm);
+    LAUNCHED("k_slab_pack");
+}
+
+void dpuf_hip_slab_unpack(void* s, int32_t M, int32_t K, const int32_t* sq, const float* ss, const int32_t* sm,
+                          DpufPrep rows) {
+    hipLaunchKernelGGL(k_slab_unpack, dim3(256), dim3(256), 0, ST(s), M, K, sq, ss, sm, rows);
+    LAUNCHED("k_slab_unpack");
+}
+
+}  // extern "C"

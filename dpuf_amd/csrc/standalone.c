@@ -1,0 +1,292 @@
+/*
+ * standalone.c -- the mode 12 entry points of the ABI that take host
+ * pointers (reference dpuf_avx2.c:774-788, 2364-2449, 2585-2783).  Each call
+ * validates its tiles on the host, stages inputs to HBM, runs the same HIP
+ * kernels as the engine, and copies results back before returning.  They are
+ * synchronous and allocate per call; throughput users keep weights resident
+ * in an engine instead.
+ */
+#include <stdlib.h>
+#include <string.h>
+
+#include "../../include/dpuf_kernels.h"
+#include "hip_layer.h"
+
+static void* g_stream = NULL;
+
+static void* stream(void) {
+    if (!g_stream && dpuf_hip_device_count() > 0) g_stream = dpuf_hip_stream_create();
+    return g_stream;
+}
+
+/* Checks tiles [t0, t1) of a mode 12 payload (row counts in [1, 16] and
+ * inside `rows`, groups inside the byte range) and returns the byte range
+ * [*lo, *hi). */
+static int check_tiles(int32_t rows, int32_t cols, int32_t t0, int32_t t1, const uint8_t* base,
+                       const uint64_t* offs, uint64_t* lo, uint64_t* hi) {
+    if (cols <= 0 || (cols % 64) != 0 || t0 < 0 || t1 <= t0 || !base || !offs) return 0;
+    const uint64_t grp = (uint64_t)(cols / 32) * 144u;
+    *lo = offs[t0];
+    *hi = offs[t1];
+    if (*hi < *lo) return 0;
+    for (int32_t t = t0; t < t1; t++) {
+        if (offs[t] < *lo || offs[t] + 16 > *hi || ((offs[t] - *lo) % 16) != 0) return 0;
+        DpufQrTileHdr th;
+        memcpy(&th, base + offs[t], sizeof th);
+        if (th.n_rows < 1 || th.n_rows > 16 || (int64_t)t * 16 + th.n_rows > rows) return 0;
+        if (offs[t] + 16 + (uint64_t)((th.n_rows + 7) / 8) * grp > *hi) return 0;
+    }
+    return 1;
+}
+
+typedef struct {
+    void* tiles;
+    void* offs;
+    void* sign;
+    DpufDevW w;
+} Staged;
+
+/* Uploads tiles [t0, t1) with offsets rebased to the uploaded range. */
+static int stage_weights(int32_t rows, int32_t cols, int32_t t0, int32_t t1, const uint8_t* base,
+                         const uint64_t* offs, const uint8_t* sign, Staged* st) {
+    uint64_t lo, hi;
+    memset(st, 0, sizeof *st);
+    if (!check_tiles(rows, cols, t0, t1, base, offs, &lo, &hi)) return 0;
+    void* s = stream();
+    uint64_t* rel = (uint64_t*)calloc((size_t)t1 + 1, 8);
+    if (!rel) return 0;
+    for (int32_t t = t0; t <= t1; t++) rel[t] = offs[t] - lo;
+    st->tiles = dpuf_hip_malloc((size_t)(hi - lo));
+    st->offs = dpuf_hip_malloc(((size_t)t1 + 1) * 8);
+    if (sign) st->sign = dpuf_hip_malloc((size_t)cols / 8);
+    if (!st->tiles || !st->offs || (sign && !st->sign)) {
+        free(rel);
+        return 0;
+    }
+    dpuf_hip_h2d(st->tiles, base + lo, (size_t)(hi - lo), s);
+    dpuf_hip_h2d(st->offs, rel, ((size_t)t1 + 1) * 8, s);
+    if (sign) dpuf_hip_h2d(st->sign, sign, (size_t)cols / 8, s);
+    dpuf_hip_sync(s);
+    free(rel);
+    st->w.tiles = (const uint8_t*)st->tiles;
+    st->w.offs = (const uint64_t*)st->offs;
+    st->w.sign = (const uint8_t*)st->sign;
+    st->w.rows = rows;
+    st->w.cols = cols;
+    st->w.n_tiles = t1;
+    return 1;
+}
+
+static void unstage(Staged* st) {
+    dpuf_hip_free(st->tiles);
+    dpuf_hip_free(st->offs);
+    dpuf_hip_free(st->sign);
+}
+
+static int prep_alloc(DpufPrep* p, int32_t M, int32_t K) {
+    p->q = (int8_t*)dpuf_hip_malloc((size_t)M * K);
+    p->s = (float*)dpuf_hip_malloc((size_t)M * (K / 32) * 4);
+    p->m = (int32_t*)dpuf_hip_malloc((size_t)M * (K / 32) * 4);
+    return p->q && p->s && p->m;
+}
+
+static void prep_free(DpufPrep* p) {
+    dpuf_hip_free(p->q);
+    dpuf_hip_free(p->s);
+    dpuf_hip_free(p->m);
+}
+
+DPUF_EXPORT void dpuf_fwht64_sign_f32(int32_t cols, const float* x_in, const uint8_t* sign_bits, float* x_out) {
+    void* s = stream();
+    if (!s || cols <= 0 || (cols % 64) != 0 || !x_in || !x_out) return;
+    float* dx = (float*)dpuf_hip_malloc((size_t)cols * 4);
+    float* dy = (float*)dpuf_hip_malloc((size_t)cols * 4);
+    void* ds = sign_bits ? dpuf_hip_malloc((size_t)cols / 8) : NULL;
+    if (dx && dy && (!sign_bits || ds)) {
+        dpuf_hip_h2d(dx, x_in, (size_t)cols * 4, s);
+        if (ds) dpuf_hip_h2d(ds, sign_bits, (size_t)cols / 8, s);
+        dpuf_hip_fwht_sign(s, 1, cols, dx, (const uint8_t*)ds, dy);
+        dpuf_hip_d2h(x_out, dy, (size_t)cols * 4, s);
+        dpuf_hip_sync(s);
+    }
+    dpuf_hip_free(dx); dpuf_hip_free(dy); dpuf_hip_free(ds);
+}
+
+DPUF_EXPORT void dpuf_prep_had4_packed_slab(int32_t mc, int32_t cols, const float* x_slab_f32,
+                                            const uint8_t* sign_bits, float* f_scratch, int8_t* x_out,
+                                            float* x_scale_out, int32_t* x_sum8_out, int32_t pack_slab) {
+    void* s = stream();
+    if (!s || mc <= 0 || mc > 6 || cols <= 0 || (cols % 64) != 0 || !x_slab_f32 || !x_out || !x_scale_out ||
+        !x_sum8_out)
+        return;
+    const int32_t nb = cols / 32;
+    float* dx = (float*)dpuf_hip_malloc((size_t)mc * cols * 4);
+    float* df = (float*)dpuf_hip_malloc((size_t)mc * cols * 4);
+    void* ds = sign_bits ? dpuf_hip_malloc((size_t)cols / 8) : NULL;
+    DpufPrep rows = {0, 0, 0};
+    int32_t* sq = (int32_t*)dpuf_hip_malloc((size_t)nb * 192);
+    float* ss = (float*)dpuf_hip_malloc((size_t)nb * 6 * 4);
+    int32_t* sm = (int32_t*)dpuf_hip_malloc((size_t)nb * 6 * 4);
+    if (dx && df && (!sign_bits || ds) && prep_alloc(&rows, mc, cols) && sq && ss && sm) {
+        dpuf_hip_h2d(dx, x_slab_f32, (size_t)mc * cols * 4, s);
+        if (ds) dpuf_hip_h2d(ds, sign_bits, (size_t)cols / 8, s);
+        dpuf_hip_prep(s, mc, cols, dx, (const uint8_t*)ds, rows);
+        if (f_scratch) {
+            dpuf_hip_fwht_sign(s, mc, cols, dx, (const uint8_t*)ds, df);
+            dpuf_hip_d2h(f_scratch, df, (size_t)mc * cols * 4, s);
+        }
+        if (pack_slab) {
+            /* token lanes j >= mc keep the caller's previous contents */
+            dpuf_hip_h2d(sq, x_out, (size_t)nb * 192, s);
+            dpuf_hip_h2d(ss, x_scale_out, (size_t)nb * 6 * 4, s);
+            dpuf_hip_h2d(sm, x_sum8_out, (size_t)nb * 6 * 4, s);
+            dpuf_hip_slab_pack(s, mc, cols, rows, sq, ss, sm);
+            dpuf_hip_d2h(x_out, sq, (size_t)nb * 192, s);
+            dpuf_hip_d2h(x_scale_out, ss, (size_t)nb * 6 * 4, s);
+            dpuf_hip_d2h(x_sum8_out, sm, (size_t)nb * 6 * 4, s);
+        } else {
+            /* row layout: every row writes the same outputs, the last one stays */
+            const size_t r = (size_t)(mc - 1);
+            dpuf_hip_d2h(x_out, rows.q + r * cols, (size_t)cols, s);
+            dpuf_hip_d2h(x_scale_out, rows.s + r * nb, (size_t)nb * 4, s);
+            dpuf_hip_d2h(x_sum8_out, rows.m + r * nb, (size_t)nb * 4, s);
+        }
+        dpuf_hip_sync(s);
+    }
+    dpuf_hip_free(dx); dpuf_hip_free(df); dpuf_hip_free(ds);
+    dpuf_hip_free(sq); dpuf_hip_free(ss); dpuf_hip_free(sm);
+    prep_free(&rows);
+}
+
+/* Copies rows [r0, r1) of M output rows of width `rows` back to the host. */
+static void fetch_rows(float* out, const float* dout, int32_t M, int32_t rows, int32_t r0, int32_t r1, void* s) {
+    if (r1 <= r0) return;
+    if (r0 == 0 && r1 == rows) {
+        dpuf_hip_d2h(out, dout, (size_t)M * rows * 4, s);
+        return;
+    }
+    for (int32_t m = 0; m < M; m++)
+        dpuf_hip_d2h(out + (size_t)m * rows + r0, dout + (size_t)m * rows + r0, (size_t)(r1 - r0) * 4, s);
+}
+
+DPUF_EXPORT void dpuf_matmul_qr_hadamard4_packed_tile_range(int32_t M, int32_t rows, int32_t cols, int32_t t_start,
+                                                            int32_t t_end, const int8_t* x_q8,
+                                                            const float* x_blk_scale, const int32_t* x_sum8,
+                                                            const uint8_t* tensor_base, const uint64_t* tile_offsets,
+                                                            float* out) {
+    void* s = stream();
+    if (!s || M <= 0 || rows <= 0 || t_start < 0 || t_end <= t_start || (int64_t)t_start * 16 >= rows || !x_q8 ||
+        !x_blk_scale || !x_sum8 || !out)
+        return;
+    if ((int64_t)t_end * 16 > (int64_t)rows + 15) return;
+    Staged st;
+    if (!stage_weights(rows, cols, t_start, t_end, tensor_base, tile_offsets, NULL, &st)) return;
+    const int32_t nb = cols / 32;
+    DpufPrep p = {0, 0, 0};
+    float* dout = (float*)dpuf_hip_malloc((size_t)M * rows * 4);
+    if (prep_alloc(&p, M, cols) && dout) {
+        if (M == 1) {
+            dpuf_hip_h2d(p.q, x_q8, (size_t)cols, s);
+            dpuf_hip_h2d(p.s, x_blk_scale, (size_t)nb * 4, s);
+            dpuf_hip_h2d(p.m, x_sum8, (size_t)nb * 4, s);
+        } else {
+            const int32_t ns = (M + 5) / 6;
+            int32_t* sq = (int32_t*)dpuf_hip_malloc((size_t)ns * nb * 192);
+            float* ss = (float*)dpuf_hip_malloc((size_t)ns * nb * 6 * 4);
+            int32_t* sm = (int32_t*)dpuf_hip_malloc((size_t)ns * nb * 6 * 4);
+            if (sq && ss && sm) {
+                dpuf_hip_h2d(sq, x_q8, (size_t)ns * nb * 192, s);
+                dpuf_hip_h2d(ss, x_blk_scale, (size_t)ns * nb * 6 * 4, s);
+                dpuf_hip_h2d(sm, x_sum8, (size_t)ns * nb * 6 * 4, s);
+                dpuf_hip_slab_unpack(s, M, cols, sq, ss, sm, p);
+                dpuf_hip_sync(s);
+            }
+            dpuf_hip_free(sq); dpuf_hip_free(ss); dpuf_hip_free(sm);
+        }
+        DpufGemvJob j;
+        j.w = st.w;
+        j.t0 = t_start;
+        j.t1 = t_end;
+        j.p = p;
+        j.out = dout;
+        j.ldo = rows;
+        dpuf_hip_gemv(s, M, 1, &j, NULL, 0.0f);
+        int32_t r1 = t_end * 16 < rows ? t_end * 16 : rows;
+        fetch_rows(out, dout, M, rows, t_start * 16, r1, s);
+        dpuf_hip_sync(s);
+    }
+    prep_free(&p);
+    dpuf_hip_free(dout);
+    unstage(&st);
+}
+
+DPUF_EXPORT void dpuf_matmul_qr_hadamard4_packed_f32(int32_t M, int32_t rows, int32_t cols, int32_t n_tiles,
+                                                     const float* x_in, const uint8_t* tensor_base,
+                                                     const uint64_t* tile_offsets, const uint8_t* sign_bits,
+                                                     float* out) {
+    void* s = stream();
+    if (!s || M <= 0 || rows <= 0 || n_tiles <= 0 || !x_in || !out) return;
+    if ((int64_t)n_tiles * 16 > (int64_t)rows + 15 || (int64_t)n_tiles * 16 < rows) return;
+    Staged st;
+    if (!stage_weights(rows, cols, 0, n_tiles, tensor_base, tile_offsets, sign_bits, &st)) return;
+    DpufPrep p = {0, 0, 0};
+    float* dx = (float*)dpuf_hip_malloc((size_t)M * cols * 4);
+    float* dout = (float*)dpuf_hip_malloc((size_t)M * rows * 4);
+    if (prep_alloc(&p, M, cols) && dx && dout) {
+        dpuf_hip_h2d(dx, x_in, (size_t)M * cols * 4, s);
+        dpuf_hip_prep(s, M, cols, dx, st.w.sign, p);
+        DpufGemvJob j;
+        j.w = st.w;
+        j.t0 = 0;
+        j.t1 = n_tiles;
+        j.p = p;
+        j.out = dout;
+        j.ldo = rows;
+        dpuf_hip_gemv(s, M, 1, &j, NULL, 0.0f);
+        dpuf_hip_d2h(out, dout, (size_t)M * rows * 4, s);
+        dpuf_hip_sync(s);
+    }
+    prep_free(&p);
+    dpuf_hip_free(dx);
+    dpuf_hip_free(dout);
+    unstage(&st);
+}
+
+DPUF_EXPORT void dpuf_embed_qr_hadamard4_packed_f32(int32_t n_tokens, int32_t cols, const int32_t* token_ids,
+                                                    const uint8_t* tensor_base, const uint64_t* tile_offsets,
+                                                    const uint8_t* sign_bits, float* out) {
+    void* s = stream();
+    if (!s || n_tokens <= 0 || !token_ids || !out) return;
+    int32_t max_id = 0;
+    for (int32_t i = 0; i < n_tokens; i++) {
+        if (token_ids[i] < 0) return;
+        if (token_ids[i] > max_id) max_id = token_ids[i];
+    }
+    const int32_t nt = max_id / 16 + 1;
+    Staged st;
+    if (!stage_weights(nt * 16, cols, 0, nt, tensor_base, tile_offsets, sign_bits, &st)) return;
+    for (int32_t i = 0; i < n_tokens; i++) {
+        DpufQrTileHdr th;
+        memcpy(&th, tensor_base + tile_offsets[token_ids[i] / 16], sizeof th);
+        if (token_ids[i] % 16 >= th.n_rows) { unstage(&st); return; }
+    }
+    int32_t* dids = (int32_t*)dpuf_hip_malloc((size_t)n_tokens * 4);
+    float* dout = (float*)dpuf_hip_malloc((size_t)n_tokens * cols * 4);
+    if (dids && dout) {
+        dpuf_hip_h2d(dids, token_ids, (size_t)n_tokens * 4, s);
+        dpuf_hip_embed(s, st.w, dids, n_tokens, NULL, dout);
+        dpuf_hip_d2h(out, dout, (size_t)n_tokens * cols * 4, s);
+        dpuf_hip_sync(s);
+    }
+    dpuf_hip_free(dids);
+    dpuf_hip_free(dout);
+    unstage(&st);
+}
+
+DPUF_EXPORT void dpuf_embed_qr_any_f32(const DpufWeightDesc* w, int32_t n_tokens, const int32_t* token_ids,
+                                       float* out, float* scratch_f32) {
+    (void)scratch_f32;
+    if (!w || w->mode != DPUF_MODE_QR_HAD4_PACKED) return; /* other modes are not built */
+    dpuf_embed_qr_hadamard4_packed_f32(n_tokens, w->cols, token_ids, w->tensor_base, w->tile_offsets, w->sign_bits,
+                                       out);
+}

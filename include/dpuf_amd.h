@@ -1,0 +1,77 @@
+/*
+ * dpuf_amd.h -- entry points this build adds next to the dpuf_kernels.h ABI.
+ * None of them has a counterpart in the reference; they exist for callers
+ * that want device-side greedy sampling, for parity tests (per-layer residual
+ * capture, KV injection) and for measurement.  The reference ABI does not
+ * depend on any of them.
+ */
+#ifndef DPUF_AMD_H
+#define DPUF_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include "dpuf_kernels.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Largest n_tokens a single forward call accepts (the reference caps at 256;
+ * 512 is a compatible superset). */
+#define DPUF_AMD_MAX_BATCH 512
+
+/* 1 when a HIP device is usable, else 0. */
+DPUF_EXPORT int32_t dpuf_amd_device_ok(void);
+
+/* Text of the first HIP error recorded by the library ("" if none). */
+DPUF_EXPORT const char* dpuf_amd_last_error(void);
+
+/* forward_batch_ex plus greedy sampling on the device: *token_out receives the
+ * first-max argmax (dpuf-cli.c:1997-2004 rule) of the last row's logits, so a
+ * decode loop moves 4 bytes per token instead of V floats.  logits_out may be
+ * NULL (no copy) or receive the last row's logits.  Same return codes as
+ * dpuf_engine_forward_batch_ex. */
+DPUF_EXPORT int32_t dpuf_amd_engine_forward_argmax(void* handle, int32_t n_tokens, const int32_t* token_ids,
+                                                   int32_t pos0, const float* embeds_in, int32_t use_graph,
+                                                   int32_t* token_out, float* logits_out);
+
+/* Writes / reads positions [pos0, pos0+n) of (layer, kv head) of the active
+ * slot, host pointers of n * head_dim floats.  0 ok, -1 bad arguments. */
+DPUF_EXPORT int32_t dpuf_amd_engine_set_kv(void* handle, int32_t layer, int32_t kv_head, int32_t pos0, int32_t n,
+                                           const float* k, const float* v);
+DPUF_EXPORT int32_t dpuf_amd_engine_get_kv(void* handle, int32_t layer, int32_t kv_head, int32_t pos0, int32_t n,
+                                           float* k, float* v);
+
+/* Captures the residual stream after every layer ([num_layers][n][hidden])
+ * for calls with n_tokens <= max_tokens (0 disables).  get_capture copies
+ * num_layers * max_tokens * hidden floats.  0 ok, -1 error. */
+DPUF_EXPORT int32_t dpuf_amd_engine_set_capture(void* handle, int32_t max_tokens);
+DPUF_EXPORT int32_t dpuf_amd_engine_get_capture(void* handle, float* out, size_t n_floats);
+
+/* Kernel timing with HIP events on the engine's stream.  Kinds:
+ * 0 gate/up GEMV, 1 down GEMV, 2 QKV GEMV, 3 O GEMV, 4 LM head, 5 attention,
+ * 6 norm+prep, 7 whole forward call.  get_timing returns total ms, launch
+ * count and algorithmic bytes for a kind; enabling resets the counters. */
+DPUF_EXPORT void dpuf_amd_engine_set_timing(void* handle, int32_t enable);
+DPUF_EXPORT int32_t dpuf_amd_engine_get_timing(void* handle, int32_t kind, double* total_ms, int64_t* count,
+                                               double* bytes);
+
+/* Mode 12 tile bytes resident in HBM (all layers + LM head). */
+DPUF_EXPORT uint64_t dpuf_amd_engine_weight_bytes(void* handle);
+
+/* Number of forward calls in which the LM-head early exit fired. */
+DPUF_EXPORT int64_t dpuf_amd_engine_early_exit_count(void* handle);
+
+/* Times `iters` launches of one resident matrix's M-row GEMV (which: 0 q,
+ * 1 k, 2 v, 3 o, 4 gate, 5 up, 6 down, 7 LM head), cycling through layers
+ * start..num_layers-1 so that consecutive launches read distinct weights.
+ * Returns the mean ms per launch (or < 0 on error); *bytes gets the
+ * algorithmic bytes of one launch. */
+DPUF_EXPORT double dpuf_amd_gemv_bench(void* handle, int32_t which, int32_t M, int32_t iters, int32_t start_layer,
+                                       double* bytes);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

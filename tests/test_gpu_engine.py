@@ -1,0 +1,107 @@
+"""End-to-end parity of the GPU engine (C ABI) against the CPU oracle."""
+import numpy as np
+import pytest
+
+from dpuf_amd import model as M
+
+pytestmark = pytest.mark.gpu
+
+TINY = dict(hidden_size=256, intermediate_size=512, num_layers=3, num_q_heads=4, num_kv_heads=2, head_dim=64,
+            vocab_size=4096, tie_word_embeddings=1)
+
+
+def _bits_equal(a, b):
+    return np.array_equal(np.asarray(a, np.float32).view(np.uint32), np.asarray(b, np.float32).view(np.uint32))
+
+
+def _close(a, b, rtol=1e-3, atol=1e-4):
+    return np.allclose(a, b, rtol=rtol, atol=atol)
+
+
+class Pair:
+    """A GPU engine and an oracle engine over the same model."""
+
+    def __init__(self, eng, orc, model, cfg=None):
+        self.eng, self.orc, self.m = eng, orc, model
+        self.g = eng.dpuf_engine_create(*model.create_args(cfg))
+        assert self.g, eng.dpuf_amd_last_error()
+        self.o = orc.orc_engine_create(*model.create_args(cfg))
+        assert self.o
+        self.V = model.cfg.contents.vocab_size
+
+    def forward(self, ids, pos0, only_last=1, embeds=None):
+        n = len(ids) if ids is not None else embeds.shape[0]
+        rows = 1 if only_last == 1 else n
+        lg = np.zeros((rows, self.V), np.float32)
+        lo = np.zeros((rows, self.V), np.float32)
+        ip = M.ptr(ids) if ids is not None else None
+        ep = M.ptr(embeds) if embeds is not None else None
+        rg = self.eng.dpuf_engine_forward_batch_ex(self.g, n, ip, pos0, ep, None, None, None, None, only_last,
+                                                   M.ptr(lg) if only_last != 2 else None)
+        ro = self.orc.orc_engine_forward(self.o, n, ip, pos0, ep, only_last, M.ptr(lo) if only_last != 2 else None)
+        assert rg == 0 and ro == 0, (rg, ro)
+        return lg, lo
+
+    def close(self):
+        self.eng.dpuf_engine_destroy(self.g)
+        self.orc.orc_engine_destroy(self.o)
+
+
+@pytest.fixture(scope="module")
+def tiny():
+    return M.Model.build(TINY, max_seq_len=96, seed=5)
+
+
+def test_tiny_prefill_decode_bit_exact(eng, orc, tiny):
+    p = Pair(eng, orc, tiny)
+    ids = np.random.default_rng(1).integers(0, 4096, 13).astype(np.int32)
+    lg, lo = p.forward(ids, 0, only_last=0)
+    assert _bits_equal(lg, lo), np.max(np.abs(lg - lo))
+    tok = int(np.argmax(lo[-1]))
+    for step in range(12):
+        lg, lo = p.forward(np.array([tok], np.int32), 13 + step)
+        assert _bits_equal(lg, lo), (step, np.max(np.abs(lg - lo)))
+        tok = int(np.argmax(lo[0]))
+    p.close()
+
+
+def test_argmax_entry_and_graph(eng, orc, tiny):
+    p = Pair(eng, orc, tiny)
+    ids = np.random.default_rng(2).integers(0, 4096, 5).astype(np.int32)
+    lg, lo = p.forward(ids, 0)
+    tok = int(np.argmax(lo[0]))
+    import ctypes as C
+    out = C.c_int32(-1)
+    for step in range(6):
+        rc = eng.dpuf_amd_engine_forward_argmax(p.g, 1, M.ptr(np.array([tok], np.int32)), 5 + step, None, 1,
+                                                C.byref(out), None)
+        assert rc == 0
+        lo = np.zeros(4096, np.float32)
+        orc.orc_engine_forward(p.o, 1, M.ptr(np.array([tok], np.int32)), 5 + step, None, 1, M.ptr(lo))
+        assert out.value == orc.orc_argmax(M.ptr(lo), 4096)
+        tok = out.value
+    p.close()
+
+
+def test_qwen3_06b_token_exact(eng, orc):
+    """Qwen3-0.6B shape, random-init: 32-token prompt + 32 greedy tokens."""
+    m = M.Model.build(M.QWEN3_0_6B, max_seq_len=80, seed=1234)
+    p = Pair(eng, orc, m)
+    ids = np.random.default_rng(2024).integers(0, 151936, 32).astype(np.int32)
+    print("0.6B pp32", flush=True)
+    lg, lo = p.forward(ids, 0)
+    assert _close(lg, lo)
+    tg, to = [], []
+    tok_g, tok_o = int(np.argmax(lg[0])), int(np.argmax(lo[0]))
+    exact = _bits_equal(lg, lo)
+    for step in range(32):
+        tg.append(tok_g)
+        to.append(tok_o)
+        lg, lo = p.forward(np.array([tok_o], np.int32), 32 + step)
+        assert _close(lg, lo), step
+        exact = exact and _bits_equal(lg, lo)
+        tok_g, tok_o = int(np.argmax(lg[0])), int(np.argmax(lo[0]))
+    print("greedy", tg, "bit-exact logits:", exact)
+    assert tg == to
+    assert exact
+    p.close()

@@ -1,0 +1,137 @@
+"""GPU parity of the mode 12 kernels behind the standalone C ABI entry points
+against the CPU oracle: bit-exact for the integer/packed work, and for the
+fp32 chains whose order the reference fixes."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from dpuf_amd import model as M
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [(16, 64), (40, 128), (200, 1024), (1000, 3072)]
+SHAPES_8B = [(1024, 4096), (4096, 12288)]
+
+
+def _mat(rows, cols, seed, std=0.02):
+    W = M.random_normal(rows * cols, std, seed, f"w{rows}x{cols}").reshape(rows, cols)
+    sb = M.sign_bits(cols, seed, f"s{rows}x{cols}")
+    blob, d = M.pack_matrix(W, sb)
+    return blob, d
+
+
+def _x(rows, cols, seed):
+    return np.random.default_rng(seed).standard_normal((rows, cols)).astype(np.float32)
+
+
+def _same_bits(a, b):
+    return np.array_equal(np.asarray(a, np.float32).view(np.uint32), np.asarray(b, np.float32).view(np.uint32))
+
+
+@pytest.mark.parametrize("rows,cols", SHAPES + SHAPES_8B)
+@pytest.mark.parametrize("m", [1, 7])
+def test_matmul_f32_bit_exact(eng, orc, rows, cols, m):
+    if cols >= 4096 and m > 1:
+        pytest.skip("covered at M=1 for the large shapes")
+    blob, d = _mat(rows, cols, 11 + rows)
+    x = _x(m, cols, rows + cols)
+    # a block with amax <= 1e-4 exercises the zero-scale path
+    x[0, :32] = 1e-6
+    out_g = np.full((m, rows), np.nan, np.float32)
+    out_o = np.full((m, rows), np.nan, np.float32)
+    print(f"matmul_f32 rows={rows} cols={cols} M={m}", flush=True)
+    eng.dpuf_matmul_qr_hadamard4_packed_f32(m, rows, cols, d.n_tiles, M.ptr(x), d.tensor_base, d.tile_offsets,
+                                            d.sign_bits, M.ptr(out_g))
+    orc.orc_matmul_f32(m, rows, cols, d.n_tiles, M.ptr(x), d.tensor_base, d.tile_offsets, d.sign_bits,
+                       M.ptr(out_o))
+    assert np.isfinite(out_o).all()
+    assert _same_bits(out_g, out_o), f"max abs diff {np.nanmax(np.abs(out_g - out_o))}"
+
+
+@pytest.mark.parametrize("cols", [64, 1024, 4096])
+def test_fwht_and_prep_row(eng, orc, cols):
+    x = _x(1, cols, cols)[0]
+    x[:32] *= 1e-7  # zero block
+    x[40] = 1e4      # saturating block
+    sb = M.sign_bits(cols, 5, "p")
+    fg = np.zeros(cols, np.float32)
+    fo = np.zeros(cols, np.float32)
+    eng.dpuf_fwht64_sign_f32(cols, M.ptr(x), M.ptr(sb), M.ptr(fg))
+    orc.orc_fwht64_sign(cols, M.ptr(x), M.ptr(sb), M.ptr(fo))
+    assert _same_bits(fg, fo)
+    nb = cols // 32
+    qg, qo = np.zeros(cols, np.int8), np.zeros(cols, np.int8)
+    sg, so = np.zeros(nb, np.float32), np.zeros(nb, np.float32)
+    mg, mo = np.zeros(nb, np.int32), np.zeros(nb, np.int32)
+    scr = np.zeros(cols, np.float32)
+    eng.dpuf_prep_had4_packed_slab(1, cols, M.ptr(x), M.ptr(sb), M.ptr(scr), M.ptr(qg), M.ptr(sg), M.ptr(mg), 0)
+    orc.orc_prep_row(cols, M.ptr(x), M.ptr(sb), M.ptr(qo), M.ptr(so), M.ptr(mo))
+    assert np.array_equal(qg, qo) and np.array_equal(mg, mo) and _same_bits(sg, so)
+    assert _same_bits(scr, fo)
+
+
+@pytest.mark.parametrize("mc", [1, 4, 6])
+def test_prep_slab(eng, orc, mc):
+    cols = 256
+    nb = cols // 32
+    x = _x(mc, cols, 77 + mc)
+    sb = M.sign_bits(cols, 9, "slab")
+    qg = np.full(nb * 192, 0x55, np.int8)
+    sg = np.full(nb * 6, -3.0, np.float32)
+    mg = np.full(nb * 6, 99, np.int32)
+    qo, so, mo = qg.copy(), sg.copy(), mg.copy()
+    scr = np.zeros(mc * cols, np.float32)
+    eng.dpuf_prep_had4_packed_slab(mc, cols, M.ptr(x), M.ptr(sb), M.ptr(scr), M.ptr(qg), M.ptr(sg), M.ptr(mg), 1)
+    orc.orc_prep_slab(mc, cols, M.ptr(x), M.ptr(sb), M.ptr(qo), M.ptr(so), M.ptr(mo))
+    assert np.array_equal(qg, qo) and np.array_equal(mg, mo) and _same_bits(sg, so)
+
+
+@pytest.mark.parametrize("m", [1, 9])
+def test_tile_range(eng, orc, m):
+    rows, cols = 100, 512
+    blob, d = _mat(rows, cols, 21)
+    x = _x(m, cols, 5)
+    nb = cols // 32
+    # row-layout prep from the oracle, and the slab layout the reference takes for M > 1
+    q = np.zeros((m, cols), np.int8)
+    s = np.zeros((m, nb), np.float32)
+    mm = np.zeros((m, nb), np.int32)
+    for i in range(m):
+        orc.orc_prep_row(cols, M.ptr(x[i]), d.sign_bits, M.ptr(q[i]), M.ptr(s[i]), M.ptr(mm[i]))
+    t0, t1 = 2, 6
+    out_g = np.full((m, rows), 7.0, np.float32)
+    out_o = np.full((m, rows), 7.0, np.float32)
+    orc.orc_gemm_tiles(m, rows, cols, t0, t1, M.ptr(q), M.ptr(s), M.ptr(mm), d.tensor_base, d.tile_offsets,
+                       M.ptr(out_o), int(m == 1))
+    if m == 1:
+        eng.dpuf_matmul_qr_hadamard4_packed_tile_range(1, rows, cols, t0, t1, M.ptr(q), M.ptr(s), M.ptr(mm),
+                                                       d.tensor_base, d.tile_offsets, M.ptr(out_g))
+    else:
+        ns = (m + 5) // 6
+        sq = np.zeros(ns * nb * 192, np.int8)
+        ss = np.zeros(ns * nb * 6, np.float32)
+        sm = np.zeros(ns * nb * 6, np.int32)
+        for sl in range(ns):
+            mc = min(6, m - 6 * sl)
+            orc.orc_prep_slab(mc, cols, M.ptr(np.ascontiguousarray(x[6 * sl:6 * sl + mc])), d.sign_bits,
+                              M.ptr(sq[sl * nb * 192:]), M.ptr(ss[sl * nb * 6:]), M.ptr(sm[sl * nb * 6:]))
+        eng.dpuf_matmul_qr_hadamard4_packed_tile_range(m, rows, cols, t0, t1, M.ptr(sq), M.ptr(ss), M.ptr(sm),
+                                                       d.tensor_base, d.tile_offsets, M.ptr(out_g))
+    assert _same_bits(out_g, out_o)
+    assert (out_g[:, :t0 * 16] == 7.0).all() and (out_g[:, t1 * 16:] == 7.0).all()
+
+
+def test_embed(eng, orc):
+    rows, cols = 300, 1024
+    blob, d = _mat(rows, cols, 31)
+    ids = np.array([0, 7, 8, 15, 16, 299, 123], np.int32)
+    eg = np.zeros((len(ids), cols), np.float32)
+    eo = np.zeros((len(ids), cols), np.float32)
+    eng.dpuf_embed_qr_hadamard4_packed_f32(len(ids), cols, M.ptr(ids), d.tensor_base, d.tile_offsets, d.sign_bits,
+                                           M.ptr(eg))
+    orc.orc_embed(len(ids), cols, M.ptr(ids), d.tensor_base, d.tile_offsets, d.sign_bits, M.ptr(eo))
+    assert _same_bits(eg, eo)
+    e2 = np.zeros_like(eg)
+    eng.dpuf_embed_qr_any_f32(C.byref(d), len(ids), M.ptr(ids), M.ptr(e2), None)
+    assert _same_bits(e2, eo)
