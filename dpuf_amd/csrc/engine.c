@@ -86,19 +86,25 @@ static int env_int(const char* name, int* out) {
     return 1;
 }
 
-static void tm_begin(Engine* e, int kind, double bytes) {
-    if (!e->timing || e->n_ev + 2 > MAX_EVENTS) return;
-    if (!e->ev[e->n_ev]) e->ev[e->n_ev] = dpuf_hip_event_create();
-    if (!e->ev[e->n_ev + 1]) e->ev[e->n_ev + 1] = dpuf_hip_event_create();
-    e->ev_kind[e->n_ev / 2] = kind;
-    e->ev_bytes[e->n_ev / 2] = bytes;
-    dpuf_hip_event_record(e->ev[e->n_ev], e->stream);
+/* Starts a timed region: reserves an event pair, records its start and
+ * returns its index (-1 when timing is off or the table is full).  Regions
+ * may nest (the whole-call region encloses the per-kernel ones). */
+static int tm_begin(Engine* e, int kind, double bytes) {
+    if (!e->timing || e->n_ev + 2 > MAX_EVENTS) return -1;
+    const int i = e->n_ev;
+    if (!e->ev[i]) e->ev[i] = dpuf_hip_event_create();
+    if (!e->ev[i + 1]) e->ev[i + 1] = dpuf_hip_event_create();
+    if (!e->ev[i] || !e->ev[i + 1]) return -1;
+    e->ev_kind[i / 2] = kind;
+    e->ev_bytes[i / 2] = bytes;
+    e->n_ev += 2;
+    dpuf_hip_event_record(e->ev[i], e->stream);
+    return i;
 }
 
-static void tm_end(Engine* e) {
-    if (!e->timing || e->n_ev + 2 > MAX_EVENTS) return;
-    dpuf_hip_event_record(e->ev[e->n_ev + 1], e->stream);
-    e->n_ev += 2;
+static void tm_end(Engine* e, int i) {
+    if (i < 0) return;
+    dpuf_hip_event_record(e->ev[i + 1], e->stream);
 }
 
 static void tm_collect(Engine* e) {
@@ -522,9 +528,9 @@ static void enqueue_forward(Engine* e, int32_t M, int32_t use_embeds, int32_t on
             const int32_t np = qi[3];
             const uint8_t* ps[3] = {NULL, NULL, NULL};
             for (int k = 2; k >= 0; k--) ps[qi[k]] = signs[k];
-            tm_begin(e, K_PREP, 0);
+            const int tm1 = tm_begin(e, K_PREP, 0);
             dpuf_hip_resnorm_prep(s, M, H, e->h, l > 0 ? e->hn : NULL, e->d_norm[4 * l], eps, np, ps, e->prep, NULL);
-            tm_end(e);
+            tm_end(e, tm1);
         }
         /* (2) Q, K, V in one launch */
         {
@@ -535,33 +541,33 @@ static void enqueue_forward(Engine* e, int32_t M, int32_t use_embeds, int32_t on
             };
             double b = gemv_bytes(&W[W_Q], 0, W[W_Q].n_tiles, M) + gemv_bytes(&W[W_K], 0, W[W_K].n_tiles, M) +
                        gemv_bytes(&W[W_V], 0, W[W_V].n_tiles, M);
-            tm_begin(e, K_QKV, b);
+            const int tm2 = tm_begin(e, K_QKV, b);
             dpuf_hip_gemv(s, M, 3, js, NULL, 0.0f);
-            tm_end(e);
+            tm_end(e, tm2);
         }
         /* (3) QK-norm + RoPE + KV store, (4) attention */
-        tm_begin(e, K_ATTN, 0);
+        const int tm3 = tm_begin(e, K_ATTN, 0);
         dpuf_hip_qk_rope_kv(s, M, e->q, e->k, e->v, e->d_norm[4 * l + 1], e->d_norm[4 * l + 2], eps, e->d_cos,
                             e->d_sin, kc, vc, e->d_pos0, e->nq, e->nkv, e->hd, e->max_seq);
         dpuf_hip_attn(s, M, e->q, kc, vc, e->ao, e->scores, e->d_pos0, e->nq, e->nkv, e->hd, e->max_seq, scale);
-        tm_end(e);
+        tm_end(e, tm3);
         /* (5) O projection into hn */
-        tm_begin(e, K_PREP, 0);
+        const int tm4 = tm_begin(e, K_PREP, 0);
         dpuf_hip_prep(s, M, e->qd, e->ao, W[W_O].sign, e->prep[0]);
-        tm_end(e);
+        tm_end(e, tm4);
         {
             DpufGemvJob j = job(&W[W_O], 0, W[W_O].n_tiles, e->prep[0], e->hn, H);
-            tm_begin(e, K_O, gemv_bytes(&W[W_O], 0, W[W_O].n_tiles, M));
+            const int tm5 = tm_begin(e, K_O, gemv_bytes(&W[W_O], 0, W[W_O].n_tiles, M));
             dpuf_hip_gemv(s, M, 1, &j, NULL, 0.0f);
-            tm_end(e);
+            tm_end(e, tm5);
         }
         /* (6) h += O; FFN RMSNorm; prep of gate/up input */
         {
             int32_t np = qi[4] ? 2 : 1;
             const uint8_t* ps[2] = {W[W_GATE].sign, W[W_UP].sign};
-            tm_begin(e, K_PREP, 0);
+            const int tm6 = tm_begin(e, K_PREP, 0);
             dpuf_hip_resnorm_prep(s, M, H, e->h, e->hn, e->d_norm[4 * l + 3], eps, np, ps, e->prep, NULL);
-            tm_end(e);
+            tm_end(e, tm6);
         }
         /* (7) gate + up in one launch */
         {
@@ -570,23 +576,23 @@ static void enqueue_forward(Engine* e, int32_t M, int32_t use_embeds, int32_t on
                 job(&W[W_UP], 0, W[W_UP].n_tiles, e->prep[qi[4]], e->up, I),
             };
             double b = gemv_bytes(&W[W_GATE], 0, W[W_GATE].n_tiles, M) + gemv_bytes(&W[W_UP], 0, W[W_UP].n_tiles, M);
-            tm_begin(e, K_GU, b);
+            const int tm7 = tm_begin(e, K_GU, b);
             dpuf_hip_gemv(s, M, 2, js, NULL, 0.0f);
-            tm_end(e);
+            tm_end(e, tm7);
         }
         /* (8) SwiGLU + dead zone + prep of the down input */
-        tm_begin(e, K_PREP, 0);
+        const int tm8 = tm_begin(e, K_PREP, 0);
         dpuf_hip_swiglu_prep(s, M, I, e->gate, e->up, e->deadzone, W[W_DOWN].sign, e->prep[0]);
-        tm_end(e);
+        tm_end(e, tm8);
         /* (9) down projection, pruned to keep_tiles with the rest zeroed
          * (dpuf_engine.c:2018-2044) */
         {
             int32_t nt = W[W_DOWN].n_tiles;
             int32_t kt = (keep_tiles > 0 && keep_tiles < nt) ? keep_tiles : nt;
             DpufGemvJob j = job(&W[W_DOWN], 0, kt, e->prep[0], e->hn, H);
-            tm_begin(e, K_DOWN, gemv_bytes(&W[W_DOWN], 0, kt, M));
+            const int tm9 = tm_begin(e, K_DOWN, gemv_bytes(&W[W_DOWN], 0, kt, M));
             dpuf_hip_gemv(s, M, 1, &j, NULL, 0.0f);
-            tm_end(e);
+            tm_end(e, tm9);
             if (kt < nt) dpuf_hip_zero_rows(s, M, e->hn, H, kt * 16, W[W_DOWN].rows);
         }
         if (e->capture && M <= e->capture_cap)
@@ -597,10 +603,10 @@ static void enqueue_forward(Engine* e, int32_t M, int32_t use_embeds, int32_t on
     const int32_t lm0 = only_last ? M - 1 : 0, lmM = M - lm0;
     {
         const uint8_t* ps[1] = {e->lm.sign};
-        tm_begin(e, K_PREP, 0);
+        const int tm10 = tm_begin(e, K_PREP, 0);
         dpuf_hip_resnorm_prep(s, lmM, H, e->h + (size_t)lm0 * H, e->L > 0 ? e->hn + (size_t)lm0 * H : NULL,
                               e->d_out_norm, eps, 1, ps, e->prep, NULL);
-        tm_end(e);
+        tm_end(e, tm10);
     }
     const int32_t nt = e->lm.n_tiles;
     if (early_tiles > 0 && lmM == 1 && nt > 2048) {
@@ -611,19 +617,19 @@ static void enqueue_forward(Engine* e, int32_t M, int32_t use_embeds, int32_t on
         if (za > nt) za = nt;
         int32_t nz = za * 16 < e->V ? za * 16 : e->V;
         DpufGemvJob j0 = job(&e->lm, 0, za, e->prep[0], e->logits, e->V);
-        tm_begin(e, K_LM, gemv_bytes(&e->lm, 0, za, 1));
+        const int tm11 = tm_begin(e, K_LM, gemv_bytes(&e->lm, 0, za, 1));
         dpuf_hip_gemv(s, 1, 1, &j0, NULL, 0.0f);
         dpuf_hip_topcheck(s, e->logits, nz, early_margin, e->d_flag);
         if (za < nt) {
             DpufGemvJob j1 = job(&e->lm, za, nt, e->prep[0], e->logits, e->V);
             dpuf_hip_gemv(s, 1, 1, &j1, e->d_flag, -1e9f);
         }
-        tm_end(e);
+        tm_end(e, tm11);
     } else {
         DpufGemvJob j = job(&e->lm, 0, nt, e->prep[0], e->logits, e->V);
-        tm_begin(e, K_LM, gemv_bytes(&e->lm, 0, nt, lmM));
+        const int tm12 = tm_begin(e, K_LM, gemv_bytes(&e->lm, 0, nt, lmM));
         dpuf_hip_gemv(s, lmM, 1, &j, NULL, 0.0f);
-        tm_end(e);
+        tm_end(e, tm12);
         dpuf_hip_fill_zero(e->d_flag, 4, s);
     }
     if (want_argmax) dpuf_hip_argmax(s, e->logits + (size_t)(lmM - 1) * e->V, e->V, e->d_tok);
@@ -663,7 +669,7 @@ static int32_t forward_common(Engine* e, int32_t n_tokens, const int32_t* token_
     dpuf_hip_h2d(e->d_pos0, hp, 4, e->stream);
     if (embeds_in) dpuf_hip_h2d(e->embeds, embeds_in, (size_t)M * e->H * 4, e->stream);
 
-    tm_begin(e, K_CALL, (double)e->weight_bytes);
+    const int tm13 = tm_begin(e, K_CALL, (double)e->weight_bytes);
     const int graphable = use_graph && M == 1 && !e->timing && !embeds_in && !e->capture;
     if (graphable) {
         int32_t key[5] = {only_last, keep, early, e->active, 0};
@@ -684,7 +690,7 @@ static int32_t forward_common(Engine* e, int32_t n_tokens, const int32_t* token_
     } else {
         enqueue_forward(e, M, embeds_in != NULL, only_last, keep, early, margin, token_out != NULL);
     }
-    tm_end(e);
+    tm_end(e, tm13);
     if (only_last != 2) {
         const int32_t rows = only_last ? 1 : M;
         if (logits_out) dpuf_hip_d2h(logits_out, e->logits, (size_t)rows * e->V * 4, e->stream);
