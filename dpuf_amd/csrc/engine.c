@@ -287,6 +287,7 @@ DPUF_EXPORT void* dpuf_engine_create(const DpufModelConfig* cfg, const DpufLayer
         cfg->head_dim > 256 || cfg->num_kv_heads <= 0 || cfg->num_q_heads <= 0 ||
         (cfg->num_q_heads % cfg->num_kv_heads) != 0 || cfg->max_seq_len <= 0 || cfg->vocab_size <= 0 ||
         cfg->kv_type != DPUF_KV_F32 || cfg->has_mrope || (cfg->hidden_size % 64) != 0 ||
+        cfg->hidden_size < 128 || cfg->hidden_size > 16384 ||
         (cfg->intermediate_size % 64) != 0)
         return NULL;
     if (dpuf_hip_device_count() <= 0) return NULL;

@@ -19,6 +19,8 @@
 
 #define DEV __device__ __forceinline__
 
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
 // ---------------------------------------------------------------------------
 // Error bookkeeping
 // ---------------------------------------------------------------------------
@@ -132,78 +134,6 @@ DEV void fwht64(float* y) {
     for (int i = 0; i < 64; i++) y[i] = y[i] * 0.125f;
 }
 
-// Quantises 32 FWHT'd values like dpuf_prep_had4_packed_slab
-// (dpuf_avx2.c:2400-2446): returns the scale, writes 8 packed int8 words and
-// 8 * sum(q).
-DEV float quant32(const float* f, uint32_t* qw, int32_t* sum8) {
-    float amax = 0.0f;
-#pragma unroll
-    for (int k = 0; k < 32; k++) {
-        float a = fabsf(f[k]);
-        amax = a > amax ? a : amax;
-    }
-    if (amax <= 1e-4f) {
-#pragma unroll
-        for (int g = 0; g < 8; g++) qw[g] = 0u;
-        *sum8 = 0;
-        return 0.0f;
-    }
-    float d = amax / 127.0f;
-    float inv = (amax > 1e-12f) ? (127.0f / amax) : 0.0f;
-    int32_t s = 0;
-#pragma unroll
-    for (int g = 0; g < 8; g++) {
-        uint32_t w = 0;
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            float v = f[4 * g + k] * inv;
-            int32_t qi;
-            if (!(v > -2147483648.0f && v < 2147483648.0f)) qi = -127;  // cvtps -> INT_MIN -> -127
-            else qi = (int32_t)rintf(v);
-            qi = qi > 127 ? 127 : qi;
-            qi = qi < -127 ? -127 : qi;
-            s += qi;
-            w |= ((uint32_t)(qi & 0xFF)) << (8 * k);
-        }
-        qw[g] = w;
-    }
-    *sum8 = s * 8;
-    return d;
-}
-
-// sign (.) x then FWHT-64 then quantisation of the two 32-blocks of one
-// 64-column block `blk` (reference dpuf_prep_had4_packed_slab).
-DEV void prep_block64(const float* x, const uint8_t* sign, int blk, int8_t* q, float* s, int32_t* m) {
-    float v[64];
-    const float4* x4 = (const float4*)(x + 64 * blk);
-#pragma unroll
-    for (int i = 0; i < 16; i++) {
-        float4 t = x4[i];
-        v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
-    }
-    if (sign) {
-#pragma unroll
-        for (int bb = 0; bb < 8; bb++) {
-            uint32_t sb = sign[8 * blk + bb];
-#pragma unroll
-            for (int k = 0; k < 8; k++)
-                if ((sb >> k) & 1u) v[8 * bb + k] = -v[8 * bb + k];
-        }
-    }
-    fwht64(v);
-#pragma unroll
-    for (int hb = 0; hb < 2; hb++) {
-        uint32_t qw[8];
-        int32_t sum8;
-        float d = quant32(v + 32 * hb, qw, &sum8);
-        uint4* qo = (uint4*)(q + 64 * blk + 32 * hb);
-        qo[0] = make_uint4(qw[0], qw[1], qw[2], qw[3]);
-        qo[1] = make_uint4(qw[4], qw[5], qw[6], qw[7]);
-        s[2 * blk + hb] = d;
-        m[2 * blk + hb] = sum8;
-    }
-}
-
 // DPP quad permutations: xor 1 = (1,0,3,2), xor 2 = (2,3,0,1).
 DEV int dpp_xor1(int v) { return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false); }
 DEV int dpp_xor2(int v) { return __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false); }
@@ -260,9 +190,16 @@ __global__ void k_embed(DpufDevW w, const int32_t* __restrict__ ids, const float
 }
 
 // ---------------------------------------------------------------------------
-// Residual add + RMSNorm + activation prep for up to three sign vectors
-// (reference add_and_rms_norm_f32 dpuf_engine.c:243-272 and
-// dpuf_prep_had4_packed_slab).  grid: M rows, 256 threads, LDS = H floats.
+// Activation prep spread over lane quads.
+//
+// A 64-column block is owned by 4 consecutive lanes (a quad); quarter qp
+// holds columns 16*qp .. 16*qp+15 in registers.  FWHT stages with strides
+// 1, 2, 4, 8 run inside the lane, stride 16 pairs lanes qp and qp^1, stride
+// 32 pairs qp and qp^2 (DPP quad permutes).  Every butterfly is the same
+// single a+b / a-b as in the reference (dpuf_avx2.c:724-772) and the stages
+// keep its ascending order, so results are bit-identical.  Lanes (0,1) and
+// (2,3) of a quad then quantise one 32-block each
+// (dpuf_prep_had4_packed_slab, dpuf_avx2.c:2400-2446).
 // ---------------------------------------------------------------------------
 struct PrepSet {
     const uint8_t* sign[3];
@@ -270,101 +207,199 @@ struct PrepSet {
     int n;
 };
 
-__global__ __launch_bounds__(256) void k_resnorm_prep(int H, float* __restrict__ h, const float* __restrict__ res,
-                                                      const float* __restrict__ w, float eps, PrepSet ps,
-                                                      float* __restrict__ xn_out) {
-    extern __shared__ float sx[];
-    __shared__ float part[8];
-    __shared__ float inv_sh;
-    const int m = blockIdx.x;
-    float* hr = h + (size_t)m * H;
-    for (int i = threadIdx.x; i < H; i += blockDim.x) {
-        float v = hr[i];
-        if (res) {
-            v = v + res[(size_t)m * H + i];
-            hr[i] = v;
+DEV float fxor1(float v) { return __int_as_float(dpp_xor1(__float_as_int(v))); }
+DEV float fxor2(float v) { return __int_as_float(dpp_xor2(__float_as_int(v))); }
+
+// sign (.) x for the lane's 16 columns (bit c%8 of byte c/8 set = negate).
+DEV void quad_sign(float* v, const uint8_t* sign, int blk, int qp) {
+    if (!sign) return;
+    const uint32_t sb = *(const uint16_t*)(sign + 8 * blk + 2 * qp);
+#pragma unroll
+    for (int k = 0; k < 16; k++)
+        if ((sb >> k) & 1u) v[k] = -v[k];
+}
+
+DEV void quad_fwht64(float* v, int qp) {
+#pragma unroll
+    for (int h = 1; h < 16; h <<= 1) {
+#pragma unroll
+        for (int i = 0; i < 16; i += 2 * h) {
+#pragma unroll
+            for (int j = i; j < i + h; j++) {
+                const float a = v[j], b = v[j + h];
+                v[j] = a + b;
+                v[j + h] = a - b;
+            }
         }
-        sx[i] = v;
     }
-    __syncthreads();
-    if (threadIdx.x < 8) {
-        // lane j of the reference's 8-wide FMA accumulator: elements j, j+8, ...
-        float a = 0.0f;
-        for (int i = threadIdx.x; i < H; i += 8) a = fmaf(sx[i], sx[i], a);
-        part[threadIdx.x] = a;
+    const bool lo1 = (qp & 1) == 0, lo2 = (qp & 2) == 0;
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+        const float p = fxor1(v[j]);
+        v[j] = lo1 ? v[j] + p : p - v[j];
     }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        float ss = hsum8(part);
-        inv_sh = 1.0f / sqrtf(ss / (float)H + eps);
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+        const float p = fxor2(v[j]);
+        v[j] = lo2 ? v[j] + p : p - v[j];
     }
-    __syncthreads();
-    const float inv = inv_sh;
-    for (int i = threadIdx.x; i < H; i += blockDim.x) {
-        float v = (sx[i] * inv) * w[i];
-        sx[i] = v;
-        if (xn_out) xn_out[(size_t)m * H + i] = v;
+#pragma unroll
+    for (int j = 0; j < 16; j++) v[j] = v[j] * 0.125f;
+}
+
+// Quantises the lane's 16 FWHT'd values (half of 32-block 2*blk + qp/2) and
+// stores the int8 values, and from the even lane the block scale and 8*sum(q).
+DEV void quad_quant_store(const float* v, int qp, int blk, int8_t* q, float* s, int32_t* m) {
+    float amax = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+        const float a = fabsf(v[k]);
+        amax = a > amax ? a : amax;
     }
-    __syncthreads();
-    const int nb = H >> 5;
-    for (int p = 0; p < ps.n; p++) {
-        for (int blk = threadIdx.x; blk < (H >> 6); blk += blockDim.x)
-            prep_block64(sx, ps.sign[p], blk, ps.p[p].q + (size_t)m * H, ps.p[p].s + (size_t)m * nb,
-                         ps.p[p].m + (size_t)m * nb);
+    const float other = fxor1(amax);
+    amax = other > amax ? other : amax;
+    uint32_t w[4] = {0u, 0u, 0u, 0u};
+    int32_t sum = 0;
+    float d = 0.0f;
+    if (!(amax <= 1e-4f)) {
+        d = amax / 127.0f;
+        const float inv = (amax > 1e-12f) ? (127.0f / amax) : 0.0f;
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const float x = v[4 * g + k] * inv;
+                int32_t qi;
+                if (!(x > -2147483648.0f && x < 2147483648.0f)) qi = -127;  // cvtps -> INT_MIN -> -127
+                else qi = (int32_t)rintf(x);
+                qi = qi > 127 ? 127 : qi;
+                qi = qi < -127 ? -127 : qi;
+                sum += qi;
+                w[g] |= ((uint32_t)(qi & 0xFF)) << (8 * k);
+            }
+        }
+    }
+    sum += dpp_xor1(sum);
+    *(uint4*)(q + 64 * blk + 16 * qp) = make_uint4(w[0], w[1], w[2], w[3]);
+    if ((qp & 1) == 0) {
+        s[2 * blk + (qp >> 1)] = d;
+        m[2 * blk + (qp >> 1)] = sum * 8;
     }
 }
 
-// Plain activation prep of M rows of x [M][K].
-__global__ void k_prep(int K, const float* __restrict__ x, const uint8_t* __restrict__ sign, DpufPrep p) {
-    const int m = blockIdx.x, nb = K >> 5;
-    for (int blk = threadIdx.x; blk < (K >> 6); blk += blockDim.x)
-        prep_block64(x + (size_t)m * K, sign, blk, p.q + (size_t)m * K, p.s + (size_t)m * nb, p.m + (size_t)m * nb);
+DEV void load16(const float* p, float* v) {
+    const float4* p4 = (const float4*)p;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float4 t = p4[i];
+        v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
+    }
+}
+
+DEV void store16(float* p, const float* v) {
+    float4* p4 = (float4*)p;
+#pragma unroll
+    for (int i = 0; i < 4; i++) p4[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+}
+
+// ---------------------------------------------------------------------------
+// Residual add + RMSNorm + prep for up to three sign vectors (reference
+// add_and_rms_norm_f32, dpuf_engine.c:243-272, then the prep above).
+// grid: M rows; block: H/16 threads, thread t owning columns 16t..16t+15.
+// The sum of squares keeps the reference's 8 FMA lanes (lane j accumulates
+// elements j, j+8, j+16, ... in order) and its hsum tree; a transposed LDS
+// copy gives each of the 8 chain lanes its elements contiguously.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(1024) void k_resnorm_prep(int H, float* __restrict__ h, const float* __restrict__ res,
+                                                       const float* __restrict__ w, float eps, PrepSet ps,
+                                                       float* __restrict__ xn_out) {
+    extern __shared__ float tr[];  // [8][H/8 + 4]
+    __shared__ float part[8];
+    const int m = blockIdx.x, t = threadIdx.x, qp = t & 3, blk = t >> 2, nb = H >> 5;
+    const int L = (H >> 3) + 4;
+    float v[16];
+    float* hr = h + (size_t)m * H + 16 * t;
+    load16(hr, v);
+    if (res) {
+        float r[16];
+        load16(res + (size_t)m * H + 16 * t, r);
+#pragma unroll
+        for (int k = 0; k < 16; k++) v[k] = v[k] + r[k];
+        store16(hr, v);
+    }
+#pragma unroll
+    for (int k = 0; k < 8; k++) *(float2*)(tr + k * L + 2 * t) = make_float2(v[k], v[k + 8]);
+    __syncthreads();
+    if (t < 8) {
+        const float4* row = (const float4*)(tr + t * L);
+        const int n4 = H >> 5;
+        float a = 0.0f;
+        int i = 0;
+        for (; i + 4 <= n4; i += 4) {
+            const float4 e0 = row[i], e1 = row[i + 1], e2 = row[i + 2], e3 = row[i + 3];
+            a = fmaf(e0.x, e0.x, a); a = fmaf(e0.y, e0.y, a); a = fmaf(e0.z, e0.z, a); a = fmaf(e0.w, e0.w, a);
+            a = fmaf(e1.x, e1.x, a); a = fmaf(e1.y, e1.y, a); a = fmaf(e1.z, e1.z, a); a = fmaf(e1.w, e1.w, a);
+            a = fmaf(e2.x, e2.x, a); a = fmaf(e2.y, e2.y, a); a = fmaf(e2.z, e2.z, a); a = fmaf(e2.w, e2.w, a);
+            a = fmaf(e3.x, e3.x, a); a = fmaf(e3.y, e3.y, a); a = fmaf(e3.z, e3.z, a); a = fmaf(e3.w, e3.w, a);
+        }
+        for (; i < n4; i++) {
+            const float4 e = row[i];
+            a = fmaf(e.x, e.x, a); a = fmaf(e.y, e.y, a); a = fmaf(e.z, e.z, a); a = fmaf(e.w, e.w, a);
+        }
+        part[t] = a;
+    }
+    __syncthreads();
+    const float inv = 1.0f / sqrtf(hsum8(part) / (float)H + eps);
+    float wv[16];
+    load16(w + 16 * t, wv);
+#pragma unroll
+    for (int k = 0; k < 16; k++) v[k] = (v[k] * inv) * wv[k];
+    if (xn_out) store16(xn_out + (size_t)m * H + 16 * t, v);
+    for (int p = 0; p < ps.n; p++) {
+        float y[16];
+#pragma unroll
+        for (int k = 0; k < 16; k++) y[k] = v[k];
+        quad_sign(y, ps.sign[p], blk, qp);
+        quad_fwht64(y, qp);
+        quad_quant_store(y, qp, blk, ps.p[p].q + (size_t)m * H, ps.p[p].s + (size_t)m * nb, ps.p[p].m + (size_t)m * nb);
+    }
+}
+
+// Plain activation prep of M rows of x [M][K].  grid: (ceil(K/16/256), M).
+__global__ __launch_bounds__(256) void k_prep(int K, const float* __restrict__ x, const uint8_t* __restrict__ sign,
+                                              DpufPrep p) {
+    const int m = blockIdx.y, t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (16 * t >= K) return;  // whole quads: K is a multiple of 64
+    const int qp = t & 3, blk = t >> 2, nb = K >> 5;
+    float v[16];
+    load16(x + (size_t)m * K + 16 * t, v);
+    quad_sign(v, sign, blk, qp);
+    quad_fwht64(v, qp);
+    quad_quant_store(v, qp, blk, p.q + (size_t)m * K, p.s + (size_t)m * nb, p.m + (size_t)m * nb);
 }
 
 // SwiGLU with dead zone (reference swiglu_range_avx2, 8-wide path,
 // dpuf_engine.c:976-989) fused with the prep of the down projection's input.
-__global__ void k_swiglu_prep(int I, const float* __restrict__ gate, const float* __restrict__ up, float dz,
-                              const uint8_t* __restrict__ sign, DpufPrep p) {
-    const int m = blockIdx.x, nb = I >> 5;
-    for (int blk = threadIdx.x; blk < (I >> 6); blk += blockDim.x) {
-        float v[64];
-        const float4* g4 = (const float4*)(gate + (size_t)m * I + 64 * blk);
-        const float4* u4 = (const float4*)(up + (size_t)m * I + 64 * blk);
+// grid: (ceil(I/16/256), M).
+__global__ __launch_bounds__(256) void k_swiglu_prep(int I, const float* __restrict__ gate, const float* __restrict__ up,
+                                                     float dz, const uint8_t* __restrict__ sign, DpufPrep p) {
+    const int m = blockIdx.y, t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (16 * t >= I) return;
+    const int qp = t & 3, blk = t >> 2, nb = I >> 5;
+    float g[16], u[16], v[16];
+    load16(gate + (size_t)m * I + 16 * t, g);
+    load16(up + (size_t)m * I + 16 * t, u);
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const float4 g = g4[i], u = u4[i];
-            const float gg[4] = {g.x, g.y, g.z, g.w}, uu[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                float ng = fmaxf(-40.0f, fminf(0.0f - gg[k], 40.0f));
-                float silu = gg[k] / (1.0f + exp_poly(ng));
-                float r = silu * uu[k];
-                if (dz > 0.0f && !(fabsf(r) >= dz)) r = 0.0f;
-                v[4 * i + k] = r;
-            }
-        }
-        if (sign) {
-#pragma unroll
-            for (int bb = 0; bb < 8; bb++) {
-                const uint32_t sb = sign[8 * blk + bb];
-#pragma unroll
-                for (int k = 0; k < 8; k++)
-                    if ((sb >> k) & 1u) v[8 * bb + k] = -v[8 * bb + k];
-            }
-        }
-        fwht64(v);
-#pragma unroll
-        for (int hb = 0; hb < 2; hb++) {
-            uint32_t qw[8];
-            int32_t sum8;
-            float d = quant32(v + 32 * hb, qw, &sum8);
-            uint4* qo = (uint4*)(p.q + (size_t)m * I + 64 * blk + 32 * hb);
-            qo[0] = make_uint4(qw[0], qw[1], qw[2], qw[3]);
-            qo[1] = make_uint4(qw[4], qw[5], qw[6], qw[7]);
-            p.s[(size_t)m * nb + 2 * blk + hb] = d;
-            p.m[(size_t)m * nb + 2 * blk + hb] = sum8;
-        }
+    for (int k = 0; k < 16; k++) {
+        const float ng = fmaxf(-40.0f, fminf(0.0f - g[k], 40.0f));
+        const float silu = g[k] / (1.0f + exp_poly(ng));
+        float r = silu * u[k];
+        if (dz > 0.0f && !(fabsf(r) >= dz)) r = 0.0f;
+        v[k] = r;
     }
+    quad_sign(v, sign, blk, qp);
+    quad_fwht64(v, qp);
+    quad_quant_store(v, qp, blk, p.q + (size_t)m * I, p.s + (size_t)m * nb, p.m + (size_t)m * nb);
 }
 
 // ---------------------------------------------------------------------------
@@ -474,6 +509,103 @@ __global__ __launch_bounds__(64) void k_gemv1(GemvBatch B, const int32_t* __rest
         __syncthreads();
     }
     if (lane < n8) J.out[r0 + lane] = acc;
+}
+
+// M == 1 decode GEMV, one 8-row group per workgroup of 4 waves.
+//
+// The group's K blocks are split over the 4 waves in steps of 8 blocks (1 KB
+// of nibbles per wave-wide 16-byte load).  Each wave first issues ALL of its
+// nibble and scale loads (NL steps in flight per lane, so a workgroup keeps
+// up to 4 * NL KB of weights in flight), then forms the exact integer dots.
+// The (float(D - sum8), ws * xs) pairs land in LDS as [row][block]; after one
+// barrier lanes 0..7 run the per-row fp32 FMA chains in ascending block order
+// (dpuf_avx2.c:2620-2636), reading two pairs per 16-byte LDS load.  The row
+// stride n_blk + 2 keeps those 8 lanes on distinct banks.
+template <int NL>
+__global__ __launch_bounds__(256) void k_gemv1w(GemvBatch B, const int32_t* __restrict__ skip_flag, float fill) {
+    extern __shared__ float2 pairs[];
+    const int ji = find_job(B, blockIdx.x);
+    const DpufGemvJob& J = B.j[ji];
+    const uint8_t* grp;
+    int r0, n8;
+    if (!group_of(J, blockIdx.x - B.g_begin[ji], grp, r0, n8)) return;
+    const int tid = threadIdx.x;
+    if (skip_flag && *skip_flag) {
+        if (tid < n8) J.out[r0 + tid] = fill;
+        return;
+    }
+    const int n_blk = J.w.cols >> 5, S = (n_blk + 7) >> 3, ld = n_blk + 2;
+    const int w = tid >> 6, lane = tid & 63;
+    const int bi = lane >> 3, h = (lane >> 2) & 1, c = lane & 3, rr = 4 * h + c;
+    const uint16_t* sc = (const uint16_t*)grp;
+    const uint8_t* qg = grp + (size_t)n_blk * 16;
+    for (int base = 0; base < S; base += 4 * NL) {
+        const int s0 = base + w * NL;
+        // every load of this pass (weights, scales and the matching
+        // activations) is issued before the first one is consumed
+        uint4 wq[NL];
+        int2 xw[NL];
+        float xs[NL];
+        int32_t xm[NL];
+        uint32_t wsr[NL];
+#pragma unroll
+        for (int i = 0; i < NL; i++) {
+            const int s = s0 + i, b = s * 8 + bi;
+            if (s < S && b < n_blk) {
+                const u32x4 v = __builtin_nontemporal_load((const u32x4*)(qg + (size_t)b * 128 + c * 32 + h * 16));
+                wq[i] = make_uint4(v.x, v.y, v.z, v.w);
+                wsr[i] = sc[(size_t)b * 8 + rr];
+                xw[i] = *(const int2*)(J.p.q + b * 32 + c * 8);
+                xs[i] = J.p.s[b];
+                xm[i] = J.p.m[b];
+            } else {
+                wq[i] = make_uint4(0u, 0u, 0u, 0u);
+                wsr[i] = 0u;
+                xw[i] = make_int2(0, 0);
+                xs[i] = 0.0f;
+                xm[i] = 0;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < NL; i++) {
+            const int s = s0 + i;
+            if (s >= S) break;  // wave-uniform
+            const int b = s * 8 + bi;
+            const int dot = lane_row_dot(wq[i], xw[i], c);
+            if (b < n_blk) {
+                float dcf = 0.0f, sp = 0.0f;
+                if (xs[i] > 0.0f) {
+                    dcf = (float)(dot - xm[i]);
+                    sp = h2f((uint16_t)wsr[i]) * xs[i];
+                }
+                pairs[rr * ld + b] = make_float2(dcf, sp);
+            }
+        }
+    }
+    __syncthreads();
+    if (tid < 8) {
+        const float4* row = (const float4*)(pairs + tid * ld);
+        float acc = 0.0f;
+        const int n2 = n_blk >> 1;
+        int k = 0;
+        for (; k + 4 <= n2; k += 4) {
+            const float4 e0 = row[k], e1 = row[k + 1], e2 = row[k + 2], e3 = row[k + 3];
+            acc = fmaf(e0.x, e0.y, acc);
+            acc = fmaf(e0.z, e0.w, acc);
+            acc = fmaf(e1.x, e1.y, acc);
+            acc = fmaf(e1.z, e1.w, acc);
+            acc = fmaf(e2.x, e2.y, acc);
+            acc = fmaf(e2.z, e2.w, acc);
+            acc = fmaf(e3.x, e3.y, acc);
+            acc = fmaf(e3.z, e3.w, acc);
+        }
+        for (; k < n2; k++) {
+            const float4 e = row[k];
+            acc = fmaf(e.x, e.y, acc);
+            acc = fmaf(e.z, e.w, acc);
+        }
+        if (tid < n8) J.out[r0 + tid] = acc;
+    }
 }
 
 __global__ __launch_bounds__(64) void k_gemm8(GemvBatch B, int M) {
@@ -979,23 +1111,22 @@ void dpuf_hip_resnorm_prep(void* s, int32_t M, int32_t H, float* h, const float*
         ps.sign[i] = signs[i];
         ps.p[i] = preps[i];
     }
-    hipLaunchKernelGGL(k_resnorm_prep, dim3(M), dim3(256), (size_t)H * sizeof(float), ST(s), H, h, res, w, eps, ps,
-                       xn_out);
+    const int threads = H / 16;  // H is a multiple of 1024 or 64 * 16 * k; checked at engine create
+    const size_t lds = (size_t)8 * ((H >> 3) + 4) * sizeof(float);
+    hipLaunchKernelGGL(k_resnorm_prep, dim3(M), dim3(threads), lds, ST(s), H, h, res, w, eps, ps, xn_out);
     LAUNCHED("k_resnorm_prep");
 }
 
 void dpuf_hip_prep(void* s, int32_t M, int32_t K, const float* x, const uint8_t* sign, DpufPrep p) {
-    int threads = (K >> 6) < 256 ? (K >> 6) : 256;
-    threads = (threads + 63) & ~63;
-    hipLaunchKernelGGL(k_prep, dim3(M), dim3(threads), 0, ST(s), K, x, sign, p);
+    const int quads = K / 16;
+    hipLaunchKernelGGL(k_prep, dim3((quads + 255) / 256, M), dim3(256), 0, ST(s), K, x, sign, p);
     LAUNCHED("k_prep");
 }
 
 void dpuf_hip_swiglu_prep(void* s, int32_t M, int32_t I, const float* gate, const float* up, float dz,
                           const uint8_t* sign, DpufPrep p) {
-    int threads = (I >> 6) < 256 ? (I >> 6) : 256;
-    threads = (threads + 63) & ~63;
-    hipLaunchKernelGGL(k_swiglu_prep, dim3(M), dim3(threads), 0, ST(s), I, gate, up, dz, sign, p);
+    const int quads = I / 16;
+    hipLaunchKernelGGL(k_swiglu_prep, dim3((quads + 255) / 256, M), dim3(256), 0, ST(s), I, gate, up, dz, sign, p);
     LAUNCHED("k_swiglu_prep");
 }
 
@@ -1013,8 +1144,15 @@ void dpuf_hip_gemv(void* s, int32_t M, int32_t n_jobs, const DpufGemvJob* jobs, 
     B.g_begin[n_jobs] = g;
     if (g <= 0) return;
     if (M == 1) {
-        hipLaunchKernelGGL(k_gemv1, dim3(g), dim3(64), 0, ST(s), B, skip_flag, fill);
-        LAUNCHED("k_gemv1");
+        int n_blk = 0;
+        for (int i = 0; i < n_jobs; i++) n_blk = jobs[i].w.cols / 32 > n_blk ? jobs[i].w.cols / 32 : n_blk;
+        const size_t lds = (size_t)8 * (n_blk + 2) * sizeof(float2);
+        if ((n_blk + 7) / 8 <= 16) {
+            hipLaunchKernelGGL(k_gemv1w<4>, dim3(g), dim3(256), lds, ST(s), B, skip_flag, fill);
+        } else {
+            hipLaunchKernelGGL(k_gemv1w<12>, dim3(g), dim3(256), lds, ST(s), B, skip_flag, fill);
+        }
+        LAUNCHED("k_gemv1w");
     } else {
         hipLaunchKernelGGL(k_gemm8, dim3(g, (M + 7) / 8), dim3(64), 0, ST(s), B, M);
         LAUNCHED("k_gemm8");
