@@ -546,16 +546,23 @@ static void enqueue_forward(Engine* e, int32_t M, int32_t use_embeds, int32_t on
             dpuf_hip_gemv(s, M, 3, js, NULL, 0.0f);
             tm_end(e, tm2);
         }
-        /* (3) QK-norm + RoPE + KV store, (4) attention */
-        const int tm3 = tm_begin(e, K_ATTN, 0);
-        dpuf_hip_qk_rope_kv(s, M, e->q, e->k, e->v, e->d_norm[4 * l + 1], e->d_norm[4 * l + 2], eps, e->d_cos,
-                            e->d_sin, kc, vc, e->d_pos0, e->nq, e->nkv, e->hd, e->max_seq);
-        dpuf_hip_attn(s, M, e->q, kc, vc, e->ao, e->scores, e->d_pos0, e->nq, e->nkv, e->hd, e->max_seq, scale);
-        tm_end(e, tm3);
-        /* (5) O projection into hn */
-        const int tm4 = tm_begin(e, K_PREP, 0);
-        dpuf_hip_prep(s, M, e->qd, e->ao, W[W_O].sign, e->prep[0]);
-        tm_end(e, tm4);
+        /* (3) QK-norm + RoPE + KV store, (4) attention, (5) prep of the O input */
+        {
+            const int tm = tm_begin(e, K_ATTN, 0);
+            int fused = 0;
+            if (M == 1)
+                fused = dpuf_hip_attn_dec(s, e->q, e->k, e->v, e->d_norm[4 * l + 1], e->d_norm[4 * l + 2], eps,
+                                          e->d_cos, e->d_sin, kc, vc, e->d_pos0, e->nq, e->nkv, e->hd, e->max_seq,
+                                          scale, e->scores, e->ao, W[W_O].sign, e->prep[0]) == 0;
+            if (!fused) {
+                dpuf_hip_qk_rope_kv(s, M, e->q, e->k, e->v, e->d_norm[4 * l + 1], e->d_norm[4 * l + 2], eps,
+                                    e->d_cos, e->d_sin, kc, vc, e->d_pos0, e->nq, e->nkv, e->hd, e->max_seq);
+                dpuf_hip_attn(s, M, e->q, kc, vc, e->ao, e->scores, e->d_pos0, e->nq, e->nkv, e->hd, e->max_seq,
+                              scale);
+                dpuf_hip_prep(s, M, e->qd, e->ao, W[W_O].sign, e->prep[0]);
+            }
+            tm_end(e, tm);
+        }
         {
             DpufGemvJob j = job(&W[W_O], 0, W[W_O].n_tiles, e->prep[0], e->hn, H);
             const int tm5 = tm_begin(e, K_O, gemv_bytes(&W[W_O], 0, W[W_O].n_tiles, M));

@@ -87,6 +87,12 @@ void dpuf_hip_qk_rope_kv(void* s, int32_t M, float* q, float* k, const float* v,
 void dpuf_hip_attn(void* s, int32_t M, const float* q, const float* kc, const float* vc, float* out,
                    float* scores, const int32_t* pos0, int32_t n_q, int32_t n_kv, int32_t hd,
                    int32_t max_seq, float scale);
+/* M == 1 fused QK-norm + RoPE + KV store + attention + O-input prep.
+ * Returns -1 (nothing launched) for head dims other than 64, 128, 256. */
+int32_t dpuf_hip_attn_dec(void* s, const float* q, const float* k, const float* v, const float* q_norm,
+                          const float* k_norm, float eps, const float* cos_tab, const float* sin_tab, float* kc,
+                          float* vc, const int32_t* pos0, int32_t n_q, int32_t n_kv, int32_t hd, int32_t max_seq,
+                          float scale, float* scores, float* ao, const uint8_t* o_sign, DpufPrep op);
 void dpuf_hip_zero_rows(void* s, int32_t M, float* out, int32_t ld, int32_t r0, int32_t r1);
 void dpuf_hip_capture(void* s, int32_t M, int32_t H, const float* h, const float* hn, float* cap);
 void dpuf_hip_topcheck(void* s, const float* logits, int32_t n, float thr, int32_t* flag);

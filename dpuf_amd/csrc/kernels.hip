@@ -850,6 +850,304 @@ __global__ __launch_bounds__(256) void k_attn(const float* __restrict__ q, const
 }
 
 // ---------------------------------------------------------------------------
+// Decode attention (M == 1), one workgroup (4 waves) per (kv head,
+// query-head pair): QK-norm + NeoX RoPE of the pair's queries and of the new
+// key, the KV-cache store of position pos (pair 0 only), causal attention
+// over [0, pos], and the prep of the O projection's input for the pair's
+// 2 * HD columns.
+//
+// Arithmetic follows gqa_attn_head_pair_f32 (dpuf_engine.c:341-577) term by
+// term: each score is 8 lane-accumulators (lane j: elements j, j+8, ... in
+// order) reduced by the reference's hadd / hsum tree (here a 3-step xor
+// butterfly whose adds are exactly the tree's), the exp polynomial with the
+// libm expf tail, the 8-lane softmax sum, and the per-output P.V FMA chains.
+//
+// Latency: the K rows of the first 128 positions are loaded into registers
+// (8 lanes per key, 16 floats each) and the first V_ROWS rows of V are copied
+// straight into LDS (global_load_lds, 1 KB per wave instruction) at kernel
+// entry, so both streams are in flight while the norms and RoPE run.
+// ---------------------------------------------------------------------------
+#define ATT_KEYS 128  // keys whose K rows are loaded per round (32 keys x 4 passes)
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+DEV float shx(float v, int m) { return __shfl_xor(v, m, 64); }
+
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_dec(const float* __restrict__ q, const float* __restrict__ k,
+                                                  const float* __restrict__ v, const float* __restrict__ qn,
+                                                  const float* __restrict__ kn, float eps,
+                                                  const float* __restrict__ cos_tab, const float* __restrict__ sin_tab,
+                                                  float* __restrict__ kc, float* __restrict__ vc,
+                                                  const int32_t* __restrict__ pos0p, int n_q, int n_kv, int max_seq,
+                                                  float scale, int sc_cap, float* __restrict__ scores_g,
+                                                  float* __restrict__ ao, const uint8_t* __restrict__ o_sign,
+                                                  DpufPrep op) {
+    constexpr int V_ROWS = 16384 / HD;  // 64 KB of V rows per LDS chunk
+    constexpr int NQ8 = HD / 8;         // elements per accumulator lane
+    constexpr int KP = ATT_KEYS / 32;
+    constexpr int half = HD / 2;
+    extern __shared__ float sm[];
+    float* vst = sm;                    // [V_ROWS][HD], 1 KB aligned
+    float* qs = vst + V_ROWS * HD;      // [2][HD]
+    float* ks = qs + 2 * HD;            // [HD]
+    float* vn = ks + HD;                // [HD]
+    float* aout = vn + HD;              // [2][HD]
+    float* scl = aout + 2 * HD;         // [max(2 * sc_cap, 3 * HD)]
+    __shared__ float part[3][8];
+    __shared__ float red[2][256];
+    __shared__ float vs8[2][8];
+    __shared__ float inv_sh[2];
+    const int kvh = blockIdx.x, gp = blockIdx.y, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int groups = n_q / n_kv, g0 = 2 * gp;
+    const bool pair = (g0 + 1 < groups);
+    const int nh = pair ? 2 : 1;
+    const int qh0 = kvh * groups + g0;
+    const int pos = *pos0p;
+    const int kv_len = pos + 1;
+    const float* Kc = kc + (size_t)kvh * max_seq * HD;
+    const float* Vc = vc + (size_t)kvh * max_seq * HD;
+
+    // V rows [c0, c0 + V_ROWS) -> vst, 1 KB per wave instruction; rows past
+    // the cache end are redirected to row 0 (never read back).
+    auto stage_v = [&](int c0) {
+        constexpr int n_ins = V_ROWS * HD / 256;
+        for (int ii = wave; ii < n_ins; ii += 4) {
+            const int e = ii * 256 + lane * 4;  // float index inside the chunk
+            int t = c0 + e / HD;
+            if (t >= max_seq) t = 0;
+            __builtin_amdgcn_global_load_lds((const void*)(Vc + (size_t)t * HD + (e % HD)),
+                                             (lds_ptr_t)(vst + ii * 256), 16, 0, 0);
+        }
+    };
+    if (pos > 0) stage_v(0);
+
+    // K rows of keys kq + 32p (p < KP): lane j holds elements j, j+8, ...
+    const int kq = tid >> 3, j = tid & 7;
+    float kr[KP][NQ8];
+    auto load_k = [&](int t0) {
+#pragma unroll
+        for (int p = 0; p < KP; p++) {
+            const int t = t0 + kq + 32 * p;
+            const bool ok = t < pos;
+#pragma unroll
+            for (int i = 0; i < NQ8; i++) kr[p][i] = ok ? Kc[(size_t)t * HD + j + 8 * i] : 0.0f;
+        }
+    };
+    load_k(0);
+
+    // stage the raw vectors: q0, q1, k, v
+    float* tmp = scl;  // [3][HD] normalised vectors, before the scores use this space
+    for (int i = tid; i < HD; i += 256) {
+        qs[i] = q[(size_t)qh0 * HD + i];
+        if (pair) qs[HD + i] = q[(size_t)(qh0 + 1) * HD + i];
+        ks[i] = k[(size_t)kvh * HD + i];
+        vn[i] = v[(size_t)kvh * HD + i];
+    }
+    __syncthreads();
+    // QK-norm (rms_norm_f32 over hd: 8 FMA lanes + hsum tree), vectors 0 = q0, 1 = q1, 2 = k
+    if (tid < 24) {
+        const int vi = tid >> 3, jj = tid & 7;
+        const float* vec = vi == 2 ? ks : qs + vi * HD;
+        const float* nw = vi == 2 ? kn : qn;
+        if ((vi != 1 || pair) && nw) {
+            float a = 0.0f;
+            for (int i = jj; i < HD; i += 8) a = fmaf(vec[i], vec[i], a);
+            part[vi][jj] = a;
+        }
+    }
+    __syncthreads();
+    for (int e = tid; e < 3 * HD; e += 256) {
+        const int vi = e / HD, i = e % HD;
+        if (vi == 1 && !pair) continue;
+        const float* vec = vi == 2 ? ks : qs + vi * HD;
+        const float* nw = vi == 2 ? kn : qn;
+        float x = vec[i];
+        if (nw) {
+            const float inv = 1.0f / sqrtf(hsum8(part[vi]) / (float)HD + eps);
+            x = (x * inv) * nw[i];
+        }
+        tmp[e] = x;
+    }
+    __syncthreads();
+    // NeoX RoPE (apply_rope_neox_f32, dpuf_engine.c:274-295)
+    const float* c_row = cos_tab + (size_t)pos * half;
+    const float* s_row = sin_tab + (size_t)pos * half;
+    for (int e = tid; e < 3 * HD; e += 256) {
+        const int vi = e / HD, i = e % HD;
+        if (vi == 1 && !pair) continue;
+        const float* x = tmp + vi * HD;
+        float o;
+        if (i < half) o = fmaf(x[i], c_row[i], -(x[i + half] * s_row[i]));
+        else o = fmaf(x[i], c_row[i - half], x[i - half] * s_row[i - half]);
+        if (vi == 2) ks[i] = o;
+        else qs[vi * HD + i] = o;
+    }
+    __syncthreads();
+    if (gp == 0) {
+        for (int i = tid; i < HD; i += 256) {
+            kc[((size_t)kvh * max_seq + pos) * HD + i] = ks[i];
+            vc[((size_t)kvh * max_seq + pos) * HD + i] = vn[i];
+        }
+    }
+
+    // scores
+    float* sc0 = kv_len <= sc_cap ? scl : scores_g + (size_t)qh0 * max_seq;
+    float* sc1 = kv_len <= sc_cap ? scl + sc_cap : sc0 + max_seq;
+    const int n4 = kv_len & ~3;
+    float qv0[NQ8], qv1[NQ8];
+#pragma unroll
+    for (int i = 0; i < NQ8; i++) {
+        qv0[i] = qs[j + 8 * i];
+        qv1[i] = pair ? qs[HD + j + 8 * i] : 0.0f;
+    }
+    float mx0 = -1e30f, mx1 = -1e30f;
+    for (int t0 = 0; t0 < kv_len; t0 += ATT_KEYS) {
+        if (t0 > 0) load_k(t0);
+#pragma unroll
+        for (int p = 0; p < KP; p++) {
+            const int t = t0 + kq + 32 * p;
+            if (t0 + 32 * p >= kv_len) break;  // uniform over the workgroup
+            float kv[NQ8];
+#pragma unroll
+            for (int i = 0; i < NQ8; i++) kv[i] = (t == pos) ? ks[j + 8 * i] : kr[p][i];
+            float s0, s1 = 0.0f;
+            if (pair || t < n4) {
+                // one accumulator lane per head: a_j = sum_i q[j+8i] k[j+8i] in order
+                float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+                for (int i = 0; i < NQ8; i++) {
+                    a0 = fmaf(qv0[i], kv[i], a0);
+                    a1 = fmaf(qv1[i], kv[i], a1);
+                }
+                if (t < n4) {  // hsum4_256_ps tree: ((a0+a1)+(a2+a3)) + ((a4+a5)+(a6+a7))
+                    a0 = a0 + shx(a0, 1); a1 = a1 + shx(a1, 1);
+                    a0 = a0 + shx(a0, 2); a1 = a1 + shx(a1, 2);
+                    a0 = a0 + shx(a0, 4); a1 = a1 + shx(a1, 4);
+                } else {       // eng_hsum256_ps tree: ((a0+a4)+(a1+a5)) + ((a2+a6)+(a3+a7))
+                    a0 = a0 + shx(a0, 4); a1 = a1 + shx(a1, 4);
+                    a0 = a0 + shx(a0, 1); a1 = a1 + shx(a1, 1);
+                    a0 = a0 + shx(a0, 2); a1 = a1 + shx(a1, 2);
+                }
+                s0 = a0 * scale;
+                s1 = a1 * scale;
+            } else {
+                // single-head tail: dot_f32_avx2's two interleaved accumulators
+                float a0 = 0.0f, b0 = 0.0f;
+#pragma unroll
+                for (int i = 0; i < NQ8; i += 2) {
+                    a0 = fmaf(qv0[i], kv[i], a0);
+                    if (i + 1 < NQ8) b0 = fmaf(qv0[i + 1], kv[i + 1], b0);
+                }
+                float c = a0 + b0;
+                c = c + shx(c, 4);
+                c = c + shx(c, 1);
+                c = c + shx(c, 2);
+                s0 = c * scale;
+            }
+            if (t < kv_len) {
+                if (j == 0) {
+                    sc0[t] = s0;
+                    if (pair) sc1[t] = s1;
+                }
+                mx0 = s0 > mx0 ? s0 : mx0;
+                mx1 = s1 > mx1 ? s1 : mx1;
+            }
+        }
+    }
+    red[0][tid] = mx0;
+    red[1][tid] = mx1;
+    __syncthreads();
+    for (int w = 128; w > 0; w >>= 1) {
+        if (tid < w) {
+            red[0][tid] = fmaxf(red[0][tid], red[0][tid + w]);
+            red[1][tid] = fmaxf(red[1][tid], red[1][tid + w]);
+        }
+        __syncthreads();
+    }
+    const float M0 = red[0][0], M1 = red[1][0];
+    const int n8 = kv_len & ~7;
+    for (int t = tid; t < kv_len; t += 256) {
+        sc0[t] = t < n8 ? exp_poly(sc0[t] - M0) : expf_libc(sc0[t] - M0);
+        if (pair) sc1[t] = t < n8 ? exp_poly(sc1[t] - M1) : expf_libc(sc1[t] - M1);
+    }
+    __syncthreads();
+    if (tid < 16) {
+        const int hsel = tid >> 3, jj = tid & 7;
+        if (hsel < nh) {
+            const float* sc = hsel ? sc1 : sc0;
+            float a = 0.0f;
+            for (int t = jj; t < n8; t += 8) a = a + sc[t];
+            vs8[hsel][jj] = a;
+        }
+    }
+    __syncthreads();
+    if (tid < nh) {
+        const float* sc = tid ? sc1 : sc0;
+        float sp = hsum8(vs8[tid]);
+        for (int t = n8; t < kv_len; t++) sp += sc[t];
+        inv_sh[tid] = 1.0f / (sp + 1e-12f);
+    }
+    __syncthreads();
+    for (int t = tid; t < kv_len; t += 256) {
+        sc0[t] = sc0[t] * inv_sh[0];
+        if (pair) sc1[t] = sc1[t] * inv_sh[1];
+    }
+
+    // P.V over LDS chunks of V; output o = (hsel, d); row pos comes from vn
+    constexpr int NO = (2 * HD + 255) / 256;
+    float acc[NO];
+#pragma unroll
+    for (int jo = 0; jo < NO; jo++) acc[jo] = 0.0f;
+    for (int c0 = 0; c0 < kv_len; c0 += V_ROWS) {
+        if (c0 > 0) {
+            __syncthreads();  // previous chunk consumed
+            stage_v(c0);
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        const int cn = kv_len - c0 < V_ROWS ? kv_len - c0 : V_ROWS;
+#pragma unroll
+        for (int jo = 0; jo < NO; jo++) {
+            const int o = tid + 256 * jo;
+            if (o >= nh * HD) break;
+            const int hsel = o / HD, d = o % HD;
+            const float* p = (hsel ? sc1 : sc0) + c0;
+            auto vat = [&](int r) { return (c0 + r == pos) ? vn[d] : vst[r * HD + d]; };
+            float a = acc[jo];
+            if (pair) {
+                for (int r = 0; r < cn; r++) a = fmaf(p[r], vat(r), a);
+            } else {
+                int r = 0;
+                for (; r + 1 < cn; r += 2) a = fmaf(p[r], vat(r), fmaf(p[r + 1], vat(r + 1), a));
+                if (r < cn) a = fmaf(p[r], vat(r), a);
+            }
+            acc[jo] = a;
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int jo = 0; jo < NO; jo++) {
+        const int o = tid + 256 * jo;
+        if (o < nh * HD) {
+            aout[o] = acc[jo];
+            ao[(size_t)qh0 * HD + o] = acc[jo];
+        }
+    }
+    __syncthreads();
+    // prep of the O input for columns [qh0*HD, (qh0+nh)*HD)
+    if (tid < nh * HD / 16) {
+        const int qp = tid & 3, blk = (qh0 * HD) / 64 + (tid >> 2);
+        float x[16];
+#pragma unroll
+        for (int kk = 0; kk < 16; kk++) x[kk] = aout[16 * tid + kk];
+        quad_sign(x, o_sign, blk, qp);
+        quad_fwht64(x, qp);
+        quad_quant_store(x, qp, blk, op.q, op.s, op.m);
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Small utility kernels
 // ---------------------------------------------------------------------------
 __global__ void k_fill_f32(float* p, size_t n, float v) {
@@ -1173,6 +1471,29 @@ void dpuf_hip_attn(void* s, int32_t M, const float* q, const float* kc, const fl
     hipLaunchKernelGGL(k_attn, dim3(M, n_kv, (groups + 1) / 2), dim3(256), (size_t)2 * hd * sizeof(float), ST(s), q,
                        kc, vc, out, scores, pos0, n_q, n_kv, hd, max_seq, scale);
     LAUNCHED("k_attn");
+}
+
+int32_t dpuf_hip_attn_dec(void* s, const float* q, const float* k, const float* v, const float* q_norm,
+                          const float* k_norm, float eps, const float* cos_tab, const float* sin_tab, float* kc,
+                          float* vc, const int32_t* pos0, int32_t n_q, int32_t n_kv, int32_t hd, int32_t max_seq,
+                          float scale, float* scores, float* ao, const uint8_t* o_sign, DpufPrep op) {
+    const int groups = n_q / n_kv;
+    const int sc_cap = max_seq < 8192 ? max_seq : 8192;
+    const size_t scl = 2 * (size_t)sc_cap > 3 * (size_t)hd ? 2 * (size_t)sc_cap : 3 * (size_t)hd;
+    const size_t lds = ((size_t)16384 + (size_t)6 * hd + scl) * sizeof(float);
+    const dim3 grid(n_kv, (groups + 1) / 2);
+#define ATT_LAUNCH(HDV)                                                                                            \
+    hipLaunchKernelGGL(k_attn_dec<HDV>, grid, dim3(256), lds, ST(s), q, k, v, q_norm, k_norm, eps, cos_tab, sin_tab, \
+                       kc, vc, pos0, n_q, n_kv, max_seq, scale, sc_cap, scores, ao, o_sign, op)
+    switch (hd) {
+        case 64: ATT_LAUNCH(64); break;
+        case 128: ATT_LAUNCH(128); break;
+        case 256: ATT_LAUNCH(256); break;
+        default: return -1;
+    }
+#undef ATT_LAUNCH
+    LAUNCHED("k_attn_dec");
+    return 0;
 }
 
 void dpuf_hip_zero_rows(void* s, int32_t M, float* out, int32_t ld, int32_t r0, int32_t r1) {

@@ -1,0 +1,417 @@
+"""Pins the CPU oracle (oracle/oracle.c) with what the mathematics fixes.
+
+The reference ships no golden vectors or known-answer tests for the Mode 12
+path, and its C sources cannot be built here unmodified.  Each oracle
+function is therefore checked against closed forms, invariants, special
+cases and float64 brute force, chosen so that a plausible slip (a dropped
+term, a wrong sign or index, a transposed operand, a wrong stage order)
+fails at least one of them.  Runs on the CPU only.
+"""
+import ctypes as C
+import math
+
+import numpy as np
+import pytest
+
+from dpuf_amd import model as M
+
+def walsh(n=64):
+    """Natural-order (Sylvester) Hadamard matrix H[i, j] = (-1)^popcount(i & j)."""
+    i = np.arange(n)[:, None]
+    j = np.arange(n)[None, :]
+    bits = np.vectorize(lambda v: bin(int(v)).count("1"))(i & j)
+    return np.where(bits % 2 == 0, 1.0, -1.0)
+
+
+def f32(x):
+    return np.ascontiguousarray(x, dtype=np.float32)
+
+
+# --------------------------------------------------------------------------- FWHT
+
+def test_fwht_unit_vectors_are_walsh_rows(orc):
+    H = walsh()
+    for i in range(64):
+        e = np.zeros(64, np.float32)
+        e[i] = 1.0
+        orc.orc_fwht64(M.ptr(e))
+        assert np.array_equal(e, (0.125 * H[i]).astype(np.float32)), i
+
+
+def test_fwht_matches_matrix_and_is_involution(orc):
+    rng = np.random.default_rng(0)
+    H = walsh()
+    for _ in range(20):
+        x = f32(rng.standard_normal(64))
+        y = x.copy()
+        orc.orc_fwht64(M.ptr(y))
+        ref = (H @ x.astype(np.float64)) / 8.0
+        assert np.allclose(y, ref, rtol=0, atol=1e-5)
+        # Parseval: H/8 is orthonormal
+        assert math.isclose(float(np.sum(y.astype(np.float64) ** 2)), float(np.sum(x.astype(np.float64) ** 2)),
+                            rel_tol=1e-5)
+        z = y.copy()
+        orc.orc_fwht64(M.ptr(z))
+        assert np.allclose(z, x, atol=1e-5)
+
+
+def test_fwht_stage_order_is_fixed(orc):
+    """Butterfly stages run with strides 1, 2, ..., 32 in that order: a
+    different order gives different fp32 roundings on ill-conditioned input."""
+    x = f32([1e8, 1.0, -1e8, 3.0] * 16)
+    y = x.copy()
+    orc.orc_fwht64(M.ptr(y))
+
+    def fwht(v, order):
+        v = v.astype(np.float32).copy()
+        for h in order:
+            for i in range(0, 64, 2 * h):
+                for j in range(i, i + h):
+                    a, b = v[j], v[j + h]
+                    v[j], v[j + h] = np.float32(a + b), np.float32(a - b)
+        return (v * np.float32(0.125)).astype(np.float32)
+
+    assert np.array_equal(y, fwht(x, [1, 2, 4, 8, 16, 32]))
+
+
+def test_fwht_sign_mask(orc):
+    rng = np.random.default_rng(1)
+    cols = 256
+    x = f32(rng.standard_normal(cols))
+    sb = rng.integers(0, 256, cols // 8).astype(np.uint8)
+    out = np.zeros(cols, np.float32)
+    orc.orc_fwht64_sign(cols, M.ptr(x), M.ptr(sb), M.ptr(out))
+    signs = np.where(np.unpackbits(sb, bitorder="little").astype(bool), -1.0, 1.0)
+    H = walsh()
+    ref = np.concatenate([H @ (signs * x)[c:c + 64] / 8.0 for c in range(0, cols, 64)])
+    assert np.allclose(out, ref, atol=1e-5)
+    # bit c%8 of byte c/8 negates column c: flipping one bit flips one input
+    sb2 = sb.copy()
+    sb2[3] ^= 0x04  # column 26
+    out2 = np.zeros(cols, np.float32)
+    orc.orc_fwht64_sign(cols, M.ptr(x), M.ptr(sb2), M.ptr(out2))
+    delta = np.zeros(cols)
+    delta[26] = -2.0 * signs[26] * x[26]
+    assert np.allclose(out2 - out, np.concatenate([H @ delta[c:c + 64] / 8.0 for c in range(0, cols, 64)]),
+                       atol=1e-5)
+
+
+# --------------------------------------------------------------------------- quantisation
+
+def prep(orc, x, sb=None):
+    cols = x.size
+    q = np.zeros(cols, np.int8)
+    s = np.zeros(cols // 32, np.float32)
+    m = np.zeros(cols // 32, np.int32)
+    orc.orc_prep_row(cols, M.ptr(f32(x)), M.ptr(sb) if sb is not None else None, M.ptr(q), M.ptr(s), M.ptr(m))
+    return q, s, m
+
+
+def rotated(orc, x, sb=None):
+    out = np.zeros(x.size, np.float32)
+    orc.orc_fwht64_sign(x.size, M.ptr(f32(x)), M.ptr(sb) if sb is not None else None, M.ptr(out))
+    return out
+
+
+def test_quant_zero_block(orc):
+    x = np.zeros(64, np.float32)
+    x[:32] = 1e-6           # rotated amax <= 1e-4 -> scale 0, q 0, sum 0
+    x[32:] = np.linspace(-1, 1, 32)
+    f = rotated(orc, x)
+    q, s, m = prep(orc, x)
+    amax = np.abs(f.reshape(2, 32)).max(axis=1)
+    for b in range(2):
+        if amax[b] <= 1e-4:
+            assert s[b] == 0 and m[b] == 0 and not q[32 * b:32 * b + 32].any()
+        else:
+            assert s[b] == np.float32(amax[b]) / np.float32(127.0)
+
+
+def test_quant_saturation_and_symmetric_clamp(orc):
+    # a block whose FWHT output has one dominant coefficient: q = +-127 exactly there
+    x = np.zeros(64, np.float32)
+    x[0] = 8.0  # FWHT of 8*e0 is all ones -> every value equals amax
+    q, s, m = prep(orc, x)
+    assert (q == 127).all() and s[0] == np.float32(1.0) / np.float32(127.0)
+    assert m[0] == 8 * 127 * 32
+    x[0] = -8.0
+    q, s, m = prep(orc, x)
+    assert (q == -127).all() and m[0] == -8 * 127 * 32  # never -128
+
+
+def test_quant_round_half_even(orc):
+    """x * (127/amax) lands exactly on k + 0.5: ties go to even (cvtps_epi32
+    under the default rounding mode)."""
+    cols = 64
+    H = walsh()
+    f = np.zeros(64, np.float64)
+    f[:32] = [127.0, 2.5, 3.5, -2.5, -3.5, 0.5, 1.5, -0.5] + [0.0] * 24
+    f[32:] = 1.0
+    x = f32(H @ f / 8.0)            # FWHT(x) == f up to rounding of the exact dyadic values
+    fr = rotated(orc, x)
+    assert np.array_equal(fr[:8], f32(f[:8]))
+    q, s, m = prep(orc, x)
+    assert list(q[:8]) == [127, 2, 4, -2, -4, 0, 2, 0]
+    assert m[0] == 8 * int(q[:32].astype(np.int64).sum())
+
+
+def test_quant_error_bound_and_sums(orc):
+    rng = np.random.default_rng(3)
+    x = f32(rng.standard_normal(1024) * 3)
+    f = rotated(orc, x)
+    q, s, m = prep(orc, x)
+    for b in range(32):
+        blk = f[32 * b:32 * b + 32].astype(np.float64)
+        deq = q[32 * b:32 * b + 32].astype(np.float64) * s[b]
+        assert np.max(np.abs(deq - blk)) <= 0.5 * s[b] * (1 + 1e-5) + 1e-7
+        assert m[b] == 8 * int(q[32 * b:32 * b + 32].astype(np.int64).sum())
+
+
+def test_prep_slab_is_row_layout_transposed(orc):
+    rng = np.random.default_rng(4)
+    cols, mc = 128, 5
+    nb = cols // 32
+    x = f32(rng.standard_normal((mc, cols)))
+    sb = rng.integers(0, 256, cols // 8).astype(np.uint8)
+    sq = np.full(nb * 192, 0x33, np.int8)
+    ss = np.full(nb * 6, -7.0, np.float32)
+    sm = np.full(nb * 6, 11, np.int32)
+    orc.orc_prep_slab(mc, cols, M.ptr(x), M.ptr(sb), M.ptr(sq), M.ptr(ss), M.ptr(sm))
+    words = sq.view(np.int32).reshape(nb, 8, 6)
+    for j in range(mc):
+        q, s, m = prep(orc, x[j], sb)
+        assert np.array_equal(words[:, :, j], q.view(np.int32).reshape(nb, 8))
+        assert np.array_equal(ss.reshape(nb, 6)[:, j], s) and np.array_equal(sm.reshape(nb, 6)[:, j], m)
+    # token lane 5 of the partial slab is left untouched
+    assert (words[:, :, 5] == np.int32(0x33333333)).all() and (ss.reshape(nb, 6)[:, 5] == -7).all()
+
+
+# --------------------------------------------------------------------------- pack / embed / GEMV
+
+def packed(rows, cols, seed, std=0.02):
+    W = M.random_normal(rows * cols, std, seed, f"oracle{rows}x{cols}").reshape(rows, cols)
+    sb = M.sign_bits(cols, seed, f"oracle-s{cols}")
+    blob, d = M.pack_matrix(W, sb)
+    return W, sb, blob, d
+
+
+def embed_rows(orc, d, ids):
+    out = np.zeros((len(ids), d.cols), np.float32)
+    ids = np.ascontiguousarray(ids, np.int32)
+    orc.orc_embed(len(ids), d.cols, M.ptr(ids), d.tensor_base, d.tile_offsets, d.sign_bits, M.ptr(out))
+    return out
+
+
+def test_pack_embed_roundtrip(orc):
+    """Packing N(0, 0.02) weights and reading rows back through the embedding
+    path (sign (.) FWHT((u - 8) * scale)) recovers W to 4-bit accuracy."""
+    W, sb, blob, d = packed(40, 256, 5)
+    E = embed_rows(orc, d, np.arange(40))
+    err = np.linalg.norm(E - W) / np.linalg.norm(W)
+    assert err < 0.15, err
+    corr = np.corrcoef(E.ravel(), W.ravel())[0, 1]
+    assert corr > 0.99, corr
+
+
+def test_embed_closed_form(orc):
+    """Embedding row r = sign (.) FWHT64(w_rot): the inverse transform of a
+    row gives back w_rot, whose 32-blocks hold at most 16 distinct integer
+    multiples (u - 8, in [-8, 7]) of one fp16 scale."""
+    W, sb, blob, d = packed(24, 128, 6)
+    E = embed_rows(orc, d, [0, 7, 8, 15, 16, 23])
+    for row in E:
+        wr = rotated(orc, row, sb).astype(np.float64)
+        for b in range(4):
+            blk = wr[32 * b:32 * b + 32]
+            vals = np.unique(np.round(blk, 9))
+            assert vals.size <= 16
+            if vals.size < 2:
+                continue
+            step = np.min(np.diff(vals))
+            k = blk / step
+            assert np.allclose(k, np.round(k), atol=1e-3), b
+            assert np.round(k).min() >= -8 and np.round(k).max() <= 8
+
+
+def gemv(orc, d, x, skip=True):
+    Mt = x.shape[0]
+    nb = d.cols // 32
+    q = np.zeros((Mt, d.cols), np.int8)
+    s = np.zeros((Mt, nb), np.float32)
+    m = np.zeros((Mt, nb), np.int32)
+    for i in range(Mt):
+        orc.orc_prep_row(d.cols, M.ptr(f32(x[i])), d.sign_bits, M.ptr(q[i]), M.ptr(s[i]), M.ptr(m[i]))
+    out = np.zeros((Mt, d.rows), np.float32)
+    orc.orc_gemm_tiles(Mt, d.rows, d.cols, 0, d.n_tiles, M.ptr(q), M.ptr(s), M.ptr(m), d.tensor_base,
+                       d.tile_offsets, M.ptr(out), int(skip))
+    return out, q, s
+
+
+def test_gemv_equals_dense_product_of_embedded_rows(orc):
+    """y = W_rec x where W_rec are the rows read back through the embedding
+    path: with the activation quantised the same way, the two agree to fp32
+    accumulation error.  Catches nibble-order, scale-index, sign and
+    transposition slips in either path."""
+    rng = np.random.default_rng(7)
+    W, sb, blob, d = packed(72, 512, 8)
+    x = f32(rng.standard_normal((3, 512)))
+    y, q, s = gemv(orc, d, x)
+    E = embed_rows(orc, d, np.arange(72)).astype(np.float64)
+    for i in range(3):
+        # dequantised activation in the rotated domain, mapped back through the orthonormal transform
+        xr = (q[i].astype(np.float64).reshape(-1, 32) * s[i][:, None].astype(np.float64)).ravel()
+        xd = rotated(orc, f32(xr), None).astype(np.float64)          # FWHT is its own inverse
+        signs = np.where(np.unpackbits(sb, bitorder="little").astype(bool), -1.0, 1.0)
+        ref = E @ (signs * xd)
+        assert np.allclose(y[i], ref, rtol=2e-4, atol=2e-5), np.max(np.abs(y[i] - ref))
+        # and close to the unquantised product
+        assert np.allclose(y[i], W @ x[i].astype(np.float64), rtol=0.2, atol=0.2)
+
+
+def test_gemv_m1_equals_slab_bitwise(orc):
+    rng = np.random.default_rng(9)
+    W, sb, blob, d = packed(48, 256, 10)
+    x = f32(rng.standard_normal((7, 256)))
+    y7, _, _ = gemv(orc, d, x, skip=False)
+    for i in range(7):
+        y1, _, _ = gemv(orc, d, x[i:i + 1], skip=True)
+        assert np.array_equal(y1[0].view(np.uint32), y7[i].view(np.uint32))
+
+
+def test_gemv_tile_range_leaves_other_rows(orc):
+    rng = np.random.default_rng(11)
+    W, sb, blob, d = packed(100, 128, 12)
+    x = f32(rng.standard_normal((1, 128)))
+    full, q, s = gemv(orc, d, x)
+    m = np.zeros((1, 4), np.int32)
+    orc.orc_prep_row(128, M.ptr(x[0]), d.sign_bits, M.ptr(q[0]), M.ptr(s[0]), M.ptr(m[0]))
+    out = np.full((1, 100), 9.0, np.float32)
+    orc.orc_gemm_tiles(1, 100, 128, 2, 5, M.ptr(q), M.ptr(s), M.ptr(m), d.tensor_base, d.tile_offsets,
+                       M.ptr(out), 1)
+    assert (out[0, :32] == 9).all() and (out[0, 80:] == 9).all()
+    assert np.array_equal(out[0, 32:80], full[0, 32:80])
+
+
+# --------------------------------------------------------------------------- scalar pieces
+
+def test_exp_poly_accuracy(orc):
+    for v in np.concatenate([np.linspace(-44, 0, 4001), [0.0, -1e-7, -0.5, -10.0]]):
+        got = orc.orc_exp_poly(float(v))
+        assert math.isclose(got, math.exp(float(np.float32(v))), rel_tol=2e-7, abs_tol=1e-30), v
+    assert orc.orc_exp_poly(0.0) == 1.0
+
+
+def test_h2f_matches_numpy(orc):
+    for h in [0x0000, 0x8000, 0x0001, 0x03FF, 0x0400, 0x3C00, 0x7BFF, 0xFBFF, 0x3555, 0x7C00, 0xFC00]:
+        assert orc.orc_h2f(h) == float(np.array([h], np.uint16).view(np.float16)[0].astype(np.float32)), hex(h)
+
+
+def test_rmsnorm_float64(orc):
+    rng = np.random.default_rng(13)
+    n = 1024
+    x = f32(rng.standard_normal(n))
+    r = f32(rng.standard_normal(n))
+    w = f32(rng.uniform(0.5, 1.5, n))
+    xs = x.copy()
+    out = np.zeros(n, np.float32)
+    orc.orc_add_rmsnorm(n, M.ptr(xs), M.ptr(r), M.ptr(w), C.c_float(1e-6), M.ptr(out))
+    h = x.astype(np.float64) + r
+    assert np.array_equal(xs, f32(x + r))  # residual is stored back
+    ref = h / np.sqrt(np.mean(h * h) + 1e-6) * w
+    assert np.allclose(out, ref, rtol=1e-5, atol=1e-6)
+    # constant input: every output equals w * c / sqrt(c^2 + eps)
+    c = np.full(n, 3.0, np.float32)
+    orc.orc_add_rmsnorm(n, M.ptr(c), None, M.ptr(np.ones(n, np.float32)), C.c_float(1e-6), M.ptr(out))
+    assert np.allclose(out, 3.0 / math.sqrt(9.0 + 1e-6), rtol=1e-6)
+
+
+def rope_tables(orc, theta=1e6, hd=128, seq=64):
+    cfg = M.abi.DpufModelConfig()
+    cfg.head_dim, cfg.max_seq_len, cfg.rope_theta = hd, seq, theta
+    ct = np.zeros(seq * hd // 2, np.float32)
+    st = np.zeros(seq * hd // 2, np.float32)
+    orc.orc_rope_tables(C.byref(cfg), M.ptr(ct), M.ptr(st))
+    return ct.reshape(seq, hd // 2), st.reshape(seq, hd // 2)
+
+
+def test_rope_tables_and_rotation(orc):
+    ct, st = rope_tables(orc)
+    assert (ct[0] == 1).all() and (st[0] == 0).all()
+    j = np.arange(64)
+    inv = 1.0 / (1e6 ** (2 * j / 128.0))
+    for p in (1, 7, 63):
+        assert np.allclose(ct[p], np.cos(p * inv), atol=2e-6) and np.allclose(st[p], np.sin(p * inv), atol=2e-6)
+    rng = np.random.default_rng(14)
+    v = f32(rng.standard_normal(128))
+    for p in (0, 5):
+        w = v.copy()
+        orc.orc_rope_apply(128, M.ptr(w), M.ptr(np.ascontiguousarray(ct[p])), M.ptr(np.ascontiguousarray(st[p])))
+        if p == 0:
+            assert np.array_equal(w, v)
+        # NeoX halves: pair (j, j + 64) is rotated by angle p * inv_j; norms are preserved
+        a = v[:64].astype(np.float64) + 1j * v[64:].astype(np.float64)
+        b = w[:64].astype(np.float64) + 1j * w[64:].astype(np.float64)
+        assert np.allclose(b, a * np.exp(1j * p * inv), atol=1e-5)
+
+
+def attn(orc, q0, q1, K, V, scale):
+    hd = K.shape[1]
+    n = K.shape[0]
+    s0 = np.zeros(n, np.float32)
+    s1 = np.zeros(n, np.float32)
+    o0 = np.zeros(hd, np.float32)
+    o1 = np.zeros(hd, np.float32)
+    orc.orc_attn_heads(hd, n, C.c_float(scale), M.ptr(f32(K)), M.ptr(f32(V)), M.ptr(f32(q0)),
+                       M.ptr(f32(q1)) if q1 is not None else None, M.ptr(s0), M.ptr(s1), M.ptr(o0),
+                       M.ptr(o1) if q1 is not None else None)
+    return o0, o1
+
+
+@pytest.mark.parametrize("n", [1, 3, 8, 13, 70])
+@pytest.mark.parametrize("pair", [False, True])
+def test_attention_float64(orc, n, pair):
+    rng = np.random.default_rng(n + 100 * pair)
+    hd = 128
+    K = rng.standard_normal((n, hd))
+    V = rng.standard_normal((n, hd))
+    q0 = rng.standard_normal(hd)
+    q1 = rng.standard_normal(hd) if pair else None
+    sc = 1 / math.sqrt(hd)
+    o0, o1 = attn(orc, q0, q1, K, V, sc)
+    for q, o in ((q0, o0), (q1, o1)):
+        if q is None:
+            continue
+        s = f32(K) .astype(np.float64) @ f32(q).astype(np.float64) * sc
+        p = np.exp(s - s.max())
+        p /= p.sum()
+        assert np.allclose(o, p @ f32(V).astype(np.float64), rtol=1e-5, atol=1e-6)
+
+
+def test_attention_special_cases(orc):
+    rng = np.random.default_rng(15)
+    V = rng.standard_normal((9, 128))
+    # identical keys -> uniform weights -> mean of V
+    K = np.tile(rng.standard_normal(128), (9, 1))
+    o0, _ = attn(orc, rng.standard_normal(128), None, K, V, 0.1)
+    assert np.allclose(o0, f32(V).astype(np.float64).mean(axis=0), atol=1e-5)
+    # one key -> that value row
+    o0, _ = attn(orc, rng.standard_normal(128), None, K[:1], V[:1], 0.1)
+    assert np.allclose(o0, f32(V[0]), atol=1e-6)
+
+
+def test_swiglu_deadzone(orc):
+    for g in [-50.0, -40.0, -3.0, -0.1, 0.0, 0.2, 2.0, 39.9, 41.0]:
+        for u in [-2.0, 0.01, 1.5]:
+            got = orc.orc_swiglu1(g, u, 0.0)
+            gg = max(-40.0, min(g, 40.0))
+            ref = g / (1.0 + math.exp(-gg)) * u
+            assert math.isclose(got, ref, rel_tol=2e-6, abs_tol=1e-30), (g, u)
+    assert orc.orc_swiglu1(0.001, 1.0, 0.005) == 0.0          # |silu * u| < dz -> 0
+    assert orc.orc_swiglu1(3.0, 1.0, 0.005) != 0.0
+
+
+def test_argmax_first_max(orc):
+    x = np.array([1.0, 5.0, 2.0, 5.0, -1.0], np.float32)
+    assert orc.orc_argmax(M.ptr(x), 5) == 1
+    x = np.full(100, -3.0, np.float32)
+    assert orc.orc_argmax(M.ptr(x), 100) == 0
