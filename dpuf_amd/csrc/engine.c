@@ -29,8 +29,7 @@ enum { W_Q = 0, W_K, W_V, W_O, W_GATE, W_UP, W_DOWN };
 
 typedef struct {
     const uint8_t* host_base;
-    void* d_tiles;
-    void* d_offs;
+    void* d_groups;   /* row-block layout, n_groups * (cols/32) * 144 bytes */
     void* d_sign;
     uint64_t bytes;
 } Upload;
@@ -138,43 +137,55 @@ static int validate_desc(const DpufWeightDesc* d) {
     return 1;
 }
 
+static void set_devw(DpufDevW* out, const Upload* u, const DpufWeightDesc* d) {
+    out->g = (const uint8_t*)u->d_groups;
+    out->sign = (const uint8_t*)u->d_sign;
+    out->rows = d->rows;
+    out->cols = d->cols;
+    out->n_groups = (d->rows + 7) / 8;
+}
+
+/* Uploads one validated mode 12 matrix: the .dpuf tile region and its offset
+ * table go to a staging buffer, dpuf_hip_relayout writes the row-block
+ * layout the kernels read, and the staging buffer is released. */
 static int upload_desc(Engine* e, const DpufWeightDesc* d, DpufDevW* out) {
     if (!validate_desc(d)) return 0;
     for (int32_t i = 0; i < e->n_ups; i++) {
         if (e->ups[i].host_base == d->tensor_base) {
-            out->tiles = (const uint8_t*)e->ups[i].d_tiles;
-            out->offs = (const uint64_t*)e->ups[i].d_offs;
-            out->sign = (const uint8_t*)e->ups[i].d_sign;
-            out->rows = d->rows;
-            out->cols = d->cols;
-            out->n_tiles = d->n_tiles;
+            set_devw(out, &e->ups[i], d);
             return 1;
         }
     }
     Upload u;
     memset(&u, 0, sizeof u);
     u.host_base = d->tensor_base;
-    u.bytes = d->tile_offsets[d->n_tiles];
-    u.d_tiles = dpuf_hip_malloc((size_t)u.bytes);
-    u.d_offs = dpuf_hip_malloc(((size_t)d->n_tiles + 1) * 8u);
+    const int32_t n_groups = (d->rows + 7) / 8, n_blk = d->cols / 32;
+    u.bytes = (uint64_t)n_groups * (uint64_t)n_blk * 144u;
+    const uint64_t raw = d->tile_offsets[d->n_tiles];
+    void* d_raw = dpuf_hip_malloc((size_t)raw);
+    void* d_offs = dpuf_hip_malloc(((size_t)d->n_tiles + 1) * 8u);
+    u.d_groups = dpuf_hip_malloc((size_t)u.bytes);
     if (d->sign_bits) u.d_sign = dpuf_hip_malloc((size_t)d->cols / 8u);
-    if (!u.d_tiles || !u.d_offs || (d->sign_bits && !u.d_sign)) {
-        dpuf_hip_free(u.d_tiles); dpuf_hip_free(u.d_offs); dpuf_hip_free(u.d_sign);
+    if (!d_raw || !d_offs || !u.d_groups || (d->sign_bits && !u.d_sign)) {
+        dpuf_hip_free(d_raw); dpuf_hip_free(d_offs); dpuf_hip_free(u.d_groups); dpuf_hip_free(u.d_sign);
         return 0;
     }
-    dpuf_hip_h2d(u.d_tiles, d->tensor_base, (size_t)u.bytes, e->stream);
-    dpuf_hip_h2d(u.d_offs, d->tile_offsets, ((size_t)d->n_tiles + 1) * 8u, e->stream);
+    dpuf_hip_h2d(d_raw, d->tensor_base, (size_t)raw, e->stream);
+    dpuf_hip_h2d(d_offs, d->tile_offsets, ((size_t)d->n_tiles + 1) * 8u, e->stream);
     if (d->sign_bits) dpuf_hip_h2d(u.d_sign, d->sign_bits, (size_t)d->cols / 8u, e->stream);
-    /* synchronous upload: the caller's pageable buffers may be released later */
-    if (dpuf_hip_sync(e->stream) != 0) return 0;
+    dpuf_hip_relayout(e->stream, (const uint8_t*)d_raw, (const uint64_t*)d_offs, n_groups, n_blk,
+                      (uint8_t*)u.d_groups);
+    /* synchronous: the caller's pageable buffers may be released after create */
+    const int ok = dpuf_hip_sync(e->stream) == 0;
+    dpuf_hip_free(d_raw);
+    dpuf_hip_free(d_offs);
+    if (!ok) {
+        dpuf_hip_free(u.d_groups); dpuf_hip_free(u.d_sign);
+        return 0;
+    }
     e->ups = (Upload*)realloc(e->ups, (size_t)(e->n_ups + 1) * sizeof(Upload));
     e->ups[e->n_ups++] = u;
-    out->tiles = (const uint8_t*)u.d_tiles;
-    out->offs = (const uint64_t*)u.d_offs;
-    out->sign = (const uint8_t*)u.d_sign;
-    out->rows = d->rows;
-    out->cols = d->cols;
-    out->n_tiles = d->n_tiles;
+    set_devw(out, &u, d);
     return 1;
 }
 
@@ -254,7 +265,7 @@ static void engine_free(Engine* e) {
     if (e->stream) dpuf_hip_sync(e->stream);
     dpuf_hip_graph_destroy(e->graph);
     for (int32_t i = 0; i < e->n_ups; i++) {
-        dpuf_hip_free(e->ups[i].d_tiles); dpuf_hip_free(e->ups[i].d_offs); dpuf_hip_free(e->ups[i].d_sign);
+        dpuf_hip_free(e->ups[i].d_groups); dpuf_hip_free(e->ups[i].d_sign);
     }
     free(e->ups);
     if (e->d_norm) {
@@ -491,32 +502,51 @@ DPUF_EXPORT int32_t dpuf_engine_get_prefix_len(void* handle, int32_t pfx_id) {
 /* Forward                                                                    */
 /* ------------------------------------------------------------------------- */
 
+/* Algorithmic bytes of one GEMV launch over tiles [t0, t1): the weight
+ * groups (8 rows x 32 columns = 144 bytes each) plus, per token row, the
+ * prepped activations (K int8 + 8 bytes per 32-block) and the fp32 outputs. */
 static double gemv_bytes(const DpufDevW* w, int32_t t0, int32_t t1, int32_t M) {
-    const double rows = (double)((t1 * 16 < w->rows ? t1 * 16 : w->rows) - t0 * 16);
+    const int32_t g0 = 2 * t0, g1 = 2 * t1 < w->n_groups ? 2 * t1 : w->n_groups;
+    const int32_t r1 = 16 * t1 < w->rows ? 16 * t1 : w->rows;
     const double n_blk = (double)(w->cols / 32);
-    return rows / 8.0 * n_blk * 144.0 + (double)M * (w->cols + n_blk * 8.0 + rows * 4.0);
+    return (double)(g1 - g0) * n_blk * 144.0 + (double)M * (w->cols + n_blk * 8.0 + (r1 - 16 * t0) * 4.0);
 }
 
+/* Tiles [t0, t1) of w (16 rows each) as a GEMV job over 8-row groups. */
 static DpufGemvJob job(const DpufDevW* w, int32_t t0, int32_t t1, DpufPrep p, float* out, int32_t ldo) {
     DpufGemvJob j;
     j.w = *w;
-    j.t0 = t0;
-    j.t1 = t1;
+    j.g0 = 2 * t0;
+    j.g1 = 2 * t1 < w->n_groups ? 2 * t1 : w->n_groups;
     j.p = p;
     j.out = out;
     j.ldo = ldo;
     return j;
 }
 
+static int32_t n_tiles_of(const DpufDevW* w) { return (w->rows + 15) / 16; }
+
+static void enqueue_layers(Engine* e, int32_t M, int32_t keep_tiles);
+static void enqueue_head(Engine* e, int32_t M, int32_t only_last, int32_t early_tiles, float early_margin,
+                         int32_t want_argmax);
+
 /* Enqueues one forward step (ids/embeds/pos0 already on the device). */
 static void enqueue_forward(Engine* e, int32_t M, int32_t use_embeds, int32_t only_last, int32_t keep_tiles,
                             int32_t early_tiles, float early_margin, int32_t want_argmax) {
+    dpuf_hip_embed(e->stream, e->tok, e->d_ids, M, use_embeds ? e->embeds : NULL, e->h);
+    enqueue_layers(e, M, keep_tiles);
+    enqueue_head(e, M, only_last, early_tiles, early_margin, want_argmax);
+}
+
+/* Layer loop: residual + RMSNorm + prep, fused Q/K/V GEMV, attention (for
+ * M == 1 one kernel with QK-norm, RoPE, the KV store and the O-input prep),
+ * O GEMV, residual + RMSNorm + prep, fused gate/up GEMV, SwiGLU + prep, down
+ * GEMV; the residual stream lives in e->h and the last projection in e->hn. */
+static void enqueue_layers(Engine* e, int32_t M, int32_t keep_tiles) {
     void* s = e->stream;
     const int32_t H = e->H, I = e->I;
     const float eps = e->cfg.rms_eps;
     const float scale = 1.0f / sqrtf((float)e->hd);
-
-    dpuf_hip_embed(s, e->tok, e->d_ids, M, use_embeds ? e->embeds : NULL, e->h);
     for (int32_t l = 0; l < e->L; l++) {
         const DpufDevW* W = e->lw + (size_t)l * 7;
         const uint8_t* qi = e->q_idx + (size_t)l * 5;
@@ -536,12 +566,12 @@ static void enqueue_forward(Engine* e, int32_t M, int32_t use_embeds, int32_t on
         /* (2) Q, K, V in one launch */
         {
             DpufGemvJob js[3] = {
-                job(&W[W_Q], 0, W[W_Q].n_tiles, e->prep[qi[0]], e->q, e->qd),
-                job(&W[W_K], 0, W[W_K].n_tiles, e->prep[qi[1]], e->k, e->kvd),
-                job(&W[W_V], 0, W[W_V].n_tiles, e->prep[qi[2]], e->v, e->kvd),
+                job(&W[W_Q], 0, n_tiles_of(&W[W_Q]), e->prep[qi[0]], e->q, e->qd),
+                job(&W[W_K], 0, n_tiles_of(&W[W_K]), e->prep[qi[1]], e->k, e->kvd),
+                job(&W[W_V], 0, n_tiles_of(&W[W_V]), e->prep[qi[2]], e->v, e->kvd),
             };
-            double b = gemv_bytes(&W[W_Q], 0, W[W_Q].n_tiles, M) + gemv_bytes(&W[W_K], 0, W[W_K].n_tiles, M) +
-                       gemv_bytes(&W[W_V], 0, W[W_V].n_tiles, M);
+            double b = gemv_bytes(&W[W_Q], 0, n_tiles_of(&W[W_Q]), M) + gemv_bytes(&W[W_K], 0, n_tiles_of(&W[W_K]), M) +
+                       gemv_bytes(&W[W_V], 0, n_tiles_of(&W[W_V]), M);
             const int tm2 = tm_begin(e, K_QKV, b);
             dpuf_hip_gemv(s, M, 3, js, NULL, 0.0f);
             tm_end(e, tm2);
@@ -564,8 +594,8 @@ static void enqueue_forward(Engine* e, int32_t M, int32_t use_embeds, int32_t on
             tm_end(e, tm);
         }
         {
-            DpufGemvJob j = job(&W[W_O], 0, W[W_O].n_tiles, e->prep[0], e->hn, H);
-            const int tm5 = tm_begin(e, K_O, gemv_bytes(&W[W_O], 0, W[W_O].n_tiles, M));
+            DpufGemvJob j = job(&W[W_O], 0, n_tiles_of(&W[W_O]), e->prep[0], e->hn, H);
+            const int tm5 = tm_begin(e, K_O, gemv_bytes(&W[W_O], 0, n_tiles_of(&W[W_O]), M));
             dpuf_hip_gemv(s, M, 1, &j, NULL, 0.0f);
             tm_end(e, tm5);
         }
@@ -580,10 +610,10 @@ static void enqueue_forward(Engine* e, int32_t M, int32_t use_embeds, int32_t on
         /* (7) gate + up in one launch */
         {
             DpufGemvJob js[2] = {
-                job(&W[W_GATE], 0, W[W_GATE].n_tiles, e->prep[0], e->gate, I),
-                job(&W[W_UP], 0, W[W_UP].n_tiles, e->prep[qi[4]], e->up, I),
+                job(&W[W_GATE], 0, n_tiles_of(&W[W_GATE]), e->prep[0], e->gate, I),
+                job(&W[W_UP], 0, n_tiles_of(&W[W_UP]), e->prep[qi[4]], e->up, I),
             };
-            double b = gemv_bytes(&W[W_GATE], 0, W[W_GATE].n_tiles, M) + gemv_bytes(&W[W_UP], 0, W[W_UP].n_tiles, M);
+            double b = gemv_bytes(&W[W_GATE], 0, n_tiles_of(&W[W_GATE]), M) + gemv_bytes(&W[W_UP], 0, n_tiles_of(&W[W_UP]), M);
             const int tm7 = tm_begin(e, K_GU, b);
             dpuf_hip_gemv(s, M, 2, js, NULL, 0.0f);
             tm_end(e, tm7);
@@ -595,7 +625,7 @@ static void enqueue_forward(Engine* e, int32_t M, int32_t use_embeds, int32_t on
         /* (9) down projection, pruned to keep_tiles with the rest zeroed
          * (dpuf_engine.c:2018-2044) */
         {
-            int32_t nt = W[W_DOWN].n_tiles;
+            int32_t nt = n_tiles_of(&W[W_DOWN]);
             int32_t kt = (keep_tiles > 0 && keep_tiles < nt) ? keep_tiles : nt;
             DpufGemvJob j = job(&W[W_DOWN], 0, kt, e->prep[0], e->hn, H);
             const int tm9 = tm_begin(e, K_DOWN, gemv_bytes(&W[W_DOWN], 0, kt, M));
@@ -606,7 +636,15 @@ static void enqueue_forward(Engine* e, int32_t M, int32_t use_embeds, int32_t on
         if (e->capture && M <= e->capture_cap)
             dpuf_hip_capture(s, M, H, e->h, e->hn, e->capture + (size_t)l * e->capture_cap * H);
     }
+}
 
+/* Final residual + output RMSNorm + LM head (with the optional Zone-A early
+ * exit) and the device argmax; reads the residual stream h (+ hn). */
+static void enqueue_head(Engine* e, int32_t M, int32_t only_last, int32_t early_tiles, float early_margin,
+                         int32_t want_argmax) {
+    void* s = e->stream;
+    const int32_t H = e->H;
+    const float eps = e->cfg.rms_eps;
     if (only_last == 2) return;
     const int32_t lm0 = only_last ? M - 1 : 0, lmM = M - lm0;
     {
@@ -616,7 +654,7 @@ static void enqueue_forward(Engine* e, int32_t M, int32_t use_embeds, int32_t on
                               e->d_out_norm, eps, 1, ps, e->prep, NULL);
         tm_end(e, tm10);
     }
-    const int32_t nt = e->lm.n_tiles;
+    const int32_t nt = n_tiles_of(&e->lm);
     if (early_tiles > 0 && lmM == 1 && nt > 2048) {
         /* Zone-A early exit (dpuf_engine.c:2091-2136): zone tiles, top-2
          * margin test on the device, then either the -1e9 fill or the
@@ -825,13 +863,46 @@ DPUF_EXPORT int64_t dpuf_amd_engine_early_exit_count(void* handle) {
     return e ? e->early_exits : 0;
 }
 
+/* Jobs of one GEMV launch of kind `which` in layer l (see dpuf_amd_gemv_bench). */
+static int32_t bench_jobs(Engine* e, int32_t which, int32_t l, DpufGemvJob* js, double* bytes, int32_t M) {
+    static const int32_t mats[2][3] = {{W_GATE, W_UP, -1}, {W_Q, W_K, W_V}};
+    if (which == 7) {
+        js[0] = job(&e->lm, 0, n_tiles_of(&e->lm), e->prep[0], e->logits, e->lm.rows);
+        *bytes = gemv_bytes(&e->lm, 0, n_tiles_of(&e->lm), M);
+        return 1;
+    }
+    const DpufDevW* W = e->lw + (size_t)l * 7;
+    if (which < 7) {
+        js[0] = job(&W[which], 0, n_tiles_of(&W[which]), e->prep[0], e->up, W[which].rows);
+        *bytes = gemv_bytes(&W[which], 0, n_tiles_of(&W[which]), M);
+        return 1;
+    }
+    const int32_t* ms = mats[which - 8];
+    float* outs[3] = {e->gate, e->up, e->v};
+    if (which == 9) {
+        outs[0] = e->q;
+        outs[1] = e->k;
+    }
+    int32_t n = 0;
+    *bytes = 0.0;
+    for (int k = 0; k < 3 && ms[k] >= 0; k++, n++) {
+        const DpufDevW* w = &W[ms[k]];
+        js[k] = job(w, 0, n_tiles_of(w), e->prep[0], outs[k], w->rows);
+        *bytes += gemv_bytes(w, 0, n_tiles_of(w), M);
+    }
+    return n;
+}
+
 DPUF_EXPORT double dpuf_amd_gemv_bench(void* handle, int32_t which, int32_t M, int32_t iters, int32_t start_layer,
                                        double* bytes) {
     Engine* e = (Engine*)handle;
-    if (!e || which < 0 || which > 7 || M < 1 || M > DPUF_AMD_MAX_BATCH || iters < 1) return -1.0;
-    if (which < 7 && (e->L == 0 || start_layer < 0 || start_layer >= e->L)) return -1.0;
-    const DpufDevW* w0 = which == 7 ? &e->lm : &e->lw[(size_t)start_layer * 7 + which];
-    const int32_t K = w0->cols;
+    if (!e || which < 0 || which > 9 || M < 1 || iters < 1) return -1.0;
+    if (which != 7 && (e->L == 0 || start_layer < 0 || start_layer >= e->L)) return -1.0;
+    if (M > DPUF_AMD_MAX_BATCH) return -1.0;
+    DpufGemvJob js[3];
+    double b0 = 0.0;
+    bench_jobs(e, which, start_layer, js, &b0, M);
+    const int32_t K = js[0].w.cols;
     /* activations: the prep of a fixed, non-trivial vector per row */
     float* x = (float*)malloc((size_t)M * K * 4);
     if (!x) return -1.0;
@@ -840,28 +911,57 @@ DPUF_EXPORT double dpuf_amd_gemv_bench(void* handle, int32_t which, int32_t M, i
         st = st * 1664525u + 1013904223u;
         x[i] = ((float)(st >> 8) / 16777216.0f) * 2.0f - 1.0f;
     }
-    dpuf_hip_h2d(e->gate, x, (size_t)M * K * 4, e->stream);
-    dpuf_hip_prep(e->stream, M, K, e->gate, w0->sign, e->prep[0]);
+    float* dx = (float*)dpuf_hip_malloc((size_t)M * K * 4);
+    if (!dx) {
+        free(x);
+        return -1.0;
+    }
+    dpuf_hip_h2d(dx, x, (size_t)M * K * 4, e->stream);
+    dpuf_hip_prep(e->stream, M, K, dx, js[0].w.sign, e->prep[0]);
     dpuf_hip_sync(e->stream);
+    dpuf_hip_free(dx);
     free(x);
     void* a = dpuf_hip_event_create();
     void* b = dpuf_hip_event_create();
-    float* out = which == 7 ? e->logits : e->up;
     const int32_t nl = which == 7 ? 1 : e->L - start_layer;
-    /* warm-up launch */
-    DpufGemvJob j = job(w0, 0, w0->n_tiles, e->prep[0], out, w0->rows);
-    dpuf_hip_gemv(e->stream, M, 1, &j, NULL, 0.0f);
+    int32_t n = bench_jobs(e, which, start_layer, js, &b0, M);
+    dpuf_hip_gemv(e->stream, M, n, js, NULL, 0.0f); /* warm-up launch */
     dpuf_hip_event_record(a, e->stream);
     for (int32_t i = 0; i < iters; i++) {
-        const DpufDevW* w = which == 7 ? &e->lm : &e->lw[(size_t)(start_layer + (i % nl)) * 7 + which];
-        j = job(w, 0, w->n_tiles, e->prep[0], out, w->rows);
-        dpuf_hip_gemv(e->stream, M, 1, &j, NULL, 0.0f);
+        double bb;
+        n = bench_jobs(e, which, start_layer + (i % nl), js, &bb, M);
+        dpuf_hip_gemv(e->stream, M, n, js, NULL, 0.0f);
     }
     dpuf_hip_event_record(b, e->stream);
     float ms = dpuf_hip_event_elapsed_ms(a, b);
     dpuf_hip_event_destroy(a);
     dpuf_hip_event_destroy(b);
-    if (bytes) *bytes = gemv_bytes(w0, 0, w0->n_tiles, M);
+    if (bytes) *bytes = b0;
     if (!dpuf_hip_ok()) return -1.0;
     return (double)ms / iters;
+}
+
+DPUF_EXPORT double dpuf_amd_copy_bench(size_t bytes, int32_t iters) {
+    if (bytes == 0 || iters < 1 || dpuf_hip_device_count() <= 0) return -1.0;
+    void* s = dpuf_hip_stream_create();
+    void* src = dpuf_hip_malloc(bytes);
+    void* dst = dpuf_hip_malloc(bytes);
+    double r = -1.0;
+    if (s && src && dst) {
+        dpuf_hip_fill_zero(src, bytes, s);
+        dpuf_hip_d2d(dst, src, bytes, s);
+        void* a = dpuf_hip_event_create();
+        void* b = dpuf_hip_event_create();
+        dpuf_hip_event_record(a, s);
+        for (int32_t i = 0; i < iters; i++) dpuf_hip_d2d(dst, src, bytes, s);
+        dpuf_hip_event_record(b, s);
+        r = dpuf_hip_event_elapsed_ms(a, b) / iters;
+        dpuf_hip_event_destroy(a);
+        dpuf_hip_event_destroy(b);
+        if (!dpuf_hip_ok()) r = -1.0;
+    }
+    dpuf_hip_free(src);
+    dpuf_hip_free(dst);
+    if (s) dpuf_hip_stream_destroy(s);
+    return r;
 }

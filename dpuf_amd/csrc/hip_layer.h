@@ -13,13 +13,15 @@
 extern "C" {
 #endif
 
-/* One mode 12 matrix resident in HBM: the tile region exactly as stored in
- * the .dpuf blob (tile t at tiles + offs[t]) and its tile offset table. */
+/* One mode 12 matrix resident in HBM in the row-block layout written by
+ * dpuf_hip_relayout: group g (rows 8g .. 8g+7) at g + g * (cols/32) * 144,
+ * holding [cols/32][8] fp16 scales, then per 32-column block 8 rows x 16
+ * bytes of nibbles (row ri's four .dpuf chunk words of the block, in chunk
+ * order). */
 typedef struct {
-    const uint8_t*  tiles;
-    const uint64_t* offs;
+    const uint8_t*  g;
     const uint8_t*  sign;
-    int32_t rows, cols, n_tiles;
+    int32_t rows, cols, n_groups;
 } DpufDevW;
 
 /* Prepped activations of M rows: q int8 [M][K], s f32 [M][K/32], m i32 [M][K/32]. */
@@ -29,11 +31,11 @@ typedef struct {
     int32_t* m;
 } DpufPrep;
 
-/* One matrix of a fused GEMV launch: tiles [t0, t1) of w, reading prep p,
+/* One matrix of a fused GEMV launch: groups [g0, g1) of w, reading prep p,
  * writing out[m * ldo + row]. */
 typedef struct {
     DpufDevW w;
-    int32_t t0, t1;
+    int32_t g0, g1;
     DpufPrep p;
     float* out;
     int32_t ldo;
@@ -78,6 +80,12 @@ void dpuf_hip_resnorm_prep(void* s, int32_t M, int32_t H, float* h, const float*
 void dpuf_hip_prep(void* s, int32_t M, int32_t K, const float* x, const uint8_t* sign, DpufPrep p);
 void dpuf_hip_swiglu_prep(void* s, int32_t M, int32_t I, const float* gate, const float* up,
                           float dz, const uint8_t* sign, DpufPrep p);
+/* .dpuf tile region (tile t at src + offs[t]) -> row-block layout. */
+void dpuf_hip_relayout(void* s, const uint8_t* src, const uint64_t* offs, int32_t n_groups, int32_t n_blk,
+                       uint8_t* dst);
+/* M == 1: GEMV of up to three matrices sharing K, with the activations of
+ * each job in jobs[i].p; a non-NULL skip_flag that reads non-zero makes the
+ * launch write `fill` to every row instead.  M > 1: the slab GEMM. */
 void dpuf_hip_gemv(void* s, int32_t M, int32_t n_jobs, const DpufGemvJob* jobs,
                    const int32_t* skip_flag, float fill);
 void dpuf_hip_qk_rope_kv(void* s, int32_t M, float* q, float* k, const float* v,

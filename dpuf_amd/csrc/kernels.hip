@@ -152,8 +152,8 @@ __global__ void k_embed(DpufDevW w, const int32_t* __restrict__ ids, const float
         for (int i = threadIdx.x; i < H; i += blockDim.x) dst[i] = embeds[(size_t)m * H + i];
         return;
     }
-    const int t = id >> 4, lr = id & 15, rg = lr >> 3, ri = lr & 7;
-    const uint8_t* grp = w.tiles + w.offs[t] + 16 + (size_t)rg * n_blk * 144;
+    const int g = id >> 3, ri = id & 7;
+    const uint8_t* grp = w.g + (size_t)g * n_blk * 144;
     const uint16_t* sc = (const uint16_t*)grp;
     const uint8_t* qg = grp + (size_t)n_blk * 16;
     for (int blk = threadIdx.x; blk < (H >> 6); blk += blockDim.x) {
@@ -162,12 +162,13 @@ __global__ void k_embed(DpufDevW w, const int32_t* __restrict__ ids, const float
         for (int hb = 0; hb < 2; hb++) {
             const int b = 2 * blk + hb;
             const float ws = h2f(sc[b * 8 + ri]);
+            const uint4 rw = *(const uint4*)(qg + (size_t)b * 128 + ri * 16);
+            const uint32_t words[4] = {rw.x, rw.y, rw.z, rw.w};
 #pragma unroll
             for (int c = 0; c < 4; c++) {
-                const uint32_t word = *(const uint32_t*)(qg + (size_t)b * 128 + c * 32 + ri * 4);
 #pragma unroll
                 for (int k = 0; k < 4; k++) {
-                    const uint32_t by = (word >> (8 * k)) & 0xFFu;
+                    const uint32_t by = (words[c] >> (8 * k)) & 0xFFu;
                     v[32 * hb + 8 * c + k] = (float)((int)(by & 15u) - 8) * ws;
                     v[32 * hb + 8 * c + 4 + k] = (float)((int)(by >> 4) - 8) * ws;
                 }
@@ -210,10 +211,13 @@ struct PrepSet {
 DEV float fxor1(float v) { return __int_as_float(dpp_xor1(__float_as_int(v))); }
 DEV float fxor2(float v) { return __int_as_float(dpp_xor2(__float_as_int(v))); }
 
-// sign (.) x for the lane's 16 columns (bit c%8 of byte c/8 set = negate).
-DEV void quad_sign(float* v, const uint8_t* sign, int blk, int qp) {
-    if (!sign) return;
-    const uint32_t sb = *(const uint16_t*)(sign + 8 * blk + 2 * qp);
+// Sign bits of the lane's 16 columns of 64-block blk (bit c%8 of byte c/8
+// set = negate column c).
+DEV uint32_t quad_sign_bits(const uint8_t* sign, int blk, int qp) {
+    return sign ? *(const uint16_t*)(sign + 8 * blk + 2 * qp) : 0u;
+}
+
+DEV void apply_sign_bits(float* v, uint32_t sb) {
 #pragma unroll
     for (int k = 0; k < 16; k++)
         if ((sb >> k) & 1u) v[k] = -v[k];
@@ -317,9 +321,12 @@ __global__ __launch_bounds__(1024) void k_resnorm_prep(int H, float* __restrict_
     __shared__ float part[8];
     const int m = blockIdx.x, t = threadIdx.x, qp = t & 3, blk = t >> 2, nb = H >> 5;
     const int L = (H >> 3) + 4;
-    float v[16];
+    float v[16], wv[16];
+    uint32_t sb[3];
     float* hr = h + (size_t)m * H + 16 * t;
     load16(hr, v);
+    load16(w + 16 * t, wv);
+    for (int p = 0; p < 3; p++) sb[p] = p < ps.n ? quad_sign_bits(ps.sign[p], blk, qp) : 0u;
     if (res) {
         float r[16];
         load16(res + (size_t)m * H + 16 * t, r);
@@ -350,8 +357,6 @@ __global__ __launch_bounds__(1024) void k_resnorm_prep(int H, float* __restrict_
     }
     __syncthreads();
     const float inv = 1.0f / sqrtf(hsum8(part) / (float)H + eps);
-    float wv[16];
-    load16(w + 16 * t, wv);
 #pragma unroll
     for (int k = 0; k < 16; k++) v[k] = (v[k] * inv) * wv[k];
     if (xn_out) store16(xn_out + (size_t)m * H + 16 * t, v);
@@ -359,7 +364,7 @@ __global__ __launch_bounds__(1024) void k_resnorm_prep(int H, float* __restrict_
         float y[16];
 #pragma unroll
         for (int k = 0; k < 16; k++) y[k] = v[k];
-        quad_sign(y, ps.sign[p], blk, qp);
+        apply_sign_bits(y, sb[p]);
         quad_fwht64(y, qp);
         quad_quant_store(y, qp, blk, ps.p[p].q + (size_t)m * H, ps.p[p].s + (size_t)m * nb, ps.p[p].m + (size_t)m * nb);
     }
@@ -373,7 +378,7 @@ __global__ __launch_bounds__(256) void k_prep(int K, const float* __restrict__ x
     const int qp = t & 3, blk = t >> 2, nb = K >> 5;
     float v[16];
     load16(x + (size_t)m * K + 16 * t, v);
-    quad_sign(v, sign, blk, qp);
+    apply_sign_bits(v, quad_sign_bits(sign, blk, qp));
     quad_fwht64(v, qp);
     quad_quant_store(v, qp, blk, p.q + (size_t)m * K, p.s + (size_t)m * nb, p.m + (size_t)m * nb);
 }
@@ -389,6 +394,7 @@ __global__ __launch_bounds__(256) void k_swiglu_prep(int I, const float* __restr
     float g[16], u[16], v[16];
     load16(gate + (size_t)m * I + 16 * t, g);
     load16(up + (size_t)m * I + 16 * t, u);
+    const uint32_t sb = quad_sign_bits(sign, blk, qp);
 #pragma unroll
     for (int k = 0; k < 16; k++) {
         const float ng = fmaxf(-40.0f, fminf(0.0f - g[k], 40.0f));
@@ -397,31 +403,215 @@ __global__ __launch_bounds__(256) void k_swiglu_prep(int I, const float* __restr
         if (dz > 0.0f && !(fabsf(r) >= dz)) r = 0.0f;
         v[k] = r;
     }
-    quad_sign(v, sign, blk, qp);
+    apply_sign_bits(v, sb);
     quad_fwht64(v, qp);
     quad_quant_store(v, qp, blk, p.q + (size_t)m * I, p.s + (size_t)m * nb, p.m + (size_t)m * nb);
 }
 
 // ---------------------------------------------------------------------------
-// Mode 12 GEMV / GEMM.
+// Mode 12 matrices in HBM: the row-block layout.
 //
-// One wave (64 lanes) owns one 8-row group of a tile.  The group is stored as
-// [n_blk x 8 fp16 scales][n_blk x 128 B nibbles]; in 32-byte chunk c of block
-// b, byte ri*4+k holds row ri, column 32b+8c+k (low nibble) and 32b+8c+4+k
-// (high nibble) (reference layout, dpuf_avx2.c:2347-2353).
+// A .dpuf group (8 rows) holds [n_blk][8] fp16 scales, then per 32-column
+// block b four 32-byte chunks; byte ri*4+k of chunk c holds row ri, column
+// 32b+8c+k (low nibble) and 32b+8c+4+k (high nibble) (dpuf_avx2.c:2347-2353).
+// At upload k_relayout stores every group densely (group g of a matrix at
+// g * n_blk * 144; tile headers and padding dropped) and gathers each row's
+// four chunk words of a block into 16 contiguous bytes:
+//   row ri, block b: byte b*128 + ri*16 + 4c + k  <-  .dpuf b*128 + c*32 + ri*4 + k
+// One 16-byte load then gives a lane a whole 32-column row block, and the 64
+// lanes of a wave (lane = 8*bi + ri) read 8 blocks x 8 rows = 1 KB with
+// consecutive addresses.  Scales stay [n_blk][8]: lane (bi, ri) of step s
+// reads scale s*64 + lane.
+// ---------------------------------------------------------------------------
+__global__ void k_relayout(const uint8_t* __restrict__ src, const uint64_t* __restrict__ offs, int n_groups,
+                           int n_blk, uint8_t* __restrict__ dst) {
+    const size_t total = (size_t)n_groups * n_blk * 8;
+    const size_t gbytes = (size_t)n_blk * 144;
+    for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += (size_t)gridDim.x * blockDim.x) {
+        const int g = (int)(idx / ((size_t)n_blk * 8));
+        const int rem = (int)(idx % ((size_t)n_blk * 8));
+        const int b = rem >> 3, ri = rem & 7;
+        const uint8_t* sg = src + offs[g >> 1] + 16 + (size_t)(g & 1) * gbytes;
+        uint8_t* dg = dst + (size_t)g * gbytes;
+        ((uint16_t*)dg)[b * 8 + ri] = ((const uint16_t*)sg)[b * 8 + ri];
+        const uint32_t* sq = (const uint32_t*)(sg + (size_t)n_blk * 16 + (size_t)b * 128);
+        *(uint4*)(dg + (size_t)n_blk * 16 + (size_t)b * 128 + ri * 16) =
+            make_uint4(sq[ri], sq[8 + ri], sq[16 + ri], sq[24 + ri]);
+    }
+}
+
+// Exact integer dot of one row block: 32 nibbles u in [0, 15] against 32 int8
+// activations (x as 8 words, word 2c = columns 8c..8c+3, word 2c+1 = 8c+4..8c+7).
+// Equals the reference's maddubs/madd sum (dpuf_avx2.c:2623-2632), whose int16
+// partials cannot overflow (|sum| <= 30480).
+DEV int row_block_dot(uint4 w, int4 xa, int4 xb) {
+    const uint32_t m = 0x0F0F0F0Fu;
+    int d = __builtin_amdgcn_sdot4((int)(w.x & m), xa.x, 0, false);
+    d = __builtin_amdgcn_sdot4((int)((w.x >> 4) & m), xa.y, d, false);
+    d = __builtin_amdgcn_sdot4((int)(w.y & m), xa.z, d, false);
+    d = __builtin_amdgcn_sdot4((int)((w.y >> 4) & m), xa.w, d, false);
+    d = __builtin_amdgcn_sdot4((int)(w.z & m), xb.x, d, false);
+    d = __builtin_amdgcn_sdot4((int)((w.z >> 4) & m), xb.y, d, false);
+    d = __builtin_amdgcn_sdot4((int)(w.w & m), xb.z, d, false);
+    d = __builtin_amdgcn_sdot4((int)((w.w >> 4) & m), xb.w, d, false);
+    return d;
+}
+
+DEV uint4 nt_load16(const uint8_t* p) {
+    const u32x4 v = __builtin_nontemporal_load((const u32x4*)p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// Per-row fp32 chain acc = fma(float(D - sum8), ws * xs, acc) over blocks in
+// ascending order (dpuf_avx2.c:2633-2635); `row` holds (dcf, sp) pairs, two
+// per float4, n_blk even.  Pairs are read in batches of 16 with the next
+// batch in flight while the current one is consumed, so LDS latency stays
+// off the dependent FMA chain.
+DEV void chain8(const float4* e, float& acc) {
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        acc = fmaf(e[i].x, e[i].y, acc);
+        acc = fmaf(e[i].z, e[i].w, acc);
+    }
+}
+
+DEV float run_chain(const float4* row, int n2) {
+    float acc = 0.0f;
+    int k = 0;
+    if (n2 >= 16) {
+        float4 cur[8], nxt[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) cur[i] = row[i];
+        for (k = 8; k + 8 <= n2; k += 8) {
+#pragma unroll
+            for (int i = 0; i < 8; i++) nxt[i] = row[k + i];
+            chain8(cur, acc);
+#pragma unroll
+            for (int i = 0; i < 8; i++) cur[i] = nxt[i];
+        }
+        chain8(cur, acc);
+    }
+    for (; k < n2; k++) {
+        const float4 e = row[k];
+        acc = fmaf(e.x, e.y, acc);
+        acc = fmaf(e.z, e.w, acc);
+    }
+    return acc;
+}
+
+// ---------------------------------------------------------------------------
+// M == 1 GEMV, one 8-row group per workgroup of MV_NW waves (split over K).
 //
-// Per step the wave streams 8 blocks = 1 KB of nibbles with one coalesced
-// 16-byte load per lane: lane = bi*8 + h*4 + c holds chunk c of block b0+bi,
-// rows 4h..4h+3.  Each lane forms 4 exact int32 row dots with sdot4, the
-// quad (c = 0..3) is reduced with two DPP adds, and lane (bi, h, c) keeps
-// row 4h+c.  The per-row fp32 chain acc = fma(float(D - sum8), ws * xs, acc)
-// must run over blocks in ascending order (dpuf_avx2.c:2633-2635), so the
-// (D, ws*xs) pairs go through LDS to the chain lanes.
-//
-// k_gemv1: M == 1, blocks with xs <= 0 are skipped (dpuf_avx2.c:2621-2622).
-// k_gemm8: up to 8 tokens per wave, every block accumulated (slab path,
-//          dpuf_avx2.c:2643-2676); the 64 lanes then run 8 rows x 8 tokens
-//          chains.
+// A step is 8 blocks x 8 rows = 1 KB of nibbles, one 16-byte load per lane
+// (lane = 8*bi + ri: row ri of block 8s + bi).  In each round every wave owns
+// MV_NL consecutive steps and issues all of their loads (nibbles, scales and
+// the block's 32 activation bytes, scale and sum) before consuming any.  Dots
+// go to LDS as (float(D - sum8), ws * xs) pairs [row][block]; after one
+// barrier lanes 0..7 run the per-row chains.  Blocks whose activation scale is
+// <= 0 contribute nothing, as the M == 1 reference skips them
+// (dpuf_avx2.c:2621-2622).  Eight waves with two steps each keep enough
+// loads in flight per CU; the group count (rows / 8) gives the parallelism.
+// ---------------------------------------------------------------------------
+#define MV_NW 8
+#define MV_NL 2
+
+struct MvJob {
+    const uint8_t* g;  // dense groups of the matrix (row-block layout)
+    float* out;        // row r of the matrix -> out[r]
+    int g0, g1;        // groups computed by this launch
+    int rows;
+    DpufPrep x;        // prepped activations (row 0)
+};
+
+struct MvArgs {
+    MvJob j[3];
+    int n_jobs;
+    int gb[4];              // prefix sums of (g1 - g0)
+    int K;
+    const int32_t* skip_flag;
+    float fill;
+};
+
+DEV int find_mv_job(const MvArgs& A, int g) {
+    int j = 0;
+    if (A.n_jobs > 1 && g >= A.gb[1]) j = 1;
+    if (A.n_jobs > 2 && g >= A.gb[2]) j = 2;
+    return j;
+}
+
+__global__ __launch_bounds__(MV_NW * 64) void k_mv(MvArgs A) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int ji = find_mv_job(A, blockIdx.x);
+    const MvJob& J = A.j[ji];
+    const int g = J.g0 + (blockIdx.x - A.gb[ji]);
+    const int tid = threadIdx.x;
+    const int r0 = g * 8;
+    const int n8 = J.rows - r0 < 8 ? J.rows - r0 : 8;
+    if (A.skip_flag && *A.skip_flag) {
+        if (tid < n8) J.out[r0 + tid] = A.fill;
+        return;
+    }
+    const int K = A.K, n_blk = K >> 5, S = (n_blk + 7) >> 3, ld = n_blk + 2;
+    const int w = tid >> 6, lane = tid & 63, bi = lane >> 3, ri = lane & 7;
+    const uint8_t* grp = J.g + (size_t)g * n_blk * 144;
+    const uint16_t* sc = (const uint16_t*)grp;
+    const uint8_t* qg = grp + (size_t)n_blk * 16;
+    float2* pairs = (float2*)smem;  // [8][ld]
+    const DpufPrep P = J.x;
+
+    for (int base = 0; base < S; base += MV_NW * MV_NL) {
+        uint4 wq[MV_NL];
+        uint32_t wsr[MV_NL];
+        int4 xa[MV_NL], xb[MV_NL];
+        float xs[MV_NL];
+        int32_t xm[MV_NL];
+#pragma unroll
+        for (int i = 0; i < MV_NL; i++) {
+            const int s = base + w * MV_NL + i, b = s * 8 + bi;
+            if (s < S && b < n_blk) {
+                wq[i] = nt_load16(qg + (size_t)s * 1024 + lane * 16);
+                wsr[i] = sc[(size_t)s * 64 + lane];
+                xa[i] = *(const int4*)(P.q + b * 32);
+                xb[i] = *(const int4*)(P.q + b * 32 + 16);
+                xs[i] = P.s[b];
+                xm[i] = P.m[b];
+            } else {
+                wq[i] = make_uint4(0u, 0u, 0u, 0u);
+                wsr[i] = 0u;
+                xa[i] = xb[i] = make_int4(0, 0, 0, 0);
+                xs[i] = 0.0f;
+                xm[i] = 0;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < MV_NL; i++) {
+            const int s = base + w * MV_NL + i;
+            if (s >= S) break;  // wave-uniform
+            const int b = s * 8 + bi;
+            if (b < n_blk) {
+                const int dot = row_block_dot(wq[i], xa[i], xb[i]);
+                float dcf = 0.0f, sp = 0.0f;
+                if (xs[i] > 0.0f) {
+                    dcf = (float)(dot - xm[i]);
+                    sp = h2f((uint16_t)wsr[i]) * xs[i];
+                }
+                pairs[ri * ld + b] = make_float2(dcf, sp);
+            }
+        }
+    }
+    __syncthreads();
+    if (tid < 8) {
+        const float acc = run_chain((const float4*)(pairs + tid * ld), n_blk >> 1);
+        if (tid < n8) J.out[r0 + tid] = acc;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// M > 1 GEMM (slab path, dpuf_avx2.c:2643-2676): one 8-row group and up to 8
+// tokens per wave; lane (bi, ri) holds row ri of block b0+bi and forms its
+// dot for each token; every block is accumulated (no skip), as in the slab
+// kernels.  Chain lanes (token cm, row cr) run the 8 x 8 chains.
 // ---------------------------------------------------------------------------
 struct GemvBatch {
     DpufGemvJob j[3];
@@ -436,192 +626,21 @@ DEV int find_job(const GemvBatch& B, int g) {
     return j;
 }
 
-
-// Locates group g of a job: tile pointer, first row, rows in the group.
-// Returns false when the group does not exist (second group of a short tile).
-DEV bool group_of(const DpufGemvJob& J, int g, const uint8_t*& grp, int& r0, int& n8) {
-    const int t = J.t0 + (g >> 1), rg = g & 1;
-    const uint8_t* tp = J.w.tiles + J.w.offs[t];
-    const int n_r = *(const uint16_t*)(tp + 4);
-    if (rg * 8 >= n_r) return false;
-    const int n_blk = J.w.cols >> 5;
-    grp = tp + 16 + (size_t)rg * n_blk * 144;
-    r0 = t * 16 + rg * 8;
-    n8 = n_r - rg * 8 < 8 ? n_r - rg * 8 : 8;
-    return true;
-}
-
-// Integer part for one lane: 4 row dots (rows 4h..4h+3) of one chunk against
-// 8 int8 activations, quad-reduced; returns the dot of row 4h+c.
-DEV int lane_row_dot(uint4 wq, int2 xw, int c) {
-    int d0 = __builtin_amdgcn_sdot4((int)(wq.x & 0x0F0F0F0Fu), xw.x, 0, false);
-    int d1 = __builtin_amdgcn_sdot4((int)(wq.y & 0x0F0F0F0Fu), xw.x, 0, false);
-    int d2 = __builtin_amdgcn_sdot4((int)(wq.z & 0x0F0F0F0Fu), xw.x, 0, false);
-    int d3 = __builtin_amdgcn_sdot4((int)(wq.w & 0x0F0F0F0Fu), xw.x, 0, false);
-    d0 = __builtin_amdgcn_sdot4((int)((wq.x >> 4) & 0x0F0F0F0Fu), xw.y, d0, false);
-    d1 = __builtin_amdgcn_sdot4((int)((wq.y >> 4) & 0x0F0F0F0Fu), xw.y, d1, false);
-    d2 = __builtin_amdgcn_sdot4((int)((wq.z >> 4) & 0x0F0F0F0Fu), xw.y, d2, false);
-    d3 = __builtin_amdgcn_sdot4((int)((wq.w >> 4) & 0x0F0F0F0Fu), xw.y, d3, false);
-    d0 += dpp_xor1(d0); d1 += dpp_xor1(d1); d2 += dpp_xor1(d2); d3 += dpp_xor1(d3);
-    d0 += dpp_xor2(d0); d1 += dpp_xor2(d1); d2 += dpp_xor2(d2); d3 += dpp_xor2(d3);
-    return c == 0 ? d0 : (c == 1 ? d1 : (c == 2 ? d2 : d3));
-}
-
-__global__ __launch_bounds__(64) void k_gemv1(GemvBatch B, const int32_t* __restrict__ skip_flag, float fill) {
-    __shared__ float2 st[8][8];
-    const int ji = find_job(B, blockIdx.x);
-    const DpufGemvJob& J = B.j[ji];
-    const uint8_t* grp;
-    int r0, n8;
-    if (!group_of(J, blockIdx.x - B.g_begin[ji], grp, r0, n8)) return;
-    const int lane = threadIdx.x;
-    if (skip_flag && *skip_flag) {
-        if (lane < n8) J.out[r0 + lane] = fill;
-        return;
-    }
-    const int n_blk = J.w.cols >> 5;
-    const uint16_t* sc = (const uint16_t*)grp;
-    const uint8_t* qg = grp + (size_t)n_blk * 16;
-    const int bi = lane >> 3, h = (lane >> 2) & 1, c = lane & 3, rr = 4 * h + c;
-    float acc = 0.0f;
-    for (int b0 = 0; b0 < n_blk; b0 += 8) {
-        const int b = b0 + bi;
-        float dcf = 0.0f, sp = 0.0f;
-        if (b < n_blk) {
-            const uint4 wq = *(const uint4*)(qg + (size_t)b * 128 + c * 32 + h * 16);
-            const int2 xw = *(const int2*)(J.p.q + b * 32 + c * 8);
-            const int dot = lane_row_dot(wq, xw, c);
-            const float bs = J.p.s[b];
-            if (bs > 0.0f) {
-                dcf = (float)(dot - J.p.m[b]);
-                sp = h2f(sc[b * 8 + rr]) * bs;
-            }
-        }
-        st[rr][bi] = make_float2(dcf, sp);
-        __syncthreads();
-        if (lane < 8) {
-#pragma unroll
-            for (int k = 0; k < 8; k++) {
-                const float2 e = st[lane][k];
-                if (b0 + k < n_blk) acc = fmaf(e.x, e.y, acc);
-            }
-        }
-        __syncthreads();
-    }
-    if (lane < n8) J.out[r0 + lane] = acc;
-}
-
-// M == 1 decode GEMV, one 8-row group per workgroup of 4 waves.
-//
-// The group's K blocks are split over the 4 waves in steps of 8 blocks (1 KB
-// of nibbles per wave-wide 16-byte load).  Each wave first issues ALL of its
-// nibble and scale loads (NL steps in flight per lane, so a workgroup keeps
-// up to 4 * NL KB of weights in flight), then forms the exact integer dots.
-// The (float(D - sum8), ws * xs) pairs land in LDS as [row][block]; after one
-// barrier lanes 0..7 run the per-row fp32 FMA chains in ascending block order
-// (dpuf_avx2.c:2620-2636), reading two pairs per 16-byte LDS load.  The row
-// stride n_blk + 2 keeps those 8 lanes on distinct banks.
-template <int NL>
-__global__ __launch_bounds__(256) void k_gemv1w(GemvBatch B, const int32_t* __restrict__ skip_flag, float fill) {
-    extern __shared__ float2 pairs[];
-    const int ji = find_job(B, blockIdx.x);
-    const DpufGemvJob& J = B.j[ji];
-    const uint8_t* grp;
-    int r0, n8;
-    if (!group_of(J, blockIdx.x - B.g_begin[ji], grp, r0, n8)) return;
-    const int tid = threadIdx.x;
-    if (skip_flag && *skip_flag) {
-        if (tid < n8) J.out[r0 + tid] = fill;
-        return;
-    }
-    const int n_blk = J.w.cols >> 5, S = (n_blk + 7) >> 3, ld = n_blk + 2;
-    const int w = tid >> 6, lane = tid & 63;
-    const int bi = lane >> 3, h = (lane >> 2) & 1, c = lane & 3, rr = 4 * h + c;
-    const uint16_t* sc = (const uint16_t*)grp;
-    const uint8_t* qg = grp + (size_t)n_blk * 16;
-    for (int base = 0; base < S; base += 4 * NL) {
-        const int s0 = base + w * NL;
-        // every load of this pass (weights, scales and the matching
-        // activations) is issued before the first one is consumed
-        uint4 wq[NL];
-        int2 xw[NL];
-        float xs[NL];
-        int32_t xm[NL];
-        uint32_t wsr[NL];
-#pragma unroll
-        for (int i = 0; i < NL; i++) {
-            const int s = s0 + i, b = s * 8 + bi;
-            if (s < S && b < n_blk) {
-                const u32x4 v = __builtin_nontemporal_load((const u32x4*)(qg + (size_t)b * 128 + c * 32 + h * 16));
-                wq[i] = make_uint4(v.x, v.y, v.z, v.w);
-                wsr[i] = sc[(size_t)b * 8 + rr];
-                xw[i] = *(const int2*)(J.p.q + b * 32 + c * 8);
-                xs[i] = J.p.s[b];
-                xm[i] = J.p.m[b];
-            } else {
-                wq[i] = make_uint4(0u, 0u, 0u, 0u);
-                wsr[i] = 0u;
-                xw[i] = make_int2(0, 0);
-                xs[i] = 0.0f;
-                xm[i] = 0;
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < NL; i++) {
-            const int s = s0 + i;
-            if (s >= S) break;  // wave-uniform
-            const int b = s * 8 + bi;
-            const int dot = lane_row_dot(wq[i], xw[i], c);
-            if (b < n_blk) {
-                float dcf = 0.0f, sp = 0.0f;
-                if (xs[i] > 0.0f) {
-                    dcf = (float)(dot - xm[i]);
-                    sp = h2f((uint16_t)wsr[i]) * xs[i];
-                }
-                pairs[rr * ld + b] = make_float2(dcf, sp);
-            }
-        }
-    }
-    __syncthreads();
-    if (tid < 8) {
-        const float4* row = (const float4*)(pairs + tid * ld);
-        float acc = 0.0f;
-        const int n2 = n_blk >> 1;
-        int k = 0;
-        for (; k + 4 <= n2; k += 4) {
-            const float4 e0 = row[k], e1 = row[k + 1], e2 = row[k + 2], e3 = row[k + 3];
-            acc = fmaf(e0.x, e0.y, acc);
-            acc = fmaf(e0.z, e0.w, acc);
-            acc = fmaf(e1.x, e1.y, acc);
-            acc = fmaf(e1.z, e1.w, acc);
-            acc = fmaf(e2.x, e2.y, acc);
-            acc = fmaf(e2.z, e2.w, acc);
-            acc = fmaf(e3.x, e3.y, acc);
-            acc = fmaf(e3.z, e3.w, acc);
-        }
-        for (; k < n2; k++) {
-            const float4 e = row[k];
-            acc = fmaf(e.x, e.y, acc);
-            acc = fmaf(e.z, e.w, acc);
-        }
-        if (tid < n8) J.out[r0 + tid] = acc;
-    }
-}
-
 __global__ __launch_bounds__(64) void k_gemm8(GemvBatch B, int M) {
     __shared__ float2 st[8][8][8];  // [token][row][block]
     const int ji = find_job(B, blockIdx.x);
     const DpufGemvJob& J = B.j[ji];
-    const uint8_t* grp;
-    int r0, n8;
-    if (!group_of(J, blockIdx.x - B.g_begin[ji], grp, r0, n8)) return;
+    const int g = J.g0 + (blockIdx.x - B.g_begin[ji]);
+    const int r0 = g * 8;
+    const int n8 = J.w.rows - r0 < 8 ? J.w.rows - r0 : 8;
     const int m0 = blockIdx.y * 8;
     const int mt = M - m0 < 8 ? M - m0 : 8;
     const int K = J.w.cols, n_blk = K >> 5;
+    const uint8_t* grp = J.w.g + (size_t)g * n_blk * 144;
     const uint16_t* sc = (const uint16_t*)grp;
     const uint8_t* qg = grp + (size_t)n_blk * 16;
     const int lane = threadIdx.x;
-    const int bi = lane >> 3, h = (lane >> 2) & 1, c = lane & 3, rr = 4 * h + c;
+    const int bi = lane >> 3, ri = lane & 7;
     const int cm = lane >> 3, cr = lane & 7;  // chain lane: token cm, row cr
     float acc = 0.0f;
     for (int b0 = 0; b0 < n_blk; b0 += 8) {
@@ -629,19 +648,19 @@ __global__ __launch_bounds__(64) void k_gemm8(GemvBatch B, int M) {
         uint4 wq = make_uint4(0, 0, 0, 0);
         float ws = 0.0f;
         if (b < n_blk) {
-            wq = *(const uint4*)(qg + (size_t)b * 128 + c * 32 + h * 16);
-            ws = h2f(sc[b * 8 + rr]);
+            wq = *(const uint4*)(qg + (size_t)b * 128 + ri * 16);
+            ws = h2f(sc[b * 8 + ri]);
         }
         for (int mi = 0; mi < mt; mi++) {
             const int m = m0 + mi;
             float dcf = 0.0f, sp = 0.0f;
             if (b < n_blk) {
-                const int2 xw = *(const int2*)(J.p.q + (size_t)m * K + b * 32 + c * 8);
-                const int dot = lane_row_dot(wq, xw, c);
+                const int8_t* xq = J.p.q + (size_t)m * K + b * 32;
+                const int dot = row_block_dot(wq, *(const int4*)xq, *(const int4*)(xq + 16));
                 dcf = (float)(dot - J.p.m[(size_t)m * n_blk + b]);
                 sp = ws * J.p.s[(size_t)m * n_blk + b];
             }
-            st[mi][rr][bi] = make_float2(dcf, sp);
+            st[mi][ri][bi] = make_float2(dcf, sp);
         }
         __syncthreads();
         if (cm < mt) {
@@ -857,17 +876,18 @@ __global__ __launch_bounds__(256) void k_attn(const float* __restrict__ q, const
 // 2 * HD columns.
 //
 // Arithmetic follows gqa_attn_head_pair_f32 (dpuf_engine.c:341-577) term by
-// term: each score is 8 lane-accumulators (lane j: elements j, j+8, ... in
-// order) reduced by the reference's hadd / hsum tree (here a 3-step xor
-// butterfly whose adds are exactly the tree's), the exp polynomial with the
-// libm expf tail, the 8-lane softmax sum, and the per-output P.V FMA chains.
+// term.  A score's 8 lane-accumulators (accumulator j: elements j, j+8, ...,
+// in order) are split over 2 lanes (lane h holds accumulators 4h .. 4h+3, fed
+// by float4 loads of elements 8i + 4h), and the reference's hadd / hsum trees
+// are evaluated on them with the same pairings.  Then the exp polynomial with
+// the libm expf tail, the 8-lane softmax sum and the per-output P.V chains.
 //
-// Latency: the K rows of the first 128 positions are loaded into registers
-// (8 lanes per key, 16 floats each) and the first V_ROWS rows of V are copied
-// straight into LDS (global_load_lds, 1 KB per wave instruction) at kernel
-// entry, so both streams are in flight while the norms and RoPE run.
+// Latency: the K rows of the first ATT_KEYS positions are loaded into
+// registers and the first V_ROWS rows of V are copied straight into LDS
+// (global_load_lds, 1 KB per wave instruction) at kernel entry, so both
+// streams are in flight while the norms and RoPE run.
 // ---------------------------------------------------------------------------
-#define ATT_KEYS 128  // keys whose K rows are loaded per round (32 keys x 4 passes)
+#define ATT_KEYS 128  // keys per pass: 2 lanes per key, 256 threads
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
@@ -884,8 +904,7 @@ __global__ __launch_bounds__(256) void k_attn_dec(const float* __restrict__ q, c
                                                   float* __restrict__ ao, const uint8_t* __restrict__ o_sign,
                                                   DpufPrep op) {
     constexpr int V_ROWS = 16384 / HD;  // 64 KB of V rows per LDS chunk
-    constexpr int NQ8 = HD / 8;         // elements per accumulator lane
-    constexpr int KP = ATT_KEYS / 32;
+    constexpr int NI = HD / 8;          // float4 steps per key and lane
     constexpr int half = HD / 2;
     extern __shared__ float sm[];
     float* vst = sm;                    // [V_ROWS][HD], 1 KB aligned
@@ -895,7 +914,7 @@ __global__ __launch_bounds__(256) void k_attn_dec(const float* __restrict__ q, c
     float* aout = vn + HD;              // [2][HD]
     float* scl = aout + 2 * HD;         // [max(2 * sc_cap, 3 * HD)]
     __shared__ float part[3][8];
-    __shared__ float red[2][256];
+    __shared__ float red[2][4];
     __shared__ float vs8[2][8];
     __shared__ float inv_sh[2];
     const int kvh = blockIdx.x, gp = blockIdx.y, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -903,10 +922,40 @@ __global__ __launch_bounds__(256) void k_attn_dec(const float* __restrict__ q, c
     const bool pair = (g0 + 1 < groups);
     const int nh = pair ? 2 : 1;
     const int qh0 = kvh * groups + g0;
-    const int pos = *pos0p;
-    const int kv_len = pos + 1;
     const float* Kc = kc + (size_t)kvh * max_seq * HD;
     const float* Vc = vc + (size_t)kvh * max_seq * HD;
+
+    // Every load that does not depend on the position is issued first, so
+    // the kernel waits for one memory round trip before the position-
+    // dependent ones (K rows, V rows, RoPE tables) and one after.
+    // Thread tid owns normalised elements e = tid + 256 * r of [q0 | q1 | k].
+    constexpr int NE = (3 * HD + 255) / 256;
+    float xe[NE], we[NE];
+#pragma unroll
+    for (int r = 0; r < NE; r++) {
+        const int e = tid + 256 * r, vi = e / HD, i = e % HD;
+        xe[r] = 0.0f;
+        we[r] = 1.0f;
+        if (e < 3 * HD && (vi != 1 || pair)) {
+            xe[r] = vi == 2 ? k[(size_t)kvh * HD + i] : q[(size_t)(qh0 + vi) * HD + i];
+            const float* nw = vi == 2 ? kn : qn;
+            if (nw) we[r] = nw[i];
+        }
+    }
+    constexpr int NV = (HD + 255) / 256;
+    float vv0[NV];
+#pragma unroll
+    for (int r = 0; r < NV; r++) {
+        const int i = tid + 256 * r;
+        vv0[r] = i < HD ? v[(size_t)kvh * HD + i] : 0.0f;
+    }
+    uint32_t osb = 0;
+    if (tid < nh * HD / 16) {
+        const int blk = (qh0 * HD) / 64 + (tid >> 2);
+        if (o_sign) osb = *(const uint16_t*)(o_sign + 8 * blk + 2 * (tid & 3));
+    }
+    const int pos = *pos0p;
+    const int kv_len = pos + 1;
 
     // V rows [c0, c0 + V_ROWS) -> vst, 1 KB per wave instruction; rows past
     // the cache end are redirected to row 0 (never read back).
@@ -920,35 +969,45 @@ __global__ __launch_bounds__(256) void k_attn_dec(const float* __restrict__ q, c
                                              (lds_ptr_t)(vst + ii * 256), 16, 0, 0);
         }
     };
-    if (pos > 0) stage_v(0);
-
-    // K rows of keys kq + 32p (p < KP): lane j holds elements j, j+8, ...
-    const int kq = tid >> 3, j = tid & 7;
-    float kr[KP][NQ8];
+    // key kq (one per lane pair) of each pass; lane h holds elements 8i + 4h .. +3
+    const int kq = tid >> 1, h = tid & 1;
+    float4 kr[NI];
     auto load_k = [&](int t0) {
+        const int t = t0 + kq;
+        const bool ok = t < pos;
+        const float4* kp = (const float4*)(Kc + (size_t)(ok ? t : 0) * HD + 4 * h);
 #pragma unroll
-        for (int p = 0; p < KP; p++) {
-            const int t = t0 + kq + 32 * p;
-            const bool ok = t < pos;
-#pragma unroll
-            for (int i = 0; i < NQ8; i++) kr[p][i] = ok ? Kc[(size_t)t * HD + j + 8 * i] : 0.0f;
-        }
+        for (int i = 0; i < NI; i++) kr[i] = ok ? kp[2 * i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     };
+    // RoPE table entries of the owned elements
+    const float* c_row = cos_tab + (size_t)pos * half;
+    const float* s_row = sin_tab + (size_t)pos * half;
+    float ce[NE], se[NE];
+#pragma unroll
+    for (int r = 0; r < NE; r++) {
+        const int i = (tid + 256 * r) % HD, j = i < half ? i : i - half;
+        ce[r] = c_row[j];
+        se[r] = s_row[j];
+    }
+    if (pos > 0) stage_v(0);
     load_k(0);
 
-    // stage the raw vectors: q0, q1, k, v
     float* tmp = scl;  // [3][HD] normalised vectors, before the scores use this space
-    for (int i = tid; i < HD; i += 256) {
-        qs[i] = q[(size_t)qh0 * HD + i];
-        if (pair) qs[HD + i] = q[(size_t)(qh0 + 1) * HD + i];
-        ks[i] = k[(size_t)kvh * HD + i];
-        vn[i] = v[(size_t)kvh * HD + i];
+#pragma unroll
+    for (int r = 0; r < NE; r++) {
+        const int e = tid + 256 * r;
+        if (e < 3 * HD) tmp[e] = xe[r];
+    }
+#pragma unroll
+    for (int r = 0; r < NV; r++) {
+        const int i = tid + 256 * r;
+        if (i < HD) vn[i] = vv0[r];
     }
     __syncthreads();
     // QK-norm (rms_norm_f32 over hd: 8 FMA lanes + hsum tree), vectors 0 = q0, 1 = q1, 2 = k
     if (tid < 24) {
         const int vi = tid >> 3, jj = tid & 7;
-        const float* vec = vi == 2 ? ks : qs + vi * HD;
+        const float* vec = tmp + vi * HD;
         const float* nw = vi == 2 ? kn : qn;
         if ((vi != 1 || pair) && nw) {
             float a = 0.0f;
@@ -957,29 +1016,24 @@ __global__ __launch_bounds__(256) void k_attn_dec(const float* __restrict__ q, c
         }
     }
     __syncthreads();
-    for (int e = tid; e < 3 * HD; e += 256) {
-        const int vi = e / HD, i = e % HD;
-        if (vi == 1 && !pair) continue;
-        const float* vec = vi == 2 ? ks : qs + vi * HD;
-        const float* nw = vi == 2 ? kn : qn;
-        float x = vec[i];
-        if (nw) {
+#pragma unroll
+    for (int r = 0; r < NE; r++) {
+        const int e = tid + 256 * r, vi = e / HD;
+        if (e < 3 * HD && (vi != 1 || pair) && (vi == 2 ? kn : qn)) {
             const float inv = 1.0f / sqrtf(hsum8(part[vi]) / (float)HD + eps);
-            x = (x * inv) * nw[i];
+            tmp[e] = (xe[r] * inv) * we[r];
         }
-        tmp[e] = x;
     }
     __syncthreads();
     // NeoX RoPE (apply_rope_neox_f32, dpuf_engine.c:274-295)
-    const float* c_row = cos_tab + (size_t)pos * half;
-    const float* s_row = sin_tab + (size_t)pos * half;
-    for (int e = tid; e < 3 * HD; e += 256) {
-        const int vi = e / HD, i = e % HD;
-        if (vi == 1 && !pair) continue;
+#pragma unroll
+    for (int r = 0; r < NE; r++) {
+        const int e = tid + 256 * r, vi = e / HD, i = e % HD;
+        if (e >= 3 * HD || (vi == 1 && !pair)) continue;
         const float* x = tmp + vi * HD;
         float o;
-        if (i < half) o = fmaf(x[i], c_row[i], -(x[i + half] * s_row[i]));
-        else o = fmaf(x[i], c_row[i - half], x[i - half] * s_row[i - half]);
+        if (i < half) o = fmaf(x[i], ce[r], -(x[i + half] * se[r]));
+        else o = fmaf(x[i], ce[r], x[i - half] * se[r]);
         if (vi == 2) ks[i] = o;
         else qs[vi * HD + i] = o;
     }
@@ -995,77 +1049,80 @@ __global__ __launch_bounds__(256) void k_attn_dec(const float* __restrict__ q, c
     float* sc0 = kv_len <= sc_cap ? scl : scores_g + (size_t)qh0 * max_seq;
     float* sc1 = kv_len <= sc_cap ? scl + sc_cap : sc0 + max_seq;
     const int n4 = kv_len & ~3;
-    float qv0[NQ8], qv1[NQ8];
-#pragma unroll
-    for (int i = 0; i < NQ8; i++) {
-        qv0[i] = qs[j + 8 * i];
-        qv1[i] = pair ? qs[HD + j + 8 * i] : 0.0f;
-    }
     float mx0 = -1e30f, mx1 = -1e30f;
     for (int t0 = 0; t0 < kv_len; t0 += ATT_KEYS) {
         if (t0 > 0) load_k(t0);
+        const int t = t0 + kq;
+        if (t == pos) {
 #pragma unroll
-        for (int p = 0; p < KP; p++) {
-            const int t = t0 + kq + 32 * p;
-            if (t0 + 32 * p >= kv_len) break;  // uniform over the workgroup
-            float kv[NQ8];
+            for (int i = 0; i < NI; i++) kr[i] = *(const float4*)(ks + 8 * i + 4 * h);
+        }
+        // accumulators 4h .. 4h+3 of both heads
+        float a[4] = {0.0f, 0.0f, 0.0f, 0.0f}, b[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        float c[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // single-head tail: dot_f32_avx2's second accumulator
+        const bool tail1 = !pair && t >= n4;
 #pragma unroll
-            for (int i = 0; i < NQ8; i++) kv[i] = (t == pos) ? ks[j + 8 * i] : kr[p][i];
-            float s0, s1 = 0.0f;
-            if (pair || t < n4) {
-                // one accumulator lane per head: a_j = sum_i q[j+8i] k[j+8i] in order
-                float a0 = 0.0f, a1 = 0.0f;
-#pragma unroll
-                for (int i = 0; i < NQ8; i++) {
-                    a0 = fmaf(qv0[i], kv[i], a0);
-                    a1 = fmaf(qv1[i], kv[i], a1);
-                }
-                if (t < n4) {  // hsum4_256_ps tree: ((a0+a1)+(a2+a3)) + ((a4+a5)+(a6+a7))
-                    a0 = a0 + shx(a0, 1); a1 = a1 + shx(a1, 1);
-                    a0 = a0 + shx(a0, 2); a1 = a1 + shx(a1, 2);
-                    a0 = a0 + shx(a0, 4); a1 = a1 + shx(a1, 4);
-                } else {       // eng_hsum256_ps tree: ((a0+a4)+(a1+a5)) + ((a2+a6)+(a3+a7))
-                    a0 = a0 + shx(a0, 4); a1 = a1 + shx(a1, 4);
-                    a0 = a0 + shx(a0, 1); a1 = a1 + shx(a1, 1);
-                    a0 = a0 + shx(a0, 2); a1 = a1 + shx(a1, 2);
-                }
-                s0 = a0 * scale;
-                s1 = a1 * scale;
+        for (int i = 0; i < NI; i++) {
+            const float4 q0 = *(const float4*)(qs + 8 * i + 4 * h);
+            const float4 kk = kr[i];
+            if (tail1 && (i & 1)) {
+                c[0] = fmaf(q0.x, kk.x, c[0]); c[1] = fmaf(q0.y, kk.y, c[1]);
+                c[2] = fmaf(q0.z, kk.z, c[2]); c[3] = fmaf(q0.w, kk.w, c[3]);
             } else {
-                // single-head tail: dot_f32_avx2's two interleaved accumulators
-                float a0 = 0.0f, b0 = 0.0f;
+                a[0] = fmaf(q0.x, kk.x, a[0]); a[1] = fmaf(q0.y, kk.y, a[1]);
+                a[2] = fmaf(q0.z, kk.z, a[2]); a[3] = fmaf(q0.w, kk.w, a[3]);
+            }
+            if (pair) {
+                const float4 q1 = *(const float4*)(qs + HD + 8 * i + 4 * h);
+                b[0] = fmaf(q1.x, kk.x, b[0]); b[1] = fmaf(q1.y, kk.y, b[1]);
+                b[2] = fmaf(q1.z, kk.z, b[2]); b[3] = fmaf(q1.w, kk.w, b[3]);
+            }
+        }
+        float s0, s1 = 0.0f;
+        if (t < n4) {
+            // hsum4_256_ps: ((a0+a1)+(a2+a3)) + ((a4+a5)+(a6+a7)); lane 0 holds a0..a3
+            const float l0 = (a[0] + a[1]) + (a[2] + a[3]);
+            const float l1 = (b[0] + b[1]) + (b[2] + b[3]);
+            const float o0 = shx(l0, 1), o1 = shx(l1, 1);
+            s0 = (h ? o0 + l0 : l0 + o0) * scale;
+            s1 = (h ? o1 + l1 : l1 + o1) * scale;
+        } else {
+            if (tail1) {
 #pragma unroll
-                for (int i = 0; i < NQ8; i += 2) {
-                    a0 = fmaf(qv0[i], kv[i], a0);
-                    if (i + 1 < NQ8) b0 = fmaf(qv0[i + 1], kv[i + 1], b0);
-                }
-                float c = a0 + b0;
-                c = c + shx(c, 4);
-                c = c + shx(c, 1);
-                c = c + shx(c, 2);
-                s0 = c * scale;
+                for (int jj = 0; jj < 4; jj++) a[jj] = a[jj] + c[jj];
             }
-            if (t < kv_len) {
-                if (j == 0) {
-                    sc0[t] = s0;
-                    if (pair) sc1[t] = s1;
-                }
-                mx0 = s0 > mx0 ? s0 : mx0;
-                mx1 = s1 > mx1 ? s1 : mx1;
+            // eng_hsum256_ps: ((a0+a4)+(a1+a5)) + ((a2+a6)+(a3+a7))
+            float u[4], ub[4];
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++) {
+                const float pa = shx(a[jj], 1), pb = shx(b[jj], 1);
+                u[jj] = h ? pa + a[jj] : a[jj] + pa;
+                ub[jj] = h ? pb + b[jj] : b[jj] + pb;
             }
+            s0 = ((u[0] + u[1]) + (u[2] + u[3])) * scale;
+            s1 = ((ub[0] + ub[1]) + (ub[2] + ub[3])) * scale;
+        }
+        if (t < kv_len) {
+            if (h == 0) {
+                sc0[t] = s0;
+                if (pair) sc1[t] = s1;
+            }
+            mx0 = s0 > mx0 ? s0 : mx0;
+            mx1 = s1 > mx1 ? s1 : mx1;
         }
     }
-    red[0][tid] = mx0;
-    red[1][tid] = mx1;
+#pragma unroll
+    for (int m = 32; m > 0; m >>= 1) {
+        mx0 = fmaxf(mx0, shx(mx0, m));
+        mx1 = fmaxf(mx1, shx(mx1, m));
+    }
+    if (lane == 0) {
+        red[0][wave] = mx0;
+        red[1][wave] = mx1;
+    }
     __syncthreads();
-    for (int w = 128; w > 0; w >>= 1) {
-        if (tid < w) {
-            red[0][tid] = fmaxf(red[0][tid], red[0][tid + w]);
-            red[1][tid] = fmaxf(red[1][tid], red[1][tid + w]);
-        }
-        __syncthreads();
-    }
-    const float M0 = red[0][0], M1 = red[1][0];
+    const float M0 = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
+    const float M1 = fmaxf(fmaxf(red[1][0], red[1][1]), fmaxf(red[1][2], red[1][3]));
     const int n8 = kv_len & ~7;
     for (int t = tid; t < kv_len; t += 256) {
         sc0[t] = t < n8 ? exp_poly(sc0[t] - M0) : expf_libc(sc0[t] - M0);
@@ -1075,17 +1132,17 @@ __global__ __launch_bounds__(256) void k_attn_dec(const float* __restrict__ q, c
     if (tid < 16) {
         const int hsel = tid >> 3, jj = tid & 7;
         if (hsel < nh) {
-            const float* sc = hsel ? sc1 : sc0;
-            float a = 0.0f;
-            for (int t = jj; t < n8; t += 8) a = a + sc[t];
-            vs8[hsel][jj] = a;
+            const float* scp = hsel ? sc1 : sc0;
+            float acc = 0.0f;
+            for (int t = jj; t < n8; t += 8) acc = acc + scp[t];
+            vs8[hsel][jj] = acc;
         }
     }
     __syncthreads();
     if (tid < nh) {
-        const float* sc = tid ? sc1 : sc0;
+        const float* scp = tid ? sc1 : sc0;
         float sp = hsum8(vs8[tid]);
-        for (int t = n8; t < kv_len; t++) sp += sc[t];
+        for (int t = n8; t < kv_len; t++) sp += scp[t];
         inv_sh[tid] = 1.0f / (sp + 1e-12f);
     }
     __syncthreads();
@@ -1094,7 +1151,7 @@ __global__ __launch_bounds__(256) void k_attn_dec(const float* __restrict__ q, c
         if (pair) sc1[t] = sc1[t] * inv_sh[1];
     }
 
-    // P.V over LDS chunks of V; output o = (hsel, d); row pos comes from vn
+    // P.V over LDS chunks of V (row pos comes from vn); output o = (hsel, d)
     constexpr int NO = (2 * HD + 255) / 256;
     float acc[NO];
 #pragma unroll
@@ -1106,6 +1163,10 @@ __global__ __launch_bounds__(256) void k_attn_dec(const float* __restrict__ q, c
         }
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
+        if (pos >= c0 && pos < c0 + V_ROWS) {
+            for (int i = tid; i < HD; i += 256) vst[(pos - c0) * HD + i] = vn[i];
+            __syncthreads();
+        }
         const int cn = kv_len - c0 < V_ROWS ? kv_len - c0 : V_ROWS;
 #pragma unroll
         for (int jo = 0; jo < NO; jo++) {
@@ -1113,14 +1174,34 @@ __global__ __launch_bounds__(256) void k_attn_dec(const float* __restrict__ q, c
             if (o >= nh * HD) break;
             const int hsel = o / HD, d = o % HD;
             const float* p = (hsel ? sc1 : sc0) + c0;
-            auto vat = [&](int r) { return (c0 + r == pos) ? vn[d] : vst[r * HD + d]; };
+            const float* vcol = vst + d;
             float a = acc[jo];
+            int r = 0;
             if (pair) {
-                for (int r = 0; r < cn; r++) a = fmaf(p[r], vat(r), a);
+                for (; r + 8 <= cn; r += 8) {
+                    float pv[8], vv[8];
+#pragma unroll
+                    for (int u = 0; u < 8; u++) {
+                        pv[u] = p[r + u];
+                        vv[u] = vcol[(r + u) * HD];
+                    }
+#pragma unroll
+                    for (int u = 0; u < 8; u++) a = fmaf(pv[u], vv[u], a);
+                }
+                for (; r < cn; r++) a = fmaf(p[r], vcol[r * HD], a);
             } else {
-                int r = 0;
-                for (; r + 1 < cn; r += 2) a = fmaf(p[r], vat(r), fmaf(p[r + 1], vat(r + 1), a));
-                if (r < cn) a = fmaf(p[r], vat(r), a);
+                for (; r + 8 <= cn; r += 8) {
+                    float pv[8], vv[8];
+#pragma unroll
+                    for (int u = 0; u < 8; u++) {
+                        pv[u] = p[r + u];
+                        vv[u] = vcol[(r + u) * HD];
+                    }
+#pragma unroll
+                    for (int u = 0; u < 8; u += 2) a = fmaf(pv[u], vv[u], fmaf(pv[u + 1], vv[u + 1], a));
+                }
+                for (; r + 1 < cn; r += 2) a = fmaf(p[r], vcol[r * HD], fmaf(p[r + 1], vcol[(r + 1) * HD], a));
+                if (r < cn) a = fmaf(p[r], vcol[r * HD], a);
             }
             acc[jo] = a;
         }
@@ -1141,7 +1222,9 @@ __global__ __launch_bounds__(256) void k_attn_dec(const float* __restrict__ q, c
         float x[16];
 #pragma unroll
         for (int kk = 0; kk < 16; kk++) x[kk] = aout[16 * tid + kk];
-        quad_sign(x, o_sign, blk, qp);
+#pragma unroll
+        for (int kk = 0; kk < 16; kk++)
+            if ((osb >> kk) & 1u) x[kk] = -x[kk];
         quad_fwht64(x, qp);
         quad_quant_store(x, qp, blk, op.q, op.s, op.m);
     }
@@ -1428,8 +1511,44 @@ void dpuf_hip_swiglu_prep(void* s, int32_t M, int32_t I, const float* gate, cons
     LAUNCHED("k_swiglu_prep");
 }
 
+void dpuf_hip_relayout(void* s, const uint8_t* src, const uint64_t* offs, int32_t n_groups, int32_t n_blk,
+                       uint8_t* dst) {
+    const size_t total = (size_t)n_groups * n_blk * 8;
+    const int blocks = (int)((total + 255) / 256 < 65536 ? (total + 255) / 256 : 65536);
+    hipLaunchKernelGGL(k_relayout, dim3(blocks), dim3(256), 0, ST(s), src, offs, n_groups, n_blk, dst);
+    LAUNCHED("k_relayout");
+}
+
+static void mv_launch(void* s, MvArgs& A, int n_groups) {
+    const size_t lds = (size_t)8 * ((A.K >> 5) + 2) * 8;
+    hipLaunchKernelGGL(k_mv, dim3(n_groups), dim3(MV_NW * 64), lds, ST(s), A);
+    LAUNCHED("k_mv");
+}
+
 void dpuf_hip_gemv(void* s, int32_t M, int32_t n_jobs, const DpufGemvJob* jobs, const int32_t* skip_flag,
                    float fill) {
+    if (M == 1) {
+        MvArgs A;
+        memset(&A, 0, sizeof A);
+        int g = 0;
+        A.n_jobs = n_jobs;
+        A.K = jobs[0].w.cols;
+        for (int i = 0; i < n_jobs; i++) {
+            A.j[i].g = jobs[i].w.g;
+            A.j[i].out = jobs[i].out;
+            A.j[i].g0 = jobs[i].g0;
+            A.j[i].g1 = jobs[i].g1;
+            A.j[i].rows = jobs[i].w.rows;
+            A.j[i].x = jobs[i].p;
+            A.gb[i] = g;
+            g += jobs[i].g1 - jobs[i].g0;
+        }
+        A.gb[n_jobs] = g;
+        A.skip_flag = skip_flag;
+        A.fill = fill;
+        if (g > 0) mv_launch(s, A, g);
+        return;
+    }
     GemvBatch B;
     memset(&B, 0, sizeof B);
     int g = 0;
@@ -1437,24 +1556,12 @@ void dpuf_hip_gemv(void* s, int32_t M, int32_t n_jobs, const DpufGemvJob* jobs, 
     for (int i = 0; i < n_jobs; i++) {
         B.j[i] = jobs[i];
         B.g_begin[i] = g;
-        g += 2 * (jobs[i].t1 - jobs[i].t0);
+        g += jobs[i].g1 - jobs[i].g0;
     }
     B.g_begin[n_jobs] = g;
     if (g <= 0) return;
-    if (M == 1) {
-        int n_blk = 0;
-        for (int i = 0; i < n_jobs; i++) n_blk = jobs[i].w.cols / 32 > n_blk ? jobs[i].w.cols / 32 : n_blk;
-        const size_t lds = (size_t)8 * (n_blk + 2) * sizeof(float2);
-        if ((n_blk + 7) / 8 <= 16) {
-            hipLaunchKernelGGL(k_gemv1w<4>, dim3(g), dim3(256), lds, ST(s), B, skip_flag, fill);
-        } else {
-            hipLaunchKernelGGL(k_gemv1w<12>, dim3(g), dim3(256), lds, ST(s), B, skip_flag, fill);
-        }
-        LAUNCHED("k_gemv1w");
-    } else {
-        hipLaunchKernelGGL(k_gemm8, dim3(g, (M + 7) / 8), dim3(64), 0, ST(s), B, M);
-        LAUNCHED("k_gemm8");
-    }
+    hipLaunchKernelGGL(k_gemm8, dim3(g, (M + 7) / 8), dim3(64), 0, ST(s), B, M);
+    LAUNCHED("k_gemm8");
 }
 
 void dpuf_hip_qk_rope_kv(void* s, int32_t M, float* q, float* k, const float* v, const float* q_norm,

@@ -19,9 +19,9 @@ static void* stream(void) {
     return g_stream;
 }
 
-/* Checks tiles [t0, t1) of a mode 12 payload (row counts in [1, 16] and
- * inside `rows`, groups inside the byte range) and returns the byte range
- * [*lo, *hi). */
+/* Checks tiles [t0, t1) of a mode 12 payload (tile t holds min(16, rows -
+ * 16t) rows, its groups lie inside the byte range) and returns the byte
+ * range [*lo, *hi). */
 static int check_tiles(int32_t rows, int32_t cols, int32_t t0, int32_t t1, const uint8_t* base,
                        const uint64_t* offs, uint64_t* lo, uint64_t* hi) {
     if (cols <= 0 || (cols % 64) != 0 || t0 < 0 || t1 <= t0 || !base || !offs) return 0;
@@ -33,53 +33,63 @@ static int check_tiles(int32_t rows, int32_t cols, int32_t t0, int32_t t1, const
         if (offs[t] < *lo || offs[t] + 16 > *hi || ((offs[t] - *lo) % 16) != 0) return 0;
         DpufQrTileHdr th;
         memcpy(&th, base + offs[t], sizeof th);
-        if (th.n_rows < 1 || th.n_rows > 16 || (int64_t)t * 16 + th.n_rows > rows) return 0;
+        const int64_t want = (int64_t)rows - (int64_t)t * 16 < 16 ? (int64_t)rows - (int64_t)t * 16 : 16;
+        if (want < 1 || th.n_rows != want) return 0;
         if (offs[t] + 16 + (uint64_t)((th.n_rows + 7) / 8) * grp > *hi) return 0;
     }
     return 1;
 }
 
 typedef struct {
-    void* tiles;
-    void* offs;
+    void* groups;
     void* sign;
-    DpufDevW w;
+    DpufDevW w;   /* row 0 of w is row 16 * t0 of the matrix */
 } Staged;
 
-/* Uploads tiles [t0, t1) with offsets rebased to the uploaded range. */
+/* Uploads tiles [t0, t1) and converts them to the row-block layout. */
 static int stage_weights(int32_t rows, int32_t cols, int32_t t0, int32_t t1, const uint8_t* base,
                          const uint64_t* offs, const uint8_t* sign, Staged* st) {
     uint64_t lo, hi;
     memset(st, 0, sizeof *st);
     if (!check_tiles(rows, cols, t0, t1, base, offs, &lo, &hi)) return 0;
     void* s = stream();
-    uint64_t* rel = (uint64_t*)calloc((size_t)t1 + 1, 8);
+    const int32_t nt = t1 - t0, n_blk = cols / 32;
+    const int32_t rows_st = (rows < 16 * t1 ? rows : 16 * t1) - 16 * t0;
+    const int32_t n_groups = (rows_st + 7) / 8;
+    uint64_t* rel = (uint64_t*)calloc((size_t)nt + 1, 8);
     if (!rel) return 0;
-    for (int32_t t = t0; t <= t1; t++) rel[t] = offs[t] - lo;
-    st->tiles = dpuf_hip_malloc((size_t)(hi - lo));
-    st->offs = dpuf_hip_malloc(((size_t)t1 + 1) * 8);
+    for (int32_t t = 0; t <= nt; t++) rel[t] = offs[t0 + t] - lo;
+    void* d_raw = dpuf_hip_malloc((size_t)(hi - lo));
+    void* d_offs = dpuf_hip_malloc(((size_t)nt + 1) * 8);
+    st->groups = dpuf_hip_malloc((size_t)n_groups * n_blk * 144);
     if (sign) st->sign = dpuf_hip_malloc((size_t)cols / 8);
-    if (!st->tiles || !st->offs || (sign && !st->sign)) {
-        free(rel);
+    int ok = d_raw && d_offs && st->groups && (!sign || st->sign);
+    if (ok) {
+        dpuf_hip_h2d(d_raw, base + lo, (size_t)(hi - lo), s);
+        dpuf_hip_h2d(d_offs, rel, ((size_t)nt + 1) * 8, s);
+        if (sign) dpuf_hip_h2d(st->sign, sign, (size_t)cols / 8, s);
+        dpuf_hip_relayout(s, (const uint8_t*)d_raw, (const uint64_t*)d_offs, n_groups, n_blk, (uint8_t*)st->groups);
+        ok = dpuf_hip_sync(s) == 0;
+    }
+    free(rel);
+    dpuf_hip_free(d_raw);
+    dpuf_hip_free(d_offs);
+    if (!ok) {
+        dpuf_hip_free(st->groups);
+        dpuf_hip_free(st->sign);
+        memset(st, 0, sizeof *st);
         return 0;
     }
-    dpuf_hip_h2d(st->tiles, base + lo, (size_t)(hi - lo), s);
-    dpuf_hip_h2d(st->offs, rel, ((size_t)t1 + 1) * 8, s);
-    if (sign) dpuf_hip_h2d(st->sign, sign, (size_t)cols / 8, s);
-    dpuf_hip_sync(s);
-    free(rel);
-    st->w.tiles = (const uint8_t*)st->tiles;
-    st->w.offs = (const uint64_t*)st->offs;
+    st->w.g = (const uint8_t*)st->groups;
     st->w.sign = (const uint8_t*)st->sign;
-    st->w.rows = rows;
+    st->w.rows = rows_st;
     st->w.cols = cols;
-    st->w.n_tiles = t1;
+    st->w.n_groups = n_groups;
     return 1;
 }
 
 static void unstage(Staged* st) {
-    dpuf_hip_free(st->tiles);
-    dpuf_hip_free(st->offs);
+    dpuf_hip_free(st->groups);
     dpuf_hip_free(st->sign);
 }
 
@@ -205,10 +215,10 @@ DPUF_EXPORT void dpuf_matmul_qr_hadamard4_packed_tile_range(int32_t M, int32_t r
         }
         DpufGemvJob j;
         j.w = st.w;
-        j.t0 = t_start;
-        j.t1 = t_end;
+        j.g0 = 0;
+        j.g1 = st.w.n_groups;
         j.p = p;
-        j.out = dout;
+        j.out = dout + (size_t)t_start * 16;
         j.ldo = rows;
         dpuf_hip_gemv(s, M, 1, &j, NULL, 0.0f);
         int32_t r1 = t_end * 16 < rows ? t_end * 16 : rows;
@@ -237,8 +247,8 @@ DPUF_EXPORT void dpuf_matmul_qr_hadamard4_packed_f32(int32_t M, int32_t rows, in
         dpuf_hip_prep(s, M, cols, dx, st.w.sign, p);
         DpufGemvJob j;
         j.w = st.w;
-        j.t0 = 0;
-        j.t1 = n_tiles;
+        j.g0 = 0;
+        j.g1 = st.w.n_groups;
         j.p = p;
         j.out = dout;
         j.ldo = rows;
@@ -263,13 +273,16 @@ DPUF_EXPORT void dpuf_embed_qr_hadamard4_packed_f32(int32_t n_tokens, int32_t co
         if (token_ids[i] > max_id) max_id = token_ids[i];
     }
     const int32_t nt = max_id / 16 + 1;
-    Staged st;
-    if (!stage_weights(nt * 16, cols, 0, nt, tensor_base, tile_offsets, sign_bits, &st)) return;
     for (int32_t i = 0; i < n_tokens; i++) {
         DpufQrTileHdr th;
         memcpy(&th, tensor_base + tile_offsets[token_ids[i] / 16], sizeof th);
-        if (token_ids[i] % 16 >= th.n_rows) { unstage(&st); return; }
+        if (token_ids[i] % 16 >= th.n_rows) return;
     }
+    /* rows covered by tiles [0, nt): the last one may be a short final tile */
+    DpufQrTileHdr last;
+    memcpy(&last, tensor_base + tile_offsets[nt - 1], sizeof last);
+    Staged st;
+    if (!stage_weights((nt - 1) * 16 + last.n_rows, cols, 0, nt, tensor_base, tile_offsets, sign_bits, &st)) return;
     int32_t* dids = (int32_t*)dpuf_hip_malloc((size_t)n_tokens * 4);
     float* dout = (float*)dpuf_hip_malloc((size_t)n_tokens * cols * 4);
     if (dids && dout) {

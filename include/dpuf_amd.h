@@ -62,13 +62,19 @@ DPUF_EXPORT uint64_t dpuf_amd_engine_weight_bytes(void* handle);
 /* Number of forward calls in which the LM-head early exit fired. */
 DPUF_EXPORT int64_t dpuf_amd_engine_early_exit_count(void* handle);
 
-/* Times `iters` launches of one resident matrix's M-row GEMV (which: 0 q,
- * 1 k, 2 v, 3 o, 4 gate, 5 up, 6 down, 7 LM head), cycling through layers
+/* Times `iters` back-to-back launches of one GEMV kind over resident weights
+ * (which: 0 q, 1 k, 2 v, 3 o, 4 gate, 5 up, 6 down, 7 LM head, 8 gate+up as
+ * one launch, 9 q+k+v as one launch), cycling through layers
  * start..num_layers-1 so that consecutive launches read distinct weights.
  * Returns the mean ms per launch (or < 0 on error); *bytes gets the
- * algorithmic bytes of one launch. */
+ * algorithmic bytes of one launch (weight groups + activations + outputs). */
 DPUF_EXPORT double dpuf_amd_gemv_bench(void* handle, int32_t which, int32_t M, int32_t iters, int32_t start_layer,
                                        double* bytes);
+
+/* Copies `bytes` between two device buffers `iters` times (hipMemcpyAsync
+ * device to device) and returns the mean ms per copy; a reference of known
+ * traffic for calibrating hardware byte counters.  < 0 on error. */
+DPUF_EXPORT double dpuf_amd_copy_bench(size_t bytes, int32_t iters);
 
 #ifdef __cplusplus
 }
