@@ -941,6 +941,8 @@ DPUF_EXPORT double dpuf_amd_gemv_bench(void* handle, int32_t which, int32_t M, i
     return (double)ms / iters;
 }
 
+DPUF_EXPORT void dpuf_amd_set_gemv_max_workgroups(int32_t n) { dpuf_hip_set_gemv_max_wg(n); }
+
 DPUF_EXPORT double dpuf_amd_copy_bench(size_t bytes, int32_t iters) {
     if (bytes == 0 || iters < 1 || dpuf_hip_device_count() <= 0) return -1.0;
     void* s = dpuf_hip_stream_create();

@@ -88,6 +88,8 @@ void dpuf_hip_relayout(void* s, const uint8_t* src, const uint64_t* offs, int32_
  * launch write `fill` to every row instead.  M > 1: the slab GEMM. */
 void dpuf_hip_gemv(void* s, int32_t M, int32_t n_jobs, const DpufGemvJob* jobs,
                    const int32_t* skip_flag, float fill);
+/* Caps M == 1 GEMV workgroups per launch (<= 0: device capacity only). */
+void dpuf_hip_set_gemv_max_wg(int32_t n);
 void dpuf_hip_qk_rope_kv(void* s, int32_t M, float* q, float* k, const float* v,
                          const float* q_norm, const float* k_norm, float eps,
                          const float* cos_tab, const float* sin_tab, float* kc, float* vc,

@@ -465,32 +465,34 @@ DEV uint4 nt_load16(const uint8_t* p) {
 
 // Per-row fp32 chain acc = fma(float(D - sum8), ws * xs, acc) over blocks in
 // ascending order (dpuf_avx2.c:2633-2635); `row` holds (dcf, sp) pairs, two
-// per float4, n_blk even.  Pairs are read in batches of 16 with the next
-// batch in flight while the current one is consumed, so LDS latency stays
-// off the dependent FMA chain.
-DEV void chain8(const float4* e, float& acc) {
+// per float4, n_blk even.  Pairs are read in batches of NB float4 with the
+// next batch in flight while the current one is consumed, so LDS latency
+// stays off the dependent FMA chain (about 13 cycles per FMA on gfx950).
+template <int NB>
+DEV void chain_batch(const float4* e, float& acc) {
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
+    for (int i = 0; i < NB; i++) {
         acc = fmaf(e[i].x, e[i].y, acc);
         acc = fmaf(e[i].z, e[i].w, acc);
     }
 }
 
+template <int NB>
 DEV float run_chain(const float4* row, int n2) {
     float acc = 0.0f;
     int k = 0;
-    if (n2 >= 16) {
-        float4 cur[8], nxt[8];
+    if (n2 >= 2 * NB) {
+        float4 cur[NB], nxt[NB];
 #pragma unroll
-        for (int i = 0; i < 8; i++) cur[i] = row[i];
-        for (k = 8; k + 8 <= n2; k += 8) {
+        for (int i = 0; i < NB; i++) cur[i] = row[i];
+        for (k = NB; k + NB <= n2; k += NB) {
 #pragma unroll
-            for (int i = 0; i < 8; i++) nxt[i] = row[k + i];
-            chain8(cur, acc);
+            for (int i = 0; i < NB; i++) nxt[i] = row[k + i];
+            chain_batch<NB>(cur, acc);
 #pragma unroll
-            for (int i = 0; i < 8; i++) cur[i] = nxt[i];
+            for (int i = 0; i < NB; i++) cur[i] = nxt[i];
         }
-        chain8(cur, acc);
+        chain_batch<NB>(cur, acc);
     }
     for (; k < n2; k++) {
         const float4 e = row[k];
@@ -501,20 +503,53 @@ DEV float run_chain(const float4* row, int n2) {
 }
 
 // ---------------------------------------------------------------------------
-// M == 1 GEMV, one 8-row group per workgroup of MV_NW waves (split over K).
+// M == 1 GEMV.
 //
-// A step is 8 blocks x 8 rows = 1 KB of nibbles, one 16-byte load per lane
-// (lane = 8*bi + ri: row ri of block 8s + bi).  In each round every wave owns
-// MV_NL consecutive steps and issues all of their loads (nibbles, scales and
-// the block's 32 activation bytes, scale and sum) before consuming any.  Dots
-// go to LDS as (float(D - sum8), ws * xs) pairs [row][block]; after one
-// barrier lanes 0..7 run the per-row chains.  Blocks whose activation scale is
-// <= 0 contribute nothing, as the M == 1 reference skips them
-// (dpuf_avx2.c:2621-2622).  Eight waves with two steps each keep enough
-// loads in flight per CU; the group count (rows / 8) gives the parallelism.
+// A step is 8 blocks x 8 rows of one 8-row group = 1 KB of nibbles, one
+// 16-byte load per lane (lane = 8*bi + ri: row ri of block 8s + bi), plus the
+// lane's fp16 scale.  A workgroup has NW loader waves, each taking NL
+// consecutive steps of a group per round (R rounds per group).  The fp32
+// chains of a group, acc = fma(float(D - sum8), ws * xs, acc) over its blocks
+// in ascending order (dpuf_avx2.c:2633-2635), are one dependent FMA per block
+// (about 13 cycles each on gfx950), so how they are scheduled decides the
+// kernel's speed.  Two launch modes:
+//
+// One group per workgroup (SINGLE), when the chip holds a workgroup for every
+// group at once: load, dots to LDS, one barrier, lanes 0..7 of wave 0 chain.
+//
+// Persistent workgroups, when there are more groups: job j gets
+// wb[j+1] - wb[j] workgroups, sized so the whole grid is resident, and
+// workgroup lb of the job walks the job's groups lb, lb + nwg, ...  With one
+// round per group (every K up to 14336) a loader wave always works on the
+// same steps, so its 32 activation bytes, scale and sum per step are loaded
+// into registers once and the steady state issues only the weight and scale
+// loads, one (group, round) unit ahead.  Dots go to LDS as
+// (float(D - sum8), ws * xs) pairs [row][block] in one of up to MV_NBUF
+// rotating buffers; after its last round of a group a loader wave counts
+// itself in with an LDS atomic and goes on without waiting.  MV_NC extra
+// chain waves take the groups in turn (group lg -> chain wave lg % MV_NC),
+// wait for the group's loader waves, run its 8 row chains on lanes 0..7 and
+// free the buffer, so chains overlap the loads of later groups; a loader
+// wave only waits when it is MV_NBUF groups ahead of the chains.
+//
+// In both modes blocks whose activation scale is <= 0 contribute nothing, as
+// the M == 1 reference skips them (dpuf_avx2.c:2621-2622): their pair is
+// (0, 0), which leaves a chain unchanged (an accumulator is never -0).
 // ---------------------------------------------------------------------------
-#define MV_NW 8
-#define MV_NL 2
+#define MV_NBUF 4   // pair buffers in flight per workgroup
+#define MV_CHAIN 4  // float4 pairs per LDS read batch of a chain (chain waves)
+#ifndef MV_CHAIN1
+#define MV_CHAIN1 8  // the same for the one-group-per-workgroup instances
+#endif
+#ifndef MV_NC
+#define MV_NC 2     // chain waves per workgroup
+#endif
+// Launch-shape choice (compile-time): whether groups of 43..56 steps (K up to
+// 14336) keep their activations in registers (11..14 loader waves x 4 steps)
+// or load them per round.
+#ifndef MV_HOIST48
+#define MV_HOIST48 1
+#endif
 
 struct MvJob {
     const uint8_t* g;  // dense groups of the matrix (row-block layout)
@@ -527,83 +562,236 @@ struct MvJob {
 struct MvArgs {
     MvJob j[3];
     int n_jobs;
-    int gb[4];              // prefix sums of (g1 - g0)
+    int wb[4];  // prefix sums of the workgroups given to each job
     int K;
+    int nbuf;   // pair buffers in LDS: min(MV_NBUF, most groups of one workgroup)
+    int nc;     // chain waves: MV_NC, or 0 when every workgroup has one group
     const int32_t* skip_flag;
     float fill;
 };
 
-DEV int find_mv_job(const MvArgs& A, int g) {
-    int j = 0;
-    if (A.n_jobs > 1 && g >= A.gb[1]) j = 1;
-    if (A.n_jobs > 2 && g >= A.gb[2]) j = 2;
-    return j;
+// Activations of one round of one wave.
+template <int NL>
+struct MvX {
+    int4 xa[NL], xb[NL];
+    float xs[NL];
+    int32_t xm[NL];
+};
+
+// Loads of one unit (a round of one group) of one wave; x only when the
+// activations are not held for the whole launch.
+template <int NL>
+struct MvU {
+    uint4 wq[NL];
+    uint32_t ws[NL];
+    MvX<NL> x;
+};
+
+// Uniform over the workgroup.
+struct MvGeo {
+    int n_blk, S, ld, R, NW;
+    int lb, nwg;     // this workgroup's index within its job, the job's workgroup count
+    int nbuf;        // pair buffers in LDS (<= MV_NBUF)
+    const uint8_t* g;
+    float* out;
+    int g0, rows;
+    DpufPrep x;
+};
+
+// Loads are unconditional (indices clamped into the group), so the number of
+// memory operations in flight is the same on every path and the wait for one
+// unit never includes the next unit's loads.
+template <int NL>
+DEV void mv_load_x(const MvGeo& G, int r, int w, int lane, MvX<NL>& X) {
+    const int s0 = (r * G.NW + w) * NL;
+#pragma unroll
+    for (int i = 0; i < NL; i++) {
+        const int s = min(s0 + i, G.S - 1);
+        const uint32_t b = (uint32_t)min(s * 8 + (lane >> 3), G.n_blk - 1);
+        X.xa[i] = *(const int4*)(G.x.q + b * 32u);
+        X.xb[i] = *(const int4*)(G.x.q + b * 32u + 16u);
+        X.xs[i] = G.x.s[b];
+        X.xm[i] = G.x.m[b];
+    }
 }
 
-__global__ __launch_bounds__(MV_NW * 64) void k_mv(MvArgs A) {
+template <int NL, bool HOIST>
+DEV void mv_issue(const MvGeo& G, int u, int w, int lane, MvU<NL>& L) {
+    const int lg = u / G.R, r = u - lg * G.R;
+    const int g = G.g0 + G.lb + lg * G.nwg;
+    const uint8_t* grp = G.g + (size_t)g * G.n_blk * 144;
+    const uint16_t* sc = (const uint16_t*)grp;
+    const uint8_t* qg = grp + (size_t)G.n_blk * 16;
+    const int s0 = (r * G.NW + w) * NL;
+#pragma unroll
+    for (int i = 0; i < NL; i++) {
+        const int s = min(s0 + i, G.S - 1);
+        const uint32_t b = (uint32_t)min(s * 8 + (lane >> 3), G.n_blk - 1);
+        const uint32_t e = b * 8u + (uint32_t)(lane & 7);  // == 64 s + lane unless clamped
+        L.wq[i] = nt_load16(qg + e * 16u);
+        L.ws[i] = sc[e];
+    }
+    if (!HOIST) mv_load_x<NL>(G, r, w, lane, L.x);
+}
+
+// (float(D - sum8), ws * xs) pairs of one round of one wave into pairs[row][block].
+template <int NL, bool HOIST>
+DEV void mv_dots(const MvGeo& G, int r, int w, int lane, const MvU<NL>& L, const MvX<NL>& X0, float2* pairs) {
+    const MvX<NL>& X = HOIST ? X0 : L.x;
+    const int bi = lane >> 3, ri = lane & 7;
+    const int s0 = (r * G.NW + w) * NL;
+#pragma unroll
+    for (int i = 0; i < NL; i++) {
+        const int s = s0 + i;
+        if (s >= G.S) break;  // wave-uniform
+        const int b = s * 8 + bi;
+        if (b < G.n_blk) {
+            const int dot = row_block_dot(L.wq[i], X.xa[i], X.xb[i]);
+            float dcf = 0.0f, sp = 0.0f;
+            if (X.xs[i] > 0.0f) {
+                dcf = (float)(dot - X.xm[i]);
+                sp = h2f((uint16_t)L.ws[i]) * X.xs[i];
+            }
+            pairs[ri * G.ld + b] = make_float2(dcf, sp);
+        }
+    }
+}
+
+// LDS bookkeeping of the pair buffers: loader-wave arrivals per buffer
+// (cumulative over the launch) and the last group whose chains finished in it.
+struct MvSync {
+    uint32_t cnt[MV_NBUF];
+    int32_t done[MV_NBUF];
+};
+
+template <int NL, bool HOIST>
+DEV void mv_consume(const MvGeo& G, int u, int w, int lane, const MvU<NL>& L, const MvX<NL>& X0, uint8_t* smem,
+                    MvSync* sy) {
+    const int lg = u / G.R, r = u - lg * G.R;
+    const int buf = lg % G.nbuf;
+    float2* pairs = (float2*)smem + (size_t)buf * 8 * G.ld;
+    if (r == 0 && lg >= G.nbuf) {
+        // the buffer is free once the chains of group lg - nbuf have read it
+        int spins = 0;
+        while (__hip_atomic_load(&sy->done[buf], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != lg - G.nbuf &&
+               ++spins < (1 << 22))
+            __builtin_amdgcn_s_sleep(1);
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    }
+    mv_dots<NL, HOIST>(G, r, w, lane, L, X0, pairs);
+    if (r == G.R - 1) {
+        // publish this wave's pairs of the group to the chain wave
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+        if (lane == 0) __hip_atomic_fetch_add(&sy->cnt[buf], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+}
+
+// The chain wave: for each group of the workgroup in order, wait until all
+// loader waves have published their pairs, run the 8 rows' chains on lanes
+// 0..7 at raised issue priority, write the rows, free the buffer.  Every wait
+// is bounded.
+DEV void mv_chains(const MvGeo& G, int c, int n_my, int lane, uint8_t* smem, MvSync* sy) {
+    for (int lg = c; lg < n_my; lg += MV_NC) {
+        const int buf = lg % G.nbuf;
+        // arrivals in this buffer are cumulative: use lg / nbuf of the buffer is
+        // complete at NW * (lg / nbuf + 1), and the next use cannot start
+        // arriving before this group's chains free the buffer
+        const uint32_t want = (uint32_t)G.NW * (uint32_t)(lg / G.nbuf + 1);
+        int spins = 0;
+        while (__hip_atomic_load(&sy->cnt[buf], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != want &&
+               ++spins < (1 << 22))
+            __builtin_amdgcn_s_sleep(1);
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+        __builtin_amdgcn_s_setprio(2);
+        if (lane < 8) {
+            const float2* pairs = (const float2*)smem + (size_t)buf * 8 * G.ld;
+            const float acc = run_chain<MV_CHAIN>((const float4*)(pairs + lane * G.ld), G.n_blk >> 1);
+            const int r = (G.g0 + G.lb + lg * G.nwg) * 8 + lane;
+            if (r < G.rows) G.out[r] = acc;
+        }
+        __builtin_amdgcn_s_setprio(0);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+        if (lane == 0) __hip_atomic_store(&sy->done[buf], lg, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+}
+
+template <int NL, bool HOIST, bool SINGLE>
+__global__ __launch_bounds__(1024) void k_mv(MvArgs A) {
     extern __shared__ __align__(16) uint8_t smem[];
-    const int ji = find_mv_job(A, blockIdx.x);
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    int ji = 0;
+    if (A.n_jobs > 1 && (int)blockIdx.x >= A.wb[1]) ji = 1;
+    if (A.n_jobs > 2 && (int)blockIdx.x >= A.wb[2]) ji = 2;
     const MvJob& J = A.j[ji];
-    const int g = J.g0 + (blockIdx.x - A.gb[ji]);
-    const int tid = threadIdx.x;
-    const int r0 = g * 8;
-    const int n8 = J.rows - r0 < 8 ? J.rows - r0 : 8;
+    MvGeo G;
+    G.lb = blockIdx.x - A.wb[ji];
+    G.nwg = A.wb[ji + 1] - A.wb[ji];
+    G.g = J.g;
+    G.out = J.out;
+    G.g0 = J.g0;
+    G.rows = J.rows;
+    G.x = J.x;
+    const int n_my = (J.g1 - J.g0 - G.lb + G.nwg - 1) / G.nwg;
     if (A.skip_flag && *A.skip_flag) {
-        if (tid < n8) J.out[r0 + tid] = A.fill;
+        for (int lg = 0; lg < n_my; lg++) {
+            const int r0 = (G.g0 + G.lb + lg * G.nwg) * 8;
+            if (tid < 8 && r0 + tid < G.rows) G.out[r0 + tid] = A.fill;
+        }
         return;
     }
-    const int K = A.K, n_blk = K >> 5, S = (n_blk + 7) >> 3, ld = n_blk + 2;
-    const int w = tid >> 6, lane = tid & 63, bi = lane >> 3, ri = lane & 7;
-    const uint8_t* grp = J.g + (size_t)g * n_blk * 144;
-    const uint16_t* sc = (const uint16_t*)grp;
-    const uint8_t* qg = grp + (size_t)n_blk * 16;
-    float2* pairs = (float2*)smem;  // [8][ld]
-    const DpufPrep P = J.x;
-
-    for (int base = 0; base < S; base += MV_NW * MV_NL) {
-        uint4 wq[MV_NL];
-        uint32_t wsr[MV_NL];
-        int4 xa[MV_NL], xb[MV_NL];
-        float xs[MV_NL];
-        int32_t xm[MV_NL];
-#pragma unroll
-        for (int i = 0; i < MV_NL; i++) {
-            const int s = base + w * MV_NL + i, b = s * 8 + bi;
-            if (s < S && b < n_blk) {
-                wq[i] = nt_load16(qg + (size_t)s * 1024 + lane * 16);
-                wsr[i] = sc[(size_t)s * 64 + lane];
-                xa[i] = *(const int4*)(P.q + b * 32);
-                xb[i] = *(const int4*)(P.q + b * 32 + 16);
-                xs[i] = P.s[b];
-                xm[i] = P.m[b];
-            } else {
-                wq[i] = make_uint4(0u, 0u, 0u, 0u);
-                wsr[i] = 0u;
-                xa[i] = xb[i] = make_int4(0, 0, 0, 0);
-                xs[i] = 0.0f;
-                xm[i] = 0;
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < MV_NL; i++) {
-            const int s = base + w * MV_NL + i;
-            if (s >= S) break;  // wave-uniform
-            const int b = s * 8 + bi;
-            if (b < n_blk) {
-                const int dot = row_block_dot(wq[i], xa[i], xb[i]);
-                float dcf = 0.0f, sp = 0.0f;
-                if (xs[i] > 0.0f) {
-                    dcf = (float)(dot - xm[i]);
-                    sp = h2f((uint16_t)wsr[i]) * xs[i];
-                }
-                pairs[ri * ld + b] = make_float2(dcf, sp);
-            }
-        }
+    G.NW = (blockDim.x >> 6) - A.nc;  // loader waves; the last A.nc waves run the chains
+    G.n_blk = A.K >> 5;
+    G.S = (G.n_blk + 7) >> 3;
+    G.ld = G.n_blk + 2;
+    G.R = HOIST ? 1 : (G.S + G.NW * NL - 1) / (G.NW * NL);
+    const int n_units = n_my * G.R;
+    G.nbuf = A.nbuf;
+    __shared__ MvSync sy;
+    if (tid < MV_NBUF) {
+        sy.cnt[tid] = 0u;
+        sy.done[tid] = -1;
     }
     __syncthreads();
-    if (tid < 8) {
-        const float acc = run_chain((const float4*)(pairs + tid * ld), n_blk >> 1);
-        if (tid < n8) J.out[r0 + tid] = acc;
+    if (w >= G.NW) {
+        mv_chains(G, w - G.NW, n_my, lane, smem, &sy);
+        return;
+    }
+    if (SINGLE) {
+        // one group per workgroup: no chain waves, one barrier, wave 0 chains
+        MvX<NL> X1;
+        MvU<NL> L1;
+        if (HOIST) mv_load_x<NL>(G, 0, w, lane, X1);
+        for (int r = 0; r < G.R; r++) {
+            mv_issue<NL, HOIST>(G, r, w, lane, L1);
+            mv_dots<NL, HOIST>(G, r, w, lane, L1, X1, (float2*)smem);
+        }
+        __syncthreads();
+        if (w == 0 && lane < 8) {
+            const float acc = run_chain<MV_CHAIN1>((const float4*)((float2*)smem + lane * G.ld), G.n_blk >> 1);
+            const int r = G.g0 * 8 + G.lb * 8 + lane;
+            if (r < G.rows) G.out[r] = acc;
+        }
+        return;
+    }
+    MvX<NL> X;
+    if (HOIST) mv_load_x<NL>(G, 0, w, lane, X);
+    // Steady state: both issues unconditional, so each consume waits only for
+    // its own loads; the last one or two units drain after the loop.
+    MvU<NL> La, Lb;
+    mv_issue<NL, HOIST>(G, 0, w, lane, La);
+    int u = 0;
+    for (; u + 2 < n_units; u += 2) {
+        mv_issue<NL, HOIST>(G, u + 1, w, lane, Lb);
+        mv_consume<NL, HOIST>(G, u, w, lane, La, X, smem, &sy);
+        mv_issue<NL, HOIST>(G, u + 2, w, lane, La);
+        mv_consume<NL, HOIST>(G, u + 1, w, lane, Lb, X, smem, &sy);
+    }
+    if (u + 1 < n_units) {
+        mv_issue<NL, HOIST>(G, u + 1, w, lane, Lb);
+        mv_consume<NL, HOIST>(G, u, w, lane, La, X, smem, &sy);
+        mv_consume<NL, HOIST>(G, u + 1, w, lane, Lb, X, smem, &sy);
+    } else {
+        mv_consume<NL, HOIST>(G, u, w, lane, La, X, smem, &sy);
     }
 }
 
@@ -1519,9 +1707,98 @@ void dpuf_hip_relayout(void* s, const uint8_t* src, const uint64_t* offs, int32_
     LAUNCHED("k_relayout");
 }
 
-static void mv_launch(void* s, MvArgs& A, int n_groups) {
-    const size_t lds = (size_t)8 * ((A.K >> 5) + 2) * 8;
-    hipLaunchKernelGGL(k_mv, dim3(n_groups), dim3(MV_NW * 64), lds, ST(s), A);
+typedef void (*MvKernel)(MvArgs);
+
+static int g_mv_max_wg = 0;  // test/tuning cap on M == 1 GEMV workgroups
+
+void dpuf_hip_set_gemv_max_wg(int32_t n) { g_mv_max_wg = n > 0 ? n : 0; }
+
+// Workgroups of one k_mv instance the device holds at once (occupancy x CUs),
+// cached per (instance, block size, LDS size).
+static int mv_capacity(MvKernel k, int threads, size_t lds) {
+    static int n_cu = 0;
+    static MvKernel c_k[16];
+    static int c_t[16], c_cap[16], c_n = 0;
+    static size_t c_lds[16];
+    for (int i = 0; i < c_n; i++)
+        if (c_k[i] == k && c_t[i] == threads && c_lds[i] == lds) return c_cap[i];
+    if (n_cu == 0) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n_cu <= 0)
+            n_cu = 1;
+    }
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, threads, lds) != hipSuccess || per_cu <= 0)
+        per_cu = 1;
+    const int cap = per_cu * n_cu;
+    if (c_n < 16) {
+        c_k[c_n] = k;
+        c_t[c_n] = threads;
+        c_lds[c_n] = lds;
+        c_cap[c_n++] = cap;
+    }
+    return cap;
+}
+
+// Picks the instance for S steps per group: one round per group with
+// NL = 1..4 steps per loader wave and at most 15 loader waves (S <= 60),
+// otherwise 8 loader waves x 2 steps per round with the activations loaded
+// per round.  The block has one more wave, the chain wave.
+static void mv_launch(void* s, MvArgs& A, const int* n_groups) {
+    const int n_blk = A.K >> 5, S = (n_blk + 7) >> 3;
+    MvKernel k, k1;  // persistent and one-group-per-workgroup instances
+    int nl, nw;
+    if (S <= 16 - MV_NC) {
+        nl = 1;
+        k = k_mv<1, true, false>;
+        k1 = k_mv<1, true, true>;
+    } else if (S <= 2 * (16 - MV_NC)) {
+        nl = 2;
+        k = k_mv<2, true, false>;
+        k1 = k_mv<2, true, true>;
+    } else if (S <= 3 * (16 - MV_NC)) {
+        nl = 3;
+        k = k_mv<3, true, false>;
+        k1 = k_mv<3, true, true>;
+    } else if (S <= 4 * (16 - MV_NC) && MV_HOIST48) {
+        nl = 4;
+        k = k_mv<4, true, false>;
+        k1 = k_mv<4, true, true>;
+    } else {
+        nl = 2;
+        k = k_mv<2, false, false>;
+        k1 = k_mv<2, false, true>;
+    }
+    nw = k == k_mv<2, false, false> ? 8 : (S + nl - 1) / nl;
+    const int threads_p = (nw + MV_NC) * 64;  // + the chain waves
+    const size_t buf = (size_t)8 * (n_blk + 2) * 8;
+    int total = 0;
+    for (int i = 0; i < A.n_jobs; i++) total += n_groups[i];
+    if (total <= 0) return;
+    // one group per workgroup when the chip holds all of them at once,
+    // otherwise persistent workgroups with chain waves
+    int cap1 = mv_capacity(k1, nw * 64, buf);
+    if (g_mv_max_wg > 0 && cap1 > g_mv_max_wg) cap1 = g_mv_max_wg;
+    int cap = total <= cap1 ? total : mv_capacity(k, threads_p, MV_NBUF * buf);
+    if (g_mv_max_wg > 0 && cap > g_mv_max_wg) cap = g_mv_max_wg;
+    int grid = 0, most = 1;
+    A.wb[0] = 0;
+    for (int i = 0; i < A.n_jobs; i++) {
+        int nwg = n_groups[i];
+        if (total > cap && nwg > 0) {
+            nwg = (int)((long long)cap * n_groups[i] / total);
+            if (nwg < 1) nwg = 1;
+        }
+        if (nwg > 0 && (n_groups[i] + nwg - 1) / nwg > most) most = (n_groups[i] + nwg - 1) / nwg;
+        grid += nwg;
+        A.wb[i + 1] = grid;
+    }
+    A.nbuf = most < MV_NBUF ? most : MV_NBUF;
+    A.nc = most > 1 ? MV_NC : 0;
+    const int threads = (nw + A.nc) * 64;
+    const size_t lds = (size_t)A.nbuf * buf;
+    hipLaunchKernelGGL(A.nc ? k : k1, dim3(grid), dim3(threads), lds, ST(s), A);
     LAUNCHED("k_mv");
 }
 
@@ -1530,7 +1807,7 @@ void dpuf_hip_gemv(void* s, int32_t M, int32_t n_jobs, const DpufGemvJob* jobs, 
     if (M == 1) {
         MvArgs A;
         memset(&A, 0, sizeof A);
-        int g = 0;
+        int ng[3] = {0, 0, 0};
         A.n_jobs = n_jobs;
         A.K = jobs[0].w.cols;
         for (int i = 0; i < n_jobs; i++) {
@@ -1540,13 +1817,11 @@ void dpuf_hip_gemv(void* s, int32_t M, int32_t n_jobs, const DpufGemvJob* jobs, 
             A.j[i].g1 = jobs[i].g1;
             A.j[i].rows = jobs[i].w.rows;
             A.j[i].x = jobs[i].p;
-            A.gb[i] = g;
-            g += jobs[i].g1 - jobs[i].g0;
+            ng[i] = jobs[i].g1 - jobs[i].g0 > 0 ? jobs[i].g1 - jobs[i].g0 : 0;
         }
-        A.gb[n_jobs] = g;
         A.skip_flag = skip_flag;
         A.fill = fill;
-        if (g > 0) mv_launch(s, A, g);
+        mv_launch(s, A, ng);
         return;
     }
     GemvBatch B;

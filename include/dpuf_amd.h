@@ -76,6 +76,12 @@ DPUF_EXPORT double dpuf_amd_gemv_bench(void* handle, int32_t which, int32_t M, i
  * traffic for calibrating hardware byte counters.  < 0 on error. */
 DPUF_EXPORT double dpuf_amd_copy_bench(size_t bytes, int32_t iters);
 
+/* Caps the workgroups of an M = 1 GEMV launch at n (n <= 0: no cap beyond
+ * what the device holds at once), process-wide.  A smaller cap gives each
+ * workgroup more 8-row groups to walk; results do not depend on it.  For
+ * tests of the multi-group path and for tuning. */
+DPUF_EXPORT void dpuf_amd_set_gemv_max_workgroups(int32_t n);
+
 #ifdef __cplusplus
 }
 #endif

@@ -52,7 +52,18 @@ def tiny():
     return M.Model.build(TINY, max_seq_len=96, seed=5)
 
 
-def test_tiny_prefill_decode_bit_exact(eng, orc, tiny):
+@pytest.mark.parametrize("cap", [0, 3])
+def test_tiny_prefill_decode_bit_exact(eng, orc, tiny, cap):
+    """cap 3 runs every M = 1 GEMV (QKV, O, gate/up, down, LM head) with three
+    workgroups, each walking many groups."""
+    eng.dpuf_amd_set_gemv_max_workgroups(cap)
+    try:
+        _prefill_decode(eng, orc, tiny)
+    finally:
+        eng.dpuf_amd_set_gemv_max_workgroups(0)
+
+
+def _prefill_decode(eng, orc, tiny):
     p = Pair(eng, orc, tiny)
     ids = np.random.default_rng(1).integers(0, 4096, 13).astype(np.int32)
     lg, lo = p.forward(ids, 0, only_last=0)
@@ -105,3 +116,38 @@ def test_qwen3_06b_token_exact(eng, orc):
     assert tg == to
     assert exact
     p.close()
+
+
+@pytest.mark.parametrize("cap", [0, 3])
+def test_lm_early_exit(eng, orc, monkeypatch, cap):
+    """Zone-A early exit of the LM head (more than 2048 tiles): with a tiny
+    margin the zone's top-2 test fires and the rest of the vocabulary reads
+    -1e9; with a huge margin it never fires and the full head runs.  Logits
+    bit-identical to the oracle in both cases, at the default launch and with
+    the GEMV workgroups capped (flag-gated launch walking many groups)."""
+    shape = dict(TINY, vocab_size=40960)
+    m = M.Model.build(shape, max_seq_len=32, seed=9)
+    p = Pair(eng, orc, m)
+    eng.dpuf_amd_set_gemv_max_workgroups(cap)
+    try:
+        ids = np.random.default_rng(3).integers(0, 40960, 6).astype(np.int32)
+        monkeypatch.delenv("DPUF_EARLY_TILES", raising=False)
+        lg, lo = p.forward(ids, 0)
+        assert _bits_equal(lg, lo)
+        tok = int(np.argmax(lo[0]))
+        monkeypatch.setenv("DPUF_EARLY_TILES", "300")
+        for step, margin in enumerate(["1e-7", "1e9", "1e-7"]):
+            monkeypatch.setenv("DPUF_EARLY_MARGIN", margin)
+            before = eng.dpuf_amd_engine_early_exit_count(p.g)
+            lg, lo = p.forward(np.array([tok], np.int32), 6 + step)
+            fired = eng.dpuf_amd_engine_early_exit_count(p.g) - before
+            print(f"early exit cap={cap} margin={margin} fired={fired}", flush=True)
+            assert _bits_equal(lg, lo), (margin, np.max(np.abs(lg - lo)))
+            if margin == "1e9":
+                assert fired == 0 and np.all(lo[0, 300 * 16:] > -1e8)
+            else:
+                assert fired == 1 and np.all(lo[0, 300 * 16:] == -1e9)
+            tok = int(np.argmax(lo[0]))
+    finally:
+        eng.dpuf_amd_set_gemv_max_workgroups(0)
+        p.close()

@@ -49,6 +49,31 @@ def test_matmul_f32_bit_exact(eng, orc, rows, cols, m):
     assert _same_bits(out_g, out_o), f"max abs diff {np.nanmax(np.abs(out_g - out_o))}"
 
 
+@pytest.mark.parametrize("rows,cols", [(24, 192), (8, 320), (1000, 3072), (1024, 4096), (4096, 12288),
+                                       (64, 16384)])
+@pytest.mark.parametrize("cap", [1, 2, 3, 5, 7, 0])
+def test_matmul_m1_workgroup_caps(eng, orc, rows, cols, cap):
+    """M = 1 GEMV with the workgroup count capped so each workgroup walks
+    several 8-row groups (pipelined loads, chain waves, rotating pair
+    buffers); cap 0 is the default launch.  Covers partial 8-block steps
+    (cols 192, 320) and the per-round activation path (cols 16384)."""
+    blob, d = _mat(rows, cols, 29 + cols)
+    x = _x(1, cols, rows * 3 + cols)
+    x[0, 32:64] = 1e-6  # a zero-scale block
+    out_g = np.full((1, rows), np.nan, np.float32)
+    out_o = np.full((1, rows), np.nan, np.float32)
+    print(f"matmul M=1 rows={rows} cols={cols} max_workgroups={cap}", flush=True)
+    eng.dpuf_amd_set_gemv_max_workgroups(cap)
+    try:
+        eng.dpuf_matmul_qr_hadamard4_packed_f32(1, rows, cols, d.n_tiles, M.ptr(x), d.tensor_base, d.tile_offsets,
+                                                d.sign_bits, M.ptr(out_g))
+    finally:
+        eng.dpuf_amd_set_gemv_max_workgroups(0)
+    orc.orc_matmul_f32(1, rows, cols, d.n_tiles, M.ptr(x), d.tensor_base, d.tile_offsets, d.sign_bits,
+                       M.ptr(out_o))
+    assert _same_bits(out_g, out_o), f"max abs diff {np.nanmax(np.abs(out_g - out_o))}"
+
+
 @pytest.mark.parametrize("cols", [64, 1024, 4096])
 def test_fwht_and_prep_row(eng, orc, cols):
     x = _x(1, cols, cols)[0]
