@@ -796,71 +796,228 @@ __global__ __launch_bounds__(1024) void k_mv(MvArgs A) {
 }
 
 // ---------------------------------------------------------------------------
-// M > 1 GEMM (slab path, dpuf_avx2.c:2643-2676): one 8-row group and up to 8
-// tokens per wave; lane (bi, ri) holds row ri of block b0+bi and forms its
-// dot for each token; every block is accumulated (no skip), as in the slab
-// kernels.  Chain lanes (token cm, row cr) run the 8 x 8 chains.
+// M > 1 GEMM on the matrix cores (slab path, dpuf_avx2.c:2643-2676).
+//
+// For every (row, token) the reference accumulates every block:
+//   acc = fma(float(D - sum8), fp16(ws) * xs, acc), blocks ascending,
+// with D the u4 x i8 dot of the block and sum8 = 8 * sum(q).  Since
+// D - sum8 = sum((u - 8) * q) exactly, one v_mfma_f32_16x16x32_f16 per block
+// with A = (u - 8) and B = q, both exact in f16, gives float(D - sum8) for a
+// 16-row x 16-token tile (every partial sum is an integer below 2^15, exact
+// in the fp32 accumulator).  The epilogue is the reference's two rounded
+// operations, sp = ws * xs and the fma, with the chains in registers across
+// the block loop, so the block order is the reference's.
+//
+// A workgroup of 4 waves computes 128 rows (16 groups) x 64 tokens; wave w
+// owns rows 32w .. 32w + 31 as two 16-row fragments and all 64 tokens as four
+// 16-token tiles (8 MFMAs per block).  Activations are staged in LDS, GM_SB
+// blocks per stage, converted from int8 to f16 on the way in and double-
+// buffered, one barrier per stage; a token's 64 bytes per block are four
+// 16-byte chunks stored XOR-swizzled by token so a fragment read is free of
+// bank conflicts.  Weights, nibbles and scales, are read straight into
+// registers one stage ahead.  MFMA lane layouts (gfx950, checked on the
+// device): A lane l = row l % 16, k = 8 (l / 16) + e; B lane l = token
+// l % 16, same k; D lane l = token l % 16, rows 4 (l / 16) + v.
 // ---------------------------------------------------------------------------
-struct GemvBatch {
-    DpufGemvJob j[3];
-    int g_begin[4];
-    int n;
+#define GM_SB 4  // blocks per LDS stage
+
+typedef _Float16 gm_h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 gm_h8 __attribute__((ext_vector_type(8)));
+typedef float gm_f4 __attribute__((ext_vector_type(4)));
+
+struct GmJob {
+    const uint8_t* g;  // dense groups of the matrix
+    int g0, g1;        // groups computed
+    int rows;
+    const int8_t* q;   // activations [M][K]
+    const float* s;    // block scales [M][K/32]
+    float* out;        // out[m * ldo + row]
+    int ldo;
 };
 
-DEV int find_job(const GemvBatch& B, int g) {
-    int j = 0;
-    if (B.n > 1 && g >= B.g_begin[1]) j = 1;
-    if (B.n > 2 && g >= B.g_begin[2]) j = 2;
-    return j;
+struct GmArgs {
+    GmJob j[3];
+    int n_jobs;
+    int tb[4];  // prefix sums of 16-group row tiles per job
+    int K, M;
+};
+
+// Two fp16 values from bytes b0, b1 of x and 0x64: 1024 + byte each.
+DEV uint32_t gm_pair(uint32_t x, uint32_t sel) { return __builtin_amdgcn_perm(0x64646464u, x, sel); }
+
+DEV uint32_t gm_sub(uint32_t v, _Float16 c) {
+    gm_h2 h = __builtin_bit_cast(gm_h2, v);
+    h = h - (gm_h2){c, c};
+    return __builtin_bit_cast(uint32_t, h);
 }
 
-__global__ __launch_bounds__(64) void k_gemm8(GemvBatch B, int M) {
-    __shared__ float2 st[8][8][8];  // [token][row][block]
-    const int ji = find_job(B, blockIdx.x);
-    const DpufGemvJob& J = B.j[ji];
-    const int g = J.g0 + (blockIdx.x - B.g_begin[ji]);
-    const int r0 = g * 8;
-    const int n8 = J.w.rows - r0 < 8 ? J.w.rows - r0 : 8;
-    const int m0 = blockIdx.y * 8;
-    const int mt = M - m0 < 8 ? M - m0 : 8;
-    const int K = J.w.cols, n_blk = K >> 5;
-    const uint8_t* grp = J.w.g + (size_t)g * n_blk * 144;
-    const uint16_t* sc = (const uint16_t*)grp;
-    const uint8_t* qg = grp + (size_t)n_blk * 16;
-    const int lane = threadIdx.x;
-    const int bi = lane >> 3, ri = lane & 7;
-    const int cm = lane >> 3, cr = lane & 7;  // chain lane: token cm, row cr
-    float acc = 0.0f;
-    for (int b0 = 0; b0 < n_blk; b0 += 8) {
-        const int b = b0 + bi;
-        uint4 wq = make_uint4(0, 0, 0, 0);
-        float ws = 0.0f;
-        if (b < n_blk) {
-            wq = *(const uint4*)(qg + (size_t)b * 128 + ri * 16);
-            ws = h2f(sc[b * 8 + ri]);
-        }
-        for (int mi = 0; mi < mt; mi++) {
-            const int m = m0 + mi;
-            float dcf = 0.0f, sp = 0.0f;
-            if (b < n_blk) {
-                const int8_t* xq = J.p.q + (size_t)m * K + b * 32;
-                const int dot = row_block_dot(wq, *(const int4*)xq, *(const int4*)(xq + 16));
-                dcf = (float)(dot - J.p.m[(size_t)m * n_blk + b]);
-                sp = ws * J.p.s[(size_t)m * n_blk + b];
-            }
-            st[mi][ri][bi] = make_float2(dcf, sp);
-        }
-        __syncthreads();
-        if (cm < mt) {
+// A fragment from one nibble word (row i, columns 8 kc .. 8 kc + 7 of a
+// block: low nibbles = columns +0..+3, high nibbles = +4..+7): u - 8 as f16.
+DEV gm_h8 gm_unpack_a(uint32_t w) {
+    const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+    const uint32_t r0 = gm_sub(gm_pair(lo, 0x04010400u), (_Float16)1032.0f);
+    const uint32_t r1 = gm_sub(gm_pair(lo, 0x04030402u), (_Float16)1032.0f);
+    const uint32_t r2 = gm_sub(gm_pair(hi, 0x04010400u), (_Float16)1032.0f);
+    const uint32_t r3 = gm_sub(gm_pair(hi, 0x04030402u), (_Float16)1032.0f);
+    return __builtin_bit_cast(gm_h8, make_uint4(r0, r1, r2, r3));
+}
+
+// Four int8 (one word) -> four f16 in two words.
+DEV void gm_i8_to_h(uint32_t x, uint32_t& a, uint32_t& b) {
+    const uint32_t u = x ^ 0x80808080u;  // q + 128 per byte
+    a = gm_sub(gm_pair(u, 0x04010400u), (_Float16)1152.0f);
+    b = gm_sub(gm_pair(u, 0x04030402u), (_Float16)1152.0f);
+}
+
+__global__ __launch_bounds__(256) void k_gemm_mfma(GmArgs A) {
+    __shared__ __align__(16) uint8_t bq[2][GM_SB][64][64];  // f16 activations [stage][block][token][k]
+    __shared__ __align__(16) float bs[2][GM_SB][16][4];     // block scales [stage][block][token % 16][token / 16]
+    const int rt = blockIdx.x;
+    if (rt >= A.tb[A.n_jobs]) return;  // padding of the grid (whole workgroup)
+    int ji = 0;
+    if (A.n_jobs > 1 && rt >= A.tb[1]) ji = 1;
+    if (A.n_jobs > 2 && rt >= A.tb[2]) ji = 2;
+    const GmJob& J = A.j[ji];
+    const int gb = J.g0 + (rt - A.tb[ji]) * 16;  // first group of the workgroup
+    const int m0 = blockIdx.y * 64;
+    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, i16 = l & 15, kc = l >> 4;
+    const int K = A.K, M = A.M, n_blk = K >> 5;
+    const size_t gstride = (size_t)n_blk * 144;
+
+    // weight pointers of the wave's two fragments (groups clamped into the job)
+    const uint8_t* an[2];
+    const uint8_t* aw[2];
 #pragma unroll
-            for (int k = 0; k < 8; k++) {
-                const float2 e = st[cm][cr][k];
-                if (b0 + k < n_blk) acc = fmaf(e.x, e.y, acc);
+    for (int f = 0; f < 2; f++) {
+        int ga = gb + 4 * w + 2 * f + (i16 >> 3);
+        ga = ga < J.g1 ? ga : J.g1 - 1;
+        an[f] = J.g + (size_t)ga * gstride + (size_t)n_blk * 16 + (i16 & 7) * 16 + kc * 4;
+        int gw = gb + 4 * w + 2 * f + (kc >> 1);
+        gw = gw < J.g1 ? gw : J.g1 - 1;
+        aw[f] = J.g + (size_t)gw * gstride + (kc & 1) * 8;
+    }
+    // staging: thread (token tk, block sb of the stage)
+    const int tk = tid & 63, sbt = tid >> 6;
+    const bool tok_ok = m0 + tk < M;
+    const int8_t* qrow = J.q + (size_t)(tok_ok ? m0 + tk : 0) * K;
+    const float* srow = J.s + (size_t)(tok_ok ? m0 + tk : 0) * n_blk;
+    const int sw = (tk >> 1) & 3;  // chunk swizzle of this token
+
+    const int n_st = (n_blk + GM_SB - 1) / GM_SB;
+    uint4 sq0, sq1;
+    float ss;
+    auto stage_load = [&](int st) {
+        const int b = st * GM_SB + sbt;
+        if (tok_ok && b < n_blk) {
+            sq0 = *(const uint4*)(qrow + b * 32);
+            sq1 = *(const uint4*)(qrow + b * 32 + 16);
+            ss = srow[b];
+        } else {
+            sq0 = sq1 = make_uint4(0u, 0u, 0u, 0u);
+            ss = 0.0f;
+        }
+    };
+    auto stage_store = [&](int buf) {
+        const uint32_t d[8] = {sq0.x, sq0.y, sq0.z, sq0.w, sq1.x, sq1.y, sq1.z, sq1.w};
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            uint32_t h0, h1, h2, h3;
+            gm_i8_to_h(d[2 * c], h0, h1);
+            gm_i8_to_h(d[2 * c + 1], h2, h3);
+            *(uint4*)&bq[buf][sbt][tk][16 * (c ^ sw)] = make_uint4(h0, h1, h2, h3);
+        }
+        bs[buf][sbt][tk & 15][tk >> 4] = ss;
+    };
+    // weights of one stage: nibble word and 4 scales per fragment and block
+    uint32_t wn[2][GM_SB][2];
+    uint2 ws[2][GM_SB][2];
+    auto weights_load = [&](int st, uint32_t (&n)[GM_SB][2], uint2 (&sc)[GM_SB][2]) {
+#pragma unroll
+        for (int sb = 0; sb < GM_SB; sb++) {
+            const int b = min(st * GM_SB + sb, n_blk - 1);
+#pragma unroll
+            for (int f = 0; f < 2; f++) {
+                n[sb][f] = *(const uint32_t*)(an[f] + (size_t)b * 128);
+                sc[sb][f] = *(const uint2*)(aw[f] + (size_t)b * 16);
             }
         }
+    };
+
+    gm_f4 acc[2][4];
+#pragma unroll
+    for (int f = 0; f < 2; f++)
+#pragma unroll
+        for (int t = 0; t < 4; t++) acc[f][t] = (gm_f4){0.0f, 0.0f, 0.0f, 0.0f};
+
+    auto compute = [&](int st, int buf, const uint32_t (&n)[GM_SB][2], const uint2 (&sc)[GM_SB][2]) {
+#pragma unroll
+        for (int sb = 0; sb < GM_SB; sb++) {
+            if (st * GM_SB + sb >= n_blk) break;  // uniform
+            gm_h8 a[2];
+            float wsf[2][4];
+#pragma unroll
+            for (int f = 0; f < 2; f++) {
+                a[f] = gm_unpack_a(n[sb][f]);
+                wsf[f][0] = h2f((uint16_t)(sc[sb][f].x & 0xFFFFu));
+                wsf[f][1] = h2f((uint16_t)(sc[sb][f].x >> 16));
+                wsf[f][2] = h2f((uint16_t)(sc[sb][f].y & 0xFFFFu));
+                wsf[f][3] = h2f((uint16_t)(sc[sb][f].y >> 16));
+            }
+            const float4 xs4 = *(const float4*)&bs[buf][sb][i16][0];
+            const float xs[4] = {xs4.x, xs4.y, xs4.z, xs4.w};
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const int tok = 16 * t + i16;
+                const gm_h8 bf = *(const gm_h8*)&bq[buf][sb][tok][16 * (kc ^ ((tok >> 1) & 3))];
+#pragma unroll
+                for (int f = 0; f < 2; f++) {
+                    const gm_f4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[f], bf, (gm_f4){0.0f, 0.0f, 0.0f, 0.0f},
+                                                                         0, 0, 0);
+#pragma unroll
+                    for (int v = 0; v < 4; v++) acc[f][t][v] = fmaf(d[v], wsf[f][v] * xs[t], acc[f][t][v]);
+                }
+            }
+        }
+    };
+
+    // prologue: stage 0 into LDS buffer 0, weights of stage 0
+    stage_load(0);
+    weights_load(0, wn[0], ws[0]);
+    stage_store(0);
+    __syncthreads();
+    int st = 0;
+    for (; st + 2 <= n_st; st += 2) {
+        stage_load(st + 1);
+        weights_load(st + 1, wn[1], ws[1]);
+        compute(st, 0, wn[0], ws[0]);
+        stage_store(1);
+        __syncthreads();
+        if (st + 2 < n_st) {
+            stage_load(st + 2);
+            weights_load(st + 2, wn[0], ws[0]);
+        }
+        compute(st + 1, 1, wn[1], ws[1]);
+        if (st + 2 < n_st) stage_store(0);
         __syncthreads();
     }
-    if (cm < mt && cr < n8) J.out[(size_t)(m0 + cm) * J.ldo + r0 + cr] = acc;
+    if (st < n_st) compute(st, 0, wn[0], ws[0]);
+
+    // rows 32w + 16f + 4kc + v of the workgroup, token m0 + 16t + i16
+#pragma unroll
+    for (int f = 0; f < 2; f++) {
+        const int grp = gb + 4 * w + 2 * f + (kc >> 1);
+        if (grp >= J.g1) continue;
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const int m = m0 + 16 * t + i16;
+            if (m >= M) continue;
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int r = grp * 8 + (kc & 1) * 4 + v;
+                if (r < J.rows) J.out[(size_t)m * J.ldo + r] = acc[f][t][v];
+            }
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -1824,19 +1981,33 @@ void dpuf_hip_gemv(void* s, int32_t M, int32_t n_jobs, const DpufGemvJob* jobs, 
         mv_launch(s, A, ng);
         return;
     }
-    GemvBatch B;
-    memset(&B, 0, sizeof B);
-    int g = 0;
-    B.n = n_jobs;
-    for (int i = 0; i < n_jobs; i++) {
-        B.j[i] = jobs[i];
-        B.g_begin[i] = g;
-        g += jobs[i].g1 - jobs[i].g0;
+    {
+        GmArgs G;
+        memset(&G, 0, sizeof G);
+        int t = 0;
+        G.n_jobs = n_jobs;
+        G.K = jobs[0].w.cols;
+        G.M = M;
+        for (int i = 0; i < n_jobs; i++) {
+            G.j[i].g = jobs[i].w.g;
+            G.j[i].g0 = jobs[i].g0;
+            G.j[i].g1 = jobs[i].g1;
+            G.j[i].rows = jobs[i].w.rows;
+            G.j[i].q = jobs[i].p.q;
+            G.j[i].s = jobs[i].p.s;
+            G.j[i].out = jobs[i].out;
+            G.j[i].ldo = jobs[i].ldo;
+            G.tb[i] = t;
+            const int ng = jobs[i].g1 - jobs[i].g0;
+            t += ng > 0 ? (ng + 15) / 16 : 0;
+        }
+        G.tb[n_jobs] = t;
+        if (t <= 0) return;
+        // a multiple of 8 row tiles keeps a row tile's token tiles on one XCD
+        const int gx = (t + 7) & ~7;
+        hipLaunchKernelGGL(k_gemm_mfma, dim3(gx, (M + 63) / 64), dim3(256), 0, ST(s), G);
+        LAUNCHED("k_gemm_mfma");
     }
-    B.g_begin[n_jobs] = g;
-    if (g <= 0) return;
-    hipLaunchKernelGGL(k_gemm8, dim3(g, (M + 7) / 8), dim3(64), 0, ST(s), B, M);
-    LAUNCHED("k_gemm8");
 }
 
 void dpuf_hip_qk_rope_kv(void* s, int32_t M, float* q, float* k, const float* v, const float* q_norm,
