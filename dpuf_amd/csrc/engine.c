@@ -73,8 +73,16 @@ typedef struct {
     double t_bytes[N_KINDS];
     /* decode graph */
     void* graph;
-    int32_t graph_key[5];
+    int32_t graph_key[6];
+    /* the forward being enqueued: host copy of pos0, and whether it is being
+     * captured into a graph that replays at any position */
+    int32_t host_pos0;
+    int32_t capturing;
 } Engine;
+
+/* Decode attention switches from the fused short-context kernel to the split
+ * (scores + softmax/P.V) kernels once kv_len exceeds this. */
+#define ATT_SPLIT_MIN 192
 
 /* ------------------------------------------------------------------------- */
 
@@ -580,15 +588,18 @@ static void enqueue_layers(Engine* e, int32_t M, int32_t keep_tiles) {
         {
             const int tm = tm_begin(e, K_ATTN, 0);
             int fused = 0;
-            if (M == 1)
+            if (M == 1 && e->host_pos0 + 1 <= ATT_SPLIT_MIN)
                 fused = dpuf_hip_attn_dec(s, e->q, e->k, e->v, e->d_norm[4 * l + 1], e->d_norm[4 * l + 2], eps,
                                           e->d_cos, e->d_sin, kc, vc, e->d_pos0, e->nq, e->nkv, e->hd, e->max_seq,
                                           scale, e->scores, e->ao, W[W_O].sign, e->prep[0]) == 0;
             if (!fused) {
                 dpuf_hip_qk_rope_kv(s, M, e->q, e->k, e->v, e->d_norm[4 * l + 1], e->d_norm[4 * l + 2], eps,
                                     e->d_cos, e->d_sin, kc, vc, e->d_pos0, e->nq, e->nkv, e->hd, e->max_seq);
-                dpuf_hip_attn(s, M, e->q, kc, vc, e->ao, e->scores, e->d_pos0, e->nq, e->nkv, e->hd, e->max_seq,
-                              scale);
+                const int32_t lmax = e->capturing ? e->max_seq : e->host_pos0 + M;
+                if (dpuf_hip_attn_split(s, M, lmax, e->q, kc, vc, e->ao, e->scores, e->d_pos0, e->nq, e->nkv, e->hd,
+                                        e->max_seq, scale) != 0)
+                    dpuf_hip_attn(s, M, e->q, kc, vc, e->ao, e->scores, e->d_pos0, e->nq, e->nkv, e->hd,
+                                  e->max_seq, scale);
                 dpuf_hip_prep(s, M, e->qd, e->ao, W[W_O].sign, e->prep[0]);
             }
             tm_end(e, tm);
@@ -717,8 +728,10 @@ static int32_t forward_common(Engine* e, int32_t n_tokens, const int32_t* token_
 
     const int tm13 = tm_begin(e, K_CALL, (double)e->weight_bytes);
     const int graphable = use_graph && M == 1 && !e->timing && !embeds_in && !e->capture;
+    e->host_pos0 = pos0;
+    e->capturing = 0;
     if (graphable) {
-        int32_t key[5] = {only_last, keep, early, e->active, 0};
+        int32_t key[6] = {only_last, keep, early, e->active, 0, pos0 + 1 > ATT_SPLIT_MIN};
         memcpy(&key[4], &margin, 4);
         if (e->graph && memcmp(key, e->graph_key, sizeof key) != 0) {
             dpuf_hip_graph_destroy(e->graph);
@@ -726,7 +739,9 @@ static int32_t forward_common(Engine* e, int32_t n_tokens, const int32_t* token_
         }
         if (!e->graph) {
             if (dpuf_hip_capture_begin(e->stream) == 0) {
+                e->capturing = 1;
                 enqueue_forward(e, 1, 0, only_last, keep, early, margin, 1);
+                e->capturing = 0;
                 e->graph = dpuf_hip_capture_end(e->stream);
                 memcpy(e->graph_key, key, sizeof key);
             }

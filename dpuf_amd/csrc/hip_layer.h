@@ -97,6 +97,11 @@ void dpuf_hip_qk_rope_kv(void* s, int32_t M, float* q, float* k, const float* v,
 void dpuf_hip_attn(void* s, int32_t M, const float* q, const float* kc, const float* vc, float* out,
                    float* scores, const int32_t* pos0, int32_t n_q, int32_t n_kv, int32_t hd,
                    int32_t max_seq, float scale);
+/* Split attention (scores kernel + softmax/P.V kernel) over keys up to
+ * lmax; -1 (nothing launched) when the shape does not fit. */
+int32_t dpuf_hip_attn_split(void* s, int32_t M, int32_t lmax, const float* q, const float* kc, const float* vc,
+                            float* out, float* scores, const int32_t* pos0p, int32_t n_q, int32_t n_kv, int32_t hd,
+                            int32_t max_seq, float scale);
 /* M == 1 fused QK-norm + RoPE + KV store + attention + O-input prep.
  * Returns -1 (nothing launched) for head dims other than 64, 128, 256. */
 int32_t dpuf_hip_attn_dec(void* s, const float* q, const float* k, const float* v, const float* q_norm,

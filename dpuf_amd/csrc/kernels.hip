@@ -1114,6 +1114,228 @@ DEV float score_dot2(const float* q, const float* kp, int hd) {
     return hsum8(cc);
 }
 
+// ---------------------------------------------------------------------------
+// Split attention for prefill and long-context decode: the same arithmetic as
+// gqa_attn_head_pair_f32 (dpuf_engine.c:341-577) spread over the GPU.
+//
+// k_attn_sc: scores.  Workgroup (kv head, tile of qt queries, 64 keys): the
+// key chunk and the tile's q rows (qt x G heads, <= 32 rows) are staged in
+// LDS; thread (rp, kq) forms rows 2rp, 2rp + 1 against keys 4kq .. 4kq + 3 as
+// the reference's 8-lane accumulators (a[j] = fma chain over i of
+// q[8i + j] * k[8i + j]), then applies the reference's horizontal sum for
+// that (query, key): the hadd tree for keys below kv_len & ~3, eng_hsum256
+// above it (dot_f32_avx2's two-accumulator form for a single trailing head),
+// times the scale.  Writes S[m][head][t] for t < kv_len(m) = pos0 + m + 1.
+// ---------------------------------------------------------------------------
+#define AS_KC 64  // keys per scores workgroup
+
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_sc(const float* __restrict__ q, const float* __restrict__ kc,
+                                                 const int32_t* __restrict__ pos0p, int M, int n_q, int n_kv,
+                                                 int max_seq, float scale, int qt, float* __restrict__ S) {
+    constexpr int LD = HD + 4;
+    extern __shared__ __align__(16) float sm[];
+    float* ks = sm;               // [AS_KC][LD]
+    float* qs = ks + AS_KC * LD;  // [32][LD], row r = mi * G + hi
+    const int kvh = blockIdx.x, m0 = blockIdx.y * qt, t0 = blockIdx.z * AS_KC, tid = threadIdx.x;
+    const int G = n_q / n_kv, R = qt * G;
+    const int pos0 = *pos0p;
+    const int mlast = (m0 + qt < M ? m0 + qt : M) - 1;
+    if (t0 > pos0 + mlast) return;  // no query of the tile reaches these keys
+    for (int e = tid; e < AS_KC * (HD / 4); e += 256) {
+        const int kr = e / (HD / 4), c = e % (HD / 4);
+        const int t = t0 + kr < max_seq ? t0 + kr : max_seq - 1;
+        *(float4*)&ks[kr * LD + 4 * c] = *(const float4*)(kc + ((size_t)kvh * max_seq + t) * HD + 4 * c);
+    }
+    for (int e = tid; e < R * (HD / 4); e += 256) {
+        const int r = e / (HD / 4), c = e % (HD / 4);
+        const int mi = r / G, hi = r % G, m = m0 + mi < M ? m0 + mi : M - 1;
+        *(float4*)&qs[r * LD + 4 * c] = *(const float4*)(q + ((size_t)m * n_q + kvh * G + hi) * HD + 4 * c);
+    }
+    __syncthreads();
+    const int rp = tid >> 4, kq = tid & 15;
+    if (2 * rp >= R) return;
+    float acc[2][4][8];
+#pragma unroll
+    for (int a = 0; a < 2; a++)
+#pragma unroll
+        for (int b = 0; b < 4; b++)
+#pragma unroll
+            for (int j = 0; j < 8; j++) acc[a][b][j] = 0.0f;
+    const float* q0 = qs + (2 * rp) * LD;
+    const float* q1 = qs + (2 * rp + 1 < R ? 2 * rp + 1 : 2 * rp) * LD;
+    const float* k0 = ks + (4 * kq) * LD;
+    for (int i = 0; i < HD; i += 8) {
+        float qa[2][8], ka[4][8];
+        *(float4*)&qa[0][0] = *(const float4*)(q0 + i);
+        *(float4*)&qa[0][4] = *(const float4*)(q0 + i + 4);
+        *(float4*)&qa[1][0] = *(const float4*)(q1 + i);
+        *(float4*)&qa[1][4] = *(const float4*)(q1 + i + 4);
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            *(float4*)&ka[b][0] = *(const float4*)(k0 + b * LD + i);
+            *(float4*)&ka[b][4] = *(const float4*)(k0 + b * LD + i + 4);
+        }
+#pragma unroll
+        for (int a = 0; a < 2; a++)
+#pragma unroll
+            for (int b = 0; b < 4; b++)
+#pragma unroll
+                for (int j = 0; j < 8; j++) acc[a][b][j] = fmaf(qa[a][j], ka[b][j], acc[a][b][j]);
+    }
+#pragma unroll
+    for (int a = 0; a < 2; a++) {
+        const int r = 2 * rp + a;
+        if (r >= R) continue;
+        const int mi = r / G, hi = r % G, m = m0 + mi;
+        if (m >= M) continue;
+        const int L = pos0 + m + 1, n4 = L & ~3;
+        const bool single = (G & 1) && hi == G - 1;
+        float* srow = S + ((size_t)m * n_q + kvh * G + hi) * max_seq;
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            const int t = t0 + 4 * kq + b;
+            if (t >= L) continue;
+            float sc;
+            if (t < n4) sc = hsum8_hadd(acc[a][b]);
+            else if (!single) sc = hsum8(acc[a][b]);
+            else sc = score_dot2(qs + r * LD, ks + (4 * kq + b) * LD, HD);
+            srow[t] = sc * scale;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// k_attn_pv: softmax and P.V.  Workgroup (kv head, tile of qt queries, dim
+// chunk of HD / dc): the tile's score rows (R = qt x G, each kv_len(m) long)
+// are read into LDS and turned into probabilities as the reference does
+// (max; exp polynomial on the 8-aligned part, expf on the tail; the 8-lane
+// sum chains + eng_hsum256 + the tail added in order; 1 / (sum + 1e-12);
+// multiply), then thread (r, d) runs the row's P.V chain for dim d over the
+// keys in order (nested pairs for a single trailing head, as the reference's
+// single-head path), V staged in LDS in chunks of vk keys.  Every dim chunk
+// recomputes its rows' softmax (cheap next to P.V).
+// ---------------------------------------------------------------------------
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_pv(const float* __restrict__ S, const float* __restrict__ vc,
+                                                 const int32_t* __restrict__ pos0p, int M, int n_q, int n_kv,
+                                                 int max_seq, int qt, int dw, int lcap, int vk,
+                                                 float* __restrict__ out) {
+    extern __shared__ __align__(16) float sm[];
+    __shared__ float part[32][8];
+    __shared__ float rowv[32][2];  // max, 1 / sum
+    const int kvh = blockIdx.x, m0 = blockIdx.y * qt, d0 = blockIdx.z * dw, tid = threadIdx.x;
+    const int G = n_q / n_kv, R = qt * G;
+    const int pos0 = *pos0p;
+    float* P = sm;              // [R][lcap]
+    float* Vs = sm + R * lcap;  // [vk][dw]
+    int Lmax = 0;
+    for (int r = 0; r < R; r++) {
+        const int m = m0 + r / G;
+        if (m < M && pos0 + m + 1 > Lmax) Lmax = pos0 + m + 1;
+    }
+    // scores -> LDS
+    for (int r = 0; r < R; r++) {
+        const int m = m0 + r / G;
+        if (m >= M) continue;
+        const int L = pos0 + m + 1;
+        const float* srow = S + ((size_t)m * n_q + kvh * G + r % G) * max_seq;
+        for (int t = tid; t < L; t += 256) P[r * lcap + t] = srow[t];
+    }
+    __syncthreads();
+    // row max: thread (r, j) over t = j mod 8, then the 8 partials
+    {
+        const int r = tid >> 3, j = tid & 7;
+        if (r < R && m0 + r / G < M) {
+            const int L = pos0 + m0 + r / G + 1;
+            float mx = -1e30f;
+            for (int t = j; t < L; t += 8) mx = fmaxf(mx, P[r * lcap + t]);
+            part[r][j] = mx;
+        }
+    }
+    __syncthreads();
+    if (tid < R && m0 + tid / G < M) {
+        float mx = part[tid][0];
+        for (int j = 1; j < 8; j++) mx = fmaxf(mx, part[tid][j]);
+        rowv[tid][0] = mx;
+    }
+    __syncthreads();
+    for (int r = 0; r < R; r++) {
+        const int m = m0 + r / G;
+        if (m >= M) continue;
+        const int L = pos0 + m + 1, n8 = L & ~7;
+        const float mx = rowv[r][0];
+        for (int t = tid; t < L; t += 256) {
+            const float x = P[r * lcap + t] - mx;
+            P[r * lcap + t] = t < n8 ? exp_poly(x) : expf_libc(x);
+        }
+    }
+    __syncthreads();
+    {
+        const int r = tid >> 3, j = tid & 7;
+        if (r < R && m0 + r / G < M) {
+            const int L = pos0 + m0 + r / G + 1, n8 = L & ~7;
+            float a = 0.0f;
+            for (int t = j; t < n8; t += 8) a = a + P[r * lcap + t];
+            part[r][j] = a;
+        }
+    }
+    __syncthreads();
+    if (tid < R && m0 + tid / G < M) {
+        const int L = pos0 + m0 + tid / G + 1, n8 = L & ~7;
+        float sp = hsum8(part[tid]);
+        for (int t = n8; t < L; t++) sp += P[tid * lcap + t];
+        rowv[tid][1] = 1.0f / (sp + 1e-12f);
+    }
+    __syncthreads();
+    for (int r = 0; r < R; r++) {
+        const int m = m0 + r / G;
+        if (m >= M) continue;
+        const int L = pos0 + m + 1;
+        const float inv = rowv[r][1];
+        for (int t = tid; t < L; t += 256) P[r * lcap + t] = P[r * lcap + t] * inv;
+    }
+    // P.V
+    const int r = tid / dw, d = tid % dw;
+    const bool act = r < R && m0 + r / G < M;
+    const int L = act ? pos0 + m0 + r / G + 1 : 0;
+    const bool nested = (G & 1) && (r % G) == G - 1 && (HD & 63) == 0;
+    const float* prow = P + (act ? r : 0) * lcap;
+    const float* Vh = vc + (size_t)kvh * max_seq * HD + d0;
+    float a = 0.0f;
+    for (int c0 = 0; c0 < Lmax; c0 += vk) {
+        __syncthreads();  // previous chunk consumed (and P final on the first pass)
+        const int nk = Lmax - c0 < vk ? Lmax - c0 : vk;
+        for (int e = tid; e < nk * (dw / 4); e += 256) {
+            const int kr = e / (dw / 4), c = e % (dw / 4);
+            *(float4*)&Vs[kr * dw + 4 * c] = *(const float4*)(Vh + (size_t)(c0 + kr) * HD + 4 * c);
+        }
+        __syncthreads();
+        if (act && c0 < L) {
+            const int n = L - c0 < nk ? L - c0 : nk;
+            const float* pp = prow + c0;
+            if (!nested) {
+                int t = 0;
+                for (; t + 4 <= n; t += 4) {
+                    const float4 p4 = *(const float4*)(pp + t);
+                    const float v0 = Vs[t * dw + d], v1 = Vs[(t + 1) * dw + d];
+                    const float v2 = Vs[(t + 2) * dw + d], v3 = Vs[(t + 3) * dw + d];
+                    a = fmaf(p4.x, v0, a);
+                    a = fmaf(p4.y, v1, a);
+                    a = fmaf(p4.z, v2, a);
+                    a = fmaf(p4.w, v3, a);
+                }
+                for (; t < n; t++) a = fmaf(pp[t], Vs[t * dw + d], a);
+            } else {
+                int t = 0;
+                for (; t + 1 < n; t += 2) a = fmaf(pp[t], Vs[t * dw + d], fmaf(pp[t + 1], Vs[(t + 1) * dw + d], a));
+                if (t < n) a = fmaf(pp[t], Vs[t * dw + d], a);
+            }
+        }
+    }
+    if (act) out[((size_t)(m0 + r / G) * n_q + kvh * G + r % G) * HD + d0 + d] = a;
+}
+
 __global__ __launch_bounds__(256) void k_attn(const float* __restrict__ q, const float* __restrict__ kc,
                                               const float* __restrict__ vc, float* __restrict__ out,
                                               float* __restrict__ scores, const int32_t* __restrict__ pos0p,
@@ -2016,6 +2238,58 @@ void dpuf_hip_qk_rope_kv(void* s, int32_t M, float* q, float* k, const float* v,
     hipLaunchKernelGGL(k_qk_rope_kv, dim3(M, n_q + n_kv), dim3(hd), (size_t)hd * sizeof(float), ST(s), q, k, v,
                        q_norm, k_norm, eps, cos_tab, sin_tab, kc, vc, pos0, n_q, n_kv, hd, max_seq);
     LAUNCHED("k_qk_rope_kv");
+}
+
+// Split attention (k_attn_sc + k_attn_pv) over keys up to lmax = pos0 + M
+// (or max_seq when the launch is captured for replay at any position).
+// Returns -1 without launching when the shape does not fit (group > 32, head
+// dim not 64/128/256, or a tile's probabilities not fitting in LDS).
+int32_t dpuf_hip_attn_split(void* s, int32_t M, int32_t lmax, const float* q, const float* kc, const float* vc,
+                            float* out, float* scores, const int32_t* pos0p, int32_t n_q, int32_t n_kv, int32_t hd,
+                            int32_t max_seq, float scale) {
+    if (n_kv <= 0 || n_q % n_kv || n_q / n_kv > 32 || (hd != 64 && hd != 128 && hd != 256)) return -1;
+    if (lmax > max_seq) lmax = max_seq;
+    const int G = n_q / n_kv;
+    // scores: up to 32 q rows (queries x group heads) per workgroup
+    const int qt1 = 32 / G < M ? 32 / G : M;
+    const dim3 g1(n_kv, (M + qt1 - 1) / qt1, (lmax + AS_KC - 1) / AS_KC);
+    const size_t lds1 = (size_t)(AS_KC + 32) * (hd + 4) * 4;
+    // softmax + P.V: R = qt2 * G rows of lcap probabilities in LDS; about 8
+    // rows per workgroup keeps >= 32 dims per P.V chain group, so the
+    // softmax each dim chunk repeats stays small next to P.V
+    const int lcap = (lmax + 7) & ~7;
+    const size_t budget = 112 * 1024;
+    int qt2 = 8 / G > 1 ? 8 / G : 1;
+    if (qt2 > M) qt2 = M;
+    while (qt2 > 1 && (size_t)qt2 * G * lcap * 4 > budget) qt2--;
+    if ((size_t)qt2 * G * lcap * 4 > budget) return -1;
+    const int R = qt2 * G;
+    int dc = 1;
+    while (dc < hd / 4 && R * (hd / dc) > 256) dc *= 2;
+    const int tiles = n_kv * ((M + qt2 - 1) / qt2);
+    while (dc < hd / 4 && tiles * dc < 128) dc *= 2;  // enough workgroups to spread the V reads
+    const int dw = hd / dc;
+    const int vk = 4096 / dw;
+    const size_t lds2 = ((size_t)R * lcap + (size_t)vk * dw) * 4;
+    const dim3 g2(n_kv, (M + qt2 - 1) / qt2, dc);
+    if (hd == 64) {
+        hipLaunchKernelGGL(k_attn_sc<64>, g1, dim3(256), lds1, ST(s), q, kc, pos0p, M, n_q, n_kv, max_seq, scale,
+                           qt1, scores);
+        hipLaunchKernelGGL(k_attn_pv<64>, g2, dim3(256), lds2, ST(s), scores, vc, pos0p, M, n_q, n_kv, max_seq,
+                           qt2, dw, lcap, vk, out);
+    } else if (hd == 128) {
+        hipLaunchKernelGGL(k_attn_sc<128>, g1, dim3(256), lds1, ST(s), q, kc, pos0p, M, n_q, n_kv, max_seq, scale,
+                           qt1, scores);
+        hipLaunchKernelGGL(k_attn_pv<128>, g2, dim3(256), lds2, ST(s), scores, vc, pos0p, M, n_q, n_kv, max_seq,
+                           qt2, dw, lcap, vk, out);
+    } else {
+        hipLaunchKernelGGL(k_attn_sc<256>, g1, dim3(256), lds1, ST(s), q, kc, pos0p, M, n_q, n_kv, max_seq, scale,
+                           qt1, scores);
+        hipLaunchKernelGGL(k_attn_pv<256>, g2, dim3(256), lds2, ST(s), scores, vc, pos0p, M, n_q, n_kv, max_seq,
+                           qt2, dw, lcap, vk, out);
+    }
+    LAUNCHED("k_attn_split");
+    return 0;
 }
 
 void dpuf_hip_attn(void* s, int32_t M, const float* q, const float* kc, const float* vc, float* out, float* scores,

@@ -151,3 +151,39 @@ def test_lm_early_exit(eng, orc, monkeypatch, cap):
     finally:
         eng.dpuf_amd_set_gemv_max_workgroups(0)
         p.close()
+
+
+@pytest.mark.parametrize("heads", [(4, 2), (6, 2)])
+def test_long_context_split_attention(eng, orc, heads):
+    """Prefill in two chunks (M > 1 at pos0 0 and pos0 > 0) and decode past
+    192 keys, where decode switches to the split attention kernels; also the
+    captured-graph decode at that length.  (6, 2) heads give groups of three,
+    so the third head takes the reference's single-head path.  Logits
+    bit-identical to the oracle throughout."""
+    nq, nkv = heads
+    shape = dict(TINY, num_q_heads=nq, num_kv_heads=nkv)
+    m = M.Model.build(shape, max_seq_len=320, seed=11)
+    p = Pair(eng, orc, m)
+    rng = np.random.default_rng(7)
+    ids = rng.integers(0, 4096, 260).astype(np.int32)
+    print(f"split attention heads={heads}: prefill 160 + 100", flush=True)
+    lg, lo = p.forward(ids[:160], 0, only_last=0)
+    assert _bits_equal(lg, lo), np.max(np.abs(lg - lo))
+    lg, lo = p.forward(ids[160:], 160, only_last=0)
+    assert _bits_equal(lg, lo), np.max(np.abs(lg - lo))
+    tok = int(np.argmax(lo[-1]))
+    for step in range(4):
+        lg, lo = p.forward(np.array([tok], np.int32), 260 + step)
+        assert _bits_equal(lg, lo), (step, np.max(np.abs(lg - lo)))
+        tok = int(np.argmax(lo[0]))
+    import ctypes as C
+    out = C.c_int32(-1)
+    for step in range(4, 8):
+        rc = eng.dpuf_amd_engine_forward_argmax(p.g, 1, M.ptr(np.array([tok], np.int32)), 260 + step, None, 1,
+                                                C.byref(out), None)
+        assert rc == 0
+        lo = np.zeros(4096, np.float32)
+        orc.orc_engine_forward(p.o, 1, M.ptr(np.array([tok], np.int32)), 260 + step, None, 1, M.ptr(lo))
+        assert out.value == orc.orc_argmax(M.ptr(lo), 4096)
+        tok = out.value
+    p.close()
