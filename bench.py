@@ -65,6 +65,9 @@ def main():
     ap.add_argument("--prompt", type=int, default=32)
     ap.add_argument("--pp", type=int, default=512, help="prefill length of the pp measurement (0 = skip)")
     ap.add_argument("--keep-tiles", type=int, default=224, help="down-projection tiles kept in the pp run")
+    ap.add_argument("--long-ctx", type=int, default=4096,
+                    help="KV-cache length of the long-context decode leg (0 = skip)")
+    ap.add_argument("--long-steps", type=int, default=128, help="decode steps of the long-context leg")
     ap.add_argument("--cpu-seconds", type=float, default=20.0, help="budget of the CPU baseline (0 = skip)")
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--graph", type=int, default=1, help="also time the device-argmax entry with HIP graph replay")
@@ -89,6 +92,8 @@ def main():
     shape = M.QWEN3_8B if args.model == "8b" else M.QWEN3_0_6B
     V = shape["vocab_size"]
     max_seq = max(args.prompt + args.warmup + args.steps + 8, args.pp, 64)
+    if args.long_ctx > 0:
+        max_seq = max(max_seq, args.long_ctx + args.long_steps + 8)
     t = time.time()
     model = M.Model.build(shape, max_seq_len=max_seq, seed=args.seed)
     log(f"model {args.model}: {model.weight_bytes()} bytes of packed weights, built in {time.time() - t:.1f}s")
@@ -225,6 +230,42 @@ def main():
         pp = dict(tokens=args.pp, keep_tiles=args.keep_tiles, ms=best * 1e3, tok_s=args.pp / best)
         log(f"pp{args.pp}: {best * 1e3:.1f} ms, {args.pp / best:.1f} tok/s")
 
+    # --- long context: decode against an injected fp32 KV cache ------------
+    long = None
+    if args.long_ctx > 0:
+        L, nkv, hd = shape["num_layers"], shape["num_kv_heads"], shape["head_dim"]
+        krng = np.random.default_rng(args.seed + 4096)
+        eng.dpuf_engine_reset_cache(h)
+        t = time.time()
+        for layer in range(L):
+            for kh in range(nkv):
+                kk = krng.standard_normal((args.long_ctx, hd), dtype=np.float32)
+                vv = krng.standard_normal((args.long_ctx, hd), dtype=np.float32)
+                assert eng.dpuf_amd_engine_set_kv(h, layer, kh, 0, args.long_ctx, M.ptr(kk), M.ptr(vv)) == 0
+        log(f"long context: {args.long_ctx}-token N(0,1) KV cache injected in {time.time() - t:.1f}s")
+        tok = int(rng.integers(0, V))
+        tok = decode(tok, args.long_ctx, 2)  # warm-up (positions long_ctx, +1)
+        lids = []
+        t0 = time.perf_counter()
+        decode(tok, args.long_ctx + 2, args.long_steps, lids)
+        t1 = time.perf_counter()
+        ms_long = (t1 - t0) * 1e3 / args.long_steps
+        # attention time per token from HIP events (re-decoding the last 8 positions)
+        eng.dpuf_amd_engine_set_timing(h, 1)
+        decode(tok, args.long_ctx + 2 + args.long_steps - 8, 8)
+        ams, acnt, aby = C.c_double(), C.c_int64(), C.c_double()
+        eng.dpuf_amd_engine_get_timing(h, KINDS.index("attention"), C.byref(ams), C.byref(acnt), C.byref(aby))
+        eng.dpuf_amd_engine_set_timing(h, 0)
+        att_ms = ams.value / 8
+        ctx_mid = args.long_ctx + 2 + args.long_steps // 2
+        kv_bytes = 2 * L * nkv * ctx_mid * hd * 4  # K and V rows read per decoded token
+        long = dict(ctx=args.long_ctx, steps=args.long_steps, ms_per_token=round(ms_long, 4),
+                    tok_s=round(1e3 / ms_long, 3), attention_ms_per_token=round(att_ms, 4),
+                    kv_bytes_per_token=kv_bytes, kv_read_GBs=round(kv_bytes / (att_ms * 1e-3) / 1e9, 1),
+                    ids_head=lids[:8])
+        log(f"long context {args.long_ctx}: {ms_long:.3f} ms/token ({1e3 / ms_long:.1f} tok/s), attention "
+            f"{att_ms:.3f} ms/token -> KV reads {long['kv_read_GBs']} GB/s")
+
     eng.dpuf_engine_destroy(h)
 
     # --- CPU baseline: the oracle on the host cores, bounded sample ---------
@@ -276,6 +317,7 @@ def main():
                    "ms_per_token_by_kind": {k: round(v["ms"] / (args.warmup + args.steps), 4)
                                             for k, v in kinds.items()}},
         "pp": pp,
+        "long_context": long,
         "roofline": rl,
         "cpu_baseline": cpu,
         "resident_weight_bytes": wbytes,

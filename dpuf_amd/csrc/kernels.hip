@@ -1114,6 +1114,8 @@ DEV float score_dot2(const float* q, const float* kp, int hd) {
     return hsum8(cc);
 }
 
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
 // ---------------------------------------------------------------------------
 // Split attention for prefill and long-context decode: the same arithmetic as
 // gqa_attn_head_pair_f32 (dpuf_engine.c:341-577) spread over the GPU.
@@ -1216,122 +1218,233 @@ __global__ __launch_bounds__(256) void k_attn_sc(const float* __restrict__ q, co
 // single-head path), V staged in LDS in chunks of vk keys.  Every dim chunk
 // recomputes its rows' softmax (cheap next to P.V).
 // ---------------------------------------------------------------------------
+// Sequential chain a = a + x[0] + x[step] + x[2 step] ... over n LDS values,
+// read in batches of 16 with the next batch in flight.
+DEV float lds_sum_chain(const float* x, int step, int n) {
+    float a = 0.0f;
+    int k = 0;
+    if (n >= 32) {
+        float cur[16], nxt[16];
+#pragma unroll
+        for (int i = 0; i < 16; i++) cur[i] = x[i * step];
+        for (k = 16; k + 16 <= n; k += 16) {
+#pragma unroll
+            for (int i = 0; i < 16; i++) nxt[i] = x[(k + i) * step];
+#pragma unroll
+            for (int i = 0; i < 16; i++) a = a + cur[i];
+#pragma unroll
+            for (int i = 0; i < 16; i++) cur[i] = nxt[i];
+        }
+#pragma unroll
+        for (int i = 0; i < 16; i++) a = a + cur[i];
+    }
+    for (; k < n; k++) a = a + x[k * step];
+    return a;
+}
+
+// P.V chain of one (row, dim) over n keys of a chunk, in key order:
+// a = fma(p[t], v[t], a), or the nested pairs a = fma(p[t], v[t],
+// fma(p[t+1], v[t+1], a)) of the reference's single-head path.  p and v are
+// 16-byte aligned LDS rows (v: this dim's values for consecutive keys); keys
+// go in batches of 16 from two alternating register sets, so one batch's
+// reads are in flight while the other's FMAs run.
+DEV void pv_load16(const float* p, const float* v, int t, float4 (&pb)[4], float4 (&vb)[4]) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        pb[i] = *(const float4*)(p + t + 4 * i);
+        vb[i] = *(const float4*)(v + t + 4 * i);
+    }
+}
+
+template <bool NESTED>
+DEV float pv_fma16(const float4 (&pb)[4], const float4 (&vb)[4], float a) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        if (NESTED) {
+            a = fmaf(pb[i].x, vb[i].x, fmaf(pb[i].y, vb[i].y, a));
+            a = fmaf(pb[i].z, vb[i].z, fmaf(pb[i].w, vb[i].w, a));
+        } else {
+            a = fmaf(pb[i].x, vb[i].x, a);
+            a = fmaf(pb[i].y, vb[i].y, a);
+            a = fmaf(pb[i].z, vb[i].z, a);
+            a = fmaf(pb[i].w, vb[i].w, a);
+        }
+    }
+    return a;
+}
+
+template <bool NESTED>
+DEV float pv_chain(const float* p, const float* v, int n, float a) {
+    const int n16 = n & ~15;
+    int t = 0;
+    if (n16 > 0) {
+        float4 pa[4], va[4], pb[4], vb[4];
+        pv_load16(p, v, 0, pa, va);
+        for (t = 0; t + 32 <= n16; t += 32) {
+            pv_load16(p, v, t + 16, pb, vb);
+            a = pv_fma16<NESTED>(pa, va, a);
+            pv_load16(p, v, t + 32 < n16 ? t + 32 : t, pa, va);  // the last reload is unused
+            a = pv_fma16<NESTED>(pb, vb, a);
+        }
+        if (t < n16) {
+            a = pv_fma16<NESTED>(pa, va, a);
+            t += 16;
+        }
+    }
+    if (NESTED) {
+        for (; t + 1 < n; t += 2) a = fmaf(p[t], v[t], fmaf(p[t + 1], v[t + 1], a));
+        if (t < n) a = fmaf(p[t], v[t], a);
+    } else {
+        for (; t < n; t++) a = fmaf(p[t], v[t], a);
+    }
+    return a;
+}
+
 template <int HD>
 __global__ __launch_bounds__(256) void k_attn_pv(const float* __restrict__ S, const float* __restrict__ vc,
                                                  const int32_t* __restrict__ pos0p, int M, int n_q, int n_kv,
                                                  int max_seq, int qt, int dw, int lcap, int vk,
                                                  float* __restrict__ out) {
     extern __shared__ __align__(16) float sm[];
-    __shared__ float part[32][8];
+    __shared__ float part[256];
     __shared__ float rowv[32][2];  // max, 1 / sum
     const int kvh = blockIdx.x, m0 = blockIdx.y * qt, d0 = blockIdx.z * dw, tid = threadIdx.x;
-    const int G = n_q / n_kv, R = qt * G;
+    const int lane = tid & 63, wv = tid >> 6;
+    const int G = n_q / n_kv, R = qt * G, tpr = 256 / R;
     const int pos0 = *pos0p;
-    float* P = sm;              // [R][lcap]
-    float* Vs = sm + R * lcap;  // [vk][dw]
+    float* P = sm;  // [R][lcap], padded to a multiple of 1024 floats
+    float* Vs = sm + ((R * lcap + 1023) & ~1023);  // [2][dw][vk + 4]: a dim's keys contiguous
+    const int vld = vk + 4;
+    auto row_len = [&](int r) { return m0 + r / G < M ? pos0 + m0 + r / G + 1 : 0; };
     int Lmax = 0;
-    for (int r = 0; r < R; r++) {
-        const int m = m0 + r / G;
-        if (m < M && pos0 + m + 1 > Lmax) Lmax = pos0 + m + 1;
-    }
-    // scores -> LDS
-    for (int r = 0; r < R; r++) {
-        const int m = m0 + r / G;
-        if (m >= M) continue;
-        const int L = pos0 + m + 1;
-        const float* srow = S + ((size_t)m * n_q + kvh * G + r % G) * max_seq;
-        for (int t = tid; t < L; t += 256) P[r * lcap + t] = srow[t];
-    }
-    __syncthreads();
-    // row max: thread (r, j) over t = j mod 8, then the 8 partials
+    for (int r = 0; r < R; r++) Lmax = row_len(r) > Lmax ? row_len(r) : Lmax;
+    // V chunk c -> registers (issued early); registers -> LDS, transposed
+    const float* Vh = vc + (size_t)kvh * max_seq * HD + d0;
+    const int nv4 = vk * (dw / 4);  // float4 per chunk (1024)
+    float4 vreg[4];
+    auto v_load = [&](int c0) {
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int e = tid + 256 * k, kr = e / (dw / 4), c = e % (dw / 4);
+            vreg[k] = (e < nv4 && c0 + kr < Lmax) ? *(const float4*)(Vh + (size_t)(c0 + kr) * HD + 4 * c)
+                                                  : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+    };
+    auto v_store = [&](int buf) {
+        float* vb = Vs + buf * dw * vld;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int e = tid + 256 * k, kr = e / (dw / 4), c = e % (dw / 4);
+            if (e < nv4) {
+                vb[(4 * c + 0) * vld + kr] = vreg[k].x;
+                vb[(4 * c + 1) * vld + kr] = vreg[k].y;
+                vb[(4 * c + 2) * vld + kr] = vreg[k].z;
+                vb[(4 * c + 3) * vld + kr] = vreg[k].w;
+            }
+        }
+    };
+    v_load(0);
+    // score rows -> LDS by direct-to-LDS loads (1 KB per wave instruction,
+    // all in flight together; the last one may run into the padding);
+    // elements past a row's length are don't-care
     {
-        const int r = tid >> 3, j = tid & 7;
-        if (r < R && m0 + r / G < M) {
-            const int L = pos0 + m0 + r / G + 1;
-            float mx = -1e30f;
-            for (int t = j; t < L; t += 8) mx = fmaxf(mx, P[r * lcap + t]);
-            part[r][j] = mx;
+        const int n4w = lcap >> 2, tot = R * n4w;
+        for (int base = wv * 64; base < tot; base += 256) {
+            const int e = base + lane, r = e / n4w, c = e % n4w;
+            const int rr = e < tot ? r : 0, mq = m0 + rr / G < M ? m0 + rr / G : M - 1;
+            int t = 4 * c;
+            if (e >= tot || t + 3 >= max_seq) t = 0;
+            const float* src = S + ((size_t)mq * n_q + kvh * G + rr % G) * max_seq + t;
+            __builtin_amdgcn_global_load_lds((const void*)src, (lds_ptr_t)(P + 4 * base), 16, 0, 0);
         }
     }
+    v_store(0);
     __syncthreads();
-    if (tid < R && m0 + tid / G < M) {
-        float mx = part[tid][0];
-        for (int j = 1; j < 8; j++) mx = fmaxf(mx, part[tid][j]);
+    // row max (tpr threads per row)
+    {
+        const int r = tid / tpr, j = tid % tpr;
+        float mx = -1e30f;
+        if (r < R) {
+            const int L = row_len(r);
+            for (int t = j; t < L; t += tpr) mx = fmaxf(mx, P[r * lcap + t]);
+        }
+        part[tid] = mx;
+    }
+    __syncthreads();
+    if (tid < R) {
+        float mx = part[tid * tpr];
+        for (int j = 1; j < tpr; j++) mx = fmaxf(mx, part[tid * tpr + j]);
         rowv[tid][0] = mx;
     }
     __syncthreads();
-    for (int r = 0; r < R; r++) {
-        const int m = m0 + r / G;
-        if (m >= M) continue;
-        const int L = pos0 + m + 1, n8 = L & ~7;
-        const float mx = rowv[r][0];
-        for (int t = tid; t < L; t += 256) {
-            const float x = P[r * lcap + t] - mx;
-            P[r * lcap + t] = t < n8 ? exp_poly(x) : expf_libc(x);
-        }
-    }
-    __syncthreads();
+    // exp: the polynomial on t < kv_len & ~7 (float4 at a time), expf on the tail
     {
-        const int r = tid >> 3, j = tid & 7;
-        if (r < R && m0 + r / G < M) {
-            const int L = pos0 + m0 + r / G + 1, n8 = L & ~7;
-            float a = 0.0f;
-            for (int t = j; t < n8; t += 8) a = a + P[r * lcap + t];
-            part[r][j] = a;
+        const int n4w = lcap >> 2;
+        for (int e = tid; e < R * n4w; e += 256) {
+            const int r = e / n4w, c = e % n4w, n8 = row_len(r) & ~7;
+            if (4 * c >= n8) continue;
+            const float mx = rowv[r][0];
+            float4 x = *(float4*)&P[r * lcap + 4 * c];
+            x.x = exp_poly(x.x - mx);
+            x.y = exp_poly(x.y - mx);
+            x.z = exp_poly(x.z - mx);
+            x.w = exp_poly(x.w - mx);
+            *(float4*)&P[r * lcap + 4 * c] = x;
+        }
+        if (tid < 8 * R) {
+            const int r = tid >> 3, L = row_len(r), t = (L & ~7) + (tid & 7);
+            if (t < L) P[r * lcap + t] = expf_libc(P[r * lcap + t] - rowv[r][0]);
         }
     }
     __syncthreads();
-    if (tid < R && m0 + tid / G < M) {
-        const int L = pos0 + m0 + tid / G + 1, n8 = L & ~7;
-        float sp = hsum8(part[tid]);
+    // the reference's eight sum lanes, each a chain over t = j (mod 8)
+    if (tid < 8 * R) {
+        const int r = tid >> 3, j = tid & 7;
+        const int n8 = row_len(r) & ~7;
+        part[tid] = lds_sum_chain(P + r * lcap + j, 8, n8 >> 3);
+    }
+    __syncthreads();
+    if (tid < R) {
+        const int L = row_len(tid), n8 = L & ~7;
+        float sp = hsum8(part + 8 * tid);
         for (int t = n8; t < L; t++) sp += P[tid * lcap + t];
         rowv[tid][1] = 1.0f / (sp + 1e-12f);
     }
     __syncthreads();
-    for (int r = 0; r < R; r++) {
-        const int m = m0 + r / G;
-        if (m >= M) continue;
-        const int L = pos0 + m + 1;
-        const float inv = rowv[r][1];
-        for (int t = tid; t < L; t += 256) P[r * lcap + t] = P[r * lcap + t] * inv;
+    {
+        const int n4w = lcap >> 2;
+        for (int e = tid; e < R * n4w; e += 256) {
+            const int r = e / n4w, c = e % n4w;
+            if (4 * c >= row_len(r)) continue;
+            const float inv = rowv[r][1];
+            float4 x = *(float4*)&P[r * lcap + 4 * c];
+            x.x = x.x * inv;
+            x.y = x.y * inv;
+            x.z = x.z * inv;
+            x.w = x.w * inv;
+            *(float4*)&P[r * lcap + 4 * c] = x;
+        }
     }
-    // P.V
+    // P.V: thread (r, d); V chunks double-buffered, the next one loading
+    // while the current one is consumed
     const int r = tid / dw, d = tid % dw;
-    const bool act = r < R && m0 + r / G < M;
-    const int L = act ? pos0 + m0 + r / G + 1 : 0;
+    const bool act = r < R && row_len(r) > 0;
+    const int L = act ? row_len(r) : 0;
     const bool nested = (G & 1) && (r % G) == G - 1 && (HD & 63) == 0;
     const float* prow = P + (act ? r : 0) * lcap;
-    const float* Vh = vc + (size_t)kvh * max_seq * HD + d0;
     float a = 0.0f;
+    int buf = 0;
     for (int c0 = 0; c0 < Lmax; c0 += vk) {
-        __syncthreads();  // previous chunk consumed (and P final on the first pass)
-        const int nk = Lmax - c0 < vk ? Lmax - c0 : vk;
-        for (int e = tid; e < nk * (dw / 4); e += 256) {
-            const int kr = e / (dw / 4), c = e % (dw / 4);
-            *(float4*)&Vs[kr * dw + 4 * c] = *(const float4*)(Vh + (size_t)(c0 + kr) * HD + 4 * c);
-        }
-        __syncthreads();
+        const bool more = c0 + vk < Lmax;
+        if (more) v_load(c0 + vk);
+        __syncthreads();  // chunk c0 in Vs[buf] (and P final on the first pass)
         if (act && c0 < L) {
-            const int n = L - c0 < nk ? L - c0 : nk;
-            const float* pp = prow + c0;
-            if (!nested) {
-                int t = 0;
-                for (; t + 4 <= n; t += 4) {
-                    const float4 p4 = *(const float4*)(pp + t);
-                    const float v0 = Vs[t * dw + d], v1 = Vs[(t + 1) * dw + d];
-                    const float v2 = Vs[(t + 2) * dw + d], v3 = Vs[(t + 3) * dw + d];
-                    a = fmaf(p4.x, v0, a);
-                    a = fmaf(p4.y, v1, a);
-                    a = fmaf(p4.z, v2, a);
-                    a = fmaf(p4.w, v3, a);
-                }
-                for (; t < n; t++) a = fmaf(pp[t], Vs[t * dw + d], a);
-            } else {
-                int t = 0;
-                for (; t + 1 < n; t += 2) a = fmaf(pp[t], Vs[t * dw + d], fmaf(pp[t + 1], Vs[(t + 1) * dw + d], a));
-                if (t < n) a = fmaf(pp[t], Vs[t * dw + d], a);
-            }
+            const int n = L - c0 < vk ? L - c0 : vk;
+            const float* vp = Vs + buf * dw * vld + d * vld;
+            a = nested ? pv_chain<true>(prow + c0, vp, n, a) : pv_chain<false>(prow + c0, vp, n, a);
         }
+        if (more) v_store(buf ^ 1);
+        buf ^= 1;
     }
     if (act) out[((size_t)(m0 + r / G) * n_q + kvh * G + r % G) * HD + d0 + d] = a;
 }
@@ -1456,7 +1569,6 @@ __global__ __launch_bounds__(256) void k_attn(const float* __restrict__ q, const
 // ---------------------------------------------------------------------------
 #define ATT_KEYS 128  // keys per pass: 2 lanes per key, 256 threads
 
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 DEV float shx(float v, int m) { return __shfl_xor(v, m, 64); }
 
@@ -2269,8 +2381,8 @@ int32_t dpuf_hip_attn_split(void* s, int32_t M, int32_t lmax, const float* q, co
     const int tiles = n_kv * ((M + qt2 - 1) / qt2);
     while (dc < hd / 4 && tiles * dc < 128) dc *= 2;  // enough workgroups to spread the V reads
     const int dw = hd / dc;
-    const int vk = 4096 / dw;
-    const size_t lds2 = ((size_t)R * lcap + (size_t)vk * dw) * 4;
+    const int vk = 4096 / dw;  // V chunk: 16 KB (+ padding), two buffers
+    const size_t lds2 = ((((size_t)R * lcap + 1023) & ~(size_t)1023) + 2 * (size_t)(vk + 4) * dw) * 4;
     const dim3 g2(n_kv, (M + qt2 - 1) / qt2, dc);
     if (hd == 64) {
         hipLaunchKernelGGL(k_attn_sc<64>, g1, dim3(256), lds1, ST(s), q, kc, pos0p, M, n_q, n_kv, max_seq, scale,
