@@ -1144,15 +1144,33 @@ __global__ __launch_bounds__(256) void k_attn_sc(const float* __restrict__ q, co
     const int pos0 = *pos0p;
     const int mlast = (m0 + qt < M ? m0 + qt : M) - 1;
     if (t0 > pos0 + mlast) return;  // no query of the tile reaches these keys
-    for (int e = tid; e < AS_KC * (HD / 4); e += 256) {
-        const int kr = e / (HD / 4), c = e % (HD / 4);
-        const int t = t0 + kr < max_seq ? t0 + kr : max_seq - 1;
-        *(float4*)&ks[kr * LD + 4 * c] = *(const float4*)(kc + ((size_t)kvh * max_seq + t) * HD + 4 * c);
-    }
-    for (int e = tid; e < R * (HD / 4); e += 256) {
-        const int r = e / (HD / 4), c = e % (HD / 4);
-        const int mi = r / G, hi = r % G, m = m0 + mi < M ? m0 + mi : M - 1;
-        *(float4*)&qs[r * LD + 4 * c] = *(const float4*)(q + ((size_t)m * n_q + kvh * G + hi) * HD + 4 * c);
+    {
+        // every thread's K and q loads are issued before any LDS store
+        constexpr int NK = AS_KC * (HD / 4) / 256, NQ = 32 * (HD / 4) / 256;
+        float4 kx[NK], qx[NQ];
+#pragma unroll
+        for (int k = 0; k < NK; k++) {
+            const int e = tid + 256 * k, kr = e / (HD / 4), c = e % (HD / 4);
+            const int t = t0 + kr < max_seq ? t0 + kr : max_seq - 1;
+            kx[k] = *(const float4*)(kc + ((size_t)kvh * max_seq + t) * HD + 4 * c);
+        }
+#pragma unroll
+        for (int k = 0; k < NQ; k++) {
+            const int e = tid + 256 * k, r = e / (HD / 4), c = e % (HD / 4);
+            const int mi = r / G, hi = r % G, m = m0 + mi < M ? m0 + mi : M - 1;
+            qx[k] = r < R ? *(const float4*)(q + ((size_t)m * n_q + kvh * G + hi) * HD + 4 * c)
+                          : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+#pragma unroll
+        for (int k = 0; k < NK; k++) {
+            const int e = tid + 256 * k, kr = e / (HD / 4), c = e % (HD / 4);
+            *(float4*)&ks[kr * LD + 4 * c] = kx[k];
+        }
+#pragma unroll
+        for (int k = 0; k < NQ; k++) {
+            const int e = tid + 256 * k, r = e / (HD / 4), c = e % (HD / 4);
+            *(float4*)&qs[r * LD + 4 * c] = qx[k];
+        }
     }
     __syncthreads();
     const int rp = tid >> 4, kq = tid & 15;
@@ -1242,9 +1260,10 @@ DEV float lds_sum_chain(const float* x, int step, int n) {
     return a;
 }
 
-// P.V chain of one (row, dim) over n keys of a chunk, in key order:
-// a = fma(p[t], v[t], a), or the nested pairs a = fma(p[t], v[t],
-// fma(p[t+1], v[t+1], a)) of the reference's single-head path.  p and v are
+// P.V chain of one (row, dim) over n keys of a chunk, in key order, with
+// p[t] = e[t] * inv: a = fma(p[t], v[t], a), or the nested pairs
+// a = fma(p[t], v[t], fma(p[t+1], v[t+1], a)) of the reference's
+// single-head path.  p and v are
 // 16-byte aligned LDS rows (v: this dim's values for consecutive keys); keys
 // go in batches of 16 from two alternating register sets, so one batch's
 // reads are in flight while the other's FMAs run.
@@ -1257,24 +1276,25 @@ DEV void pv_load16(const float* p, const float* v, int t, float4 (&pb)[4], float
 }
 
 template <bool NESTED>
-DEV float pv_fma16(const float4 (&pb)[4], const float4 (&vb)[4], float a) {
+DEV float pv_fma16(const float4 (&pb)[4], const float4 (&vb)[4], float inv, float a) {
 #pragma unroll
     for (int i = 0; i < 4; i++) {
+        const float p0 = pb[i].x * inv, p1 = pb[i].y * inv, p2 = pb[i].z * inv, p3 = pb[i].w * inv;
         if (NESTED) {
-            a = fmaf(pb[i].x, vb[i].x, fmaf(pb[i].y, vb[i].y, a));
-            a = fmaf(pb[i].z, vb[i].z, fmaf(pb[i].w, vb[i].w, a));
+            a = fmaf(p0, vb[i].x, fmaf(p1, vb[i].y, a));
+            a = fmaf(p2, vb[i].z, fmaf(p3, vb[i].w, a));
         } else {
-            a = fmaf(pb[i].x, vb[i].x, a);
-            a = fmaf(pb[i].y, vb[i].y, a);
-            a = fmaf(pb[i].z, vb[i].z, a);
-            a = fmaf(pb[i].w, vb[i].w, a);
+            a = fmaf(p0, vb[i].x, a);
+            a = fmaf(p1, vb[i].y, a);
+            a = fmaf(p2, vb[i].z, a);
+            a = fmaf(p3, vb[i].w, a);
         }
     }
     return a;
 }
 
 template <bool NESTED>
-DEV float pv_chain(const float* p, const float* v, int n, float a) {
+DEV float pv_chain(const float* p, const float* v, int n, float inv, float a) {
     const int n16 = n & ~15;
     int t = 0;
     if (n16 > 0) {
@@ -1282,20 +1302,22 @@ DEV float pv_chain(const float* p, const float* v, int n, float a) {
         pv_load16(p, v, 0, pa, va);
         for (t = 0; t + 32 <= n16; t += 32) {
             pv_load16(p, v, t + 16, pb, vb);
-            a = pv_fma16<NESTED>(pa, va, a);
+            __builtin_amdgcn_sched_barrier(0);  // keep the next batch's reads ahead of these FMAs
+            a = pv_fma16<NESTED>(pa, va, inv, a);
             pv_load16(p, v, t + 32 < n16 ? t + 32 : t, pa, va);  // the last reload is unused
-            a = pv_fma16<NESTED>(pb, vb, a);
+            __builtin_amdgcn_sched_barrier(0);
+            a = pv_fma16<NESTED>(pb, vb, inv, a);
         }
         if (t < n16) {
-            a = pv_fma16<NESTED>(pa, va, a);
+            a = pv_fma16<NESTED>(pa, va, inv, a);
             t += 16;
         }
     }
     if (NESTED) {
-        for (; t + 1 < n; t += 2) a = fmaf(p[t], v[t], fmaf(p[t + 1], v[t + 1], a));
-        if (t < n) a = fmaf(p[t], v[t], a);
+        for (; t + 1 < n; t += 2) a = fmaf(p[t] * inv, v[t], fmaf(p[t + 1] * inv, v[t + 1], a));
+        if (t < n) a = fmaf(p[t] * inv, v[t], a);
     } else {
-        for (; t < n; t++) a = fmaf(p[t], v[t], a);
+        for (; t < n; t++) a = fmaf(p[t] * inv, v[t], a);
     }
     return a;
 }
@@ -1360,15 +1382,22 @@ __global__ __launch_bounds__(256) void k_attn_pv(const float* __restrict__ S, co
     }
     v_store(0);
     __syncthreads();
-    // row max (tpr threads per row)
+    // row max (tpr threads per row, float4 reads, four running maxima)
     {
         const int r = tid / tpr, j = tid % tpr;
-        float mx = -1e30f;
+        float m4[4] = {-1e30f, -1e30f, -1e30f, -1e30f};
         if (r < R) {
-            const int L = row_len(r);
-            for (int t = j; t < L; t += tpr) mx = fmaxf(mx, P[r * lcap + t]);
+            const int L = row_len(r), L4 = L & ~3;
+            for (int t = 4 * j; t < L4; t += 4 * tpr) {
+                const float4 x = *(const float4*)&P[r * lcap + t];
+                m4[0] = fmaxf(m4[0], x.x);
+                m4[1] = fmaxf(m4[1], x.y);
+                m4[2] = fmaxf(m4[2], x.z);
+                m4[3] = fmaxf(m4[3], x.w);
+            }
+            if (j < L - L4) m4[0] = fmaxf(m4[0], P[r * lcap + L4 + j]);
         }
-        part[tid] = mx;
+        part[tid] = fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3]));
     }
     __syncthreads();
     if (tid < R) {
@@ -1410,23 +1439,10 @@ __global__ __launch_bounds__(256) void k_attn_pv(const float* __restrict__ S, co
         for (int t = n8; t < L; t++) sp += P[tid * lcap + t];
         rowv[tid][1] = 1.0f / (sp + 1e-12f);
     }
-    __syncthreads();
-    {
-        const int n4w = lcap >> 2;
-        for (int e = tid; e < R * n4w; e += 256) {
-            const int r = e / n4w, c = e % n4w;
-            if (4 * c >= row_len(r)) continue;
-            const float inv = rowv[r][1];
-            float4 x = *(float4*)&P[r * lcap + 4 * c];
-            x.x = x.x * inv;
-            x.y = x.y * inv;
-            x.z = x.z * inv;
-            x.w = x.w * inv;
-            *(float4*)&P[r * lcap + 4 * c] = x;
-        }
-    }
-    // P.V: thread (r, d); V chunks double-buffered, the next one loading
-    // while the current one is consumed
+    // P.V: thread (r, d); the probability p = e * inv is formed as each key
+    // is consumed (the reference's normalising multiply, off the FMA chain);
+    // V chunks double-buffered, the next one loading while the current one is
+    // consumed
     const int r = tid / dw, d = tid % dw;
     const bool act = r < R && row_len(r) > 0;
     const int L = act ? row_len(r) : 0;
@@ -1437,11 +1453,12 @@ __global__ __launch_bounds__(256) void k_attn_pv(const float* __restrict__ S, co
     for (int c0 = 0; c0 < Lmax; c0 += vk) {
         const bool more = c0 + vk < Lmax;
         if (more) v_load(c0 + vk);
-        __syncthreads();  // chunk c0 in Vs[buf] (and P final on the first pass)
+        __syncthreads();  // chunk c0 in Vs[buf] (and rowv final on the first pass)
         if (act && c0 < L) {
             const int n = L - c0 < vk ? L - c0 : vk;
             const float* vp = Vs + buf * dw * vld + d * vld;
-            a = nested ? pv_chain<true>(prow + c0, vp, n, a) : pv_chain<false>(prow + c0, vp, n, a);
+            const float inv = rowv[r][1];
+            a = nested ? pv_chain<true>(prow + c0, vp, n, inv, a) : pv_chain<false>(prow + c0, vp, n, inv, a);
         }
         if (more) v_store(buf ^ 1);
         buf ^= 1;
