@@ -7,11 +7,19 @@ N(0, 0.02) weights packed by the repository's own Hadamard-4bit packer.  A
 seeded 32-token prompt is prefilled, then greedy decode runs; one "step" is
 one decoded token (forward_token over the resident weights + greedy argmax).
 `value` is the decode throughput in tokens/s over the timed steps (tg32 with
-the default --steps 32).  The same line also reports pp512 prefill
-throughput (M = 512, 224 of 256 down-projection tiles kept), the roofline of
-the dominant kernel (the fused gate+up decode GEMV, HBM-bound) timed with HIP
-events on the engine stream, and a CPU baseline: the oracle (a C restatement
-of the reference AVX2/OpenMP path) on the host cores, on a bounded sample.
+the default --steps 32).  The same line also reports:
+  - pp512 prefill throughput (M = 512, 224 of 256 down-projection tiles kept);
+  - long-context decode: 128 steps against a 4096-token fp32 KV cache filled
+    with seeded N(0, 1) K/V, with the attention time and KV-read bandwidth;
+  - the LM head in isolation (151936 x 4096, no layers, hidden states fed in):
+    1000 seeded steps, ~70 % with a planted zone-token bias, Zone-A early exit
+    (1424 zone tiles, margin 0.8) against the full vocabulary, three LM-head
+    copies rotated so the 256 MB cache cannot serve repeats;
+  - the roofline of the dominant kernel (the fused gate+up decode GEMV,
+    HBM-bound) timed with HIP events on the engine stream;
+  - a CPU baseline: the oracle (a C restatement of the reference AVX2/OpenMP
+    path) on the host cores, on a bounded sample, which also checks the LM-head
+    leg's argmax ids on a sample of its steps.
 
 Weights for the 8B shape are 4.26 GB per decoded token, far above the 256 MB
 Infinity Cache, so decode reads them from HBM every token.
@@ -68,6 +76,12 @@ def main():
     ap.add_argument("--long-ctx", type=int, default=4096,
                     help="KV-cache length of the long-context decode leg (0 = skip)")
     ap.add_argument("--long-steps", type=int, default=128, help="decode steps of the long-context leg")
+    ap.add_argument("--lm-steps", type=int, default=1000, help="steps of the isolated LM-head leg (0 = skip)")
+    ap.add_argument("--lm-zone", type=int, default=1424, help="Zone-A tiles of the LM-head leg")
+    ap.add_argument("--lm-margin", type=float, default=0.8, help="early-exit top-1 margin of the LM-head leg")
+    ap.add_argument("--lm-copies", type=int, default=3,
+                    help="distinct LM-head copies rotated per step (>= 1 GB, so the 256 MB cache cannot serve repeats)")
+    ap.add_argument("--lm-alpha", type=float, default=8.0, help="planted bias: h += alpha * row(t*)")
     ap.add_argument("--cpu-seconds", type=float, default=20.0, help="budget of the CPU baseline (0 = skip)")
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--graph", type=int, default=1, help="also time the device-argmax entry with HIP graph replay")
@@ -268,6 +282,87 @@ def main():
 
     eng.dpuf_engine_destroy(h)
 
+    # --- LM head in isolation: Zone-A early exit vs the full vocabulary -----
+    # An engine with no layers, fed hidden states through embeds_in (final
+    # RMSNorm with weight 1, LM head, device argmax).  In a seeded ~70 % of the
+    # steps h ~ N(0, 1) gets alpha * row(t*) of a zone token t* added, so its
+    # logit clears the margin and the early exit fires.
+    lmh, lm_inputs = None, None
+    if args.lm_steps > 0:
+        H = shape["hidden_size"]
+        lshape = dict(shape, num_layers=0, tie_word_embeddings=1)
+        t = time.time()
+        copies = []
+        for c in range(args.lm_copies):
+            lm_model = M.Model.build(lshape, max_seq_len=16, seed=args.seed + 100 + c)
+            he = eng.dpuf_engine_create(*lm_model.create_args())
+            if not he:
+                sys.exit("dpuf_engine_create (LM head) failed: " + eng.dpuf_amd_last_error().decode())
+            copies.append((lm_model, he))
+        log(f"LM head: {args.lm_copies} copies of {copies[0][0].weight_bytes()} bytes built in {time.time() - t:.1f}s")
+        n, K = args.lm_steps, args.lm_copies
+        srng = np.random.default_rng(args.seed + 5)
+        planted = srng.random(n) < 0.7
+        tstar = srng.integers(0, args.lm_zone * 16, n).astype(np.int32)
+        hs = srng.standard_normal((n, H), dtype=np.float32)
+        for c, (lm_model, _) in enumerate(copies):
+            idx = np.nonzero(planted & (np.arange(n) % K == c))[0]
+            if idx.size:
+                d = lm_model.tok.contents
+                rows = np.zeros((idx.size, H), np.float32)
+                ti = np.ascontiguousarray(tstar[idx])
+                eng.dpuf_embed_qr_hadamard4_packed_f32(idx.size, H, M.ptr(ti), d.tensor_base, d.tile_offsets,
+                                                      d.sign_bits, M.ptr(rows))
+                hs[idx] += np.float32(args.lm_alpha) * rows
+        out = C.c_int32(-1)
+
+        def lm_run(early):
+            if early:
+                os.environ["DPUF_EARLY_TILES"] = str(args.lm_zone)
+                os.environ["DPUF_EARLY_MARGIN"] = str(args.lm_margin)
+            exits0 = sum(eng.dpuf_amd_engine_early_exit_count(he) for _, he in copies)
+            ids_out = np.zeros(n, np.int32)
+            t0 = time.perf_counter()
+            for i in range(n):
+                rc = eng.dpuf_amd_engine_forward_argmax(copies[i % K][1], 1, None, 0, M.ptr(hs[i]), 0,
+                                                        C.byref(out), None)
+                assert rc == 0, rc
+                ids_out[i] = out.value
+            dt = time.perf_counter() - t0
+            exits = sum(eng.dpuf_amd_engine_early_exit_count(he) for _, he in copies) - exits0
+            # LM-head kernel time per step (HIP events), over the first 64 steps of copy 0..K-1
+            for _, he in copies:
+                eng.dpuf_amd_engine_set_timing(he, 1)
+            for i in range(64):
+                eng.dpuf_amd_engine_forward_argmax(copies[i % K][1], 1, None, 0, M.ptr(hs[i]), 0, C.byref(out), None)
+            kms = 0.0
+            for _, he in copies:
+                ms_, cnt_, by_ = C.c_double(), C.c_int64(), C.c_double()
+                eng.dpuf_amd_engine_get_timing(he, KINDS.index("lm_head"), C.byref(ms_), C.byref(cnt_),
+                                               C.byref(by_))
+                kms += ms_.value
+                eng.dpuf_amd_engine_set_timing(he, 0)
+            if early:
+                del os.environ["DPUF_EARLY_TILES"], os.environ["DPUF_EARLY_MARGIN"]
+            return ids_out, dt, exits, kms / 64
+
+        ids_full, dt_full, _, k_full = lm_run(False)
+        ids_early, dt_early, exits, k_early = lm_run(True)
+        zone_bytes = args.lm_zone * (copies[0][0].weight_bytes() // copies[0][0].tok.contents.n_tiles)
+        lmh = dict(steps=n, zone_tiles=args.lm_zone, margin=args.lm_margin, copies=K, planted=int(planted.sum()),
+                   early_exit_fraction=round(exits / n, 4),
+                   full_tok_s=round(n / dt_full, 1), early_tok_s=round(n / dt_early, 1),
+                   full_lm_head_us=round(k_full * 1e3, 2), early_lm_head_us=round(k_early * 1e3, 2),
+                   zone_bytes=int(zone_bytes),
+                   ids_equal_full_vs_early=round(float(np.mean(ids_full == ids_early)), 4),
+                   ids_head=ids_early[:8].tolist())
+        log(f"LM head {n} steps: full {lmh['full_tok_s']} tok/s ({lmh['full_lm_head_us']} us kernels), "
+            f"early exit {lmh['early_tok_s']} tok/s ({lmh['early_lm_head_us']} us kernels), "
+            f"exits {lmh['early_exit_fraction']:.2f}")
+        lm_inputs = (copies, hs, ids_early)
+        for _, he in copies:
+            eng.dpuf_engine_destroy(he)
+
     # --- CPU baseline: the oracle on the host cores, bounded sample ---------
     cpu = None
     if args.cpu_seconds > 0:
@@ -292,6 +387,27 @@ def main():
                    sample=f"{args.model} greedy decode of {n_dec} tokens after a {n_prompt}-token prompt "
                           f"(oracle C restatement, OpenMP)")
         log(f"cpu baseline: {cpu['value']} tok/s on {cpu['cores']} threads")
+        if lm_inputs is not None:
+            # the oracle's LM head (early exit on) on the first steps that used copy 0
+            copies, hs, ids_early = lm_inputs
+            os.environ["DPUF_EARLY_TILES"] = str(args.lm_zone)
+            os.environ["DPUF_EARLY_MARGIN"] = str(args.lm_margin)
+            lo_m = copies[0][0]
+            oh = o.orc_engine_create(*lo_m.create_args())
+            lo = np.zeros(V, np.float32)
+            steps0 = list(range(0, min(len(hs), 16 * args.lm_copies), args.lm_copies))
+            match = 0
+            t0 = time.perf_counter()
+            for i in steps0:
+                assert o.orc_engine_forward(oh, 1, None, 0, M.ptr(hs[i]), 1, M.ptr(lo)) == 0
+                match += int(o.orc_argmax(M.ptr(lo), V) == ids_early[i])
+            dt = time.perf_counter() - t0
+            o.orc_engine_destroy(oh)
+            del os.environ["DPUF_EARLY_TILES"], os.environ["DPUF_EARLY_MARGIN"]
+            lmh["oracle_ids_checked"] = len(steps0)
+            lmh["oracle_ids_match"] = match
+            lmh["oracle_tok_s"] = round(len(steps0) / dt, 2)
+            log(f"LM head oracle check: {match}/{len(steps0)} argmax ids equal, oracle {lmh['oracle_tok_s']} steps/s")
 
     line = {
         "metric": "tg32 & pp512 tok/s at Qwen3-8B shape; decode HBM GB/s vs peak",
@@ -318,6 +434,7 @@ def main():
                                             for k, v in kinds.items()}},
         "pp": pp,
         "long_context": long,
+        "lm_head_early_exit": lmh,
         "roofline": rl,
         "cpu_baseline": cpu,
         "resident_weight_bytes": wbytes,
