@@ -808,9 +808,10 @@ __global__ __launch_bounds__(1024) void k_mv(MvArgs A) {
 // operations, sp = ws * xs and the fma, with the chains in registers across
 // the block loop, so the block order is the reference's.
 //
-// A workgroup of 4 waves computes 128 rows (16 groups) x 64 tokens; wave w
-// owns rows 32w .. 32w + 31 as two 16-row fragments and all 64 tokens as four
-// 16-token tiles (8 MFMAs per block).  Activations are staged in LDS, GM_SB
+// A workgroup of 4 waves computes 128 rows (16 groups) x 16 TT tokens; wave
+// w owns rows 32w .. 32w + 31 as two 16-row fragments and all the tokens as
+// TT 16-token tiles (2 TT MFMAs per block); TT = 4, 2 or 1 per launch, the
+// widest that still fills the chip.  Activations are staged in LDS, GM_SB
 // blocks per stage, converted from int8 to f16 on the way in and double-
 // buffered, one barrier per stage; a token's 64 bytes per block are four
 // 16-byte chunks stored XOR-swizzled by token so a fragment read is free of
@@ -820,6 +821,9 @@ __global__ __launch_bounds__(1024) void k_mv(MvArgs A) {
 // l % 16, same k; D lane l = token l % 16, rows 4 (l / 16) + v.
 // ---------------------------------------------------------------------------
 #define GM_SB 4  // blocks per LDS stage
+#ifndef GM_RF
+#define GM_RF 1  // 16-row fragments per wave (workgroup = 64 GM_RF rows)
+#endif
 
 typedef _Float16 gm_h2 __attribute__((ext_vector_type(2)));
 typedef _Float16 gm_h8 __attribute__((ext_vector_type(8)));
@@ -869,108 +873,106 @@ DEV void gm_i8_to_h(uint32_t x, uint32_t& a, uint32_t& b) {
     b = gm_sub(gm_pair(u, 0x04030402u), (_Float16)1152.0f);
 }
 
+template <int TT, int RF>
 __global__ __launch_bounds__(256) void k_gemm_mfma(GmArgs A) {
-    __shared__ __align__(16) uint8_t bq[2][GM_SB][64][64];  // f16 activations [stage][block][token][k]
-    __shared__ __align__(16) float bs[2][GM_SB][16][4];     // block scales [stage][block][token % 16][token / 16]
+    constexpr int NT = 16 * TT;  // tokens per workgroup
+    __shared__ __align__(16) uint8_t bq[2][GM_SB][NT][64];  // f16 activations [stage][block][token][k]
+    __shared__ __align__(16) float bs[2][GM_SB][16][TT];    // block scales [stage][block][token % 16][token / 16]
     const int rt = blockIdx.x;
     if (rt >= A.tb[A.n_jobs]) return;  // padding of the grid (whole workgroup)
     int ji = 0;
     if (A.n_jobs > 1 && rt >= A.tb[1]) ji = 1;
     if (A.n_jobs > 2 && rt >= A.tb[2]) ji = 2;
     const GmJob& J = A.j[ji];
-    const int gb = J.g0 + (rt - A.tb[ji]) * 16;  // first group of the workgroup
-    const int m0 = blockIdx.y * 64;
+    const int gb = J.g0 + (rt - A.tb[ji]) * 8 * RF;  // first group of the workgroup
+    const int m0 = blockIdx.y * NT;
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, i16 = l & 15, kc = l >> 4;
     const int K = A.K, M = A.M, n_blk = K >> 5;
     const size_t gstride = (size_t)n_blk * 144;
 
-    // weight pointers of the wave's two fragments (groups clamped into the job)
-    const uint8_t* an[2];
-    const uint8_t* aw[2];
+    // weight pointers of the wave's RF fragments (groups clamped into the job)
+    const uint8_t* an[RF];
+    const uint8_t* aw[RF];
 #pragma unroll
-    for (int f = 0; f < 2; f++) {
-        int ga = gb + 4 * w + 2 * f + (i16 >> 3);
+    for (int f = 0; f < RF; f++) {
+        int ga = gb + 2 * RF * w + 2 * f + (i16 >> 3);
         ga = ga < J.g1 ? ga : J.g1 - 1;
         an[f] = J.g + (size_t)ga * gstride + (size_t)n_blk * 16 + (i16 & 7) * 16 + kc * 4;
-        int gw = gb + 4 * w + 2 * f + (kc >> 1);
+        int gw = gb + 2 * RF * w + 2 * f + (kc >> 1);
         gw = gw < J.g1 ? gw : J.g1 - 1;
         aw[f] = J.g + (size_t)gw * gstride + (kc & 1) * 8;
     }
-    // staging: thread (token tk, block sb of the stage)
-    const int tk = tid & 63, sbt = tid >> 6;
-    const bool tok_ok = m0 + tk < M;
-    const int8_t* qrow = J.q + (size_t)(tok_ok ? m0 + tk : 0) * K;
-    const float* srow = J.s + (size_t)(tok_ok ? m0 + tk : 0) * n_blk;
-    const int sw = (tk >> 1) & 3;  // chunk swizzle of this token
-
+    // staging: thread tid takes UPT consecutive 8-byte quarters of one
+    // (token tk, block sb of the stage) pair's 32 activation bytes
+    constexpr int UPT = NT * GM_SB * 4 / 256;  // 4, 2 or 1
     const int n_st = (n_blk + GM_SB - 1) / GM_SB;
-    uint4 sq0, sq1;
+    const int pr = tid * UPT / 4, q0 = tid * UPT % 4;  // pair and first quarter
+    const int tk = pr % NT, sbt = pr / NT;
+    uint2 sq[UPT];
     float ss;
     auto stage_load = [&](int st) {
-        const int b = st * GM_SB + sbt;
-        if (tok_ok && b < n_blk) {
-            sq0 = *(const uint4*)(qrow + b * 32);
-            sq1 = *(const uint4*)(qrow + b * 32 + 16);
-            ss = srow[b];
-        } else {
-            sq0 = sq1 = make_uint4(0u, 0u, 0u, 0u);
-            ss = 0.0f;
-        }
+        const int b = st * GM_SB + sbt, m = m0 + tk;
+        const bool ok = m < M && b < n_blk;
+#pragma unroll
+        for (int k = 0; k < UPT; k++)
+            sq[k] = ok ? *(const uint2*)(J.q + (size_t)m * K + b * 32 + 8 * (q0 + k)) : make_uint2(0u, 0u);
+        ss = ok && q0 == 0 ? J.s[(size_t)m * n_blk + b] : 0.0f;
     };
     auto stage_store = [&](int buf) {
-        const uint32_t d[8] = {sq0.x, sq0.y, sq0.z, sq0.w, sq1.x, sq1.y, sq1.z, sq1.w};
 #pragma unroll
-        for (int c = 0; c < 4; c++) {
+        for (int k = 0; k < UPT; k++) {
+            const int qu = q0 + k;
             uint32_t h0, h1, h2, h3;
-            gm_i8_to_h(d[2 * c], h0, h1);
-            gm_i8_to_h(d[2 * c + 1], h2, h3);
-            *(uint4*)&bq[buf][sbt][tk][16 * (c ^ sw)] = make_uint4(h0, h1, h2, h3);
+            gm_i8_to_h(sq[k].x, h0, h1);
+            gm_i8_to_h(sq[k].y, h2, h3);
+            *(uint4*)&bq[buf][sbt][tk][16 * (qu ^ ((tk >> 1) & 3))] = make_uint4(h0, h1, h2, h3);
         }
-        bs[buf][sbt][tk & 15][tk >> 4] = ss;
+        if (q0 == 0) bs[buf][sbt][tk & 15][tk >> 4] = ss;
     };
     // weights of one stage: nibble word and 4 scales per fragment and block
-    uint32_t wn[2][GM_SB][2];
-    uint2 ws[2][GM_SB][2];
-    auto weights_load = [&](int st, uint32_t (&n)[GM_SB][2], uint2 (&sc)[GM_SB][2]) {
+    uint32_t wn[2][GM_SB][RF];
+    uint2 ws[2][GM_SB][RF];
+    auto weights_load = [&](int st, uint32_t (&n)[GM_SB][RF], uint2 (&sc)[GM_SB][RF]) {
 #pragma unroll
         for (int sb = 0; sb < GM_SB; sb++) {
             const int b = min(st * GM_SB + sb, n_blk - 1);
 #pragma unroll
-            for (int f = 0; f < 2; f++) {
+            for (int f = 0; f < RF; f++) {
                 n[sb][f] = *(const uint32_t*)(an[f] + (size_t)b * 128);
                 sc[sb][f] = *(const uint2*)(aw[f] + (size_t)b * 16);
             }
         }
     };
 
-    gm_f4 acc[2][4];
+    gm_f4 acc[RF][TT];
 #pragma unroll
-    for (int f = 0; f < 2; f++)
+    for (int f = 0; f < RF; f++)
 #pragma unroll
-        for (int t = 0; t < 4; t++) acc[f][t] = (gm_f4){0.0f, 0.0f, 0.0f, 0.0f};
+        for (int t = 0; t < TT; t++) acc[f][t] = (gm_f4){0.0f, 0.0f, 0.0f, 0.0f};
 
-    auto compute = [&](int st, int buf, const uint32_t (&n)[GM_SB][2], const uint2 (&sc)[GM_SB][2]) {
+    auto compute = [&](int st, int buf, const uint32_t (&n)[GM_SB][RF], const uint2 (&sc)[GM_SB][RF]) {
 #pragma unroll
         for (int sb = 0; sb < GM_SB; sb++) {
             if (st * GM_SB + sb >= n_blk) break;  // uniform
-            gm_h8 a[2];
-            float wsf[2][4];
+            gm_h8 a[RF];
+            float wsf[RF][4];
 #pragma unroll
-            for (int f = 0; f < 2; f++) {
+            for (int f = 0; f < RF; f++) {
                 a[f] = gm_unpack_a(n[sb][f]);
                 wsf[f][0] = h2f((uint16_t)(sc[sb][f].x & 0xFFFFu));
                 wsf[f][1] = h2f((uint16_t)(sc[sb][f].x >> 16));
                 wsf[f][2] = h2f((uint16_t)(sc[sb][f].y & 0xFFFFu));
                 wsf[f][3] = h2f((uint16_t)(sc[sb][f].y >> 16));
             }
-            const float4 xs4 = *(const float4*)&bs[buf][sb][i16][0];
-            const float xs[4] = {xs4.x, xs4.y, xs4.z, xs4.w};
+            float xs[TT];
 #pragma unroll
-            for (int t = 0; t < 4; t++) {
+            for (int t = 0; t < TT; t++) xs[t] = bs[buf][sb][i16][t];
+#pragma unroll
+            for (int t = 0; t < TT; t++) {
                 const int tok = 16 * t + i16;
                 const gm_h8 bf = *(const gm_h8*)&bq[buf][sb][tok][16 * (kc ^ ((tok >> 1) & 3))];
 #pragma unroll
-                for (int f = 0; f < 2; f++) {
+                for (int f = 0; f < RF; f++) {
                     const gm_f4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[f], bf, (gm_f4){0.0f, 0.0f, 0.0f, 0.0f},
                                                                          0, 0, 0);
 #pragma unroll
@@ -1002,13 +1004,13 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(GmArgs A) {
     }
     if (st < n_st) compute(st, 0, wn[0], ws[0]);
 
-    // rows 32w + 16f + 4kc + v of the workgroup, token m0 + 16t + i16
+    // rows 16 RF w + 16f + 4kc + v of the workgroup, token m0 + 16t + i16
 #pragma unroll
-    for (int f = 0; f < 2; f++) {
-        const int grp = gb + 4 * w + 2 * f + (kc >> 1);
+    for (int f = 0; f < RF; f++) {
+        const int grp = gb + 2 * RF * w + 2 * f + (kc >> 1);
         if (grp >= J.g1) continue;
 #pragma unroll
-        for (int t = 0; t < 4; t++) {
+        for (int t = 0; t < TT; t++) {
             const int m = m0 + 16 * t + i16;
             if (m >= M) continue;
 #pragma unroll
@@ -2350,13 +2352,16 @@ void dpuf_hip_gemv(void* s, int32_t M, int32_t n_jobs, const DpufGemvJob* jobs, 
             G.j[i].ldo = jobs[i].ldo;
             G.tb[i] = t;
             const int ng = jobs[i].g1 - jobs[i].g0;
-            t += ng > 0 ? (ng + 15) / 16 : 0;
+            t += ng > 0 ? (ng + 8 * GM_RF - 1) / (8 * GM_RF) : 0;
         }
         G.tb[n_jobs] = t;
         if (t <= 0) return;
         // a multiple of 8 row tiles keeps a row tile's token tiles on one XCD
         const int gx = (t + 7) & ~7;
-        hipLaunchKernelGGL(k_gemm_mfma, dim3(gx, (M + 63) / 64), dim3(256), 0, ST(s), G);
+        if (GM_RF == 2)
+            hipLaunchKernelGGL((k_gemm_mfma<4, 2>), dim3(gx, (M + 63) / 64), dim3(256), 0, ST(s), G);
+        else
+            hipLaunchKernelGGL((k_gemm_mfma<4, 1>), dim3(gx, (M + 63) / 64), dim3(256), 0, ST(s), G);
         LAUNCHED("k_gemm_mfma");
     }
 }
