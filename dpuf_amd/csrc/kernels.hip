@@ -2198,14 +2198,15 @@ void dpuf_hip_resnorm_prep(void* s, int32_t M, int32_t H, float* h, const float*
 
 void dpuf_hip_prep(void* s, int32_t M, int32_t K, const float* x, const uint8_t* sign, DpufPrep p) {
     const int quads = K / 16;
-    hipLaunchKernelGGL(k_prep, dim3((quads + 255) / 256, M), dim3(256), 0, ST(s), K, x, sign, p);
+    // one wave per workgroup: the rows' loads spread over many CUs
+    hipLaunchKernelGGL(k_prep, dim3((quads + 63) / 64, M), dim3(64), 0, ST(s), K, x, sign, p);
     LAUNCHED("k_prep");
 }
 
 void dpuf_hip_swiglu_prep(void* s, int32_t M, int32_t I, const float* gate, const float* up, float dz,
                           const uint8_t* sign, DpufPrep p) {
     const int quads = I / 16;
-    hipLaunchKernelGGL(k_swiglu_prep, dim3((quads + 255) / 256, M), dim3(256), 0, ST(s), I, gate, up, dz, sign, p);
+    hipLaunchKernelGGL(k_swiglu_prep, dim3((quads + 63) / 64, M), dim3(64), 0, ST(s), I, gate, up, dz, sign, p);
     LAUNCHED("k_swiglu_prep");
 }
 
