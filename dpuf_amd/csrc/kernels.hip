@@ -1324,17 +1324,17 @@ DEV float pv_chain(const float* p, const float* v, int n, float inv, float a) {
     return a;
 }
 
-template <int HD>
-__global__ __launch_bounds__(256) void k_attn_pv(const float* __restrict__ S, const float* __restrict__ vc,
+template <int HD, int AP_NT>
+__global__ __launch_bounds__(AP_NT) void k_attn_pv(const float* __restrict__ S, const float* __restrict__ vc,
                                                  const int32_t* __restrict__ pos0p, int M, int n_q, int n_kv,
                                                  int max_seq, int qt, int dw, int lcap, int vk,
                                                  float* __restrict__ out) {
     extern __shared__ __align__(16) float sm[];
-    __shared__ float part[256];
+    __shared__ float part[AP_NT];
     __shared__ float rowv[32][2];  // max, 1 / sum
     const int kvh = blockIdx.x, m0 = blockIdx.y * qt, d0 = blockIdx.z * dw, tid = threadIdx.x;
     const int lane = tid & 63, wv = tid >> 6;
-    const int G = n_q / n_kv, R = qt * G, tpr = 256 / R;
+    const int G = n_q / n_kv, R = qt * G, tpr = AP_NT / R;
     const int pos0 = *pos0p;
     float* P = sm;  // [R][lcap], padded to a multiple of 1024 floats
     float* Vs = sm + ((R * lcap + 1023) & ~1023);  // [2][dw][vk + 4]: a dim's keys contiguous
@@ -1345,11 +1345,12 @@ __global__ __launch_bounds__(256) void k_attn_pv(const float* __restrict__ S, co
     // V chunk c -> registers (issued early); registers -> LDS, transposed
     const float* Vh = vc + (size_t)kvh * max_seq * HD + d0;
     const int nv4 = vk * (dw / 4);  // float4 per chunk (1024)
-    float4 vreg[4];
+    constexpr int NV = 1024 / AP_NT;
+    float4 vreg[NV];
     auto v_load = [&](int c0) {
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const int e = tid + 256 * k, kr = e / (dw / 4), c = e % (dw / 4);
+        for (int k = 0; k < NV; k++) {
+            const int e = tid + AP_NT * k, kr = e / (dw / 4), c = e % (dw / 4);
             vreg[k] = (e < nv4 && c0 + kr < Lmax) ? *(const float4*)(Vh + (size_t)(c0 + kr) * HD + 4 * c)
                                                   : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         }
@@ -1357,8 +1358,8 @@ __global__ __launch_bounds__(256) void k_attn_pv(const float* __restrict__ S, co
     auto v_store = [&](int buf) {
         float* vb = Vs + buf * dw * vld;
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const int e = tid + 256 * k, kr = e / (dw / 4), c = e % (dw / 4);
+        for (int k = 0; k < NV; k++) {
+            const int e = tid + AP_NT * k, kr = e / (dw / 4), c = e % (dw / 4);
             if (e < nv4) {
                 vb[(4 * c + 0) * vld + kr] = vreg[k].x;
                 vb[(4 * c + 1) * vld + kr] = vreg[k].y;
@@ -1373,7 +1374,7 @@ __global__ __launch_bounds__(256) void k_attn_pv(const float* __restrict__ S, co
     // elements past a row's length are don't-care
     {
         const int n4w = lcap >> 2, tot = R * n4w;
-        for (int base = wv * 64; base < tot; base += 256) {
+        for (int base = wv * 64; base < tot; base += AP_NT) {
             const int e = base + lane, r = e / n4w, c = e % n4w;
             const int rr = e < tot ? r : 0, mq = m0 + rr / G < M ? m0 + rr / G : M - 1;
             int t = 4 * c;
@@ -1411,7 +1412,7 @@ __global__ __launch_bounds__(256) void k_attn_pv(const float* __restrict__ S, co
     // exp: the polynomial on t < kv_len & ~7 (float4 at a time), expf on the tail
     {
         const int n4w = lcap >> 2;
-        for (int e = tid; e < R * n4w; e += 256) {
+        for (int e = tid; e < R * n4w; e += AP_NT) {
             const int r = e / n4w, c = e % n4w, n8 = row_len(r) & ~7;
             if (4 * c >= n8) continue;
             const float mx = rowv[r][0];
@@ -2407,21 +2408,37 @@ int32_t dpuf_hip_attn_split(void* s, int32_t M, int32_t lmax, const float* q, co
     const int vk = 4096 / dw;  // V chunk: 16 KB (+ padding), two buffers
     const size_t lds2 = ((((size_t)R * lcap + 1023) & ~(size_t)1023) + 2 * (size_t)(vk + 4) * dw) * 4;
     const dim3 g2(n_kv, (M + qt2 - 1) / qt2, dc);
+    // 1024 threads for launches of few workgroups (decode: the softmax phases
+    // go 4x wider), 256 when many workgroups already fill the chip (prefill)
+    const bool wide = (size_t)g2.x * g2.y * g2.z < 1024;
+    const dim3 b2(wide ? 1024 : 256);
     if (hd == 64) {
         hipLaunchKernelGGL(k_attn_sc<64>, g1, dim3(256), lds1, ST(s), q, kc, pos0p, M, n_q, n_kv, max_seq, scale,
                            qt1, scores);
-        hipLaunchKernelGGL(k_attn_pv<64>, g2, dim3(256), lds2, ST(s), scores, vc, pos0p, M, n_q, n_kv, max_seq,
-                           qt2, dw, lcap, vk, out);
+        if (wide)
+            hipLaunchKernelGGL((k_attn_pv<64, 1024>), g2, b2, lds2, ST(s), scores, vc, pos0p, M, n_q, n_kv, max_seq,
+                               qt2, dw, lcap, vk, out);
+        else
+            hipLaunchKernelGGL((k_attn_pv<64, 256>), g2, b2, lds2, ST(s), scores, vc, pos0p, M, n_q, n_kv, max_seq,
+                               qt2, dw, lcap, vk, out);
     } else if (hd == 128) {
         hipLaunchKernelGGL(k_attn_sc<128>, g1, dim3(256), lds1, ST(s), q, kc, pos0p, M, n_q, n_kv, max_seq, scale,
                            qt1, scores);
-        hipLaunchKernelGGL(k_attn_pv<128>, g2, dim3(256), lds2, ST(s), scores, vc, pos0p, M, n_q, n_kv, max_seq,
-                           qt2, dw, lcap, vk, out);
+        if (wide)
+            hipLaunchKernelGGL((k_attn_pv<128, 1024>), g2, b2, lds2, ST(s), scores, vc, pos0p, M, n_q, n_kv,
+                               max_seq, qt2, dw, lcap, vk, out);
+        else
+            hipLaunchKernelGGL((k_attn_pv<128, 256>), g2, b2, lds2, ST(s), scores, vc, pos0p, M, n_q, n_kv,
+                               max_seq, qt2, dw, lcap, vk, out);
     } else {
         hipLaunchKernelGGL(k_attn_sc<256>, g1, dim3(256), lds1, ST(s), q, kc, pos0p, M, n_q, n_kv, max_seq, scale,
                            qt1, scores);
-        hipLaunchKernelGGL(k_attn_pv<256>, g2, dim3(256), lds2, ST(s), scores, vc, pos0p, M, n_q, n_kv, max_seq,
-                           qt2, dw, lcap, vk, out);
+        if (wide)
+            hipLaunchKernelGGL((k_attn_pv<256, 1024>), g2, b2, lds2, ST(s), scores, vc, pos0p, M, n_q, n_kv,
+                               max_seq, qt2, dw, lcap, vk, out);
+        else
+            hipLaunchKernelGGL((k_attn_pv<256, 256>), g2, b2, lds2, ST(s), scores, vc, pos0p, M, n_q, n_kv,
+                               max_seq, qt2, dw, lcap, vk, out);
     }
     LAUNCHED("k_attn_split");
     return 0;
