@@ -1400,12 +1400,20 @@ __global__ __launch_bounds__(AP_NT) void k_attn_pv(const float* __restrict__ S, 
             }
             if (j < L - L4) m4[0] = fmaxf(m4[0], P[r * lcap + L4 + j]);
         }
-        part[tid] = fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3]));
+        // when a row's tpr threads are whole waves (tpr a multiple of 64),
+        // reduce within the wave first
+        float mx = fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3]));
+        if (tpr % 64 == 0) {
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+        }
+        part[tid] = mx;
     }
     __syncthreads();
     if (tid < R) {
+        const int step = tpr % 64 == 0 ? 64 : 1;
         float mx = part[tid * tpr];
-        for (int j = 1; j < tpr; j++) mx = fmaxf(mx, part[tid * tpr + j]);
+        for (int j = step; j < tpr; j += step) mx = fmaxf(mx, part[tid * tpr + j]);
         rowv[tid][0] = mx;
     }
     __syncthreads();
