@@ -149,7 +149,18 @@ __global__ void k_embed(DpufDevW w, const int32_t* __restrict__ ids, const float
     float* dst = out + (size_t)m * H;
     const int id = ids ? ids[m] : -1;
     if (embeds && id < 0) {
-        for (int i = threadIdx.x; i < H; i += blockDim.x) dst[i] = embeds[(size_t)m * H + i];
+        // H is a multiple of 64: float4 copies, eight loads in flight per thread
+        const float4* src4 = (const float4*)(embeds + (size_t)m * H);
+        float4* dst4 = (float4*)dst;
+        const int n4 = H >> 2, T = blockDim.x;
+        for (int i0 = threadIdx.x; i0 < n4; i0 += 8 * T) {
+            float4 v[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) v[k] = i0 + k * T < n4 ? src4[i0 + k * T] : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (int k = 0; k < 8; k++)
+                if (i0 + k * T < n4) dst4[i0 + k * T] = v[k];
+        }
         return;
     }
     const int g = id >> 3, ri = id & 7;
@@ -1964,11 +1975,27 @@ __global__ void k_capture(int H, const float* h, const float* hn, float* cap) {
 __global__ __launch_bounds__(1024) void k_topcheck(const float* __restrict__ x, int n, float thr, int32_t* flag) {
     __shared__ float s1[1024], s2[1024];
     float b1 = -1e30f, b2 = -1e30f;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
-        const float v = x[i];
+    auto take = [&](float v) {
         if (v > b1) { b2 = b1; b1 = v; }
         else if (v > b2) { b2 = v; }
+    };
+    // float4 loads, four in flight per thread (x is 16-byte aligned); the
+    // multiset top-2 does not depend on the order values are taken in
+    const int n4 = n >> 2, T = blockDim.x;
+    const float4* x4 = (const float4*)x;
+    int i = threadIdx.x;
+    for (; i + 3 * T < n4; i += 4 * T) {
+        const float4 a = x4[i], b = x4[i + T], c = x4[i + 2 * T], d = x4[i + 3 * T];
+        take(a.x); take(a.y); take(a.z); take(a.w);
+        take(b.x); take(b.y); take(b.z); take(b.w);
+        take(c.x); take(c.y); take(c.z); take(c.w);
+        take(d.x); take(d.y); take(d.z); take(d.w);
     }
+    for (; i < n4; i += T) {
+        const float4 a = x4[i];
+        take(a.x); take(a.y); take(a.z); take(a.w);
+    }
+    for (int j = 4 * n4 + threadIdx.x; j < n; j += T) take(x[j]);
     s1[threadIdx.x] = b1;
     s2[threadIdx.x] = b2;
     __syncthreads();
@@ -1993,10 +2020,27 @@ __global__ __launch_bounds__(1024) void k_argmax(const float* __restrict__ x, in
     __shared__ int si[1024];
     float bv = x[0];
     int bi = 0;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
-        const float v = x[i];
+    auto take = [&](float v, int i) {
         if (v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
+    };
+    // float4 loads, four in flight per thread (x is 16-byte aligned); ties go
+    // to the smaller index, so the result is the first maximum
+    const int n4 = n >> 2, T = blockDim.x;
+    const float4* x4 = (const float4*)x;
+    int i = threadIdx.x;
+    for (; i + 3 * T < n4; i += 4 * T) {
+        const float4 a = x4[i], b = x4[i + T], c = x4[i + 2 * T], d = x4[i + 3 * T];
+        take(a.x, 4 * i); take(a.y, 4 * i + 1); take(a.z, 4 * i + 2); take(a.w, 4 * i + 3);
+        const int ib = i + T, ic = i + 2 * T, id = i + 3 * T;
+        take(b.x, 4 * ib); take(b.y, 4 * ib + 1); take(b.z, 4 * ib + 2); take(b.w, 4 * ib + 3);
+        take(c.x, 4 * ic); take(c.y, 4 * ic + 1); take(c.z, 4 * ic + 2); take(c.w, 4 * ic + 3);
+        take(d.x, 4 * id); take(d.y, 4 * id + 1); take(d.z, 4 * id + 2); take(d.w, 4 * id + 3);
     }
+    for (; i < n4; i += T) {
+        const float4 a = x4[i];
+        take(a.x, 4 * i); take(a.y, 4 * i + 1); take(a.z, 4 * i + 2); take(a.w, 4 * i + 3);
+    }
+    for (int j = 4 * n4 + threadIdx.x; j < n; j += T) take(x[j], j);
     sv[threadIdx.x] = bv;
     si[threadIdx.x] = bi;
     __syncthreads();
