@@ -1488,6 +1488,217 @@ __global__ __launch_bounds__(AP_NT) void k_attn_pv(const float* __restrict__ S, 
     if (act) out[((size_t)(m0 + r / G) * n_q + kvh * G + r % G) * HD + d0 + d] = a;
 }
 
+// ---------------------------------------------------------------------------
+// k_attn_pvt: softmax and P.V for prefill, register-tiled.  Workgroup (kv
+// head, tile of qt = 32 / G queries): R = 32 score rows, all HD dims.  The
+// rows come into LDS by direct-to-LDS loads and go through the same softmax
+// as k_attn_pv (max; exp polynomial on the 8-aligned part, expf on the tail;
+// the reference's eight sum lanes, eng_hsum256 and the tail in order;
+// 1 / (sum + 1e-12)), and are normalised in place once (p = e * inv, the
+// reference's multiply).  Thread (ri, di) then keeps the 4 x 4 outputs of
+// rows 4ri .. 4ri + 3 and dims 4di .. 4di + 3 in registers and runs each
+// output's chain a = fma(p[t], v[t], a) over the keys in order: per 4 keys
+// one float4 of p per row from LDS and one float4 of V per key, 64 FMAs.  V
+// comes from L2 straight into registers, PVT_KV keys a batch with the next
+// batch in flight: the eight lanes of a wave that share a row group hold
+// eight consecutive float4 of the key's row, one 128-byte read per wave.
+// Keys at or past a row's kv_len (only the tile's last few keys: its rows end
+// at consecutive positions) leave that row's chains untouched.  G even (no
+// single trailing head), HD in {64, 128, 256}.
+// ---------------------------------------------------------------------------
+#define PVT_R 32  // score rows per workgroup
+#define PVT_KV 8  // keys per register batch of V
+
+// 4 keys t .. t + 3 of the tile: rows' p from LDS, V from registers
+DEV void pvt_keys4(float (&acc)[4][4], const float* pr, int ldp, int t, const float4* v) {
+    float4 p4[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) p4[k] = *(const float4*)(pr + (size_t)k * ldp + t);
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const float pk = j == 0 ? p4[k].x : j == 1 ? p4[k].y : j == 2 ? p4[k].z : p4[k].w;
+            acc[k][0] = fmaf(pk, v[j].x, acc[k][0]);
+            acc[k][1] = fmaf(pk, v[j].y, acc[k][1]);
+            acc[k][2] = fmaf(pk, v[j].z, acc[k][2]);
+            acc[k][3] = fmaf(pk, v[j].w, acc[k][3]);
+        }
+    }
+}
+
+template <int HD>
+__global__ __launch_bounds__(2 * HD) void k_attn_pvt(const float* __restrict__ S, const float* __restrict__ vc,
+                                                    const int32_t* __restrict__ pos0p, int M, int n_q, int n_kv,
+                                                    int max_seq, int qt, int ldp, float* __restrict__ out) {
+    constexpr int NT = 2 * HD, R = PVT_R, KV = PVT_KV;
+    constexpr int TPR = NT / R;  // threads per row in the softmax phases
+    extern __shared__ __align__(16) float P[];  // [R][ldp]
+    __shared__ float part[8 * R];
+    __shared__ float rowv[R][2];  // max, 1 / sum
+    // query tiles in dispatch order: the later (longer) half descending, then
+    // the earlier half ascending, so the two workgroups a CU takes together
+    // carry about the same number of keys
+    const int ny = gridDim.y, half = (ny + 1) / 2;
+    const int ty = (int)blockIdx.y < half ? ny - 1 - (int)blockIdx.y : (int)blockIdx.y - half;
+    const int kvh = blockIdx.x, m0 = ty * qt, tid = threadIdx.x;
+    const int lane = tid & 63, wv = tid >> 6;
+    const int G = n_q / n_kv;
+    const int pos0 = *pos0p;
+    const int mq = (m0 + qt < M ? m0 + qt : M) - m0;  // queries of this tile
+    auto row_len = [&](int r) { return r / G < mq ? pos0 + m0 + r / G + 1 : 0; };
+    const int Lmax = pos0 + m0 + mq, Lmin = pos0 + m0 + 1;
+    // score rows -> P (row r at r * ldp; 256 floats per wave instruction, ldp
+    // >= the rows' length rounded up to 256, so rows never overlap)
+    {
+        const int nch = (Lmax + 255) >> 8;
+        for (int u = wv; u < R * nch; u += NT / 64) {
+            const int r = u / nch, ch = u % nch;
+            const int rr = r / G < mq ? r : 0;
+            int t = 256 * ch + 4 * lane;
+            if (t + 3 >= max_seq) t = 0;
+            const float* src = S + ((size_t)(m0 + rr / G) * n_q + kvh * G + rr % G) * max_seq + t;
+            __builtin_amdgcn_global_load_lds((const void*)src, (lds_ptr_t)(P + (size_t)r * ldp + 256 * ch), 16, 0,
+                                             0);
+        }
+    }
+    __syncthreads();
+    // row max: TPR consecutive threads per row, four running maxima each
+    {
+        const int r = tid / TPR, j = tid % TPR;
+        float m4[4] = {-1e30f, -1e30f, -1e30f, -1e30f};
+        const int L = row_len(r), L4 = L & ~3;
+        for (int t = 4 * j; t < L4; t += 4 * TPR) {
+            const float4 x = *(const float4*)&P[r * ldp + t];
+            m4[0] = fmaxf(m4[0], x.x);
+            m4[1] = fmaxf(m4[1], x.y);
+            m4[2] = fmaxf(m4[2], x.z);
+            m4[3] = fmaxf(m4[3], x.w);
+        }
+        if (j < L - L4) m4[0] = fmaxf(m4[0], P[r * ldp + L4 + j]);
+        float mx = fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3]));
+#pragma unroll
+        for (int o = TPR / 2; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+        if (j == 0) rowv[r][0] = mx;
+    }
+    __syncthreads();
+    // exp: the polynomial on t < kv_len & ~7 (float4 at a time), expf on the tail
+    {
+        const int n4w = ldp >> 2;
+        for (int e = tid; e < R * n4w; e += NT) {
+            const int r = e / n4w, c = e % n4w, n8 = row_len(r) & ~7;
+            if (4 * c >= n8) continue;
+            const float mx = rowv[r][0];
+            float4 x = *(float4*)&P[r * ldp + 4 * c];
+            x.x = exp_poly(x.x - mx);
+            x.y = exp_poly(x.y - mx);
+            x.z = exp_poly(x.z - mx);
+            x.w = exp_poly(x.w - mx);
+            *(float4*)&P[r * ldp + 4 * c] = x;
+        }
+        for (int e = tid; e < 8 * R; e += NT) {
+            const int r = e >> 3, L = row_len(r), t = (L & ~7) + (e & 7);
+            if (t < L) P[r * ldp + t] = expf_libc(P[r * ldp + t] - rowv[r][0]);
+        }
+    }
+    __syncthreads();
+    // the reference's eight sum lanes, each a chain over t = j (mod 8)
+    for (int e = tid; e < 8 * R; e += NT) {
+        const int r = e >> 3, j = e & 7;
+        part[e] = lds_sum_chain(P + r * ldp + j, 8, (row_len(r) & ~7) >> 3);
+    }
+    __syncthreads();
+    if (tid < R) {
+        const int L = row_len(tid), n8 = L & ~7;
+        float sp = hsum8(part + 8 * tid);
+        for (int t = n8; t < L; t++) sp += P[tid * ldp + t];
+        rowv[tid][1] = 1.0f / (sp + 1e-12f);
+    }
+    __syncthreads();
+    // p = e * inv, in place
+    {
+        const int n4w = ldp >> 2;
+        for (int e = tid; e < R * n4w; e += NT) {
+            const int r = e / n4w, c = e % n4w;
+            if (4 * c >= row_len(r)) continue;
+            const float inv = rowv[r][1];
+            float4 x = *(float4*)&P[r * ldp + 4 * c];
+            x.x = x.x * inv;
+            x.y = x.y * inv;
+            x.z = x.z * inv;
+            x.w = x.w * inv;
+            *(float4*)&P[r * ldp + 4 * c] = x;
+        }
+    }
+    __syncthreads();
+    // P.V: lane = 8 * ri + (di & 7), wave w holds di = 8w .. 8w + 7
+    const int ri = lane >> 3, di = 8 * wv + (lane & 7);
+    float acc[4][4];
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[k][i] = 0.0f;
+    int Lr[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) Lr[k] = row_len(4 * ri + k);
+    const float* pr = P + (size_t)(4 * ri) * ldp;
+    const float* vg = vc + (size_t)kvh * max_seq * HD + 4 * di;
+    // keys below Lmin, in whole batches, go to every row unconditionally
+    const int nfull = Lmin / KV * KV;
+    float4 va[KV], vb[KV];
+#pragma unroll
+    for (int j = 0; j < KV; j++) va[j] = *(const float4*)(vg + (size_t)(j < max_seq ? j : max_seq - 1) * HD);
+    int t0 = 0;
+    // (the scheduling barriers keep each batch's loads ahead of the FMAs of
+    // the batch before it, so their latency is covered)
+    for (; t0 + 2 * KV <= nfull; t0 += 2 * KV) {
+#pragma unroll
+        for (int j = 0; j < KV; j++) {
+            const int t = t0 + KV + j;
+            vb[j] = *(const float4*)(vg + (size_t)(t < max_seq ? t : max_seq - 1) * HD);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < KV; j += 4) pvt_keys4(acc, pr, ldp, t0 + j, va + j);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < KV; j++) {
+            const int t = t0 + 2 * KV + j;
+            va[j] = *(const float4*)(vg + (size_t)(t < max_seq ? t : max_seq - 1) * HD);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < KV; j += 4) pvt_keys4(acc, pr, ldp, t0 + KV + j, vb + j);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    if (t0 + KV <= nfull) {
+#pragma unroll
+        for (int j = 0; j < KV; j += 4) pvt_keys4(acc, pr, ldp, t0 + j, va + j);
+        t0 += KV;
+    }
+    // the tile's last keys: row k takes key t only while t < its kv_len
+    for (int t = t0; t < Lmax; t++) {
+        const float4 v = *(const float4*)(vg + (size_t)t * HD);
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            if (t < Lr[k]) {
+                const float pk = pr[(size_t)k * ldp + t];
+                acc[k][0] = fmaf(pk, v.x, acc[k][0]);
+                acc[k][1] = fmaf(pk, v.y, acc[k][1]);
+                acc[k][2] = fmaf(pk, v.z, acc[k][2]);
+                acc[k][3] = fmaf(pk, v.w, acc[k][3]);
+            }
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int r = 4 * ri + k;
+        if (Lr[k] > 0)
+            *(float4*)(out + ((size_t)(m0 + r / G) * n_q + kvh * G + r % G) * HD + 4 * di) =
+                make_float4(acc[k][0], acc[k][1], acc[k][2], acc[k][3]);
+    }
+}
+
 __global__ __launch_bounds__(256) void k_attn(const float* __restrict__ q, const float* __restrict__ kc,
                                               const float* __restrict__ vc, float* __restrict__ out,
                                               float* __restrict__ scores, const int32_t* __restrict__ pos0p,
@@ -2452,6 +2663,33 @@ int32_t dpuf_hip_attn_split(void* s, int32_t M, int32_t lmax, const float* q, co
     while (qt2 > 1 && (size_t)qt2 * G * lcap * 4 > budget) qt2--;
     if ((size_t)qt2 * G * lcap * 4 > budget) return -1;
     const int R = qt2 * G;
+    // prefill with an even group: the register-tiled softmax + P.V kernel
+    if (M > 1 && (G & 1) == 0 && 32 % G == 0) {
+        const int ldp = 256 * ((lmax + 255) / 256) + 4;
+        const size_t ldst = (size_t)PVT_R * ldp * 4;
+        if (ldst <= 150 * 1024) {
+            const int qt = 32 / G;
+            const dim3 gt(n_kv, (M + qt - 1) / qt);
+            if (hd == 64) {
+                hipLaunchKernelGGL(k_attn_sc<64>, g1, dim3(256), lds1, ST(s), q, kc, pos0p, M, n_q, n_kv, max_seq,
+                                   scale, qt1, scores);
+                hipLaunchKernelGGL(k_attn_pvt<64>, gt, dim3(128), ldst, ST(s), scores, vc, pos0p, M, n_q, n_kv,
+                                   max_seq, qt, ldp, out);
+            } else if (hd == 128) {
+                hipLaunchKernelGGL(k_attn_sc<128>, g1, dim3(256), lds1, ST(s), q, kc, pos0p, M, n_q, n_kv, max_seq,
+                                   scale, qt1, scores);
+                hipLaunchKernelGGL(k_attn_pvt<128>, gt, dim3(256), ldst, ST(s), scores, vc, pos0p, M, n_q, n_kv,
+                                   max_seq, qt, ldp, out);
+            } else {
+                hipLaunchKernelGGL(k_attn_sc<256>, g1, dim3(256), lds1, ST(s), q, kc, pos0p, M, n_q, n_kv, max_seq,
+                                   scale, qt1, scores);
+                hipLaunchKernelGGL(k_attn_pvt<256>, gt, dim3(512), ldst, ST(s), scores, vc, pos0p, M, n_q, n_kv,
+                                   max_seq, qt, ldp, out);
+            }
+            LAUNCHED("k_attn_split_tiled");
+            return 0;
+        }
+    }
     int dc = 1;
     while (dc < hd / 4 && R * (hd / dc) > 256) dc *= 2;
     const int tiles = n_kv * ((M + qt2 - 1) / qt2);

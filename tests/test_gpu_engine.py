@@ -63,6 +63,43 @@ def test_tiny_prefill_decode_bit_exact(eng, orc, tiny, cap):
         eng.dpuf_amd_set_gemv_max_workgroups(0)
 
 
+def test_hidden_states_and_down_pruning(eng, orc, tiny, monkeypatch):
+    """Per-layer residual stream (h + hn after every layer) captured on both
+    engines, with the down projection pruned to 10 of 16 tiles in decode and
+    12 in prefill: bit-identical after the prefill and after every decode
+    step."""
+    import ctypes as C
+    monkeypatch.setenv("DPUF_GEN_KEEP_TILES", "10")
+    monkeypatch.setenv("DPUF_PREFILL_KEEP_TILES", "12")
+    p = Pair(eng, orc, tiny)
+    L, H, cap = TINY["num_layers"], TINY["hidden_size"], 8
+    assert eng.dpuf_amd_engine_set_capture(p.g, cap) == 0
+    orc.orc_engine_set_capture(p.o, cap)
+
+    def check(rows, what):
+        g = np.zeros(L * cap * H, np.float32)
+        assert eng.dpuf_amd_engine_get_capture(p.g, M.ptr(g), g.size) == 0
+        o = np.ctypeslib.as_array(C.cast(orc.orc_engine_get_capture(p.o), C.POINTER(C.c_float)), (L * cap * H,))
+        g = g.reshape(L, cap, H)[:, :rows]
+        o = o.reshape(L, cap, H)[:, :rows]
+        assert _bits_equal(g, o), (what, np.max(np.abs(g - o)))
+
+    try:
+        ids = np.random.default_rng(4).integers(0, 4096, 7).astype(np.int32)
+        lg, lo = p.forward(ids, 0, only_last=0)
+        assert _bits_equal(lg, lo)
+        check(7, "prefill")
+        tok = int(np.argmax(lo[-1]))
+        for step in range(6):
+            lg, lo = p.forward(np.array([tok], np.int32), 7 + step)
+            assert _bits_equal(lg, lo), step
+            check(1, f"decode step {step}")
+            tok = int(np.argmax(lo[0]))
+    finally:
+        eng.dpuf_amd_engine_set_capture(p.g, 0)
+        p.close()
+
+
 def _prefill_decode(eng, orc, tiny):
     p = Pair(eng, orc, tiny)
     ids = np.random.default_rng(1).integers(0, 4096, 13).astype(np.int32)
