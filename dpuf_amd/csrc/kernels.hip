@@ -1135,7 +1135,7 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 //
 // k_attn_sc: scores.  Workgroup (kv head, tile of qt queries, 64 keys): the
 // key chunk and the tile's q rows (qt x G heads, <= 32 rows) are staged in
-// LDS; thread (rp, kq) forms rows 2rp, 2rp + 1 against keys 4kq .. 4kq + 3 as
+// LDS; thread (rp, kq) forms rows 2rp, 2rp + 1 against keys kq + 16b, b < 4, as
 // the reference's 8-lane accumulators (a[j] = fma chain over i of
 // q[8i + j] * k[8i + j]), then applies the reference's horizontal sum for
 // that (query, key): the hadd tree for keys below kv_len & ~3, eng_hsum256
@@ -1197,7 +1197,9 @@ __global__ __launch_bounds__(256) void k_attn_sc(const float* __restrict__ q, co
             for (int j = 0; j < 8; j++) acc[a][b][j] = 0.0f;
     const float* q0 = qs + (2 * rp) * LD;
     const float* q1 = qs + (2 * rp + 1 < R ? 2 * rp + 1 : 2 * rp) * LD;
-    const float* k0 = ks + (4 * kq) * LD;
+    // keys kq, kq + 16, kq + 32, kq + 48: adjacent lanes read adjacent K rows
+    // (stride LD = 4 mod 32 words), which spreads them over the banks
+    const float* k0 = ks + kq * LD;
     for (int i = 0; i < HD; i += 8) {
         float qa[2][8], ka[4][8];
         *(float4*)&qa[0][0] = *(const float4*)(q0 + i);
@@ -1206,8 +1208,8 @@ __global__ __launch_bounds__(256) void k_attn_sc(const float* __restrict__ q, co
         *(float4*)&qa[1][4] = *(const float4*)(q1 + i + 4);
 #pragma unroll
         for (int b = 0; b < 4; b++) {
-            *(float4*)&ka[b][0] = *(const float4*)(k0 + b * LD + i);
-            *(float4*)&ka[b][4] = *(const float4*)(k0 + b * LD + i + 4);
+            *(float4*)&ka[b][0] = *(const float4*)(k0 + 16 * b * LD + i);
+            *(float4*)&ka[b][4] = *(const float4*)(k0 + 16 * b * LD + i + 4);
         }
 #pragma unroll
         for (int a = 0; a < 2; a++)
@@ -1227,12 +1229,12 @@ __global__ __launch_bounds__(256) void k_attn_sc(const float* __restrict__ q, co
         float* srow = S + ((size_t)m * n_q + kvh * G + hi) * max_seq;
 #pragma unroll
         for (int b = 0; b < 4; b++) {
-            const int t = t0 + 4 * kq + b;
+            const int t = t0 + kq + 16 * b;
             if (t >= L) continue;
             float sc;
             if (t < n4) sc = hsum8_hadd(acc[a][b]);
             else if (!single) sc = hsum8(acc[a][b]);
-            else sc = score_dot2(qs + r * LD, ks + (4 * kq + b) * LD, HD);
+            else sc = score_dot2(qs + r * LD, ks + (kq + 16 * b) * LD, HD);
             srow[t] = sc * scale;
         }
     }
