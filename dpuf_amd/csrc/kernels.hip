@@ -1246,7 +1246,7 @@ __global__ __launch_bounds__(256) void k_attn_sc(const float* __restrict__ q, co
 // are read into LDS and turned into probabilities as the reference does
 // (max; exp polynomial on the 8-aligned part, expf on the tail; the 8-lane
 // sum chains + eng_hsum256 + the tail added in order; 1 / (sum + 1e-12);
-// multiply), then thread (r, d) runs the row's P.V chain for dim d over the
+// multiply, in place), then thread (r, d) runs the row's P.V chain for dim d over the
 // keys in order (nested pairs for a single trailing head, as the reference's
 // single-head path), V staged in LDS in chunks of vk keys.  Every dim chunk
 // recomputes its rows' softmax (cheap next to P.V).
@@ -1275,8 +1275,8 @@ DEV float lds_sum_chain(const float* x, int step, int n) {
     return a;
 }
 
-// P.V chain of one (row, dim) over n keys of a chunk, in key order, with
-// p[t] = e[t] * inv: a = fma(p[t], v[t], a), or the nested pairs
+// P.V chain of one (row, dim) over n keys of a chunk, in key order, with the
+// normalised probabilities p[t]: a = fma(p[t], v[t], a), or the nested pairs
 // a = fma(p[t], v[t], fma(p[t+1], v[t+1], a)) of the reference's
 // single-head path.  p and v are
 // 16-byte aligned LDS rows (v: this dim's values for consecutive keys); keys
@@ -1291,10 +1291,10 @@ DEV void pv_load16(const float* p, const float* v, int t, float4 (&pb)[4], float
 }
 
 template <bool NESTED>
-DEV float pv_fma16(const float4 (&pb)[4], const float4 (&vb)[4], float inv, float a) {
+DEV float pv_fma16(const float4 (&pb)[4], const float4 (&vb)[4], float a) {
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        const float p0 = pb[i].x * inv, p1 = pb[i].y * inv, p2 = pb[i].z * inv, p3 = pb[i].w * inv;
+        const float p0 = pb[i].x, p1 = pb[i].y, p2 = pb[i].z, p3 = pb[i].w;
         if (NESTED) {
             a = fmaf(p0, vb[i].x, fmaf(p1, vb[i].y, a));
             a = fmaf(p2, vb[i].z, fmaf(p3, vb[i].w, a));
@@ -1309,7 +1309,7 @@ DEV float pv_fma16(const float4 (&pb)[4], const float4 (&vb)[4], float inv, floa
 }
 
 template <bool NESTED>
-DEV float pv_chain(const float* p, const float* v, int n, float inv, float a) {
+DEV float pv_chain(const float* p, const float* v, int n, float a) {
     const int n16 = n & ~15;
     int t = 0;
     if (n16 > 0) {
@@ -1318,21 +1318,21 @@ DEV float pv_chain(const float* p, const float* v, int n, float inv, float a) {
         for (t = 0; t + 32 <= n16; t += 32) {
             pv_load16(p, v, t + 16, pb, vb);
             __builtin_amdgcn_sched_barrier(0);  // keep the next batch's reads ahead of these FMAs
-            a = pv_fma16<NESTED>(pa, va, inv, a);
+            a = pv_fma16<NESTED>(pa, va, a);
             pv_load16(p, v, t + 32 < n16 ? t + 32 : t, pa, va);  // the last reload is unused
             __builtin_amdgcn_sched_barrier(0);
-            a = pv_fma16<NESTED>(pb, vb, inv, a);
+            a = pv_fma16<NESTED>(pb, vb, a);
         }
         if (t < n16) {
-            a = pv_fma16<NESTED>(pa, va, inv, a);
+            a = pv_fma16<NESTED>(pa, va, a);
             t += 16;
         }
     }
     if (NESTED) {
-        for (; t + 1 < n; t += 2) a = fmaf(p[t] * inv, v[t], fmaf(p[t + 1] * inv, v[t + 1], a));
-        if (t < n) a = fmaf(p[t] * inv, v[t], a);
+        for (; t + 1 < n; t += 2) a = fmaf(p[t], v[t], fmaf(p[t + 1], v[t + 1], a));
+        if (t < n) a = fmaf(p[t], v[t], a);
     } else {
-        for (; t < n; t++) a = fmaf(p[t] * inv, v[t], a);
+        for (; t < n; t++) a = fmaf(p[t], v[t], a);
     }
     return a;
 }
@@ -1463,10 +1463,25 @@ __global__ __launch_bounds__(AP_NT) void k_attn_pv(const float* __restrict__ S, 
         for (int t = n8; t < L; t++) sp += P[tid * lcap + t];
         rowv[tid][1] = 1.0f / (sp + 1e-12f);
     }
-    // P.V: thread (r, d); the probability p = e * inv is formed as each key
-    // is consumed (the reference's normalising multiply, off the FMA chain);
-    // V chunks double-buffered, the next one loading while the current one is
-    // consumed
+    __syncthreads();
+    // p = e * inv in place (the reference's normalising multiply), once for
+    // all the dims' chains
+    {
+        const int n4w = lcap >> 2;
+        for (int e = tid; e < R * n4w; e += AP_NT) {
+            const int r = e / n4w, c = e % n4w;
+            if (4 * c >= row_len(r)) continue;
+            const float inv = rowv[r][1];
+            float4 x = *(float4*)&P[r * lcap + 4 * c];
+            x.x = x.x * inv;
+            x.y = x.y * inv;
+            x.z = x.z * inv;
+            x.w = x.w * inv;
+            *(float4*)&P[r * lcap + 4 * c] = x;
+        }
+    }
+    // P.V: thread (r, d); V chunks double-buffered, the next one loading
+    // while the current one is consumed
     const int r = tid / dw, d = tid % dw;
     const bool act = r < R && row_len(r) > 0;
     const int L = act ? row_len(r) : 0;
@@ -1477,12 +1492,11 @@ __global__ __launch_bounds__(AP_NT) void k_attn_pv(const float* __restrict__ S, 
     for (int c0 = 0; c0 < Lmax; c0 += vk) {
         const bool more = c0 + vk < Lmax;
         if (more) v_load(c0 + vk);
-        __syncthreads();  // chunk c0 in Vs[buf] (and rowv final on the first pass)
+        __syncthreads();  // chunk c0 in Vs[buf] (and P normalised on the first pass)
         if (act && c0 < L) {
             const int n = L - c0 < vk ? L - c0 : vk;
             const float* vp = Vs + buf * dw * vld + d * vld;
-            const float inv = rowv[r][1];
-            a = nested ? pv_chain<true>(prow + c0, vp, n, inv, a) : pv_chain<false>(prow + c0, vp, n, inv, a);
+            a = nested ? pv_chain<true>(prow + c0, vp, n, a) : pv_chain<false>(prow + c0, vp, n, a);
         }
         if (more) v_store(buf ^ 1);
         buf ^= 1;
