@@ -207,5 +207,6 @@ def load_engine():
     _sig(lib, "dpuf_amd_gemv_bench", C.c_double, [P, I32, I32, I32, I32, C.POINTER(C.c_double)])
     _sig(lib, "dpuf_amd_copy_bench", C.c_double, [C.c_size_t, I32])
     _sig(lib, "dpuf_amd_set_gemv_max_workgroups", None, [I32])
+    _sig(lib, "dpuf_amd_reduce_check", I32, [P, I32, I32, I32, C.c_float])
     _engine = lib
     return lib

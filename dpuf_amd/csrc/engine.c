@@ -54,6 +54,7 @@ typedef struct {
     int32_t capture_cap;
     DpufPrep prep[3];
     int32_t *d_ids, *d_pos0, *d_flag, *d_tok;
+    void* d_red; /* partials of the device argmax / top-2 reductions */
     int32_t* h_pinned;   /* host staging: [0] pos0, [1] flag, [2] token, [8..] ids */
     uint8_t* q_idx;      /* per layer: prep index of q,k,v (3 bytes) and gate/up (2 bytes) */
     float deadzone;
@@ -289,6 +290,7 @@ static void engine_free(Engine* e) {
     for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++) dpuf_hip_free(bufs[i]);
     for (int i = 0; i < 3; i++) { dpuf_hip_free(e->prep[i].q); dpuf_hip_free(e->prep[i].s); dpuf_hip_free(e->prep[i].m); }
     dpuf_hip_free(e->d_ids);
+    dpuf_hip_free(e->d_red);
     dpuf_hip_host_free(e->h_pinned);
     for (int i = 0; i < MAX_EVENTS; i++) if (e->ev[i]) dpuf_hip_event_destroy(e->ev[i]);
     if (e->stream) dpuf_hip_stream_destroy(e->stream);
@@ -394,8 +396,9 @@ DPUF_EXPORT void* dpuf_engine_create(const DpufModelConfig* cfg, const DpufLayer
         }
         e->d_ids = (int32_t*)dpuf_hip_malloc((B + 64) * 4);
         e->h_pinned = (int32_t*)dpuf_hip_host_alloc((B + 64) * 4);
+        e->d_red = dpuf_hip_malloc(DPUF_HIP_RED_SCRATCH);
         if (!e->h || !e->hn || !e->q || !e->k || !e->v || !e->ao || !e->gate || !e->up || !e->logits ||
-            !e->scores || !e->embeds || !e->d_ids || !e->h_pinned)
+            !e->scores || !e->embeds || !e->d_ids || !e->h_pinned || !e->d_red)
             goto fail;
         e->d_pos0 = e->d_ids + B;
         e->d_flag = e->d_ids + B + 1;
@@ -676,7 +679,7 @@ static void enqueue_head(Engine* e, int32_t M, int32_t only_last, int32_t early_
         DpufGemvJob j0 = job(&e->lm, 0, za, e->prep[0], e->logits, e->V);
         const int tm11 = tm_begin(e, K_LM, gemv_bytes(&e->lm, 0, za, 1));
         dpuf_hip_gemv(s, 1, 1, &j0, NULL, 0.0f);
-        dpuf_hip_topcheck(s, e->logits, nz, early_margin, e->d_flag);
+        dpuf_hip_topcheck(s, e->logits, nz, early_margin, e->d_flag, e->d_red);
         if (za < nt) {
             DpufGemvJob j1 = job(&e->lm, za, nt, e->prep[0], e->logits, e->V);
             dpuf_hip_gemv(s, 1, 1, &j1, e->d_flag, -1e9f);
@@ -689,7 +692,7 @@ static void enqueue_head(Engine* e, int32_t M, int32_t only_last, int32_t early_
         tm_end(e, tm12);
         dpuf_hip_fill_zero(e->d_flag, 4, s);
     }
-    if (want_argmax) dpuf_hip_argmax(s, e->logits + (size_t)(lmM - 1) * e->V, e->V, e->d_tok);
+    if (want_argmax) dpuf_hip_argmax(s, e->logits + (size_t)(lmM - 1) * e->V, e->V, e->d_tok, e->d_red);
 }
 
 static int32_t forward_common(Engine* e, int32_t n_tokens, const int32_t* token_ids, int32_t pos0,
@@ -957,6 +960,28 @@ DPUF_EXPORT double dpuf_amd_gemv_bench(void* handle, int32_t which, int32_t M, i
 }
 
 DPUF_EXPORT void dpuf_amd_set_gemv_max_workgroups(int32_t n) { dpuf_hip_set_gemv_max_wg(n); }
+
+DPUF_EXPORT int32_t dpuf_amd_reduce_check(const float* x, int32_t n, int32_t offset, int32_t mode, float thr) {
+    if (!x || n < 1 || offset < 0 || offset > 3 || (mode != 0 && mode != 1) || dpuf_hip_device_count() <= 0)
+        return -1;
+    void* s = dpuf_hip_stream_create();
+    float* d = (float*)dpuf_hip_malloc(((size_t)n + 4) * 4);
+    void* red = dpuf_hip_malloc(DPUF_HIP_RED_SCRATCH);
+    int32_t* o = (int32_t*)dpuf_hip_malloc(4);
+    int32_t r = -1;
+    if (s && d && red && o) {
+        dpuf_hip_h2d(d + offset, x, (size_t)n * 4, s);
+        if (mode == 1) dpuf_hip_argmax(s, d + offset, n, o, red);
+        else dpuf_hip_topcheck(s, d + offset, n, thr, o, red);
+        dpuf_hip_d2h(&r, o, 4, s);
+        if (dpuf_hip_sync(s) != 0 || !dpuf_hip_ok()) r = -1;
+    }
+    dpuf_hip_free(o);
+    dpuf_hip_free(red);
+    dpuf_hip_free(d);
+    if (s) dpuf_hip_stream_destroy(s);
+    return r;
+}
 
 DPUF_EXPORT double dpuf_amd_copy_bench(size_t bytes, int32_t iters) {
     if (bytes == 0 || iters < 1 || dpuf_hip_device_count() <= 0) return -1.0;

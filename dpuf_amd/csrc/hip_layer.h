@@ -110,8 +110,11 @@ int32_t dpuf_hip_attn_dec(void* s, const float* q, const float* k, const float* 
                           float scale, float* scores, float* ao, const uint8_t* o_sign, DpufPrep op);
 void dpuf_hip_zero_rows(void* s, int32_t M, float* out, int32_t ld, int32_t r0, int32_t r1);
 void dpuf_hip_capture(void* s, int32_t M, int32_t H, const float* h, const float* hn, float* cap);
-void dpuf_hip_topcheck(void* s, const float* logits, int32_t n, float thr, int32_t* flag);
-void dpuf_hip_argmax(void* s, const float* logits, int32_t V, int32_t* out);
+/* Device reductions of a logit row (two launches each); scratch holds
+ * DPUF_HIP_RED_SCRATCH bytes of partials. */
+#define DPUF_HIP_RED_SCRATCH 512
+void dpuf_hip_topcheck(void* s, const float* logits, int32_t n, float thr, int32_t* flag, void* scratch);
+void dpuf_hip_argmax(void* s, const float* logits, int32_t V, int32_t* out, void* scratch);
 void dpuf_hip_fwht_sign(void* s, int32_t M, int32_t K, const float* x, const uint8_t* sign, float* out);
 void dpuf_hip_slab_pack(void* s, int32_t mc, int32_t K, DpufPrep rows, int32_t* sq, float* ss, int32_t* sm);
 void dpuf_hip_slab_unpack(void* s, int32_t M, int32_t K, const int32_t* sq, const float* ss, const int32_t* sm,

@@ -2196,93 +2196,134 @@ __global__ void k_capture(int H, const float* h, const float* hn, float* cap) {
     for (int i = threadIdx.x; i < H; i += blockDim.x) cap[(size_t)m * H + i] = h[(size_t)m * H + i] + hn[(size_t)m * H + i];
 }
 
-// Top-2 over logits [0, n) with multiplicity (the reference's sequential
-// b1/b2 scan, dpuf_engine.c:2101-2110, is order independent), then the
-// early-exit decision b1 - b2 >= thr (thr > 0).  One block of 1024.
-__global__ __launch_bounds__(1024) void k_topcheck(const float* __restrict__ x, int n, float thr, int32_t* flag) {
-    __shared__ float s1[1024], s2[1024];
-    float b1 = -1e30f, b2 = -1e30f;
-    auto take = [&](float v) {
-        if (v > b1) { b2 = b1; b1 = v; }
-        else if (v > b2) { b2 = v; }
-    };
-    // float4 loads, four in flight per thread (x is 16-byte aligned); the
-    // multiset top-2 does not depend on the order values are taken in
-    const int n4 = n >> 2, T = blockDim.x;
-    const float4* x4 = (const float4*)x;
-    int i = threadIdx.x;
-    for (; i + 3 * T < n4; i += 4 * T) {
-        const float4 a = x4[i], b = x4[i + T], c = x4[i + 2 * T], d = x4[i + 3 * T];
-        take(a.x); take(a.y); take(a.z); take(a.w);
-        take(b.x); take(b.y); take(b.z); take(b.w);
-        take(c.x); take(c.y); take(c.z); take(c.w);
-        take(d.x); take(d.y); take(d.z); take(d.w);
+// Device reductions over a logit row, in two launches: RED_NB workgroups each
+// reduce a contiguous slice (float4 loads, all of a thread's loads in flight,
+// wave shuffles, one LDS step) into a partial, then one wave merges the
+// partials.  Scratch: RED_NB partials of 8 bytes.
+#define RED_NB 64
+
+// Top-2 with multiplicity (the reference's sequential b1/b2 scan,
+// dpuf_engine.c:2101-2110, is order independent), then the early-exit
+// decision b1 - b2 >= thr (thr > 0).
+DEV void top2_take(float v, float& b1, float& b2) {
+    if (v > b1) {
+        b2 = b1;
+        b1 = v;
+    } else if (v > b2) {
+        b2 = v;
     }
-    for (; i < n4; i += T) {
-        const float4 a = x4[i];
-        take(a.x); take(a.y); take(a.z); take(a.w);
-    }
-    for (int j = 4 * n4 + threadIdx.x; j < n; j += T) take(x[j]);
-    s1[threadIdx.x] = b1;
-    s2[threadIdx.x] = b2;
-    __syncthreads();
-    for (int w = blockDim.x / 2; w > 0; w >>= 1) {
-        if (threadIdx.x < w) {
-            const float a1 = s1[threadIdx.x], a2 = s2[threadIdx.x];
-            const float c1 = s1[threadIdx.x + w], c2 = s2[threadIdx.x + w];
-            float n1, n2;
-            if (a1 >= c1) { n1 = a1; n2 = fmaxf(a2, c1); }
-            else { n1 = c1; n2 = fmaxf(c2, a1); }
-            s1[threadIdx.x] = n1;
-            s2[threadIdx.x] = n2;
-        }
-        __syncthreads();
-    }
-    if (threadIdx.x == 0) *flag = (thr > 0.0f && (s1[0] - s2[0]) >= thr) ? 1 : 0;
 }
 
-// First index of the maximum under strict '>' (dpuf-cli.c:1997-2004).
-__global__ __launch_bounds__(1024) void k_argmax(const float* __restrict__ x, int n, int32_t* out) {
-    __shared__ float sv[1024];
-    __shared__ int si[1024];
-    float bv = x[0];
-    int bi = 0;
-    auto take = [&](float v, int i) {
-        if (v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
-    };
-    // float4 loads, four in flight per thread (x is 16-byte aligned); ties go
-    // to the smaller index, so the result is the first maximum
-    const int n4 = n >> 2, T = blockDim.x;
-    const float4* x4 = (const float4*)x;
-    int i = threadIdx.x;
-    for (; i + 3 * T < n4; i += 4 * T) {
-        const float4 a = x4[i], b = x4[i + T], c = x4[i + 2 * T], d = x4[i + 3 * T];
-        take(a.x, 4 * i); take(a.y, 4 * i + 1); take(a.z, 4 * i + 2); take(a.w, 4 * i + 3);
-        const int ib = i + T, ic = i + 2 * T, id = i + 3 * T;
-        take(b.x, 4 * ib); take(b.y, 4 * ib + 1); take(b.z, 4 * ib + 2); take(b.w, 4 * ib + 3);
-        take(c.x, 4 * ic); take(c.y, 4 * ic + 1); take(c.z, 4 * ic + 2); take(c.w, 4 * ic + 3);
-        take(d.x, 4 * id); take(d.y, 4 * id + 1); take(d.z, 4 * id + 2); take(d.w, 4 * id + 3);
+DEV void top2_merge(float& b1, float& b2, float c1, float c2) {
+    if (b1 >= c1) {
+        b2 = fmaxf(b2, c1);
+    } else {
+        b2 = fmaxf(c2, b1);
+        b1 = c1;
     }
-    for (; i < n4; i += T) {
-        const float4 a = x4[i];
-        take(a.x, 4 * i); take(a.y, 4 * i + 1); take(a.z, 4 * i + 2); take(a.w, 4 * i + 3);
+}
+
+// First maximum (dpuf-cli.c:1997-2004: `if (x[i] > best)` from best = x[0]):
+// the larger value, the smaller index on ties; every partial starts from
+// (x[0], 0), so a NaN x[0] gives 0 as the reference does and other NaNs are
+// never taken.
+DEV void amax_merge(float& bv, int& bi, float v, int i) {
+    if (v > bv || (v == bv && i < bi)) {
+        bv = v;
+        bi = i;
     }
-    for (int j = 4 * n4 + threadIdx.x; j < n; j += T) take(x[j], j);
-    sv[threadIdx.x] = bv;
-    si[threadIdx.x] = bi;
-    __syncthreads();
-    for (int w = blockDim.x / 2; w > 0; w >>= 1) {
-        if (threadIdx.x < w) {
-            const float v = sv[threadIdx.x + w];
-            const int i = si[threadIdx.x + w];
-            if (v > sv[threadIdx.x] || (v == sv[threadIdx.x] && i < si[threadIdx.x])) {
-                sv[threadIdx.x] = v;
-                si[threadIdx.x] = i;
+}
+
+__global__ __launch_bounds__(256) void k_red_part(const float* __restrict__ x, int n, int argmax, float2* part) {
+    __shared__ float2 wp[4];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    // h leading elements up to 16-byte alignment (workgroup 0), then float4
+    // slices, then the tail (the last workgroup)
+    const int h = min((int)((16u - ((uint32_t)(uintptr_t)x & 15u)) & 15u) >> 2, n);
+    const int n4 = (n - h) >> 2, per = (n4 + RED_NB - 1) / RED_NB;
+    const int c0 = blockIdx.x * per, c1 = min(c0 + per, n4);
+    const float4* x4 = (const float4*)(x + h);
+    float a = argmax ? x[0] : -1e30f, b = -1e30f;  // argmax: (value, index bits); top-2: (b1, b2)
+    int ai = 0;
+    if (blockIdx.x == 0 && tid < h) {
+        if (argmax) amax_merge(a, ai, x[tid], tid);
+        else top2_take(x[tid], a, b);
+    }
+    constexpr int U = 4;
+    for (int c = c0 + tid; c < c1; c += 256 * U) {
+        float4 v[U];
+#pragma unroll
+        for (int k = 0; k < U; k++) v[k] = c + 256 * k < c1 ? x4[c + 256 * k] : make_float4(-1e30f, -1e30f, -1e30f, -1e30f);
+#pragma unroll
+        for (int k = 0; k < U; k++) {
+            if (c + 256 * k >= c1) continue;
+            const int e = h + 4 * (c + 256 * k);
+            if (argmax) {
+                amax_merge(a, ai, v[k].x, e);
+                amax_merge(a, ai, v[k].y, e + 1);
+                amax_merge(a, ai, v[k].z, e + 2);
+                amax_merge(a, ai, v[k].w, e + 3);
+            } else {
+                top2_take(v[k].x, a, b);
+                top2_take(v[k].y, a, b);
+                top2_take(v[k].z, a, b);
+                top2_take(v[k].w, a, b);
             }
         }
-        __syncthreads();
     }
-    if (threadIdx.x == 0) *out = si[0];
+    if (blockIdx.x == RED_NB - 1)  // the n % 4 tail
+        for (int e = h + 4 * n4 + tid; e < n; e += 256) {
+            if (argmax) amax_merge(a, ai, x[e], e);
+            else top2_take(x[e], a, b);
+        }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float oa = __shfl_xor(a, o, 64);
+        if (argmax) {
+            const int oi = __shfl_xor(ai, o, 64);
+            amax_merge(a, ai, oa, oi);
+        } else {
+            const float ob = __shfl_xor(b, o, 64);
+            top2_merge(a, b, oa, ob);
+        }
+    }
+    if (lane == 0) wp[w] = argmax ? make_float2(a, __int_as_float(ai)) : make_float2(a, b);
+    __syncthreads();
+    if (tid == 0) {
+        float2 r = wp[0];
+        for (int k = 1; k < 4; k++) {
+            if (argmax) {
+                int ri = __float_as_int(r.y);
+                amax_merge(r.x, ri, wp[k].x, __float_as_int(wp[k].y));
+                r.y = __int_as_float(ri);
+            } else {
+                top2_merge(r.x, r.y, wp[k].x, wp[k].y);
+            }
+        }
+        part[blockIdx.x] = r;
+    }
+}
+
+// One wave: merge the RED_NB partials; argmax writes the index to out[0],
+// the top-2 check writes out[0] = (thr > 0 && b1 - b2 >= thr).
+__global__ __launch_bounds__(64) void k_red_fin(const float2* __restrict__ part, int argmax, float thr,
+                                                int32_t* out) {
+    const int lane = threadIdx.x;
+    // lanes past the partials hold the identity (argmax: partial 0 again)
+    float2 r = lane < RED_NB ? part[lane] : (argmax ? part[0] : make_float2(-1e30f, -1e30f));
+    int ri = __float_as_int(r.y);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float oa = __shfl_xor(r.x, o, 64);
+        if (argmax) {
+            const int oi = __shfl_xor(ri, o, 64);
+            amax_merge(r.x, ri, oa, oi);
+        } else {
+            const float ob = __shfl_xor(r.y, o, 64);
+            top2_merge(r.x, r.y, oa, ob);
+        }
+    }
+    if (lane == 0) *out = argmax ? ri : ((thr > 0.0f && (r.x - r.y) >= thr) ? 1 : 0);
 }
 
 
@@ -2792,13 +2833,15 @@ void dpuf_hip_capture(void* s, int32_t M, int32_t H, const float* h, const float
     LAUNCHED("k_capture");
 }
 
-void dpuf_hip_topcheck(void* s, const float* logits, int32_t n, float thr, int32_t* flag) {
-    hipLaunchKernelGGL(k_topcheck, dim3(1), dim3(1024), 0, ST(s), logits, n, thr, flag);
+void dpuf_hip_topcheck(void* s, const float* logits, int32_t n, float thr, int32_t* flag, void* scratch) {
+    hipLaunchKernelGGL(k_red_part, dim3(RED_NB), dim3(256), 0, ST(s), logits, n, 0, (float2*)scratch);
+    hipLaunchKernelGGL(k_red_fin, dim3(1), dim3(64), 0, ST(s), (const float2*)scratch, 0, thr, flag);
     LAUNCHED("k_topcheck");
 }
 
-void dpuf_hip_argmax(void* s, const float* logits, int32_t V, int32_t* out) {
-    hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, ST(s), logits, V, out);
+void dpuf_hip_argmax(void* s, const float* logits, int32_t V, int32_t* out, void* scratch) {
+    hipLaunchKernelGGL(k_red_part, dim3(RED_NB), dim3(256), 0, ST(s), logits, V, 1, (float2*)scratch);
+    hipLaunchKernelGGL(k_red_fin, dim3(1), dim3(64), 0, ST(s), (const float2*)scratch, 1, 0.0f, out);
     LAUNCHED("k_argmax");
 }
 

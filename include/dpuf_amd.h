@@ -82,6 +82,13 @@ DPUF_EXPORT double dpuf_amd_copy_bench(size_t bytes, int32_t iters);
  * tests of the multi-group path and for tuning. */
 DPUF_EXPORT void dpuf_amd_set_gemv_max_workgroups(int32_t n);
 
+/* Runs the device logit reductions on n host floats placed `offset` floats
+ * (0..3) past a 16-byte boundary: mode 1 returns the first-maximum index the
+ * greedy sampler takes (dpuf-cli.c:1997-2004); mode 0 returns the Zone-A
+ * early-exit flag, 1 when thr > 0 and top1 - top2 >= thr over the multiset
+ * (dpuf_engine.c:2101-2110).  -1 on error.  For tests. */
+DPUF_EXPORT int32_t dpuf_amd_reduce_check(const float* x, int32_t n, int32_t offset, int32_t mode, float thr);
+
 #ifdef __cplusplus
 }
 #endif

@@ -812,15 +812,9 @@ int32_t orc_engine_forward(OrcEngine* e, int32_t n_tokens, const int32_t* ids, i
             run_weight(w, 1, xn, logits, 0, za, pq, ps, pm);
             int32_t nz = za * 16;
             if (nz > c->vocab_size) nz = c->vocab_size;
-            float b1 = -1e30f, b2 = -1e30f;
-            for (int32_t i = 0; i < nz; i++) {
-                float v = logits[i];
-                if (v > b1) { b2 = b1; b1 = v; }
-                else if (v > b2) { b2 = v; }
-            }
             const char* em = getenv("DPUF_EARLY_MARGIN");
             float thr = em ? (float)atof(em) : 1.25f;
-            if (thr > 0.0f && (b1 - b2) >= thr) {
+            if (orc_top2_exit(logits, nz, thr)) {
                 for (int32_t i = za * 16; i < c->vocab_size; i++) logits[i] = -1e9f;
             } else {
                 /* Prep again and finish the remaining tiles (same values). */
@@ -834,6 +828,19 @@ int32_t orc_engine_forward(OrcEngine* e, int32_t n_tokens, const int32_t* ids, i
     free(h); free(hn); free(xn); free(qb); free(kb); free(vb); free(ao);
     free(gb); free(ub); free(pq); free(ps); free(pm);
     return 0;
+}
+
+/* Zone-A early-exit test of dpuf_engine.c:2101-2110: the sequential top-1 /
+ * top-2 scan from -1e30 (a value equal to the top counts as the second), then
+ * exit when thr > 0 and top1 - top2 >= thr. */
+int32_t orc_top2_exit(const float* x, int32_t n, float thr) {
+    float b1 = -1e30f, b2 = -1e30f;
+    for (int32_t i = 0; i < n; i++) {
+        float v = x[i];
+        if (v > b1) { b2 = b1; b1 = v; }
+        else if (v > b2) { b2 = v; }
+    }
+    return (thr > 0.0f && (b1 - b2) >= thr) ? 1 : 0;
 }
 
 /* Greedy sampler of dpuf-cli.c:1997-2004: first maximum under strict '>'. */

@@ -56,6 +56,7 @@ const float* orc_engine_get_capture(OrcEngine* e);
 int32_t orc_engine_forward(OrcEngine* e, int32_t n_tokens, const int32_t* ids, int32_t pos0,
                            const float* embeds_in, int32_t only_last, float* logits);
 int32_t orc_argmax(const float* logits, int32_t V);
+int32_t orc_top2_exit(const float* x, int32_t n, float thr);
 int32_t orc_num_threads(void);
 
 #ifdef __cplusplus

@@ -59,6 +59,7 @@ def load():
     _sig(lib, "orc_engine_get_capture", P, [P])
     _sig(lib, "orc_engine_forward", I32, [P, I32, P, I32, P, I32, P])
     _sig(lib, "orc_argmax", I32, [P, I32])
+    _sig(lib, "orc_top2_exit", I32, [P, I32, C.c_float])
     _sig(lib, "orc_num_threads", I32, [])
     _lib = lib
     return lib

@@ -415,3 +415,36 @@ def test_argmax_first_max(orc):
     assert orc.orc_argmax(M.ptr(x), 5) == 1
     x = np.full(100, -3.0, np.float32)
     assert orc.orc_argmax(M.ptr(x), 100) == 0
+    # NaN: never greater than anything, so a NaN first element stays the answer
+    x = np.array([np.nan, 1.0, 7.0], np.float32)
+    assert orc.orc_argmax(M.ptr(x), 3) == 0
+    x = np.array([1.0, np.nan, 7.0, np.nan], np.float32)
+    assert orc.orc_argmax(M.ptr(x), 4) == 2
+    # agrees with numpy's first-maximum rule on NaN-free rows with ties
+    rng = np.random.default_rng(5)
+    for n in (1, 3, 17, 4096):
+        x = rng.integers(-3, 4, n).astype(np.float32)
+        assert orc.orc_argmax(M.ptr(x), n) == int(np.argmax(x))
+
+
+def test_top2_exit(orc):
+    """The multiset top-2 margin: a repeated maximum has margin 0; the margin
+    is top1 - top2 over values, whatever their order."""
+    x = np.array([1.0, 4.0, 2.5], np.float32)
+    assert orc.orc_top2_exit(M.ptr(x), 3, 1.5) == 1      # 4 - 2.5 = 1.5 >= 1.5
+    assert orc.orc_top2_exit(M.ptr(x), 3, 1.6) == 0
+    assert orc.orc_top2_exit(M.ptr(x), 3, 0.0) == 0      # thr <= 0 never exits
+    x = np.array([4.0, 1.0, 4.0], np.float32)
+    assert orc.orc_top2_exit(M.ptr(x), 3, 1e-7) == 0     # tie at the top: margin 0
+    x = np.array([7.0], np.float32)
+    assert orc.orc_top2_exit(M.ptr(x), 1, 1.0) == 1      # second is the -1e30 start
+    rng = np.random.default_rng(6)
+    for n in (2, 33, 5000):
+        x = rng.standard_normal(n).astype(np.float32)
+        s = np.sort(x)[::-1]
+        margin = np.float32(s[0]) - np.float32(s[1])
+        for thr in (margin * np.float32(0.5), margin, margin * np.float32(2.0)):
+            thr = float(np.float32(thr))
+            assert orc.orc_top2_exit(M.ptr(x), n, thr) == int(thr > 0 and margin >= np.float32(thr))
+            xp = rng.permutation(x)
+            assert orc.orc_top2_exit(M.ptr(xp), n, thr) == orc.orc_top2_exit(M.ptr(x), n, thr)

@@ -160,3 +160,32 @@ def test_embed(eng, orc):
     e2 = np.zeros_like(eg)
     eng.dpuf_embed_qr_any_f32(C.byref(d), len(ids), M.ptr(ids), M.ptr(e2), None)
     assert _same_bits(e2, eo)
+
+
+@pytest.mark.parametrize("offset", [0, 1, 2, 3])
+def test_logit_reductions(eng, orc, offset):
+    """Device argmax (first maximum) and Zone-A top-2 exit flag against the
+    oracle: rows of every length class (n % 4, shorter than a float4, longer
+    than the 64 workgroup slices), 16-byte misaligned starts, ties, a NaN
+    first element, repeated maxima."""
+    rng = np.random.default_rng(40 + offset)
+    cases = []
+    for n in (1, 2, 3, 5, 63, 257, 4096, 40961, 151936):
+        cases.append(rng.standard_normal(n).astype(np.float32))
+        cases.append(rng.integers(-2, 3, n).astype(np.float32))  # many ties
+    x = rng.standard_normal(5000).astype(np.float32)
+    x[[17, 4000]] = 9.0  # repeated maximum
+    cases.append(x)
+    x = rng.standard_normal(3000).astype(np.float32)
+    x[0] = np.nan
+    cases.append(x)
+    x = rng.standard_normal(3000).astype(np.float32)
+    x[[5, 2999]] = np.nan
+    cases.append(x)
+    for x in cases:
+        n = x.size
+        got = eng.dpuf_amd_reduce_check(M.ptr(x), n, offset, 1, 0.0)
+        assert got == orc.orc_argmax(M.ptr(x), n), (n, offset)
+        for thr in (1e-7, 0.05, 0.5, 3.0):
+            got = eng.dpuf_amd_reduce_check(M.ptr(x), n, offset, 0, thr)
+            assert got == orc.orc_top2_exit(M.ptr(x), n, thr), (n, offset, thr)
