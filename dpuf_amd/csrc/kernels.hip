@@ -1902,10 +1902,12 @@ __global__ __launch_bounds__(256) void k_attn_dec(const float* __restrict__ q, c
     const int pos = *pos0p;
     const int kv_len = pos + 1;
 
-    // V rows [c0, c0 + V_ROWS) -> vst, 1 KB per wave instruction; rows past
+    // V rows [c0, min(c0 + V_ROWS, kv_len)) -> vst, 1 KB per wave instruction
+    // (whole instructions: a few rows past kv_len may come along); rows past
     // the cache end are redirected to row 0 (never read back).
     auto stage_v = [&](int c0) {
-        constexpr int n_ins = V_ROWS * HD / 256;
+        const int rows = kv_len - c0 < V_ROWS ? kv_len - c0 : V_ROWS;
+        const int n_ins = (rows * HD + 255) / 256;
         for (int ii = wave; ii < n_ins; ii += 4) {
             const int e = ii * 256 + lane * 4;  // float index inside the chunk
             int t = c0 + e / HD;
