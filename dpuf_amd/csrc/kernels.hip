@@ -1523,13 +1523,20 @@ __global__ __launch_bounds__(AP_NT) void k_attn_pv(const float* __restrict__ S, 
 // single trailing head), HD in {64, 128, 256}.
 // ---------------------------------------------------------------------------
 #define PVT_R 32  // score rows per workgroup
+#ifndef PVT_KV
 #define PVT_KV 8  // keys per register batch of V
+#endif
 
-// 4 keys t .. t + 3 of the tile: rows' p from LDS, V from registers
-DEV void pvt_keys4(float (&acc)[4][4], const float* pr, int ldp, int t, const float4* v) {
-    float4 p4[4];
+// p of keys t .. t + 3 for the thread's 4 rows (t clamped into the row so a
+// read ahead of the last keys stays inside it; such values are not used)
+DEV void pvt_readp(const float* pr, int ldp, int t, float4 (&p4)[4]) {
+    t = t < ldp - 4 ? t : ldp - 4;
 #pragma unroll
     for (int k = 0; k < 4; k++) p4[k] = *(const float4*)(pr + (size_t)k * ldp + t);
+}
+
+// 4 keys of the tile: rows' p (already read), V from registers
+DEV void pvt_keys4(float (&acc)[4][4], const float4 (&p4)[4], const float4* v) {
 #pragma unroll
     for (int j = 0; j < 4; j++) {
 #pragma unroll
@@ -1665,8 +1672,11 @@ __global__ __launch_bounds__(2 * HD) void k_attn_pvt(const float* __restrict__ S
 #pragma unroll
     for (int j = 0; j < KV; j++) va[j] = *(const float4*)(vg + (size_t)(j < max_seq ? j : max_seq - 1) * HD);
     int t0 = 0;
-    // (the scheduling barriers keep each batch's loads ahead of the FMAs of
-    // the batch before it, so their latency is covered)
+    // (the scheduling barriers keep each batch's V loads ahead of the FMAs of
+    // the batch before it, and each 4 keys' p reads ahead of the FMAs of the 4
+    // keys before them, so their latencies are covered)
+    float4 pa[4], pb[4];
+    pvt_readp(pr, ldp, 0, pa);
     for (; t0 + 2 * KV <= nfull; t0 += 2 * KV) {
 #pragma unroll
         for (int j = 0; j < KV; j++) {
@@ -1675,21 +1685,32 @@ __global__ __launch_bounds__(2 * HD) void k_attn_pvt(const float* __restrict__ S
         }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int j = 0; j < KV; j += 4) pvt_keys4(acc, pr, ldp, t0 + j, va + j);
-        __builtin_amdgcn_sched_barrier(0);
+        for (int j = 0; j < 2 * KV; j += 8) {
+            const float4* vv = j < KV ? va + j : vb + (j - KV);
+            pvt_readp(pr, ldp, t0 + j + 4, pb);
+            __builtin_amdgcn_sched_barrier(0);
+            pvt_keys4(acc, pa, vv);
+            __builtin_amdgcn_sched_barrier(0);
+            pvt_readp(pr, ldp, t0 + j + 8, pa);
+            __builtin_amdgcn_sched_barrier(0);
+            pvt_keys4(acc, pb, vv + 4);
+            __builtin_amdgcn_sched_barrier(0);
+            if (j + 8 == KV) {
 #pragma unroll
-        for (int j = 0; j < KV; j++) {
-            const int t = t0 + 2 * KV + j;
-            va[j] = *(const float4*)(vg + (size_t)(t < max_seq ? t : max_seq - 1) * HD);
+                for (int jj = 0; jj < KV; jj++) {
+                    const int t = t0 + 2 * KV + jj;
+                    va[jj] = *(const float4*)(vg + (size_t)(t < max_seq ? t : max_seq - 1) * HD);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
         }
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int j = 0; j < KV; j += 4) pvt_keys4(acc, pr, ldp, t0 + KV + j, vb + j);
-        __builtin_amdgcn_sched_barrier(0);
     }
     if (t0 + KV <= nfull) {
 #pragma unroll
-        for (int j = 0; j < KV; j += 4) pvt_keys4(acc, pr, ldp, t0 + j, va + j);
+        for (int j = 0; j < KV; j += 4) {
+            pvt_readp(pr, ldp, t0 + j, pa);
+            pvt_keys4(acc, pa, va + j);
+        }
         t0 += KV;
     }
     // the tile's last keys: row k takes key t only while t < its kv_len
