@@ -835,6 +835,9 @@ __global__ __launch_bounds__(1024) void k_mv(MvArgs A) {
 #ifndef GM_RF
 #define GM_RF 1  // 16-row fragments per wave (workgroup = 64 GM_RF rows)
 #endif
+#ifndef GM_TT
+#define GM_TT 4  // 16-token tiles per workgroup
+#endif
 
 typedef _Float16 gm_h2 __attribute__((ext_vector_type(2)));
 typedef _Float16 gm_h8 __attribute__((ext_vector_type(8)));
@@ -1523,24 +1526,29 @@ __global__ __launch_bounds__(AP_NT) void k_attn_pv(const float* __restrict__ S, 
 // single trailing head), HD in {64, 128, 256}.
 // ---------------------------------------------------------------------------
 #define PVT_R 32  // score rows per workgroup
+#ifndef PVT_RT
+#define PVT_RT 4  // rows per thread in P.V (workgroup of 8 HD / PVT_RT threads)
+#endif
 #ifndef PVT_KV
 #define PVT_KV 8  // keys per register batch of V
 #endif
 
-// p of keys t .. t + 3 for the thread's 4 rows (t clamped into the row so a
+// p of keys t .. t + 3 for the thread's RT rows (t clamped into the row so a
 // read ahead of the last keys stays inside it; such values are not used)
-DEV void pvt_readp(const float* pr, int ldp, int t, float4 (&p4)[4]) {
+template <int RT>
+DEV void pvt_readp(const float* pr, int ldp, int t, float4 (&p4)[RT]) {
     t = t < ldp - 4 ? t : ldp - 4;
 #pragma unroll
-    for (int k = 0; k < 4; k++) p4[k] = *(const float4*)(pr + (size_t)k * ldp + t);
+    for (int k = 0; k < RT; k++) p4[k] = *(const float4*)(pr + (size_t)k * ldp + t);
 }
 
 // 4 keys of the tile: rows' p (already read), V from registers
-DEV void pvt_keys4(float (&acc)[4][4], const float4 (&p4)[4], const float4* v) {
+template <int RT>
+DEV void pvt_keys4(float (&acc)[RT][4], const float4 (&p4)[RT], const float4* v) {
 #pragma unroll
     for (int j = 0; j < 4; j++) {
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
+        for (int k = 0; k < RT; k++) {
             const float pk = j == 0 ? p4[k].x : j == 1 ? p4[k].y : j == 2 ? p4[k].z : p4[k].w;
             acc[k][0] = fmaf(pk, v[j].x, acc[k][0]);
             acc[k][1] = fmaf(pk, v[j].y, acc[k][1]);
@@ -1550,11 +1558,11 @@ DEV void pvt_keys4(float (&acc)[4][4], const float4 (&p4)[4], const float4* v) {
     }
 }
 
-template <int HD>
-__global__ __launch_bounds__(2 * HD) void k_attn_pvt(const float* __restrict__ S, const float* __restrict__ vc,
-                                                    const int32_t* __restrict__ pos0p, int M, int n_q, int n_kv,
-                                                    int max_seq, int qt, int ldp, float* __restrict__ out) {
-    constexpr int NT = 2 * HD, R = PVT_R, KV = PVT_KV;
+template <int HD, int RT>
+__global__ __launch_bounds__(8 * HD / RT) void k_attn_pvt(const float* __restrict__ S, const float* __restrict__ vc,
+                                                         const int32_t* __restrict__ pos0p, int M, int n_q, int n_kv,
+                                                         int max_seq, int qt, int ldp, float* __restrict__ out) {
+    constexpr int NT = 8 * HD / RT, R = PVT_R, KV = PVT_KV;  // (R / RT) row groups x (HD / 4) dim groups
     constexpr int TPR = NT / R;  // threads per row in the softmax phases
     extern __shared__ __align__(16) float P[];  // [R][ldp]
     __shared__ float part[8 * R];
@@ -1654,17 +1662,18 @@ __global__ __launch_bounds__(2 * HD) void k_attn_pvt(const float* __restrict__ S
         }
     }
     __syncthreads();
-    // P.V: lane = 8 * ri + (di & 7), wave w holds di = 8w .. 8w + 7
-    const int ri = lane >> 3, di = 8 * wv + (lane & 7);
-    float acc[4][4];
+    // P.V: a wave holds 8 row groups x 8 dim groups, lane = 8 * (ri % 8) + di % 8
+    constexpr int WPR = HD / 32;  // waves per block of 8 row groups
+    const int ri = 8 * (wv / WPR) + (lane >> 3), di = 8 * (wv % WPR) + (lane & 7);
+    float acc[RT][4];
 #pragma unroll
-    for (int k = 0; k < 4; k++)
+    for (int k = 0; k < RT; k++)
 #pragma unroll
         for (int i = 0; i < 4; i++) acc[k][i] = 0.0f;
-    int Lr[4];
+    int Lr[RT];
 #pragma unroll
-    for (int k = 0; k < 4; k++) Lr[k] = row_len(4 * ri + k);
-    const float* pr = P + (size_t)(4 * ri) * ldp;
+    for (int k = 0; k < RT; k++) Lr[k] = row_len(RT * ri + k);
+    const float* pr = P + (size_t)(RT * ri) * ldp;
     const float* vg = vc + (size_t)kvh * max_seq * HD + 4 * di;
     // keys below Lmin, in whole batches, go to every row unconditionally
     const int nfull = Lmin / KV * KV;
@@ -1675,8 +1684,8 @@ __global__ __launch_bounds__(2 * HD) void k_attn_pvt(const float* __restrict__ S
     // (the scheduling barriers keep each batch's V loads ahead of the FMAs of
     // the batch before it, and each 4 keys' p reads ahead of the FMAs of the 4
     // keys before them, so their latencies are covered)
-    float4 pa[4], pb[4];
-    pvt_readp(pr, ldp, 0, pa);
+    float4 pa[RT], pb[RT];
+    pvt_readp<RT>(pr, ldp, 0, pa);
     for (; t0 + 2 * KV <= nfull; t0 += 2 * KV) {
 #pragma unroll
         for (int j = 0; j < KV; j++) {
@@ -1687,13 +1696,13 @@ __global__ __launch_bounds__(2 * HD) void k_attn_pvt(const float* __restrict__ S
 #pragma unroll
         for (int j = 0; j < 2 * KV; j += 8) {
             const float4* vv = j < KV ? va + j : vb + (j - KV);
-            pvt_readp(pr, ldp, t0 + j + 4, pb);
+            pvt_readp<RT>(pr, ldp, t0 + j + 4, pb);
             __builtin_amdgcn_sched_barrier(0);
-            pvt_keys4(acc, pa, vv);
+            pvt_keys4<RT>(acc, pa, vv);
             __builtin_amdgcn_sched_barrier(0);
-            pvt_readp(pr, ldp, t0 + j + 8, pa);
+            pvt_readp<RT>(pr, ldp, t0 + j + 8, pa);
             __builtin_amdgcn_sched_barrier(0);
-            pvt_keys4(acc, pb, vv + 4);
+            pvt_keys4<RT>(acc, pb, vv + 4);
             __builtin_amdgcn_sched_barrier(0);
             if (j + 8 == KV) {
 #pragma unroll
@@ -1708,8 +1717,8 @@ __global__ __launch_bounds__(2 * HD) void k_attn_pvt(const float* __restrict__ S
     if (t0 + KV <= nfull) {
 #pragma unroll
         for (int j = 0; j < KV; j += 4) {
-            pvt_readp(pr, ldp, t0 + j, pa);
-            pvt_keys4(acc, pa, va + j);
+            pvt_readp<RT>(pr, ldp, t0 + j, pa);
+            pvt_keys4<RT>(acc, pa, va + j);
         }
         t0 += KV;
     }
@@ -1717,7 +1726,7 @@ __global__ __launch_bounds__(2 * HD) void k_attn_pvt(const float* __restrict__ S
     for (int t = t0; t < Lmax; t++) {
         const float4 v = *(const float4*)(vg + (size_t)t * HD);
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
+        for (int k = 0; k < RT; k++) {
             if (t < Lr[k]) {
                 const float pk = pr[(size_t)k * ldp + t];
                 acc[k][0] = fmaf(pk, v.x, acc[k][0]);
@@ -1728,8 +1737,8 @@ __global__ __launch_bounds__(2 * HD) void k_attn_pvt(const float* __restrict__ S
         }
     }
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
-        const int r = 4 * ri + k;
+    for (int k = 0; k < RT; k++) {
+        const int r = RT * ri + k;
         if (Lr[k] > 0)
             *(float4*)(out + ((size_t)(m0 + r / G) * n_q + kvh * G + r % G) * HD + 4 * di) =
                 make_float4(acc[k][0], acc[k][1], acc[k][2], acc[k][3]);
@@ -2704,9 +2713,11 @@ void dpuf_hip_gemv(void* s, int32_t M, int32_t n_jobs, const DpufGemvJob* jobs, 
         // a multiple of 8 row tiles keeps a row tile's token tiles on one XCD
         const int gx = (t + 7) & ~7;
         if (GM_RF == 2)
-            hipLaunchKernelGGL((k_gemm_mfma<4, 2>), dim3(gx, (M + 63) / 64), dim3(256), 0, ST(s), G);
+            hipLaunchKernelGGL((k_gemm_mfma<GM_TT, 2>), dim3(gx, (M + 16 * GM_TT - 1) / (16 * GM_TT)), dim3(256), 0,
+                               ST(s), G);
         else
-            hipLaunchKernelGGL((k_gemm_mfma<4, 1>), dim3(gx, (M + 63) / 64), dim3(256), 0, ST(s), G);
+            hipLaunchKernelGGL((k_gemm_mfma<GM_TT, 1>), dim3(gx, (M + 16 * GM_TT - 1) / (16 * GM_TT)), dim3(256), 0,
+                               ST(s), G);
         LAUNCHED("k_gemm_mfma");
     }
 }
@@ -2753,18 +2764,18 @@ int32_t dpuf_hip_attn_split(void* s, int32_t M, int32_t lmax, const float* q, co
             if (hd == 64) {
                 hipLaunchKernelGGL(k_attn_sc<64>, g1, dim3(256), lds1, ST(s), q, kc, pos0p, M, n_q, n_kv, max_seq,
                                    scale, qt1, scores);
-                hipLaunchKernelGGL(k_attn_pvt<64>, gt, dim3(128), ldst, ST(s), scores, vc, pos0p, M, n_q, n_kv,
-                                   max_seq, qt, ldp, out);
+                hipLaunchKernelGGL((k_attn_pvt<64, PVT_RT>), gt, dim3(8 * 64 / PVT_RT), ldst, ST(s), scores, vc,
+                                   pos0p, M, n_q, n_kv, max_seq, qt, ldp, out);
             } else if (hd == 128) {
                 hipLaunchKernelGGL(k_attn_sc<128>, g1, dim3(256), lds1, ST(s), q, kc, pos0p, M, n_q, n_kv, max_seq,
                                    scale, qt1, scores);
-                hipLaunchKernelGGL(k_attn_pvt<128>, gt, dim3(256), ldst, ST(s), scores, vc, pos0p, M, n_q, n_kv,
-                                   max_seq, qt, ldp, out);
+                hipLaunchKernelGGL((k_attn_pvt<128, PVT_RT>), gt, dim3(8 * 128 / PVT_RT), ldst, ST(s), scores, vc,
+                                   pos0p, M, n_q, n_kv, max_seq, qt, ldp, out);
             } else {
                 hipLaunchKernelGGL(k_attn_sc<256>, g1, dim3(256), lds1, ST(s), q, kc, pos0p, M, n_q, n_kv, max_seq,
                                    scale, qt1, scores);
-                hipLaunchKernelGGL(k_attn_pvt<256>, gt, dim3(512), ldst, ST(s), scores, vc, pos0p, M, n_q, n_kv,
-                                   max_seq, qt, ldp, out);
+                hipLaunchKernelGGL((k_attn_pvt<256, PVT_RT>), gt, dim3(8 * 256 / PVT_RT), ldst, ST(s), scores, vc,
+                                   pos0p, M, n_q, n_kv, max_seq, qt, ldp, out);
             }
             LAUNCHED("k_attn_split_tiled");
             return 0;
