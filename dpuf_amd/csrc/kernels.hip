@@ -1040,6 +1040,79 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(GmArgs A) {
 // QK-norm + NeoX RoPE + KV-cache store (reference dpuf_engine.c:1791-1817,
 // 1841-1879).  grid: (M, n_q + n_kv); block: hd threads.
 // ---------------------------------------------------------------------------
+// The same per (token, head) with one wave each, four per workgroup, for
+// HD = 64, 128, 256: lane l holds elements l + 64e (e < HD / 64), so a RoPE
+// pair (i, i + HD/2) sits in one lane for HD >= 128 and in lanes l, l ^ 32
+// for HD = 64; the norm's 8 accumulator chains (lane j: elements j, j + 8,
+// ... in order) gather their elements by shuffles, the hsum tree follows.
+template <int HD>
+__global__ __launch_bounds__(256) void k_qk_rope_kv_w(float* __restrict__ q, float* __restrict__ k,
+                                                      const float* __restrict__ v, const float* __restrict__ qn,
+                                                      const float* __restrict__ kn, float eps,
+                                                      const float* __restrict__ cos_tab,
+                                                      const float* __restrict__ sin_tab, float* __restrict__ kc,
+                                                      float* __restrict__ vc, const int32_t* __restrict__ pos0p, int M,
+                                                      int n_q, int n_kv, int max_seq) {
+    constexpr int E = HD / 64, half = HD / 2;
+    const int lane = threadIdx.x & 63;
+    const int u = blockIdx.x * 4 + (threadIdx.x >> 6);  // (token, head) unit of this wave
+    const int nh = n_q + n_kv;
+    if (u >= M * nh) return;  // whole wave
+    const int m = u / nh, head = u % nh;
+    const int pos = *pos0p + m;
+    const bool is_k = head >= n_q;
+    const int hh = is_k ? head - n_q : head;
+    float* vec = is_k ? (k + ((size_t)m * n_kv + hh) * HD) : (q + ((size_t)m * n_q + hh) * HD);
+    const float* nw = is_k ? kn : qn;
+    // every load first: one memory round trip for the whole wave
+    float x[E], wn[E], cs[E], sn[E], vv[E];
+#pragma unroll
+    for (int e = 0; e < E; e++) {
+        const int i = lane + 64 * e, j = i < half ? i : i - half;
+        x[e] = vec[i];
+        wn[e] = nw ? nw[i] : 1.0f;
+        cs[e] = cos_tab[(size_t)pos * half + j];
+        sn[e] = sin_tab[(size_t)pos * half + j];
+        vv[e] = is_k ? v[((size_t)m * n_kv + hh) * HD + i] : 0.0f;
+    }
+    if (nw) {
+        // chain j = lane (< 8): elements j + 8i, i = 0 .. HD/8 - 1, in order
+        float a = 0.0f;
+#pragma unroll
+        for (int i = 0; i < HD / 8; i++) {
+            // element (lane & 7) + 8i: register i / 8 of lane (lane & 7) + 8 (i % 8)
+            const float xv = __shfl(x[i / 8], (lane & 7) + 8 * (i % 8), 64);
+            a = fmaf(xv, xv, a);
+        }
+        float pt[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) pt[j] = __shfl(a, j, 64);
+        const float inv = 1.0f / sqrtf(hsum8(pt) / (float)HD + eps);
+#pragma unroll
+        for (int e = 0; e < E; e++) x[e] = (x[e] * inv) * wn[e];
+    }
+    float o[E];
+#pragma unroll
+    for (int e = 0; e < E; e++) {
+        const int i = lane + 64 * e;
+        float partner;
+        if (E == 1) partner = __shfl_xor(x[0], 32, 64);  // element i ^ 32 = i +- half
+        else partner = x[i < half ? e + E / 2 : e - E / 2];
+        if (i < half) o[e] = fmaf(x[e], cs[e], -(partner * sn[e]));
+        else o[e] = fmaf(x[e], cs[e], partner * sn[e]);
+    }
+#pragma unroll
+    for (int e = 0; e < E; e++) vec[lane + 64 * e] = o[e];
+    if (is_k) {
+#pragma unroll
+        for (int e = 0; e < E; e++) {
+            const size_t off = ((size_t)hh * max_seq + pos) * HD + lane + 64 * e;
+            kc[off] = o[e];
+            vc[off] = vv[e];
+        }
+    }
+}
+
 __global__ void k_qk_rope_kv(float* __restrict__ q, float* __restrict__ k, const float* __restrict__ v,
                              const float* __restrict__ qn, const float* __restrict__ kn, float eps,
                              const float* __restrict__ cos_tab, const float* __restrict__ sin_tab,
@@ -2725,8 +2798,19 @@ void dpuf_hip_gemv(void* s, int32_t M, int32_t n_jobs, const DpufGemvJob* jobs, 
 void dpuf_hip_qk_rope_kv(void* s, int32_t M, float* q, float* k, const float* v, const float* q_norm,
                          const float* k_norm, float eps, const float* cos_tab, const float* sin_tab, float* kc,
                          float* vc, const int32_t* pos0, int32_t n_q, int32_t n_kv, int32_t hd, int32_t max_seq) {
-    hipLaunchKernelGGL(k_qk_rope_kv, dim3(M, n_q + n_kv), dim3(hd), (size_t)hd * sizeof(float), ST(s), q, k, v,
-                       q_norm, k_norm, eps, cos_tab, sin_tab, kc, vc, pos0, n_q, n_kv, hd, max_seq);
+    const dim3 gw((M * (n_q + n_kv) + 3) / 4);
+    if (hd == 64)
+        hipLaunchKernelGGL(k_qk_rope_kv_w<64>, gw, dim3(256), 0, ST(s), q, k, v, q_norm, k_norm, eps, cos_tab, sin_tab,
+                           kc, vc, pos0, M, n_q, n_kv, max_seq);
+    else if (hd == 128)
+        hipLaunchKernelGGL(k_qk_rope_kv_w<128>, gw, dim3(256), 0, ST(s), q, k, v, q_norm, k_norm, eps, cos_tab,
+                           sin_tab, kc, vc, pos0, M, n_q, n_kv, max_seq);
+    else if (hd == 256)
+        hipLaunchKernelGGL(k_qk_rope_kv_w<256>, gw, dim3(256), 0, ST(s), q, k, v, q_norm, k_norm, eps, cos_tab,
+                           sin_tab, kc, vc, pos0, M, n_q, n_kv, max_seq);
+    else
+        hipLaunchKernelGGL(k_qk_rope_kv, dim3(M, n_q + n_kv), dim3(hd), (size_t)hd * sizeof(float), ST(s), q, k, v,
+                           q_norm, k_norm, eps, cos_tab, sin_tab, kc, vc, pos0, n_q, n_kv, hd, max_seq);
     LAUNCHED("k_qk_rope_kv");
 }
 
