@@ -916,32 +916,41 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(GmArgs A) {
         gw = gw < J.g1 ? gw : J.g1 - 1;
         aw[f] = J.g + (size_t)gw * gstride + (kc & 1) * 8;
     }
-    // staging: thread tid takes UPT consecutive 8-byte quarters of one
-    // (token tk, block sb of the stage) pair's 32 activation bytes
-    constexpr int UPT = NT * GM_SB * 4 / 256;  // 4, 2 or 1
+    // staging: thread tid takes UPT consecutive 8-byte quarters of the
+    // stage's (token tk, block sb) pairs' 32 activation bytes: QPT quarters of
+    // each of PPT consecutive pairs
+    constexpr int UPT = NT * GM_SB * 4 / 256;
+    constexpr int PPT = UPT > 4 ? UPT / 4 : 1, QPT = UPT > 4 ? 4 : UPT;
     const int n_st = (n_blk + GM_SB - 1) / GM_SB;
-    const int pr = tid * UPT / 4, q0 = tid * UPT % 4;  // pair and first quarter
-    const int tk = pr % NT, sbt = pr / NT;
-    uint2 sq[UPT];
-    float ss;
+    const int pr0 = tid * UPT / 4, q0 = tid * UPT % 4;  // first pair and first quarter
+    uint2 sq[PPT][QPT];
+    float ss[PPT];
     auto stage_load = [&](int st) {
-        const int b = st * GM_SB + sbt, m = m0 + tk;
-        const bool ok = m < M && b < n_blk;
 #pragma unroll
-        for (int k = 0; k < UPT; k++)
-            sq[k] = ok ? *(const uint2*)(J.q + (size_t)m * K + b * 32 + 8 * (q0 + k)) : make_uint2(0u, 0u);
-        ss = ok && q0 == 0 ? J.s[(size_t)m * n_blk + b] : 0.0f;
+        for (int pp = 0; pp < PPT; pp++) {
+            const int pr = pr0 + pp, tk = pr % NT, sbt = pr / NT;
+            const int b = st * GM_SB + sbt, m = m0 + tk;
+            const bool ok = m < M && b < n_blk;
+#pragma unroll
+            for (int k = 0; k < QPT; k++)
+                sq[pp][k] = ok ? *(const uint2*)(J.q + (size_t)m * K + b * 32 + 8 * (q0 + k)) : make_uint2(0u, 0u);
+            ss[pp] = ok && q0 == 0 ? J.s[(size_t)m * n_blk + b] : 0.0f;
+        }
     };
     auto stage_store = [&](int buf) {
 #pragma unroll
-        for (int k = 0; k < UPT; k++) {
-            const int qu = q0 + k;
-            uint32_t h0, h1, h2, h3;
-            gm_i8_to_h(sq[k].x, h0, h1);
-            gm_i8_to_h(sq[k].y, h2, h3);
-            *(uint4*)&bq[buf][sbt][tk][16 * (qu ^ ((tk >> 1) & 3))] = make_uint4(h0, h1, h2, h3);
+        for (int pp = 0; pp < PPT; pp++) {
+            const int pr = pr0 + pp, tk = pr % NT, sbt = pr / NT;
+#pragma unroll
+            for (int k = 0; k < QPT; k++) {
+                const int qu = q0 + k;
+                uint32_t h0, h1, h2, h3;
+                gm_i8_to_h(sq[pp][k].x, h0, h1);
+                gm_i8_to_h(sq[pp][k].y, h2, h3);
+                *(uint4*)&bq[buf][sbt][tk][16 * (qu ^ ((tk >> 1) & 3))] = make_uint4(h0, h1, h2, h3);
+            }
+            if (q0 == 0) bs[buf][sbt][tk & 15][tk >> 4] = ss[pp];
         }
-        if (q0 == 0) bs[buf][sbt][tk & 15][tk >> 4] = ss;
     };
     // weights of one stage: nibble word and 4 scales per fragment and block
     uint32_t wn[2][GM_SB][RF];
