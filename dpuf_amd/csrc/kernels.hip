@@ -838,6 +838,12 @@ __global__ __launch_bounds__(1024) void k_mv(MvArgs A) {
 #ifndef GM_TT
 #define GM_TT 4  // 16-token tiles per workgroup
 #endif
+#ifndef GM_XCD
+#define GM_XCD 1  // XCD-grouped workgroup order
+#endif
+#ifndef GM_PF
+#define GM_PF 1  // LDS reads one block ahead
+#endif
 
 typedef _Float16 gm_h2 __attribute__((ext_vector_type(2)));
 typedef _Float16 gm_h8 __attribute__((ext_vector_type(8)));
@@ -858,6 +864,7 @@ struct GmArgs {
     int n_jobs;
     int tb[4];  // prefix sums of 16-group row tiles per job
     int K, M;
+    int gy;     // token tiles
 };
 
 // Two fp16 values from bytes b0, b1 of x and 0x64: 1024 + byte each.
@@ -892,14 +899,27 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(GmArgs A) {
     constexpr int NT = 16 * TT;  // tokens per workgroup
     __shared__ __align__(16) uint8_t bq[2][GM_SB][NT][64];  // f16 activations [stage][block][token][k]
     __shared__ __align__(16) float bs[2][GM_SB][16][TT];    // block scales [stage][block][token % 16][token / 16]
-    const int rt = blockIdx.x;
+    // Workgroups go to the 8 XCDs round-robin by linear id L.  L = xcd +
+    // 8 j with j = gy r + ty puts row tile 8 r + xcd of every token tile ty on
+    // one XCD, dispatched back to back, so the gy workgroups that read the
+    // same weights run together and share them through that XCD's L2.
+#if GM_XCD
+    const int jx = blockIdx.x >> 3, ty = jx % A.gy;
+    const int rt = (jx / A.gy) * 8 + (blockIdx.x & 7);
+#else
+    const int rt = blockIdx.x, ty = blockIdx.y;
+#endif
     if (rt >= A.tb[A.n_jobs]) return;  // padding of the grid (whole workgroup)
     int ji = 0;
     if (A.n_jobs > 1 && rt >= A.tb[1]) ji = 1;
     if (A.n_jobs > 2 && rt >= A.tb[2]) ji = 2;
-    const GmJob& J = A.j[ji];
+    // the job's fields picked from the kernel arguments by uniform selects,
+    // so they stay in scalar registers through the loop
+    const GmJob& J = ji == 0 ? A.j[0] : ji == 1 ? A.j[1] : A.j[2];
+    const int8_t* const Jq = ji == 0 ? A.j[0].q : ji == 1 ? A.j[1].q : A.j[2].q;
+    const float* const Js = ji == 0 ? A.j[0].s : ji == 1 ? A.j[1].s : A.j[2].s;
     const int gb = J.g0 + (rt - A.tb[ji]) * 8 * RF;  // first group of the workgroup
-    const int m0 = blockIdx.y * NT;
+    const int m0 = ty * NT;
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, i16 = l & 15, kc = l >> 4;
     const int K = A.K, M = A.M, n_blk = K >> 5;
     const size_t gstride = (size_t)n_blk * 144;
@@ -925,16 +945,18 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(GmArgs A) {
     const int pr0 = tid * UPT / 4, q0 = tid * UPT % 4;  // first pair and first quarter
     uint2 sq[PPT][QPT];
     float ss[PPT];
+    // Loads are unconditional, at token and block clamped into range: a
+    // token past M only feeds output columns that are never stored, a block
+    // past the end is never computed, and a load without a branch around it
+    // keeps the compiler's wait counts exact.
     auto stage_load = [&](int st) {
 #pragma unroll
         for (int pp = 0; pp < PPT; pp++) {
             const int pr = pr0 + pp, tk = pr % NT, sbt = pr / NT;
-            const int b = st * GM_SB + sbt, m = m0 + tk;
-            const bool ok = m < M && b < n_blk;
+            const int b = min(st * GM_SB + sbt, n_blk - 1), m = min(m0 + tk, M - 1);
 #pragma unroll
-            for (int k = 0; k < QPT; k++)
-                sq[pp][k] = ok ? *(const uint2*)(J.q + (size_t)m * K + b * 32 + 8 * (q0 + k)) : make_uint2(0u, 0u);
-            ss[pp] = ok && q0 == 0 ? J.s[(size_t)m * n_blk + b] : 0.0f;
+            for (int k = 0; k < QPT; k++) sq[pp][k] = *(const uint2*)(Jq + (size_t)m * K + b * 32 + 8 * (q0 + k));
+            ss[pp] = Js[(size_t)m * n_blk + b];
         }
     };
     auto stage_store = [&](int buf) {
@@ -973,10 +995,32 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(GmArgs A) {
 #pragma unroll
         for (int t = 0; t < TT; t++) acc[f][t] = (gm_f4){0.0f, 0.0f, 0.0f, 0.0f};
 
+#if GM_PF
+    // B fragments and token scales of one block, read from LDS one block
+    // ahead of its MFMAs so the read latency hides behind the block before
+    gm_h8 bfr[2][TT];
+    float xsr[2][TT];
+    auto lds_b = [&](int buf, int sb, int slot) {
+#pragma unroll
+        for (int t = 0; t < TT; t++) xsr[slot][t] = bs[buf][sb][i16][t];
+#pragma unroll
+        for (int t = 0; t < TT; t++) {
+            const int tok = 16 * t + i16;
+            bfr[slot][t] = *(const gm_h8*)&bq[buf][sb][tok][16 * (kc ^ ((tok >> 1) & 3))];
+        }
+    };
+#endif
     auto compute = [&](int st, int buf, const uint32_t (&n)[GM_SB][RF], const uint2 (&sc)[GM_SB][RF]) {
+#if GM_PF
+        lds_b(buf, 0, 0);
+#endif
 #pragma unroll
         for (int sb = 0; sb < GM_SB; sb++) {
             if (st * GM_SB + sb >= n_blk) break;  // uniform
+#if GM_PF
+            if (sb + 1 < GM_SB) lds_b(buf, sb + 1, (sb + 1) & 1);
+            __builtin_amdgcn_sched_barrier(0);
+#endif
             gm_h8 a[RF];
             float wsf[RF][4];
 #pragma unroll
@@ -988,12 +1032,21 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(GmArgs A) {
                 wsf[f][3] = h2f((uint16_t)(sc[sb][f].y >> 16));
             }
             float xs[TT];
+#if GM_PF
+#pragma unroll
+            for (int t = 0; t < TT; t++) xs[t] = xsr[sb & 1][t];
+#else
 #pragma unroll
             for (int t = 0; t < TT; t++) xs[t] = bs[buf][sb][i16][t];
+#endif
 #pragma unroll
             for (int t = 0; t < TT; t++) {
+#if GM_PF
+                const gm_h8 bf = bfr[sb & 1][t];
+#else
                 const int tok = 16 * t + i16;
                 const gm_h8 bf = *(const gm_h8*)&bq[buf][sb][tok][16 * (kc ^ ((tok >> 1) & 3))];
+#endif
 #pragma unroll
                 for (int f = 0; f < RF; f++) {
                     const gm_f4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[f], bf, (gm_f4){0.0f, 0.0f, 0.0f, 0.0f},
@@ -1017,12 +1070,12 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(GmArgs A) {
         compute(st, 0, wn[0], ws[0]);
         stage_store(1);
         __syncthreads();
-        if (st + 2 < n_st) {
-            stage_load(st + 2);
-            weights_load(st + 2, wn[0], ws[0]);
-        }
+        // on the last pair this stages clamped data that is never computed;
+        // the loop body has no branch around its loads
+        stage_load(st + 2);
+        weights_load(st + 2, wn[0], ws[0]);
         compute(st + 1, 1, wn[1], ws[1]);
-        if (st + 2 < n_st) stage_store(0);
+        stage_store(0);
         __syncthreads();
     }
     if (st < n_st) compute(st, 0, wn[0], ws[0]);
@@ -2794,12 +2847,12 @@ void dpuf_hip_gemv(void* s, int32_t M, int32_t n_jobs, const DpufGemvJob* jobs, 
         if (t <= 0) return;
         // a multiple of 8 row tiles keeps a row tile's token tiles on one XCD
         const int gx = (t + 7) & ~7;
+        G.gy = (M + 16 * GM_TT - 1) / (16 * GM_TT);
+        const dim3 grid = GM_XCD ? dim3(gx * G.gy) : dim3(gx, G.gy);
         if (GM_RF == 2)
-            hipLaunchKernelGGL((k_gemm_mfma<GM_TT, 2>), dim3(gx, (M + 16 * GM_TT - 1) / (16 * GM_TT)), dim3(256), 0,
-                               ST(s), G);
+            hipLaunchKernelGGL((k_gemm_mfma<GM_TT, 2>), grid, dim3(256), 0, ST(s), G);
         else
-            hipLaunchKernelGGL((k_gemm_mfma<GM_TT, 1>), dim3(gx, (M + 16 * GM_TT - 1) / (16 * GM_TT)), dim3(256), 0,
-                               ST(s), G);
+            hipLaunchKernelGGL((k_gemm_mfma<GM_TT, 1>), grid, dim3(256), 0, ST(s), G);
         LAUNCHED("k_gemm_mfma");
     }
 }
