@@ -288,7 +288,12 @@ static void engine_free(Engine* e) {
     for (int p = 0; p < N_PREFIX; p++) { dpuf_hip_free(e->pk[p]); dpuf_hip_free(e->pv[p]); }
     float* bufs[] = {e->h, e->hn, e->q, e->k, e->v, e->ao, e->gate, e->up, e->logits, e->scores, e->embeds, e->capture};
     for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++) dpuf_hip_free(bufs[i]);
-    for (int i = 0; i < 3; i++) { dpuf_hip_free(e->prep[i].q); dpuf_hip_free(e->prep[i].s); dpuf_hip_free(e->prep[i].m); }
+    for (int i = 0; i < 3; i++) {
+        dpuf_hip_free(e->prep[i].q);
+        dpuf_hip_free(e->prep[i].s);
+        dpuf_hip_free(e->prep[i].m);
+        dpuf_hip_free(e->prep[i].h);
+    }
     dpuf_hip_free(e->d_ids);
     dpuf_hip_free(e->d_red);
     dpuf_hip_host_free(e->h_pinned);
@@ -392,7 +397,8 @@ DPUF_EXPORT void* dpuf_engine_create(const DpufModelConfig* cfg, const DpufLayer
             e->prep[i].q = (int8_t*)dpuf_hip_malloc(B * maxd);
             e->prep[i].s = (float*)dpuf_hip_malloc(B * (maxd / 32) * 4);
             e->prep[i].m = (int32_t*)dpuf_hip_malloc(B * (maxd / 32) * 4);
-            if (!e->prep[i].q || !e->prep[i].s || !e->prep[i].m) goto fail;
+            e->prep[i].h = (uint16_t*)dpuf_hip_malloc(B * maxd * 2);
+            if (!e->prep[i].q || !e->prep[i].s || !e->prep[i].m || !e->prep[i].h) goto fail;
         }
         e->d_ids = (int32_t*)dpuf_hip_malloc((B + 64) * 4);
         e->h_pinned = (int32_t*)dpuf_hip_host_alloc((B + 64) * 4);

@@ -24,11 +24,14 @@ typedef struct {
     int32_t rows, cols, n_groups;
 } DpufDevW;
 
-/* Prepped activations of M rows: q int8 [M][K], s f32 [M][K/32], m i32 [M][K/32]. */
+/* Prepped activations of M rows: q int8 [M][K], s f32 [M][K/32], m i32 [M][K/32],
+ * and h, the same q as fp16 [M][K] (the M > 1 GEMM's input; the prep
+ * kernels fill it when non-NULL and M > 1). */
 typedef struct {
     int8_t*  q;
     float*   s;
     int32_t* m;
+    uint16_t* h;
 } DpufPrep;
 
 /* One matrix of a fused GEMV launch: groups [g0, g1) of w, reading prep p,

@@ -264,7 +264,25 @@ DEV void quad_fwht64(float* v, int qp) {
 
 // Quantises the lane's 16 FWHT'd values (half of 32-block 2*blk + qp/2) and
 // stores the int8 values, and from the even lane the block scale and 8*sum(q).
-DEV void quad_quant_store(const float* v, int qp, int blk, int8_t* q, float* s, int32_t* m) {
+typedef _Float16 gm_h2 __attribute__((ext_vector_type(2)));
+
+// Two fp16 values from bytes b0, b1 of x and 0x64: 1024 + byte each.
+DEV uint32_t gm_pair(uint32_t x, uint32_t sel) { return __builtin_amdgcn_perm(0x64646464u, x, sel); }
+
+DEV uint32_t gm_sub(uint32_t v, _Float16 c) {
+    gm_h2 h = __builtin_bit_cast(gm_h2, v);
+    h = h - (gm_h2){c, c};
+    return __builtin_bit_cast(uint32_t, h);
+}
+
+// Four int8 (one word) -> four f16 in two words (exact).
+DEV void i8x4_to_h(uint32_t x, uint32_t& a, uint32_t& b) {
+    const uint32_t u = x ^ 0x80808080u;  // q + 128 per byte
+    a = gm_sub(gm_pair(u, 0x04010400u), (_Float16)1152.0f);
+    b = gm_sub(gm_pair(u, 0x04030402u), (_Float16)1152.0f);
+}
+
+DEV void quad_quant_store(const float* v, int qp, int blk, int8_t* q, float* s, int32_t* m, uint16_t* h) {
     float amax = 0.0f;
 #pragma unroll
     for (int k = 0; k < 16; k++) {
@@ -296,6 +314,13 @@ DEV void quad_quant_store(const float* v, int qp, int blk, int8_t* q, float* s, 
     }
     sum += dpp_xor1(sum);
     *(uint4*)(q + 64 * blk + 16 * qp) = make_uint4(w[0], w[1], w[2], w[3]);
+    if (h) {  // the same 16 values as fp16 (exact: |q| <= 127)
+        uint32_t hw[8];
+#pragma unroll
+        for (int g = 0; g < 4; g++) i8x4_to_h(w[g], hw[2 * g], hw[2 * g + 1]);
+        *(uint4*)(h + 64 * blk + 16 * qp) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+        *(uint4*)(h + 64 * blk + 16 * qp + 8) = make_uint4(hw[4], hw[5], hw[6], hw[7]);
+    }
     if ((qp & 1) == 0) {
         s[2 * blk + (qp >> 1)] = d;
         m[2 * blk + (qp >> 1)] = sum * 8;
@@ -377,7 +402,8 @@ __global__ __launch_bounds__(1024) void k_resnorm_prep(int H, float* __restrict_
         for (int k = 0; k < 16; k++) y[k] = v[k];
         apply_sign_bits(y, sb[p]);
         quad_fwht64(y, qp);
-        quad_quant_store(y, qp, blk, ps.p[p].q + (size_t)m * H, ps.p[p].s + (size_t)m * nb, ps.p[p].m + (size_t)m * nb);
+        quad_quant_store(y, qp, blk, ps.p[p].q + (size_t)m * H, ps.p[p].s + (size_t)m * nb, ps.p[p].m + (size_t)m * nb,
+                         ps.p[p].h ? ps.p[p].h + (size_t)m * H : nullptr);
     }
 }
 
@@ -391,7 +417,8 @@ __global__ __launch_bounds__(256) void k_prep(int K, const float* __restrict__ x
     load16(x + (size_t)m * K + 16 * t, v);
     apply_sign_bits(v, quad_sign_bits(sign, blk, qp));
     quad_fwht64(v, qp);
-    quad_quant_store(v, qp, blk, p.q + (size_t)m * K, p.s + (size_t)m * nb, p.m + (size_t)m * nb);
+    quad_quant_store(v, qp, blk, p.q + (size_t)m * K, p.s + (size_t)m * nb, p.m + (size_t)m * nb,
+                     p.h ? p.h + (size_t)m * K : nullptr);
 }
 
 // SwiGLU with dead zone (reference swiglu_range_avx2, 8-wide path,
@@ -416,7 +443,8 @@ __global__ __launch_bounds__(256) void k_swiglu_prep(int I, const float* __restr
     }
     apply_sign_bits(v, sb);
     quad_fwht64(v, qp);
-    quad_quant_store(v, qp, blk, p.q + (size_t)m * I, p.s + (size_t)m * nb, p.m + (size_t)m * nb);
+    quad_quant_store(v, qp, blk, p.q + (size_t)m * I, p.s + (size_t)m * nb, p.m + (size_t)m * nb,
+                     p.h ? p.h + (size_t)m * I : nullptr);
 }
 
 // ---------------------------------------------------------------------------
@@ -845,16 +873,16 @@ __global__ __launch_bounds__(1024) void k_mv(MvArgs A) {
 #define GM_PF 1  // LDS reads one block ahead
 #endif
 
-typedef _Float16 gm_h2 __attribute__((ext_vector_type(2)));
 typedef _Float16 gm_h8 __attribute__((ext_vector_type(8)));
 typedef float gm_f4 __attribute__((ext_vector_type(4)));
+typedef uint32_t gm_u4 __attribute__((ext_vector_type(4)));
 
 struct GmJob {
     const uint8_t* g;  // dense groups of the matrix
     int g0, g1;        // groups computed
     int rows;
-    const int8_t* q;   // activations [M][K]
-    const float* s;    // block scales [M][K/32]
+    const uint16_t* h;  // activations as fp16 [M][K]
+    const float* s;     // block scales [M][K/32]
     float* out;        // out[m * ldo + row]
     int ldo;
 };
@@ -867,14 +895,6 @@ struct GmArgs {
     int gy;     // token tiles
 };
 
-// Two fp16 values from bytes b0, b1 of x and 0x64: 1024 + byte each.
-DEV uint32_t gm_pair(uint32_t x, uint32_t sel) { return __builtin_amdgcn_perm(0x64646464u, x, sel); }
-
-DEV uint32_t gm_sub(uint32_t v, _Float16 c) {
-    gm_h2 h = __builtin_bit_cast(gm_h2, v);
-    h = h - (gm_h2){c, c};
-    return __builtin_bit_cast(uint32_t, h);
-}
 
 // A fragment from one nibble word (row i, columns 8 kc .. 8 kc + 7 of a
 // block: low nibbles = columns +0..+3, high nibbles = +4..+7): u - 8 as f16.
@@ -887,15 +907,9 @@ DEV gm_h8 gm_unpack_a(uint32_t w) {
     return __builtin_bit_cast(gm_h8, make_uint4(r0, r1, r2, r3));
 }
 
-// Four int8 (one word) -> four f16 in two words.
-DEV void gm_i8_to_h(uint32_t x, uint32_t& a, uint32_t& b) {
-    const uint32_t u = x ^ 0x80808080u;  // q + 128 per byte
-    a = gm_sub(gm_pair(u, 0x04010400u), (_Float16)1152.0f);
-    b = gm_sub(gm_pair(u, 0x04030402u), (_Float16)1152.0f);
-}
 
 template <int TT, int RF>
-__global__ __launch_bounds__(256) void k_gemm_mfma(GmArgs A) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k_gemm_mfma(GmArgs A) {
     constexpr int NT = 16 * TT;  // tokens per workgroup
     __shared__ __align__(16) uint8_t bq[2][GM_SB][NT][64];  // f16 activations [stage][block][token][k]
     __shared__ __align__(16) float bs[2][GM_SB][16][TT];    // block scales [stage][block][token % 16][token / 16]
@@ -916,7 +930,7 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(GmArgs A) {
     // the job's fields picked from the kernel arguments by uniform selects,
     // so they stay in scalar registers through the loop
     const GmJob& J = ji == 0 ? A.j[0] : ji == 1 ? A.j[1] : A.j[2];
-    const int8_t* const Jq = ji == 0 ? A.j[0].q : ji == 1 ? A.j[1].q : A.j[2].q;
+    const uint16_t* const Jh = ji == 0 ? A.j[0].h : ji == 1 ? A.j[1].h : A.j[2].h;
     const float* const Js = ji == 0 ? A.j[0].s : ji == 1 ? A.j[1].s : A.j[2].s;
     const int gb = J.g0 + (rt - A.tb[ji]) * 8 * RF;  // first group of the workgroup
     const int m0 = ty * NT;
@@ -936,42 +950,43 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(GmArgs A) {
         gw = gw < J.g1 ? gw : J.g1 - 1;
         aw[f] = J.g + (size_t)gw * gstride + (kc & 1) * 8;
     }
-    // staging: thread tid takes UPT consecutive 8-byte quarters of the
-    // stage's (token tk, block sb) pairs' 32 activation bytes: QPT quarters of
-    // each of PPT consecutive pairs
-    constexpr int UPT = NT * GM_SB * 4 / 256;
-    constexpr int PPT = UPT > 4 ? UPT / 4 : 1, QPT = UPT > 4 ? 4 : UPT;
+    // staging: a stage holds NT tokens x GM_SB blocks of 64 fp16 bytes, four
+    // 16-byte chunks each.  Chunk c = tid + 256 k of the stage is chunk c & 3
+    // of pair c / 4 = (token (c / 4) % NT, block (c / 4) / NT), so the 64
+    // lanes of a load read 16 tokens' 64 contiguous bytes.  Scale i = tid +
+    // 256 k is pair i.  Loads are unconditional, at token and block clamped
+    // into range: a token past M only feeds output columns that are never
+    // stored, a block past the end is never computed, and a load without a
+    // branch around it keeps the compiler's wait counts exact.
+    constexpr int CPT = NT * GM_SB * 4 / 256, SPT = (NT * GM_SB + 255) / 256;
+    static_assert(CPT >= 1 && NT * GM_SB * 4 % 256 == 0, "whole chunks per thread");
     const int n_st = (n_blk + GM_SB - 1) / GM_SB;
-    const int pr0 = tid * UPT / 4, q0 = tid * UPT % 4;  // first pair and first quarter
-    uint2 sq[PPT][QPT];
-    float ss[PPT];
-    // Loads are unconditional, at token and block clamped into range: a
-    // token past M only feeds output columns that are never stored, a block
-    // past the end is never computed, and a load without a branch around it
-    // keeps the compiler's wait counts exact.
+    gm_u4 sq[CPT];  // a native vector: a struct copy would keep the array in scratch
+    float ss[SPT];
     auto stage_load = [&](int st) {
 #pragma unroll
-        for (int pp = 0; pp < PPT; pp++) {
-            const int pr = pr0 + pp, tk = pr % NT, sbt = pr / NT;
+        for (int k = 0; k < CPT; k++) {
+            const int c = tid + 256 * k, pr = c >> 2, tk = pr % NT, sbt = pr / NT;
             const int b = min(st * GM_SB + sbt, n_blk - 1), m = min(m0 + tk, M - 1);
+            sq[k] = *(const gm_u4*)(Jh + (size_t)m * K + b * 32 + 8 * (c & 3));
+        }
 #pragma unroll
-            for (int k = 0; k < QPT; k++) sq[pp][k] = *(const uint2*)(Jq + (size_t)m * K + b * 32 + 8 * (q0 + k));
-            ss[pp] = Js[(size_t)m * n_blk + b];
+        for (int k = 0; k < SPT; k++) {
+            const int i = min(tid + 256 * k, NT * GM_SB - 1), tk = i % NT, sbt = i / NT;
+            const int b = min(st * GM_SB + sbt, n_blk - 1), m = min(m0 + tk, M - 1);
+            ss[k] = Js[(size_t)m * n_blk + b];
         }
     };
     auto stage_store = [&](int buf) {
 #pragma unroll
-        for (int pp = 0; pp < PPT; pp++) {
-            const int pr = pr0 + pp, tk = pr % NT, sbt = pr / NT;
+        for (int k = 0; k < CPT; k++) {
+            const int c = tid + 256 * k, pr = c >> 2, tk = pr % NT, sbt = pr / NT, qu = c & 3;
+            *(gm_u4*)&bq[buf][sbt][tk][16 * (qu ^ ((tk >> 1) & 3))] = sq[k];
+        }
 #pragma unroll
-            for (int k = 0; k < QPT; k++) {
-                const int qu = q0 + k;
-                uint32_t h0, h1, h2, h3;
-                gm_i8_to_h(sq[pp][k].x, h0, h1);
-                gm_i8_to_h(sq[pp][k].y, h2, h3);
-                *(uint4*)&bq[buf][sbt][tk][16 * (qu ^ ((tk >> 1) & 3))] = make_uint4(h0, h1, h2, h3);
-            }
-            if (q0 == 0) bs[buf][sbt][tk & 15][tk >> 4] = ss[pp];
+        for (int k = 0; k < SPT; k++) {
+            const int i = tid + 256 * k, tk = i % NT, sbt = i / NT;
+            if (NT * GM_SB % 256 == 0 || i < NT * GM_SB) bs[buf][sbt][tk & 15][tk >> 4] = ss[k];
         }
     };
     // weights of one stage: nibble word and 4 scales per fragment and block
@@ -1022,14 +1037,15 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(GmArgs A) {
             __builtin_amdgcn_sched_barrier(0);
 #endif
             gm_h8 a[RF];
-            float wsf[RF][4];
+            _Float16 wsh[RF][4];
 #pragma unroll
             for (int f = 0; f < RF; f++) {
                 a[f] = gm_unpack_a(n[sb][f]);
-                wsf[f][0] = h2f((uint16_t)(sc[sb][f].x & 0xFFFFu));
-                wsf[f][1] = h2f((uint16_t)(sc[sb][f].x >> 16));
-                wsf[f][2] = h2f((uint16_t)(sc[sb][f].y & 0xFFFFu));
-                wsf[f][3] = h2f((uint16_t)(sc[sb][f].y >> 16));
+                const gm_h2 lo = __builtin_bit_cast(gm_h2, sc[sb][f].x), hi = __builtin_bit_cast(gm_h2, sc[sb][f].y);
+                wsh[f][0] = lo[0];
+                wsh[f][1] = lo[1];
+                wsh[f][2] = hi[0];
+                wsh[f][3] = hi[1];
             }
             float xs[TT];
 #if GM_PF
@@ -1049,10 +1065,18 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(GmArgs A) {
 #endif
 #pragma unroll
                 for (int f = 0; f < RF; f++) {
+                    // float(ws) * xs as one mixed-precision FMA with a +0
+                    // addend: the same rounding as the product, and a zero
+                    // product's sign cannot reach acc, which is never -0.
+                    // All four before their uses, so no product is read by
+                    // the instruction right after the one writing it.
+                    float wx[4];
+#pragma unroll
+                    for (int v = 0; v < 4; v++) wx[v] = __builtin_fmaf((float)wsh[f][v], xs[t], 0.0f);
                     const gm_f4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[f], bf, (gm_f4){0.0f, 0.0f, 0.0f, 0.0f},
                                                                          0, 0, 0);
 #pragma unroll
-                    for (int v = 0; v < 4; v++) acc[f][t][v] = fmaf(d[v], wsf[f][v] * xs[t], acc[f][t][v]);
+                    for (int v = 0; v < 4; v++) acc[f][t][v] = fmaf(d[v], wx[v], acc[f][t][v]);
                 }
             }
         }
@@ -2338,7 +2362,7 @@ __global__ __launch_bounds__(256) void k_attn_dec(const float* __restrict__ q, c
         for (int kk = 0; kk < 16; kk++)
             if ((osb >> kk) & 1u) x[kk] = -x[kk];
         quad_fwht64(x, qp);
-        quad_quant_store(x, qp, blk, op.q, op.s, op.m);
+        quad_quant_store(x, qp, blk, op.q, op.s, op.m, nullptr);
     }
 }
 
@@ -2544,7 +2568,13 @@ __global__ void k_slab_unpack(int M, int K, const int32_t* __restrict__ sq, cons
         const int g = i % 8, b = (i / 8) % nb, m = i / (8 * nb);
         const int slab = m / 6, j = m % 6;
         const size_t base = (size_t)slab * nb;
-        *(int32_t*)(rows.q + (size_t)m * K + b * 32 + g * 4) = sq[(base + b) * 48 + g * 6 + j];
+        const int32_t w4 = sq[(base + b) * 48 + g * 6 + j];
+        *(int32_t*)(rows.q + (size_t)m * K + b * 32 + g * 4) = w4;
+        if (rows.h) {
+            uint32_t a, c;
+            i8x4_to_h((uint32_t)w4, a, c);
+            *(uint2*)(rows.h + (size_t)m * K + b * 32 + g * 4) = make_uint2(a, c);
+        }
         if (g == 0) {
             rows.s[(size_t)m * nb + b] = ss[(base + b) * 6 + j];
             rows.m[(size_t)m * nb + b] = sm[(base + b) * 6 + j];
@@ -2677,6 +2707,7 @@ void dpuf_hip_resnorm_prep(void* s, int32_t M, int32_t H, float* h, const float*
     for (int i = 0; i < n_prep; i++) {
         ps.sign[i] = signs[i];
         ps.p[i] = preps[i];
+        if (M == 1) ps.p[i].h = NULL;  // the one-row GEMV reads q only
     }
     const int threads = H / 16;  // H is a multiple of 1024 or 64 * 16 * k; checked at engine create
     const size_t lds = (size_t)8 * ((H >> 3) + 4) * sizeof(float);
@@ -2686,6 +2717,7 @@ void dpuf_hip_resnorm_prep(void* s, int32_t M, int32_t H, float* h, const float*
 
 void dpuf_hip_prep(void* s, int32_t M, int32_t K, const float* x, const uint8_t* sign, DpufPrep p) {
     const int quads = K / 16;
+    if (M == 1) p.h = NULL;
     // one wave per workgroup: the rows' loads spread over many CUs
     hipLaunchKernelGGL(k_prep, dim3((quads + 63) / 64, M), dim3(64), 0, ST(s), K, x, sign, p);
     LAUNCHED("k_prep");
@@ -2694,6 +2726,7 @@ void dpuf_hip_prep(void* s, int32_t M, int32_t K, const float* x, const uint8_t*
 void dpuf_hip_swiglu_prep(void* s, int32_t M, int32_t I, const float* gate, const float* up, float dz,
                           const uint8_t* sign, DpufPrep p) {
     const int quads = I / 16;
+    if (M == 1) p.h = NULL;
     hipLaunchKernelGGL(k_swiglu_prep, dim3((quads + 63) / 64, M), dim3(64), 0, ST(s), I, gate, up, dz, sign, p);
     LAUNCHED("k_swiglu_prep");
 }
@@ -2835,7 +2868,11 @@ void dpuf_hip_gemv(void* s, int32_t M, int32_t n_jobs, const DpufGemvJob* jobs, 
             G.j[i].g0 = jobs[i].g0;
             G.j[i].g1 = jobs[i].g1;
             G.j[i].rows = jobs[i].w.rows;
-            G.j[i].q = jobs[i].p.q;
+            G.j[i].h = jobs[i].p.h;
+            if (!jobs[i].p.h) {
+                note(hipErrorInvalidValue, "dpuf_hip_gemv: M > 1 needs the fp16 activations (DpufPrep.h)");
+                return;
+            }
             G.j[i].s = jobs[i].p.s;
             G.j[i].out = jobs[i].out;
             G.j[i].ldo = jobs[i].ldo;

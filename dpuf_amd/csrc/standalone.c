@@ -93,17 +93,20 @@ static void unstage(Staged* st) {
     dpuf_hip_free(st->sign);
 }
 
+/* M > 1 also gets the fp16 copy of q that the slab GEMM reads. */
 static int prep_alloc(DpufPrep* p, int32_t M, int32_t K) {
     p->q = (int8_t*)dpuf_hip_malloc((size_t)M * K);
     p->s = (float*)dpuf_hip_malloc((size_t)M * (K / 32) * 4);
     p->m = (int32_t*)dpuf_hip_malloc((size_t)M * (K / 32) * 4);
-    return p->q && p->s && p->m;
+    p->h = M > 1 ? (uint16_t*)dpuf_hip_malloc((size_t)M * K * 2) : NULL;
+    return p->q && p->s && p->m && (M == 1 || p->h);
 }
 
 static void prep_free(DpufPrep* p) {
     dpuf_hip_free(p->q);
     dpuf_hip_free(p->s);
     dpuf_hip_free(p->m);
+    dpuf_hip_free(p->h);
 }
 
 DPUF_EXPORT void dpuf_fwht64_sign_f32(int32_t cols, const float* x_in, const uint8_t* sign_bits, float* x_out) {
@@ -133,7 +136,7 @@ DPUF_EXPORT void dpuf_prep_had4_packed_slab(int32_t mc, int32_t cols, const floa
     float* dx = (float*)dpuf_hip_malloc((size_t)mc * cols * 4);
     float* df = (float*)dpuf_hip_malloc((size_t)mc * cols * 4);
     void* ds = sign_bits ? dpuf_hip_malloc((size_t)cols / 8) : NULL;
-    DpufPrep rows = {0, 0, 0};
+    DpufPrep rows = {0, 0, 0, 0};
     int32_t* sq = (int32_t*)dpuf_hip_malloc((size_t)nb * 192);
     float* ss = (float*)dpuf_hip_malloc((size_t)nb * 6 * 4);
     int32_t* sm = (int32_t*)dpuf_hip_malloc((size_t)nb * 6 * 4);
@@ -192,7 +195,7 @@ DPUF_EXPORT void dpuf_matmul_qr_hadamard4_packed_tile_range(int32_t M, int32_t r
     Staged st;
     if (!stage_weights(rows, cols, t_start, t_end, tensor_base, tile_offsets, NULL, &st)) return;
     const int32_t nb = cols / 32;
-    DpufPrep p = {0, 0, 0};
+    DpufPrep p = {0, 0, 0, 0};
     float* dout = (float*)dpuf_hip_malloc((size_t)M * rows * 4);
     if (prep_alloc(&p, M, cols) && dout) {
         if (M == 1) {
@@ -239,7 +242,7 @@ DPUF_EXPORT void dpuf_matmul_qr_hadamard4_packed_f32(int32_t M, int32_t rows, in
     if ((int64_t)n_tiles * 16 > (int64_t)rows + 15 || (int64_t)n_tiles * 16 < rows) return;
     Staged st;
     if (!stage_weights(rows, cols, 0, n_tiles, tensor_base, tile_offsets, sign_bits, &st)) return;
-    DpufPrep p = {0, 0, 0};
+    DpufPrep p = {0, 0, 0, 0};
     float* dx = (float*)dpuf_hip_malloc((size_t)M * cols * 4);
     float* dout = (float*)dpuf_hip_malloc((size_t)M * rows * 4);
     if (prep_alloc(&p, M, cols) && dx && dout) {
