@@ -847,17 +847,17 @@ __global__ __launch_bounds__(1024) void k_mv(MvArgs A) {
 // operations, sp = ws * xs and the fma, with the chains in registers across
 // the block loop, so the block order is the reference's.
 //
-// A workgroup of 4 waves computes 128 rows (16 groups) x 16 TT tokens; wave
-// w owns rows 32w .. 32w + 31 as two 16-row fragments and all the tokens as
-// TT 16-token tiles (2 TT MFMAs per block); TT = 4, 2 or 1 per launch, the
-// widest that still fills the chip.  Activations are staged in LDS, GM_SB
-// blocks per stage, converted from int8 to f16 on the way in and double-
+// A workgroup of 4 waves computes 64 GM_RF rows x 16 TT tokens; wave w owns
+// GM_RF 16-row fragments and all the tokens as TT 16-token tiles (GM_RF TT
+// MFMAs per block).  Activations arrive as fp16 (DpufPrep.h, written by the
+// prep kernels) and are staged in LDS, GM_SB blocks per stage, double-
 // buffered, one barrier per stage; a token's 64 bytes per block are four
 // 16-byte chunks stored XOR-swizzled by token so a fragment read is free of
-// bank conflicts.  Weights, nibbles and scales, are read straight into
-// registers one stage ahead.  MFMA lane layouts (gfx950, checked on the
-// device): A lane l = row l % 16, k = 8 (l / 16) + e; B lane l = token
-// l % 16, same k; D lane l = token l % 16, rows 4 (l / 16) + v.
+// bank conflicts.  A block's fragments are read from LDS one block ahead of
+// its MFMAs.  Weights, nibbles and scales, are read straight into registers
+// one stage ahead.  MFMA lane layouts (gfx950, checked on the device): A lane
+// l = row l % 16, k = 8 (l / 16) + e; B lane l = token l % 16, same k; D lane
+// l = token l % 16, rows 4 (l / 16) + v.
 // ---------------------------------------------------------------------------
 #define GM_SB 4  // blocks per LDS stage
 #ifndef GM_RF
