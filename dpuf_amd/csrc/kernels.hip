@@ -876,6 +876,7 @@ __global__ __launch_bounds__(1024) void k_mv(MvArgs A) {
 typedef _Float16 gm_h8 __attribute__((ext_vector_type(8)));
 typedef float gm_f4 __attribute__((ext_vector_type(4)));
 typedef uint32_t gm_u4 __attribute__((ext_vector_type(4)));
+#define GM_RSRC3 0x00020000  // buffer descriptor word 3 (gfx9 family): 32-bit raw data
 
 struct GmJob {
     const uint8_t* g;  // dense groups of the matrix
@@ -938,17 +939,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
     const int K = A.K, M = A.M, n_blk = K >> 5;
     const size_t gstride = (size_t)n_blk * 144;
 
-    // weight pointers of the wave's RF fragments (groups clamped into the job)
-    const uint8_t* an[RF];
-    const uint8_t* aw[RF];
+    // Every load is a buffer load: a wave-uniform descriptor, a 32-bit lane
+    // offset fixed for the launch and a scalar block offset, so addressing
+    // costs no vector instructions in the loop (and a load past a
+    // descriptor's range reads 0 instead of faulting).  Weights of the
+    // wave's RF fragments (groups clamped into the job) are addressed from
+    // the wave's first group.
+    const int wu = __builtin_amdgcn_readfirstlane(w);
+    const int gw0 = min(gb + 2 * RF * wu, J.g1 - 1);
+    const size_t wbytes = (size_t)(J.g1 - gw0) * gstride;
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(J.g + (size_t)gw0 * gstride), 0, (int)(wbytes < 0xFFFFFFFFu ? wbytes : 0xFFFFFFFFu), GM_RSRC3);
+    uint32_t on[RF], ow[RF];
 #pragma unroll
     for (int f = 0; f < RF; f++) {
-        int ga = gb + 2 * RF * w + 2 * f + (i16 >> 3);
-        ga = ga < J.g1 ? ga : J.g1 - 1;
-        an[f] = J.g + (size_t)ga * gstride + (size_t)n_blk * 16 + (i16 & 7) * 16 + kc * 4;
-        int gw = gb + 2 * RF * w + 2 * f + (kc >> 1);
-        gw = gw < J.g1 ? gw : J.g1 - 1;
-        aw[f] = J.g + (size_t)gw * gstride + (kc & 1) * 8;
+        const int ga = min(gb + 2 * RF * wu + 2 * f + (i16 >> 3), J.g1 - 1);
+        on[f] = (uint32_t)((size_t)(ga - gw0) * gstride + (size_t)n_blk * 16 + (i16 & 7) * 16 + kc * 4);
+        const int gs = min(gb + 2 * RF * wu + 2 * f + (kc >> 1), J.g1 - 1);
+        ow[f] = (uint32_t)((size_t)(gs - gw0) * gstride + (kc & 1) * 8);
     }
     // staging: a stage holds NT tokens x GM_SB blocks of 64 fp16 bytes, four
     // 16-byte chunks each.  Chunk c = tid + 256 k of the stage is chunk c & 3
@@ -963,18 +971,37 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
     const int n_st = (n_blk + GM_SB - 1) / GM_SB;
     gm_u4 sq[CPT];  // a native vector: a struct copy would keep the array in scratch
     float ss[SPT];
+    // byte offsets of the token rows (M K < 2^30 is checked at launch); with
+    // NT = 64 a chunk's block (k) and a scale's block (the wave, + 4 k) are
+    // uniform and go into the scalar offset
+    const __amdgpu_buffer_rsrc_t rh = __builtin_amdgcn_make_buffer_rsrc((void*)Jh, 0, M * K * 2, GM_RSRC3);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)Js, 0, M * n_blk * 4, GM_RSRC3);
+    uint32_t ho[CPT], so[SPT];
+#pragma unroll
+    for (int k = 0; k < CPT; k++) {
+        const int pr = (tid >> 2) + 64 * k, m = min(m0 + pr % NT, M - 1);
+        const int sbt = NT == 64 ? 0 : pr / NT;
+        ho[k] = (uint32_t)(2 * (m * K + 32 * sbt + 8 * (tid & 3)));
+    }
+#pragma unroll
+    for (int k = 0; k < SPT; k++) {
+        const int i = min(tid + 256 * k, NT * GM_SB - 1), m = min(m0 + i % NT, M - 1);
+        const int sbt = NT == 64 ? 0 : i / NT;
+        so[k] = (uint32_t)(4 * (m * n_blk + sbt));
+    }
+    // the stage's first block, clamped so that a stage's blocks stay in range
+    // when it starts in range (blocks past the end are never computed)
     auto stage_load = [&](int st) {
 #pragma unroll
         for (int k = 0; k < CPT; k++) {
-            const int c = tid + 256 * k, pr = c >> 2, tk = pr % NT, sbt = pr / NT;
-            const int b = min(st * GM_SB + sbt, n_blk - 1), m = min(m0 + tk, M - 1);
-            sq[k] = *(const gm_u4*)(Jh + (size_t)m * K + b * 32 + 8 * (c & 3));
+            const int sbt = NT == 64 ? k : 0;
+            const int b = NT == 64 ? min(st * GM_SB + sbt, n_blk - 1) : st * GM_SB;
+            sq[k] = __builtin_bit_cast(gm_u4, __builtin_amdgcn_raw_buffer_load_b128(rh, ho[k], b * 64, 0));
         }
 #pragma unroll
         for (int k = 0; k < SPT; k++) {
-            const int i = min(tid + 256 * k, NT * GM_SB - 1), tk = i % NT, sbt = i / NT;
-            const int b = min(st * GM_SB + sbt, n_blk - 1), m = min(m0 + tk, M - 1);
-            ss[k] = Js[(size_t)m * n_blk + b];
+            const int b = NT == 64 ? min(st * GM_SB + wu + 4 * k, n_blk - 1) : st * GM_SB;
+            ss[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, so[k], b * 4, 0));
         }
     };
     auto stage_store = [&](int buf) {
@@ -990,16 +1017,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
         }
     };
     // weights of one stage: nibble word and 4 scales per fragment and block
+    // (the two scale words stay separate 32-bit values: this compiler
+    // selected the first word's register for both words' fp16 halves when
+    // they came as one 2 x 32-bit vector into v_fma_mix_f32)
     uint32_t wn[2][GM_SB][RF];
-    uint2 ws[2][GM_SB][RF];
-    auto weights_load = [&](int st, uint32_t (&n)[GM_SB][RF], uint2 (&sc)[GM_SB][RF]) {
+    uint32_t ws[2][GM_SB][RF][2];
+    auto weights_load = [&](int st, uint32_t (&n)[GM_SB][RF], uint32_t (&sc)[GM_SB][RF][2]) {
 #pragma unroll
         for (int sb = 0; sb < GM_SB; sb++) {
             const int b = min(st * GM_SB + sb, n_blk - 1);
 #pragma unroll
             for (int f = 0; f < RF; f++) {
-                n[sb][f] = *(const uint32_t*)(an[f] + (size_t)b * 128);
-                sc[sb][f] = *(const uint2*)(aw[f] + (size_t)b * 16);
+                n[sb][f] = __builtin_amdgcn_raw_buffer_load_b32(rw, on[f], b * 128, 0);
+                sc[sb][f][0] = __builtin_amdgcn_raw_buffer_load_b32(rw, ow[f], b * 16, 0);
+                sc[sb][f][1] = __builtin_amdgcn_raw_buffer_load_b32(rw, ow[f], b * 16 + 4, 0);
             }
         }
     };
@@ -1025,7 +1056,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
         }
     };
 #endif
-    auto compute = [&](int st, int buf, const uint32_t (&n)[GM_SB][RF], const uint2 (&sc)[GM_SB][RF]) {
+    auto compute = [&](int st, int buf, const uint32_t (&n)[GM_SB][RF], const uint32_t (&sc)[GM_SB][RF][2]) {
 #if GM_PF
         lds_b(buf, 0, 0);
 #endif
@@ -1041,7 +1072,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
 #pragma unroll
             for (int f = 0; f < RF; f++) {
                 a[f] = gm_unpack_a(n[sb][f]);
-                const gm_h2 lo = __builtin_bit_cast(gm_h2, sc[sb][f].x), hi = __builtin_bit_cast(gm_h2, sc[sb][f].y);
+                const gm_h2 lo = __builtin_bit_cast(gm_h2, sc[sb][f][0]), hi = __builtin_bit_cast(gm_h2, sc[sb][f][1]);
                 wsh[f][0] = lo[0];
                 wsh[f][1] = lo[1];
                 wsh[f][2] = hi[0];
@@ -2869,6 +2900,10 @@ void dpuf_hip_gemv(void* s, int32_t M, int32_t n_jobs, const DpufGemvJob* jobs, 
             G.j[i].g1 = jobs[i].g1;
             G.j[i].rows = jobs[i].w.rows;
             G.j[i].h = jobs[i].p.h;
+            if ((long long)M * G.K >= (1ll << 30)) {
+                note(hipErrorInvalidValue, "dpuf_hip_gemv: M * K must stay below 2^30");
+                return;
+            }
             if (!jobs[i].p.h) {
                 note(hipErrorInvalidValue, "dpuf_hip_gemv: M > 1 needs the fp16 activations (DpufPrep.h)");
                 return;
