@@ -869,9 +869,6 @@ __global__ __launch_bounds__(1024) void k_mv(MvArgs A) {
 #ifndef GM_XCD
 #define GM_XCD 1  // XCD-grouped workgroup order
 #endif
-#ifndef GM_PF
-#define GM_PF 1  // LDS reads one block ahead
-#endif
 
 typedef _Float16 gm_h8 __attribute__((ext_vector_type(8)));
 typedef float gm_f4 __attribute__((ext_vector_type(4)));
@@ -914,6 +911,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
     constexpr int NT = 16 * TT;  // tokens per workgroup
     __shared__ __align__(16) uint8_t bq[2][GM_SB][NT][64];  // f16 activations [stage][block][token][k]
     __shared__ __align__(16) float bs[2][GM_SB][16][TT];    // block scales [stage][block][token % 16][token / 16]
+    __shared__ __align__(16) uint32_t bw[2][GM_SB][32 * RF];  // weight scales [stage][block][group * 4 + word]
     // Workgroups go to the 8 XCDs round-robin by linear id L.  L = xcd +
     // 8 j with j = gy r + ty puts row tile 8 r + xcd of every token tile ty on
     // one XCD, dispatched back to back, so the gy workgroups that read the
@@ -950,14 +948,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
     const size_t wbytes = (size_t)(J.g1 - gw0) * gstride;
     const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(J.g + (size_t)gw0 * gstride), 0, (int)(wbytes < 0xFFFFFFFFu ? wbytes : 0xFFFFFFFFu), GM_RSRC3);
-    uint32_t on[RF], ow[RF];
+    uint32_t on[RF];
 #pragma unroll
     for (int f = 0; f < RF; f++) {
         const int ga = min(gb + 2 * RF * wu + 2 * f + (i16 >> 3), J.g1 - 1);
         on[f] = (uint32_t)((size_t)(ga - gw0) * gstride + (size_t)n_blk * 16 + (i16 & 7) * 16 + kc * 4);
-        const int gs = min(gb + 2 * RF * wu + 2 * f + (kc >> 1), J.g1 - 1);
-        ow[f] = (uint32_t)((size_t)(gs - gw0) * gstride + (kc & 1) * 8);
     }
+    // Weight scales go through LDS with the activations: a stage's 8 RF
+    // groups x GM_SB blocks x 8 fp16 scales are WD dwords, dword d = tid % WD
+    // (group d / (4 GM_SB), block (d / 4) % GM_SB, word d % 4), addressed
+    // from the workgroup's first group; threads past WD repeat a dword.
+    // Blocks past the end read bytes that are never used.
+    constexpr int WD = 32 * RF * GM_SB;
+    static_assert(WD <= 256, "one scale dword per thread and stage");
+    const __amdgpu_buffer_rsrc_t rg = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(J.g + (size_t)gb * gstride), 0,
+        (int)((size_t)(J.g1 - gb) * gstride < 0xFFFFFFFFu ? (size_t)(J.g1 - gb) * gstride : 0xFFFFFFFFu), GM_RSRC3);
+    const int wd = tid % WD, wg_g = wd / (4 * GM_SB), wg_b = (wd >> 2) % GM_SB, wg_w = wd & 3;
+    const uint32_t og = (uint32_t)((size_t)(min(gb + wg_g, J.g1 - 1) - gb) * gstride + wg_b * 16 + wg_w * 4);
+    uint32_t sw;  // this thread's scale dword of the stage in flight
     // staging: a stage holds NT tokens x GM_SB blocks of 64 fp16 bytes, four
     // 16-byte chunks each.  Chunk c = tid + 256 k of the stage is chunk c & 3
     // of pair c / 4 = (token (c / 4) % NT, block (c / 4) / NT), so the 64
@@ -1003,6 +1012,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
             const int b = NT == 64 ? min(st * GM_SB + wu + 4 * k, n_blk - 1) : st * GM_SB;
             ss[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, so[k], b * 4, 0));
         }
+        sw = __builtin_amdgcn_raw_buffer_load_b32(rg, og, st * GM_SB * 16, 0);
     };
     auto stage_store = [&](int buf) {
 #pragma unroll
@@ -1015,23 +1025,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
             const int i = tid + 256 * k, tk = i % NT, sbt = i / NT;
             if (NT * GM_SB % 256 == 0 || i < NT * GM_SB) bs[buf][sbt][tk & 15][tk >> 4] = ss[k];
         }
+        bw[buf][wg_b][wg_g * 4 + wg_w] = sw;
     };
-    // weights of one stage: nibble word and 4 scales per fragment and block
-    // (the two scale words stay separate 32-bit values: this compiler
-    // selected the first word's register for both words' fp16 halves when
-    // they came as one 2 x 32-bit vector into v_fma_mix_f32)
+    // nibble words of one stage, per fragment and block
     uint32_t wn[2][GM_SB][RF];
-    uint32_t ws[2][GM_SB][RF][2];
-    auto weights_load = [&](int st, uint32_t (&n)[GM_SB][RF], uint32_t (&sc)[GM_SB][RF][2]) {
+    auto weights_load = [&](int st, uint32_t (&n)[GM_SB][RF]) {
 #pragma unroll
         for (int sb = 0; sb < GM_SB; sb++) {
             const int b = min(st * GM_SB + sb, n_blk - 1);
 #pragma unroll
-            for (int f = 0; f < RF; f++) {
-                n[sb][f] = __builtin_amdgcn_raw_buffer_load_b32(rw, on[f], b * 128, 0);
-                sc[sb][f][0] = __builtin_amdgcn_raw_buffer_load_b32(rw, ow[f], b * 16, 0);
-                sc[sb][f][1] = __builtin_amdgcn_raw_buffer_load_b32(rw, ow[f], b * 16 + 4, 0);
-            }
+            for (int f = 0; f < RF; f++) n[sb][f] = __builtin_amdgcn_raw_buffer_load_b32(rw, on[f], b * 128, 0);
         }
     };
 
@@ -1041,12 +1044,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
 #pragma unroll
         for (int t = 0; t < TT; t++) acc[f][t] = (gm_f4){0.0f, 0.0f, 0.0f, 0.0f};
 
-#if GM_PF
-    // B fragments and token scales of one block, read from LDS one block
-    // ahead of its MFMAs so the read latency hides behind the block before
+    // B fragments, token scales and the lane's 4 row scales of one block,
+    // read from LDS one block ahead of its MFMAs so the read latency hides
+    // behind the block before.  The row scales stay two separate 32-bit
+    // words: this compiler selected the first word's register for both
+    // words' fp16 halves when they came as one 2 x 32-bit vector into
+    // v_fma_mix_f32.
     gm_h8 bfr[2][TT];
     float xsr[2][TT];
+    uint32_t wsr[2][RF][2];
     auto lds_b = [&](int buf, int sb, int slot) {
+#pragma unroll
+        for (int f = 0; f < RF; f++) {
+            const int e = (2 * (RF * wu + f) + (kc >> 1)) * 4 + (kc & 1) * 2;
+            wsr[slot][f][0] = bw[buf][sb][e];
+            wsr[slot][f][1] = bw[buf][sb][e + 1];
+        }
 #pragma unroll
         for (int t = 0; t < TT; t++) xsr[slot][t] = bs[buf][sb][i16][t];
 #pragma unroll
@@ -1055,45 +1068,31 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
             bfr[slot][t] = *(const gm_h8*)&bq[buf][sb][tok][16 * (kc ^ ((tok >> 1) & 3))];
         }
     };
-#endif
-    auto compute = [&](int st, int buf, const uint32_t (&n)[GM_SB][RF], const uint32_t (&sc)[GM_SB][RF][2]) {
-#if GM_PF
+    auto compute = [&](int st, int buf, const uint32_t (&n)[GM_SB][RF]) {
         lds_b(buf, 0, 0);
-#endif
 #pragma unroll
         for (int sb = 0; sb < GM_SB; sb++) {
             if (st * GM_SB + sb >= n_blk) break;  // uniform
-#if GM_PF
             if (sb + 1 < GM_SB) lds_b(buf, sb + 1, (sb + 1) & 1);
             __builtin_amdgcn_sched_barrier(0);
-#endif
             gm_h8 a[RF];
             _Float16 wsh[RF][4];
 #pragma unroll
             for (int f = 0; f < RF; f++) {
                 a[f] = gm_unpack_a(n[sb][f]);
-                const gm_h2 lo = __builtin_bit_cast(gm_h2, sc[sb][f][0]), hi = __builtin_bit_cast(gm_h2, sc[sb][f][1]);
+                const gm_h2 lo = __builtin_bit_cast(gm_h2, wsr[sb & 1][f][0]),
+                            hi = __builtin_bit_cast(gm_h2, wsr[sb & 1][f][1]);
                 wsh[f][0] = lo[0];
                 wsh[f][1] = lo[1];
                 wsh[f][2] = hi[0];
                 wsh[f][3] = hi[1];
             }
             float xs[TT];
-#if GM_PF
 #pragma unroll
             for (int t = 0; t < TT; t++) xs[t] = xsr[sb & 1][t];
-#else
-#pragma unroll
-            for (int t = 0; t < TT; t++) xs[t] = bs[buf][sb][i16][t];
-#endif
 #pragma unroll
             for (int t = 0; t < TT; t++) {
-#if GM_PF
                 const gm_h8 bf = bfr[sb & 1][t];
-#else
-                const int tok = 16 * t + i16;
-                const gm_h8 bf = *(const gm_h8*)&bq[buf][sb][tok][16 * (kc ^ ((tok >> 1) & 3))];
-#endif
 #pragma unroll
                 for (int f = 0; f < RF; f++) {
                     // float(ws) * xs as one mixed-precision FMA with a +0
@@ -1115,25 +1114,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
 
     // prologue: stage 0 into LDS buffer 0, weights of stage 0
     stage_load(0);
-    weights_load(0, wn[0], ws[0]);
+    weights_load(0, wn[0]);
     stage_store(0);
     __syncthreads();
     int st = 0;
     for (; st + 2 <= n_st; st += 2) {
         stage_load(st + 1);
-        weights_load(st + 1, wn[1], ws[1]);
-        compute(st, 0, wn[0], ws[0]);
+        weights_load(st + 1, wn[1]);
+        compute(st, 0, wn[0]);
         stage_store(1);
         __syncthreads();
         // on the last pair this stages clamped data that is never computed;
         // the loop body has no branch around its loads
         stage_load(st + 2);
-        weights_load(st + 2, wn[0], ws[0]);
-        compute(st + 1, 1, wn[1], ws[1]);
+        weights_load(st + 2, wn[0]);
+        compute(st + 1, 1, wn[1]);
         stage_store(0);
         __syncthreads();
     }
-    if (st < n_st) compute(st, 0, wn[0], ws[0]);
+    if (st < n_st) compute(st, 0, wn[0]);
 
     // rows 16 RF w + 16f + 4kc + v of the workgroup, token m0 + 16t + i16
 #pragma unroll
