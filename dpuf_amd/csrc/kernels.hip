@@ -859,7 +859,9 @@ __global__ __launch_bounds__(1024) void k_mv(MvArgs A) {
 // l = row l % 16, k = 8 (l / 16) + e; B lane l = token l % 16, same k; D lane
 // l = token l % 16, rows 4 (l / 16) + v.
 // ---------------------------------------------------------------------------
+#ifndef GM_SB
 #define GM_SB 4  // blocks per LDS stage
+#endif
 #ifndef GM_RF
 #define GM_RF 1  // 16-row fragments per wave (workgroup = 64 GM_RF rows)
 #endif
@@ -955,18 +957,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
         on[f] = (uint32_t)((size_t)(ga - gw0) * gstride + (size_t)n_blk * 16 + (i16 & 7) * 16 + kc * 4);
     }
     // Weight scales go through LDS with the activations: a stage's 8 RF
-    // groups x GM_SB blocks x 8 fp16 scales are WD dwords, dword d = tid % WD
-    // (group d / (4 GM_SB), block (d / 4) % GM_SB, word d % 4), addressed
-    // from the workgroup's first group; threads past WD repeat a dword.
-    // Blocks past the end read bytes that are never used.
-    constexpr int WD = 32 * RF * GM_SB;
-    static_assert(WD <= 256, "one scale dword per thread and stage");
+    // groups x GM_SB blocks x 8 fp16 scales are WD dwords, dword d = (tid +
+    // 256 k) % WD (group d / (4 GM_SB), block (d / 4) % GM_SB, word d % 4),
+    // addressed from the workgroup's first group; threads past WD repeat a
+    // dword.  Blocks past the end read bytes that are never used.
+    constexpr int WD = 32 * RF * GM_SB, WPT = (WD + 255) / 256;
     const __amdgpu_buffer_rsrc_t rg = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(J.g + (size_t)gb * gstride), 0,
         (int)((size_t)(J.g1 - gb) * gstride < 0xFFFFFFFFu ? (size_t)(J.g1 - gb) * gstride : 0xFFFFFFFFu), GM_RSRC3);
-    const int wd = tid % WD, wg_g = wd / (4 * GM_SB), wg_b = (wd >> 2) % GM_SB, wg_w = wd & 3;
-    const uint32_t og = (uint32_t)((size_t)(min(gb + wg_g, J.g1 - 1) - gb) * gstride + wg_b * 16 + wg_w * 4);
-    uint32_t sw;  // this thread's scale dword of the stage in flight
+    uint32_t og[WPT], sw[WPT];  // load offsets; the thread's scale dwords of the stage in flight
+    int wgi[WPT];               // their LDS word index in a stage buffer
+#pragma unroll
+    for (int k = 0; k < WPT; k++) {
+        const int wd = (tid + 256 * k) % WD, g = wd / (4 * GM_SB), b = (wd >> 2) % GM_SB, w4 = wd & 3;
+        og[k] = (uint32_t)((size_t)(min(gb + g, J.g1 - 1) - gb) * gstride + b * 16 + w4 * 4);
+        wgi[k] = b * 32 * RF + g * 4 + w4;
+    }
     // staging: a stage holds NT tokens x GM_SB blocks of 64 fp16 bytes, four
     // 16-byte chunks each.  Chunk c = tid + 256 k of the stage is chunk c & 3
     // of pair c / 4 = (token (c / 4) % NT, block (c / 4) / NT), so the 64
@@ -1012,7 +1018,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
             const int b = NT == 64 ? min(st * GM_SB + wu + 4 * k, n_blk - 1) : st * GM_SB;
             ss[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, so[k], b * 4, 0));
         }
-        sw = __builtin_amdgcn_raw_buffer_load_b32(rg, og, st * GM_SB * 16, 0);
+#pragma unroll
+        for (int k = 0; k < WPT; k++) sw[k] = __builtin_amdgcn_raw_buffer_load_b32(rg, og[k], st * GM_SB * 16, 0);
     };
     auto stage_store = [&](int buf) {
 #pragma unroll
@@ -1025,7 +1032,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
             const int i = tid + 256 * k, tk = i % NT, sbt = i / NT;
             if (NT * GM_SB % 256 == 0 || i < NT * GM_SB) bs[buf][sbt][tk & 15][tk >> 4] = ss[k];
         }
-        bw[buf][wg_b][wg_g * 4 + wg_w] = sw;
+#pragma unroll
+        for (int k = 0; k < WPT; k++) (&bw[buf][0][0])[wgi[k]] = sw[k];
     };
     // nibble words of one stage, per fragment and block
     uint32_t wn[2][GM_SB][RF];
