@@ -605,11 +605,14 @@ static void enqueue_layers(Engine* e, int32_t M, int32_t keep_tiles) {
                 dpuf_hip_qk_rope_kv(s, M, e->q, e->k, e->v, e->d_norm[4 * l + 1], e->d_norm[4 * l + 2], eps,
                                     e->d_cos, e->d_sin, kc, vc, e->d_pos0, e->nq, e->nkv, e->hd, e->max_seq);
                 const int32_t lmax = e->capturing ? e->max_seq : e->host_pos0 + M;
+                /* the O-input prep rides with the prefill softmax + P.V
+                 * kernel when it can; otherwise it is a launch of its own */
+                int32_t prepped = 0;
                 if (dpuf_hip_attn_split(s, M, lmax, e->q, kc, vc, e->ao, e->scores, e->d_pos0, e->nq, e->nkv, e->hd,
-                                        e->max_seq, scale) != 0)
+                                        e->max_seq, scale, W[W_O].sign, e->prep[0], &prepped) != 0)
                     dpuf_hip_attn(s, M, e->q, kc, vc, e->ao, e->scores, e->d_pos0, e->nq, e->nkv, e->hd,
                                   e->max_seq, scale);
-                dpuf_hip_prep(s, M, e->qd, e->ao, W[W_O].sign, e->prep[0]);
+                if (!prepped) dpuf_hip_prep(s, M, e->qd, e->ao, W[W_O].sign, e->prep[0]);
             }
             tm_end(e, tm);
         }
@@ -649,9 +652,11 @@ static void enqueue_layers(Engine* e, int32_t M, int32_t keep_tiles) {
             int32_t kt = (keep_tiles > 0 && keep_tiles < nt) ? keep_tiles : nt;
             DpufGemvJob j = job(&W[W_DOWN], 0, kt, e->prep[0], e->hn, H);
             const int tm9 = tm_begin(e, K_DOWN, gemv_bytes(&W[W_DOWN], 0, kt, M));
-            dpuf_hip_gemv(s, M, 1, &j, NULL, 0.0f);
+            if (kt < nt)
+                dpuf_hip_gemv_zero(s, M, &j, kt * 16, W[W_DOWN].rows);
+            else
+                dpuf_hip_gemv(s, M, 1, &j, NULL, 0.0f);
             tm_end(e, tm9);
-            if (kt < nt) dpuf_hip_zero_rows(s, M, e->hn, H, kt * 16, W[W_DOWN].rows);
         }
         if (e->capture && M <= e->capture_cap)
             dpuf_hip_capture(s, M, H, e->h, e->hn, e->capture + (size_t)l * e->capture_cap * H);

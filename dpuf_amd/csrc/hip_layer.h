@@ -91,6 +91,9 @@ void dpuf_hip_relayout(void* s, const uint8_t* src, const uint64_t* offs, int32_
  * launch write `fill` to every row instead.  M > 1: the slab GEMM. */
 void dpuf_hip_gemv(void* s, int32_t M, int32_t n_jobs, const DpufGemvJob* jobs,
                    const int32_t* skip_flag, float fill);
+/* One GEMV job that also sets rows [r0, r1) of job->out to 0 (every token
+ * row): for M > 1 inside the GEMM launch, for M == 1 with a second launch. */
+void dpuf_hip_gemv_zero(void* s, int32_t M, const DpufGemvJob* job, int32_t r0, int32_t r1);
 /* Caps M == 1 GEMV workgroups per launch (<= 0: device capacity only). */
 void dpuf_hip_set_gemv_max_wg(int32_t n);
 void dpuf_hip_qk_rope_kv(void* s, int32_t M, float* q, float* k, const float* v,
@@ -101,10 +104,12 @@ void dpuf_hip_attn(void* s, int32_t M, const float* q, const float* kc, const fl
                    float* scores, const int32_t* pos0, int32_t n_q, int32_t n_kv, int32_t hd,
                    int32_t max_seq, float scale);
 /* Split attention (scores kernel + softmax/P.V kernel) over keys up to
- * lmax; -1 (nothing launched) when the shape does not fit. */
+ * lmax; -1 (nothing launched) when the shape does not fit.  With op.q and
+ * prepped set, a launch that can also writes the O projection's input prep
+ * (signs o_sign) in place of `out` and sets *prepped to 1. */
 int32_t dpuf_hip_attn_split(void* s, int32_t M, int32_t lmax, const float* q, const float* kc, const float* vc,
                             float* out, float* scores, const int32_t* pos0p, int32_t n_q, int32_t n_kv, int32_t hd,
-                            int32_t max_seq, float scale);
+                            int32_t max_seq, float scale, const uint8_t* o_sign, DpufPrep op, int32_t* prepped);
 /* M == 1 fused QK-norm + RoPE + KV store + attention + O-input prep.
  * Returns -1 (nothing launched) for head dims other than 64, 128, 256. */
 int32_t dpuf_hip_attn_dec(void* s, const float* q, const float* k, const float* v, const float* q_norm,

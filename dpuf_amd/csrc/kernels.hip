@@ -893,6 +893,10 @@ struct GmArgs {
     int tb[4];  // prefix sums of 16-group row tiles per job
     int K, M;
     int gy;     // token tiles
+    // rows [z0, z1) of zo (row stride zld) set to 0 by zt extra row tiles of
+    // 64 rows placed after the jobs' tiles
+    float* zo;
+    int zld, z0, z1, zt;
 };
 
 
@@ -924,7 +928,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
 #else
     const int rt = blockIdx.x, ty = blockIdx.y;
 #endif
-    if (rt >= A.tb[A.n_jobs]) return;  // padding of the grid (whole workgroup)
+    if (rt >= A.tb[A.n_jobs]) {
+        // zeroing tiles, then padding of the grid (whole workgroups)
+        const int zi = rt - A.tb[A.n_jobs];
+        if (zi < A.zt) {
+            const int r = A.z0 + 64 * zi + (threadIdx.x & 63);
+            for (int t = threadIdx.x >> 6; t < 16 * TT; t += 4) {
+                const int m = ty * 16 * TT + t;
+                if (m < A.M && r < A.z1) A.zo[(size_t)m * A.zld + r] = 0.0f;
+            }
+        }
+        return;
+    }
     int ji = 0;
     if (A.n_jobs > 1 && rt >= A.tb[1]) ji = 1;
     if (A.n_jobs > 2 && rt >= A.tb[2]) ji = 2;
@@ -1758,7 +1773,8 @@ DEV void pvt_keys4(float (&acc)[RT][4], const float4 (&p4)[RT], const float4* v)
 template <int HD, int RT>
 __global__ __launch_bounds__(8 * HD / RT) void k_attn_pvt(const float* __restrict__ S, const float* __restrict__ vc,
                                                          const int32_t* __restrict__ pos0p, int M, int n_q, int n_kv,
-                                                         int max_seq, int qt, int ldp, float* __restrict__ out) {
+                                                         int max_seq, int qt, int ldp, float* __restrict__ out,
+                                                         const uint8_t* __restrict__ o_sign, DpufPrep op) {
     constexpr int NT = 8 * HD / RT, R = PVT_R, KV = PVT_KV;  // (R / RT) row groups x (HD / 4) dim groups
     constexpr int TPR = NT / R;  // threads per row in the softmax phases
     extern __shared__ __align__(16) float P[];  // [R][ldp]
@@ -1933,12 +1949,37 @@ __global__ __launch_bounds__(8 * HD / RT) void k_attn_pvt(const float* __restric
             }
         }
     }
+    if (!op.q) {
 #pragma unroll
-    for (int k = 0; k < RT; k++) {
-        const int r = RT * ri + k;
-        if (Lr[k] > 0)
-            *(float4*)(out + ((size_t)(m0 + r / G) * n_q + kvh * G + r % G) * HD + 4 * di) =
-                make_float4(acc[k][0], acc[k][1], acc[k][2], acc[k][3]);
+        for (int k = 0; k < RT; k++) {
+            const int r = RT * ri + k;
+            if (Lr[k] > 0)
+                *(float4*)(out + ((size_t)(m0 + r / G) * n_q + kvh * G + r % G) * HD + 4 * di) =
+                    make_float4(acc[k][0], acc[k][1], acc[k][2], acc[k][3]);
+        }
+        return;
+    }
+    // The prep of the O projection's input for the tile's rows (k_prep's
+    // arithmetic): the tile goes to LDS (over P, once every thread is done
+    // with it), then quad q = (row, 64-column block of the head) takes 16
+    // columns per lane through the signs, the FWHT-64 and the quantisation.
+    constexpr int LDT = HD + 4;
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < RT; k++)
+        *(float4*)(P + (size_t)(RT * ri + k) * LDT + 4 * di) = make_float4(acc[k][0], acc[k][1], acc[k][2], acc[k][3]);
+    __syncthreads();
+    const int qd = n_q * HD, nb = qd >> 5;
+    for (int qq = tid; qq < R * HD / 16; qq += NT) {  // quads of a row never straddle the loop's steps
+        const int bi = qq >> 2, qp = qq & 3, r = bi / (HD / 64), bh = bi % (HD / 64);
+        if (r / G >= mq) continue;  // whole quads
+        float v[16];
+        load16(P + (size_t)r * LDT + 64 * bh + 16 * qp, v);
+        const int m = m0 + r / G, blk = (kvh * G + r % G) * (HD / 64) + bh;
+        apply_sign_bits(v, quad_sign_bits(o_sign, blk, qp));
+        quad_fwht64(v, qp);
+        quad_quant_store(v, qp, blk, op.q + (size_t)m * qd, op.s + (size_t)m * nb, op.m + (size_t)m * nb,
+                         op.h ? op.h + (size_t)m * qd : nullptr);
     }
 }
 
@@ -2872,6 +2913,18 @@ static void mv_launch(void* s, MvArgs& A, const int* n_groups) {
     LAUNCHED("k_mv");
 }
 
+static void gm_launch(void* s, int32_t M, int32_t n_jobs, const DpufGemvJob* jobs, float* zo, int32_t zld, int32_t z0,
+                      int32_t z1);
+
+void dpuf_hip_gemv_zero(void* s, int32_t M, const DpufGemvJob* job, int32_t r0, int32_t r1) {
+    if (M == 1) {
+        dpuf_hip_gemv(s, 1, 1, job, NULL, 0.0f);
+        if (r1 > r0) dpuf_hip_zero_rows(s, 1, job->out, job->ldo, r0, r1);
+        return;
+    }
+    gm_launch(s, M, 1, job, job->out, job->ldo, r0, r1);
+}
+
 void dpuf_hip_gemv(void* s, int32_t M, int32_t n_jobs, const DpufGemvJob* jobs, const int32_t* skip_flag,
                    float fill) {
     if (M == 1) {
@@ -2894,6 +2947,12 @@ void dpuf_hip_gemv(void* s, int32_t M, int32_t n_jobs, const DpufGemvJob* jobs, 
         mv_launch(s, A, ng);
         return;
     }
+    gm_launch(s, M, n_jobs, jobs, NULL, 0, 0, 0);
+}
+
+// The M > 1 GEMM; rows [z0, z1) of zo are zeroed by the same launch.
+static void gm_launch(void* s, int32_t M, int32_t n_jobs, const DpufGemvJob* jobs, float* zo, int32_t zld, int32_t z0,
+                      int32_t z1) {
     {
         GmArgs G;
         memset(&G, 0, sizeof G);
@@ -2923,9 +2982,16 @@ void dpuf_hip_gemv(void* s, int32_t M, int32_t n_jobs, const DpufGemvJob* jobs, 
             t += ng > 0 ? (ng + 8 * GM_RF - 1) / (8 * GM_RF) : 0;
         }
         G.tb[n_jobs] = t;
-        if (t <= 0) return;
+        if (zo && z1 > z0) {
+            G.zo = zo;
+            G.zld = zld;
+            G.z0 = z0;
+            G.z1 = z1;
+            G.zt = (z1 - z0 + 63) / 64;
+        }
+        if (t + G.zt <= 0) return;
         // a multiple of 8 row tiles keeps a row tile's token tiles on one XCD
-        const int gx = (t + 7) & ~7;
+        const int gx = (t + G.zt + 7) & ~7;
         G.gy = (M + 16 * GM_TT - 1) / (16 * GM_TT);
         const dim3 grid = GM_XCD ? dim3(gx * G.gy) : dim3(gx, G.gy);
         if (GM_RF == 2)
@@ -2961,7 +3027,8 @@ void dpuf_hip_qk_rope_kv(void* s, int32_t M, float* q, float* k, const float* v,
 // dim not 64/128/256, or a tile's probabilities not fitting in LDS).
 int32_t dpuf_hip_attn_split(void* s, int32_t M, int32_t lmax, const float* q, const float* kc, const float* vc,
                             float* out, float* scores, const int32_t* pos0p, int32_t n_q, int32_t n_kv, int32_t hd,
-                            int32_t max_seq, float scale) {
+                            int32_t max_seq, float scale, const uint8_t* o_sign, DpufPrep op, int32_t* prepped) {
+    if (prepped) *prepped = 0;
     if (n_kv <= 0 || n_q % n_kv || n_q / n_kv > 32 || (hd != 64 && hd != 128 && hd != 256)) return -1;
     if (lmax > max_seq) lmax = max_seq;
     const int G = n_q / n_kv;
@@ -2986,21 +3053,25 @@ int32_t dpuf_hip_attn_split(void* s, int32_t M, int32_t lmax, const float* q, co
         if (ldst <= 150 * 1024) {
             const int qt = 32 / G;
             const dim3 gt(n_kv, (M + qt - 1) / qt);
+            // the O input prep rides along when asked for (op.q set)
+            DpufPrep fop = op;
+            if (!prepped) fop.q = NULL;
+            if (fop.q) *prepped = 1;
             if (hd == 64) {
                 hipLaunchKernelGGL(k_attn_sc<64>, g1, dim3(256), lds1, ST(s), q, kc, pos0p, M, n_q, n_kv, max_seq,
                                    scale, qt1, scores);
                 hipLaunchKernelGGL((k_attn_pvt<64, PVT_RT>), gt, dim3(8 * 64 / PVT_RT), ldst, ST(s), scores, vc,
-                                   pos0p, M, n_q, n_kv, max_seq, qt, ldp, out);
+                                   pos0p, M, n_q, n_kv, max_seq, qt, ldp, out, o_sign, fop);
             } else if (hd == 128) {
                 hipLaunchKernelGGL(k_attn_sc<128>, g1, dim3(256), lds1, ST(s), q, kc, pos0p, M, n_q, n_kv, max_seq,
                                    scale, qt1, scores);
                 hipLaunchKernelGGL((k_attn_pvt<128, PVT_RT>), gt, dim3(8 * 128 / PVT_RT), ldst, ST(s), scores, vc,
-                                   pos0p, M, n_q, n_kv, max_seq, qt, ldp, out);
+                                   pos0p, M, n_q, n_kv, max_seq, qt, ldp, out, o_sign, fop);
             } else {
                 hipLaunchKernelGGL(k_attn_sc<256>, g1, dim3(256), lds1, ST(s), q, kc, pos0p, M, n_q, n_kv, max_seq,
                                    scale, qt1, scores);
                 hipLaunchKernelGGL((k_attn_pvt<256, PVT_RT>), gt, dim3(8 * 256 / PVT_RT), ldst, ST(s), scores, vc,
-                                   pos0p, M, n_q, n_kv, max_seq, qt, ldp, out);
+                                   pos0p, M, n_q, n_kv, max_seq, qt, ldp, out, o_sign, fop);
             }
             LAUNCHED("k_attn_split_tiled");
             return 0;

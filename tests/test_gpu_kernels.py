@@ -49,6 +49,24 @@ def test_matmul_f32_bit_exact(eng, orc, rows, cols, m):
     assert _same_bits(out_g, out_o), f"max abs diff {np.nanmax(np.abs(out_g - out_o))}"
 
 
+@pytest.mark.parametrize("rows,cols,m", [(200, 320, 65), (200, 320, 130), (1000, 1024, 130), (72, 64, 200)])
+def test_matmul_token_tiles_bit_exact(eng, orc, rows, cols, m):
+    """M > 64: several 64-token tiles of the slab GEMM (the last one ragged),
+    partial 64-row tiles, and 10-block rows (a partial last LDS stage)."""
+    blob, d = _mat(rows, cols, 31 + rows)
+    x = _x(m, cols, 3 * rows + cols)
+    x[m - 1, 32:64] = 1e-6  # a zero-scale block in the last tile
+    out_g = np.full((m, rows), np.nan, np.float32)
+    out_o = np.full((m, rows), np.nan, np.float32)
+    print(f"matmul_f32 rows={rows} cols={cols} M={m}", flush=True)
+    eng.dpuf_matmul_qr_hadamard4_packed_f32(m, rows, cols, d.n_tiles, M.ptr(x), d.tensor_base, d.tile_offsets,
+                                            d.sign_bits, M.ptr(out_g))
+    orc.orc_matmul_f32(m, rows, cols, d.n_tiles, M.ptr(x), d.tensor_base, d.tile_offsets, d.sign_bits,
+                       M.ptr(out_o))
+    assert np.isfinite(out_o).all()
+    assert _same_bits(out_g, out_o), f"max abs diff {np.nanmax(np.abs(out_g - out_o))}"
+
+
 @pytest.mark.parametrize("rows,cols", [(24, 192), (8, 320), (1000, 3072), (1024, 4096), (4096, 12288),
                                        (64, 16384)])
 @pytest.mark.parametrize("cap", [1, 2, 3, 5, 7, 0])
