@@ -3166,13 +3166,13 @@ void dpuf_hip_capture(void* s, int32_t M, int32_t H, const float* h, const float
 void dpuf_hip_topcheck(void* s, const float* logits, int32_t n, float thr, int32_t* flag, void* scratch) {
     hipLaunchKernelGGL(k_red_part, dim3(RED_NB), dim3(256), 0, ST(s), logits, n, 0, (float2*)scratch);
     hipLaunchKernelGGL(k_red_fin, dim3(1), dim3(64), 0, ST(s), (const float2*)scratch, 0, thr, flag);
-    LAUNCHED("k_topcheck");
+    LAUNCHED("k_red_part/k_red_fin (top-2 check)");
 }
 
 void dpuf_hip_argmax(void* s, const float* logits, int32_t V, int32_t* out, void* scratch) {
     hipLaunchKernelGGL(k_red_part, dim3(RED_NB), dim3(256), 0, ST(s), logits, V, 1, (float2*)scratch);
     hipLaunchKernelGGL(k_red_fin, dim3(1), dim3(64), 0, ST(s), (const float2*)scratch, 1, 0.0f, out);
-    LAUNCHED("k_argmax");
+    LAUNCHED("k_red_part/k_red_fin (argmax)");
 }
 
 void dpuf_hip_fwht_sign(void* s, int32_t M, int32_t K, const float* x, const uint8_t* sign, float* out) {
