@@ -1737,7 +1737,9 @@ __global__ __launch_bounds__(AP_NT) void k_attn_pv(const float* __restrict__ S, 
 // at consecutive positions) leave that row's chains untouched.  G even (no
 // single trailing head), HD in {64, 128, 256}.
 // ---------------------------------------------------------------------------
-#define PVT_R 32  // score rows per workgroup
+#ifndef PVT_R
+#define PVT_R 32  // score rows per workgroup (a multiple of 8 PVT_RT)
+#endif
 #ifndef PVT_RT
 #define PVT_RT 4  // rows per thread in P.V (workgroup of 8 HD / PVT_RT threads)
 #endif
@@ -1771,11 +1773,12 @@ DEV void pvt_keys4(float (&acc)[RT][4], const float4 (&p4)[RT], const float4* v)
 }
 
 template <int HD, int RT>
-__global__ __launch_bounds__(8 * HD / RT) void k_attn_pvt(const float* __restrict__ S, const float* __restrict__ vc,
+__global__ __launch_bounds__(PVT_R * HD / (4 * RT)) void k_attn_pvt(const float* __restrict__ S, const float* __restrict__ vc,
                                                          const int32_t* __restrict__ pos0p, int M, int n_q, int n_kv,
                                                          int max_seq, int qt, int ldp, float* __restrict__ out,
                                                          const uint8_t* __restrict__ o_sign, DpufPrep op) {
-    constexpr int NT = 8 * HD / RT, R = PVT_R, KV = PVT_KV;  // (R / RT) row groups x (HD / 4) dim groups
+    constexpr int R = PVT_R, NT = R * HD / (4 * RT), KV = PVT_KV;  // (R / RT) row groups x (HD / 4) dim groups
+    static_assert(R % (8 * RT) == 0 || R == 8 * RT, "whole row bands of 8 row groups");
     constexpr int TPR = NT / R;  // threads per row in the softmax phases
     extern __shared__ __align__(16) float P[];  // [R][ldp]
     __shared__ float part[8 * R];
@@ -3047,11 +3050,11 @@ int32_t dpuf_hip_attn_split(void* s, int32_t M, int32_t lmax, const float* q, co
     if ((size_t)qt2 * G * lcap * 4 > budget) return -1;
     const int R = qt2 * G;
     // prefill with an even group: the register-tiled softmax + P.V kernel
-    if (M > 1 && (G & 1) == 0 && 32 % G == 0) {
+    if (M > 1 && (G & 1) == 0 && PVT_R % G == 0) {
         const int ldp = 256 * ((lmax + 255) / 256) + 4;
         const size_t ldst = (size_t)PVT_R * ldp * 4;
         if (ldst <= 150 * 1024) {
-            const int qt = 32 / G;
+            const int qt = PVT_R / G;
             const dim3 gt(n_kv, (M + qt - 1) / qt);
             // the O input prep rides along when asked for (op.q set)
             DpufPrep fop = op;
@@ -3060,17 +3063,17 @@ int32_t dpuf_hip_attn_split(void* s, int32_t M, int32_t lmax, const float* q, co
             if (hd == 64) {
                 hipLaunchKernelGGL(k_attn_sc<64>, g1, dim3(256), lds1, ST(s), q, kc, pos0p, M, n_q, n_kv, max_seq,
                                    scale, qt1, scores);
-                hipLaunchKernelGGL((k_attn_pvt<64, PVT_RT>), gt, dim3(8 * 64 / PVT_RT), ldst, ST(s), scores, vc,
+                hipLaunchKernelGGL((k_attn_pvt<64, PVT_RT>), gt, dim3(PVT_R * 64 / (4 * PVT_RT)), ldst, ST(s), scores, vc,
                                    pos0p, M, n_q, n_kv, max_seq, qt, ldp, out, o_sign, fop);
             } else if (hd == 128) {
                 hipLaunchKernelGGL(k_attn_sc<128>, g1, dim3(256), lds1, ST(s), q, kc, pos0p, M, n_q, n_kv, max_seq,
                                    scale, qt1, scores);
-                hipLaunchKernelGGL((k_attn_pvt<128, PVT_RT>), gt, dim3(8 * 128 / PVT_RT), ldst, ST(s), scores, vc,
+                hipLaunchKernelGGL((k_attn_pvt<128, PVT_RT>), gt, dim3(PVT_R * 128 / (4 * PVT_RT)), ldst, ST(s), scores, vc,
                                    pos0p, M, n_q, n_kv, max_seq, qt, ldp, out, o_sign, fop);
             } else {
                 hipLaunchKernelGGL(k_attn_sc<256>, g1, dim3(256), lds1, ST(s), q, kc, pos0p, M, n_q, n_kv, max_seq,
                                    scale, qt1, scores);
-                hipLaunchKernelGGL((k_attn_pvt<256, PVT_RT>), gt, dim3(8 * 256 / PVT_RT), ldst, ST(s), scores, vc,
+                hipLaunchKernelGGL((k_attn_pvt<256, PVT_RT>), gt, dim3(PVT_R * 256 / (4 * PVT_RT)), ldst, ST(s), scores, vc,
                                    pos0p, M, n_q, n_kv, max_seq, qt, ldp, out, o_sign, fop);
             }
             LAUNCHED("k_attn_split_tiled");
