@@ -8,8 +8,13 @@
  * them while binding tensors, before dpuf_engine_create), not to the token
  * loop.  Body sizes per mode follow the tile layouts of dpuf_format.py:940-963.
  */
+#include <stdlib.h>
 #include <string.h>
 #include "../../include/dpuf_kernels.h"
+#ifdef DPUF_WITH_HIP  /* the build inside libdpuf_amd.so (libdpuf_tools.so has no GPU code) */
+#include "../../include/dpuf_amd.h"
+#include "hip_layer.h"
+#endif
 
 static uint32_t g_tab[256];
 static volatile int g_ready = 0;
@@ -77,3 +82,64 @@ DPUF_EXPORT int32_t dpuf_qr_verify_tiles(int32_t n_tiles, int32_t cols, const ui
                                          const uint64_t* tile_offsets, uint8_t* tile_ok_out) {
     return dpuf_qr_verify_tiles_ex(DPUF_MODE_QR_ZD4, n_tiles, cols, tensor_base, tile_offsets, tile_ok_out);
 }
+
+#ifdef DPUF_WITH_HIP
+/* The same check on the GPU: the host reads each tile header for its body
+ * range and stored CRC, the tile region goes to HBM in one copy and one
+ * workgroup per tile computes the CRC (dpuf_hip_crc_tiles). */
+static void* g_crc_stream = NULL;
+
+DPUF_EXPORT int32_t dpuf_amd_verify_tiles_device(int32_t mode, int32_t n_tiles, int32_t cols,
+                                                 const uint8_t* tensor_base, const uint64_t* tile_offsets,
+                                                 uint8_t* tile_ok_out) {
+    if (n_tiles <= 0) return 0;
+    if (!tensor_base || !tile_offsets || !tile_ok_out || cols <= 0 || dpuf_hip_device_count() <= 0) return -1;
+    if (!g_crc_stream) g_crc_stream = dpuf_hip_stream_create();
+    void* s = g_crc_stream;
+    if (!s) return -1;
+    uint64_t* off = (uint64_t*)malloc((size_t)n_tiles * 8);
+    uint32_t* len = (uint32_t*)malloc((size_t)n_tiles * 4);
+    uint32_t* want = (uint32_t*)malloc((size_t)n_tiles * 4);
+    int32_t rc = -1;
+    uint8_t *d_base = NULL, *d_ok = NULL;
+    uint64_t *d_off = NULL;
+    uint32_t *d_len = NULL, *d_want = NULL;
+    if (off && len && want) {
+        uint64_t end = 0;
+        for (int32_t t = 0; t < n_tiles; t++) {
+            DpufQrTileHdr th;
+            memcpy(&th, tensor_base + tile_offsets[t], sizeof th);
+            off[t] = tile_offsets[t] + sizeof(DpufQrTileHdr);
+            len[t] = body_bytes(mode, &th, cols);
+            want[t] = th.tile_crc32;
+            if (off[t] + len[t] > end) end = off[t] + len[t];
+        }
+        d_base = (uint8_t*)dpuf_hip_malloc((size_t)end);
+        d_off = (uint64_t*)dpuf_hip_malloc((size_t)n_tiles * 8);
+        d_len = (uint32_t*)dpuf_hip_malloc((size_t)n_tiles * 4);
+        d_want = (uint32_t*)dpuf_hip_malloc((size_t)n_tiles * 4);
+        d_ok = (uint8_t*)dpuf_hip_malloc((size_t)n_tiles);
+        if (d_base && d_off && d_len && d_want && d_ok) {
+            dpuf_hip_h2d(d_base, tensor_base, (size_t)end, s);
+            dpuf_hip_h2d(d_off, off, (size_t)n_tiles * 8, s);
+            dpuf_hip_h2d(d_len, len, (size_t)n_tiles * 4, s);
+            dpuf_hip_h2d(d_want, want, (size_t)n_tiles * 4, s);
+            dpuf_hip_crc_tiles(s, d_base, d_off, d_len, d_want, d_ok, n_tiles);
+            dpuf_hip_d2h(tile_ok_out, d_ok, (size_t)n_tiles, s);
+            if (dpuf_hip_sync(s) == 0) {
+                rc = 0;
+                for (int32_t t = 0; t < n_tiles; t++) rc += tile_ok_out[t] ? 0 : 1;
+            }
+        }
+    }
+    dpuf_hip_free(d_base);
+    dpuf_hip_free(d_off);
+    dpuf_hip_free(d_len);
+    dpuf_hip_free(d_want);
+    dpuf_hip_free(d_ok);
+    free(off);
+    free(len);
+    free(want);
+    return rc;
+}
+#endif

@@ -117,6 +117,9 @@ int32_t dpuf_hip_attn_dec(void* s, const float* q, const float* k, const float* 
                           float* vc, const int32_t* pos0, int32_t n_q, int32_t n_kv, int32_t hd, int32_t max_seq,
                           float scale, float* scores, float* ao, const uint8_t* o_sign, DpufPrep op);
 void dpuf_hip_zero_rows(void* s, int32_t M, float* out, int32_t ld, int32_t r0, int32_t r1);
+/* CRC32 of n tile bodies (base + off[t], len[t] bytes) against want[t]: ok[t] = 1 when equal. */
+void dpuf_hip_crc_tiles(void* s, const uint8_t* base, const uint64_t* off, const uint32_t* len,
+                        const uint32_t* want, uint8_t* ok, int32_t n);
 void dpuf_hip_capture(void* s, int32_t M, int32_t H, const float* h, const float* hn, float* cap);
 /* Device reductions of a logit row (two launches each); scratch holds
  * DPUF_HIP_RED_SCRATCH bytes of partials. */

@@ -2451,6 +2451,64 @@ __global__ __launch_bounds__(256) void k_attn_dec(const float* __restrict__ q, c
 // ---------------------------------------------------------------------------
 // Small utility kernels
 // ---------------------------------------------------------------------------
+// ---------------------------------------------------------------------------
+// CRC32 of tile bodies (reflected polynomial 0xEDB88320, init and final xor
+// 0xFFFFFFFF: the check of reference dpuf_avx2.c:347-398), one workgroup per
+// tile.  Thread i folds chunk i of the body with the byte table; chunk CRCs
+// combine by linearity, crc(A || B) = crc(A) * x^(8 |B|) xor crc0(B) in
+// GF(2)[x] / P (crc0: register started at 0), so each thread multiplies its
+// chunk's CRC by x^(8 * bytes after the chunk) and the results are xor-ed.
+// ---------------------------------------------------------------------------
+#define CRC_POLY 0xEDB88320u
+
+// a * b mod P for reflected CRC32 polynomials (bit 31 is x^0).
+DEV uint32_t crc_mulmod(uint32_t a, uint32_t b) {
+    uint32_t p = 0;
+    for (int i = 0; i < 32; i++) {
+        if (a & (0x80000000u >> i)) p ^= b;
+        b = (b & 1u) ? (b >> 1) ^ CRC_POLY : b >> 1;  // b * x
+    }
+    return p;
+}
+
+// x^(8 n) mod P by square-and-multiply (x^0 = 0x80000000, x^8 = 0x00800000).
+DEV uint32_t crc_xpow8(uint32_t n) {
+    uint32_t r = 0x80000000u, sq = 0x00800000u;
+    while (n) {
+        if (n & 1u) r = crc_mulmod(r, sq);
+        sq = crc_mulmod(sq, sq);
+        n >>= 1;
+    }
+    return r;
+}
+
+__global__ __launch_bounds__(256) void k_crc_tiles(const uint8_t* __restrict__ base, const uint64_t* __restrict__ off,
+                                                   const uint32_t* __restrict__ len, const uint32_t* __restrict__ want,
+                                                   uint8_t* __restrict__ ok) {
+    __shared__ uint32_t tab[256];
+    __shared__ uint32_t red[4];
+    const int tid = threadIdx.x, t = blockIdx.x;
+    {
+        uint32_t c = (uint32_t)tid;
+        for (int k = 0; k < 8; k++) c = (c & 1u) ? (CRC_POLY ^ (c >> 1)) : (c >> 1);
+        tab[tid] = c;
+    }
+    __syncthreads();
+    const uint8_t* body = base + off[t];
+    const uint32_t L = len[t], S = (L + 255u) / 256u;
+    const uint32_t b0 = min((uint32_t)tid * S, L), b1 = min(b0 + S, L);
+    uint32_t c = tid == 0 ? 0xFFFFFFFFu : 0u;
+    for (uint32_t i = b0; i < b1; i++) c = tab[(c ^ body[i]) & 0xFFu] ^ (c >> 8);
+    c = crc_mulmod(c, crc_xpow8(L - b1));
+    for (int o = 32; o > 0; o >>= 1) c ^= __shfl_xor(c, o, 64);
+    if ((tid & 63) == 0) red[tid >> 6] = c;
+    __syncthreads();
+    if (tid == 0) {
+        const uint32_t crc = (red[0] ^ red[1] ^ red[2] ^ red[3]) ^ 0xFFFFFFFFu;
+        ok[t] = crc == want[t] ? 1u : 0u;
+    }
+}
+
 __global__ void k_fill_f32(float* p, size_t n, float v) {
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) p[i] = v;
 }
@@ -3153,6 +3211,13 @@ int32_t dpuf_hip_attn_dec(void* s, const float* q, const float* k, const float* 
 #undef ATT_LAUNCH
     LAUNCHED("k_attn_dec");
     return 0;
+}
+
+void dpuf_hip_crc_tiles(void* s, const uint8_t* base, const uint64_t* off, const uint32_t* len,
+                        const uint32_t* want, uint8_t* ok, int32_t n) {
+    if (n <= 0) return;
+    hipLaunchKernelGGL(k_crc_tiles, dim3(n), dim3(256), 0, ST(s), base, off, len, want, ok);
+    LAUNCHED("k_crc_tiles");
 }
 
 void dpuf_hip_zero_rows(void* s, int32_t M, float* out, int32_t ld, int32_t r0, int32_t r1) {

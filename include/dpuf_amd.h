@@ -89,6 +89,15 @@ DPUF_EXPORT void dpuf_amd_set_gemv_max_workgroups(int32_t n);
  * (dpuf_engine.c:2101-2110).  -1 on error.  For tests. */
 DPUF_EXPORT int32_t dpuf_amd_reduce_check(const float* x, int32_t n, int32_t offset, int32_t mode, float thr);
 
+/* dpuf_qr_verify_tiles_ex (reference dpuf_avx2.c:846-908) with the CRC32 of
+ * every tile body computed on the GPU: same arguments, tile_ok_out and return
+ * value (the number of bad tiles; -1 on error).  No counterpart in the
+ * reference, which checks tiles on the CPU while binding tensors; for hosts
+ * that verify multi-GB files before dpuf_engine_create. */
+DPUF_EXPORT int32_t dpuf_amd_verify_tiles_device(int32_t mode, int32_t n_tiles, int32_t cols,
+                                                 const uint8_t* tensor_base, const uint64_t* tile_offsets,
+                                                 uint8_t* tile_ok_out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -207,3 +207,25 @@ def test_logit_reductions(eng, orc, offset):
         for thr in (1e-7, 0.05, 0.5, 3.0):
             got = eng.dpuf_amd_reduce_check(M.ptr(x), n, offset, 0, thr)
             assert got == orc.orc_top2_exit(M.ptr(x), n, thr), (n, offset, thr)
+
+
+@pytest.mark.parametrize("rows,cols", [(40, 128), (1000, 3072)])
+def test_verify_tiles_device(eng, rows, cols):
+    """The GPU tile CRC32 check against the host one (reference
+    dpuf_avx2.c:846-908): all tiles good, then one corrupted body byte at a
+    time (first, a middle and the last tile) flagged by both."""
+    blob, d = _mat(rows, cols, 41 + rows)
+    n = d.n_tiles
+    offs = np.ctypeslib.as_array(C.cast(d.tile_offsets, C.POINTER(C.c_uint64)), (n,)).copy()
+    region = blob[C.cast(d.tensor_base, C.c_void_p).value - blob.ctypes.data:].copy()
+    ok_h, ok_d = np.zeros(n, np.uint8), np.full(n, 7, np.uint8)
+    print(f"verify_tiles rows={rows} cols={cols} tiles={n}", flush=True)
+    assert eng.dpuf_qr_verify_tiles_ex(12, n, cols, M.ptr(region), M.ptr(offs), M.ptr(ok_h)) == 0
+    assert eng.dpuf_amd_verify_tiles_device(12, n, cols, M.ptr(region), M.ptr(offs), M.ptr(ok_d)) == 0
+    assert ok_h.all() and ok_d.all()
+    for t, at in ((0, 1), (n // 2, 777 % (cols // 2)), (n - 1, 5)):
+        bad = region.copy()
+        bad[int(offs[t]) + 16 + at] ^= 0x5A  # 16-byte tile header, then the body
+        nh = eng.dpuf_qr_verify_tiles_ex(12, n, cols, M.ptr(bad), M.ptr(offs), M.ptr(ok_h))
+        nd = eng.dpuf_amd_verify_tiles_device(12, n, cols, M.ptr(bad), M.ptr(offs), M.ptr(ok_d))
+        assert nh == 1 and nd == 1 and ok_d[t] == 0 and np.array_equal(ok_h, ok_d), (t, nh, nd)
