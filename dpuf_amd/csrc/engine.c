@@ -55,6 +55,12 @@ typedef struct {
     DpufPrep prep[3];
     int32_t *d_ids, *d_pos0, *d_flag, *d_tok;
     void* d_red; /* partials of the device argmax / top-2 reductions */
+    /* one token per session (dpuf_amd_engine_forward_slots): while ms_n > 0
+     * the layers run the ms_n tokens through the fused decode attention, token
+     * m at position d_ms_pos[m] with the KV cache at d_ms_kc[m] / d_ms_vc[m] */
+    int32_t ms_n;
+    int32_t *d_ms_pos, *d_ms_tok;
+    float **d_ms_kc, **d_ms_vc;
     int32_t* h_pinned;   /* host staging: [0] pos0, [1] flag, [2] token, [8..] ids */
     uint8_t* q_idx;      /* per layer: prep index of q,k,v (3 bytes) and gate/up (2 bytes) */
     float deadzone;
@@ -296,6 +302,7 @@ static void engine_free(Engine* e) {
     }
     dpuf_hip_free(e->d_ids);
     dpuf_hip_free(e->d_red);
+    dpuf_hip_free(e->d_ms_kc);
     dpuf_hip_host_free(e->h_pinned);
     for (int i = 0; i < MAX_EVENTS; i++) if (e->ev[i]) dpuf_hip_event_destroy(e->ev[i]);
     if (e->stream) dpuf_hip_stream_destroy(e->stream);
@@ -403,6 +410,11 @@ DPUF_EXPORT void* dpuf_engine_create(const DpufModelConfig* cfg, const DpufLayer
         e->d_ids = (int32_t*)dpuf_hip_malloc((B + 64) * 4);
         e->h_pinned = (int32_t*)dpuf_hip_host_alloc((B + 64) * 4);
         e->d_red = dpuf_hip_malloc(DPUF_HIP_RED_SCRATCH);
+        e->d_ms_kc = (float**)dpuf_hip_malloc(B * 2 * sizeof(float*) + B * 8);
+        if (!e->d_ms_kc) goto fail;
+        e->d_ms_vc = e->d_ms_kc + B;
+        e->d_ms_pos = (int32_t*)(e->d_ms_vc + B);
+        e->d_ms_tok = e->d_ms_pos + B;
         if (!e->h || !e->hn || !e->q || !e->k || !e->v || !e->ao || !e->gate || !e->up || !e->logits ||
             !e->scores || !e->embeds || !e->d_ids || !e->h_pinned || !e->d_red)
             goto fail;
@@ -597,10 +609,15 @@ static void enqueue_layers(Engine* e, int32_t M, int32_t keep_tiles) {
         {
             const int tm = tm_begin(e, K_ATTN, 0);
             int fused = 0;
-            if (M == 1 && e->host_pos0 + 1 <= ATT_SPLIT_MIN)
-                fused = dpuf_hip_attn_dec(s, e->q, e->k, e->v, e->d_norm[4 * l + 1], e->d_norm[4 * l + 2], eps,
+            if (e->ms_n > 0)  /* one token per session, each with its own cache */
+                fused = dpuf_hip_attn_dec(s, M, e->q, e->k, e->v, e->d_norm[4 * l + 1], e->d_norm[4 * l + 2], eps,
+                                          e->d_cos, e->d_sin, NULL, NULL, e->d_ms_pos, e->nq, e->nkv, e->hd,
+                                          e->max_seq, scale, e->scores, e->ao, W[W_O].sign, e->prep[0], e->d_ms_kc,
+                                          e->d_ms_vc, (size_t)l * e->nkv * e->max_seq * e->hd) == 0;
+            else if (M == 1 && e->host_pos0 + 1 <= ATT_SPLIT_MIN)
+                fused = dpuf_hip_attn_dec(s, 1, e->q, e->k, e->v, e->d_norm[4 * l + 1], e->d_norm[4 * l + 2], eps,
                                           e->d_cos, e->d_sin, kc, vc, e->d_pos0, e->nq, e->nkv, e->hd, e->max_seq,
-                                          scale, e->scores, e->ao, W[W_O].sign, e->prep[0]) == 0;
+                                          scale, e->scores, e->ao, W[W_O].sign, e->prep[0], NULL, NULL, 0) == 0;
             if (!fused) {
                 dpuf_hip_qk_rope_kv(s, M, e->q, e->k, e->v, e->d_norm[4 * l + 1], e->d_norm[4 * l + 2], eps,
                                     e->d_cos, e->d_sin, kc, vc, e->d_pos0, e->nq, e->nkv, e->hd, e->max_seq);
@@ -800,6 +817,56 @@ DPUF_EXPORT int32_t dpuf_engine_forward_batch(void* handle, int32_t n_tokens, co
 DPUF_EXPORT int32_t dpuf_engine_forward_token(void* handle, int32_t token_id, int32_t pos, float* logits_out) {
     int32_t t = token_id;
     return dpuf_engine_forward_batch(handle, 1, &t, pos, 1, logits_out);
+}
+
+/* One next token for each of n sessions in one pass: token_ids[i] goes into
+ * session slot_ids[i] (distinct) at positions[i], every row of every GEMM
+ * serves all n.  Per token the arithmetic is the one-token decode's, with the
+ * decode keep-tiles setting and no Zone-A early exit. */
+DPUF_EXPORT int32_t dpuf_amd_engine_forward_slots(void* handle, int32_t n, const int32_t* slot_ids,
+                                                  const int32_t* token_ids, const int32_t* positions,
+                                                  float* logits_out, int32_t* tokens_out) {
+    Engine* e = (Engine*)handle;
+    if (!e || n <= 0 || !slot_ids || !token_ids || !positions || (!logits_out && !tokens_out)) return -1;
+    if (n > DPUF_AMD_MAX_BATCH) return -2;
+    if (e->hd != 64 && e->hd != 128 && e->hd != 256) return -5;
+    for (int32_t i = 0; i < n; i++) {
+        if (slot_ids[i] < 0 || slot_ids[i] >= N_SLOTS) return -1;
+        for (int32_t j = 0; j < i; j++)
+            if (slot_ids[j] == slot_ids[i]) return -1;
+        if (positions[i] < 0 || positions[i] + 1 > e->max_seq || positions[i] + 1 > ATT_SPLIT_MIN) return -3;
+        if (token_ids[i] < 0 || token_ids[i] >= e->V) return -4;
+        if (!slot_alloc(e, slot_ids[i])) return -2;
+    }
+    float** ptrs = (float**)malloc((size_t)n * 2 * sizeof(float*));
+    if (!ptrs) return -2;
+    for (int32_t i = 0; i < n; i++) {
+        ptrs[i] = e->kc[slot_ids[i]];
+        ptrs[n + i] = e->vc[slot_ids[i]];
+    }
+    int32_t* hp = e->h_pinned;
+    for (int32_t i = 0; i < n; i++) hp[8 + i] = token_ids[i];
+    dpuf_hip_h2d(e->d_ids, hp + 8, (size_t)n * 4, e->stream);
+    dpuf_hip_h2d(e->d_ms_pos, positions, (size_t)n * 4, e->stream);
+    dpuf_hip_h2d(e->d_ms_kc, ptrs, (size_t)n * sizeof(float*), e->stream);
+    dpuf_hip_h2d(e->d_ms_vc, ptrs + n, (size_t)n * sizeof(float*), e->stream);
+    int32_t keep = 0;
+    env_int("DPUF_GEN_KEEP_TILES", &keep);
+    e->ms_n = n;
+    e->capturing = 0;
+    const int tm = tm_begin(e, K_CALL, (double)e->weight_bytes);
+    enqueue_forward(e, n, 0, 0, keep, 0, 1.25f, 0);
+    e->ms_n = 0;
+    if (tokens_out)
+        for (int32_t i = 0; i < n; i++)
+            dpuf_hip_argmax(e->stream, e->logits + (size_t)i * e->V, e->V, e->d_ms_tok + i, e->d_red);
+    tm_end(e, tm);
+    if (logits_out) dpuf_hip_d2h(logits_out, e->logits, (size_t)n * e->V * 4, e->stream);
+    if (tokens_out) dpuf_hip_d2h(tokens_out, e->d_ms_tok, (size_t)n * 4, e->stream);
+    const int32_t rc = dpuf_hip_sync(e->stream);
+    free(ptrs);
+    tm_collect(e);
+    return rc == 0 && dpuf_hip_ok() ? 0 : -6;
 }
 
 DPUF_EXPORT int32_t dpuf_amd_engine_forward_argmax(void* handle, int32_t n_tokens, const int32_t* token_ids,

@@ -2118,8 +2118,28 @@ __global__ __launch_bounds__(256) void k_attn_dec(const float* __restrict__ q, c
                                                   const int32_t* __restrict__ pos0p, int n_q, int n_kv, int max_seq,
                                                   float scale, int sc_cap, float* __restrict__ scores_g,
                                                   float* __restrict__ ao, const uint8_t* __restrict__ o_sign,
-                                                  DpufPrep op) {
+                                                  DpufPrep op, float* const* kcs, float* const* vcs, size_t l_off) {
     constexpr int V_ROWS = 16384 / HD;  // 64 KB of V rows per LDS chunk
+    // token blockIdx.z of a multi-session step: its own q/k/v rows, position
+    // and output rows, and (kcs set) its own session's KV cache
+    {
+        const int mt = blockIdx.z;
+        if (kcs) {
+            kc = kcs[mt] + l_off;
+            vc = vcs[mt] + l_off;
+        }
+        q += (size_t)mt * n_q * HD;
+        k += (size_t)mt * n_kv * HD;
+        v += (size_t)mt * n_kv * HD;
+        ao += (size_t)mt * n_q * HD;
+        scores_g += (size_t)mt * n_q * max_seq;
+        pos0p += mt;
+        const size_t qd = (size_t)n_q * HD;
+        op.q += mt * qd;
+        op.s += mt * (qd >> 5);
+        op.m += mt * (qd >> 5);
+        if (op.h) op.h += mt * qd;
+    }
     constexpr int NI = HD / 8;          // float4 steps per key and lane
     constexpr int half = HD / 2;
     extern __shared__ float sm[];
@@ -2444,7 +2464,7 @@ __global__ __launch_bounds__(256) void k_attn_dec(const float* __restrict__ q, c
         for (int kk = 0; kk < 16; kk++)
             if ((osb >> kk) & 1u) x[kk] = -x[kk];
         quad_fwht64(x, qp);
-        quad_quant_store(x, qp, blk, op.q, op.s, op.m, nullptr);
+        quad_quant_store(x, qp, blk, op.q, op.s, op.m, op.h);
     }
 }
 
@@ -3190,18 +3210,21 @@ void dpuf_hip_attn(void* s, int32_t M, const float* q, const float* kc, const fl
     LAUNCHED("k_attn");
 }
 
-int32_t dpuf_hip_attn_dec(void* s, const float* q, const float* k, const float* v, const float* q_norm,
+int32_t dpuf_hip_attn_dec(void* s, int32_t M, const float* q, const float* k, const float* v, const float* q_norm,
                           const float* k_norm, float eps, const float* cos_tab, const float* sin_tab, float* kc,
                           float* vc, const int32_t* pos0, int32_t n_q, int32_t n_kv, int32_t hd, int32_t max_seq,
-                          float scale, float* scores, float* ao, const uint8_t* o_sign, DpufPrep op) {
+                          float scale, float* scores, float* ao, const uint8_t* o_sign, DpufPrep op,
+                          float* const* kcs, float* const* vcs, size_t l_off) {
+    if (M < 1) return -1;
+    if (M == 1) op.h = NULL;  // the one-row GEMV reads q only
     const int groups = n_q / n_kv;
     const int sc_cap = max_seq < 8192 ? max_seq : 8192;
     const size_t scl = 2 * (size_t)sc_cap > 3 * (size_t)hd ? 2 * (size_t)sc_cap : 3 * (size_t)hd;
     const size_t lds = ((size_t)16384 + (size_t)6 * hd + scl) * sizeof(float);
-    const dim3 grid(n_kv, (groups + 1) / 2);
+    const dim3 grid(n_kv, (groups + 1) / 2, M);
 #define ATT_LAUNCH(HDV)                                                                                            \
     hipLaunchKernelGGL(k_attn_dec<HDV>, grid, dim3(256), lds, ST(s), q, k, v, q_norm, k_norm, eps, cos_tab, sin_tab, \
-                       kc, vc, pos0, n_q, n_kv, max_seq, scale, sc_cap, scores, ao, o_sign, op)
+                       kc, vc, pos0, n_q, n_kv, max_seq, scale, sc_cap, scores, ao, o_sign, op, kcs, vcs, l_off)
     switch (hd) {
         case 64: ATT_LAUNCH(64); break;
         case 128: ATT_LAUNCH(128); break;

@@ -89,6 +89,21 @@ DPUF_EXPORT void dpuf_amd_set_gemv_max_workgroups(int32_t n);
  * (dpuf_engine.c:2101-2110).  -1 on error.  For tests. */
 DPUF_EXPORT int32_t dpuf_amd_reduce_check(const float* x, int32_t n, int32_t offset, int32_t mode, float thr);
 
+/* One next token for each of n sessions in one pass (serving several
+ * conversations with one read of the weights): token_ids[i] is appended to
+ * KV slot slot_ids[i] (distinct slots, allocated on demand) at positions[i]
+ * (positions[i] < 192); logits_out [n][V] and/or tokens_out [n] (greedy ids).
+ * Per token the results equal a one-token dpuf_engine_forward_batch on that
+ * slot (decode keep-tiles setting, no Zone-A early exit).  0 on success; -1
+ * bad arguments or a repeated slot, -2 above DPUF_AMD_MAX_BATCH or out of
+ * memory, -3 position out of range, -4 token id out of range, -5 head dim
+ * other than 64/128/256, -6 device error.  No counterpart in the reference,
+ * whose forward serves one slot per call; for serving loops (dpuf-cli.c's
+ * one-slot-per-call generation stays as it is). */
+DPUF_EXPORT int32_t dpuf_amd_engine_forward_slots(void* handle, int32_t n, const int32_t* slot_ids,
+                                                  const int32_t* token_ids, const int32_t* positions,
+                                                  float* logits_out, int32_t* tokens_out);
+
 /* dpuf_qr_verify_tiles_ex (reference dpuf_avx2.c:846-908) with the CRC32 of
  * every tile body computed on the GPU: same arguments, tile_ok_out and return
  * value (the number of bad tiles; -1 on error).  No counterpart in the

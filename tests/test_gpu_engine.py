@@ -224,3 +224,42 @@ def test_long_context_split_attention(eng, orc, heads):
         assert out.value == orc.orc_argmax(M.ptr(lo), 4096)
         tok = out.value
     p.close()
+
+
+def test_multi_session_decode(eng, orc, tiny):
+    """Three sessions (KV slots 1, 4, 6) prefilled with prompts of different
+    lengths, then four steps of one next token each through
+    dpuf_amd_engine_forward_slots: every row's logits and greedy id equal the
+    oracle decoding that slot on its own; a repeated slot is refused."""
+    p = Pair(eng, orc, tiny)
+    V = p.V
+    slots = np.array([1, 4, 6], np.int32)
+    rng = np.random.default_rng(17)
+    toks, pos = [], []
+    for s, n in zip(slots, (5, 9, 3)):
+        assert eng.dpuf_engine_set_slot(p.g, int(s)) == 0
+        assert orc.orc_engine_set_slot(p.o, int(s)) == 0
+        lg, lo = p.forward(rng.integers(0, V, n).astype(np.int32), 0)
+        assert _bits_equal(lg, lo)
+        toks.append(int(np.argmax(lo[0])))
+        pos.append(n)
+    try:
+        for step in range(4):
+            lg = np.zeros((3, V), np.float32)
+            ids = np.full(3, -1, np.int32)
+            rc = eng.dpuf_amd_engine_forward_slots(p.g, 3, M.ptr(slots), M.ptr(np.array(toks, np.int32)),
+                                                  M.ptr(np.array(pos, np.int32)), M.ptr(lg), M.ptr(ids))
+            assert rc == 0, rc
+            for i, s in enumerate(slots):
+                assert orc.orc_engine_set_slot(p.o, int(s)) == 0
+                lo = np.zeros(V, np.float32)
+                orc.orc_engine_forward(p.o, 1, M.ptr(np.array([toks[i]], np.int32)), pos[i], None, 1, M.ptr(lo))
+                assert _bits_equal(lg[i], lo), (step, i, np.max(np.abs(lg[i] - lo)))
+                assert ids[i] == orc.orc_argmax(M.ptr(lo), V), (step, i)
+                toks[i] = int(ids[i])
+                pos[i] += 1
+        dup = np.array([1, 1], np.int32)
+        assert eng.dpuf_amd_engine_forward_slots(p.g, 2, M.ptr(dup), M.ptr(np.array(toks[:2], np.int32)),
+                                                M.ptr(np.array(pos[:2], np.int32)), None, M.ptr(ids)) == -1
+    finally:
+        p.close()
