@@ -73,6 +73,8 @@ def main():
     ap.add_argument("--prompt", type=int, default=32)
     ap.add_argument("--pp", type=int, default=512, help="prefill length of the pp measurement (0 = skip)")
     ap.add_argument("--keep-tiles", type=int, default=224, help="down-projection tiles kept in the pp run")
+    ap.add_argument("--sessions", type=int, default=8,
+                    help="sessions of the multi-session decode leg, one token each per pass (<= 1 = skip)")
     ap.add_argument("--long-ctx", type=int, default=4096,
                     help="KV-cache length of the long-context decode leg (0 = skip)")
     ap.add_argument("--long-steps", type=int, default=128, help="decode steps of the long-context leg")
@@ -243,6 +245,40 @@ def main():
         del os.environ["DPUF_PREFILL_KEEP_TILES"]
         pp = dict(tokens=args.pp, keep_tiles=args.keep_tiles, ms=best * 1e3, tok_s=args.pp / best)
         log(f"pp{args.pp}: {best * 1e3:.1f} ms, {args.pp / best:.1f} tok/s")
+
+    # --- multi-session decode: one next token for each of S sessions (KV
+    # slots 0..S-1, each prefilled with its own prompt) per pass ---------------
+    multi = None
+    if args.sessions > 1:
+        S = min(args.sessions, 8)
+        slots = np.arange(S, dtype=np.int32)
+        mtoks = np.zeros(S, np.int32)
+        mpos = np.full(S, args.prompt, np.int32)
+        for i in range(S):
+            assert eng.dpuf_engine_set_slot(h, i) == 0
+            eng.dpuf_engine_reset_cache(h)
+            pr = rng.integers(0, V, args.prompt).astype(np.int32)
+            assert eng.dpuf_engine_forward_batch(h, args.prompt, M.ptr(pr), 0, 1, M.ptr(logits)) == 0
+            mtoks[i] = int(np.argmax(logits.reshape(-1)[:V]))
+        assert eng.dpuf_engine_set_slot(h, 0) == 0
+        mids = np.zeros(S, np.int32)
+
+        def mstep():
+            rc = eng.dpuf_amd_engine_forward_slots(h, S, M.ptr(slots), M.ptr(mtoks), M.ptr(mpos), None, M.ptr(mids))
+            assert rc == 0, rc
+            mtoks[:] = mids
+            mpos[:] += 1
+
+        for _ in range(2):
+            mstep()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            mstep()
+        dt = time.perf_counter() - t0
+        multi = dict(sessions=S, steps=args.steps, ms_per_pass=round(dt / args.steps * 1e3, 4),
+                     tok_s=round(S * args.steps / dt, 1), tok_s_per_session=round(args.steps / dt, 1))
+        log(f"multi-session decode, {S} sessions: {dt / args.steps * 1e3:.3f} ms per pass, "
+            f"{S * args.steps / dt:.1f} tok/s in all ({args.steps / dt:.1f} per session)")
 
     # --- long context: decode against an injected fp32 KV cache ------------
     long = None
@@ -433,6 +469,7 @@ def main():
                    "ms_per_token_by_kind": {k: round(v["ms"] / (args.warmup + args.steps), 4)
                                             for k, v in kinds.items()}},
         "pp": pp,
+        "multi_session": multi,
         "long_context": long,
         "lm_head_early_exit": lmh,
         "roofline": rl,

@@ -13,6 +13,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include "hip_layer.h"
@@ -1171,6 +1172,348 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
                 const int r = grp * 8 + (kc & 1) * 4 + v;
                 if (r < J.rows) J.out[(size_t)m * J.ldo + r] = acc[f][t][v];
             }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// M <= 16 GEMM (one 16-token tile): the chains of k_gemm_mfma with K split
+// across the waves of a workgroup.
+//
+// With one token tile k_gemm_mfma has one wave per 16 rows, each streaming
+// all of K: a 4096-row matrix keeps only 256 waves busy.  Here a workgroup
+// computes one 16-row fragment (2 groups) for the M tokens.  SK_NP producer
+// waves take the blocks of a round (SK_RB consecutive blocks each, SK_RS per
+// round): one v_mfma_f32_16x16x32_f16 per block gives float(D - sum8) of the
+// 16 x 16 tile exactly, stored to LDS.  SK_NC = 4 chain waves run the fp32
+// chains one round behind: chain wave c owns output (token l % 16, row
+// 4 (l / 16) + c) of the MFMA D layout and applies the round's blocks in
+// ascending order, acc = fma(d, fp16(ws) * xs, acc), the same two rounded
+// operations as k_gemm_mfma, so every output is bit-identical to it.  One
+// barrier per round hands the (double-buffered) D tiles over.
+//
+// Weight nibbles (one dword per lane per block) and activations (fp16, 16
+// bytes per lane per block) are loaded SK_P - 1 rounds ahead into a register
+// ring, the round loop unrolled by SK_P so every slot index is static: both
+// in one ring because the wait counter retires loads in issue order, so
+// activations loaded later than the weights would hold every wait to the
+// newest weights.  The scales ride in the same ring: 16 lanes of each
+// producer wave load the weight-scale dwords of the wave's blocks and store
+// them transposed, [row][block], so a chain lane reads its row's scales of a
+// round with two 16-byte LDS reads, and 32 lanes the token scales,
+// [token][block]; the chains read LDS only, so no memory latency sits
+// between two barriers.
+// ---------------------------------------------------------------------------
+#define SK_NP 8   // producer waves
+#define SK_NC 4   // chain waves (one per D component)
+#define SK_RB 2   // blocks per producer wave per round
+#ifndef SK_P
+#define SK_P 6    // load ring depth in rounds (even)
+#endif
+#define SK_RS (SK_NP * SK_RB)
+static_assert(SK_RS == 16 && SK_P % 2 == 0, "chain reads assume 16 blocks per round");
+
+__global__ __launch_bounds__(64 * (SK_NP + SK_NC)) void k_gemm_sk(GmArgs A) {
+    __shared__ __align__(16) float dq[2][SK_RS][4][64];   // D tiles [buf][block][v][lane]
+    __shared__ __align__(16) uint16_t wsl[2][16][SK_RS];  // weight scales [buf][row][block]
+    __shared__ __align__(16) float xsl[2][16][SK_RS + 4];   // token scales [buf][token][block], rows padded
+    const int fr = blockIdx.x;
+    // the wave index through readfirstlane: uniform for the compiler, so the
+    // role branch and every scalar block offset stay scalar
+    const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63;
+    const int M = A.M;
+    if (fr >= A.tb[A.n_jobs]) {
+        const int zi = fr - A.tb[A.n_jobs];
+        if (zi < A.zt) {
+            const int r = A.z0 + 64 * zi + l;
+            for (int t = w; t < M; t += SK_NP + SK_NC)
+                if (r < A.z1) A.zo[(size_t)t * A.zld + r] = 0.0f;
+        }
+        return;
+    }
+    int ji = 0;
+    if (A.n_jobs > 1 && fr >= A.tb[1]) ji = 1;
+    if (A.n_jobs > 2 && fr >= A.tb[2]) ji = 2;
+    const GmJob& J = ji == 0 ? A.j[0] : ji == 1 ? A.j[1] : A.j[2];
+    const uint16_t* const Jh = ji == 0 ? A.j[0].h : ji == 1 ? A.j[1].h : A.j[2].h;
+    const float* const Js = ji == 0 ? A.j[0].s : ji == 1 ? A.j[1].s : A.j[2].s;
+    const int gf = J.g0 + 2 * (fr - A.tb[ji]);  // first group of the fragment
+    const int K = A.K, n_blk = K >> 5, n_r = (n_blk + SK_RS - 1) / SK_RS;
+    const size_t gstride = (size_t)n_blk * 144;
+    const int i16 = l & 15, kc = l >> 4;
+
+    if (w < SK_NP) {
+        // ---- producer ----
+        const size_t wbytes = (size_t)(J.g1 - gf) * gstride;
+        const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(J.g + (size_t)gf * gstride), 0, (int)(wbytes < 0xFFFFFFFFu ? wbytes : 0xFFFFFFFFu), GM_RSRC3);
+        const int ga = min(gf + (i16 >> 3), J.g1 - 1);
+        const uint32_t on = (uint32_t)((size_t)(ga - gf) * gstride + (size_t)n_blk * 16 + (i16 & 7) * 16 + kc * 4);
+        // scale dword of lane l & 15: block (l >> 3) & 1 of the wave, group
+        // (l >> 2) & 1 of the fragment, rows 2 (l & 3), 2 (l & 3) + 1.  Past
+        // the last block it reads nibble bytes of the same group (unused).
+        const int sj = (l >> 3) & 1, sg = min(gf + ((l >> 2) & 1), J.g1 - 1), sd = l & 3;
+        const uint32_t os = (uint32_t)((size_t)(sg - gf) * gstride + sj * 16 + sd * 4);
+        const __amdgpu_buffer_rsrc_t rh = __builtin_amdgcn_make_buffer_rsrc((void*)Jh, 0, M * K * 2, GM_RSRC3);
+        const uint32_t ho = (uint32_t)(2 * (min(i16, M - 1) * K + 8 * kc));
+        // token scale of lane l & 31: token l & 15, block (l >> 4) & 1 of the wave
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)Js, 0, M * n_blk * 4, GM_RSRC3);
+        const int xj = (l >> 4) & 1;
+        const int xt = min(i16, M - 1) * n_blk;
+        uint32_t wq[SK_P][SK_RB], wsq[SK_P];
+        float xsq[SK_P];
+        gm_u4 ax[SK_P][SK_RB];
+        auto wload = [&](int r, uint32_t (&q)[SK_RB], uint32_t& sq) {
+            const int b0 = r * SK_RS + w * SK_RB;
+#pragma unroll
+            for (int j = 0; j < SK_RB; j++)
+                q[j] = __builtin_amdgcn_raw_buffer_load_b32(rw, on, min(b0 + j, n_blk - 1) * 128, 0);
+            sq = __builtin_amdgcn_raw_buffer_load_b32(rw, os, min(b0, n_blk - 1) * 16, 0);
+        };
+        // the whole block index clamped per lane: the scalar offset is not
+        // range-checked, so no part of a read may point past the array
+        auto xload = [&](int r, float& x) {
+            const uint32_t xo = (uint32_t)(4 * (xt + min(r * SK_RS + w * SK_RB + xj, n_blk - 1)));
+            x = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, xo, 0, 0));
+        };
+        auto aload = [&](int r, gm_u4 (&a)[SK_RB]) {
+            const int b0 = r * SK_RS + w * SK_RB;
+#pragma unroll
+            for (int j = 0; j < SK_RB; j++)
+                a[j] = __builtin_bit_cast(gm_u4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                     rh, ho, min(b0 + j, n_blk - 1) * 64, 0));
+        };
+#pragma unroll
+        for (int u = 0; u < SK_P - 1; u++) {
+            wload(u, wq[u], wsq[u]);
+            aload(u, ax[u]);
+            xload(u, xsq[u]);
+        }
+        for (int it0 = 0; it0 <= n_r; it0 += SK_P) {
+#pragma unroll
+            for (int u = 0; u < SK_P; u++) {
+                const int it = it0 + u;
+                if (it > n_r) break;  // uniform
+                wload(it + SK_P - 1, wq[(u + SK_P - 1) % SK_P], wsq[(u + SK_P - 1) % SK_P]);
+                aload(it + SK_P - 1, ax[(u + SK_P - 1) % SK_P]);
+                xload(it + SK_P - 1, xsq[(u + SK_P - 1) % SK_P]);
+                if (it < n_r) {
+                    const int buf = u & 1;
+#pragma unroll
+                    for (int j = 0; j < SK_RB; j++) {
+                        const gm_f4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                            gm_unpack_a(wq[u][j]), __builtin_bit_cast(gm_h8, ax[u][j]),
+                            (gm_f4){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+#pragma unroll
+                        for (int v = 0; v < 4; v++) dq[buf][w * SK_RB + j][v][l] = d[v];
+                    }
+                    if (l < 16) {
+                        const int row = ((l >> 2) & 1) * 8 + 2 * sd;
+                        wsl[buf][row][w * SK_RB + sj] = (uint16_t)(wsq[u] & 0xFFFFu);
+                        wsl[buf][row + 1][w * SK_RB + sj] = (uint16_t)(wsq[u] >> 16);
+                    }
+                    if (l < 32) xsl[buf][i16][w * SK_RB + xj] = xsq[u];
+                }
+                __syncthreads();
+            }
+        }
+        return;
+    }
+
+    // ---- chain wave c: output (token l % 16, row 4 (l / 16) + c) ----
+    const int c = w - SK_NP, rr = 4 * kc + c;
+    float acc = 0.0f;
+    for (int it = 0; it <= n_r; it++) {
+        {
+            if (it >= 1) {
+                const int buf = (it + 1) & 1, b0 = (it - 1) * SK_RS;
+                float d[SK_RS];
+#pragma unroll
+                for (int j = 0; j < SK_RS; j++) d[j] = dq[buf][j][c][l];
+                const gm_u4 w0 = *(const gm_u4*)&wsl[buf][rr][0], w1 = *(const gm_u4*)&wsl[buf][rr][8];
+                gm_f4 xr[SK_RS / 4];
+#pragma unroll
+                for (int q = 0; q < SK_RS / 4; q++) xr[q] = *(const gm_f4*)&xsl[buf][i16][4 * q];
+                const uint32_t wv[8] = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
+                const int nj = min(SK_RS, n_blk - b0);  // uniform
+#pragma unroll
+                for (int j = 0; j < SK_RS; j++) {
+                    const gm_h2 hw = __builtin_bit_cast(gm_h2, wv[j >> 1]);
+                    const float wx = __builtin_fmaf((float)hw[j & 1], xr[j >> 2][j & 3], 0.0f);
+                    if (j < nj) acc = fmaf(d[j], wx, acc);
+                }
+            }
+            __syncthreads();
+        }
+    }
+    const int grp = gf + (rr >> 3);
+    const int r = grp * 8 + (rr & 7);
+    if (i16 < M && grp < J.g1 && r < J.rows) J.out[(size_t)i16 * J.ldo + r] = acc;
+}
+
+// The same for K <= 128 NR blocks (NR rounds per fragment, NR <= 8), with
+// persistent workgroups: job j gets tb[j + 1] - tb[j] workgroups, sized to
+// the chip, and workgroup lb walks the job's fragments lb, lb + nwg, ...
+// with one load ring running across fragment boundaries, so the ring fills
+// once per workgroup instead of once per fragment.  The activations and token
+// scales a producer wave needs are the same for every fragment: they are
+// loaded once, before the loop, and the ring holds only weight nibbles and
+// weight scales, SKP_P - 1 rounds (14 blocks per wave) ahead.  Rounds past
+// the matrix's last (K < 128 NR) compute nothing.
+// ---------------------------------------------------------------------------
+#ifndef SKP_P
+#define SKP_P 8  // ring depth in rounds: a multiple of every NR (8 measured faster than 16)
+#endif
+
+template <int NR>
+__global__ __launch_bounds__(64 * (SK_NP + SK_NC)) void k_gemm_skp(GmArgs A) {
+    static_assert(SKP_P % NR == 0 && NR <= 8, "ring depth must be a multiple of the rounds per fragment");
+    __shared__ __align__(16) float dq[2][SK_RS][4][64];
+    __shared__ __align__(16) uint16_t wsl[2][16][SK_RS];
+    __shared__ __align__(16) float xsl[2][16][SK_RS + 4];
+    const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63;
+    const int M = A.M, bid = blockIdx.x;
+    if (bid >= A.tb[A.n_jobs]) {
+        const int zi = bid - A.tb[A.n_jobs];
+        if (zi < A.zt) {
+            const int r = A.z0 + 64 * zi + l;
+            for (int t = w; t < M; t += SK_NP + SK_NC)
+                if (r < A.z1) A.zo[(size_t)t * A.zld + r] = 0.0f;
+        }
+        return;
+    }
+    int ji = 0;
+    if (A.n_jobs > 1 && bid >= A.tb[1]) ji = 1;
+    if (A.n_jobs > 2 && bid >= A.tb[2]) ji = 2;
+    const GmJob& J = ji == 0 ? A.j[0] : ji == 1 ? A.j[1] : A.j[2];
+    const uint16_t* const Jh = ji == 0 ? A.j[0].h : ji == 1 ? A.j[1].h : A.j[2].h;
+    const float* const Js = ji == 0 ? A.j[0].s : ji == 1 ? A.j[1].s : A.j[2].s;
+    const int lb = bid - A.tb[ji], nwg = A.tb[ji + 1] - A.tb[ji];
+    const int nf = (J.g1 - J.g0 + 1) >> 1;              // fragments of the job
+    const int n_my = (nf - lb + nwg - 1) / nwg;         // >= 1: nwg <= nf
+    const int K = A.K, n_blk = K >> 5, S = n_my * NR;   // steps: NR rounds per fragment
+    const uint32_t gstride = (uint32_t)n_blk * 144u;    // J.g1 gstride < 2^32 is checked at launch
+    const int i16 = l & 15, kc = l >> 4;
+
+    if (w < SK_NP) {
+        // ---- producer: one descriptor over the job's groups up to g1; the
+        // fragment's base goes into the scalar offset, which the range check
+        // does not cover, so the lanes of a fragment's second group add it
+        // only when it exists (a one-group fragment re-reads its first) ----
+        const __amdgpu_buffer_rsrc_t rw =
+            __builtin_amdgcn_make_buffer_rsrc((void*)J.g, 0, (int)((uint32_t)J.g1 * gstride), GM_RSRC3);
+        const uint32_t on = (uint32_t)n_blk * 16u + (i16 & 7) * 16 + kc * 4;
+        const bool on_hi = i16 >= 8;
+        const int sj = (l >> 3) & 1, sd = l & 3;
+        const uint32_t os = sj * 16 + sd * 4;
+        const bool os_hi = ((l >> 2) & 1) != 0;
+        const int xj = (l >> 4) & 1;
+        uint32_t wq[SKP_P][SK_RB], wsq[SKP_P];
+        gm_u4 ax[NR][SK_RB];
+        float xh[NR];
+        {
+            const __amdgpu_buffer_rsrc_t rh = __builtin_amdgcn_make_buffer_rsrc((void*)Jh, 0, M * K * 2, GM_RSRC3);
+            const __amdgpu_buffer_rsrc_t rs =
+                __builtin_amdgcn_make_buffer_rsrc((void*)Js, 0, M * n_blk * 4, GM_RSRC3);
+            const uint32_t ho = (uint32_t)(2 * (min(i16, M - 1) * K + 8 * kc));
+            const int xt = min(i16, M - 1) * n_blk;
+#pragma unroll
+            for (int r = 0; r < NR; r++) {
+                const int b0 = r * SK_RS + w * SK_RB;
+#pragma unroll
+                for (int j = 0; j < SK_RB; j++)
+                    ax[r][j] = __builtin_bit_cast(
+                        gm_u4, __builtin_amdgcn_raw_buffer_load_b128(rh, ho, min(b0 + j, n_blk - 1) * 64, 0));
+                const uint32_t xo = (uint32_t)(4 * (xt + min(b0 + xj, n_blk - 1)));
+                xh[r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, xo, 0, 0));
+            }
+        }
+        // loads of step s = NR fl + r: fragment lb + fl nwg, round r.  Steps
+        // past the workgroup's last fragment re-read that fragment.
+        const int fr_last = lb + (n_my - 1) * nwg;
+        auto wload = [&](int fl, int r, uint32_t (&q)[SK_RB], uint32_t& sq) {
+            const int fr = min(lb + fl * nwg, fr_last);
+            const uint32_t gb = (uint32_t)(J.g0 + 2 * fr) * gstride;
+            const uint32_t g2 = J.g0 + 2 * fr + 1 < J.g1 ? gstride : 0u;  // uniform
+            const uint32_t von = on + (on_hi ? g2 : 0u), vos = os + (os_hi ? g2 : 0u);
+            const int b0 = r * SK_RS + w * SK_RB;
+#pragma unroll
+            for (int j = 0; j < SK_RB; j++)
+                q[j] = __builtin_amdgcn_raw_buffer_load_b32(rw, von, gb + (uint32_t)min(b0 + j, n_blk - 1) * 128u, 0);
+            sq = __builtin_amdgcn_raw_buffer_load_b32(rw, vos, gb + (uint32_t)min(b0, n_blk - 1) * 16u, 0);
+        };
+#pragma unroll
+        for (int u = 0; u < SKP_P - 1; u++) wload(u / NR, u % NR, wq[u], wsq[u]);
+        for (int it0 = 0; it0 <= S; it0 += SKP_P) {
+#pragma unroll
+            for (int u = 0; u < SKP_P; u++) {
+                const int it = it0 + u;
+                if (it > S) break;  // uniform
+                const int un = (u + SKP_P - 1) % SKP_P;
+                wload((it0 + u + SKP_P - 1) / NR, un % NR, wq[un], wsq[un]);
+                const int r = u % NR;
+                if (it < S && r * SK_RS < n_blk) {
+                    const int buf = u & 1;
+#pragma unroll
+                    for (int j = 0; j < SK_RB; j++) {
+                        const gm_f4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                            gm_unpack_a(wq[u][j]), __builtin_bit_cast(gm_h8, ax[r][j]),
+                            (gm_f4){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+#pragma unroll
+                        for (int v = 0; v < 4; v++) dq[buf][w * SK_RB + j][v][l] = d[v];
+                    }
+                    if (l < 16) {
+                        const int row = ((l >> 2) & 1) * 8 + 2 * sd;
+                        wsl[buf][row][w * SK_RB + sj] = (uint16_t)(wsq[u] & 0xFFFFu);
+                        wsl[buf][row + 1][w * SK_RB + sj] = (uint16_t)(wsq[u] >> 16);
+                    }
+                    if (l < 32) xsl[buf][i16][w * SK_RB + xj] = xh[r];
+                }
+                __syncthreads();
+            }
+        }
+        return;
+    }
+
+    // ---- chain wave c: output (token l % 16, row 4 (l / 16) + c) ----
+    const int c = w - SK_NP, rr = 4 * kc + c;
+    float acc = 0.0f;
+    for (int it0 = 0; it0 <= S; it0 += SKP_P) {
+#pragma unroll
+        for (int u = 0; u < SKP_P; u++) {
+            const int it = it0 + u;
+            if (it > S) break;  // uniform
+            if (it >= 1) {
+                // step it - 1: round r of local fragment fl
+                const int um = (u + SKP_P - 1) % SKP_P, r = um % NR;
+                const int fl = (u >= 1 ? it0 : it0 - SKP_P) / NR + um / NR;
+                const int buf = (u + 1) & 1, b0 = r * SK_RS;
+                const int nj = min(SK_RS, n_blk - b0);  // uniform, <= 0 past the last round
+                if (nj > 0) {
+                    float d[SK_RS];
+#pragma unroll
+                    for (int j = 0; j < SK_RS; j++) d[j] = dq[buf][j][c][l];
+                    const gm_u4 w0 = *(const gm_u4*)&wsl[buf][rr][0], w1 = *(const gm_u4*)&wsl[buf][rr][8];
+                    gm_f4 xr[SK_RS / 4];
+#pragma unroll
+                    for (int q = 0; q < SK_RS / 4; q++) xr[q] = *(const gm_f4*)&xsl[buf][i16][4 * q];
+                    const uint32_t wv[8] = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
+#pragma unroll
+                    for (int j = 0; j < SK_RS; j++) {
+                        const gm_h2 hw = __builtin_bit_cast(gm_h2, wv[j >> 1]);
+                        const float wx = __builtin_fmaf((float)hw[j & 1], xr[j >> 2][j & 3], 0.0f);
+                        if (j < nj) acc = fmaf(d[j], wx, acc);
+                    }
+                }
+                if (r == NR - 1) {
+                    const int fr = lb + fl * nwg;
+                    const int grp = J.g0 + 2 * fr + (rr >> 3);
+                    const int row = grp * 8 + (rr & 7);
+                    if (fr < nf && i16 < M && grp < J.g1 && row < J.rows) J.out[(size_t)i16 * J.ldo + row] = acc;
+                    acc = 0.0f;
+                }
+            }
+            __syncthreads();
         }
     }
 }
@@ -2997,6 +3340,43 @@ static void mv_launch(void* s, MvArgs& A, const int* n_groups) {
 static void gm_launch(void* s, int32_t M, int32_t n_jobs, const DpufGemvJob* jobs, float* zo, int32_t zld, int32_t z0,
                       int32_t z1);
 
+typedef void (*GmKernel)(GmArgs);
+
+// Workgroups of a K-split GEMM instance the device holds at once.
+static int gm_capacity(GmKernel k, int threads) {
+    static int n_cu = 0;
+    static GmKernel c_k[4];
+    static int c_cap[4], c_n = 0;
+    for (int i = 0; i < c_n; i++)
+        if (c_k[i] == k) return c_cap[i];
+    if (n_cu == 0) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n_cu <= 0)
+            n_cu = 1;
+    }
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, threads, 0) != hipSuccess || per_cu <= 0)
+        per_cu = 1;
+    const int cap = per_cu * n_cu;
+    if (c_n < 4) {
+        c_k[c_n] = k;
+        c_cap[c_n++] = cap;
+    }
+    return cap;
+}
+
+// The M <= 16 path of the GEMM: on unless DPUF_GEMM_SKINNY=0 (which keeps
+// k_gemm_mfma for every M, for comparisons).
+static int sk_enabled(void) {
+    static int v = -1;
+    if (v < 0) {
+        const char* e = getenv("DPUF_GEMM_SKINNY");
+        v = !(e && e[0] == '0');
+    }
+    return v;
+}
+
 void dpuf_hip_gemv_zero(void* s, int32_t M, const DpufGemvJob* job, int32_t r0, int32_t r1) {
     if (M == 1) {
         dpuf_hip_gemv(s, 1, 1, job, NULL, 0.0f);
@@ -3071,6 +3451,46 @@ static void gm_launch(void* s, int32_t M, int32_t n_jobs, const DpufGemvJob* job
             G.zt = (z1 - z0 + 63) / 64;
         }
         if (t + G.zt <= 0) return;
+        const int n_blk = G.K >> 5;
+        long long gmax = 0;
+        for (int i = 0; i < n_jobs; i++) gmax = gmax > jobs[i].g1 ? gmax : jobs[i].g1;
+        if (M <= 16 && sk_enabled() && n_blk <= 128 && gmax * n_blk * 144 < 0xFFFFFFFFll) {
+            // one 16-token tile, K <= 4096: persistent K-split workgroups,
+            // each job's share of the chip in proportion to its fragments
+            const int NR = n_blk <= 32 ? 2 : n_blk <= 64 ? 4 : 8;
+            GmKernel k = NR == 2 ? k_gemm_skp<2> : NR == 4 ? k_gemm_skp<4> : k_gemm_skp<8>;
+            const int cap = gm_capacity(k, 64 * (SK_NP + SK_NC));
+            int nfr[3], ftot = 0;
+            for (int i = 0; i < n_jobs; i++) {
+                const int ng = jobs[i].g1 - jobs[i].g0;
+                nfr[i] = ng > 0 ? (ng + 1) / 2 : 0;
+                ftot += nfr[i];
+            }
+            int wgs = 0;
+            for (int i = 0; i < n_jobs; i++) {
+                G.tb[i] = wgs;
+                int nw = ftot > 0 ? (int)(((long long)cap * nfr[i] + ftot - 1) / ftot) : 0;
+                nw = nw < 1 ? 1 : nw;
+                wgs += nfr[i] > 0 ? (nw < nfr[i] ? nw : nfr[i]) : 0;
+            }
+            G.tb[n_jobs] = wgs;
+            hipLaunchKernelGGL(k, dim3(wgs + G.zt), dim3(64 * (SK_NP + SK_NC)), 0, ST(s), G);
+            LAUNCHED("k_gemm_skp");
+            return;
+        }
+        if (M <= 16 && sk_enabled()) {
+            // one 16-token tile: the K-split kernel, one workgroup per 16 rows
+            int f = 0;
+            for (int i = 0; i < n_jobs; i++) {
+                G.tb[i] = f;
+                const int ng = jobs[i].g1 - jobs[i].g0;
+                f += ng > 0 ? (ng + 1) / 2 : 0;
+            }
+            G.tb[n_jobs] = f;
+            hipLaunchKernelGGL(k_gemm_sk, dim3(f + G.zt), dim3(64 * (SK_NP + SK_NC)), 0, ST(s), G);
+            LAUNCHED("k_gemm_sk");
+            return;
+        }
         // a multiple of 8 row tiles keeps a row tile's token tiles on one XCD
         const int gx = (t + G.zt + 7) & ~7;
         G.gy = (M + 16 * GM_TT - 1) / (16 * GM_TT);

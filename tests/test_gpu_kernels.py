@@ -67,6 +67,26 @@ def test_matmul_token_tiles_bit_exact(eng, orc, rows, cols, m):
     assert _same_bits(out_g, out_o), f"max abs diff {np.nanmax(np.abs(out_g - out_o))}"
 
 
+@pytest.mark.parametrize("rows,cols,m", [(72, 320, 2), (136, 64, 16), (200, 1088, 16), (1000, 3072, 9),
+                                         (4096, 12288, 8), (12288, 4096, 16), (200, 320, 17)])
+def test_matmul_skinny_bit_exact(eng, orc, rows, cols, m):
+    """M <= 16, the K-split GEMM: odd group counts (a fragment with one
+    group), block counts that are not a multiple of the 16-block round (10,
+    34), the 8B shapes; M = 17 is the slab GEMM next to it."""
+    blob, d = _mat(rows, cols, 41 + rows)
+    x = _x(m, cols, 5 * rows + cols)
+    x[m - 1, 32:64] = 1e-6  # a zero-scale block
+    out_g = np.full((m, rows), np.nan, np.float32)
+    out_o = np.full((m, rows), np.nan, np.float32)
+    print(f"matmul_f32 rows={rows} cols={cols} M={m}", flush=True)
+    eng.dpuf_matmul_qr_hadamard4_packed_f32(m, rows, cols, d.n_tiles, M.ptr(x), d.tensor_base, d.tile_offsets,
+                                            d.sign_bits, M.ptr(out_g))
+    orc.orc_matmul_f32(m, rows, cols, d.n_tiles, M.ptr(x), d.tensor_base, d.tile_offsets, d.sign_bits,
+                       M.ptr(out_o))
+    assert np.isfinite(out_o).all()
+    assert _same_bits(out_g, out_o), f"max abs diff {np.nanmax(np.abs(out_g - out_o))}"
+
+
 @pytest.mark.parametrize("rows,cols", [(24, 192), (8, 320), (1000, 3072), (1024, 4096), (4096, 12288),
                                        (64, 16384)])
 @pytest.mark.parametrize("cap", [1, 2, 3, 5, 7, 0])
