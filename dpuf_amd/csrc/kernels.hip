@@ -1351,26 +1351,51 @@ __global__ __launch_bounds__(64 * (SK_NP + SK_NC)) void k_gemm_sk(GmArgs A) {
     if (i16 < M && grp < J.g1 && r < J.rows) J.out[(size_t)i16 * J.ldo + r] = acc;
 }
 
-// The same for K <= 128 NR blocks (NR rounds per fragment, NR <= 8), with
-// persistent workgroups: job j gets tb[j + 1] - tb[j] workgroups, sized to
-// the chip, and workgroup lb walks the job's fragments lb, lb + nwg, ...
-// with one load ring running across fragment boundaries, so the ring fills
-// once per workgroup instead of once per fragment.  The activations and token
-// scales a producer wave needs are the same for every fragment: they are
-// loaded once, before the loop, and the ring holds only weight nibbles and
-// weight scales, SKP_P - 1 rounds (14 blocks per wave) ahead.  Rounds past
-// the matrix's last (K < 128 NR) compute nothing.
+// The same for K <= 32 NR blocks (NR rounds of 32 blocks per fragment, NR
+// <= 4), with persistent workgroups: job j gets tb[j + 1] - tb[j]
+// workgroups, sized to the chip, and workgroup lb walks the job's fragments
+// lb, lb + nwg, ... with one load ring running across fragment boundaries,
+// so the ring fills once per workgroup instead of once per fragment.  The
+// activations and token scales a producer wave needs are the same for every
+// fragment: they are loaded once, before the loop, and the ring holds only
+// weight nibbles and weight scales, SKP_P - 1 rounds ahead.  Rounds past the
+// matrix's last (K < 1024 NR) compute nothing.
+//
+// A producer wave takes 4 consecutive blocks per round with one 16-byte load
+// per lane: lane (row i, kc) reads row i's 16 bytes of block b0 + kc, 1 KB
+// per load instruction (four times the bytes of a dword per lane, for the
+// same number of load instructions in flight).  A 4 x 4 transpose across the
+// four 16-lane rows of the wave (v_permlane32_swap, then v_permlane16_swap)
+// turns that into the MFMA A layout: word kc of each of the 4 blocks in lane
+// (i, kc).
 // ---------------------------------------------------------------------------
 #ifndef SKP_P
-#define SKP_P 8  // ring depth in rounds: a multiple of every NR (8 measured faster than 16)
+#define SKP_P 8  // ring depth in rounds: a multiple of every NR
 #endif
+#define SKP_RB 4                 // blocks per producer wave per round
+#define SKP_RS (SK_NP * SKP_RB)  // 32 blocks per round
+
+// 4 x 4 transpose of (16-lane row, register): afterwards register j of lane
+// row g holds what register g of lane row j held.
+DEV void skp_transpose(uint32_t& r0, uint32_t& r1, uint32_t& r2, uint32_t& r3) {
+    // rows 2, 3 of r0 <-> rows 0, 1 of r2; the same for r1, r3
+    const auto a = __builtin_amdgcn_permlane32_swap(r0, r2, false, false);
+    const auto b = __builtin_amdgcn_permlane32_swap(r1, r3, false, false);
+    // rows 1, 3 of the first <-> rows 0, 2 of the second
+    const auto c = __builtin_amdgcn_permlane16_swap(a[0], b[0], false, false);
+    const auto d = __builtin_amdgcn_permlane16_swap(a[1], b[1], false, false);
+    r0 = c[0];
+    r1 = c[1];
+    r2 = d[0];
+    r3 = d[1];
+}
 
 template <int NR>
 __global__ __launch_bounds__(64 * (SK_NP + SK_NC)) void k_gemm_skp(GmArgs A) {
-    static_assert(SKP_P % NR == 0 && NR <= 8, "ring depth must be a multiple of the rounds per fragment");
-    __shared__ __align__(16) float dq[2][SK_RS][4][64];
-    __shared__ __align__(16) uint16_t wsl[2][16][SK_RS];
-    __shared__ __align__(16) float xsl[2][16][SK_RS + 4];
+    static_assert(SKP_P % NR == 0 && NR <= 4, "ring depth must be a multiple of the rounds per fragment");
+    __shared__ __align__(16) float dq[2][SKP_RS][4][64];    // D tiles [buf][block][v][lane]
+    __shared__ __align__(16) uint16_t wsl[2][16][SKP_RS];   // weight scales [buf][row][block]
+    __shared__ __align__(16) float xsl[2][16][SKP_RS + 4];  // token scales [buf][token][block], rows padded
     const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63;
     const int M = A.M, bid = blockIdx.x;
     if (bid >= A.tb[A.n_jobs]) {
@@ -1399,18 +1424,19 @@ __global__ __launch_bounds__(64 * (SK_NP + SK_NC)) void k_gemm_skp(GmArgs A) {
         // ---- producer: one descriptor over the job's groups up to g1; the
         // fragment's base goes into the scalar offset, which the range check
         // does not cover, so the lanes of a fragment's second group add it
-        // only when it exists (a one-group fragment re-reads its first) ----
+        // only when it exists (a one-group fragment re-reads its first), and
+        // block indices are clamped per lane ----
         const __amdgpu_buffer_rsrc_t rw =
             __builtin_amdgcn_make_buffer_rsrc((void*)J.g, 0, (int)((uint32_t)J.g1 * gstride), GM_RSRC3);
-        const uint32_t on = (uint32_t)n_blk * 16u + (i16 & 7) * 16 + kc * 4;
+        const uint32_t on = (uint32_t)n_blk * 16u + (i16 & 7) * 16;
         const bool on_hi = i16 >= 8;
-        const int sj = (l >> 3) & 1, sd = l & 3;
-        const uint32_t os = sj * 16 + sd * 4;
-        const bool os_hi = ((l >> 2) & 1) != 0;
-        const int xj = (l >> 4) & 1;
-        uint32_t wq[SKP_P][SK_RB], wsq[SKP_P];
-        gm_u4 ax[NR][SK_RB];
-        float xh[NR];
+        // weight-scale dword of lane l < 32: group (l >> 4) & 1 of the
+        // fragment, block (l >> 2) & 3 of the wave, rows 2 (l & 3), 2 (l & 3) + 1
+        const int sj = (l >> 2) & 3, sd = l & 3;
+        const bool os_hi = ((l >> 4) & 1) != 0;
+        uint32_t wq[SKP_P][4], wsq[SKP_P];
+        gm_u4 ax[NR][SKP_RB];
+        float xh[NR];  // token l & 15, block l >> 4 of the wave, per round
         {
             const __amdgpu_buffer_rsrc_t rh = __builtin_amdgcn_make_buffer_rsrc((void*)Jh, 0, M * K * 2, GM_RSRC3);
             const __amdgpu_buffer_rsrc_t rs =
@@ -1419,28 +1445,31 @@ __global__ __launch_bounds__(64 * (SK_NP + SK_NC)) void k_gemm_skp(GmArgs A) {
             const int xt = min(i16, M - 1) * n_blk;
 #pragma unroll
             for (int r = 0; r < NR; r++) {
-                const int b0 = r * SK_RS + w * SK_RB;
+                const int b0 = r * SKP_RS + w * SKP_RB;
 #pragma unroll
-                for (int j = 0; j < SK_RB; j++)
+                for (int j = 0; j < SKP_RB; j++)
                     ax[r][j] = __builtin_bit_cast(
                         gm_u4, __builtin_amdgcn_raw_buffer_load_b128(rh, ho, min(b0 + j, n_blk - 1) * 64, 0));
-                const uint32_t xo = (uint32_t)(4 * (xt + min(b0 + xj, n_blk - 1)));
+                const uint32_t xo = (uint32_t)(4 * (xt + min(b0 + kc, n_blk - 1)));
                 xh[r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, xo, 0, 0));
             }
         }
         // loads of step s = NR fl + r: fragment lb + fl nwg, round r.  Steps
         // past the workgroup's last fragment re-read that fragment.
         const int fr_last = lb + (n_my - 1) * nwg;
-        auto wload = [&](int fl, int r, uint32_t (&q)[SK_RB], uint32_t& sq) {
+        auto wload = [&](int fl, int r, uint32_t (&q)[4], uint32_t& sq) {
             const int fr = min(lb + fl * nwg, fr_last);
             const uint32_t gb = (uint32_t)(J.g0 + 2 * fr) * gstride;
             const uint32_t g2 = J.g0 + 2 * fr + 1 < J.g1 ? gstride : 0u;  // uniform
-            const uint32_t von = on + (on_hi ? g2 : 0u), vos = os + (os_hi ? g2 : 0u);
-            const int b0 = r * SK_RS + w * SK_RB;
-#pragma unroll
-            for (int j = 0; j < SK_RB; j++)
-                q[j] = __builtin_amdgcn_raw_buffer_load_b32(rw, von, gb + (uint32_t)min(b0 + j, n_blk - 1) * 128u, 0);
-            sq = __builtin_amdgcn_raw_buffer_load_b32(rw, vos, gb + (uint32_t)min(b0, n_blk - 1) * 16u, 0);
+            const int b0 = r * SKP_RS + w * SKP_RB;
+            const uint32_t von = on + (on_hi ? g2 : 0u) + (uint32_t)min(b0 + kc, n_blk - 1) * 128u;
+            const gm_u4 v = __builtin_bit_cast(gm_u4, __builtin_amdgcn_raw_buffer_load_b128(rw, von, gb, 0));
+            q[0] = v[0];
+            q[1] = v[1];
+            q[2] = v[2];
+            q[3] = v[3];
+            const uint32_t vos = (os_hi ? g2 : 0u) + (uint32_t)min(b0 + sj, n_blk - 1) * 16u + sd * 4;
+            sq = __builtin_amdgcn_raw_buffer_load_b32(rw, vos, gb, 0);
         };
 #pragma unroll
         for (int u = 0; u < SKP_P - 1; u++) wload(u / NR, u % NR, wq[u], wsq[u]);
@@ -1452,22 +1481,25 @@ __global__ __launch_bounds__(64 * (SK_NP + SK_NC)) void k_gemm_skp(GmArgs A) {
                 const int un = (u + SKP_P - 1) % SKP_P;
                 wload((it0 + u + SKP_P - 1) / NR, un % NR, wq[un], wsq[un]);
                 const int r = u % NR;
-                if (it < S && r * SK_RS < n_blk) {
+                if (it < S && r * SKP_RS < n_blk) {
                     const int buf = u & 1;
+                    uint32_t t0 = wq[u][0], t1 = wq[u][1], t2 = wq[u][2], t3 = wq[u][3];
+                    skp_transpose(t0, t1, t2, t3);
+                    const uint32_t tw[4] = {t0, t1, t2, t3};
 #pragma unroll
-                    for (int j = 0; j < SK_RB; j++) {
+                    for (int j = 0; j < SKP_RB; j++) {
                         const gm_f4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                            gm_unpack_a(wq[u][j]), __builtin_bit_cast(gm_h8, ax[r][j]),
+                            gm_unpack_a(tw[j]), __builtin_bit_cast(gm_h8, ax[r][j]),
                             (gm_f4){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
 #pragma unroll
-                        for (int v = 0; v < 4; v++) dq[buf][w * SK_RB + j][v][l] = d[v];
+                        for (int v = 0; v < 4; v++) dq[buf][w * SKP_RB + j][v][l] = d[v];
                     }
-                    if (l < 16) {
-                        const int row = ((l >> 2) & 1) * 8 + 2 * sd;
-                        wsl[buf][row][w * SK_RB + sj] = (uint16_t)(wsq[u] & 0xFFFFu);
-                        wsl[buf][row + 1][w * SK_RB + sj] = (uint16_t)(wsq[u] >> 16);
+                    if (l < 32) {
+                        const int row = ((l >> 4) & 1) * 8 + 2 * sd;
+                        wsl[buf][row][w * SKP_RB + sj] = (uint16_t)(wsq[u] & 0xFFFFu);
+                        wsl[buf][row + 1][w * SKP_RB + sj] = (uint16_t)(wsq[u] >> 16);
                     }
-                    if (l < 32) xsl[buf][i16][w * SK_RB + xj] = xh[r];
+                    xsl[buf][i16][w * SKP_RB + kc] = xh[r];
                 }
                 __syncthreads();
             }
@@ -1487,19 +1519,29 @@ __global__ __launch_bounds__(64 * (SK_NP + SK_NC)) void k_gemm_skp(GmArgs A) {
                 // step it - 1: round r of local fragment fl
                 const int um = (u + SKP_P - 1) % SKP_P, r = um % NR;
                 const int fl = (u >= 1 ? it0 : it0 - SKP_P) / NR + um / NR;
-                const int buf = (u + 1) & 1, b0 = r * SK_RS;
-                const int nj = min(SK_RS, n_blk - b0);  // uniform, <= 0 past the last round
+                const int buf = (u + 1) & 1, b0 = r * SKP_RS;
+                const int nj = min(SKP_RS, n_blk - b0);  // uniform, <= 0 past the last round
                 if (nj > 0) {
-                    float d[SK_RS];
+                    float d[SKP_RS];
 #pragma unroll
-                    for (int j = 0; j < SK_RS; j++) d[j] = dq[buf][j][c][l];
-                    const gm_u4 w0 = *(const gm_u4*)&wsl[buf][rr][0], w1 = *(const gm_u4*)&wsl[buf][rr][8];
-                    gm_f4 xr[SK_RS / 4];
+                    for (int j = 0; j < SKP_RS; j++) d[j] = dq[buf][j][c][l];
+                    // the scale words as separate 32-bit values: this compiler
+                    // selected the wrong register for words 1..3 when they
+                    // went from a 4 x 32-bit vector into v_fma_mix_f32
+                    uint32_t wv[SKP_RS / 2];
 #pragma unroll
-                    for (int q = 0; q < SK_RS / 4; q++) xr[q] = *(const gm_f4*)&xsl[buf][i16][4 * q];
-                    const uint32_t wv[8] = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
+                    for (int q = 0; q < SKP_RS / 8; q++) {
+                        const gm_u4 t = *(const gm_u4*)&wsl[buf][rr][8 * q];
+                        wv[4 * q] = t[0];
+                        wv[4 * q + 1] = t[1];
+                        wv[4 * q + 2] = t[2];
+                        wv[4 * q + 3] = t[3];
+                    }
+                    gm_f4 xr[SKP_RS / 4];
 #pragma unroll
-                    for (int j = 0; j < SK_RS; j++) {
+                    for (int q = 0; q < SKP_RS / 4; q++) xr[q] = *(const gm_f4*)&xsl[buf][i16][4 * q];
+#pragma unroll
+                    for (int j = 0; j < SKP_RS; j++) {
                         const gm_h2 hw = __builtin_bit_cast(gm_h2, wv[j >> 1]);
                         const float wx = __builtin_fmaf((float)hw[j & 1], xr[j >> 2][j & 3], 0.0f);
                         if (j < nj) acc = fmaf(d[j], wx, acc);
@@ -3457,8 +3499,8 @@ static void gm_launch(void* s, int32_t M, int32_t n_jobs, const DpufGemvJob* job
         if (M <= 16 && sk_enabled() && n_blk <= 128 && gmax * n_blk * 144 < 0xFFFFFFFFll) {
             // one 16-token tile, K <= 4096: persistent K-split workgroups,
             // each job's share of the chip in proportion to its fragments
-            const int NR = n_blk <= 32 ? 2 : n_blk <= 64 ? 4 : 8;
-            GmKernel k = NR == 2 ? k_gemm_skp<2> : NR == 4 ? k_gemm_skp<4> : k_gemm_skp<8>;
+            const int NR = n_blk <= 32 ? 1 : n_blk <= 64 ? 2 : 4;
+            GmKernel k = NR == 1 ? k_gemm_skp<1> : NR == 2 ? k_gemm_skp<2> : k_gemm_skp<4>;
             const int cap = gm_capacity(k, 64 * (SK_NP + SK_NC));
             int nfr[3], ftot = 0;
             for (int i = 0; i < n_jobs; i++) {
