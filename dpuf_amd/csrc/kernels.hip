@@ -1183,40 +1183,60 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
 // With one token tile k_gemm_mfma has one wave per 16 rows, each streaming
 // all of K: a 4096-row matrix keeps only 256 waves busy.  Here a workgroup
 // computes one 16-row fragment (2 groups) for the M tokens.  SK_NP producer
-// waves take the blocks of a round (SK_RB consecutive blocks each, SK_RS per
-// round): one v_mfma_f32_16x16x32_f16 per block gives float(D - sum8) of the
-// 16 x 16 tile exactly, stored to LDS.  SK_NC = 4 chain waves run the fp32
-// chains one round behind: chain wave c owns output (token l % 16, row
+// waves take the blocks of a round (SKP_RB consecutive blocks each, SKP_RS
+// per round): one v_mfma_f32_16x16x32_f16 per block gives float(D - sum8) of
+// the 16 x 16 tile exactly, stored to LDS.  SK_NC = 4 chain waves run the
+// fp32 chains one round behind: chain wave c owns output (token l % 16, row
 // 4 (l / 16) + c) of the MFMA D layout and applies the round's blocks in
 // ascending order, acc = fma(d, fp16(ws) * xs, acc), the same two rounded
 // operations as k_gemm_mfma, so every output is bit-identical to it.  One
 // barrier per round hands the (double-buffered) D tiles over.
 //
-// Weight nibbles (one dword per lane per block) and activations (fp16, 16
-// bytes per lane per block) are loaded SK_P - 1 rounds ahead into a register
-// ring, the round loop unrolled by SK_P so every slot index is static: both
-// in one ring because the wait counter retires loads in issue order, so
-// activations loaded later than the weights would hold every wait to the
-// newest weights.  The scales ride in the same ring: 16 lanes of each
-// producer wave load the weight-scale dwords of the wave's blocks and store
-// them transposed, [row][block], so a chain lane reads its row's scales of a
-// round with two 16-byte LDS reads, and 32 lanes the token scales,
-// [token][block]; the chains read LDS only, so no memory latency sits
-// between two barriers.
+// A producer wave reads its 4 blocks with one 16-byte load per lane (lane
+// (row i, kc): row i's 16 bytes of block b0 + kc) and a 4 x 4 lane transpose
+// restores the MFMA A layout (skp_transpose).  Weights, scales and
+// activations are loaded SK_P - 1 rounds ahead into a register ring, the
+// round loop unrolled by SK_P so every slot index is static: all in one ring
+// because the wait counter retires loads in issue order, so activations
+// loaded later than the weights would hold every wait to the newest weights.
+// The scales ride in the same ring: 32 lanes of each producer wave load the
+// weight-scale dwords of the wave's blocks and store them transposed,
+// [row][block], so a chain lane reads its row's scales of a round with 16-byte
+// LDS reads, and every lane a token scale, [token][block]; the chains read
+// LDS only, so no memory latency sits between two barriers.
 // ---------------------------------------------------------------------------
 #define SK_NP 8   // producer waves
 #define SK_NC 4   // chain waves (one per D component)
-#define SK_RB 2   // blocks per producer wave per round
 #ifndef SK_P
 #define SK_P 4    // load ring depth in rounds (even; 4 measured faster than 6, 8, 10)
 #endif
-#define SK_RS (SK_NP * SK_RB)
-static_assert(SK_RS == 16 && SK_P % 2 == 0, "chain reads assume 16 blocks per round");
+static_assert(SK_P % 2 == 0, "the D buffers alternate with the round");
+
+#ifndef SKP_P
+#define SKP_P 8  // ring depth in rounds: a multiple of every NR
+#endif
+#define SKP_RB 4                 // blocks per producer wave per round
+#define SKP_RS (SK_NP * SKP_RB)  // 32 blocks per round
+
+// 4 x 4 transpose of (16-lane row, register): afterwards register j of lane
+// row g holds what register g of lane row j held.
+DEV void skp_transpose(uint32_t& r0, uint32_t& r1, uint32_t& r2, uint32_t& r3) {
+    // rows 2, 3 of r0 <-> rows 0, 1 of r2; the same for r1, r3
+    const auto a = __builtin_amdgcn_permlane32_swap(r0, r2, false, false);
+    const auto b = __builtin_amdgcn_permlane32_swap(r1, r3, false, false);
+    // rows 1, 3 of the first <-> rows 0, 2 of the second
+    const auto c = __builtin_amdgcn_permlane16_swap(a[0], b[0], false, false);
+    const auto d = __builtin_amdgcn_permlane16_swap(a[1], b[1], false, false);
+    r0 = c[0];
+    r1 = c[1];
+    r2 = d[0];
+    r3 = d[1];
+}
 
 __global__ __launch_bounds__(64 * (SK_NP + SK_NC)) void k_gemm_sk(GmArgs A) {
-    __shared__ __align__(16) float dq[2][SK_RS][4][64];   // D tiles [buf][block][v][lane]
-    __shared__ __align__(16) uint16_t wsl[2][16][SK_RS];  // weight scales [buf][row][block]
-    __shared__ __align__(16) float xsl[2][16][SK_RS + 4];   // token scales [buf][token][block], rows padded
+    __shared__ __align__(16) float dq[2][SKP_RS][4][64];    // D tiles [buf][block][v][lane]
+    __shared__ __align__(16) uint16_t wsl[2][16][SKP_RS];   // weight scales [buf][row][block]
+    __shared__ __align__(16) float xsl[2][16][SKP_RS + 4];  // token scales [buf][token][block], rows padded
     const int fr = blockIdx.x;
     // the wave index through readfirstlane: uniform for the compiler, so the
     // role branch and every scalar block offset stay scalar
@@ -1238,81 +1258,74 @@ __global__ __launch_bounds__(64 * (SK_NP + SK_NC)) void k_gemm_sk(GmArgs A) {
     const uint16_t* const Jh = ji == 0 ? A.j[0].h : ji == 1 ? A.j[1].h : A.j[2].h;
     const float* const Js = ji == 0 ? A.j[0].s : ji == 1 ? A.j[1].s : A.j[2].s;
     const int gf = J.g0 + 2 * (fr - A.tb[ji]);  // first group of the fragment
-    const int K = A.K, n_blk = K >> 5, n_r = (n_blk + SK_RS - 1) / SK_RS;
+    const int K = A.K, n_blk = K >> 5, n_r = (n_blk + SKP_RS - 1) / SKP_RS;
     const size_t gstride = (size_t)n_blk * 144;
     const int i16 = l & 15, kc = l >> 4;
 
     if (w < SK_NP) {
-        // ---- producer ----
+        // ---- producer: 4 blocks per round, one 16-byte weight load per lane
+        // (row i16, block b0 + kc) and the lane transpose, as in k_gemm_skp;
+        // groups and blocks clamped per lane ----
         const size_t wbytes = (size_t)(J.g1 - gf) * gstride;
         const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
             (void*)(J.g + (size_t)gf * gstride), 0, (int)(wbytes < 0xFFFFFFFFu ? wbytes : 0xFFFFFFFFu), GM_RSRC3);
         const int ga = min(gf + (i16 >> 3), J.g1 - 1);
-        const uint32_t on = (uint32_t)((size_t)(ga - gf) * gstride + (size_t)n_blk * 16 + (i16 & 7) * 16 + kc * 4);
-        // scale dword of lane l & 15: block (l >> 3) & 1 of the wave, group
-        // (l >> 2) & 1 of the fragment, rows 2 (l & 3), 2 (l & 3) + 1.  Past
-        // the last block it reads nibble bytes of the same group (unused).
-        const int sj = (l >> 3) & 1, sg = min(gf + ((l >> 2) & 1), J.g1 - 1), sd = l & 3;
-        const uint32_t os = (uint32_t)((size_t)(sg - gf) * gstride + sj * 16 + sd * 4);
+        const uint32_t on = (uint32_t)((size_t)(ga - gf) * gstride + (size_t)n_blk * 16 + (i16 & 7) * 16);
+        const int sj = (l >> 2) & 3, sd = l & 3, sg = min(gf + ((l >> 4) & 1), J.g1 - 1);
+        const uint32_t os = (uint32_t)((size_t)(sg - gf) * gstride + sd * 4);
         const __amdgpu_buffer_rsrc_t rh = __builtin_amdgcn_make_buffer_rsrc((void*)Jh, 0, M * K * 2, GM_RSRC3);
         const uint32_t ho = (uint32_t)(2 * (min(i16, M - 1) * K + 8 * kc));
-        // token scale of lane l & 31: token l & 15, block (l >> 4) & 1 of the wave
         const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)Js, 0, M * n_blk * 4, GM_RSRC3);
-        const int xj = (l >> 4) & 1;
         const int xt = min(i16, M - 1) * n_blk;
-        uint32_t wq[SK_P][SK_RB], wsq[SK_P];
+        uint32_t wq[SK_P][4], wsq[SK_P];
+        gm_u4 ax[SK_P][SKP_RB];
         float xsq[SK_P];
-        gm_u4 ax[SK_P][SK_RB];
-        auto wload = [&](int r, uint32_t (&q)[SK_RB], uint32_t& sq) {
-            const int b0 = r * SK_RS + w * SK_RB;
+        // weights, scales and activations of round r in one ring slot (the
+        // wait counter retires loads in issue order)
+        auto load = [&](int r, uint32_t (&q)[4], uint32_t& sq, gm_u4 (&a)[SKP_RB], float& x) {
+            const int b0 = r * SKP_RS + w * SKP_RB;
+            const gm_u4 v = __builtin_bit_cast(
+                gm_u4, __builtin_amdgcn_raw_buffer_load_b128(rw, on + (uint32_t)min(b0 + kc, n_blk - 1) * 128u, 0, 0));
+            q[0] = v[0];
+            q[1] = v[1];
+            q[2] = v[2];
+            q[3] = v[3];
+            sq = __builtin_amdgcn_raw_buffer_load_b32(rw, os + (uint32_t)min(b0 + sj, n_blk - 1) * 16u, 0, 0);
 #pragma unroll
-            for (int j = 0; j < SK_RB; j++)
-                q[j] = __builtin_amdgcn_raw_buffer_load_b32(rw, on, min(b0 + j, n_blk - 1) * 128, 0);
-            sq = __builtin_amdgcn_raw_buffer_load_b32(rw, os, min(b0, n_blk - 1) * 16, 0);
-        };
-        // the whole block index clamped per lane: the scalar offset is not
-        // range-checked, so no part of a read may point past the array
-        auto xload = [&](int r, float& x) {
-            const uint32_t xo = (uint32_t)(4 * (xt + min(r * SK_RS + w * SK_RB + xj, n_blk - 1)));
-            x = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, xo, 0, 0));
-        };
-        auto aload = [&](int r, gm_u4 (&a)[SK_RB]) {
-            const int b0 = r * SK_RS + w * SK_RB;
-#pragma unroll
-            for (int j = 0; j < SK_RB; j++)
-                a[j] = __builtin_bit_cast(gm_u4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                     rh, ho, min(b0 + j, n_blk - 1) * 64, 0));
+            for (int j = 0; j < SKP_RB; j++)
+                a[j] = __builtin_bit_cast(gm_u4,
+                                          __builtin_amdgcn_raw_buffer_load_b128(rh, ho, min(b0 + j, n_blk - 1) * 64, 0));
+            x = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                              rs, (uint32_t)(4 * (xt + min(b0 + kc, n_blk - 1))), 0, 0));
         };
 #pragma unroll
-        for (int u = 0; u < SK_P - 1; u++) {
-            wload(u, wq[u], wsq[u]);
-            aload(u, ax[u]);
-            xload(u, xsq[u]);
-        }
+        for (int u = 0; u < SK_P - 1; u++) load(u, wq[u], wsq[u], ax[u], xsq[u]);
         for (int it0 = 0; it0 <= n_r; it0 += SK_P) {
 #pragma unroll
             for (int u = 0; u < SK_P; u++) {
                 const int it = it0 + u;
                 if (it > n_r) break;  // uniform
-                wload(it + SK_P - 1, wq[(u + SK_P - 1) % SK_P], wsq[(u + SK_P - 1) % SK_P]);
-                aload(it + SK_P - 1, ax[(u + SK_P - 1) % SK_P]);
-                xload(it + SK_P - 1, xsq[(u + SK_P - 1) % SK_P]);
+                const int un = (u + SK_P - 1) % SK_P;
+                load(it + SK_P - 1, wq[un], wsq[un], ax[un], xsq[un]);
                 if (it < n_r) {
                     const int buf = u & 1;
+                    uint32_t t0 = wq[u][0], t1 = wq[u][1], t2 = wq[u][2], t3 = wq[u][3];
+                    skp_transpose(t0, t1, t2, t3);
+                    const uint32_t tw[4] = {t0, t1, t2, t3};
 #pragma unroll
-                    for (int j = 0; j < SK_RB; j++) {
+                    for (int j = 0; j < SKP_RB; j++) {
                         const gm_f4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                            gm_unpack_a(wq[u][j]), __builtin_bit_cast(gm_h8, ax[u][j]),
+                            gm_unpack_a(tw[j]), __builtin_bit_cast(gm_h8, ax[u][j]),
                             (gm_f4){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
 #pragma unroll
-                        for (int v = 0; v < 4; v++) dq[buf][w * SK_RB + j][v][l] = d[v];
+                        for (int v = 0; v < 4; v++) dq[buf][w * SKP_RB + j][v][l] = d[v];
                     }
-                    if (l < 16) {
-                        const int row = ((l >> 2) & 1) * 8 + 2 * sd;
-                        wsl[buf][row][w * SK_RB + sj] = (uint16_t)(wsq[u] & 0xFFFFu);
-                        wsl[buf][row + 1][w * SK_RB + sj] = (uint16_t)(wsq[u] >> 16);
+                    if (l < 32) {
+                        const int row = ((l >> 4) & 1) * 8 + 2 * sd;
+                        wsl[buf][row][w * SKP_RB + sj] = (uint16_t)(wsq[u] & 0xFFFFu);
+                        wsl[buf][row + 1][w * SKP_RB + sj] = (uint16_t)(wsq[u] >> 16);
                     }
-                    if (l < 32) xsl[buf][i16][w * SK_RB + xj] = xsq[u];
+                    xsl[buf][i16][w * SKP_RB + kc] = xsq[u];
                 }
                 __syncthreads();
             }
@@ -1324,27 +1337,33 @@ __global__ __launch_bounds__(64 * (SK_NP + SK_NC)) void k_gemm_sk(GmArgs A) {
     const int c = w - SK_NP, rr = 4 * kc + c;
     float acc = 0.0f;
     for (int it = 0; it <= n_r; it++) {
-        {
-            if (it >= 1) {
-                const int buf = (it + 1) & 1, b0 = (it - 1) * SK_RS;
-                float d[SK_RS];
+        if (it >= 1) {
+            const int buf = (it + 1) & 1, b0 = (it - 1) * SKP_RS;
+            const int nj = min(SKP_RS, n_blk - b0);  // uniform
+            float d[SKP_RS];
 #pragma unroll
-                for (int j = 0; j < SK_RS; j++) d[j] = dq[buf][j][c][l];
-                const gm_u4 w0 = *(const gm_u4*)&wsl[buf][rr][0], w1 = *(const gm_u4*)&wsl[buf][rr][8];
-                gm_f4 xr[SK_RS / 4];
+            for (int j = 0; j < SKP_RS; j++) d[j] = dq[buf][j][c][l];
+            // scale words as separate 32-bit values (see k_gemm_skp)
+            uint32_t wv[SKP_RS / 2];
 #pragma unroll
-                for (int q = 0; q < SK_RS / 4; q++) xr[q] = *(const gm_f4*)&xsl[buf][i16][4 * q];
-                const uint32_t wv[8] = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
-                const int nj = min(SK_RS, n_blk - b0);  // uniform
-#pragma unroll
-                for (int j = 0; j < SK_RS; j++) {
-                    const gm_h2 hw = __builtin_bit_cast(gm_h2, wv[j >> 1]);
-                    const float wx = __builtin_fmaf((float)hw[j & 1], xr[j >> 2][j & 3], 0.0f);
-                    if (j < nj) acc = fmaf(d[j], wx, acc);
-                }
+            for (int q = 0; q < SKP_RS / 8; q++) {
+                const gm_u4 t = *(const gm_u4*)&wsl[buf][rr][8 * q];
+                wv[4 * q] = t[0];
+                wv[4 * q + 1] = t[1];
+                wv[4 * q + 2] = t[2];
+                wv[4 * q + 3] = t[3];
             }
-            __syncthreads();
+            gm_f4 xr[SKP_RS / 4];
+#pragma unroll
+            for (int q = 0; q < SKP_RS / 4; q++) xr[q] = *(const gm_f4*)&xsl[buf][i16][4 * q];
+#pragma unroll
+            for (int j = 0; j < SKP_RS; j++) {
+                const gm_h2 hw = __builtin_bit_cast(gm_h2, wv[j >> 1]);
+                const float wx = __builtin_fmaf((float)hw[j & 1], xr[j >> 2][j & 3], 0.0f);
+                if (j < nj) acc = fmaf(d[j], wx, acc);
+            }
         }
+        __syncthreads();
     }
     const int grp = gf + (rr >> 3);
     const int r = grp * 8 + (rr & 7);
@@ -1369,27 +1388,6 @@ __global__ __launch_bounds__(64 * (SK_NP + SK_NC)) void k_gemm_sk(GmArgs A) {
 // turns that into the MFMA A layout: word kc of each of the 4 blocks in lane
 // (i, kc).
 // ---------------------------------------------------------------------------
-#ifndef SKP_P
-#define SKP_P 8  // ring depth in rounds: a multiple of every NR
-#endif
-#define SKP_RB 4                 // blocks per producer wave per round
-#define SKP_RS (SK_NP * SKP_RB)  // 32 blocks per round
-
-// 4 x 4 transpose of (16-lane row, register): afterwards register j of lane
-// row g holds what register g of lane row j held.
-DEV void skp_transpose(uint32_t& r0, uint32_t& r1, uint32_t& r2, uint32_t& r3) {
-    // rows 2, 3 of r0 <-> rows 0, 1 of r2; the same for r1, r3
-    const auto a = __builtin_amdgcn_permlane32_swap(r0, r2, false, false);
-    const auto b = __builtin_amdgcn_permlane32_swap(r1, r3, false, false);
-    // rows 1, 3 of the first <-> rows 0, 2 of the second
-    const auto c = __builtin_amdgcn_permlane16_swap(a[0], b[0], false, false);
-    const auto d = __builtin_amdgcn_permlane16_swap(a[1], b[1], false, false);
-    r0 = c[0];
-    r1 = c[1];
-    r2 = d[0];
-    r3 = d[1];
-}
-
 template <int NR>
 __global__ __launch_bounds__(64 * (SK_NP + SK_NC)) void k_gemm_skp(GmArgs A) {
     static_assert(SKP_P % NR == 0 && NR <= 4, "ring depth must be a multiple of the rounds per fragment");

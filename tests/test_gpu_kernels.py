@@ -68,11 +68,13 @@ def test_matmul_token_tiles_bit_exact(eng, orc, rows, cols, m):
 
 
 @pytest.mark.parametrize("rows,cols,m", [(72, 320, 2), (136, 64, 16), (200, 1088, 16), (1000, 3072, 9),
-                                         (4096, 12288, 8), (12288, 4096, 16), (200, 320, 17)])
+                                         (4096, 12288, 8), (12288, 4096, 16), (72, 4160, 5),
+                                         (200, 320, 17)])
 def test_matmul_skinny_bit_exact(eng, orc, rows, cols, m):
-    """M <= 16, the K-split GEMM: odd group counts (a fragment with one
-    group), block counts that are not a multiple of the 16-block round (10,
-    34), the 8B shapes; M = 17 is the slab GEMM next to it."""
+    """M <= 16, the K-split GEMMs: odd group counts (a fragment with one
+    group), block counts that are not a multiple of the 32-block round (10,
+    34, 130: K > 4096 with a partial last round), the 8B shapes; M = 17 is
+    the slab GEMM next to it."""
     blob, d = _mat(rows, cols, 41 + rows)
     x = _x(m, cols, 5 * rows + cols)
     x[m - 1, 32:64] = 1e-6  # a zero-scale block
