@@ -1208,7 +1208,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
 #define SK_NP 8   // producer waves
 #define SK_NC 4   // chain waves (one per D component)
 #ifndef SK_P
-#define SK_P 4    // load ring depth in rounds (even; 4 measured faster than 6, 8, 10)
+#define SK_P 4    // load ring depth in rounds (even; fastest of 4..10 in a sweep of the dword-load version)
 #endif
 static_assert(SK_P % 2 == 0, "the D buffers alternate with the round");
 
