@@ -53,7 +53,7 @@ typedef struct {
     float *h, *hn, *q, *k, *v, *ao, *gate, *up, *logits, *scores, *embeds, *capture;
     int32_t capture_cap;
     DpufPrep prep[3];
-    int32_t *d_ids, *d_pos0, *d_flag, *d_tok;
+    int32_t *d_ids, *d_pos0, *d_flag, *d_tok, *d_err;
     void* d_red; /* partials of the device argmax / top-2 reductions */
     /* one token per session (dpuf_amd_engine_forward_slots): while ms_n > 0
      * the layers run the ms_n tokens through the fused decode attention, token
@@ -61,7 +61,7 @@ typedef struct {
     int32_t ms_n;
     int32_t *d_ms_pos, *d_ms_tok;
     float **d_ms_kc, **d_ms_vc;
-    int32_t* h_pinned;   /* host staging: [0] pos0, [1] flag, [2] token, [8..] ids */
+    int32_t* h_pinned;   /* host staging: [0] pos0, [1] flag, [2] token, [3] error word, [8..] ids */
     uint8_t* q_idx;      /* per layer: prep index of q,k,v (3 bytes) and gate/up (2 bytes) */
     float deadzone;
     void* stream;
@@ -98,6 +98,25 @@ static int env_int(const char* name, int* out) {
     if (!s) return 0;
     *out = atoi(s);
     return 1;
+}
+
+/* Start of every entry point that launches work: a fresh per-call error
+ * state, and the engine's device error word for the GEMV kernels. */
+static void begin_call(Engine* e) {
+    dpuf_hip_clear_error();
+    dpuf_hip_bind_error_word(e->d_err);
+}
+
+/* After the stream has drained: 0 when neither the runtime nor a kernel
+ * (through the device error word, already copied to *word) reported a
+ * failure; else the word is cleared for the next call and -6 returned. */
+static int32_t end_call(Engine* e, int32_t word) {
+    if (word != 0) {
+        dpuf_hip_fill_zero(e->d_err, 4, e->stream);
+        dpuf_hip_sync(e->stream);
+        return -6;
+    }
+    return dpuf_hip_ok() ? 0 : -6;
 }
 
 /* Starts a timed region: reserves an event pair, records its start and
@@ -277,6 +296,7 @@ static int slot_alloc(Engine* e, int32_t s) {
 
 static void engine_free(Engine* e) {
     if (!e) return;
+    dpuf_hip_bind_error_word(NULL);
     if (e->stream) dpuf_hip_sync(e->stream);
     dpuf_hip_graph_destroy(e->graph);
     for (int32_t i = 0; i < e->n_ups; i++) {
@@ -315,10 +335,14 @@ DPUF_EXPORT const char* dpuf_amd_last_error(void) { return dpuf_hip_error_string
 DPUF_EXPORT void* dpuf_engine_create(const DpufModelConfig* cfg, const DpufLayerWeights* layers,
                                      const DpufWeightDesc* w_tok_embd, const DpufWeightDesc* w_lm_head,
                                      const float* output_norm) {
+    dpuf_hip_clear_error();
     if (!cfg || !layers || !w_tok_embd || !w_lm_head || !output_norm) return NULL;
-    if (cfg->num_layers < 0 || cfg->hidden_size <= 0 || cfg->head_dim <= 0 || (cfg->head_dim % 64) != 0 ||
-        cfg->head_dim > 256 || cfg->num_kv_heads <= 0 || cfg->num_q_heads <= 0 ||
-        (cfg->num_q_heads % cfg->num_kv_heads) != 0 || cfg->max_seq_len <= 0 || cfg->vocab_size <= 0 ||
+    /* head dims 64, 128, 256 and groups of at most 32 query heads per KV head:
+     * the shapes the attention kernels are built and tested for */
+    if (cfg->num_layers < 0 || cfg->hidden_size <= 0 ||
+        (cfg->head_dim != 64 && cfg->head_dim != 128 && cfg->head_dim != 256) || cfg->num_kv_heads <= 0 ||
+        cfg->num_q_heads <= 0 || (cfg->num_q_heads % cfg->num_kv_heads) != 0 ||
+        cfg->num_q_heads / cfg->num_kv_heads > 32 || cfg->max_seq_len <= 0 || cfg->vocab_size <= 0 ||
         cfg->kv_type != DPUF_KV_F32 || cfg->has_mrope || (cfg->hidden_size % 64) != 0 ||
         cfg->hidden_size < 128 || cfg->hidden_size > 16384 ||
         (cfg->intermediate_size % 64) != 0)
@@ -421,6 +445,7 @@ DPUF_EXPORT void* dpuf_engine_create(const DpufModelConfig* cfg, const DpufLayer
         e->d_pos0 = e->d_ids + B;
         e->d_flag = e->d_ids + B + 1;
         e->d_tok = e->d_ids + B + 2;
+        e->d_err = e->d_ids + B + 3;
         dpuf_hip_fill_zero(e->d_ids, (B + 64) * 4, e->stream);
         dpuf_hip_fill_zero(e->hn, B * e->H * 4, e->stream);
     }
@@ -435,6 +460,7 @@ fail:
 DPUF_EXPORT void dpuf_engine_destroy(void* handle) { engine_free((Engine*)handle); }
 
 DPUF_EXPORT int32_t dpuf_engine_set_slot(void* handle, int32_t slot_id) {
+    dpuf_hip_clear_error();
     Engine* e = (Engine*)handle;
     if (!e || slot_id < 0 || slot_id >= N_SLOTS) return -1;
     if (!slot_alloc(e, slot_id)) return -2;
@@ -450,6 +476,7 @@ DPUF_EXPORT int32_t dpuf_engine_get_slot(void* handle) {
 DPUF_EXPORT int32_t dpuf_engine_num_slots(void* handle) { return handle ? N_SLOTS : 1; }
 
 DPUF_EXPORT void dpuf_engine_reset_slot(void* handle, int32_t slot_id) {
+    dpuf_hip_clear_error();
     Engine* e = (Engine*)handle;
     if (!e || slot_id < 0 || slot_id >= N_SLOTS || !e->kc[slot_id]) return;
     size_t n = kv_floats(e) * sizeof(float);
@@ -472,6 +499,7 @@ DPUF_EXPORT size_t dpuf_engine_slot_memory(void* handle) {
 
 /* Prefix caches are [L][kv head][len][hd] (dpuf_engine.c:1471-1600). */
 DPUF_EXPORT int32_t dpuf_engine_freeze_prefix(void* handle, int32_t pfx_id, int32_t prefix_len) {
+    dpuf_hip_clear_error();
     Engine* e = (Engine*)handle;
     if (!e || pfx_id < 0 || pfx_id >= N_PREFIX || prefix_len <= 0 || prefix_len > e->max_seq) return 0;
     if (e->pcap[pfx_id] < prefix_len || !e->pk[pfx_id]) {
@@ -504,6 +532,7 @@ DPUF_EXPORT int32_t dpuf_engine_freeze_prefix(void* handle, int32_t pfx_id, int3
 }
 
 DPUF_EXPORT int32_t dpuf_engine_apply_prefix(void* handle, int32_t slot_id, int32_t pfx_id) {
+    dpuf_hip_clear_error();
     Engine* e = (Engine*)handle;
     if (!e || slot_id < 0 || slot_id >= N_SLOTS || pfx_id < 0 || pfx_id >= N_PREFIX) return 0;
     if (!e->pvalid[pfx_id] || e->plen[pfx_id] <= 0) return 0;
@@ -742,6 +771,7 @@ static int32_t forward_common(Engine* e, int32_t n_tokens, const int32_t* token_
         if (id >= e->V || (id < 0 && !embeds_in)) return -4;
     }
     const int32_t M = n_tokens;
+    begin_call(e);
     int32_t keep = 0, early = 0;
     env_int(M > 1 ? "DPUF_PREFILL_KEEP_TILES" : "DPUF_GEN_KEEP_TILES", &keep);
     int32_t has_early = env_int("DPUF_EARLY_TILES", &early);
@@ -786,15 +816,16 @@ static int32_t forward_common(Engine* e, int32_t n_tokens, const int32_t* token_
     if (only_last != 2) {
         const int32_t rows = only_last ? 1 : M;
         if (logits_out) dpuf_hip_d2h(logits_out, e->logits, (size_t)rows * e->V * 4, e->stream);
-        dpuf_hip_d2h(hp + 1, e->d_flag, 8, e->stream); /* flag and token */
     }
+    dpuf_hip_d2h(hp + 1, e->d_flag, 12, e->stream); /* flag, token, error word */
     if (dpuf_hip_sync(e->stream) != 0) return -6;
     tm_collect(e);
-    if (only_last != 2) {
+    const int32_t rc = end_call(e, hp[3]);
+    if (rc == 0 && only_last != 2) {
         if (hp[1]) e->early_exits++;
         if (token_out) *token_out = hp[2];
     }
-    return dpuf_hip_ok() ? 0 : -6;
+    return rc;
 }
 
 DPUF_EXPORT int32_t dpuf_engine_forward_batch_ex(void* handle, int32_t n_tokens, const int32_t* token_ids,
@@ -840,6 +871,7 @@ DPUF_EXPORT int32_t dpuf_amd_engine_forward_slots(void* handle, int32_t n, const
     }
     float** ptrs = (float**)malloc((size_t)n * 2 * sizeof(float*));
     if (!ptrs) return -2;
+    begin_call(e);
     for (int32_t i = 0; i < n; i++) {
         ptrs[i] = e->kc[slot_ids[i]];
         ptrs[n + i] = e->vc[slot_ids[i]];
@@ -863,10 +895,12 @@ DPUF_EXPORT int32_t dpuf_amd_engine_forward_slots(void* handle, int32_t n, const
     tm_end(e, tm);
     if (logits_out) dpuf_hip_d2h(logits_out, e->logits, (size_t)n * e->V * 4, e->stream);
     if (tokens_out) dpuf_hip_d2h(tokens_out, e->d_ms_tok, (size_t)n * 4, e->stream);
+    dpuf_hip_d2h(hp + 3, e->d_err, 4, e->stream);
     const int32_t rc = dpuf_hip_sync(e->stream);
     free(ptrs);
     tm_collect(e);
-    return rc == 0 && dpuf_hip_ok() ? 0 : -6;
+    if (rc != 0) return -6;
+    return end_call(e, hp[3]);
 }
 
 DPUF_EXPORT int32_t dpuf_amd_engine_forward_argmax(void* handle, int32_t n_tokens, const int32_t* token_ids,
@@ -888,6 +922,7 @@ DPUF_EXPORT int32_t dpuf_amd_engine_set_kv(void* handle, int32_t layer, int32_t 
     if (!e || layer < 0 || layer >= e->L || kvh < 0 || kvh >= e->nkv || pos0 < 0 || n < 0 || pos0 + n > e->max_seq ||
         !k || !v)
         return -1;
+    dpuf_hip_clear_error();
     size_t off = (((size_t)layer * e->nkv + kvh) * (size_t)e->max_seq + pos0) * e->hd;
     dpuf_hip_h2d(e->kc[e->active] + off, k, (size_t)n * e->hd * 4, e->stream);
     dpuf_hip_h2d(e->vc[e->active] + off, v, (size_t)n * e->hd * 4, e->stream);
@@ -900,6 +935,7 @@ DPUF_EXPORT int32_t dpuf_amd_engine_get_kv(void* handle, int32_t layer, int32_t 
     if (!e || layer < 0 || layer >= e->L || kvh < 0 || kvh >= e->nkv || pos0 < 0 || n < 0 || pos0 + n > e->max_seq ||
         !k || !v)
         return -1;
+    dpuf_hip_clear_error();
     size_t off = (((size_t)layer * e->nkv + kvh) * (size_t)e->max_seq + pos0) * e->hd;
     dpuf_hip_d2h(k, e->kc[e->active] + off, (size_t)n * e->hd * 4, e->stream);
     dpuf_hip_d2h(v, e->vc[e->active] + off, (size_t)n * e->hd * 4, e->stream);
@@ -907,6 +943,7 @@ DPUF_EXPORT int32_t dpuf_amd_engine_get_kv(void* handle, int32_t layer, int32_t 
 }
 
 DPUF_EXPORT int32_t dpuf_amd_engine_set_capture(void* handle, int32_t max_tokens) {
+    dpuf_hip_clear_error();
     Engine* e = (Engine*)handle;
     if (!e || max_tokens < 0 || max_tokens > DPUF_AMD_MAX_BATCH) return -1;
     dpuf_hip_free(e->capture);
@@ -921,6 +958,7 @@ DPUF_EXPORT int32_t dpuf_amd_engine_set_capture(void* handle, int32_t max_tokens
 }
 
 DPUF_EXPORT int32_t dpuf_amd_engine_get_capture(void* handle, float* out, size_t n_floats) {
+    dpuf_hip_clear_error();
     Engine* e = (Engine*)handle;
     if (!e || !e->capture || !out) return -1;
     size_t total = (size_t)e->L * e->capture_cap * e->H;
@@ -995,6 +1033,7 @@ DPUF_EXPORT double dpuf_amd_gemv_bench(void* handle, int32_t which, int32_t M, i
     if (!e || which < 0 || which > 9 || M < 1 || iters < 1) return -1.0;
     if (which != 7 && (e->L == 0 || start_layer < 0 || start_layer >= e->L)) return -1.0;
     if (M > DPUF_AMD_MAX_BATCH) return -1.0;
+    begin_call(e);
     DpufGemvJob js[3];
     double b0 = 0.0;
     bench_jobs(e, which, start_layer, js, &b0, M);
@@ -1033,13 +1072,16 @@ DPUF_EXPORT double dpuf_amd_gemv_bench(void* handle, int32_t which, int32_t M, i
     dpuf_hip_event_destroy(a);
     dpuf_hip_event_destroy(b);
     if (bytes) *bytes = b0;
-    if (!dpuf_hip_ok()) return -1.0;
+    int32_t* hp = e->h_pinned;
+    dpuf_hip_d2h(hp + 3, e->d_err, 4, e->stream);
+    if (dpuf_hip_sync(e->stream) != 0 || end_call(e, hp[3]) != 0) return -1.0;
     return (double)ms / iters;
 }
 
 DPUF_EXPORT void dpuf_amd_set_gemv_max_workgroups(int32_t n) { dpuf_hip_set_gemv_max_wg(n); }
 
 DPUF_EXPORT int32_t dpuf_amd_reduce_check(const float* x, int32_t n, int32_t offset, int32_t mode, float thr) {
+    dpuf_hip_clear_error();
     if (!x || n < 1 || offset < 0 || offset > 3 || (mode != 0 && mode != 1) || dpuf_hip_device_count() <= 0)
         return -1;
     void* s = dpuf_hip_stream_create();
@@ -1062,6 +1104,7 @@ DPUF_EXPORT int32_t dpuf_amd_reduce_check(const float* x, int32_t n, int32_t off
 }
 
 DPUF_EXPORT double dpuf_amd_copy_bench(size_t bytes, int32_t iters) {
+    dpuf_hip_clear_error();
     if (bytes == 0 || iters < 1 || dpuf_hip_device_count() <= 0) return -1.0;
     void* s = dpuf_hip_stream_create();
     void* src = dpuf_hip_malloc(bytes);

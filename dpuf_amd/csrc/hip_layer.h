@@ -94,8 +94,13 @@ void dpuf_hip_gemv(void* s, int32_t M, int32_t n_jobs, const DpufGemvJob* jobs,
 /* One GEMV job that also sets rows [r0, r1) of job->out to 0 (every token
  * row): for M > 1 inside the GEMM launch, for M == 1 with a second launch. */
 void dpuf_hip_gemv_zero(void* s, int32_t M, const DpufGemvJob* job, int32_t r0, int32_t r1);
-/* Caps M == 1 GEMV workgroups per launch (<= 0: device capacity only). */
+/* Caps the workgroups of an M == 1 GEMV or K-split GEMM launch (<= 0:
+ * device capacity only). */
 void dpuf_hip_set_gemv_max_wg(int32_t n);
+/* Device word (4 bytes, zero) that the GEMV kernels of this thread's
+ * following launches set non-zero when a bounded wait runs out; the caller
+ * reads it after synchronising.  M == 1 GEMV launches fail without one. */
+void dpuf_hip_bind_error_word(int32_t* d_word);
 void dpuf_hip_qk_rope_kv(void* s, int32_t M, float* q, float* k, const float* v,
                          const float* q_norm, const float* k_norm, float eps,
                          const float* cos_tab, const float* sin_tab, float* kc, float* vc,

@@ -25,8 +25,11 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 // ---------------------------------------------------------------------------
 // Error bookkeeping
 // ---------------------------------------------------------------------------
-static hipError_t g_err = hipSuccess;
-static char g_err_msg[256];
+// First HIP error of the current API call on this thread: every entry point
+// of the library clears it on entry (dpuf_hip_clear_error) and reports it on
+// exit, so one failed call does not fail the next one or another thread's.
+static thread_local hipError_t g_err = hipSuccess;
+static thread_local char g_err_msg[256];
 
 static void note(hipError_t e, const char* what) {
     if (e != hipSuccess && g_err == hipSuccess) {
@@ -578,18 +581,12 @@ DEV float run_chain(const float4* row, int n2) {
 // ---------------------------------------------------------------------------
 #define MV_NBUF 4   // pair buffers in flight per workgroup
 #define MV_CHAIN 4  // float4 pairs per LDS read batch of a chain (chain waves)
-#ifndef MV_CHAIN1
 #define MV_CHAIN1 8  // the same for the one-group-per-workgroup instances
-#endif
-#ifndef MV_NC
 #define MV_NC 2     // chain waves per workgroup
-#endif
 // Launch-shape choice (compile-time): whether groups of 43..56 steps (K up to
 // 14336) keep their activations in registers (11..14 loader waves x 4 steps)
 // or load them per round.
-#ifndef MV_HOIST48
 #define MV_HOIST48 1
-#endif
 
 struct MvJob {
     const uint8_t* g;  // dense groups of the matrix (row-block layout)
@@ -608,6 +605,7 @@ struct MvArgs {
     int nc;     // chain waves: MV_NC, or 0 when every workgroup has one group
     const int32_t* skip_flag;
     float fill;
+    int32_t* err;  // device error word: bit 0 set when a bounded LDS wait ran out
 };
 
 // Activations of one round of one wave.
@@ -636,7 +634,13 @@ struct MvGeo {
     float* out;
     int g0, rows;
     DpufPrep x;
+    int32_t* err;
 };
+
+// A bounded wait that ran out leaves its buffer's data incomplete: the launch
+// goes on (every wave still ends) and the host, which reads this word after
+// the call, reports the call as failed.
+DEV void mv_wait_failed(int32_t* err) { atomicOr(err, 1); }
 
 // Loads are unconditional (indices clamped into the group), so the number of
 // memory operations in flight is the same on every path and the wait for one
@@ -716,6 +720,7 @@ DEV void mv_consume(const MvGeo& G, int u, int w, int lane, const MvU<NL>& L, co
         while (__hip_atomic_load(&sy->done[buf], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != lg - G.nbuf &&
                ++spins < (1 << 22))
             __builtin_amdgcn_s_sleep(1);
+        if (spins >= (1 << 22) && lane == 0) mv_wait_failed(G.err);
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
     }
     mv_dots<NL, HOIST>(G, r, w, lane, L, X0, pairs);
@@ -741,6 +746,7 @@ DEV void mv_chains(const MvGeo& G, int c, int n_my, int lane, uint8_t* smem, MvS
         while (__hip_atomic_load(&sy->cnt[buf], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != want &&
                ++spins < (1 << 22))
             __builtin_amdgcn_s_sleep(1);
+        if (spins >= (1 << 22) && lane == 0) mv_wait_failed(G.err);
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
         __builtin_amdgcn_s_setprio(2);
         if (lane < 8) {
@@ -771,6 +777,7 @@ __global__ __launch_bounds__(1024) void k_mv(MvArgs A) {
     G.g0 = J.g0;
     G.rows = J.rows;
     G.x = J.x;
+    G.err = A.err;
     const int n_my = (J.g1 - J.g0 - G.lb + G.nwg - 1) / G.nwg;
     if (A.skip_flag && *A.skip_flag) {
         for (int lg = 0; lg < n_my; lg++) {
@@ -860,18 +867,10 @@ __global__ __launch_bounds__(1024) void k_mv(MvArgs A) {
 // l = row l % 16, k = 8 (l / 16) + e; B lane l = token l % 16, same k; D lane
 // l = token l % 16, rows 4 (l / 16) + v.
 // ---------------------------------------------------------------------------
-#ifndef GM_SB
 #define GM_SB 4  // blocks per LDS stage
-#endif
-#ifndef GM_RF
 #define GM_RF 1  // 16-row fragments per wave (workgroup = 64 GM_RF rows)
-#endif
-#ifndef GM_TT
 #define GM_TT 4  // 16-token tiles per workgroup
-#endif
-#ifndef GM_XCD
 #define GM_XCD 1  // XCD-grouped workgroup order
-#endif
 
 typedef _Float16 gm_h8 __attribute__((ext_vector_type(8)));
 typedef float gm_f4 __attribute__((ext_vector_type(4)));
@@ -1207,14 +1206,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
 // ---------------------------------------------------------------------------
 #define SK_NP 8   // producer waves
 #define SK_NC 4   // chain waves (one per D component)
-#ifndef SK_P
 #define SK_P 4    // load ring depth in rounds (even; fastest of 4..10 in a sweep of the dword-load version)
-#endif
 static_assert(SK_P % 2 == 0, "the D buffers alternate with the round");
 
-#ifndef SKP_P
 #define SKP_P 8  // ring depth in rounds: a multiple of every NR
-#endif
 #define SKP_RB 4                 // blocks per producer wave per round
 #define SKP_RS (SK_NP * SKP_RB)  // 32 blocks per round
 
@@ -1632,54 +1627,6 @@ __global__ __launch_bounds__(256) void k_qk_rope_kv_w(float* __restrict__ q, flo
             kc[off] = o[e];
             vc[off] = vv[e];
         }
-    }
-}
-
-__global__ void k_qk_rope_kv(float* __restrict__ q, float* __restrict__ k, const float* __restrict__ v,
-                             const float* __restrict__ qn, const float* __restrict__ kn, float eps,
-                             const float* __restrict__ cos_tab, const float* __restrict__ sin_tab,
-                             float* __restrict__ kc, float* __restrict__ vc, const int32_t* __restrict__ pos0p,
-                             int n_q, int n_kv, int hd, int max_seq) {
-    extern __shared__ float sv[];
-    __shared__ float part[8];
-    __shared__ float inv_sh;
-    const int m = blockIdx.x, head = blockIdx.y, tid = threadIdx.x;
-    const int pos = *pos0p + m;
-    const bool is_k = head >= n_q;
-    const int hh = is_k ? head - n_q : head;
-    float* vec = is_k ? (k + ((size_t)m * n_kv + hh) * hd) : (q + ((size_t)m * n_q + hh) * hd);
-    const float* nw = is_k ? kn : qn;
-    sv[tid] = vec[tid];
-    __syncthreads();
-    if (nw) {
-        if (tid < 8) {
-            float a = 0.0f;
-            for (int i = tid; i < hd; i += 8) a = fmaf(sv[i], sv[i], a);
-            part[tid] = a;
-        }
-        __syncthreads();
-        if (tid == 0) inv_sh = 1.0f / sqrtf(hsum8(part) / (float)hd + eps);
-        __syncthreads();
-        const float x = (sv[tid] * inv_sh) * nw[tid];
-        __syncthreads();
-        sv[tid] = x;
-        __syncthreads();
-    }
-    const int half = hd >> 1;
-    float o;
-    if (tid < half) {
-        const float c = cos_tab[(size_t)pos * half + tid], s = sin_tab[(size_t)pos * half + tid];
-        o = fmaf(sv[tid], c, -(sv[tid + half] * s));
-    } else {
-        const int j = tid - half;
-        const float c = cos_tab[(size_t)pos * half + j], s = sin_tab[(size_t)pos * half + j];
-        o = fmaf(sv[tid], c, sv[j] * s);
-    }
-    vec[tid] = o;
-    if (is_k) {
-        const size_t off = ((size_t)hh * max_seq + pos) * hd + tid;
-        kc[off] = o;
-        vc[off] = v[((size_t)m * n_kv + hh) * hd + tid];
     }
 }
 
@@ -2120,15 +2067,9 @@ __global__ __launch_bounds__(AP_NT) void k_attn_pv(const float* __restrict__ S, 
 // at consecutive positions) leave that row's chains untouched.  G even (no
 // single trailing head), HD in {64, 128, 256}.
 // ---------------------------------------------------------------------------
-#ifndef PVT_R
 #define PVT_R 32  // score rows per workgroup (a multiple of 8 PVT_RT)
-#endif
-#ifndef PVT_RT
 #define PVT_RT 4  // rows per thread in P.V (workgroup of 8 HD / PVT_RT threads)
-#endif
-#ifndef PVT_KV
 #define PVT_KV 8  // keys per register batch of V
-#endif
 
 // p of keys t .. t + 3 for the thread's RT rows (t clamped into the row so a
 // read ahead of the last keys stays inside it; such values are not used)
@@ -3284,9 +3225,14 @@ void dpuf_hip_relayout(void* s, const uint8_t* src, const uint64_t* offs, int32_
 
 typedef void (*MvKernel)(MvArgs);
 
-static int g_mv_max_wg = 0;  // test/tuning cap on M == 1 GEMV workgroups
+static int g_mv_max_wg = 0;  // test/tuning cap on GEMV / K-split GEMM workgroups
 
 void dpuf_hip_set_gemv_max_wg(int32_t n) { g_mv_max_wg = n > 0 ? n : 0; }
+
+// Device error word of the current API call on this thread (see MvArgs::err).
+static thread_local int32_t* g_err_word = NULL;
+
+void dpuf_hip_bind_error_word(int32_t* d_word) { g_err_word = d_word; }
 
 // Workgroups of one k_mv instance the device holds at once (occupancy x CUs),
 // cached per (instance, block size, LDS size).
@@ -3369,6 +3315,11 @@ static void mv_launch(void* s, MvArgs& A, const int* n_groups) {
         grid += nwg;
         A.wb[i + 1] = grid;
     }
+    if (!g_err_word) {
+        note(hipErrorInvalidValue, "dpuf_hip_gemv: no device error word bound");
+        return;
+    }
+    A.err = g_err_word;
     A.nbuf = most < MV_NBUF ? most : MV_NBUF;
     A.nc = most > 1 ? MV_NC : 0;
     const int threads = (nw + A.nc) * 64;
@@ -3404,17 +3355,6 @@ static int gm_capacity(GmKernel k, int threads) {
         c_cap[c_n++] = cap;
     }
     return cap;
-}
-
-// The M <= 16 path of the GEMM: on unless DPUF_GEMM_SKINNY=0 (which keeps
-// k_gemm_mfma for every M, for comparisons).
-static int sk_enabled(void) {
-    static int v = -1;
-    if (v < 0) {
-        const char* e = getenv("DPUF_GEMM_SKINNY");
-        v = !(e && e[0] == '0');
-    }
-    return v;
 }
 
 void dpuf_hip_gemv_zero(void* s, int32_t M, const DpufGemvJob* job, int32_t r0, int32_t r1) {
@@ -3494,12 +3434,13 @@ static void gm_launch(void* s, int32_t M, int32_t n_jobs, const DpufGemvJob* job
         const int n_blk = G.K >> 5;
         long long gmax = 0;
         for (int i = 0; i < n_jobs; i++) gmax = gmax > jobs[i].g1 ? gmax : jobs[i].g1;
-        if (M <= 16 && sk_enabled() && n_blk <= 128 && gmax * n_blk * 144 < 0xFFFFFFFFll) {
+        if (M <= 16 && n_blk <= 128 && gmax * n_blk * 144 < 0xFFFFFFFFll) {
             // one 16-token tile, K <= 4096: persistent K-split workgroups,
             // each job's share of the chip in proportion to its fragments
             const int NR = n_blk <= 32 ? 1 : n_blk <= 64 ? 2 : 4;
             GmKernel k = NR == 1 ? k_gemm_skp<1> : NR == 2 ? k_gemm_skp<2> : k_gemm_skp<4>;
-            const int cap = gm_capacity(k, 64 * (SK_NP + SK_NC));
+            int cap = gm_capacity(k, 64 * (SK_NP + SK_NC));
+            if (g_mv_max_wg > 0 && cap > g_mv_max_wg) cap = g_mv_max_wg;
             int nfr[3], ftot = 0;
             for (int i = 0; i < n_jobs; i++) {
                 const int ng = jobs[i].g1 - jobs[i].g0;
@@ -3518,7 +3459,7 @@ static void gm_launch(void* s, int32_t M, int32_t n_jobs, const DpufGemvJob* job
             LAUNCHED("k_gemm_skp");
             return;
         }
-        if (M <= 16 && sk_enabled()) {
+        if (M <= 16) {
             // one 16-token tile: the K-split kernel, one workgroup per 16 rows
             int f = 0;
             for (int i = 0; i < n_jobs; i++) {
@@ -3557,8 +3498,7 @@ void dpuf_hip_qk_rope_kv(void* s, int32_t M, float* q, float* k, const float* v,
         hipLaunchKernelGGL(k_qk_rope_kv_w<256>, gw, dim3(256), 0, ST(s), q, k, v, q_norm, k_norm, eps, cos_tab,
                            sin_tab, kc, vc, pos0, M, n_q, n_kv, max_seq);
     else
-        hipLaunchKernelGGL(k_qk_rope_kv, dim3(M, n_q + n_kv), dim3(hd), (size_t)hd * sizeof(float), ST(s), q, k, v,
-                           q_norm, k_norm, eps, cos_tab, sin_tab, kc, vc, pos0, n_q, n_kv, hd, max_seq);
+        note(hipErrorInvalidValue, "dpuf_hip_qk_rope_kv: head dim must be 64, 128 or 256");
     LAUNCHED("k_qk_rope_kv");
 }
 

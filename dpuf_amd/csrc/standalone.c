@@ -14,9 +14,29 @@
 
 static void* g_stream = NULL;
 
+/* The library's stream for the host-pointer entries; also starts the call's
+ * error state afresh. */
 static void* stream(void) {
+    dpuf_hip_clear_error();
     if (!g_stream && dpuf_hip_device_count() > 0) g_stream = dpuf_hip_stream_create();
     return g_stream;
+}
+
+/* A call that validated its arguments but could not finish (allocation,
+ * runtime or kernel failure) writes NaN to every output it owns, so the
+ * failure cannot pass for a result; dpuf_amd_last_error() says why. */
+static void fail_rows(float* out, int32_t M, int32_t ld, int32_t r0, int32_t r1) {
+    const uint32_t nan_bits = 0x7FC00000u;
+    float nanv;
+    memcpy(&nanv, &nan_bits, 4);
+    for (int32_t m = 0; m < M; m++)
+        for (int32_t r = r0; r < r1; r++) out[(size_t)m * ld + r] = nanv;
+}
+
+/* Largest token count of one GEMM launch at K columns (M * K < 2^30). */
+static int32_t max_chunk(int32_t M, int32_t cols) {
+    const int64_t cap = ((int64_t)1 << 30) / cols - 1;
+    return (int64_t)M < cap ? M : (int32_t)cap;
 }
 
 /* Checks tiles [t0, t1) of a mode 12 payload (tile t holds min(16, rows -
@@ -192,12 +212,21 @@ DPUF_EXPORT void dpuf_matmul_qr_hadamard4_packed_tile_range(int32_t M, int32_t r
         !x_blk_scale || !x_sum8 || !out)
         return;
     if ((int64_t)t_end * 16 > (int64_t)rows + 15) return;
+    if ((int64_t)M * cols >= ((int64_t)1 << 30)) return; /* the slab inputs are one block */
+    const int32_t r1 = t_end * 16 < rows ? t_end * 16 : rows;
     Staged st;
-    if (!stage_weights(rows, cols, t_start, t_end, tensor_base, tile_offsets, NULL, &st)) return;
+    if (!stage_weights(rows, cols, t_start, t_end, tensor_base, tile_offsets, NULL, &st)) {
+        fail_rows(out, M, rows, t_start * 16, r1);
+        return;
+    }
     const int32_t nb = cols / 32;
     DpufPrep p = {0, 0, 0, 0};
     float* dout = (float*)dpuf_hip_malloc((size_t)M * rows * 4);
-    if (prep_alloc(&p, M, cols) && dout) {
+    int32_t* derr = (int32_t*)dpuf_hip_malloc(4);
+    int32_t herr = 1;
+    if (prep_alloc(&p, M, cols) && dout && derr) {
+        dpuf_hip_fill_zero(derr, 4, s);
+        dpuf_hip_bind_error_word(derr);
         if (M == 1) {
             dpuf_hip_h2d(p.q, x_q8, (size_t)cols, s);
             dpuf_hip_h2d(p.s, x_blk_scale, (size_t)nb * 4, s);
@@ -224,12 +253,15 @@ DPUF_EXPORT void dpuf_matmul_qr_hadamard4_packed_tile_range(int32_t M, int32_t r
         j.out = dout + (size_t)t_start * 16;
         j.ldo = rows;
         dpuf_hip_gemv(s, M, 1, &j, NULL, 0.0f);
-        int32_t r1 = t_end * 16 < rows ? t_end * 16 : rows;
         fetch_rows(out, dout, M, rows, t_start * 16, r1, s);
-        dpuf_hip_sync(s);
+        dpuf_hip_d2h(&herr, derr, 4, s);
+        if (dpuf_hip_sync(s) != 0) herr = 1;
     }
+    if (herr != 0) fail_rows(out, M, rows, t_start * 16, r1);
+    dpuf_hip_bind_error_word(NULL);
     prep_free(&p);
     dpuf_hip_free(dout);
+    dpuf_hip_free(derr);
     unstage(&st);
 }
 
@@ -241,27 +273,44 @@ DPUF_EXPORT void dpuf_matmul_qr_hadamard4_packed_f32(int32_t M, int32_t rows, in
     if (!s || M <= 0 || rows <= 0 || n_tiles <= 0 || !x_in || !out) return;
     if ((int64_t)n_tiles * 16 > (int64_t)rows + 15 || (int64_t)n_tiles * 16 < rows) return;
     Staged st;
-    if (!stage_weights(rows, cols, 0, n_tiles, tensor_base, tile_offsets, sign_bits, &st)) return;
-    DpufPrep p = {0, 0, 0, 0};
-    float* dx = (float*)dpuf_hip_malloc((size_t)M * cols * 4);
-    float* dout = (float*)dpuf_hip_malloc((size_t)M * rows * 4);
-    if (prep_alloc(&p, M, cols) && dx && dout) {
-        dpuf_hip_h2d(dx, x_in, (size_t)M * cols * 4, s);
-        dpuf_hip_prep(s, M, cols, dx, st.w.sign, p);
-        DpufGemvJob j;
-        j.w = st.w;
-        j.g0 = 0;
-        j.g1 = st.w.n_groups;
-        j.p = p;
-        j.out = dout;
-        j.ldo = rows;
-        dpuf_hip_gemv(s, M, 1, &j, NULL, 0.0f);
-        dpuf_hip_d2h(out, dout, (size_t)M * rows * 4, s);
-        dpuf_hip_sync(s);
+    if (!stage_weights(rows, cols, 0, n_tiles, tensor_base, tile_offsets, sign_bits, &st)) {
+        fail_rows(out, M, rows, 0, rows);
+        return;
     }
+    /* token chunks keep every launch below 2^30 activation bytes; each
+     * (row, token) result does not depend on the other tokens */
+    const int32_t mc = max_chunk(M, cols);
+    DpufPrep p = {0, 0, 0, 0};
+    float* dx = (float*)dpuf_hip_malloc((size_t)mc * cols * 4);
+    float* dout = (float*)dpuf_hip_malloc((size_t)mc * rows * 4);
+    int32_t* derr = (int32_t*)dpuf_hip_malloc(4);
+    int32_t herr = 1;
+    if (prep_alloc(&p, mc, cols) && dx && dout && derr) {
+        dpuf_hip_fill_zero(derr, 4, s);
+        dpuf_hip_bind_error_word(derr);
+        for (int32_t m0 = 0; m0 < M; m0 += mc) {
+            const int32_t n = M - m0 < mc ? M - m0 : mc;
+            dpuf_hip_h2d(dx, x_in + (size_t)m0 * cols, (size_t)n * cols * 4, s);
+            dpuf_hip_prep(s, n, cols, dx, st.w.sign, p);
+            DpufGemvJob j;
+            j.w = st.w;
+            j.g0 = 0;
+            j.g1 = st.w.n_groups;
+            j.p = p;
+            j.out = dout;
+            j.ldo = rows;
+            dpuf_hip_gemv(s, n, 1, &j, NULL, 0.0f);
+            dpuf_hip_d2h(out + (size_t)m0 * rows, dout, (size_t)n * rows * 4, s);
+        }
+        dpuf_hip_d2h(&herr, derr, 4, s);
+        if (dpuf_hip_sync(s) != 0) herr = 1;
+    }
+    if (herr != 0) fail_rows(out, M, rows, 0, rows);
+    dpuf_hip_bind_error_word(NULL);
     prep_free(&p);
     dpuf_hip_free(dx);
     dpuf_hip_free(dout);
+    dpuf_hip_free(derr);
     unstage(&st);
 }
 

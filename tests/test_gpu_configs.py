@@ -1,0 +1,365 @@
+"""GPU parity at the benchmark workloads' own shapes, and on every host path
+the reference CLI drives, against the CPU oracle, through the C ABI.
+
+Each test prints what it runs before it runs it.  Results are compared bit
+for bit (logits, per-layer residuals, greedy ids): the engine reproduces the
+reference's fp32 operation order, so equality is the bar, which is stricter
+than the 1e-3 relative / 1e-4 absolute tolerance the workloads state.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from dpuf_amd import model as M
+
+pytestmark = pytest.mark.gpu
+
+
+def log(*a):
+    print(*a, flush=True)
+
+
+def bits_equal(a, b):
+    return np.array_equal(np.asarray(a, np.float32).view(np.uint32), np.asarray(b, np.float32).view(np.uint32))
+
+
+def maxdiff(a, b):
+    return float(np.max(np.abs(np.asarray(a, np.float64) - np.asarray(b, np.float64))))
+
+
+def top_gap(x):
+    t = np.sort(np.asarray(x, np.float64))[-2:]
+    return float(t[1] - t[0])
+
+
+class Pair:
+    """A GPU engine and an oracle engine over the same model."""
+
+    def __init__(self, eng, orc, model):
+        self.eng, self.orc, self.m = eng, orc, model
+        self.g = eng.dpuf_engine_create(*model.create_args())
+        assert self.g, eng.dpuf_amd_last_error()
+        self.o = orc.orc_engine_create(*model.create_args())
+        assert self.o
+        c = model.cfg.contents
+        self.V, self.L, self.H = c.vocab_size, c.num_layers, c.hidden_size
+
+    def forward(self, ids, pos0, only_last=1, embeds=None):
+        n = len(ids) if ids is not None else embeds.shape[0]
+        rows = 1 if only_last == 1 else n
+        lg = np.zeros((rows, self.V), np.float32)
+        lo = np.zeros((rows, self.V), np.float32)
+        ip, ep = M.ptr(ids), M.ptr(embeds)
+        rg = self.eng.dpuf_engine_forward_batch_ex(self.g, n, ip, pos0, ep, None, None, None, None, only_last,
+                                                   M.ptr(lg) if only_last != 2 else None)
+        ro = self.orc.orc_engine_forward(self.o, n, ip, pos0, ep, only_last, M.ptr(lo) if only_last != 2 else None)
+        assert rg == 0 and ro == 0, (rg, ro, self.eng.dpuf_amd_last_error())
+        return lg, lo
+
+    def set_slot(self, s):
+        assert self.eng.dpuf_engine_set_slot(self.g, s) == 0
+        assert self.orc.orc_engine_set_slot(self.o, s) == 0
+
+    def set_kv(self, layer, kvh, pos0, k, v):
+        assert self.eng.dpuf_amd_engine_set_kv(self.g, layer, kvh, pos0, k.shape[0], M.ptr(k), M.ptr(v)) == 0
+        assert self.orc.orc_engine_set_kv(self.o, layer, kvh, pos0, k.shape[0], M.ptr(k), M.ptr(v)) == 0
+
+    def capture(self, cap):
+        assert self.eng.dpuf_amd_engine_set_capture(self.g, cap) == 0
+        self.orc.orc_engine_set_capture(self.o, cap)
+        self.cap = cap
+
+    def captured(self, rows):
+        g = np.zeros(self.L * self.cap * self.H, np.float32)
+        assert self.eng.dpuf_amd_engine_get_capture(self.g, M.ptr(g), g.size) == 0
+        o = np.ctypeslib.as_array(C.cast(self.orc.orc_engine_get_capture(self.o), C.POINTER(C.c_float)),
+                                  (self.L * self.cap * self.H,))
+        return (g.reshape(self.L, self.cap, self.H)[:, :rows], o.reshape(self.L, self.cap, self.H)[:, :rows].copy())
+
+    def close(self):
+        self.eng.dpuf_engine_destroy(self.g)
+        self.orc.orc_engine_destroy(self.o)
+
+
+def greedy(p, first_logits_g, first_logits_o, pos, steps, what):
+    """Greedy decode on both engines, each from its own argmax, comparing
+    logits bit for bit and ids at every step; returns (ids, smallest
+    top-1 / top-2 logit gap seen)."""
+    tg, gap = [], float("inf")
+    lg, lo = first_logits_g, first_logits_o
+    for s in range(steps):
+        a, b = int(np.argmax(lg[-1])), int(np.argmax(lo[-1]))
+        assert a == b, (what, s, a, b)
+        gap = min(gap, top_gap(lo[-1]))
+        tg.append(a)
+        lg, lo = p.forward(np.array([a], np.int32), pos + s)
+        assert bits_equal(lg, lo), (what, s, maxdiff(lg, lo))
+    return tg, gap
+
+
+@pytest.mark.timeout(900)
+def test_qwen3_8b_pp32_tg32_token_exact(eng, orc):
+    """Qwen3-8B shape (36 layers, hidden 4096, 32 / 8 heads, FFN 12288,
+    vocab 151936, untied LM head), N(0, 0.02) weights: a seeded 32-token
+    prompt, then 32 greedy tokens.  Logits bit-identical at every step, ids
+    identical."""
+    log("building the Qwen3-8B-shape model (4.26 GB of packed weights)")
+    m = M.Model.build(M.QWEN3_8B, max_seq_len=80, seed=1234)
+    p = Pair(eng, orc, m)
+    ids = np.random.default_rng(2024).integers(0, 151936, 32).astype(np.int32)
+    log("8B pp32")
+    lg, lo = p.forward(ids, 0)
+    assert bits_equal(lg, lo), maxdiff(lg, lo)
+    log("8B tg32")
+    toks, gap = greedy(p, lg, lo, 32, 32, "8B")
+    log("8B greedy ids", toks, "smallest top-1/top-2 gap", gap)
+    p.close()
+
+
+def test_gqa4_long_context_injected_kv(eng, orc):
+    """The Qwen3-8B attention geometry (32 Q / 8 KV heads: groups of 4,
+    head_dim 128) on a small hidden size.  (1) Short context, the fused decode
+    kernel: a 20-token prompt and 8 greedy steps.  (2) A 4096-position N(0, 1)
+    KV cache injected into both engines, then 4 decode steps through the
+    split attention (the long-context workload's kernels), then 3 more through
+    the captured-graph device-argmax entry."""
+    shape = dict(hidden_size=256, intermediate_size=512, num_layers=2, num_q_heads=32, num_kv_heads=8,
+                 head_dim=128, vocab_size=4096, tie_word_embeddings=1)
+    m = M.Model.build(shape, max_seq_len=4104, seed=71)
+    p = Pair(eng, orc, m)
+    log("G=4 short context: pp20 + 8 steps")
+    ids = np.random.default_rng(72).integers(0, 4096, 20).astype(np.int32)
+    lg, lo = p.forward(ids, 0)
+    assert bits_equal(lg, lo)
+    greedy(p, lg, lo, 20, 8, "G4 short")
+    log("G=4: injecting a 4096-position KV cache")
+    rng = np.random.default_rng(73)
+    for layer in range(2):
+        for kvh in range(8):
+            k = rng.standard_normal((4096, 128), dtype=np.float32)
+            v = rng.standard_normal((4096, 128), dtype=np.float32)
+            p.set_kv(layer, kvh, 0, k, v)
+    lg, lo = p.forward(np.array([11], np.int32), 4096)
+    assert bits_equal(lg, lo), maxdiff(lg, lo)
+    toks, _ = greedy(p, lg, lo, 4097, 3, "G4 4096")
+    tok = int(np.argmax(lo[-1]))
+    out = C.c_int32(-1)
+    for s in range(3):
+        pos = 4100 + s
+        log(f"G=4 graph decode at position {pos}")
+        rc = eng.dpuf_amd_engine_forward_argmax(p.g, 1, M.ptr(np.array([tok], np.int32)), pos, None, 1,
+                                                C.byref(out), None)
+        assert rc == 0
+        lo = np.zeros(4096, np.float32)
+        assert orc.orc_engine_forward(p.o, 1, M.ptr(np.array([tok], np.int32)), pos, None, 1, M.ptr(lo)) == 0
+        assert out.value == orc.orc_argmax(M.ptr(lo), 4096)
+        tok = out.value
+    p.close()
+
+
+def test_attention_beyond_split_lds_budget(eng, orc):
+    """Groups of 4 with 7200 cached positions: a row of probabilities no
+    longer fits the split kernels' LDS budget, so decode attention takes the
+    one-pair-per-workgroup kernel (k_attn).  Logits bit-identical."""
+    shape = dict(hidden_size=256, intermediate_size=512, num_layers=1, num_q_heads=8, num_kv_heads=2,
+                 head_dim=128, vocab_size=4096, tie_word_embeddings=1)
+    m = M.Model.build(shape, max_seq_len=7240, seed=81)
+    p = Pair(eng, orc, m)
+    rng = np.random.default_rng(82)
+    for kvh in range(2):
+        p.set_kv(0, kvh, 0, rng.standard_normal((7200, 128), dtype=np.float32),
+                 rng.standard_normal((7200, 128), dtype=np.float32))
+    log("k_attn fallback: decode at position 7200")
+    lg, lo = p.forward(np.array([3], np.int32), 7200)
+    assert bits_equal(lg, lo), maxdiff(lg, lo)
+    greedy(p, lg, lo, 7201, 2, "fallback")
+    p.close()
+
+
+@pytest.mark.timeout(600)
+def test_prefill_m512_8b_width_pruned(eng, orc, monkeypatch):
+    """pp512 on the M > 1 path at the Qwen3-8B width (hidden 4096, FFN
+    12288, 32 / 8 heads), two layers, down projection pruned to 224 of 256
+    tiles: per-layer residual stream of all 512 rows and the last row's
+    logits bit-identical; then 3 decode steps with the pruning off."""
+    monkeypatch.setenv("DPUF_PREFILL_KEEP_TILES", "224")
+    monkeypatch.delenv("DPUF_GEN_KEEP_TILES", raising=False)
+    shape = dict(M.QWEN3_8B, num_layers=2, vocab_size=4096, tie_word_embeddings=1)
+    m = M.Model.build(shape, max_seq_len=520, seed=91)
+    p = Pair(eng, orc, m)
+    p.capture(512)
+    ids = np.random.default_rng(92).integers(0, 4096, 512).astype(np.int32)
+    log("8B-width pp512, keep 224 of 256 down tiles")
+    lg, lo = p.forward(ids, 0)
+    assert bits_equal(lg, lo), maxdiff(lg, lo)
+    cg, co = p.captured(512)
+    assert bits_equal(cg, co), maxdiff(cg, co)
+    assert np.all(co[:, :, 224 * 16:] != 0)  # the residual keeps its earlier values in pruned rows
+    p.capture(0)
+    greedy(p, lg, lo, 512, 3, "after pp512")
+    p.close()
+
+
+@pytest.mark.timeout(600)
+def test_lm_head_zone_a_151936(eng, orc, monkeypatch):
+    """The LM head at its real size (151936 x 4096, 9496 tiles) with no
+    layers, hidden states fed through embeds_in: 150 seeded steps, about 70 %
+    with a planted zone token, Zone-A early exit on (1424 zone tiles, margin
+    0.8), then 30 steps with it off.  Logits bit-identical at every step, so
+    argmax ids and exit decisions are too."""
+    shape = dict(M.QWEN3_8B, num_layers=0, tie_word_embeddings=1)
+    m = M.Model.build(shape, max_seq_len=16, seed=101)
+    p = Pair(eng, orc, m)
+    rng = np.random.default_rng(102)
+    n = 150
+    planted = rng.random(n) < 0.7
+    tstar = rng.integers(0, 1424 * 16, n).astype(np.int32)
+    hs = rng.standard_normal((n, 4096), dtype=np.float32)
+    rows = np.zeros((n, 4096), np.float32)
+    d = m.tok.contents
+    orc.orc_embed(n, 4096, M.ptr(tstar), d.tensor_base, d.tile_offsets, d.sign_bits, M.ptr(rows))
+    hs[planted] += np.float32(8.0) * rows[planted]
+    monkeypatch.setenv("DPUF_EARLY_TILES", "1424")
+    monkeypatch.setenv("DPUF_EARLY_MARGIN", "0.8")
+    exits0 = eng.dpuf_amd_engine_early_exit_count(p.g)
+    for i in range(n):
+        if i % 25 == 0:
+            log(f"LM head early exit step {i}")
+        lg, lo = p.forward(None, 0, embeds=np.ascontiguousarray(hs[i:i + 1]))
+        assert bits_equal(lg, lo), (i, maxdiff(lg, lo))
+    exits = eng.dpuf_amd_engine_early_exit_count(p.g) - exits0
+    log(f"early exit fired on {exits} of {n} steps ({planted.sum()} planted)")
+    assert 0.5 * n < exits < n
+    monkeypatch.delenv("DPUF_EARLY_TILES")
+    for i in range(30):
+        lg, lo = p.forward(None, 0, embeds=np.ascontiguousarray(hs[i:i + 1]))
+        assert bits_equal(lg, lo), (i, maxdiff(lg, lo))
+    p.close()
+
+
+TINY = dict(hidden_size=256, intermediate_size=512, num_layers=3, num_q_heads=4, num_kv_heads=2, head_dim=64,
+            vocab_size=4096, tie_word_embeddings=1)
+
+
+def test_chunked_prefill_only_last_2(eng, orc):
+    """The CLI's long-prompt pattern (dpuf-cli.c:2384-2395): a 512-token
+    prompt as two 256-token chunks, the first with only_last_logits = 2 (KV
+    only, logits NULL), the second with 1; then greedy decode past 192
+    positions."""
+    m = M.Model.build(TINY, max_seq_len=600, seed=111)
+    p = Pair(eng, orc, m)
+    ids = np.random.default_rng(112).integers(0, 4096, 512).astype(np.int32)
+    log("chunk 1 of 2, only_last_logits = 2")
+    p.forward(ids[:256], 0, only_last=2)
+    log("chunk 2 of 2, only_last_logits = 1")
+    lg, lo = p.forward(ids[256:], 256)
+    assert bits_equal(lg, lo), maxdiff(lg, lo)
+    greedy(p, lg, lo, 512, 4, "after chunks")
+    p.close()
+
+
+def test_embeds_in_rows(eng, orc):
+    """embeds_in rows replace the embedding where token_ids[m] < 0, and for
+    every row when token_ids is NULL (dpuf_engine.c:1658-1672)."""
+    m = M.Model.build(TINY, max_seq_len=64, seed=121)
+    p = Pair(eng, orc, m)
+    rng = np.random.default_rng(122)
+    emb = rng.standard_normal((6, 256), dtype=np.float32) * np.float32(0.05)
+    ids = np.array([5, -1, 1000, -1, 7, -1], np.int32)
+    log("embeds_in mixed with ids")
+    lg, lo = p.forward(ids, 0, only_last=0, embeds=emb)
+    assert bits_equal(lg, lo), maxdiff(lg, lo)
+    log("embeds_in only")
+    lg, lo = p.forward(None, 6, only_last=0, embeds=emb[:3].copy())
+    assert bits_equal(lg, lo), maxdiff(lg, lo)
+    greedy(p, lg, lo, 9, 3, "after embeds")
+    p.close()
+
+
+def test_unshared_projection_signs(eng, orc):
+    """Q, K, V with three different sign vectors (three activation preps,
+    dpuf_engine.c:1760-1777) and gate / up with two, in every layer."""
+    m = M.Model.build(TINY, max_seq_len=64, seed=131)
+    rng = np.random.default_rng(132)
+    for l in range(TINY["num_layers"]):
+        lw = m.layers[l]
+        for name in ("w_k", "w_v", "w_up"):
+            d = getattr(lw, name)
+            sb = np.ctypeslib.as_array(C.cast(d.sign_bits, C.POINTER(C.c_uint8)), (d.cols // 8,))
+            sb[:] = rng.integers(0, 256, d.cols // 8)
+    p = Pair(eng, orc, m)
+    ids = rng.integers(0, 4096, 7).astype(np.int32)
+    log("unshared signs: prefill 7 + 5 steps")
+    lg, lo = p.forward(ids, 0, only_last=0)
+    assert bits_equal(lg, lo), maxdiff(lg, lo)
+    greedy(p, lg, lo, 7, 5, "unshared")
+    p.close()
+
+
+def test_prefix_freeze_apply_reset(eng, orc):
+    """Prefix cache (dpuf_engine.c:1438-1600) on both engines in lockstep: a
+    12-token prompt on slot 0; positions [0, 8) frozen as prefix 2 and applied
+    to slot 5; the rest of the prompt and 3 greedy steps on slot 5; slot 0
+    continues on its own; after reset_slot(5) the same call on slot 5 sees
+    zeros in positions [0, 8)."""
+    m = M.Model.build(TINY, max_seq_len=64, seed=141)
+    p = Pair(eng, orc, m)
+    ids = np.random.default_rng(142).integers(0, 4096, 12).astype(np.int32)
+    lg, lo = p.forward(ids, 0, only_last=0)
+    assert bits_equal(lg, lo)
+    assert eng.dpuf_engine_freeze_prefix(p.g, 2, 8) == 1 and orc.orc_engine_freeze_prefix(p.o, 2, 8) == 1
+    assert eng.dpuf_engine_get_prefix_len(p.g, 2) == 8
+    assert eng.dpuf_engine_apply_prefix(p.g, 5, 2) == 8 and orc.orc_engine_apply_prefix(p.o, 5, 2) == 8
+    p.set_slot(5)
+    assert eng.dpuf_engine_get_slot(p.g) == 5
+    lg5, lo5 = p.forward(ids[8:], 8, only_last=0)
+    assert bits_equal(lg5, lo5) and bits_equal(lg5, lg[8:])
+    greedy(p, lg5, lo5, 12, 3, "slot 5")
+    p.set_slot(0)
+    greedy(p, lg, lo, 12, 2, "slot 0")
+    eng.dpuf_engine_reset_slot(p.g, 5)
+    orc.orc_engine_reset_slot(p.o, 5)
+    p.set_slot(5)
+    lr, lor = p.forward(ids[8:], 8, only_last=0)
+    assert bits_equal(lr, lor) and not bits_equal(lr, lg5)
+    assert eng.dpuf_engine_slot_memory(p.g) == 2 * 3 * 2 * 64 * 64 * 4
+    p.close()
+
+
+def test_multi_session_8b_attention_geometry(eng, orc):
+    """dpuf_amd_engine_forward_slots with groups of 4 and head_dim 128 (two
+    decode-attention workgroups per KV head, the second of which stores no
+    KV) and an FFN of 4160 (the down projection's K > 4096 takes the
+    one-fragment-per-workgroup K-split GEMM): three sessions, 4 steps, every
+    row bit-identical to the oracle decoding that slot alone."""
+    shape = dict(hidden_size=256, intermediate_size=4160, num_layers=2, num_q_heads=8, num_kv_heads=2,
+                 head_dim=128, vocab_size=4096, tie_word_embeddings=1)
+    m = M.Model.build(shape, max_seq_len=64, seed=151)
+    p = Pair(eng, orc, m)
+    slots = np.array([2, 0, 7], np.int32)
+    rng = np.random.default_rng(152)
+    toks, pos = [], []
+    for s, n in zip(slots, (6, 11, 4)):
+        p.set_slot(int(s))
+        lg, lo = p.forward(rng.integers(0, 4096, n).astype(np.int32), 0)
+        assert bits_equal(lg, lo)
+        toks.append(int(np.argmax(lo[0])))
+        pos.append(n)
+    for step in range(4):
+        log(f"multi-session step {step}")
+        lg = np.zeros((3, 4096), np.float32)
+        got = np.full(3, -1, np.int32)
+        rc = eng.dpuf_amd_engine_forward_slots(p.g, 3, M.ptr(slots), M.ptr(np.array(toks, np.int32)),
+                                              M.ptr(np.array(pos, np.int32)), M.ptr(lg), M.ptr(got))
+        assert rc == 0, rc
+        for i, s in enumerate(slots):
+            assert orc.orc_engine_set_slot(p.o, int(s)) == 0
+            lo = np.zeros(4096, np.float32)
+            assert orc.orc_engine_forward(p.o, 1, M.ptr(np.array([toks[i]], np.int32)), pos[i], None, 1,
+                                          M.ptr(lo)) == 0
+            assert bits_equal(lg[i], lo), (step, i, maxdiff(lg[i], lo))
+            assert got[i] == orc.orc_argmax(M.ptr(lo), 4096)
+            toks[i] = int(got[i])
+            pos[i] += 1
+    p.close()

@@ -11,7 +11,8 @@ from dpuf_amd import model as M
 pytestmark = pytest.mark.gpu
 
 SHAPES = [(16, 64), (40, 128), (200, 1024), (1000, 3072)]
-SHAPES_8B = [(1024, 4096), (4096, 12288)]
+# Qwen3-8B GEMV shapes (rows, cols): K/V, down, gate/up, Q/O
+SHAPES_8B = [(1024, 4096), (4096, 12288), (12288, 4096), (4096, 4096)]
 
 
 def _mat(rows, cols, seed, std=0.02):
@@ -46,6 +47,88 @@ def test_matmul_f32_bit_exact(eng, orc, rows, cols, m):
     orc.orc_matmul_f32(m, rows, cols, d.n_tiles, M.ptr(x), d.tensor_base, d.tile_offsets, d.sign_bits,
                        M.ptr(out_o))
     assert np.isfinite(out_o).all()
+    assert _same_bits(out_g, out_o), f"max abs diff {np.nanmax(np.abs(out_g - out_o))}"
+
+
+def test_matmul_down_8b_dead_zone(eng, orc):
+    """The down projection's shape [12288 -> 4096] at M = 1 with its input
+    through the SwiGLU dead zone (|x| < 0.005 -> 0, dpuf_engine.c:983-987),
+    x shaped like SwiGLU outputs (products of two N(0, 1) halves, scaled):
+    zero and near-zero blocks as the real input has them."""
+    rows, cols = 4096, 12288
+    blob, d = _mat(rows, cols, 61)
+    rng = np.random.default_rng(62)
+    x = (rng.standard_normal((1, cols)) * rng.standard_normal((1, cols)) * 0.02).astype(np.float32)
+    x[np.abs(x) < 0.005] = 0.0
+    x[0, 64:96] = 0.0  # a whole zero block
+    print(f"down + dead zone: {np.mean(x == 0):.2f} of the input is zero", flush=True)
+    out_g = np.full((1, rows), np.nan, np.float32)
+    out_o = np.full((1, rows), np.nan, np.float32)
+    eng.dpuf_matmul_qr_hadamard4_packed_f32(1, rows, cols, d.n_tiles, M.ptr(x), d.tensor_base, d.tile_offsets,
+                                            d.sign_bits, M.ptr(out_g))
+    orc.orc_matmul_f32(1, rows, cols, d.n_tiles, M.ptr(x), d.tensor_base, d.tile_offsets, d.sign_bits,
+                       M.ptr(out_o))
+    assert _same_bits(out_g, out_o), f"max abs diff {np.nanmax(np.abs(out_g - out_o))}"
+
+
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("rows,cols", [(12288, 4096), (4096, 12288)])
+def test_gemm_m512_8b_shapes(eng, orc, rows, cols):
+    """M = 512, the prefill GEMM at the Qwen3-8B gate/up and down shapes;
+    the down shape also pruned to its first 224 of 256 tiles through the
+    tile-range entry (slab-layout inputs), the prefill's 56/64 pruning."""
+    blob, d = _mat(rows, cols, 71 + rows)
+    m = 512
+    x = _x(m, cols, 72 + rows)
+    x[3, 32:64] = 1e-6
+    out_g = np.full((m, rows), np.nan, np.float32)
+    out_o = np.full((m, rows), np.nan, np.float32)
+    print(f"matmul_f32 rows={rows} cols={cols} M=512", flush=True)
+    eng.dpuf_matmul_qr_hadamard4_packed_f32(m, rows, cols, d.n_tiles, M.ptr(x), d.tensor_base, d.tile_offsets,
+                                            d.sign_bits, M.ptr(out_g))
+    orc.orc_matmul_f32(m, rows, cols, d.n_tiles, M.ptr(x), d.tensor_base, d.tile_offsets, d.sign_bits,
+                       M.ptr(out_o))
+    assert _same_bits(out_g, out_o), f"max abs diff {np.nanmax(np.abs(out_g - out_o))}"
+    if rows != 4096:
+        return
+    nb = cols // 32
+    ns = (m + 5) // 6
+    sq = np.zeros(ns * nb * 192, np.int8)
+    ss = np.zeros(ns * nb * 6, np.float32)
+    sm = np.zeros(ns * nb * 6, np.int32)
+    for sl in range(ns):
+        mc = min(6, m - 6 * sl)
+        orc.orc_prep_slab(mc, cols, M.ptr(np.ascontiguousarray(x[6 * sl:6 * sl + mc])), d.sign_bits,
+                          M.ptr(sq[sl * nb * 192:]), M.ptr(ss[sl * nb * 6:]), M.ptr(sm[sl * nb * 6:]))
+    print("tile range [0, 224) of the down shape, M=512", flush=True)
+    out_t = np.full((m, rows), 7.0, np.float32)
+    eng.dpuf_matmul_qr_hadamard4_packed_tile_range(m, rows, cols, 0, 224, M.ptr(sq), M.ptr(ss), M.ptr(sm),
+                                                   d.tensor_base, d.tile_offsets, M.ptr(out_t))
+    assert _same_bits(out_t[:, :224 * 16], out_o[:, :224 * 16])
+    assert (out_t[:, 224 * 16:] == 7.0).all()
+
+
+@pytest.mark.parametrize("cols", [320, 1088, 3072])
+@pytest.mark.parametrize("cap", [1, 3, 7])
+def test_matmul_skinny_workgroup_caps(eng, orc, cols, cap):
+    """The persistent K-split GEMM (2 <= M <= 16, K <= 4096) with its
+    workgroups capped so each walks many 16-row fragments through one
+    register ring, at 1, 2 and 3 rounds of 32 blocks per fragment."""
+    rows, m = 1000, 6
+    blob, d = _mat(rows, cols, 81 + cols)
+    x = _x(m, cols, 83 + cols)
+    x[2, 32:64] = 1e-6
+    out_g = np.full((m, rows), np.nan, np.float32)
+    out_o = np.full((m, rows), np.nan, np.float32)
+    print(f"skinny rows={rows} cols={cols} M={m} max_workgroups={cap}", flush=True)
+    eng.dpuf_amd_set_gemv_max_workgroups(cap)
+    try:
+        eng.dpuf_matmul_qr_hadamard4_packed_f32(m, rows, cols, d.n_tiles, M.ptr(x), d.tensor_base, d.tile_offsets,
+                                                d.sign_bits, M.ptr(out_g))
+    finally:
+        eng.dpuf_amd_set_gemv_max_workgroups(0)
+    orc.orc_matmul_f32(m, rows, cols, d.n_tiles, M.ptr(x), d.tensor_base, d.tile_offsets, d.sign_bits,
+                       M.ptr(out_o))
     assert _same_bits(out_g, out_o), f"max abs diff {np.nanmax(np.abs(out_g - out_o))}"
 
 
