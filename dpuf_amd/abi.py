@@ -208,6 +208,7 @@ def load_engine():
     _sig(lib, "dpuf_amd_copy_bench", C.c_double, [C.c_size_t, I32])
     _sig(lib, "dpuf_amd_set_gemv_max_workgroups", None, [I32])
     _sig(lib, "dpuf_amd_reduce_check", I32, [P, I32, I32, I32, C.c_float])
+    _sig(lib, "dpuf_amd_reduce_check_noalloc", I32, [P, I32, I32, C.c_float, P, P])
     _sig(lib, "dpuf_amd_verify_tiles_device", I32, [I32, I32, I32, P, P, P])
     _sig(lib, "dpuf_amd_engine_forward_slots", I32, [P, I32, P, P, P, P, P])
     _engine = lib

@@ -1103,6 +1103,14 @@ DPUF_EXPORT int32_t dpuf_amd_reduce_check(const float* x, int32_t n, int32_t off
     return r;
 }
 
+DPUF_EXPORT int32_t dpuf_amd_reduce_check_noalloc(const float* d_x, int32_t n, int32_t mode, float thr,
+                                                  int32_t* d_out, void* hip_stream) {
+    dpuf_hip_clear_error();
+    if (!d_x || !d_out || (mode != 0 && mode != 1)) return -1;
+    if (n < 1 || n > DPUF_AMD_NOALLOC_MAX_N) return -2;
+    return dpuf_hip_reduce_noalloc(d_x, n, mode, thr, d_out, hip_stream);
+}
+
 DPUF_EXPORT double dpuf_amd_copy_bench(size_t bytes, int32_t iters) {
     dpuf_hip_clear_error();
     if (bytes == 0 || iters < 1 || dpuf_hip_device_count() <= 0) return -1.0;

@@ -135,6 +135,11 @@ void dpuf_hip_capture(void* s, int32_t M, int32_t H, const float* h, const float
 #define DPUF_HIP_RED_SCRATCH 512
 void dpuf_hip_topcheck(void* s, const float* logits, int32_t n, float thr, int32_t* flag, void* scratch);
 void dpuf_hip_argmax(void* s, const float* logits, int32_t V, int32_t* out, void* scratch);
+/* The same reductions with the partials in the library's own file-scope
+ * device array (one per device, RED_NB float2): no allocation.  mode 1
+ * argmax, 0 top-2 check.  Concurrent calls on one device share the array.
+ * 0 ok, -6 when the array's address or the launch failed. */
+int32_t dpuf_hip_reduce_noalloc(const float* x, int32_t n, int32_t mode, float thr, int32_t* out, void* s);
 void dpuf_hip_fwht_sign(void* s, int32_t M, int32_t K, const float* x, const uint8_t* sign, float* out);
 void dpuf_hip_slab_pack(void* s, int32_t mc, int32_t K, DpufPrep rows, int32_t* sq, float* ss, int32_t* sm);
 void dpuf_hip_slab_unpack(void* s, int32_t M, int32_t K, const int32_t* sq, const float* ss, const int32_t* sm,

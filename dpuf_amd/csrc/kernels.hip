@@ -16,6 +16,8 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <mutex>
+
 #include "hip_layer.h"
 
 #define DEV __device__ __forceinline__
@@ -3664,6 +3666,46 @@ void dpuf_hip_argmax(void* s, const float* logits, int32_t V, int32_t* out, void
     hipLaunchKernelGGL(k_red_part, dim3(RED_NB), dim3(256), 0, ST(s), logits, V, 1, (float2*)scratch);
     hipLaunchKernelGGL(k_red_fin, dim3(1), dim3(64), 0, ST(s), (const float2*)scratch, 1, 0.0f, out);
     LAUNCHED("k_red_part/k_red_fin (argmax)");
+}
+
+// The allocation-free reduction entry's partials: one file-scope array per
+// device, RED_NB float2 (512 bytes), held until the process ends.  Host code
+// never passes the array's name to a kernel (in host code it is a stand-in,
+// not a device address): each device's address comes from
+// hipGetSymbolAddress, taken once per device with that device current.
+static __device__ __align__(256) float2 scratch[RED_NB];
+#define RED_MAX_DEVICES 64
+static void* g_scratch_ptr[RED_MAX_DEVICES];
+static std::mutex g_scratch_mu;
+
+static float2* scratch_on_current_device(void) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= RED_MAX_DEVICES) {
+        note(hipErrorInvalidDevice, "dpuf_hip_reduce_noalloc: no usable current device");
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            note(e != hipSuccess ? e : hipErrorInvalidSymbol, "hipGetSymbolAddress(scratch)");
+            return nullptr;
+        }
+        g_scratch_ptr[dev] = p;
+    }
+    return (float2*)g_scratch_ptr[dev];
+}
+
+int32_t dpuf_hip_reduce_noalloc(const float* x, int32_t n, int32_t mode, float thr, int32_t* out, void* s) {
+    float2* part = scratch_on_current_device();
+    if (!part) return -6;
+    // every partial slot is written by its workgroup before k_red_fin reads
+    // it, so nothing from an earlier call needs clearing
+    hipLaunchKernelGGL(k_red_part, dim3(RED_NB), dim3(256), 0, ST(s), x, n, mode, part);
+    hipLaunchKernelGGL(k_red_fin, dim3(1), dim3(64), 0, ST(s), (const float2*)part, mode, mode ? 0.0f : thr, out);
+    LAUNCHED("k_red_part/k_red_fin (allocation-free)");
+    return g_err == hipSuccess ? 0 : -6;
 }
 
 void dpuf_hip_fwht_sign(void* s, int32_t M, int32_t K, const float* x, const uint8_t* sign, float* out) {

@@ -89,6 +89,23 @@ DPUF_EXPORT void dpuf_amd_set_gemv_max_workgroups(int32_t n);
  * (dpuf_engine.c:2101-2110).  -1 on error.  For tests. */
 DPUF_EXPORT int32_t dpuf_amd_reduce_check(const float* x, int32_t n, int32_t offset, int32_t mode, float thr);
 
+/* dpuf_amd_reduce_check without allocating: the reduction of n floats
+ * already in device memory (d_x) into one int32 in device memory (d_out),
+ * enqueued on hip_stream (a hipStream_t; NULL is the default stream) without
+ * synchronising.  mode and thr as in dpuf_amd_reduce_check.  The partials
+ * live in a 512-byte array of the library's that each device holds until the
+ * process ends; every call on a device shares it, so calls that overlap on
+ * one device (two streams, two threads) race and must be serialised by the
+ * caller.  n is at most DPUF_AMD_NOALLOC_MAX_N.  Returns 0 when enqueued, -1
+ * bad pointer or mode, -2 n out of range, -6 device error
+ * (dpuf_amd_last_error says which).
+ * No counterpart in the reference: for callers that cannot allocate device
+ * memory -- code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc -- and sample the greedy token on the device. */
+#define DPUF_AMD_NOALLOC_MAX_N (1 << 30)
+DPUF_EXPORT int32_t dpuf_amd_reduce_check_noalloc(const float* d_x, int32_t n, int32_t mode, float thr,
+                                                  int32_t* d_out, void* hip_stream);
+
 /* One next token for each of n sessions in one pass (serving several
  * conversations with one read of the weights): token_ids[i] is appended to
  * KV slot slot_ids[i] (distinct slots, allocated on demand) at positions[i]
