@@ -18,8 +18,10 @@ the default --steps 32).  The same line also reports:
   - the roofline of the dominant kernel (the fused gate+up decode GEMV,
     HBM-bound) timed with HIP events on the engine stream;
   - a CPU baseline: the oracle (a C restatement of the reference AVX2/OpenMP
-    path) on the host cores, on a bounded sample, which also checks the LM-head
-    leg's argmax ids on a sample of its steps.
+    path) on the host cores, on the same prompt (pp32, then greedy decode for a
+    bounded time), whose greedy ids are compared with the GPU's; it also
+    re-checks the LM-head leg's argmax ids on as many steps as fit the budget;
+  - every projection's M = 1 GEMV in isolation (us and GB/s per shape).
 
 Weights for the 8B shape are 4.26 GB per decoded token, far above the 256 MB
 Infinity Cache, so decode reads them from HBM every token.
@@ -117,7 +119,8 @@ def main():
     h = eng.dpuf_engine_create(*model.create_args())
     if not h:
         sys.exit("dpuf_engine_create failed: " + eng.dpuf_amd_last_error().decode())
-    log(f"engine created (weights uploaded to HBM) in {time.time() - t:.1f}s")
+    create_s = time.time() - t
+    log(f"engine created (weights uploaded to HBM) in {create_s:.2f}s")
 
     # --- roofline of the dominant decode kernel ------------------------------
     # The fused gate+up GEMV (one launch per layer, 56.7 MB at the 8B shape) is
@@ -169,12 +172,14 @@ def main():
 
     # --- tg: prompt, warm-up, timed decode through the reference API --------
     tok = prefill()
-    tok = decode(tok, args.prompt, args.warmup)
+    gpu_greedy = [tok]  # greedy ids from the prompt on: the prefill's, then every decoded one
+    tok = decode(tok, args.prompt, args.warmup, gpu_greedy)
     ids = []
     pos = args.prompt + args.warmup
     t0 = time.perf_counter()
     decode(tok, pos, args.steps, ids)
     t1 = time.perf_counter()
+    gpu_greedy += ids
     ms_step = (t1 - t0) * 1e3 / args.steps
     tg = 1e3 / ms_step
     log(f"tg{args.steps}: {ms_step:.3f} ms/token, {tg:.1f} tok/s; ids {ids[:8]}...")
@@ -217,6 +222,20 @@ def main():
     log("per-kind decode time incl. launch gaps (ms/token): " +
         ", ".join(f"{k} {v['ms'] / (args.warmup + args.steps):.3f}" for k, v in kinds.items()))
     rl = roofline()
+
+    # --- isolated M = 1 GEMVs at every projection shape ----------------------
+    # back-to-back launches cycling through all layers' copies of the matrix
+    # (distinct weights each launch: 36 copies are far beyond the 256 MB cache)
+    gemv_shapes = {}
+    for which, name in ((0, "q [4096->4096]"), (1, "k [4096->1024]"), (2, "v [4096->1024]"), (3, "o [4096->4096]"),
+                        (4, "gate [4096->12288]"), (5, "up [4096->12288]"), (6, "down [12288->4096]"),
+                        (9, "q+k+v fused"), (8, "gate+up fused")):
+        by = C.c_double()
+        ms = eng.dpuf_amd_gemv_bench(h, which, 1, 2 * shape["num_layers"], 0, C.byref(by))
+        if ms > 0:
+            gemv_shapes[name] = dict(us=round(ms * 1e3, 3), bytes=by.value,
+                                     GBs=round(by.value / (ms * 1e-3) / 1e9, 1))
+    log("isolated GEMVs (us, GB/s): " + ", ".join(f"{k} {v['us']} {v['GBs']}" for k, v in gemv_shapes.items()))
     all_gemv_ms = sum(kinds[k]["ms"] for k in ("gate_up_gemv", "down_gemv", "qkv_gemv", "o_gemv", "lm_head")
                       if k in kinds)
     all_gemv_bytes = sum(kinds[k]["bytes"] for k in ("gate_up_gemv", "down_gemv", "qkv_gemv", "o_gemv", "lm_head")
@@ -399,51 +418,73 @@ def main():
         for _, he in copies:
             eng.dpuf_engine_destroy(he)
 
-    # --- CPU baseline: the oracle on the host cores, bounded sample ---------
+    # --- CPU baseline: the oracle on the host cores, on the GPU's workload --
+    # The same model and the same 32-token prompt: pp32, then greedy decode
+    # for up to --cpu-seconds; its ids are compared with the GPU's greedy ids
+    # from the same prompt.  Then the oracle re-checks the LM-head leg's argmax
+    # ids (early exit on) for as many of its steps as fit the same budget.
     cpu = None
+    oracle_ids = None
     if args.cpu_seconds > 0:
         from oracle import oracle as O
         o = O.load()
         oh = o.orc_engine_create(*model.create_args())
         lo = np.zeros(V, np.float32)
-        n_prompt = 4
         t0 = time.perf_counter()
-        assert o.orc_engine_forward(oh, n_prompt, M.ptr(prompt[:n_prompt]), 0, None, 1, M.ptr(lo)) == 0
-        t_first = time.perf_counter() - t0
-        n_dec = int(max(1, min(64, args.cpu_seconds / max(t_first / 2, 1e-3))))
-        tok = int(np.argmax(lo))
+        assert o.orc_engine_forward(oh, len(prompt), M.ptr(prompt), 0, None, 1, M.ptr(lo)) == 0
+        t_pp = time.perf_counter() - t0
+        tok = int(o.orc_argmax(M.ptr(lo), V))
+        oracle_ids = [tok]
+        n_dec = 0
         t0 = time.perf_counter()
-        for i in range(n_dec):
+        while n_dec < len(gpu_greedy) - 1 and time.perf_counter() - t0 < args.cpu_seconds:
             tok_arr[0] = tok
-            assert o.orc_engine_forward(oh, 1, M.ptr(tok_arr), n_prompt + i, None, 1, M.ptr(lo)) == 0
-            tok = int(np.argmax(lo))
+            assert o.orc_engine_forward(oh, 1, M.ptr(tok_arr), len(prompt) + n_dec, None, 1, M.ptr(lo)) == 0
+            tok = int(o.orc_argmax(M.ptr(lo), V))
+            oracle_ids.append(tok)
+            n_dec += 1
         dt = time.perf_counter() - t0
         o.orc_engine_destroy(oh)
-        cpu = dict(value=round(n_dec / dt, 3), unit="tok/s", cores=int(o.orc_num_threads()), kind="port",
-                   sample=f"{args.model} greedy decode of {n_dec} tokens after a {n_prompt}-token prompt "
-                          f"(oracle C restatement, OpenMP)")
-        log(f"cpu baseline: {cpu['value']} tok/s on {cpu['cores']} threads")
+        n_cmp = min(len(oracle_ids), len(gpu_greedy))
+        cpu_model = ""
+        try:
+            for ln in open("/proc/cpuinfo"):
+                if ln.startswith("model name"):
+                    cpu_model = ln.split(":", 1)[1].strip()
+                    break
+        except OSError:
+            pass
+        cpu = dict(value=round(n_dec / dt, 3) if n_dec else None, unit="tok/s", cores=int(o.orc_num_threads()),
+                   kind="port", cpu_model=cpu_model, pp_tok_s=round(len(prompt) / t_pp, 3),
+                   sample=f"{args.model} pp{len(prompt)} of the bench's own prompt, then {n_dec} greedy decode "
+                          f"tokens (oracle C restatement of the reference AVX2/OpenMP path, "
+                          f"{o.orc_num_threads()} OpenMP threads)",
+                   greedy_ids_compared=n_cmp, greedy_ids_equal=oracle_ids[:n_cmp] == gpu_greedy[:n_cmp])
+        log(f"cpu baseline: pp{len(prompt)} {cpu['pp_tok_s']} tok/s, decode {cpu['value']} tok/s on "
+            f"{cpu['cores']} threads ({cpu_model}); greedy ids vs GPU: {n_cmp} compared, "
+            f"equal {cpu['greedy_ids_equal']}")
         if lm_inputs is not None:
-            # the oracle's LM head (early exit on) on the first steps that used copy 0
             copies, hs, ids_early = lm_inputs
             os.environ["DPUF_EARLY_TILES"] = str(args.lm_zone)
             os.environ["DPUF_EARLY_MARGIN"] = str(args.lm_margin)
-            lo_m = copies[0][0]
-            oh = o.orc_engine_create(*lo_m.create_args())
+            ohs = [o.orc_engine_create(*c[0].create_args()) for c in copies]
             lo = np.zeros(V, np.float32)
-            steps0 = list(range(0, min(len(hs), 16 * args.lm_copies), args.lm_copies))
-            match = 0
+            match = checked = 0
             t0 = time.perf_counter()
-            for i in steps0:
-                assert o.orc_engine_forward(oh, 1, None, 0, M.ptr(hs[i]), 1, M.ptr(lo)) == 0
+            for i in range(len(hs)):
+                if time.perf_counter() - t0 > args.cpu_seconds:
+                    break
+                assert o.orc_engine_forward(ohs[i % len(ohs)], 1, None, 0, M.ptr(hs[i]), 1, M.ptr(lo)) == 0
                 match += int(o.orc_argmax(M.ptr(lo), V) == ids_early[i])
+                checked += 1
             dt = time.perf_counter() - t0
-            o.orc_engine_destroy(oh)
+            for x in ohs:
+                o.orc_engine_destroy(x)
             del os.environ["DPUF_EARLY_TILES"], os.environ["DPUF_EARLY_MARGIN"]
-            lmh["oracle_ids_checked"] = len(steps0)
+            lmh["oracle_ids_checked"] = checked
             lmh["oracle_ids_match"] = match
-            lmh["oracle_tok_s"] = round(len(steps0) / dt, 2)
-            log(f"LM head oracle check: {match}/{len(steps0)} argmax ids equal, oracle {lmh['oracle_tok_s']} steps/s")
+            lmh["oracle_tok_s"] = round(checked / dt, 2)
+            log(f"LM head oracle check: {match}/{checked} argmax ids equal, oracle {lmh['oracle_tok_s']} steps/s")
 
     line = {
         "metric": "tg32 & pp512 tok/s at Qwen3-8B shape; decode HBM GB/s vs peak",
@@ -464,6 +505,8 @@ def main():
                    "parallelism": "single-gpu"},
         "decode": {"tok_s_reference_api": round(tg, 3), "tok_s_device_argmax_graph": round(1e3 / ms_dev, 3) if ms_dev else None,
                    "ids_match": ids_dev == ids, "weight_bytes_per_token": tok_bytes,
+                   "oracle_greedy_ids_equal": cpu["greedy_ids_equal"] if cpu else None,
+                   "oracle_greedy_ids_compared": cpu["greedy_ids_compared"] if cpu else 0,
                    "effective_GBs": round(decode_gbs, 1), "frac_of_hbm_peak": round(decode_gbs / HBM_PEAK_GBS, 4),
                    "gemv_GBs_all_kinds": round(gemv_gbs, 1),
                    "ms_per_token_by_kind": {k: round(v["ms"] / (args.warmup + args.steps), 4)
@@ -472,9 +515,11 @@ def main():
         "multi_session": multi,
         "long_context": long,
         "lm_head_early_exit": lmh,
+        "gemv_shapes": gemv_shapes,
         "roofline": rl,
         "cpu_baseline": cpu,
         "resident_weight_bytes": wbytes,
+        "create_s": round(create_s, 3),
     }
     print(json.dumps(line), flush=True)
 

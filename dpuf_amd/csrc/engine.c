@@ -162,11 +162,15 @@ static int validate_desc(const DpufWeightDesc* d) {
     for (int32_t t = 0; t < d->n_tiles; t++) {
         uint64_t o = d->tile_offsets[t];
         if (o % 16 != 0 || o + 16 > total) return 0;
+        if (t > 0 && o <= d->tile_offsets[t - 1]) return 0; /* tiles in file order */
         DpufQrTileHdr th;
         memcpy(&th, d->tensor_base + o, sizeof th);
         int32_t want = (t * 16 + 16 <= d->rows) ? 16 : d->rows - t * 16;
         if (th.n_rows != want) return 0;
-        if (o + 16 + (uint64_t)((th.n_rows + 7) / 8) * grp > total) return 0;
+        /* a tile's groups end before the next tile starts (the upload copies
+         * byte ranges of whole tiles) */
+        const uint64_t end = t + 1 < d->n_tiles ? d->tile_offsets[t + 1] : total;
+        if (end <= o || o + 16 + (uint64_t)((th.n_rows + 7) / 8) * grp > end) return 0;
     }
     return 1;
 }
@@ -179,10 +183,86 @@ static void set_devw(DpufDevW* out, const Upload* u, const DpufWeightDesc* d) {
     out->n_groups = (d->rows + 7) / 8;
 }
 
-/* Uploads one validated mode 12 matrix: the .dpuf tile region and its offset
- * table go to a staging buffer, dpuf_hip_relayout writes the row-block
- * layout the kernels read, and the staging buffer is released. */
-static int upload_desc(Engine* e, const DpufWeightDesc* d, DpufDevW* out) {
+/* Weight upload at create: the .dpuf tile bytes go through two pinned host
+ * buffers of UP_CHUNK bytes.  For each chunk of whole tiles the host copies
+ * the bytes out of the caller's (typically mmapped) tensor into one pinned
+ * buffer -- the page-in happens here -- while the DMA engine moves the other
+ * buffer's previous chunk to HBM and k_relayout writes its tiles into the
+ * row-block layout.  A buffer is refilled only after the event recorded
+ * behind its last relayout has fired, and create synchronises once at the
+ * end. */
+#define UP_CHUNK ((size_t)16 << 20)
+
+typedef struct {
+    void* pin[2];        /* pinned host: tile bytes */
+    uint64_t* pin_offs[2];
+    void* dev[2];        /* device: the same chunk, relayout input */
+    uint64_t* dev_offs[2];
+    void* ev[2];
+    int used[2];
+    int next;
+    int32_t max_tiles;   /* capacity of the offset tables */
+} Stager;
+
+static void stager_free(Stager* st) {
+    for (int b = 0; b < 2; b++) {
+        dpuf_hip_host_free(st->pin[b]);
+        dpuf_hip_host_free(st->pin_offs[b]);
+        dpuf_hip_free(st->dev[b]);
+        dpuf_hip_free(st->dev_offs[b]);
+        if (st->ev[b]) dpuf_hip_event_destroy(st->ev[b]);
+    }
+    memset(st, 0, sizeof *st);
+}
+
+static int stager_init(Stager* st) {
+    memset(st, 0, sizeof *st);
+    /* a chunk holds at least one tile: 16 + 2 * (16384 / 32) * 144 bytes at the
+     * widest matrix create accepts, far below UP_CHUNK */
+    st->max_tiles = (int32_t)(UP_CHUNK / 16) + 1;
+    for (int b = 0; b < 2; b++) {
+        st->pin[b] = dpuf_hip_host_alloc(UP_CHUNK);
+        st->pin_offs[b] = (uint64_t*)dpuf_hip_host_alloc((size_t)st->max_tiles * 8u);
+        st->dev[b] = dpuf_hip_malloc(UP_CHUNK);
+        st->dev_offs[b] = (uint64_t*)dpuf_hip_malloc((size_t)st->max_tiles * 8u);
+        st->ev[b] = dpuf_hip_event_create();
+        if (!st->pin[b] || !st->pin_offs[b] || !st->dev[b] || !st->dev_offs[b] || !st->ev[b]) {
+            stager_free(st);
+            return 0;
+        }
+    }
+    return 1;
+}
+
+/* Uploads tiles of d chunk by chunk into the row-block layout at dst. */
+static void stage_tiles(Engine* e, Stager* st, const DpufWeightDesc* d, uint8_t* dst) {
+    const int32_t n_blk = d->cols / 32;
+    const uint64_t gbytes = (uint64_t)n_blk * 144u;
+    int32_t t0 = 0;
+    while (t0 < d->n_tiles) {
+        const uint64_t lo = d->tile_offsets[t0];
+        int32_t t1 = t0 + 1;
+        while (t1 < d->n_tiles && d->tile_offsets[t1 + 1] - lo <= UP_CHUNK && t1 - t0 + 1 < st->max_tiles) t1++;
+        const uint64_t hi = d->tile_offsets[t1];
+        const int b = st->next;
+        st->next ^= 1;
+        if (st->used[b]) dpuf_hip_event_sync(st->ev[b]);
+        memcpy(st->pin[b], d->tensor_base + lo, (size_t)(hi - lo));
+        for (int32_t t = t0; t <= t1; t++) st->pin_offs[b][t - t0] = d->tile_offsets[t] - lo;
+        const int32_t r1 = 16 * t1 < d->rows ? 16 * t1 : d->rows;
+        const int32_t n_groups = (r1 - 16 * t0 + 7) / 8;
+        dpuf_hip_h2d(st->dev[b], st->pin[b], (size_t)(hi - lo), e->stream);
+        dpuf_hip_h2d(st->dev_offs[b], st->pin_offs[b], (size_t)(t1 - t0 + 1) * 8u, e->stream);
+        dpuf_hip_relayout(e->stream, (const uint8_t*)st->dev[b], st->dev_offs[b], n_groups, n_blk,
+                          dst + (size_t)(2 * t0) * gbytes);
+        dpuf_hip_event_record(st->ev[b], e->stream);
+        st->used[b] = 1;
+        t0 = t1;
+    }
+}
+
+/* Uploads one validated mode 12 matrix (tied tensors once). */
+static int upload_desc(Engine* e, Stager* st, const DpufWeightDesc* d, DpufDevW* out) {
     if (!validate_desc(d)) return 0;
     for (int32_t i = 0; i < e->n_ups; i++) {
         if (e->ups[i].host_base == d->tensor_base) {
@@ -195,32 +275,23 @@ static int upload_desc(Engine* e, const DpufWeightDesc* d, DpufDevW* out) {
     u.host_base = d->tensor_base;
     const int32_t n_groups = (d->rows + 7) / 8, n_blk = d->cols / 32;
     u.bytes = (uint64_t)n_groups * (uint64_t)n_blk * 144u;
-    const uint64_t raw = d->tile_offsets[d->n_tiles];
-    void* d_raw = dpuf_hip_malloc((size_t)raw);
-    void* d_offs = dpuf_hip_malloc(((size_t)d->n_tiles + 1) * 8u);
     u.d_groups = dpuf_hip_malloc((size_t)u.bytes);
     if (d->sign_bits) u.d_sign = dpuf_hip_malloc((size_t)d->cols / 8u);
-    if (!d_raw || !d_offs || !u.d_groups || (d->sign_bits && !u.d_sign)) {
-        dpuf_hip_free(d_raw); dpuf_hip_free(d_offs); dpuf_hip_free(u.d_groups); dpuf_hip_free(u.d_sign);
-        return 0;
-    }
-    dpuf_hip_h2d(d_raw, d->tensor_base, (size_t)raw, e->stream);
-    dpuf_hip_h2d(d_offs, d->tile_offsets, ((size_t)d->n_tiles + 1) * 8u, e->stream);
-    if (d->sign_bits) dpuf_hip_h2d(u.d_sign, d->sign_bits, (size_t)d->cols / 8u, e->stream);
-    dpuf_hip_relayout(e->stream, (const uint8_t*)d_raw, (const uint64_t*)d_offs, n_groups, n_blk,
-                      (uint8_t*)u.d_groups);
-    /* synchronous: the caller's pageable buffers may be released after create */
-    const int ok = dpuf_hip_sync(e->stream) == 0;
-    dpuf_hip_free(d_raw);
-    dpuf_hip_free(d_offs);
-    if (!ok) {
+    if (!u.d_groups || (d->sign_bits && !u.d_sign)) {
         dpuf_hip_free(u.d_groups); dpuf_hip_free(u.d_sign);
         return 0;
     }
-    e->ups = (Upload*)realloc(e->ups, (size_t)(e->n_ups + 1) * sizeof(Upload));
-    e->ups[e->n_ups++] = u;
+    Upload* grown = (Upload*)realloc(e->ups, (size_t)(e->n_ups + 1) * sizeof(Upload));
+    if (!grown) {
+        dpuf_hip_free(u.d_groups); dpuf_hip_free(u.d_sign);
+        return 0;
+    }
+    e->ups = grown;
+    e->ups[e->n_ups++] = u;  /* owned by the engine from here on, also on failure */
+    if (d->sign_bits) dpuf_hip_h2d(u.d_sign, d->sign_bits, (size_t)d->cols / 8u, e->stream);
+    stage_tiles(e, st, d, (uint8_t*)u.d_groups);
     set_devw(out, &u, d);
-    return 1;
+    return dpuf_hip_ok();
 }
 
 static float* upload_floats(Engine* e, const float* src, size_t n) {
@@ -350,6 +421,8 @@ DPUF_EXPORT void* dpuf_engine_create(const DpufModelConfig* cfg, const DpufLayer
     if (dpuf_hip_device_count() <= 0) return NULL;
     Engine* e = (Engine*)calloc(1, sizeof(Engine));
     if (!e) return NULL;
+    Stager stg;
+    memset(&stg, 0, sizeof stg);
     e->cfg = *cfg;
     e->L = cfg->num_layers;
     e->H = cfg->hidden_size;
@@ -373,7 +446,8 @@ DPUF_EXPORT void* dpuf_engine_create(const DpufModelConfig* cfg, const DpufLayer
     if (!e->lw || !e->d_norm || !e->q_idx) goto fail;
     if (w_tok_embd->rows != e->V || w_tok_embd->cols != e->H || w_lm_head->rows != e->V || w_lm_head->cols != e->H)
         goto fail;
-    if (!upload_desc(e, w_tok_embd, &e->tok) || !upload_desc(e, w_lm_head, &e->lm)) goto fail;
+    if (!stager_init(&stg)) goto fail;
+    if (!upload_desc(e, &stg, w_tok_embd, &e->tok) || !upload_desc(e, &stg, w_lm_head, &e->lm)) goto fail;
     for (int32_t l = 0; l < e->L; l++) {
         const DpufLayerWeights* lw = &layers[l];
         const DpufWeightDesc* ds[7] = {&lw->w_q, &lw->w_k, &lw->w_v, &lw->w_o, &lw->w_gate, &lw->w_up, &lw->w_down};
@@ -381,7 +455,7 @@ DPUF_EXPORT void* dpuf_engine_create(const DpufModelConfig* cfg, const DpufLayer
         const int32_t want_c[7] = {e->H, e->H, e->H, e->qd, e->H, e->H, e->I};
         for (int k = 0; k < 7; k++) {
             if (ds[k]->rows != want_r[k] || ds[k]->cols != want_c[k]) goto fail;
-            if (!upload_desc(e, ds[k], &e->lw[(size_t)l * 7 + k])) goto fail;
+            if (!upload_desc(e, &stg, ds[k], &e->lw[(size_t)l * 7 + k])) goto fail;
         }
         if (!lw->attn_norm || !lw->ffn_norm) goto fail;
         e->d_norm[4 * l + 0] = upload_floats(e, lw->attn_norm, (size_t)e->H);
@@ -451,8 +525,11 @@ DPUF_EXPORT void* dpuf_engine_create(const DpufModelConfig* cfg, const DpufLayer
     }
     if (!slot_alloc(e, 0)) goto fail;
     if (dpuf_hip_sync(e->stream) != 0) goto fail;
+    stager_free(&stg);
     return e;
 fail:
+    if (e->stream) dpuf_hip_sync(e->stream);
+    stager_free(&stg);
     engine_free(e);
     return NULL;
 }

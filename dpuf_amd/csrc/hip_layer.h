@@ -66,6 +66,7 @@ void* dpuf_hip_event_create(void);
 void  dpuf_hip_event_destroy(void* e);
 void  dpuf_hip_event_record(void* e, void* s);
 float dpuf_hip_event_elapsed_ms(void* a, void* b);   /* synchronises on b */
+void  dpuf_hip_event_sync(void* e);                  /* waits for the work before e */
 
 /* Graph capture of a stream into a replayable executable graph. */
 int32_t dpuf_hip_capture_begin(void* s);

@@ -3148,6 +3148,7 @@ void* dpuf_hip_event_create(void) {
 }
 void dpuf_hip_event_destroy(void* e) { if (e) CK(hipEventDestroy((hipEvent_t)e)); }
 void dpuf_hip_event_record(void* e, void* s) { CK(hipEventRecord((hipEvent_t)e, ST(s))); }
+void dpuf_hip_event_sync(void* e) { CK(hipEventSynchronize((hipEvent_t)e)); }
 float dpuf_hip_event_elapsed_ms(void* a, void* b) {
     float ms = 0.0f;
     CK(hipEventSynchronize((hipEvent_t)b));
