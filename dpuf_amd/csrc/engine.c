@@ -43,11 +43,14 @@ typedef struct {
     float* d_out_norm;
     float* d_cos;
     float* d_sin;
-    float* kc[N_SLOTS];
-    float* vc[N_SLOTS];
+    /* KV cache arrays per slot and per frozen prefix, [L][n_kv][positions]
+     * rows of kv_row[i] bytes: fp32 K, V (kv_type 0), or int8 K, V and their
+     * per-32 fp32 scales (kv_type 1, dpuf_engine.c:1182-1206) */
+    int32_t kv_n;
+    size_t kv_row[4];
+    void* kv[N_SLOTS][4];
     int32_t active;
-    float* pk[N_PREFIX];
-    float* pv[N_PREFIX];
+    void* pkv[N_PREFIX][4];
     int32_t plen[N_PREFIX], pcap[N_PREFIX], pvalid[N_PREFIX];
     /* scratch for up to DPUF_AMD_MAX_BATCH rows */
     float *h, *hn, *q, *k, *v, *ao, *gate, *up, *logits, *scores, *embeds, *capture;
@@ -346,23 +349,71 @@ static int rope_tables(Engine* e) {
     return ok;
 }
 
-static size_t kv_floats(const Engine* e) {
-    return (size_t)e->L * (size_t)e->nkv * (size_t)e->max_seq * (size_t)e->hd;
+static int is_q8(const Engine* e) { return e->cfg.kv_type == DPUF_KV_Q8; }
+
+static void kv_layout(Engine* e) {
+    const size_t hd = (size_t)e->hd;
+    if (is_q8(e)) {
+        e->kv_n = 4;
+        e->kv_row[0] = e->kv_row[1] = hd;
+        e->kv_row[2] = e->kv_row[3] = (hd / 32) * sizeof(float);
+    } else {
+        e->kv_n = 2;
+        e->kv_row[0] = e->kv_row[1] = hd * sizeof(float);
+    }
+}
+
+/* Bytes of KV array i for `len` positions of every (layer, kv head). */
+static size_t kv_bytes(const Engine* e, int i, int32_t len) {
+    return (size_t)e->L * (size_t)e->nkv * (size_t)len * e->kv_row[i];
+}
+
+static float* slot_k(const Engine* e, int32_t s) { return (float*)e->kv[s][0]; }
+static float* slot_v(const Engine* e, int32_t s) { return (float*)e->kv[s][1]; }
+
+/* The int8 cache of layer l of slot s. */
+static DpufKvQ8 slot_q8(const Engine* e, int32_t s, int32_t l) {
+    const size_t rows = (size_t)l * e->nkv * e->max_seq;
+    DpufKvQ8 c;
+    c.kq = (int8_t*)e->kv[s][0] + rows * e->kv_row[0];
+    c.vq = (int8_t*)e->kv[s][1] + rows * e->kv_row[1];
+    c.ks = (float*)((uint8_t*)e->kv[s][2] + rows * e->kv_row[2]);
+    c.vs = (float*)((uint8_t*)e->kv[s][3] + rows * e->kv_row[3]);
+    return c;
+}
+
+static void kv_free(void* a[4]) {
+    for (int i = 0; i < 4; i++) {
+        dpuf_hip_free(a[i]);
+        a[i] = NULL;
+    }
 }
 
 static int slot_alloc(Engine* e, int32_t s) {
-    if (e->kc[s]) return 1;
-    size_t n = kv_floats(e);
-    e->kc[s] = (float*)dpuf_hip_malloc(n * sizeof(float));
-    e->vc[s] = (float*)dpuf_hip_malloc(n * sizeof(float));
-    if (!e->kc[s] || !e->vc[s]) {
-        dpuf_hip_free(e->kc[s]); dpuf_hip_free(e->vc[s]);
-        e->kc[s] = e->vc[s] = NULL;
-        return 0;
+    if (e->kv[s][0]) return 1;
+    for (int i = 0; i < e->kv_n; i++) {
+        e->kv[s][i] = dpuf_hip_malloc(kv_bytes(e, i, e->max_seq));
+        if (!e->kv[s][i]) {
+            kv_free(e->kv[s]);
+            return 0;
+        }
+        dpuf_hip_fill_zero(e->kv[s][i], kv_bytes(e, i, e->max_seq), e->stream);
     }
-    dpuf_hip_fill_zero(e->kc[s], n * sizeof(float), e->stream);
-    dpuf_hip_fill_zero(e->vc[s], n * sizeof(float), e->stream);
     return dpuf_hip_sync(e->stream) == 0;
+}
+
+/* Positions [0, len) of every (layer, kv head) between a slot ([..][max_seq]
+ * rows) and a prefix ([..][len] rows), to_prefix selecting the direction. */
+static void prefix_copy(Engine* e, int32_t s, int32_t p, int32_t len, int to_prefix) {
+    for (int i = 0; i < e->kv_n; i++) {
+        const size_t rb = e->kv_row[i];
+        for (int32_t lh = 0; lh < e->L * e->nkv; lh++) {
+            uint8_t* so = (uint8_t*)e->kv[s][i] + (size_t)lh * e->max_seq * rb;
+            uint8_t* po = (uint8_t*)e->pkv[p][i] + (size_t)lh * len * rb;
+            if (to_prefix) dpuf_hip_d2d(po, so, (size_t)len * rb, e->stream);
+            else dpuf_hip_d2d(so, po, (size_t)len * rb, e->stream);
+        }
+    }
 }
 
 static void engine_free(Engine* e) {
@@ -381,8 +432,8 @@ static void engine_free(Engine* e) {
     free(e->lw);
     free(e->q_idx);
     dpuf_hip_free(e->d_out_norm); dpuf_hip_free(e->d_cos); dpuf_hip_free(e->d_sin);
-    for (int s = 0; s < N_SLOTS; s++) { dpuf_hip_free(e->kc[s]); dpuf_hip_free(e->vc[s]); }
-    for (int p = 0; p < N_PREFIX; p++) { dpuf_hip_free(e->pk[p]); dpuf_hip_free(e->pv[p]); }
+    for (int s = 0; s < N_SLOTS; s++) kv_free(e->kv[s]);
+    for (int p = 0; p < N_PREFIX; p++) kv_free(e->pkv[p]);
     float* bufs[] = {e->h, e->hn, e->q, e->k, e->v, e->ao, e->gate, e->up, e->logits, e->scores, e->embeds, e->capture};
     for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++) dpuf_hip_free(bufs[i]);
     for (int i = 0; i < 3; i++) {
@@ -414,7 +465,7 @@ DPUF_EXPORT void* dpuf_engine_create(const DpufModelConfig* cfg, const DpufLayer
         (cfg->head_dim != 64 && cfg->head_dim != 128 && cfg->head_dim != 256) || cfg->num_kv_heads <= 0 ||
         cfg->num_q_heads <= 0 || (cfg->num_q_heads % cfg->num_kv_heads) != 0 ||
         cfg->num_q_heads / cfg->num_kv_heads > 32 || cfg->max_seq_len <= 0 || cfg->vocab_size <= 0 ||
-        cfg->kv_type != DPUF_KV_F32 || cfg->has_mrope || (cfg->hidden_size % 64) != 0 ||
+        (cfg->kv_type != DPUF_KV_F32 && cfg->kv_type != DPUF_KV_Q8) || cfg->has_mrope || (cfg->hidden_size % 64) != 0 ||
         cfg->hidden_size < 128 || cfg->hidden_size > 16384 ||
         (cfg->intermediate_size % 64) != 0)
         return NULL;
@@ -434,6 +485,7 @@ DPUF_EXPORT void* dpuf_engine_create(const DpufModelConfig* cfg, const DpufLayer
     e->kvd = e->nkv * e->hd;
     e->V = cfg->vocab_size;
     e->max_seq = cfg->max_seq_len;
+    kv_layout(e);
     const char* dz = getenv("DPUF_SWIGLU_DEADZONE");
     e->deadzone = dz ? (float)atof(dz) : 0.005f;
     e->stream = dpuf_hip_stream_create();
@@ -555,10 +607,8 @@ DPUF_EXPORT int32_t dpuf_engine_num_slots(void* handle) { return handle ? N_SLOT
 DPUF_EXPORT void dpuf_engine_reset_slot(void* handle, int32_t slot_id) {
     dpuf_hip_clear_error();
     Engine* e = (Engine*)handle;
-    if (!e || slot_id < 0 || slot_id >= N_SLOTS || !e->kc[slot_id]) return;
-    size_t n = kv_floats(e) * sizeof(float);
-    dpuf_hip_fill_zero(e->kc[slot_id], n, e->stream);
-    dpuf_hip_fill_zero(e->vc[slot_id], n, e->stream);
+    if (!e || slot_id < 0 || slot_id >= N_SLOTS || !e->kv[slot_id][0]) return;
+    for (int i = 0; i < e->kv_n; i++) dpuf_hip_fill_zero(e->kv[slot_id][i], kv_bytes(e, i, e->max_seq), e->stream);
     dpuf_hip_sync(e->stream);
 }
 
@@ -571,7 +621,9 @@ DPUF_EXPORT void dpuf_engine_reset_cache(void* handle) {
 DPUF_EXPORT size_t dpuf_engine_slot_memory(void* handle) {
     Engine* e = (Engine*)handle;
     if (!e) return 0;
-    return 2 * kv_floats(e) * sizeof(float);
+    size_t n = 0;
+    for (int i = 0; i < e->kv_n; i++) n += kv_bytes(e, i, e->max_seq);
+    return n;
 }
 
 /* Prefix caches are [L][kv head][len][hd] (dpuf_engine.c:1471-1600). */
@@ -579,29 +631,22 @@ DPUF_EXPORT int32_t dpuf_engine_freeze_prefix(void* handle, int32_t pfx_id, int3
     dpuf_hip_clear_error();
     Engine* e = (Engine*)handle;
     if (!e || pfx_id < 0 || pfx_id >= N_PREFIX || prefix_len <= 0 || prefix_len > e->max_seq) return 0;
-    if (e->pcap[pfx_id] < prefix_len || !e->pk[pfx_id]) {
-        dpuf_hip_free(e->pk[pfx_id]); dpuf_hip_free(e->pv[pfx_id]);
-        size_t n = (size_t)e->L * e->nkv * (size_t)prefix_len * e->hd * sizeof(float);
-        e->pk[pfx_id] = (float*)dpuf_hip_malloc(n);
-        e->pv[pfx_id] = (float*)dpuf_hip_malloc(n);
+    /* a prefix's arrays hold exactly its length: [L][kv head][len] rows */
+    if (e->pcap[pfx_id] != prefix_len || !e->pkv[pfx_id][0]) {
+        kv_free(e->pkv[pfx_id]);
         e->pvalid[pfx_id] = 0;
         e->pcap[pfx_id] = 0;
-        if (!e->pk[pfx_id] || !e->pv[pfx_id]) {
-            dpuf_hip_free(e->pk[pfx_id]); dpuf_hip_free(e->pv[pfx_id]);
-            e->pk[pfx_id] = e->pv[pfx_id] = NULL;
-            return 0;
+        for (int i = 0; i < e->kv_n; i++) {
+            e->pkv[pfx_id][i] = dpuf_hip_malloc(kv_bytes(e, i, prefix_len));
+            if (!e->pkv[pfx_id][i]) {
+                kv_free(e->pkv[pfx_id]);
+                return 0;
+            }
         }
         e->pcap[pfx_id] = prefix_len;
     }
-    if (!e->kc[e->active]) return 0;
-    const size_t hd = (size_t)e->hd, chunk = (size_t)prefix_len * hd * sizeof(float);
-    for (int32_t l = 0; l < e->L; l++)
-        for (int32_t h = 0; h < e->nkv; h++) {
-            size_t po = ((size_t)l * e->nkv + h) * (size_t)prefix_len * hd;
-            size_t so = ((size_t)l * e->nkv + h) * (size_t)e->max_seq * hd;
-            dpuf_hip_d2d(e->pk[pfx_id] + po, e->kc[e->active] + so, chunk, e->stream);
-            dpuf_hip_d2d(e->pv[pfx_id] + po, e->vc[e->active] + so, chunk, e->stream);
-        }
+    if (!e->kv[e->active][0]) return 0;
+    prefix_copy(e, e->active, pfx_id, prefix_len, 1);
     if (dpuf_hip_sync(e->stream) != 0) return 0;
     e->plen[pfx_id] = prefix_len;
     e->pvalid[pfx_id] = 1;
@@ -615,14 +660,7 @@ DPUF_EXPORT int32_t dpuf_engine_apply_prefix(void* handle, int32_t slot_id, int3
     if (!e->pvalid[pfx_id] || e->plen[pfx_id] <= 0) return 0;
     if (!slot_alloc(e, slot_id)) return 0;
     const int32_t len = e->plen[pfx_id];
-    const size_t hd = (size_t)e->hd, chunk = (size_t)len * hd * sizeof(float);
-    for (int32_t l = 0; l < e->L; l++)
-        for (int32_t h = 0; h < e->nkv; h++) {
-            size_t po = ((size_t)l * e->nkv + h) * (size_t)len * hd;
-            size_t so = ((size_t)l * e->nkv + h) * (size_t)e->max_seq * hd;
-            dpuf_hip_d2d(e->kc[slot_id] + so, e->pk[pfx_id] + po, chunk, e->stream);
-            dpuf_hip_d2d(e->vc[slot_id] + so, e->pv[pfx_id] + po, chunk, e->stream);
-        }
+    prefix_copy(e, slot_id, pfx_id, len, 0);
     if (dpuf_hip_sync(e->stream) != 0) return 0;
     return len;
 }
@@ -685,8 +723,9 @@ static void enqueue_layers(Engine* e, int32_t M, int32_t keep_tiles) {
     for (int32_t l = 0; l < e->L; l++) {
         const DpufDevW* W = e->lw + (size_t)l * 7;
         const uint8_t* qi = e->q_idx + (size_t)l * 5;
-        float* kc = e->kc[e->active] + (size_t)l * e->nkv * e->max_seq * e->hd;
-        float* vc = e->vc[e->active] + (size_t)l * e->nkv * e->max_seq * e->hd;
+        const size_t lo = (size_t)l * e->nkv * e->max_seq * e->hd;
+        float* kc = is_q8(e) ? NULL : slot_k(e, e->active) + lo;
+        float* vc = is_q8(e) ? NULL : slot_v(e, e->active) + lo;
 
         /* (1) [h += down] + attn RMSNorm + prep of the Q/K/V input */
         {
@@ -715,7 +754,17 @@ static void enqueue_layers(Engine* e, int32_t M, int32_t keep_tiles) {
         {
             const int tm = tm_begin(e, K_ATTN, 0);
             int fused = 0;
-            if (e->ms_n > 0)  /* one token per session, each with its own cache */
+            if (is_q8(e)) {
+                /* int8 KV cache: QK-norm + RoPE + quantising store, then the
+                 * int8-cache attention (dpuf_engine.c:1800-1806, 595-752) */
+                const DpufKvQ8 c8 = slot_q8(e, e->active, l);
+                dpuf_hip_qk_rope_kv(s, M, e->q, e->k, e->v, e->d_norm[4 * l + 1], e->d_norm[4 * l + 2], eps,
+                                    e->d_cos, e->d_sin, NULL, NULL, e->d_pos0, e->nq, e->nkv, e->hd, e->max_seq, &c8);
+                dpuf_hip_attn_q8(s, M, e->q, c8, e->ao, e->scores, e->d_pos0, e->nq, e->nkv, e->hd, e->max_seq,
+                                 scale);
+                dpuf_hip_prep(s, M, e->qd, e->ao, W[W_O].sign, e->prep[0]);
+                fused = 1;
+            } else if (e->ms_n > 0)  /* one token per session, each with its own cache */
                 fused = dpuf_hip_attn_dec(s, M, e->q, e->k, e->v, e->d_norm[4 * l + 1], e->d_norm[4 * l + 2], eps,
                                           e->d_cos, e->d_sin, NULL, NULL, e->d_ms_pos, e->nq, e->nkv, e->hd,
                                           e->max_seq, scale, e->scores, e->ao, W[W_O].sign, e->prep[0], e->d_ms_kc,
@@ -726,7 +775,7 @@ static void enqueue_layers(Engine* e, int32_t M, int32_t keep_tiles) {
                                           scale, e->scores, e->ao, W[W_O].sign, e->prep[0], NULL, NULL, 0) == 0;
             if (!fused) {
                 dpuf_hip_qk_rope_kv(s, M, e->q, e->k, e->v, e->d_norm[4 * l + 1], e->d_norm[4 * l + 2], eps,
-                                    e->d_cos, e->d_sin, kc, vc, e->d_pos0, e->nq, e->nkv, e->hd, e->max_seq);
+                                    e->d_cos, e->d_sin, kc, vc, e->d_pos0, e->nq, e->nkv, e->hd, e->max_seq, NULL);
                 const int32_t lmax = e->capturing ? e->max_seq : e->host_pos0 + M;
                 /* the O-input prep rides with the prefill softmax + P.V
                  * kernel when it can; otherwise it is a launch of its own */
@@ -938,6 +987,7 @@ DPUF_EXPORT int32_t dpuf_amd_engine_forward_slots(void* handle, int32_t n, const
     if (!e || n <= 0 || !slot_ids || !token_ids || !positions || (!logits_out && !tokens_out)) return -1;
     if (n > DPUF_AMD_MAX_BATCH) return -2;
     if (e->hd != 64 && e->hd != 128 && e->hd != 256) return -5;
+    if (is_q8(e)) return -5; /* the one-token-per-session attention reads the fp32 cache */
     for (int32_t i = 0; i < n; i++) {
         if (slot_ids[i] < 0 || slot_ids[i] >= N_SLOTS) return -1;
         for (int32_t j = 0; j < i; j++)
@@ -950,8 +1000,8 @@ DPUF_EXPORT int32_t dpuf_amd_engine_forward_slots(void* handle, int32_t n, const
     if (!ptrs) return -2;
     begin_call(e);
     for (int32_t i = 0; i < n; i++) {
-        ptrs[i] = e->kc[slot_ids[i]];
-        ptrs[n + i] = e->vc[slot_ids[i]];
+        ptrs[i] = slot_k(e, slot_ids[i]);
+        ptrs[n + i] = slot_v(e, slot_ids[i]);
     }
     int32_t* hp = e->h_pinned;
     for (int32_t i = 0; i < n; i++) hp[8 + i] = token_ids[i];
@@ -1001,8 +1051,21 @@ DPUF_EXPORT int32_t dpuf_amd_engine_set_kv(void* handle, int32_t layer, int32_t 
         return -1;
     dpuf_hip_clear_error();
     size_t off = (((size_t)layer * e->nkv + kvh) * (size_t)e->max_seq + pos0) * e->hd;
-    dpuf_hip_h2d(e->kc[e->active] + off, k, (size_t)n * e->hd * 4, e->stream);
-    dpuf_hip_h2d(e->vc[e->active] + off, v, (size_t)n * e->hd * 4, e->stream);
+    if (is_q8(e)) {
+        /* quantised on the device exactly as the KV store does */
+        if (n == 0) return 0;
+        float* tmp = (float*)dpuf_hip_malloc((size_t)n * e->hd * 8);
+        if (!tmp) return -1;
+        dpuf_hip_h2d(tmp, k, (size_t)n * e->hd * 4, e->stream);
+        dpuf_hip_h2d(tmp + (size_t)n * e->hd, v, (size_t)n * e->hd * 4, e->stream);
+        dpuf_hip_q8_rows(e->stream, tmp, tmp + (size_t)n * e->hd, n, e->hd, slot_q8(e, e->active, 0),
+                         off / (size_t)e->hd);
+        const int32_t rc = dpuf_hip_sync(e->stream);
+        dpuf_hip_free(tmp);
+        return rc;
+    }
+    dpuf_hip_h2d(slot_k(e, e->active) + off, k, (size_t)n * e->hd * 4, e->stream);
+    dpuf_hip_h2d(slot_v(e, e->active) + off, v, (size_t)n * e->hd * 4, e->stream);
     return dpuf_hip_sync(e->stream);
 }
 
@@ -1014,8 +1077,20 @@ DPUF_EXPORT int32_t dpuf_amd_engine_get_kv(void* handle, int32_t layer, int32_t 
         return -1;
     dpuf_hip_clear_error();
     size_t off = (((size_t)layer * e->nkv + kvh) * (size_t)e->max_seq + pos0) * e->hd;
-    dpuf_hip_d2h(k, e->kc[e->active] + off, (size_t)n * e->hd * 4, e->stream);
-    dpuf_hip_d2h(v, e->vc[e->active] + off, (size_t)n * e->hd * 4, e->stream);
+    if (is_q8(e)) { /* dequantised: q * scale */
+        if (n == 0) return 0;
+        float* tmp = (float*)dpuf_hip_malloc((size_t)n * e->hd * 8);
+        if (!tmp) return -1;
+        dpuf_hip_q8_dequant(e->stream, slot_q8(e, e->active, 0), off, (size_t)n * e->hd, tmp,
+                            tmp + (size_t)n * e->hd);
+        dpuf_hip_d2h(k, tmp, (size_t)n * e->hd * 4, e->stream);
+        dpuf_hip_d2h(v, tmp + (size_t)n * e->hd, (size_t)n * e->hd * 4, e->stream);
+        const int32_t rc = dpuf_hip_sync(e->stream);
+        dpuf_hip_free(tmp);
+        return rc;
+    }
+    dpuf_hip_d2h(k, slot_k(e, e->active) + off, (size_t)n * e->hd * 4, e->stream);
+    dpuf_hip_d2h(v, slot_v(e, e->active) + off, (size_t)n * e->hd * 4, e->stream);
     return dpuf_hip_sync(e->stream);
 }
 

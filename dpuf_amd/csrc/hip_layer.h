@@ -34,6 +34,15 @@ typedef struct {
     uint16_t* h;
 } DpufPrep;
 
+/* One layer's int8 KV cache (kv_type 1): K and V [n_kv][max_seq][hd] int8
+ * with per-32-column scales [n_kv][max_seq][hd / 32]. */
+typedef struct {
+    int8_t* kq;
+    int8_t* vq;
+    float* ks;
+    float* vs;
+} DpufKvQ8;
+
 /* One matrix of a fused GEMV launch: groups [g0, g1) of w, reading prep p,
  * writing out[m * ldo + row]. */
 typedef struct {
@@ -105,7 +114,10 @@ void dpuf_hip_bind_error_word(int32_t* d_word);
 void dpuf_hip_qk_rope_kv(void* s, int32_t M, float* q, float* k, const float* v,
                          const float* q_norm, const float* k_norm, float eps,
                          const float* cos_tab, const float* sin_tab, float* kc, float* vc,
-                         const int32_t* pos0, int32_t n_q, int32_t n_kv, int32_t hd, int32_t max_seq);
+                         const int32_t* pos0, int32_t n_q, int32_t n_kv, int32_t hd, int32_t max_seq,
+                         const DpufKvQ8* c8);
+/* With c8 set, K (after QK-norm and RoPE) and V go into the int8 cache
+ * instead of kc / vc. */
 void dpuf_hip_attn(void* s, int32_t M, const float* q, const float* kc, const float* vc, float* out,
                    float* scores, const int32_t* pos0, int32_t n_q, int32_t n_kv, int32_t hd,
                    int32_t max_seq, float scale);
@@ -116,6 +128,14 @@ void dpuf_hip_attn(void* s, int32_t M, const float* q, const float* kc, const fl
 int32_t dpuf_hip_attn_split(void* s, int32_t M, int32_t lmax, const float* q, const float* kc, const float* vc,
                             float* out, float* scores, const int32_t* pos0p, int32_t n_q, int32_t n_kv, int32_t hd,
                             int32_t max_seq, float scale, const uint8_t* o_sign, DpufPrep op, int32_t* prepped);
+/* Attention over the int8 KV cache (kv_type 1) for M tokens at positions
+ * pos0 .. pos0 + M - 1 of one layer. */
+void dpuf_hip_attn_q8(void* s, int32_t M, const float* q, DpufKvQ8 c8, float* out, float* scores,
+                      const int32_t* pos0, int32_t n_q, int32_t n_kv, int32_t hd, int32_t max_seq, float scale);
+/* n rows of fp32 K and V (device) quantised into rows row0 .. of the int8
+ * cache, as the KV store does; and n values from element off dequantised. */
+void dpuf_hip_q8_rows(void* s, const float* k, const float* v, int32_t n, int32_t hd, DpufKvQ8 c8, size_t row0);
+void dpuf_hip_q8_dequant(void* s, DpufKvQ8 c8, size_t off, size_t n, float* k, float* v);
 /* One-token-per-session fused QK-norm + RoPE + KV store + attention +
  * O-input prep for M tokens: token m at position pos0[m]; with kcs / vcs set
  * (device arrays of M session KV-cache bases, plus l_off floats) each token

@@ -1564,14 +1564,34 @@ __global__ __launch_bounds__(64 * (SK_NP + SK_NC)) void k_gemm_skp(GmArgs A) {
 // pair (i, i + HD/2) sits in one lane for HD >= 128 and in lanes l, l ^ 32
 // for HD = 64; the norm's 8 accumulator chains (lane j: elements j, j + 8,
 // ... in order) gather their elements by shuffles, the hsum tree follows.
-template <int HD>
+// Int8 KV cache store of one value per lane (quantize_vec_q8_blk32,
+// dpuf_engine.c:754-781): a wave's lanes 0-31 and 32-63 each hold one
+// 32-block (elements 64e .. 64e+31 and 64e+32 .. 64e+63); amax over the half
+// wave, q = RNE(x * (127 / amax)) saturated to [-127, 127] (a value the
+// conversion cannot represent gives -127), scale amax / 127 stored by the
+// half's first lane.  amax <= 1e-12 gives q = 0.
+DEV void q8_store_lane(float val, int lane, int e, int8_t* row, float* srow) {
+    float a = fabsf(val);
+#pragma unroll
+    for (int o = 1; o < 32; o <<= 1) a = fmaxf(a, __shfl_xor(a, o, 64));
+    const float inv = a > 1e-12f ? 127.0f / a : 0.0f;
+    const float x = val * inv;
+    int qv;
+    if (!(x > -2147483648.0f && x < 2147483648.0f)) qv = -127;
+    else qv = (int)rintf(x);
+    qv = qv > 127 ? 127 : (qv < -127 ? -127 : qv);
+    row[lane + 64 * e] = (int8_t)qv;
+    if ((lane & 31) == 0) srow[2 * e + (lane >> 5)] = a / 127.0f;
+}
+
+template <int HD, bool Q8>
 __global__ __launch_bounds__(256) void k_qk_rope_kv_w(float* __restrict__ q, float* __restrict__ k,
                                                       const float* __restrict__ v, const float* __restrict__ qn,
                                                       const float* __restrict__ kn, float eps,
                                                       const float* __restrict__ cos_tab,
                                                       const float* __restrict__ sin_tab, float* __restrict__ kc,
                                                       float* __restrict__ vc, const int32_t* __restrict__ pos0p, int M,
-                                                      int n_q, int n_kv, int max_seq) {
+                                                      int n_q, int n_kv, int max_seq, DpufKvQ8 c8) {
     constexpr int E = HD / 64, half = HD / 2;
     const int lane = threadIdx.x & 63;
     const int u = blockIdx.x * 4 + (threadIdx.x >> 6);  // (token, head) unit of this wave
@@ -1622,7 +1642,14 @@ __global__ __launch_bounds__(256) void k_qk_rope_kv_w(float* __restrict__ q, flo
     }
 #pragma unroll
     for (int e = 0; e < E; e++) vec[lane + 64 * e] = o[e];
-    if (is_k) {
+    if (is_k && Q8) {
+        const size_t row = (size_t)hh * max_seq + pos;
+#pragma unroll
+        for (int e = 0; e < E; e++) {
+            q8_store_lane(o[e], lane, e, c8.kq + row * HD, c8.ks + row * (HD / 32));
+            q8_store_lane(vv[e], lane, e, c8.vq + row * HD, c8.vs + row * (HD / 32));
+        }
+    } else if (is_k) {
 #pragma unroll
         for (int e = 0; e < E; e++) {
             const size_t off = ((size_t)hh * max_seq + pos) * HD + lane + 64 * e;
@@ -2408,6 +2435,168 @@ __global__ __launch_bounds__(256) void k_attn(const float* __restrict__ q, const
             for (int t = 0; t < kv_len; t++) a = fmaf(p[t], V[(size_t)t * hd + d], a);
         }
         out[((size_t)m * n_q + qh0 + hsel) * hd + d] = a;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Attention over the int8 KV cache (kv_type 1; reference
+// gqa_attn_head_pair_q8, dpuf_engine.c:579-752), one workgroup per (token,
+// kv head, query-head pair), any M.  Scores: a key of the pair path (keys in
+// pairs t, t + 1 while t + 1 < kv_len) keeps 8 lane accumulators, per
+// 32-block t = fma(q_lo, k_lo, fma(q_hi, k_hi, t)) over the block's two
+// 16-column halves then s = fma(t, k_scale, s), summed by the hadd tree; the
+// pair path's last odd key and every key of the single-head path use
+// dot_f32_q8_blk32's two accumulators per block and eng_hsum256.  Softmax as
+// the fp32 path.  P.V: a = fma(p_k * v_scale[k][block], float(v[k][d]), a),
+// keys in order.
+// ---------------------------------------------------------------------------
+DEV float q8_pair_score(const float* q, const int8_t* kp, const float* ks, int hd) {
+    float sa[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int b = 0; b < (hd >> 5); b++) {
+        const int c0 = 32 * b;
+        const int4 kw0 = *(const int4*)(kp + c0), kw1 = *(const int4*)(kp + c0 + 16);
+        const int8_t* k0 = (const int8_t*)&kw0;
+        const int8_t* k1 = (const int8_t*)&kw1;
+        const float sc = ks[b];
+#pragma unroll
+        for (int L = 0; L < 8; L++) {
+            float t = fmaf(q[c0 + L], (float)k0[L], fmaf(q[c0 + 8 + L], (float)k0[8 + L], 0.0f));
+            t = fmaf(q[c0 + 16 + L], (float)k1[L], fmaf(q[c0 + 24 + L], (float)k1[8 + L], t));
+            sa[L] = fmaf(t, sc, sa[L]);
+        }
+    }
+    return hsum8_hadd(sa);
+}
+
+DEV float q8_dot_score(const float* q, const int8_t* kp, const float* ks, int hd) {
+    float tot[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int b = 0; b < (hd >> 5); b++) {
+        const int c0 = 32 * b;
+        const int4 kw0 = *(const int4*)(kp + c0), kw1 = *(const int4*)(kp + c0 + 16);
+        const int8_t* k0 = (const int8_t*)&kw0;
+        const int8_t* k1 = (const int8_t*)&kw1;
+        const float sc = ks[b];
+#pragma unroll
+        for (int L = 0; L < 8; L++) {
+            float a0 = fmaf(q[c0 + L], (float)k0[L], 0.0f);
+            float a1 = fmaf(q[c0 + 8 + L], (float)k0[8 + L], 0.0f);
+            a0 = fmaf(q[c0 + 16 + L], (float)k1[L], a0);
+            a1 = fmaf(q[c0 + 24 + L], (float)k1[8 + L], a1);
+            tot[L] = fmaf(a0 + a1, sc, tot[L]);
+        }
+    }
+    return hsum8(tot);
+}
+
+__global__ __launch_bounds__(256) void k_attn_q8(const float* __restrict__ q, DpufKvQ8 c8, float* __restrict__ out,
+                                                 float* __restrict__ scores, const int32_t* __restrict__ pos0p,
+                                                 int n_q, int n_kv, int hd, int max_seq, float scale) {
+    extern __shared__ float qs[];  // 2 * hd
+    __shared__ float red[2][256];
+    __shared__ float vs8[2][8];
+    __shared__ float inv_sh[2];
+    const int m = blockIdx.x, kvh = blockIdx.y, gp = blockIdx.z, tid = threadIdx.x;
+    const int groups = n_q / n_kv, nb = hd >> 5;
+    const int g0 = 2 * gp;
+    const bool pair = (g0 + 1 < groups);
+    const int nh = pair ? 2 : 1;
+    const int qh0 = kvh * groups + g0;
+    const int kv_len = *pos0p + m + 1;
+    const int8_t* K = c8.kq + (size_t)kvh * max_seq * hd;
+    const int8_t* V = c8.vq + (size_t)kvh * max_seq * hd;
+    const float* KS = c8.ks + (size_t)kvh * max_seq * nb;
+    const float* VS = c8.vs + (size_t)kvh * max_seq * nb;
+    for (int i = tid; i < nh * hd; i += blockDim.x) qs[i] = q[((size_t)m * n_q + qh0) * hd + i];
+    __syncthreads();
+    float* sc0 = scores + ((size_t)m * n_q + qh0) * max_seq;
+    float* sc1 = sc0 + max_seq;
+    const int n2 = kv_len & ~1;  // keys of the pair path's two-key steps
+    float mx0 = -1e30f, mx1 = -1e30f;
+    for (int t = tid; t < kv_len; t += blockDim.x) {
+        const int8_t* kp = K + (size_t)t * hd;
+        const float* ksp = KS + (size_t)t * nb;
+        float s0, s1 = 0.0f;
+        if (pair && t < n2) {
+            s0 = q8_pair_score(qs, kp, ksp, hd) * scale;
+            s1 = q8_pair_score(qs + hd, kp, ksp, hd) * scale;
+        } else {
+            s0 = q8_dot_score(qs, kp, ksp, hd) * scale;
+            if (pair) s1 = q8_dot_score(qs + hd, kp, ksp, hd) * scale;
+        }
+        sc0[t] = s0;
+        mx0 = s0 > mx0 ? s0 : mx0;
+        if (pair) {
+            sc1[t] = s1;
+            mx1 = s1 > mx1 ? s1 : mx1;
+        }
+    }
+    red[0][tid] = mx0;
+    red[1][tid] = mx1;
+    __syncthreads();
+    for (int w = blockDim.x / 2; w > 0; w >>= 1) {
+        if (tid < w) {
+            red[0][tid] = fmaxf(red[0][tid], red[0][tid + w]);
+            red[1][tid] = fmaxf(red[1][tid], red[1][tid + w]);
+        }
+        __syncthreads();
+    }
+    const float M0 = red[0][0], M1 = red[1][0];
+    const int n8 = kv_len & ~7;
+    for (int t = tid; t < kv_len; t += blockDim.x) {
+        sc0[t] = t < n8 ? exp_poly(sc0[t] - M0) : expf_libc(sc0[t] - M0);
+        if (pair) sc1[t] = t < n8 ? exp_poly(sc1[t] - M1) : expf_libc(sc1[t] - M1);
+    }
+    __syncthreads();
+    if (tid < 16) {
+        const int hsel = tid >> 3, j = tid & 7;
+        if (hsel < nh) {
+            const float* sc = hsel ? sc1 : sc0;
+            float a = 0.0f;
+            for (int t = j; t < n8; t += 8) a = a + sc[t];
+            vs8[hsel][j] = a;
+        }
+    }
+    __syncthreads();
+    if (tid < nh) {
+        const float* sc = tid ? sc1 : sc0;
+        float sp = hsum8(vs8[tid]);
+        for (int t = n8; t < kv_len; t++) sp += sc[t];
+        inv_sh[tid] = 1.0f / (sp + 1e-12f);
+    }
+    __syncthreads();
+    for (int t = tid; t < kv_len; t += blockDim.x) {
+        sc0[t] = sc0[t] * inv_sh[0];
+        if (pair) sc1[t] = sc1[t] * inv_sh[1];
+    }
+    __syncthreads();
+    for (int o = tid; o < nh * hd; o += blockDim.x) {
+        const int hsel = o / hd, d = o % hd, b = d >> 5;
+        const float* p = hsel ? sc1 : sc0;
+        float a = 0.0f;
+        for (int t = 0; t < kv_len; t++) a = fmaf(p[t] * VS[(size_t)t * nb + b], (float)V[(size_t)t * hd + d], a);
+        out[((size_t)m * n_q + qh0 + hsel) * hd + d] = a;
+    }
+}
+
+// Rows of fp32 K and V (n rows of HD, one wave per row and tensor) into the
+// int8 cache at rows row0 .. row0 + n - 1 (KV injection), and back out as
+// q * scale.
+template <int HD>
+__global__ __launch_bounds__(64) void k_q8_rows(const float* __restrict__ k, const float* __restrict__ v, int n,
+                                                DpufKvQ8 c8, size_t row0) {
+    const int r = blockIdx.x, lane = threadIdx.x, which = blockIdx.y;
+    if (r >= n) return;
+    const float* src = (which ? v : k) + (size_t)r * HD;
+    int8_t* dst = (which ? c8.vq : c8.kq) + (row0 + r) * HD;
+    float* sdst = (which ? c8.vs : c8.ks) + (row0 + r) * (HD / 32);
+#pragma unroll
+    for (int e = 0; e < HD / 64; e++) q8_store_lane(src[lane + 64 * e], lane, e, dst, sdst);
+}
+
+__global__ void k_q8_dequant(DpufKvQ8 c8, size_t off, size_t n, float* __restrict__ k, float* __restrict__ v) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        k[i] = (float)c8.kq[off + i] * c8.ks[(off + i) >> 5];
+        v[i] = (float)c8.vq[off + i] * c8.vs[(off + i) >> 5];
     }
 }
 
@@ -3489,19 +3678,26 @@ static void gm_launch(void* s, int32_t M, int32_t n_jobs, const DpufGemvJob* job
 
 void dpuf_hip_qk_rope_kv(void* s, int32_t M, float* q, float* k, const float* v, const float* q_norm,
                          const float* k_norm, float eps, const float* cos_tab, const float* sin_tab, float* kc,
-                         float* vc, const int32_t* pos0, int32_t n_q, int32_t n_kv, int32_t hd, int32_t max_seq) {
+                         float* vc, const int32_t* pos0, int32_t n_q, int32_t n_kv, int32_t hd, int32_t max_seq,
+                         const DpufKvQ8* c8) {
     const dim3 gw((M * (n_q + n_kv) + 3) / 4);
-    if (hd == 64)
-        hipLaunchKernelGGL(k_qk_rope_kv_w<64>, gw, dim3(256), 0, ST(s), q, k, v, q_norm, k_norm, eps, cos_tab, sin_tab,
-                           kc, vc, pos0, M, n_q, n_kv, max_seq);
-    else if (hd == 128)
-        hipLaunchKernelGGL(k_qk_rope_kv_w<128>, gw, dim3(256), 0, ST(s), q, k, v, q_norm, k_norm, eps, cos_tab,
-                           sin_tab, kc, vc, pos0, M, n_q, n_kv, max_seq);
-    else if (hd == 256)
-        hipLaunchKernelGGL(k_qk_rope_kv_w<256>, gw, dim3(256), 0, ST(s), q, k, v, q_norm, k_norm, eps, cos_tab,
-                           sin_tab, kc, vc, pos0, M, n_q, n_kv, max_seq);
-    else
-        note(hipErrorInvalidValue, "dpuf_hip_qk_rope_kv: head dim must be 64, 128 or 256");
+    DpufKvQ8 z;
+    memset(&z, 0, sizeof z);
+    const DpufKvQ8 c = c8 ? *c8 : z;
+#define QKR(HDV)                                                                                                  \
+    do {                                                                                                          \
+        if (c8)                                                                                                   \
+            hipLaunchKernelGGL((k_qk_rope_kv_w<HDV, true>), gw, dim3(256), 0, ST(s), q, k, v, q_norm, k_norm, eps,  \
+                               cos_tab, sin_tab, kc, vc, pos0, M, n_q, n_kv, max_seq, c);                         \
+        else                                                                                                      \
+            hipLaunchKernelGGL((k_qk_rope_kv_w<HDV, false>), gw, dim3(256), 0, ST(s), q, k, v, q_norm, k_norm, eps, \
+                               cos_tab, sin_tab, kc, vc, pos0, M, n_q, n_kv, max_seq, c);                         \
+    } while (0)
+    if (hd == 64) QKR(64);
+    else if (hd == 128) QKR(128);
+    else if (hd == 256) QKR(256);
+    else note(hipErrorInvalidValue, "dpuf_hip_qk_rope_kv: head dim must be 64, 128 or 256");
+#undef QKR
     LAUNCHED("k_qk_rope_kv");
 }
 
@@ -3611,6 +3807,31 @@ void dpuf_hip_attn(void* s, int32_t M, const float* q, const float* kc, const fl
     hipLaunchKernelGGL(k_attn, dim3(M, n_kv, (groups + 1) / 2), dim3(256), (size_t)2 * hd * sizeof(float), ST(s), q,
                        kc, vc, out, scores, pos0, n_q, n_kv, hd, max_seq, scale);
     LAUNCHED("k_attn");
+}
+
+void dpuf_hip_attn_q8(void* s, int32_t M, const float* q, DpufKvQ8 c8, float* out, float* scores,
+                      const int32_t* pos0, int32_t n_q, int32_t n_kv, int32_t hd, int32_t max_seq, float scale) {
+    const int groups = n_q / n_kv;
+    hipLaunchKernelGGL(k_attn_q8, dim3(M, n_kv, (groups + 1) / 2), dim3(256), (size_t)2 * hd * sizeof(float), ST(s),
+                       q, c8, out, scores, pos0, n_q, n_kv, hd, max_seq, scale);
+    LAUNCHED("k_attn_q8");
+}
+
+void dpuf_hip_q8_rows(void* s, const float* k, const float* v, int32_t n, int32_t hd, DpufKvQ8 c8, size_t row0) {
+    if (n <= 0) return;
+    const dim3 g(n, 2);
+    if (hd == 64) hipLaunchKernelGGL(k_q8_rows<64>, g, dim3(64), 0, ST(s), k, v, n, c8, row0);
+    else if (hd == 128) hipLaunchKernelGGL(k_q8_rows<128>, g, dim3(64), 0, ST(s), k, v, n, c8, row0);
+    else if (hd == 256) hipLaunchKernelGGL(k_q8_rows<256>, g, dim3(64), 0, ST(s), k, v, n, c8, row0);
+    else note(hipErrorInvalidValue, "dpuf_hip_q8_rows: head dim must be 64, 128 or 256");
+    LAUNCHED("k_q8_rows");
+}
+
+void dpuf_hip_q8_dequant(void* s, DpufKvQ8 c8, size_t off, size_t n, float* k, float* v) {
+    if (n == 0) return;
+    const size_t blocks = (n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096;
+    hipLaunchKernelGGL(k_q8_dequant, dim3((unsigned)blocks), dim3(256), 0, ST(s), c8, off, n, k, v);
+    LAUNCHED("k_q8_dequant");
 }
 
 int32_t dpuf_hip_attn_dec(void* s, int32_t M, const float* q, const float* k, const float* v, const float* q_norm,

@@ -493,6 +493,135 @@ void orc_attn_heads(int32_t hd, int32_t kv_len, float scale, const float* kc, co
 }
 
 /* ------------------------------------------------------------------------- */
+/* Q8 KV cache (kv_type 1): per-32 int8 K/V and its attention                 */
+/* (reference dpuf_engine.c:579-781)                                          */
+/* ------------------------------------------------------------------------- */
+
+/* quantize_vec_q8_blk32 (dpuf_engine.c:754-781): per 32-block amax,
+ * scale = amax / 127, q = RNE(v * (127 / amax)) saturated and clamped to
+ * >= -127 (a value the conversion cannot represent becomes -127, as
+ * cvtps_epi32's 0x80000000 does after the saturating packs); amax <= 1e-12
+ * gives q = 0 with scale amax / 127. */
+void orc_quant_q8(int32_t n, const float* src, int8_t* dst, float* scales) {
+    for (int32_t b = 0; b < (n >> 5); b++) {
+        const float* v = src + 32 * b;
+        float amax = 0.0f;
+        for (int j = 0; j < 32; j++) {
+            float a = fabsf(v[j]);
+            amax = a > amax ? a : amax;
+        }
+        scales[b] = amax / 127.0f;
+        const float inv = (amax > 1e-12f) ? (127.0f / amax) : 0.0f;
+        for (int j = 0; j < 32; j++) {
+            const float x = v[j] * inv;
+            int32_t q;
+            if (!(x > -2147483648.0f && x < 2147483648.0f)) q = -127;
+            else q = (int32_t)rintf(x);
+            q = q > 127 ? 127 : q;
+            q = q < -127 ? -127 : q;
+            dst[32 * b + j] = (int8_t)q;
+        }
+    }
+}
+
+/* dot_f32_q8_blk32_avx2 (dpuf_engine.c:579-593): per block two 8-lane
+ * accumulators (columns 0-7 then 16-23, and 8-15 then 24-31), their lane sum
+ * scaled into a running 8-lane total, then eng_hsum256. */
+static float dot_q8(int32_t hd, const float* q, const int8_t* k, const float* ks) {
+    float tot[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int32_t b = 0; b < (hd >> 5); b++) {
+        const int32_t c0 = 32 * b;
+        for (int L = 0; L < 8; L++) {
+            float a0 = fmaf(q[c0 + L], (float)k[c0 + L], 0.0f);
+            float a1 = fmaf(q[c0 + 8 + L], (float)k[c0 + 8 + L], 0.0f);
+            a0 = fmaf(q[c0 + 16 + L], (float)k[c0 + 16 + L], a0);
+            a1 = fmaf(q[c0 + 24 + L], (float)k[c0 + 24 + L], a1);
+            tot[L] = fmaf(a0 + a1, ks[b], tot[L]);
+        }
+    }
+    return hsum8(tot);
+}
+
+/* The pair path's score of one query against one key (dpuf_engine.c:611-648):
+ * per block, lanes accumulate fma(q_lo, k_lo, fma(q_hi, k_hi, t)) over the two
+ * 16-column halves, then fma(t, ks, s); the hadd tree of hsum4_256_ps. */
+static float pair_score_q8(int32_t hd, const float* q, const int8_t* k, const float* ks) {
+    float sa[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int32_t b = 0; b < (hd >> 5); b++) {
+        const int32_t c0 = 32 * b;
+        for (int L = 0; L < 8; L++) {
+            float t = 0.0f;
+            for (int j = 0; j < 32; j += 16)
+                t = fmaf(q[c0 + j + L], (float)k[c0 + j + L], fmaf(q[c0 + j + 8 + L], (float)k[c0 + j + 8 + L], t));
+            sa[L] = fmaf(t, ks[b], sa[L]);
+        }
+    }
+    return hsum8_hadd(sa);
+}
+
+/* gqa_attn_head_pair_q8 (dpuf_engine.c:595-752) over a head's int8 K/V
+ * [kv_len][hd] and per-32 scales [kv_len][hd/32].  q1 == NULL selects the
+ * single-head path. */
+void orc_attn_heads_q8(int32_t hd, int32_t kv_len, float scale, const int8_t* kq, const float* ks,
+                       const int8_t* vq, const float* vs, const float* q0, const float* q1,
+                       float* sc0, float* sc1, float* out0, float* out1) {
+    const int32_t nb = hd >> 5;
+    float m0 = -1e30f, m1 = -1e30f;
+    if (q1) {
+        int32_t t = 0;
+        for (; t + 1 < kv_len; t += 2) {
+            for (int u = 0; u < 2; u++) {
+                const int8_t* kp = kq + (size_t)(t + u) * hd;
+                const float* kps = ks + (size_t)(t + u) * nb;
+                sc0[t + u] = pair_score_q8(hd, q0, kp, kps) * scale;
+                sc1[t + u] = pair_score_q8(hd, q1, kp, kps) * scale;
+            }
+            const float a = sc0[t] > sc0[t + 1] ? sc0[t] : sc0[t + 1];
+            const float c = sc1[t] > sc1[t + 1] ? sc1[t] : sc1[t + 1];
+            m0 = a > m0 ? a : m0;
+            m1 = c > m1 ? c : m1;
+        }
+        for (; t < kv_len; t++) {
+            const int8_t* kp = kq + (size_t)t * hd;
+            const float* kps = ks + (size_t)t * nb;
+            const float s0 = dot_q8(hd, q0, kp, kps) * scale, s1 = dot_q8(hd, q1, kp, kps) * scale;
+            sc0[t] = s0;
+            if (s0 > m0) m0 = s0;
+            sc1[t] = s1;
+            if (s1 > m1) m1 = s1;
+        }
+        softmax_ref(kv_len, sc0, m0);
+        softmax_ref(kv_len, sc1, m1);
+        for (int32_t d = 0; d < hd; d++) {
+            const int32_t b = d >> 5;
+            float a = 0.0f, c = 0.0f;
+            for (int32_t k = 0; k < kv_len; k++) {
+                const float vsk = vs[(size_t)k * nb + b];
+                const float v = (float)vq[(size_t)k * hd + d];
+                a = fmaf(sc0[k] * vsk, v, a);
+                c = fmaf(sc1[k] * vsk, v, c);
+            }
+            out0[d] = a;
+            out1[d] = c;
+        }
+        return;
+    }
+    for (int32_t t = 0; t < kv_len; t++) {
+        const float s = dot_q8(hd, q0, kq + (size_t)t * hd, ks + (size_t)t * nb) * scale;
+        sc0[t] = s;
+        if (s > m0) m0 = s;
+    }
+    softmax_ref(kv_len, sc0, m0);
+    for (int32_t d = 0; d < hd; d++) {
+        const int32_t b = d >> 5;
+        float a = 0.0f;
+        for (int32_t k = 0; k < kv_len; k++)
+            a = fmaf(sc0[k] * vs[(size_t)k * nb + b], (float)vq[(size_t)k * hd + d], a);
+        out0[d] = a;
+    }
+}
+
+/* ------------------------------------------------------------------------- */
 /* A11: SwiGLU with dead zone, 8-wide path (reference dpuf_engine.c:967-989)  */
 /* ------------------------------------------------------------------------- */
 
@@ -508,15 +637,25 @@ float orc_swiglu1(float g, float u, float dz) {
 /* A14/A15: engine (reference dpuf_engine.c:1182-2170)                        */
 /* ------------------------------------------------------------------------- */
 
+/* fp32 K/V [L][n_kv][max_seq][hd], or with kv_type 1 int8 K/V of that
+ * layout plus per-32 scales [L][n_kv][max_seq][hd/32] (dpuf_engine.c:1182-1206). */
 typedef struct {
     float* k;
     float* v;
+    int8_t* kq;
+    int8_t* vq;
+    float* ks;
+    float* vs;
     int allocated;
 } OrcSlot;
 
 typedef struct {
     float* k;
     float* v;
+    int8_t* kq;
+    int8_t* vq;
+    float* ks;
+    float* vs;
     int32_t len;
     int valid;
 } OrcPrefix;
@@ -541,12 +680,23 @@ static size_t kv_elems(const OrcEngine* e) {
            (size_t)e->cfg.num_kv_heads * (size_t)e->cfg.head_dim;
 }
 
+static int is_q8(const OrcEngine* e) { return e->cfg.kv_type == DPUF_KV_Q8; }
+
 static int slot_alloc(OrcEngine* e, int32_t s) {
-    if (e->slots[s].allocated) return 1;
-    e->slots[s].k = (float*)calloc(kv_elems(e), sizeof(float));
-    e->slots[s].v = (float*)calloc(kv_elems(e), sizeof(float));
-    if (!e->slots[s].k || !e->slots[s].v) return 0;
-    e->slots[s].allocated = 1;
+    OrcSlot* sl = &e->slots[s];
+    if (sl->allocated) return 1;
+    if (is_q8(e)) {
+        sl->kq = (int8_t*)calloc(kv_elems(e), 1);
+        sl->vq = (int8_t*)calloc(kv_elems(e), 1);
+        sl->ks = (float*)calloc(kv_elems(e) / 32, sizeof(float));
+        sl->vs = (float*)calloc(kv_elems(e) / 32, sizeof(float));
+        if (!sl->kq || !sl->vq || !sl->ks || !sl->vs) return 0;
+    } else {
+        sl->k = (float*)calloc(kv_elems(e), sizeof(float));
+        sl->v = (float*)calloc(kv_elems(e), sizeof(float));
+        if (!sl->k || !sl->v) return 0;
+    }
+    sl->allocated = 1;
     return 1;
 }
 
@@ -573,8 +723,14 @@ OrcEngine* orc_engine_create(const DpufModelConfig* cfg, const DpufLayerWeights*
 
 void orc_engine_destroy(OrcEngine* e) {
     if (!e) return;
-    for (int s = 0; s < ORC_MAX_SLOTS; s++) { free(e->slots[s].k); free(e->slots[s].v); }
-    for (int p = 0; p < ORC_MAX_PREFIXES; p++) { free(e->prefixes[p].k); free(e->prefixes[p].v); }
+    for (int s = 0; s < ORC_MAX_SLOTS; s++) {
+        OrcSlot* sl = &e->slots[s];
+        free(sl->k); free(sl->v); free(sl->kq); free(sl->vq); free(sl->ks); free(sl->vs);
+    }
+    for (int p = 0; p < ORC_MAX_PREFIXES; p++) {
+        OrcPrefix* pf = &e->prefixes[p];
+        free(pf->k); free(pf->v); free(pf->kq); free(pf->vq); free(pf->ks); free(pf->vs);
+    }
     free(e->cos_tab); free(e->sin_tab); free(e->layers); free(e->capture);
     free(e);
 }
@@ -588,8 +744,44 @@ int32_t orc_engine_set_slot(OrcEngine* e, int32_t s) {
 
 void orc_engine_reset_slot(OrcEngine* e, int32_t s) {
     if (!e || s < 0 || s >= ORC_MAX_SLOTS || !e->slots[s].allocated) return;
-    memset(e->slots[s].k, 0, kv_elems(e) * sizeof(float));
-    memset(e->slots[s].v, 0, kv_elems(e) * sizeof(float));
+    OrcSlot* sl = &e->slots[s];
+    if (is_q8(e)) {
+        memset(sl->kq, 0, kv_elems(e));
+        memset(sl->vq, 0, kv_elems(e));
+        memset(sl->ks, 0, kv_elems(e) / 32 * sizeof(float));
+        memset(sl->vs, 0, kv_elems(e) / 32 * sizeof(float));
+    } else {
+        memset(sl->k, 0, kv_elems(e) * sizeof(float));
+        memset(sl->v, 0, kv_elems(e) * sizeof(float));
+    }
+}
+
+/* Copies positions [0, len) of every (layer, kv head) between a slot's
+ * layout [..][max_seq][..] and a prefix's [..][len][..] (to_prefix selects
+ * the direction), for each array the cache has. */
+static void prefix_copy(OrcEngine* e, OrcSlot* sl, OrcPrefix* p, int32_t len, int to_prefix) {
+    const size_t hd = (size_t)e->cfg.head_dim, nkv = (size_t)e->cfg.num_kv_heads, L = (size_t)e->cfg.num_layers;
+    const size_t ms = (size_t)e->cfg.max_seq_len;
+    for (size_t l = 0; l < L; l++)
+        for (size_t h = 0; h < nkv; h++) {
+            const size_t po = (l * nkv + h) * (size_t)len, so = (l * nkv + h) * ms;
+#define PCOPY(S, P, T, W)                                                                        \
+    do {                                                                                           \
+        T* dst = to_prefix ? (P) + po * (W) : (S) + so * (W);                                     \
+        const T* src = to_prefix ? (S) + so * (W) : (P) + po * (W);                               \
+        memcpy(dst, src, (size_t)len * (W) * sizeof(T));                                           \
+    } while (0)
+            if (is_q8(e)) {
+                PCOPY(sl->kq, p->kq, int8_t, hd);
+                PCOPY(sl->vq, p->vq, int8_t, hd);
+                PCOPY(sl->ks, p->ks, float, hd / 32);
+                PCOPY(sl->vs, p->vs, float, hd / 32);
+            } else {
+                PCOPY(sl->k, p->k, float, hd);
+                PCOPY(sl->v, p->v, float, hd);
+            }
+#undef PCOPY
+        }
 }
 
 /* Prefix copies follow dpuf_engine.c:1471-1600 (layout [L][kvh][len][hd]). */
@@ -597,17 +789,19 @@ int32_t orc_engine_freeze_prefix(OrcEngine* e, int32_t id, int32_t len) {
     if (!e || id < 0 || id >= ORC_MAX_PREFIXES || len <= 0 || len > e->cfg.max_seq_len) return 0;
     OrcPrefix* p = &e->prefixes[id];
     size_t hd = (size_t)e->cfg.head_dim, nkv = (size_t)e->cfg.num_kv_heads, L = (size_t)e->cfg.num_layers;
-    free(p->k); free(p->v);
-    p->k = (float*)calloc(L * nkv * (size_t)len * hd, sizeof(float));
-    p->v = (float*)calloc(L * nkv * (size_t)len * hd, sizeof(float));
-    OrcSlot* sl = &e->slots[e->active];
-    for (size_t l = 0; l < L; l++)
-        for (size_t h = 0; h < nkv; h++) {
-            size_t po = (l * nkv + h) * (size_t)len * hd;
-            size_t so = (l * nkv + h) * (size_t)e->cfg.max_seq_len * hd;
-            memcpy(p->k + po, sl->k + so, (size_t)len * hd * sizeof(float));
-            memcpy(p->v + po, sl->v + so, (size_t)len * hd * sizeof(float));
-        }
+    const size_t n = L * nkv * (size_t)len * hd;
+    free(p->k); free(p->v); free(p->kq); free(p->vq); free(p->ks); free(p->vs);
+    memset(p, 0, sizeof *p);
+    if (is_q8(e)) {
+        p->kq = (int8_t*)calloc(n, 1);
+        p->vq = (int8_t*)calloc(n, 1);
+        p->ks = (float*)calloc(n / 32, sizeof(float));
+        p->vs = (float*)calloc(n / 32, sizeof(float));
+    } else {
+        p->k = (float*)calloc(n, sizeof(float));
+        p->v = (float*)calloc(n, sizeof(float));
+    }
+    prefix_copy(e, &e->slots[e->active], p, len, 1);
     p->len = len;
     p->valid = 1;
     return 1;
@@ -618,15 +812,7 @@ int32_t orc_engine_apply_prefix(OrcEngine* e, int32_t slot, int32_t id) {
     OrcPrefix* p = &e->prefixes[id];
     if (!p->valid || p->len <= 0) return 0;
     if (!slot_alloc(e, slot)) return 0;
-    OrcSlot* sl = &e->slots[slot];
-    size_t hd = (size_t)e->cfg.head_dim, nkv = (size_t)e->cfg.num_kv_heads, L = (size_t)e->cfg.num_layers;
-    for (size_t l = 0; l < L; l++)
-        for (size_t h = 0; h < nkv; h++) {
-            size_t po = (l * nkv + h) * (size_t)p->len * hd;
-            size_t so = (l * nkv + h) * (size_t)e->cfg.max_seq_len * hd;
-            memcpy(sl->k + so, p->k + po, (size_t)p->len * hd * sizeof(float));
-            memcpy(sl->v + so, p->v + po, (size_t)p->len * hd * sizeof(float));
-        }
+    prefix_copy(e, &e->slots[slot], p, p->len, 0);
     return p->len;
 }
 
@@ -639,6 +825,14 @@ int32_t orc_engine_set_kv(OrcEngine* e, int32_t layer, int32_t kvh, int32_t pos0
     OrcSlot* sl = &e->slots[e->active];
     size_t hd = (size_t)e->cfg.head_dim;
     size_t off = (((size_t)layer * e->cfg.num_kv_heads + kvh) * (size_t)e->cfg.max_seq_len + pos0) * hd;
+    if (is_q8(e)) {
+        /* rows are quantised as the KV store does (dpuf_engine.c:1800-1806) */
+        for (int32_t i = 0; i < n; i++) {
+            orc_quant_q8((int32_t)hd, k + (size_t)i * hd, sl->kq + off + (size_t)i * hd, sl->ks + (off + (size_t)i * hd) / 32);
+            orc_quant_q8((int32_t)hd, v + (size_t)i * hd, sl->vq + off + (size_t)i * hd, sl->vs + (off + (size_t)i * hd) / 32);
+        }
+        return 0;
+    }
     memcpy(sl->k + off, k, (size_t)n * hd * sizeof(float));
     memcpy(sl->v + off, v, (size_t)n * hd * sizeof(float));
     return 0;
@@ -651,6 +845,13 @@ int32_t orc_engine_get_kv(OrcEngine* e, int32_t layer, int32_t kvh, int32_t pos0
     OrcSlot* sl = &e->slots[e->active];
     size_t hd = (size_t)e->cfg.head_dim;
     size_t off = (((size_t)layer * e->cfg.num_kv_heads + kvh) * (size_t)e->cfg.max_seq_len + pos0) * hd;
+    if (is_q8(e)) { /* dequantised: q * scale */
+        for (size_t i = 0; i < (size_t)n * hd; i++) {
+            k[i] = (float)sl->kq[off + i] * sl->ks[(off + i) / 32];
+            v[i] = (float)sl->vq[off + i] * sl->vs[(off + i) / 32];
+        }
+        return 0;
+    }
     memcpy(k, sl->k + off, (size_t)n * hd * sizeof(float));
     memcpy(v, sl->v + off, (size_t)n * hd * sizeof(float));
     return 0;
@@ -728,8 +929,8 @@ int32_t orc_engine_forward(OrcEngine* e, int32_t n_tokens, const int32_t* ids, i
         run_weight(&lw->w_k, M, xn, kb, 0, lw->w_k.n_tiles, pq, ps, pm);
         run_weight(&lw->w_v, M, xn, vb, 0, lw->w_v.n_tiles, pq, ps, pm);
         /* (3) K: QK-norm, RoPE, cache store; Q: QK-norm, RoPE (dpuf_engine.c:1791-1817). */
-        float* kc = sl->k + (size_t)l * lstride;
-        float* vc = sl->v + (size_t)l * lstride;
+        float* kc = is_q8(e) ? NULL : sl->k + (size_t)l * lstride;
+        float* vc = is_q8(e) ? NULL : sl->v + (size_t)l * lstride;
         for (int32_t m = 0; m < M; m++) {
             int32_t pos = pos0 + m;
             const float* cp = e->cos_tab + (size_t)pos * half;
@@ -739,8 +940,14 @@ int32_t orc_engine_forward(OrcEngine* e, int32_t n_tokens, const int32_t* ids, i
                 float* vs = vb + (size_t)m * kvd + (size_t)k * hd;
                 if (c->has_qk_norm && lw->attn_k_norm) orc_add_rmsnorm(hd, ks, NULL, lw->attn_k_norm, eps, ks);
                 orc_rope_apply(hd, ks, cp, sp);
-                memcpy(kc + (size_t)k * hstride + (size_t)pos * hd, ks, (size_t)hd * sizeof(float));
-                memcpy(vc + (size_t)k * hstride + (size_t)pos * hd, vs, (size_t)hd * sizeof(float));
+                if (is_q8(e)) {
+                    const size_t o = (size_t)l * lstride + (size_t)k * hstride + (size_t)pos * hd;
+                    orc_quant_q8(hd, ks, sl->kq + o, sl->ks + o / 32);
+                    orc_quant_q8(hd, vs, sl->vq + o, sl->vs + o / 32);
+                } else {
+                    memcpy(kc + (size_t)k * hstride + (size_t)pos * hd, ks, (size_t)hd * sizeof(float));
+                    memcpy(vc + (size_t)k * hstride + (size_t)pos * hd, vs, (size_t)hd * sizeof(float));
+                }
             }
             for (int32_t qh = 0; qh < nq; qh++) {
                 float* qv = qb + (size_t)m * qd + (size_t)qh * hd;
@@ -761,8 +968,14 @@ int32_t orc_engine_forward(OrcEngine* e, int32_t n_tokens, const int32_t* ids, i
                 int has_p = (g + 1 < groups);
                 const float* q0 = qb + (size_t)m * qd + (size_t)qh * hd;
                 float* a0 = ao + (size_t)m * qd + (size_t)qh * hd;
-                orc_attn_heads(hd, kv_len, scale, kc + (size_t)k * hstride, vc + (size_t)k * hstride,
-                               q0, has_p ? q0 + hd : NULL, s0, s1, a0, has_p ? a0 + hd : NULL);
+                if (is_q8(e)) {
+                    const size_t o = (size_t)l * lstride + (size_t)k * hstride;
+                    orc_attn_heads_q8(hd, kv_len, scale, sl->kq + o, sl->ks + o / 32, sl->vq + o, sl->vs + o / 32,
+                                      q0, has_p ? q0 + hd : NULL, s0, s1, a0, has_p ? a0 + hd : NULL);
+                } else {
+                    orc_attn_heads(hd, kv_len, scale, kc + (size_t)k * hstride, vc + (size_t)k * hstride,
+                                   q0, has_p ? q0 + hd : NULL, s0, s1, a0, has_p ? a0 + hd : NULL);
+                }
             }
             free(s0); free(s1);
         }

@@ -39,6 +39,10 @@ void orc_rope_apply(int32_t hd, float* v, const float* c, const float* s);
 void orc_attn_heads(int32_t hd, int32_t kv_len, float scale, const float* kc, const float* vc,
                     const float* q0, const float* q1, float* sc0, float* sc1, float* out0, float* out1);
 float orc_swiglu1(float g, float u, float dz);
+void orc_quant_q8(int32_t n, const float* src, int8_t* dst, float* scales);
+void orc_attn_heads_q8(int32_t hd, int32_t kv_len, float scale, const int8_t* kq, const float* ks,
+                       const int8_t* vq, const float* vs, const float* q0, const float* q1,
+                       float* sc0, float* sc1, float* out0, float* out1);
 
 OrcEngine* orc_engine_create(const DpufModelConfig* cfg, const DpufLayerWeights* layers,
                              const DpufWeightDesc* tok, const DpufWeightDesc* lm, const float* out_norm);

@@ -46,6 +46,8 @@ def load():
     _sig(lib, "orc_rope_apply", None, [I32, P, P, P])
     _sig(lib, "orc_attn_heads", None, [I32, I32, C.c_float, P, P, P, P, P, P, P, P])
     _sig(lib, "orc_swiglu1", C.c_float, [C.c_float, C.c_float, C.c_float])
+    _sig(lib, "orc_quant_q8", None, [I32, P, P, P])
+    _sig(lib, "orc_attn_heads_q8", None, [I32, I32, C.c_float, P, P, P, P, P, P, P, P, P, P])
     _sig(lib, "orc_engine_create", P, [C.POINTER(DpufModelConfig), C.POINTER(DpufLayerWeights),
                                         C.POINTER(DpufWeightDesc), C.POINTER(DpufWeightDesc), P])
     _sig(lib, "orc_engine_destroy", None, [P])

@@ -18,7 +18,9 @@ the block is the textbook Qwen3 decoder layer:
     logits = Wlm (RMSNorm(h) * w_out); Zone-A early exit fills -1e9 past the zone
 
 Activations are not quantised here, so the oracle differs from this model by
-its int8 activation noise only.  `mut` switches on one deliberate mistake at a
+its int8 activation noise only.  With kv_q8 the cache holds K and V as the
+int8 KV cache represents them: each 32-value block rounded to multiples of
+amax / 127.  `mut` switches on one deliberate mistake at a
 time; the pinning test checks that each one is caught.
 """
 import ctypes as C
@@ -62,11 +64,26 @@ class F64Model:
             self.layers.append(W)
         self.reset()
 
+    def q8(self, x, mut=()):
+        """Per-32-block int8 round trip of the last axis: q = round(x * 127 /
+        amax) clamped to [-127, 127], value q * amax / 127 (amax <= 1e-12: 0)."""
+        shp = x.shape
+        b = x.reshape(-1, 32)
+        amax = np.max(np.abs(b), axis=1, keepdims=True)
+        inv = np.where(amax > 1e-12, 127.0 / np.where(amax > 0, amax, 1.0), 0.0)
+        q = np.clip(np.round(b * inv), -127, 127)
+        sc = amax / 127.0
+        if "q8_scale_shift" in mut:  # the scale of the neighbouring block
+            sc = np.roll(sc.reshape(-1, self.hd // 32), 1, axis=1).reshape(-1, 1)
+        return (q * sc).reshape(shp)
+
     def reset(self):
         self.kc = np.zeros((self.L, self.nkv, 0, self.hd))
         self.vc = np.zeros((self.L, self.nkv, 0, self.hd))
 
-    def set_kv(self, layer, kvh, pos0, k, v):
+    def set_kv(self, layer, kvh, pos0, k, v, kv_q8=False):
+        if kv_q8:
+            k, v = self.q8(k), self.q8(v)
         n = k.shape[0]
         need = pos0 + n
         if self.kc.shape[2] < need:
@@ -99,7 +116,8 @@ class F64Model:
             s = -s
         return np.concatenate([x1 * c - x2 * s, x2 * c + x1 * s], axis=-1)
 
-    def forward(self, ids, pos0, embeds=None, keep_tiles=0, deadzone=0.005, early=None, mut=(), capture=None):
+    def forward(self, ids, pos0, embeds=None, keep_tiles=0, deadzone=0.005, early=None, mut=(), capture=None,
+                kv_q8=False):
         """Returns logits [M, V] of every row; capture (a list) receives the
         residual stream after each layer, [M, H] per layer."""
         mut = set(mut)
@@ -127,6 +145,8 @@ class F64Model:
             pos = np.arange(pos0, end)[:, None, None]
             q = self._rope(q, pos, mut)
             k = self._rope(k, pos, mut)
+            if kv_q8:
+                k, v = self.q8(k, mut), self.q8(v, mut)
             self.kc[l, :, pos0:end] = k.transpose(1, 0, 2)
             self.vc[l, :, pos0:end] = v.transpose(1, 0, 2)
             ao = np.zeros((M_, nq, hd))

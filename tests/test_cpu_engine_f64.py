@@ -254,3 +254,133 @@ def test_oracle_embeds_rows_replace_embedding(orc):
     b, _ = o.forward(mixed, 0, embeds=emb)
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
     o.close()
+
+
+# --------------------------------------------------------------------------- Q8 KV cache
+
+def _q8(orc, x):
+    n = x.size
+    q = np.zeros(n, np.int8)
+    s = np.zeros(n // 32, np.float32)
+    orc.orc_quant_q8(n, M.ptr(np.ascontiguousarray(x, np.float32)), M.ptr(q), M.ptr(s))
+    return q, s
+
+
+def test_q8_quantisation_cases(orc):
+    """quantize_vec_q8_blk32 (dpuf_engine.c:754-781): per 32-block scale
+    amax / 127; the extreme value maps to +-127; an all-zero block gives q = 0;
+    exact ties k + 1/2 round to even; |x - q * scale| <= scale / 2; the block
+    boundaries are every 32 values."""
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal(128).astype(np.float32)
+    x[32:64] = 0.0
+    x[70] = -9.0  # block 2's extreme, negative
+    q, s = _q8(orc, x)
+    for b in range(4):
+        blk = x[32 * b:32 * b + 32]
+        amax = np.float32(np.max(np.abs(blk)))
+        assert s[b] == np.float32(amax / np.float32(127.0))
+        if amax == 0:
+            assert (q[32 * b:32 * b + 32] == 0).all()
+            continue
+        err = np.abs(blk.astype(np.float64) - q[32 * b:32 * b + 32].astype(np.float64) * s[b])
+        assert err.max() <= s[b] / 2 * (1 + 1e-5)
+    assert q[70] == -127 and q.min() >= -127
+    # ties: amax 127 makes inv exactly 1, so x = k + 0.5 rounds to even
+    t = np.zeros(32, np.float32)
+    t[0] = 127.0
+    t[1:6] = [0.5, 1.5, 2.5, -0.5, -3.5]
+    q, s = _q8(orc, t)
+    assert list(q[:6]) == [127, 0, 2, 2, 0, -4] and s[0] == np.float32(1.0)
+
+
+@pytest.mark.parametrize("n,pair", [(1, False), (7, True), (9, False), (40, True)])
+def test_q8_attention_float64(orc, n, pair):
+    """gqa_attn_head_pair_q8 restated: softmax(q . k_deq / sqrt(hd)) v_deq in
+    float64 over the dequantised int8 K/V to 1e-5 (both query paths, odd key
+    counts that take the single-key tail)."""
+    rng = np.random.default_rng(100 + n)
+    hd = 128
+    K = rng.standard_normal((n, hd)).astype(np.float32)
+    V = rng.standard_normal((n, hd)).astype(np.float32)
+    kq, ks = _q8(orc, K.ravel())
+    vq, vs = _q8(orc, V.ravel())
+    Kd = kq.reshape(n, hd).astype(np.float64) * np.repeat(ks.reshape(n, hd // 32), 32, axis=1)
+    Vd = vq.reshape(n, hd).astype(np.float64) * np.repeat(vs.reshape(n, hd // 32), 32, axis=1)
+    q0 = rng.standard_normal(hd).astype(np.float32)
+    q1 = rng.standard_normal(hd).astype(np.float32) if pair else None
+    sc0, sc1 = np.zeros(n, np.float32), np.zeros(n, np.float32)
+    o0, o1 = np.zeros(hd, np.float32), np.zeros(hd, np.float32)
+    orc.orc_attn_heads_q8(hd, n, C.c_float(1 / np.sqrt(hd)), M.ptr(kq), M.ptr(ks), M.ptr(vq), M.ptr(vs), M.ptr(q0),
+                          M.ptr(q1), M.ptr(sc0), M.ptr(sc1), M.ptr(o0), M.ptr(o1) if pair else None)
+    for q, o in ((q0, o0), (q1, o1)):
+        if q is None:
+            continue
+        s = Kd @ q.astype(np.float64) / np.sqrt(hd)
+        p = np.exp(s - s.max())
+        p /= p.sum()
+        assert np.allclose(o, p @ Vd, rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("heads", [(4, 2), (8, 2), (6, 2)])
+def test_oracle_q8_engine_matches_float64(orc, heads):
+    """kv_type 1 (the int8 KV cache, dpuf_engine.c:1191-1197, 1800-1806):
+    prefill + 3 decode steps of the oracle within BOUND of the float64
+    decoder holding the same int8 round trip of K and V; using a neighbouring
+    block's scale is caught."""
+    nq, nkv = heads
+    m = M.Model.build(dict(TINY, num_q_heads=nq, num_kv_heads=nkv), max_seq_len=64, seed=7)
+    randomise_norms(m, 8)
+    cfg = M.abi.DpufModelConfig.from_buffer_copy(m.cfg.contents)
+    cfg.kv_type = 1
+    f = F64Model(orc, m)
+    oh = orc.orc_engine_create(C.byref(cfg), m.layers, m.tok, m.lm, m.out_norm)
+    assert oh
+    ids = np.random.default_rng(9).integers(0, 4096, 9).astype(np.int32)
+    calls = []
+    lo = np.zeros((9, 4096), np.float32)
+    assert orc.orc_engine_forward(oh, 9, M.ptr(ids), 0, None, 0, M.ptr(lo)) == 0
+    calls.append((ids, 0, lo.copy()))
+    tok = int(np.argmax(lo[-1]))
+    for s in range(3):
+        t = np.array([tok], np.int32)
+        l1 = np.zeros((1, 4096), np.float32)
+        assert orc.orc_engine_forward(oh, 1, M.ptr(t), 9 + s, None, 1, M.ptr(l1)) == 0
+        calls.append((t, 9 + s, l1.copy()))
+        tok = int(np.argmax(l1[-1]))
+    orc.orc_engine_destroy(oh)
+    errs = {}
+    for mut in ((), ("q8_scale_shift",)):
+        f.reset()
+        errs[mut] = max(rel(lo_, f.forward(i_, p_, kv_q8=True, mut=mut)[-lo_.shape[0]:]) for i_, p_, lo_ in calls)
+    print(errs)
+    assert errs[()] < BOUND and errs[("q8_scale_shift",)] > CAUGHT
+
+
+def test_oracle_q8_prefix_and_inject(orc):
+    """With kv_type 1, freeze -> apply reproduces the prompt's logits bit
+    for bit from the prefix position, and set_kv quantises injected rows as
+    the store does: get_kv returns them dequantised within half a step."""
+    m = M.Model.build(TINY, max_seq_len=64, seed=11)
+    cfg = M.abi.DpufModelConfig.from_buffer_copy(m.cfg.contents)
+    cfg.kv_type = 1
+    oh = orc.orc_engine_create(C.byref(cfg), m.layers, m.tok, m.lm, m.out_norm)
+    ids = np.random.default_rng(12).integers(0, 4096, 12).astype(np.int32)
+    full = np.zeros((12, 4096), np.float32)
+    assert orc.orc_engine_forward(oh, 12, M.ptr(ids), 0, None, 0, M.ptr(full)) == 0
+    assert orc.orc_engine_freeze_prefix(oh, 1, 8) == 1
+    assert orc.orc_engine_apply_prefix(oh, 3, 1) == 8
+    assert orc.orc_engine_set_slot(oh, 3) == 0
+    part = np.zeros((4, 4096), np.float32)
+    assert orc.orc_engine_forward(oh, 4, M.ptr(ids[8:]), 8, None, 0, M.ptr(part)) == 0
+    assert np.array_equal(part.view(np.uint32), full[8:].view(np.uint32))
+    rng = np.random.default_rng(13)
+    k = rng.standard_normal((5, 64)).astype(np.float32)
+    v = rng.standard_normal((5, 64)).astype(np.float32)
+    assert orc.orc_engine_set_kv(oh, 1, 1, 20, 5, M.ptr(k), M.ptr(v)) == 0
+    kb, vb = np.zeros_like(k), np.zeros_like(v)
+    assert orc.orc_engine_get_kv(oh, 1, 1, 20, 5, M.ptr(kb), M.ptr(vb)) == 0
+    for a, b in ((k, kb), (v, vb)):
+        step = np.max(np.abs(a.reshape(-1, 32)), axis=1) / 127
+        assert np.all(np.abs(a - b).reshape(-1, 32) <= step[:, None] * 0.5 * (1 + 1e-5))
+    orc.orc_engine_destroy(oh)

@@ -1,0 +1,119 @@
+"""The int8 KV cache (kv_type 1; reference dpuf_engine.c:579-781, 1182-1206,
+1800-1806) on the GPU against the oracle's restatement: per-32-block int8 K
+and V with fp32 scales, the quantising store after QK-norm and RoPE, and the
+int8-cache attention.  Bit for bit, through the C ABI."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from dpuf_amd import abi
+from dpuf_amd import model as M
+from test_gpu_configs import Pair, bits_equal, greedy, log, maxdiff
+
+pytestmark = pytest.mark.gpu
+
+
+def q8_model(shape, max_seq, seed):
+    m = M.Model.build(shape, max_seq_len=max_seq, seed=seed)
+    cfg = abi.DpufModelConfig.from_buffer_copy(m.cfg.contents)
+    cfg.kv_type = 1
+    return m, cfg
+
+
+class Q8Pair(Pair):
+    def __init__(self, eng, orc, model, cfg):
+        self.eng, self.orc, self.m = eng, orc, model
+        self.cfg = cfg
+        self.g = eng.dpuf_engine_create(*model.create_args(cfg))
+        assert self.g, eng.dpuf_amd_last_error()
+        self.o = orc.orc_engine_create(*model.create_args(cfg))
+        assert self.o
+        self.V, self.L, self.H = cfg.vocab_size, cfg.num_layers, cfg.hidden_size
+
+
+TINY = dict(hidden_size=256, intermediate_size=512, num_layers=3, num_q_heads=4, num_kv_heads=2, head_dim=64,
+            vocab_size=4096, tie_word_embeddings=1)
+
+
+@pytest.mark.parametrize("heads,hd", [((4, 2), 64), ((6, 2), 64), ((8, 2), 128)])
+def test_q8_prefill_decode_bit_exact(eng, orc, heads, hd):
+    """Prefill of 13 tokens (M > 1) and 10 greedy steps (M = 1): logits and
+    the per-layer residual stream bit-identical; groups of 2, 3 (the single
+    trailing head) and 4; the slot memory is the int8 layout's."""
+    nq, nkv = heads
+    m, cfg = q8_model(dict(TINY, num_q_heads=nq, num_kv_heads=nkv, head_dim=hd), 64, 201)
+    p = Q8Pair(eng, orc, m, cfg)
+    p.capture(16)
+    ids = np.random.default_rng(202).integers(0, 4096, 13).astype(np.int32)
+    log(f"q8 kv heads={heads} hd={hd}: prefill 13")
+    lg, lo = p.forward(ids, 0, only_last=0)
+    assert bits_equal(lg, lo), maxdiff(lg, lo)
+    cg, co = p.captured(13)
+    assert bits_equal(cg, co), maxdiff(cg, co)
+    greedy(p, lg, lo, 13, 10, "q8")
+    rows = 3 * nkv * 64
+    assert eng.dpuf_engine_slot_memory(p.g) == 2 * rows * hd + 2 * rows * (hd // 32) * 4
+    p.close()
+
+
+def test_q8_injected_context_and_graph(eng, orc):
+    """300 N(0, 1) K/V positions injected through set_kv (quantised on both
+    sides as the store does) at the Qwen3-8B attention geometry, then decode
+    on the reference entry and on the captured-graph device-argmax entry;
+    get_kv returns the dequantised rows of both engines bit for bit."""
+    shape = dict(TINY, num_layers=2, num_q_heads=32, num_kv_heads=8, head_dim=128)
+    m, cfg = q8_model(shape, 320, 211)
+    p = Q8Pair(eng, orc, m, cfg)
+    rng = np.random.default_rng(212)
+    for layer in range(2):
+        for kvh in range(8):
+            p.set_kv(layer, kvh, 0, rng.standard_normal((300, 128), dtype=np.float32),
+                     rng.standard_normal((300, 128), dtype=np.float32))
+    kg, vg = np.zeros((300, 128), np.float32), np.zeros((300, 128), np.float32)
+    ko, vo = kg.copy(), vg.copy()
+    assert eng.dpuf_amd_engine_get_kv(p.g, 1, 5, 0, 300, M.ptr(kg), M.ptr(vg)) == 0
+    assert orc.orc_engine_get_kv(p.o, 1, 5, 0, 300, M.ptr(ko), M.ptr(vo)) == 0
+    assert bits_equal(kg, ko) and bits_equal(vg, vo)
+    log("q8 kv: decode after 300 injected positions")
+    lg, lo = p.forward(np.array([17], np.int32), 300)
+    assert bits_equal(lg, lo), maxdiff(lg, lo)
+    greedy(p, lg, lo, 301, 3, "q8 inject")
+    tok = int(np.argmax(lo[-1]))
+    out = C.c_int32(-1)
+    for s in range(3):
+        pos = 304 + s
+        rc = eng.dpuf_amd_engine_forward_argmax(p.g, 1, M.ptr(np.array([tok], np.int32)), pos, None, 1,
+                                                C.byref(out), None)
+        assert rc == 0
+        lo = np.zeros(4096, np.float32)
+        assert orc.orc_engine_forward(p.o, 1, M.ptr(np.array([tok], np.int32)), pos, None, 1, M.ptr(lo)) == 0
+        assert out.value == orc.orc_argmax(M.ptr(lo), 4096)
+        tok = out.value
+    p.close()
+
+
+def test_q8_prefix_slots_and_refusals(eng, orc):
+    """Prefix freeze / apply / reset and a second slot with the int8 cache,
+    in lockstep with the oracle; the multi-session entry refuses an int8
+    cache (-5)."""
+    m, cfg = q8_model(TINY, 64, 221)
+    p = Q8Pair(eng, orc, m, cfg)
+    ids = np.random.default_rng(222).integers(0, 4096, 12).astype(np.int32)
+    lg, lo = p.forward(ids, 0, only_last=0)
+    assert bits_equal(lg, lo)
+    assert eng.dpuf_engine_freeze_prefix(p.g, 1, 8) == 1 and orc.orc_engine_freeze_prefix(p.o, 1, 8) == 1
+    assert eng.dpuf_engine_apply_prefix(p.g, 4, 1) == 8 and orc.orc_engine_apply_prefix(p.o, 4, 1) == 8
+    p.set_slot(4)
+    l4, o4 = p.forward(ids[8:], 8, only_last=0)
+    assert bits_equal(l4, o4) and bits_equal(l4, lg[8:])
+    greedy(p, l4, o4, 12, 3, "q8 slot 4")
+    eng.dpuf_engine_reset_slot(p.g, 4)
+    orc.orc_engine_reset_slot(p.o, 4)
+    lr, lor = p.forward(ids[8:], 8, only_last=0)
+    assert bits_equal(lr, lor)
+    got = np.zeros(1, np.int32)
+    rc = eng.dpuf_amd_engine_forward_slots(p.g, 1, M.ptr(np.array([4], np.int32)), M.ptr(np.array([5], np.int32)),
+                                          M.ptr(np.array([12], np.int32)), None, M.ptr(got))
+    assert rc == -5
+    p.close()
