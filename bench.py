@@ -335,6 +335,49 @@ def main():
         log(f"long context {args.long_ctx}: {ms_long:.3f} ms/token ({1e3 / ms_long:.1f} tok/s), attention "
             f"{att_ms:.3f} ms/token -> KV reads {long['kv_read_GBs']} GB/s")
 
+    # --- the same long-context decode over the int8 KV cache (kv_type 1) -----
+    long_q8 = None
+    if args.long_ctx > 0:
+        from dpuf_amd import abi as A
+        qcfg = A.DpufModelConfig.from_buffer_copy(model.cfg.contents)
+        qcfg.kv_type = 1
+        hq = eng.dpuf_engine_create(*model.create_args(qcfg))
+        if not hq:
+            sys.exit("dpuf_engine_create (int8 KV) failed: " + eng.dpuf_amd_last_error().decode())
+        L, nkv, hd = shape["num_layers"], shape["num_kv_heads"], shape["head_dim"]
+        krng = np.random.default_rng(args.seed + 4096)  # the fp32 leg's K/V, quantised by set_kv
+        for layer in range(L):
+            for kh in range(nkv):
+                kk = krng.standard_normal((args.long_ctx, hd), dtype=np.float32)
+                vv = krng.standard_normal((args.long_ctx, hd), dtype=np.float32)
+                assert eng.dpuf_amd_engine_set_kv(hq, layer, kh, 0, args.long_ctx, M.ptr(kk), M.ptr(vv)) == 0
+
+        def qdecode(tok, pos, n):
+            for i in range(n):
+                rc = eng.dpuf_engine_forward_token(hq, tok, pos + i, M.ptr(logits))
+                assert rc == 0, (rc, eng.dpuf_amd_last_error())
+                tok = int(np.argmax(logits))
+            return tok
+
+        qsteps = min(args.long_steps, 32)
+        tok = qdecode(int(rng.integers(0, V)), args.long_ctx, 2)
+        t0 = time.perf_counter()
+        qdecode(tok, args.long_ctx + 2, qsteps)
+        ms_q = (time.perf_counter() - t0) * 1e3 / qsteps
+        eng.dpuf_amd_engine_set_timing(hq, 1)
+        qdecode(tok, args.long_ctx + 2 + qsteps, 4)
+        ams, acnt, aby = C.c_double(), C.c_int64(), C.c_double()
+        eng.dpuf_amd_engine_get_timing(hq, KINDS.index("attention"), C.byref(ams), C.byref(acnt), C.byref(aby))
+        eng.dpuf_amd_engine_set_timing(hq, 0)
+        att_q = ams.value / 4
+        kvq_bytes = 2 * L * nkv * (args.long_ctx + qsteps) * (hd + hd // 32 * 4)
+        long_q8 = dict(ctx=args.long_ctx, steps=qsteps, ms_per_token=round(ms_q, 4), tok_s=round(1e3 / ms_q, 3),
+                       attention_ms_per_token=round(att_q, 4), kv_bytes_per_token=kvq_bytes,
+                       kv_read_GBs=round(kvq_bytes / (att_q * 1e-3) / 1e9, 1))
+        log(f"long context {args.long_ctx}, int8 KV cache: {ms_q:.3f} ms/token ({1e3 / ms_q:.1f} tok/s), attention "
+            f"{att_q:.3f} ms/token")
+        eng.dpuf_engine_destroy(hq)
+
     eng.dpuf_engine_destroy(h)
 
     # --- LM head in isolation: Zone-A early exit vs the full vocabulary -----
@@ -514,6 +557,7 @@ def main():
         "pp": pp,
         "multi_session": multi,
         "long_context": long,
+        "long_context_kv_q8": long_q8,
         "lm_head_early_exit": lmh,
         "gemv_shapes": gemv_shapes,
         "roofline": rl,

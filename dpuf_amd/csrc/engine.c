@@ -760,8 +760,8 @@ static void enqueue_layers(Engine* e, int32_t M, int32_t keep_tiles) {
                 const DpufKvQ8 c8 = slot_q8(e, e->active, l);
                 dpuf_hip_qk_rope_kv(s, M, e->q, e->k, e->v, e->d_norm[4 * l + 1], e->d_norm[4 * l + 2], eps,
                                     e->d_cos, e->d_sin, NULL, NULL, e->d_pos0, e->nq, e->nkv, e->hd, e->max_seq, &c8);
-                dpuf_hip_attn_q8(s, M, e->q, c8, e->ao, e->scores, e->d_pos0, e->nq, e->nkv, e->hd, e->max_seq,
-                                 scale);
+                dpuf_hip_attn_q8(s, M, e->capturing ? e->max_seq : e->host_pos0 + M, e->q, c8, e->ao, e->scores,
+                                 e->d_pos0, e->nq, e->nkv, e->hd, e->max_seq, scale);
                 dpuf_hip_prep(s, M, e->qd, e->ao, W[W_O].sign, e->prep[0]);
                 fused = 1;
             } else if (e->ms_n > 0)  /* one token per session, each with its own cache */
@@ -777,11 +777,11 @@ static void enqueue_layers(Engine* e, int32_t M, int32_t keep_tiles) {
                 dpuf_hip_qk_rope_kv(s, M, e->q, e->k, e->v, e->d_norm[4 * l + 1], e->d_norm[4 * l + 2], eps,
                                     e->d_cos, e->d_sin, kc, vc, e->d_pos0, e->nq, e->nkv, e->hd, e->max_seq, NULL);
                 const int32_t lmax = e->capturing ? e->max_seq : e->host_pos0 + M;
-                /* the O-input prep rides with the prefill softmax + P.V
-                 * kernel when it can; otherwise it is a launch of its own */
+                /* the O-input prep rides with the last attention kernel when
+                 * it can; otherwise it is a launch of its own */
                 int32_t prepped = 0;
-                if (dpuf_hip_attn_split(s, M, lmax, e->q, kc, vc, e->ao, e->scores, e->d_pos0, e->nq, e->nkv, e->hd,
-                                        e->max_seq, scale, W[W_O].sign, e->prep[0], &prepped) != 0)
+                if (dpuf_hip_attn_split(s, M, lmax, e->q, kc, vc, e->ao, e->scores, e->d_pos0, e->nq, e->nkv,
+                                        e->hd, e->max_seq, scale, W[W_O].sign, e->prep[0], &prepped) != 0)
                     dpuf_hip_attn(s, M, e->q, kc, vc, e->ao, e->scores, e->d_pos0, e->nq, e->nkv, e->hd,
                                   e->max_seq, scale);
                 if (!prepped) dpuf_hip_prep(s, M, e->qd, e->ao, W[W_O].sign, e->prep[0]);

@@ -129,8 +129,8 @@ int32_t dpuf_hip_attn_split(void* s, int32_t M, int32_t lmax, const float* q, co
                             float* out, float* scores, const int32_t* pos0p, int32_t n_q, int32_t n_kv, int32_t hd,
                             int32_t max_seq, float scale, const uint8_t* o_sign, DpufPrep op, int32_t* prepped);
 /* Attention over the int8 KV cache (kv_type 1) for M tokens at positions
- * pos0 .. pos0 + M - 1 of one layer. */
-void dpuf_hip_attn_q8(void* s, int32_t M, const float* q, DpufKvQ8 c8, float* out, float* scores,
+ * pos0 .. pos0 + M - 1 of one layer; lmax bounds the keys any replay reaches. */
+void dpuf_hip_attn_q8(void* s, int32_t M, int32_t lmax, const float* q, DpufKvQ8 c8, float* out, float* scores,
                       const int32_t* pos0, int32_t n_q, int32_t n_kv, int32_t hd, int32_t max_seq, float scale);
 /* n rows of fp32 K and V (device) quantised into rows row0 .. of the int8
  * cache, as the KV store does; and n values from element off dequantised. */

@@ -1911,11 +1911,17 @@ DEV float pv_chain(const float* p, const float* v, int n, float a) {
     return a;
 }
 
-template <int HD, int AP_NT>
+// With Q8 (the int8 KV cache) V comes from vq / vsc instead of vc: the dim
+// chunk lies inside one 32-column block (dw <= 32), its int8 values are
+// widened to floats in LDS (exact), and per chunk W[r][t] = p[r][t] * vs[t]
+// (the reference's p * v_scale, dpuf_engine.c:726-747) takes p's place in the
+// chains.
+template <int HD, int AP_NT, bool Q8>
 __global__ __launch_bounds__(AP_NT) void k_attn_pv(const float* __restrict__ S, const float* __restrict__ vc,
                                                  const int32_t* __restrict__ pos0p, int M, int n_q, int n_kv,
                                                  int max_seq, int qt, int dw, int lcap, int vk,
-                                                 float* __restrict__ out) {
+                                                 float* __restrict__ out, const int8_t* __restrict__ vq,
+                                                 const float* __restrict__ vsc) {
     extern __shared__ __align__(16) float sm[];
     __shared__ float part[AP_NT];
     __shared__ float rowv[32][2];  // max, 1 / sum
@@ -1926,20 +1932,33 @@ __global__ __launch_bounds__(AP_NT) void k_attn_pv(const float* __restrict__ S, 
     float* P = sm;  // [R][lcap], padded to a multiple of 1024 floats
     float* Vs = sm + ((R * lcap + 1023) & ~1023);  // [2][dw][vk + 4]: a dim's keys contiguous
     const int vld = vk + 4;
+    float* scl = Vs + 2 * dw * vld;  // Q8: [2][vk] scales of the chunk's keys
+    float* Wq = scl + 2 * vk;        // Q8: [R][vk] weights p * scale
     auto row_len = [&](int r) { return m0 + r / G < M ? pos0 + m0 + r / G + 1 : 0; };
     int Lmax = 0;
     for (int r = 0; r < R; r++) Lmax = row_len(r) > Lmax ? row_len(r) : Lmax;
     // V chunk c -> registers (issued early); registers -> LDS, transposed
-    const float* Vh = vc + (size_t)kvh * max_seq * HD + d0;
-    const int nv4 = vk * (dw / 4);  // float4 per chunk (1024)
+    const float* Vh = Q8 ? nullptr : vc + (size_t)kvh * max_seq * HD + d0;
+    const int8_t* Vq = Q8 ? vq + (size_t)kvh * max_seq * HD + d0 : nullptr;
+    const float* Vsc = Q8 ? vsc + (size_t)kvh * max_seq * (HD / 32) + (d0 >> 5) : nullptr;
+    const int nv4 = vk * (dw / 4);  // 4-dim pieces per chunk (1024)
     constexpr int NV = 1024 / AP_NT;
     float4 vreg[NV];
+    float sreg[NV];  // Q8: scales of keys tid + AP_NT k of the chunk (vk <= 1024)
     auto v_load = [&](int c0) {
 #pragma unroll
         for (int k = 0; k < NV; k++) {
             const int e = tid + AP_NT * k, kr = e / (dw / 4), c = e % (dw / 4);
-            vreg[k] = (e < nv4 && c0 + kr < Lmax) ? *(const float4*)(Vh + (size_t)(c0 + kr) * HD + 4 * c)
-                                                  : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            const bool ok = e < nv4 && c0 + kr < Lmax;
+            if (Q8) {
+                const uint32_t w = ok ? *(const uint32_t*)(Vq + (size_t)(c0 + kr) * HD + 4 * c) : 0u;
+                vreg[k] = make_float4((float)(int8_t)(w & 0xFF), (float)(int8_t)((w >> 8) & 0xFF),
+                                      (float)(int8_t)((w >> 16) & 0xFF), (float)(int8_t)(w >> 24));
+                sreg[k] = (e < vk && c0 + e < Lmax) ? Vsc[(size_t)(c0 + e) * (HD / 32)] : 0.0f;
+            } else {
+                vreg[k] = ok ? *(const float4*)(Vh + (size_t)(c0 + kr) * HD + 4 * c)
+                             : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            }
         }
     };
     auto v_store = [&](int buf) {
@@ -1953,6 +1972,7 @@ __global__ __launch_bounds__(AP_NT) void k_attn_pv(const float* __restrict__ S, 
                 vb[(4 * c + 2) * vld + kr] = vreg[k].z;
                 vb[(4 * c + 3) * vld + kr] = vreg[k].w;
             }
+            if (Q8 && e < vk) scl[buf * vk + e] = sreg[k];
         }
     };
     v_load(0);
@@ -2059,19 +2079,30 @@ __global__ __launch_bounds__(AP_NT) void k_attn_pv(const float* __restrict__ S, 
     const int r = tid / dw, d = tid % dw;
     const bool act = r < R && row_len(r) > 0;
     const int L = act ? row_len(r) : 0;
-    const bool nested = (G & 1) && (r % G) == G - 1 && (HD & 63) == 0;
-    const float* prow = P + (act ? r : 0) * lcap;
+    // the fp32 single-head path chains nested key pairs; the int8 one does not
+    // (dpuf_engine.c:535-558 against 764-778)
+    const bool nested = !Q8 && (G & 1) && (r % G) == G - 1 && (HD & 63) == 0;
+    const float* prow = Q8 ? Wq + (act ? r : 0) * vk : P + (act ? r : 0) * lcap;
     float a = 0.0f;
     int buf = 0;
     for (int c0 = 0; c0 < Lmax; c0 += vk) {
         const bool more = c0 + vk < Lmax;
         if (more) v_load(c0 + vk);
         __syncthreads();  // chunk c0 in Vs[buf] (and P normalised on the first pass)
+        if (Q8) {
+            for (int e = tid; e < R * vk; e += AP_NT) {
+                const int rr = e / vk, t = e % vk;
+                Wq[e] = c0 + t < row_len(rr) ? P[rr * lcap + c0 + t] * scl[buf * vk + t] : 0.0f;
+            }
+            __syncthreads();
+        }
         if (act && c0 < L) {
             const int n = L - c0 < vk ? L - c0 : vk;
             const float* vp = Vs + buf * dw * vld + d * vld;
-            a = nested ? pv_chain<true>(prow + c0, vp, n, a) : pv_chain<false>(prow + c0, vp, n, a);
+            const float* pr = Q8 ? prow : prow + c0;
+            a = nested ? pv_chain<true>(pr, vp, n, a) : pv_chain<false>(pr, vp, n, a);
         }
+        if (Q8) __syncthreads();  // every chain is done with Wq
         if (more) v_store(buf ^ 1);
         buf ^= 1;
     }
@@ -2488,10 +2519,98 @@ DEV float q8_dot_score(const float* q, const int8_t* kp, const float* ks, int hd
     return hsum8(tot);
 }
 
-__global__ __launch_bounds__(256) void k_attn_q8(const float* __restrict__ q, DpufKvQ8 c8, float* __restrict__ out,
-                                                 float* __restrict__ scores, const int32_t* __restrict__ pos0p,
-                                                 int n_q, int n_kv, int hd, int max_seq, float scale) {
-    extern __shared__ float qs[];  // 2 * hd
+// Scores over the int8 cache: workgroup (kv head, 64 keys, token); the key
+// chunk (int8 rows and scales) and the G query rows in LDS; thread (head,
+// key) forms one score with the pair path's or dot_f32_q8_blk32's order.
+#define Q8_SCK 64
+
+__global__ __launch_bounds__(256) void k_attn_q8_sc(const float* __restrict__ q, DpufKvQ8 c8,
+                                                    float* __restrict__ scores, const int32_t* __restrict__ pos0p,
+                                                    int n_q, int n_kv, int hd, int max_seq, float scale) {
+    extern __shared__ __align__(16) float sq[];  // [G][hd] q rows, then [Q8_SCK][hd] int8 K, [Q8_SCK][nb] scales
+    const int kvh = blockIdx.x, t0 = blockIdx.y * Q8_SCK, m = blockIdx.z, tid = threadIdx.x;
+    const int G = n_q / n_kv, nb = hd >> 5;
+    const int kv_len = *pos0p + m + 1, n2 = kv_len & ~1;
+    if (t0 >= kv_len) return;  // whole workgroup
+    int8_t* kl = (int8_t*)(sq + G * hd);
+    float* kls = (float*)(kl + Q8_SCK * hd);
+    for (int e = tid; e < G * hd / 4; e += 256)
+        *(float4*)&sq[4 * e] = *(const float4*)(q + ((size_t)m * n_q + kvh * G) * hd + 4 * e);
+    const int8_t* K = c8.kq + (size_t)kvh * max_seq * hd;
+    const float* KS = c8.ks + (size_t)kvh * max_seq * nb;
+    for (int e = tid; e < Q8_SCK * hd / 16; e += 256) {
+        const int t = t0 + (16 * e) / hd;
+        *(int4*)(kl + 16 * e) =
+            t < kv_len ? *(const int4*)(K + (size_t)t0 * hd + 16 * (size_t)e) : make_int4(0, 0, 0, 0);
+    }
+    for (int e = tid; e < Q8_SCK * nb; e += 256) {
+        const int t = t0 + e / nb;
+        kls[e] = t < kv_len ? KS[(size_t)t0 * nb + e] : 0.0f;
+    }
+    __syncthreads();
+    for (int o = tid; o < G * Q8_SCK; o += 256) {
+        const int r = o / Q8_SCK, kk = o % Q8_SCK, t = t0 + kk;
+        if (t >= kv_len) continue;
+        const bool pair = 2 * (r / 2) + 1 < G;  // r belongs to a query-head pair
+        const float* qr = sq + r * hd;
+        const int8_t* kp = kl + kk * hd;
+        const float* ksp = kls + kk * nb;
+        const float sc = (pair && t < n2) ? q8_pair_score(qr, kp, ksp, hd) : q8_dot_score(qr, kp, ksp, hd);
+        scores[((size_t)m * n_q + kvh * G + r) * max_seq + t] = sc * scale;
+    }
+}
+
+// One output's chain a = fma(w[t], float(v[t * ld]), a) over n keys of an
+// LDS chunk, in key order; 16 keys a batch, the next batch's LDS reads issued
+// before the current batch's FMAs so LDS latency stays off the chain.
+DEV void q8_pv_load(const float* w, const int8_t* v, int ld, int t, float4 (&wb)[4], int (&vb)[16]) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) wb[i] = *(const float4*)(w + t + 4 * i);
+#pragma unroll
+    for (int j = 0; j < 16; j++) vb[j] = v[(t + j) * ld];
+}
+
+DEV float q8_pv_fma(const float4 (&wb)[4], const int (&vb)[16], float a) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        a = fmaf(wb[i].x, (float)vb[4 * i], a);
+        a = fmaf(wb[i].y, (float)vb[4 * i + 1], a);
+        a = fmaf(wb[i].z, (float)vb[4 * i + 2], a);
+        a = fmaf(wb[i].w, (float)vb[4 * i + 3], a);
+    }
+    return a;
+}
+
+DEV float q8_pv_chain(const float* w, const int8_t* v, int ld, int n, float a) {
+    const int n16 = n & ~15;
+    int t = 0;
+    if (n16 > 0) {
+        float4 wa[4], wc[4];
+        int va[16], vc[16];
+        q8_pv_load(w, v, ld, 0, wa, va);
+        for (t = 0; t + 32 <= n16; t += 32) {
+            q8_pv_load(w, v, ld, t + 16, wc, vc);
+            __builtin_amdgcn_sched_barrier(0);  // keep the next batch's reads ahead of these FMAs
+            a = q8_pv_fma(wa, va, a);
+            q8_pv_load(w, v, ld, t + 32 < n16 ? t + 32 : t, wa, va);  // the last reload is unused
+            __builtin_amdgcn_sched_barrier(0);
+            a = q8_pv_fma(wc, vc, a);
+        }
+        if (t < n16) {
+            a = q8_pv_fma(wa, va, a);
+            t += 16;
+        }
+    }
+    for (; t < n; t++) a = fmaf(w[t], (float)v[t * ld], a);
+    return a;
+}
+
+// Softmax and P.V over the int8 cache, workgroup (token, kv head, pair),
+// from the scores k_attn_q8_sc wrote.
+__global__ __launch_bounds__(256) void k_attn_q8(DpufKvQ8 c8, float* __restrict__ out, float* __restrict__ scores,
+                                                 const int32_t* __restrict__ pos0p, int n_q, int n_kv, int hd,
+                                                 int max_seq) {
+    extern __shared__ __align__(16) uint8_t lds_q8[];
     __shared__ float red[2][256];
     __shared__ float vs8[2][8];
     __shared__ float inv_sh[2];
@@ -2502,31 +2621,16 @@ __global__ __launch_bounds__(256) void k_attn_q8(const float* __restrict__ q, Dp
     const int nh = pair ? 2 : 1;
     const int qh0 = kvh * groups + g0;
     const int kv_len = *pos0p + m + 1;
-    const int8_t* K = c8.kq + (size_t)kvh * max_seq * hd;
     const int8_t* V = c8.vq + (size_t)kvh * max_seq * hd;
-    const float* KS = c8.ks + (size_t)kvh * max_seq * nb;
     const float* VS = c8.vs + (size_t)kvh * max_seq * nb;
-    for (int i = tid; i < nh * hd; i += blockDim.x) qs[i] = q[((size_t)m * n_q + qh0) * hd + i];
-    __syncthreads();
     float* sc0 = scores + ((size_t)m * n_q + qh0) * max_seq;
     float* sc1 = sc0 + max_seq;
-    const int n2 = kv_len & ~1;  // keys of the pair path's two-key steps
     float mx0 = -1e30f, mx1 = -1e30f;
     for (int t = tid; t < kv_len; t += blockDim.x) {
-        const int8_t* kp = K + (size_t)t * hd;
-        const float* ksp = KS + (size_t)t * nb;
-        float s0, s1 = 0.0f;
-        if (pair && t < n2) {
-            s0 = q8_pair_score(qs, kp, ksp, hd) * scale;
-            s1 = q8_pair_score(qs + hd, kp, ksp, hd) * scale;
-        } else {
-            s0 = q8_dot_score(qs, kp, ksp, hd) * scale;
-            if (pair) s1 = q8_dot_score(qs + hd, kp, ksp, hd) * scale;
-        }
-        sc0[t] = s0;
+        const float s0 = sc0[t];
         mx0 = s0 > mx0 ? s0 : mx0;
         if (pair) {
-            sc1[t] = s1;
+            const float s1 = sc1[t];
             mx1 = s1 > mx1 ? s1 : mx1;
         }
     }
@@ -2569,13 +2673,84 @@ __global__ __launch_bounds__(256) void k_attn_q8(const float* __restrict__ q, Dp
         if (pair) sc1[t] = sc1[t] * inv_sh[1];
     }
     __syncthreads();
-    for (int o = tid; o < nh * hd; o += blockDim.x) {
-        const int hsel = o / hd, d = o % hd, b = d >> 5;
-        const float* p = hsel ? sc1 : sc0;
-        float a = 0.0f;
-        for (int t = 0; t < kv_len; t++) a = fmaf(p[t] * VS[(size_t)t * nb + b], (float)V[(size_t)t * hd + d], a);
-        out[((size_t)m * n_q + qh0 + hsel) * hd + d] = a;
+    // P.V over chunks of ck keys staged in LDS: the chunk's int8 V rows and,
+    // per (head, key, block), the weight w = p * v_scale (the reference's
+    // p * vs product, formed once per chunk instead of once per dim); the next
+    // chunk's V and scales are read into registers while this one's chains
+    // run.  Thread (head, dim) then runs a = fma(w, float(v), a) in key order.
+    const int ck = 32768 / hd;                 // keys per chunk: 32 KB of V
+    int8_t* vl = (int8_t*)lds_q8;              // [2][ck][hd]
+    float* wl = (float*)(vl + 2 * ck * hd);    // [2][2][nb][ck]
+    constexpr int VR = 8;                      // 16-byte V loads per thread per chunk
+    int4 vr[VR];
+    float4 sr;
+    const int vper = ck * hd / 16;             // 16-byte pieces of a V chunk (2048)
+    const int sper = ck * nb / 4;              // float4 of its scales
+    auto ld = [&](int c0) {
+#pragma unroll
+        for (int k = 0; k < VR; k++) {
+            const int e = tid + 256 * k;
+            const int t = c0 + (16 * e) / hd;
+            vr[k] = e < vper && t < kv_len ? *(const int4*)(V + (size_t)c0 * hd + 16 * (size_t)e)
+                                           : make_int4(0, 0, 0, 0);
+        }
+        // 4 (key, block) scales per thread; keys past kv_len are not read
+        float sv4[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int e = 4 * tid + i;
+            sv4[i] = tid < sper && c0 + e / nb < kv_len ? VS[(size_t)c0 * nb + e] : 0.0f;
+        }
+        sr = make_float4(sv4[0], sv4[1], sv4[2], sv4[3]);
+    };
+    auto st = [&](int buf, int c0) {
+        int8_t* vb = vl + (size_t)buf * ck * hd;
+#pragma unroll
+        for (int k = 0; k < VR; k++) {
+            const int e = tid + 256 * k;
+            if (e < vper) *(int4*)(vb + 16 * e) = vr[k];
+        }
+        // weights from the scales just read: element 4 tid + i is (key, block)
+        float* wb = wl + (size_t)buf * 2 * nb * ck;
+        if (tid < sper) {
+            const float sv[4] = {sr.x, sr.y, sr.z, sr.w};
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int e = 4 * tid + i, tk = e / nb, b = e % nb;
+                if (c0 + tk < kv_len) {
+                    wb[b * ck + tk] = sc0[c0 + tk] * sv[i];
+                    if (pair) wb[(nb + b) * ck + tk] = sc1[c0 + tk] * sv[i];
+                }
+            }
+        }
+    };
+    const int o0 = tid, o1 = tid + 256;  // up to two outputs per thread (2 x 256 dims)
+    float acc0 = 0.0f, acc1 = 0.0f;
+    ld(0);
+    st(0, 0);
+    __syncthreads();
+    int buf = 0;
+    for (int c0 = 0; c0 < kv_len; c0 += ck) {
+        const bool more = c0 + ck < kv_len;
+        if (more) ld(c0 + ck);
+        const int n = kv_len - c0 < ck ? kv_len - c0 : ck;
+        const int8_t* vb = vl + (size_t)buf * ck * hd;
+        const float* wb = wl + (size_t)buf * 2 * nb * ck;
+        if (o0 < nh * hd) {
+            const int hsel = o0 / hd, d = o0 % hd;
+            acc0 = q8_pv_chain(wb + (size_t)(hsel * nb + (d >> 5)) * ck, vb + d, hd, n, acc0);
+        }
+        if (o1 < nh * hd) {
+            const int hsel = o1 / hd, d = o1 % hd;
+            acc1 = q8_pv_chain(wb + (size_t)(hsel * nb + (d >> 5)) * ck, vb + d, hd, n, acc1);
+        }
+        __syncthreads();  // every chain is done with buffer buf ^ 1's last use
+        if (more) st(buf ^ 1, c0 + ck);
+        __syncthreads();
+        buf ^= 1;
     }
+    if (o0 < nh * hd) out[((size_t)m * n_q + qh0) * hd + o0] = acc0;
+    if (o1 < nh * hd) out[((size_t)m * n_q + qh0) * hd + o1] = acc1;
 }
 
 // Rows of fp32 K and V (n rows of HD, one wave per row and tensor) into the
@@ -3773,29 +3948,29 @@ int32_t dpuf_hip_attn_split(void* s, int32_t M, int32_t lmax, const float* q, co
         hipLaunchKernelGGL(k_attn_sc<64>, g1, dim3(256), lds1, ST(s), q, kc, pos0p, M, n_q, n_kv, max_seq, scale,
                            qt1, scores);
         if (wide)
-            hipLaunchKernelGGL((k_attn_pv<64, 1024>), g2, b2, lds2, ST(s), scores, vc, pos0p, M, n_q, n_kv, max_seq,
-                               qt2, dw, lcap, vk, out);
+            hipLaunchKernelGGL((k_attn_pv<64, 1024, false>), g2, b2, lds2, ST(s), scores, vc, pos0p, M, n_q, n_kv,
+                               max_seq, qt2, dw, lcap, vk, out, nullptr, nullptr);
         else
-            hipLaunchKernelGGL((k_attn_pv<64, 256>), g2, b2, lds2, ST(s), scores, vc, pos0p, M, n_q, n_kv, max_seq,
-                               qt2, dw, lcap, vk, out);
+            hipLaunchKernelGGL((k_attn_pv<64, 256, false>), g2, b2, lds2, ST(s), scores, vc, pos0p, M, n_q, n_kv,
+                               max_seq, qt2, dw, lcap, vk, out, nullptr, nullptr);
     } else if (hd == 128) {
         hipLaunchKernelGGL(k_attn_sc<128>, g1, dim3(256), lds1, ST(s), q, kc, pos0p, M, n_q, n_kv, max_seq, scale,
                            qt1, scores);
         if (wide)
-            hipLaunchKernelGGL((k_attn_pv<128, 1024>), g2, b2, lds2, ST(s), scores, vc, pos0p, M, n_q, n_kv,
-                               max_seq, qt2, dw, lcap, vk, out);
+            hipLaunchKernelGGL((k_attn_pv<128, 1024, false>), g2, b2, lds2, ST(s), scores, vc, pos0p, M, n_q,
+                               n_kv, max_seq, qt2, dw, lcap, vk, out, nullptr, nullptr);
         else
-            hipLaunchKernelGGL((k_attn_pv<128, 256>), g2, b2, lds2, ST(s), scores, vc, pos0p, M, n_q, n_kv,
-                               max_seq, qt2, dw, lcap, vk, out);
+            hipLaunchKernelGGL((k_attn_pv<128, 256, false>), g2, b2, lds2, ST(s), scores, vc, pos0p, M, n_q,
+                               n_kv, max_seq, qt2, dw, lcap, vk, out, nullptr, nullptr);
     } else {
         hipLaunchKernelGGL(k_attn_sc<256>, g1, dim3(256), lds1, ST(s), q, kc, pos0p, M, n_q, n_kv, max_seq, scale,
                            qt1, scores);
         if (wide)
-            hipLaunchKernelGGL((k_attn_pv<256, 1024>), g2, b2, lds2, ST(s), scores, vc, pos0p, M, n_q, n_kv,
-                               max_seq, qt2, dw, lcap, vk, out);
+            hipLaunchKernelGGL((k_attn_pv<256, 1024, false>), g2, b2, lds2, ST(s), scores, vc, pos0p, M, n_q,
+                               n_kv, max_seq, qt2, dw, lcap, vk, out, nullptr, nullptr);
         else
-            hipLaunchKernelGGL((k_attn_pv<256, 256>), g2, b2, lds2, ST(s), scores, vc, pos0p, M, n_q, n_kv,
-                               max_seq, qt2, dw, lcap, vk, out);
+            hipLaunchKernelGGL((k_attn_pv<256, 256, false>), g2, b2, lds2, ST(s), scores, vc, pos0p, M, n_q,
+                               n_kv, max_seq, qt2, dw, lcap, vk, out, nullptr, nullptr);
     }
     LAUNCHED("k_attn_split");
     return 0;
@@ -3809,12 +3984,49 @@ void dpuf_hip_attn(void* s, int32_t M, const float* q, const float* kc, const fl
     LAUNCHED("k_attn");
 }
 
-void dpuf_hip_attn_q8(void* s, int32_t M, const float* q, DpufKvQ8 c8, float* out, float* scores,
+void dpuf_hip_attn_q8(void* s, int32_t M, int32_t lmax, const float* q, DpufKvQ8 c8, float* out, float* scores,
                       const int32_t* pos0, int32_t n_q, int32_t n_kv, int32_t hd, int32_t max_seq, float scale) {
-    const int groups = n_q / n_kv;
-    hipLaunchKernelGGL(k_attn_q8, dim3(M, n_kv, (groups + 1) / 2), dim3(256), (size_t)2 * hd * sizeof(float), ST(s),
-                       q, c8, out, scores, pos0, n_q, n_kv, hd, max_seq, scale);
-    LAUNCHED("k_attn_q8");
+    const int G = n_q / n_kv;
+    if (lmax > max_seq) lmax = max_seq;
+    const size_t lds1 = (size_t)G * hd * 4 + (size_t)Q8_SCK * hd + (size_t)Q8_SCK * (hd / 32) * 4;
+    hipLaunchKernelGGL(k_attn_q8_sc, dim3(n_kv, (lmax + Q8_SCK - 1) / Q8_SCK, M), dim3(256), lds1, ST(s), q, c8,
+                       scores, pos0, n_q, n_kv, hd, max_seq, scale);
+    // softmax + P.V: the split kernel (as the fp32 cache's) when its tile of
+    // probability rows fits in LDS, each dim chunk inside one 32-column block
+    const int lcap = (lmax + 7) & ~7;
+    const size_t budget = 112 * 1024;
+    int qt2 = 8 / G > 1 ? 8 / G : 1;
+    if (qt2 > M) qt2 = M;
+    while (qt2 > 1 && (size_t)qt2 * G * lcap * 4 > budget) qt2--;
+    if (G <= 32 && (size_t)qt2 * G * lcap * 4 <= budget) {
+        const int R = qt2 * G;
+        int dc = 1;
+        while (dc < hd / 4 && R * (hd / dc) > 256) dc *= 2;
+        const int tiles = n_kv * ((M + qt2 - 1) / qt2);
+        while (dc < hd / 4 && tiles * dc < 128) dc *= 2;
+        while (hd / dc > 32) dc *= 2;
+        const int dw = hd / dc, vk = 4096 / dw;
+        const size_t lds2 = ((((size_t)R * lcap + 1023) & ~(size_t)1023) + 2 * (size_t)(vk + 4) * dw +
+                             2 * (size_t)vk + (size_t)R * vk) * 4;
+        const dim3 g2(n_kv, (M + qt2 - 1) / qt2, dc);
+        const bool wide = (size_t)g2.x * g2.y * g2.z < 1024;
+#define PVQ(HDV, NT)                                                                                              \
+    hipLaunchKernelGGL((k_attn_pv<HDV, NT, true>), g2, dim3(NT), lds2, ST(s), scores, nullptr, pos0, M, n_q, n_kv, \
+                       max_seq, qt2, dw, lcap, vk, out, c8.vq, c8.vs)
+        if (lds2 <= 160 * 1024) {
+            if (hd == 64) { if (wide) PVQ(64, 1024); else PVQ(64, 256); }
+            else if (hd == 128) { if (wide) PVQ(128, 1024); else PVQ(128, 256); }
+            else { if (wide) PVQ(256, 1024); else PVQ(256, 256); }
+            LAUNCHED("k_attn_q8_sc/k_attn_pv<q8>");
+            return;
+        }
+#undef PVQ
+    }
+    // rows too long for LDS: softmax in memory, P.V per (token, kv head, pair)
+    const size_t lds2 = 2 * 32768 + (size_t)2 * 2 * (hd / 32) * (32768 / hd) * 4;
+    hipLaunchKernelGGL(k_attn_q8, dim3(M, n_kv, (G + 1) / 2), dim3(256), lds2, ST(s), c8, out, scores, pos0,
+                       n_q, n_kv, hd, max_seq);
+    LAUNCHED("k_attn_q8_sc/k_attn_q8");
 }
 
 void dpuf_hip_q8_rows(void* s, const float* k, const float* v, int32_t n, int32_t hd, DpufKvQ8 c8, size_t row0) {

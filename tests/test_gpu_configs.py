@@ -159,9 +159,10 @@ def test_gqa4_long_context_injected_kv(eng, orc):
 
 
 def test_attention_beyond_split_lds_budget(eng, orc):
-    """Groups of 4 with 7200 cached positions: a row of probabilities no
-    longer fits the split kernels' LDS budget, so decode attention takes the
-    one-pair-per-workgroup kernel (k_attn).  Logits bit-identical."""
+    """Groups of 4 with 7200 cached positions.  A two-token forward there:
+    its rows of probabilities no longer fit the split kernels' LDS budget, so
+    it takes the one-pair-per-workgroup kernel (k_attn); then one-token decode
+    steps (the three-launch long-context path).  Logits bit-identical."""
     shape = dict(hidden_size=256, intermediate_size=512, num_layers=1, num_q_heads=8, num_kv_heads=2,
                  head_dim=128, vocab_size=4096, tie_word_embeddings=1)
     m = M.Model.build(shape, max_seq_len=7240, seed=81)
@@ -170,10 +171,10 @@ def test_attention_beyond_split_lds_budget(eng, orc):
     for kvh in range(2):
         p.set_kv(0, kvh, 0, rng.standard_normal((7200, 128), dtype=np.float32),
                  rng.standard_normal((7200, 128), dtype=np.float32))
-    log("k_attn fallback: decode at position 7200")
-    lg, lo = p.forward(np.array([3], np.int32), 7200)
+    log("k_attn fallback: two tokens at position 7200")
+    lg, lo = p.forward(np.array([3, 4000], np.int32), 7200, only_last=0)
     assert bits_equal(lg, lo), maxdiff(lg, lo)
-    greedy(p, lg, lo, 7201, 2, "fallback")
+    greedy(p, lg, lo, 7202, 3, "after fallback")
     p.close()
 
 

@@ -117,3 +117,22 @@ def test_q8_prefix_slots_and_refusals(eng, orc):
                                           M.ptr(np.array([12], np.int32)), None, M.ptr(got))
     assert rc == -5
     p.close()
+
+
+def test_q8_rows_beyond_lds(eng, orc):
+    """7200 cached positions with groups of 4: a two-token forward's
+    probability rows no longer fit the split kernel's LDS budget, so it takes
+    the softmax-in-memory kernel (k_attn_q8); one-token steps after it take
+    the split kernel again.  Bit-identical."""
+    shape = dict(TINY, num_layers=1, num_q_heads=8, num_kv_heads=2, head_dim=128)
+    m, cfg = q8_model(shape, 7240, 231)
+    p = Q8Pair(eng, orc, m, cfg)
+    rng = np.random.default_rng(232)
+    for kvh in range(2):
+        p.set_kv(0, kvh, 0, rng.standard_normal((7200, 128), dtype=np.float32),
+                 rng.standard_normal((7200, 128), dtype=np.float32))
+    log("q8 kv: two tokens at position 7200")
+    lg, lo = p.forward(np.array([3, 4000], np.int32), 7200, only_last=0)
+    assert bits_equal(lg, lo), maxdiff(lg, lo)
+    greedy(p, lg, lo, 7202, 3, "q8 after 7200")
+    p.close()
