@@ -86,6 +86,7 @@ class DpufToolsSpec(C.Structure):
         ("rms_eps", C.c_float),
         ("rope_theta", C.c_float),
         ("seed", C.c_uint64),
+        ("weight_plan", C.c_int32),
     ]
 
 
@@ -124,6 +125,7 @@ def load_tools():
     _sig(lib, "dpuf_tools_f16_to_f32", C.c_float, [C.c_uint16])
     _sig(lib, "dpuf_tools_sign_bits", None, [P, I32, C.c_uint64, C.c_char_p])
     _sig(lib, "dpuf_tools_pack_mode12", P, [P, I32, I32, P, I32, C.POINTER(C.c_size_t)])
+    _sig(lib, "dpuf_tools_pack_asym", P, [P, I32, I32, P, I32, I32, C.c_float, C.POINTER(C.c_size_t)])
     _sig(lib, "dpuf_tools_bind_blob", I32, [P, C.c_size_t, C.POINTER(DpufWeightDesc)])
     _sig(lib, "dpuf_tools_pack_raw_tiny", P, [P, I32, C.POINTER(C.c_size_t)])
     _sig(lib, "dpuf_tools_build_model", P, [C.POINTER(DpufToolsSpec)])
@@ -150,6 +152,8 @@ ENGINE_SYMBOLS = [
     "dpuf_fwht64_sign_f32", "dpuf_prep_had4_packed_slab",
     "dpuf_matmul_qr_hadamard4_packed_tile_range", "dpuf_matmul_qr_hadamard4_packed_f32",
     "dpuf_embed_qr_hadamard4_packed_f32", "dpuf_embed_qr_any_f32",
+    "dpuf_matmul_qr_had4_asym_tile_range", "dpuf_matmul_qr_had4_asym_f32", "dpuf_embed_qr_had4_asym_f32",
+    "dpuf_matmul_qr_had6_tile_range", "dpuf_matmul_qr_had6_f32", "dpuf_embed_qr_had6_f32",
     "dpuf_engine_create", "dpuf_engine_destroy", "dpuf_engine_reset_cache",
     "dpuf_engine_set_slot", "dpuf_engine_get_slot", "dpuf_engine_reset_slot",
     "dpuf_engine_slot_memory", "dpuf_engine_num_slots", "dpuf_engine_freeze_prefix",
@@ -176,6 +180,10 @@ def load_engine():
     _sig(lib, "dpuf_matmul_qr_hadamard4_packed_f32", None, [I32, I32, I32, I32, P, P, P, P, P])
     _sig(lib, "dpuf_embed_qr_hadamard4_packed_f32", None, [I32, I32, P, P, P, P, P])
     _sig(lib, "dpuf_embed_qr_any_f32", None, [C.POINTER(DpufWeightDesc), I32, P, P, P])
+    for mode in ("had4_asym", "had6"):
+        _sig(lib, f"dpuf_matmul_qr_{mode}_tile_range", None, [I32, I32, I32, I32, I32, P, P, P, P, P, P])
+        _sig(lib, f"dpuf_matmul_qr_{mode}_f32", None, [I32, I32, I32, I32, P, P, P, P, P])
+        _sig(lib, f"dpuf_embed_qr_{mode}_f32", None, [I32, I32, P, P, P, P, P])
     _sig(lib, "dpuf_engine_create", P, [C.POINTER(DpufModelConfig), C.POINTER(DpufLayerWeights),
                                          C.POINTER(DpufWeightDesc), C.POINTER(DpufWeightDesc), P])
     _sig(lib, "dpuf_engine_destroy", None, [P])

@@ -199,13 +199,163 @@ static void encode_row(const float* w, int32_t cols, const float* signs, uint8_t
 
 static size_t pad64(size_t n) { return (64 - (n % 64)) % 64; }
 
-DPUF_EXPORT uint8_t* dpuf_tools_pack_mode12(const float* W, int32_t rows, int32_t cols,
-                                            const uint8_t* sign_bits, int32_t ecc_group, size_t* len) {
+/* One mode 12 group (8 rows from W, rows past n_8 padded): [n_blk][8] fp16
+ * scales, then per 32-block four 32-byte chunks, byte c*32 + ri*4 + k holding
+ * columns 8c+k (low nibble) and 8c+4+k (high nibble) of row ri
+ * (dpuf_format.py:1500-1523). */
+static void encode_group_m12(const float* W, int32_t cols, int32_t n_8, const float* signs, uint8_t* grp,
+                             float* tmp, uint8_t* u4) {
+    const int32_t n_blk = cols / 32;
+    uint16_t* sc = (uint16_t*)grp;
+    uint16_t* scrow = (uint16_t*)malloc((size_t)n_blk * sizeof(uint16_t));
+    for (int ri = 0; ri < 8; ri++) {
+        if (ri < n_8) {
+            encode_row(W + (size_t)ri * cols, cols, signs, u4 + (size_t)ri * cols, scrow, tmp);
+            for (int32_t b = 0; b < n_blk; b++) sc[(size_t)b * 8 + ri] = scrow[b];
+        } else {
+            /* padding rows: u = 8, scale 0 (dpuf_format.py:1507-1511) */
+            memset(u4 + (size_t)ri * cols, 8, (size_t)cols);
+            for (int32_t b = 0; b < n_blk; b++) sc[(size_t)b * 8 + ri] = 0;
+        }
+    }
+    free(scrow);
+    uint8_t* qg = grp + (size_t)n_blk * 16u;
+    for (int32_t b = 0; b < n_blk; b++)
+        for (int c = 0; c < 4; c++)
+            for (int ri = 0; ri < 8; ri++)
+                for (int k = 0; k < 4; k++) {
+                    const uint8_t* ur = u4 + (size_t)ri * cols + 32 * b + 8 * c;
+                    qg[(size_t)b * 128 + c * 32 + ri * 4 + k] = (uint8_t)((ur[4 + k] << 4) | ur[k]);
+                }
+}
+
+/* Weighted least-squares asymmetric code of one 64-block v (after sign and
+ * FWHT): q in [0, qmax], value m + q * d with fp16 d and m.  The search of
+ * dpuf_format.py:1602-1667: for shrink in {0.90, 0.96, 1.00} start from the
+ * shrunk min/max range, refine (d, lo) by lsq_iters weighted least-squares
+ * fits of the rounded codes (weights (|v| + 1e-6)^w_pow, or 1 when w_pow <=
+ * 0), round d and m to fp16, requantise, and keep the candidate of smallest
+ * squared error (strict <, so the first of equal errors stays). */
+static void encode_blk64_asym(const float* v, int qmax, float w_pow, uint16_t* d_out, uint16_t* m_out, uint8_t* q_out) {
+    static const float shrinks[3] = {0.90f, 0.96f, 1.00f};
+    float wt[64];
+    float wmin = v[0], wmax = v[0];
+    for (int k = 0; k < 64; k++) {
+        wt[k] = w_pow > 0.0f ? powf(fabsf(v[k]) + 1e-6f, w_pow) : 1.0f;
+        wmin = v[k] < wmin ? v[k] : wmin;
+        wmax = v[k] > wmax ? v[k] : wmax;
+    }
+    float best_err = INFINITY;
+    uint16_t best_d = 0, best_m = 0;
+    uint8_t best_q[64];
+    memset(best_q, 0, sizeof best_q);
+    for (int si = 0; si < 3; si++) {
+        const float mid = 0.5f * (wmin + wmax);
+        const float half = 0.5f * (wmax - wmin) * shrinks[si];
+        float lo = mid - half;
+        float d = half > 1e-12f ? (2.0f * half) / (float)qmax : 0.0f;
+        for (int it = 0; it < 2; it++) {
+            const float sd = d > 1e-12f ? d : 1.0f;
+            float s0 = 0.0f, sq = 0.0f, sq2 = 0.0f, sw = 0.0f, sqw = 0.0f;
+            for (int k = 0; k < 64; k++) {
+                float q = rintf((v[k] - lo) / sd);
+                q = q < 0.0f ? 0.0f : (q > (float)qmax ? (float)qmax : q);
+                s0 += wt[k];
+                sq += wt[k] * q;
+                sq2 += wt[k] * q * q;
+                sw += wt[k] * v[k];
+                sqw += wt[k] * q * v[k];
+            }
+            const float det = s0 * sq2 - sq * sq;
+            if (det > 1e-12f) {
+                const float dn = (s0 * sqw - sq * sw) / det;
+                const float ln = (sw - dn * sq) / s0;
+                if (dn > 1e-12f) {
+                    d = dn;
+                    lo = ln;
+                }
+            }
+        }
+        const uint16_t m16 = dpuf_tools_f32_to_f16(lo);
+        const uint16_t d16 = dpuf_tools_f32_to_f16(d > 0.0f ? d : 0.0f);
+        const float m32 = dpuf_tools_f16_to_f32(m16), d32 = dpuf_tools_f16_to_f32(d16);
+        const float sdf = d32 > 0.0f ? d32 : 1.0f;
+        uint8_t qc[64];
+        float err = 0.0f;
+        for (int k = 0; k < 64; k++) {
+            float q = rintf((v[k] - m32) / sdf);
+            q = q < 0.0f ? 0.0f : (q > (float)qmax ? (float)qmax : q);
+            qc[k] = d32 > 0.0f ? (uint8_t)q : 0;
+            const float e = (m32 + (float)qc[k] * d32) - v[k];
+            err += e * e;
+        }
+        if (err < best_err) {
+            best_err = err;
+            best_d = d16;
+            best_m = m16;
+            memcpy(best_q, qc, 64);
+        }
+    }
+    *d_out = best_d;
+    *m_out = best_m;
+    memcpy(q_out, best_q, 64);
+}
+
+/* One mode 13 / 14 group (8 rows, rows past n_8 all zero as in
+ * dpuf_format.py:1688-1697): dm [n_64][16] fp16 (d of rows 0..7, then m),
+ * q4 [n_blk][128] in the mode 12 nibble interleave of the low 4 bits, and
+ * for 6 bits q2 [n_blk][64] with bits 4..5 of row ri, column 32b+8c+4h+k at
+ * bits 2(ri>>1) of byte c*16 + h*8 + (ri&1)*4 + k (dpuf_format.py:1699-1718). */
+static void encode_group_asym(const float* W, int32_t cols, int32_t n_8, const float* signs, int bits, float w_pow,
+                              uint8_t* grp, float* tmp, uint8_t* u) {
+    const int32_t n_64 = cols / 64, n_blk = cols / 32;
+    const int qmax = (1 << bits) - 1;
+    uint16_t* dm = (uint16_t*)grp;
+    memset(u, 0, (size_t)8 * cols);
+    memset(dm, 0, (size_t)n_64 * 32u);
+    for (int ri = 0; ri < n_8; ri++) {
+        const float* w = W + (size_t)ri * cols;
+        for (int32_t c = 0; c < cols; c++) tmp[c] = w[c] * signs[c];
+        for (int32_t c = 0; c < cols; c += 64) fwht64(tmp + c);
+        for (int32_t g = 0; g < n_64; g++)
+            encode_blk64_asym(tmp + 64 * g, qmax, w_pow, &dm[(size_t)g * 16 + ri], &dm[(size_t)g * 16 + 8 + ri],
+                              u + (size_t)ri * cols + 64 * g);
+    }
+    uint8_t* q4 = grp + (size_t)n_64 * 32u;
+    for (int32_t b = 0; b < n_blk; b++)
+        for (int c = 0; c < 4; c++)
+            for (int ri = 0; ri < 8; ri++)
+                for (int k = 0; k < 4; k++) {
+                    const uint8_t* ur = u + (size_t)ri * cols + 32 * b + 8 * c;
+                    q4[(size_t)b * 128 + c * 32 + ri * 4 + k] = (uint8_t)(((ur[4 + k] & 15) << 4) | (ur[k] & 15));
+                }
+    if (bits == 6) {
+        uint8_t* q2 = q4 + (size_t)n_blk * 128u;
+        memset(q2, 0, (size_t)n_blk * 64u);
+        for (int32_t b = 0; b < n_blk; b++)
+            for (int c = 0; c < 4; c++)
+                for (int h = 0; h < 2; h++)
+                    for (int ri = 0; ri < 8; ri++)
+                        for (int k = 0; k < 4; k++) {
+                            const uint8_t hv = (uint8_t)((u[(size_t)ri * cols + 32 * b + 8 * c + 4 * h + k] >> 4) & 3);
+                            q2[(size_t)b * 64 + c * 16 + h * 8 + (ri & 1) * 4 + k] |= (uint8_t)(hv << ((ri >> 1) * 2));
+                        }
+    }
+}
+
+/* A QR blob of one matrix (dpuf_format.py:1182-1252 _assemble_qr_blob): the
+ * 64-byte finder header "<B4sBHIIIIQQQ16x", tile offsets, ECC offsets, sign
+ * bits, the tiles (16-byte header with the body's CRC32 and n_rows, body
+ * n_8g * grp_bytes, padded to 64), then per ECC group the XOR parity of its
+ * padded tiles.  bits 0 packs mode 12, 4 mode 13, 6 mode 14. */
+static uint8_t* pack_qr(const float* W, int32_t rows, int32_t cols, const uint8_t* sign_bits, int32_t ecc_group,
+                        int bits, float w_pow, size_t* len) {
     crc_init();
-    if (rows <= 0 || cols <= 0 || (cols % 64) != 0) return NULL;
+    if (rows <= 0 || cols <= 0 || (cols % 64) != 0 || (bits != 0 && bits != 4 && bits != 6)) return NULL;
     const int32_t n_blk = cols / 32;
     const int32_t n_tiles = (rows + 15) / 16;
-    const size_t grp_bytes = (size_t)n_blk * 144u;
+    const size_t grp_bytes = (size_t)n_blk * (bits == 6 ? 208u : 144u);
+    const uint8_t mode = bits == 0 ? DPUF_MODE_QR_HAD4_PACKED : bits == 4 ? DPUF_MODE_QR_HAD4_ASYM : DPUF_MODE_QR_HAD6;
     /* Every tile but possibly the last holds 2 groups; sizes are padded to 64. */
     size_t* t_off = (size_t*)malloc(((size_t)n_tiles + 1) * sizeof(size_t));
     size_t cur = 0;
@@ -238,9 +388,8 @@ DPUF_EXPORT uint8_t* dpuf_tools_pack_mode12(const float* W, int32_t rows, int32_
     uint8_t* blob = (uint8_t*)calloc(total, 1);
     if (!blob) { free(t_off); free(e_off); return NULL; }
 
-    /* finder header "<B4sBHIIIIQQQ16x" */
     uint8_t* h = blob;
-    h[0] = DPUF_MODE_QR_HAD4_PACKED;
+    h[0] = mode;
     memcpy(h + 1, "QRDP", 4);
     h[5] = 16;
     uint16_t eg = (uint16_t)ecc_group;
@@ -268,44 +417,24 @@ DPUF_EXPORT uint8_t* dpuf_tools_pack_mode12(const float* W, int32_t rows, int32_
 #pragma omp parallel for schedule(dynamic, 4)
     for (t = 0; t < n_tiles; t++) {
         float* tmp = (float*)malloc((size_t)cols * sizeof(float));
-        uint8_t* u4 = (uint8_t*)malloc((size_t)cols * 8u);
-        uint16_t* sc = (uint16_t*)malloc((size_t)n_blk * 8u * sizeof(uint16_t));
+        uint8_t* u = (uint8_t*)malloc((size_t)cols * 8u);
         int32_t n_r = (t * 16 + 16 <= rows) ? 16 : rows - t * 16;
         int32_t n_8g = (n_r + 7) / 8;
         uint8_t* tile = blob + tiles_off + t_off[t];
         uint8_t* body = tile + 16;
         for (int32_t rg = 0; rg < n_8g; rg++) {
-            for (int ri = 0; ri < 8; ri++) {
-                int32_t lr = rg * 8 + ri;
-                if (lr < n_r) {
-                    uint16_t scr[4096];
-                    uint16_t* scrow = n_blk <= 4096 ? scr : (uint16_t*)malloc((size_t)n_blk * 2u);
-                    encode_row(W + ((size_t)t * 16 + lr) * (size_t)cols, cols, signs, u4 + (size_t)ri * cols, scrow, tmp);
-                    for (int32_t b = 0; b < n_blk; b++) sc[(size_t)b * 8 + ri] = scrow[b];
-                    if (scrow != scr) free(scrow);
-                } else {
-                    /* padding rows: u = 8, scale 0 (dpuf_format.py:1507-1511) */
-                    memset(u4 + (size_t)ri * cols, 8, (size_t)cols);
-                    for (int32_t b = 0; b < n_blk; b++) sc[(size_t)b * 8 + ri] = 0;
-                }
-            }
+            const int32_t n_8 = n_r - rg * 8 < 8 ? n_r - rg * 8 : 8;
+            const float* Wg = W + ((size_t)t * 16 + (size_t)rg * 8) * (size_t)cols;
             uint8_t* grp = body + (size_t)rg * grp_bytes;
-            memcpy(grp, sc, (size_t)n_blk * 16u);
-            uint8_t* qg = grp + (size_t)n_blk * 16u;
-            for (int32_t b = 0; b < n_blk; b++)
-                for (int c = 0; c < 4; c++)
-                    for (int ri = 0; ri < 8; ri++)
-                        for (int k = 0; k < 4; k++) {
-                            const uint8_t* ur = u4 + (size_t)ri * cols + 32 * b + 8 * c;
-                            qg[(size_t)b * 128 + c * 32 + ri * 4 + k] = (uint8_t)((ur[4 + k] << 4) | ur[k]);
-                        }
+            if (bits == 0) encode_group_m12(Wg, cols, n_8, signs, grp, tmp, u);
+            else encode_group_asym(Wg, cols, n_8, signs, bits, w_pow, grp, tmp, u);
         }
         size_t body_len = (size_t)n_8g * grp_bytes;
         uint32_t crc = crc32_update(0, body, body_len);
         memcpy(tile, &crc, 4);
         uint16_t nr16 = (uint16_t)n_r;
         memcpy(tile + 4, &nr16, 2);
-        free(tmp); free(u4); free(sc);
+        free(tmp); free(u);
     }
     free(signs);
 
@@ -326,6 +455,17 @@ DPUF_EXPORT uint8_t* dpuf_tools_pack_mode12(const float* W, int32_t rows, int32_
     free(t_off); free(e_off);
     *len = total;
     return blob;
+}
+
+DPUF_EXPORT uint8_t* dpuf_tools_pack_mode12(const float* W, int32_t rows, int32_t cols,
+                                            const uint8_t* sign_bits, int32_t ecc_group, size_t* len) {
+    return pack_qr(W, rows, cols, sign_bits, ecc_group, 0, 0.0f, len);
+}
+
+DPUF_EXPORT uint8_t* dpuf_tools_pack_asym(const float* W, int32_t rows, int32_t cols, const uint8_t* sign_bits,
+                                          int32_t ecc_group, int32_t bits, float w_pow, size_t* len) {
+    if (bits != 4 && bits != 6) return NULL;
+    return pack_qr(W, rows, cols, sign_bits, ecc_group, bits, w_pow, len);
 }
 
 DPUF_EXPORT int32_t dpuf_tools_bind_blob(const uint8_t* blob, size_t len, DpufWeightDesc* out) {
@@ -419,16 +559,33 @@ static const NamedBlob* find_blob(const DpufToolsModel* m, const char* name) {
     return NULL;
 }
 
-/* Tensor names of pack_dpuf.py:122-151; sign sharing of pack_dpuf.py:206-216. */
+/* Mode of a matrix under the had4p-hybrid plan (pack_dpuf.py:249-266): 6 bits
+ * for ffn_down, attn_v, attn_k, the even layers' attn_output and
+ * output.weight, 4 bits for the rest, token_embd included. */
+static int hybrid_bits(const char* name) {
+    const size_t n = strlen(name);
+#define ENDS(sfx) (n >= strlen(sfx) && strcmp(name + n - strlen(sfx), sfx) == 0)
+    if (ENDS(".ffn_down.weight") || ENDS(".attn_v.weight") || ENDS(".attn_k.weight") ||
+        strcmp(name, "output.weight") == 0)
+        return 6;
+    if (ENDS(".attn_output.weight") && strncmp(name, "blk.", 4) == 0 && atoi(name + 4) % 2 == 0) return 6;
+#undef ENDS
+    return 4;
+}
+
+/* Tensor names of pack_dpuf.py:122-151.  Plan 0: mode 12 with the sign
+ * sharing of pack_dpuf.py:206-216 (sign_name).  Plan 1: the had4p-hybrid
+ * plan, each matrix with signs of its own name (pack_dpuf.py:262-264). */
 static void build_matrix(DpufToolsModel* m, const DpufToolsSpec* s, const char* name, const char* sign_name,
                          int32_t rows, int32_t cols) {
     float* W = (float*)malloc((size_t)rows * (size_t)cols * sizeof(float));
     dpuf_tools_random_normal(W, (size_t)rows * (size_t)cols, s->weight_std, s->seed, name);
     dpuf_tools_round_bf16(W, (size_t)rows * (size_t)cols);
     uint8_t* sb = (uint8_t*)malloc((size_t)cols / 8u);
-    dpuf_tools_sign_bits(sb, cols, s->seed, sign_name);
+    dpuf_tools_sign_bits(sb, cols, s->seed, s->weight_plan == 1 ? name : sign_name);
     size_t len = 0;
-    uint8_t* blob = dpuf_tools_pack_mode12(W, rows, cols, sb, 64, &len);
+    uint8_t* blob = s->weight_plan == 1 ? dpuf_tools_pack_asym(W, rows, cols, sb, 64, hybrid_bits(name), 0.0f, &len)
+                                        : dpuf_tools_pack_mode12(W, rows, cols, sb, 64, &len);
     free(W);
     free(sb);
     add_blob(m, name, blob, len, 1);

@@ -1,7 +1,7 @@
 /*
  * dpuf_tools.h -- host tooling around the DPUF container for the MI355X build:
  * deterministic random-init weights, the mode 12 (Hadamard-4bit packed)
- * packer, the .dpuf container writer, and the mmap reader that binds tensors
+ * and mode 13 / 14 (asymmetric blk64 4 / 6-bit) packers, the .dpuf container writer, and the mmap reader that binds tensors
  * into DpufWeightDesc the way dpuf-cli.c does.  Plain C, no GPU code.
  */
 #ifndef DPUF_TOOLS_H
@@ -29,6 +29,8 @@ typedef struct {
     float   rms_eps;
     float   rope_theta;
     uint64_t seed;
+    int32_t weight_plan;     /* 0: mode 12, shared Q/K/V and gate/up signs;
+                                1: had4p-hybrid modes 13 / 14, signs per tensor */
 } DpufToolsSpec;
 
 typedef struct DpufToolsModel DpufToolsModel;
@@ -52,6 +54,12 @@ DPUF_EXPORT void dpuf_tools_sign_bits(uint8_t* out, int32_t cols, uint64_t seed,
 DPUF_EXPORT uint8_t* dpuf_tools_pack_mode12(const float* W, int32_t rows, int32_t cols,
                                             const uint8_t* sign_bits, int32_t ecc_group,
                                             size_t* len);
+
+/* Packs W into a mode 13 (bits 4) or mode 14 (bits 6) asymmetric blk64 QR
+ * blob, weighted least-squares codes with weights (|w| + 1e-6)^w_pow (w_pow
+ * <= 0: unweighted).  cols % 64 == 0.  Returns a malloc'd blob or NULL. */
+DPUF_EXPORT uint8_t* dpuf_tools_pack_asym(const float* W, int32_t rows, int32_t cols, const uint8_t* sign_bits,
+                                          int32_t ecc_group, int32_t bits, float w_pow, size_t* len);
 
 /* Fills a DpufWeightDesc that points into a QR blob (no verification). */
 DPUF_EXPORT int32_t dpuf_tools_bind_blob(const uint8_t* blob, size_t len, DpufWeightDesc* out);

@@ -154,14 +154,19 @@ static void tm_collect(Engine* e) {
     e->n_ev = 0;
 }
 
-/* Checks that every tile of a mode 12 descriptor lies inside its payload and
- * that row counts are consistent, so that no kernel can read out of bounds. */
+static int mode_ok(int32_t mode) {
+    return mode == DPUF_MODE_QR_HAD4_PACKED || mode == DPUF_MODE_QR_HAD4_ASYM || mode == DPUF_MODE_QR_HAD6;
+}
+
+/* Checks that every tile of a mode 12, 13 or 14 descriptor lies inside its
+ * payload and that row counts are consistent, so that no kernel can read out
+ * of bounds. */
 static int validate_desc(const DpufWeightDesc* d) {
-    if (!d || d->mode != DPUF_MODE_QR_HAD4_PACKED) return 0;
+    if (!d || !mode_ok(d->mode)) return 0;
     if (d->rows <= 0 || d->cols <= 0 || (d->cols % 64) != 0 || d->n_tiles != (d->rows + 15) / 16) return 0;
     if (!d->tensor_base || !d->tile_offsets) return 0;
     const uint64_t total = d->tile_offsets[d->n_tiles];
-    const uint64_t grp = (uint64_t)(d->cols / 32) * 144u;
+    const uint64_t grp = (uint64_t)(d->cols / 32) * (uint64_t)dpuf_grp_unit(d->mode);
     for (int32_t t = 0; t < d->n_tiles; t++) {
         uint64_t o = d->tile_offsets[t];
         if (o % 16 != 0 || o + 16 > total) return 0;
@@ -184,6 +189,7 @@ static void set_devw(DpufDevW* out, const Upload* u, const DpufWeightDesc* d) {
     out->rows = d->rows;
     out->cols = d->cols;
     out->n_groups = (d->rows + 7) / 8;
+    out->mode = d->mode;
 }
 
 /* Weight upload at create: the .dpuf tile bytes go through two pinned host
@@ -220,7 +226,7 @@ static void stager_free(Stager* st) {
 
 static int stager_init(Stager* st) {
     memset(st, 0, sizeof *st);
-    /* a chunk holds at least one tile: 16 + 2 * (16384 / 32) * 144 bytes at the
+    /* a chunk holds at least one tile: 16 + 2 * (16384 / 32) * 208 bytes at the
      * widest matrix create accepts, far below UP_CHUNK */
     st->max_tiles = (int32_t)(UP_CHUNK / 16) + 1;
     for (int b = 0; b < 2; b++) {
@@ -240,7 +246,7 @@ static int stager_init(Stager* st) {
 /* Uploads tiles of d chunk by chunk into the row-block layout at dst. */
 static void stage_tiles(Engine* e, Stager* st, const DpufWeightDesc* d, uint8_t* dst) {
     const int32_t n_blk = d->cols / 32;
-    const uint64_t gbytes = (uint64_t)n_blk * 144u;
+    const uint64_t gbytes = (uint64_t)n_blk * (uint64_t)dpuf_grp_unit(d->mode);
     int32_t t0 = 0;
     while (t0 < d->n_tiles) {
         const uint64_t lo = d->tile_offsets[t0];
@@ -256,7 +262,7 @@ static void stage_tiles(Engine* e, Stager* st, const DpufWeightDesc* d, uint8_t*
         const int32_t n_groups = (r1 - 16 * t0 + 7) / 8;
         dpuf_hip_h2d(st->dev[b], st->pin[b], (size_t)(hi - lo), e->stream);
         dpuf_hip_h2d(st->dev_offs[b], st->pin_offs[b], (size_t)(t1 - t0 + 1) * 8u, e->stream);
-        dpuf_hip_relayout(e->stream, (const uint8_t*)st->dev[b], st->dev_offs[b], n_groups, n_blk,
+        dpuf_hip_relayout(e->stream, (const uint8_t*)st->dev[b], st->dev_offs[b], n_groups, n_blk, d->mode,
                           dst + (size_t)(2 * t0) * gbytes);
         dpuf_hip_event_record(st->ev[b], e->stream);
         st->used[b] = 1;
@@ -264,7 +270,7 @@ static void stage_tiles(Engine* e, Stager* st, const DpufWeightDesc* d, uint8_t*
     }
 }
 
-/* Uploads one validated mode 12 matrix (tied tensors once). */
+/* Uploads one validated mode 12 / 13 / 14 matrix (tied tensors once). */
 static int upload_desc(Engine* e, Stager* st, const DpufWeightDesc* d, DpufDevW* out) {
     if (!validate_desc(d)) return 0;
     for (int32_t i = 0; i < e->n_ups; i++) {
@@ -277,7 +283,7 @@ static int upload_desc(Engine* e, Stager* st, const DpufWeightDesc* d, DpufDevW*
     memset(&u, 0, sizeof u);
     u.host_base = d->tensor_base;
     const int32_t n_groups = (d->rows + 7) / 8, n_blk = d->cols / 32;
-    u.bytes = (uint64_t)n_groups * (uint64_t)n_blk * 144u;
+    u.bytes = (uint64_t)n_groups * (uint64_t)n_blk * (uint64_t)dpuf_grp_unit(d->mode);
     u.d_groups = dpuf_hip_malloc((size_t)u.bytes);
     if (d->sign_bits) u.d_sign = dpuf_hip_malloc((size_t)d->cols / 8u);
     if (!u.d_groups || (d->sign_bits && !u.d_sign)) {
@@ -676,13 +682,15 @@ DPUF_EXPORT int32_t dpuf_engine_get_prefix_len(void* handle, int32_t pfx_id) {
 /* ------------------------------------------------------------------------- */
 
 /* Algorithmic bytes of one GEMV launch over tiles [t0, t1): the weight
- * groups (8 rows x 32 columns = 144 bytes each) plus, per token row, the
- * prepped activations (K int8 + 8 bytes per 32-block) and the fp32 outputs. */
+ * groups (8 rows x 32 columns = 144 bytes each, 208 for mode 14) plus, per
+ * token row, the prepped activations (K int8 + 8 bytes per 32-block) and the
+ * fp32 outputs. */
 static double gemv_bytes(const DpufDevW* w, int32_t t0, int32_t t1, int32_t M) {
     const int32_t g0 = 2 * t0, g1 = 2 * t1 < w->n_groups ? 2 * t1 : w->n_groups;
     const int32_t r1 = 16 * t1 < w->rows ? 16 * t1 : w->rows;
     const double n_blk = (double)(w->cols / 32);
-    return (double)(g1 - g0) * n_blk * 144.0 + (double)M * (w->cols + n_blk * 8.0 + (r1 - 16 * t0) * 4.0);
+    return (double)(g1 - g0) * n_blk * dpuf_grp_unit(w->mode) +
+           (double)M * (w->cols + n_blk * 8.0 + (r1 - 16 * t0) * 4.0);
 }
 
 /* Tiles [t0, t1) of w (16 rows each) as a GEMV job over 8-row groups. */

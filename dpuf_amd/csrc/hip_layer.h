@@ -13,16 +13,24 @@
 extern "C" {
 #endif
 
-/* One mode 12 matrix resident in HBM in the row-block layout written by
- * dpuf_hip_relayout: group g (rows 8g .. 8g+7) at g + g * (cols/32) * 144,
- * holding [cols/32][8] fp16 scales, then per 32-column block 8 rows x 16
- * bytes of nibbles (row ri's four .dpuf chunk words of the block, in chunk
- * order). */
+/* One mode 12, 13 or 14 matrix resident in HBM in the row-block layout
+ * written by dpuf_hip_relayout: group g (rows 8g .. 8g+7) at
+ * g + g * (cols/32) * U (U = 144, or 208 for mode 14), holding [cols/32][8]
+ * fp16 scales (mode 12: the 32-block scales; modes 13 / 14: d of 64-block j
+ * as "block" 2j, m as 2j+1), then per 32-column block 8 rows x 16 bytes of
+ * nibbles (row ri's four .dpuf chunk words of the block, in chunk order),
+ * and for mode 14 per block 8 rows x 8 bytes of bits 4..5: word w, byte k
+ * holds chunk 2w's columns +k and +4+k in bits 0-1 and 2-3, chunk 2w+1's in
+ * bits 4-5 and 6-7. */
 typedef struct {
     const uint8_t*  g;
     const uint8_t*  sign;
     int32_t rows, cols, n_groups;
+    int32_t mode;   /* 12, 13 or 14 */
 } DpufDevW;
+
+/* Bytes of one 8-row group per 32 columns in .dpuf tiles and on the device. */
+static inline int32_t dpuf_grp_unit(int32_t mode) { return mode == 14 ? 208 : 144; }
 
 /* Prepped activations of M rows: q int8 [M][K], s f32 [M][K/32], m i32 [M][K/32],
  * and h, the same q as fp16 [M][K] (the M > 1 GEMM's input; the prep
@@ -93,9 +101,10 @@ void dpuf_hip_resnorm_prep(void* s, int32_t M, int32_t H, float* h, const float*
 void dpuf_hip_prep(void* s, int32_t M, int32_t K, const float* x, const uint8_t* sign, DpufPrep p);
 void dpuf_hip_swiglu_prep(void* s, int32_t M, int32_t I, const float* gate, const float* up,
                           float dz, const uint8_t* sign, DpufPrep p);
-/* .dpuf tile region (tile t at src + offs[t]) -> row-block layout. */
+/* .dpuf tile region of a mode 12 / 13 / 14 matrix (tile t at src + offs[t])
+ * -> row-block layout. */
 void dpuf_hip_relayout(void* s, const uint8_t* src, const uint64_t* offs, int32_t n_groups, int32_t n_blk,
-                       uint8_t* dst);
+                       int32_t mode, uint8_t* dst);
 /* M == 1: GEMV of up to three matrices sharing K, with the activations of
  * each job in jobs[i].p; a non-NULL skip_flag that reads non-zero makes the
  * launch write `fill` to every row instead.  M > 1: the slab GEMM. */

@@ -145,7 +145,8 @@ DEV int dpp_xor1(int v) { return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0x
 DEV int dpp_xor2(int v) { return __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false); }
 
 // ---------------------------------------------------------------------------
-// Embedding (reference dpuf_embed_qr_hadamard4_packed_f32, dpuf_avx2.c:2738-2783)
+// Embedding (reference dpuf_embed_qr_hadamard4_packed_f32, dpuf_avx2.c:2738-2783,
+// and embed_qr_had_asym_impl, dpuf_avx2.c:3154-3207, for modes 13 / 14)
 // grid: M rows; thread per 64-column block.
 // ---------------------------------------------------------------------------
 __global__ void k_embed(DpufDevW w, const int32_t* __restrict__ ids, const float* __restrict__ embeds,
@@ -170,24 +171,39 @@ __global__ void k_embed(DpufDevW w, const int32_t* __restrict__ ids, const float
         return;
     }
     const int g = id >> 3, ri = id & 7;
-    const uint8_t* grp = w.g + (size_t)g * n_blk * 144;
+    const bool asym = w.mode != 12, hi6 = w.mode == 14;
+    const uint8_t* grp = w.g + (size_t)g * n_blk * (hi6 ? 208 : 144);
     const uint16_t* sc = (const uint16_t*)grp;
     const uint8_t* qg = grp + (size_t)n_blk * 16;
     for (int blk = threadIdx.x; blk < (H >> 6); blk += blockDim.x) {
         float v[64];
+        // modes 13 / 14: (float)u * d + m, a rounded product then a rounded
+        // sum (dpuf_avx2.c:3194-3195); mode 12: (u - 8) * ws
+        const float wd = h2f(sc[2 * blk * 8 + ri]), wm = h2f(sc[(2 * blk + 1) * 8 + ri]);
 #pragma unroll
         for (int hb = 0; hb < 2; hb++) {
             const int b = 2 * blk + hb;
             const float ws = h2f(sc[b * 8 + ri]);
             const uint4 rw = *(const uint4*)(qg + (size_t)b * 128 + ri * 16);
             const uint32_t words[4] = {rw.x, rw.y, rw.z, rw.w};
+            uint2 hw = make_uint2(0u, 0u);
+            if (hi6) hw = *(const uint2*)(grp + (size_t)n_blk * 144 + ((size_t)b * 8 + ri) * 8);
+            const uint32_t hws[2] = {hw.x, hw.y};
 #pragma unroll
             for (int c = 0; c < 4; c++) {
 #pragma unroll
                 for (int k = 0; k < 4; k++) {
                     const uint32_t by = (words[c] >> (8 * k)) & 0xFFu;
-                    v[32 * hb + 8 * c + k] = (float)((int)(by & 15u) - 8) * ws;
-                    v[32 * hb + 8 * c + 4 + k] = (float)((int)(by >> 4) - 8) * ws;
+                    if (asym) {
+                        const uint32_t hb2 = (hws[c >> 1] >> (8 * k + (c & 1) * 4)) & 0xFu;
+                        const int u0 = (int)((by & 15u) | ((hb2 & 3u) << 4));
+                        const int u1 = (int)((by >> 4) | ((hb2 >> 2) << 4));
+                        v[32 * hb + 8 * c + k] = (float)u0 * wd + wm;
+                        v[32 * hb + 8 * c + 4 + k] = (float)u1 * wd + wm;
+                    } else {
+                        v[32 * hb + 8 * c + k] = (float)((int)(by & 15u) - 8) * ws;
+                        v[32 * hb + 8 * c + 4 + k] = (float)((int)(by >> 4) - 8) * ws;
+                    }
                 }
             }
         }
@@ -468,10 +484,21 @@ __global__ __launch_bounds__(256) void k_swiglu_prep(int I, const float* __restr
 // consecutive addresses.  Scales stay [n_blk][8]: lane (bi, ri) of step s
 // reads scale s*64 + lane.
 // ---------------------------------------------------------------------------
+//
+// Modes 13 / 14 (asymmetric blk64, dpuf_avx2.c:2786-2791) have the same group
+// prefix: their [n_64][16] fp16 (d of rows 0..7, then m) is, viewed as
+// [n_blk][8], "block" 2j = d and 2j+1 = m of 64-block j, and their nibbles
+// use the mode 12 interleave, so the same gather applies (144 bytes per 32
+// columns).  Mode 14 then holds per block 64 bytes of bits 4..5: bits
+// 2(ri>>1) of byte c*16 + h*8 + (ri&1)*4 + k belong to row ri, column
+// 32b+8c+4h+k.  Those are regathered per row into two words, word w byte k =
+// chunk 2w's columns +k, +4+k in bits 0-1, 2-3 and chunk 2w+1's in bits 4-5,
+// 6-7, stored after the nibbles: row ri, block b at n_blk*144 + (b*8+ri)*8.
+// ---------------------------------------------------------------------------
 __global__ void k_relayout(const uint8_t* __restrict__ src, const uint64_t* __restrict__ offs, int n_groups,
-                           int n_blk, uint8_t* __restrict__ dst) {
+                           int n_blk, int hi6, uint8_t* __restrict__ dst) {
     const size_t total = (size_t)n_groups * n_blk * 8;
-    const size_t gbytes = (size_t)n_blk * 144;
+    const size_t gbytes = (size_t)n_blk * (hi6 ? 208 : 144);
     for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
          idx += (size_t)gridDim.x * blockDim.x) {
         const int g = (int)(idx / ((size_t)n_blk * 8));
@@ -483,6 +510,21 @@ __global__ void k_relayout(const uint8_t* __restrict__ src, const uint64_t* __re
         const uint32_t* sq = (const uint32_t*)(sg + (size_t)n_blk * 16 + (size_t)b * 128);
         *(uint4*)(dg + (size_t)n_blk * 16 + (size_t)b * 128 + ri * 16) =
             make_uint4(sq[ri], sq[8 + ri], sq[16 + ri], sq[24 + ri]);
+        if (hi6) {
+            const uint8_t* sh = sg + (size_t)n_blk * 144 + (size_t)b * 64 + (ri & 1) * 4;
+            const int sft = (ri >> 1) * 2;
+            uint32_t w[2] = {0u, 0u};
+#pragma unroll
+            for (int c = 0; c < 4; c++)
+#pragma unroll
+                for (int h = 0; h < 2; h++)
+#pragma unroll
+                    for (int k = 0; k < 4; k++) {
+                        const uint32_t hv = (sh[c * 16 + h * 8 + k] >> sft) & 3u;
+                        w[c >> 1] |= hv << (8 * k + (c & 1) * 4 + h * 2);
+                    }
+            *(uint2*)(dg + (size_t)n_blk * 144 + ((size_t)b * 8 + ri) * 8) = make_uint2(w[0], w[1]);
+        }
     }
 }
 
@@ -502,6 +544,29 @@ DEV int row_block_dot(uint4 w, int4 xa, int4 xb) {
     d = __builtin_amdgcn_sdot4((int)((w.w >> 4) & m), xb.w, d, false);
     return d;
 }
+
+// The same for a mode 14 row block: bits 4..5 of each value come from the
+// row's two words of high bits (word c >> 1, bits (c & 1) * 4 + {0,1} of byte
+// k for column 8c+k, + {2,3} for 8c+4+k).  u <= 63, so the sdot4 products are
+// exact, as the reference's maddubs sums (dpuf_avx2.c:2824-2846).
+DEV int row_block_dot6(uint4 w, uint2 hw, int4 xa, int4 xb) {
+    const uint32_t m = 0x0F0F0F0Fu, m2 = 0x03030303u;
+    const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+    const int xw[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+    int d = 0;
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const uint32_t h = ((c >> 1) ? hw.y : hw.x) >> ((c & 1) * 4);
+        const uint32_t lo = (wd[c] & m) | ((h & m2) << 4);
+        const uint32_t hi = ((wd[c] >> 4) & m) | (((h >> 2) & m2) << 4);
+        d = __builtin_amdgcn_sdot4((int)lo, xw[2 * c], d, false);
+        d = __builtin_amdgcn_sdot4((int)hi, xw[2 * c + 1], d, false);
+    }
+    return d;
+}
+
+// Lane i + 8 of a 16-lane row for lane i and the reverse (DPP row_ror:8).
+DEV int dpp_ror8(int v) { return __builtin_amdgcn_update_dpp(0, v, 0x128, 0xF, 0xF, false); }
 
 DEV uint4 nt_load16(const uint8_t* p) {
     const u32x4 v = __builtin_nontemporal_load((const u32x4*)p);
@@ -623,6 +688,7 @@ struct MvX {
 template <int NL>
 struct MvU {
     uint4 wq[NL];
+    uint2 wh[NL];  // mode 14: the row block's bits 4..5
     uint32_t ws[NL];
     MvX<NL> x;
 };
@@ -661,13 +727,14 @@ DEV void mv_load_x(const MvGeo& G, int r, int w, int lane, MvX<NL>& X) {
     }
 }
 
-template <int NL, bool HOIST>
+template <int NL, bool HOIST, int MODE>
 DEV void mv_issue(const MvGeo& G, int u, int w, int lane, MvU<NL>& L) {
     const int lg = u / G.R, r = u - lg * G.R;
     const int g = G.g0 + G.lb + lg * G.nwg;
-    const uint8_t* grp = G.g + (size_t)g * G.n_blk * 144;
+    const uint8_t* grp = G.g + (size_t)g * G.n_blk * (MODE == 14 ? 208 : 144);
     const uint16_t* sc = (const uint16_t*)grp;
     const uint8_t* qg = grp + (size_t)G.n_blk * 16;
+    const uint8_t* hg = grp + (size_t)G.n_blk * 144;
     const int s0 = (r * G.NW + w) * NL;
 #pragma unroll
     for (int i = 0; i < NL; i++) {
@@ -675,13 +742,21 @@ DEV void mv_issue(const MvGeo& G, int u, int w, int lane, MvU<NL>& L) {
         const uint32_t b = (uint32_t)min(s * 8 + (lane >> 3), G.n_blk - 1);
         const uint32_t e = b * 8u + (uint32_t)(lane & 7);  // == 64 s + lane unless clamped
         L.wq[i] = nt_load16(qg + e * 16u);
+        if (MODE == 14) L.wh[i] = *(const uint2*)(hg + e * 8u);
         L.ws[i] = sc[e];
     }
     if (!HOIST) mv_load_x<NL>(G, r, w, lane, L.x);
 }
 
-// (float(D - sum8), ws * xs) pairs of one round of one wave into pairs[row][block].
-template <int NL, bool HOIST>
+// Mode 12: (float(D - sum8), ws * xs) pairs of one round of one wave into
+// pairs[row][block].  Modes 13 / 14: the two 32-blocks 2j, 2j+1 of 64-block
+// j sit on lanes (bi, ri) and (bi + 1, ri), 8 lanes apart, and swap their dot,
+// activation scale and sum over DPP; the even lane writes (fdot, d) with
+// fdot = fma(float(D0), xs0, float(D1) * xs1), the odd lane (m, xm_s) with
+// xm_s = ((float)sum8_0 * xs0 + (float)sum8_1 * xs1) * 0.125f, so the chain
+// fma(a, b, acc) over the pairs in order is the reference's
+// acc = fma(fdot, d, acc); acc = fma(m, xm_s, acc) (dpuf_avx2.c:3029-3037).
+template <int NL, bool HOIST, int MODE>
 DEV void mv_dots(const MvGeo& G, int r, int w, int lane, const MvU<NL>& L, const MvX<NL>& X0, float2* pairs) {
     const MvX<NL>& X = HOIST ? X0 : L.x;
     const int bi = lane >> 3, ri = lane & 7;
@@ -691,6 +766,24 @@ DEV void mv_dots(const MvGeo& G, int r, int w, int lane, const MvU<NL>& L, const
         const int s = s0 + i;
         if (s >= G.S) break;  // wave-uniform
         const int b = s * 8 + bi;
+        if (MODE != 12) {
+            const int dot = MODE == 14 ? row_block_dot6(L.wq[i], L.wh[i], X.xa[i], X.xb[i])
+                                       : row_block_dot(L.wq[i], X.xa[i], X.xb[i]);
+            const int dp = dpp_ror8(dot), xmp = dpp_ror8(X.xm[i]);
+            const float xsp = __int_as_float(dpp_ror8(__float_as_int(X.xs[i])));
+            const float sc = h2f((uint16_t)L.ws[i]);
+            float2 pr;
+            if ((bi & 1) == 0) {
+                pr.x = fmaf((float)dot, X.xs[i], (float)dp * xsp);
+                pr.y = sc;
+            } else {
+                const float a = (float)xmp * xsp, c = (float)X.xm[i] * X.xs[i];
+                pr.x = sc;
+                pr.y = (a + c) * 0.125f;
+            }
+            if (b < G.n_blk) pairs[ri * G.ld + b] = pr;
+            continue;
+        }
         if (b < G.n_blk) {
             const int dot = row_block_dot(L.wq[i], X.xa[i], X.xb[i]);
             float dcf = 0.0f, sp = 0.0f;
@@ -710,7 +803,7 @@ struct MvSync {
     int32_t done[MV_NBUF];
 };
 
-template <int NL, bool HOIST>
+template <int NL, bool HOIST, int MODE>
 DEV void mv_consume(const MvGeo& G, int u, int w, int lane, const MvU<NL>& L, const MvX<NL>& X0, uint8_t* smem,
                     MvSync* sy) {
     const int lg = u / G.R, r = u - lg * G.R;
@@ -725,7 +818,7 @@ DEV void mv_consume(const MvGeo& G, int u, int w, int lane, const MvU<NL>& L, co
         if (spins >= (1 << 22) && lane == 0) mv_wait_failed(G.err);
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
     }
-    mv_dots<NL, HOIST>(G, r, w, lane, L, X0, pairs);
+    mv_dots<NL, HOIST, MODE>(G, r, w, lane, L, X0, pairs);
     if (r == G.R - 1) {
         // publish this wave's pairs of the group to the chain wave
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
@@ -763,7 +856,7 @@ DEV void mv_chains(const MvGeo& G, int c, int n_my, int lane, uint8_t* smem, MvS
     }
 }
 
-template <int NL, bool HOIST, bool SINGLE>
+template <int NL, bool HOIST, bool SINGLE, int MODE>
 __global__ __launch_bounds__(1024) void k_mv(MvArgs A) {
     extern __shared__ __align__(16) uint8_t smem[];
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
@@ -811,8 +904,8 @@ __global__ __launch_bounds__(1024) void k_mv(MvArgs A) {
         MvU<NL> L1;
         if (HOIST) mv_load_x<NL>(G, 0, w, lane, X1);
         for (int r = 0; r < G.R; r++) {
-            mv_issue<NL, HOIST>(G, r, w, lane, L1);
-            mv_dots<NL, HOIST>(G, r, w, lane, L1, X1, (float2*)smem);
+            mv_issue<NL, HOIST, MODE>(G, r, w, lane, L1);
+            mv_dots<NL, HOIST, MODE>(G, r, w, lane, L1, X1, (float2*)smem);
         }
         __syncthreads();
         if (w == 0 && lane < 8) {
@@ -827,20 +920,20 @@ __global__ __launch_bounds__(1024) void k_mv(MvArgs A) {
     // Steady state: both issues unconditional, so each consume waits only for
     // its own loads; the last one or two units drain after the loop.
     MvU<NL> La, Lb;
-    mv_issue<NL, HOIST>(G, 0, w, lane, La);
+    mv_issue<NL, HOIST, MODE>(G, 0, w, lane, La);
     int u = 0;
     for (; u + 2 < n_units; u += 2) {
-        mv_issue<NL, HOIST>(G, u + 1, w, lane, Lb);
-        mv_consume<NL, HOIST>(G, u, w, lane, La, X, smem, &sy);
-        mv_issue<NL, HOIST>(G, u + 2, w, lane, La);
-        mv_consume<NL, HOIST>(G, u + 1, w, lane, Lb, X, smem, &sy);
+        mv_issue<NL, HOIST, MODE>(G, u + 1, w, lane, Lb);
+        mv_consume<NL, HOIST, MODE>(G, u, w, lane, La, X, smem, &sy);
+        mv_issue<NL, HOIST, MODE>(G, u + 2, w, lane, La);
+        mv_consume<NL, HOIST, MODE>(G, u + 1, w, lane, Lb, X, smem, &sy);
     }
     if (u + 1 < n_units) {
-        mv_issue<NL, HOIST>(G, u + 1, w, lane, Lb);
-        mv_consume<NL, HOIST>(G, u, w, lane, La, X, smem, &sy);
-        mv_consume<NL, HOIST>(G, u + 1, w, lane, Lb, X, smem, &sy);
+        mv_issue<NL, HOIST, MODE>(G, u + 1, w, lane, Lb);
+        mv_consume<NL, HOIST, MODE>(G, u, w, lane, La, X, smem, &sy);
+        mv_consume<NL, HOIST, MODE>(G, u + 1, w, lane, Lb, X, smem, &sy);
     } else {
-        mv_consume<NL, HOIST>(G, u, w, lane, La, X, smem, &sy);
+        mv_consume<NL, HOIST, MODE>(G, u, w, lane, La, X, smem, &sy);
     }
 }
 
@@ -885,6 +978,7 @@ struct GmJob {
     int rows;
     const uint16_t* h;  // activations as fp16 [M][K]
     const float* s;     // block scales [M][K/32]
+    const int32_t* m;   // 8 * block sums of q [M][K/32] (modes 13 / 14)
     float* out;        // out[m * ldo + row]
     int ldo;
 };
@@ -913,12 +1007,32 @@ DEV gm_h8 gm_unpack_a(uint32_t w) {
     return __builtin_bit_cast(gm_h8, make_uint4(r0, r1, r2, r3));
 }
 
+// The same for modes 13 / 14: u itself (no offset) as f16, with bits 4..5
+// from h (bits 0-1 of byte k for the low half, 2-3 for the high half; 0 for
+// mode 13).
+DEV gm_h8 gm_unpack_a_asym(uint32_t w, uint32_t h) {
+    const uint32_t lo = (w & 0x0F0F0F0Fu) | ((h & 0x03030303u) << 4);
+    const uint32_t hi = ((w >> 4) & 0x0F0F0F0Fu) | (((h >> 2) & 0x03030303u) << 4);
+    const uint32_t r0 = gm_sub(gm_pair(lo, 0x04010400u), (_Float16)1024.0f);
+    const uint32_t r1 = gm_sub(gm_pair(lo, 0x04030402u), (_Float16)1024.0f);
+    const uint32_t r2 = gm_sub(gm_pair(hi, 0x04010400u), (_Float16)1024.0f);
+    const uint32_t r3 = gm_sub(gm_pair(hi, 0x04030402u), (_Float16)1024.0f);
+    return __builtin_bit_cast(gm_h8, make_uint4(r0, r1, r2, r3));
+}
 
-template <int TT, int RF>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k_gemm_mfma(GmArgs A) {
+
+// Modes 13 / 14 hold a 64-block's even half (its D tiles, token scales and
+// sums, row scales) across the odd one: 2 waves per SIMD keep that in
+// registers instead of spilling at the 128 VGPRs of 4.
+template <int TT, int RF, int MODE>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MODE == 12 ? 4 : 2))) void k_gemm_mfma(
+    GmArgs A) {
     constexpr int NT = 16 * TT;  // tokens per workgroup
+    constexpr bool ASYM = MODE != 12;
+    static_assert(GM_SB % 2 == 0, "a stage holds whole 64-blocks");
     __shared__ __align__(16) uint8_t bq[2][GM_SB][NT][64];  // f16 activations [stage][block][token][k]
     __shared__ __align__(16) float bs[2][GM_SB][16][TT];    // block scales [stage][block][token % 16][token / 16]
+    __shared__ __align__(16) int32_t bm[ASYM ? 2 : 1][GM_SB][16][TT];  // 8 * block sums (modes 13 / 14)
     __shared__ __align__(16) uint32_t bw[2][GM_SB][32 * RF];  // weight scales [stage][block][group * 4 + word]
     // Workgroups go to the 8 XCDs round-robin by linear id L.  L = xcd +
     // 8 j with j = gy r + ty puts row tile 8 r + xcd of every token tile ty on
@@ -950,11 +1064,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
     const GmJob& J = ji == 0 ? A.j[0] : ji == 1 ? A.j[1] : A.j[2];
     const uint16_t* const Jh = ji == 0 ? A.j[0].h : ji == 1 ? A.j[1].h : A.j[2].h;
     const float* const Js = ji == 0 ? A.j[0].s : ji == 1 ? A.j[1].s : A.j[2].s;
+    const int32_t* const Jm = ji == 0 ? A.j[0].m : ji == 1 ? A.j[1].m : A.j[2].m;
     const int gb = J.g0 + (rt - A.tb[ji]) * 8 * RF;  // first group of the workgroup
     const int m0 = ty * NT;
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, i16 = l & 15, kc = l >> 4;
     const int K = A.K, M = A.M, n_blk = K >> 5;
-    const size_t gstride = (size_t)n_blk * 144;
+    const size_t gstride = (size_t)n_blk * (MODE == 14 ? 208 : 144);
 
     // Every load is a buffer load: a wave-uniform descriptor, a 32-bit lane
     // offset fixed for the launch and a scalar block offset, so addressing
@@ -967,11 +1082,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
     const size_t wbytes = (size_t)(J.g1 - gw0) * gstride;
     const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(J.g + (size_t)gw0 * gstride), 0, (int)(wbytes < 0xFFFFFFFFu ? wbytes : 0xFFFFFFFFu), GM_RSRC3);
-    uint32_t on[RF];
+    uint32_t on[RF], oh[RF];
 #pragma unroll
     for (int f = 0; f < RF; f++) {
         const int ga = min(gb + 2 * RF * wu + 2 * f + (i16 >> 3), J.g1 - 1);
         on[f] = (uint32_t)((size_t)(ga - gw0) * gstride + (size_t)n_blk * 16 + (i16 & 7) * 16 + kc * 4);
+        // mode 14: the lane's high-bit word (chunk kc's bits are in word kc / 2)
+        oh[f] = (uint32_t)((size_t)(ga - gw0) * gstride + (size_t)n_blk * 144 + (i16 & 7) * 8 + (kc >> 1) * 4);
     }
     // Weight scales go through LDS with the activations: a stage's 8 RF
     // groups x GM_SB blocks x 8 fp16 scales are WD dwords, dword d = (tid +
@@ -1003,11 +1120,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
     const int n_st = (n_blk + GM_SB - 1) / GM_SB;
     gm_u4 sq[CPT];  // a native vector: a struct copy would keep the array in scratch
     float ss[SPT];
+    int32_t sm[SPT];
     // byte offsets of the token rows (M K < 2^30 is checked at launch); with
     // NT = 64 a chunk's block (k) and a scale's block (the wave, + 4 k) are
     // uniform and go into the scalar offset
     const __amdgpu_buffer_rsrc_t rh = __builtin_amdgcn_make_buffer_rsrc((void*)Jh, 0, M * K * 2, GM_RSRC3);
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)Js, 0, M * n_blk * 4, GM_RSRC3);
+    const __amdgpu_buffer_rsrc_t rm =
+        __builtin_amdgcn_make_buffer_rsrc(ASYM ? (void*)Jm : (void*)Js, 0, M * n_blk * 4, GM_RSRC3);
     uint32_t ho[CPT], so[SPT];
 #pragma unroll
     for (int k = 0; k < CPT; k++) {
@@ -1034,6 +1154,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
         for (int k = 0; k < SPT; k++) {
             const int b = NT == 64 ? min(st * GM_SB + wu + 4 * k, n_blk - 1) : st * GM_SB;
             ss[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, so[k], b * 4, 0));
+            if (ASYM) sm[k] = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(rm, so[k], b * 4, 0);
         }
 #pragma unroll
         for (int k = 0; k < WPT; k++) sw[k] = __builtin_amdgcn_raw_buffer_load_b32(rg, og[k], st * GM_SB * 16, 0);
@@ -1047,19 +1168,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
 #pragma unroll
         for (int k = 0; k < SPT; k++) {
             const int i = tid + 256 * k, tk = i % NT, sbt = i / NT;
-            if (NT * GM_SB % 256 == 0 || i < NT * GM_SB) bs[buf][sbt][tk & 15][tk >> 4] = ss[k];
+            if (NT * GM_SB % 256 == 0 || i < NT * GM_SB) {
+                bs[buf][sbt][tk & 15][tk >> 4] = ss[k];
+                if (ASYM) bm[ASYM ? buf : 0][sbt][tk & 15][tk >> 4] = sm[k];
+            }
         }
 #pragma unroll
         for (int k = 0; k < WPT; k++) (&bw[buf][0][0])[wgi[k]] = sw[k];
     };
-    // nibble words of one stage, per fragment and block
+    // nibble words (and mode 14 high-bit words) of one stage, per fragment and block
     uint32_t wn[2][GM_SB][RF];
-    auto weights_load = [&](int st, uint32_t (&n)[GM_SB][RF]) {
+    uint32_t wh[2][GM_SB][RF];
+    auto weights_load = [&](int st, uint32_t (&n)[GM_SB][RF], uint32_t (&hn)[GM_SB][RF]) {
 #pragma unroll
         for (int sb = 0; sb < GM_SB; sb++) {
             const int b = min(st * GM_SB + sb, n_blk - 1);
 #pragma unroll
-            for (int f = 0; f < RF; f++) n[sb][f] = __builtin_amdgcn_raw_buffer_load_b32(rw, on[f], b * 128, 0);
+            for (int f = 0; f < RF; f++) {
+                n[sb][f] = __builtin_amdgcn_raw_buffer_load_b32(rw, on[f], b * 128, 0);
+                hn[sb][f] = MODE == 14 ? __builtin_amdgcn_raw_buffer_load_b32(rw, oh[f], b * 64, 0) : 0u;
+            }
         }
     };
 
@@ -1077,6 +1205,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
     // v_fma_mix_f32.
     gm_h8 bfr[2][TT];
     float xsr[2][TT];
+    int32_t xmr[2][TT];
     uint32_t wsr[2][RF][2];
     auto lds_b = [&](int buf, int sb, int slot) {
 #pragma unroll
@@ -1087,13 +1216,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
         }
 #pragma unroll
         for (int t = 0; t < TT; t++) xsr[slot][t] = bs[buf][sb][i16][t];
+        if (ASYM) {
+#pragma unroll
+            for (int t = 0; t < TT; t++) xmr[slot][t] = bm[ASYM ? buf : 0][sb][i16][t];
+        }
 #pragma unroll
         for (int t = 0; t < TT; t++) {
             const int tok = 16 * t + i16;
             bfr[slot][t] = *(const gm_h8*)&bq[buf][sb][tok][16 * (kc ^ ((tok >> 1) & 3))];
         }
     };
-    auto compute = [&](int st, int buf, const uint32_t (&n)[GM_SB][RF]) {
+    // modes 13 / 14: the even block of a 64-block pair waits in registers for
+    // the odd one: its D tiles, token scales and sums, and the lane's 4 d
+    gm_f4 dk[RF][TT];
+    float xs0k[TT];
+    int32_t xm0k[TT];
+    float dsk[RF][4];
+    auto compute = [&](int st, int buf, const uint32_t (&n)[GM_SB][RF], const uint32_t (&hn)[GM_SB][RF]) {
         lds_b(buf, 0, 0);
 #pragma unroll
         for (int sb = 0; sb < GM_SB; sb++) {
@@ -1104,7 +1243,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
             _Float16 wsh[RF][4];
 #pragma unroll
             for (int f = 0; f < RF; f++) {
-                a[f] = gm_unpack_a(n[sb][f]);
+                a[f] = ASYM ? gm_unpack_a_asym(n[sb][f], (hn[sb][f] >> ((kc & 1) * 4)))
+                            : gm_unpack_a(n[sb][f]);
                 const gm_h2 lo = __builtin_bit_cast(gm_h2, wsr[sb & 1][f][0]),
                             hi = __builtin_bit_cast(gm_h2, wsr[sb & 1][f][1]);
                 wsh[f][0] = lo[0];
@@ -1115,6 +1255,46 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
             float xs[TT];
 #pragma unroll
             for (int t = 0; t < TT; t++) xs[t] = xsr[sb & 1][t];
+            if (ASYM) {
+                // 64-block epilogue (dpuf_avx2.c:2871-2882), rows 4 kc' + v
+                // of the fragment for token 16 t + i16:
+                //   fdot = fma(float(D0), xs0, float(D1) * xs1)
+                //   acc = fma(fdot, d, acc); acc = fma(m, xm_s, acc)
+                if ((sb & 1) == 0) {
+#pragma unroll
+                    for (int t = 0; t < TT; t++) {
+                        xs0k[t] = xs[t];
+                        xm0k[t] = xmr[sb & 1][t];
+#pragma unroll
+                        for (int f = 0; f < RF; f++)
+                            dk[f][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[f], bfr[sb & 1][t],
+                                                                              (gm_f4){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+                    }
+#pragma unroll
+                    for (int f = 0; f < RF; f++)
+#pragma unroll
+                        for (int v = 0; v < 4; v++) dsk[f][v] = (float)wsh[f][v];
+                } else {
+#pragma unroll
+                    for (int t = 0; t < TT; t++) {
+                        const float pa = (float)xm0k[t] * xs0k[t], pb = (float)xmr[sb & 1][t] * xs[t];
+                        const float xms = (pa + pb) * 0.125f;
+#pragma unroll
+                        for (int f = 0; f < RF; f++) {
+                            const gm_f4 d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                                a[f], bfr[sb & 1][t], (gm_f4){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+#pragma unroll
+                            for (int v = 0; v < 4; v++) {
+                                const float p1 = d1[v] * xs[t];
+                                const float fd = fmaf(dk[f][t][v], xs0k[t], p1);
+                                acc[f][t][v] = fmaf(fd, dsk[f][v], acc[f][t][v]);
+                                acc[f][t][v] = fmaf((float)wsh[f][v], xms, acc[f][t][v]);
+                            }
+                        }
+                    }
+                }
+                continue;
+            }
 #pragma unroll
             for (int t = 0; t < TT; t++) {
                 const gm_h8 bf = bfr[sb & 1][t];
@@ -1139,25 +1319,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
 
     // prologue: stage 0 into LDS buffer 0, weights of stage 0
     stage_load(0);
-    weights_load(0, wn[0]);
+    weights_load(0, wn[0], wh[0]);
     stage_store(0);
     __syncthreads();
     int st = 0;
     for (; st + 2 <= n_st; st += 2) {
         stage_load(st + 1);
-        weights_load(st + 1, wn[1]);
-        compute(st, 0, wn[0]);
+        weights_load(st + 1, wn[1], wh[1]);
+        compute(st, 0, wn[0], wh[0]);
         stage_store(1);
         __syncthreads();
         // on the last pair this stages clamped data that is never computed;
         // the loop body has no branch around its loads
         stage_load(st + 2);
-        weights_load(st + 2, wn[0]);
-        compute(st + 1, 1, wn[1]);
+        weights_load(st + 2, wn[0], wh[0]);
+        compute(st + 1, 1, wn[1], wh[1]);
         stage_store(0);
         __syncthreads();
     }
-    if (st < n_st) compute(st, 0, wn[0]);
+    if (st < n_st) compute(st, 0, wn[0], wh[0]);
 
     // rows 16 RF w + 16f + 4kc + v of the workgroup, token m0 + 16t + i16
 #pragma unroll
@@ -3583,10 +3763,11 @@ void dpuf_hip_swiglu_prep(void* s, int32_t M, int32_t I, const float* gate, cons
 }
 
 void dpuf_hip_relayout(void* s, const uint8_t* src, const uint64_t* offs, int32_t n_groups, int32_t n_blk,
-                       uint8_t* dst) {
+                       int32_t mode, uint8_t* dst) {
     const size_t total = (size_t)n_groups * n_blk * 8;
     const int blocks = (int)((total + 255) / 256 < 65536 ? (total + 255) / 256 : 65536);
-    hipLaunchKernelGGL(k_relayout, dim3(blocks), dim3(256), 0, ST(s), src, offs, n_groups, n_blk, dst);
+    hipLaunchKernelGGL(k_relayout, dim3(blocks), dim3(256), 0, ST(s), src, offs, n_groups, n_blk, (int)(mode == 14),
+                       dst);
     LAUNCHED("k_relayout");
 }
 
@@ -3605,9 +3786,9 @@ void dpuf_hip_bind_error_word(int32_t* d_word) { g_err_word = d_word; }
 // cached per (instance, block size, LDS size).
 static int mv_capacity(MvKernel k, int threads, size_t lds) {
     static int n_cu = 0;
-    static MvKernel c_k[16];
-    static int c_t[16], c_cap[16], c_n = 0;
-    static size_t c_lds[16];
+    static MvKernel c_k[64];
+    static int c_t[64], c_cap[64], c_n = 0;
+    static size_t c_lds[64];
     for (int i = 0; i < c_n; i++)
         if (c_k[i] == k && c_t[i] == threads && c_lds[i] == lds) return c_cap[i];
     if (n_cu == 0) {
@@ -3620,7 +3801,7 @@ static int mv_capacity(MvKernel k, int threads, size_t lds) {
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, threads, lds) != hipSuccess || per_cu <= 0)
         per_cu = 1;
     const int cap = per_cu * n_cu;
-    if (c_n < 16) {
+    if (c_n < 64) {
         c_k[c_n] = k;
         c_t[c_n] = threads;
         c_lds[c_n] = lds;
@@ -3633,32 +3814,43 @@ static int mv_capacity(MvKernel k, int threads, size_t lds) {
 // NL = 1..4 steps per loader wave and at most 15 loader waves (S <= 60),
 // otherwise 8 loader waves x 2 steps per round with the activations loaded
 // per round.  The block has one more wave, the chain wave.
-static void mv_launch(void* s, MvArgs& A, const int* n_groups) {
+extern "C++" {
+template <int MODE>
+static void mv_pick(int S, MvKernel& k, MvKernel& k1, int& nl, int& nw) {
+    if (S <= 16 - MV_NC) {
+        nl = 1;
+        k = k_mv<1, true, false, MODE>;
+        k1 = k_mv<1, true, true, MODE>;
+    } else if (S <= 2 * (16 - MV_NC)) {
+        nl = 2;
+        k = k_mv<2, true, false, MODE>;
+        k1 = k_mv<2, true, true, MODE>;
+    } else if (S <= 3 * (16 - MV_NC)) {
+        nl = 3;
+        k = k_mv<3, true, false, MODE>;
+        k1 = k_mv<3, true, true, MODE>;
+    } else if (S <= 4 * (16 - MV_NC) && MV_HOIST48) {
+        nl = 4;
+        k = k_mv<4, true, false, MODE>;
+        k1 = k_mv<4, true, true, MODE>;
+    } else {
+        nl = 2;
+        k = k_mv<2, false, false, MODE>;
+        k1 = k_mv<2, false, true, MODE>;
+    }
+    nw = k == k_mv<2, false, false, MODE> ? 8 : (S + nl - 1) / nl;
+}
+}
+
+// One launch over jobs of one mode.
+static void mv_launch(void* s, MvArgs& A, const int* n_groups, int mode) {
     const int n_blk = A.K >> 5, S = (n_blk + 7) >> 3;
     MvKernel k, k1;  // persistent and one-group-per-workgroup instances
     int nl, nw;
-    if (S <= 16 - MV_NC) {
-        nl = 1;
-        k = k_mv<1, true, false>;
-        k1 = k_mv<1, true, true>;
-    } else if (S <= 2 * (16 - MV_NC)) {
-        nl = 2;
-        k = k_mv<2, true, false>;
-        k1 = k_mv<2, true, true>;
-    } else if (S <= 3 * (16 - MV_NC)) {
-        nl = 3;
-        k = k_mv<3, true, false>;
-        k1 = k_mv<3, true, true>;
-    } else if (S <= 4 * (16 - MV_NC) && MV_HOIST48) {
-        nl = 4;
-        k = k_mv<4, true, false>;
-        k1 = k_mv<4, true, true>;
-    } else {
-        nl = 2;
-        k = k_mv<2, false, false>;
-        k1 = k_mv<2, false, true>;
-    }
-    nw = k == k_mv<2, false, false> ? 8 : (S + nl - 1) / nl;
+    if (mode == 13) mv_pick<13>(S, k, k1, nl, nw);
+    else if (mode == 14) mv_pick<14>(S, k, k1, nl, nw);
+    else mv_pick<12>(S, k, k1, nl, nw);
+    (void)nl;
     const int threads_p = (nw + MV_NC) * 64;  // + the chain waves
     const size_t buf = (size_t)8 * (n_blk + 2) * 8;
     int total = 0;
@@ -3735,27 +3927,42 @@ void dpuf_hip_gemv_zero(void* s, int32_t M, const DpufGemvJob* job, int32_t r0, 
 
 void dpuf_hip_gemv(void* s, int32_t M, int32_t n_jobs, const DpufGemvJob* jobs, const int32_t* skip_flag,
                    float fill) {
-    if (M == 1) {
+    // jobs of different modes go to one launch per mode, in order of first use
+    for (int i = 0; i < n_jobs; i++) {
+        const int mode = jobs[i].w.mode;
+        if (mode != 12 && mode != 13 && mode != 14) {
+            note(hipErrorInvalidValue, "dpuf_hip_gemv: matrix mode other than 12, 13, 14");
+            return;
+        }
+        bool seen = false;
+        for (int j = 0; j < i; j++) seen = seen || jobs[j].w.mode == mode;
+        if (seen) continue;
+        DpufGemvJob sub[3];
+        int n = 0;
+        for (int j = i; j < n_jobs; j++)
+            if (jobs[j].w.mode == mode) sub[n++] = jobs[j];
+        if (M > 1) {
+            gm_launch(s, M, n, sub, NULL, 0, 0, 0);
+            continue;
+        }
         MvArgs A;
         memset(&A, 0, sizeof A);
         int ng[3] = {0, 0, 0};
-        A.n_jobs = n_jobs;
-        A.K = jobs[0].w.cols;
-        for (int i = 0; i < n_jobs; i++) {
-            A.j[i].g = jobs[i].w.g;
-            A.j[i].out = jobs[i].out;
-            A.j[i].g0 = jobs[i].g0;
-            A.j[i].g1 = jobs[i].g1;
-            A.j[i].rows = jobs[i].w.rows;
-            A.j[i].x = jobs[i].p;
-            ng[i] = jobs[i].g1 - jobs[i].g0 > 0 ? jobs[i].g1 - jobs[i].g0 : 0;
+        A.n_jobs = n;
+        A.K = sub[0].w.cols;
+        for (int j = 0; j < n; j++) {
+            A.j[j].g = sub[j].w.g;
+            A.j[j].out = sub[j].out;
+            A.j[j].g0 = sub[j].g0;
+            A.j[j].g1 = sub[j].g1;
+            A.j[j].rows = sub[j].w.rows;
+            A.j[j].x = sub[j].p;
+            ng[j] = sub[j].g1 - sub[j].g0 > 0 ? sub[j].g1 - sub[j].g0 : 0;
         }
         A.skip_flag = skip_flag;
         A.fill = fill;
-        mv_launch(s, A, ng);
-        return;
+        mv_launch(s, A, ng, mode);
     }
-    gm_launch(s, M, n_jobs, jobs, NULL, 0, 0, 0);
 }
 
 // The M > 1 GEMM; rows [z0, z1) of zo are zeroed by the same launch.
@@ -3783,6 +3990,7 @@ static void gm_launch(void* s, int32_t M, int32_t n_jobs, const DpufGemvJob* job
                 return;
             }
             G.j[i].s = jobs[i].p.s;
+            G.j[i].m = jobs[i].p.m;
             G.j[i].out = jobs[i].out;
             G.j[i].ldo = jobs[i].ldo;
             G.tb[i] = t;
@@ -3799,9 +4007,10 @@ static void gm_launch(void* s, int32_t M, int32_t n_jobs, const DpufGemvJob* job
         }
         if (t + G.zt <= 0) return;
         const int n_blk = G.K >> 5;
+        const int mode = jobs[0].w.mode;  // one mode per launch (dpuf_hip_gemv groups them)
         long long gmax = 0;
         for (int i = 0; i < n_jobs; i++) gmax = gmax > jobs[i].g1 ? gmax : jobs[i].g1;
-        if (M <= 16 && n_blk <= 128 && gmax * n_blk * 144 < 0xFFFFFFFFll) {
+        if (mode == 12 && M <= 16 && n_blk <= 128 && gmax * n_blk * 144 < 0xFFFFFFFFll) {
             // one 16-token tile, K <= 4096: persistent K-split workgroups,
             // each job's share of the chip in proportion to its fragments
             const int NR = n_blk <= 32 ? 1 : n_blk <= 64 ? 2 : 4;
@@ -3826,7 +4035,7 @@ static void gm_launch(void* s, int32_t M, int32_t n_jobs, const DpufGemvJob* job
             LAUNCHED("k_gemm_skp");
             return;
         }
-        if (M <= 16) {
+        if (mode == 12 && M <= 16) {
             // one 16-token tile: the K-split kernel, one workgroup per 16 rows
             int f = 0;
             for (int i = 0; i < n_jobs; i++) {
@@ -3843,10 +4052,14 @@ static void gm_launch(void* s, int32_t M, int32_t n_jobs, const DpufGemvJob* job
         const int gx = (t + G.zt + 7) & ~7;
         G.gy = (M + 16 * GM_TT - 1) / (16 * GM_TT);
         const dim3 grid = GM_XCD ? dim3(gx * G.gy) : dim3(gx, G.gy);
-        if (GM_RF == 2)
-            hipLaunchKernelGGL((k_gemm_mfma<GM_TT, 2>), grid, dim3(256), 0, ST(s), G);
+        // modes 13 / 14 take this kernel at every M (the K-split kernels
+        // are mode 12 only)
+        if (mode == 13)
+            hipLaunchKernelGGL((k_gemm_mfma<GM_TT, GM_RF, 13>), grid, dim3(256), 0, ST(s), G);
+        else if (mode == 14)
+            hipLaunchKernelGGL((k_gemm_mfma<GM_TT, GM_RF, 14>), grid, dim3(256), 0, ST(s), G);
         else
-            hipLaunchKernelGGL((k_gemm_mfma<GM_TT, 1>), grid, dim3(256), 0, ST(s), G);
+            hipLaunchKernelGGL((k_gemm_mfma<GM_TT, GM_RF, 12>), grid, dim3(256), 0, ST(s), G);
         LAUNCHED("k_gemm_mfma");
     }
 }

@@ -1,6 +1,7 @@
 /*
- * standalone.c -- the mode 12 entry points of the ABI that take host
- * pointers (reference dpuf_avx2.c:774-788, 2364-2449, 2585-2783).  Each call
+ * standalone.c -- the mode 12, 13 and 14 entry points of the ABI that take
+ * host pointers (reference dpuf_avx2.c:774-788, 2364-2449, 2585-2783,
+ * 2947-3221).  Each call
  * validates its tiles on the host, stages inputs to HBM, runs the same HIP
  * kernels as the engine, and copies results back before returning.  They are
  * synchronous and allocate per call; throughput users keep weights resident
@@ -39,13 +40,13 @@ static int32_t max_chunk(int32_t M, int32_t cols) {
     return (int64_t)M < cap ? M : (int32_t)cap;
 }
 
-/* Checks tiles [t0, t1) of a mode 12 payload (tile t holds min(16, rows -
- * 16t) rows, its groups lie inside the byte range) and returns the byte
- * range [*lo, *hi). */
-static int check_tiles(int32_t rows, int32_t cols, int32_t t0, int32_t t1, const uint8_t* base,
+/* Checks tiles [t0, t1) of a mode 12 / 13 / 14 payload (tile t holds
+ * min(16, rows - 16t) rows, its groups lie inside the byte range) and
+ * returns the byte range [*lo, *hi). */
+static int check_tiles(int32_t mode, int32_t rows, int32_t cols, int32_t t0, int32_t t1, const uint8_t* base,
                        const uint64_t* offs, uint64_t* lo, uint64_t* hi) {
     if (cols <= 0 || (cols % 64) != 0 || t0 < 0 || t1 <= t0 || !base || !offs) return 0;
-    const uint64_t grp = (uint64_t)(cols / 32) * 144u;
+    const uint64_t grp = (uint64_t)(cols / 32) * (uint64_t)dpuf_grp_unit(mode);
     *lo = offs[t0];
     *hi = offs[t1];
     if (*hi < *lo) return 0;
@@ -67,11 +68,11 @@ typedef struct {
 } Staged;
 
 /* Uploads tiles [t0, t1) and converts them to the row-block layout. */
-static int stage_weights(int32_t rows, int32_t cols, int32_t t0, int32_t t1, const uint8_t* base,
+static int stage_weights(int32_t mode, int32_t rows, int32_t cols, int32_t t0, int32_t t1, const uint8_t* base,
                          const uint64_t* offs, const uint8_t* sign, Staged* st) {
     uint64_t lo, hi;
     memset(st, 0, sizeof *st);
-    if (!check_tiles(rows, cols, t0, t1, base, offs, &lo, &hi)) return 0;
+    if (!check_tiles(mode, rows, cols, t0, t1, base, offs, &lo, &hi)) return 0;
     void* s = stream();
     const int32_t nt = t1 - t0, n_blk = cols / 32;
     const int32_t rows_st = (rows < 16 * t1 ? rows : 16 * t1) - 16 * t0;
@@ -81,14 +82,15 @@ static int stage_weights(int32_t rows, int32_t cols, int32_t t0, int32_t t1, con
     for (int32_t t = 0; t <= nt; t++) rel[t] = offs[t0 + t] - lo;
     void* d_raw = dpuf_hip_malloc((size_t)(hi - lo));
     void* d_offs = dpuf_hip_malloc(((size_t)nt + 1) * 8);
-    st->groups = dpuf_hip_malloc((size_t)n_groups * n_blk * 144);
+    st->groups = dpuf_hip_malloc((size_t)n_groups * n_blk * dpuf_grp_unit(mode));
     if (sign) st->sign = dpuf_hip_malloc((size_t)cols / 8);
     int ok = d_raw && d_offs && st->groups && (!sign || st->sign);
     if (ok) {
         dpuf_hip_h2d(d_raw, base + lo, (size_t)(hi - lo), s);
         dpuf_hip_h2d(d_offs, rel, ((size_t)nt + 1) * 8, s);
         if (sign) dpuf_hip_h2d(st->sign, sign, (size_t)cols / 8, s);
-        dpuf_hip_relayout(s, (const uint8_t*)d_raw, (const uint64_t*)d_offs, n_groups, n_blk, (uint8_t*)st->groups);
+        dpuf_hip_relayout(s, (const uint8_t*)d_raw, (const uint64_t*)d_offs, n_groups, n_blk, mode,
+                          (uint8_t*)st->groups);
         ok = dpuf_hip_sync(s) == 0;
     }
     free(rel);
@@ -105,6 +107,7 @@ static int stage_weights(int32_t rows, int32_t cols, int32_t t0, int32_t t1, con
     st->w.rows = rows_st;
     st->w.cols = cols;
     st->w.n_groups = n_groups;
+    st->w.mode = mode;
     return 1;
 }
 
@@ -202,11 +205,11 @@ static void fetch_rows(float* out, const float* dout, int32_t M, int32_t rows, i
         dpuf_hip_d2h(out + (size_t)m * rows + r0, dout + (size_t)m * rows + r0, (size_t)(r1 - r0) * 4, s);
 }
 
-DPUF_EXPORT void dpuf_matmul_qr_hadamard4_packed_tile_range(int32_t M, int32_t rows, int32_t cols, int32_t t_start,
-                                                            int32_t t_end, const int8_t* x_q8,
-                                                            const float* x_blk_scale, const int32_t* x_sum8,
-                                                            const uint8_t* tensor_base, const uint64_t* tile_offsets,
-                                                            float* out) {
+/* Tiles [t_start, t_end) of a mode 12 / 13 / 14 matrix from prepped
+ * activations (row layout for M == 1, slab layout for M > 1). */
+static void tile_range(int32_t mode, int32_t M, int32_t rows, int32_t cols, int32_t t_start, int32_t t_end,
+                       const int8_t* x_q8, const float* x_blk_scale, const int32_t* x_sum8,
+                       const uint8_t* tensor_base, const uint64_t* tile_offsets, float* out) {
     void* s = stream();
     if (!s || M <= 0 || rows <= 0 || t_start < 0 || t_end <= t_start || (int64_t)t_start * 16 >= rows || !x_q8 ||
         !x_blk_scale || !x_sum8 || !out)
@@ -215,7 +218,7 @@ DPUF_EXPORT void dpuf_matmul_qr_hadamard4_packed_tile_range(int32_t M, int32_t r
     if ((int64_t)M * cols >= ((int64_t)1 << 30)) return; /* the slab inputs are one block */
     const int32_t r1 = t_end * 16 < rows ? t_end * 16 : rows;
     Staged st;
-    if (!stage_weights(rows, cols, t_start, t_end, tensor_base, tile_offsets, NULL, &st)) {
+    if (!stage_weights(mode, rows, cols, t_start, t_end, tensor_base, tile_offsets, NULL, &st)) {
         fail_rows(out, M, rows, t_start * 16, r1);
         return;
     }
@@ -265,15 +268,40 @@ DPUF_EXPORT void dpuf_matmul_qr_hadamard4_packed_tile_range(int32_t M, int32_t r
     unstage(&st);
 }
 
-DPUF_EXPORT void dpuf_matmul_qr_hadamard4_packed_f32(int32_t M, int32_t rows, int32_t cols, int32_t n_tiles,
-                                                     const float* x_in, const uint8_t* tensor_base,
-                                                     const uint64_t* tile_offsets, const uint8_t* sign_bits,
-                                                     float* out) {
+DPUF_EXPORT void dpuf_matmul_qr_hadamard4_packed_tile_range(int32_t M, int32_t rows, int32_t cols, int32_t t_start,
+                                                            int32_t t_end, const int8_t* x_q8,
+                                                            const float* x_blk_scale, const int32_t* x_sum8,
+                                                            const uint8_t* tensor_base, const uint64_t* tile_offsets,
+                                                            float* out) {
+    tile_range(DPUF_MODE_QR_HAD4_PACKED, M, rows, cols, t_start, t_end, x_q8, x_blk_scale, x_sum8, tensor_base,
+               tile_offsets, out);
+}
+
+DPUF_EXPORT void dpuf_matmul_qr_had4_asym_tile_range(int32_t M, int32_t rows, int32_t cols, int32_t t_start,
+                                                     int32_t t_end, const int8_t* x_q8, const float* x_blk_scale,
+                                                     const int32_t* x_sum8, const uint8_t* tensor_base,
+                                                     const uint64_t* tile_offsets, float* out) {
+    tile_range(DPUF_MODE_QR_HAD4_ASYM, M, rows, cols, t_start, t_end, x_q8, x_blk_scale, x_sum8, tensor_base,
+               tile_offsets, out);
+}
+
+DPUF_EXPORT void dpuf_matmul_qr_had6_tile_range(int32_t M, int32_t rows, int32_t cols, int32_t t_start,
+                                                int32_t t_end, const int8_t* x_q8, const float* x_blk_scale,
+                                                const int32_t* x_sum8, const uint8_t* tensor_base,
+                                                const uint64_t* tile_offsets, float* out) {
+    tile_range(DPUF_MODE_QR_HAD6, M, rows, cols, t_start, t_end, x_q8, x_blk_scale, x_sum8, tensor_base,
+               tile_offsets, out);
+}
+
+/* out[M][rows] = W x for a mode 12 / 13 / 14 matrix: prep + GEMV / GEMM. */
+static void matmul_f32(int32_t mode, int32_t M, int32_t rows, int32_t cols, int32_t n_tiles, const float* x_in,
+                       const uint8_t* tensor_base, const uint64_t* tile_offsets, const uint8_t* sign_bits,
+                       float* out) {
     void* s = stream();
     if (!s || M <= 0 || rows <= 0 || n_tiles <= 0 || !x_in || !out) return;
     if ((int64_t)n_tiles * 16 > (int64_t)rows + 15 || (int64_t)n_tiles * 16 < rows) return;
     Staged st;
-    if (!stage_weights(rows, cols, 0, n_tiles, tensor_base, tile_offsets, sign_bits, &st)) {
+    if (!stage_weights(mode, rows, cols, 0, n_tiles, tensor_base, tile_offsets, sign_bits, &st)) {
         fail_rows(out, M, rows, 0, rows);
         return;
     }
@@ -314,9 +342,29 @@ DPUF_EXPORT void dpuf_matmul_qr_hadamard4_packed_f32(int32_t M, int32_t rows, in
     unstage(&st);
 }
 
-DPUF_EXPORT void dpuf_embed_qr_hadamard4_packed_f32(int32_t n_tokens, int32_t cols, const int32_t* token_ids,
-                                                    const uint8_t* tensor_base, const uint64_t* tile_offsets,
-                                                    const uint8_t* sign_bits, float* out) {
+DPUF_EXPORT void dpuf_matmul_qr_hadamard4_packed_f32(int32_t M, int32_t rows, int32_t cols, int32_t n_tiles,
+                                                     const float* x_in, const uint8_t* tensor_base,
+                                                     const uint64_t* tile_offsets, const uint8_t* sign_bits,
+                                                     float* out) {
+    matmul_f32(DPUF_MODE_QR_HAD4_PACKED, M, rows, cols, n_tiles, x_in, tensor_base, tile_offsets, sign_bits, out);
+}
+
+DPUF_EXPORT void dpuf_matmul_qr_had4_asym_f32(int32_t M, int32_t rows, int32_t cols, int32_t n_tiles,
+                                              const float* x_in, const uint8_t* tensor_base,
+                                              const uint64_t* tile_offsets, const uint8_t* sign_bits, float* out) {
+    matmul_f32(DPUF_MODE_QR_HAD4_ASYM, M, rows, cols, n_tiles, x_in, tensor_base, tile_offsets, sign_bits, out);
+}
+
+DPUF_EXPORT void dpuf_matmul_qr_had6_f32(int32_t M, int32_t rows, int32_t cols, int32_t n_tiles,
+                                         const float* x_in, const uint8_t* tensor_base,
+                                         const uint64_t* tile_offsets, const uint8_t* sign_bits, float* out) {
+    matmul_f32(DPUF_MODE_QR_HAD6, M, rows, cols, n_tiles, x_in, tensor_base, tile_offsets, sign_bits, out);
+}
+
+/* Embedding rows of a mode 12 / 13 / 14 matrix. */
+static void embed_f32(int32_t mode, int32_t n_tokens, int32_t cols, const int32_t* token_ids,
+                      const uint8_t* tensor_base, const uint64_t* tile_offsets, const uint8_t* sign_bits,
+                      float* out) {
     void* s = stream();
     if (!s || n_tokens <= 0 || !token_ids || !out) return;
     int32_t max_id = 0;
@@ -334,7 +382,8 @@ DPUF_EXPORT void dpuf_embed_qr_hadamard4_packed_f32(int32_t n_tokens, int32_t co
     DpufQrTileHdr last;
     memcpy(&last, tensor_base + tile_offsets[nt - 1], sizeof last);
     Staged st;
-    if (!stage_weights((nt - 1) * 16 + last.n_rows, cols, 0, nt, tensor_base, tile_offsets, sign_bits, &st)) return;
+    if (!stage_weights(mode, (nt - 1) * 16 + last.n_rows, cols, 0, nt, tensor_base, tile_offsets, sign_bits, &st))
+        return;
     int32_t* dids = (int32_t*)dpuf_hip_malloc((size_t)n_tokens * 4);
     float* dout = (float*)dpuf_hip_malloc((size_t)n_tokens * cols * 4);
     if (dids && dout) {
@@ -348,10 +397,29 @@ DPUF_EXPORT void dpuf_embed_qr_hadamard4_packed_f32(int32_t n_tokens, int32_t co
     unstage(&st);
 }
 
+DPUF_EXPORT void dpuf_embed_qr_hadamard4_packed_f32(int32_t n_tokens, int32_t cols, const int32_t* token_ids,
+                                                    const uint8_t* tensor_base, const uint64_t* tile_offsets,
+                                                    const uint8_t* sign_bits, float* out) {
+    embed_f32(DPUF_MODE_QR_HAD4_PACKED, n_tokens, cols, token_ids, tensor_base, tile_offsets, sign_bits, out);
+}
+
+DPUF_EXPORT void dpuf_embed_qr_had4_asym_f32(int32_t n_tokens, int32_t cols, const int32_t* token_ids,
+                                             const uint8_t* tensor_base, const uint64_t* tile_offsets,
+                                             const uint8_t* sign_bits, float* out) {
+    embed_f32(DPUF_MODE_QR_HAD4_ASYM, n_tokens, cols, token_ids, tensor_base, tile_offsets, sign_bits, out);
+}
+
+DPUF_EXPORT void dpuf_embed_qr_had6_f32(int32_t n_tokens, int32_t cols, const int32_t* token_ids,
+                                        const uint8_t* tensor_base, const uint64_t* tile_offsets,
+                                        const uint8_t* sign_bits, float* out) {
+    embed_f32(DPUF_MODE_QR_HAD6, n_tokens, cols, token_ids, tensor_base, tile_offsets, sign_bits, out);
+}
+
 DPUF_EXPORT void dpuf_embed_qr_any_f32(const DpufWeightDesc* w, int32_t n_tokens, const int32_t* token_ids,
                                        float* out, float* scratch_f32) {
     (void)scratch_f32;
-    if (!w || w->mode != DPUF_MODE_QR_HAD4_PACKED) return; /* other modes are not built */
-    dpuf_embed_qr_hadamard4_packed_f32(n_tokens, w->cols, token_ids, w->tensor_base, w->tile_offsets, w->sign_bits,
-                                       out);
+    if (!w || (w->mode != DPUF_MODE_QR_HAD4_PACKED && w->mode != DPUF_MODE_QR_HAD4_ASYM &&
+               w->mode != DPUF_MODE_QR_HAD6))
+        return; /* other modes are not built */
+    embed_f32(w->mode, n_tokens, w->cols, token_ids, w->tensor_base, w->tile_offsets, w->sign_bits, out);
 }

@@ -1,4 +1,5 @@
-"""Python host helpers around libdpuf_tools.so: build or open a mode 12 model
+"""Python host helpers around libdpuf_tools.so: build or open a model (mode 12,
+or the mode 13 / 14 had4p-hybrid plan with weight_plan=1)
 and hand its C descriptors to an engine.  Mirrors the role of the reference's
 Python host (dpuf_format.py:2130-2357), with the token loop on the GPU.
 """
@@ -115,14 +116,19 @@ def ptr(a):
     return a.ctypes.data_as(C.c_void_p)
 
 
-def pack_matrix(W, sign_bits, ecc_group=64):
-    """Packs an fp32 [rows, cols] array into a mode 12 blob (bytes-like ndarray)
-    and returns (blob, desc).  The blob must outlive the desc."""
+def pack_matrix(W, sign_bits, ecc_group=64, mode=12, w_pow=0.0):
+    """Packs an fp32 [rows, cols] array into a mode 12, 13 or 14 blob
+    (bytes-like ndarray) and returns (blob, desc).  The blob must outlive the
+    desc."""
     lib = abi.load_tools()
     W = np.ascontiguousarray(W, dtype=np.float32)
     sb = np.ascontiguousarray(sign_bits, dtype=np.uint8)
     n = C.c_size_t(0)
-    p = lib.dpuf_tools_pack_mode12(ptr(W), W.shape[0], W.shape[1], ptr(sb), ecc_group, C.byref(n))
+    if mode == 12:
+        p = lib.dpuf_tools_pack_mode12(ptr(W), W.shape[0], W.shape[1], ptr(sb), ecc_group, C.byref(n))
+    else:
+        p = lib.dpuf_tools_pack_asym(ptr(W), W.shape[0], W.shape[1], ptr(sb), ecc_group, 4 if mode == 13 else 6,
+                                     w_pow, C.byref(n))
     if not p:
         raise RuntimeError("pack failed")
     blob = np.frombuffer((C.c_uint8 * n.value).from_address(p), dtype=np.uint8).copy()

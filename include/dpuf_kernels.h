@@ -1,5 +1,5 @@
 /*
- * dpuf_kernels.h -- C ABI of the MI355X DPUF token loop (Mode 12 only).
+ * dpuf_kernels.h -- C ABI of the MI355X DPUF token loop (Modes 12, 13, 14).
  *
  * This header is the drop-in boundary.  Every type and entry point below keeps
  * the layout, the argument meaning and the return codes of the reference
@@ -9,8 +9,10 @@
  * kernels, and nothing here computes on the CPU except the CRC32 tile check,
  * which is host ingest in the reference as well.
  *
- * Only the Hadamard-4bit packed format (mode 12) is implemented.  Weight
- * descriptors of any other mode make dpuf_engine_create return NULL.
+ * The Hadamard-4bit packed format (mode 12) and the asymmetric blk64 4-bit
+ * and 6-bit formats (modes 13, 14; the had4p-hybrid packing) are
+ * implemented, mixed freely per matrix.  Weight descriptors of any other mode
+ * make dpuf_engine_create return NULL.
  */
 #ifndef DPUF_KERNELS_H
 #define DPUF_KERNELS_H
@@ -31,7 +33,7 @@ enum {
     DPUF_MODE_QR_HAD6        = 14
 };
 
-/* KV cache element type (reference dpuf_kernels.h:39-42).  Only F32 is built. */
+/* KV cache element type (reference dpuf_kernels.h:39-42). */
 enum {
     DPUF_KV_F32 = 0,
     DPUF_KV_Q8  = 1
@@ -43,14 +45,14 @@ typedef struct {
     uint32_t tile_crc32;   /* CRC32 of the tile body that follows            */
     uint16_t n_rows;       /* rows stored in this tile (<= 16)                */
     uint16_t flags;        /* 0                                               */
-    uint32_t n_over8;      /* 0 for mode 12                                   */
-    uint32_t n_super16;    /* 0 for mode 12                                   */
+    uint32_t n_over8;      /* 0 for modes 12-14                               */
+    uint32_t n_super16;    /* 0 for modes 12-14                               */
 } DpufQrTileHdr;
 #pragma pack(pop)
 
 /* Borrowed view of one QR-tiled weight matrix (reference dpuf_kernels.h:53-62).
- * 48 bytes on LP64.  For mode 12 col_scale is NULL and sign_bits holds cols/8
- * bytes (bit c%8 of byte c/8 set = negate column c). */
+ * 48 bytes on LP64.  For modes 12-14 col_scale is NULL and sign_bits holds
+ * cols/8 bytes (bit c%8 of byte c/8 set = negate column c). */
 typedef struct {
     int32_t mode;
     int32_t rows;
@@ -170,8 +172,50 @@ DPUF_EXPORT void dpuf_embed_qr_hadamard4_packed_f32(
     const uint8_t* tensor_base, const uint64_t* tile_offsets,
     const uint8_t* sign_bits, float* out);
 
-/* Mode dispatcher for embeddings (mode 12 only here).
- * Replaces reference dpuf_kernels.h:170-176 (dpuf_avx2.c:2044-2067). */
+/* ---- Modes 13 / 14: asymmetric blk64 4-bit / 6-bit ----------------------
+ * Tile groups of 8 rows: [cols/64][16] fp16 (d of rows 0..7, then m), the
+ * 4-bit codes in the mode 12 nibble interleave, and for mode 14 the 2-bit
+ * high planes.  Row value (rotated) = m + u * d per 64-column block.  The
+ * activations are prepped as for mode 12 (dpuf_prep_had4_packed_slab). */
+
+/* Replaces reference dpuf_kernels.h:280-284 (dpuf_avx2.c:2947-3074). */
+DPUF_EXPORT void dpuf_matmul_qr_had4_asym_tile_range(
+    int32_t M, int32_t rows, int32_t cols, int32_t t_start, int32_t t_end,
+    const int8_t* x_q8, const float* x_blk_scale, const int32_t* x_sum8,
+    const uint8_t* tensor_base, const uint64_t* tile_offsets, float* out);
+
+/* Replaces reference dpuf_kernels.h:286-290 (dpuf_avx2.c:3084-3136). */
+DPUF_EXPORT void dpuf_matmul_qr_had4_asym_f32(
+    int32_t M, int32_t rows, int32_t cols, int32_t n_tiles,
+    const float* x_in, const uint8_t* tensor_base, const uint64_t* tile_offsets,
+    const uint8_t* sign_bits, float* out);
+
+/* Replaces reference dpuf_kernels.h:292-296 (dpuf_avx2.c:3146-3213). */
+DPUF_EXPORT void dpuf_embed_qr_had4_asym_f32(
+    int32_t n_tokens, int32_t cols, const int32_t* token_ids,
+    const uint8_t* tensor_base, const uint64_t* tile_offsets,
+    const uint8_t* sign_bits, float* out);
+
+/* Replaces reference dpuf_kernels.h:298-302 (dpuf_avx2.c:2947-3082). */
+DPUF_EXPORT void dpuf_matmul_qr_had6_tile_range(
+    int32_t M, int32_t rows, int32_t cols, int32_t t_start, int32_t t_end,
+    const int8_t* x_q8, const float* x_blk_scale, const int32_t* x_sum8,
+    const uint8_t* tensor_base, const uint64_t* tile_offsets, float* out);
+
+/* Replaces reference dpuf_kernels.h:304-308 (dpuf_avx2.c:3084-3144). */
+DPUF_EXPORT void dpuf_matmul_qr_had6_f32(
+    int32_t M, int32_t rows, int32_t cols, int32_t n_tiles,
+    const float* x_in, const uint8_t* tensor_base, const uint64_t* tile_offsets,
+    const uint8_t* sign_bits, float* out);
+
+/* Replaces reference dpuf_kernels.h:310-314 (dpuf_avx2.c:3146-3221). */
+DPUF_EXPORT void dpuf_embed_qr_had6_f32(
+    int32_t n_tokens, int32_t cols, const int32_t* token_ids,
+    const uint8_t* tensor_base, const uint64_t* tile_offsets,
+    const uint8_t* sign_bits, float* out);
+
+/* Mode dispatcher for embeddings (modes 12, 13, 14 here; other modes write
+ * nothing).  Replaces reference dpuf_kernels.h:170-176 (dpuf_avx2.c:2044-2067). */
 DPUF_EXPORT void dpuf_embed_qr_any_f32(const DpufWeightDesc* w, int32_t n_tokens,
                                        const int32_t* token_ids, float* out,
                                        float* scratch_f32);
@@ -180,7 +224,8 @@ DPUF_EXPORT void dpuf_embed_qr_any_f32(const DpufWeightDesc* w, int32_t n_tokens
 
 /* Copies *cfg and layers[0..num_layers); everything the descriptors point to
  * is read once and uploaded to HBM.  Returns NULL on bad arguments, a mode
- * other than 12, or allocation failure.  Reads DPUF_SWIGLU_DEADZONE here. */
+ * other than 12, 13, 14, or allocation failure.  Reads DPUF_SWIGLU_DEADZONE
+ * here. */
 DPUF_EXPORT void* dpuf_engine_create(const DpufModelConfig* cfg,
                                      const DpufLayerWeights* layers,
                                      const DpufWeightDesc* w_tok_embd,

@@ -1,5 +1,6 @@
 /*
- * oracle.c -- CPU restatement of the reference DPUF Mode 12 token loop.
+ * oracle.c -- CPU restatement of the reference DPUF token loop: the Mode 12
+ * (Hadamard-4bit packed) path and the asymmetric blk64 Modes 13 / 14.
  *
  * TEST INFRASTRUCTURE ONLY.  Nothing in the product links, loads or calls
  * this file: it is the checker that tests/, __graft_entry__.smoke() and the
@@ -20,6 +21,10 @@
  *     intermediate sizes that are multiples of 64.
  *   - RMSNorm / dot scalar tails (n % 8 != 0) are not restated; all dims are
  *     multiples of 8.
+ *   - The scalar expression of Modes 13 / 14, xm_s = (a * b + c * d) * 0.125f
+ *     (dpuf_avx2.c:2877, 3031), is evaluated unfused, as the reference's
+ *     Linux build (Makefile: gcc -std=c11, whose default is
+ *     -ffp-contract=off) compiles it.
  */
 #include <math.h>
 #include <stdint.h>
@@ -310,6 +315,154 @@ void orc_embed(int32_t n_tokens, int32_t cols, const int32_t* ids,
             }
         }
     }
+}
+
+/* ------------------------------------------------------------------------- */
+/* Modes 13 / 14: asymmetric blk64 4-bit and 6-bit (reference                 */
+/* dpuf_avx2.c:2785-3221)                                                     */
+/* ------------------------------------------------------------------------- */
+
+/* A tile's 8-row group g (rows 8g .. 8g+7) holds, for n_64 = cols/64 blocks of
+ * 64 columns (dpuf_avx2.c:2786-2791, dpuf_format.py:1699-1725):
+ *   dm  [n_64][16] fp16: d of rows 0..7, then m of rows 0..7;
+ *   q4  [n_blk][128] bytes, the mode 12 nibble interleave: byte c*32 + ri*4 + k
+ *       of 32-block b holds row ri, column 32b+8c+k (low nibble) and 32b+8c+4+k
+ *       (high nibble);
+ *   q2  (mode 14 only) [n_blk][64] bytes: bits 2(ri>>1) .. +1 of byte
+ *       c*16 + h*8 + (ri&1)*4 + k are bits 4..5 of row ri, column 32b+8c+4h+k.
+ * Group bytes per 64 columns: 288 (mode 13), 416 (mode 14). */
+static size_t asym_grp_bytes(int is_had6, int32_t n_64) { return (size_t)n_64 * (is_had6 ? 416u : 288u); }
+
+/* Quantised value u of row ri, column j (0..31) of one 32-block. */
+static inline int32_t asym_u(const uint8_t* qp, const uint8_t* h2p, int ri, int j) {
+    const int c = j >> 3, h = (j >> 2) & 1, k = j & 3;
+    const uint8_t by = qp[c * 32 + ri * 4 + k];
+    int32_t u = h ? (by >> 4) : (by & 0x0F);
+    if (h2p) u |= ((h2p[c * 16 + h * 8 + (ri & 1) * 4 + k] >> ((ri >> 1) * 2)) & 3) << 4;
+    return u;
+}
+
+/* Exact integer dot of row ri of one 32-block with int8 activations: the
+ * reference's maddubs / madd sums (dpuf_avx2.c:2802-2846) never saturate or
+ * wrap, since |u q| <= 63 * 127 and at most 8 products share an int16 lane. */
+static inline int32_t asym_block_dot(const uint8_t* qp, const uint8_t* h2p, int ri, const int8_t* xq) {
+    int32_t d = 0;
+    for (int j = 0; j < 32; j++) d += asym_u(qp, h2p, ri, j) * (int32_t)xq[j];
+    return d;
+}
+
+/* Rows of tiles [t0, t1) for M tokens prepped in row layout (as
+ * orc_gemm_tiles).  For each (row, token), over 64-blocks g ascending
+ * (dpuf_avx2.c:3029-3037 for M == 1, 2871-2882 for the slabs, identical):
+ *   fdot = fma(float(D0), xs0, float(D1) * xs1)
+ *   xm_s = ((float)sum8_0 * xs0 + (float)sum8_1 * xs1) * 0.125f   (no fusion)
+ *   acc  = fma(fdot, d, acc);  acc = fma(m, xm_s, acc)
+ * with D0, D1 the dots of 32-blocks 2g, 2g+1.  No block is skipped. */
+void orc_gemm_tiles_asym(int32_t is_had6, int32_t M, int32_t rows, int32_t cols, int32_t t0, int32_t t1,
+                         const int8_t* xq, const float* xs, const int32_t* xsum,
+                         const uint8_t* base, const uint64_t* offs, float* out) {
+    const int32_t n_blk = cols >> 5, n_64 = cols >> 6;
+    const size_t gbytes = asym_grp_bytes(is_had6, n_64);
+    int32_t t;
+#pragma omp parallel for schedule(static) if (t1 - t0 >= 8)
+    for (t = t0; t < t1; t++) {
+        const uint8_t* tp = base + offs[t];
+        const DpufQrTileHdr* th = (const DpufQrTileHdr*)tp;
+        int32_t n_r = th->n_rows;
+        int32_t n_8g = (n_r + 7) >> 3;
+        for (int32_t rg = 0; rg < n_8g; rg++) {
+            int32_t n_8 = (rg * 8 + 8 <= n_r) ? 8 : (n_r - rg * 8);
+            const uint8_t* grp = tp + sizeof(DpufQrTileHdr) + (size_t)rg * gbytes;
+            const uint16_t* dm = (const uint16_t*)grp;
+            const uint8_t* q4 = grp + (size_t)n_64 * 32u;
+            const uint8_t* q2 = is_had6 ? q4 + (size_t)n_64 * 256u : NULL;
+            for (int32_t m = 0; m < M; m++) {
+                const int8_t* xm = xq + (size_t)m * cols;
+                const float* sm = xs + (size_t)m * n_blk;
+                const int32_t* um = xsum + (size_t)m * n_blk;
+                for (int ri = 0; ri < n_8; ri++) {
+                    float acc = 0.0f;
+                    for (int32_t g = 0; g < n_64; g++) {
+                        const int32_t b0 = 2 * g, b1 = b0 + 1;
+                        const int32_t d0 = asym_block_dot(q4 + (size_t)b0 * 128u, q2 ? q2 + (size_t)b0 * 64u : NULL,
+                                                          ri, xm + 32 * b0);
+                        const int32_t d1 = asym_block_dot(q4 + (size_t)b1 * 128u, q2 ? q2 + (size_t)b1 * 64u : NULL,
+                                                          ri, xm + 32 * b1);
+                        const float xs0 = sm[b0], xs1 = sm[b1];
+                        const float fdot = fmaf((float)d0, xs0, (float)d1 * xs1);
+                        const float xm_s = ((float)um[b0] * xs0 + (float)um[b1] * xs1) * 0.125f;
+                        const float wd = orc_h2f(dm[(size_t)g * 16u + ri]);
+                        const float wm = orc_h2f(dm[(size_t)g * 16u + 8u + ri]);
+                        acc = fmaf(fdot, wd, acc);
+                        acc = fmaf(wm, xm_s, acc);
+                    }
+                    out[(size_t)m * rows + (size_t)t * 16 + rg * 8 + ri] = acc;
+                }
+            }
+        }
+    }
+}
+
+/* Standalone fp32 entries (reference had_asym_matmul_f32_impl,
+ * dpuf_avx2.c:3084-3136): the mode 12 prep, then the tiles above. */
+void orc_matmul_asym_f32(int32_t is_had6, int32_t M, int32_t rows, int32_t cols, int32_t n_tiles,
+                         const float* x, const uint8_t* base, const uint64_t* offs,
+                         const uint8_t* sb, float* out) {
+    int32_t n_blk = cols >> 5;
+    int8_t* q = (int8_t*)malloc((size_t)M * cols);
+    float* s = (float*)malloc((size_t)M * n_blk * sizeof(float));
+    int32_t* m = (int32_t*)malloc((size_t)M * n_blk * sizeof(int32_t));
+    for (int32_t i = 0; i < M; i++)
+        orc_prep_row(cols, x + (size_t)i * cols, sb, q + (size_t)i * cols, s + (size_t)i * n_blk, m + (size_t)i * n_blk);
+    orc_gemm_tiles_asym(is_had6, M, rows, cols, 0, n_tiles, q, s, m, base, offs, out);
+    free(q); free(s); free(m);
+}
+
+/* Embedding rows (reference embed_qr_had_asym_impl, dpuf_avx2.c:3154-3207):
+ * value (float)u * d + m (a rounded product, then a rounded sum), FWHT-64
+ * per 64 columns, then the signs. */
+void orc_embed_asym(int32_t is_had6, int32_t n_tokens, int32_t cols, const int32_t* ids,
+                    const uint8_t* base, const uint64_t* offs, const uint8_t* sb, float* out) {
+    const int32_t n_64 = cols >> 6;
+    const size_t gbytes = asym_grp_bytes(is_had6, n_64);
+    for (int32_t i = 0; i < n_tokens; i++) {
+        int32_t r = ids[i];
+        int32_t t = r / 16, lr = r % 16, rg = lr >> 3, ri = lr & 7;
+        const uint8_t* grp = base + offs[t] + sizeof(DpufQrTileHdr) + (size_t)rg * gbytes;
+        const uint16_t* dm = (const uint16_t*)grp;
+        const uint8_t* q4 = grp + (size_t)n_64 * 32u;
+        const uint8_t* q2 = is_had6 ? q4 + (size_t)n_64 * 256u : NULL;
+        float* dst = out + (size_t)i * cols;
+        for (int32_t g = 0; g < n_64; g++) {
+            const float wd = orc_h2f(dm[(size_t)g * 16u + ri]);
+            const float wm = orc_h2f(dm[(size_t)g * 16u + 8u + ri]);
+            for (int sub = 0; sub < 2; sub++) {
+                const int32_t b = 2 * g + sub;
+                const uint8_t* qp = q4 + (size_t)b * 128u;
+                const uint8_t* hp = q2 ? q2 + (size_t)b * 64u : NULL;
+                for (int j = 0; j < 32; j++) {
+                    const float pr = (float)asym_u(qp, hp, ri, j) * wd;
+                    dst[32 * b + j] = pr + wm;
+                }
+            }
+        }
+        for (int32_t c = 0; c < cols; c += 64) orc_fwht64(dst + c);
+        if (sb) {
+            for (int32_t c = 0; c < cols; c++) {
+                if ((sb[c >> 3] >> (c & 7)) & 1u) dst[c] = -dst[c];
+            }
+        }
+    }
+}
+
+/* Embedding of any supported mode (reference dpuf_embed_qr_any_f32,
+ * dpuf_avx2.c:2044-2067). */
+void orc_embed_desc(const DpufWeightDesc* w, int32_t n_tokens, const int32_t* ids, float* out) {
+    if (w->mode == DPUF_MODE_QR_HAD4_PACKED)
+        orc_embed(n_tokens, w->cols, ids, w->tensor_base, w->tile_offsets, w->sign_bits, out);
+    else if (w->mode == DPUF_MODE_QR_HAD4_ASYM || w->mode == DPUF_MODE_QR_HAD6)
+        orc_embed_asym(w->mode == DPUF_MODE_QR_HAD6, n_tokens, w->cols, ids, w->tensor_base, w->tile_offsets,
+                       w->sign_bits, out);
 }
 
 /* ------------------------------------------------------------------------- */
@@ -878,7 +1031,11 @@ static void run_weight(const DpufWeightDesc* w, int32_t M, const float* x, float
     for (int32_t i = 0; i < M; i++)
         orc_prep_row(cols, x + (size_t)i * cols, w->sign_bits, q + (size_t)i * cols,
                      s + (size_t)i * n_blk, m + (size_t)i * n_blk);
-    orc_gemm_tiles(M, w->rows, cols, t0, t1, q, s, m, w->tensor_base, w->tile_offsets, out, M == 1);
+    if (w->mode == DPUF_MODE_QR_HAD4_PACKED)
+        orc_gemm_tiles(M, w->rows, cols, t0, t1, q, s, m, w->tensor_base, w->tile_offsets, out, M == 1);
+    else
+        orc_gemm_tiles_asym(w->mode == DPUF_MODE_QR_HAD6, M, w->rows, cols, t0, t1, q, s, m, w->tensor_base,
+                            w->tile_offsets, out);
 }
 
 int32_t orc_engine_forward(OrcEngine* e, int32_t n_tokens, const int32_t* ids, int32_t pos0,
@@ -913,7 +1070,7 @@ int32_t orc_engine_forward(OrcEngine* e, int32_t n_tokens, const int32_t* ids, i
         if (embeds_in && (!ids || ids[m] < 0))
             memcpy(h + (size_t)m * H, embeds_in + (size_t)m * H, (size_t)H * sizeof(float));
         else
-            orc_embed(1, H, ids + m, e->tok.tensor_base, e->tok.tile_offsets, e->tok.sign_bits, h + (size_t)m * H);
+            orc_embed_desc(&e->tok, 1, ids + m, h + (size_t)m * H);
     }
 
     OrcSlot* sl = &e->slots[e->active];

@@ -1,5 +1,5 @@
 /*
- * oracle.h -- CPU restatement of the reference Mode 12 token loop.
+ * oracle.h -- CPU restatement of the reference DPUF token loop (modes 12, 13, 14).
  * TEST INFRASTRUCTURE ONLY: used by tests/, the smoke check and the CPU
  * baseline of bench.py as the checker; never linked into libdpuf_amd.so.
  */
@@ -33,6 +33,15 @@ void orc_matmul_f32(int32_t M, int32_t rows, int32_t cols, int32_t n_tiles, cons
                     const uint8_t* base, const uint64_t* offs, const uint8_t* sb, float* out);
 void orc_embed(int32_t n_tokens, int32_t cols, const int32_t* ids, const uint8_t* base,
                const uint64_t* offs, const uint8_t* sb, float* out);
+void orc_gemm_tiles_asym(int32_t is_had6, int32_t M, int32_t rows, int32_t cols, int32_t t0, int32_t t1,
+                         const int8_t* xq, const float* xs, const int32_t* xsum,
+                         const uint8_t* base, const uint64_t* offs, float* out);
+void orc_matmul_asym_f32(int32_t is_had6, int32_t M, int32_t rows, int32_t cols, int32_t n_tiles,
+                         const float* x, const uint8_t* base, const uint64_t* offs,
+                         const uint8_t* sb, float* out);
+void orc_embed_asym(int32_t is_had6, int32_t n_tokens, int32_t cols, const int32_t* ids,
+                    const uint8_t* base, const uint64_t* offs, const uint8_t* sb, float* out);
+void orc_embed_desc(const DpufWeightDesc* w, int32_t n_tokens, const int32_t* ids, float* out);
 void orc_add_rmsnorm(int32_t n, float* x, const float* res, const float* w, float eps, float* out);
 void orc_rope_tables(const DpufModelConfig* cfg, float* cos_tab, float* sin_tab);
 void orc_rope_apply(int32_t hd, float* v, const float* c, const float* s);

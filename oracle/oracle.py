@@ -41,6 +41,10 @@ def load():
     _sig(lib, "orc_gemm_tiles", None, [I32, I32, I32, I32, I32, P, P, P, P, P, P, C.c_int])
     _sig(lib, "orc_matmul_f32", None, [I32, I32, I32, I32, P, P, P, P, P])
     _sig(lib, "orc_embed", None, [I32, I32, P, P, P, P, P])
+    _sig(lib, "orc_gemm_tiles_asym", None, [I32, I32, I32, I32, I32, I32, P, P, P, P, P, P])
+    _sig(lib, "orc_matmul_asym_f32", None, [I32, I32, I32, I32, I32, P, P, P, P, P])
+    _sig(lib, "orc_embed_asym", None, [I32, I32, I32, P, P, P, P, P])
+    _sig(lib, "orc_embed_desc", None, [C.POINTER(DpufWeightDesc), I32, P, P])
     _sig(lib, "orc_add_rmsnorm", None, [I32, P, P, P, C.c_float, P])
     _sig(lib, "orc_rope_tables", None, [C.POINTER(DpufModelConfig), P, P])
     _sig(lib, "orc_rope_apply", None, [I32, P, P, P])

@@ -3,7 +3,8 @@ oracle's engine composition (oracle/oracle.c orc_engine_forward).
 
 Test infrastructure only.  It shares no code with the oracle: every matrix is
 read back row by row through the embedding path (row r of a Mode 12 matrix is
-sign * FWHT64((u - 8) * ws), the dense weight the packed bytes stand for), and
+sign * FWHT64((u - 8) * ws), of a Mode 13 / 14 matrix sign * FWHT64(m + u d):
+the dense weight the packed bytes stand for), and
 the block is the textbook Qwen3 decoder layer:
 
     h_0 = E[ids] (or the caller's embedding rows)
@@ -31,10 +32,10 @@ from dpuf_amd import model as M
 
 
 def dense(orc, d):
-    """Dense [rows, cols] float64 weight of a Mode 12 descriptor."""
+    """Dense [rows, cols] float64 weight of a Mode 12, 13 or 14 descriptor."""
     ids = np.arange(d.rows, dtype=np.int32)
     out = np.zeros((d.rows, d.cols), np.float32)
-    orc.orc_embed(d.rows, d.cols, M.ptr(ids), d.tensor_base, d.tile_offsets, d.sign_bits, M.ptr(out))
+    orc.orc_embed_desc(C.byref(d), d.rows, M.ptr(ids), M.ptr(out))
     return out.astype(np.float64)
 
 

@@ -73,8 +73,8 @@ class OrcRun:
         self.orc.orc_engine_destroy(self.h)
 
 
-def _run_both(orc, shape, keep, mut_list, steps=3, prompt=9, seed=5):
-    m = M.Model.build(shape, max_seq_len=64, seed=seed)
+def _run_both(orc, shape, keep, mut_list, steps=3, prompt=9, seed=5, plan=0):
+    m = M.Model.build(shape, max_seq_len=64, seed=seed, weight_plan=plan)
     randomise_norms(m, seed + 1)
     f = F64Model(orc, m)
     o = OrcRun(orc, m)
@@ -101,6 +101,20 @@ def _run_both(orc, shape, keep, mut_list, steps=3, prompt=9, seed=5):
             e = max(e, rel(lo, lf), max(rel(capo[l], capf[l]) for l in range(len(capf))))
         worst[mut] = e
     return worst
+
+
+def test_oracle_engine_hybrid_matches_float64(orc, monkeypatch):
+    """The same pinning for the had4p-hybrid plan (Modes 13 and 14 per
+    pack_dpuf.py:249-266, separate signs for every matrix), group of 4, with
+    the down projection pruned to 12 of 16 tiles."""
+    monkeypatch.setenv("DPUF_PREFILL_KEEP_TILES", "12")
+    monkeypatch.setenv("DPUF_GEN_KEEP_TILES", "12")
+    monkeypatch.delenv("DPUF_SWIGLU_DEADZONE", raising=False)
+    w = _run_both(orc, dict(TINY, num_q_heads=8, num_kv_heads=2, tie_word_embeddings=0), 12, MUTATIONS, plan=1)
+    print({k[0] if k else "exact": round(v, 4) for k, v in w.items()})
+    assert w[()] < BOUND, w[()]
+    for mut in MUTATIONS:
+        assert w[(mut,)] > CAUGHT, (mut, w[(mut,)])
 
 
 @pytest.mark.parametrize("heads", [(4, 2), (8, 2), (6, 2)])
