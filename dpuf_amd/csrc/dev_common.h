@@ -1,0 +1,252 @@
+// dev_common.h -- gfx950 device helpers of the DPUF engine's HIP code: fp16
+// scales, the reference's hsum trees and exp polynomial, FWHT-64 in registers
+// and over lane quads, the activation prep (int8 quantisation per 32-block)
+// and the exact u4 x i8 row-block dot.
+#ifndef DPUF_DEV_COMMON_H
+#define DPUF_DEV_COMMON_H
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "hip_layer.h"
+
+#define DEV __device__ __forceinline__
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------------------
+// Scalar helpers
+// ---------------------------------------------------------------------------
+DEV float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+
+// 8-lane sum in the order of the reference's eng_hsum256_ps
+// (dpuf_engine.c:37-46): ((a0+a4)+(a1+a5)) + ((a2+a6)+(a3+a7)).
+DEV float hsum8(const float* a) {
+    float s0 = a[0] + a[4], s1 = a[1] + a[5], s2 = a[2] + a[6], s3 = a[3] + a[7];
+    return (s0 + s1) + (s2 + s3);
+}
+
+// 8-lane sum as hsum4_256_ps's hadd tree leaves it (dpuf_engine.c:318-323):
+// ((a0+a1)+(a2+a3)) + ((a4+a5)+(a6+a7)).
+DEV float hsum8_hadd(const float* a) {
+    float lo = (a[0] + a[1]) + (a[2] + a[3]);
+    float hi = (a[4] + a[5]) + (a[6] + a[7]);
+    return lo + hi;
+}
+
+// The reference's own 8-wide exp polynomial (dpuf_engine.c:297-316), per lane.
+DEV float exp_poly(float x) {
+    x = fmaxf(-45.0f, fminf(x, 45.0f));
+    float fx = rintf(x * 1.44269504088896341f);
+    float r = fmaf(-fx, 0.693359375f, x);
+    r = fmaf(-fx, -2.12194440e-4f, r);
+    float p = 1.9875691500e-4f;
+    p = fmaf(p, r, 1.3981999507e-3f);
+    p = fmaf(p, r, 8.3334519073e-3f);
+    p = fmaf(p, r, 4.1665795894e-2f);
+    p = fmaf(p, r, 1.6666665459e-1f);
+    p = fmaf(p, r, 5.0000001201e-1f);
+    float r2 = r * r;
+    float er = fmaf(p, r2, r) + 1.0f;
+    int n = (int)fx;
+    return er * __int_as_float((n + 127) << 23);
+}
+
+
+// In-register FWHT-64: radix-2 butterflies with strides 1..32, then x 1/8
+// (reference fwht64_block_f32, dpuf_avx2.c:724-772).
+DEV void fwht64(float* y) {
+#pragma unroll
+    for (int h = 1; h < 64; h <<= 1) {
+#pragma unroll
+        for (int i = 0; i < 64; i += 2 * h) {
+#pragma unroll
+            for (int j = i; j < i + h; j++) {
+                float a = y[j], b = y[j + h];
+                y[j] = a + b;
+                y[j + h] = a - b;
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 64; i++) y[i] = y[i] * 0.125f;
+}
+
+// DPP quad permutations: xor 1 = (1,0,3,2), xor 2 = (2,3,0,1).
+DEV int dpp_xor1(int v) { return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false); }
+DEV int dpp_xor2(int v) { return __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false); }
+
+
+// ---------------------------------------------------------------------------
+// Activation prep spread over lane quads.
+//
+// A 64-column block is owned by 4 consecutive lanes (a quad); quarter qp
+// holds columns 16*qp .. 16*qp+15 in registers.  FWHT stages with strides
+// 1, 2, 4, 8 run inside the lane, stride 16 pairs lanes qp and qp^1, stride
+// 32 pairs qp and qp^2 (DPP quad permutes).  Every butterfly is the same
+// single a+b / a-b as in the reference (dpuf_avx2.c:724-772) and the stages
+// keep its ascending order, so results are bit-identical.  Lanes (0,1) and
+// (2,3) of a quad then quantise one 32-block each
+// (dpuf_prep_had4_packed_slab, dpuf_avx2.c:2400-2446).
+// ---------------------------------------------------------------------------
+struct PrepSet {
+    const uint8_t* sign[3];
+    DpufPrep p[3];
+    int n;
+};
+
+DEV float fxor1(float v) { return __int_as_float(dpp_xor1(__float_as_int(v))); }
+DEV float fxor2(float v) { return __int_as_float(dpp_xor2(__float_as_int(v))); }
+
+// Sign bits of the lane's 16 columns of 64-block blk (bit c%8 of byte c/8
+// set = negate column c).
+DEV uint32_t quad_sign_bits(const uint8_t* sign, int blk, int qp) {
+    return sign ? *(const uint16_t*)(sign + 8 * blk + 2 * qp) : 0u;
+}
+
+DEV void apply_sign_bits(float* v, uint32_t sb) {
+#pragma unroll
+    for (int k = 0; k < 16; k++)
+        if ((sb >> k) & 1u) v[k] = -v[k];
+}
+
+DEV void quad_fwht64(float* v, int qp) {
+#pragma unroll
+    for (int h = 1; h < 16; h <<= 1) {
+#pragma unroll
+        for (int i = 0; i < 16; i += 2 * h) {
+#pragma unroll
+            for (int j = i; j < i + h; j++) {
+                const float a = v[j], b = v[j + h];
+                v[j] = a + b;
+                v[j + h] = a - b;
+            }
+        }
+    }
+    const bool lo1 = (qp & 1) == 0, lo2 = (qp & 2) == 0;
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+        const float p = fxor1(v[j]);
+        v[j] = lo1 ? v[j] + p : p - v[j];
+    }
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+        const float p = fxor2(v[j]);
+        v[j] = lo2 ? v[j] + p : p - v[j];
+    }
+#pragma unroll
+    for (int j = 0; j < 16; j++) v[j] = v[j] * 0.125f;
+}
+
+// Quantises the lane's 16 FWHT'd values (half of 32-block 2*blk + qp/2) and
+// stores the int8 values, and from the even lane the block scale and 8*sum(q).
+typedef _Float16 gm_h2 __attribute__((ext_vector_type(2)));
+
+// Two fp16 values from bytes b0, b1 of x and 0x64: 1024 + byte each.
+DEV uint32_t gm_pair(uint32_t x, uint32_t sel) { return __builtin_amdgcn_perm(0x64646464u, x, sel); }
+
+DEV uint32_t gm_sub(uint32_t v, _Float16 c) {
+    gm_h2 h = __builtin_bit_cast(gm_h2, v);
+    h = h - (gm_h2){c, c};
+    return __builtin_bit_cast(uint32_t, h);
+}
+
+// Four int8 (one word) -> four f16 in two words (exact).
+DEV void i8x4_to_h(uint32_t x, uint32_t& a, uint32_t& b) {
+    const uint32_t u = x ^ 0x80808080u;  // q + 128 per byte
+    a = gm_sub(gm_pair(u, 0x04010400u), (_Float16)1152.0f);
+    b = gm_sub(gm_pair(u, 0x04030402u), (_Float16)1152.0f);
+}
+
+DEV void quad_quant_store(const float* v, int qp, int blk, int8_t* q, float* s, int32_t* m, uint16_t* h) {
+    float amax = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+        const float a = fabsf(v[k]);
+        amax = a > amax ? a : amax;
+    }
+    const float other = fxor1(amax);
+    amax = other > amax ? other : amax;
+    uint32_t w[4] = {0u, 0u, 0u, 0u};
+    int32_t sum = 0;
+    float d = 0.0f;
+    if (!(amax <= 1e-4f)) {
+        d = amax / 127.0f;
+        const float inv = (amax > 1e-12f) ? (127.0f / amax) : 0.0f;
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const float x = v[4 * g + k] * inv;
+                int32_t qi;
+                if (!(x > -2147483648.0f && x < 2147483648.0f)) qi = -127;  // cvtps -> INT_MIN -> -127
+                else qi = (int32_t)rintf(x);
+                qi = qi > 127 ? 127 : qi;
+                qi = qi < -127 ? -127 : qi;
+                sum += qi;
+                w[g] |= ((uint32_t)(qi & 0xFF)) << (8 * k);
+            }
+        }
+    }
+    sum += dpp_xor1(sum);
+    *(uint4*)(q + 64 * blk + 16 * qp) = make_uint4(w[0], w[1], w[2], w[3]);
+    if (h) {  // the same 16 values as fp16 (exact: |q| <= 127)
+        uint32_t hw[8];
+#pragma unroll
+        for (int g = 0; g < 4; g++) i8x4_to_h(w[g], hw[2 * g], hw[2 * g + 1]);
+        *(uint4*)(h + 64 * blk + 16 * qp) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+        *(uint4*)(h + 64 * blk + 16 * qp + 8) = make_uint4(hw[4], hw[5], hw[6], hw[7]);
+    }
+    if ((qp & 1) == 0) {
+        s[2 * blk + (qp >> 1)] = d;
+        m[2 * blk + (qp >> 1)] = sum * 8;
+    }
+}
+
+DEV void load16(const float* p, float* v) {
+    const float4* p4 = (const float4*)p;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float4 t = p4[i];
+        v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
+    }
+}
+
+DEV void store16(float* p, const float* v) {
+    float4* p4 = (float4*)p;
+#pragma unroll
+    for (int i = 0; i < 4; i++) p4[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+}
+
+
+// Exact integer dot of one row block: 32 nibbles u in [0, 15] against 32 int8
+// activations (x as 8 words, word 2c = columns 8c..8c+3, word 2c+1 = 8c+4..8c+7).
+// Equals the reference's maddubs/madd sum (dpuf_avx2.c:2623-2632), whose int16
+// partials cannot overflow (|sum| <= 30480).
+DEV int row_block_dot(uint4 w, int4 xa, int4 xb) {
+    const uint32_t m = 0x0F0F0F0Fu;
+    int d = __builtin_amdgcn_sdot4((int)(w.x & m), xa.x, 0, false);
+    d = __builtin_amdgcn_sdot4((int)((w.x >> 4) & m), xa.y, d, false);
+    d = __builtin_amdgcn_sdot4((int)(w.y & m), xa.z, d, false);
+    d = __builtin_amdgcn_sdot4((int)((w.y >> 4) & m), xa.w, d, false);
+    d = __builtin_amdgcn_sdot4((int)(w.z & m), xb.x, d, false);
+    d = __builtin_amdgcn_sdot4((int)((w.z >> 4) & m), xb.y, d, false);
+    d = __builtin_amdgcn_sdot4((int)(w.w & m), xb.z, d, false);
+    d = __builtin_amdgcn_sdot4((int)((w.w >> 4) & m), xb.w, d, false);
+    return d;
+}
+
+
+// Lane i + 8 of a 16-lane row for lane i and the reverse (DPP row_ror:8).
+DEV int dpp_ror8(int v) { return __builtin_amdgcn_update_dpp(0, v, 0x128, 0xF, 0xF, false); }
+
+DEV uint4 nt_load16(const uint8_t* p) {
+    const u32x4 v = __builtin_nontemporal_load((const u32x4*)p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+
+// Records the first HIP error of the current API call (kernels.hip).
+void dpuf_note(hipError_t e, const char* what);
+
+#endif

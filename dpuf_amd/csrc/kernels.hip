@@ -19,10 +19,8 @@
 #include <mutex>
 
 #include "hip_layer.h"
+#include "dev_common.h"
 
-#define DEV __device__ __forceinline__
-
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 // ---------------------------------------------------------------------------
 // Error bookkeeping
@@ -42,43 +40,7 @@ static void note(hipError_t e, const char* what) {
 #define CK(x) note((x), #x)
 #define LAUNCHED(name) note(hipGetLastError(), name)
 
-// ---------------------------------------------------------------------------
-// Scalar helpers
-// ---------------------------------------------------------------------------
-DEV float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
-
-// 8-lane sum in the order of the reference's eng_hsum256_ps
-// (dpuf_engine.c:37-46): ((a0+a4)+(a1+a5)) + ((a2+a6)+(a3+a7)).
-DEV float hsum8(const float* a) {
-    float s0 = a[0] + a[4], s1 = a[1] + a[5], s2 = a[2] + a[6], s3 = a[3] + a[7];
-    return (s0 + s1) + (s2 + s3);
-}
-
-// 8-lane sum as hsum4_256_ps's hadd tree leaves it (dpuf_engine.c:318-323):
-// ((a0+a1)+(a2+a3)) + ((a4+a5)+(a6+a7)).
-DEV float hsum8_hadd(const float* a) {
-    float lo = (a[0] + a[1]) + (a[2] + a[3]);
-    float hi = (a[4] + a[5]) + (a[6] + a[7]);
-    return lo + hi;
-}
-
-// The reference's own 8-wide exp polynomial (dpuf_engine.c:297-316), per lane.
-DEV float exp_poly(float x) {
-    x = fmaxf(-45.0f, fminf(x, 45.0f));
-    float fx = rintf(x * 1.44269504088896341f);
-    float r = fmaf(-fx, 0.693359375f, x);
-    r = fmaf(-fx, -2.12194440e-4f, r);
-    float p = 1.9875691500e-4f;
-    p = fmaf(p, r, 1.3981999507e-3f);
-    p = fmaf(p, r, 8.3334519073e-3f);
-    p = fmaf(p, r, 4.1665795894e-2f);
-    p = fmaf(p, r, 1.6666665459e-1f);
-    p = fmaf(p, r, 5.0000001201e-1f);
-    float r2 = r * r;
-    float er = fmaf(p, r2, r) + 1.0f;
-    int n = (int)fx;
-    return er * __int_as_float((n + 127) << 23);
-}
+void dpuf_note(hipError_t e, const char* what) { note(e, what); }
 
 // exp for x <= 0 with the results of the host C library's expf, which the
 // reference calls on the scalar tail of its softmax (dpuf_engine.c:423-426).
@@ -120,29 +82,6 @@ DEV float expf_libc(float x) {
     y = y * sc;
     return (float)y;
 }
-
-// In-register FWHT-64: radix-2 butterflies with strides 1..32, then x 1/8
-// (reference fwht64_block_f32, dpuf_avx2.c:724-772).
-DEV void fwht64(float* y) {
-#pragma unroll
-    for (int h = 1; h < 64; h <<= 1) {
-#pragma unroll
-        for (int i = 0; i < 64; i += 2 * h) {
-#pragma unroll
-            for (int j = i; j < i + h; j++) {
-                float a = y[j], b = y[j + h];
-                y[j] = a + b;
-                y[j + h] = a - b;
-            }
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < 64; i++) y[i] = y[i] * 0.125f;
-}
-
-// DPP quad permutations: xor 1 = (1,0,3,2), xor 2 = (2,3,0,1).
-DEV int dpp_xor1(int v) { return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false); }
-DEV int dpp_xor2(int v) { return __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false); }
 
 // ---------------------------------------------------------------------------
 // Embedding (reference dpuf_embed_qr_hadamard4_packed_f32, dpuf_avx2.c:2738-2783,
@@ -224,147 +163,6 @@ __global__ void k_embed(DpufDevW w, const int32_t* __restrict__ ids, const float
 }
 
 // ---------------------------------------------------------------------------
-// Activation prep spread over lane quads.
-//
-// A 64-column block is owned by 4 consecutive lanes (a quad); quarter qp
-// holds columns 16*qp .. 16*qp+15 in registers.  FWHT stages with strides
-// 1, 2, 4, 8 run inside the lane, stride 16 pairs lanes qp and qp^1, stride
-// 32 pairs qp and qp^2 (DPP quad permutes).  Every butterfly is the same
-// single a+b / a-b as in the reference (dpuf_avx2.c:724-772) and the stages
-// keep its ascending order, so results are bit-identical.  Lanes (0,1) and
-// (2,3) of a quad then quantise one 32-block each
-// (dpuf_prep_had4_packed_slab, dpuf_avx2.c:2400-2446).
-// ---------------------------------------------------------------------------
-struct PrepSet {
-    const uint8_t* sign[3];
-    DpufPrep p[3];
-    int n;
-};
-
-DEV float fxor1(float v) { return __int_as_float(dpp_xor1(__float_as_int(v))); }
-DEV float fxor2(float v) { return __int_as_float(dpp_xor2(__float_as_int(v))); }
-
-// Sign bits of the lane's 16 columns of 64-block blk (bit c%8 of byte c/8
-// set = negate column c).
-DEV uint32_t quad_sign_bits(const uint8_t* sign, int blk, int qp) {
-    return sign ? *(const uint16_t*)(sign + 8 * blk + 2 * qp) : 0u;
-}
-
-DEV void apply_sign_bits(float* v, uint32_t sb) {
-#pragma unroll
-    for (int k = 0; k < 16; k++)
-        if ((sb >> k) & 1u) v[k] = -v[k];
-}
-
-DEV void quad_fwht64(float* v, int qp) {
-#pragma unroll
-    for (int h = 1; h < 16; h <<= 1) {
-#pragma unroll
-        for (int i = 0; i < 16; i += 2 * h) {
-#pragma unroll
-            for (int j = i; j < i + h; j++) {
-                const float a = v[j], b = v[j + h];
-                v[j] = a + b;
-                v[j + h] = a - b;
-            }
-        }
-    }
-    const bool lo1 = (qp & 1) == 0, lo2 = (qp & 2) == 0;
-#pragma unroll
-    for (int j = 0; j < 16; j++) {
-        const float p = fxor1(v[j]);
-        v[j] = lo1 ? v[j] + p : p - v[j];
-    }
-#pragma unroll
-    for (int j = 0; j < 16; j++) {
-        const float p = fxor2(v[j]);
-        v[j] = lo2 ? v[j] + p : p - v[j];
-    }
-#pragma unroll
-    for (int j = 0; j < 16; j++) v[j] = v[j] * 0.125f;
-}
-
-// Quantises the lane's 16 FWHT'd values (half of 32-block 2*blk + qp/2) and
-// stores the int8 values, and from the even lane the block scale and 8*sum(q).
-typedef _Float16 gm_h2 __attribute__((ext_vector_type(2)));
-
-// Two fp16 values from bytes b0, b1 of x and 0x64: 1024 + byte each.
-DEV uint32_t gm_pair(uint32_t x, uint32_t sel) { return __builtin_amdgcn_perm(0x64646464u, x, sel); }
-
-DEV uint32_t gm_sub(uint32_t v, _Float16 c) {
-    gm_h2 h = __builtin_bit_cast(gm_h2, v);
-    h = h - (gm_h2){c, c};
-    return __builtin_bit_cast(uint32_t, h);
-}
-
-// Four int8 (one word) -> four f16 in two words (exact).
-DEV void i8x4_to_h(uint32_t x, uint32_t& a, uint32_t& b) {
-    const uint32_t u = x ^ 0x80808080u;  // q + 128 per byte
-    a = gm_sub(gm_pair(u, 0x04010400u), (_Float16)1152.0f);
-    b = gm_sub(gm_pair(u, 0x04030402u), (_Float16)1152.0f);
-}
-
-DEV void quad_quant_store(const float* v, int qp, int blk, int8_t* q, float* s, int32_t* m, uint16_t* h) {
-    float amax = 0.0f;
-#pragma unroll
-    for (int k = 0; k < 16; k++) {
-        const float a = fabsf(v[k]);
-        amax = a > amax ? a : amax;
-    }
-    const float other = fxor1(amax);
-    amax = other > amax ? other : amax;
-    uint32_t w[4] = {0u, 0u, 0u, 0u};
-    int32_t sum = 0;
-    float d = 0.0f;
-    if (!(amax <= 1e-4f)) {
-        d = amax / 127.0f;
-        const float inv = (amax > 1e-12f) ? (127.0f / amax) : 0.0f;
-#pragma unroll
-        for (int g = 0; g < 4; g++) {
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                const float x = v[4 * g + k] * inv;
-                int32_t qi;
-                if (!(x > -2147483648.0f && x < 2147483648.0f)) qi = -127;  // cvtps -> INT_MIN -> -127
-                else qi = (int32_t)rintf(x);
-                qi = qi > 127 ? 127 : qi;
-                qi = qi < -127 ? -127 : qi;
-                sum += qi;
-                w[g] |= ((uint32_t)(qi & 0xFF)) << (8 * k);
-            }
-        }
-    }
-    sum += dpp_xor1(sum);
-    *(uint4*)(q + 64 * blk + 16 * qp) = make_uint4(w[0], w[1], w[2], w[3]);
-    if (h) {  // the same 16 values as fp16 (exact: |q| <= 127)
-        uint32_t hw[8];
-#pragma unroll
-        for (int g = 0; g < 4; g++) i8x4_to_h(w[g], hw[2 * g], hw[2 * g + 1]);
-        *(uint4*)(h + 64 * blk + 16 * qp) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
-        *(uint4*)(h + 64 * blk + 16 * qp + 8) = make_uint4(hw[4], hw[5], hw[6], hw[7]);
-    }
-    if ((qp & 1) == 0) {
-        s[2 * blk + (qp >> 1)] = d;
-        m[2 * blk + (qp >> 1)] = sum * 8;
-    }
-}
-
-DEV void load16(const float* p, float* v) {
-    const float4* p4 = (const float4*)p;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const float4 t = p4[i];
-        v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
-    }
-}
-
-DEV void store16(float* p, const float* v) {
-    float4* p4 = (float4*)p;
-#pragma unroll
-    for (int i = 0; i < 4; i++) p4[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
-}
-
-// ---------------------------------------------------------------------------
 // Residual add + RMSNorm + prep for up to three sign vectors (reference
 // add_and_rms_norm_f32, dpuf_engine.c:243-272, then the prep above).
 // grid: M rows; block: H/16 threads, thread t owning columns 16t..16t+15.
@@ -372,6 +170,7 @@ DEV void store16(float* p, const float* v) {
 // elements j, j+8, j+16, ... in order) and its hsum tree; a transposed LDS
 // copy gives each of the 8 chain lanes its elements contiguously.
 // ---------------------------------------------------------------------------
+template <int SEG>
 __global__ __launch_bounds__(1024) void k_resnorm_prep(int H, float* __restrict__ h, const float* __restrict__ res,
                                                        const float* __restrict__ w, float eps, PrepSet ps,
                                                        float* __restrict__ xn_out) {
@@ -395,7 +194,39 @@ __global__ __launch_bounds__(1024) void k_resnorm_prep(int H, float* __restrict_
 #pragma unroll
     for (int k = 0; k < 8; k++) *(float2*)(tr + k * L + 2 * t) = make_float2(v[k], v[k + 8]);
     __syncthreads();
-    if (t < 8) {
+    if (SEG > 0) {
+        // H = 64 SEG.  Chain j (lanes 8j .. 8j+7 of wave 0) in 8 consecutive
+        // segments of SEG elements held in registers: lane 8j + s runs
+        // segment s, then hands the accumulator to lane 8j + s + 1 (DPP
+        // row_shr:1, inside a 16-lane row).  A register-fed dependent fma
+        // costs about 1.9 ns on gfx950 against 4-5 ns fed from LDS; the order
+        // is the reference's.
+        if (t < 64) {
+            const int j = t >> 3, s = t & 7;
+            const float4* rowp = (const float4*)(tr + j * L + s * SEG);
+            float x[SEG > 0 ? SEG : 1];
+#pragma unroll
+            for (int i = 0; i < SEG / 4; i++) {
+                const float4 e = rowp[i];
+                x[4 * i] = e.x;
+                x[4 * i + 1] = e.y;
+                x[4 * i + 2] = e.z;
+                x[4 * i + 3] = e.w;
+            }
+            float a = 0.0f;
+#pragma unroll
+            for (int ss = 0; ss < 8; ss++) {
+                if (s == ss) {
+#pragma unroll
+                    for (int i = 0; i < SEG; i++) a = fmaf(x[i], x[i], a);
+                }
+                const float prev = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x111, 0xF, 0xF,
+                                                                              false));
+                if (s == ss + 1) a = prev;
+            }
+            if (s == 7) part[j] = a;
+        }
+    } else if (t < 8) {
         const float4* row = (const float4*)(tr + t * L);
         const int n4 = H >> 5;
         float a = 0.0f;
@@ -528,23 +359,6 @@ __global__ void k_relayout(const uint8_t* __restrict__ src, const uint64_t* __re
     }
 }
 
-// Exact integer dot of one row block: 32 nibbles u in [0, 15] against 32 int8
-// activations (x as 8 words, word 2c = columns 8c..8c+3, word 2c+1 = 8c+4..8c+7).
-// Equals the reference's maddubs/madd sum (dpuf_avx2.c:2623-2632), whose int16
-// partials cannot overflow (|sum| <= 30480).
-DEV int row_block_dot(uint4 w, int4 xa, int4 xb) {
-    const uint32_t m = 0x0F0F0F0Fu;
-    int d = __builtin_amdgcn_sdot4((int)(w.x & m), xa.x, 0, false);
-    d = __builtin_amdgcn_sdot4((int)((w.x >> 4) & m), xa.y, d, false);
-    d = __builtin_amdgcn_sdot4((int)(w.y & m), xa.z, d, false);
-    d = __builtin_amdgcn_sdot4((int)((w.y >> 4) & m), xa.w, d, false);
-    d = __builtin_amdgcn_sdot4((int)(w.z & m), xb.x, d, false);
-    d = __builtin_amdgcn_sdot4((int)((w.z >> 4) & m), xb.y, d, false);
-    d = __builtin_amdgcn_sdot4((int)(w.w & m), xb.z, d, false);
-    d = __builtin_amdgcn_sdot4((int)((w.w >> 4) & m), xb.w, d, false);
-    return d;
-}
-
 // The same for a mode 14 row block: bits 4..5 of each value come from the
 // row's two words of high bits (word c >> 1, bits (c & 1) * 4 + {0,1} of byte
 // k for column 8c+k, + {2,3} for 8c+4+k).  u <= 63, so the sdot4 products are
@@ -563,14 +377,6 @@ DEV int row_block_dot6(uint4 w, uint2 hw, int4 xa, int4 xb) {
         d = __builtin_amdgcn_sdot4((int)hi, xw[2 * c + 1], d, false);
     }
     return d;
-}
-
-// Lane i + 8 of a 16-lane row for lane i and the reverse (DPP row_ror:8).
-DEV int dpp_ror8(int v) { return __builtin_amdgcn_update_dpp(0, v, 0x128, 0xF, 0xF, false); }
-
-DEV uint4 nt_load16(const uint8_t* p) {
-    const u32x4 v = __builtin_nontemporal_load((const u32x4*)p);
-    return make_uint4(v.x, v.y, v.z, v.w);
 }
 
 // Per-row fp32 chain acc = fma(float(D - sum8), ws * xs, acc) over blocks in
@@ -2290,6 +2096,242 @@ __global__ __launch_bounds__(AP_NT) void k_attn_pv(const float* __restrict__ S, 
 }
 
 // ---------------------------------------------------------------------------
+// One-token decode over long contexts: the softmax once per score row
+// (k_attn_smx), then P.V spread over the chip (k_attn_pvw).
+//
+// k_attn_pv computes the softmax of its rows in every dim-chunk workgroup and
+// runs each output's chain a = fma(p[t], v[t], a) over all keys from LDS; at
+// 4096 keys its 128 workgroups spend ~39 us per layer.  Here a row's softmax
+// is computed once, in the reference's order (max; exp polynomial on the
+// 8-aligned keys, libm expf on the tail; eight sum lanes over t = j mod 8 and
+// their eng_hsum256 tree, then the tail in order; 1 / (sum + 1e-12); p = e *
+// inv, dpuf_engine.c:371-468), and written back in place.  The P.V chains,
+// one per (head, dim) and in key order as before, then run on one wave per
+// (kv head, DW dims): 256 workgroups at head dim 128 and DW 4, each streaming
+// its 16-byte slice of every V row and its heads' probabilities through an
+// LDS ring by direct-to-LDS loads several chunks ahead, so a chain step waits
+// for neither memory nor another wave.
+// ---------------------------------------------------------------------------
+
+// Softmax of one score row of a one-token decode step, in place: row r =
+// blockIdx.x of S (stride max_seq), length pos + 1 <= 64 SEG, 256 threads.
+// The row is read once, into registers: exps of the 8-aligned part go to LDS as [8][8 SEG] (lane j's
+// elements t = j mod 8 in order, zero past the row: adding +0.0 leaves the
+// non-negative sums exact), the tail's (< 8) to a small array.  Wave 0 runs
+// the eight sum chains register-fed, chain j on lanes 8j .. 8j+7 in segments
+// of SEG (as k_resnorm_prep), then the eng_hsum256 tree and the tail in
+// order; the row is normalised from LDS and written once.
+template <int SEG>
+__global__ __launch_bounds__(256) void k_attn_smx(float* __restrict__ S, const int32_t* __restrict__ pos0p,
+                                                  int max_seq) {
+    constexpr int LDT = 8 * SEG + 4;  // row stride of the transposed copy
+    __shared__ __align__(16) float tr[8][LDT];
+    __shared__ float tail[8];
+    __shared__ float red[4];
+    __shared__ float part[8];
+    float* row = S + (size_t)blockIdx.x * max_seq;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int L = *pos0p + 1, n8 = L & ~7;
+    // zero the positions past the row that the chains read
+    for (int i = tid; i < 8 * LDT; i += 256) (&tr[0][0])[i] = 0.0f;
+    // the row in registers, all loads in flight at once (keys t = tid +
+    // 256 k, k < SEG / 4, cover the 64 SEG keys of the largest row)
+    constexpr int KR = SEG / 4;
+    float xr[KR];
+#pragma unroll
+    for (int k = 0; k < KR; k++) xr[k] = row[min(tid + 256 * k, L - 1)];
+    float mx = -1e30f;
+#pragma unroll
+    for (int k = 0; k < KR; k++)
+        if (tid + 256 * k < L) mx = fmaxf(mx, xr[k]);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    if (lane == 0) red[wv] = mx;
+    __syncthreads();
+    const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+#pragma unroll
+    for (int k = 0; k < KR; k++) {
+        const int t = tid + 256 * k;
+        if (t < n8) tr[t & 7][t >> 3] = exp_poly(xr[k] - M);
+        else if (t < L) tail[t - n8] = expf_libc(xr[k] - M);
+    }
+    __syncthreads();
+    if (tid < 64) {
+        const int j = tid >> 3, sg = tid & 7;
+        float x[SEG];
+#pragma unroll
+        for (int i = 0; i < SEG / 4; i++) {
+            const float4 e = *(const float4*)&tr[j][sg * SEG + 4 * i];
+            x[4 * i] = e.x;
+            x[4 * i + 1] = e.y;
+            x[4 * i + 2] = e.z;
+            x[4 * i + 3] = e.w;
+        }
+        float a = 0.0f;
+#pragma unroll
+        for (int ss = 0; ss < 8; ss++) {
+            if (sg == ss) {
+#pragma unroll
+                for (int i = 0; i < SEG; i++) a = a + x[i];
+            }
+            const float prev = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x111, 0xF, 0xF,
+                                                                          false));
+            if (sg == ss + 1) a = prev;
+        }
+        if (sg == 7) part[j] = a;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        float sp = hsum8(part);
+        for (int t = n8; t < L; t++) sp += tail[t - n8];  // the tail keys in order
+        red[0] = 1.0f / (sp + 1e-12f);
+    }
+    __syncthreads();
+    const float inv = red[0];
+#pragma unroll
+    for (int k = 0; k < KR; k++) {
+        const int t = tid + 256 * k;
+        if (t < L) row[t] = (t < n8 ? tr[t & 7][t >> 3] : tail[t - n8]) * inv;
+    }
+}
+
+#define PVW_CK 256  // keys per chunk
+
+#define PVW_LD (PVW_CK + 4)  // LDS row stride of a chunk (rows on distinct banks)
+
+// a = fma(p[t], v[t], a) over the first n keys of a chunk, in order; p and v
+// are 16-byte aligned LDS rows.  A full chunk is unrolled, so the compiler
+// counts outstanding LDS reads exactly; a partial chunk takes the loop.
+DEV float pvw_chunk(const float* p, const float* v, int n, float a) {
+    if (n == PVW_CK) {
+        constexpr int NB = PVW_CK / 16;
+        float4 pb[3][4], vb[3][4];
+#pragma unroll
+        for (int k = 0; k < 2; k++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                pb[k][i] = *(const float4*)(p + 16 * k + 4 * i);
+                vb[k][i] = *(const float4*)(v + 16 * k + 4 * i);
+            }
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+            const int cur = b % 3;
+            if (b + 2 < NB) {
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    pb[(b + 2) % 3][i] = *(const float4*)(p + 16 * (b + 2) + 4 * i);
+                    vb[(b + 2) % 3][i] = *(const float4*)(v + 16 * (b + 2) + 4 * i);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                a = fmaf(pb[cur][i].x, vb[cur][i].x, a);
+                a = fmaf(pb[cur][i].y, vb[cur][i].y, a);
+                a = fmaf(pb[cur][i].z, vb[cur][i].z, a);
+                a = fmaf(pb[cur][i].w, vb[cur][i].w, a);
+            }
+        }
+        return a;
+    }
+    for (int t = 0; t < n; t++) a = fmaf(p[t], v[t], a);
+    return a;
+}
+
+// Chunk c (clamped to the last one) of a k_attn_pvw workgroup into a
+// producer lane's registers (producer lane pl of 128): V rows c0 + pl and
+// c0 + 128 + pl, the key's 4 dims each (16 bytes); P 16-byte pieces 4 pl and
+// 4 pl + 512 of the chunk's [GM][PVW_CK] block (heads past G read head G - 1,
+// keys clamped into the row).
+template <int HD, int GM>
+DEV void pvw_load(const float* Vh, const float* Ph, int c, int nck, int G, int max_seq, int pl,
+                  gm_f4 (&r)[2 + GM / 2]) {
+    const int c0 = (c < nck ? c : nck - 1) * PVW_CK;
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int key = min(c0 + 128 * i + pl, max_seq - 1);
+        r[i] = *(const gm_f4*)(Vh + (size_t)key * HD);
+    }
+#pragma unroll
+    for (int i = 0; i < GM / 2; i++) {
+        const int f = 512 * i + 4 * pl, hh = min(f / PVW_CK, G - 1), t = min(c0 + f % PVW_CK, max_seq - 4);
+        r[2 + i] = *(const gm_f4*)(Ph + (size_t)hh * max_seq + t);
+    }
+}
+
+// A producer lane's chunk into an LDS slot, V transposed to [dim][key].
+template <int GM>
+DEV void pvw_store(float (*Vt)[PVW_LD], float (*Pt)[PVW_LD], int pl, const gm_f4 (&r)[2 + GM / 2]) {
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int k = 128 * i + pl;
+        Vt[0][k] = r[i][0];
+        Vt[1][k] = r[i][1];
+        Vt[2][k] = r[i][2];
+        Vt[3][k] = r[i][3];
+    }
+#pragma unroll
+    for (int i = 0; i < GM / 2; i++) {
+        const int f = 512 * i + 4 * pl;
+        *(gm_f4*)&Pt[f / PVW_CK][f % PVW_CK] = r[2 + i];
+    }
+}
+
+// P.V of a one-token step over normalised probabilities P (row kvh * G + h
+// of stride max_seq) for the G <= GM query heads of kv head blockIdx.x and
+// dims 4 blockIdx.y .. + 3.  Wave 0 runs the chains, lane h * 4 + d, over
+// LDS only; waves 1 and 2 produce: chunk c of PVW_CK keys is loaded into
+// register set c % 4 four chunks ahead and written to LDS slot c % 2 one
+// chunk ahead of its chains, one barrier per chunk.  The loop is unrolled by
+// 4 so every register set index is static.
+template <int HD, int GM>
+__global__ __launch_bounds__(192) void k_attn_pvw(const float* __restrict__ P, const float* __restrict__ vc,
+                                                  const int32_t* __restrict__ pos0p, int n_q, int n_kv,
+                                                  int max_seq, float* __restrict__ out) {
+    static_assert(GM >= 2 && GM * 4 <= 64 && GM % 2 == 0, "lane layout");
+    __shared__ __align__(16) float Vt[2][4][PVW_LD];
+    __shared__ __align__(16) float Pt[2][GM][PVW_LD];
+    const int kvh = blockIdx.x, d0 = blockIdx.y * 4, tid = threadIdx.x, w = tid >> 6;
+    const int G = n_q / n_kv, h = tid >> 2, d = tid & 3, pl = tid - 64;
+    const int L = *pos0p + 1, nck = (L + PVW_CK - 1) / PVW_CK;
+    const float* Vh = vc + (size_t)kvh * max_seq * HD + d0;
+    const float* Ph = P + (size_t)kvh * G * max_seq;
+    gm_f4 r0[2 + GM / 2], r1[2 + GM / 2], r2[2 + GM / 2], r3[2 + GM / 2];  // native vectors: no struct copies
+    if (w > 0) {
+        pvw_load<HD, GM>(Vh, Ph, 0, nck, G, max_seq, pl, r0);
+        pvw_load<HD, GM>(Vh, Ph, 1, nck, G, max_seq, pl, r1);
+        pvw_load<HD, GM>(Vh, Ph, 2, nck, G, max_seq, pl, r2);
+        pvw_load<HD, GM>(Vh, Ph, 3, nck, G, max_seq, pl, r3);
+        pvw_store<GM>(Vt[0], Pt[0], pl, r0);
+    }
+    __syncthreads();
+    float a = 0.0f;
+    // chunk C is in LDS slot C & 1; producers load chunk C + 4 into RL (which
+    // held chunk C) and write chunk C + 1 (in RN) to the other slot
+#define PVW_STEP(C, RL, RN)                                                                           \
+    {                                                                                                 \
+        const int sl = (C) & 1;                                                                       \
+        if (w == 0) {                                                                                 \
+            if (h < G) a = pvw_chunk(&Pt[sl][h][0], &Vt[sl][d][0], min(PVW_CK, L - (C) * PVW_CK), a); \
+        } else {                                                                                      \
+            pvw_load<HD, GM>(Vh, Ph, (C) + 4, nck, G, max_seq, pl, RL);                               \
+            pvw_store<GM>(Vt[sl ^ 1], Pt[sl ^ 1], pl, RN);                                            \
+        }                                                                                             \
+        __syncthreads();                                                                              \
+    }
+    for (int c = 0; c < nck; c += 4) {
+        PVW_STEP(c, r0, r1)
+        if (c + 1 >= nck) break;
+        PVW_STEP(c + 1, r1, r2)
+        if (c + 2 >= nck) break;
+        PVW_STEP(c + 2, r2, r3)
+        if (c + 3 >= nck) break;
+        PVW_STEP(c + 3, r3, r0)
+    }
+#undef PVW_STEP
+    if (w == 0 && h < G) out[(size_t)(kvh * G + h) * HD + d0 + d] = a;
+}
+
+// ---------------------------------------------------------------------------
 // k_attn_pvt: softmax and P.V for prefill, register-tiled.  Workgroup (kv
 // head, tile of qt = 32 / G queries): R = 32 score rows, all HD dims.  The
 // rows come into LDS by direct-to-LDS loads and go through the same softmax
@@ -3742,7 +3784,11 @@ void dpuf_hip_resnorm_prep(void* s, int32_t M, int32_t H, float* h, const float*
     }
     const int threads = H / 16;  // H is a multiple of 1024 or 64 * 16 * k; checked at engine create
     const size_t lds = (size_t)8 * ((H >> 3) + 4) * sizeof(float);
-    hipLaunchKernelGGL(k_resnorm_prep, dim3(M), dim3(threads), lds, ST(s), H, h, res, w, eps, ps, xn_out);
+    // register-fed chains for the widths with a 16-byte-aligned segment
+    // (8 * (H / 8 + 4) floats per row keeps segments of 16, 32, 64 aligned)
+    auto k = H == 4096 ? k_resnorm_prep<64> : H == 2048 ? k_resnorm_prep<32> : H == 1024 ? k_resnorm_prep<16>
+                                                                                          : k_resnorm_prep<0>;
+    hipLaunchKernelGGL(k, dim3(M), dim3(threads), lds, ST(s), H, h, res, w, eps, ps, xn_out);
     LAUNCHED("k_resnorm_prep");
 }
 
@@ -4142,6 +4188,47 @@ int32_t dpuf_hip_attn_split(void* s, int32_t M, int32_t lmax, const float* q, co
                                    pos0p, M, n_q, n_kv, max_seq, qt, ldp, out, o_sign, fop);
             }
             LAUNCHED("k_attn_split_tiled");
+            return 0;
+        }
+    }
+    // one-token decode with an even group: softmax once per row, then the
+    // wide P.V (one wave per kv head and 4 dims)
+    {
+        // chain segments of the softmax: 8 SEG positions per sum lane cover
+        // keys up to 64 SEG
+        const int segs[7] = {16, 32, 48, 64, 80, 96, 128};
+        int seg = 0;
+        for (int i = 0; i < 7 && !seg; i++)
+            if (64 * segs[i] >= lmax) seg = segs[i];
+        if (M == 1 && (G & 1) == 0 && G <= 8 && seg) {
+            const dim3 gs1(n_kv, 1, (lmax + AS_KC - 1) / AS_KC);
+            const int gm = G <= 2 ? 2 : G <= 4 ? 4 : 8;
+            const dim3 gp(n_kv, hd / 4);
+#define SMX_LAUNCH(SG)                                                                                            \
+    if (seg == SG) hipLaunchKernelGGL(k_attn_smx<SG>, dim3(n_q), dim3(256), 0, ST(s), scores, pos0p, max_seq);
+#define PVW_LAUNCH(HDV)                                                                                           \
+    hipLaunchKernelGGL(k_attn_sc<HDV>, gs1, dim3(256), lds1, ST(s), q, kc, pos0p, 1, n_q, n_kv, max_seq, scale, qt1, \
+                       scores);                                                                                   \
+    SMX_LAUNCH(16) SMX_LAUNCH(32) SMX_LAUNCH(48) SMX_LAUNCH(64) SMX_LAUNCH(80) SMX_LAUNCH(96) SMX_LAUNCH(128)  \
+    if (gm == 2)                                                                                                  \
+        hipLaunchKernelGGL((k_attn_pvw<HDV, 2>), gp, dim3(192), 0, ST(s), scores, vc, pos0p, n_q, n_kv, max_seq,   \
+                           out);                                                                                  \
+    else if (gm == 4)                                                                                             \
+        hipLaunchKernelGGL((k_attn_pvw<HDV, 4>), gp, dim3(192), 0, ST(s), scores, vc, pos0p, n_q, n_kv, max_seq,   \
+                           out);                                                                                  \
+    else                                                                                                          \
+        hipLaunchKernelGGL((k_attn_pvw<HDV, 8>), gp, dim3(192), 0, ST(s), scores, vc, pos0p, n_q, n_kv, max_seq,   \
+                           out);
+            if (hd == 64) {
+                PVW_LAUNCH(64)
+            } else if (hd == 128) {
+                PVW_LAUNCH(128)
+            } else {
+                PVW_LAUNCH(256)
+            }
+#undef PVW_LAUNCH
+#undef SMX_LAUNCH
+            LAUNCHED("k_attn_split_wide");
             return 0;
         }
     }
