@@ -3073,9 +3073,43 @@ __global__ __launch_bounds__(256) void k_attn_dec(const float* __restrict__ q, c
     const float* Kc = kc + (size_t)kvh * max_seq * HD;
     const float* Vc = vc + (size_t)kvh * max_seq * HD;
 
-    // Every load that does not depend on the position is issued first, so
-    // the kernel waits for one memory round trip before the position-
-    // dependent ones (K rows, V rows, RoPE tables) and one after.
+    // V rows [c0, c0 + rows) -> vst, 1 KB per wave instruction (whole
+    // instructions: a few rows past the end may come along); rows past the
+    // cache end are redirected to row 0 (never read back).
+    auto stage_v = [&](int c0, int rows) {
+        const int n_ins = (rows * HD + 255) / 256;
+        for (int ii = wave; ii < n_ins; ii += 4) {
+            const int e = ii * 256 + lane * 4;  // float index inside the chunk
+            int t = c0 + e / HD;
+            if (t >= max_seq) t = 0;
+            __builtin_amdgcn_global_load_lds((const void*)(Vc + (size_t)t * HD + (e % HD)),
+                                             (lds_ptr_t)(vst + ii * 256), 16, 0, 0);
+        }
+    };
+    // key kq (one per lane pair) of each pass; lane h holds elements 8i + 4h
+    // .. +3.  Rows clamped into the cache, read through a global pointer (the
+    // cache base may come from kcs[], and loads through a generic pointer
+    // would wait for the V-row LDS DMA before each one).  Keys at or past pos
+    // only feed scores that are never stored; key pos itself is replaced by
+    // the new key.
+    const int kq = tid >> 1, h = tid & 1;
+    float4 kr[NI];
+    auto load_k = [&](int t0) {
+        const int t = min(t0 + kq, max_seq - 1);
+        const __attribute__((address_space(1))) gm_f4* kp =
+            (const __attribute__((address_space(1))) gm_f4*)(Kc + (size_t)t * HD + 4 * h);
+#pragma unroll
+        for (int i = 0; i < NI; i++) {
+            const gm_f4 x = kp[2 * i];
+            kr[i] = make_float4(x[0], x[1], x[2], x[3]);
+        }
+    };
+    // The first pass's K rows and the first chunk of V rows are requested
+    // before the position is known, so their round trip overlaps the
+    // position's and the q / k / v loads'.
+    stage_v(0, V_ROWS);
+    load_k(0);
+
     // Thread tid owns normalised elements e = tid + 256 * r of [q0 | q1 | k].
     constexpr int NE = (3 * HD + 255) / 256;
     float xe[NE], we[NE];
@@ -3105,30 +3139,6 @@ __global__ __launch_bounds__(256) void k_attn_dec(const float* __restrict__ q, c
     const int pos = *pos0p;
     const int kv_len = pos + 1;
 
-    // V rows [c0, min(c0 + V_ROWS, kv_len)) -> vst, 1 KB per wave instruction
-    // (whole instructions: a few rows past kv_len may come along); rows past
-    // the cache end are redirected to row 0 (never read back).
-    auto stage_v = [&](int c0) {
-        const int rows = kv_len - c0 < V_ROWS ? kv_len - c0 : V_ROWS;
-        const int n_ins = (rows * HD + 255) / 256;
-        for (int ii = wave; ii < n_ins; ii += 4) {
-            const int e = ii * 256 + lane * 4;  // float index inside the chunk
-            int t = c0 + e / HD;
-            if (t >= max_seq) t = 0;
-            __builtin_amdgcn_global_load_lds((const void*)(Vc + (size_t)t * HD + (e % HD)),
-                                             (lds_ptr_t)(vst + ii * 256), 16, 0, 0);
-        }
-    };
-    // key kq (one per lane pair) of each pass; lane h holds elements 8i + 4h .. +3
-    const int kq = tid >> 1, h = tid & 1;
-    float4 kr[NI];
-    auto load_k = [&](int t0) {
-        const int t = t0 + kq;
-        const bool ok = t < pos;
-        const float4* kp = (const float4*)(Kc + (size_t)(ok ? t : 0) * HD + 4 * h);
-#pragma unroll
-        for (int i = 0; i < NI; i++) kr[i] = ok ? kp[2 * i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    };
     // RoPE table entries of the owned elements
     const float* c_row = cos_tab + (size_t)pos * half;
     const float* s_row = sin_tab + (size_t)pos * half;
@@ -3139,8 +3149,6 @@ __global__ __launch_bounds__(256) void k_attn_dec(const float* __restrict__ q, c
         ce[r] = c_row[j];
         se[r] = s_row[j];
     }
-    if (pos > 0) stage_v(0);
-    load_k(0);
 
     float* tmp = scl;  // [3][HD] normalised vectors, before the scores use this space
 #pragma unroll
@@ -3160,8 +3168,13 @@ __global__ __launch_bounds__(256) void k_attn_dec(const float* __restrict__ q, c
         const float* vec = tmp + vi * HD;
         const float* nw = vi == 2 ? kn : qn;
         if ((vi != 1 || pair) && nw) {
+            // all of the lane's elements into registers, then the chain
+            float xv[HD / 8];
+#pragma unroll
+            for (int i = 0; i < HD / 8; i++) xv[i] = vec[jj + 8 * i];
             float a = 0.0f;
-            for (int i = jj; i < HD; i += 8) a = fmaf(vec[i], vec[i], a);
+#pragma unroll
+            for (int i = 0; i < HD / 8; i++) a = fmaf(xv[i], xv[i], a);
             part[vi][jj] = a;
         }
     }
@@ -3211,21 +3224,36 @@ __global__ __launch_bounds__(256) void k_attn_dec(const float* __restrict__ q, c
         float a[4] = {0.0f, 0.0f, 0.0f, 0.0f}, b[4] = {0.0f, 0.0f, 0.0f, 0.0f};
         float c[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // single-head tail: dot_f32_avx2's second accumulator
         const bool tail1 = !pair && t >= n4;
+        // No divergent branch inside the loop (the LDS reads of q then
+        // batch instead of each waiting alone): pair is uniform, and a
+        // single-head tail key's odd steps go to c by selects.
+        if (pair) {
 #pragma unroll
-        for (int i = 0; i < NI; i++) {
-            const float4 q0 = *(const float4*)(qs + 8 * i + 4 * h);
-            const float4 kk = kr[i];
-            if (tail1 && (i & 1)) {
-                c[0] = fmaf(q0.x, kk.x, c[0]); c[1] = fmaf(q0.y, kk.y, c[1]);
-                c[2] = fmaf(q0.z, kk.z, c[2]); c[3] = fmaf(q0.w, kk.w, c[3]);
-            } else {
+            for (int i = 0; i < NI; i++) {
+                const float4 q0 = *(const float4*)(qs + 8 * i + 4 * h);
+                const float4 q1 = *(const float4*)(qs + HD + 8 * i + 4 * h);
+                const float4 kk = kr[i];
                 a[0] = fmaf(q0.x, kk.x, a[0]); a[1] = fmaf(q0.y, kk.y, a[1]);
                 a[2] = fmaf(q0.z, kk.z, a[2]); a[3] = fmaf(q0.w, kk.w, a[3]);
-            }
-            if (pair) {
-                const float4 q1 = *(const float4*)(qs + HD + 8 * i + 4 * h);
                 b[0] = fmaf(q1.x, kk.x, b[0]); b[1] = fmaf(q1.y, kk.y, b[1]);
                 b[2] = fmaf(q1.z, kk.z, b[2]); b[3] = fmaf(q1.w, kk.w, b[3]);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < NI; i++) {
+                const float4 q0 = *(const float4*)(qs + 8 * i + 4 * h);
+                const float4 kk = kr[i];
+                const float qv[4] = {q0.x, q0.y, q0.z, q0.w}, kv[4] = {kk.x, kk.y, kk.z, kk.w};
+#pragma unroll
+                for (int jj = 0; jj < 4; jj++) {
+                    if (i & 1) {
+                        const float x = fmaf(qv[jj], kv[jj], tail1 ? c[jj] : a[jj]);
+                        c[jj] = tail1 ? x : c[jj];
+                        a[jj] = tail1 ? a[jj] : x;
+                    } else {
+                        a[jj] = fmaf(qv[jj], kv[jj], a[jj]);
+                    }
+                }
             }
         }
         float s0, s1 = 0.0f;
@@ -3309,7 +3337,7 @@ __global__ __launch_bounds__(256) void k_attn_dec(const float* __restrict__ q, c
     for (int c0 = 0; c0 < kv_len; c0 += V_ROWS) {
         if (c0 > 0) {
             __syncthreads();  // previous chunk consumed
-            stage_v(c0);
+            stage_v(c0, kv_len - c0 < V_ROWS ? kv_len - c0 : V_ROWS);
         }
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
