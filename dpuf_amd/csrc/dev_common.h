@@ -98,6 +98,86 @@ struct PrepSet {
 DEV float fxor1(float v) { return __int_as_float(dpp_xor1(__float_as_int(v))); }
 DEV float fxor2(float v) { return __int_as_float(dpp_xor2(__float_as_int(v))); }
 
+// Maximum over the 64 lanes, in every lane: DPP inside each 16-lane row
+// (xor 1, xor 2, half-row mirror, row mirror), then the four rows' values
+// read into scalars.  fmaxf is exact, so the grouping is free.
+DEV float wave_max(float v) {
+    v = fmaxf(v, fxor1(v));
+    v = fmaxf(v, fxor2(v));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false)));
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
+// ---------------------------------------------------------------------------
+// Activation prep of one 64-block by one wave, lane l holding column l: the
+// latency-bound form for a few blocks at the end of a kernel.
+//
+// FWHT stride h pairs lane l with l ^ h: DPP quad permutes for h = 1, 2,
+// row rotations for 4 and 8 (row_ror:N hands lane i the value of lane
+// (i - N) mod 16, so l ^ 4 is ror 4 for lanes with bit 2 set and ror 12
+// for the others, and l ^ 8 is ror 8), shuffles for 16 and 32.  Each
+// butterfly is the reference's a + b / a - b with a the lower column, in
+// ascending stride order, so the values equal quad_fwht64's.  The 32-block
+// maximum and the integer sum (both order-free) use the same moves.
+// ---------------------------------------------------------------------------
+#define DPP_F(v, ctrl) __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), ctrl, 0xF, 0xF, false))
+#define DPP_I(v, ctrl) __builtin_amdgcn_update_dpp(0, (v), ctrl, 0xF, 0xF, false)
+
+DEV void wave_prep64(float x, int lane, int blk, int8_t* q, float* s, int32_t* m, uint16_t* h) {
+    // FWHT-64 across the wave
+    {
+        float p = DPP_F(x, 0xB1);  // l ^ 1
+        x = (lane & 1) ? p - x : x + p;
+        p = DPP_F(x, 0x4E);  // l ^ 2
+        x = (lane & 2) ? p - x : x + p;
+        const float r4 = DPP_F(x, 0x124), r12 = DPP_F(x, 0x12C);
+        p = (lane & 4) ? r4 : r12;  // l ^ 4
+        x = (lane & 4) ? p - x : x + p;
+        p = DPP_F(x, 0x128);  // l ^ 8
+        x = (lane & 8) ? p - x : x + p;
+        p = __shfl_xor(x, 16, 64);
+        x = (lane & 16) ? p - x : x + p;
+        p = __shfl_xor(x, 32, 64);
+        x = (lane & 32) ? p - x : x + p;
+        x = x * 0.125f;
+    }
+    // maximum of |x| over the lane's 32-block
+    float amax = fabsf(x);
+    amax = fmaxf(amax, DPP_F(amax, 0xB1));
+    amax = fmaxf(amax, DPP_F(amax, 0x4E));
+    amax = fmaxf(amax, DPP_F(amax, 0x124));
+    amax = fmaxf(amax, DPP_F(amax, 0x128));
+    amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
+    int32_t qi = 0;
+    float d = 0.0f;
+    if (!(amax <= 1e-4f)) {
+        d = amax / 127.0f;
+        const float inv = (amax > 1e-12f) ? (127.0f / amax) : 0.0f;
+        const float xs = x * inv;
+        if (!(xs > -2147483648.0f && xs < 2147483648.0f)) qi = -127;  // cvtps -> INT_MIN -> -127
+        else qi = (int32_t)rintf(xs);
+        qi = qi > 127 ? 127 : qi;
+        qi = qi < -127 ? -127 : qi;
+    }
+    int32_t sum = qi;
+    sum += DPP_I(sum, 0xB1);
+    sum += DPP_I(sum, 0x4E);
+    sum += DPP_I(sum, 0x124);
+    sum += DPP_I(sum, 0x128);
+    sum += __shfl_xor(sum, 16, 64);
+    q[64 * blk + lane] = (int8_t)qi;
+    if (h) h[64 * blk + lane] = __builtin_bit_cast(uint16_t, (_Float16)qi);
+    if ((lane & 31) == 0) {
+        s[2 * blk + (lane >> 5)] = d;
+        m[2 * blk + (lane >> 5)] = sum * 8;
+    }
+}
+
 // Sign bits of the lane's 16 columns of 64-block blk (bit c%8 of byte c/8
 // set = negate column c).
 DEV uint32_t quad_sign_bits(const uint8_t* sign, int blk, int qp) {

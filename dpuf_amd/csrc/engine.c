@@ -92,7 +92,7 @@ typedef struct {
 
 /* Decode attention switches from the fused short-context kernel to the split
  * (scores + softmax/P.V) kernels once kv_len exceeds this. */
-#define ATT_SPLIT_MIN 192
+#define ATT_SPLIT_MIN DPUF_HIP_DEC_MAX_KEYS
 
 /* ------------------------------------------------------------------------- */
 
@@ -775,12 +775,12 @@ static void enqueue_layers(Engine* e, int32_t M, int32_t keep_tiles) {
             } else if (e->ms_n > 0)  /* one token per session, each with its own cache */
                 fused = dpuf_hip_attn_dec(s, M, e->q, e->k, e->v, e->d_norm[4 * l + 1], e->d_norm[4 * l + 2], eps,
                                           e->d_cos, e->d_sin, NULL, NULL, e->d_ms_pos, e->nq, e->nkv, e->hd,
-                                          e->max_seq, scale, e->scores, e->ao, W[W_O].sign, e->prep[0], e->d_ms_kc,
+                                          e->max_seq, scale, e->ao, W[W_O].sign, e->prep[0], e->d_ms_kc,
                                           e->d_ms_vc, (size_t)l * e->nkv * e->max_seq * e->hd) == 0;
             else if (M == 1 && e->host_pos0 + 1 <= ATT_SPLIT_MIN)
                 fused = dpuf_hip_attn_dec(s, 1, e->q, e->k, e->v, e->d_norm[4 * l + 1], e->d_norm[4 * l + 2], eps,
                                           e->d_cos, e->d_sin, kc, vc, e->d_pos0, e->nq, e->nkv, e->hd, e->max_seq,
-                                          scale, e->scores, e->ao, W[W_O].sign, e->prep[0], NULL, NULL, 0) == 0;
+                                          scale, e->ao, W[W_O].sign, e->prep[0], NULL, NULL, 0) == 0;
             if (!fused) {
                 dpuf_hip_qk_rope_kv(s, M, e->q, e->k, e->v, e->d_norm[4 * l + 1], e->d_norm[4 * l + 2], eps,
                                     e->d_cos, e->d_sin, kc, vc, e->d_pos0, e->nq, e->nkv, e->hd, e->max_seq, NULL);

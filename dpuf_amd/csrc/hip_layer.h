@@ -145,16 +145,21 @@ void dpuf_hip_attn_q8(void* s, int32_t M, int32_t lmax, const float* q, DpufKvQ8
  * cache, as the KV store does; and n values from element off dequantised. */
 void dpuf_hip_q8_rows(void* s, const float* k, const float* v, int32_t n, int32_t hd, DpufKvQ8 c8, size_t row0);
 void dpuf_hip_q8_dequant(void* s, DpufKvQ8 c8, size_t off, size_t n, float* k, float* v);
+/* Keys the fused decode attention takes (positions 0 .. 191); longer
+ * contexts go to the split kernels. */
+#define DPUF_HIP_DEC_MAX_KEYS 192
 /* One-token-per-session fused QK-norm + RoPE + KV store + attention +
- * O-input prep for M tokens: token m at position pos0[m]; with kcs / vcs set
- * (device arrays of M session KV-cache bases, plus l_off floats) each token
- * uses its own session's cache, otherwise all use kc / vc.  Returns -1
- * (nothing launched) for head dims other than 64, 128, 256. */
+ * O-input prep for M tokens: token m at position pos0[m] (pos0[m] <
+ * DPUF_HIP_DEC_MAX_KEYS, checked by the caller: the position is read on the
+ * device); with kcs / vcs set (device arrays of M session KV-cache bases,
+ * plus l_off floats) each token uses its own session's cache, otherwise all
+ * use kc / vc.  Returns -1 (nothing launched) for head dims other than 64,
+ * 128, 256. */
 int32_t dpuf_hip_attn_dec(void* s, int32_t M, const float* q, const float* k, const float* v, const float* q_norm,
                           const float* k_norm, float eps, const float* cos_tab, const float* sin_tab, float* kc,
                           float* vc, const int32_t* pos0, int32_t n_q, int32_t n_kv, int32_t hd, int32_t max_seq,
-                          float scale, float* scores, float* ao, const uint8_t* o_sign, DpufPrep op,
-                          float* const* kcs, float* const* vcs, size_t l_off);
+                          float scale, float* ao, const uint8_t* o_sign, DpufPrep op, float* const* kcs,
+                          float* const* vcs, size_t l_off);
 void dpuf_hip_zero_rows(void* s, int32_t M, float* out, int32_t ld, int32_t r0, int32_t r1);
 /* CRC32 of n tile bodies (base + off[t], len[t] bytes) against want[t]: ok[t] = 1 when equal. */
 void dpuf_hip_crc_tiles(void* s, const uint8_t* base, const uint64_t* off, const uint32_t* len,

@@ -61,7 +61,10 @@ __constant__ uint64_t c_exp2_tab[32] = {
     0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull,
 };
 
-DEV float expf_libc(float x) {
+// tab: the 32 table words (c_exp2_tab, or a copy in LDS: a kernel whose
+// tail exponentials sit on its critical path copies the table at entry, so
+// the lookup does not wait for a global load).
+DEV float expf_libc_tab(float x, const uint64_t* tab) {
     if (x < -0x1.9fe368p6f) return 0.0f;  // below log(2^-150): rounds to +0
     const double inv_ln2_n = 0x1.71547652b82fep+0 * 32.0;
     const double shift = 0x1.8p+52;
@@ -73,7 +76,7 @@ DEV float expf_libc(float x) {
     uint64_t ki = (uint64_t)__double_as_longlong(kd);
     kd -= shift;
     double r = fma(inv_ln2_n, xd, -kd);
-    uint64_t t = c_exp2_tab[ki & 31u] + (ki << 47);
+    uint64_t t = tab[ki & 31u] + (ki << 47);
     double sc = __longlong_as_double((long long)t);
     double z = fma(c0, r, c1);
     double r2 = r * r;
@@ -82,6 +85,8 @@ DEV float expf_libc(float x) {
     y = y * sc;
     return (float)y;
 }
+
+DEV float expf_libc(float x) { return expf_libc_tab(x, c_exp2_tab); }
 
 // ---------------------------------------------------------------------------
 // Embedding (reference dpuf_embed_qr_hadamard4_packed_f32, dpuf_avx2.c:2738-2783,
@@ -3019,7 +3024,6 @@ __global__ void k_q8_dequant(DpufKvQ8 c8, size_t off, size_t n, float* __restric
 #define ATT_KEYS 128  // keys per pass: 2 lanes per key, 256 threads
 
 
-DEV float shx(float v, int m) { return __shfl_xor(v, m, 64); }
 
 template <int HD>
 __global__ __launch_bounds__(256) void k_attn_dec(const float* __restrict__ q, const float* __restrict__ k,
@@ -3028,7 +3032,7 @@ __global__ __launch_bounds__(256) void k_attn_dec(const float* __restrict__ q, c
                                                   const float* __restrict__ cos_tab, const float* __restrict__ sin_tab,
                                                   float* __restrict__ kc, float* __restrict__ vc,
                                                   const int32_t* __restrict__ pos0p, int n_q, int n_kv, int max_seq,
-                                                  float scale, int sc_cap, float* __restrict__ scores_g,
+                                                  float scale,
                                                   float* __restrict__ ao, const uint8_t* __restrict__ o_sign,
                                                   DpufPrep op, float* const* kcs, float* const* vcs, size_t l_off) {
     constexpr int V_ROWS = 16384 / HD;  // 64 KB of V rows per LDS chunk
@@ -3044,7 +3048,6 @@ __global__ __launch_bounds__(256) void k_attn_dec(const float* __restrict__ q, c
         k += (size_t)mt * n_kv * HD;
         v += (size_t)mt * n_kv * HD;
         ao += (size_t)mt * n_q * HD;
-        scores_g += (size_t)mt * n_q * max_seq;
         pos0p += mt;
         const size_t qd = (size_t)n_q * HD;
         op.q += mt * qd;
@@ -3060,11 +3063,10 @@ __global__ __launch_bounds__(256) void k_attn_dec(const float* __restrict__ q, c
     float* ks = qs + 2 * HD;            // [HD]
     float* vn = ks + HD;                // [HD]
     float* aout = vn + HD;              // [2][HD]
-    float* scl = aout + 2 * HD;         // [max(2 * sc_cap, 3 * HD)]
+    float* scl = aout + 2 * HD;         // [max(2 * DPUF_HIP_DEC_MAX_KEYS, 3 * HD)]
     __shared__ float part[3][8];
-    __shared__ float red[2][4];
     __shared__ float vs8[2][8];
-    __shared__ float inv_sh[2];
+    __shared__ uint64_t etab[32];  // the expf table (read by the softmax tails)
     const int kvh = blockIdx.x, gp = blockIdx.y, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int groups = n_q / n_kv, g0 = 2 * gp;
     const bool pair = (g0 + 1 < groups);
@@ -3109,6 +3111,7 @@ __global__ __launch_bounds__(256) void k_attn_dec(const float* __restrict__ q, c
     // position's and the q / k / v loads'.
     stage_v(0, V_ROWS);
     load_k(0);
+    const uint64_t etab_w = c_exp2_tab[tid & 31];  // to LDS with the first stores below
 
     // Thread tid owns normalised elements e = tid + 256 * r of [q0 | q1 | k].
     constexpr int NE = (3 * HD + 255) / 256;
@@ -3131,10 +3134,14 @@ __global__ __launch_bounds__(256) void k_attn_dec(const float* __restrict__ q, c
         const int i = tid + 256 * r;
         vv0[r] = i < HD ? v[(size_t)kvh * HD + i] : 0.0f;
     }
+    // the O input's sign bits of this lane's columns in the prep below:
+    // block b = wave + 4 k of the pair's nh * HD / 64, column lane
+    constexpr int NPB = (2 * HD / 64 + 3) / 4;
     uint32_t osb = 0;
-    if (tid < nh * HD / 16) {
-        const int blk = (qh0 * HD) / 64 + (tid >> 2);
-        if (o_sign) osb = *(const uint16_t*)(o_sign + 8 * blk + 2 * (tid & 3));
+#pragma unroll
+    for (int k = 0; k < NPB; k++) {
+        const int b = wave + 4 * k;
+        if (o_sign && b < nh * HD / 64) osb |= ((o_sign[8 * ((qh0 * HD) / 64 + b) + (lane >> 3)] >> (lane & 7)) & 1u) << k;
     }
     const int pos = *pos0p;
     const int kv_len = pos + 1;
@@ -3150,6 +3157,7 @@ __global__ __launch_bounds__(256) void k_attn_dec(const float* __restrict__ q, c
         se[r] = s_row[j];
     }
 
+    if (tid < 32) etab[tid] = etab_w;
     float* tmp = scl;  // [3][HD] normalised vectors, before the scores use this space
 #pragma unroll
     for (int r = 0; r < NE; r++) {
@@ -3203,16 +3211,17 @@ __global__ __launch_bounds__(256) void k_attn_dec(const float* __restrict__ q, c
     __syncthreads();
     if (gp == 0) {
         for (int i = tid; i < HD; i += 256) {
-            kc[((size_t)kvh * max_seq + pos) * HD + i] = ks[i];
-            vc[((size_t)kvh * max_seq + pos) * HD + i] = vn[i];
+            // global stores (kc / vc may come from kcs[] / vcs[])
+            ((__attribute__((address_space(1))) float*)kc)[((size_t)kvh * max_seq + pos) * HD + i] = ks[i];
+            ((__attribute__((address_space(1))) float*)vc)[((size_t)kvh * max_seq + pos) * HD + i] = vn[i];
         }
     }
 
     // scores
-    float* sc0 = kv_len <= sc_cap ? scl : scores_g + (size_t)qh0 * max_seq;
-    float* sc1 = kv_len <= sc_cap ? scl + sc_cap : sc0 + max_seq;
+    // score rows in LDS (kv_len <= DPUF_HIP_DEC_MAX_KEYS, the launch contract)
+    float* sc0 = scl;
+    float* sc1 = scl + DPUF_HIP_DEC_MAX_KEYS;
     const int n4 = kv_len & ~3;
-    float mx0 = -1e30f, mx1 = -1e30f;
     for (int t0 = 0; t0 < kv_len; t0 += ATT_KEYS) {
         if (t0 > 0) load_k(t0);
         const int t = t0 + kq;
@@ -3261,7 +3270,7 @@ __global__ __launch_bounds__(256) void k_attn_dec(const float* __restrict__ q, c
             // hsum4_256_ps: ((a0+a1)+(a2+a3)) + ((a4+a5)+(a6+a7)); lane 0 holds a0..a3
             const float l0 = (a[0] + a[1]) + (a[2] + a[3]);
             const float l1 = (b[0] + b[1]) + (b[2] + b[3]);
-            const float o0 = shx(l0, 1), o1 = shx(l1, 1);
+            const float o0 = fxor1(l0), o1 = fxor1(l1);
             s0 = (h ? o0 + l0 : l0 + o0) * scale;
             s1 = (h ? o1 + l1 : l1 + o1) * scale;
         } else {
@@ -3273,7 +3282,7 @@ __global__ __launch_bounds__(256) void k_attn_dec(const float* __restrict__ q, c
             float u[4], ub[4];
 #pragma unroll
             for (int jj = 0; jj < 4; jj++) {
-                const float pa = shx(a[jj], 1), pb = shx(b[jj], 1);
+                const float pa = fxor1(a[jj]), pb = fxor1(b[jj]);
                 u[jj] = h ? pa + a[jj] : a[jj] + pa;
                 ub[jj] = h ? pb + b[jj] : b[jj] + pb;
             }
@@ -3285,48 +3294,68 @@ __global__ __launch_bounds__(256) void k_attn_dec(const float* __restrict__ q, c
                 sc0[t] = s0;
                 if (pair) sc1[t] = s1;
             }
-            mx0 = s0 > mx0 ? s0 : mx0;
-            mx1 = s1 > mx1 ? s1 : mx1;
         }
     }
-#pragma unroll
-    for (int m = 32; m > 0; m >>= 1) {
-        mx0 = fmaxf(mx0, shx(mx0, m));
-        mx1 = fmaxf(mx1, shx(mx1, m));
-    }
-    if (lane == 0) {
-        red[0][wave] = mx0;
-        red[1][wave] = mx1;
-    }
-    __syncthreads();
-    const float M0 = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
-    const float M1 = fmaxf(fmaxf(red[1][0], red[1][1]), fmaxf(red[1][2], red[1][3]));
+    __syncthreads();  // score rows complete
+    // Softmax of head w by wave w alone, keys lane + 64 r: the maximum, the
+    // exponentials (exp_poly below n8, libm expf for the tail), the
+    // reference's 8 sum chains (lane j: keys j, j + 8, ... below n8 in order),
+    // hsum8, the tail in order, and the normalisation.  The wave reads back
+    // rows it wrote itself (LDS operations of one wave complete in order), so
+    // no workgroup barrier falls between the steps.
     const int n8 = kv_len & ~7;
-    for (int t = tid; t < kv_len; t += 256) {
-        sc0[t] = t < n8 ? exp_poly(sc0[t] - M0) : expf_libc(sc0[t] - M0);
-        if (pair) sc1[t] = t < n8 ? exp_poly(sc1[t] - M1) : expf_libc(sc1[t] - M1);
-    }
-    __syncthreads();
-    if (tid < 16) {
-        const int hsel = tid >> 3, jj = tid & 7;
-        if (hsel < nh) {
-            const float* scp = hsel ? sc1 : sc0;
-            float acc = 0.0f;
-            for (int t = jj; t < n8; t += 8) acc = acc + scp[t];
-            vs8[hsel][jj] = acc;
+    if (wave < nh) {
+        constexpr int KPL = (DPUF_HIP_DEC_MAX_KEYS + 63) / 64;
+        float* sp = wave ? sc1 : sc0;
+        float ev[KPL];
+        float mx = -1e30f;
+#pragma unroll
+        for (int r = 0; r < KPL; r++) {
+            const int t = lane + 64 * r;
+            ev[r] = t < kv_len ? sp[t] : -1e30f;
+            mx = ev[r] > mx ? ev[r] : mx;
         }
-    }
-    __syncthreads();
-    if (tid < nh) {
-        const float* scp = tid ? sc1 : sc0;
-        float sp = hsum8(vs8[tid]);
-        for (int t = n8; t < kv_len; t++) sp += scp[t];
-        inv_sh[tid] = 1.0f / (sp + 1e-12f);
-    }
-    __syncthreads();
-    for (int t = tid; t < kv_len; t += 256) {
-        sc0[t] = sc0[t] * inv_sh[0];
-        if (pair) sc1[t] = sc1[t] * inv_sh[1];
+        mx = wave_max(mx);
+#pragma unroll
+        for (int r = 0; r < KPL; r++) {
+            const int t = lane + 64 * r;
+            if (t < kv_len) {
+                ev[r] = t < n8 ? exp_poly(ev[r] - mx) : expf_libc_tab(ev[r] - mx, etab);
+                sp[t] = ev[r];
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's rows are in LDS
+        __builtin_amdgcn_wave_barrier();
+        float inv = 0.0f;
+        if (lane < 8) {
+            constexpr int NS = DPUF_HIP_DEC_MAX_KEYS / 8;
+            float pv[NS];
+#pragma unroll
+            for (int i = 0; i < NS; i++) pv[i] = lane + 8 * i < n8 ? sp[lane + 8 * i] : 0.0f;
+            float a = 0.0f;
+#pragma unroll
+            for (int i = 0; i < NS; i++)
+                if (lane + 8 * i < n8) a = a + pv[i];
+            vs8[wave][lane] = a;
+        }
+        __builtin_amdgcn_s_waitcnt(0xc07f);
+        __builtin_amdgcn_wave_barrier();
+        if (lane == 0) {
+            float tl[7];  // the tail (at most 7 keys), loaded before its ordered adds
+#pragma unroll
+            for (int i = 0; i < 7; i++) tl[i] = n8 + i < kv_len ? sp[n8 + i] : 0.0f;
+            float su = hsum8(vs8[wave]);
+#pragma unroll
+            for (int i = 0; i < 7; i++)
+                if (n8 + i < kv_len) su += tl[i];
+            inv = 1.0f / (su + 1e-12f);
+        }
+        inv = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(inv)));
+#pragma unroll
+        for (int r = 0; r < KPL; r++) {
+            const int t = lane + 64 * r;
+            if (t < kv_len) sp[t] = ev[r] * inv;
+        }
     }
 
     // P.V over LDS chunks of V (row pos comes from vn); output o = (hsel, d)
@@ -3394,17 +3423,16 @@ __global__ __launch_bounds__(256) void k_attn_dec(const float* __restrict__ q, c
         }
     }
     __syncthreads();
-    // prep of the O input for columns [qh0*HD, (qh0+nh)*HD)
-    if (tid < nh * HD / 16) {
-        const int qp = tid & 3, blk = (qh0 * HD) / 64 + (tid >> 2);
-        float x[16];
+    // prep of the O input for columns [qh0*HD, (qh0+nh)*HD): a wave per
+    // 64-block, a column per lane
 #pragma unroll
-        for (int kk = 0; kk < 16; kk++) x[kk] = aout[16 * tid + kk];
-#pragma unroll
-        for (int kk = 0; kk < 16; kk++)
-            if ((osb >> kk) & 1u) x[kk] = -x[kk];
-        quad_fwht64(x, qp);
-        quad_quant_store(x, qp, blk, op.q, op.s, op.m, op.h);
+    for (int k = 0; k < NPB; k++) {
+        const int b = wave + 4 * k;
+        if (b < nh * HD / 64) {
+            float x = aout[64 * b + lane];
+            if ((osb >> k) & 1u) x = -x;
+            wave_prep64(x, lane, (qh0 * HD) / 64 + b, op.q, op.s, op.m, op.h);
+        }
     }
 }
 
@@ -4377,18 +4405,18 @@ void dpuf_hip_q8_dequant(void* s, DpufKvQ8 c8, size_t off, size_t n, float* k, f
 int32_t dpuf_hip_attn_dec(void* s, int32_t M, const float* q, const float* k, const float* v, const float* q_norm,
                           const float* k_norm, float eps, const float* cos_tab, const float* sin_tab, float* kc,
                           float* vc, const int32_t* pos0, int32_t n_q, int32_t n_kv, int32_t hd, int32_t max_seq,
-                          float scale, float* scores, float* ao, const uint8_t* o_sign, DpufPrep op,
-                          float* const* kcs, float* const* vcs, size_t l_off) {
+                          float scale, float* ao, const uint8_t* o_sign, DpufPrep op, float* const* kcs,
+                          float* const* vcs, size_t l_off) {
     if (M < 1) return -1;
     if (M == 1) op.h = NULL;  // the one-row GEMV reads q only
     const int groups = n_q / n_kv;
-    const int sc_cap = max_seq < 8192 ? max_seq : 8192;
-    const size_t scl = 2 * (size_t)sc_cap > 3 * (size_t)hd ? 2 * (size_t)sc_cap : 3 * (size_t)hd;
+    const size_t scl = 2 * (size_t)DPUF_HIP_DEC_MAX_KEYS > 3 * (size_t)hd ? 2 * (size_t)DPUF_HIP_DEC_MAX_KEYS
+                                                                       : 3 * (size_t)hd;
     const size_t lds = ((size_t)16384 + (size_t)6 * hd + scl) * sizeof(float);
     const dim3 grid(n_kv, (groups + 1) / 2, M);
 #define ATT_LAUNCH(HDV)                                                                                            \
     hipLaunchKernelGGL(k_attn_dec<HDV>, grid, dim3(256), lds, ST(s), q, k, v, q_norm, k_norm, eps, cos_tab, sin_tab, \
-                       kc, vc, pos0, n_q, n_kv, max_seq, scale, sc_cap, scores, ao, o_sign, op, kcs, vcs, l_off)
+                       kc, vc, pos0, n_q, n_kv, max_seq, scale, ao, o_sign, op, kcs, vcs, l_off)
     switch (hd) {
         case 64: ATT_LAUNCH(64); break;
         case 128: ATT_LAUNCH(128); break;
