@@ -238,6 +238,92 @@ DEV void i8x4_to_h(uint32_t x, uint32_t& a, uint32_t& b) {
     b = gm_sub(gm_pair(u, 0x04030402u), (_Float16)1152.0f);
 }
 
+// Activation prep of one 64-block by the 16 lanes of a DPP row, lane r of
+// the row holding columns 4r .. 4r + 3 in x[0..3]: FWHT strides 1 and 2
+// inside the lane, strides 4, 8, 16, 32 between lanes r ^ 1, r ^ 2, r ^ 4,
+// r ^ 8 (the moves of wave_prep64), the same butterflies in the same order
+// as quad_fwht64; then the quantisation of quad_quant_store with the
+// 32-block (lanes 0-7 or 8-15 of the row) maximum and sum over r ^ 1, r ^ 2
+// and the half-row mirror.  All 16 lanes of the row must be active.
+DEV void row_prep64(float* x, int r, int blk, int8_t* q, float* s, int32_t* m, uint16_t* h) {
+    {
+        float a = x[0], b = x[1];
+        x[0] = a + b;
+        x[1] = a - b;
+        a = x[2];
+        b = x[3];
+        x[2] = a + b;
+        x[3] = a - b;
+        a = x[0];
+        b = x[2];
+        x[0] = a + b;
+        x[2] = a - b;
+        a = x[1];
+        b = x[3];
+        x[1] = a + b;
+        x[3] = a - b;
+    }
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const float p = DPP_F(x[k], 0xB1);  // column stride 4: lane r ^ 1
+        x[k] = (r & 1) ? p - x[k] : x[k] + p;
+    }
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const float p = DPP_F(x[k], 0x4E);  // stride 8: r ^ 2
+        x[k] = (r & 2) ? p - x[k] : x[k] + p;
+    }
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const float r4 = DPP_F(x[k], 0x124), r12 = DPP_F(x[k], 0x12C);  // stride 16: r ^ 4
+        const float p = (r & 4) ? r4 : r12;
+        x[k] = (r & 4) ? p - x[k] : x[k] + p;
+    }
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const float p = DPP_F(x[k], 0x128);  // stride 32: r ^ 8
+        x[k] = (r & 8) ? p - x[k] : x[k] + p;
+    }
+#pragma unroll
+    for (int k = 0; k < 4; k++) x[k] = x[k] * 0.125f;
+    float amax = fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3])));
+    amax = fmaxf(amax, DPP_F(amax, 0xB1));
+    amax = fmaxf(amax, DPP_F(amax, 0x4E));
+    amax = fmaxf(amax, DPP_F(amax, 0x141));
+    int32_t qi[4] = {0, 0, 0, 0};
+    float d = 0.0f;
+    if (!(amax <= 1e-4f)) {
+        d = amax / 127.0f;
+        const float inv = (amax > 1e-12f) ? (127.0f / amax) : 0.0f;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const float xs = x[k] * inv;
+            int32_t v;
+            if (!(xs > -2147483648.0f && xs < 2147483648.0f)) v = -127;  // cvtps -> INT_MIN -> -127
+            else v = (int32_t)rintf(xs);
+            v = v > 127 ? 127 : v;
+            qi[k] = v < -127 ? -127 : v;
+        }
+    }
+    int32_t sum = (qi[0] + qi[1]) + (qi[2] + qi[3]);
+    sum += DPP_I(sum, 0xB1);
+    sum += DPP_I(sum, 0x4E);
+    sum += DPP_I(sum, 0x141);
+    const uint32_t w = (uint32_t)(qi[0] & 0xFF) | ((uint32_t)(qi[1] & 0xFF) << 8) | ((uint32_t)(qi[2] & 0xFF) << 16) |
+                       ((uint32_t)(qi[3] & 0xFF) << 24);
+    *(uint32_t*)(q + 64 * blk + 4 * r) = w;
+    if (h) {
+        uint32_t a, b;
+        i8x4_to_h(w, a, b);
+        *(uint2*)(h + 64 * blk + 4 * r) = make_uint2(a, b);
+    }
+    if ((r & 7) == 0) {
+        s[2 * blk + (r >> 3)] = d;
+        m[2 * blk + (r >> 3)] = sum * 8;
+    }
+}
+
+
 DEV void quad_quant_store(const float* v, int qp, int blk, int8_t* q, float* s, int32_t* m, uint16_t* h) {
     float amax = 0.0f;
 #pragma unroll

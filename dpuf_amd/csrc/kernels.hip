@@ -281,28 +281,29 @@ __global__ __launch_bounds__(256) void k_prep(int K, const float* __restrict__ x
 
 // SwiGLU with dead zone (reference swiglu_range_avx2, 8-wide path,
 // dpuf_engine.c:976-989) fused with the prep of the down projection's input.
-// grid: (ceil(I/16/256), M).
-__global__ __launch_bounds__(256) void k_swiglu_prep(int I, const float* __restrict__ gate, const float* __restrict__ up,
-                                                     float dz, const uint8_t* __restrict__ sign, DpufPrep p) {
-    const int m = blockIdx.y, t = blockIdx.x * blockDim.x + threadIdx.x;
-    if (16 * t >= I) return;
-    const int qp = t & 3, blk = t >> 2, nb = I >> 5;
-    float g[16], u[16], v[16];
-    load16(gate + (size_t)m * I + 16 * t, g);
-    load16(up + (size_t)m * I + 16 * t, u);
-    const uint32_t sb = quad_sign_bits(sign, blk, qp);
+// A 64-block per 16-lane row, 4 columns per lane (row_prep64): a quarter of
+// the per-lane work of a quad per block, which is what bounds this
+// latency-bound step.  grid: (ceil(I / 256), M), one wave per workgroup.
+__global__ __launch_bounds__(64) void k_swiglu_prep(int I, const float* __restrict__ gate, const float* __restrict__ up,
+                                                    float dz, const uint8_t* __restrict__ sign, DpufPrep p) {
+    const int m = blockIdx.y, t = blockIdx.x * 64 + threadIdx.x;
+    const int blk = t >> 4, r = t & 15, nb = I >> 5;
+    if (64 * blk >= I) return;  // whole rows: I is a multiple of 64
+    const float4 g4 = *(const float4*)(gate + (size_t)m * I + 4 * t);
+    const float4 u4 = *(const float4*)(up + (size_t)m * I + 4 * t);
+    const uint32_t sb = sign ? (sign[8 * blk + (r >> 1)] >> (4 * (r & 1))) & 0xFu : 0u;
+    const float g[4] = {g4.x, g4.y, g4.z, g4.w}, u[4] = {u4.x, u4.y, u4.z, u4.w};
+    float v[4];
 #pragma unroll
-    for (int k = 0; k < 16; k++) {
+    for (int k = 0; k < 4; k++) {
         const float ng = fmaxf(-40.0f, fminf(0.0f - g[k], 40.0f));
         const float silu = g[k] / (1.0f + exp_poly(ng));
-        float r = silu * u[k];
-        if (dz > 0.0f && !(fabsf(r) >= dz)) r = 0.0f;
-        v[k] = r;
+        float rr = silu * u[k];
+        if (dz > 0.0f && !(fabsf(rr) >= dz)) rr = 0.0f;
+        v[k] = ((sb >> k) & 1u) ? -rr : rr;
     }
-    apply_sign_bits(v, sb);
-    quad_fwht64(v, qp);
-    quad_quant_store(v, qp, blk, p.q + (size_t)m * I, p.s + (size_t)m * nb, p.m + (size_t)m * nb,
-                     p.h ? p.h + (size_t)m * I : nullptr);
+    row_prep64(v, r, blk, p.q + (size_t)m * I, p.s + (size_t)m * nb, p.m + (size_t)m * nb,
+               p.h ? p.h + (size_t)m * I : nullptr);
 }
 
 // ---------------------------------------------------------------------------
@@ -3858,9 +3859,8 @@ void dpuf_hip_prep(void* s, int32_t M, int32_t K, const float* x, const uint8_t*
 
 void dpuf_hip_swiglu_prep(void* s, int32_t M, int32_t I, const float* gate, const float* up, float dz,
                           const uint8_t* sign, DpufPrep p) {
-    const int quads = I / 16;
     if (M == 1) p.h = NULL;
-    hipLaunchKernelGGL(k_swiglu_prep, dim3((quads + 63) / 64, M), dim3(64), 0, ST(s), I, gate, up, dz, sign, p);
+    hipLaunchKernelGGL(k_swiglu_prep, dim3((I + 255) / 256, M), dim3(64), 0, ST(s), I, gate, up, dz, sign, p);
     LAUNCHED("k_swiglu_prep");
 }
 
