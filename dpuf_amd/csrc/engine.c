@@ -54,6 +54,10 @@ typedef struct {
     int32_t plen[N_PREFIX], pcap[N_PREFIX], pvalid[N_PREFIX];
     /* scratch for up to DPUF_AMD_MAX_BATCH rows */
     float *h, *hn, *q, *k, *v, *ao, *gate, *up, *logits, *scores, *embeds, *capture;
+    /* the residual stream alternates between h and h2: each residual add
+     * reads one and writes the other (its kernel's workgroups all read the
+     * old stream); hcur is the current one while a step is enqueued */
+    float *h2, *hcur;
     int32_t capture_cap;
     DpufPrep prep[3];
     int32_t *d_ids, *d_pos0, *d_flag, *d_tok, *d_err;
@@ -440,7 +444,8 @@ static void engine_free(Engine* e) {
     dpuf_hip_free(e->d_out_norm); dpuf_hip_free(e->d_cos); dpuf_hip_free(e->d_sin);
     for (int s = 0; s < N_SLOTS; s++) kv_free(e->kv[s]);
     for (int p = 0; p < N_PREFIX; p++) kv_free(e->pkv[p]);
-    float* bufs[] = {e->h, e->hn, e->q, e->k, e->v, e->ao, e->gate, e->up, e->logits, e->scores, e->embeds, e->capture};
+    float* bufs[] = {e->h, e->h2, e->hn, e->q, e->k, e->v, e->ao, e->gate, e->up, e->logits, e->scores, e->embeds,
+                     e->capture};
     for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++) dpuf_hip_free(bufs[i]);
     for (int i = 0; i < 3; i++) {
         dpuf_hip_free(e->prep[i].q);
@@ -546,6 +551,7 @@ DPUF_EXPORT void* dpuf_engine_create(const DpufModelConfig* cfg, const DpufLayer
         int32_t maxd = e->H > e->I ? e->H : e->I;
         if (e->qd > maxd) maxd = e->qd;
         e->h = (float*)dpuf_hip_malloc(B * e->H * 4);
+        e->h2 = (float*)dpuf_hip_malloc(B * e->H * 4);
         e->hn = (float*)dpuf_hip_malloc(B * e->H * 4);
         e->q = (float*)dpuf_hip_malloc(B * e->qd * 4);
         e->k = (float*)dpuf_hip_malloc(B * e->kvd * 4);
@@ -571,7 +577,7 @@ DPUF_EXPORT void* dpuf_engine_create(const DpufModelConfig* cfg, const DpufLayer
         e->d_ms_vc = e->d_ms_kc + B;
         e->d_ms_pos = (int32_t*)(e->d_ms_vc + B);
         e->d_ms_tok = e->d_ms_pos + B;
-        if (!e->h || !e->hn || !e->q || !e->k || !e->v || !e->ao || !e->gate || !e->up || !e->logits ||
+        if (!e->h || !e->h2 || !e->hn || !e->q || !e->k || !e->v || !e->ao || !e->gate || !e->up || !e->logits ||
             !e->scores || !e->embeds || !e->d_ids || !e->h_pinned || !e->d_red)
             goto fail;
         e->d_pos0 = e->d_ids + B;
@@ -715,6 +721,7 @@ static void enqueue_head(Engine* e, int32_t M, int32_t only_last, int32_t early_
 static void enqueue_forward(Engine* e, int32_t M, int32_t use_embeds, int32_t only_last, int32_t keep_tiles,
                             int32_t early_tiles, float early_margin, int32_t want_argmax) {
     dpuf_hip_embed(e->stream, e->tok, e->d_ids, M, use_embeds ? e->embeds : NULL, e->h);
+    e->hcur = e->h;
     enqueue_layers(e, M, keep_tiles);
     enqueue_head(e, M, only_last, early_tiles, early_margin, want_argmax);
 }
@@ -722,7 +729,10 @@ static void enqueue_forward(Engine* e, int32_t M, int32_t use_embeds, int32_t on
 /* Layer loop: residual + RMSNorm + prep, fused Q/K/V GEMV, attention (for
  * M == 1 one kernel with QK-norm, RoPE, the KV store and the O-input prep),
  * O GEMV, residual + RMSNorm + prep, fused gate/up GEMV, SwiGLU + prep, down
- * GEMV; the residual stream lives in e->h and the last projection in e->hn. */
+ * GEMV; the residual stream is e->hcur (e->h or e->h2) and the last projection
+ * e->hn. */
+static float* h_other(const Engine* e) { return e->hcur == e->h ? e->h2 : e->h; }
+
 static void enqueue_layers(Engine* e, int32_t M, int32_t keep_tiles) {
     void* s = e->stream;
     const int32_t H = e->H, I = e->I;
@@ -742,7 +752,10 @@ static void enqueue_layers(Engine* e, int32_t M, int32_t keep_tiles) {
             const uint8_t* ps[3] = {NULL, NULL, NULL};
             for (int k = 2; k >= 0; k--) ps[qi[k]] = signs[k];
             const int tm1 = tm_begin(e, K_PREP, 0);
-            dpuf_hip_resnorm_prep(s, M, H, e->h, l > 0 ? e->hn : NULL, e->d_norm[4 * l], eps, np, ps, e->prep, NULL);
+            float* ho = l > 0 ? h_other(e) : NULL;
+            dpuf_hip_resnorm_prep(s, M, H, e->hcur, l > 0 ? e->hn : NULL, ho, e->d_norm[4 * l], eps, np, ps, e->prep,
+                                  NULL);
+            if (ho) e->hcur = ho;
             tm_end(e, tm1);
         }
         /* (2) Q, K, V in one launch */
@@ -807,7 +820,9 @@ static void enqueue_layers(Engine* e, int32_t M, int32_t keep_tiles) {
             int32_t np = qi[4] ? 2 : 1;
             const uint8_t* ps[2] = {W[W_GATE].sign, W[W_UP].sign};
             const int tm6 = tm_begin(e, K_PREP, 0);
-            dpuf_hip_resnorm_prep(s, M, H, e->h, e->hn, e->d_norm[4 * l + 3], eps, np, ps, e->prep, NULL);
+            float* ho = h_other(e);
+            dpuf_hip_resnorm_prep(s, M, H, e->hcur, e->hn, ho, e->d_norm[4 * l + 3], eps, np, ps, e->prep, NULL);
+            e->hcur = ho;
             tm_end(e, tm6);
         }
         /* (7) gate + up in one launch */
@@ -839,7 +854,7 @@ static void enqueue_layers(Engine* e, int32_t M, int32_t keep_tiles) {
             tm_end(e, tm9);
         }
         if (e->capture && M <= e->capture_cap)
-            dpuf_hip_capture(s, M, H, e->h, e->hn, e->capture + (size_t)l * e->capture_cap * H);
+            dpuf_hip_capture(s, M, H, e->hcur, e->hn, e->capture + (size_t)l * e->capture_cap * H);
     }
 }
 
@@ -855,8 +870,8 @@ static void enqueue_head(Engine* e, int32_t M, int32_t only_last, int32_t early_
     {
         const uint8_t* ps[1] = {e->lm.sign};
         const int tm10 = tm_begin(e, K_PREP, 0);
-        dpuf_hip_resnorm_prep(s, lmM, H, e->h + (size_t)lm0 * H, e->L > 0 ? e->hn + (size_t)lm0 * H : NULL,
-                              e->d_out_norm, eps, 1, ps, e->prep, NULL);
+        dpuf_hip_resnorm_prep(s, lmM, H, e->hcur + (size_t)lm0 * H, e->L > 0 ? e->hn + (size_t)lm0 * H : NULL,
+                              h_other(e) + (size_t)lm0 * H, e->d_out_norm, eps, 1, ps, e->prep, NULL);
         tm_end(e, tm10);
     }
     const int32_t nt = n_tiles_of(&e->lm);

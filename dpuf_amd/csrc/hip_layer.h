@@ -95,7 +95,12 @@ void dpuf_hip_graph_destroy(void* g);
  * any position. */
 void dpuf_hip_embed(void* s, DpufDevW w, const int32_t* ids, int32_t M, const float* embeds,
                     float* out);
-void dpuf_hip_resnorm_prep(void* s, int32_t M, int32_t H, float* h, const float* res,
+/* h_out = h + res for M rows of H (res NULL: no add, h_out unused), then
+ * the RMSNorm of that sum (of h when res is NULL) with weights w and the
+ * prep of the result for each of the n_prep sign vectors into preps[i] (and
+ * into xn_out when non-NULL).  h_out may equal h, at the cost of the
+ * one-workgroup-per-row form. */
+void dpuf_hip_resnorm_prep(void* s, int32_t M, int32_t H, const float* h, const float* res, float* h_out,
                            const float* w, float eps, int32_t n_prep, const uint8_t* const* signs,
                            const DpufPrep* preps, float* xn_out);
 void dpuf_hip_prep(void* s, int32_t M, int32_t K, const float* x, const uint8_t* sign, DpufPrep p);

@@ -175,26 +175,45 @@ __global__ void k_embed(DpufDevW w, const int32_t* __restrict__ ids, const float
 // elements j, j+8, j+16, ... in order) and its hsum tree; a transposed LDS
 // copy gives each of the 8 chain lanes its elements contiguously.
 // ---------------------------------------------------------------------------
-template <int SEG>
-__global__ __launch_bounds__(1024) void k_resnorm_prep(int H, float* __restrict__ h, const float* __restrict__ res,
-                                                       const float* __restrict__ w, float eps, PrepSet ps,
-                                                       float* __restrict__ xn_out) {
+//
+// G = 4 (H a multiple of 256, no xn_out): four workgroups per row
+// (blockIdx.y), each running the whole sum chain and then the prep of a
+// quarter of the row's 64-blocks, a block per 16-lane row with 4 columns
+// per lane (row_prep64): the prep's per-lane work, which bounds it, is a
+// sixteenth of one workgroup doing every block by lane quads.  Every
+// workgroup reads h + res, so the sum goes to h_out (not in place); each
+// writes its quarter.
+template <int SEG, int G>
+__global__ __launch_bounds__(1024) void k_resnorm_prep(int H, const float* h, const float* __restrict__ res, float* h_out,
+                                                       const float* __restrict__ w,
+                                                       float eps, PrepSet ps, float* __restrict__ xn_out) {
     extern __shared__ float tr[];  // [8][H/8 + 4]
     __shared__ float part[8];
     const int m = blockIdx.x, t = threadIdx.x, qp = t & 3, blk = t >> 2, nb = H >> 5;
     const int L = (H >> 3) + 4;
+    const int T = H >> 4;  // threads
     float v[16], wv[16];
     uint32_t sb[3];
-    float* hr = h + (size_t)m * H + 16 * t;
-    load16(hr, v);
-    load16(w + 16 * t, wv);
-    for (int p = 0; p < 3; p++) sb[p] = p < ps.n ? quad_sign_bits(ps.sign[p], blk, qp) : 0u;
+    // G = 4: block b4 of the row (a quarter's 16-lane rows), lane r4, its
+    // 4 columns, their norm weights and sign bits
+    const int b4 = (int)blockIdx.y * (H >> 8) + (t >> 4), r4 = t & 15, c4 = 64 * b4 + 4 * r4;
+    float4 w4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    load16(h + (size_t)m * H + 16 * t, v);
+    if (G == 1) {
+        load16(w + 16 * t, wv);
+        for (int p = 0; p < 3; p++) sb[p] = p < ps.n ? quad_sign_bits(ps.sign[p], blk, qp) : 0u;
+    } else {
+        w4 = *(const float4*)(w + c4);
+        for (int p = 0; p < 3; p++)
+            sb[p] = p < ps.n && ps.sign[p] ? (ps.sign[p][8 * b4 + (r4 >> 1)] >> (4 * (r4 & 1))) & 0xFu : 0u;
+    }
     if (res) {
         float r[16];
         load16(res + (size_t)m * H + 16 * t, r);
 #pragma unroll
         for (int k = 0; k < 16; k++) v[k] = v[k] + r[k];
-        store16(hr, v);
+        if (G == 1 || (t >> 2) / (T >> 4) == (int)blockIdx.y)  // this workgroup's quarter
+            store16(h_out + (size_t)m * H + 16 * t, v);
     }
 #pragma unroll
     for (int k = 0; k < 8; k++) *(float2*)(tr + k * L + 2 * t) = make_float2(v[k], v[k + 8]);
@@ -251,6 +270,21 @@ __global__ __launch_bounds__(1024) void k_resnorm_prep(int H, float* __restrict_
     }
     __syncthreads();
     const float inv = 1.0f / sqrtf(hsum8(part) / (float)H + eps);
+    if (G > 1) {
+        // element e of the row is tr[(e % 8) L + e / 8]
+        const float wk[4] = {w4.x, w4.y, w4.z, w4.w};
+        float x0[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) x0[k] = (tr[((c4 + k) & 7) * L + ((c4 + k) >> 3)] * inv) * wk[k];
+        for (int p = 0; p < ps.n; p++) {
+            float y[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++) y[k] = ((sb[p] >> k) & 1u) ? -x0[k] : x0[k];
+            row_prep64(y, r4, b4, ps.p[p].q + (size_t)m * H, ps.p[p].s + (size_t)m * nb, ps.p[p].m + (size_t)m * nb,
+                       ps.p[p].h ? ps.p[p].h + (size_t)m * H : nullptr);
+        }
+        return;
+    }
 #pragma unroll
     for (int k = 0; k < 16; k++) v[k] = (v[k] * inv) * wv[k];
     if (xn_out) store16(xn_out + (size_t)m * H + 16 * t, v);
@@ -3829,8 +3863,13 @@ void dpuf_hip_embed(void* s, DpufDevW w, const int32_t* ids, int32_t M, const fl
     LAUNCHED("k_embed");
 }
 
-void dpuf_hip_resnorm_prep(void* s, int32_t M, int32_t H, float* h, const float* res, const float* w, float eps,
-                           int32_t n_prep, const uint8_t* const* signs, const DpufPrep* preps, float* xn_out) {
+void dpuf_hip_resnorm_prep(void* s, int32_t M, int32_t H, const float* h, const float* res, float* h_out,
+                           const float* w, float eps, int32_t n_prep, const uint8_t* const* signs,
+                           const DpufPrep* preps, float* xn_out) {
+    if (res && !h_out) {
+        note(hipErrorInvalidValue, "dpuf_hip_resnorm_prep: a residual add needs h_out");
+        return;
+    }
     PrepSet ps;
     memset(&ps, 0, sizeof ps);
     ps.n = n_prep;
@@ -3843,9 +3882,18 @@ void dpuf_hip_resnorm_prep(void* s, int32_t M, int32_t H, float* h, const float*
     const size_t lds = (size_t)8 * ((H >> 3) + 4) * sizeof(float);
     // register-fed chains for the widths with a 16-byte-aligned segment
     // (8 * (H / 8 + 4) floats per row keeps segments of 16, 32, 64 aligned)
-    auto k = H == 4096 ? k_resnorm_prep<64> : H == 2048 ? k_resnorm_prep<32> : H == 1024 ? k_resnorm_prep<16>
-                                                                                          : k_resnorm_prep<0>;
-    hipLaunchKernelGGL(k, dim3(M), dim3(threads), lds, ST(s), H, h, res, w, eps, ps, xn_out);
+    // four workgroups per row when the row splits into quarters of whole
+    // 16-lane rows of blocks (and no normalised copy is asked for)
+    const bool split = H % 256 == 0 && !xn_out && !(res && h_out == h);
+    auto k = split ? (H == 4096   ? k_resnorm_prep<64, 4>
+                      : H == 2048 ? k_resnorm_prep<32, 4>
+                      : H == 1024 ? k_resnorm_prep<16, 4>
+                                  : k_resnorm_prep<0, 4>)
+                   : (H == 4096   ? k_resnorm_prep<64, 1>
+                      : H == 2048 ? k_resnorm_prep<32, 1>
+                      : H == 1024 ? k_resnorm_prep<16, 1>
+                                  : k_resnorm_prep<0, 1>);
+    hipLaunchKernelGGL(k, dim3(M, split ? 4 : 1), dim3(threads), lds, ST(s), H, h, res, h_out, w, eps, ps, xn_out);
     LAUNCHED("k_resnorm_prep");
 }
 
