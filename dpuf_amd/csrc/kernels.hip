@@ -556,6 +556,23 @@ struct MvGeo {
 // the call, reports the call as failed.
 DEV void mv_wait_failed(int32_t* err) { atomicOr(err, 1); }
 
+// Waits until *p == want, at most 2^22 polls; false when it ran out.  The
+// polled value is made wave-uniform, so the loop is a scalar loop: a
+// per-lane loop condition made the compiler unroll the waits eightfold with
+// an exec mask per step, doubling the kernel's SGPRs (one wave per SIMD
+// fewer) and its code.
+template <typename T>
+DEV bool mv_wait(T* p, T want) {
+    int spins = 0;
+#pragma clang loop unroll(disable)
+    while ((T)__builtin_amdgcn_readfirstlane((int)__hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) !=
+           want) {
+        if (++spins >= (1 << 22)) return false;
+        __builtin_amdgcn_s_sleep(1);
+    }
+    return true;
+}
+
 // Loads are unconditional (indices clamped into the group), so the number of
 // memory operations in flight is the same on every path and the wait for one
 // unit never includes the next unit's loads.
@@ -657,11 +674,7 @@ DEV void mv_consume(const MvGeo& G, int u, int w, int lane, const MvU<NL>& L, co
     float2* pairs = (float2*)smem + (size_t)buf * 8 * G.ld;
     if (r == 0 && lg >= G.nbuf) {
         // the buffer is free once the chains of group lg - nbuf have read it
-        int spins = 0;
-        while (__hip_atomic_load(&sy->done[buf], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != lg - G.nbuf &&
-               ++spins < (1 << 22))
-            __builtin_amdgcn_s_sleep(1);
-        if (spins >= (1 << 22) && lane == 0) mv_wait_failed(G.err);
+        if (!mv_wait(&sy->done[buf], (int32_t)(lg - G.nbuf)) && lane == 0) mv_wait_failed(G.err);
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
     }
     mv_dots<NL, HOIST, MODE>(G, r, w, lane, L, X0, pairs);
@@ -683,11 +696,7 @@ DEV void mv_chains(const MvGeo& G, int c, int n_my, int lane, uint8_t* smem, MvS
         // complete at NW * (lg / nbuf + 1), and the next use cannot start
         // arriving before this group's chains free the buffer
         const uint32_t want = (uint32_t)G.NW * (uint32_t)(lg / G.nbuf + 1);
-        int spins = 0;
-        while (__hip_atomic_load(&sy->cnt[buf], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != want &&
-               ++spins < (1 << 22))
-            __builtin_amdgcn_s_sleep(1);
-        if (spins >= (1 << 22) && lane == 0) mv_wait_failed(G.err);
+        if (!mv_wait(&sy->cnt[buf], want) && lane == 0) mv_wait_failed(G.err);
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
         __builtin_amdgcn_s_setprio(2);
         if (lane < 8) {
