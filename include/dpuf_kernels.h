@@ -83,7 +83,7 @@ typedef struct {
     float   rope_low_freq;
     float   rope_high_freq;
     int32_t rope_orig_max_pos;
-    int32_t kv_type;            /* DPUF_KV_F32 only                              */
+    int32_t kv_type;            /* DPUF_KV_F32 or DPUF_KV_Q8 (int8 per 32 values) */
     int32_t has_mrope;          /* must be 0 (multimodal RoPE is not built)      */
     int32_t mrope_section[3];
     int32_t mrope_interleaved;
