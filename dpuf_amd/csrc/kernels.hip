@@ -2249,36 +2249,46 @@ __global__ __launch_bounds__(256) void k_attn_smx(float* __restrict__ S, const i
 #define PVW_LD (PVW_CK + 4)  // LDS row stride of a chunk (rows on distinct banks)
 
 // a = fma(p[t], v[t], a) over the first n keys of a chunk, in order; p and v
-// are 16-byte aligned LDS rows.  A full chunk is unrolled, so the compiler
-// counts outstanding LDS reads exactly; a partial chunk takes the loop.
+// are 16-byte aligned LDS rows.  A full chunk is unrolled in 8-key blocks,
+// each block's four 16-byte reads issued three blocks ahead: at most 12 LDS
+// reads are in flight, within what the LDS wait counter can express (15), so
+// every wait is for exactly the block about to be used (with 16 in flight the
+// compiler fell back to waiting for all of them).  A partial chunk takes the
+// loop.
 DEV float pvw_chunk(const float* p, const float* v, int n, float a) {
     if (n == PVW_CK) {
-        constexpr int NB = PVW_CK / 16;
-        float4 pb[3][4], vb[3][4];
+        constexpr int NB = PVW_CK / 8, AH = 3;
+        float4 pb[AH + 1][2], vb[AH + 1][2];
 #pragma unroll
-        for (int k = 0; k < 2; k++)
+        for (int k = 0; k < AH; k++)
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                pb[k][i] = *(const float4*)(p + 16 * k + 4 * i);
-                vb[k][i] = *(const float4*)(v + 16 * k + 4 * i);
+            for (int i = 0; i < 2; i++) {
+                pb[k][i] = *(const float4*)(p + 8 * k + 4 * i);
+                vb[k][i] = *(const float4*)(v + 8 * k + 4 * i);
             }
+        // the schedule is pinned (the scheduler otherwise moved each block's
+        // reads down to just before its FMAs): the prologue's reads, then per
+        // block the next reads followed by its 8 FMAs
+        __builtin_amdgcn_sched_group_barrier(0x100, 4 * AH, 0);
 #pragma unroll
         for (int b = 0; b < NB; b++) {
-            const int cur = b % 3;
-            if (b + 2 < NB) {
+            const int cur = b % (AH + 1);
+            if (b + AH < NB) {
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    pb[(b + 2) % 3][i] = *(const float4*)(p + 16 * (b + 2) + 4 * i);
-                    vb[(b + 2) % 3][i] = *(const float4*)(v + 16 * (b + 2) + 4 * i);
+                for (int i = 0; i < 2; i++) {
+                    pb[(b + AH) % (AH + 1)][i] = *(const float4*)(p + 8 * (b + AH) + 4 * i);
+                    vb[(b + AH) % (AH + 1)][i] = *(const float4*)(v + 8 * (b + AH) + 4 * i);
                 }
+                __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
             }
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
+            for (int i = 0; i < 2; i++) {
                 a = fmaf(pb[cur][i].x, vb[cur][i].x, a);
                 a = fmaf(pb[cur][i].y, vb[cur][i].y, a);
                 a = fmaf(pb[cur][i].z, vb[cur][i].z, a);
                 a = fmaf(pb[cur][i].w, vb[cur][i].w, a);
             }
+            __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
         }
         return a;
     }
