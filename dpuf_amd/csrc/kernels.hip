@@ -2301,37 +2301,60 @@ DEV float pvw_chunk(const float* p, const float* v, int n, float a) {
 // c0 + 128 + pl, the key's 4 dims each (16 bytes); P 16-byte pieces 4 pl and
 // 4 pl + 512 of the chunk's [GM][PVW_CK] block (heads past G read head G - 1,
 // keys clamped into the row).
-template <int HD, int GM>
-DEV void pvw_load(const float* Vh, const float* Ph, int c, int nck, int G, int max_seq, int pl,
-                  gm_f4 (&r)[2 + GM / 2]) {
+//
+// Q8 (the int8 KV cache): V comes as 4 int8 per key (in r[i].x) and the lane
+// also loads the V scales of its P pieces' 4 keys (r[2 + GM / 2]; every piece
+// of a lane covers the same keys), so the store can write W = p * vs (the
+// reference's p * v_scale, dpuf_engine.c:726-747) in p's place and V widened
+// to floats (exact).
+template <int HD, int GM, bool Q8>
+DEV void pvw_load(const float* Vh, const float* Ph, const int8_t* Vq, const float* Vs, int c, int nck, int G,
+                  int max_seq, int pl, gm_f4 (&r)[3 + GM / 2]) {
     const int c0 = (c < nck ? c : nck - 1) * PVW_CK;
 #pragma unroll
     for (int i = 0; i < 2; i++) {
         const int key = min(c0 + 128 * i + pl, max_seq - 1);
-        r[i] = *(const gm_f4*)(Vh + (size_t)key * HD);
+        if (Q8) r[i][0] = __int_as_float(*(const int32_t*)(Vq + (size_t)key * HD));
+        else r[i] = *(const gm_f4*)(Vh + (size_t)key * HD);
     }
 #pragma unroll
     for (int i = 0; i < GM / 2; i++) {
         const int f = 512 * i + 4 * pl, hh = min(f / PVW_CK, G - 1), t = min(c0 + f % PVW_CK, max_seq - 4);
         r[2 + i] = *(const gm_f4*)(Ph + (size_t)hh * max_seq + t);
     }
+    if (Q8) {
+        const int t = min(c0 + (4 * pl) % PVW_CK, max_seq - 4);
+#pragma unroll
+        for (int k = 0; k < 4; k++) r[2 + GM / 2][k] = Vs[(size_t)(t + k) * (HD / 32)];
+    }
 }
 
 // A producer lane's chunk into an LDS slot, V transposed to [dim][key].
-template <int GM>
-DEV void pvw_store(float (*Vt)[PVW_LD], float (*Pt)[PVW_LD], int pl, const gm_f4 (&r)[2 + GM / 2]) {
+template <int GM, bool Q8>
+DEV void pvw_store(float (*Vt)[PVW_LD], float (*Pt)[PVW_LD], int pl, const gm_f4 (&r)[3 + GM / 2]) {
 #pragma unroll
     for (int i = 0; i < 2; i++) {
         const int k = 128 * i + pl;
-        Vt[0][k] = r[i][0];
-        Vt[1][k] = r[i][1];
-        Vt[2][k] = r[i][2];
-        Vt[3][k] = r[i][3];
+        if (Q8) {
+            const int32_t b = __float_as_int(r[i][0]);
+#pragma unroll
+            for (int dd = 0; dd < 4; dd++) Vt[dd][k] = (float)(int8_t)(b >> (8 * dd));
+        } else {
+            Vt[0][k] = r[i][0];
+            Vt[1][k] = r[i][1];
+            Vt[2][k] = r[i][2];
+            Vt[3][k] = r[i][3];
+        }
     }
 #pragma unroll
     for (int i = 0; i < GM / 2; i++) {
         const int f = 512 * i + 4 * pl;
-        *(gm_f4*)&Pt[f / PVW_CK][f % PVW_CK] = r[2 + i];
+        gm_f4 w = r[2 + i];
+        if (Q8) {
+#pragma unroll
+            for (int k = 0; k < 4; k++) w[k] = w[k] * r[2 + GM / 2][k];
+        }
+        *(gm_f4*)&Pt[f / PVW_CK][f % PVW_CK] = w;
     }
 }
 
@@ -2342,25 +2365,27 @@ DEV void pvw_store(float (*Vt)[PVW_LD], float (*Pt)[PVW_LD], int pl, const gm_f4
 // register set c % 4 four chunks ahead and written to LDS slot c % 2 one
 // chunk ahead of its chains, one barrier per chunk.  The loop is unrolled by
 // 4 so every register set index is static.
-template <int HD, int GM>
+template <int HD, int GM, bool Q8>
 __global__ __launch_bounds__(192) void k_attn_pvw(const float* __restrict__ P, const float* __restrict__ vc,
                                                   const int32_t* __restrict__ pos0p, int n_q, int n_kv,
-                                                  int max_seq, float* __restrict__ out) {
+                                                  int max_seq, float* __restrict__ out, DpufKvQ8 c8) {
     static_assert(GM >= 2 && GM * 4 <= 64 && GM % 2 == 0, "lane layout");
     __shared__ __align__(16) float Vt[2][4][PVW_LD];
     __shared__ __align__(16) float Pt[2][GM][PVW_LD];
     const int kvh = blockIdx.x, d0 = blockIdx.y * 4, tid = threadIdx.x, w = tid >> 6;
     const int G = n_q / n_kv, h = tid >> 2, d = tid & 3, pl = tid - 64;
     const int L = *pos0p + 1, nck = (L + PVW_CK - 1) / PVW_CK;
-    const float* Vh = vc + (size_t)kvh * max_seq * HD + d0;
+    const float* Vh = Q8 ? nullptr : vc + (size_t)kvh * max_seq * HD + d0;
+    const int8_t* Vq = Q8 ? c8.vq + (size_t)kvh * max_seq * HD + d0 : nullptr;
+    const float* Vs = Q8 ? c8.vs + (size_t)kvh * max_seq * (HD / 32) + d0 / 32 : nullptr;
     const float* Ph = P + (size_t)kvh * G * max_seq;
-    gm_f4 r0[2 + GM / 2], r1[2 + GM / 2], r2[2 + GM / 2], r3[2 + GM / 2];  // native vectors: no struct copies
+    gm_f4 r0[3 + GM / 2], r1[3 + GM / 2], r2[3 + GM / 2], r3[3 + GM / 2];  // native vectors: no struct copies
     if (w > 0) {
-        pvw_load<HD, GM>(Vh, Ph, 0, nck, G, max_seq, pl, r0);
-        pvw_load<HD, GM>(Vh, Ph, 1, nck, G, max_seq, pl, r1);
-        pvw_load<HD, GM>(Vh, Ph, 2, nck, G, max_seq, pl, r2);
-        pvw_load<HD, GM>(Vh, Ph, 3, nck, G, max_seq, pl, r3);
-        pvw_store<GM>(Vt[0], Pt[0], pl, r0);
+        pvw_load<HD, GM, Q8>(Vh, Ph, Vq, Vs, 0, nck, G, max_seq, pl, r0);
+        pvw_load<HD, GM, Q8>(Vh, Ph, Vq, Vs, 1, nck, G, max_seq, pl, r1);
+        pvw_load<HD, GM, Q8>(Vh, Ph, Vq, Vs, 2, nck, G, max_seq, pl, r2);
+        pvw_load<HD, GM, Q8>(Vh, Ph, Vq, Vs, 3, nck, G, max_seq, pl, r3);
+        pvw_store<GM, Q8>(Vt[0], Pt[0], pl, r0);
     }
     __syncthreads();
     float a = 0.0f;
@@ -2372,8 +2397,8 @@ __global__ __launch_bounds__(192) void k_attn_pvw(const float* __restrict__ P, c
         if (w == 0) {                                                                                 \
             if (h < G) a = pvw_chunk(&Pt[sl][h][0], &Vt[sl][d][0], min(PVW_CK, L - (C) * PVW_CK), a); \
         } else {                                                                                      \
-            pvw_load<HD, GM>(Vh, Ph, (C) + 4, nck, G, max_seq, pl, RL);                               \
-            pvw_store<GM>(Vt[sl ^ 1], Pt[sl ^ 1], pl, RN);                                            \
+            pvw_load<HD, GM, Q8>(Vh, Ph, Vq, Vs, (C) + 4, nck, G, max_seq, pl, RL);                   \
+            pvw_store<GM, Q8>(Vt[sl ^ 1], Pt[sl ^ 1], pl, RN);                                        \
         }                                                                                             \
         __syncthreads();                                                                              \
     }
@@ -4334,14 +4359,14 @@ int32_t dpuf_hip_attn_split(void* s, int32_t M, int32_t lmax, const float* q, co
                        scores);                                                                                   \
     SMX_LAUNCH(16) SMX_LAUNCH(32) SMX_LAUNCH(48) SMX_LAUNCH(64) SMX_LAUNCH(80) SMX_LAUNCH(96) SMX_LAUNCH(128)  \
     if (gm == 2)                                                                                                  \
-        hipLaunchKernelGGL((k_attn_pvw<HDV, 2>), gp, dim3(192), 0, ST(s), scores, vc, pos0p, n_q, n_kv, max_seq,   \
-                           out);                                                                                  \
+        hipLaunchKernelGGL((k_attn_pvw<HDV, 2, false>), gp, dim3(192), 0, ST(s), scores, vc, pos0p, n_q, n_kv,  \
+                           max_seq, out, DpufKvQ8{});                                                                                  \
     else if (gm == 4)                                                                                             \
-        hipLaunchKernelGGL((k_attn_pvw<HDV, 4>), gp, dim3(192), 0, ST(s), scores, vc, pos0p, n_q, n_kv, max_seq,   \
-                           out);                                                                                  \
+        hipLaunchKernelGGL((k_attn_pvw<HDV, 4, false>), gp, dim3(192), 0, ST(s), scores, vc, pos0p, n_q, n_kv,  \
+                           max_seq, out, DpufKvQ8{});                                                                                  \
     else                                                                                                          \
-        hipLaunchKernelGGL((k_attn_pvw<HDV, 8>), gp, dim3(192), 0, ST(s), scores, vc, pos0p, n_q, n_kv, max_seq,   \
-                           out);
+        hipLaunchKernelGGL((k_attn_pvw<HDV, 8, false>), gp, dim3(192), 0, ST(s), scores, vc, pos0p, n_q, n_kv,  \
+                           max_seq, out, DpufKvQ8{});
             if (hd == 64) {
                 PVW_LAUNCH(64)
             } else if (hd == 128) {
@@ -4414,6 +4439,41 @@ void dpuf_hip_attn_q8(void* s, int32_t M, int32_t lmax, const float* q, DpufKvQ8
     const size_t lds1 = (size_t)G * hd * 4 + (size_t)Q8_SCK * hd + (size_t)Q8_SCK * (hd / 32) * 4;
     hipLaunchKernelGGL(k_attn_q8_sc, dim3(n_kv, (lmax + Q8_SCK - 1) / Q8_SCK, M), dim3(256), lds1, ST(s), q, c8,
                        scores, pos0, n_q, n_kv, hd, max_seq, scale);
+    // one token, groups of 2, 4 or 8: the softmax once per row and P.V on one
+    // chain wave per (kv head, 4 dims), as for the fp32 cache, with W = p *
+    // v_scale and V widened in the producers
+    if (M == 1 && (G & 1) == 0 && G <= 8) {
+        const int segs[7] = {16, 32, 48, 64, 80, 96, 128};
+        int seg = 0;
+        for (int i = 0; i < 7 && !seg; i++)
+            if (64 * segs[i] >= lmax) seg = segs[i];
+        if (seg) {
+            const int gm = G <= 2 ? 2 : G <= 4 ? 4 : 8;
+            const dim3 gp(n_kv, hd / 4);
+#define SMXQ(SG) \
+    if (seg == SG) hipLaunchKernelGGL(k_attn_smx<SG>, dim3(n_q), dim3(256), 0, ST(s), scores, pos0, max_seq);
+            SMXQ(16) SMXQ(32) SMXQ(48) SMXQ(64) SMXQ(80) SMXQ(96) SMXQ(128)
+#undef SMXQ
+#define PVWQ(HDV)                                                                                                  \
+    do {                                                                                                           \
+        if (gm == 2)                                                                                               \
+            hipLaunchKernelGGL((k_attn_pvw<HDV, 2, true>), gp, dim3(192), 0, ST(s), scores, nullptr, pos0, n_q, n_kv, \
+                               max_seq, out, c8);                                                                  \
+        else if (gm == 4)                                                                                          \
+            hipLaunchKernelGGL((k_attn_pvw<HDV, 4, true>), gp, dim3(192), 0, ST(s), scores, nullptr, pos0, n_q, n_kv, \
+                               max_seq, out, c8);                                                                  \
+        else                                                                                                       \
+            hipLaunchKernelGGL((k_attn_pvw<HDV, 8, true>), gp, dim3(192), 0, ST(s), scores, nullptr, pos0, n_q, n_kv, \
+                               max_seq, out, c8);                                                                  \
+    } while (0)
+            if (hd == 64) PVWQ(64);
+            else if (hd == 128) PVWQ(128);
+            else PVWQ(256);
+#undef PVWQ
+            LAUNCHED("k_attn_q8_sc/k_attn_smx/k_attn_pvw<q8>");
+            return;
+        }
+    }
     // softmax + P.V: the split kernel (as the fp32 cache's) when its tile of
     // probability rows fits in LDS, each dim chunk inside one 32-column block
     const int lcap = (lmax + 7) & ~7;

@@ -136,3 +136,25 @@ def test_q8_rows_beyond_lds(eng, orc):
     assert bits_equal(lg, lo), maxdiff(lg, lo)
     greedy(p, lg, lo, 7202, 3, "q8 after 7200")
     p.close()
+
+
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("nq", [32, 64])
+def test_q8_4096_injected_keys(eng, orc, nq):
+    """A 4096-position N(0, 1) KV cache injected into the int8 cache of both
+    engines (8 KV heads, head_dim 128, groups of 4 and 8), then 3 decode steps
+    through the one-token long-context kernels (softmax once per row, P.V
+    chain waves fed W = p * v_scale and widened V by producer waves): logits
+    bit for bit at every step."""
+    shape = dict(TINY, num_layers=1, num_q_heads=nq, num_kv_heads=8, head_dim=128)
+    m, cfg = q8_model(shape, 4104, 221)
+    p = Q8Pair(eng, orc, m, cfg)
+    rng = np.random.default_rng(222)
+    log(f"q8 kv: injecting 4096 positions, groups of {nq // 8}")
+    for kvh in range(8):
+        p.set_kv(0, kvh, 0, rng.standard_normal((4096, 128), dtype=np.float32),
+                 rng.standard_normal((4096, 128), dtype=np.float32))
+    lg, lo = p.forward(np.array([23], np.int32), 4096)
+    assert bits_equal(lg, lo), maxdiff(lg, lo)
+    greedy(p, lg, lo, 4097, 3, f"q8 4096 G{nq // 8}")
+    p.close()
