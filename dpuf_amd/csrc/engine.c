@@ -20,6 +20,7 @@
 #include "hip_layer.h"
 
 #define N_SLOTS 8
+#define N_GRAPHS 8  /* captured one-token steps kept per engine */
 #define N_PREFIX 8
 #define N_KINDS 8
 #define MAX_EVENTS 8192
@@ -85,9 +86,14 @@ typedef struct {
     double t_ms[N_KINDS];
     int64_t t_cnt[N_KINDS];
     double t_bytes[N_KINDS];
-    /* decode graph */
-    void* graph;
-    int32_t graph_key[6];
+    /* one-token steps captured as HIP graphs that replay at any position,
+     * one per key (only_last, keep tiles, early tiles, slot, margin, split
+     * attention, argmax): a host that alternates slots or entry points keeps
+     * its graphs; the least recently used one makes room */
+    void* graphs[N_GRAPHS];
+    int32_t graph_keys[N_GRAPHS][7];
+    uint32_t graph_used[N_GRAPHS];
+    uint32_t graph_tick;
     /* the forward being enqueued: host copy of pos0, and whether it is being
      * captured into a graph that replays at any position */
     int32_t host_pos0;
@@ -430,7 +436,7 @@ static void engine_free(Engine* e) {
     if (!e) return;
     dpuf_hip_bind_error_word(NULL);
     if (e->stream) dpuf_hip_sync(e->stream);
-    dpuf_hip_graph_destroy(e->graph);
+    for (int i = 0; i < N_GRAPHS; i++) dpuf_hip_graph_destroy(e->graphs[i]);
     for (int32_t i = 0; i < e->n_ups; i++) {
         dpuf_hip_free(e->ups[i].d_groups); dpuf_hip_free(e->ups[i].d_sign);
     }
@@ -941,23 +947,35 @@ static int32_t forward_common(Engine* e, int32_t n_tokens, const int32_t* token_
     e->host_pos0 = pos0;
     e->capturing = 0;
     if (graphable) {
-        int32_t key[6] = {only_last, keep, early, e->active, 0, pos0 + 1 > ATT_SPLIT_MIN};
+        const int32_t want_argmax = token_out != NULL;
+        int32_t key[7] = {only_last, keep, early, e->active, 0, pos0 + 1 > ATT_SPLIT_MIN, want_argmax};
         memcpy(&key[4], &margin, 4);
-        if (e->graph && memcmp(key, e->graph_key, sizeof key) != 0) {
-            dpuf_hip_graph_destroy(e->graph);
-            e->graph = NULL;
-        }
-        if (!e->graph) {
+        int gi = -1;
+        for (int i = 0; i < N_GRAPHS && gi < 0; i++)
+            if (e->graphs[i] && memcmp(key, e->graph_keys[i], sizeof key) == 0) gi = i;
+        if (gi < 0) {
+            /* a free entry, else the least recently used */
+            gi = 0;
+            for (int i = 0; i < N_GRAPHS; i++) {
+                if (!e->graphs[i]) { gi = i; break; }
+                if (e->graph_used[i] < e->graph_used[gi]) gi = i;
+            }
+            dpuf_hip_graph_destroy(e->graphs[gi]);
+            e->graphs[gi] = NULL;
             if (dpuf_hip_capture_begin(e->stream) == 0) {
                 e->capturing = 1;
-                enqueue_forward(e, 1, 0, only_last, keep, early, margin, 1);
+                enqueue_forward(e, 1, 0, only_last, keep, early, margin, want_argmax);
                 e->capturing = 0;
-                e->graph = dpuf_hip_capture_end(e->stream);
-                memcpy(e->graph_key, key, sizeof key);
+                e->graphs[gi] = dpuf_hip_capture_end(e->stream);
+                memcpy(e->graph_keys[gi], key, sizeof key);
             }
         }
-        if (e->graph) dpuf_hip_graph_launch(e->graph, e->stream);
-        else enqueue_forward(e, M, embeds_in != NULL, only_last, keep, early, margin, token_out != NULL);
+        if (e->graphs[gi]) {
+            e->graph_used[gi] = ++e->graph_tick;
+            dpuf_hip_graph_launch(e->graphs[gi], e->stream);
+        } else {
+            enqueue_forward(e, M, embeds_in != NULL, only_last, keep, early, margin, want_argmax);
+        }
     } else {
         enqueue_forward(e, M, embeds_in != NULL, only_last, keep, early, margin, token_out != NULL);
     }
@@ -984,8 +1002,9 @@ DPUF_EXPORT int32_t dpuf_engine_forward_batch_ex(void* handle, int32_t n_tokens,
                                                  float* logits_out) {
     Engine* e = (Engine*)handle;
     if (!e || (!logits_out && only_last_logits != 2)) return -1;
+    /* one-token steps replay a captured graph (forward_common decides) */
     return forward_common(e, n_tokens, token_ids, pos0, embeds_in, pos_t, pos_h, pos_w, deepstack_in,
-                          only_last_logits, logits_out, NULL, 0);
+                          only_last_logits, logits_out, NULL, 1);
 }
 
 DPUF_EXPORT int32_t dpuf_engine_forward_batch(void* handle, int32_t n_tokens, const int32_t* token_ids, int32_t pos0,
