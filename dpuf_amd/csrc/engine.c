@@ -69,7 +69,14 @@ typedef struct {
     int32_t ms_n;
     int32_t *d_ms_pos, *d_ms_tok;
     float **d_ms_kc, **d_ms_vc;
-    int32_t* h_pinned;   /* host staging: [0] pos0, [1] flag, [2] token, [3] error word, [8..] ids */
+    int32_t* h_pinned;   /* host staging: [3] error word of the GEMV bench */
+    /* fine-grained host memory the kernels use directly (no copies): h_io
+     * holds a step's ids [0, B), its pos0 at IO_POS (read by the embedding
+     * kernel) and the published flag, token and error word at IO_OUT;
+     * h_logits receives the one LM-head row of a step whose logits go to the
+     * host (written by the GEMV itself) */
+    int32_t* h_io;
+    float* h_logits;
     uint8_t* q_idx;      /* per layer: prep index of q,k,v (3 bytes) and gate/up (2 bytes) */
     float deadzone;
     void* stream;
@@ -99,6 +106,9 @@ typedef struct {
     int32_t host_pos0;
     int32_t capturing;
 } Engine;
+
+#define IO_POS DPUF_AMD_MAX_BATCH
+#define IO_OUT (DPUF_AMD_MAX_BATCH + 4)
 
 /* Decode attention switches from the fused short-context kernel to the split
  * (scores + softmax/P.V) kernels once kv_len exceeds this. */
@@ -463,6 +473,8 @@ static void engine_free(Engine* e) {
     dpuf_hip_free(e->d_red);
     dpuf_hip_free(e->d_ms_kc);
     dpuf_hip_host_free(e->h_pinned);
+    dpuf_hip_host_free(e->h_io);
+    dpuf_hip_host_free(e->h_logits);
     for (int i = 0; i < MAX_EVENTS; i++) if (e->ev[i]) dpuf_hip_event_destroy(e->ev[i]);
     if (e->stream) dpuf_hip_stream_destroy(e->stream);
     free(e);
@@ -577,6 +589,8 @@ DPUF_EXPORT void* dpuf_engine_create(const DpufModelConfig* cfg, const DpufLayer
         }
         e->d_ids = (int32_t*)dpuf_hip_malloc((B + 64) * 4);
         e->h_pinned = (int32_t*)dpuf_hip_host_alloc((B + 64) * 4);
+        e->h_io = (int32_t*)dpuf_hip_host_alloc_io((B + 64) * 4);
+        e->h_logits = (float*)dpuf_hip_host_alloc_io((size_t)e->V * 4);
         e->d_red = dpuf_hip_malloc(DPUF_HIP_RED_SCRATCH);
         e->d_ms_kc = (float**)dpuf_hip_malloc(B * 2 * sizeof(float*) + B * 8);
         if (!e->d_ms_kc) goto fail;
@@ -584,13 +598,14 @@ DPUF_EXPORT void* dpuf_engine_create(const DpufModelConfig* cfg, const DpufLayer
         e->d_ms_pos = (int32_t*)(e->d_ms_vc + B);
         e->d_ms_tok = e->d_ms_pos + B;
         if (!e->h || !e->h2 || !e->hn || !e->q || !e->k || !e->v || !e->ao || !e->gate || !e->up || !e->logits ||
-            !e->scores || !e->embeds || !e->d_ids || !e->h_pinned || !e->d_red)
+            !e->scores || !e->embeds || !e->d_ids || !e->h_pinned || !e->h_io || !e->h_logits || !e->d_red)
             goto fail;
         e->d_pos0 = e->d_ids + B;
         e->d_flag = e->d_ids + B + 1;
         e->d_tok = e->d_ids + B + 2;
         e->d_err = e->d_ids + B + 3;
         dpuf_hip_fill_zero(e->d_ids, (B + 64) * 4, e->stream);
+        memset(e->h_io, 0, (B + 64) * 4);
         dpuf_hip_fill_zero(e->hn, B * e->H * 4, e->stream);
     }
     if (!slot_alloc(e, 0)) goto fail;
@@ -720,16 +735,27 @@ static DpufGemvJob job(const DpufDevW* w, int32_t t0, int32_t t1, DpufPrep p, fl
 static int32_t n_tiles_of(const DpufDevW* w) { return (w->rows + 15) / 16; }
 
 static void enqueue_layers(Engine* e, int32_t M, int32_t keep_tiles);
-static void enqueue_head(Engine* e, int32_t M, int32_t only_last, int32_t early_tiles, float early_margin,
-                         int32_t want_argmax);
+static int enqueue_head(Engine* e, int32_t M, int32_t only_last, int32_t early_tiles, float early_margin,
+                        int32_t want_argmax, float* lm_host);
 
-/* Enqueues one forward step (ids/embeds/pos0 already on the device). */
+/* Whether the LM head of a step runs the Zone-A early exit (one row, the
+ * vocabulary above 2048 tiles, zone tiles set). */
+static int head_early(const Engine* e, int32_t lm_rows, int32_t early_tiles) {
+    return early_tiles > 0 && lm_rows == 1 && n_tiles_of(&e->lm) > 2048;
+}
+
+/* Enqueues one forward step: ids in h_io[0, M) and pos0 in h_io[IO_POS] (or
+ * embeds rows already on the device); lm_host, when set, takes the one LM-head
+ * row in place of e->logits.  Ends by publishing the flag, token and error
+ * word to h_io[IO_OUT..]. */
 static void enqueue_forward(Engine* e, int32_t M, int32_t use_embeds, int32_t only_last, int32_t keep_tiles,
-                            int32_t early_tiles, float early_margin, int32_t want_argmax) {
-    dpuf_hip_embed(e->stream, e->tok, e->d_ids, M, use_embeds ? e->embeds : NULL, e->h);
+                            int32_t early_tiles, float early_margin, int32_t want_argmax, float* lm_host) {
+    dpuf_hip_embed(e->stream, e->tok, e->h_io, M, use_embeds ? e->embeds : NULL, e->h, e->h_io + IO_POS,
+                   e->d_pos0);
     e->hcur = e->h;
     enqueue_layers(e, M, keep_tiles);
-    enqueue_head(e, M, only_last, early_tiles, early_margin, want_argmax);
+    const int flag_valid = enqueue_head(e, M, only_last, early_tiles, early_margin, want_argmax, lm_host);
+    dpuf_hip_publish(e->stream, e->d_flag, flag_valid, e->h_io + IO_OUT);
 }
 
 /* Layer loop: residual + RMSNorm + prep, fused Q/K/V GEMV, attention (for
@@ -865,13 +891,14 @@ static void enqueue_layers(Engine* e, int32_t M, int32_t keep_tiles) {
 }
 
 /* Final residual + output RMSNorm + LM head (with the optional Zone-A early
- * exit) and the device argmax; reads the residual stream h (+ hn). */
-static void enqueue_head(Engine* e, int32_t M, int32_t only_last, int32_t early_tiles, float early_margin,
-                         int32_t want_argmax) {
+ * exit) and the device argmax; reads the residual stream h (+ hn).  Returns
+ * whether the early-exit flag was computed. */
+static int enqueue_head(Engine* e, int32_t M, int32_t only_last, int32_t early_tiles, float early_margin,
+                        int32_t want_argmax, float* lm_host) {
     void* s = e->stream;
     const int32_t H = e->H;
     const float eps = e->cfg.rms_eps;
-    if (only_last == 2) return;
+    if (only_last == 2) return 0;
     const int32_t lm0 = only_last ? M - 1 : 0, lmM = M - lm0;
     {
         const uint8_t* ps[1] = {e->lm.sign};
@@ -881,7 +908,7 @@ static void enqueue_head(Engine* e, int32_t M, int32_t only_last, int32_t early_
         tm_end(e, tm10);
     }
     const int32_t nt = n_tiles_of(&e->lm);
-    if (early_tiles > 0 && lmM == 1 && nt > 2048) {
+    if (head_early(e, lmM, early_tiles)) {
         /* Zone-A early exit (dpuf_engine.c:2091-2136): zone tiles, top-2
          * margin test on the device, then either the -1e9 fill or the
          * remaining tiles, decided by a device flag (no host round trip). */
@@ -897,14 +924,15 @@ static void enqueue_head(Engine* e, int32_t M, int32_t only_last, int32_t early_
             dpuf_hip_gemv(s, 1, 1, &j1, e->d_flag, -1e9f);
         }
         tm_end(e, tm11);
-    } else {
-        DpufGemvJob j = job(&e->lm, 0, nt, e->prep[0], e->logits, e->V);
-        const int tm12 = tm_begin(e, K_LM, gemv_bytes(&e->lm, 0, nt, lmM));
-        dpuf_hip_gemv(s, lmM, 1, &j, NULL, 0.0f);
-        tm_end(e, tm12);
-        dpuf_hip_fill_zero(e->d_flag, 4, s);
+        if (want_argmax) dpuf_hip_argmax(s, e->logits, e->V, e->d_tok, e->d_red);
+        return 1;
     }
+    DpufGemvJob j = job(&e->lm, 0, nt, e->prep[0], lm_host && lmM == 1 ? lm_host : e->logits, e->V);
+    const int tm12 = tm_begin(e, K_LM, gemv_bytes(&e->lm, 0, nt, lmM));
+    dpuf_hip_gemv(s, lmM, 1, &j, NULL, 0.0f);
+    tm_end(e, tm12);
     if (want_argmax) dpuf_hip_argmax(s, e->logits + (size_t)(lmM - 1) * e->V, e->V, e->d_tok, e->d_red);
+    return 0;
 }
 
 static int32_t forward_common(Engine* e, int32_t n_tokens, const int32_t* token_ids, int32_t pos0,
@@ -935,19 +963,25 @@ static int32_t forward_common(Engine* e, int32_t n_tokens, const int32_t* token_
     if (!has_early) early = 0;
     else if (early <= 0) early = 1; /* env set: the zone is at least 256 tiles */
 
-    int32_t* hp = e->h_pinned;
-    hp[0] = pos0;
-    for (int32_t m = 0; m < M; m++) hp[8 + m] = token_ids ? token_ids[m] : -1;
-    dpuf_hip_h2d(e->d_ids, hp + 8, (size_t)M * 4, e->stream);
-    dpuf_hip_h2d(e->d_pos0, hp, 4, e->stream);
+    /* the embedding kernel reads ids and pos0 from h_io (no copy) */
+    volatile int32_t* io = e->h_io;
+    for (int32_t m = 0; m < M; m++) io[m] = token_ids ? token_ids[m] : -1;
+    io[IO_POS] = pos0;
     if (embeds_in) dpuf_hip_h2d(e->embeds, embeds_in, (size_t)M * e->H * 4, e->stream);
+    /* a one-row LM head whose logits go to the host writes them to h_logits
+     * itself (the same for every step of a graph key: want_argmax clear and
+     * only_last != 2 imply logits_out) */
+    const int32_t want_argmax = token_out != NULL;
+    const int32_t lm_rows = only_last ? 1 : M;
+    float* lm_host = only_last != 2 && logits_out && !want_argmax && lm_rows == 1 && !head_early(e, 1, early)
+                         ? e->h_logits
+                         : NULL;
 
     const int tm13 = tm_begin(e, K_CALL, (double)e->weight_bytes);
     const int graphable = use_graph && M == 1 && !e->timing && !embeds_in && !e->capture;
     e->host_pos0 = pos0;
     e->capturing = 0;
     if (graphable) {
-        const int32_t want_argmax = token_out != NULL;
         int32_t key[7] = {only_last, keep, early, e->active, 0, pos0 + 1 > ATT_SPLIT_MIN, want_argmax};
         memcpy(&key[4], &margin, 4);
         int gi = -1;
@@ -964,7 +998,7 @@ static int32_t forward_common(Engine* e, int32_t n_tokens, const int32_t* token_
             e->graphs[gi] = NULL;
             if (dpuf_hip_capture_begin(e->stream) == 0) {
                 e->capturing = 1;
-                enqueue_forward(e, 1, 0, only_last, keep, early, margin, want_argmax);
+                enqueue_forward(e, 1, 0, only_last, keep, early, margin, want_argmax, lm_host);
                 e->capturing = 0;
                 e->graphs[gi] = dpuf_hip_capture_end(e->stream);
                 memcpy(e->graph_keys[gi], key, sizeof key);
@@ -974,23 +1008,22 @@ static int32_t forward_common(Engine* e, int32_t n_tokens, const int32_t* token_
             e->graph_used[gi] = ++e->graph_tick;
             dpuf_hip_graph_launch(e->graphs[gi], e->stream);
         } else {
-            enqueue_forward(e, M, embeds_in != NULL, only_last, keep, early, margin, want_argmax);
+            enqueue_forward(e, M, 0, only_last, keep, early, margin, want_argmax, lm_host);
         }
     } else {
-        enqueue_forward(e, M, embeds_in != NULL, only_last, keep, early, margin, token_out != NULL);
+        enqueue_forward(e, M, embeds_in != NULL, only_last, keep, early, margin, want_argmax, lm_host);
     }
     tm_end(e, tm13);
-    if (only_last != 2) {
-        const int32_t rows = only_last ? 1 : M;
-        if (logits_out) dpuf_hip_d2h(logits_out, e->logits, (size_t)rows * e->V * 4, e->stream);
-    }
-    dpuf_hip_d2h(hp + 1, e->d_flag, 12, e->stream); /* flag, token, error word */
+    if (only_last != 2 && logits_out && !lm_host)
+        dpuf_hip_d2h(logits_out, e->logits, (size_t)lm_rows * e->V * 4, e->stream);
     if (dpuf_hip_sync(e->stream) != 0) return -6;
     tm_collect(e);
-    const int32_t rc = end_call(e, hp[3]);
+    const int32_t flag = io[IO_OUT], tok = io[IO_OUT + 1];
+    const int32_t rc = end_call(e, io[IO_OUT + 2]);
     if (rc == 0 && only_last != 2) {
-        if (hp[1]) e->early_exits++;
-        if (token_out) *token_out = hp[2];
+        if (lm_host) memcpy(logits_out, e->h_logits, (size_t)e->V * 4);
+        if (flag) e->early_exits++;
+        if (token_out) *token_out = tok;
     }
     return rc;
 }
@@ -1045,9 +1078,9 @@ DPUF_EXPORT int32_t dpuf_amd_engine_forward_slots(void* handle, int32_t n, const
         ptrs[i] = slot_k(e, slot_ids[i]);
         ptrs[n + i] = slot_v(e, slot_ids[i]);
     }
-    int32_t* hp = e->h_pinned;
-    for (int32_t i = 0; i < n; i++) hp[8 + i] = token_ids[i];
-    dpuf_hip_h2d(e->d_ids, hp + 8, (size_t)n * 4, e->stream);
+    volatile int32_t* io = e->h_io;
+    for (int32_t i = 0; i < n; i++) io[i] = token_ids[i];
+    io[IO_POS] = 0;
     dpuf_hip_h2d(e->d_ms_pos, positions, (size_t)n * 4, e->stream);
     dpuf_hip_h2d(e->d_ms_kc, ptrs, (size_t)n * sizeof(float*), e->stream);
     dpuf_hip_h2d(e->d_ms_vc, ptrs + n, (size_t)n * sizeof(float*), e->stream);
@@ -1056,7 +1089,7 @@ DPUF_EXPORT int32_t dpuf_amd_engine_forward_slots(void* handle, int32_t n, const
     e->ms_n = n;
     e->capturing = 0;
     const int tm = tm_begin(e, K_CALL, (double)e->weight_bytes);
-    enqueue_forward(e, n, 0, 0, keep, 0, 1.25f, 0);
+    enqueue_forward(e, n, 0, 0, keep, 0, 1.25f, 0, NULL);
     e->ms_n = 0;
     if (tokens_out)
         for (int32_t i = 0; i < n; i++)
@@ -1064,12 +1097,11 @@ DPUF_EXPORT int32_t dpuf_amd_engine_forward_slots(void* handle, int32_t n, const
     tm_end(e, tm);
     if (logits_out) dpuf_hip_d2h(logits_out, e->logits, (size_t)n * e->V * 4, e->stream);
     if (tokens_out) dpuf_hip_d2h(tokens_out, e->d_ms_tok, (size_t)n * 4, e->stream);
-    dpuf_hip_d2h(hp + 3, e->d_err, 4, e->stream);
     const int32_t rc = dpuf_hip_sync(e->stream);
     free(ptrs);
     tm_collect(e);
     if (rc != 0) return -6;
-    return end_call(e, hp[3]);
+    return end_call(e, io[IO_OUT + 2]);
 }
 
 DPUF_EXPORT int32_t dpuf_amd_engine_forward_argmax(void* handle, int32_t n_tokens, const int32_t* token_ids,

@@ -69,6 +69,9 @@ void dpuf_hip_clear_error(void);
 void* dpuf_hip_malloc(size_t bytes);
 void  dpuf_hip_free(void* p);
 void* dpuf_hip_host_alloc(size_t bytes);   /* pinned */
+/* pinned and fine-grained: kernels read and write it directly, the host sees
+ * their stores once the stream has drained */
+void* dpuf_hip_host_alloc_io(size_t bytes);
 void  dpuf_hip_host_free(void* p);
 void* dpuf_hip_stream_create(void);
 void  dpuf_hip_stream_destroy(void* s);
@@ -94,7 +97,10 @@ void dpuf_hip_graph_destroy(void* g);
 /* Kernels.  pos0 is read from device memory so a captured step replays at
  * any position. */
 void dpuf_hip_embed(void* s, DpufDevW w, const int32_t* ids, int32_t M, const float* embeds,
-                    float* out);
+                    float* out, const int32_t* pos_src, int32_t* pos_dst);
+/* host[0..3) = {flag_valid ? words[0] : 0, words[1], words[2]} (words: the
+ * device's early-exit flag, argmax token, error word) */
+void dpuf_hip_publish(void* s, const int32_t* words, int32_t flag_valid, int32_t* host);
 /* h_out = h + res for M rows of H (res NULL: no add, h_out unused), then
  * the RMSNorm of that sum (of h when res is NULL) with weights w and the
  * prep of the result for each of the n_prep sign vectors into preps[i] (and

@@ -93,12 +93,18 @@ DEV float expf_libc(float x) { return expf_libc_tab(x, c_exp2_tab); }
 // and embed_qr_had_asym_impl, dpuf_avx2.c:3154-3207, for modes 13 / 14)
 // grid: M rows; thread per 64-column block.
 // ---------------------------------------------------------------------------
+// ids (and pos_src) may sit in fine-grained host memory that the host wrote
+// just before the launch: system-scope loads read them past every cache.
+// Workgroup 0 copies the step's start position to pos_dst in device memory,
+// where the kernels after it read it.
 __global__ void k_embed(DpufDevW w, const int32_t* __restrict__ ids, const float* __restrict__ embeds,
-                        float* __restrict__ out) {
+                        float* __restrict__ out, const int32_t* pos_src, int32_t* pos_dst) {
     const int m = blockIdx.x;
     const int H = w.cols, n_blk = H >> 5;
     float* dst = out + (size_t)m * H;
-    const int id = ids ? ids[m] : -1;
+    if (pos_dst && m == 0 && threadIdx.x == 0)
+        *pos_dst = __hip_atomic_load(pos_src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    const int id = ids ? __hip_atomic_load(ids + m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) : -1;
     if (embeds && id < 0) {
         // H is a multiple of 64: float4 copies, eight loads in flight per thread
         const float4* src4 = (const float4*)(embeds + (size_t)m * H);
@@ -3823,6 +3829,14 @@ void* dpuf_hip_host_alloc(size_t bytes) {
     }
     return p;
 }
+void* dpuf_hip_host_alloc_io(size_t bytes) {
+    void* p = nullptr;
+    if (hipHostMalloc(&p, bytes ? bytes : 64, hipHostMallocCoherent) != hipSuccess) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    return p;
+}
 void dpuf_hip_host_free(void* p) { if (p) CK(hipHostFree(p)); }
 void* dpuf_hip_stream_create(void) {
     hipStream_t s = nullptr;
@@ -3900,11 +3914,28 @@ int32_t dpuf_hip_graph_launch(void* g, void* s) {
 }
 void dpuf_hip_graph_destroy(void* g) { if (g) (void)hipGraphExecDestroy((hipGraphExec_t)g); }
 
-void dpuf_hip_embed(void* s, DpufDevW w, const int32_t* ids, int32_t M, const float* embeds, float* out) {
+void dpuf_hip_embed(void* s, DpufDevW w, const int32_t* ids, int32_t M, const float* embeds, float* out,
+                    const int32_t* pos_src, int32_t* pos_dst) {
     int threads = (w.cols >> 6) < 256 ? (w.cols >> 6) : 256;
     threads = (threads + 63) & ~63;
-    hipLaunchKernelGGL(k_embed, dim3(M), dim3(threads), 0, ST(s), w, ids, embeds, out);
+    hipLaunchKernelGGL(k_embed, dim3(M), dim3(threads), 0, ST(s), w, ids, embeds, out, pos_src, pos_dst);
     LAUNCHED("k_embed");
+}
+
+// Copies a step's result words (early-exit flag, argmax token, error word)
+// to host memory with vector stores, so the host reads them after the
+// stream drains without a copy; the flag is 0 when no top-2 check ran.
+__global__ void k_publish(const int32_t* __restrict__ words, int flag_valid, int32_t* host) {
+    if (threadIdx.x == 0) {
+        host[0] = flag_valid ? words[0] : 0;
+        host[1] = words[1];
+        host[2] = words[2];
+    }
+}
+
+void dpuf_hip_publish(void* s, const int32_t* words, int32_t flag_valid, int32_t* host) {
+    hipLaunchKernelGGL(k_publish, dim3(1), dim3(64), 0, ST(s), words, flag_valid, host);
+    LAUNCHED("k_publish");
 }
 
 void dpuf_hip_resnorm_prep(void* s, int32_t M, int32_t H, const float* h, const float* res, float* h_out,
