@@ -734,6 +734,7 @@ static DpufGemvJob job(const DpufDevW* w, int32_t t0, int32_t t1, DpufPrep p, fl
 
 static int32_t n_tiles_of(const DpufDevW* w) { return (w->rows + 15) / 16; }
 
+
 static void enqueue_layers(Engine* e, int32_t M, int32_t keep_tiles);
 static int enqueue_head(Engine* e, int32_t M, int32_t only_last, int32_t early_tiles, float early_margin,
                         int32_t want_argmax, float* lm_host);
@@ -765,9 +766,47 @@ static void enqueue_forward(Engine* e, int32_t M, int32_t use_embeds, int32_t on
  * e->hn. */
 static float* h_other(const Engine* e) { return e->hcur == e->h ? e->h2 : e->h; }
 
+/* The one-row GEMV jobs of layer l: Q/K/V, O, gate/up, down (pruned to
+ * keep_tiles). */
+typedef struct {
+    DpufGemvJob qkv[3], o, gu[2], down;
+} LayerJobs;
+
+static LayerJobs layer_jobs(Engine* e, int32_t l, int32_t keep_tiles) {
+    const DpufDevW* W = e->lw + (size_t)l * 7;
+    const uint8_t* qi = e->q_idx + (size_t)l * 5;
+    LayerJobs r;
+    r.qkv[0] = job(&W[W_Q], 0, n_tiles_of(&W[W_Q]), e->prep[qi[0]], e->q, e->qd);
+    r.qkv[1] = job(&W[W_K], 0, n_tiles_of(&W[W_K]), e->prep[qi[1]], e->k, e->kvd);
+    r.qkv[2] = job(&W[W_V], 0, n_tiles_of(&W[W_V]), e->prep[qi[2]], e->v, e->kvd);
+    r.o = job(&W[W_O], 0, n_tiles_of(&W[W_O]), e->prep[0], e->hn, e->H);
+    r.gu[0] = job(&W[W_GATE], 0, n_tiles_of(&W[W_GATE]), e->prep[0], e->gate, e->I);
+    r.gu[1] = job(&W[W_UP], 0, n_tiles_of(&W[W_UP]), e->prep[qi[4]], e->up, e->I);
+    const int32_t nt = n_tiles_of(&W[W_DOWN]);
+    const int32_t kt = (keep_tiles > 0 && keep_tiles < nt) ? keep_tiles : nt;
+    r.down = job(&W[W_DOWN], 0, kt, e->prep[0], e->hn, e->H);
+    return r;
+}
+
+/* What the decode attention of layer l warms while its workgroups run on a
+ * few CUs: the O projection after it, the first round of gate/up, and the
+ * next layer's Q/K/V (the Infinity Cache keeps them across the launches in
+ * between).  The down projection and the later gate/up rounds stay cold:
+ * reading them too made the attention launch longer than the GEMVs gained. */
+static DpufWarm attn_warm(Engine* e, const LayerJobs* lj, const LayerJobs* ln) {
+    DpufWarm w;
+    memset(&w, 0, sizeof w);
+    dpuf_hip_warm_add(&w, 1, &lj->o, 0, 1);
+    dpuf_hip_warm_add(&w, 2, lj->gu, 0, 1);
+    if (ln) dpuf_hip_warm_add(&w, 3, ln->qkv, 0, 1);
+    w.sink = e->d_ids + DPUF_AMD_MAX_BATCH + 8;
+    return w;
+}
+
 static void enqueue_layers(Engine* e, int32_t M, int32_t keep_tiles) {
     void* s = e->stream;
     const int32_t H = e->H, I = e->I;
+    const DpufWarm no_warm = {0};
     const float eps = e->cfg.rms_eps;
     const float scale = 1.0f / sqrtf((float)e->hd);
     for (int32_t l = 0; l < e->L; l++) {
@@ -776,6 +815,18 @@ static void enqueue_layers(Engine* e, int32_t M, int32_t keep_tiles) {
         const size_t lo = (size_t)l * e->nkv * e->max_seq * e->hd;
         float* kc = is_q8(e) ? NULL : slot_k(e, e->active) + lo;
         float* vc = is_q8(e) ? NULL : slot_v(e, e->active) + lo;
+        /* the layer's GEMV jobs (and the next layer's, whose Q/K/V the
+         * decode attention warms) */
+        const LayerJobs lj = layer_jobs(e, l, keep_tiles);
+        LayerJobs ln_;
+        const LayerJobs* ln = NULL;
+        if (l + 1 < e->L) {
+            ln_ = layer_jobs(e, l + 1, keep_tiles);
+            ln = &ln_;
+        }
+        const DpufGemvJob* jqkv = lj.qkv;
+        const DpufGemvJob jo = lj.o;
+        const DpufGemvJob* jgu = lj.gu;
 
         /* (1) [h += down] + attn RMSNorm + prep of the Q/K/V input */
         {
@@ -792,11 +843,7 @@ static void enqueue_layers(Engine* e, int32_t M, int32_t keep_tiles) {
         }
         /* (2) Q, K, V in one launch */
         {
-            DpufGemvJob js[3] = {
-                job(&W[W_Q], 0, n_tiles_of(&W[W_Q]), e->prep[qi[0]], e->q, e->qd),
-                job(&W[W_K], 0, n_tiles_of(&W[W_K]), e->prep[qi[1]], e->k, e->kvd),
-                job(&W[W_V], 0, n_tiles_of(&W[W_V]), e->prep[qi[2]], e->v, e->kvd),
-            };
+            const DpufGemvJob* js = jqkv;
             double b = gemv_bytes(&W[W_Q], 0, n_tiles_of(&W[W_Q]), M) + gemv_bytes(&W[W_K], 0, n_tiles_of(&W[W_K]), M) +
                        gemv_bytes(&W[W_V], 0, n_tiles_of(&W[W_V]), M);
             const int tm2 = tm_begin(e, K_QKV, b);
@@ -821,11 +868,12 @@ static void enqueue_layers(Engine* e, int32_t M, int32_t keep_tiles) {
                 fused = dpuf_hip_attn_dec(s, M, e->q, e->k, e->v, e->d_norm[4 * l + 1], e->d_norm[4 * l + 2], eps,
                                           e->d_cos, e->d_sin, NULL, NULL, e->d_ms_pos, e->nq, e->nkv, e->hd,
                                           e->max_seq, scale, e->ao, W[W_O].sign, e->prep[0], e->d_ms_kc,
-                                          e->d_ms_vc, (size_t)l * e->nkv * e->max_seq * e->hd) == 0;
+                                          e->d_ms_vc, (size_t)l * e->nkv * e->max_seq * e->hd, no_warm) == 0;
             else if (M == 1 && e->host_pos0 + 1 <= ATT_SPLIT_MIN)
                 fused = dpuf_hip_attn_dec(s, 1, e->q, e->k, e->v, e->d_norm[4 * l + 1], e->d_norm[4 * l + 2], eps,
                                           e->d_cos, e->d_sin, kc, vc, e->d_pos0, e->nq, e->nkv, e->hd, e->max_seq,
-                                          scale, e->ao, W[W_O].sign, e->prep[0], NULL, NULL, 0) == 0;
+                                          scale, e->ao, W[W_O].sign, e->prep[0], NULL, NULL, 0,
+                                          attn_warm(e, &lj, ln)) == 0;
             if (!fused) {
                 dpuf_hip_qk_rope_kv(s, M, e->q, e->k, e->v, e->d_norm[4 * l + 1], e->d_norm[4 * l + 2], eps,
                                     e->d_cos, e->d_sin, kc, vc, e->d_pos0, e->nq, e->nkv, e->hd, e->max_seq, NULL);
@@ -842,7 +890,7 @@ static void enqueue_layers(Engine* e, int32_t M, int32_t keep_tiles) {
             tm_end(e, tm);
         }
         {
-            DpufGemvJob j = job(&W[W_O], 0, n_tiles_of(&W[W_O]), e->prep[0], e->hn, H);
+            const DpufGemvJob j = jo;
             const int tm5 = tm_begin(e, K_O, gemv_bytes(&W[W_O], 0, n_tiles_of(&W[W_O]), M));
             dpuf_hip_gemv(s, M, 1, &j, NULL, 0.0f);
             tm_end(e, tm5);
@@ -859,10 +907,7 @@ static void enqueue_layers(Engine* e, int32_t M, int32_t keep_tiles) {
         }
         /* (7) gate + up in one launch */
         {
-            DpufGemvJob js[2] = {
-                job(&W[W_GATE], 0, n_tiles_of(&W[W_GATE]), e->prep[0], e->gate, I),
-                job(&W[W_UP], 0, n_tiles_of(&W[W_UP]), e->prep[qi[4]], e->up, I),
-            };
+            const DpufGemvJob* js = jgu;
             double b = gemv_bytes(&W[W_GATE], 0, n_tiles_of(&W[W_GATE]), M) + gemv_bytes(&W[W_UP], 0, n_tiles_of(&W[W_UP]), M);
             const int tm7 = tm_begin(e, K_GU, b);
             dpuf_hip_gemv(s, M, 2, js, NULL, 0.0f);
@@ -877,7 +922,7 @@ static void enqueue_layers(Engine* e, int32_t M, int32_t keep_tiles) {
         {
             int32_t nt = n_tiles_of(&W[W_DOWN]);
             int32_t kt = (keep_tiles > 0 && keep_tiles < nt) ? keep_tiles : nt;
-            DpufGemvJob j = job(&W[W_DOWN], 0, kt, e->prep[0], e->hn, H);
+            const DpufGemvJob j = lj.down;
             const int tm9 = tm_begin(e, K_DOWN, gemv_bytes(&W[W_DOWN], 0, kt, M));
             if (kt < nt)
                 dpuf_hip_gemv_zero(s, M, &j, kt * 16, W[W_DOWN].rows);
@@ -900,6 +945,7 @@ static int enqueue_head(Engine* e, int32_t M, int32_t only_last, int32_t early_t
     const float eps = e->cfg.rms_eps;
     if (only_last == 2) return 0;
     const int32_t lm0 = only_last ? M - 1 : 0, lmM = M - lm0;
+    const int32_t nt = n_tiles_of(&e->lm);
     {
         const uint8_t* ps[1] = {e->lm.sign};
         const int tm10 = tm_begin(e, K_PREP, 0);
@@ -907,7 +953,6 @@ static int enqueue_head(Engine* e, int32_t M, int32_t only_last, int32_t early_t
                               h_other(e) + (size_t)lm0 * H, e->d_out_norm, eps, 1, ps, e->prep, NULL);
         tm_end(e, tm10);
     }
-    const int32_t nt = n_tiles_of(&e->lm);
     if (head_early(e, lmM, early_tiles)) {
         /* Zone-A early exit (dpuf_engine.c:2091-2136): zone tiles, top-2
          * margin test on the device, then either the -1e9 fill or the

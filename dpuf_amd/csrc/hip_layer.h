@@ -51,6 +51,27 @@ typedef struct {
     float* vs;
 } DpufKvQ8;
 
+/* A cache warm-up by otherwise idle workgroups of a latency-bound launch:
+ * they read weight groups that later one-row GEMVs stream, on the XCD whose
+ * workgroups will read them (a GEMV's workgroup b runs on XCD b % 8), so
+ * those reads hit the XCD's L2 or the Infinity Cache instead of waiting on
+ * HBM.  Job j: group g (of n_groups, group_bytes each, from p) is read by its
+ * GEMV's workgroup wb + g % nwg in round g / nwg; rounds [r0, r0 + nr) are
+ * warmed.  n_wg warm-up workgroups (a multiple of 8; the launcher sets it);
+ * sink: a device word written only when the bytes hash to one value, so the
+ * reads are kept. */
+#define DPUF_WARM_JOBS 6
+typedef struct {
+    const uint8_t* p;
+    int32_t n_groups, group_bytes, wb, nwg, r0, nr;
+} DpufWarmJob;
+typedef struct {
+    DpufWarmJob j[DPUF_WARM_JOBS];
+    int32_t n_jobs;
+    int32_t n_wg;
+    int32_t* sink;
+} DpufWarm;
+
 /* One matrix of a fused GEMV launch: groups [g0, g1) of w, reading prep p,
  * writing out[m * ldo + row]. */
 typedef struct {
@@ -124,6 +145,10 @@ void dpuf_hip_gemv(void* s, int32_t M, int32_t n_jobs, const DpufGemvJob* jobs,
 /* One GEMV job that also sets rows [r0, r1) of job->out to 0 (every token
  * row): for M > 1 inside the GEMM launch, for M == 1 with a second launch. */
 void dpuf_hip_gemv_zero(void* s, int32_t M, const DpufGemvJob* job, int32_t r0, int32_t r1);
+/* Appends to wm the rounds [r0, r0 + nr) of the one-row GEMV over these
+ * jobs (one mode) as the GEMV will be launched; returns 0 when they do not
+ * fit (wm unchanged). */
+int32_t dpuf_hip_warm_add(DpufWarm* wm, int32_t n_jobs, const DpufGemvJob* jobs, int32_t r0, int32_t nr);
 /* Caps the workgroups of an M == 1 GEMV or K-split GEMM launch (<= 0:
  * device capacity only). */
 void dpuf_hip_set_gemv_max_wg(int32_t n);
@@ -170,7 +195,7 @@ int32_t dpuf_hip_attn_dec(void* s, int32_t M, const float* q, const float* k, co
                           const float* k_norm, float eps, const float* cos_tab, const float* sin_tab, float* kc,
                           float* vc, const int32_t* pos0, int32_t n_q, int32_t n_kv, int32_t hd, int32_t max_seq,
                           float scale, float* ao, const uint8_t* o_sign, DpufPrep op, float* const* kcs,
-                          float* const* vcs, size_t l_off);
+                          float* const* vcs, size_t l_off, DpufWarm warm);
 void dpuf_hip_zero_rows(void* s, int32_t M, float* out, int32_t ld, int32_t r0, int32_t r1);
 /* CRC32 of n tile bodies (base + off[t], len[t] bytes) against want[t]: ok[t] = 1 when equal. */
 void dpuf_hip_crc_tiles(void* s, const uint8_t* base, const uint64_t* off, const uint32_t* len,

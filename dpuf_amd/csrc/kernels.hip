@@ -173,6 +173,74 @@ __global__ void k_embed(DpufDevW w, const int32_t* __restrict__ ids, const float
     }
 }
 
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// Warm-up workgroup i (of wm.n_wg; grid position L, so XCD L % 8): the
+// units of its XCD are (job j, round lg, the k-th workgroup of job j on that
+// XCD), job by job; it takes a share of at most WARM_MAXU of them, puts their
+// group addresses and sizes in LDS, and reads the groups with 16-byte loads,
+// sixteen in flight per lane.  Called by every thread of the workgroup.
+#define WARM_MAXU 48
+DEV void warm_read(const DpufWarm& wm, int i, int L, int tid, int nthr) {
+    __shared__ const uint8_t* gtab[WARM_MAXU];
+    __shared__ int gqt[WARM_MAXU];
+    const int x = L & 7, r = i >> 3, per_x = wm.n_wg >> 3;
+    if (per_x <= 0 || wm.n_jobs <= 0) return;
+    int U = 0;
+    for (int j = 0; j < wm.n_jobs; j++) {
+        const DpufWarmJob& J = wm.j[j];
+        const int c = (x - J.wb) & 7;
+        if ((J.group_bytes >> 4) < nthr) return;  // one wrap per step below
+        U += (J.nwg > c ? (J.nwg - c + 7) >> 3 : 0) * J.nr;
+    }
+    if (U <= 0) return;
+    const int tp = (U + per_x - 1) / per_x, u0 = r * tp;
+    int nu = U - u0 < tp ? U - u0 : tp;
+    if (nu > WARM_MAXU) nu = WARM_MAXU;
+    if (nu <= 0) return;
+    if (tid < nu) {
+        int u = u0 + tid;
+        const uint8_t* gp = nullptr;
+        int gq = 0;
+        for (int j = 0; j < wm.n_jobs; j++) {
+            const DpufWarmJob& J = wm.j[j];
+            const int c = (x - J.wb) & 7, cnt = J.nwg > c ? (J.nwg - c + 7) >> 3 : 0;
+            if (u < cnt * J.nr) {
+                const int lg = J.r0 + u / cnt, k = u - (u / cnt) * cnt;
+                const int g = c + 8 * k + lg * J.nwg;
+                if (g < J.n_groups) gp = J.p + (size_t)g * J.group_bytes;
+                gq = J.group_bytes >> 4;
+                break;
+            }
+            u -= cnt * J.nr;
+        }
+        gtab[tid] = gp;
+        gqt[tid] = gq > 0 ? gq : nthr;
+    }
+    __syncthreads();
+    int t = 0, o = tid;
+    uint32_t acc = 0;
+    while (t < nu) {
+        uint4 v[16];
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            v[k] = make_uint4(0u, 0u, 0u, 0u);
+            if (t < nu) {
+                const uint8_t* gp = gtab[t];
+                const int gq = gqt[t];
+                if (gp) v[k] = ((const uint4*)gp)[o];
+                o += nthr;  // nthr <= gq: at most one wrap
+                const bool wr = o >= gq;
+                o = wr ? o - gq : o;
+                t += wr ? 1 : 0;
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < 16; k++) acc ^= v[k].x ^ v[k].w;
+    }
+    if (acc == 0x9E3779B9u) *wm.sink = (int32_t)acc;
+}
+
 // ---------------------------------------------------------------------------
 // Residual add + RMSNorm + prep for up to three sign vectors (reference
 // add_and_rms_norm_f32, dpuf_engine.c:243-272, then the prep above).
@@ -1742,7 +1810,6 @@ DEV float score_dot2(const float* q, const float* kp, int hd) {
     return hsum8(cc);
 }
 
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 // ---------------------------------------------------------------------------
 // Split attention for prefill and long-context decode: the same arithmetic as
@@ -3110,6 +3177,7 @@ __global__ void k_q8_dequant(DpufKvQ8 c8, size_t off, size_t n, float* __restric
 
 
 
+
 template <int HD>
 __global__ __launch_bounds__(256) void k_attn_dec(const float* __restrict__ q, const float* __restrict__ k,
                                                   const float* __restrict__ v, const float* __restrict__ qn,
@@ -3119,8 +3187,18 @@ __global__ __launch_bounds__(256) void k_attn_dec(const float* __restrict__ q, c
                                                   const int32_t* __restrict__ pos0p, int n_q, int n_kv, int max_seq,
                                                   float scale,
                                                   float* __restrict__ ao, const uint8_t* __restrict__ o_sign,
-                                                  DpufPrep op, float* const* kcs, float* const* vcs, size_t l_off) {
+                                                  DpufPrep op, float* const* kcs, float* const* vcs, size_t l_off,
+                                                  DpufWarm warm) {
     constexpr int V_ROWS = 16384 / HD;  // 64 KB of V rows per LDS chunk
+    {
+        // workgroups past the query pairs warm the caches for the next launch
+        const int ny = (n_q / n_kv + 1) / 2;
+        if ((int)blockIdx.y >= ny) {
+            warm_read(warm, ((int)blockIdx.y - ny) * (int)gridDim.x + (int)blockIdx.x,
+                      (int)(blockIdx.y * gridDim.x + blockIdx.x), threadIdx.x, 256);
+            return;
+        }
+    }
     // token blockIdx.z of a multi-session step: its own q/k/v rows, position
     // and output rows, and (kcs set) its own session's KV cache
     {
@@ -4000,6 +4078,18 @@ typedef void (*MvKernel)(MvArgs);
 
 static int g_mv_max_wg = 0;  // test/tuning cap on GEMV / K-split GEMM workgroups
 
+// Compute units of the current device (cached; 1 when the query fails).
+static int dpuf_hip_cu_count() {
+    static int n_cu = 0;
+    if (n_cu == 0) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n_cu <= 0)
+            n_cu = 1;
+    }
+    return n_cu;
+}
+
 void dpuf_hip_set_gemv_max_wg(int32_t n) { g_mv_max_wg = n > 0 ? n : 0; }
 
 // Device error word of the current API call on this thread (see MvArgs::err).
@@ -4067,11 +4157,14 @@ static void mv_pick(int S, MvKernel& k, MvKernel& k1, int& nl, int& nw) {
 }
 }
 
-// One launch over jobs of one mode.
-static void mv_launch(void* s, MvArgs& A, const int* n_groups, int mode) {
-    const int n_blk = A.K >> 5, S = (n_blk + 7) >> 3;
-    MvKernel k, k1;  // persistent and one-group-per-workgroup instances
-    int nl, nw;
+// The launch plan of a one-row GEMV over n_jobs jobs of one mode: the
+// instances (persistent, one group per workgroup), loader waves nw, the
+// workgroup prefix sums wb[0..n_jobs] and the most groups of one workgroup.
+// Returns the total group count (0: nothing to launch).
+static int mv_plan(int n_jobs, const int* n_groups, int K, int mode, MvKernel& k, MvKernel& k1, int& nw, int* wb,
+                   int& most) {
+    const int n_blk = K >> 5, S = (n_blk + 7) >> 3;
+    int nl;
     if (mode == 13) mv_pick<13>(S, k, k1, nl, nw);
     else if (mode == 14) mv_pick<14>(S, k, k1, nl, nw);
     else mv_pick<12>(S, k, k1, nl, nw);
@@ -4079,17 +4172,18 @@ static void mv_launch(void* s, MvArgs& A, const int* n_groups, int mode) {
     const int threads_p = (nw + MV_NC) * 64;  // + the chain waves
     const size_t buf = (size_t)8 * (n_blk + 2) * 8;
     int total = 0;
-    for (int i = 0; i < A.n_jobs; i++) total += n_groups[i];
-    if (total <= 0) return;
+    for (int i = 0; i < n_jobs; i++) total += n_groups[i];
+    if (total <= 0) return 0;
     // one group per workgroup when the chip holds all of them at once,
     // otherwise persistent workgroups with chain waves
     int cap1 = mv_capacity(k1, nw * 64, buf);
     if (g_mv_max_wg > 0 && cap1 > g_mv_max_wg) cap1 = g_mv_max_wg;
     int cap = total <= cap1 ? total : mv_capacity(k, threads_p, MV_NBUF * buf);
     if (g_mv_max_wg > 0 && cap > g_mv_max_wg) cap = g_mv_max_wg;
-    int grid = 0, most = 1;
-    A.wb[0] = 0;
-    for (int i = 0; i < A.n_jobs; i++) {
+    int grid = 0;
+    most = 1;
+    wb[0] = 0;
+    for (int i = 0; i < n_jobs; i++) {
         int nwg = n_groups[i];
         if (total > cap && nwg > 0) {
             nwg = (int)((long long)cap * n_groups[i] / total);
@@ -4097,8 +4191,19 @@ static void mv_launch(void* s, MvArgs& A, const int* n_groups, int mode) {
         }
         if (nwg > 0 && (n_groups[i] + nwg - 1) / nwg > most) most = (n_groups[i] + nwg - 1) / nwg;
         grid += nwg;
-        A.wb[i + 1] = grid;
+        wb[i + 1] = grid;
     }
+    return total;
+}
+
+// One launch over jobs of one mode.
+static void mv_launch(void* s, MvArgs& A, const int* n_groups, int mode) {
+    const int n_blk = A.K >> 5;
+    MvKernel k, k1;
+    int nw, most;
+    if (mv_plan(A.n_jobs, n_groups, A.K, mode, k, k1, nw, A.wb, most) == 0) return;
+    const int grid = A.wb[A.n_jobs];
+    const size_t buf = (size_t)8 * (n_blk + 2) * 8;
     if (!g_err_word) {
         note(hipErrorInvalidValue, "dpuf_hip_gemv: no device error word bound");
         return;
@@ -4148,6 +4253,33 @@ void dpuf_hip_gemv_zero(void* s, int32_t M, const DpufGemvJob* job, int32_t r0, 
         return;
     }
     gm_launch(s, M, 1, job, job->out, job->ldo, r0, r1);
+}
+
+int32_t dpuf_hip_warm_add(DpufWarm* wm, int32_t n_jobs, const DpufGemvJob* jobs, int32_t r0, int32_t nr) {
+    if (!wm || n_jobs < 1 || n_jobs > 3 || nr < 1 || r0 < 0 || wm->n_jobs + n_jobs > DPUF_WARM_JOBS) return 0;
+    const int mode = jobs[0].w.mode;
+    int ng[3] = {0, 0, 0};
+    for (int j = 0; j < n_jobs; j++) {
+        if (jobs[j].w.mode != mode || jobs[j].w.cols != jobs[0].w.cols) return 0;
+        ng[j] = jobs[j].g1 - jobs[j].g0 > 0 ? jobs[j].g1 - jobs[j].g0 : 0;
+    }
+    MvKernel k, k1;
+    int nw, most, wb[4];
+    if (mv_plan(n_jobs, ng, jobs[0].w.cols, mode, k, k1, nw, wb, most) == 0 || r0 >= most) return 0;
+    if (nr > most - r0) nr = most - r0;
+    const int gb = (jobs[0].w.cols >> 5) * dpuf_grp_unit(mode);
+    for (int j = 0; j < n_jobs; j++) {
+        DpufWarmJob& J = wm->j[wm->n_jobs + j];
+        J.p = jobs[j].w.g + (size_t)jobs[j].g0 * gb;
+        J.n_groups = ng[j];
+        J.group_bytes = gb;
+        J.wb = wb[j];
+        J.nwg = wb[j + 1] - wb[j];
+        J.r0 = r0;
+        J.nr = nr;
+    }
+    wm->n_jobs += n_jobs;
+    return 1;
 }
 
 void dpuf_hip_gemv(void* s, int32_t M, int32_t n_jobs, const DpufGemvJob* jobs, const int32_t* skip_flag,
@@ -4564,17 +4696,23 @@ int32_t dpuf_hip_attn_dec(void* s, int32_t M, const float* q, const float* k, co
                           const float* k_norm, float eps, const float* cos_tab, const float* sin_tab, float* kc,
                           float* vc, const int32_t* pos0, int32_t n_q, int32_t n_kv, int32_t hd, int32_t max_seq,
                           float scale, float* ao, const uint8_t* o_sign, DpufPrep op, float* const* kcs,
-                          float* const* vcs, size_t l_off) {
+                          float* const* vcs, size_t l_off, DpufWarm warm) {
     if (M < 1) return -1;
+    warm.n_wg = 0;
+    if (M == 1 && warm.sink && warm.n_jobs > 0) {
+        // one warm-up workgroup on every CU the attention leaves idle
+        const int n_cu = dpuf_hip_cu_count(), busy = n_kv * ((n_q / n_kv + 1) / 2);
+        warm.n_wg = n_cu > busy + 8 ? (n_cu - busy) & ~7 : 0;
+    }
     if (M == 1) op.h = NULL;  // the one-row GEMV reads q only
     const int groups = n_q / n_kv;
     const size_t scl = 2 * (size_t)DPUF_HIP_DEC_MAX_KEYS > 3 * (size_t)hd ? 2 * (size_t)DPUF_HIP_DEC_MAX_KEYS
                                                                        : 3 * (size_t)hd;
     const size_t lds = ((size_t)16384 + (size_t)6 * hd + scl) * sizeof(float);
-    const dim3 grid(n_kv, (groups + 1) / 2, M);
+    const dim3 grid(n_kv, (groups + 1) / 2 + (warm.n_wg + n_kv - 1) / n_kv, M);
 #define ATT_LAUNCH(HDV)                                                                                            \
     hipLaunchKernelGGL(k_attn_dec<HDV>, grid, dim3(256), lds, ST(s), q, k, v, q_norm, k_norm, eps, cos_tab, sin_tab, \
-                       kc, vc, pos0, n_q, n_kv, max_seq, scale, ao, o_sign, op, kcs, vcs, l_off)
+                       kc, vc, pos0, n_q, n_kv, max_seq, scale, ao, o_sign, op, kcs, vcs, l_off, warm)
     switch (hd) {
         case 64: ATT_LAUNCH(64); break;
         case 128: ATT_LAUNCH(128); break;
