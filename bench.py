@@ -88,7 +88,9 @@ def main():
     ap.add_argument("--lm-alpha", type=float, default=8.0, help="planted bias: h += alpha * row(t*)")
     ap.add_argument("--cpu-seconds", type=float, default=20.0, help="budget of the CPU baseline (0 = skip)")
     ap.add_argument("--seed", type=int, default=1234)
-    ap.add_argument("--graph", type=int, default=1, help="also time the device-argmax entry with HIP graph replay")
+    ap.add_argument("--graph", type=int, default=1,
+                    help="1: one-token steps replay HIP graphs (the default) and the device-argmax entry is timed "
+                         "too; 0: every kernel is enqueued (per-kernel traces)")
     ap.add_argument("--roofline-only", action="store_true",
                     help="only the dominant-kernel roofline measurement (for the matching rocprofv3 run)")
     args = ap.parse_args()
@@ -120,6 +122,8 @@ def main():
     if not h:
         sys.exit("dpuf_engine_create failed: " + eng.dpuf_amd_last_error().decode())
     create_s = time.time() - t
+    if not args.graph:
+        eng.dpuf_amd_engine_set_graphs(h, 0)
     log(f"engine created (weights uploaded to HBM) in {create_s:.2f}s")
 
     # --- roofline of the dominant decode kernel ------------------------------
@@ -344,6 +348,8 @@ def main():
         hq = eng.dpuf_engine_create(*model.create_args(qcfg))
         if not hq:
             sys.exit("dpuf_engine_create (int8 KV) failed: " + eng.dpuf_amd_last_error().decode())
+        if not args.graph:
+            eng.dpuf_amd_engine_set_graphs(hq, 0)
         L, nkv, hd = shape["num_layers"], shape["num_kv_heads"], shape["head_dim"]
         krng = np.random.default_rng(args.seed + 4096)  # the fp32 leg's K/V, quantised by set_kv
         for layer in range(L):

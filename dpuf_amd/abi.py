@@ -208,6 +208,7 @@ def load_engine():
     _sig(lib, "dpuf_amd_engine_set_capture", I32, [P, I32])
     _sig(lib, "dpuf_amd_engine_get_capture", I32, [P, P, C.c_size_t])
     _sig(lib, "dpuf_amd_engine_set_timing", None, [P, I32])
+    _sig(lib, "dpuf_amd_engine_set_graphs", None, [P, I32])
     _sig(lib, "dpuf_amd_engine_get_timing", I32, [P, I32, C.POINTER(C.c_double), C.POINTER(C.c_int64),
                                                   C.POINTER(C.c_double)])
     _sig(lib, "dpuf_amd_engine_weight_bytes", C.c_uint64, [P])

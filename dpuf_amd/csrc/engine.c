@@ -101,6 +101,7 @@ typedef struct {
     int32_t graph_keys[N_GRAPHS][7];
     uint32_t graph_used[N_GRAPHS];
     uint32_t graph_tick;
+    int32_t no_graphs; /* dpuf_amd_engine_set_graphs(0) */
     /* the forward being enqueued: host copy of pos0, and whether it is being
      * captured into a graph that replays at any position */
     int32_t host_pos0;
@@ -1023,7 +1024,7 @@ static int32_t forward_common(Engine* e, int32_t n_tokens, const int32_t* token_
                          : NULL;
 
     const int tm13 = tm_begin(e, K_CALL, (double)e->weight_bytes);
-    const int graphable = use_graph && M == 1 && !e->timing && !embeds_in && !e->capture;
+    const int graphable = use_graph && !e->no_graphs && M == 1 && !e->timing && !embeds_in && !e->capture;
     e->host_pos0 = pos0;
     e->capturing = 0;
     if (graphable) {
@@ -1236,6 +1237,18 @@ DPUF_EXPORT int32_t dpuf_amd_engine_get_capture(void* handle, float* out, size_t
     if (n_floats > total) n_floats = total;
     dpuf_hip_d2h(out, e->capture, n_floats * 4, e->stream);
     return dpuf_hip_sync(e->stream);
+}
+
+DPUF_EXPORT void dpuf_amd_engine_set_graphs(void* handle, int32_t enable) {
+    Engine* e = (Engine*)handle;
+    if (!e) return;
+    e->no_graphs = enable ? 0 : 1;
+    if (e->no_graphs) {
+        for (int i = 0; i < N_GRAPHS; i++) {
+            dpuf_hip_graph_destroy(e->graphs[i]);
+            e->graphs[i] = NULL;
+        }
+    }
 }
 
 DPUF_EXPORT void dpuf_amd_engine_set_timing(void* handle, int32_t enable) {

@@ -56,6 +56,12 @@ DPUF_EXPORT void dpuf_amd_engine_set_timing(void* handle, int32_t enable);
 DPUF_EXPORT int32_t dpuf_amd_engine_get_timing(void* handle, int32_t kind, double* total_ms, int64_t* count,
                                                double* bytes);
 
+/* Graph replay of one-token steps, on by default: the reference entry points
+ * and dpuf_amd_engine_forward_argmax (use_graph set) replay a HIP graph
+ * captured once per step shape.  0 enqueues every kernel of every step
+ * instead (for per-kernel traces) and releases the graphs kept so far. */
+DPUF_EXPORT void dpuf_amd_engine_set_graphs(void* handle, int32_t enable);
+
 /* Mode 12 tile bytes resident in HBM (all layers + LM head). */
 DPUF_EXPORT uint64_t dpuf_amd_engine_weight_bytes(void* handle);
 
