@@ -131,6 +131,30 @@ def test_argmax_entry_and_graph(eng, orc, tiny):
     p.close()
 
 
+def test_graph_replay_switch(eng, orc):
+    """Reference-API decode at 0.6B widths (2 layers, 8 kv heads of 4 query
+    heads, hidden 1024): graph replay with the attention launch's cache
+    warm-up (on by default), then every kernel enqueued
+    (dpuf_amd_engine_set_graphs 0), then replay again; every step bit-equal
+    to the oracle."""
+    shape = dict(M.QWEN3_0_6B, num_layers=2, num_q_heads=32, vocab_size=8192)
+    m = M.Model.build(shape, max_seq_len=64, seed=77)
+    p = Pair(eng, orc, m)
+    ids = np.random.default_rng(3).integers(0, 8192, 7).astype(np.int32)
+    lg, lo = p.forward(ids, 0)
+    assert _bits_equal(lg, lo)
+    tok = int(np.argmax(lo[0]))
+    for step in range(9):
+        if step == 3:
+            eng.dpuf_amd_engine_set_graphs(p.g, 0)
+        if step == 6:
+            eng.dpuf_amd_engine_set_graphs(p.g, 1)
+        lg, lo = p.forward(np.array([tok], np.int32), 7 + step)
+        assert _bits_equal(lg, lo), step
+        tok = int(np.argmax(lo[0]))
+    p.close()
+
+
 def test_qwen3_06b_token_exact(eng, orc):
     """Qwen3-0.6B shape, random-init: 32-token prompt + 32 greedy tokens."""
     m = M.Model.build(M.QWEN3_0_6B, max_seq_len=80, seed=1234)
