@@ -4037,7 +4037,7 @@ void dpuf_hip_resnorm_prep(void* s, int32_t M, int32_t H, const float* h, const 
     // (8 * (H / 8 + 4) floats per row keeps segments of 16, 32, 64 aligned)
     // four workgroups per row when the row splits into quarters of whole
     // 16-lane rows of blocks (and no normalised copy is asked for)
-    const bool split = H % 256 == 0 && !xn_out && !(res && h_out == h);
+    const bool split = M <= 16 && H % 256 == 0 && !xn_out && !(res && h_out == h);
     auto k = split ? (H == 4096   ? k_resnorm_prep<64, 4>
                       : H == 2048 ? k_resnorm_prep<32, 4>
                       : H == 1024 ? k_resnorm_prep<16, 4>
