@@ -179,8 +179,9 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 // units of its XCD are (job j, round lg, the k-th workgroup of job j on that
 // XCD), job by job; it takes a share of at most WARM_MAXU of them, puts their
 // group addresses and sizes in LDS, and reads the groups with 16-byte loads,
-// sixteen in flight per lane.  Called by every thread of the workgroup.
+// WARM_DEPTH in flight per lane.  Called by every thread of the workgroup.
 #define WARM_MAXU 48
+#define WARM_DEPTH 32  // loads in flight per lane (16 and 64 measured slower)
 DEV void warm_read(const DpufWarm& wm, int i, int L, int tid, int nthr) {
     __shared__ const uint8_t* gtab[WARM_MAXU];
     __shared__ int gqt[WARM_MAXU];
@@ -221,9 +222,9 @@ DEV void warm_read(const DpufWarm& wm, int i, int L, int tid, int nthr) {
     int t = 0, o = tid;
     uint32_t acc = 0;
     while (t < nu) {
-        uint4 v[16];
+        uint4 v[WARM_DEPTH];
 #pragma unroll
-        for (int k = 0; k < 16; k++) {
+        for (int k = 0; k < WARM_DEPTH; k++) {
             v[k] = make_uint4(0u, 0u, 0u, 0u);
             if (t < nu) {
                 const uint8_t* gp = gtab[t];
@@ -236,7 +237,7 @@ DEV void warm_read(const DpufWarm& wm, int i, int L, int tid, int nthr) {
             }
         }
 #pragma unroll
-        for (int k = 0; k < 16; k++) acc ^= v[k].x ^ v[k].w;
+        for (int k = 0; k < WARM_DEPTH; k++) acc ^= v[k].x ^ v[k].w;
     }
     if (acc == 0x9E3779B9u) *wm.sink = (int32_t)acc;
 }
