@@ -1923,6 +1923,91 @@ __global__ __launch_bounds__(256) void k_attn_sc(const float* __restrict__ q, co
     }
 }
 
+// k_attn_sc1: the scores of a one-token step (M = 1) for an even group of at
+// most GM query heads.  k_attn_sc's tiling gives each thread two rows and four
+// keys, so with G <= 8 rows only G / 2 x 16 threads of a workgroup compute;
+// here every thread works: thread (key kq = tid / 4, jp = tid % 4) runs the
+// reference's accumulators j = 2 jp and 2 jp + 1 (a[j] = fma chain over i of
+// q[8i + j] * k[8i + j]) for all the group's rows, and the lane quad of a key
+// combines its eight accumulators by DPP exchanges that form exactly the
+// reference's trees: the hadd tree ((a0+a1)+(a2+a3)) + ((a4+a5)+(a6+a7)) for
+// keys below kv_len & ~3, eng_hsum256 ((a0+a4)+(a1+a5)) + ((a2+a6)+(a3+a7))
+// above it (fp32 addition is commutative, so every lane of the quad holds the
+// same bits).  Workgroup (kv head, 64 keys); K rows staged in LDS with a row
+// stride of HD + 8 words, so the quad reads of 8 consecutive keys fall on
+// distinct banks.
+// ---------------------------------------------------------------------------
+template <int HD, int GM>
+__global__ __launch_bounds__(256) void k_attn_sc1(const float* __restrict__ q, const float* __restrict__ kc,
+                                                  const int32_t* __restrict__ pos0p, int n_q, int n_kv, int max_seq,
+                                                  float scale, float* __restrict__ S) {
+    constexpr int LD = HD + 8;
+    extern __shared__ __align__(16) float sm[];
+    float* ks = sm;               // [AS_KC][LD]
+    float* qs = ks + AS_KC * LD;  // [GM][HD]
+    const int kvh = blockIdx.x, t0 = blockIdx.y * AS_KC, tid = threadIdx.x;
+    const int G = n_q / n_kv;
+    const int L = *pos0p + 1;
+    if (t0 >= L) return;  // every key of the chunk is past the row
+    {
+        constexpr int NK = AS_KC * (HD / 4) / 256, NQ = (GM * (HD / 4) + 255) / 256;
+        float4 kx[NK], qx[NQ];
+#pragma unroll
+        for (int k = 0; k < NK; k++) {
+            const int e = tid + 256 * k, kr = e / (HD / 4), c = e % (HD / 4);
+            const int t = t0 + kr < max_seq ? t0 + kr : max_seq - 1;
+            kx[k] = *(const float4*)(kc + ((size_t)kvh * max_seq + t) * HD + 4 * c);
+        }
+#pragma unroll
+        for (int k = 0; k < NQ; k++) {
+            const int e = tid + 256 * k, r = e / (HD / 4), c = e % (HD / 4);
+            const int hr = r < G ? r : G - 1;  // rows past the group repeat the last head (never written)
+            if (e < GM * (HD / 4)) qx[k] = *(const float4*)(q + ((size_t)kvh * G + hr) * HD + 4 * c);
+        }
+#pragma unroll
+        for (int k = 0; k < NK; k++) {
+            const int e = tid + 256 * k, kr = e / (HD / 4), c = e % (HD / 4);
+            *(float4*)&ks[kr * LD + 4 * c] = kx[k];
+        }
+#pragma unroll
+        for (int k = 0; k < NQ; k++) {
+            const int e = tid + 256 * k;
+            if (e < GM * (HD / 4)) *(float4*)&qs[4 * e] = qx[k];
+        }
+    }
+    __syncthreads();
+    const int kq = tid >> 2, jp = tid & 3;
+    float acc[GM][2];
+#pragma unroll
+    for (int r = 0; r < GM; r++) acc[r][0] = acc[r][1] = 0.0f;
+    const float* kr = ks + kq * LD + 2 * jp;
+#pragma unroll 4
+    for (int i = 0; i < HD; i += 8) {
+        const float2 kv = *(const float2*)(kr + i);
+#pragma unroll
+        for (int r = 0; r < GM; r++) {
+            const float2 qv = *(const float2*)(qs + r * HD + i + 2 * jp);
+            acc[r][0] = fmaf(qv.x, kv.x, acc[r][0]);
+            acc[r][1] = fmaf(qv.y, kv.y, acc[r][1]);
+        }
+    }
+    const int t = t0 + kq;
+    const int n4 = L & ~3;
+#pragma unroll
+    for (int r = 0; r < GM; r++) {
+        // hadd tree: pair sums, then (jp 0 + jp 1) and (jp 2 + jp 3), then lo + hi
+        const float s = acc[r][0] + acc[r][1];
+        const float u = s + fxor1(s);
+        const float th = u + fxor2(u);
+        // eng_hsum256: (a_j + a_{j+4}) with the quad partner two lanes away
+        const float x0 = fxor2(acc[r][0]), x1 = fxor2(acc[r][1]);
+        const float p = (acc[r][0] + x0) + (acc[r][1] + x1);
+        const float te = p + fxor1(p);
+        if (r < G && (r & 3) == jp && t < L)
+            S[((size_t)kvh * G + r) * max_seq + t] = (t < n4 ? th : te) * scale;
+    }
+}
+
 // ---------------------------------------------------------------------------
 // k_attn_pv: softmax and P.V.  Workgroup (kv head, tile of qt queries, dim
 // chunk of HD / dc): the tile's score rows (R = qt x G, each kv_len(m) long)
@@ -4513,14 +4598,16 @@ int32_t dpuf_hip_attn_split(void* s, int32_t M, int32_t lmax, const float* q, co
         for (int i = 0; i < 7 && !seg; i++)
             if (64 * segs[i] >= lmax) seg = segs[i];
         if (M == 1 && (G & 1) == 0 && G <= 8 && seg) {
-            const dim3 gs1(n_kv, 1, (lmax + AS_KC - 1) / AS_KC);
             const int gm = G <= 2 ? 2 : G <= 4 ? 4 : 8;
             const dim3 gp(n_kv, hd / 4);
 #define SMX_LAUNCH(SG)                                                                                            \
     if (seg == SG) hipLaunchKernelGGL(k_attn_smx<SG>, dim3(n_q), dim3(256), 0, ST(s), scores, pos0p, max_seq);
+#define SC1_LAUNCH(HDV, GMV)                                                                                      \
+    hipLaunchKernelGGL((k_attn_sc1<HDV, GMV>), dim3(n_kv, (lmax + AS_KC - 1) / AS_KC), dim3(256),                   \
+                       (size_t)(AS_KC * (HDV + 8) + GMV * HDV) * 4, ST(s), q, kc, pos0p, n_q, n_kv, max_seq, scale,  \
+                       scores);
 #define PVW_LAUNCH(HDV)                                                                                           \
-    hipLaunchKernelGGL(k_attn_sc<HDV>, gs1, dim3(256), lds1, ST(s), q, kc, pos0p, 1, n_q, n_kv, max_seq, scale, qt1, \
-                       scores);                                                                                   \
+    if (gm == 2) SC1_LAUNCH(HDV, 2) else if (gm == 4) SC1_LAUNCH(HDV, 4) else SC1_LAUNCH(HDV, 8)                  \
     SMX_LAUNCH(16) SMX_LAUNCH(32) SMX_LAUNCH(48) SMX_LAUNCH(64) SMX_LAUNCH(80) SMX_LAUNCH(96) SMX_LAUNCH(128)  \
     if (gm == 2)                                                                                                  \
         hipLaunchKernelGGL((k_attn_pvw<HDV, 2, false>), gp, dim3(192), 0, ST(s), scores, vc, pos0p, n_q, n_kv,  \
@@ -4539,6 +4626,7 @@ int32_t dpuf_hip_attn_split(void* s, int32_t M, int32_t lmax, const float* q, co
                 PVW_LAUNCH(256)
             }
 #undef PVW_LAUNCH
+#undef SC1_LAUNCH
 #undef SMX_LAUNCH
             LAUNCHED("k_attn_split_wide");
             return 0;
