@@ -158,6 +158,28 @@ def test_gqa4_long_context_injected_kv(eng, orc):
     p.close()
 
 
+@pytest.mark.parametrize("nq,nkv,hd,ctx", [(16, 2, 128, 1000), (12, 2, 64, 700), (4, 2, 128, 2500)])
+def test_one_token_long_context_groups(eng, orc, nq, nkv, hd, ctx):
+    """One-token decode past the fused kernel's range with groups of 8, 6
+    and 2 (the scores kernel's 8- and 2-row instances, the P.V kernel's 8-
+    and 2-head ones): a ctx-position N(0, 1) KV cache injected into both
+    engines, then 3 greedy steps, logits bit-identical."""
+    shape = dict(hidden_size=256, intermediate_size=512, num_layers=2, num_q_heads=nq, num_kv_heads=nkv,
+                 head_dim=hd, vocab_size=4096, tie_word_embeddings=1)
+    m = M.Model.build(shape, max_seq_len=ctx + 8, seed=91)
+    p = Pair(eng, orc, m)
+    rng = np.random.default_rng(92)
+    log(f"groups of {nq // nkv}, head dim {hd}: injecting {ctx} positions")
+    for layer in range(2):
+        for kvh in range(nkv):
+            p.set_kv(layer, kvh, 0, rng.standard_normal((ctx, hd), dtype=np.float32),
+                     rng.standard_normal((ctx, hd), dtype=np.float32))
+    lg, lo = p.forward(np.array([5], np.int32), ctx)
+    assert bits_equal(lg, lo), maxdiff(lg, lo)
+    greedy(p, lg, lo, ctx + 1, 3, f"G{nq // nkv} ctx {ctx}")
+    p.close()
+
+
 def test_attention_beyond_split_lds_budget(eng, orc):
     """Groups of 4 with 7200 cached positions.  A two-token forward there:
     its rows of probabilities no longer fit the split kernels' LDS budget, so
