@@ -244,7 +244,10 @@ DEV void i8x4_to_h(uint32_t x, uint32_t& a, uint32_t& b) {
 // r ^ 8 (the moves of wave_prep64), the same butterflies in the same order
 // as quad_fwht64; then the quantisation of quad_quant_store with the
 // 32-block (lanes 0-7 or 8-15 of the row) maximum and sum over r ^ 1, r ^ 2
-// and the half-row mirror.  All 16 lanes of the row must be active.
+// and the half-row mirror.  All 16 lanes of the row must be active.  COH:
+// q, s and m are written with agent-scope stores (they go past the L2 to
+// where every XCD reads, for readers in the same launch).
+template <bool COH = false>
 DEV void row_prep64(float* x, int r, int blk, int8_t* q, float* s, int32_t* m, uint16_t* h) {
     {
         float a = x[0], b = x[1];
@@ -311,6 +314,15 @@ DEV void row_prep64(float* x, int r, int blk, int8_t* q, float* s, int32_t* m, u
     sum += DPP_I(sum, 0x141);
     const uint32_t w = (uint32_t)(qi[0] & 0xFF) | ((uint32_t)(qi[1] & 0xFF) << 8) | ((uint32_t)(qi[2] & 0xFF) << 16) |
                        ((uint32_t)(qi[3] & 0xFF) << 24);
+    if (COH) {
+        __hip_atomic_store((uint32_t*)(q + 64 * blk + 4 * r), w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if ((r & 7) == 0) {
+            __hip_atomic_store((uint32_t*)(s + 2 * blk + (r >> 3)), __float_as_uint(d), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(m + 2 * blk + (r >> 3), sum * 8, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        return;
+    }
     *(uint32_t*)(q + 64 * blk + 4 * r) = w;
     if (h) {
         uint32_t a, b;

@@ -62,6 +62,12 @@ typedef struct {
     int32_t capture_cap;
     DpufPrep prep[3];
     int32_t *d_ids, *d_pos0, *d_flag, *d_tok, *d_err;
+    /* step serial: the host numbers every forward call (h_io[IO_POS + 1]),
+     * the embedding kernel copies it to d_serial; d_pflag [L][512] are the
+     * producer flags of the one-row SwiGLU + down launches, which take the
+     * serial of the step that set them (never reset) */
+    int32_t *d_serial, *d_pflag;
+    int32_t serial;
     void* d_red; /* partials of the device argmax / top-2 reductions */
     /* one token per session (dpuf_amd_engine_forward_slots): while ms_n > 0
      * the layers run the ms_n tokens through the fused decode attention, token
@@ -471,6 +477,7 @@ static void engine_free(Engine* e) {
         dpuf_hip_free(e->prep[i].h);
     }
     dpuf_hip_free(e->d_ids);
+    dpuf_hip_free(e->d_pflag);
     dpuf_hip_free(e->d_red);
     dpuf_hip_free(e->d_ms_kc);
     dpuf_hip_host_free(e->h_pinned);
@@ -605,6 +612,10 @@ DPUF_EXPORT void* dpuf_engine_create(const DpufModelConfig* cfg, const DpufLayer
         e->d_flag = e->d_ids + B + 1;
         e->d_tok = e->d_ids + B + 2;
         e->d_err = e->d_ids + B + 3;
+        e->d_serial = e->d_ids + B + 4;
+        e->d_pflag = (int32_t*)dpuf_hip_malloc((size_t)(e->L > 0 ? e->L : 1) * 512 * 4);
+        if (!e->d_pflag) goto fail;
+        dpuf_hip_fill_zero(e->d_pflag, (size_t)(e->L > 0 ? e->L : 1) * 512 * 4, e->stream);
         dpuf_hip_fill_zero(e->d_ids, (B + 64) * 4, e->stream);
         memset(e->h_io, 0, (B + 64) * 4);
         dpuf_hip_fill_zero(e->hn, B * e->H * 4, e->stream);
@@ -742,6 +753,13 @@ static int enqueue_head(Engine* e, int32_t M, int32_t only_last, int32_t early_t
 
 /* Whether the LM head of a step runs the Zone-A early exit (one row, the
  * vocabulary above 2048 tiles, zone tiles set). */
+/* The serial of the next forward call: positive, never the same twice in a
+ * row of 2^31 - 1 calls, never 0 (the producer flags start at 0). */
+static int32_t next_serial(Engine* e) {
+    e->serial = e->serial >= 0x7FFFFFFF - 1 ? 1 : e->serial + 1;
+    return e->serial;
+}
+
 static int head_early(const Engine* e, int32_t lm_rows, int32_t early_tiles) {
     return early_tiles > 0 && lm_rows == 1 && n_tiles_of(&e->lm) > 2048;
 }
@@ -753,7 +771,7 @@ static int head_early(const Engine* e, int32_t lm_rows, int32_t early_tiles) {
 static void enqueue_forward(Engine* e, int32_t M, int32_t use_embeds, int32_t only_last, int32_t keep_tiles,
                             int32_t early_tiles, float early_margin, int32_t want_argmax, float* lm_host) {
     dpuf_hip_embed(e->stream, e->tok, e->h_io, M, use_embeds ? e->embeds : NULL, e->h, e->h_io + IO_POS,
-                   e->d_pos0);
+                   e->d_pos0, e->d_serial);
     e->hcur = e->h;
     enqueue_layers(e, M, keep_tiles);
     const int flag_valid = enqueue_head(e, M, only_last, early_tiles, early_margin, want_argmax, lm_host);
@@ -914,22 +932,33 @@ static void enqueue_layers(Engine* e, int32_t M, int32_t keep_tiles) {
             dpuf_hip_gemv(s, M, 2, js, NULL, 0.0f);
             tm_end(e, tm7);
         }
-        /* (8) SwiGLU + dead zone + prep of the down input */
-        const int tm8 = tm_begin(e, K_PREP, 0);
-        dpuf_hip_swiglu_prep(s, M, I, e->gate, e->up, e->deadzone, W[W_DOWN].sign, e->prep[0]);
-        tm_end(e, tm8);
-        /* (9) down projection, pruned to keep_tiles with the rest zeroed
-         * (dpuf_engine.c:2018-2044) */
+        /* (8) SwiGLU + dead zone + prep of the down input, (9) down
+         * projection, pruned to keep_tiles with the rest zeroed
+         * (dpuf_engine.c:2018-2044).  One row, nothing pruned: one launch
+         * whose producer workgroups run (8) while the GEMV workgroups stream
+         * their weights. */
         {
             int32_t nt = n_tiles_of(&W[W_DOWN]);
             int32_t kt = (keep_tiles > 0 && keep_tiles < nt) ? keep_tiles : nt;
             const DpufGemvJob j = lj.down;
-            const int tm9 = tm_begin(e, K_DOWN, gemv_bytes(&W[W_DOWN], 0, kt, M));
-            if (kt < nt)
-                dpuf_hip_gemv_zero(s, M, &j, kt * 16, W[W_DOWN].rows);
-            else
-                dpuf_hip_gemv(s, M, 1, &j, NULL, 0.0f);
-            tm_end(e, tm9);
+            int fused = 0;
+            if (M == 1 && kt == nt) {
+                const int tm9 = tm_begin(e, K_DOWN, gemv_bytes(&W[W_DOWN], 0, kt, M));
+                fused = dpuf_hip_swiglu_gemv(s, I, e->gate, e->up, e->deadzone, W[W_DOWN].sign, &j,
+                                             e->d_pflag + (size_t)l * 512, e->d_serial) == 0;
+                tm_end(e, tm9);
+            }
+            if (!fused) {
+                const int tm8 = tm_begin(e, K_PREP, 0);
+                dpuf_hip_swiglu_prep(s, M, I, e->gate, e->up, e->deadzone, W[W_DOWN].sign, e->prep[0]);
+                tm_end(e, tm8);
+                const int tm9 = tm_begin(e, K_DOWN, gemv_bytes(&W[W_DOWN], 0, kt, M));
+                if (kt < nt)
+                    dpuf_hip_gemv_zero(s, M, &j, kt * 16, W[W_DOWN].rows);
+                else
+                    dpuf_hip_gemv(s, M, 1, &j, NULL, 0.0f);
+                tm_end(e, tm9);
+            }
         }
         if (e->capture && M <= e->capture_cap)
             dpuf_hip_capture(s, M, H, e->hcur, e->hn, e->capture + (size_t)l * e->capture_cap * H);
@@ -1013,6 +1042,7 @@ static int32_t forward_common(Engine* e, int32_t n_tokens, const int32_t* token_
     volatile int32_t* io = e->h_io;
     for (int32_t m = 0; m < M; m++) io[m] = token_ids ? token_ids[m] : -1;
     io[IO_POS] = pos0;
+    io[IO_POS + 1] = next_serial(e);
     if (embeds_in) dpuf_hip_h2d(e->embeds, embeds_in, (size_t)M * e->H * 4, e->stream);
     /* a one-row LM head whose logits go to the host writes them to h_logits
      * itself (the same for every step of a graph key: want_argmax clear and
@@ -1127,6 +1157,7 @@ DPUF_EXPORT int32_t dpuf_amd_engine_forward_slots(void* handle, int32_t n, const
     volatile int32_t* io = e->h_io;
     for (int32_t i = 0; i < n; i++) io[i] = token_ids[i];
     io[IO_POS] = 0;
+    io[IO_POS + 1] = next_serial(e);
     dpuf_hip_h2d(e->d_ms_pos, positions, (size_t)n * 4, e->stream);
     dpuf_hip_h2d(e->d_ms_kc, ptrs, (size_t)n * sizeof(float*), e->stream);
     dpuf_hip_h2d(e->d_ms_vc, ptrs + n, (size_t)n * sizeof(float*), e->stream);

@@ -118,7 +118,7 @@ void dpuf_hip_graph_destroy(void* g);
 /* Kernels.  pos0 is read from device memory so a captured step replays at
  * any position. */
 void dpuf_hip_embed(void* s, DpufDevW w, const int32_t* ids, int32_t M, const float* embeds,
-                    float* out, const int32_t* pos_src, int32_t* pos_dst);
+                    float* out, const int32_t* pos_src, int32_t* pos_dst, int32_t* serial_dst);
 /* host[0..3) = {flag_valid ? words[0] : 0, words[1], words[2]} (words: the
  * device's early-exit flag, argmax token, error word) */
 void dpuf_hip_publish(void* s, const int32_t* words, int32_t flag_valid, int32_t* host);
@@ -133,6 +133,12 @@ void dpuf_hip_resnorm_prep(void* s, int32_t M, int32_t H, const float* h, const 
 void dpuf_hip_prep(void* s, int32_t M, int32_t K, const float* x, const uint8_t* sign, DpufPrep p);
 void dpuf_hip_swiglu_prep(void* s, int32_t M, int32_t I, const float* gate, const float* up,
                           float dz, const uint8_t* sign, DpufPrep p);
+/* M == 1: SwiGLU + prep of gate / up [I] and the GEMV of job over it in one
+ * launch; the producing workgroups set flags[0 .. 512) entries to the step
+ * serial *serial (device memory, a value new to these flags).  -1: the plan
+ * does not allow it (nothing launched; use the two calls above). */
+int32_t dpuf_hip_swiglu_gemv(void* s, int32_t I, const float* gate, const float* up, float dz, const uint8_t* sign,
+                             const DpufGemvJob* job, int32_t* flags, const int32_t* serial);
 /* .dpuf tile region of a mode 12 / 13 / 14 matrix (tile t at src + offs[t])
  * -> row-block layout. */
 void dpuf_hip_relayout(void* s, const uint8_t* src, const uint64_t* offs, int32_t n_groups, int32_t n_blk,

@@ -96,14 +96,17 @@ DEV float expf_libc(float x) { return expf_libc_tab(x, c_exp2_tab); }
 // ids (and pos_src) may sit in fine-grained host memory that the host wrote
 // just before the launch: system-scope loads read them past every cache.
 // Workgroup 0 copies the step's start position to pos_dst in device memory,
-// where the kernels after it read it.
+// where the kernels after it read it, and the step serial the host put next
+// to it (pos_src[1]) to serial_dst.
 __global__ void k_embed(DpufDevW w, const int32_t* __restrict__ ids, const float* __restrict__ embeds,
-                        float* __restrict__ out, const int32_t* pos_src, int32_t* pos_dst) {
+                        float* __restrict__ out, const int32_t* pos_src, int32_t* pos_dst, int32_t* serial_dst) {
     const int m = blockIdx.x;
     const int H = w.cols, n_blk = H >> 5;
     float* dst = out + (size_t)m * H;
     if (pos_dst && m == 0 && threadIdx.x == 0)
         *pos_dst = __hip_atomic_load(pos_src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    if (serial_dst && m == 0 && threadIdx.x == 0)
+        *serial_dst = __hip_atomic_load(pos_src + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     const int id = ids ? __hip_atomic_load(ids + m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) : -1;
     if (embeds && id < 0) {
         // H is a multiple of 64: float4 copies, eight loads in flight per thread
@@ -393,13 +396,14 @@ __global__ __launch_bounds__(256) void k_prep(int K, const float* __restrict__ x
 // A 64-block per 16-lane row, 4 columns per lane (row_prep64): a quarter of
 // the per-lane work of a quad per block, which is what bounds this
 // latency-bound step.  grid: (ceil(I / 256), M), one wave per workgroup.
-__global__ __launch_bounds__(64) void k_swiglu_prep(int I, const float* __restrict__ gate, const float* __restrict__ up,
-                                                    float dz, const uint8_t* __restrict__ sign, DpufPrep p) {
-    const int m = blockIdx.y, t = blockIdx.x * 64 + threadIdx.x;
-    const int blk = t >> 4, r = t & 15, nb = I >> 5;
-    if (64 * blk >= I) return;  // whole rows: I is a multiple of 64
-    const float4 g4 = *(const float4*)(gate + (size_t)m * I + 4 * t);
-    const float4 u4 = *(const float4*)(up + (size_t)m * I + 4 * t);
+// Lane t of one row: columns 4t .. 4t + 3 of the 64-block t / 16 (COH: see
+// row_prep64).
+template <bool COH = false>
+DEV void swiglu_prep_lane(int I, const float* __restrict__ gate, const float* __restrict__ up, float dz,
+                          const uint8_t* __restrict__ sign, int8_t* q, float* s, int32_t* m, uint16_t* h, int t) {
+    const int blk = t >> 4, r = t & 15;
+    const float4 g4 = *(const float4*)(gate + 4 * t);
+    const float4 u4 = *(const float4*)(up + 4 * t);
     const uint32_t sb = sign ? (sign[8 * blk + (r >> 1)] >> (4 * (r & 1))) & 0xFu : 0u;
     const float g[4] = {g4.x, g4.y, g4.z, g4.w}, u[4] = {u4.x, u4.y, u4.z, u4.w};
     float v[4];
@@ -411,8 +415,16 @@ __global__ __launch_bounds__(64) void k_swiglu_prep(int I, const float* __restri
         if (dz > 0.0f && !(fabsf(rr) >= dz)) rr = 0.0f;
         v[k] = ((sb >> k) & 1u) ? -rr : rr;
     }
-    row_prep64(v, r, blk, p.q + (size_t)m * I, p.s + (size_t)m * nb, p.m + (size_t)m * nb,
-               p.h ? p.h + (size_t)m * I : nullptr);
+    row_prep64<COH>(v, r, blk, q, s, m, h);
+}
+
+__global__ __launch_bounds__(64) void k_swiglu_prep(int I, const float* __restrict__ gate, const float* __restrict__ up,
+                                                    float dz, const uint8_t* __restrict__ sign, DpufPrep p) {
+    const int m = blockIdx.y, t = blockIdx.x * 64 + threadIdx.x;
+    const int nb = I >> 5;
+    if (64 * (t >> 4) >= I) return;  // whole rows: I is a multiple of 64
+    swiglu_prep_lane(I, gate + (size_t)m * I, up + (size_t)m * I, dz, sign, p.q + (size_t)m * I, p.s + (size_t)m * nb,
+                     p.m + (size_t)m * nb, p.h ? p.h + (size_t)m * I : nullptr, t);
 }
 
 // ---------------------------------------------------------------------------
@@ -594,6 +606,19 @@ struct MvArgs {
     const int32_t* skip_flag;
     float fill;
     int32_t* err;  // device error word: bit 0 set when a bounded LDS wait ran out
+    // Producer-fed launch (one job, one group per workgroup, activations
+    // held for the launch): the first np workgroups compute the job's
+    // activations, SwiGLU + dead zone + prep of gate / up [pI]
+    // (k_swiglu_prep's arithmetic), and each sets its flag pflag[p] to the
+    // step serial *pep; the GEMV workgroups after them issue their weight
+    // loads first and read the activations once every flag holds the serial.
+    int np, pI;
+    const float* pg;
+    const float* pu;
+    float pdz;
+    const uint8_t* psign;
+    int32_t* pflag;
+    const int32_t* pep;
 };
 
 // Activations of one round of one wave.
@@ -786,16 +811,61 @@ DEV void mv_chains(const MvGeo& G, int c, int n_my, int lane, uint8_t* smem, MvS
     }
 }
 
+// Flags of a producer-fed launch: MV_FLAG_COPIES copies of the np flags, 64
+// apart; a GEMV workgroup polls the copy of its XCD (workgroup b runs on XCD
+// b % 8), so the polls of the launch spread over that many cache lines.
+#define MV_FLAG_COPIES 8
+
+// Producer workgroup p of a producer-fed launch: lanes p * blockDim .. of
+// the SwiGLU + prep row, written with agent-scope stores (past the L2, to
+// where every XCD reads: no L2 writeback, which walks the whole cache).
+// Every wave waits until its stores are done; after the barrier the flag
+// copies take the step serial.
+DEV void mv_produce(const MvArgs& A, int p) {
+    const int t = p * (int)blockDim.x + (int)threadIdx.x;
+    const DpufPrep& P = A.j[0].x;
+    if (64 * (t >> 4) < A.pI) swiglu_prep_lane<true>(A.pI, A.pg, A.pu, A.pdz, A.psign, P.q, P.s, P.m, nullptr, t);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int32_t ep = *A.pep;
+        for (int c = 0; c < MV_FLAG_COPIES; c++)
+            __hip_atomic_store(A.pflag + 64 * c + p, ep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+// Until every producer flag holds ep (lane i polls flag i, agent-scope
+// loads, which see the producers' written-back stores); at most 2^20 polls,
+// false when they ran out.  The exit test is a ballot: wave-uniform.
+DEV bool mv_wait_producers(const int32_t* flags, int np, int32_t ep, int lane) {
+    int spins = 0;
+#pragma clang loop unroll(disable)
+    while (true) {
+        const int32_t f = lane < np ? __hip_atomic_load(flags + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : ep;
+        if (__ballot(f != ep) == 0) return true;
+        if (++spins >= (1 << 20)) return false;
+        __builtin_amdgcn_s_sleep(2);
+    }
+}
+
 template <int NL, bool HOIST, bool SINGLE, int MODE>
 __global__ __launch_bounds__(1024) void k_mv(MvArgs A) {
     extern __shared__ __align__(16) uint8_t smem[];
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    int bid = blockIdx.x;
+    if (SINGLE && HOIST && A.np > 0) {
+        if (bid < A.np) {
+            mv_produce(A, bid);
+            return;
+        }
+        bid -= A.np;
+    }
     int ji = 0;
-    if (A.n_jobs > 1 && (int)blockIdx.x >= A.wb[1]) ji = 1;
-    if (A.n_jobs > 2 && (int)blockIdx.x >= A.wb[2]) ji = 2;
+    if (A.n_jobs > 1 && bid >= A.wb[1]) ji = 1;
+    if (A.n_jobs > 2 && bid >= A.wb[2]) ji = 2;
     const MvJob& J = A.j[ji];
     MvGeo G;
-    G.lb = blockIdx.x - A.wb[ji];
+    G.lb = bid - A.wb[ji];
     G.nwg = A.wb[ji + 1] - A.wb[ji];
     G.g = J.g;
     G.out = J.out;
@@ -832,10 +902,30 @@ __global__ __launch_bounds__(1024) void k_mv(MvArgs A) {
         // one group per workgroup: no chain waves, one barrier, wave 0 chains
         MvX<NL> X1;
         MvU<NL> L1;
-        if (HOIST) mv_load_x<NL>(G, 0, w, lane, X1);
-        for (int r = 0; r < G.R; r++) {
-            mv_issue<NL, HOIST, MODE>(G, r, w, lane, L1);
-            mv_dots<NL, HOIST, MODE>(G, r, w, lane, L1, X1, (float2*)smem);
+        if (HOIST && A.np > 0) {
+            // producer-fed (one round: HOIST): the weights first, then this
+            // step's producer flags, then the activations they published
+            const int32_t ep = *A.pep;
+            mv_issue<NL, HOIST, MODE>(G, 0, w, lane, L1);
+            // one wave polls (the flag lines see one load per workgroup and
+            // poll, not one per wave); the others wait at the barrier
+            if (w == 0 && !mv_wait_producers(A.pflag + 64 * (blockIdx.x % MV_FLAG_COPIES), A.np, ep, lane) &&
+                lane == 0)
+                mv_wait_failed(G.err);
+            __syncthreads();
+            // Plain loads see the producers' data: every cache level was
+            // invalidated when the launch began and no wave of it touches
+            // these lines before their flags are set (only the flags, which
+            // change during the launch, need the agent-scope polls).
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);  // the activation loads stay after the wait
+            mv_load_x<NL>(G, 0, w, lane, X1);
+            mv_dots<NL, HOIST, MODE>(G, 0, w, lane, L1, X1, (float2*)smem);
+        } else {
+            if (HOIST) mv_load_x<NL>(G, 0, w, lane, X1);
+            for (int r = 0; r < G.R; r++) {
+                mv_issue<NL, HOIST, MODE>(G, r, w, lane, L1);
+                mv_dots<NL, HOIST, MODE>(G, r, w, lane, L1, X1, (float2*)smem);
+            }
         }
         __syncthreads();
         if (w == 0 && lane < 8) {
@@ -4079,10 +4169,11 @@ int32_t dpuf_hip_graph_launch(void* g, void* s) {
 void dpuf_hip_graph_destroy(void* g) { if (g) (void)hipGraphExecDestroy((hipGraphExec_t)g); }
 
 void dpuf_hip_embed(void* s, DpufDevW w, const int32_t* ids, int32_t M, const float* embeds, float* out,
-                    const int32_t* pos_src, int32_t* pos_dst) {
+                    const int32_t* pos_src, int32_t* pos_dst, int32_t* serial_dst) {
     int threads = (w.cols >> 6) < 256 ? (w.cols >> 6) : 256;
     threads = (threads + 63) & ~63;
-    hipLaunchKernelGGL(k_embed, dim3(M), dim3(threads), 0, ST(s), w, ids, embeds, out, pos_src, pos_dst);
+    hipLaunchKernelGGL(k_embed, dim3(M), dim3(threads), 0, ST(s), w, ids, embeds, out, pos_src, pos_dst,
+                       serial_dst);
     LAUNCHED("k_embed");
 }
 
@@ -4301,6 +4392,59 @@ static void mv_launch(void* s, MvArgs& A, const int* n_groups, int mode) {
     const size_t lds = (size_t)A.nbuf * buf;
     hipLaunchKernelGGL(A.nc ? k : k1, dim3(grid), dim3(threads), lds, ST(s), A);
     LAUNCHED("k_mv");
+}
+
+// SwiGLU + dead zone + prep of gate / up [I] and the one-row GEMV of job over
+// them in one launch: producer workgroups first (k_mv's producer-fed mode),
+// the MV_FLAG_COPIES copies flags[64 c + p] of producer p set to the step serial *serial when its share is out.
+// Only for a plan of one group per workgroup with the activations held
+// (every workgroup resident at once, weights issued before the wait);
+// returns -1 without launching otherwise.
+int32_t dpuf_hip_swiglu_gemv(void* s, int32_t I, const float* gate, const float* up, float dz, const uint8_t* sign,
+                             const DpufGemvJob* job, int32_t* flags, const int32_t* serial) {
+    const int mode = job->w.mode;
+    if ((mode != 12 && mode != 13 && mode != 14) || job->w.cols != I || I <= 0 || I % 64 || !flags || !serial)
+        return -1;
+    const int n_blk = I >> 5, S = (n_blk + 7) >> 3;
+    if (S > (MV_HOIST48 ? 4 : 3) * (16 - MV_NC)) return -1;  // activations loaded per round: no such mode
+    const int ng = job->g1 - job->g0 > 0 ? job->g1 - job->g0 : 0;
+    MvKernel k, k1;
+    int nw, most, wb[4] = {0, 0, 0, 0};
+    if (mv_plan(1, &ng, I, mode, k, k1, nw, wb, most) == 0 || most != 1) return -1;
+    const int threads = nw * 64, np = (I / 4 + threads - 1) / threads;
+    if (np > 64) return -1;
+    if (!g_err_word) {
+        note(hipErrorInvalidValue, "dpuf_hip_swiglu_gemv: no device error word bound");
+        return -1;
+    }
+    MvArgs A;
+    memset(&A, 0, sizeof A);
+    A.n_jobs = 1;
+    A.K = I;
+    A.j[0].g = job->w.g;
+    A.j[0].out = job->out;
+    A.j[0].g0 = job->g0;
+    A.j[0].g1 = job->g1;
+    A.j[0].rows = job->w.rows;
+    A.j[0].x = job->p;
+    A.j[0].x.h = NULL;
+    A.wb[0] = wb[0];
+    A.wb[1] = wb[1];
+    A.err = g_err_word;
+    A.nbuf = 1;
+    A.nc = 0;
+    A.np = np;
+    A.pI = I;
+    A.pg = gate;
+    A.pu = up;
+    A.pdz = dz;
+    A.psign = sign;
+    A.pflag = flags;
+    A.pep = serial;
+    const size_t lds = (size_t)8 * (n_blk + 2) * 8;
+    hipLaunchKernelGGL(k1, dim3(np + wb[1]), dim3(threads), lds, ST(s), A);
+    LAUNCHED("k_mv");
+    return 0;
 }
 
 static void gm_launch(void* s, int32_t M, int32_t n_jobs, const DpufGemvJob* jobs, float* zo, int32_t zld, int32_t z0,
