@@ -63,9 +63,10 @@ typedef struct {
     DpufPrep prep[3];
     int32_t *d_ids, *d_pos0, *d_flag, *d_tok, *d_err;
     /* step serial: the host numbers every forward call (h_io[IO_POS + 1]),
-     * the embedding kernel copies it to d_serial; d_pflag [L][512] are the
-     * producer flags of the one-row SwiGLU + down launches, which take the
-     * serial of the step that set them (never reset) */
+     * the embedding kernel copies it to d_serial; d_pflag [L][2][512] are
+     * the producer flags of the one-row launches that prep their own input
+     * (O projection: slot 0, down projection: slot 1), which take the serial
+     * of the step that set them (never reset) */
     int32_t *d_serial, *d_pflag;
     int32_t serial;
     void* d_red; /* partials of the device argmax / top-2 reductions */
@@ -613,9 +614,9 @@ DPUF_EXPORT void* dpuf_engine_create(const DpufModelConfig* cfg, const DpufLayer
         e->d_tok = e->d_ids + B + 2;
         e->d_err = e->d_ids + B + 3;
         e->d_serial = e->d_ids + B + 4;
-        e->d_pflag = (int32_t*)dpuf_hip_malloc((size_t)(e->L > 0 ? e->L : 1) * 512 * 4);
+        e->d_pflag = (int32_t*)dpuf_hip_malloc((size_t)(e->L > 0 ? e->L : 1) * 1024 * 4);
         if (!e->d_pflag) goto fail;
-        dpuf_hip_fill_zero(e->d_pflag, (size_t)(e->L > 0 ? e->L : 1) * 512 * 4, e->stream);
+        dpuf_hip_fill_zero(e->d_pflag, (size_t)(e->L > 0 ? e->L : 1) * 1024 * 4, e->stream);
         dpuf_hip_fill_zero(e->d_ids, (B + 64) * 4, e->stream);
         memset(e->h_io, 0, (B + 64) * 4);
         dpuf_hip_fill_zero(e->hn, B * e->H * 4, e->stream);
@@ -846,6 +847,7 @@ static void enqueue_layers(Engine* e, int32_t M, int32_t keep_tiles) {
         const DpufGemvJob* jqkv = lj.qkv;
         const DpufGemvJob jo = lj.o;
         const DpufGemvJob* jgu = lj.gu;
+        int o_prep = 0; /* the O input still needs its prep (one-row steps) */
 
         /* (1) [h += down] + attn RMSNorm + prep of the Q/K/V input */
         {
@@ -881,7 +883,8 @@ static void enqueue_layers(Engine* e, int32_t M, int32_t keep_tiles) {
                                     e->d_cos, e->d_sin, NULL, NULL, e->d_pos0, e->nq, e->nkv, e->hd, e->max_seq, &c8);
                 dpuf_hip_attn_q8(s, M, e->capturing ? e->max_seq : e->host_pos0 + M, e->q, c8, e->ao, e->scores,
                                  e->d_pos0, e->nq, e->nkv, e->hd, e->max_seq, scale);
-                dpuf_hip_prep(s, M, e->qd, e->ao, W[W_O].sign, e->prep[0]);
+                if (M > 1) dpuf_hip_prep(s, M, e->qd, e->ao, W[W_O].sign, e->prep[0]);
+                o_prep = M == 1;
                 fused = 1;
             } else if (e->ms_n > 0)  /* one token per session, each with its own cache */
                 fused = dpuf_hip_attn_dec(s, M, e->q, e->k, e->v, e->d_norm[4 * l + 1], e->d_norm[4 * l + 2], eps,
@@ -904,14 +907,21 @@ static void enqueue_layers(Engine* e, int32_t M, int32_t keep_tiles) {
                                         e->hd, e->max_seq, scale, W[W_O].sign, e->prep[0], &prepped) != 0)
                     dpuf_hip_attn(s, M, e->q, kc, vc, e->ao, e->scores, e->d_pos0, e->nq, e->nkv, e->hd,
                                   e->max_seq, scale);
-                if (!prepped) dpuf_hip_prep(s, M, e->qd, e->ao, W[W_O].sign, e->prep[0]);
+                /* one row: the O launch preps its own input (below) */
+                if (!prepped && M > 1) dpuf_hip_prep(s, M, e->qd, e->ao, W[W_O].sign, e->prep[0]);
+                o_prep = !prepped && M == 1;
             }
             tm_end(e, tm);
         }
         {
             const DpufGemvJob j = jo;
             const int tm5 = tm_begin(e, K_O, gemv_bytes(&W[W_O], 0, n_tiles_of(&W[W_O]), M));
-            dpuf_hip_gemv(s, M, 1, &j, NULL, 0.0f);
+            /* a pending O-input prep runs inside the O launch when it can */
+            if (!o_prep || dpuf_hip_swiglu_gemv(s, e->qd, e->ao, NULL, 0.0f, W[W_O].sign, &j,
+                                                e->d_pflag + (size_t)l * 1024, e->d_serial) != 0) {
+                if (o_prep) dpuf_hip_prep(s, M, e->qd, e->ao, W[W_O].sign, e->prep[0]);
+                dpuf_hip_gemv(s, M, 1, &j, NULL, 0.0f);
+            }
             tm_end(e, tm5);
         }
         /* (6) h += O; FFN RMSNorm; prep of gate/up input */
@@ -945,7 +955,7 @@ static void enqueue_layers(Engine* e, int32_t M, int32_t keep_tiles) {
             if (M == 1 && kt == nt) {
                 const int tm9 = tm_begin(e, K_DOWN, gemv_bytes(&W[W_DOWN], 0, kt, M));
                 fused = dpuf_hip_swiglu_gemv(s, I, e->gate, e->up, e->deadzone, W[W_DOWN].sign, &j,
-                                             e->d_pflag + (size_t)l * 512, e->d_serial) == 0;
+                                             e->d_pflag + (size_t)l * 1024 + 512, e->d_serial) == 0;
                 tm_end(e, tm9);
             }
             if (!fused) {

@@ -133,8 +133,9 @@ void dpuf_hip_resnorm_prep(void* s, int32_t M, int32_t H, const float* h, const 
 void dpuf_hip_prep(void* s, int32_t M, int32_t K, const float* x, const uint8_t* sign, DpufPrep p);
 void dpuf_hip_swiglu_prep(void* s, int32_t M, int32_t I, const float* gate, const float* up,
                           float dz, const uint8_t* sign, DpufPrep p);
-/* M == 1: SwiGLU + prep of gate / up [I] and the GEMV of job over it in one
- * launch; the producing workgroups set flags[0 .. 512) entries to the step
+/* M == 1: SwiGLU + prep of gate / up [I] (up NULL: the plain prep of gate)
+ * and the GEMV of job over it in one launch; the producing workgroups set
+ * flags[0 .. 512) entries to the step
  * serial *serial (device memory, a value new to these flags).  -1: the plan
  * does not allow it (nothing launched; use the two calls above). */
 int32_t dpuf_hip_swiglu_gemv(void* s, int32_t I, const float* gate, const float* up, float dz, const uint8_t* sign,

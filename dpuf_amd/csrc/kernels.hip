@@ -418,6 +418,19 @@ DEV void swiglu_prep_lane(int I, const float* __restrict__ gate, const float* __
     row_prep64<COH>(v, r, blk, q, s, m, h);
 }
 
+// The plain prep of lane t of one row (columns 4t .. 4t + 3): sign, then
+// row_prep64 (COH: see row_prep64).
+template <bool COH = false>
+DEV void prep_lane(const float* __restrict__ x, const uint8_t* __restrict__ sign, int8_t* q, float* s, int32_t* m, int t) {
+    const int blk = t >> 4, r = t & 15;
+    const float4 x4 = *(const float4*)(x + 4 * t);
+    const uint32_t sb = sign ? (sign[8 * blk + (r >> 1)] >> (4 * (r & 1))) & 0xFu : 0u;
+    float v[4] = {x4.x, x4.y, x4.z, x4.w};
+#pragma unroll
+    for (int k = 0; k < 4; k++) v[k] = ((sb >> k) & 1u) ? -v[k] : v[k];
+    row_prep64<COH>(v, r, blk, q, s, m, nullptr);
+}
+
 __global__ __launch_bounds__(64) void k_swiglu_prep(int I, const float* __restrict__ gate, const float* __restrict__ up,
                                                     float dz, const uint8_t* __restrict__ sign, DpufPrep p) {
     const int m = blockIdx.y, t = blockIdx.x * 64 + threadIdx.x;
@@ -608,10 +621,11 @@ struct MvArgs {
     int32_t* err;  // device error word: bit 0 set when a bounded LDS wait ran out
     // Producer-fed launch (one job, one group per workgroup, activations
     // held for the launch): the first np workgroups compute the job's
-    // activations, SwiGLU + dead zone + prep of gate / up [pI]
-    // (k_swiglu_prep's arithmetic), and each sets its flag pflag[p] to the
-    // step serial *pep; the GEMV workgroups after them issue their weight
-    // loads first and read the activations once every flag holds the serial.
+    // activations, SwiGLU + dead zone + prep of gate pg / up pu [pI]
+    // (k_swiglu_prep's arithmetic), or with pu NULL the plain prep of pg
+    // (k_prep's), and each sets its flag pflag[p] to the step serial *pep;
+    // the GEMV workgroups after them issue their weight loads first and read
+    // the activations once every flag holds the serial.
     int np, pI;
     const float* pg;
     const float* pu;
@@ -824,7 +838,10 @@ DEV void mv_chains(const MvGeo& G, int c, int n_my, int lane, uint8_t* smem, MvS
 DEV void mv_produce(const MvArgs& A, int p) {
     const int t = p * (int)blockDim.x + (int)threadIdx.x;
     const DpufPrep& P = A.j[0].x;
-    if (64 * (t >> 4) < A.pI) swiglu_prep_lane<true>(A.pI, A.pg, A.pu, A.pdz, A.psign, P.q, P.s, P.m, nullptr, t);
+    if (64 * (t >> 4) < A.pI) {
+        if (A.pu) swiglu_prep_lane<true>(A.pI, A.pg, A.pu, A.pdz, A.psign, P.q, P.s, P.m, nullptr, t);
+        else prep_lane<true>(A.pg, A.psign, P.q, P.s, P.m, t);
+    }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -4394,8 +4411,9 @@ static void mv_launch(void* s, MvArgs& A, const int* n_groups, int mode) {
     LAUNCHED("k_mv");
 }
 
-// SwiGLU + dead zone + prep of gate / up [I] and the one-row GEMV of job over
-// them in one launch: producer workgroups first (k_mv's producer-fed mode),
+// SwiGLU + dead zone + prep of gate / up [I] (up NULL: the plain prep of
+// gate) and the one-row GEMV of job over them in one launch: producer
+// workgroups first (k_mv's producer-fed mode),
 // the MV_FLAG_COPIES copies flags[64 c + p] of producer p set to the step serial *serial when its share is out.
 // Only for a plan of one group per workgroup with the activations held
 // (every workgroup resident at once, weights issued before the wait);
