@@ -865,12 +865,14 @@ DEV bool mv_wait_producers(const int32_t* flags, int np, int32_t ep, int lane) {
     }
 }
 
-template <int NL, bool HOIST, bool SINGLE, int MODE>
+// FED: the producer-fed mode (one group per workgroup, activations held),
+// an instance of its own so the other instances keep their registers.
+template <int NL, bool HOIST, bool SINGLE, int MODE, bool FED = false>
 __global__ __launch_bounds__(1024) void k_mv(MvArgs A) {
     extern __shared__ __align__(16) uint8_t smem[];
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
     int bid = blockIdx.x;
-    if (SINGLE && HOIST && A.np > 0) {
+    if (FED) {
         if (bid < A.np) {
             mv_produce(A, bid);
             return;
@@ -919,7 +921,7 @@ __global__ __launch_bounds__(1024) void k_mv(MvArgs A) {
         // one group per workgroup: no chain waves, one barrier, wave 0 chains
         MvX<NL> X1;
         MvU<NL> L1;
-        if (HOIST && A.np > 0) {
+        if (FED) {
             // producer-fed (one round: HOIST): the weights first, then this
             // step's producer flags, then the activations they published
             const int32_t ep = *A.pep;
@@ -4411,6 +4413,20 @@ static void mv_launch(void* s, MvArgs& A, const int* n_groups, int mode) {
     LAUNCHED("k_mv");
 }
 
+// The producer-fed instance with nl steps per loader wave.
+extern "C++" {
+template <int MODE>
+static MvKernel mv_fed_of(int nl) {
+    return nl == 1 ? k_mv<1, true, true, MODE, true>
+         : nl == 2 ? k_mv<2, true, true, MODE, true>
+         : nl == 3 ? k_mv<3, true, true, MODE, true>
+                   : k_mv<4, true, true, MODE, true>;
+}
+}
+static MvKernel mv_fed_kernel(int mode, int nl) {
+    return mode == 13 ? mv_fed_of<13>(nl) : mode == 14 ? mv_fed_of<14>(nl) : mv_fed_of<12>(nl);
+}
+
 // SwiGLU + dead zone + prep of gate / up [I] (up NULL: the plain prep of
 // gate) and the one-row GEMV of job over them in one launch: producer
 // workgroups first (k_mv's producer-fed mode),
@@ -4431,6 +4447,10 @@ int32_t dpuf_hip_swiglu_gemv(void* s, int32_t I, const float* gate, const float*
     if (mv_plan(1, &ng, I, mode, k, k1, nw, wb, most) == 0 || most != 1) return -1;
     const int threads = nw * 64, np = (I / 4 + threads - 1) / threads;
     if (np > 64) return -1;
+    const int nl = S <= 16 - MV_NC ? 1 : S <= 2 * (16 - MV_NC) ? 2 : S <= 3 * (16 - MV_NC) ? 3 : 4;
+    MvKernel kf = mv_fed_kernel(mode, nl);
+    const size_t lds = (size_t)8 * (n_blk + 2) * 8;
+    if (ng > mv_capacity(kf, threads, lds)) return -1;  // every GEMV workgroup resident at once
     if (!g_err_word) {
         note(hipErrorInvalidValue, "dpuf_hip_swiglu_gemv: no device error word bound");
         return -1;
@@ -4459,8 +4479,7 @@ int32_t dpuf_hip_swiglu_gemv(void* s, int32_t I, const float* gate, const float*
     A.psign = sign;
     A.pflag = flags;
     A.pep = serial;
-    const size_t lds = (size_t)8 * (n_blk + 2) * 8;
-    hipLaunchKernelGGL(k1, dim3(np + wb[1]), dim3(threads), lds, ST(s), A);
+    hipLaunchKernelGGL(kf, dim3(np + wb[1]), dim3(threads), lds, ST(s), A);
     LAUNCHED("k_mv");
     return 0;
 }
