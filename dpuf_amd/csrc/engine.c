@@ -897,16 +897,25 @@ static void enqueue_layers(Engine* e, int32_t M, int32_t keep_tiles) {
                                           scale, e->ao, W[W_O].sign, e->prep[0], NULL, NULL, 0,
                                           attn_warm(e, &lj, ln)) == 0;
             if (!fused) {
-                dpuf_hip_qk_rope_kv(s, M, e->q, e->k, e->v, e->d_norm[4 * l + 1], e->d_norm[4 * l + 2], eps,
-                                    e->d_cos, e->d_sin, kc, vc, e->d_pos0, e->nq, e->nkv, e->hd, e->max_seq, NULL);
                 const int32_t lmax = e->capturing ? e->max_seq : e->host_pos0 + M;
                 /* the O-input prep rides with the last attention kernel when
                  * it can; otherwise it is a launch of its own */
                 int32_t prepped = 0;
-                if (dpuf_hip_attn_split(s, M, lmax, e->q, kc, vc, e->ao, e->scores, e->d_pos0, e->nq, e->nkv,
-                                        e->hd, e->max_seq, scale, W[W_O].sign, e->prep[0], &prepped) != 0)
-                    dpuf_hip_attn(s, M, e->q, kc, vc, e->ao, e->scores, e->d_pos0, e->nq, e->nkv, e->hd,
-                                  e->max_seq, scale);
+                /* one token: QK-norm, RoPE and the KV store inside the scores
+                 * launch when the wide kernels apply */
+                const int rope_done =
+                    M == 1 && dpuf_hip_attn_decode_rope(s, lmax, e->q, e->k, e->v, e->d_norm[4 * l + 1],
+                                                        e->d_norm[4 * l + 2], eps, e->d_cos, e->d_sin, kc, vc, e->ao,
+                                                        e->scores, e->d_pos0, e->nq, e->nkv, e->hd, e->max_seq,
+                                                        scale) == 0;
+                if (!rope_done) {
+                    dpuf_hip_qk_rope_kv(s, M, e->q, e->k, e->v, e->d_norm[4 * l + 1], e->d_norm[4 * l + 2], eps,
+                                        e->d_cos, e->d_sin, kc, vc, e->d_pos0, e->nq, e->nkv, e->hd, e->max_seq, NULL);
+                    if (dpuf_hip_attn_split(s, M, lmax, e->q, kc, vc, e->ao, e->scores, e->d_pos0, e->nq, e->nkv,
+                                            e->hd, e->max_seq, scale, W[W_O].sign, e->prep[0], &prepped) != 0)
+                        dpuf_hip_attn(s, M, e->q, kc, vc, e->ao, e->scores, e->d_pos0, e->nq, e->nkv, e->hd,
+                                      e->max_seq, scale);
+                }
                 /* one row: the O launch preps its own input (below) */
                 if (!prepped && M > 1) dpuf_hip_prep(s, M, e->qd, e->ao, W[W_O].sign, e->prep[0]);
                 o_prep = !prepped && M == 1;

@@ -180,6 +180,14 @@ void dpuf_hip_attn(void* s, int32_t M, const float* q, const float* kc, const fl
 int32_t dpuf_hip_attn_split(void* s, int32_t M, int32_t lmax, const float* q, const float* kc, const float* vc,
                             float* out, float* scores, const int32_t* pos0p, int32_t n_q, int32_t n_kv, int32_t hd,
                             int32_t max_seq, float scale, const uint8_t* o_sign, DpufPrep op, int32_t* prepped);
+/* One-token decode past the fused kernel's range (the split path's wide
+ * kernels) with the QK-norm, RoPE and KV store of the token (raw q, k, v)
+ * done inside the scores launch; -1 with nothing launched when that path
+ * does not apply (then qk_rope_kv + attn_split). */
+int32_t dpuf_hip_attn_decode_rope(void* s, int32_t lmax, float* q, const float* k, const float* v, const float* qn,
+                                  const float* kn, float eps, const float* cos_tab, const float* sin_tab, float* kc,
+                                  float* vc, float* out, float* scores, const int32_t* pos0p, int32_t n_q,
+                                  int32_t n_kv, int32_t hd, int32_t max_seq, float scale);
 /* Attention over the int8 KV cache (kv_type 1) for M tokens at positions
  * pos0 .. pos0 + M - 1 of one layer; lmax bounds the keys any replay reaches. */
 void dpuf_hip_attn_q8(void* s, int32_t M, int32_t lmax, const float* q, DpufKvQ8 c8, float* out, float* scores,

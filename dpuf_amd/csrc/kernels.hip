@@ -1803,6 +1803,58 @@ DEV void q8_store_lane(float val, int lane, int e, int8_t* row, float* srow) {
     if ((lane & 31) == 0) srow[2 * e + (lane >> 5)] = a / 127.0f;
 }
 
+// QK-norm (reference rms_norm_f32 over one head, dpuf_engine.c:225-241) and
+// NeoX RoPE of one head by one wave, element i = lane + 64 e in x[e]: the
+// inputs come from qk_head_load (every load first, one memory round trip).
+template <int HD>
+struct QkHead {
+    float x[HD / 64], wn[HD / 64], cs[HD / 64], sn[HD / 64];
+};
+
+template <int HD>
+DEV void qk_head_load(const float* vec, const float* nw, const float* cos_tab, const float* sin_tab, int pos, int lane,
+                      QkHead<HD>& h) {
+    constexpr int E = HD / 64, half = HD / 2;
+#pragma unroll
+    for (int e = 0; e < E; e++) {
+        const int i = lane + 64 * e, j = i < half ? i : i - half;
+        h.x[e] = vec[i];
+        h.wn[e] = nw ? nw[i] : 1.0f;
+        h.cs[e] = cos_tab[(size_t)pos * half + j];
+        h.sn[e] = sin_tab[(size_t)pos * half + j];
+    }
+}
+
+template <int HD>
+DEV void qk_head_rope(QkHead<HD>& h, bool norm, float eps, int lane, float (&o)[HD / 64]) {
+    constexpr int E = HD / 64, half = HD / 2;
+    if (norm) {
+        // chain j = lane (< 8): elements j + 8i, i = 0 .. HD/8 - 1, in order
+        float a = 0.0f;
+#pragma unroll
+        for (int i = 0; i < HD / 8; i++) {
+            // element (lane & 7) + 8i: register i / 8 of lane (lane & 7) + 8 (i % 8)
+            const float xv = __shfl(h.x[i / 8], (lane & 7) + 8 * (i % 8), 64);
+            a = fmaf(xv, xv, a);
+        }
+        float pt[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) pt[j] = __shfl(a, j, 64);
+        const float inv = 1.0f / sqrtf(hsum8(pt) / (float)HD + eps);
+#pragma unroll
+        for (int e = 0; e < E; e++) h.x[e] = (h.x[e] * inv) * h.wn[e];
+    }
+#pragma unroll
+    for (int e = 0; e < E; e++) {
+        const int i = lane + 64 * e;
+        float partner;
+        if (E == 1) partner = __shfl_xor(h.x[0], 32, 64);  // element i ^ 32 = i +- half
+        else partner = h.x[i < half ? e + E / 2 : e - E / 2];
+        if (i < half) o[e] = fmaf(h.x[e], h.cs[e], -(partner * h.sn[e]));
+        else o[e] = fmaf(h.x[e], h.cs[e], partner * h.sn[e]);
+    }
+}
+
 template <int HD, bool Q8>
 __global__ __launch_bounds__(256) void k_qk_rope_kv_w(float* __restrict__ q, float* __restrict__ k,
                                                       const float* __restrict__ v, const float* __restrict__ qn,
@@ -1811,7 +1863,7 @@ __global__ __launch_bounds__(256) void k_qk_rope_kv_w(float* __restrict__ q, flo
                                                       const float* __restrict__ sin_tab, float* __restrict__ kc,
                                                       float* __restrict__ vc, const int32_t* __restrict__ pos0p, int M,
                                                       int n_q, int n_kv, int max_seq, DpufKvQ8 c8) {
-    constexpr int E = HD / 64, half = HD / 2;
+    constexpr int E = HD / 64;
     const int lane = threadIdx.x & 63;
     const int u = blockIdx.x * 4 + (threadIdx.x >> 6);  // (token, head) unit of this wave
     const int nh = n_q + n_kv;
@@ -1823,42 +1875,13 @@ __global__ __launch_bounds__(256) void k_qk_rope_kv_w(float* __restrict__ q, flo
     float* vec = is_k ? (k + ((size_t)m * n_kv + hh) * HD) : (q + ((size_t)m * n_q + hh) * HD);
     const float* nw = is_k ? kn : qn;
     // every load first: one memory round trip for the whole wave
-    float x[E], wn[E], cs[E], sn[E], vv[E];
+    QkHead<HD> hd_;
+    float vv[E];
+    qk_head_load<HD>(vec, nw, cos_tab, sin_tab, pos, lane, hd_);
 #pragma unroll
-    for (int e = 0; e < E; e++) {
-        const int i = lane + 64 * e, j = i < half ? i : i - half;
-        x[e] = vec[i];
-        wn[e] = nw ? nw[i] : 1.0f;
-        cs[e] = cos_tab[(size_t)pos * half + j];
-        sn[e] = sin_tab[(size_t)pos * half + j];
-        vv[e] = is_k ? v[((size_t)m * n_kv + hh) * HD + i] : 0.0f;
-    }
-    if (nw) {
-        // chain j = lane (< 8): elements j + 8i, i = 0 .. HD/8 - 1, in order
-        float a = 0.0f;
-#pragma unroll
-        for (int i = 0; i < HD / 8; i++) {
-            // element (lane & 7) + 8i: register i / 8 of lane (lane & 7) + 8 (i % 8)
-            const float xv = __shfl(x[i / 8], (lane & 7) + 8 * (i % 8), 64);
-            a = fmaf(xv, xv, a);
-        }
-        float pt[8];
-#pragma unroll
-        for (int j = 0; j < 8; j++) pt[j] = __shfl(a, j, 64);
-        const float inv = 1.0f / sqrtf(hsum8(pt) / (float)HD + eps);
-#pragma unroll
-        for (int e = 0; e < E; e++) x[e] = (x[e] * inv) * wn[e];
-    }
+    for (int e = 0; e < E; e++) vv[e] = is_k ? v[((size_t)m * n_kv + hh) * HD + lane + 64 * e] : 0.0f;
     float o[E];
-#pragma unroll
-    for (int e = 0; e < E; e++) {
-        const int i = lane + 64 * e;
-        float partner;
-        if (E == 1) partner = __shfl_xor(x[0], 32, 64);  // element i ^ 32 = i +- half
-        else partner = x[i < half ? e + E / 2 : e - E / 2];
-        if (i < half) o[e] = fmaf(x[e], cs[e], -(partner * sn[e]));
-        else o[e] = fmaf(x[e], cs[e], partner * sn[e]);
-    }
+    qk_head_rope<HD>(hd_, nw != nullptr, eps, lane, o);
 #pragma unroll
     for (int e = 0; e < E; e++) vec[lane + 64 * e] = o[e];
     if (is_k && Q8) {
@@ -2046,18 +2069,42 @@ __global__ __launch_bounds__(256) void k_attn_sc(const float* __restrict__ q, co
 // stride of HD + 8 words, so the quad reads of 8 consecutive keys fall on
 // distinct banks.
 // ---------------------------------------------------------------------------
-template <int HD, int GM>
+// ROPE: q, k and v are the projections' raw rows; the workgroup applies the
+// QK-norm and RoPE to its group's q rows itself (as k_qk_rope_kv_w does, by
+// qk_head_rope), and the workgroup whose chunk holds the token's position
+// does the same to its K row, stores K and V to the cache at that position
+// and uses the new K row in its scores (so no launch before this one).
+struct ScRope {
+    const float* k;  // raw K and V of the token [n_kv][HD]
+    const float* v;
+    const float* qn;  // QK-norm weights (NULL: no norm)
+    const float* kn;
+    float eps;
+    const float* cos_tab;
+    const float* sin_tab;
+    float* kc;  // the cache rows written at the position
+    float* vc;
+};
+
+template <int HD, int GM, bool ROPE>
 __global__ __launch_bounds__(256) void k_attn_sc1(const float* __restrict__ q, const float* __restrict__ kc,
                                                   const int32_t* __restrict__ pos0p, int n_q, int n_kv, int max_seq,
-                                                  float scale, float* __restrict__ S) {
-    constexpr int LD = HD + 8;
+                                                  float scale, float* __restrict__ S, ScRope ra) {
+    constexpr int LD = HD + 8, E = HD / 64;
     extern __shared__ __align__(16) float sm[];
     float* ks = sm;               // [AS_KC][LD]
     float* qs = ks + AS_KC * LD;  // [GM][HD]
     const int kvh = blockIdx.x, t0 = blockIdx.y * AS_KC, tid = threadIdx.x;
     const int G = n_q / n_kv;
-    const int L = *pos0p + 1;
+    const int pos = *pos0p, L = pos + 1;
     if (t0 >= L) return;  // every key of the chunk is past the row
+    // ROPE units of wave tid / 64: q rows u < GM, then (if this chunk holds
+    // the position) the new K row as unit GM; a wave takes u = w, w + 4, w + 8
+    const int w = tid >> 6, lane = tid & 63;
+    const bool has_new = ROPE && pos < t0 + AS_KC;
+    const int nu = GM + (has_new ? 1 : 0);
+    QkHead<HD> hu[3];
+    float vv[E];
     {
         constexpr int NK = AS_KC * (HD / 4) / 256, NQ = (GM * (HD / 4) + 255) / 256;
         float4 kx[NK], qx[NQ];
@@ -2067,24 +2114,64 @@ __global__ __launch_bounds__(256) void k_attn_sc1(const float* __restrict__ q, c
             const int t = t0 + kr < max_seq ? t0 + kr : max_seq - 1;
             kx[k] = *(const float4*)(kc + ((size_t)kvh * max_seq + t) * HD + 4 * c);
         }
+        if (ROPE) {
 #pragma unroll
-        for (int k = 0; k < NQ; k++) {
-            const int e = tid + 256 * k, r = e / (HD / 4), c = e % (HD / 4);
-            const int hr = r < G ? r : G - 1;  // rows past the group repeat the last head (never written)
-            if (e < GM * (HD / 4)) qx[k] = *(const float4*)(q + ((size_t)kvh * G + hr) * HD + 4 * c);
+            for (int k = 0; k < 3; k++) {
+                const int u = w + 4 * k;
+                if (u < GM) {
+                    const int hr = u < G ? u : G - 1;  // rows past the group repeat the last head (never written)
+                    qk_head_load<HD>(q + ((size_t)kvh * G + hr) * HD, ra.qn, ra.cos_tab, ra.sin_tab, pos, lane, hu[k]);
+                } else if (u < nu) {
+                    qk_head_load<HD>(ra.k + (size_t)kvh * HD, ra.kn, ra.cos_tab, ra.sin_tab, pos, lane, hu[k]);
+#pragma unroll
+                    for (int e = 0; e < E; e++) vv[e] = ra.v[(size_t)kvh * HD + lane + 64 * e];
+                }
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < NQ; k++) {
+                const int e = tid + 256 * k, r = e / (HD / 4), c = e % (HD / 4);
+                const int hr = r < G ? r : G - 1;  // rows past the group repeat the last head (never written)
+                if (e < GM * (HD / 4)) qx[k] = *(const float4*)(q + ((size_t)kvh * G + hr) * HD + 4 * c);
+            }
         }
 #pragma unroll
         for (int k = 0; k < NK; k++) {
             const int e = tid + 256 * k, kr = e / (HD / 4), c = e % (HD / 4);
             *(float4*)&ks[kr * LD + 4 * c] = kx[k];
         }
+        if (!ROPE) {
 #pragma unroll
-        for (int k = 0; k < NQ; k++) {
-            const int e = tid + 256 * k;
-            if (e < GM * (HD / 4)) *(float4*)&qs[4 * e] = qx[k];
+            for (int k = 0; k < NQ; k++) {
+                const int e = tid + 256 * k;
+                if (e < GM * (HD / 4)) *(float4*)&qs[4 * e] = qx[k];
+            }
         }
     }
     __syncthreads();
+    if (ROPE) {
+        // after the barrier: the new K row replaces the chunk's (stale) copy
+#pragma unroll
+        for (int k = 0; k < 3; k++) {
+            const int u = w + 4 * k;
+            if (u >= nu) continue;  // wave-uniform
+            float o[E];
+            qk_head_rope<HD>(hu[k], (u < GM ? ra.qn : ra.kn) != nullptr, ra.eps, lane, o);
+            if (u < GM) {
+#pragma unroll
+                for (int e = 0; e < E; e++) qs[u * HD + lane + 64 * e] = o[e];
+            } else {
+                const size_t off = ((size_t)kvh * max_seq + pos) * HD;
+#pragma unroll
+                for (int e = 0; e < E; e++) {
+                    ks[(pos - t0) * LD + lane + 64 * e] = o[e];
+                    ra.kc[off + lane + 64 * e] = o[e];
+                    ra.vc[off + lane + 64 * e] = vv[e];
+                }
+            }
+        }
+        __syncthreads();
+    }
     const int kq = tid >> 2, jp = tid & 3;
     float acc[GM][2];
 #pragma unroll
@@ -4717,10 +4804,15 @@ void dpuf_hip_qk_rope_kv(void* s, int32_t M, float* q, float* k, const float* v,
 // (or max_seq when the launch is captured for replay at any position).
 // Returns -1 without launching when the shape does not fit (group > 32, head
 // dim not 64/128/256, or a tile's probabilities not fitting in LDS).
-int32_t dpuf_hip_attn_split(void* s, int32_t M, int32_t lmax, const float* q, const float* kc, const float* vc,
-                            float* out, float* scores, const int32_t* pos0p, int32_t n_q, int32_t n_kv, int32_t hd,
-                            int32_t max_seq, float scale, const uint8_t* o_sign, DpufPrep op, int32_t* prepped) {
+// rope (one-token steps only): the QK-norm, RoPE and KV store ride in the
+// scores launch; -1 with nothing launched when the one-token wide path does
+// not apply.
+static int32_t attn_split(void* s, int32_t M, int32_t lmax, const float* q, const float* kc, const float* vc,
+                          float* out, float* scores, const int32_t* pos0p, int32_t n_q, int32_t n_kv, int32_t hd,
+                          int32_t max_seq, float scale, const uint8_t* o_sign, DpufPrep op, int32_t* prepped,
+                          const ScRope* rope) {
     if (prepped) *prepped = 0;
+    if (rope && M != 1) return -1;
     if (n_kv <= 0 || n_q % n_kv || n_q / n_kv > 32 || (hd != 64 && hd != 128 && hd != 256)) return -1;
     if (lmax > max_seq) lmax = max_seq;
     const int G = n_q / n_kv;
@@ -4784,9 +4876,16 @@ int32_t dpuf_hip_attn_split(void* s, int32_t M, int32_t lmax, const float* q, co
 #define SMX_LAUNCH(SG)                                                                                            \
     if (seg == SG) hipLaunchKernelGGL(k_attn_smx<SG>, dim3(n_q), dim3(256), 0, ST(s), scores, pos0p, max_seq);
 #define SC1_LAUNCH(HDV, GMV)                                                                                      \
-    hipLaunchKernelGGL((k_attn_sc1<HDV, GMV>), dim3(n_kv, (lmax + AS_KC - 1) / AS_KC), dim3(256),                   \
-                       (size_t)(AS_KC * (HDV + 8) + GMV * HDV) * 4, ST(s), q, kc, pos0p, n_q, n_kv, max_seq, scale,  \
-                       scores);
+    {                                                                                                             \
+        const dim3 g1s(n_kv, (lmax + AS_KC - 1) / AS_KC);                                                         \
+        const size_t l1s = (size_t)(AS_KC * (HDV + 8) + GMV * HDV) * 4;                                           \
+        if (rope)                                                                                                 \
+            hipLaunchKernelGGL((k_attn_sc1<HDV, GMV, true>), g1s, dim3(256), l1s, ST(s), q, kc, pos0p, n_q, n_kv, \
+                               max_seq, scale, scores, *rope);                                                    \
+        else                                                                                                      \
+            hipLaunchKernelGGL((k_attn_sc1<HDV, GMV, false>), g1s, dim3(256), l1s, ST(s), q, kc, pos0p, n_q,      \
+                               n_kv, max_seq, scale, scores, ScRope{});                                           \
+    }
 #define PVW_LAUNCH(HDV)                                                                                           \
     if (gm == 2) SC1_LAUNCH(HDV, 2) else if (gm == 4) SC1_LAUNCH(HDV, 4) else SC1_LAUNCH(HDV, 8)                  \
     SMX_LAUNCH(16) SMX_LAUNCH(32) SMX_LAUNCH(48) SMX_LAUNCH(64) SMX_LAUNCH(80) SMX_LAUNCH(96) SMX_LAUNCH(128)  \
@@ -4813,6 +4912,7 @@ int32_t dpuf_hip_attn_split(void* s, int32_t M, int32_t lmax, const float* q, co
             return 0;
         }
     }
+    if (rope) return -1;
     int dc = 1;
     while (dc < hd / 4 && R * (hd / dc) > 256) dc *= 2;
     const int tiles = n_kv * ((M + qt2 - 1) / qt2);
@@ -4855,6 +4955,23 @@ int32_t dpuf_hip_attn_split(void* s, int32_t M, int32_t lmax, const float* q, co
     }
     LAUNCHED("k_attn_split");
     return 0;
+}
+
+int32_t dpuf_hip_attn_split(void* s, int32_t M, int32_t lmax, const float* q, const float* kc, const float* vc,
+                            float* out, float* scores, const int32_t* pos0p, int32_t n_q, int32_t n_kv, int32_t hd,
+                            int32_t max_seq, float scale, const uint8_t* o_sign, DpufPrep op, int32_t* prepped) {
+    return attn_split(s, M, lmax, q, kc, vc, out, scores, pos0p, n_q, n_kv, hd, max_seq, scale, o_sign, op, prepped,
+                      NULL);
+}
+
+int32_t dpuf_hip_attn_decode_rope(void* s, int32_t lmax, float* q, const float* k, const float* v, const float* qn,
+                                  const float* kn, float eps, const float* cos_tab, const float* sin_tab, float* kc,
+                                  float* vc, float* out, float* scores, const int32_t* pos0p, int32_t n_q,
+                                  int32_t n_kv, int32_t hd, int32_t max_seq, float scale) {
+    const ScRope r = {k, v, qn, kn, eps, cos_tab, sin_tab, kc, vc};
+    DpufPrep none;
+    memset(&none, 0, sizeof none);
+    return attn_split(s, 1, lmax, q, kc, vc, out, scores, pos0p, n_q, n_kv, hd, max_seq, scale, NULL, none, NULL, &r);
 }
 
 void dpuf_hip_attn(void* s, int32_t M, const float* q, const float* kc, const float* vc, float* out, float* scores,
