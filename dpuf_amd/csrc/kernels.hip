@@ -391,11 +391,6 @@ __global__ __launch_bounds__(256) void k_prep(int K, const float* __restrict__ x
                      p.h ? p.h + (size_t)m * K : nullptr);
 }
 
-// SwiGLU with dead zone (reference swiglu_range_avx2, 8-wide path,
-// dpuf_engine.c:976-989) fused with the prep of the down projection's input.
-// A 64-block per 16-lane row, 4 columns per lane (row_prep64): a quarter of
-// the per-lane work of a quad per block, which is what bounds this
-// latency-bound step.  grid: (ceil(I / 256), M), one wave per workgroup.
 // Lane t of one row: columns 4t .. 4t + 3 of the 64-block t / 16 (COH: see
 // row_prep64).
 template <bool COH = false>
@@ -431,6 +426,11 @@ DEV void prep_lane(const float* __restrict__ x, const uint8_t* __restrict__ sign
     row_prep64<COH>(v, r, blk, q, s, m, nullptr);
 }
 
+// SwiGLU with dead zone (reference swiglu_range_avx2, 8-wide path,
+// dpuf_engine.c:976-989) fused with the prep of the down projection's input.
+// A 64-block per 16-lane row, 4 columns per lane (row_prep64): a quarter of
+// the per-lane work of a quad per block, which is what bounds this
+// latency-bound step.  grid: (ceil(I / 256), M), one wave per workgroup.
 __global__ __launch_bounds__(64) void k_swiglu_prep(int I, const float* __restrict__ gate, const float* __restrict__ up,
                                                     float dz, const uint8_t* __restrict__ sign, DpufPrep p) {
     const int m = blockIdx.y, t = blockIdx.x * 64 + threadIdx.x;
