@@ -2778,7 +2778,7 @@ __global__ __launch_bounds__(192) void k_attn_pvw(const float* __restrict__ P, c
 // the reference's eight sum lanes, eng_hsum256 and the tail in order;
 // 1 / (sum + 1e-12)), and are normalised in place once (p = e * inv, the
 // reference's multiply).  Thread (ri, di) then keeps the 4 x 4 outputs of
-// rows 4ri .. 4ri + 3 and dims 4di .. 4di + 3 in registers and runs each
+// rows ri + 8k (k < 4) and dims 4di .. 4di + 3 in registers and runs each
 // output's chain a = fma(p[t], v[t], a) over the keys in order: per 4 keys
 // one float4 of p per row from LDS and one float4 of V per key, 64 FMAs.  V
 // comes from L2 straight into registers, PVT_KV keys a batch with the next
@@ -2795,10 +2795,10 @@ __global__ __launch_bounds__(192) void k_attn_pvw(const float* __restrict__ P, c
 // p of keys t .. t + 3 for the thread's RT rows (t clamped into the row so a
 // read ahead of the last keys stays inside it; such values are not used)
 template <int RT>
-DEV void pvt_readp(const float* pr, int ldp, int t, float4 (&p4)[RT]) {
+DEV void pvt_readp(const float* pr, int ldp, int rs, int t, float4 (&p4)[RT]) {
     t = t < ldp - 4 ? t : ldp - 4;
 #pragma unroll
-    for (int k = 0; k < RT; k++) p4[k] = *(const float4*)(pr + (size_t)k * ldp + t);
+    for (int k = 0; k < RT; k++) p4[k] = *(const float4*)(pr + (size_t)k * rs + t);
 }
 
 // 4 keys of the tile: rows' p (already read), V from registers
@@ -2823,6 +2823,7 @@ __global__ __launch_bounds__(PVT_R * HD / (4 * RT)) void k_attn_pvt(const float*
                                                          int max_seq, int qt, int ldp, float* __restrict__ out,
                                                          const uint8_t* __restrict__ o_sign, DpufPrep op) {
     constexpr int R = PVT_R, NT = R * HD / (4 * RT), KV = PVT_KV;  // (R / RT) row groups x (HD / 4) dim groups
+    constexpr int NRG = R / RT;                                     // row groups
     static_assert(R % (8 * RT) == 0 || R == 8 * RT, "whole row bands of 8 row groups");
     constexpr int TPR = NT / R;  // threads per row in the softmax phases
     extern __shared__ __align__(16) float P[];  // [R][ldp]
@@ -2933,8 +2934,12 @@ __global__ __launch_bounds__(PVT_R * HD / (4 * RT)) void k_attn_pvt(const float*
         for (int i = 0; i < 4; i++) acc[k][i] = 0.0f;
     int Lr[RT];
 #pragma unroll
-    for (int k = 0; k < RT; k++) Lr[k] = row_len(RT * ri + k);
-    const float* pr = P + (size_t)(RT * ri) * ldp;
+    for (int k = 0; k < RT; k++) Lr[k] = row_len(ri + NRG * k);
+    // the thread's rows ri + 8k: the 8 row groups of a wave read rows ldp
+    // apart (ldp = 4 mod 64 words), on distinct banks; 4 consecutive rows per
+    // thread put them only 4 ldp apart, two to four groups per bank
+    const int rs = NRG * ldp;
+    const float* pr = P + (size_t)ri * ldp;
     const float* vg = vc + (size_t)kvh * max_seq * HD + 4 * di;
     // keys below Lmin, in whole batches, go to every row unconditionally
     const int nfull = Lmin / KV * KV;
@@ -2946,7 +2951,7 @@ __global__ __launch_bounds__(PVT_R * HD / (4 * RT)) void k_attn_pvt(const float*
     // the batch before it, and each 4 keys' p reads ahead of the FMAs of the 4
     // keys before them, so their latencies are covered)
     float4 pa[RT], pb[RT];
-    pvt_readp<RT>(pr, ldp, 0, pa);
+    pvt_readp<RT>(pr, ldp, rs, 0, pa);
     for (; t0 + 2 * KV <= nfull; t0 += 2 * KV) {
 #pragma unroll
         for (int j = 0; j < KV; j++) {
@@ -2957,11 +2962,11 @@ __global__ __launch_bounds__(PVT_R * HD / (4 * RT)) void k_attn_pvt(const float*
 #pragma unroll
         for (int j = 0; j < 2 * KV; j += 8) {
             const float4* vv = j < KV ? va + j : vb + (j - KV);
-            pvt_readp<RT>(pr, ldp, t0 + j + 4, pb);
+            pvt_readp<RT>(pr, ldp, rs, t0 + j + 4, pb);
             __builtin_amdgcn_sched_barrier(0);
             pvt_keys4<RT>(acc, pa, vv);
             __builtin_amdgcn_sched_barrier(0);
-            pvt_readp<RT>(pr, ldp, t0 + j + 8, pa);
+            pvt_readp<RT>(pr, ldp, rs, t0 + j + 8, pa);
             __builtin_amdgcn_sched_barrier(0);
             pvt_keys4<RT>(acc, pb, vv + 4);
             __builtin_amdgcn_sched_barrier(0);
@@ -2978,7 +2983,7 @@ __global__ __launch_bounds__(PVT_R * HD / (4 * RT)) void k_attn_pvt(const float*
     if (t0 + KV <= nfull) {
 #pragma unroll
         for (int j = 0; j < KV; j += 4) {
-            pvt_readp<RT>(pr, ldp, t0 + j, pa);
+            pvt_readp<RT>(pr, ldp, rs, t0 + j, pa);
             pvt_keys4<RT>(acc, pa, va + j);
         }
         t0 += KV;
@@ -2989,7 +2994,7 @@ __global__ __launch_bounds__(PVT_R * HD / (4 * RT)) void k_attn_pvt(const float*
 #pragma unroll
         for (int k = 0; k < RT; k++) {
             if (t < Lr[k]) {
-                const float pk = pr[(size_t)k * ldp + t];
+                const float pk = pr[(size_t)k * rs + t];
                 acc[k][0] = fmaf(pk, v.x, acc[k][0]);
                 acc[k][1] = fmaf(pk, v.y, acc[k][1]);
                 acc[k][2] = fmaf(pk, v.z, acc[k][2]);
@@ -3000,7 +3005,7 @@ __global__ __launch_bounds__(PVT_R * HD / (4 * RT)) void k_attn_pvt(const float*
     if (!op.q) {
 #pragma unroll
         for (int k = 0; k < RT; k++) {
-            const int r = RT * ri + k;
+            const int r = ri + NRG * k;
             if (Lr[k] > 0)
                 *(float4*)(out + ((size_t)(m0 + r / G) * n_q + kvh * G + r % G) * HD + 4 * di) =
                     make_float4(acc[k][0], acc[k][1], acc[k][2], acc[k][3]);
@@ -3015,7 +3020,7 @@ __global__ __launch_bounds__(PVT_R * HD / (4 * RT)) void k_attn_pvt(const float*
     __syncthreads();
 #pragma unroll
     for (int k = 0; k < RT; k++)
-        *(float4*)(P + (size_t)(RT * ri + k) * LDT + 4 * di) = make_float4(acc[k][0], acc[k][1], acc[k][2], acc[k][3]);
+        *(float4*)(P + (size_t)(ri + NRG * k) * LDT + 4 * di) = make_float4(acc[k][0], acc[k][1], acc[k][2], acc[k][3]);
     __syncthreads();
     const int qd = n_q * HD, nb = qd >> 5;
     for (int qq = tid; qq < R * HD / 16; qq += NT) {  // quads of a row never straddle the loop's steps
