@@ -2518,44 +2518,48 @@ __global__ __launch_bounds__(AP_NT) void k_attn_pv(const float* __restrict__ S, 
 // ---------------------------------------------------------------------------
 
 // Softmax of one score row of a one-token decode step, in place: row r =
-// blockIdx.x of S (stride max_seq), length pos + 1 <= 64 SEG, 256 threads.
+// blockIdx.x of S (stride max_seq), length pos + 1 <= 64 SEG, SMX_NT threads.
 // The row is read once, into registers: exps of the 8-aligned part go to LDS as [8][8 SEG] (lane j's
 // elements t = j mod 8 in order, zero past the row: adding +0.0 leaves the
 // non-negative sums exact), the tail's (< 8) to a small array.  Wave 0 runs
 // the eight sum chains register-fed, chain j on lanes 8j .. 8j+7 in segments
 // of SEG (as k_resnorm_prep), then the eng_hsum256 tree and the tail in
 // order; the row is normalised from LDS and written once.
+#define SMX_NT 1024  // threads per softmax row (SEG a multiple of 16)
+
 template <int SEG>
-__global__ __launch_bounds__(256) void k_attn_smx(float* __restrict__ S, const int32_t* __restrict__ pos0p,
+__global__ __launch_bounds__(SMX_NT) void k_attn_smx(float* __restrict__ S, const int32_t* __restrict__ pos0p,
                                                   int max_seq) {
     constexpr int LDT = 8 * SEG + 4;  // row stride of the transposed copy
     __shared__ __align__(16) float tr[8][LDT];
     __shared__ float tail[8];
-    __shared__ float red[4];
+    __shared__ float red[SMX_NT / 64];
     __shared__ float part[8];
     float* row = S + (size_t)blockIdx.x * max_seq;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int L = *pos0p + 1, n8 = L & ~7;
     // zero the positions past the row that the chains read
-    for (int i = tid; i < 8 * LDT; i += 256) (&tr[0][0])[i] = 0.0f;
+    for (int i = tid; i < 8 * LDT; i += SMX_NT) (&tr[0][0])[i] = 0.0f;
     // the row in registers, all loads in flight at once (keys t = tid +
-    // 256 k, k < SEG / 4, cover the 64 SEG keys of the largest row)
-    constexpr int KR = SEG / 4;
+    // SMX_NT k, k < 64 SEG / SMX_NT, cover the 64 SEG keys of the largest row)
+    constexpr int KR = 64 * SEG / SMX_NT;
     float xr[KR];
 #pragma unroll
-    for (int k = 0; k < KR; k++) xr[k] = row[min(tid + 256 * k, L - 1)];
+    for (int k = 0; k < KR; k++) xr[k] = row[min(tid + SMX_NT * k, L - 1)];
     float mx = -1e30f;
 #pragma unroll
     for (int k = 0; k < KR; k++)
-        if (tid + 256 * k < L) mx = fmaxf(mx, xr[k]);
+        if (tid + SMX_NT * k < L) mx = fmaxf(mx, xr[k]);
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
     if (lane == 0) red[wv] = mx;
     __syncthreads();
-    const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    float M = red[0];
+#pragma unroll
+    for (int i = 1; i < SMX_NT / 64; i++) M = fmaxf(M, red[i]);
 #pragma unroll
     for (int k = 0; k < KR; k++) {
-        const int t = tid + 256 * k;
+        const int t = tid + SMX_NT * k;
         if (t < n8) tr[t & 7][t >> 3] = exp_poly(xr[k] - M);
         else if (t < L) tail[t - n8] = expf_libc(xr[k] - M);
     }
@@ -2594,7 +2598,7 @@ __global__ __launch_bounds__(256) void k_attn_smx(float* __restrict__ S, const i
     const float inv = red[0];
 #pragma unroll
     for (int k = 0; k < KR; k++) {
-        const int t = tid + 256 * k;
+        const int t = tid + SMX_NT * k;
         if (t < L) row[t] = (t < n8 ? tr[t & 7][t >> 3] : tail[t - n8]) * inv;
     }
 }
@@ -4879,7 +4883,7 @@ static int32_t attn_split(void* s, int32_t M, int32_t lmax, const float* q, cons
             const int gm = G <= 2 ? 2 : G <= 4 ? 4 : 8;
             const dim3 gp(n_kv, hd / 4);
 #define SMX_LAUNCH(SG)                                                                                            \
-    if (seg == SG) hipLaunchKernelGGL(k_attn_smx<SG>, dim3(n_q), dim3(256), 0, ST(s), scores, pos0p, max_seq);
+    if (seg == SG) hipLaunchKernelGGL(k_attn_smx<SG>, dim3(n_q), dim3(SMX_NT), 0, ST(s), scores, pos0p, max_seq);
 #define SC1_LAUNCH(HDV, GMV)                                                                                      \
     {                                                                                                             \
         const dim3 g1s(n_kv, (lmax + AS_KC - 1) / AS_KC);                                                         \
@@ -5006,7 +5010,7 @@ void dpuf_hip_attn_q8(void* s, int32_t M, int32_t lmax, const float* q, DpufKvQ8
             const int gm = G <= 2 ? 2 : G <= 4 ? 4 : 8;
             const dim3 gp(n_kv, hd / 4);
 #define SMXQ(SG) \
-    if (seg == SG) hipLaunchKernelGGL(k_attn_smx<SG>, dim3(n_q), dim3(256), 0, ST(s), scores, pos0, max_seq);
+    if (seg == SG) hipLaunchKernelGGL(k_attn_smx<SG>, dim3(n_q), dim3(SMX_NT), 0, ST(s), scores, pos0, max_seq);
             SMXQ(16) SMXQ(32) SMXQ(48) SMXQ(64) SMXQ(80) SMXQ(96) SMXQ(128)
 #undef SMXQ
 #define PVWQ(HDV)                                                                                                  \
