@@ -213,6 +213,7 @@ def load_engine():
                                                   C.POINTER(C.c_double)])
     _sig(lib, "dpuf_amd_engine_weight_bytes", C.c_uint64, [P])
     _sig(lib, "dpuf_amd_engine_early_exit_count", C.c_int64, [P])
+    _sig(lib, "dpuf_amd_attn_path_count", C.c_int64, [I32])
     _sig(lib, "dpuf_amd_gemv_bench", C.c_double, [P, I32, I32, I32, I32, C.POINTER(C.c_double)])
     _sig(lib, "dpuf_amd_copy_bench", C.c_double, [C.c_size_t, I32])
     _sig(lib, "dpuf_amd_set_gemv_max_workgroups", None, [I32])

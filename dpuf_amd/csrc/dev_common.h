@@ -415,6 +415,27 @@ DEV int row_block_dot(uint4 w, int4 xa, int4 xb) {
 }
 
 
+
+// The same for a mode 14 row block: bits 4..5 of each value come from the
+// row's two words of high bits (word c >> 1, bits (c & 1) * 4 + {0,1} of byte
+// k for column 8c+k, + {2,3} for 8c+4+k).  u <= 63, so the sdot4 products are
+// exact, as the reference's maddubs sums (dpuf_avx2.c:2824-2846).
+DEV int row_block_dot6(uint4 w, uint2 hw, int4 xa, int4 xb) {
+    const uint32_t m = 0x0F0F0F0Fu, m2 = 0x03030303u;
+    const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+    const int xw[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+    int d = 0;
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const uint32_t h = ((c >> 1) ? hw.y : hw.x) >> ((c & 1) * 4);
+        const uint32_t lo = (wd[c] & m) | ((h & m2) << 4);
+        const uint32_t hi = ((wd[c] >> 4) & m) | (((h >> 2) & m2) << 4);
+        d = __builtin_amdgcn_sdot4((int)lo, xw[2 * c], d, false);
+        d = __builtin_amdgcn_sdot4((int)hi, xw[2 * c + 1], d, false);
+    }
+    return d;
+}
+
 // Lane i + 8 of a 16-lane row for lane i and the reverse (DPP row_ror:8).
 DEV int dpp_ror8(int v) { return __builtin_amdgcn_update_dpp(0, v, 0x128, 0xF, 0xF, false); }
 
@@ -424,7 +445,51 @@ DEV uint4 nt_load16(const uint8_t* p) {
 }
 
 
-// Records the first HIP error of the current API call (kernels.hip).
+
+// LDS address space pointer of the direct-to-LDS loads.
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// Vector types of the MFMA kernels.
+typedef _Float16 gm_h8 __attribute__((ext_vector_type(8)));
+typedef float gm_f4 __attribute__((ext_vector_type(4)));
+typedef uint32_t gm_u4 __attribute__((ext_vector_type(4)));
+
+// Lane t of one row: columns 4t .. 4t + 3 of the 64-block t / 16 (COH: see
+// row_prep64).
+template <bool COH = false>
+DEV void swiglu_prep_lane(int I, const float* __restrict__ gate, const float* __restrict__ up, float dz,
+                          const uint8_t* __restrict__ sign, int8_t* q, float* s, int32_t* m, uint16_t* h, int t) {
+    const int blk = t >> 4, r = t & 15;
+    const float4 g4 = *(const float4*)(gate + 4 * t);
+    const float4 u4 = *(const float4*)(up + 4 * t);
+    const uint32_t sb = sign ? (sign[8 * blk + (r >> 1)] >> (4 * (r & 1))) & 0xFu : 0u;
+    const float g[4] = {g4.x, g4.y, g4.z, g4.w}, u[4] = {u4.x, u4.y, u4.z, u4.w};
+    float v[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const float ng = fmaxf(-40.0f, fminf(0.0f - g[k], 40.0f));
+        const float silu = g[k] / (1.0f + exp_poly(ng));
+        float rr = silu * u[k];
+        if (dz > 0.0f && !(fabsf(rr) >= dz)) rr = 0.0f;
+        v[k] = ((sb >> k) & 1u) ? -rr : rr;
+    }
+    row_prep64<COH>(v, r, blk, q, s, m, h);
+}
+
+// The plain prep of lane t of one row (columns 4t .. 4t + 3): sign, then
+// row_prep64 (COH: see row_prep64).
+template <bool COH = false>
+DEV void prep_lane(const float* __restrict__ x, const uint8_t* __restrict__ sign, int8_t* q, float* s, int32_t* m, int t) {
+    const int blk = t >> 4, r = t & 15;
+    const float4 x4 = *(const float4*)(x + 4 * t);
+    const uint32_t sb = sign ? (sign[8 * blk + (r >> 1)] >> (4 * (r & 1))) & 0xFu : 0u;
+    float v[4] = {x4.x, x4.y, x4.z, x4.w};
+#pragma unroll
+    for (int k = 0; k < 4; k++) v[k] = ((sb >> k) & 1u) ? -v[k] : v[k];
+    row_prep64<COH>(v, r, blk, q, s, m, nullptr);
+}
+
+// Records the first HIP error of the current API call (rt.hip).
 void dpuf_note(hipError_t e, const char* what);
 
 #endif

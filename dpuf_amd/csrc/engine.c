@@ -100,19 +100,22 @@ typedef struct {
     double t_ms[N_KINDS];
     int64_t t_cnt[N_KINDS];
     double t_bytes[N_KINDS];
-    /* one-token steps captured as HIP graphs that replay at any position,
-     * one per key (only_last, keep tiles, early tiles, slot, margin, split
-     * attention, argmax): a host that alternates slots or entry points keeps
-     * its graphs; the least recently used one makes room */
+    /* one-token steps captured as HIP graphs, one per key (only_last, keep
+     * tiles, early tiles, slot, margin, attention key bucket, argmax); a
+     * graph replays at every position of its bucket (attn_bucket): a host
+     * that alternates slots or entry points keeps its graphs; the least
+     * recently used one makes room */
     void* graphs[N_GRAPHS];
     int32_t graph_keys[N_GRAPHS][7];
     uint32_t graph_used[N_GRAPHS];
     uint32_t graph_tick;
     int32_t no_graphs; /* dpuf_amd_engine_set_graphs(0) */
     /* the forward being enqueued: host copy of pos0, and whether it is being
-     * captured into a graph that replays at any position */
+     * captured into a graph that replays at every position of the key bucket
+     * cap_lmax (the largest key count the captured attention launches serve) */
     int32_t host_pos0;
     int32_t capturing;
+    int32_t cap_lmax;
 } Engine;
 
 #define IO_POS DPUF_AMD_MAX_BATCH
@@ -121,6 +124,20 @@ typedef struct {
 /* Decode attention switches from the fused short-context kernel to the split
  * (scores + softmax/P.V) kernels once kv_len exceeds this. */
 #define ATT_SPLIT_MIN DPUF_HIP_DEC_MAX_KEYS
+
+/* Key bucket of a captured one-token step that attends over `keys` keys: the
+ * fused kernel's range as one bucket, then 256, 512, 1024 and multiples of
+ * 1024 (at most max_seq).  The captured attention launches are sized for the
+ * bucket's top, so they take the path, and about the launch shapes, of an
+ * eager step at that many keys, whatever max_seq is; a longer context
+ * captures the next bucket (at most one capture per 1024 decoded tokens). */
+static int32_t attn_bucket(const Engine* e, int32_t keys) {
+    int32_t b;
+    if (keys <= ATT_SPLIT_MIN) b = ATT_SPLIT_MIN;
+    else if (keys <= 1024) for (b = 256; b < keys; b <<= 1) {}
+    else b = (keys + 1023) & ~1023;
+    return b < e->max_seq ? b : e->max_seq;
+}
 
 /* ------------------------------------------------------------------------- */
 
@@ -881,7 +898,7 @@ static void enqueue_layers(Engine* e, int32_t M, int32_t keep_tiles) {
                 const DpufKvQ8 c8 = slot_q8(e, e->active, l);
                 dpuf_hip_qk_rope_kv(s, M, e->q, e->k, e->v, e->d_norm[4 * l + 1], e->d_norm[4 * l + 2], eps,
                                     e->d_cos, e->d_sin, NULL, NULL, e->d_pos0, e->nq, e->nkv, e->hd, e->max_seq, &c8);
-                dpuf_hip_attn_q8(s, M, e->capturing ? e->max_seq : e->host_pos0 + M, e->q, c8, e->ao, e->scores,
+                dpuf_hip_attn_q8(s, M, e->capturing ? e->cap_lmax : e->host_pos0 + M, e->q, c8, e->ao, e->scores,
                                  e->d_pos0, e->nq, e->nkv, e->hd, e->max_seq, scale);
                 if (M > 1) dpuf_hip_prep(s, M, e->qd, e->ao, W[W_O].sign, e->prep[0]);
                 o_prep = M == 1;
@@ -897,7 +914,7 @@ static void enqueue_layers(Engine* e, int32_t M, int32_t keep_tiles) {
                                           scale, e->ao, W[W_O].sign, e->prep[0], NULL, NULL, 0,
                                           attn_warm(e, &lj, ln)) == 0;
             if (!fused) {
-                const int32_t lmax = e->capturing ? e->max_seq : e->host_pos0 + M;
+                const int32_t lmax = e->capturing ? e->cap_lmax : e->host_pos0 + M;
                 /* the O-input prep rides with the last attention kernel when
                  * it can; otherwise it is a launch of its own */
                 int32_t prepped = 0;
@@ -1077,7 +1094,8 @@ static int32_t forward_common(Engine* e, int32_t n_tokens, const int32_t* token_
     e->host_pos0 = pos0;
     e->capturing = 0;
     if (graphable) {
-        int32_t key[7] = {only_last, keep, early, e->active, 0, pos0 + 1 > ATT_SPLIT_MIN, want_argmax};
+        const int32_t bucket = attn_bucket(e, pos0 + 1);
+        int32_t key[7] = {only_last, keep, early, e->active, 0, bucket, want_argmax};
         memcpy(&key[4], &margin, 4);
         int gi = -1;
         for (int i = 0; i < N_GRAPHS && gi < 0; i++)
@@ -1093,6 +1111,7 @@ static int32_t forward_common(Engine* e, int32_t n_tokens, const int32_t* token_
             e->graphs[gi] = NULL;
             if (dpuf_hip_capture_begin(e->stream) == 0) {
                 e->capturing = 1;
+                e->cap_lmax = bucket;
                 enqueue_forward(e, 1, 0, only_last, keep, early, margin, want_argmax, lm_host);
                 e->capturing = 0;
                 e->graphs[gi] = dpuf_hip_capture_end(e->stream);
@@ -1330,6 +1349,8 @@ DPUF_EXPORT int64_t dpuf_amd_engine_early_exit_count(void* handle) {
     Engine* e = (Engine*)handle;
     return e ? e->early_exits : 0;
 }
+
+DPUF_EXPORT int64_t dpuf_amd_attn_path_count(int32_t which) { return dpuf_hip_attn_path_count(which); }
 
 /* Jobs of one GEMV launch of kind `which` in layer l (see dpuf_amd_gemv_bench). */
 static int32_t bench_jobs(Engine* e, int32_t which, int32_t l, DpufGemvJob* js, double* bytes, int32_t M) {

@@ -1,6 +1,7 @@
 /*
  * hip_layer.h -- the thin C ABI between the C host engine (engine.c) and the
- * gfx950 HIP code (kernels.hip).  Plain pointers and sizes only; every
+ * gfx950 HIP code (rt.hip, gemv.hip, gemm.hip, attn.hip, attn_wide.hip,
+ * attn_dec.hip).  Plain pointers and sizes only; every
  * function that launches work takes the engine's stream as an opaque handle.
  */
 #ifndef DPUF_HIP_LAYER_H
@@ -211,6 +212,10 @@ int32_t dpuf_hip_attn_dec(void* s, int32_t M, const float* q, const float* k, co
                           float* vc, const int32_t* pos0, int32_t n_q, int32_t n_kv, int32_t hd, int32_t max_seq,
                           float scale, float* ao, const uint8_t* o_sign, DpufPrep op, float* const* kcs,
                           float* const* vcs, size_t l_off, DpufWarm warm);
+/* Attention launches enqueued per path (dpuf_amd_attn_path_count); -1 for
+ * another `which`. */
+#define DPUF_HIP_ATTN_PATHS 6
+int64_t dpuf_hip_attn_path_count(int32_t which);
 void dpuf_hip_zero_rows(void* s, int32_t M, float* out, int32_t ld, int32_t r0, int32_t r1);
 /* CRC32 of n tile bodies (base + off[t], len[t] bytes) against want[t]: ok[t] = 1 when equal. */
 void dpuf_hip_crc_tiles(void* s, const uint8_t* base, const uint64_t* off, const uint32_t* len,

@@ -68,6 +68,16 @@ DPUF_EXPORT uint64_t dpuf_amd_engine_weight_bytes(void* handle);
 /* Number of forward calls in which the LM-head early exit fired. */
 DPUF_EXPORT int64_t dpuf_amd_engine_early_exit_count(void* handle);
 
+/* Attention launches enqueued so far in this process, by path (which: 0 the
+ * prefill split kernels with the register-tiled softmax + P.V, 1 the
+ * one-token long-context kernels (scores, softmax once per row, wide P.V),
+ * 2 the split scores + LDS softmax / P.V kernels, 3 the one-pair-per-workgroup
+ * fallback, 4 the fused short-context decode kernel, 5 the int8-cache
+ * kernels); -1 for another `which`.  Enqueued, not executed: a replayed graph
+ * counts at its capture only.  For tests that check which path a shape
+ * takes. */
+DPUF_EXPORT int64_t dpuf_amd_attn_path_count(int32_t which);
+
 /* Times `iters` back-to-back launches of one GEMV kind over resident weights
  * (which: 0 q, 1 k, 2 v, 3 o, 4 gate, 5 up, 6 down, 7 LM head, 8 gate+up as
  * one launch, 9 q+k+v as one launch), cycling through layers

@@ -52,7 +52,12 @@ def test_reference_cli_links_and_loads(tmp_path):
     # everything before engine creation succeeded: no header, metadata or tile error
     for bad in ("Invalid DPUF magic", "CRC32 mismatch", "lacks embedded", "Cannot open", "missing", "corrupt"):
         assert bad not in out, out
-    assert "dpuf_engine_create failed!" in out, out  # no HIP device in this container
+    if os.path.exists("/dev/kfd"):
+        # a host with a HIP device (checked by its device node, without
+        # initialising HIP here): engine creation may succeed and the CLI go
+        # on past the loader, so only the loader's own checks are asserted
+        return
+    assert "dpuf_engine_create failed!" in out, out  # no HIP device on this host
     assert r.returncode == 1
 
 
