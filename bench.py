@@ -66,6 +66,70 @@ def log(*a):
     print("[bench]", *a, file=sys.stderr, flush=True)
 
 
+def cpu_topology():
+    """The host's CPU model and the physical cores of NUMA node 0 this
+    process may run on (one hardware thread per core), from /proc and /sys."""
+    info = {"model_name": "", "family": "", "model": "", "stepping": "", "numa_nodes": 0,
+            "node0_physical_cores": [], "allowed_cpus": 0, "logical_cpus": os.cpu_count()}
+    try:
+        for ln in open("/proc/cpuinfo"):
+            k, _, v = ln.partition(":")
+            k, v = k.strip(), v.strip()
+            if k == "model name" and not info["model_name"]:
+                info["model_name"] = v
+            elif k == "cpu family" and not info["family"]:
+                info["family"] = v
+            elif k == "model" and not info["model"]:
+                info["model"] = v
+            elif k == "stepping" and not info["stepping"]:
+                info["stepping"] = v
+    except OSError:
+        pass
+
+    def cpulist(path):
+        out = set()
+        try:
+            for part in open(path).read().strip().split(","):
+                if "-" in part:
+                    a, b = part.split("-")
+                    out.update(range(int(a), int(b) + 1))
+                elif part:
+                    out.add(int(part))
+        except (OSError, ValueError):
+            pass
+        return out
+
+    try:
+        info["numa_nodes"] = len([d for d in os.listdir("/sys/devices/system/node") if d.startswith("node")])
+    except OSError:
+        pass
+    allowed = os.sched_getaffinity(0)
+    info["allowed_cpus"] = len(allowed)
+    node0 = cpulist("/sys/devices/system/node/node0/cpulist") or set(allowed)
+    cores, seen = [], set()
+    for c in sorted(allowed & node0):
+        sib = cpulist(f"/sys/devices/system/cpu/cpu{c}/topology/thread_siblings_list") or {c}
+        key = min(sib)
+        if key not in seen:
+            seen.add(key)
+            cores.append(c)
+    info["node0_physical_cores"] = cores
+    return info
+
+
+def pin_openmp(threads):
+    """OpenMP threads of the CPU baseline pinned to physical cores of NUMA node
+    0 (one per core, OMP_PROC_BIND=close over explicit places).  Must run
+    before libgomp initialises, i.e. before any library is loaded."""
+    topo = cpu_topology()
+    cores = topo["node0_physical_cores"][:threads]
+    if cores and "OMP_PLACES" not in os.environ:
+        os.environ["OMP_PLACES"] = ",".join("{%d}" % c for c in cores)
+        os.environ.setdefault("OMP_PROC_BIND", "close")
+    topo["pinned_cores"] = cores if "OMP_PLACES" in os.environ else []
+    return topo
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -86,7 +150,13 @@ def main():
     ap.add_argument("--lm-copies", type=int, default=3,
                     help="distinct LM-head copies rotated per step (>= 1 GB, so the 256 MB cache cannot serve repeats)")
     ap.add_argument("--lm-alpha", type=float, default=8.0, help="planted bias: h += alpha * row(t*)")
-    ap.add_argument("--cpu-seconds", type=float, default=20.0, help="budget of the CPU baseline (0 = skip)")
+    ap.add_argument("--cpu-seconds", type=float, default=30.0,
+                    help="budget of each CPU-baseline part: tg32 decode, the 6-thread sample, the LM-head and "
+                         "long-context id checks (0 = skip the CPU baseline)")
+    ap.add_argument("--cpu-threads", type=int, default=16,
+                    help="OpenMP threads of the CPU baseline (pinned to NUMA node 0 physical cores)")
+    ap.add_argument("--max-seq", type=int, default=32768,
+                    help="context the engine is created for (Qwen3-8B's 32K; slots and graphs sized for it)")
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--graph", type=int, default=1,
                     help="1: one-token steps replay HIP graphs (the default) and the device-argmax entry is timed "
@@ -102,6 +172,9 @@ def main():
     if args.steps < 1 or args.warmup < 0:
         sys.exit("--steps must be >= 1 and --warmup >= 0")
 
+    # pinning of the CPU baseline's OpenMP threads: before libgomp starts
+    topo = pin_openmp(args.cpu_threads) if args.cpu_seconds > 0 else None
+
     from dpuf_amd import abi
     from dpuf_amd import model as M
 
@@ -111,7 +184,7 @@ def main():
 
     shape = M.QWEN3_8B if args.model == "8b" else M.QWEN3_0_6B
     V = shape["vocab_size"]
-    max_seq = max(args.prompt + args.warmup + args.steps + 8, args.pp, 64)
+    max_seq = max(args.prompt + args.warmup + args.steps + 40, args.pp, 64, args.max_seq)
     if args.long_ctx > 0:
         max_seq = max(max_seq, args.long_ctx + args.long_steps + 8)
     t = time.time()
@@ -184,6 +257,11 @@ def main():
     decode(tok, pos, args.steps, ids)
     t1 = time.perf_counter()
     gpu_greedy += ids
+    if len(gpu_greedy) < 33:
+        # greedy ids through tg32 for the CPU baseline's comparison (untimed)
+        extra = []
+        decode(gpu_greedy[-1], pos + args.steps, 33 - len(gpu_greedy), extra)
+        gpu_greedy += extra
     ms_step = (t1 - t0) * 1e3 / args.steps
     tg = 1e3 / ms_step
     log(f"tg{args.steps}: {ms_step:.3f} ms/token, {tg:.1f} tok/s; ids {ids[:8]}...")
@@ -305,6 +383,7 @@ def main():
 
     # --- long context: decode against an injected fp32 KV cache ------------
     long = None
+    long_ids, q8_ids = None, None
     if args.long_ctx > 0:
         L, nkv, hd = shape["num_layers"], shape["num_kv_heads"], shape["head_dim"]
         krng = np.random.default_rng(args.seed + 4096)
@@ -316,13 +395,25 @@ def main():
                 vv = krng.standard_normal((args.long_ctx, hd), dtype=np.float32)
                 assert eng.dpuf_amd_engine_set_kv(h, layer, kh, 0, args.long_ctx, M.ptr(kk), M.ptr(vv)) == 0
         log(f"long context: {args.long_ctx}-token N(0,1) KV cache injected in {time.time() - t:.1f}s")
-        tok = int(rng.integers(0, V))
-        tok = decode(tok, args.long_ctx, 2)  # warm-up (positions long_ctx, +1)
+        long_first = int(rng.integers(0, V))
+        lwarm = []
+        tok = decode(long_first, args.long_ctx, 2, lwarm)  # warm-up (positions long_ctx, +1)
         lids = []
         t0 = time.perf_counter()
         decode(tok, args.long_ctx + 2, args.long_steps, lids)
         t1 = time.perf_counter()
         ms_long = (t1 - t0) * 1e3 / args.long_steps
+        # the same steps enqueued kernel by kernel (no graph), re-decoding 8
+        # positions: graphs are captured per key bucket, so at a 32K max_seq
+        # both take the same attention path
+        ms_eager = None
+        if args.graph:
+            eng.dpuf_amd_engine_set_graphs(h, 0)
+            decode(tok, args.long_ctx + 2, 2)
+            t0 = time.perf_counter()
+            decode(tok, args.long_ctx + 2, 8)
+            ms_eager = (time.perf_counter() - t0) * 1e3 / 8
+            eng.dpuf_amd_engine_set_graphs(h, 1)
         # attention time per token from HIP events (re-decoding the last 8 positions)
         eng.dpuf_amd_engine_set_timing(h, 1)
         decode(tok, args.long_ctx + 2 + args.long_steps - 8, 8)
@@ -332,10 +423,12 @@ def main():
         att_ms = ams.value / 8
         ctx_mid = args.long_ctx + 2 + args.long_steps // 2
         kv_bytes = 2 * L * nkv * ctx_mid * hd * 4  # K and V rows read per decoded token
-        long = dict(ctx=args.long_ctx, steps=args.long_steps, ms_per_token=round(ms_long, 4),
+        long = dict(ctx=args.long_ctx, steps=args.long_steps, max_seq=max_seq, ms_per_token=round(ms_long, 4),
                     tok_s=round(1e3 / ms_long, 3), attention_ms_per_token=round(att_ms, 4),
+                    ms_per_token_eager=round(ms_eager, 4) if ms_eager else None,
                     kv_bytes_per_token=kv_bytes, kv_read_GBs=round(kv_bytes / (att_ms * 1e-3) / 1e9, 1),
                     ids_head=lids[:8])
+        long_ids = (long_first, lwarm + lids[:4])
         log(f"long context {args.long_ctx}: {ms_long:.3f} ms/token ({1e3 / ms_long:.1f} tok/s), attention "
             f"{att_ms:.3f} ms/token -> KV reads {long['kv_read_GBs']} GB/s")
 
@@ -366,7 +459,16 @@ def main():
             return tok
 
         qsteps = min(args.long_steps, 32)
-        tok = qdecode(int(rng.integers(0, V)), args.long_ctx, 2)
+        q8_first = int(rng.integers(0, V))
+        qids = []
+        tok = q8_first
+        for i in range(6):  # the first steps' ids, for the oracle check (then re-run timed below)
+            rc = eng.dpuf_engine_forward_token(hq, tok, args.long_ctx + i, M.ptr(logits))
+            assert rc == 0, (rc, eng.dpuf_amd_last_error())
+            tok = int(np.argmax(logits))
+            qids.append(tok)
+        q8_ids = (q8_first, qids)
+        tok = qdecode(q8_first, args.long_ctx, 2)
         t0 = time.perf_counter()
         qdecode(tok, args.long_ctx + 2, qsteps)
         ms_q = (time.perf_counter() - t0) * 1e3 / qsteps
@@ -468,16 +570,22 @@ def main():
             eng.dpuf_engine_destroy(he)
 
     # --- CPU baseline: the oracle on the host cores, on the GPU's workload --
-    # The same model and the same 32-token prompt: pp32, then greedy decode
-    # for up to --cpu-seconds; its ids are compared with the GPU's greedy ids
-    # from the same prompt.  Then the oracle re-checks the LM-head leg's argmax
-    # ids (early exit on) for as many of its steps as fit the same budget.
+    # The same model and the same 32-token prompt: pp32, then tg32 greedy
+    # decode (up to --cpu-seconds) on --cpu-threads OpenMP threads pinned to
+    # physical cores of NUMA node 0; its ids are compared with the GPU's
+    # greedy ids from the same prompt.  Then a few decode steps on 6 threads
+    # (the reference README's thread count), the LM-head leg's argmax ids
+    # (early exit on) and the long-context legs' first ids (fp32 and int8
+    # caches, the same injected KV) re-checked against the oracle.
     cpu = None
     oracle_ids = None
     if args.cpu_seconds > 0:
         from oracle import oracle as O
+        from dpuf_amd import abi as A
         o = O.load()
-        oh = o.orc_engine_create(*model.create_args())
+        ocfg = A.DpufModelConfig.from_buffer_copy(model.cfg.contents)
+        ocfg.max_seq_len = args.prompt + 48
+        oh = o.orc_engine_create(*model.create_args(ocfg))
         lo = np.zeros(V, np.float32)
         t0 = time.perf_counter()
         assert o.orc_engine_forward(oh, len(prompt), M.ptr(prompt), 0, None, 1, M.ptr(lo)) == 0
@@ -486,32 +594,79 @@ def main():
         oracle_ids = [tok]
         n_dec = 0
         t0 = time.perf_counter()
-        while n_dec < len(gpu_greedy) - 1 and time.perf_counter() - t0 < args.cpu_seconds:
+        while n_dec < 32 and time.perf_counter() - t0 < args.cpu_seconds:
             tok_arr[0] = tok
             assert o.orc_engine_forward(oh, 1, M.ptr(tok_arr), len(prompt) + n_dec, None, 1, M.ptr(lo)) == 0
             tok = int(o.orc_argmax(M.ptr(lo), V))
             oracle_ids.append(tok)
             n_dec += 1
         dt = time.perf_counter() - t0
+        threads = int(o.orc_num_threads())
+        # README-comparable sample: 6 threads, decode steps continuing the sequence
+        o.orc_set_num_threads(6)
+        n6 = 0
+        t6 = time.perf_counter()
+        while n6 < 8 and time.perf_counter() - t6 < args.cpu_seconds:
+            tok_arr[0] = tok
+            assert o.orc_engine_forward(oh, 1, M.ptr(tok_arr), len(prompt) + n_dec + n6, None, 1, M.ptr(lo)) == 0
+            tok = int(o.orc_argmax(M.ptr(lo), V))
+            n6 += 1
+        dt6 = time.perf_counter() - t6
+        o.orc_set_num_threads(threads)
         o.orc_engine_destroy(oh)
         n_cmp = min(len(oracle_ids), len(gpu_greedy))
-        cpu_model = ""
-        try:
-            for ln in open("/proc/cpuinfo"):
-                if ln.startswith("model name"):
-                    cpu_model = ln.split(":", 1)[1].strip()
-                    break
-        except OSError:
-            pass
-        cpu = dict(value=round(n_dec / dt, 3) if n_dec else None, unit="tok/s", cores=int(o.orc_num_threads()),
-                   kind="port", cpu_model=cpu_model, pp_tok_s=round(len(prompt) / t_pp, 3),
-                   sample=f"{args.model} pp{len(prompt)} of the bench's own prompt, then {n_dec} greedy decode "
-                          f"tokens (oracle C restatement of the reference AVX2/OpenMP path, "
-                          f"{o.orc_num_threads()} OpenMP threads)",
+        cpu = dict(value=round(n_dec / dt, 3) if n_dec else None, unit="tok/s", cores=threads,
+                   kind="port", cpu_model=topo["model_name"],
+                   cpu_id=f"family {topo['family']} model {topo['model']} stepping {topo['stepping']}",
+                   topology=dict(numa_nodes=topo["numa_nodes"], logical_cpus=topo["logical_cpus"],
+                                 allowed_cpus=topo["allowed_cpus"],
+                                 node0_physical_cores_allowed=len(topo["node0_physical_cores"]),
+                                 pinned_cores=topo["pinned_cores"], omp_places=os.environ.get("OMP_PLACES", ""),
+                                 omp_proc_bind=os.environ.get("OMP_PROC_BIND", "")),
+                   pp_tok_s=round(len(prompt) / t_pp, 3), decode_tokens=n_dec,
+                   six_thread_tok_s=round(n6 / dt6, 3) if n6 else None, six_thread_tokens=n6,
+                   sample=f"{args.model} pp{len(prompt)} of the bench's own prompt, then tg{n_dec} greedy decode "
+                          f"(oracle C restatement of the reference AVX2/OpenMP path, {threads} OpenMP threads "
+                          f"pinned to NUMA node 0 physical cores); then {n6} more decode tokens on 6 threads",
                    greedy_ids_compared=n_cmp, greedy_ids_equal=oracle_ids[:n_cmp] == gpu_greedy[:n_cmp])
-        log(f"cpu baseline: pp{len(prompt)} {cpu['pp_tok_s']} tok/s, decode {cpu['value']} tok/s on "
-            f"{cpu['cores']} threads ({cpu_model}); greedy ids vs GPU: {n_cmp} compared, "
-            f"equal {cpu['greedy_ids_equal']}")
+        log(f"cpu baseline: pp{len(prompt)} {cpu['pp_tok_s']} tok/s, tg{n_dec} {cpu['value']} tok/s on "
+            f"{threads} threads, {cpu['six_thread_tok_s']} tok/s on 6 ({topo['model_name']}, pinned "
+            f"{topo['pinned_cores']}); greedy ids vs GPU: {n_cmp} compared, equal {cpu['greedy_ids_equal']}")
+
+        # long-context legs: the first 6 greedy ids from the same injected KV
+        def oracle_long(kv_type, first, want):
+            lcfg = A.DpufModelConfig.from_buffer_copy(model.cfg.contents)
+            lcfg.max_seq_len = args.long_ctx + 16
+            lcfg.kv_type = kv_type
+            ol = o.orc_engine_create(*model.create_args(lcfg))
+            L, nkv, hd = shape["num_layers"], shape["num_kv_heads"], shape["head_dim"]
+            krng = np.random.default_rng(args.seed + 4096)
+            for layer in range(L):
+                for kh in range(nkv):
+                    kk = krng.standard_normal((args.long_ctx, hd), dtype=np.float32)
+                    vv = krng.standard_normal((args.long_ctx, hd), dtype=np.float32)
+                    assert o.orc_engine_set_kv(ol, layer, kh, 0, args.long_ctx, M.ptr(kk), M.ptr(vv)) == 0
+            got, t = [], first
+            t0 = time.perf_counter()
+            for i in range(len(want)):
+                if time.perf_counter() - t0 > args.cpu_seconds:
+                    break
+                tok_arr[0] = t
+                assert o.orc_engine_forward(ol, 1, M.ptr(tok_arr), args.long_ctx + i, None, 1, M.ptr(lo)) == 0
+                t = int(o.orc_argmax(M.ptr(lo), V))
+                got.append(t)
+            o.orc_engine_destroy(ol)
+            return dict(oracle_ids_checked=len(got), oracle_ids_match=sum(int(a == b) for a, b in zip(got, want)),
+                        oracle_ids=got)
+
+        if long is not None and long_ids is not None:
+            long.update(oracle_long(0, *long_ids))
+            log(f"long context oracle check (fp32 cache): {long['oracle_ids_match']}/{long['oracle_ids_checked']} "
+                f"ids equal")
+        if long_q8 is not None and q8_ids is not None:
+            long_q8.update(oracle_long(1, *q8_ids))
+            log(f"long context oracle check (int8 cache): {long_q8['oracle_ids_match']}/"
+                f"{long_q8['oracle_ids_checked']} ids equal")
         if lm_inputs is not None:
             copies, hs, ids_early = lm_inputs
             os.environ["DPUF_EARLY_TILES"] = str(args.lm_zone)

@@ -1230,3 +1230,13 @@ int32_t orc_num_threads(void) {
     return 1;
 #endif
 }
+
+/* Sets the OpenMP threads of the following calls (n >= 1); the CPU baseline
+ * times a README-comparable thread count with it. */
+void orc_set_num_threads(int32_t n) {
+#ifdef _OPENMP
+    if (n >= 1) omp_set_num_threads(n);
+#else
+    (void)n;
+#endif
+}

@@ -71,6 +71,7 @@ int32_t orc_engine_forward(OrcEngine* e, int32_t n_tokens, const int32_t* ids, i
 int32_t orc_argmax(const float* logits, int32_t V);
 int32_t orc_top2_exit(const float* x, int32_t n, float thr);
 int32_t orc_num_threads(void);
+void orc_set_num_threads(int32_t n);
 
 #ifdef __cplusplus
 }

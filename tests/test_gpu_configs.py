@@ -117,6 +117,59 @@ def test_qwen3_8b_pp32_tg32_token_exact(eng, orc):
     p.close()
 
 
+@pytest.mark.timeout(900)
+def test_qwen3_8b_long_context_full_depth(eng, orc, monkeypatch):
+    """The long-context workload at the Qwen3-8B shape and depth (36 layers,
+    hidden 4096, 32 / 8 heads, FFN 12288, vocab 151936).  (a) pp512 of seeded
+    ids on the M > 1 path with the down projection pruned to 224 of 256 tiles:
+    the last row's logits bit-identical.  (b) Cache reset, a seeded N(0, 1)
+    4096-position KV cache injected into all 36 x 8 heads of both engines,
+    then 4 greedy one-token steps through the reference API (logits
+    bit-identical, ids identical) and 2 through the captured-graph
+    device-argmax entry (ids identical)."""
+    monkeypatch.setenv("DPUF_PREFILL_KEEP_TILES", "224")
+    monkeypatch.delenv("DPUF_GEN_KEEP_TILES", raising=False)
+    log("building the Qwen3-8B-shape model (4.26 GB of packed weights)")
+    m = M.Model.build(M.QWEN3_8B, max_seq_len=4112, seed=4321)
+    p = Pair(eng, orc, m)
+    c = m.cfg.contents
+    L, nkv, hd, V = c.num_layers, c.num_kv_heads, c.head_dim, c.vocab_size
+    ids = np.random.default_rng(4322).integers(0, V, 512).astype(np.int32)
+    log("8B pp512, keep 224 of 256 down tiles, 36 layers")
+    lg, lo = p.forward(ids, 0)
+    assert bits_equal(lg, lo), maxdiff(lg, lo)
+    log("8B pp512 last-row top-1/top-2 gap", top_gap(lo[-1]))
+    monkeypatch.delenv("DPUF_PREFILL_KEEP_TILES")
+    eng.dpuf_engine_reset_slot(p.g, 0)
+    orc.orc_engine_reset_slot(p.o, 0)
+    log(f"injecting a 4096-position N(0, 1) KV cache into {L} x {nkv} heads")
+    rng = np.random.default_rng(4323)
+    for layer in range(L):
+        for kvh in range(nkv):
+            k = rng.standard_normal((4096, hd), dtype=np.float32)
+            v = rng.standard_normal((4096, hd), dtype=np.float32)
+            p.set_kv(layer, kvh, 0, k, v)
+    tok = int(rng.integers(0, V))
+    log("8B decode at position 4096 (36 layers, 4096 cached keys)")
+    lg, lo = p.forward(np.array([tok], np.int32), 4096)
+    assert bits_equal(lg, lo), maxdiff(lg, lo)
+    toks, gap = greedy(p, lg, lo, 4097, 3, "8B 4096")
+    log("8B long-context greedy ids", toks, "smallest top-1/top-2 gap", gap)
+    tok = int(np.argmax(lo[-1]))
+    out = C.c_int32(-1)
+    for s in range(2):
+        pos = 4100 + s
+        log(f"8B graph decode with the device argmax at position {pos}")
+        rc = eng.dpuf_amd_engine_forward_argmax(p.g, 1, M.ptr(np.array([tok], np.int32)), pos, None, 1,
+                                                C.byref(out), None)
+        assert rc == 0, eng.dpuf_amd_last_error()
+        lo = np.zeros(V, np.float32)
+        assert orc.orc_engine_forward(p.o, 1, M.ptr(np.array([tok], np.int32)), pos, None, 1, M.ptr(lo)) == 0
+        assert out.value == orc.orc_argmax(M.ptr(lo), V)
+        tok = out.value
+    p.close()
+
+
 def test_gqa4_long_context_injected_kv(eng, orc):
     """The Qwen3-8B attention geometry (32 Q / 8 KV heads: groups of 4,
     head_dim 128) on a small hidden size.  (1) Short context, the fused decode
@@ -180,6 +233,70 @@ def test_one_token_long_context_groups(eng, orc, nq, nkv, hd, ctx):
     p.close()
 
 
+WIDE, FALLBACK = 1, 3  # dpuf_amd_attn_path_count: one-token wide kernels, one-pair fallback
+
+
+@pytest.mark.parametrize("nq,nkv,ctx", [(16, 2, 4096), (8, 2, 7500)])
+def test_one_token_wide_path_beyond_lds_budget(eng, orc, nq, nkv, ctx):
+    """One-token decode where the probability rows exceed the LDS budget of
+    the split softmax / P.V kernel (groups of 8 at 4096 keys, groups of 4 at
+    7500): the one-token kernels keep those rows in global memory, so eager
+    steps take them (scores, softmax once per row, wide P.V), not the
+    one-pair fallback; logits bit-identical."""
+    shape = dict(hidden_size=256, intermediate_size=512, num_layers=2, num_q_heads=nq, num_kv_heads=nkv,
+                 head_dim=128, vocab_size=4096, tie_word_embeddings=1)
+    m = M.Model.build(shape, max_seq_len=ctx + 8, seed=95)
+    p = Pair(eng, orc, m)
+    eng.dpuf_amd_engine_set_graphs(p.g, 0)
+    rng = np.random.default_rng(96)
+    log(f"groups of {nq // nkv}: injecting {ctx} positions, eager decode")
+    for layer in range(2):
+        for kvh in range(nkv):
+            p.set_kv(layer, kvh, 0, rng.standard_normal((ctx, 128), dtype=np.float32),
+                     rng.standard_normal((ctx, 128), dtype=np.float32))
+    w0, f0 = eng.dpuf_amd_attn_path_count(WIDE), eng.dpuf_amd_attn_path_count(FALLBACK)
+    lg, lo = p.forward(np.array([5], np.int32), ctx)
+    assert bits_equal(lg, lo), maxdiff(lg, lo)
+    assert eng.dpuf_amd_attn_path_count(WIDE) - w0 == 2  # one launch set per layer
+    assert eng.dpuf_amd_attn_path_count(FALLBACK) == f0
+    greedy(p, lg, lo, ctx + 1, 2, f"G{nq // nkv} ctx {ctx} wide")
+    p.close()
+
+
+def test_graph_bucket_with_large_max_seq(eng, orc):
+    """An engine created for 32768 positions decoding at about 300 keys
+    through the captured-graph entry: the graph is captured for the key
+    bucket of the position (512), not for max_seq, so its attention takes the
+    one-token wide kernels as an eager step there would, not the one-pair
+    fallback; ids equal the oracle's, and a step past the bucket (position
+    520) captures the next one."""
+    shape = dict(hidden_size=256, intermediate_size=512, num_layers=2, num_q_heads=8, num_kv_heads=2,
+                 head_dim=128, vocab_size=4096, tie_word_embeddings=1)
+    m = M.Model.build(shape, max_seq_len=32768, seed=97)
+    p = Pair(eng, orc, m)
+    rng = np.random.default_rng(98)
+    for layer in range(2):
+        for kvh in range(2):
+            p.set_kv(layer, kvh, 0, rng.standard_normal((520, 128), dtype=np.float32),
+                     rng.standard_normal((520, 128), dtype=np.float32))
+    out = C.c_int32(-1)
+    tok = 7
+    for pos in (300, 301, 302, 520, 521):
+        log(f"max_seq 32768: graph decode at position {pos}")
+        w0, f0 = eng.dpuf_amd_attn_path_count(WIDE), eng.dpuf_amd_attn_path_count(FALLBACK)
+        rc = eng.dpuf_amd_engine_forward_argmax(p.g, 1, M.ptr(np.array([tok], np.int32)), pos, None, 1,
+                                                C.byref(out), None)
+        assert rc == 0, eng.dpuf_amd_last_error()
+        captured = eng.dpuf_amd_attn_path_count(WIDE) - w0
+        assert captured == (2 if pos in (300, 520) else 0), (pos, captured)  # captured once per bucket
+        assert eng.dpuf_amd_attn_path_count(FALLBACK) == f0
+        lo = np.zeros(4096, np.float32)
+        assert orc.orc_engine_forward(p.o, 1, M.ptr(np.array([tok], np.int32)), pos, None, 1, M.ptr(lo)) == 0
+        assert out.value == orc.orc_argmax(M.ptr(lo), 4096)
+        tok = out.value
+    p.close()
+
+
 def test_attention_beyond_split_lds_budget(eng, orc):
     """Groups of 4 with 7200 cached positions.  A two-token forward there:
     its rows of probabilities no longer fit the split kernels' LDS budget, so
@@ -194,9 +311,12 @@ def test_attention_beyond_split_lds_budget(eng, orc):
         p.set_kv(0, kvh, 0, rng.standard_normal((7200, 128), dtype=np.float32),
                  rng.standard_normal((7200, 128), dtype=np.float32))
     log("k_attn fallback: two tokens at position 7200")
+    f0 = eng.dpuf_amd_attn_path_count(FALLBACK)
     lg, lo = p.forward(np.array([3, 4000], np.int32), 7200, only_last=0)
     assert bits_equal(lg, lo), maxdiff(lg, lo)
+    assert eng.dpuf_amd_attn_path_count(FALLBACK) - f0 == 1
     greedy(p, lg, lo, 7202, 3, "after fallback")
+    assert eng.dpuf_amd_attn_path_count(FALLBACK) - f0 == 1  # the one-token steps take the wide kernels
     p.close()
 
 
