@@ -268,11 +268,10 @@ __global__ __launch_bounds__(SMX_NT) void k_attn_smx(float* __restrict__ S, cons
 
 // a = fma(p[t], v[t], a) over the first n keys of a chunk, in order; p and v
 // are 16-byte aligned LDS rows.  A full chunk is unrolled in 8-key blocks,
-// each block's four 16-byte reads issued three blocks ahead: at most 12 LDS
-// reads are in flight, within what the LDS wait counter can express (15), so
-// every wait is for exactly the block about to be used (with 16 in flight the
-// compiler fell back to waiting for all of them).  A partial chunk takes the
-// loop.
+// each block's four 16-byte reads issued three blocks ahead; scheduling
+// regions of one block each keep the reads there (a pinned group schedule
+// of the whole chunk ran as fast but took the compiler half a minute per
+// instance).  A partial chunk takes the loop.
 DEV float pvw_chunk(const float* p, const float* v, int n, float a) {
     if (n == PVW_CK) {
         constexpr int NB = PVW_CK / 8, AH = 3;
@@ -284,10 +283,10 @@ DEV float pvw_chunk(const float* p, const float* v, int n, float a) {
                 pb[k][i] = *(const float4*)(p + 8 * k + 4 * i);
                 vb[k][i] = *(const float4*)(v + 8 * k + 4 * i);
             }
-        // the schedule is pinned (the scheduler otherwise moved each block's
-        // reads down to just before its FMAs): the prologue's reads, then per
-        // block the next reads followed by its 8 FMAs
-        __builtin_amdgcn_sched_group_barrier(0x100, 4 * AH, 0);
+        // one scheduling region per block (the scheduler otherwise moved each
+        // block's reads down to just before its FMAs): the prologue's reads,
+        // then per block the next reads followed by its 8 FMAs
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int b = 0; b < NB; b++) {
             const int cur = b % (AH + 1);
@@ -297,7 +296,6 @@ DEV float pvw_chunk(const float* p, const float* v, int n, float a) {
                     pb[(b + AH) % (AH + 1)][i] = *(const float4*)(p + 8 * (b + AH) + 4 * i);
                     vb[(b + AH) % (AH + 1)][i] = *(const float4*)(v + 8 * (b + AH) + 4 * i);
                 }
-                __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
             }
 #pragma unroll
             for (int i = 0; i < 2; i++) {
@@ -306,12 +304,34 @@ DEV float pvw_chunk(const float* p, const float* v, int n, float a) {
                 a = fmaf(pb[cur][i].z, vb[cur][i].z, a);
                 a = fmaf(pb[cur][i].w, vb[cur][i].w, a);
             }
-            __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
+            __builtin_amdgcn_sched_barrier(0);
         }
         return a;
     }
     for (int t = 0; t < n; t++) a = fmaf(p[t], v[t], a);
     return a;
+}
+
+// Keys t .. t + 3 of a probability row of max_seq entries (t a multiple of
+// 4): one 16-byte load, or at the row's end element by element with keys past
+// it clamped to its last one (their values are never used; the keys before
+// them keep their own values whatever max_seq % 4 is).
+DEV gm_f4 pv_piece(const float* row, int t, int max_seq) {
+    if (t + 4 <= max_seq) return *(const gm_f4*)(row + t);
+    gm_f4 r;
+#pragma unroll
+    for (int k = 0; k < 4; k++) r[k] = row[min(t + k, max_seq - 1)];
+    return r;
+}
+
+// The int8 cache's V scales of keys t .. t + 3 (one per 32 dims, HD / 32 per
+// key), clamped as pv_piece.
+template <int HD>
+DEV gm_f4 pv_scales(const float* Vs, int t, int max_seq) {
+    gm_f4 r;
+#pragma unroll
+    for (int k = 0; k < 4; k++) r[k] = Vs[(size_t)min(t + k, max_seq - 1) * (HD / 32)];
+    return r;
 }
 
 // Chunk c (clamped to the last one) of a k_attn_pvw workgroup into a
@@ -337,14 +357,10 @@ DEV void pvw_load(const float* Vh, const float* Ph, const int8_t* Vq, const floa
     }
 #pragma unroll
     for (int i = 0; i < GM / 2; i++) {
-        const int f = 512 * i + 4 * pl, hh = min(f / PVW_CK, G - 1), t = min(c0 + f % PVW_CK, max_seq - 4);
-        r[2 + i] = *(const gm_f4*)(Ph + (size_t)hh * max_seq + t);
+        const int f = 512 * i + 4 * pl, hh = min(f / PVW_CK, G - 1);
+        r[2 + i] = pv_piece(Ph + (size_t)hh * max_seq, c0 + f % PVW_CK, max_seq);
     }
-    if (Q8) {
-        const int t = min(c0 + (4 * pl) % PVW_CK, max_seq - 4);
-#pragma unroll
-        for (int k = 0; k < 4; k++) r[2 + GM / 2][k] = Vs[(size_t)(t + k) * (HD / 32)];
-    }
+    if (Q8) r[2 + GM / 2] = pv_scales<HD>(Vs, c0 + (4 * pl) % PVW_CK, max_seq);
 }
 
 // A producer lane's chunk into an LDS slot, V transposed to [dim][key].
@@ -434,6 +450,276 @@ __global__ __launch_bounds__(192) void k_attn_pvw(const float* __restrict__ P, c
 }
 
 
+// ---------------------------------------------------------------------------
+// k_attn_pvd: P.V of a one-token step for groups of G = 2 or 4 query heads,
+// the same chains as k_attn_pvw (a = fma(p[t], v[t], a) over the keys in
+// order, one per (head, dim)) with a quarter of its LDS reads per key.
+//
+// The chain wave's lane (h, j) = (lane / DW, lane % DW), DW = 64 / G, runs
+// the chain of head h and dim d0 + j, so every 16-lane row belongs to one
+// head.  Per 16 keys a lane reads its dim's transposed V row (four 16-byte
+// LDS reads) and ONE probability, p[h][t + lane % 16]; key t + i takes p from
+// lane i of the row through the DPP row_newbcast source of v_fmac_f32 (data
+// movement only: one instruction and one rounding per key, as fmaf).  The
+// chain is bound by instruction issue (a dependent v_fmac 4.6 cycles, a
+// 64-lane ds_read_b128 ~11), so five reads per 16 keys instead of eight.
+//
+// Two producer waves stream chunks of PVD_CK keys into a 3-slot LDS ring two
+// chunks ahead of the chain (register sets loaded five chunks ahead); the
+// chain's reads run on into the next chunk, which is complete since the
+// barrier before, so no pipeline restart per chunk.  Q8: V arrives as int8
+// (widened, exact) and the producers store W = p * vs (the reference's
+// p * v_scale, dpuf_engine.c:726-747) in p's place, vs the V scale of the
+// WG's 32-dim block.
+// ---------------------------------------------------------------------------
+#define PVD_CK 256  // keys per chunk
+#define PVD_AH 3    // 16-key groups read ahead by the chain
+#define PVD_LD (PVD_CK + 4)  // LDS row stride (rows on distinct banks)
+
+template <int G, bool Q8>
+struct PvdShape {
+    static constexpr int DW = 64 / G;            // dims per workgroup
+    static constexpr int LPK = DW / 4;           // producer lanes per key (4 dims each)
+    static constexpr int KPI = 128 / LPK;        // keys per producer load instruction
+    static constexpr int NV = PVD_CK / KPI;      // V loads per producer lane per chunk
+    static constexpr int NP = G * PVD_CK / 512;  // P pieces (4 keys) per producer lane per chunk
+    static constexpr int NR = NV + NP + (Q8 ? NP : 0);
+};
+
+template <int HD, int G, bool Q8>
+DEV void pvd_load(const float* Vh, const int8_t* Vq, const float* Vs, const float* Ph, int c, int nck, int max_seq,
+                  int pl, gm_f4 (&r)[PvdShape<G, Q8>::NR]) {
+    using S = PvdShape<G, Q8>;
+    const int c0 = (c < nck ? c : nck - 1) * PVD_CK;
+#pragma unroll
+    for (int i = 0; i < S::NV; i++) {
+        const size_t key = (size_t)min(c0 + S::KPI * i + pl / S::LPK, max_seq - 1);
+        const int dd = 4 * (pl % S::LPK);
+        if (Q8) r[i][0] = __int_as_float(*(const int32_t*)(Vq + key * HD + dd));
+        else r[i] = *(const gm_f4*)(Vh + key * HD + dd);
+    }
+#pragma unroll
+    for (int i = 0; i < S::NP; i++) {
+        const int f = 512 * i + 4 * pl, t = c0 + f % PVD_CK;
+        r[S::NV + i] = pv_piece(Ph + (size_t)(f / PVD_CK) * max_seq, t, max_seq);
+        if (Q8) r[S::NV + S::NP + i] = pv_scales<HD>(Vs, t, max_seq);
+    }
+}
+
+template <int G, bool Q8>
+DEV void pvd_store(float (*Vt)[PVD_LD], float (*Pt)[PVD_LD], int pl,
+                   const gm_f4 (&r)[PvdShape<G, Q8>::NR]) {
+    using S = PvdShape<G, Q8>;
+#pragma unroll
+    for (int i = 0; i < S::NV; i++) {
+        const int key = S::KPI * i + pl / S::LPK, dd = 4 * (pl % S::LPK);
+        if (Q8) {
+            const int32_t b = __float_as_int(r[i][0]);
+#pragma unroll
+            for (int k = 0; k < 4; k++) Vt[dd + k][key] = (float)(int8_t)(b >> (8 * k));
+        } else {
+#pragma unroll
+            for (int k = 0; k < 4; k++) Vt[dd + k][key] = r[i][k];
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < S::NP; i++) {
+        const int f = 512 * i + 4 * pl;
+        gm_f4 w = r[S::NV + i];
+        if (Q8) {
+#pragma unroll
+            for (int k = 0; k < 4; k++) w[k] = w[k] * r[S::NV + S::NP + i][k];
+        }
+        *(gm_f4*)&Pt[f / PVD_CK][f % PVD_CK] = w;
+    }
+}
+
+// 16 keys of a chain: a = fma(p[t + i], v[t + i], a), i ascending, p[t + i]
+// from lane i of the lane's 16-lane row.  One asm block: the DPP source pr
+// comes from an LDS read, never from a VALU write inside the block, so no
+// wait states are needed between the instructions.
+DEV float pvd_16(float pr, const float4 (&v)[4], float a) {
+    asm("v_fmac_f32_dpp %0, %1, %2 row_newbcast:0 row_mask:0xf bank_mask:0xf\n"
+        "v_fmac_f32_dpp %0, %1, %3 row_newbcast:1 row_mask:0xf bank_mask:0xf\n"
+        "v_fmac_f32_dpp %0, %1, %4 row_newbcast:2 row_mask:0xf bank_mask:0xf\n"
+        "v_fmac_f32_dpp %0, %1, %5 row_newbcast:3 row_mask:0xf bank_mask:0xf\n"
+        "v_fmac_f32_dpp %0, %1, %6 row_newbcast:4 row_mask:0xf bank_mask:0xf\n"
+        "v_fmac_f32_dpp %0, %1, %7 row_newbcast:5 row_mask:0xf bank_mask:0xf\n"
+        "v_fmac_f32_dpp %0, %1, %8 row_newbcast:6 row_mask:0xf bank_mask:0xf\n"
+        "v_fmac_f32_dpp %0, %1, %9 row_newbcast:7 row_mask:0xf bank_mask:0xf\n"
+        "v_fmac_f32_dpp %0, %1, %10 row_newbcast:8 row_mask:0xf bank_mask:0xf\n"
+        "v_fmac_f32_dpp %0, %1, %11 row_newbcast:9 row_mask:0xf bank_mask:0xf\n"
+        "v_fmac_f32_dpp %0, %1, %12 row_newbcast:10 row_mask:0xf bank_mask:0xf\n"
+        "v_fmac_f32_dpp %0, %1, %13 row_newbcast:11 row_mask:0xf bank_mask:0xf\n"
+        "v_fmac_f32_dpp %0, %1, %14 row_newbcast:12 row_mask:0xf bank_mask:0xf\n"
+        "v_fmac_f32_dpp %0, %1, %15 row_newbcast:13 row_mask:0xf bank_mask:0xf\n"
+        "v_fmac_f32_dpp %0, %1, %16 row_newbcast:14 row_mask:0xf bank_mask:0xf\n"
+        "v_fmac_f32_dpp %0, %1, %17 row_newbcast:15 row_mask:0xf bank_mask:0xf\n"
+        : "+v"(a)
+        : "v"(pr), "v"(v[0].x), "v"(v[0].y), "v"(v[0].z), "v"(v[0].w), "v"(v[1].x), "v"(v[1].y), "v"(v[1].z),
+          "v"(v[1].w), "v"(v[2].x), "v"(v[2].y), "v"(v[2].z), "v"(v[2].w), "v"(v[3].x), "v"(v[3].y), "v"(v[3].z),
+          "v"(v[3].w));
+    return a;
+}
+
+// The chain over one full chunk in slot SL; the reads of the last PVD_AH
+// groups' successors go to slot SN (the next chunk).  One scheduling region
+// per group keeps each group's reads ahead of its FMAs.
+template <int G, bool Q8, int SL, int SN>
+DEV float pvd_chunk(float (*Vt)[64 / G][PVD_LD], float (*Pt)[G][PVD_LD], int h, int j,
+                    int n, float a, float (&pr)[PVD_AH + 1], float4 (&vb)[PVD_AH + 1][4]) {
+    constexpr int NG = PVD_CK / 16;
+    static_assert(NG % (PVD_AH + 1) == 0, "the read-ahead ring index is static across chunks");
+#pragma unroll
+    for (int g = 0; g < NG; g++) {
+        const int cur = g % (PVD_AH + 1), ng = g + PVD_AH;
+        const int ns = ng < NG ? SL : SN, no = (ng < NG ? ng : ng - NG) * 16;
+        pr[ng % (PVD_AH + 1)] = Pt[ns][h][no + n];
+#pragma unroll
+        for (int i = 0; i < 4; i++) vb[ng % (PVD_AH + 1)][i] = *(const float4*)(&Vt[ns][j][no + 4 * i]);
+        a = pvd_16(pr[cur], vb[cur], a);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    return a;
+}
+
+// Waits until at most N vector-memory operations of this wave are in flight.
+#define PVD_VMCNT(N) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory")
+
+template <int HD, int G, bool Q8>
+__global__ __launch_bounds__(192) void k_attn_pvd(const float* __restrict__ P, const float* __restrict__ vc,
+                                                  const int32_t* __restrict__ pos0p, int n_kv, int max_seq,
+                                                  float* __restrict__ out, DpufKvQ8 c8) {
+    using S = PvdShape<G, Q8>;
+    constexpr int DW = S::DW;
+    static_assert(G == 2 || G == 4, "every 16-lane row of the chain wave holds one head");
+    __shared__ __align__(16) float Vt[3][DW][PVD_LD];
+    __shared__ __align__(16) float Pt[3][G][PVD_LD];
+    const int L = *pos0p + 1, nck = (L + PVD_CK - 1) / PVD_CK, nfull = L / PVD_CK;
+    if ((int)blockIdx.y >= HD / DW) {
+        // warm-up workgroups (after the chain workgroups in dispatch order):
+        // the V rows past the chunks the producers load at their start go
+        // into the Infinity Cache, so the producers' later loads hit there
+        // instead of each of the few chain CUs pulling its slice from HBM
+        const int wi = ((int)blockIdx.y - HD / DW) * n_kv + (int)blockIdx.x;
+        const int nw = ((int)gridDim.y - HD / DW) * n_kv;
+        constexpr int RB = Q8 ? HD : HD * 4;  // bytes per V row
+        const uint8_t* base = Q8 ? (const uint8_t*)c8.vq : (const uint8_t*)vc;
+        const int k0 = 5 * PVD_CK;
+        if (L <= k0) return;
+        const int kvw = wi % n_kv, part = wi / n_kv, parts = nw / n_kv;
+        const size_t seg = (size_t)(L - k0) * RB, lo = seg * part / parts, hi = seg * (part + 1) / parts;
+        const uint8_t* p0 = base + ((size_t)kvw * max_seq + k0) * RB;
+        uint32_t acc = 0;
+        for (size_t o = lo + 16 * (size_t)threadIdx.x; o < hi; o += 16 * 8 * (size_t)blockDim.x) {
+            uint4 v[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const size_t oo = o + (size_t)k * 16 * blockDim.x;
+                v[k] = oo + 16 <= hi ? *(const uint4*)(p0 + oo) : make_uint4(0, 0, 0, 0);
+            }
+#pragma unroll
+            for (int k = 0; k < 8; k++) acc ^= v[k].x ^ v[k].w;
+        }
+        asm volatile("" ::"v"(acc));  // the loaded values count as used: the reads stay
+        return;
+    }
+    const int kvh = blockIdx.x, d0 = blockIdx.y * DW, tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const int h = lane / DW, j = lane % DW, n = lane & 15, pl = tid - 64;
+    const float* Vh = Q8 ? nullptr : vc + (size_t)kvh * max_seq * HD + d0;
+    const int8_t* Vq = Q8 ? c8.vq + (size_t)kvh * max_seq * HD + d0 : nullptr;
+    const float* Vs = Q8 ? c8.vs + (size_t)kvh * max_seq * (HD / 32) + d0 / 32 : nullptr;
+    const float* Ph = P + (size_t)kvh * G * max_seq;
+    gm_f4 r0[S::NR], r1[S::NR], r2[S::NR];  // chunks c % 3
+    float pr[PVD_AH + 1];
+    float4 vb[PVD_AH + 1][4];
+    if (w > 0) {
+        pvd_load<HD, G, Q8>(Vh, Vq, Vs, Ph, 0, nck, max_seq, pl, r0);
+        pvd_load<HD, G, Q8>(Vh, Vq, Vs, Ph, 1, nck, max_seq, pl, r1);
+        pvd_load<HD, G, Q8>(Vh, Vq, Vs, Ph, 2, nck, max_seq, pl, r2);
+        PVD_VMCNT(2 * S::NR);
+        pvd_store<G, Q8>(Vt[0], Pt[0], pl, r0);
+        pvd_load<HD, G, Q8>(Vh, Vq, Vs, Ph, 3, nck, max_seq, pl, r0);
+        PVD_VMCNT(2 * S::NR);
+        pvd_store<G, Q8>(Vt[1], Pt[1], pl, r1);
+        pvd_load<HD, G, Q8>(Vh, Vq, Vs, Ph, 4, nck, max_seq, pl, r1);
+    }
+    __syncthreads();
+    float a = 0.0f;
+    if (w == 0) {
+#pragma unroll
+        for (int k = 0; k < PVD_AH; k++) {
+            pr[k] = Pt[0][h][16 * k + n];
+#pragma unroll
+            for (int i = 0; i < 4; i++) vb[k][i] = *(const float4*)(&Vt[0][j][16 * k + 4 * i]);
+        }
+    }
+    // Step C: the chain consumes chunk C (slot C % 3; its reads run on into
+    // slot (C + 1) % 3, written before the previous barrier); the producers
+    // store chunk C + 2 (register set (C + 2) % 3, loaded three steps ago)
+    // into slot (C + 2) % 3, whose chunk C - 1 the chain finished before that
+    // barrier, and load chunk C + 5 into the set.  The chain wave passes the
+    // barrier without waiting for its reads in flight (they target slots
+    // nobody writes in this step); the producers wait for their LDS stores.
+#define PVD_STEP(C, SL, SN, RS)                                                                        \
+    {                                                                                                  \
+        if (w == 0) {                                                                                  \
+            if ((C) < nfull) {                                                                         \
+                a = pvd_chunk<G, Q8, SL, SN>(Vt, Pt, h, j, n, a, pr, vb);                              \
+            } else if ((C) == nfull) {                                                                 \
+                const int nn = L - (C) * PVD_CK;                                                       \
+                for (int t = 0; t < nn; t++) a = fmaf(Pt[SL][h][t], Vt[SL][j][t], a);                 \
+            }                                                                                          \
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);                                                   \
+            __builtin_amdgcn_s_barrier();                                                              \
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);                                                   \
+        } else {                                                                                       \
+            PVD_VMCNT(S::NR);                                                                          \
+            pvd_store<G, Q8>(Vt[((SL) + 2) % 3], Pt[((SL) + 2) % 3], pl, RS);                          \
+            pvd_load<HD, G, Q8>(Vh, Vq, Vs, Ph, (C) + 5, nck, max_seq, pl, RS);                        \
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");                                         \
+            __builtin_amdgcn_s_barrier();                                                              \
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);                                                   \
+        }                                                                                              \
+    }
+    for (int c = 0; c < nck; c += 3) {
+        PVD_STEP(c, 0, 1, r2)
+        if (c + 1 >= nck) break;
+        PVD_STEP(c + 1, 1, 2, r0)
+        if (c + 2 >= nck) break;
+        PVD_STEP(c + 2, 2, 0, r1)
+    }
+#undef PVD_STEP
+    if (w == 0) out[(size_t)(kvh * G + h) * HD + d0 + j] = a;
+}
+
+// The one-token P.V launch: k_attn_pvd for groups of 2 and 4, else k_attn_pvw
+// (gm: its group instance, 2, 4 or 8).
+template <int HD, bool Q8>
+static void pv_wide_launch(void* s, int G, int gm, const float* scores, const float* vc, const int32_t* pos0p, int n_q,
+                           int n_kv, int max_seq, float* out, DpufKvQ8 c8) {
+    // k_attn_pvd: HD / DW chain workgroups per kv head, then warm-up
+    // workgroups up to about one per CU
+    if (G == 4 || G == 2) {
+        const int ns = HD / (64 / G), nwarm = (dpuf_hip_cu_count() / n_kv > ns ? dpuf_hip_cu_count() / n_kv : ns) - ns;
+        if (G == 4)
+            hipLaunchKernelGGL((k_attn_pvd<HD, 4, Q8>), dim3(n_kv, ns + nwarm), dim3(192), 0, ST(s), scores, vc, pos0p,
+                               n_kv, max_seq, out, c8);
+        else
+            hipLaunchKernelGGL((k_attn_pvd<HD, 2, Q8>), dim3(n_kv, ns + nwarm), dim3(192), 0, ST(s), scores, vc, pos0p,
+                               n_kv, max_seq, out, c8);
+    }
+    else if (gm == 2)
+        hipLaunchKernelGGL((k_attn_pvw<HD, 2, Q8>), dim3(n_kv, HD / 4), dim3(192), 0, ST(s), scores, vc, pos0p, n_q,
+                           n_kv, max_seq, out, c8);
+    else if (gm == 4)
+        hipLaunchKernelGGL((k_attn_pvw<HD, 4, Q8>), dim3(n_kv, HD / 4), dim3(192), 0, ST(s), scores, vc, pos0p, n_q,
+                           n_kv, max_seq, out, c8);
+    else
+        hipLaunchKernelGGL((k_attn_pvw<HD, 8, Q8>), dim3(n_kv, HD / 4), dim3(192), 0, ST(s), scores, vc, pos0p, n_q,
+                           n_kv, max_seq, out, c8);
+}
+
 int32_t attn_wide_f32(void* s, int32_t lmax, const float* q, const float* kc, const float* vc, float* out,
                       float* scores, const int32_t* pos0p, int32_t n_q, int32_t n_kv, int32_t hd, int32_t max_seq,
                       float scale, const ScRope* rope) {
@@ -442,7 +728,7 @@ int32_t attn_wide_f32(void* s, int32_t lmax, const float* q, const float* kc, co
     const int G = n_q / n_kv;
     const int M = 1;
     // one-token decode with an even group: softmax once per row, then the
-    // wide P.V (one wave per kv head and 4 dims)
+    // wide P.V (k_attn_pvd for groups of 2 and 4, else k_attn_pvw)
     {
         // chain segments of the softmax: 8 SEG positions per sum lane cover
         // keys up to 64 SEG
@@ -452,7 +738,6 @@ int32_t attn_wide_f32(void* s, int32_t lmax, const float* q, const float* kc, co
             if (64 * segs[i] >= lmax) seg = segs[i];
         if (M == 1 && (G & 1) == 0 && G <= 8 && seg) {
             const int gm = G <= 2 ? 2 : G <= 4 ? 4 : 8;
-            const dim3 gp(n_kv, hd / 4);
 #define SMX_LAUNCH(SG)                                                                                            \
     if (seg == SG) hipLaunchKernelGGL(k_attn_smx<SG>, dim3(n_q), dim3(SMX_NT), 0, ST(s), scores, pos0p, max_seq);
 #define SC1_LAUNCH(HDV, GMV)                                                                                      \
@@ -466,26 +751,18 @@ int32_t attn_wide_f32(void* s, int32_t lmax, const float* q, const float* kc, co
             hipLaunchKernelGGL((k_attn_sc1<HDV, GMV, false>), g1s, dim3(256), l1s, ST(s), q, kc, pos0p, n_q,      \
                                n_kv, max_seq, scale, scores, ScRope{});                                           \
     }
-#define PVW_LAUNCH(HDV)                                                                                           \
+#define WIDE_LAUNCH(HDV)                                                                                          \
     if (gm == 2) SC1_LAUNCH(HDV, 2) else if (gm == 4) SC1_LAUNCH(HDV, 4) else SC1_LAUNCH(HDV, 8)                  \
     SMX_LAUNCH(16) SMX_LAUNCH(32) SMX_LAUNCH(48) SMX_LAUNCH(64) SMX_LAUNCH(80) SMX_LAUNCH(96) SMX_LAUNCH(128)  \
-    if (gm == 2)                                                                                                  \
-        hipLaunchKernelGGL((k_attn_pvw<HDV, 2, false>), gp, dim3(192), 0, ST(s), scores, vc, pos0p, n_q, n_kv,  \
-                           max_seq, out, DpufKvQ8{});                                                                                  \
-    else if (gm == 4)                                                                                             \
-        hipLaunchKernelGGL((k_attn_pvw<HDV, 4, false>), gp, dim3(192), 0, ST(s), scores, vc, pos0p, n_q, n_kv,  \
-                           max_seq, out, DpufKvQ8{});                                                                                  \
-    else                                                                                                          \
-        hipLaunchKernelGGL((k_attn_pvw<HDV, 8, false>), gp, dim3(192), 0, ST(s), scores, vc, pos0p, n_q, n_kv,  \
-                           max_seq, out, DpufKvQ8{});
+    pv_wide_launch<HDV, false>(s, G, gm, scores, vc, pos0p, n_q, n_kv, max_seq, out, DpufKvQ8{});
             if (hd == 64) {
-                PVW_LAUNCH(64)
+                WIDE_LAUNCH(64)
             } else if (hd == 128) {
-                PVW_LAUNCH(128)
+                WIDE_LAUNCH(128)
             } else {
-                PVW_LAUNCH(256)
+                WIDE_LAUNCH(256)
             }
-#undef PVW_LAUNCH
+#undef WIDE_LAUNCH
 #undef SC1_LAUNCH
 #undef SMX_LAUNCH
             LAUNCHED("k_attn_split_wide");
@@ -502,9 +779,9 @@ int32_t attn_wide_q8(void* s, int32_t lmax, const int32_t* pos0, int32_t n_q, in
     if (lmax > max_seq) lmax = max_seq;
     const int G = n_q / n_kv;
     const int M = 1;
-    // one token, groups of 2, 4 or 8: the softmax once per row and P.V on one
-    // chain wave per (kv head, 4 dims), as for the fp32 cache, with W = p *
-    // v_scale and V widened in the producers
+    // one token, groups of 2, 4, 6 or 8: the softmax once per row and the
+    // wide P.V, as for the fp32 cache, with W = p * v_scale and V widened in
+    // the producers
     if (M == 1 && (G & 1) == 0 && G <= 8) {
         const int segs[7] = {16, 32, 48, 64, 80, 96, 128};
         int seg = 0;
@@ -512,28 +789,14 @@ int32_t attn_wide_q8(void* s, int32_t lmax, const int32_t* pos0, int32_t n_q, in
             if (64 * segs[i] >= lmax) seg = segs[i];
         if (seg) {
             const int gm = G <= 2 ? 2 : G <= 4 ? 4 : 8;
-            const dim3 gp(n_kv, hd / 4);
 #define SMXQ(SG) \
     if (seg == SG) hipLaunchKernelGGL(k_attn_smx<SG>, dim3(n_q), dim3(SMX_NT), 0, ST(s), scores, pos0, max_seq);
             SMXQ(16) SMXQ(32) SMXQ(48) SMXQ(64) SMXQ(80) SMXQ(96) SMXQ(128)
 #undef SMXQ
-#define PVWQ(HDV)                                                                                                  \
-    do {                                                                                                           \
-        if (gm == 2)                                                                                               \
-            hipLaunchKernelGGL((k_attn_pvw<HDV, 2, true>), gp, dim3(192), 0, ST(s), scores, nullptr, pos0, n_q, n_kv, \
-                               max_seq, out, c8);                                                                  \
-        else if (gm == 4)                                                                                          \
-            hipLaunchKernelGGL((k_attn_pvw<HDV, 4, true>), gp, dim3(192), 0, ST(s), scores, nullptr, pos0, n_q, n_kv, \
-                               max_seq, out, c8);                                                                  \
-        else                                                                                                       \
-            hipLaunchKernelGGL((k_attn_pvw<HDV, 8, true>), gp, dim3(192), 0, ST(s), scores, nullptr, pos0, n_q, n_kv, \
-                               max_seq, out, c8);                                                                  \
-    } while (0)
-            if (hd == 64) PVWQ(64);
-            else if (hd == 128) PVWQ(128);
-            else PVWQ(256);
-#undef PVWQ
-            LAUNCHED("k_attn_q8_sc/k_attn_smx/k_attn_pvw<q8>");
+            if (hd == 64) pv_wide_launch<64, true>(s, G, gm, scores, nullptr, pos0, n_q, n_kv, max_seq, out, c8);
+            else if (hd == 128) pv_wide_launch<128, true>(s, G, gm, scores, nullptr, pos0, n_q, n_kv, max_seq, out, c8);
+            else pv_wide_launch<256, true>(s, G, gm, scores, nullptr, pos0, n_q, n_kv, max_seq, out, c8);
+            LAUNCHED("k_attn_q8_sc/k_attn_smx/wide P.V<q8>");
             return 0;
         }
     }

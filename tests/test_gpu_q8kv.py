@@ -158,3 +158,27 @@ def test_q8_4096_injected_keys(eng, orc, nq):
     assert bits_equal(lg, lo), maxdiff(lg, lo)
     greedy(p, lg, lo, 4097, 3, f"q8 4096 G{nq // 8}")
     p.close()
+
+
+@pytest.mark.parametrize("nq,nkv,kv_type", [(8, 2, 0), (4, 2, 0), (16, 2, 0), (8, 2, 1), (4, 2, 1)])
+def test_one_token_last_positions_unaligned_max_seq(eng, orc, nq, nkv, kv_type):
+    """An engine created for 1029 positions (not a multiple of 4) decoding its
+    last three positions, 1026 .. 1028, after 1026 injected keys, for groups
+    of 4, 2 and 8 over the fp32 cache and groups of 4 and 2 over the int8
+    cache: the one-token kernels read the probability rows' last keys one by
+    one there (a 16-byte piece would run past the row), so the logits stay
+    bit-identical up to the context's end."""
+    shape = dict(TINY, num_layers=2, num_q_heads=nq, num_kv_heads=nkv, head_dim=128)
+    m, cfg = q8_model(shape, 1029, 301)
+    cfg.kv_type = kv_type
+    p = Q8Pair(eng, orc, m, cfg)
+    rng = np.random.default_rng(302)
+    for layer in range(2):
+        for kvh in range(nkv):
+            p.set_kv(layer, kvh, 0, rng.standard_normal((1026, 128), dtype=np.float32),
+                     rng.standard_normal((1026, 128), dtype=np.float32))
+    log(f"max_seq 1029, groups of {nq // nkv}, kv_type {kv_type}: positions 1026 .. 1028")
+    lg, lo = p.forward(np.array([9], np.int32), 1026)
+    assert bits_equal(lg, lo), maxdiff(lg, lo)
+    greedy(p, lg, lo, 1027, 2, f"unaligned max_seq G{nq // nkv} kv{kv_type}")
+    p.close()
