@@ -71,9 +71,13 @@ typedef struct {
     int32_t serial;
     void* d_red; /* partials of the device argmax / top-2 reductions */
     /* one token per session (dpuf_amd_engine_forward_slots): while ms_n > 0
-     * the layers run the ms_n tokens through the fused decode attention, token
-     * m at position d_ms_pos[m] with the KV cache at d_ms_kc[m] / d_ms_vc[m] */
-    int32_t ms_n;
+     * the layers run ms_n tokens, token m of slot ms_slot[m] at position
+     * ms_pos[m] (device copy d_ms_pos); the first ms_short of them (fp32
+     * cache, at most DPUF_HIP_DEC_MAX_KEYS keys) through one fused decode
+     * attention launch with the KV caches at d_ms_kc[m] / d_ms_vc[m], every
+     * other one through the one-token attention launches of its own slot */
+    int32_t ms_n, ms_short;
+    int32_t ms_slot[DPUF_AMD_MAX_BATCH], ms_pos[DPUF_AMD_MAX_BATCH];
     int32_t *d_ms_pos, *d_ms_tok;
     float **d_ms_kc, **d_ms_vc;
     int32_t* h_pinned;   /* host staging: [3] error word of the GEMV bench */
@@ -840,10 +844,57 @@ static DpufWarm attn_warm(Engine* e, const LayerJobs* lj, const LayerJobs* ln) {
     return w;
 }
 
+/* Attention of a multi-session step at layer l (ms_n = M tokens, one per
+ * session): the first ms_short tokens (fp32 cache, short context) in one
+ * fused decode launch over their sessions' caches; every other token alone,
+ * at its own position against its own slot's cache, through the one-token
+ * kernels a single-session step of that length takes (dpuf_engine.c:1404-1600
+ * serves each slot's sequence the same way); then, when any token took the
+ * latter, the O-input prep of all M rows (the fused kernel's rows prep to the
+ * same values). */
+static void enqueue_ms_attention(Engine* e, int32_t l, int32_t M, float eps, float scale, const uint8_t* o_sign) {
+    void* s = e->stream;
+    const DpufWarm no_warm = {0};
+    const size_t lo = (size_t)l * e->nkv * e->max_seq * e->hd;
+    const int32_t ns = e->ms_short;
+    const float *qn = e->d_norm[4 * l + 1], *kn = e->d_norm[4 * l + 2];
+    if (ns > 0)
+        dpuf_hip_attn_dec(s, ns, e->q, e->k, e->v, qn, kn, eps, e->d_cos, e->d_sin, NULL, NULL, e->d_ms_pos, e->nq,
+                          e->nkv, e->hd, e->max_seq, scale, e->ao, o_sign, e->prep[0], e->d_ms_kc, e->d_ms_vc, lo,
+                          no_warm);
+    for (int32_t m = ns; m < M; m++) {
+        float* q = e->q + (size_t)m * e->qd;
+        float* k = e->k + (size_t)m * e->kvd;
+        float* v = e->v + (size_t)m * e->kvd;
+        float* ao = e->ao + (size_t)m * e->qd;
+        const int32_t* pp = e->d_ms_pos + m;
+        const int32_t keys = e->ms_pos[m] + 1;
+        if (is_q8(e)) {
+            const DpufKvQ8 c8 = slot_q8(e, e->ms_slot[m], l);
+            dpuf_hip_qk_rope_kv(s, 1, q, k, v, qn, kn, eps, e->d_cos, e->d_sin, NULL, NULL, pp, e->nq, e->nkv, e->hd,
+                                e->max_seq, &c8);
+            dpuf_hip_attn_q8(s, 1, keys, q, c8, ao, e->scores, pp, e->nq, e->nkv, e->hd, e->max_seq, scale);
+            continue;
+        }
+        float* kc = slot_k(e, e->ms_slot[m]) + lo;
+        float* vc = slot_v(e, e->ms_slot[m]) + lo;
+        if (dpuf_hip_attn_decode_rope(s, keys, q, k, v, qn, kn, eps, e->d_cos, e->d_sin, kc, vc, ao, e->scores, pp,
+                                      e->nq, e->nkv, e->hd, e->max_seq, scale) == 0)
+            continue;
+        dpuf_hip_qk_rope_kv(s, 1, q, k, v, qn, kn, eps, e->d_cos, e->d_sin, kc, vc, pp, e->nq, e->nkv, e->hd,
+                            e->max_seq, NULL);
+        DpufPrep none;
+        memset(&none, 0, sizeof none);
+        if (dpuf_hip_attn_split(s, 1, keys, q, kc, vc, ao, e->scores, pp, e->nq, e->nkv, e->hd, e->max_seq, scale,
+                                NULL, none, NULL) != 0)
+            dpuf_hip_attn(s, 1, q, kc, vc, ao, e->scores, pp, e->nq, e->nkv, e->hd, e->max_seq, scale);
+    }
+    if (ns < M) dpuf_hip_prep(s, M, e->qd, e->ao, o_sign, e->prep[0]);
+}
+
 static void enqueue_layers(Engine* e, int32_t M, int32_t keep_tiles) {
     void* s = e->stream;
     const int32_t H = e->H, I = e->I;
-    const DpufWarm no_warm = {0};
     const float eps = e->cfg.rms_eps;
     const float scale = 1.0f / sqrtf((float)e->hd);
     for (int32_t l = 0; l < e->L; l++) {
@@ -892,7 +943,11 @@ static void enqueue_layers(Engine* e, int32_t M, int32_t keep_tiles) {
         {
             const int tm = tm_begin(e, K_ATTN, 0);
             int fused = 0;
-            if (is_q8(e)) {
+            if (e->ms_n > 0) {
+                /* one token per session, each against its own slot's cache */
+                enqueue_ms_attention(e, l, M, eps, scale, W[W_O].sign);
+                fused = 1;
+            } else if (is_q8(e)) {
                 /* int8 KV cache: QK-norm + RoPE + quantising store, then the
                  * int8-cache attention (dpuf_engine.c:1800-1806, 595-752) */
                 const DpufKvQ8 c8 = slot_q8(e, e->active, l);
@@ -903,12 +958,7 @@ static void enqueue_layers(Engine* e, int32_t M, int32_t keep_tiles) {
                 if (M > 1) dpuf_hip_prep(s, M, e->qd, e->ao, W[W_O].sign, e->prep[0]);
                 o_prep = M == 1;
                 fused = 1;
-            } else if (e->ms_n > 0)  /* one token per session, each with its own cache */
-                fused = dpuf_hip_attn_dec(s, M, e->q, e->k, e->v, e->d_norm[4 * l + 1], e->d_norm[4 * l + 2], eps,
-                                          e->d_cos, e->d_sin, NULL, NULL, e->d_ms_pos, e->nq, e->nkv, e->hd,
-                                          e->max_seq, scale, e->ao, W[W_O].sign, e->prep[0], e->d_ms_kc,
-                                          e->d_ms_vc, (size_t)l * e->nkv * e->max_seq * e->hd, no_warm) == 0;
-            else if (M == 1 && e->host_pos0 + 1 <= ATT_SPLIT_MIN)
+            } else if (M == 1 && e->host_pos0 + 1 <= ATT_SPLIT_MIN)
                 fused = dpuf_hip_attn_dec(s, 1, e->q, e->k, e->v, e->d_norm[4 * l + 1], e->d_norm[4 * l + 2], eps,
                                           e->d_cos, e->d_sin, kc, vc, e->d_pos0, e->nq, e->nkv, e->hd, e->max_seq,
                                           scale, e->ao, W[W_O].sign, e->prep[0], NULL, NULL, 0,
@@ -1176,47 +1226,84 @@ DPUF_EXPORT int32_t dpuf_amd_engine_forward_slots(void* handle, int32_t n, const
     if (!e || n <= 0 || !slot_ids || !token_ids || !positions || (!logits_out && !tokens_out)) return -1;
     if (n > DPUF_AMD_MAX_BATCH) return -2;
     if (e->hd != 64 && e->hd != 128 && e->hd != 256) return -5;
-    if (is_q8(e)) return -5; /* the one-token-per-session attention reads the fp32 cache */
     for (int32_t i = 0; i < n; i++) {
         if (slot_ids[i] < 0 || slot_ids[i] >= N_SLOTS) return -1;
         for (int32_t j = 0; j < i; j++)
             if (slot_ids[j] == slot_ids[i]) return -1;
-        if (positions[i] < 0 || positions[i] + 1 > e->max_seq || positions[i] + 1 > ATT_SPLIT_MIN) return -3;
+        if (positions[i] < 0 || positions[i] + 1 > e->max_seq) return -3;
         if (token_ids[i] < 0 || token_ids[i] >= e->V) return -4;
         if (!slot_alloc(e, slot_ids[i])) return -2;
     }
+    /* batch order: sessions the fused decode attention serves (fp32 cache,
+     * at most DPUF_HIP_DEC_MAX_KEYS keys) first, the others after them;
+     * ord[m] is the caller's index of batch row m */
+    int32_t* ord = (int32_t*)malloc((size_t)n * sizeof(int32_t));
     float** ptrs = (float**)malloc((size_t)n * 2 * sizeof(float*));
-    if (!ptrs) return -2;
-    begin_call(e);
-    for (int32_t i = 0; i < n; i++) {
-        ptrs[i] = slot_k(e, slot_ids[i]);
-        ptrs[n + i] = slot_v(e, slot_ids[i]);
+    int32_t* pos = (int32_t*)malloc((size_t)n * sizeof(int32_t));
+    float* lg = logits_out ? (float*)malloc((size_t)n * e->V * sizeof(float)) : NULL;
+    int32_t* tk = tokens_out ? (int32_t*)malloc((size_t)n * sizeof(int32_t)) : NULL;
+    if (!ord || !ptrs || !pos || (logits_out && !lg) || (tokens_out && !tk)) {
+        free(ord);
+        free(ptrs);
+        free(pos);
+        free(lg);
+        free(tk);
+        return -2;
     }
+    int32_t ns = 0;
+    for (int32_t pass = 0; pass < 2; pass++)
+        for (int32_t i = 0; i < n; i++) {
+            const int shrt = !is_q8(e) && positions[i] + 1 <= ATT_SPLIT_MIN;
+            if (shrt == (pass == 0)) ord[ns++] = i;
+        }
+    ns = 0;
+    while (ns < n && !is_q8(e) && positions[ord[ns]] + 1 <= ATT_SPLIT_MIN) ns++;
+    begin_call(e);
     volatile int32_t* io = e->h_io;
-    for (int32_t i = 0; i < n; i++) io[i] = token_ids[i];
+    for (int32_t m = 0; m < n; m++) {
+        const int32_t i = ord[m];
+        ptrs[m] = is_q8(e) ? NULL : slot_k(e, slot_ids[i]);
+        ptrs[n + m] = is_q8(e) ? NULL : slot_v(e, slot_ids[i]);
+        pos[m] = positions[i];
+        e->ms_slot[m] = slot_ids[i];
+        e->ms_pos[m] = positions[i];
+        io[m] = token_ids[i];
+    }
     io[IO_POS] = 0;
     io[IO_POS + 1] = next_serial(e);
-    dpuf_hip_h2d(e->d_ms_pos, positions, (size_t)n * 4, e->stream);
+    dpuf_hip_h2d(e->d_ms_pos, pos, (size_t)n * 4, e->stream);
     dpuf_hip_h2d(e->d_ms_kc, ptrs, (size_t)n * sizeof(float*), e->stream);
     dpuf_hip_h2d(e->d_ms_vc, ptrs + n, (size_t)n * sizeof(float*), e->stream);
     int32_t keep = 0;
     env_int("DPUF_GEN_KEEP_TILES", &keep);
     e->ms_n = n;
+    e->ms_short = ns;
     e->capturing = 0;
     const int tm = tm_begin(e, K_CALL, (double)e->weight_bytes);
     enqueue_forward(e, n, 0, 0, keep, 0, 1.25f, 0, NULL);
     e->ms_n = 0;
+    e->ms_short = 0;
     if (tokens_out)
-        for (int32_t i = 0; i < n; i++)
-            dpuf_hip_argmax(e->stream, e->logits + (size_t)i * e->V, e->V, e->d_ms_tok + i, e->d_red);
+        for (int32_t m = 0; m < n; m++)
+            dpuf_hip_argmax(e->stream, e->logits + (size_t)m * e->V, e->V, e->d_ms_tok + m, e->d_red);
     tm_end(e, tm);
-    if (logits_out) dpuf_hip_d2h(logits_out, e->logits, (size_t)n * e->V * 4, e->stream);
-    if (tokens_out) dpuf_hip_d2h(tokens_out, e->d_ms_tok, (size_t)n * 4, e->stream);
+    if (logits_out) dpuf_hip_d2h(lg, e->logits, (size_t)n * e->V * 4, e->stream);
+    if (tokens_out) dpuf_hip_d2h(tk, e->d_ms_tok, (size_t)n * 4, e->stream);
     const int32_t rc = dpuf_hip_sync(e->stream);
-    free(ptrs);
     tm_collect(e);
-    if (rc != 0) return -6;
-    return end_call(e, io[IO_OUT + 2]);
+    int32_t out = rc != 0 ? -6 : end_call(e, io[IO_OUT + 2]);
+    if (out == 0) {
+        for (int32_t m = 0; m < n; m++) {
+            if (logits_out) memcpy(logits_out + (size_t)ord[m] * e->V, lg + (size_t)m * e->V, (size_t)e->V * 4);
+            if (tokens_out) tokens_out[ord[m]] = tk[m];
+        }
+    }
+    free(ord);
+    free(ptrs);
+    free(pos);
+    free(lg);
+    free(tk);
+    return out;
 }
 
 DPUF_EXPORT int32_t dpuf_amd_engine_forward_argmax(void* handle, int32_t n_tokens, const int32_t* token_ids,

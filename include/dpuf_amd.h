@@ -125,12 +125,16 @@ DPUF_EXPORT int32_t dpuf_amd_reduce_check_noalloc(const float* d_x, int32_t n, i
 /* One next token for each of n sessions in one pass (serving several
  * conversations with one read of the weights): token_ids[i] is appended to
  * KV slot slot_ids[i] (distinct slots, allocated on demand) at positions[i]
- * (positions[i] < 192); logits_out [n][V] and/or tokens_out [n] (greedy ids).
- * Per token the results equal a one-token dpuf_engine_forward_batch on that
- * slot (decode keep-tiles setting, no Zone-A early exit).  0 on success; -1
- * bad arguments or a repeated slot, -2 above DPUF_AMD_MAX_BATCH or out of
- * memory, -3 position out of range, -4 token id out of range, -5 head dim
- * other than 64/128/256, -6 device error.  No counterpart in the reference,
+ * (any position below max_seq_len, for either KV cache type); logits_out
+ * [n][V] and/or tokens_out [n] (greedy ids), in the caller's order.  Per token
+ * the results equal a one-token dpuf_engine_forward_batch on that slot (decode
+ * keep-tiles setting, no Zone-A early exit).  The projections and the LM head
+ * run once for all n tokens; the attention of sessions with at most 192 keys
+ * (fp32 cache) is one launch, every other session's takes the one-token
+ * launches of its own length.  0 on success; -1 bad arguments or a repeated
+ * slot, -2 above DPUF_AMD_MAX_BATCH or out of memory, -3 position out of
+ * range, -4 token id out of range, -5 head dim other than 64/128/256, -6
+ * device error.  No counterpart in the reference,
  * whose forward serves one slot per call; for serving loops (dpuf-cli.c's
  * one-slot-per-call generation stays as it is). */
 DPUF_EXPORT int32_t dpuf_amd_engine_forward_slots(void* handle, int32_t n, const int32_t* slot_ids,

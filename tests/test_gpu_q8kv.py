@@ -95,8 +95,8 @@ def test_q8_injected_context_and_graph(eng, orc):
 
 def test_q8_prefix_slots_and_refusals(eng, orc):
     """Prefix freeze / apply / reset and a second slot with the int8 cache,
-    in lockstep with the oracle; the multi-session entry refuses an int8
-    cache (-5)."""
+    in lockstep with the oracle; then one multi-session step on the int8
+    cache, its greedy id equal to the oracle's."""
     m, cfg = q8_model(TINY, 64, 221)
     p = Q8Pair(eng, orc, m, cfg)
     ids = np.random.default_rng(222).integers(0, 4096, 12).astype(np.int32)
@@ -112,10 +112,15 @@ def test_q8_prefix_slots_and_refusals(eng, orc):
     orc.orc_engine_reset_slot(p.o, 4)
     lr, lor = p.forward(ids[8:], 8, only_last=0)
     assert bits_equal(lr, lor)
+    # the multi-session entry serves the int8 cache too: slot 4 at position 12
     got = np.zeros(1, np.int32)
     rc = eng.dpuf_amd_engine_forward_slots(p.g, 1, M.ptr(np.array([4], np.int32)), M.ptr(np.array([5], np.int32)),
                                           M.ptr(np.array([12], np.int32)), None, M.ptr(got))
-    assert rc == -5
+    assert rc == 0, (rc, eng.dpuf_amd_last_error())
+    assert orc.orc_engine_set_slot(p.o, 4) == 0
+    lo = np.zeros(p.V, np.float32)
+    assert orc.orc_engine_forward(p.o, 1, M.ptr(np.array([5], np.int32)), 12, None, 1, M.ptr(lo)) == 0
+    assert got[0] == orc.orc_argmax(M.ptr(lo), p.V)
     p.close()
 
 
@@ -181,4 +186,55 @@ def test_one_token_last_positions_unaligned_max_seq(eng, orc, nq, nkv, kv_type):
     lg, lo = p.forward(np.array([9], np.int32), 1026)
     assert bits_equal(lg, lo), maxdiff(lg, lo)
     greedy(p, lg, lo, 1027, 2, f"unaligned max_seq G{nq // nkv} kv{kv_type}")
+    p.close()
+
+
+@pytest.mark.parametrize("kv_type", [0, 1])
+def test_multi_session_mixed_lengths(eng, orc, kv_type):
+    """dpuf_amd_engine_forward_slots serving sessions of very different
+    lengths in one pass, over the fp32 (kv_type 0) and int8 (kv_type 1)
+    caches, at the Qwen3-8B attention geometry (groups of 4, head_dim 128):
+    four sessions, one past 4096 keys (injected), one at 300, two short ones
+    prefilled normally, passed in an order that mixes them; 3 steps, every row
+    bit-identical to the oracle decoding that slot alone, ids too."""
+    shape = dict(TINY, num_layers=2, num_q_heads=8, num_kv_heads=2, head_dim=128)
+    m, cfg = q8_model(shape, 4200, 401)
+    cfg.kv_type = kv_type
+    p = Q8Pair(eng, orc, m, cfg)
+    rng = np.random.default_rng(402)
+    slots = np.array([5, 1, 6, 3], np.int32)
+    lens = {5: 4100, 1: 9, 6: 300, 3: 40}
+    toks, pos = [], []
+    for s in slots:
+        s = int(s)
+        p.set_slot(s)
+        n = lens[s]
+        if n > 64:
+            # an injected context, then one token through the normal path
+            for layer in range(2):
+                for kvh in range(2):
+                    p.set_kv(layer, kvh, 0, rng.standard_normal((n - 1, 128), dtype=np.float32),
+                             rng.standard_normal((n - 1, 128), dtype=np.float32))
+            lg, lo = p.forward(np.array([int(rng.integers(0, 4096))], np.int32), n - 1)
+        else:
+            lg, lo = p.forward(rng.integers(0, 4096, n).astype(np.int32), 0)
+        assert bits_equal(lg, lo), (s, maxdiff(lg, lo))
+        toks.append(int(np.argmax(lo[-1])))
+        pos.append(n)
+    for step in range(3):
+        log(f"mixed-length multi-session step {step}, kv_type {kv_type}, positions {pos}")
+        lg = np.zeros((4, 4096), np.float32)
+        got = np.full(4, -1, np.int32)
+        rc = eng.dpuf_amd_engine_forward_slots(p.g, 4, M.ptr(slots), M.ptr(np.array(toks, np.int32)),
+                                              M.ptr(np.array(pos, np.int32)), M.ptr(lg), M.ptr(got))
+        assert rc == 0, (rc, eng.dpuf_amd_last_error())
+        for i, s in enumerate(slots):
+            assert orc.orc_engine_set_slot(p.o, int(s)) == 0
+            lo = np.zeros(4096, np.float32)
+            assert orc.orc_engine_forward(p.o, 1, M.ptr(np.array([toks[i]], np.int32)), pos[i], None, 1,
+                                          M.ptr(lo)) == 0
+            assert bits_equal(lg[i], lo), (step, i, maxdiff(lg[i], lo))
+            assert got[i] == orc.orc_argmax(M.ptr(lo), 4096)
+            toks[i] = int(got[i])
+            pos[i] += 1
     p.close()
