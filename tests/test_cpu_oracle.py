@@ -448,3 +448,42 @@ def test_top2_exit(orc):
             assert orc.orc_top2_exit(M.ptr(x), n, thr) == int(thr > 0 and margin >= np.float32(thr))
             xp = rng.permutation(x)
             assert orc.orc_top2_exit(M.ptr(xp), n, thr) == orc.orc_top2_exit(M.ptr(x), n, thr)
+
+
+def test_llama3_rope_scaling_table_float64(orc):
+    """The oracle's Llama-3 RoPE scaling (dpuf_engine.c:194-208) against the
+    published rule evaluated in float64: per frequency f = theta^(-2j/hd),
+    wavelength w = 2 pi / f; w > orig / low: f / factor; w < orig / high: f;
+    between: (1 - s) f / factor + s f with s = (orig / w - low) / (high - low).
+    Llama-3.1's settings (theta 5e5, factor 8, low 1, high 4, orig 8192) put
+    frequencies in all three regions at head_dim 128; positions up to 4095.
+    A dropped factor, swapped thresholds or the smooth weight on the wrong
+    term moves angles by far more than the float32 tolerance used here."""
+    hd, seq = 128, 4096
+    cfg = M.abi.DpufModelConfig()
+    cfg.head_dim, cfg.max_seq_len, cfg.rope_theta = hd, seq, 5e5
+    cfg.use_llama3_rope, cfg.rope_factor, cfg.rope_low_freq, cfg.rope_high_freq = 1, 8.0, 1.0, 4.0
+    cfg.rope_orig_max_pos = 8192
+    ct = np.zeros(seq * hd // 2, np.float32)
+    st = np.zeros(seq * hd // 2, np.float32)
+    orc.orc_rope_tables(C.byref(cfg), M.ptr(ct), M.ptr(st))
+    ct, st = ct.reshape(seq, hd // 2), st.reshape(seq, hd // 2)
+    j = np.arange(hd // 2, dtype=np.float64)
+    f = 5e5 ** (-2.0 * j / hd)
+    w = 2.0 * np.pi / f
+    orig, low, high, factor = 8192.0, 1.0, 4.0, 8.0
+    s = (orig / w - low) / (high - low)
+    g = np.where(w > orig / low, f / factor, np.where(w < orig / high, f, (1.0 - s) * f / factor + s * f))
+    regions = (w > orig / low).sum(), (w < orig / high).sum()
+    assert regions[0] > 0 and regions[1] > 0 and regions[0] + regions[1] < hd // 2  # all three regions occur
+    p = np.arange(seq, dtype=np.float64)[:, None]
+    # float32 angles p * f carry a relative error of a few ulp: tolerance grows with the angle
+    tol = 1e-6 + 4e-7 * p * g[None, :]
+    assert np.all(np.abs(ct - np.cos(p * g)) <= tol)
+    assert np.all(np.abs(st - np.sin(p * g)) <= tol)
+    # the unscaled table differs where the rule rescales (the test sees the branch)
+    cfg.use_llama3_rope = 0
+    cu = np.zeros(seq * hd // 2, np.float32)
+    su = np.zeros(seq * hd // 2, np.float32)
+    orc.orc_rope_tables(C.byref(cfg), M.ptr(cu), M.ptr(su))
+    assert np.max(np.abs(su.reshape(seq, hd // 2) - st)) > 0.1
