@@ -600,20 +600,23 @@ static void build_norm(DpufToolsModel* m, const char* name, int32_t n) {
     add_blob(m, name, b, len, 1);
 }
 
-/* RAW_TINY -> fp32 heap copy (dpuf-cli.c:1622-1644). */
-static float* bind_norm(DpufToolsModel* m, const char* name) {
+/* RAW_TINY -> fp32 heap copy (dpuf-cli.c:1622-1644); NULL unless it holds
+ * exactly `want` values (the consumers read that many). */
+static float* bind_norm(DpufToolsModel* m, const char* name, int32_t want) {
     const NamedBlob* b = find_blob(m, name);
-    if (!b || b->len < 10 || b->data[0] != 0) return NULL;
+    if (!b || b->len < 10 || b->data[0] != 0 || want <= 0) return NULL;
     uint32_t d0, d1;
     memcpy(&d0, b->data + 2, 4);
     memcpy(&d1, b->data + 6, 4);
     size_t raw = b->len - 10u;
     if (d1 == 2 && raw == (size_t)d0 * 4u) {
+        if (d0 != (uint32_t)want) return NULL;
         float* f = own_floats(m, d0);
         memcpy(f, b->data + 10, raw);
         return f;
     }
     size_t n = raw / 2u;
+    if (n != (size_t)want) return NULL;
     float* f = own_floats(m, n);
     for (size_t i = 0; i < n; i++) {
         uint16_t x;
@@ -625,9 +628,103 @@ static float* bind_norm(DpufToolsModel* m, const char* name) {
 
 static int verify_and_heal(DpufToolsModel* m, NamedBlob* nb);
 
+/* Rows of tile t of a matrix of `rows` rows (16 per tile, the last one the
+ * remainder) and the body bytes a mode 12 / 13 / 14 tile of n_r rows holds
+ * after its 16-byte header. */
+static uint32_t tile_rows(uint32_t rows, uint32_t t) { return rows - 16u * t < 16u ? rows - 16u * t : 16u; }
+static uint64_t tile_body(uint8_t mode, uint32_t n_r, uint32_t cols) {
+    const uint64_t n_8g = (n_r + 7u) / 8u;
+    return mode == DPUF_MODE_QR_HAD4_PACKED ? n_8g * (cols / 32u) * 144u
+         : mode == DPUF_MODE_QR_HAD4_ASYM   ? n_8g * (cols / 64u) * 288u
+                                            : n_8g * (cols / 64u) * 416u;
+}
+
+/* The structure of a QR blob against its length, before anything reads
+ * through its tables (a file's bytes are untrusted: a damaged count or offset
+ * is refused, never followed): mode 12 / 13 / 14, the row / column / tile /
+ * ECC-group counts consistent, the tile and ECC offset tables, the sign bytes,
+ * the tile region and the ECC region inside the blob, every tile long enough
+ * for the body its place in the matrix holds, every ECC block as long as the
+ * longest tile of its group.  Tile headers are not checked here: a damaged
+ * header is a bad tile for the verify / heal step. */
+static int qr_blob_ok(const uint8_t* b, size_t len) {
+    if (!b || len < 64 || memcmp(b + 1, "QRDP", 4) != 0) return 0;
+    const uint8_t mode = b[0];
+    if (mode != DPUF_MODE_QR_HAD4_PACKED && mode != DPUF_MODE_QR_HAD4_ASYM && mode != DPUF_MODE_QR_HAD6) return 0;
+    uint16_t G;
+    uint32_t rows, cols, n_tiles, n_ecc;
+    uint64_t aux_off, tiles_off, ecc_off;
+    memcpy(&G, b + 6, 2);
+    memcpy(&rows, b + 8, 4);
+    memcpy(&cols, b + 12, 4);
+    memcpy(&n_tiles, b + 16, 4);
+    memcpy(&n_ecc, b + 20, 4);
+    memcpy(&aux_off, b + 24, 8);
+    memcpy(&tiles_off, b + 32, 8);
+    memcpy(&ecc_off, b + 40, 8);
+    if (rows == 0 || rows > (1u << 26) || cols == 0 || cols > (1u << 20) || cols % 64u) return 0;
+    if (n_tiles != (rows + 15u) / 16u) return 0;
+    if (G ? n_ecc != (n_tiles + G - 1u) / G : n_ecc != 0) return 0;
+    const uint64_t tables = 64u + ((uint64_t)n_tiles + 1u) * 8u + ((uint64_t)n_ecc + 1u) * 8u;
+    if (tables > len || aux_off > len || cols / 8u > len - aux_off) return 0;
+    if (tiles_off > ecc_off || ecc_off > len) return 0;
+    const uint8_t* to = b + 64;
+    const uint8_t* eo = b + 64 + ((size_t)n_tiles + 1u) * 8u;
+    uint64_t prev = 0;
+    for (uint32_t t = 0; t <= n_tiles; t++) {
+        uint64_t o;
+        memcpy(&o, to + (size_t)t * 8u, 8);
+        if (o < prev || o > ecc_off - tiles_off) return 0;
+        if (t > 0 && o - prev < 16u + tile_body(mode, tile_rows(rows, t - 1u), cols)) return 0;
+        prev = o;
+    }
+    uint64_t eprev = 0;
+    for (uint32_t g = 0; g <= n_ecc; g++) {
+        uint64_t o;
+        memcpy(&o, eo + (size_t)g * 8u, 8);
+        if (o < eprev || o > len - ecc_off) return 0;
+        if (g > 0) {
+            const uint32_t g0 = (g - 1u) * G, g1 = g0 + G < n_tiles ? g0 + G : n_tiles;
+            for (uint32_t t = g0; t < g1; t++) {
+                uint64_t a, z;
+                memcpy(&a, to + (size_t)t * 8u, 8);
+                memcpy(&z, to + ((size_t)t + 1u) * 8u, 8);
+                if (z - a > o - eprev) return 0;
+            }
+        }
+        eprev = o;
+    }
+    return 1;
+}
+
+/* dpuf_qr_verify_tiles_ex over the tiles of a blob that passed qr_blob_ok:
+ * a tile whose header claims another row count than its place in the matrix
+ * holds is bad without a CRC (the CRC length comes from the header, and
+ * would run past the tile); the others are checked as usual.  Returns the
+ * number of bad tiles, ok[t] per tile. */
+static int32_t verify_tiles_bounded(uint8_t mode, uint32_t rows, uint32_t cols, uint32_t n_tiles,
+                                    const uint8_t* tiles, const uint64_t* t_offs, uint8_t* ok) {
+    int sane = 1;
+    for (uint32_t t = 0; t < n_tiles && sane; t++) {
+        DpufQrTileHdr h;
+        memcpy(&h, tiles + t_offs[t], sizeof h);
+        sane = h.n_rows == tile_rows(rows, t);
+    }
+    if (sane) return dpuf_qr_verify_tiles_ex(mode, (int32_t)n_tiles, (int32_t)cols, tiles, t_offs, ok);
+    int32_t bad = 0;
+    for (uint32_t t = 0; t < n_tiles; t++) {
+        DpufQrTileHdr h;
+        memcpy(&h, tiles + t_offs[t], sizeof h);
+        if (h.n_rows != tile_rows(rows, t)) ok[t] = 0;
+        else dpuf_qr_verify_tiles_ex(mode, 1, (int32_t)cols, tiles, t_offs + t, ok + t);
+        bad += ok[t] ? 0 : 1;
+    }
+    return bad;
+}
+
 static int bind_weight(DpufToolsModel* m, const char* name, int verify, DpufWeightDesc* out) {
     NamedBlob* b = (NamedBlob*)find_blob(m, name);
-    if (!b) return 0;
+    if (!b || !qr_blob_ok(b->data, b->len)) return 0;
     if (verify && !verify_and_heal(m, b)) return 0;
     return dpuf_tools_bind_blob(b->data, b->len, out) == 0;
 }
@@ -639,25 +736,33 @@ static int bind_all(DpufToolsModel* m, int verify) {
     } else {
         m->lm = m->tok;
     }
-    m->out_norm = bind_norm(m, "output_norm.weight");
+    /* every tensor has the shape the configuration gives it: consumers index
+     * them by the configuration alone */
+    const DpufModelConfig* c = &m->cfg;
+    const int32_t H = c->hidden_size, hd = c->head_dim, qd = c->num_q_heads * hd, kvd = c->num_kv_heads * hd;
+    if (m->tok.rows != c->vocab_size || m->tok.cols != H || m->lm.rows != c->vocab_size || m->lm.cols != H) return 0;
+    m->out_norm = bind_norm(m, "output_norm.weight", H);
     if (!m->out_norm) return 0;
     m->layers = (DpufLayerWeights*)calloc((size_t)(m->cfg.num_layers > 0 ? m->cfg.num_layers : 1), sizeof(DpufLayerWeights));
     char n[96];
     static const char* mats[7] = {"attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down"};
     for (int32_t l = 0; l < m->cfg.num_layers; l++) {
         DpufLayerWeights* lw = &m->layers[l];
-        snprintf(n, sizeof n, "blk.%d.attn_norm.weight", l); lw->attn_norm = bind_norm(m, n);
-        snprintf(n, sizeof n, "blk.%d.ffn_norm.weight", l); lw->ffn_norm = bind_norm(m, n);
+        snprintf(n, sizeof n, "blk.%d.attn_norm.weight", l); lw->attn_norm = bind_norm(m, n, H);
+        snprintf(n, sizeof n, "blk.%d.ffn_norm.weight", l); lw->ffn_norm = bind_norm(m, n, H);
         if (!lw->attn_norm || !lw->ffn_norm) return 0;
         if (m->cfg.has_qk_norm) {
-            snprintf(n, sizeof n, "blk.%d.attn_q_norm.weight", l); lw->attn_q_norm = bind_norm(m, n);
-            snprintf(n, sizeof n, "blk.%d.attn_k_norm.weight", l); lw->attn_k_norm = bind_norm(m, n);
+            snprintf(n, sizeof n, "blk.%d.attn_q_norm.weight", l); lw->attn_q_norm = bind_norm(m, n, hd);
+            snprintf(n, sizeof n, "blk.%d.attn_k_norm.weight", l); lw->attn_k_norm = bind_norm(m, n, hd);
             if (!lw->attn_q_norm || !lw->attn_k_norm) return 0;
         }
         DpufWeightDesc* ds[7] = {&lw->w_q, &lw->w_k, &lw->w_v, &lw->w_o, &lw->w_gate, &lw->w_up, &lw->w_down};
+        const int32_t want_r[7] = {qd, kvd, kvd, H, c->intermediate_size, c->intermediate_size, H};
+        const int32_t want_c[7] = {H, H, H, qd, H, H, c->intermediate_size};
         for (int k = 0; k < 7; k++) {
             snprintf(n, sizeof n, "blk.%d.%s.weight", l, mats[k]);
             if (!bind_weight(m, n, verify, ds[k])) return 0;
+            if (ds[k]->rows != want_r[k] || ds[k]->cols != want_c[k]) return 0;
         }
     }
     return 1;
@@ -938,10 +1043,12 @@ static int verify_and_heal(DpufToolsModel* m, NamedBlob* nb) {
     memcpy(&n_ecc, blob + 20, 4);
     memcpy(&tiles_off, blob + 32, 8);
     memcpy(&ecc_off, blob + 40, 8);
+    uint32_t rows;
+    memcpy(&rows, blob + 8, 4);
     const uint64_t* t_offs = (const uint64_t*)(blob + 64);
     const uint64_t* e_offs = (const uint64_t*)(blob + 64 + ((size_t)n_tiles + 1) * 8u);
     uint8_t* ok = (uint8_t*)malloc(n_tiles ? n_tiles : 1);
-    int32_t bad = dpuf_qr_verify_tiles_ex(blob[0], (int32_t)n_tiles, (int32_t)cols, blob + tiles_off, t_offs, ok);
+    int32_t bad = verify_tiles_bounded(blob[0], rows, cols, n_tiles, blob + tiles_off, t_offs, ok);
     if (bad == 0) { free(ok); return 1; }
     if (G == 0) { free(ok); return 0; }
     uint8_t* rw = (uint8_t*)malloc(nb->len);
@@ -972,7 +1079,7 @@ static int verify_and_heal(DpufToolsModel* m, NamedBlob* nb) {
         }
         m->healed++;
     }
-    int32_t bad2 = dpuf_qr_verify_tiles_ex(blob[0], (int32_t)n_tiles, (int32_t)cols, wt, t_offs, ok);
+    int32_t bad2 = verify_tiles_bounded(blob[0], rows, cols, n_tiles, wt, t_offs, ok);
     free(ok);
     if (bad2 > 0) { free(rw); return 0; }
     nb->data = rw;
