@@ -50,13 +50,17 @@ TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "qwen3_8b_gate_up_gemv_roofline
 
 
 def measured_traffic():
+    """(bytes per launch, commit the counters were measured on) from the profile."""
+    by, commit = None, None
     try:
         for line in open(TRAFFIC_PROFILE):
             if line.startswith("traffic_bytes_per_launch:"):
-                return float(line.split(":")[1])
+                by = float(line.split(":")[1])
+            elif line.startswith("traffic_commit:"):
+                commit = line.split(":")[1].strip()
     except OSError:
         pass
-    return None
+    return by, commit
 
 
 KINDS = ["gate_up_gemv", "down_gemv", "qkv_gemv", "o_gemv", "lm_head", "attention", "norm_prep", "call"]
@@ -214,7 +218,8 @@ def main():
             f"{by.value / 1e6:.2f} MB -> {ach:.0f} GB/s")
         return {"kernel": "k_mv (fused gate+up GEMV, M=1)", "bound": "hbm", "achieved": round(ach, 1),
                 "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
-                "traffic": measured_traffic() if args.model == "8b" else None,
+                "traffic": measured_traffic()[0] if args.model == "8b" else None,
+                "traffic_commit": measured_traffic()[1] if args.model == "8b" else None,
                 "bytes_per_launch": by.value, "us_per_launch": round(ms * 1e3, 3), "launches": iters}
 
     if args.roofline_only:
@@ -264,6 +269,16 @@ def main():
         gpu_greedy += extra
     ms_step = (t1 - t0) * 1e3 / args.steps
     tg = 1e3 / ms_step
+    # smallest top-1 / top-2 logit gap over the same greedy sequence (an
+    # untimed re-run from the prompt): how close greedy decoding comes to a
+    # tie, i.e. how small a numeric difference could flip an id
+    tok = prefill()
+    gaps = []
+    for i in range(32):
+        top = np.partition(logits, V - 2)[V - 2:]
+        gaps.append(float(top.max() - top.min()))
+        tok = decode(tok, args.prompt + i, 1)
+    min_gap = min(gaps)
     log(f"tg{args.steps}: {ms_step:.3f} ms/token, {tg:.1f} tok/s; ids {ids[:8]}...")
 
     # --- the same loop through the device-argmax entry (graph replay) -------
@@ -709,6 +724,7 @@ def main():
                    "parallelism": "single-gpu"},
         "decode": {"tok_s_reference_api": round(tg, 3), "tok_s_device_argmax_graph": round(1e3 / ms_dev, 3) if ms_dev else None,
                    "ids_match": ids_dev == ids, "weight_bytes_per_token": tok_bytes,
+                   "min_top1_top2_logit_gap_tg32": round(min_gap, 6),
                    "oracle_greedy_ids_equal": cpu["greedy_ids_equal"] if cpu else None,
                    "oracle_greedy_ids_compared": cpu["greedy_ids_compared"] if cpu else 0,
                    "effective_GBs": round(decode_gbs, 1), "frac_of_hbm_peak": round(decode_gbs / HBM_PEAK_GBS, 4),

@@ -469,6 +469,19 @@ void orc_embed_desc(const DpufWeightDesc* w, int32_t n_tokens, const int32_t* id
 /* A8: RMSNorm (reference dpuf_engine.c:225-272)                              */
 /* ------------------------------------------------------------------------- */
 
+/* Summation order of the RMSNorm sum of squares: 0 the reference's (eight
+ * fma lanes + hsum8), 1 a pairwise tree of the squares.  Test
+ * infrastructure only: the order-sensitivity test measures how far a
+ * reordered but equally valid fp32 sum moves logits and greedy ids. */
+static int g_norm_tree = 0;
+void orc_set_norm_order(int32_t tree) { g_norm_tree = tree; }
+
+static float tree_sum(const float* v, int32_t n) {
+    if (n == 1) return v[0];
+    const int32_t h = n / 2;
+    return tree_sum(v, h) + tree_sum(v + h, n - h);
+}
+
 /* x += res (when res != NULL, stored back), out = (x * inv) * w with
  * inv = 1 / sqrtf(ss / n + eps), ss from eight fma lanes + hsum8. */
 void orc_add_rmsnorm(int32_t n, float* x, const float* res, const float* w, float eps, float* out) {
@@ -481,6 +494,12 @@ void orc_add_rmsnorm(int32_t n, float* x, const float* res, const float* w, floa
         }
     }
     float ss = hsum8(acc);
+    if (g_norm_tree && n > 0) {
+        float* sq = (float*)malloc((size_t)n * sizeof(float));
+        for (int32_t i = 0; i < n; i++) sq[i] = x[i] * x[i];
+        ss = tree_sum(sq, n);
+        free(sq);
+    }
     float inv = 1.0f / sqrtf(ss / (float)n + eps);
     for (int32_t i = 0; i < n; i++) out[i] = (x[i] * inv) * w[i];
 }

@@ -72,6 +72,7 @@ int32_t orc_argmax(const float* logits, int32_t V);
 int32_t orc_top2_exit(const float* x, int32_t n, float thr);
 int32_t orc_num_threads(void);
 void orc_set_num_threads(int32_t n);
+void orc_set_norm_order(int32_t tree);
 
 #ifdef __cplusplus
 }

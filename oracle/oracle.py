@@ -68,5 +68,6 @@ def load():
     _sig(lib, "orc_top2_exit", I32, [P, I32, C.c_float])
     _sig(lib, "orc_num_threads", I32, [])
     _sig(lib, "orc_set_num_threads", None, [I32])
+    _sig(lib, "orc_set_norm_order", None, [I32])
     _lib = lib
     return lib
