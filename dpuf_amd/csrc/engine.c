@@ -85,9 +85,11 @@ typedef struct {
      * holds a step's ids [0, B), its pos0 at IO_POS (read by the embedding
      * kernel) and the published flag, token and error word at IO_OUT;
      * h_logits receives the one LM-head row of a step whose logits go to the
-     * host (written by the GEMV itself) */
+     * host (written by the GEMV itself); h_emb takes the hidden state of a
+     * one-row embeds_in step, read there by the embedding kernel */
     int32_t* h_io;
     float* h_logits;
+    float* h_emb;
     uint8_t* q_idx;      /* per layer: prep index of q,k,v (3 bytes) and gate/up (2 bytes) */
     float deadzone;
     void* stream;
@@ -505,6 +507,7 @@ static void engine_free(Engine* e) {
     dpuf_hip_host_free(e->h_pinned);
     dpuf_hip_host_free(e->h_io);
     dpuf_hip_host_free(e->h_logits);
+    dpuf_hip_host_free(e->h_emb);
     for (int i = 0; i < MAX_EVENTS; i++) if (e->ev[i]) dpuf_hip_event_destroy(e->ev[i]);
     if (e->stream) dpuf_hip_stream_destroy(e->stream);
     free(e);
@@ -621,6 +624,7 @@ DPUF_EXPORT void* dpuf_engine_create(const DpufModelConfig* cfg, const DpufLayer
         e->h_pinned = (int32_t*)dpuf_hip_host_alloc((B + 64) * 4);
         e->h_io = (int32_t*)dpuf_hip_host_alloc_io((B + 64) * 4);
         e->h_logits = (float*)dpuf_hip_host_alloc_io((size_t)e->V * 4);
+        e->h_emb = (float*)dpuf_hip_host_alloc_io((size_t)e->H * 4);
         e->d_red = dpuf_hip_malloc(DPUF_HIP_RED_SCRATCH);
         e->d_ms_kc = (float**)dpuf_hip_malloc(B * 2 * sizeof(float*) + B * 8);
         if (!e->d_ms_kc) goto fail;
@@ -628,7 +632,7 @@ DPUF_EXPORT void* dpuf_engine_create(const DpufModelConfig* cfg, const DpufLayer
         e->d_ms_pos = (int32_t*)(e->d_ms_vc + B);
         e->d_ms_tok = e->d_ms_pos + B;
         if (!e->h || !e->h2 || !e->hn || !e->q || !e->k || !e->v || !e->ao || !e->gate || !e->up || !e->logits ||
-            !e->scores || !e->embeds || !e->d_ids || !e->h_pinned || !e->h_io || !e->h_logits || !e->d_red)
+            !e->scores || !e->embeds || !e->d_ids || !e->h_pinned || !e->h_io || !e->h_logits || !e->h_emb || !e->d_red)
             goto fail;
         e->d_pos0 = e->d_ids + B;
         e->d_flag = e->d_ids + B + 1;
@@ -786,14 +790,17 @@ static int head_early(const Engine* e, int32_t lm_rows, int32_t early_tiles) {
     return early_tiles > 0 && lm_rows == 1 && n_tiles_of(&e->lm) > 2048;
 }
 
-/* Enqueues one forward step: ids in h_io[0, M) and pos0 in h_io[IO_POS] (or
- * embeds rows already on the device); lm_host, when set, takes the one LM-head
- * row in place of e->logits.  Ends by publishing the flag, token and error
- * word to h_io[IO_OUT..]. */
+/* Enqueues one forward step: ids in h_io[0, M) and pos0 in h_io[IO_POS];
+ * rows with id -1 take their hidden state from h_emb (M == 1: every one-row
+ * step, graphs included, points the embedding kernel there, and a row with a
+ * token id ignores it) or, for M > 1 with use_embeds, from e->embeds on the
+ * device.  lm_host, when set, takes the one LM-head row in place of
+ * e->logits.  Ends by publishing the flag, token and error word to
+ * h_io[IO_OUT..]. */
 static void enqueue_forward(Engine* e, int32_t M, int32_t use_embeds, int32_t only_last, int32_t keep_tiles,
                             int32_t early_tiles, float early_margin, int32_t want_argmax, float* lm_host) {
-    dpuf_hip_embed(e->stream, e->tok, e->h_io, M, use_embeds ? e->embeds : NULL, e->h, e->h_io + IO_POS,
-                   e->d_pos0, e->d_serial);
+    const float* emb = M == 1 ? e->h_emb : use_embeds ? e->embeds : NULL;
+    dpuf_hip_embed(e->stream, e->tok, e->h_io, M, emb, M == 1, e->h, e->h_io + IO_POS, e->d_pos0, e->d_serial);
     e->hcur = e->h;
     enqueue_layers(e, M, keep_tiles);
     const int flag_valid = enqueue_head(e, M, only_last, early_tiles, early_margin, want_argmax, lm_host);
@@ -1129,7 +1136,10 @@ static int32_t forward_common(Engine* e, int32_t n_tokens, const int32_t* token_
     for (int32_t m = 0; m < M; m++) io[m] = token_ids ? token_ids[m] : -1;
     io[IO_POS] = pos0;
     io[IO_POS + 1] = next_serial(e);
-    if (embeds_in) dpuf_hip_h2d(e->embeds, embeds_in, (size_t)M * e->H * 4, e->stream);
+    /* one row: the embedding kernel reads the hidden state from h_emb (no
+     * copy, graphs replay it); more rows go to the device first */
+    if (embeds_in && M == 1) memcpy(e->h_emb, embeds_in, (size_t)e->H * 4);
+    else if (embeds_in) dpuf_hip_h2d(e->embeds, embeds_in, (size_t)M * e->H * 4, e->stream);
     /* a one-row LM head whose logits go to the host writes them to h_logits
      * itself (the same for every step of a graph key: want_argmax clear and
      * only_last != 2 imply logits_out) */
@@ -1140,7 +1150,7 @@ static int32_t forward_common(Engine* e, int32_t n_tokens, const int32_t* token_
                          : NULL;
 
     const int tm13 = tm_begin(e, K_CALL, (double)e->weight_bytes);
-    const int graphable = use_graph && !e->no_graphs && M == 1 && !e->timing && !embeds_in && !e->capture;
+    const int graphable = use_graph && !e->no_graphs && M == 1 && !e->timing && !e->capture;
     e->host_pos0 = pos0;
     e->capturing = 0;
     if (graphable) {

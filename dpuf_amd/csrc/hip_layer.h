@@ -117,8 +117,9 @@ int32_t dpuf_hip_graph_launch(void* g, void* s);
 void dpuf_hip_graph_destroy(void* g);
 
 /* Kernels.  pos0 is read from device memory so a captured step replays at
- * any position. */
-void dpuf_hip_embed(void* s, DpufDevW w, const int32_t* ids, int32_t M, const float* embeds,
+ * any position.  Rows with a negative id take their hidden state from embeds,
+ * which is fine-grained host memory when emb_host is set. */
+void dpuf_hip_embed(void* s, DpufDevW w, const int32_t* ids, int32_t M, const float* embeds, int32_t emb_host,
                     float* out, const int32_t* pos_src, int32_t* pos_dst, int32_t* serial_dst);
 /* host[0..3) = {flag_valid ? words[0] : 0, words[1], words[2]} (words: the
  * device's early-exit flag, argmax token, error word) */

@@ -49,9 +49,13 @@ void dpuf_note(hipError_t e, const char* what) {
 // just before the launch: system-scope loads read them past every cache.
 // Workgroup 0 copies the step's start position to pos_dst in device memory,
 // where the kernels after it read it, and the step serial the host put next
-// to it (pos_src[1]) to serial_dst.
+// to it (pos_src[1]) to serial_dst.  Rows with a negative id copy their
+// hidden state from embeds: device memory (plain float4 loads), or, with
+// emb_host set, fine-grained host memory the host filled just before the
+// launch (system-scope 8-byte loads, like the ids).
 __global__ void k_embed(DpufDevW w, const int32_t* __restrict__ ids, const float* __restrict__ embeds,
-                        float* __restrict__ out, const int32_t* pos_src, int32_t* pos_dst, int32_t* serial_dst) {
+                        int emb_host, float* __restrict__ out, const int32_t* pos_src, int32_t* pos_dst,
+                        int32_t* serial_dst) {
     const int m = blockIdx.x;
     const int H = w.cols, n_blk = H >> 5;
     float* dst = out + (size_t)m * H;
@@ -60,6 +64,25 @@ __global__ void k_embed(DpufDevW w, const int32_t* __restrict__ ids, const float
     if (serial_dst && m == 0 && threadIdx.x == 0)
         *serial_dst = __hip_atomic_load(pos_src + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     const int id = ids ? __hip_atomic_load(ids + m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) : -1;
+    if (embeds && id < 0 && emb_host) {
+        // H is a multiple of 64: H / 2 words, all in flight at once with
+        // blockDim.x = 256 and H <= 4096 (the loop covers any H)
+        const uint64_t* src = (const uint64_t*)(embeds + (size_t)m * H);
+        uint64_t* dst8 = (uint64_t*)dst;
+        const int n8 = H >> 1, T = blockDim.x;
+        for (int i0 = threadIdx.x; i0 < n8; i0 += 8 * T) {
+            uint64_t v[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++)
+                v[k] = i0 + k * T < n8 ? __hip_atomic_load(src + i0 + k * T, __ATOMIC_RELAXED,
+                                                           __HIP_MEMORY_SCOPE_SYSTEM)
+                                       : 0ull;
+#pragma unroll
+            for (int k = 0; k < 8; k++)
+                if (i0 + k * T < n8) dst8[i0 + k * T] = v[k];
+        }
+        return;
+    }
     if (embeds && id < 0) {
         // H is a multiple of 64: float4 copies, eight loads in flight per thread
         const float4* src4 = (const float4*)(embeds + (size_t)m * H);
@@ -739,12 +762,14 @@ int32_t dpuf_hip_graph_launch(void* g, void* s) {
 }
 void dpuf_hip_graph_destroy(void* g) { if (g) (void)hipGraphExecDestroy((hipGraphExec_t)g); }
 
-void dpuf_hip_embed(void* s, DpufDevW w, const int32_t* ids, int32_t M, const float* embeds, float* out,
-                    const int32_t* pos_src, int32_t* pos_dst, int32_t* serial_dst) {
+void dpuf_hip_embed(void* s, DpufDevW w, const int32_t* ids, int32_t M, const float* embeds, int32_t emb_host,
+                    float* out, const int32_t* pos_src, int32_t* pos_dst, int32_t* serial_dst) {
     int threads = (w.cols >> 6) < 256 ? (w.cols >> 6) : 256;
     threads = (threads + 63) & ~63;
-    hipLaunchKernelGGL(k_embed, dim3(M), dim3(threads), 0, ST(s), w, ids, embeds, out, pos_src, pos_dst,
-                       serial_dst);
+    // host-memory rows: 256 threads put every 8-byte load of a row in flight at once
+    if (embeds && emb_host) threads = 256;
+    hipLaunchKernelGGL(k_embed, dim3(M), dim3(threads), 0, ST(s), w, ids, embeds, (int)(emb_host != 0), out,
+                       pos_src, pos_dst, serial_dst);
     LAUNCHED("k_embed");
 }
 

@@ -388,7 +388,7 @@ static void embed_f32(int32_t mode, int32_t n_tokens, int32_t cols, const int32_
     float* dout = (float*)dpuf_hip_malloc((size_t)n_tokens * cols * 4);
     if (dids && dout) {
         dpuf_hip_h2d(dids, token_ids, (size_t)n_tokens * 4, s);
-        dpuf_hip_embed(s, st.w, dids, n_tokens, NULL, dout, NULL, NULL, NULL);
+        dpuf_hip_embed(s, st.w, dids, n_tokens, NULL, 0, dout, NULL, NULL, NULL);
         dpuf_hip_d2h(out, dout, (size_t)n_tokens * cols * 4, s);
         dpuf_hip_sync(s);
     }

@@ -420,6 +420,35 @@ def test_embeds_in_rows(eng, orc):
     p.close()
 
 
+def test_one_row_embeds_steps_replay_a_graph(eng, orc):
+    """One-row steps alternate between an embeds_in row (token_ids NULL, and
+    token id -1) and a token id; the hidden state travels through host
+    memory the embedding kernel reads, so both kinds replay the one graph
+    captured for their shape: the fused decode attention is enqueued once per
+    layer (at the capture), not once per layer per step.  Logits bit-identical
+    to the oracle at every step."""
+    m = M.Model.build(TINY, max_seq_len=64, seed=123)
+    p = Pair(eng, orc, m)
+    rng = np.random.default_rng(124)
+    lg, lo = p.forward(rng.integers(0, 4096, 5).astype(np.int32), 0)
+    assert bits_equal(lg, lo), maxdiff(lg, lo)
+    emb = rng.standard_normal((12, 256), dtype=np.float32) * np.float32(0.05)
+    dec0 = eng.dpuf_amd_attn_path_count(4)
+    for s in range(12):
+        pos = 5 + s
+        if s % 3 == 0:
+            lg, lo = p.forward(None, pos, embeds=emb[s:s + 1].copy())
+        elif s % 3 == 1:
+            lg, lo = p.forward(np.array([-1], np.int32), pos, embeds=emb[s:s + 1].copy())
+        else:
+            lg, lo = p.forward(np.array([int(np.argmax(lo[-1]))], np.int32), pos)
+        assert bits_equal(lg, lo), (s, maxdiff(lg, lo))
+    launched = eng.dpuf_amd_attn_path_count(4) - dec0
+    log(f"fused decode attention enqueued {launched} times over 12 steps of {TINY['num_layers']} layers")
+    assert launched == TINY["num_layers"], launched
+    p.close()
+
+
 def test_unshared_projection_signs(eng, orc):
     """Q, K, V with three different sign vectors (three activation preps,
     dpuf_engine.c:1760-1777) and gate / up with two, in every layer."""
