@@ -186,17 +186,55 @@ __global__ __launch_bounds__(256) void k_attn_sc1(const float* __restrict__ q, c
 // order; the row is normalised from LDS and written once.
 #define SMX_NT 1024  // threads per softmax row (SEG a multiple of 16)
 
+// V rows that the workgroups after the n_rows softmax rows of a launch read
+// into the L2 of their XCD for the P.V launch after it: with n_kv a multiple
+// of 8, every chain workgroup of kv head k runs on XCD k % 8 (workgroup b of
+// a launch runs on XCD b % 8, and k_attn_pvd's linear id is y n_kv + k), so
+// the warm-up workgroups on XCD x read rows [0, L) of kv heads x, x + 8, ...
+// (rb bytes per row, base: the V cache of kv head 0).  base NULL: no warm-up.
+struct SmxWarm {
+    const uint8_t* base;
+    int rb, n_kv, n_rows;
+};
+
+DEV void smx_warm(const SmxWarm& W, int L, int max_seq) {
+    const int id = blockIdx.x, xc = id & 7;
+    const int first = W.n_rows + ((xc - W.n_rows) & 7);  // the first warm-up workgroup on XCD xc
+    const int r = (id - first) >> 3, nx = ((int)gridDim.x - first + 7) >> 3;
+    const size_t per = (size_t)L * W.rb;  // bytes of one kv head's rows [0, L), a multiple of 16
+    const size_t lo = (per * r / nx) & ~(size_t)15, hi = r + 1 == nx ? per : (per * (r + 1) / nx) & ~(size_t)15;
+    uint32_t acc = 0;
+    for (int k = xc; k < W.n_kv; k += 8) {
+        const uint8_t* p0 = W.base + (size_t)k * max_seq * W.rb;
+        for (size_t o = lo + 16 * (size_t)threadIdx.x; o < hi; o += 16 * 8 * (size_t)blockDim.x) {
+            uint4 v[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const size_t oo = o + (size_t)i * 16 * blockDim.x;
+                v[i] = oo + 16 <= hi ? *(const uint4*)(p0 + oo) : make_uint4(0, 0, 0, 0);
+            }
+#pragma unroll
+            for (int i = 0; i < 8; i++) acc ^= v[i].x ^ v[i].w;
+        }
+    }
+    asm volatile("" ::"v"(acc));  // the loaded values count as used: the reads stay
+}
+
 template <int SEG>
 __global__ __launch_bounds__(SMX_NT) void k_attn_smx(float* __restrict__ S, const int32_t* __restrict__ pos0p,
-                                                  int max_seq) {
+                                                  int max_seq, SmxWarm W) {
     constexpr int LDT = 8 * SEG + 4;  // row stride of the transposed copy
     __shared__ __align__(16) float tr[8][LDT];
     __shared__ float tail[8];
     __shared__ float red[SMX_NT / 64];
     __shared__ float part[8];
+    const int L = *pos0p + 1, n8 = L & ~7;
+    if ((int)blockIdx.x >= W.n_rows) {
+        smx_warm(W, L, max_seq);
+        return;
+    }
     float* row = S + (size_t)blockIdx.x * max_seq;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int L = *pos0p + 1, n8 = L & ~7;
     // zero the positions past the row that the chains read
     for (int i = tid; i < 8 * LDT; i += SMX_NT) (&tr[0][0])[i] = 0.0f;
     // the row in registers, all loads in flight at once (keys t = tid +
@@ -475,6 +513,9 @@ __global__ __launch_bounds__(192) void k_attn_pvw(const float* __restrict__ P, c
 #define PVD_CK 256  // keys per chunk
 #define PVD_AH 3    // 16-key groups read ahead by the chain
 #define PVD_LD (PVD_CK + 4)  // LDS row stride (rows on distinct banks)
+#ifndef PVD_SMX_WARM
+#define PVD_SMX_WARM 1  // V warmed by the softmax launch (n_kv a multiple of 8)
+#endif
 
 template <int G, bool Q8>
 struct PvdShape {
@@ -693,15 +734,39 @@ __global__ __launch_bounds__(192) void k_attn_pvd(const float* __restrict__ P, c
     if (w == 0) out[(size_t)(kvh * G + h) * HD + d0 + j] = a;
 }
 
+// The softmax launch of a one-token step over n_q score rows; before a
+// k_attn_pvd launch (groups of 2 and 4) with n_kv a multiple of 8, one
+// workgroup per remaining CU (a multiple of 8) warms the V rows (base, rb
+// bytes per row) into the L2 that reads them.
+static void smx_launch(void* s, int seg, float* scores, const int32_t* pos0p, int max_seq, int n_q, int n_kv, int G,
+                       const void* vbase, int rb) {
+    SmxWarm W{nullptr, rb, n_kv, n_q};
+    int nwarm = 0;
+    if (PVD_SMX_WARM && (G == 2 || G == 4) && n_kv % 8 == 0 && vbase) {
+        nwarm = (dpuf_hip_cu_count() - n_q) & ~7;
+        if (nwarm > 0) W.base = (const uint8_t*)vbase;
+        else nwarm = 0;
+    }
+    const dim3 g(n_q + nwarm);
+#define SMX_CASE(SG) \
+    if (seg == SG) hipLaunchKernelGGL(k_attn_smx<SG>, g, dim3(SMX_NT), 0, ST(s), scores, pos0p, max_seq, W);
+    SMX_CASE(16) SMX_CASE(32) SMX_CASE(48) SMX_CASE(64) SMX_CASE(80) SMX_CASE(96) SMX_CASE(128)
+#undef SMX_CASE
+}
+
 // The one-token P.V launch: k_attn_pvd for groups of 2 and 4, else k_attn_pvw
 // (gm: its group instance, 2, 4 or 8).
 template <int HD, bool Q8>
 static void pv_wide_launch(void* s, int G, int gm, const float* scores, const float* vc, const int32_t* pos0p, int n_q,
                            int n_kv, int max_seq, float* out, DpufKvQ8 c8) {
-    // k_attn_pvd: HD / DW chain workgroups per kv head, then warm-up
-    // workgroups up to about one per CU
+    // k_attn_pvd: HD / DW chain workgroups per kv head, then (unless the
+    // softmax launch warmed V into the L2s) warm-up workgroups up to about
+    // one per CU
     if (G == 4 || G == 2) {
-        const int ns = HD / (64 / G), nwarm = (dpuf_hip_cu_count() / n_kv > ns ? dpuf_hip_cu_count() / n_kv : ns) - ns;
+        const int ns = HD / (64 / G);
+        const int nwarm = PVD_SMX_WARM && n_kv % 8 == 0 && dpuf_hip_cu_count() - n_q >= 8
+                              ? 0
+                              : (dpuf_hip_cu_count() / n_kv > ns ? dpuf_hip_cu_count() / n_kv : ns) - ns;
         if (G == 4)
             hipLaunchKernelGGL((k_attn_pvd<HD, 4, Q8>), dim3(n_kv, ns + nwarm), dim3(192), 0, ST(s), scores, vc, pos0p,
                                n_kv, max_seq, out, c8);
@@ -738,8 +803,6 @@ int32_t attn_wide_f32(void* s, int32_t lmax, const float* q, const float* kc, co
             if (64 * segs[i] >= lmax) seg = segs[i];
         if (M == 1 && (G & 1) == 0 && G <= 8 && seg) {
             const int gm = G <= 2 ? 2 : G <= 4 ? 4 : 8;
-#define SMX_LAUNCH(SG)                                                                                            \
-    if (seg == SG) hipLaunchKernelGGL(k_attn_smx<SG>, dim3(n_q), dim3(SMX_NT), 0, ST(s), scores, pos0p, max_seq);
 #define SC1_LAUNCH(HDV, GMV)                                                                                      \
     {                                                                                                             \
         const dim3 g1s(n_kv, (lmax + AS_KC - 1) / AS_KC);                                                         \
@@ -753,7 +816,7 @@ int32_t attn_wide_f32(void* s, int32_t lmax, const float* q, const float* kc, co
     }
 #define WIDE_LAUNCH(HDV)                                                                                          \
     if (gm == 2) SC1_LAUNCH(HDV, 2) else if (gm == 4) SC1_LAUNCH(HDV, 4) else SC1_LAUNCH(HDV, 8)                  \
-    SMX_LAUNCH(16) SMX_LAUNCH(32) SMX_LAUNCH(48) SMX_LAUNCH(64) SMX_LAUNCH(80) SMX_LAUNCH(96) SMX_LAUNCH(128)  \
+    smx_launch(s, seg, scores, pos0p, max_seq, n_q, n_kv, G, vc, HDV * 4);                                         \
     pv_wide_launch<HDV, false>(s, G, gm, scores, vc, pos0p, n_q, n_kv, max_seq, out, DpufKvQ8{});
             if (hd == 64) {
                 WIDE_LAUNCH(64)
@@ -764,7 +827,6 @@ int32_t attn_wide_f32(void* s, int32_t lmax, const float* q, const float* kc, co
             }
 #undef WIDE_LAUNCH
 #undef SC1_LAUNCH
-#undef SMX_LAUNCH
             LAUNCHED("k_attn_split_wide");
             attn_path_note(1);
             return 0;
@@ -789,10 +851,7 @@ int32_t attn_wide_q8(void* s, int32_t lmax, const int32_t* pos0, int32_t n_q, in
             if (64 * segs[i] >= lmax) seg = segs[i];
         if (seg) {
             const int gm = G <= 2 ? 2 : G <= 4 ? 4 : 8;
-#define SMXQ(SG) \
-    if (seg == SG) hipLaunchKernelGGL(k_attn_smx<SG>, dim3(n_q), dim3(SMX_NT), 0, ST(s), scores, pos0, max_seq);
-            SMXQ(16) SMXQ(32) SMXQ(48) SMXQ(64) SMXQ(80) SMXQ(96) SMXQ(128)
-#undef SMXQ
+            smx_launch(s, seg, scores, pos0, max_seq, n_q, n_kv, G, c8.vq, hd);
             if (hd == 64) pv_wide_launch<64, true>(s, G, gm, scores, nullptr, pos0, n_q, n_kv, max_seq, out, c8);
             else if (hd == 128) pv_wide_launch<128, true>(s, G, gm, scores, nullptr, pos0, n_q, n_kv, max_seq, out, c8);
             else pv_wide_launch<256, true>(s, G, gm, scores, nullptr, pos0, n_q, n_kv, max_seq, out, c8);
