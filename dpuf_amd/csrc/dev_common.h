@@ -444,6 +444,21 @@ DEV uint4 nt_load16(const uint8_t* p) {
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// 4 x 4 transpose of (16-lane row, register): afterwards register j of lane
+// row g holds what register g of lane row j held.
+DEV void skp_transpose(uint32_t& r0, uint32_t& r1, uint32_t& r2, uint32_t& r3) {
+    // rows 2, 3 of r0 <-> rows 0, 1 of r2; the same for r1, r3
+    const auto a = __builtin_amdgcn_permlane32_swap(r0, r2, false, false);
+    const auto b = __builtin_amdgcn_permlane32_swap(r1, r3, false, false);
+    // rows 1, 3 of the first <-> rows 0, 2 of the second
+    const auto c = __builtin_amdgcn_permlane16_swap(a[0], b[0], false, false);
+    const auto d = __builtin_amdgcn_permlane16_swap(a[1], b[1], false, false);
+    r0 = c[0];
+    r1 = c[1];
+    r2 = d[0];
+    r3 = d[1];
+}
+
 
 
 // LDS address space pointer of the direct-to-LDS loads.

@@ -1,0 +1,368 @@
+// gemt.hip -- the few-token GEMM of the packed Mode 12 matrices (2 <= M <= 16
+// rows of activations, K <= 4096): several sessions' decode steps in one pass
+// over the weights (k_mvt), and its launch planning.
+//
+// Numerics contract: every output is the reference's per-row fp32 chain over
+// the 32-column blocks in ascending order,
+//   acc = fma(float(D - sum8), fp16(ws) * xs, acc)        (dpuf_avx2.c:2633-2635,
+// the slab path dpuf_avx2.c:2643-2676), with D the u4 x i8 dot of the block and
+// sum8 = 8 * sum(q): the same two rounded operations per block as k_gemm_mfma
+// and k_gemm_skp, so the results are bit-identical to theirs.
+//   * D - sum8 is an integer below 2^15 in magnitude: D exactly by one
+//     v_mfma_i32_16x16x32_i8 per block (A = the nibbles u, 0..15 as int8,
+//     B = the int8 activations), then an integer subtraction;
+//   * fp16(ws) * xs is one v_fma_mix_f32 with a +0 addend (the product's
+//     rounding; a zero product's sign cannot reach acc, which is never -0);
+//   * build with -ffp-contract=off; fused multiply-adds are explicit fmaf.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string.h>
+
+#include "hip_layer.h"
+#include "dev_common.h"
+#include "hip_internal.h"
+
+// ---------------------------------------------------------------------------
+// R waves compute a 16-row fragment (two 8-row groups) for all M tokens,
+// walking the blocks of K in order with the accumulators in registers (MFMA
+// D layout: lane l holds token l % 16, rows 4 (l / 16) + v); each of the R
+// waves repeats the fragment's MFMAs and runs the chains of 4 / R of the four
+// D components (R = 1 for large matrices, 2 or 4 when the fragments alone
+// would leave SIMDs idle).  No chain crosses a wave and no wave waits for
+// another after the staging.
+//
+// A workgroup of MT_FW waves serves one job (matrix); it stages that job's
+// activations once into LDS: the int8 values [block][token][32], so that an
+// MFMA B fragment (lane l: token l % 16, columns 8 (l / 16) .. + 7 of the
+// block) is one 8-byte read, and the block sums and scales [token][block]
+// (four blocks in one read).  With NT = 8 staged tokens,
+// lanes of tokens 8..15 read token l % 8: their D columns are computed and
+// never stored.
+//
+// Per fragment a wave copies its two groups' fp16 row scales (16 bytes per
+// block) to an LDS area of its own, read per block.  The nibbles stream
+// through a register ring PF 4-block quads deep: per quad one 16-byte buffer
+// load per lane (lane offset fixed per fragment, the quad in the scalar
+// offset), row l % 16's bytes of block b0 + l / 16; a 4 x 4 transpose across
+// the wave's 16-lane rows gives lane (i, kc) column chunk kc of all four
+// blocks, the MFMA A layout.
+// ---------------------------------------------------------------------------
+#define MT_FW 4  // waves per workgroup
+#define MT_RSRC3 0x00020000  // buffer descriptor word 3 (gfx9 family): 32-bit raw data
+
+typedef int mt_i4 __attribute__((ext_vector_type(4)));
+
+struct MtJob {
+    const uint8_t* g;  // dense groups of the matrix (row-block layout)
+    int g0, g1;        // groups computed
+    int rows;
+    const int8_t* q;   // activations int8 [M][K]
+    const float* s;    // block scales [M][K/32]
+    const int32_t* m;  // 8 * block sums [M][K/32]
+    float* out;        // out[m * ldo + row]
+    int ldo;
+};
+
+struct MtArgs {
+    MtJob j[3];
+    int n_jobs;
+    int wb[4];  // prefix sums of the workgroups given to each job
+    int K, M;
+};
+
+// LDS bytes of a workgroup: the staged activations of NT tokens (40 bytes
+// per token and block) and each wave's copy of two groups' row scales, every
+// array with 4 blocks of padding (the reads one quad ahead run into it after
+// the last quad; the scale rows of different tokens start on different banks).
+static constexpr size_t mt_lds(int n_blk, int nt) { return (size_t)(n_blk + 4) * (nt * 40 + MT_FW * 32); }
+
+template <int NT, int R>
+__global__ __launch_bounds__(64 * MT_FW) void k_mvt(MtArgs A) {
+    constexpr int NV = 4 / R;         // D components per wave
+    constexpr int FPW = MT_FW / R;    // fragments per workgroup round
+    constexpr int PF = R == 1 ? 8 : 12;  // quads of nibbles in flight (even)
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int bid = blockIdx.x;
+    int ji = 0;
+    if (A.n_jobs > 1 && bid >= A.wb[1]) ji = 1;
+    if (A.n_jobs > 2 && bid >= A.wb[2]) ji = 2;
+    const MtJob& J = A.j[ji];
+    const int K = A.K, M = A.M, n_blk = K >> 5, nq = n_blk >> 2;
+    const int tid = threadIdx.x, l = tid & 63, i16 = l & 15, kc = l >> 4;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: the descriptors stay scalar
+    // fragment slot; the wave's rows rotation rho: MFMA row 4c + k holds the
+    // fragment's row 4c + ((k + rho) & 3), so D components 0 .. NV - 1 are
+    // the fragment's rows 4c + rho + k, the ones this wave chains
+    const int fs = w / R, rho = (w % R) * NV;
+    const int nfr = (J.g1 - J.g0 + 1) >> 1;   // 16-row fragments of the job
+    const int lb = bid - A.wb[ji], nwg = A.wb[ji + 1] - A.wb[ji];
+    const uint32_t gstride = (uint32_t)n_blk * 144u;
+
+    const int nbp = n_blk + 4;  // padded block count of every LDS array
+    int8_t* sq = (int8_t*)smem;                             // [nbp][NT][32]
+    int32_t* sm = (int32_t*)(smem + (size_t)nbp * NT * 32); // sum8 [NT][nbp]
+    float* sx = (float*)(smem + (size_t)nbp * NT * 36);     // xs [NT][nbp]
+    uint8_t* ws = smem + (size_t)nbp * NT * 40 + (size_t)w * nbp * 32;  // [2][nbp][16 B]
+
+    // a fragment's nibble loads: lane row i16 is fragment row ri (group gf +
+    // ri / 8, clamped into the job: a fragment with one group repeats it,
+    // never stored), from a descriptor at group gf
+    __amdgpu_buffer_rsrc_t rsc;
+    uint32_t won = 0;
+    int ngr = 2;
+    auto frag_setup = [&](int f) {
+        const int gf = J.g0 + 2 * f;
+        const int ri = (i16 & 12) + ((i16 + rho) & 3);
+        const int ga = min(gf + (ri >> 3), J.g1 - 1);
+        ngr = J.g1 - gf < 2 ? J.g1 - gf : 2;
+        rsc = __builtin_amdgcn_make_buffer_rsrc((void*)(J.g + (size_t)gf * gstride), 0, (int)(ngr * gstride),
+                                                MT_RSRC3);
+        won = (uint32_t)(ga - gf) * gstride + (uint32_t)n_blk * 16u + (uint32_t)(ri & 7) * 16u + (uint32_t)kc * 128u;
+    };
+    u32x4 wr[PF];
+    auto quad_load = [&](int p, int qd) {
+        wr[p] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsc, won, qd * 512, 0));
+    };
+    // the fragment's row scales for this wave's LDS area: entry e = group
+    // e / n_blk, block e % n_blk (2 n_blk <= 256 entries, 4 per lane), loaded
+    // before the fragment's first nibble quads so that the stores wait for
+    // these loads only
+    u32x4 st[4];
+    auto scales_load = [&]() {
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int e = min(l + 64 * k, 2 * n_blk - 1), gi = min(e / n_blk, ngr - 1);
+            st[k] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                  rsc, (uint32_t)gi * gstride + (uint32_t)(e % n_blk) * 16u, 0, 0));
+        }
+    };
+    auto scales_store = [&]() {
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+            if (l + 64 * k < 2 * n_blk) {
+                const int e = l + 64 * k;
+                *(u32x4*)(ws + (size_t)((e / n_blk) * nbp + e % n_blk) * 16) = st[k];
+            }
+    };
+    auto frag_start = [&](int f) {
+        frag_setup(f);
+        scales_load();
+#pragma unroll
+        for (int p = 0; p < PF; p++) quad_load(p, min(p, nq - 1));
+    };
+    int f = lb * FPW + fs;
+
+    // staging through registers: every staging load, then the first
+    // fragment's loads, then the stores (which wait for the staging loads
+    // only: loads complete in issue order); n_blk <= 128, chunk i of the int8
+    // rows = 16 bytes of (block i / 2 NT, token (i / 2) % NT, half i % 2)
+    constexpr int QPT = 128 * NT * 2 / (64 * MT_FW), SPT = 128 * NT / (64 * MT_FW);
+    mt_i4 tq[QPT];  // a native vector: an int4 struct array would stay in scratch
+    int tm[SPT];
+    float ts[SPT];
+#pragma unroll
+    for (int k = 0; k < QPT; k++) {
+        const int i = min(tid + 64 * MT_FW * k, n_blk * NT * 2 - 1);
+        const int b = i / (2 * NT), t = (i >> 1) % NT, h = i & 1, tt = min(t, M - 1);
+        tq[k] = *(const mt_i4*)(J.q + (size_t)tt * K + b * 32 + 16 * h);
+    }
+#pragma unroll
+    for (int k = 0; k < SPT; k++) {
+        const int i = min(tid + 64 * MT_FW * k, n_blk * NT - 1), b = i / NT, tt = min(i % NT, M - 1);
+        tm[k] = J.m[(size_t)tt * n_blk + b];
+        ts[k] = J.s[(size_t)tt * n_blk + b];
+    }
+    // (unconditional, clamped to the job's last fragment when this slot has
+    // none: the same loads on every path keep the stores' waits exact)
+    frag_start(min(f, nfr - 1));
+#pragma unroll
+    for (int k = 0; k < QPT; k++) {
+        const int i = tid + 64 * MT_FW * k;
+        if (i < n_blk * NT * 2) *(mt_i4*)(sq + (size_t)i * 16) = tq[k];
+    }
+#pragma unroll
+    for (int k = 0; k < SPT; k++) {
+        const int i = tid + 64 * MT_FW * k;
+        if (i < n_blk * NT) {
+            sm[(i % NT) * nbp + i / NT] = tm[k];
+            sx[(i % NT) * nbp + i / NT] = ts[k];
+        }
+    }
+    __syncthreads();
+
+    const int tok = i16 % NT;
+    const int8_t* sqt = sq + tok * 32 + kc * 8;
+    const int32_t* smt = sm + tok * nbp;
+    const float* sxt = sx + tok * nbp;
+    // this lane's scales in the wave's copy: group kc / 2 (clamped), rows
+    // 4 (kc & 1) + rho .. of each block's 8
+    for (; f < nfr; f += nwg * FPW) {
+        if (f != lb * FPW + fs) frag_start(f);
+        scales_store();
+        const uint8_t* wst = ws + (size_t)min(kc >> 1, ngr - 1) * nbp * 16 + (kc & 1) * 8 + rho * 2;
+        float acc[NV];
+#pragma unroll
+        for (int v = 0; v < NV; v++) acc[v] = 0.0f;
+        // LDS operands of a quad in slot sl: B fragments, the lane's row
+        // scales (fp16 rows 4 (kc & 1) + rho + k, k < NV), and the four
+        // blocks' token scales and sums; read one quad ahead of their use
+        long bb[2][4];
+        uint32_t sw[2][4][2];
+        float4 xq[2];
+        int4 mq[2];
+        auto lds_quad = [&](int sl, const int8_t* sqb, const int32_t* smb, const uint8_t* wsb, const float* sxb) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                bb[sl][j] = *(const long*)(sqb + j * NT * 32);
+                if (NV == 4) {
+                    const uint2 u = *(const uint2*)(wsb + j * 16);
+                    sw[sl][j][0] = u.x;
+                    sw[sl][j][1] = u.y;
+                } else if (NV == 2) {
+                    sw[sl][j][0] = *(const uint32_t*)(wsb + j * 16);
+                } else {
+                    sw[sl][j][0] = *(const uint16_t*)(wsb + j * 16);
+                }
+            }
+            xq[sl] = *(const float4*)sxb;
+            mq[sl] = *(const int4*)smb;
+        };
+        lds_quad(0, sqt, smt, wst, sxt);
+        for (int q0 = 0; q0 < nq; q0 += PF) {
+            // LDS bases of this round of quads (the reads below add constants)
+            const int8_t* sq0 = sqt + q0 * 4 * NT * 32;
+            const int32_t* sm0 = smt + 4 * q0;
+            const float* sx0 = sxt + 4 * q0;
+            const uint8_t* ws0 = wst + q0 * 64;
+#pragma unroll
+            for (int p = 0; p < PF; p++) {
+                const int qd = q0 + p;
+                if (qd >= nq) break;  // uniform
+                const int cs = p & 1;  // PF is even: the slots alternate across rounds too
+                // the next quad's LDS operands (after the last quad: padding, never used)
+                lds_quad(cs ^ 1, sq0 + (4 * p + 4) * NT * 32, sm0 + 4 * p + 4, ws0 + (4 * p + 4) * 16,
+                         sx0 + 4 * p + 4);
+                uint32_t w0 = wr[p][0], w1 = wr[p][1], w2 = wr[p][2], w3 = wr[p][3];
+                skp_transpose(w0, w1, w2, w3);
+                // the quad PF ahead into this slot (clamped: loads past the
+                // end repeat the last quad and are never used)
+                quad_load(p, min(qd + PF, nq - 1));
+                const uint32_t wj[4] = {w0, w1, w2, w3};
+                const float xsj[4] = {xq[cs].x, xq[cs].y, xq[cs].z, xq[cs].w};
+                const int xmj[4] = {mq[cs].x, mq[cs].y, mq[cs].z, mq[cs].w};
+                // the quad's four MFMAs first (independent), then the chains
+                mt_i4 dq[4];
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const uint32_t lo = wj[j] & 0x0F0F0F0Fu, hi = (wj[j] >> 4) & 0x0F0F0F0Fu;
+                    const long a = (long)(((uint64_t)hi << 32) | lo);
+                    dq[j] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, bb[cs][j], (mt_i4){0, 0, 0, 0}, 0, 0, 0);
+                }
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+#pragma unroll
+                    for (int k = 0; k < NV; k++) {
+                        const gm_h2 h = __builtin_bit_cast(gm_h2, sw[cs][j][k >> 1]);
+                        const float sp = __builtin_fmaf((float)h[k & 1], xsj[j], 0.0f);
+                        acc[k] = fmaf((float)(dq[j][k] - xmj[j]), sp, acc[k]);
+                    }
+                }
+            }
+        }
+        // token i16, rows 4 (kc & 1) + rho + k of group gf + kc / 2
+        const int grp = J.g0 + 2 * f + (kc >> 1);
+        if (i16 < M && grp < J.g1) {
+#pragma unroll
+            for (int k = 0; k < NV; k++) {
+                const int r = grp * 8 + 4 * (kc & 1) + rho + k;
+                if (r < J.rows) J.out[(size_t)i16 * J.ldo + r] = acc[k];
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+
+extern "C" {
+
+typedef void (*MtKernel)(MtArgs);
+
+// Workgroups of instance k the device holds at once with lds bytes each.
+static int mt_capacity(MtKernel k, size_t lds) {
+    static MtKernel c_k[8];
+    static size_t c_lds[8];
+    static int c_cap[8], c_n = 0;
+    for (int i = 0; i < c_n; i++)
+        if (c_k[i] == k && c_lds[i] == lds) return c_cap[i];
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, 64 * MT_FW, lds) != hipSuccess || per_cu <= 0)
+        per_cu = 1;
+    const int cap = per_cu * dpuf_hip_cu_count();
+    if (c_n < 8) {
+        c_k[c_n] = k;
+        c_lds[c_n] = lds;
+        c_cap[c_n++] = cap;
+    }
+    return cap;
+}
+
+int32_t dpuf_hip_mvt_launch(void* s, int32_t M, int32_t n_jobs, const DpufGemvJob* jobs) {
+    if (M < 2 || M > 16 || n_jobs < 1 || n_jobs > 3) return -1;
+    const int K = jobs[0].w.cols, n_blk = K >> 5;
+    if (K <= 0 || K % 128 || n_blk > 128) return -1;
+    for (int i = 0; i < n_jobs; i++) {
+        if (jobs[i].w.mode != 12 || jobs[i].w.cols != K || !jobs[i].p.q || !jobs[i].p.s || !jobs[i].p.m) return -1;
+    }
+    const int nt = M <= 8 ? 8 : 16;
+    int nfr[3] = {0, 0, 0}, ftot = 0;
+    for (int i = 0; i < n_jobs; i++) {
+        const int ng = jobs[i].g1 - jobs[i].g0;
+        nfr[i] = ng > 0 ? (ng + 1) / 2 : 0;
+        ftot += nfr[i];
+    }
+    if (ftot == 0) return 0;
+    // up to one fragment per CU the K-split GEMM is faster (its workgroups
+    // share a fragment's blocks instead of each walking all of K)
+    if (ftot <= dpuf_hip_cu_count()) return -1;
+    // waves per fragment: as many as keep about two waves per SIMD busy
+    const int target = 8 * dpuf_hip_cu_count();
+    const int R = 4 * ftot <= target ? 4 : 2 * ftot <= target ? 2 : 1;
+    MtKernel k = nt == 8 ? (R == 4 ? k_mvt<8, 4> : R == 2 ? k_mvt<8, 2> : k_mvt<8, 1>)
+                         : (R == 4 ? k_mvt<16, 4> : R == 2 ? k_mvt<16, 2> : k_mvt<16, 1>);
+    const size_t lds = mt_lds(n_blk, nt);
+    int cap = mt_capacity(k, lds);
+    if (dpuf_hip_mv_max_wg() > 0 && cap > dpuf_hip_mv_max_wg()) cap = dpuf_hip_mv_max_wg();
+    MtArgs A;
+    memset(&A, 0, sizeof A);
+    A.n_jobs = n_jobs;
+    A.K = K;
+    A.M = M;
+    for (int i = 0; i < n_jobs; i++) {
+        A.j[i].g = jobs[i].w.g;
+        A.j[i].g0 = jobs[i].g0;
+        A.j[i].g1 = jobs[i].g1;
+        A.j[i].rows = jobs[i].w.rows;
+        A.j[i].q = jobs[i].p.q;
+        A.j[i].s = jobs[i].p.s;
+        A.j[i].m = jobs[i].p.m;
+        A.j[i].out = jobs[i].out;
+        A.j[i].ldo = jobs[i].ldo;
+    }
+    // each job's workgroups in proportion to its fragments, all resident at
+    // once; a workgroup takes MT_FW / R fragments per round
+    const int fpw = MT_FW / R;
+    int wgs = 0;
+    A.wb[0] = 0;
+    for (int i = 0; i < n_jobs; i++) {
+        const int need = (nfr[i] + fpw - 1) / fpw;
+        int nw = (int)(((long long)cap * nfr[i] + ftot - 1) / ftot);
+        nw = nw < 1 ? 1 : nw;
+        wgs += nfr[i] > 0 ? (nw < need ? nw : need) : 0;
+        A.wb[i + 1] = wgs;
+    }
+    hipLaunchKernelGGL(k, dim3(wgs), dim3(64 * MT_FW), lds, ST(s), A);
+    LAUNCHED("k_mvt");
+    return 0;
+}
+
+}  // extern "C"

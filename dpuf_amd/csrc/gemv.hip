@@ -738,7 +738,7 @@ void dpuf_hip_gemv(void* s, int32_t M, int32_t n_jobs, const DpufGemvJob* jobs, 
         for (int j = i; j < n_jobs; j++)
             if (jobs[j].w.mode == mode) sub[n++] = jobs[j];
         if (M > 1) {
-            dpuf_hip_gm_launch(s, M, n, sub, NULL, 0, 0, 0);
+            if (dpuf_hip_mvt_launch(s, M, n, sub) != 0) dpuf_hip_gm_launch(s, M, n, sub, NULL, 0, 0, 0);
             continue;
         }
         MvArgs A;

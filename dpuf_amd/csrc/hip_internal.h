@@ -1,5 +1,6 @@
 // hip_internal.h -- host-side helpers shared by the HIP translation units of
-// the engine (rt.hip, gemv.hip, gemm.hip, attn.hip, attn_dec.hip).
+// the engine (rt.hip, gemv.hip, gemm.hip, gemt.hip, attn.hip, attn_wide.hip,
+// attn_dec.hip).
 #ifndef DPUF_HIP_INTERNAL_H
 #define DPUF_HIP_INTERNAL_H
 
@@ -28,6 +29,9 @@ int dpuf_hip_mv_max_wg(void);
 // stride zld) are set to 0 by the same launch.
 void dpuf_hip_gm_launch(void* s, int32_t M, int32_t n_jobs, const DpufGemvJob* jobs, float* zo, int32_t zld,
                         int32_t z0, int32_t z1);
+// The few-token GEMM (mode 12, 2 <= M <= 16, K a multiple of 128 up to
+// 4096, more 16-row fragments than CUs); -1 without launching otherwise.
+int32_t dpuf_hip_mvt_launch(void* s, int32_t M, int32_t n_jobs, const DpufGemvJob* jobs);
 }
 
 #endif

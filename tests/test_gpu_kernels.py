@@ -132,6 +132,28 @@ def test_matmul_skinny_workgroup_caps(eng, orc, cols, cap):
     assert _same_bits(out_g, out_o), f"max abs diff {np.nanmax(np.abs(out_g - out_o))}"
 
 
+@pytest.mark.parametrize("cap", [1, 5])
+def test_matmul_few_token_workgroup_caps(eng, orc, cap):
+    """The few-token MFMA GEMM (12296 rows: 769 fragments, the last with one
+    group, 2 waves per fragment) with its workgroups capped so each walks
+    many fragments, restaging nothing between them."""
+    rows, cols, m = 12296, 1024, 6
+    blob, d = _mat(rows, cols, 91)
+    x = _x(m, cols, 93)
+    out_g = np.full((m, rows), np.nan, np.float32)
+    out_o = np.full((m, rows), np.nan, np.float32)
+    print(f"few-token rows={rows} cols={cols} M={m} max_workgroups={cap}", flush=True)
+    eng.dpuf_amd_set_gemv_max_workgroups(cap)
+    try:
+        eng.dpuf_matmul_qr_hadamard4_packed_f32(m, rows, cols, d.n_tiles, M.ptr(x), d.tensor_base, d.tile_offsets,
+                                                d.sign_bits, M.ptr(out_g))
+    finally:
+        eng.dpuf_amd_set_gemv_max_workgroups(0)
+    orc.orc_matmul_f32(m, rows, cols, d.n_tiles, M.ptr(x), d.tensor_base, d.tile_offsets, d.sign_bits,
+                       M.ptr(out_o))
+    assert _same_bits(out_g, out_o), f"max abs diff {np.nanmax(np.abs(out_g - out_o))}"
+
+
 @pytest.mark.parametrize("rows,cols,m", [(200, 320, 65), (200, 320, 130), (1000, 1024, 130), (72, 64, 200)])
 def test_matmul_token_tiles_bit_exact(eng, orc, rows, cols, m):
     """M > 64: several 64-token tiles of the slab GEMM (the last one ragged),
@@ -152,12 +174,16 @@ def test_matmul_token_tiles_bit_exact(eng, orc, rows, cols, m):
 
 @pytest.mark.parametrize("rows,cols,m", [(72, 320, 2), (136, 64, 16), (200, 1088, 16), (1000, 3072, 9),
                                          (4096, 12288, 8), (12288, 4096, 16), (72, 4160, 5),
-                                         (200, 320, 17)])
+                                         (200, 320, 17), (1000, 4096, 8), (136, 256, 2), (200, 1024, 5),
+                                         (24, 128, 3), (6152, 4096, 7), (24576, 4096, 8), (40000, 256, 3)])
 def test_matmul_skinny_bit_exact(eng, orc, rows, cols, m):
-    """M <= 16, the K-split GEMMs: odd group counts (a fragment with one
-    group), block counts that are not a multiple of the 32-block round (10,
-    34, 130: K > 4096 with a partial last round), the 8B shapes; M = 17 is
-    the slab GEMM next to it."""
+    """M <= 16: the few-token MFMA GEMM (K a multiple of 128 up to 4096 and
+    more 16-row fragments than CUs; 8 staged tokens for M <= 8, 16 above; 1,
+    2 or 4 waves per fragment: 24576 and 40000 rows take 1, 12288 rows 2,
+    6152 rows 4 and a last fragment with one group) and the K-split GEMMs
+    (the rest): odd group counts, a single 4-block quad, block counts that
+    are not a multiple of the 32-block round (10, 34, 130: K > 4096 with a
+    partial last round), the 8B shapes; M = 17 is the slab GEMM next to it."""
     blob, d = _mat(rows, cols, 41 + rows)
     x = _x(m, cols, 5 * rows + cols)
     x[m - 1, 32:64] = 1e-6  # a zero-scale block
