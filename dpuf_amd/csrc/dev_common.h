@@ -444,6 +444,71 @@ DEV uint4 nt_load16(const uint8_t* p) {
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// Top-2 with multiplicity (the reference's sequential b1/b2 scan,
+// dpuf_engine.c:2101-2110, is order independent), then the early-exit
+// decision b1 - b2 >= thr (thr > 0).
+// (Selects, not branches: with branches the compiler merged the two
+// conditional stores into a store through a selected address, which kept
+// the pair in scratch.)
+DEV void top2_take(float v, float& b1, float& b2) {
+    const bool g1 = v > b1, g2 = v > b2;
+    const float n2 = g1 ? b1 : (g2 ? v : b2);
+    b1 = g1 ? v : b1;
+    b2 = n2;
+}
+
+DEV void top2_merge(float& b1, float& b2, float c1, float c2) {
+    if (b1 >= c1) {
+        b2 = fmaxf(b2, c1);
+    } else {
+        b2 = fmaxf(c2, b1);
+        b1 = c1;
+    }
+}
+
+// First maximum (dpuf-cli.c:1997-2004: `if (x[i] > best)` from best = x[0]):
+// the larger value, the smaller index on ties; every partial starts from
+// (x[0], 0), so a NaN x[0] gives 0 as the reference does and other NaNs are
+// never taken.
+DEV void amax_merge(float& bv, int& bi, float v, int i) {
+    const bool take = v > bv || (v == bv && i < bi);
+    bv = take ? v : bv;
+    bi = take ? i : bi;
+}
+
+// A partial of the LM-head reductions over some rows of a logit row:
+// (top-1, top-2, first-max value, its row as int bits).  Top-2 starts from
+// -1e30 as the scan over the whole row does; the first maximum from (-inf,
+// INT_MAX), so that merging partials in any order gives the smallest row of
+// the largest value and never a NaN (a NaN logit 0 is the caller's case).
+// A native vector: the HIP float4 struct would be kept in scratch.
+typedef float lm4 __attribute__((ext_vector_type(4)));
+DEV lm4 lm_part_init() { return (lm4){-1e30f, -1e30f, __int_as_float(0xFF800000), __int_as_float(0x7FFFFFFF)}; }
+DEV lm4 lm_part_take(lm4 p, float v, int row) {
+    float b1 = p[0], b2 = p[1], av = p[2];
+    int bi = __float_as_int(p[3]);
+    top2_take(v, b1, b2);
+    amax_merge(av, bi, v, row);
+    return (lm4){b1, b2, av, __int_as_float(bi)};
+}
+DEV lm4 lm_part_merge(lm4 p, lm4 o) {
+    float b1 = p[0], b2 = p[1], av = p[2];
+    int bi = __float_as_int(p[3]);
+    top2_merge(b1, b2, o[0], o[1]);
+    amax_merge(av, bi, o[2], __float_as_int(o[3]));
+    return (lm4){b1, b2, av, __int_as_float(bi)};
+}
+// The merge of a wave's 64 partials, in every lane.
+DEV lm4 lm_part_wave(lm4 p) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const lm4 q = {__shfl_xor(p[0], o, 64), __shfl_xor(p[1], o, 64), __shfl_xor(p[2], o, 64),
+                       __shfl_xor(p[3], o, 64)};
+        p = lm_part_merge(p, q);
+    }
+    return p;
+}
+
 // 4 x 4 transpose of (16-lane row, register): afterwards register j of lane
 // row g holds what register g of lane row j held.
 DEV void skp_transpose(uint32_t& r0, uint32_t& r1, uint32_t& r2, uint32_t& r3) {

@@ -21,6 +21,7 @@
 
 #define N_SLOTS 8
 #define N_GRAPHS 8  /* captured one-token steps kept per engine */
+#define LM_RED_CAP 8192 /* LM-head partials (chains of one GEMV launch) */
 #define N_PREFIX 8
 #define N_KINDS 8
 #define MAX_EVENTS 8192
@@ -70,6 +71,9 @@ typedef struct {
     int32_t *d_serial, *d_pflag;
     int32_t serial;
     void* d_red; /* partials of the device argmax / top-2 reductions */
+    /* LM-head partials written by the one-row LM-head GEMV's chains
+     * (LM_RED_CAP of 16 bytes), then the Zone-A merge (16 bytes) */
+    void* d_lmred;
     /* one token per session (dpuf_amd_engine_forward_slots): while ms_n > 0
      * the layers run ms_n tokens, token m of slot ms_slot[m] at position
      * ms_pos[m] (device copy d_ms_pos); the first ms_short of them (fp32
@@ -503,6 +507,7 @@ static void engine_free(Engine* e) {
     dpuf_hip_free(e->d_ids);
     dpuf_hip_free(e->d_pflag);
     dpuf_hip_free(e->d_red);
+    dpuf_hip_free(e->d_lmred);
     dpuf_hip_free(e->d_ms_kc);
     dpuf_hip_host_free(e->h_pinned);
     dpuf_hip_host_free(e->h_io);
@@ -626,13 +631,14 @@ DPUF_EXPORT void* dpuf_engine_create(const DpufModelConfig* cfg, const DpufLayer
         e->h_logits = (float*)dpuf_hip_host_alloc_io((size_t)e->V * 4);
         e->h_emb = (float*)dpuf_hip_host_alloc_io((size_t)e->H * 4);
         e->d_red = dpuf_hip_malloc(DPUF_HIP_RED_SCRATCH);
+        e->d_lmred = dpuf_hip_malloc((size_t)(LM_RED_CAP + 1) * 16);
         e->d_ms_kc = (float**)dpuf_hip_malloc(B * 2 * sizeof(float*) + B * 8);
         if (!e->d_ms_kc) goto fail;
         e->d_ms_vc = e->d_ms_kc + B;
         e->d_ms_pos = (int32_t*)(e->d_ms_vc + B);
         e->d_ms_tok = e->d_ms_pos + B;
         if (!e->h || !e->h2 || !e->hn || !e->q || !e->k || !e->v || !e->ao || !e->gate || !e->up || !e->logits ||
-            !e->scores || !e->embeds || !e->d_ids || !e->h_pinned || !e->h_io || !e->h_logits || !e->h_emb || !e->d_red)
+            !e->scores || !e->embeds || !e->d_ids || !e->h_pinned || !e->h_io || !e->h_logits || !e->h_emb || !e->d_red || !e->d_lmred)
             goto fail;
         e->d_pos0 = e->d_ids + B;
         e->d_flag = e->d_ids + B + 1;
@@ -803,8 +809,8 @@ static void enqueue_forward(Engine* e, int32_t M, int32_t use_embeds, int32_t on
     dpuf_hip_embed(e->stream, e->tok, e->h_io, M, emb, M == 1, e->h, e->h_io + IO_POS, e->d_pos0, e->d_serial);
     e->hcur = e->h;
     enqueue_layers(e, M, keep_tiles);
-    const int flag_valid = enqueue_head(e, M, only_last, early_tiles, early_margin, want_argmax, lm_host);
-    dpuf_hip_publish(e->stream, e->d_flag, flag_valid, e->h_io + IO_OUT);
+    const int hr = enqueue_head(e, M, only_last, early_tiles, early_margin, want_argmax, lm_host);
+    if (!(hr & 2)) dpuf_hip_publish(e->stream, e->d_flag, hr & 1, e->h_io + IO_OUT);
 }
 
 /* Layer loop: residual + RMSNorm + prep, fused Q/K/V GEMV, attention (for
@@ -1060,7 +1066,9 @@ static void enqueue_layers(Engine* e, int32_t M, int32_t keep_tiles) {
 
 /* Final residual + output RMSNorm + LM head (with the optional Zone-A early
  * exit) and the device argmax; reads the residual stream h (+ hn).  Returns
- * whether the early-exit flag was computed. */
+ * bit 0: the early-exit flag was computed; bit 1: the step's result words
+ * are already published (a one-row argmax step: the LM-head GEMV's chains
+ * write partials that one workgroup merges, publishing the token). */
 static int enqueue_head(Engine* e, int32_t M, int32_t only_last, int32_t early_tiles, float early_margin,
                         int32_t want_argmax, float* lm_host) {
     void* s = e->stream;
@@ -1083,20 +1091,35 @@ static int enqueue_head(Engine* e, int32_t M, int32_t only_last, int32_t early_t
         int32_t za = early_tiles < 256 ? 256 : early_tiles;
         if (za > nt) za = nt;
         int32_t nz = za * 16 < e->V ? za * 16 : e->V;
+        /* the partials of one launch are merged before the next launch
+         * writes its own over them */
+        void* zone = (char*)e->d_lmred + (size_t)LM_RED_CAP * 16;
         DpufGemvJob j0 = job(&e->lm, 0, za, e->prep[0], e->logits, e->V);
         const int tm11 = tm_begin(e, K_LM, gemv_bytes(&e->lm, 0, za, 1));
-        dpuf_hip_gemv(s, 1, 1, &j0, NULL, 0.0f);
-        dpuf_hip_topcheck(s, e->logits, nz, early_margin, e->d_flag, e->d_red);
+        const int32_t n0 = dpuf_hip_gemv_red(s, &j0, NULL, 0.0f, e->d_lmred, LM_RED_CAP);
+        dpuf_hip_lm_zone(s, e->d_lmred, n0 > 0 ? n0 : 0, early_margin, e->d_flag, zone);
+        int32_t n1 = 0;
         if (za < nt) {
             DpufGemvJob j1 = job(&e->lm, za, nt, e->prep[0], e->logits, e->V);
-            dpuf_hip_gemv(s, 1, 1, &j1, e->d_flag, -1e9f);
+            n1 = dpuf_hip_gemv_red(s, &j1, e->d_flag, -1e9f, e->d_lmred, LM_RED_CAP);
         }
         tm_end(e, tm11);
-        if (want_argmax) dpuf_hip_argmax(s, e->logits, e->V, e->d_tok, e->d_red);
+        if (want_argmax) {
+            dpuf_hip_lm_argmax_publish(s, e->d_lmred, n1 > 0 ? n1 : 0, zone, -1e9f, nz < e->V ? nz : -1, e->logits,
+                                       e->d_flag, 1, e->h_io + IO_OUT);
+            return 3;
+        }
         return 1;
     }
     DpufGemvJob j = job(&e->lm, 0, nt, e->prep[0], lm_host && lmM == 1 ? lm_host : e->logits, e->V);
     const int tm12 = tm_begin(e, K_LM, gemv_bytes(&e->lm, 0, nt, lmM));
+    if (want_argmax && lmM == 1 && !lm_host) {
+        const int32_t n = dpuf_hip_gemv_red(s, &j, NULL, 0.0f, e->d_lmred, LM_RED_CAP);
+        tm_end(e, tm12);
+        dpuf_hip_lm_argmax_publish(s, e->d_lmred, n > 0 ? n : 0, NULL, 0.0f, -1, e->logits, e->d_flag, 0,
+                                   e->h_io + IO_OUT);
+        return 2;
+    }
     dpuf_hip_gemv(s, lmM, 1, &j, NULL, 0.0f);
     tm_end(e, tm12);
     if (want_argmax) dpuf_hip_argmax(s, e->logits + (size_t)(lmM - 1) * e->V, e->V, e->d_tok, e->d_red);

@@ -120,6 +120,10 @@ struct MvArgs {
     int nc;     // chain waves: MV_NC, or 0 when every workgroup has one group
     const int32_t* skip_flag;
     float fill;
+    // LM-head reductions: when set, every chain (each chain wave, or wave 0
+    // of a one-group workgroup) writes the partial of the rows it computed,
+    // red[workgroup * chains per workgroup + chain] (not on a skipped launch)
+    lm4* red;
     int32_t* err;  // device error word: bit 0 set when a bounded LDS wait ran out
     // Producer-fed launch (one job, one group per workgroup, activations
     // held for the launch): the first np workgroups compute the job's
@@ -305,7 +309,8 @@ DEV void mv_consume(const MvGeo& G, int u, int w, int lane, const MvU<NL>& L, co
 // loader waves have published their pairs, run the 8 rows' chains on lanes
 // 0..7 at raised issue priority, write the rows, free the buffer.  Every wait
 // is bounded.
-DEV void mv_chains(const MvGeo& G, int c, int n_my, int lane, uint8_t* smem, MvSync* sy) {
+DEV void mv_chains(const MvGeo& G, int c, int n_my, int lane, uint8_t* smem, MvSync* sy, lm4* red) {
+    lm4 part = lm_part_init();
     for (int lg = c; lg < n_my; lg += MV_NC) {
         const int buf = lg % G.nbuf;
         // arrivals in this buffer are cumulative: use lg / nbuf of the buffer is
@@ -319,11 +324,18 @@ DEV void mv_chains(const MvGeo& G, int c, int n_my, int lane, uint8_t* smem, MvS
             const float2* pairs = (const float2*)smem + (size_t)buf * 8 * G.ld;
             const float acc = run_chain<MV_CHAIN>((const float4*)(pairs + lane * G.ld), G.n_blk >> 1);
             const int r = (G.g0 + G.lb + lg * G.nwg) * 8 + lane;
-            if (r < G.rows) G.out[r] = acc;
+            if (r < G.rows) {
+                G.out[r] = acc;
+                if (red) part = lm_part_take(part, acc, r);
+            }
         }
         __builtin_amdgcn_s_setprio(0);
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
         if (lane == 0) __hip_atomic_store(&sy->done[buf], lg, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+    if (red) {
+        part = lm_part_wave(part);
+        if (lane == 0) red[blockIdx.x * MV_NC + c] = part;
     }
 }
 
@@ -416,7 +428,7 @@ __global__ __launch_bounds__(1024) void k_mv(MvArgs A) {
     }
     __syncthreads();
     if (w >= G.NW) {
-        mv_chains(G, w - G.NW, n_my, lane, smem, &sy);
+        mv_chains(G, w - G.NW, n_my, lane, smem, &sy, A.red);
         return;
     }
     if (SINGLE) {
@@ -449,10 +461,20 @@ __global__ __launch_bounds__(1024) void k_mv(MvArgs A) {
             }
         }
         __syncthreads();
-        if (w == 0 && lane < 8) {
-            const float acc = run_chain<MV_CHAIN1>((const float4*)((float2*)smem + lane * G.ld), G.n_blk >> 1);
-            const int r = G.g0 * 8 + G.lb * 8 + lane;
-            if (r < G.rows) G.out[r] = acc;
+        if (w == 0) {
+            lm4 part = lm_part_init();
+            if (lane < 8) {
+                const float acc = run_chain<MV_CHAIN1>((const float4*)((float2*)smem + lane * G.ld), G.n_blk >> 1);
+                const int r = G.g0 * 8 + G.lb * 8 + lane;
+                if (r < G.rows) {
+                    G.out[r] = acc;
+                    if (A.red) part = lm_part_take(part, acc, r);
+                }
+            }
+            if (A.red) {
+                part = lm_part_wave(part);
+                if (lane == 0) A.red[blockIdx.x] = part;
+            }
         }
         return;
     }
@@ -593,25 +615,33 @@ static int mv_plan(int n_jobs, const int* n_groups, int K, int mode, MvKernel& k
     return total;
 }
 
-// One launch over jobs of one mode.
-static void mv_launch(void* s, MvArgs& A, const int* n_groups, int mode) {
+// One launch over jobs of one mode; returns the chains of the launch (the
+// partials it writes when A.red is set), 0 when there is nothing to launch,
+// -1 on an error (reported), including more chains than red_cap.
+static int mv_launch(void* s, MvArgs& A, const int* n_groups, int mode, int red_cap = 0) {
     const int n_blk = A.K >> 5;
     MvKernel k, k1;
     int nw, most;
-    if (mv_plan(A.n_jobs, n_groups, A.K, mode, k, k1, nw, A.wb, most) == 0) return;
+    if (mv_plan(A.n_jobs, n_groups, A.K, mode, k, k1, nw, A.wb, most) == 0) return 0;
     const int grid = A.wb[A.n_jobs];
     const size_t buf = (size_t)8 * (n_blk + 2) * 8;
     if (!g_err_word) {
         note(hipErrorInvalidValue, "dpuf_hip_gemv: no device error word bound");
-        return;
+        return -1;
     }
     A.err = g_err_word;
     A.nbuf = most < MV_NBUF ? most : MV_NBUF;
     A.nc = most > 1 ? MV_NC : 0;
+    const int chains = grid * (A.nc ? MV_NC : 1);
+    if (A.red && chains > red_cap) {
+        note(hipErrorInvalidValue, "dpuf_hip_gemv_red: more partials than the buffer holds");
+        return -1;
+    }
     const int threads = (nw + A.nc) * 64;
     const size_t lds = (size_t)A.nbuf * buf;
     hipLaunchKernelGGL(A.nc ? k : k1, dim3(grid), dim3(threads), lds, ST(s), A);
     LAUNCHED("k_mv");
+    return chains;
 }
 
 // The producer-fed instance with nl steps per loader wave.
@@ -761,6 +791,30 @@ void dpuf_hip_gemv(void* s, int32_t M, int32_t n_jobs, const DpufGemvJob* jobs, 
     }
 }
 
+
+int32_t dpuf_hip_gemv_red(void* s, const DpufGemvJob* job, const int32_t* skip_flag, float fill, void* red,
+                          int32_t red_cap) {
+    const int mode = job->w.mode;
+    if ((mode != 12 && mode != 13 && mode != 14) || !red || red_cap <= 0) {
+        note(hipErrorInvalidValue, "dpuf_hip_gemv_red: bad arguments");
+        return -1;
+    }
+    MvArgs A;
+    memset(&A, 0, sizeof A);
+    A.n_jobs = 1;
+    A.K = job->w.cols;
+    A.j[0].g = job->w.g;
+    A.j[0].out = job->out;
+    A.j[0].g0 = job->g0;
+    A.j[0].g1 = job->g1;
+    A.j[0].rows = job->w.rows;
+    A.j[0].x = job->p;
+    A.skip_flag = skip_flag;
+    A.fill = fill;
+    A.red = (lm4*)red;
+    const int ng = job->g1 - job->g0 > 0 ? job->g1 - job->g0 : 0;
+    return mv_launch(s, A, &ng, mode, red_cap);
+}
 
 int dpuf_hip_mv_max_wg(void) { return g_mv_max_wg; }
 

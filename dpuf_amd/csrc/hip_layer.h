@@ -124,6 +124,22 @@ void dpuf_hip_embed(void* s, DpufDevW w, const int32_t* ids, int32_t M, const fl
 /* host[0..3) = {flag_valid ? words[0] : 0, words[1], words[2]} (words: the
  * device's early-exit flag, argmax token, error word) */
 void dpuf_hip_publish(void* s, const int32_t* words, int32_t flag_valid, int32_t* host);
+/* The one-row GEMV of job (as dpuf_hip_gemv with M = 1) whose chains also
+ * write partials of the LM-head reductions (top-2 and first maximum of the
+ * rows each computed; 16 bytes each) to red; returns their count (-1 on an
+ * error, including more than red_cap).  With skip_flag set the rows are
+ * filled and no partial is written. */
+int32_t dpuf_hip_gemv_red(void* s, const DpufGemvJob* job, const int32_t* skip_flag, float fill, void* red,
+                          int32_t red_cap);
+/* One workgroup over the zone rows' n partials: *flag = the early-exit test
+ * (thr > 0 and top-1 - top-2 >= thr), zone (16 bytes) = their merge. */
+void dpuf_hip_lm_zone(void* s, const void* part, int32_t n, float thr, int32_t* flag, void* zone);
+/* One workgroup: the first maximum of the row from n partials (with zone:
+ * the zone's merge plus, when words[0] is set, the fill value from row
+ * fill_row on instead of the partials), 0 when *x0 is NaN; writes it to
+ * words[1] and publishes words as dpuf_hip_publish does. */
+void dpuf_hip_lm_argmax_publish(void* s, const void* part, int32_t n, const void* zone, float fill, int32_t fill_row,
+                                const float* x0, int32_t* words, int32_t flag_valid, int32_t* host);
 /* h_out = h + res for M rows of H (res NULL: no add, h_out unused), then
  * the RMSNorm of that sum (of h when res is NULL) with weights w and the
  * prep of the result for each of the n_prep sign vectors into preps[i] (and

@@ -455,38 +455,6 @@ __global__ void k_capture(int H, const float* h, const float* hn, float* cap) {
 // partials.  Scratch: RED_NB partials of 8 bytes.
 #define RED_NB 64
 
-// Top-2 with multiplicity (the reference's sequential b1/b2 scan,
-// dpuf_engine.c:2101-2110, is order independent), then the early-exit
-// decision b1 - b2 >= thr (thr > 0).
-DEV void top2_take(float v, float& b1, float& b2) {
-    if (v > b1) {
-        b2 = b1;
-        b1 = v;
-    } else if (v > b2) {
-        b2 = v;
-    }
-}
-
-DEV void top2_merge(float& b1, float& b2, float c1, float c2) {
-    if (b1 >= c1) {
-        b2 = fmaxf(b2, c1);
-    } else {
-        b2 = fmaxf(c2, b1);
-        b1 = c1;
-    }
-}
-
-// First maximum (dpuf-cli.c:1997-2004: `if (x[i] > best)` from best = x[0]):
-// the larger value, the smaller index on ties; every partial starts from
-// (x[0], 0), so a NaN x[0] gives 0 as the reference does and other NaNs are
-// never taken.
-DEV void amax_merge(float& bv, int& bi, float v, int i) {
-    if (v > bv || (v == bv && i < bi)) {
-        bv = v;
-        bi = i;
-    }
-}
-
 __global__ __launch_bounds__(256) void k_red_part(const float* __restrict__ x, int n, int argmax, float2* part) {
     __shared__ float2 wp[4];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -782,6 +750,68 @@ __global__ void k_publish(const int32_t* __restrict__ words, int flag_valid, int
         host[1] = words[1];
         host[2] = words[2];
     }
+}
+
+// The LM-head reductions finished by one workgroup from the partials the
+// GEMV's chains wrote (dpuf_hip_gemv_red), merged in any order.
+DEV lm4 lm_block_merge(const lm4* __restrict__ part, int n) {  // 256 threads; the result in thread 0
+    __shared__ lm4 sh[4];
+    lm4 p = lm_part_init();
+    for (int i = threadIdx.x; i < n; i += 256) p = lm_part_merge(p, part[i]);
+    p = lm_part_wave(p);
+    if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = p;
+    __syncthreads();
+    if (threadIdx.x == 0)
+        for (int k = 1; k < 4; k++) p = lm_part_merge(p, sh[k]);
+    return p;
+}
+
+// Zone-A check over the zone rows' partials: *flag = (thr > 0 && top-1 -
+// top-2 >= thr) (dpuf_engine.c:2091-2136), *zone = the merged partial.
+__global__ __launch_bounds__(256) void k_lm_zone(const lm4* __restrict__ part, int n, float thr, int32_t* flag,
+                                                 lm4* zone) {
+    const lm4 p = lm_block_merge(part, n);
+    if (threadIdx.x == 0) {
+        *flag = (thr > 0.0f && (p[0] - p[1]) >= thr) ? 1 : 0;
+        *zone = p;
+    }
+}
+
+// The row's first maximum (dpuf-cli.c:1997-2004), then the step's result
+// words to host as k_publish does.  Without zone: over the n partials.  With
+// zone (an early-exit step, the flag in words[0]): the zone's merged
+// partial and, when the flag is set, the filled rows (fill from fill_row on;
+// fill_row < 0: none) in place of the n partials of the other rows.  A NaN
+// logit 0 gives 0 (the reference's scan starts from x[0]).  words = {flag,
+// token, error word}; the token goes to words[1].
+__global__ __launch_bounds__(256) void k_lm_argmax_publish(const lm4* __restrict__ part, int n,
+                                                           const lm4* __restrict__ zone, float fill, int fill_row,
+                                                           const float* __restrict__ x0, int32_t* words,
+                                                           int flag_valid, int32_t* host) {
+    const int32_t flag = zone ? words[0] : 0;  // uniform
+    lm4 p = flag ? lm_part_init() : lm_block_merge(part, n);
+    if (threadIdx.x == 0) {
+        if (zone) p = lm_part_merge(p, *zone);
+        if (flag && fill_row >= 0) p = lm_part_take(p, fill, fill_row);
+        const float v0 = *x0;
+        const int32_t tok = v0 != v0 ? 0 : __float_as_int(p[3]);
+        words[1] = tok;
+        host[0] = flag_valid ? flag : 0;
+        host[1] = tok;
+        host[2] = words[2];
+    }
+}
+
+void dpuf_hip_lm_zone(void* s, const void* part, int32_t n, float thr, int32_t* flag, void* zone) {
+    hipLaunchKernelGGL(k_lm_zone, dim3(1), dim3(256), 0, ST(s), (const lm4*)part, n, thr, flag, (lm4*)zone);
+    LAUNCHED("k_lm_zone");
+}
+
+void dpuf_hip_lm_argmax_publish(void* s, const void* part, int32_t n, const void* zone, float fill, int32_t fill_row,
+                                const float* x0, int32_t* words, int32_t flag_valid, int32_t* host) {
+    hipLaunchKernelGGL(k_lm_argmax_publish, dim3(1), dim3(256), 0, ST(s), (const lm4*)part, n, (const lm4*)zone,
+                       fill, fill_row, x0, words, flag_valid, host);
+    LAUNCHED("k_lm_argmax_publish");
 }
 
 void dpuf_hip_publish(void* s, const int32_t* words, int32_t flag_valid, int32_t* host) {
