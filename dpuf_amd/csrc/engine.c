@@ -21,7 +21,7 @@
 
 #define N_SLOTS 8
 #define N_GRAPHS 8  /* captured one-token steps kept per engine */
-#define LM_RED_CAP 8192 /* LM-head partials (chains of one GEMV launch) */
+#define LM_RED_CAP 16384 /* LM-head partials (chains of one GEMV launch); also the row argmax scratch */
 #define N_PREFIX 8
 #define N_KINDS 8
 #define MAX_EVENTS 8192
@@ -94,6 +94,12 @@ typedef struct {
     int32_t* h_io;
     float* h_logits;
     float* h_emb;
+    /* multi-session steps: the pinned staging of the per-session tables,
+     * laid out as on the device (B cache bases of K, B of V, then B
+     * positions: one copy), and the next tokens, which the argmax kernel
+     * writes to this fine-grained host array itself */
+    void* h_ms;
+    int32_t* h_tok;
     uint8_t* q_idx;      /* per layer: prep index of q,k,v (3 bytes) and gate/up (2 bytes) */
     float deadzone;
     void* stream;
@@ -513,6 +519,8 @@ static void engine_free(Engine* e) {
     dpuf_hip_host_free(e->h_io);
     dpuf_hip_host_free(e->h_logits);
     dpuf_hip_host_free(e->h_emb);
+    dpuf_hip_host_free(e->h_ms);
+    dpuf_hip_host_free(e->h_tok);
     for (int i = 0; i < MAX_EVENTS; i++) if (e->ev[i]) dpuf_hip_event_destroy(e->ev[i]);
     if (e->stream) dpuf_hip_stream_destroy(e->stream);
     free(e);
@@ -630,6 +638,8 @@ DPUF_EXPORT void* dpuf_engine_create(const DpufModelConfig* cfg, const DpufLayer
         e->h_io = (int32_t*)dpuf_hip_host_alloc_io((B + 64) * 4);
         e->h_logits = (float*)dpuf_hip_host_alloc_io((size_t)e->V * 4);
         e->h_emb = (float*)dpuf_hip_host_alloc_io((size_t)e->H * 4);
+        e->h_ms = dpuf_hip_host_alloc(B * 2 * sizeof(float*) + B * 4);
+        e->h_tok = (int32_t*)dpuf_hip_host_alloc_io(B * 4);
         e->d_red = dpuf_hip_malloc(DPUF_HIP_RED_SCRATCH);
         e->d_lmred = dpuf_hip_malloc((size_t)(LM_RED_CAP + 1) * 16);
         e->d_ms_kc = (float**)dpuf_hip_malloc(B * 2 * sizeof(float*) + B * 8);
@@ -638,7 +648,7 @@ DPUF_EXPORT void* dpuf_engine_create(const DpufModelConfig* cfg, const DpufLayer
         e->d_ms_pos = (int32_t*)(e->d_ms_vc + B);
         e->d_ms_tok = e->d_ms_pos + B;
         if (!e->h || !e->h2 || !e->hn || !e->q || !e->k || !e->v || !e->ao || !e->gate || !e->up || !e->logits ||
-            !e->scores || !e->embeds || !e->d_ids || !e->h_pinned || !e->h_io || !e->h_logits || !e->h_emb || !e->d_red || !e->d_lmred)
+            !e->scores || !e->embeds || !e->d_ids || !e->h_pinned || !e->h_io || !e->h_logits || !e->h_emb || !e->d_red || !e->d_lmred || !e->h_ms || !e->h_tok)
             goto fail;
         e->d_pos0 = e->d_ids + B;
         e->d_flag = e->d_ids + B + 1;
@@ -1271,16 +1281,10 @@ DPUF_EXPORT int32_t dpuf_amd_engine_forward_slots(void* handle, int32_t n, const
      * at most DPUF_HIP_DEC_MAX_KEYS keys) first, the others after them;
      * ord[m] is the caller's index of batch row m */
     int32_t* ord = (int32_t*)malloc((size_t)n * sizeof(int32_t));
-    float** ptrs = (float**)malloc((size_t)n * 2 * sizeof(float*));
-    int32_t* pos = (int32_t*)malloc((size_t)n * sizeof(int32_t));
     float* lg = logits_out ? (float*)malloc((size_t)n * e->V * sizeof(float)) : NULL;
-    int32_t* tk = tokens_out ? (int32_t*)malloc((size_t)n * sizeof(int32_t)) : NULL;
-    if (!ord || !ptrs || !pos || (logits_out && !lg) || (tokens_out && !tk)) {
+    if (!ord || (logits_out && !lg)) {
         free(ord);
-        free(ptrs);
-        free(pos);
         free(lg);
-        free(tk);
         return -2;
     }
     int32_t ns = 0;
@@ -1293,20 +1297,22 @@ DPUF_EXPORT int32_t dpuf_amd_engine_forward_slots(void* handle, int32_t n, const
     while (ns < n && !is_q8(e) && positions[ord[ns]] + 1 <= ATT_SPLIT_MIN) ns++;
     begin_call(e);
     volatile int32_t* io = e->h_io;
+    float** hk = (float**)e->h_ms;
+    int32_t* hpos = (int32_t*)(hk + 2 * DPUF_AMD_MAX_BATCH);
     for (int32_t m = 0; m < n; m++) {
         const int32_t i = ord[m];
-        ptrs[m] = is_q8(e) ? NULL : slot_k(e, slot_ids[i]);
-        ptrs[n + m] = is_q8(e) ? NULL : slot_v(e, slot_ids[i]);
-        pos[m] = positions[i];
+        hk[m] = is_q8(e) ? NULL : slot_k(e, slot_ids[i]);
+        hk[DPUF_AMD_MAX_BATCH + m] = is_q8(e) ? NULL : slot_v(e, slot_ids[i]);
+        hpos[m] = positions[i];
         e->ms_slot[m] = slot_ids[i];
         e->ms_pos[m] = positions[i];
         io[m] = token_ids[i];
     }
     io[IO_POS] = 0;
     io[IO_POS + 1] = next_serial(e);
-    dpuf_hip_h2d(e->d_ms_pos, pos, (size_t)n * 4, e->stream);
-    dpuf_hip_h2d(e->d_ms_kc, ptrs, (size_t)n * sizeof(float*), e->stream);
-    dpuf_hip_h2d(e->d_ms_vc, ptrs + n, (size_t)n * sizeof(float*), e->stream);
+    /* the tables in one copy (the device layout: d_ms_vc and d_ms_pos follow
+     * d_ms_kc) */
+    dpuf_hip_h2d(e->d_ms_kc, e->h_ms, (size_t)2 * DPUF_AMD_MAX_BATCH * sizeof(float*) + (size_t)n * 4, e->stream);
     int32_t keep = 0;
     env_int("DPUF_GEN_KEEP_TILES", &keep);
     e->ms_n = n;
@@ -1316,26 +1322,20 @@ DPUF_EXPORT int32_t dpuf_amd_engine_forward_slots(void* handle, int32_t n, const
     enqueue_forward(e, n, 0, 0, keep, 0, 1.25f, 0, NULL);
     e->ms_n = 0;
     e->ms_short = 0;
-    if (tokens_out)
-        for (int32_t m = 0; m < n; m++)
-            dpuf_hip_argmax(e->stream, e->logits + (size_t)m * e->V, e->V, e->d_ms_tok + m, e->d_red);
+    if (tokens_out) dpuf_hip_argmax_rows(e->stream, e->logits, e->V, n, e->d_ms_tok, e->h_tok, e->d_lmred);
     tm_end(e, tm);
     if (logits_out) dpuf_hip_d2h(lg, e->logits, (size_t)n * e->V * 4, e->stream);
-    if (tokens_out) dpuf_hip_d2h(tk, e->d_ms_tok, (size_t)n * 4, e->stream);
     const int32_t rc = dpuf_hip_sync(e->stream);
     tm_collect(e);
     int32_t out = rc != 0 ? -6 : end_call(e, io[IO_OUT + 2]);
     if (out == 0) {
         for (int32_t m = 0; m < n; m++) {
             if (logits_out) memcpy(logits_out + (size_t)ord[m] * e->V, lg + (size_t)m * e->V, (size_t)e->V * 4);
-            if (tokens_out) tokens_out[ord[m]] = tk[m];
+            if (tokens_out) tokens_out[ord[m]] = ((volatile int32_t*)e->h_tok)[m];
         }
     }
     free(ord);
-    free(ptrs);
-    free(pos);
     free(lg);
-    free(tk);
     return out;
 }
 

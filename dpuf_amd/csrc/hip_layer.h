@@ -243,6 +243,11 @@ void dpuf_hip_capture(void* s, int32_t M, int32_t H, const float* h, const float
 #define DPUF_HIP_RED_SCRATCH 512
 void dpuf_hip_topcheck(void* s, const float* logits, int32_t n, float thr, int32_t* flag, void* scratch);
 void dpuf_hip_argmax(void* s, const float* logits, int32_t V, int32_t* out, void* scratch);
+/* The first-max argmax of n rows of V logits (rows V apart) into out[0..n)
+ * and, when host is set, host[0..n) (fine-grained host memory); scratch
+ * holds n x 512 bytes of partials. */
+void dpuf_hip_argmax_rows(void* s, const float* logits, int32_t V, int32_t n, int32_t* out, int32_t* host,
+                          void* scratch);
 /* The same reductions with the partials in the library's own file-scope
  * device array (one per device, RED_NB float2): no allocation.  mode 1
  * argmax, 0 top-2 check.  Concurrent calls on one device share the array.

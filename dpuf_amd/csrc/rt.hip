@@ -455,7 +455,12 @@ __global__ void k_capture(int H, const float* h, const float* hn, float* cap) {
 // partials.  Scratch: RED_NB partials of 8 bytes.
 #define RED_NB 64
 
-__global__ __launch_bounds__(256) void k_red_part(const float* __restrict__ x, int n, int argmax, float2* part) {
+// Row blockIdx.y of rows ldx apart (one row: gridDim.y = 1), its partials at
+// part + RED_NB blockIdx.y.
+__global__ __launch_bounds__(256) void k_red_part(const float* __restrict__ x, int n, int argmax, float2* part,
+                                                  int ldx) {
+    x += (size_t)blockIdx.y * ldx;
+    part += (size_t)blockIdx.y * RED_NB;
     __shared__ float2 wp[4];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     // h leading elements up to 16-byte alignment (workgroup 0), then float4
@@ -527,8 +532,13 @@ __global__ __launch_bounds__(256) void k_red_part(const float* __restrict__ x, i
 
 // One wave: merge the RED_NB partials; argmax writes the index to out[0],
 // the top-2 check writes out[0] = (thr > 0 && b1 - b2 >= thr).
+// Row blockIdx.x's partials (part + RED_NB blockIdx.x) to out[blockIdx.x]; with
+// host set, argmax also stores the index to host[blockIdx.x] (fine-grained
+// host memory the caller reads after the stream drains).
 __global__ __launch_bounds__(64) void k_red_fin(const float2* __restrict__ part, int argmax, float thr,
-                                                int32_t* out) {
+                                                int32_t* out, int32_t* host) {
+    part += (size_t)blockIdx.x * RED_NB;
+    out += blockIdx.x;
     const int lane = threadIdx.x;
     // lanes past the partials hold the identity (argmax: partial 0 again)
     float2 r = lane < RED_NB ? part[lane] : (argmax ? part[0] : make_float2(-1e30f, -1e30f));
@@ -544,7 +554,10 @@ __global__ __launch_bounds__(64) void k_red_fin(const float2* __restrict__ part,
             top2_merge(r.x, r.y, oa, ob);
         }
     }
-    if (lane == 0) *out = argmax ? ri : ((thr > 0.0f && (r.x - r.y) >= thr) ? 1 : 0);
+    if (lane == 0) {
+        *out = argmax ? ri : ((thr > 0.0f && (r.x - r.y) >= thr) ? 1 : 0);
+        if (host && argmax) host[blockIdx.x] = ri;
+    }
 }
 
 
@@ -909,15 +922,23 @@ void dpuf_hip_capture(void* s, int32_t M, int32_t H, const float* h, const float
 }
 
 void dpuf_hip_topcheck(void* s, const float* logits, int32_t n, float thr, int32_t* flag, void* scratch) {
-    hipLaunchKernelGGL(k_red_part, dim3(RED_NB), dim3(256), 0, ST(s), logits, n, 0, (float2*)scratch);
-    hipLaunchKernelGGL(k_red_fin, dim3(1), dim3(64), 0, ST(s), (const float2*)scratch, 0, thr, flag);
+    hipLaunchKernelGGL(k_red_part, dim3(RED_NB), dim3(256), 0, ST(s), logits, n, 0, (float2*)scratch, 0);
+    hipLaunchKernelGGL(k_red_fin, dim3(1), dim3(64), 0, ST(s), (const float2*)scratch, 0, thr, flag, nullptr);
     LAUNCHED("k_red_part/k_red_fin (top-2 check)");
 }
 
 void dpuf_hip_argmax(void* s, const float* logits, int32_t V, int32_t* out, void* scratch) {
-    hipLaunchKernelGGL(k_red_part, dim3(RED_NB), dim3(256), 0, ST(s), logits, V, 1, (float2*)scratch);
-    hipLaunchKernelGGL(k_red_fin, dim3(1), dim3(64), 0, ST(s), (const float2*)scratch, 1, 0.0f, out);
+    hipLaunchKernelGGL(k_red_part, dim3(RED_NB), dim3(256), 0, ST(s), logits, V, 1, (float2*)scratch, 0);
+    hipLaunchKernelGGL(k_red_fin, dim3(1), dim3(64), 0, ST(s), (const float2*)scratch, 1, 0.0f, out, nullptr);
     LAUNCHED("k_red_part/k_red_fin (argmax)");
+}
+
+void dpuf_hip_argmax_rows(void* s, const float* logits, int32_t V, int32_t n, int32_t* out, int32_t* host,
+                          void* scratch) {
+    if (n <= 0) return;
+    hipLaunchKernelGGL(k_red_part, dim3(RED_NB, n), dim3(256), 0, ST(s), logits, V, 1, (float2*)scratch, V);
+    hipLaunchKernelGGL(k_red_fin, dim3(n), dim3(64), 0, ST(s), (const float2*)scratch, 1, 0.0f, out, host);
+    LAUNCHED("k_red_part/k_red_fin (argmax of rows)");
 }
 
 // The allocation-free reduction entry's partials: one file-scope array per
@@ -954,8 +975,9 @@ int32_t dpuf_hip_reduce_noalloc(const float* x, int32_t n, int32_t mode, float t
     if (!part) return -6;
     // every partial slot is written by its workgroup before k_red_fin reads
     // it, so nothing from an earlier call needs clearing
-    hipLaunchKernelGGL(k_red_part, dim3(RED_NB), dim3(256), 0, ST(s), x, n, mode, part);
-    hipLaunchKernelGGL(k_red_fin, dim3(1), dim3(64), 0, ST(s), (const float2*)part, mode, mode ? 0.0f : thr, out);
+    hipLaunchKernelGGL(k_red_part, dim3(RED_NB), dim3(256), 0, ST(s), x, n, mode, part, 0);
+    hipLaunchKernelGGL(k_red_fin, dim3(1), dim3(64), 0, ST(s), (const float2*)part, mode, mode ? 0.0f : thr, out,
+                       nullptr);
     LAUNCHED("k_red_part/k_red_fin (allocation-free)");
     return g_err == hipSuccess ? 0 : -6;
 }
