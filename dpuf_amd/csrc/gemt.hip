@@ -18,31 +18,40 @@
 #include <stdint.h>
 #include <string.h>
 
+#include <type_traits>
+
 #include "hip_layer.h"
 #include "dev_common.h"
 #include "hip_internal.h"
 
 // ---------------------------------------------------------------------------
-// R waves compute a 16-row fragment (two 8-row groups) for all M tokens,
-// walking the blocks of K in order with the accumulators in registers (MFMA
-// D layout: lane l holds token l % 16, rows 4 (l / 16) + v); each of the R
-// waves repeats the fragment's MFMAs and runs the chains of 4 / R of the four
-// D components (R = 1 for large matrices, 2 or 4 when the fragments alone
-// would leave SIMDs idle).  No chain crosses a wave and no wave waits for
-// another after the staging.
+// R waves compute a unit of P 16-row fragments (two 8-row groups each) for
+// all M tokens, walking the blocks of K in order with the accumulators in
+// registers.  MFMA D layout: lane l holds token column l % 16, rows
+// 4 (l / 16) + v.  Each of the R waves repeats the unit's MFMAs and runs the
+// chains of 4 / R of the four D components (R = 1 for large matrices, 2 or 4
+// when the units alone would leave SIMDs idle).  No chain crosses a wave and
+// no wave waits for another after the staging.
+//
+//   * 9..16 tokens (NT = 16 staged): P = 1, every D column is a token.
+//   * up to 8 tokens (NT = 8): P = 2.  Lanes of columns 8..15 read token
+//     l % 8, so each fragment's D repeats tokens 0..7 in both halves of every
+//     16-lane row; one DPP move per register (row_shr:8, banks 2-3) puts
+//     fragment b's columns 0..7 into columns 8..15 of fragment a's register,
+//     so every lane of the chain instructions carries a distinct (row, token):
+//     lane (i, kc) chains fragment i / 8, token i % 8.  Half the chain
+//     instructions of two single-fragment waves, for one extra move each.
 //
 // A workgroup of MT_FW waves serves one job (matrix); it stages that job's
 // activations once into LDS: the int8 values [block][token][32], so that an
-// MFMA B fragment (lane l: token l % 16, columns 8 (l / 16) .. + 7 of the
+// MFMA B fragment (lane l: token l % NT, columns 8 (l / 16) .. + 7 of the
 // block) is one 8-byte read, and the block sums and scales [token][block]
-// (four blocks in one read).  With NT = 8 staged tokens,
-// lanes of tokens 8..15 read token l % 8: their D columns are computed and
-// never stored.
+// (four blocks in one read).
 //
-// Per fragment a wave copies its two groups' fp16 row scales (16 bytes per
-// block) to an LDS area of its own, read per block.  The nibbles stream
-// through a register ring PF 4-block quads deep: per quad one 16-byte buffer
-// load per lane (lane offset fixed per fragment, the quad in the scalar
+// Per unit a wave copies its groups' fp16 row scales (16 bytes per block) to
+// an LDS area of its own, read per block.  The nibbles stream through a
+// register ring PF 4-block quads deep: per quad and fragment one 16-byte
+// buffer load per lane (lane offset fixed per unit, the quad in the scalar
 // offset), row l % 16's bytes of block b0 + l / 16; a 4 x 4 transpose across
 // the wave's 16-lane rows gives lane (i, kc) column chunk kc of all four
 // blocks, the MFMA A layout.
@@ -71,16 +80,20 @@ struct MtArgs {
 };
 
 // LDS bytes of a workgroup: the staged activations of NT tokens (40 bytes
-// per token and block) and each wave's copy of two groups' row scales, every
+// per token and block) and each wave's copy of 2 P groups' row scales, every
 // array with 4 blocks of padding (the reads one quad ahead run into it after
 // the last quad; the scale rows of different tokens start on different banks).
-static constexpr size_t mt_lds(int n_blk, int nt) { return (size_t)(n_blk + 4) * (nt * 40 + MT_FW * 32); }
+static constexpr size_t mt_lds(int n_blk, int nt, int p) {
+    return (size_t)(n_blk + 4) * (nt * 40 + MT_FW * 32 * p);
+}
 
-template <int NT, int R>
+template <int NT, int R, int P>
 __global__ __launch_bounds__(64 * MT_FW) void k_mvt(MtArgs A) {
-    constexpr int NV = 4 / R;         // D components per wave
-    constexpr int FPW = MT_FW / R;    // fragments per workgroup round
-    constexpr int PF = R == 1 ? 8 : 12;  // quads of nibbles in flight (even)
+    static_assert(P == 1 || NT == 8, "fragment pairs share the lanes of 8 staged tokens");
+    constexpr int NV = 4 / R;            // D components per wave
+    constexpr int FPW = MT_FW / R;       // units per workgroup round
+    constexpr int PF = R == 1 || P == 2 ? 8 : 12;  // quads of nibbles in flight (even)
+    constexpr int NG = 2 * P;            // groups per unit
     extern __shared__ __align__(16) uint8_t smem[];
     const int bid = blockIdx.x;
     int ji = 0;
@@ -90,11 +103,11 @@ __global__ __launch_bounds__(64 * MT_FW) void k_mvt(MtArgs A) {
     const int K = A.K, M = A.M, n_blk = K >> 5, nq = n_blk >> 2;
     const int tid = threadIdx.x, l = tid & 63, i16 = l & 15, kc = l >> 4;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: the descriptors stay scalar
-    // fragment slot; the wave's rows rotation rho: MFMA row 4c + k holds the
+    // unit slot; the wave's rows rotation rho: MFMA row 4c + k holds the
     // fragment's row 4c + ((k + rho) & 3), so D components 0 .. NV - 1 are
     // the fragment's rows 4c + rho + k, the ones this wave chains
     const int fs = w / R, rho = (w % R) * NV;
-    const int nfr = (J.g1 - J.g0 + 1) >> 1;   // 16-row fragments of the job
+    const int nun = (J.g1 - J.g0 + NG - 1) / NG;  // units of the job
     const int lb = bid - A.wb[ji], nwg = A.wb[ji + 1] - A.wb[ji];
     const uint32_t gstride = (uint32_t)n_blk * 144u;
 
@@ -102,60 +115,66 @@ __global__ __launch_bounds__(64 * MT_FW) void k_mvt(MtArgs A) {
     int8_t* sq = (int8_t*)smem;                             // [nbp][NT][32]
     int32_t* sm = (int32_t*)(smem + (size_t)nbp * NT * 32); // sum8 [NT][nbp]
     float* sx = (float*)(smem + (size_t)nbp * NT * 36);     // xs [NT][nbp]
-    uint8_t* ws = smem + (size_t)nbp * NT * 40 + (size_t)w * nbp * 32;  // [2][nbp][16 B]
+    uint8_t* ws = smem + (size_t)nbp * NT * 40 + (size_t)w * nbp * 16 * NG;  // [NG][nbp][16 B]
 
-    // a fragment's nibble loads: lane row i16 is fragment row ri (group gf +
-    // ri / 8, clamped into the job: a fragment with one group repeats it,
-    // never stored), from a descriptor at group gf
+    // a unit's nibble loads: lane row i16 is row ri of fragment x (group
+    // gf + 2 x + ri / 8, clamped into the job: a missing group repeats the
+    // job's last, never stored), from one descriptor at group gf
     __amdgpu_buffer_rsrc_t rsc;
-    uint32_t won = 0;
-    int ngr = 2;
-    auto frag_setup = [&](int f) {
-        const int gf = J.g0 + 2 * f;
+    uint32_t won[P];
+    int ngr = NG;
+    auto frag_setup = [&](int u) {
+        const int gf = J.g0 + NG * u;
         const int ri = (i16 & 12) + ((i16 + rho) & 3);
-        const int ga = min(gf + (ri >> 3), J.g1 - 1);
-        ngr = J.g1 - gf < 2 ? J.g1 - gf : 2;
+        ngr = J.g1 - gf < NG ? J.g1 - gf : NG;
         rsc = __builtin_amdgcn_make_buffer_rsrc((void*)(J.g + (size_t)gf * gstride), 0, (int)(ngr * gstride),
                                                 MT_RSRC3);
-        won = (uint32_t)(ga - gf) * gstride + (uint32_t)n_blk * 16u + (uint32_t)(ri & 7) * 16u + (uint32_t)kc * 128u;
+#pragma unroll
+        for (int x = 0; x < P; x++) {
+            const int ga = min(gf + 2 * x + (ri >> 3), J.g1 - 1);
+            won[x] = (uint32_t)(ga - gf) * gstride + (uint32_t)n_blk * 16u + (uint32_t)(ri & 7) * 16u +
+                     (uint32_t)kc * 128u;
+        }
     };
-    u32x4 wr[PF];
+    u32x4 wr[P][PF];
     auto quad_load = [&](int p, int qd) {
-        wr[p] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsc, won, qd * 512, 0));
+#pragma unroll
+        for (int x = 0; x < P; x++)
+            wr[x][p] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsc, won[x], qd * 512, 0));
     };
-    // the fragment's row scales for this wave's LDS area: entry e = group
-    // e / n_blk, block e % n_blk (2 n_blk <= 256 entries, 4 per lane), loaded
-    // before the fragment's first nibble quads so that the stores wait for
+    // the unit's row scales for this wave's LDS area: entry e = group
+    // e / n_blk, block e % n_blk (NG n_blk <= 128 NG entries, 2 NG per lane),
+    // loaded before the unit's first nibble quads so that the stores wait for
     // these loads only
-    u32x4 st[4];
+    u32x4 st[2 * NG];
     auto scales_load = [&]() {
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const int e = min(l + 64 * k, 2 * n_blk - 1), gi = min(e / n_blk, ngr - 1);
+        for (int k = 0; k < 2 * NG; k++) {
+            const int e = min(l + 64 * k, NG * n_blk - 1), gi = min(e / n_blk, ngr - 1);
             st[k] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
                                                   rsc, (uint32_t)gi * gstride + (uint32_t)(e % n_blk) * 16u, 0, 0));
         }
     };
     auto scales_store = [&]() {
 #pragma unroll
-        for (int k = 0; k < 4; k++)
-            if (l + 64 * k < 2 * n_blk) {
+        for (int k = 0; k < 2 * NG; k++)
+            if (l + 64 * k < NG * n_blk) {
                 const int e = l + 64 * k;
                 *(u32x4*)(ws + (size_t)((e / n_blk) * nbp + e % n_blk) * 16) = st[k];
             }
     };
-    auto frag_start = [&](int f) {
-        frag_setup(f);
+    auto frag_start = [&](int u) {
+        frag_setup(u);
         scales_load();
 #pragma unroll
         for (int p = 0; p < PF; p++) quad_load(p, min(p, nq - 1));
     };
     int f = lb * FPW + fs;
 
-    // staging through registers: every staging load, then the first
-    // fragment's loads, then the stores (which wait for the staging loads
-    // only: loads complete in issue order); n_blk <= 128, chunk i of the int8
-    // rows = 16 bytes of (block i / 2 NT, token (i / 2) % NT, half i % 2)
+    // staging through registers: every staging load, the stores, then the
+    // first unit's loads (issued before them, the unit's loads delay the
+    // staging data that every wave waits for); n_blk <= 128, chunk i of the
+    // int8 rows = 16 bytes of (block i / 2 NT, token (i / 2) % NT, half i % 2)
     constexpr int QPT = 128 * NT * 2 / (64 * MT_FW), SPT = 128 * NT / (64 * MT_FW);
     mt_i4 tq[QPT];  // a native vector: an int4 struct array would stay in scratch
     int tm[SPT];
@@ -172,9 +191,6 @@ __global__ __launch_bounds__(64 * MT_FW) void k_mvt(MtArgs A) {
         tm[k] = J.m[(size_t)tt * n_blk + b];
         ts[k] = J.s[(size_t)tt * n_blk + b];
     }
-    // (unconditional, clamped to the job's last fragment when this slot has
-    // none: the same loads on every path keep the stores' waits exact)
-    frag_start(min(f, nfr - 1));
 #pragma unroll
     for (int k = 0; k < QPT; k++) {
         const int i = tid + 64 * MT_FW * k;
@@ -188,18 +204,22 @@ __global__ __launch_bounds__(64 * MT_FW) void k_mvt(MtArgs A) {
             sx[(i % NT) * nbp + i / NT] = ts[k];
         }
     }
+    // (unconditional, clamped to the job's last unit when this slot has
+    // none: the same loads on every path keep the later waits exact)
+    frag_start(min(f, nun - 1));
     __syncthreads();
 
     const int tok = i16 % NT;
+    const int fx = P == 2 ? i16 >> 3 : 0;  // the fragment this lane chains
     const int8_t* sqt = sq + tok * 32 + kc * 8;
     const int32_t* smt = sm + tok * nbp;
     const float* sxt = sx + tok * nbp;
-    // this lane's scales in the wave's copy: group kc / 2 (clamped), rows
-    // 4 (kc & 1) + rho .. of each block's 8
-    for (; f < nfr; f += nwg * FPW) {
+    for (; f < nun; f += nwg * FPW) {
         if (f != lb * FPW + fs) frag_start(f);
         scales_store();
-        const uint8_t* wst = ws + (size_t)min(kc >> 1, ngr - 1) * nbp * 16 + (kc & 1) * 8 + rho * 2;
+        // this lane's scales in the wave's copy: group 2 fx + kc / 2
+        // (clamped), rows 4 (kc & 1) + rho .. of each block's 8
+        const uint8_t* wst = ws + (size_t)min(2 * fx + (kc >> 1), ngr - 1) * nbp * 16 + (kc & 1) * 8 + rho * 2;
         float acc[NV];
 #pragma unroll
         for (int v = 0; v < NV; v++) acc[v] = 0.0f;
@@ -227,55 +247,76 @@ __global__ __launch_bounds__(64 * MT_FW) void k_mvt(MtArgs A) {
             xq[sl] = *(const float4*)sxb;
             mq[sl] = *(const int4*)smb;
         };
-        lds_quad(0, sqt, smt, wst, sxt);
-        for (int q0 = 0; q0 < nq; q0 += PF) {
-            // LDS bases of this round of quads (the reads below add constants)
-            const int8_t* sq0 = sqt + q0 * 4 * NT * 32;
-            const int32_t* sm0 = smt + 4 * q0;
-            const float* sx0 = sxt + 4 * q0;
-            const uint8_t* ws0 = wst + q0 * 64;
+        // one quad in ring slot p: its LDS operands were read a quad ahead
+        // (slot p & 1), the next quad's are read now (after the last quad:
+        // padding, never used); with `load`, the quad PF ahead (clamped to
+        // the last) goes into the slot
+        auto quad_step = [&](auto load, int p, int qd, const int8_t* sq0, const int32_t* sm0, const float* sx0,
+                             const uint8_t* ws0) {
+            const int cs = p & 1;  // PF is even: the slots alternate across rounds too
+            lds_quad(cs ^ 1, sq0 + (4 * p + 4) * NT * 32, sm0 + 4 * p + 4, ws0 + (4 * p + 4) * 16, sx0 + 4 * p + 4);
+            uint32_t wj[P][4];
 #pragma unroll
-            for (int p = 0; p < PF; p++) {
-                const int qd = q0 + p;
-                if (qd >= nq) break;  // uniform
-                const int cs = p & 1;  // PF is even: the slots alternate across rounds too
-                // the next quad's LDS operands (after the last quad: padding, never used)
-                lds_quad(cs ^ 1, sq0 + (4 * p + 4) * NT * 32, sm0 + 4 * p + 4, ws0 + (4 * p + 4) * 16,
-                         sx0 + 4 * p + 4);
-                uint32_t w0 = wr[p][0], w1 = wr[p][1], w2 = wr[p][2], w3 = wr[p][3];
+            for (int x = 0; x < P; x++) {
+                uint32_t w0 = wr[x][p][0], w1 = wr[x][p][1], w2 = wr[x][p][2], w3 = wr[x][p][3];
                 skp_transpose(w0, w1, w2, w3);
-                // the quad PF ahead into this slot (clamped: loads past the
-                // end repeat the last quad and are never used)
-                quad_load(p, min(qd + PF, nq - 1));
-                const uint32_t wj[4] = {w0, w1, w2, w3};
-                const float xsj[4] = {xq[cs].x, xq[cs].y, xq[cs].z, xq[cs].w};
-                const int xmj[4] = {mq[cs].x, mq[cs].y, mq[cs].z, mq[cs].w};
-                // the quad's four MFMAs first (independent), then the chains
-                mt_i4 dq[4];
+                wj[x][0] = w0;
+                wj[x][1] = w1;
+                wj[x][2] = w2;
+                wj[x][3] = w3;
+            }
+            if constexpr (decltype(load)::value) quad_load(p, min(qd + PF, nq - 1));
+            const float xsj[4] = {xq[cs].x, xq[cs].y, xq[cs].z, xq[cs].w};
+            const int xmj[4] = {mq[cs].x, mq[cs].y, mq[cs].z, mq[cs].w};
+            // the quad's MFMAs first (independent), then the chains
+            mt_i4 dq[P][4];
 #pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const uint32_t lo = wj[j] & 0x0F0F0F0Fu, hi = (wj[j] >> 4) & 0x0F0F0F0Fu;
+            for (int j = 0; j < 4; j++) {
+#pragma unroll
+                for (int x = 0; x < P; x++) {
+                    const uint32_t lo = wj[x][j] & 0x0F0F0F0Fu, hi = (wj[x][j] >> 4) & 0x0F0F0F0Fu;
                     const long a = (long)(((uint64_t)hi << 32) | lo);
-                    dq[j] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, bb[cs][j], (mt_i4){0, 0, 0, 0}, 0, 0, 0);
-                }
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-#pragma unroll
-                    for (int k = 0; k < NV; k++) {
-                        const gm_h2 h = __builtin_bit_cast(gm_h2, sw[cs][j][k >> 1]);
-                        const float sp = __builtin_fmaf((float)h[k & 1], xsj[j], 0.0f);
-                        acc[k] = fmaf((float)(dq[j][k] - xmj[j]), sp, acc[k]);
-                    }
+                    dq[x][j] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, bb[cs][j], (mt_i4){0, 0, 0, 0}, 0, 0, 0);
                 }
             }
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+#pragma unroll
+                for (int k = 0; k < NV; k++) {
+                    int d = dq[0][j][k];
+                    // lanes 8..15 of each row: fragment b's columns 0..7 (DPP row_shr:8, banks 2-3)
+                    if (P == 2) d = __builtin_amdgcn_update_dpp(d, dq[P - 1][j][k], 0x118, 0xF, 0xC, false);
+                    const gm_h2 h = __builtin_bit_cast(gm_h2, sw[cs][j][k >> 1]);
+                    const float sp = __builtin_fmaf((float)h[k & 1], xsj[j], 0.0f);
+                    acc[k] = fmaf((float)(d - xmj[j]), sp, acc[k]);
+                }
+            }
+        };
+        lds_quad(0, sqt, smt, wst, sxt);
+        // rounds of PF quads that refill the ring, then the last round, which
+        // loads nothing (no load of the wave outlives its unit)
+        int q0 = 0;
+        for (; q0 + PF < nq; q0 += PF) {
+#pragma unroll
+            for (int p = 0; p < PF; p++)
+                quad_step(std::true_type{}, p, q0 + p, sqt + q0 * 4 * NT * 32, smt + 4 * q0, sxt + 4 * q0,
+                          wst + q0 * 64);
         }
-        // token i16, rows 4 (kc & 1) + rho + k of group gf + kc / 2
-        const int grp = J.g0 + 2 * f + (kc >> 1);
-        if (i16 < M && grp < J.g1) {
+#pragma unroll
+        for (int p = 0; p < PF; p++) {
+            // (a guard, not a break: a loop with an early exit is not unrolled)
+            if (q0 + p < nq)  // uniform
+                quad_step(std::false_type{}, p, q0 + p, sqt + q0 * 4 * NT * 32, smt + 4 * q0, sxt + 4 * q0,
+                          wst + q0 * 64);
+        }
+        // token tok of fragment fx, rows 4 (kc & 1) + rho + k of group
+        // gf + 2 fx + kc / 2
+        const int grp = J.g0 + NG * f + 2 * fx + (kc >> 1);
+        if (tok < M && (P == 2 || i16 < NT) && grp < J.g1) {
 #pragma unroll
             for (int k = 0; k < NV; k++) {
                 const int r = grp * 8 + 4 * (kc & 1) + rho + k;
-                if (r < J.rows) J.out[(size_t)i16 * J.ldo + r] = acc[k];
+                if (r < J.rows) J.out[(size_t)tok * J.ldo + r] = acc[k];
             }
         }
     }
@@ -313,23 +354,26 @@ int32_t dpuf_hip_mvt_launch(void* s, int32_t M, int32_t n_jobs, const DpufGemvJo
     for (int i = 0; i < n_jobs; i++) {
         if (jobs[i].w.mode != 12 || jobs[i].w.cols != K || !jobs[i].p.q || !jobs[i].p.s || !jobs[i].p.m) return -1;
     }
-    const int nt = M <= 8 ? 8 : 16;
-    int nfr[3] = {0, 0, 0}, ftot = 0;
+    // up to 8 tokens: fragment pairs on 8 staged tokens; 9..16: single fragments
+    const int nt = M <= 8 ? 8 : 16, pu = M <= 8 ? 2 : 1;
+    int nun[3] = {0, 0, 0}, ftot = 0, utot = 0;
     for (int i = 0; i < n_jobs; i++) {
         const int ng = jobs[i].g1 - jobs[i].g0;
-        nfr[i] = ng > 0 ? (ng + 1) / 2 : 0;
-        ftot += nfr[i];
+        ftot += ng > 0 ? (ng + 1) / 2 : 0;
+        nun[i] = ng > 0 ? (ng + 2 * pu - 1) / (2 * pu) : 0;
+        utot += nun[i];
     }
     if (ftot == 0) return 0;
     // up to one fragment per CU the K-split GEMM is faster (its workgroups
     // share a fragment's blocks instead of each walking all of K)
     if (ftot <= dpuf_hip_cu_count()) return -1;
-    // waves per fragment: as many as keep about two waves per SIMD busy
-    const int target = 8 * dpuf_hip_cu_count();
-    const int R = 4 * ftot <= target ? 4 : 2 * ftot <= target ? 2 : 1;
-    MtKernel k = nt == 8 ? (R == 4 ? k_mvt<8, 4> : R == 2 ? k_mvt<8, 2> : k_mvt<8, 1>)
-                         : (R == 4 ? k_mvt<16, 4> : R == 2 ? k_mvt<16, 2> : k_mvt<16, 1>);
-    const size_t lds = mt_lds(n_blk, nt);
+    // waves per unit: as many as keep about two waves per SIMD busy (one for
+    // pairs, whose waves carry twice the chains)
+    const int target = (pu == 2 ? 4 : 8) * dpuf_hip_cu_count();
+    const int R = 4 * utot <= target ? 4 : 2 * utot <= target ? 2 : 1;
+    MtKernel k = pu == 2 ? (R == 4 ? k_mvt<8, 4, 2> : R == 2 ? k_mvt<8, 2, 2> : k_mvt<8, 1, 2>)
+                         : (R == 4 ? k_mvt<16, 4, 1> : R == 2 ? k_mvt<16, 2, 1> : k_mvt<16, 1, 1>);
+    const size_t lds = mt_lds(n_blk, nt, pu);
     int cap = mt_capacity(k, lds);
     if (dpuf_hip_mv_max_wg() > 0 && cap > dpuf_hip_mv_max_wg()) cap = dpuf_hip_mv_max_wg();
     MtArgs A;
@@ -348,16 +392,16 @@ int32_t dpuf_hip_mvt_launch(void* s, int32_t M, int32_t n_jobs, const DpufGemvJo
         A.j[i].out = jobs[i].out;
         A.j[i].ldo = jobs[i].ldo;
     }
-    // each job's workgroups in proportion to its fragments, all resident at
-    // once; a workgroup takes MT_FW / R fragments per round
+    // each job's workgroups in proportion to its units, all resident at
+    // once; a workgroup takes MT_FW / R units per round
     const int fpw = MT_FW / R;
     int wgs = 0;
     A.wb[0] = 0;
     for (int i = 0; i < n_jobs; i++) {
-        const int need = (nfr[i] + fpw - 1) / fpw;
-        int nw = (int)(((long long)cap * nfr[i] + ftot - 1) / ftot);
+        const int need = (nun[i] + fpw - 1) / fpw;
+        int nw = (int)(((long long)cap * nun[i] + utot - 1) / utot);
         nw = nw < 1 ? 1 : nw;
-        wgs += nfr[i] > 0 ? (nw < need ? nw : need) : 0;
+        wgs += nun[i] > 0 ? (nw < need ? nw : need) : 0;
         A.wb[i + 1] = wgs;
     }
     hipLaunchKernelGGL(k, dim3(wgs), dim3(64 * MT_FW), lds, ST(s), A);
