@@ -84,7 +84,7 @@ struct MtArgs {
 // array with 4 blocks of padding (the reads one quad ahead run into it after
 // the last quad; the scale rows of different tokens start on different banks).
 static constexpr size_t mt_lds(int n_blk, int nt, int p) {
-    return (size_t)(n_blk + 4) * (nt * 40 + MT_FW * 32 * p);
+    return (size_t)(n_blk + 4) * ((nt + (p == 2)) * 32 + nt * 8 + MT_FW * 32 * p);
 }
 
 template <int NT, int R, int P>
@@ -111,11 +111,12 @@ __global__ __launch_bounds__(64 * MT_FW) void k_mvt(MtArgs A) {
     const int lb = bid - A.wb[ji], nwg = A.wb[ji + 1] - A.wb[ji];
     const uint32_t gstride = (uint32_t)n_blk * 144u;
 
+    constexpr int NTS = NT + (P == 2);  // token slots per staged block (pairs: + a zero slot)
     const int nbp = n_blk + 4;  // padded block count of every LDS array
-    int8_t* sq = (int8_t*)smem;                             // [nbp][NT][32]
-    int32_t* sm = (int32_t*)(smem + (size_t)nbp * NT * 32); // sum8 [NT][nbp]
-    float* sx = (float*)(smem + (size_t)nbp * NT * 36);     // xs [NT][nbp]
-    uint8_t* ws = smem + (size_t)nbp * NT * 40 + (size_t)w * nbp * 16 * NG;  // [NG][nbp][16 B]
+    int8_t* sq = (int8_t*)smem;                                       // [nbp][NTS][32]
+    int32_t* sm = (int32_t*)(smem + (size_t)nbp * NTS * 32);          // sum8 [NT][nbp]
+    float* sx = (float*)(smem + (size_t)nbp * (NTS * 32 + NT * 4));   // xs [NT][nbp]
+    uint8_t* ws = smem + (size_t)nbp * (NTS * 32 + NT * 8) + (size_t)w * nbp * 16 * NG;  // [NG][nbp][16 B]
 
     // a unit's nibble loads: lane row i16 is row ri of fragment x (group
     // gf + 2 x + ri / 8, clamped into the job: a missing group repeats the
@@ -194,7 +195,15 @@ __global__ __launch_bounds__(64 * MT_FW) void k_mvt(MtArgs A) {
 #pragma unroll
     for (int k = 0; k < QPT; k++) {
         const int i = tid + 64 * MT_FW * k;
-        if (i < n_blk * NT * 2) *(mt_i4*)(sq + (size_t)i * 16) = tq[k];
+        if (i < n_blk * NT * 2) {
+            const int b = i / (2 * NT), t = (i >> 1) % NT, h = i & 1;
+            *(mt_i4*)(sq + (size_t)((b * NTS + t) * 2 + h) * 16) = tq[k];
+        }
+    }
+    if (P == 2) {
+        // each block's zero slot (the B columns that pair with the other fragment)
+        for (int i = tid; i < nbp * 2; i += 64 * MT_FW)
+            *(mt_i4*)(sq + (size_t)(((i >> 1) * NTS + NT) * 2 + (i & 1)) * 16) = (mt_i4){0, 0, 0, 0};
     }
 #pragma unroll
     for (int k = 0; k < SPT; k++) {
@@ -211,7 +220,11 @@ __global__ __launch_bounds__(64 * MT_FW) void k_mvt(MtArgs A) {
 
     const int tok = i16 % NT;
     const int fx = P == 2 ? i16 >> 3 : 0;  // the fragment this lane chains
-    const int8_t* sqt = sq + tok * 32 + kc * 8;
+    // B fragment of a block: P = 1, 8 bytes (token l % 16, columns 8 kc ..);
+    // P = 2, 16 bytes, columns 16 (kc & 1) .. + 15 of token i16 % 8 when the
+    // lane's column half (i16 / 8) matches its k half (kc / 2), else zeros
+    const int8_t* sqt = P == 2 ? sq + ((i16 >> 3) == (kc >> 1) ? tok : NT) * 32 + (kc & 1) * 16
+                               : sq + tok * 32 + kc * 8;
     const int32_t* smt = sm + tok * nbp;
     const float* sxt = sx + tok * nbp;
     for (; f < nun; f += nwg * FPW) {
@@ -226,14 +239,15 @@ __global__ __launch_bounds__(64 * MT_FW) void k_mvt(MtArgs A) {
         // LDS operands of a quad in slot sl: B fragments, the lane's row
         // scales (fp16 rows 4 (kc & 1) + rho + k, k < NV), and the four
         // blocks' token scales and sums; read one quad ahead of their use
-        long bb[2][4];
+        using BT = typename std::conditional<P == 2, mt_i4, long>::type;
+        BT bb[2][4];
         uint32_t sw[2][4][2];
         float4 xq[2];
         int4 mq[2];
         auto lds_quad = [&](int sl, const int8_t* sqb, const int32_t* smb, const uint8_t* wsb, const float* sxb) {
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                bb[sl][j] = *(const long*)(sqb + j * NT * 32);
+                bb[sl][j] = *(const BT*)(sqb + j * NTS * 32);
                 if (NV == 4) {
                     const uint2 u = *(const uint2*)(wsb + j * 16);
                     sw[sl][j][0] = u.x;
@@ -254,41 +268,56 @@ __global__ __launch_bounds__(64 * MT_FW) void k_mvt(MtArgs A) {
         auto quad_step = [&](auto load, int p, int qd, const int8_t* sq0, const int32_t* sm0, const float* sx0,
                              const uint8_t* ws0) {
             const int cs = p & 1;  // PF is even: the slots alternate across rounds too
-            lds_quad(cs ^ 1, sq0 + (4 * p + 4) * NT * 32, sm0 + 4 * p + 4, ws0 + (4 * p + 4) * 16, sx0 + 4 * p + 4);
-            uint32_t wj[P][4];
-#pragma unroll
-            for (int x = 0; x < P; x++) {
-                uint32_t w0 = wr[x][p][0], w1 = wr[x][p][1], w2 = wr[x][p][2], w3 = wr[x][p][3];
-                skp_transpose(w0, w1, w2, w3);
-                wj[x][0] = w0;
-                wj[x][1] = w1;
-                wj[x][2] = w2;
-                wj[x][3] = w3;
-            }
-            if constexpr (decltype(load)::value) quad_load(p, min(qd + PF, nq - 1));
+            lds_quad(cs ^ 1, sq0 + (4 * p + 4) * NTS * 32, sm0 + 4 * p + 4, ws0 + (4 * p + 4) * 16, sx0 + 4 * p + 4);
             const float xsj[4] = {xq[cs].x, xq[cs].y, xq[cs].z, xq[cs].w};
             const int xmj[4] = {mq[cs].x, mq[cs].y, mq[cs].z, mq[cs].w};
-            // the quad's MFMAs first (independent), then the chains
-            mt_i4 dq[P][4];
+            mt_i4 dq[4];
+            if constexpr (P == 2) {
+                // lane row g held block g's 16 bytes of fragment a (x = 0)
+                // and b; afterwards, per block j, rows 0-1 hold fragment a's
+                // nibble words (0, 1) and (2, 3), rows 2-3 fragment b's
+                uint32_t xa[4], ya[4];
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
+                for (int r = 0; r < 4; r++) {
+                    const auto t = __builtin_amdgcn_permlane32_swap(wr[0][p][r], wr[1][p][r], false, false);
+                    xa[r] = t[0];  // rows: a blk 0, a blk 1, b blk 0, b blk 1
+                    ya[r] = t[1];  // rows: a blk 2, a blk 3, b blk 2, b blk 3
+                }
+                const auto c0 = __builtin_amdgcn_permlane16_swap(xa[0], xa[2], false, false);
+                const auto c1 = __builtin_amdgcn_permlane16_swap(xa[1], xa[3], false, false);
+                const auto c2 = __builtin_amdgcn_permlane16_swap(ya[0], ya[2], false, false);
+                const auto c3 = __builtin_amdgcn_permlane16_swap(ya[1], ya[3], false, false);
+                const uint32_t pk[4][2] = {{c0[0], c1[0]}, {c0[1], c1[1]}, {c2[0], c3[0]}, {c2[1], c3[1]}};
+                if constexpr (decltype(load)::value) quad_load(p, min(qd + PF, nq - 1));
+                // one MFMA per block for both fragments: A rows = the 16
+                // lane rows' fragment rows, k < 32 fragment a's block, k >= 32
+                // fragment b's; B columns 0-7 carry the tokens at k < 32,
+                // columns 8-15 at k >= 32, so D columns 8-15 are fragment b's
 #pragma unroll
-                for (int x = 0; x < P; x++) {
-                    const uint32_t lo = wj[x][j] & 0x0F0F0F0Fu, hi = (wj[x][j] >> 4) & 0x0F0F0F0Fu;
+                for (int j = 0; j < 4; j++) {
+                    const mt_i4 a = {(int)(pk[j][0] & 0x0F0F0F0Fu), (int)((pk[j][0] >> 4) & 0x0F0F0F0Fu),
+                                     (int)(pk[j][1] & 0x0F0F0F0Fu), (int)((pk[j][1] >> 4) & 0x0F0F0F0Fu)};
+                    dq[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, bb[cs][j], (mt_i4){0, 0, 0, 0}, 0, 0, 0);
+                }
+            } else {
+                uint32_t w0 = wr[0][p][0], w1 = wr[0][p][1], w2 = wr[0][p][2], w3 = wr[0][p][3];
+                skp_transpose(w0, w1, w2, w3);
+                const uint32_t wj[4] = {w0, w1, w2, w3};
+                if constexpr (decltype(load)::value) quad_load(p, min(qd + PF, nq - 1));
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const uint32_t lo = wj[j] & 0x0F0F0F0Fu, hi = (wj[j] >> 4) & 0x0F0F0F0Fu;
                     const long a = (long)(((uint64_t)hi << 32) | lo);
-                    dq[x][j] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, bb[cs][j], (mt_i4){0, 0, 0, 0}, 0, 0, 0);
+                    dq[j] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, bb[cs][j], (mt_i4){0, 0, 0, 0}, 0, 0, 0);
                 }
             }
 #pragma unroll
             for (int j = 0; j < 4; j++) {
 #pragma unroll
                 for (int k = 0; k < NV; k++) {
-                    int d = dq[0][j][k];
-                    // lanes 8..15 of each row: fragment b's columns 0..7 (DPP row_shr:8, banks 2-3)
-                    if (P == 2) d = __builtin_amdgcn_update_dpp(d, dq[P - 1][j][k], 0x118, 0xF, 0xC, false);
                     const gm_h2 h = __builtin_bit_cast(gm_h2, sw[cs][j][k >> 1]);
                     const float sp = __builtin_fmaf((float)h[k & 1], xsj[j], 0.0f);
-                    acc[k] = fmaf((float)(d - xmj[j]), sp, acc[k]);
+                    acc[k] = fmaf((float)(dq[j][k] - xmj[j]), sp, acc[k]);
                 }
             }
         };
@@ -299,14 +328,14 @@ __global__ __launch_bounds__(64 * MT_FW) void k_mvt(MtArgs A) {
         for (; q0 + PF < nq; q0 += PF) {
 #pragma unroll
             for (int p = 0; p < PF; p++)
-                quad_step(std::true_type{}, p, q0 + p, sqt + q0 * 4 * NT * 32, smt + 4 * q0, sxt + 4 * q0,
+                quad_step(std::true_type{}, p, q0 + p, sqt + q0 * 4 * NTS * 32, smt + 4 * q0, sxt + 4 * q0,
                           wst + q0 * 64);
         }
 #pragma unroll
         for (int p = 0; p < PF; p++) {
             // (a guard, not a break: a loop with an early exit is not unrolled)
             if (q0 + p < nq)  // uniform
-                quad_step(std::false_type{}, p, q0 + p, sqt + q0 * 4 * NT * 32, smt + 4 * q0, sxt + 4 * q0,
+                quad_step(std::false_type{}, p, q0 + p, sqt + q0 * 4 * NTS * 32, smt + 4 * q0, sxt + 4 * q0,
                           wst + q0 * 64);
         }
         // token tok of fragment fx, rows 4 (kc & 1) + rho + k of group
