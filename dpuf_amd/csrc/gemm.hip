@@ -73,6 +73,7 @@ struct GmArgs {
     // 64 rows placed after the jobs' tiles
     float* zo;
     int zld, z0, z1, zt;
+    int32_t* err;  // device error word: set when a bounded wait of k_gemm_sk runs out
 };
 
 
@@ -470,15 +471,58 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MODE == 12 
 #define SK_NC 4   // chain waves (one per D component)
 #define SK_P 4    // load ring depth in rounds (even; fastest of 4..10 in a sweep of the dword-load version)
 static_assert(SK_P % 2 == 0, "the D buffers alternate with the round");
+#ifndef SK_NB
+#define SK_NB 4   // k_gemm_sk round buffers in LDS (producers run up to SK_NB rounds ahead of the chains)
+#endif
 
 #define SKP_P 8  // ring depth in rounds: a multiple of every NR
 #define SKP_RB 4                 // blocks per producer wave per round
 #define SKP_RS (SK_NP * SKP_RB)  // 32 blocks per round
 
+// One round of a chain wave: every block's sp = fp16(ws) * xs first (they
+// do not depend on the chain), then acc = fma(d, sp, acc) over the round's
+// blocks in order; a full round runs the chain with no per-block guard, so
+// each block adds one dependent instruction, not three (product, fma and a
+// select).
+DEV float sk_round_chain(float acc, const float (&d)[SKP_RS], const uint32_t (&wv)[SKP_RS / 2],
+                         const gm_f4 (&xr)[SKP_RS / 4], int nj) {
+    float sp[SKP_RS];
+#pragma unroll
+    for (int j = 0; j < SKP_RS; j++) {
+        const gm_h2 hw = __builtin_bit_cast(gm_h2, wv[j >> 1]);
+        sp[j] = __builtin_fmaf((float)hw[j & 1], xr[j >> 2][j & 3], 0.0f);
+    }
+    if (nj >= SKP_RS) {
+#pragma unroll
+        for (int j = 0; j < SKP_RS; j++) acc = fmaf(d[j], sp[j], acc);
+    } else {
+#pragma unroll
+        for (int j = 0; j < SKP_RS; j++)
+            if (j < nj) acc = fmaf(d[j], sp[j], acc);
+    }
+    return acc;
+}
+
+// Polls an LDS counter until it reaches want, at most 2^22 polls (false when
+// it ran out); the polled value is wave-uniform, so the loop is scalar.
+DEV bool sk_wait(uint32_t* p, uint32_t want) {
+    int spins = 0;
+#pragma clang loop unroll(disable)
+    while ((uint32_t)__builtin_amdgcn_readfirstlane(
+               (int)__hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) < want) {
+        if (++spins >= (1 << 22)) return false;
+        __builtin_amdgcn_s_sleep(1);
+    }
+    return true;
+}
+
 __global__ __launch_bounds__(64 * (SK_NP + SK_NC)) void k_gemm_sk(GmArgs A) {
-    __shared__ __align__(16) float dq[2][SKP_RS][4][64];    // D tiles [buf][block][v][lane]
-    __shared__ __align__(16) uint16_t wsl[2][16][SKP_RS];   // weight scales [buf][row][block]
-    __shared__ __align__(16) float xsl[2][16][SKP_RS + 4];  // token scales [buf][token][block], rows padded
+    __shared__ __align__(16) float dq[SK_NB][SKP_RS][4][64];    // D tiles [buf][block][v][lane]
+    __shared__ __align__(16) uint16_t wsl[SK_NB][16][SKP_RS];   // weight scales [buf][row][block]
+    __shared__ __align__(16) float xsl[SK_NB][16][SKP_RS + 4];  // token scales [buf][token][block], rows padded
+    // hand-off counters per buffer, cumulative: full[b] counts producer waves
+    // done with a round in b, freed[b] chain waves done reading one
+    __shared__ uint32_t full[SK_NB], freed[SK_NB];
     const int fr = blockIdx.x;
     // the wave index through readfirstlane: uniform for the compiler, so the
     // role branch and every scalar block offset stay scalar
@@ -503,6 +547,11 @@ __global__ __launch_bounds__(64 * (SK_NP + SK_NC)) void k_gemm_sk(GmArgs A) {
     const int K = A.K, n_blk = K >> 5, n_r = (n_blk + SKP_RS - 1) / SKP_RS;
     const size_t gstride = (size_t)n_blk * 144;
     const int i16 = l & 15, kc = l >> 4;
+    if (tid < SK_NB) {
+        full[tid] = 0;
+        freed[tid] = 0;
+    }
+    __syncthreads();
 
     if (w < SK_NP) {
         // ---- producer: 4 blocks per round, one 16-byte weight load per lane
@@ -542,15 +591,21 @@ __global__ __launch_bounds__(64 * (SK_NP + SK_NC)) void k_gemm_sk(GmArgs A) {
         };
 #pragma unroll
         for (int u = 0; u < SK_P - 1; u++) load(u, wq[u], wsq[u], ax[u], xsq[u]);
-        for (int it0 = 0; it0 <= n_r; it0 += SK_P) {
+        for (int it0 = 0; it0 < n_r; it0 += SK_P) {
 #pragma unroll
             for (int u = 0; u < SK_P; u++) {
                 const int it = it0 + u;
-                if (it > n_r) break;  // uniform
+                if (it >= n_r) break;  // uniform
                 const int un = (u + SK_P - 1) % SK_P;
                 load(it + SK_P - 1, wq[un], wsq[un], ax[un], xsq[un]);
-                if (it < n_r) {
-                    const int buf = u & 1;
+                {
+                    // round it goes to buffer it % SK_NB once the chains have
+                    // read round it - SK_NB from it
+                    const int buf = it % SK_NB;
+                    if (it >= SK_NB) {
+                        if (!sk_wait(&freed[buf], (uint32_t)(SK_NC * (it / SK_NB))) && l == 0) atomicOr(A.err, 1);
+                        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+                    }
                     uint32_t t0 = wq[u][0], t1 = wq[u][1], t2 = wq[u][2], t3 = wq[u][3];
                     skp_transpose(t0, t1, t2, t3);
                     const uint32_t tw[4] = {t0, t1, t2, t3};
@@ -568,8 +623,9 @@ __global__ __launch_bounds__(64 * (SK_NP + SK_NC)) void k_gemm_sk(GmArgs A) {
                         wsl[buf][row + 1][w * SKP_RB + sj] = (uint16_t)(wsq[u] >> 16);
                     }
                     xsl[buf][i16][w * SKP_RB + kc] = xsq[u];
+                    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+                    if (l == 0) __hip_atomic_fetch_add(&full[buf], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
                 }
-                __syncthreads();
             }
         }
         return;
@@ -578,9 +634,12 @@ __global__ __launch_bounds__(64 * (SK_NP + SK_NC)) void k_gemm_sk(GmArgs A) {
     // ---- chain wave c: output (token l % 16, row 4 (l / 16) + c) ----
     const int c = w - SK_NP, rr = 4 * kc + c;
     float acc = 0.0f;
-    for (int it = 0; it <= n_r; it++) {
-        if (it >= 1) {
-            const int buf = (it + 1) & 1, b0 = (it - 1) * SKP_RS;
+    for (int it = 1; it <= n_r; it++) {
+        {
+            // round it - 1, once every producer wave has written it
+            const int buf = (it - 1) % SK_NB, b0 = (it - 1) * SKP_RS;
+            if (!sk_wait(&full[buf], (uint32_t)(SK_NP * ((it - 1) / SK_NB + 1))) && l == 0) atomicOr(A.err, 1);
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
             const int nj = min(SKP_RS, n_blk - b0);  // uniform
             float d[SKP_RS];
 #pragma unroll
@@ -598,14 +657,10 @@ __global__ __launch_bounds__(64 * (SK_NP + SK_NC)) void k_gemm_sk(GmArgs A) {
             gm_f4 xr[SKP_RS / 4];
 #pragma unroll
             for (int q = 0; q < SKP_RS / 4; q++) xr[q] = *(const gm_f4*)&xsl[buf][i16][4 * q];
-#pragma unroll
-            for (int j = 0; j < SKP_RS; j++) {
-                const gm_h2 hw = __builtin_bit_cast(gm_h2, wv[j >> 1]);
-                const float wx = __builtin_fmaf((float)hw[j & 1], xr[j >> 2][j & 3], 0.0f);
-                if (j < nj) acc = fmaf(d[j], wx, acc);
-            }
+            acc = sk_round_chain(acc, d, wv, xr, nj);
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+            if (l == 0) __hip_atomic_fetch_add(&freed[buf], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
-        __syncthreads();
     }
     const int grp = gf + (rr >> 3);
     const int r = grp * 8 + (rr & 7);
@@ -780,12 +835,7 @@ __global__ __launch_bounds__(64 * (SK_NP + SK_NC)) void k_gemm_skp(GmArgs A) {
                     gm_f4 xr[SKP_RS / 4];
 #pragma unroll
                     for (int q = 0; q < SKP_RS / 4; q++) xr[q] = *(const gm_f4*)&xsl[buf][i16][4 * q];
-#pragma unroll
-                    for (int j = 0; j < SKP_RS; j++) {
-                        const gm_h2 hw = __builtin_bit_cast(gm_h2, wv[j >> 1]);
-                        const float wx = __builtin_fmaf((float)hw[j & 1], xr[j >> 2][j & 3], 0.0f);
-                        if (j < nj) acc = fmaf(d[j], wx, acc);
-                    }
+                    acc = sk_round_chain(acc, d, wv, xr, nj);
                 }
                 if (r == NR - 1) {
                     const int fr = lb + fl * nwg;
@@ -909,6 +959,11 @@ void dpuf_hip_gm_launch(void* s, int32_t M, int32_t n_jobs, const DpufGemvJob* j
                 f += ng > 0 ? (ng + 1) / 2 : 0;
             }
             G.tb[n_jobs] = f;
+            G.err = dpuf_hip_error_word();
+            if (!G.err) {
+                note(hipErrorInvalidValue, "dpuf_hip_gemv: no device error word bound");
+                return;
+            }
             hipLaunchKernelGGL(k_gemm_sk, dim3(f + G.zt), dim3(64 * (SK_NP + SK_NC)), 0, ST(s), G);
             LAUNCHED("k_gemm_sk");
             return;

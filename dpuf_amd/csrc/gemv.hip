@@ -515,6 +515,7 @@ void dpuf_hip_set_gemv_max_wg(int32_t n) { g_mv_max_wg = n > 0 ? n : 0; }
 static thread_local int32_t* g_err_word = NULL;
 
 void dpuf_hip_bind_error_word(int32_t* d_word) { g_err_word = d_word; }
+int32_t* dpuf_hip_error_word(void) { return g_err_word; }
 
 // Workgroups of one k_mv instance the device holds at once (occupancy x CUs),
 // cached per (instance, block size, LDS size).

@@ -25,6 +25,8 @@ extern "C" {
 int dpuf_hip_cu_count(void);
 // Cap of the GEMV / K-split GEMM workgroups (dpuf_hip_set_gemv_max_wg; 0: none).
 int dpuf_hip_mv_max_wg(void);
+// Device error word bound to the current API call on this thread (NULL: none).
+int32_t* dpuf_hip_error_word(void);
 // The M > 1 GEMM of n_jobs matrices of one mode; rows [z0, z1) of zo (row
 // stride zld) are set to 0 by the same launch.
 void dpuf_hip_gm_launch(void* s, int32_t M, int32_t n_jobs, const DpufGemvJob* jobs, float* zo, int32_t zld,
