@@ -134,9 +134,9 @@ def test_matmul_skinny_workgroup_caps(eng, orc, cols, cap):
 
 @pytest.mark.parametrize("cap", [1, 5])
 def test_matmul_few_token_workgroup_caps(eng, orc, cap):
-    """The few-token MFMA GEMM (12296 rows: 769 fragments, the last with one
-    group, 2 waves per fragment) with its workgroups capped so each walks
-    many fragments, restaging nothing between them."""
+    """The few-token MFMA GEMM (12296 rows: 769 fragments in 385 pairs, the
+    last a single group, 2 waves per pair) with its workgroups capped so each
+    walks many pairs, restaging nothing between them."""
     rows, cols, m = 12296, 1024, 6
     blob, d = _mat(rows, cols, 91)
     x = _x(m, cols, 93)
@@ -175,12 +175,14 @@ def test_matmul_token_tiles_bit_exact(eng, orc, rows, cols, m):
 @pytest.mark.parametrize("rows,cols,m", [(72, 320, 2), (136, 64, 16), (200, 1088, 16), (1000, 3072, 9),
                                          (4096, 12288, 8), (12288, 4096, 16), (72, 4160, 5),
                                          (200, 320, 17), (1000, 4096, 8), (136, 256, 2), (200, 1024, 5),
-                                         (24, 128, 3), (6152, 4096, 7), (24576, 4096, 8), (40000, 256, 3)])
+                                         (24, 128, 3), (6152, 4096, 7), (24576, 4096, 8), (40000, 256, 3),
+                                         (40000, 256, 16), (6152, 4096, 12)])
 def test_matmul_skinny_bit_exact(eng, orc, rows, cols, m):
     """M <= 16: the few-token MFMA GEMM (K a multiple of 128 up to 4096 and
-    more 16-row fragments than CUs; 8 staged tokens for M <= 8, 16 above; 1,
-    2 or 4 waves per fragment: 24576 and 40000 rows take 1, 12288 rows 2,
-    6152 rows 4 and a last fragment with one group) and the K-split GEMMs
+    more 16-row fragments than CUs): up to 8 tokens in pairs of fragments
+    (24576 and 40000 rows 1 wave per pair, 6152 rows 4 and a last pair with
+    one group), 9..16 tokens one fragment per unit (40000 rows 1 wave, 12288
+    rows 2, 6152 rows 4); and the K-split GEMMs
     (the rest): odd group counts, a single 4-block quad, block counts that
     are not a multiple of the 32-block round (10, 34, 130: K > 4096 with a
     partial last round), the 8B shapes; M = 17 is the slab GEMM next to it."""
