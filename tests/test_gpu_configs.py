@@ -499,6 +499,56 @@ def test_prefix_freeze_apply_reset(eng, orc):
     p.close()
 
 
+def test_few_row_steps_8b_width(eng, orc):
+    """Steps of 2..16 rows at the Qwen3-8B width (hidden 4096, FFN 12288,
+    two layers), whose Q/K/V and gate/up projections take the few-token
+    GEMM: prefill chunks of 12 (16 staged tokens) and 5 rows (fragment
+    pairs) with per-layer residuals, then three sessions decoded together
+    for 3 steps; every row bit-identical to the oracle."""
+    shape = dict(M.QWEN3_8B, num_layers=2, vocab_size=4096, tie_word_embeddings=1)
+    m = M.Model.build(shape, max_seq_len=64, seed=161)
+    p = Pair(eng, orc, m)
+    rng = np.random.default_rng(162)
+    p.capture(16)
+    ids = rng.integers(0, 4096, 17).astype(np.int32)
+    log("8B-width prefill chunk of 12 rows")
+    lg, lo = p.forward(ids[:12], 0, only_last=0)
+    assert bits_equal(lg, lo), maxdiff(lg, lo)
+    cg, co = p.captured(12)
+    assert bits_equal(cg, co), maxdiff(cg, co)
+    log("8B-width prefill chunk of 5 rows at position 12")
+    lg, lo = p.forward(ids[12:], 12, only_last=0)
+    assert bits_equal(lg, lo), maxdiff(lg, lo)
+    cg, co = p.captured(5)
+    assert bits_equal(cg, co), maxdiff(cg, co)
+    p.capture(0)
+    slots = np.array([1, 4, 6], np.int32)
+    toks, pos = [], []
+    for s, n in zip(slots, (3, 7, 5)):
+        p.set_slot(int(s))
+        lg, lo = p.forward(rng.integers(0, 4096, n).astype(np.int32), 0)
+        assert bits_equal(lg, lo)
+        toks.append(int(np.argmax(lo[0])))
+        pos.append(n)
+    for step in range(3):
+        log(f"8B-width three-session step {step}")
+        lg = np.zeros((3, 4096), np.float32)
+        got = np.full(3, -1, np.int32)
+        rc = eng.dpuf_amd_engine_forward_slots(p.g, 3, M.ptr(slots), M.ptr(np.array(toks, np.int32)),
+                                              M.ptr(np.array(pos, np.int32)), M.ptr(lg), M.ptr(got))
+        assert rc == 0, rc
+        for i, s in enumerate(slots):
+            assert orc.orc_engine_set_slot(p.o, int(s)) == 0
+            lo = np.zeros(4096, np.float32)
+            assert orc.orc_engine_forward(p.o, 1, M.ptr(np.array([toks[i]], np.int32)), pos[i], None, 1,
+                                          M.ptr(lo)) == 0
+            assert bits_equal(lg[i], lo), (step, i, maxdiff(lg[i], lo))
+            assert got[i] == orc.orc_argmax(M.ptr(lo), 4096)
+            toks[i] = int(got[i])
+            pos[i] += 1
+    p.close()
+
+
 def test_multi_session_8b_attention_geometry(eng, orc):
     """dpuf_amd_engine_forward_slots with groups of 4 and head_dim 128 (two
     decode-attention workgroups per KV head, the second of which stores no
