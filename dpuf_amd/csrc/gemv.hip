@@ -348,7 +348,12 @@ DEV void mv_chains(const MvGeo& G, int c, int n_my, int lane, uint8_t* smem, MvS
 // the SwiGLU + prep row, written with agent-scope stores (past the L2, to
 // where every XCD reads: no L2 writeback, which walks the whole cache).
 // Every wave waits until its stores are done; after the barrier the flag
-// copies take the step serial.
+// copies take the step serial.  No agent-scope release fence precedes the
+// flag stores: on gfx950 that fence is an L2 writeback walking the whole
+// cache, and the data stores above already went through to memory and were
+// acknowledged (vmcnt 0) before the barrier.  The consumers' ordinary loads
+// of the data rely on the L1/L2 invalidate that the dispatch packet's
+// acquire fence performs at the start of every launch, graph nodes included.
 DEV void mv_produce(const MvArgs& A, int p) {
     const int t = p * (int)blockDim.x + (int)threadIdx.x;
     const DpufPrep& P = A.j[0].x;
