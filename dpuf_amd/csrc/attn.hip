@@ -1101,11 +1101,12 @@ void dpuf_hip_qk_rope_kv(void* s, int32_t M, float* q, float* k, const float* v,
 // dim not 64/128/256, or a tile's probabilities not fitting in LDS).
 // rope (one-token steps only): the QK-norm, RoPE and KV store ride in the
 // scores launch; -1 with nothing launched when the one-token wide path does
-// not apply.
+// not apply.  wm (or NULL): weight groups the one-token wide path's P.V
+// launch warms on the CUs its chain workgroups leave idle.
 static int32_t attn_split(void* s, int32_t M, int32_t lmax, const float* q, const float* kc, const float* vc,
                           float* out, float* scores, const int32_t* pos0p, int32_t n_q, int32_t n_kv, int32_t hd,
                           int32_t max_seq, float scale, const uint8_t* o_sign, DpufPrep op, int32_t* prepped,
-                          const ScRope* rope) {
+                          const ScRope* rope, const DpufWarm* wm) {
     if (prepped) *prepped = 0;
     if (rope && M != 1) return -1;
     if (n_kv <= 0 || n_q % n_kv || n_q / n_kv > 32 || (hd != 64 && hd != 128 && hd != 256)) return -1;
@@ -1150,7 +1151,7 @@ static int32_t attn_split(void* s, int32_t M, int32_t lmax, const float* q, cons
     // one-token decode with an even group: softmax once per row, then the
     // wide P.V (one wave per kv head and 4 dims); its probabilities stay in
     // global memory, so the LDS budget below does not limit it
-    if (M == 1 && attn_wide_f32(s, lmax, q, kc, vc, out, scores, pos0p, n_q, n_kv, hd, max_seq, scale, rope) == 0)
+    if (M == 1 && attn_wide_f32(s, lmax, q, kc, vc, out, scores, pos0p, n_q, n_kv, hd, max_seq, scale, rope, wm) == 0)
         return 0;
     if (rope) return -1;
     // softmax + P.V in LDS: R = qt2 * G rows of lcap probabilities; about 8
@@ -1212,17 +1213,18 @@ int32_t dpuf_hip_attn_split(void* s, int32_t M, int32_t lmax, const float* q, co
                             float* out, float* scores, const int32_t* pos0p, int32_t n_q, int32_t n_kv, int32_t hd,
                             int32_t max_seq, float scale, const uint8_t* o_sign, DpufPrep op, int32_t* prepped) {
     return attn_split(s, M, lmax, q, kc, vc, out, scores, pos0p, n_q, n_kv, hd, max_seq, scale, o_sign, op, prepped,
-                      NULL);
+                      NULL, NULL);
 }
 
 int32_t dpuf_hip_attn_decode_rope(void* s, int32_t lmax, float* q, const float* k, const float* v, const float* qn,
                                   const float* kn, float eps, const float* cos_tab, const float* sin_tab, float* kc,
                                   float* vc, float* out, float* scores, const int32_t* pos0p, int32_t n_q,
-                                  int32_t n_kv, int32_t hd, int32_t max_seq, float scale) {
+                                  int32_t n_kv, int32_t hd, int32_t max_seq, float scale, const DpufWarm* warm) {
     const ScRope r = {k, v, qn, kn, eps, cos_tab, sin_tab, kc, vc};
     DpufPrep none;
     memset(&none, 0, sizeof none);
-    return attn_split(s, 1, lmax, q, kc, vc, out, scores, pos0p, n_q, n_kv, hd, max_seq, scale, NULL, none, NULL, &r);
+    return attn_split(s, 1, lmax, q, kc, vc, out, scores, pos0p, n_q, n_kv, hd, max_seq, scale, NULL, none, NULL, &r,
+                      warm);
 }
 
 void dpuf_hip_attn(void* s, int32_t M, const float* q, const float* kc, const float* vc, float* out, float* scores,
@@ -1235,7 +1237,8 @@ void dpuf_hip_attn(void* s, int32_t M, const float* q, const float* kc, const fl
 }
 
 void dpuf_hip_attn_q8(void* s, int32_t M, int32_t lmax, const float* q, DpufKvQ8 c8, float* out, float* scores,
-                      const int32_t* pos0, int32_t n_q, int32_t n_kv, int32_t hd, int32_t max_seq, float scale) {
+                      const int32_t* pos0, int32_t n_q, int32_t n_kv, int32_t hd, int32_t max_seq, float scale,
+                      const DpufWarm* warm) {
     const int G = n_q / n_kv;
     if (lmax > max_seq) lmax = max_seq;
     const size_t lds1 = (size_t)G * hd * 4 + (size_t)Q8_SCK * hd + (size_t)Q8_SCK * (hd / 32) * 4;
@@ -1244,7 +1247,7 @@ void dpuf_hip_attn_q8(void* s, int32_t M, int32_t lmax, const float* q, DpufKvQ8
     // one token, groups of 2, 4 or 8: the softmax once per row and P.V on one
     // chain wave per (kv head, 4 dims), as for the fp32 cache, with W = p *
     // v_scale and V widened in the producers
-    if (M == 1 && attn_wide_q8(s, lmax, pos0, n_q, n_kv, hd, max_seq, scores, out, c8) == 0) {
+    if (M == 1 && attn_wide_q8(s, lmax, pos0, n_q, n_kv, hd, max_seq, scores, out, c8, warm) == 0) {
         attn_path_note(5);
         return;
     }

@@ -265,12 +265,82 @@ DEV float pv_chain(const float* p, const float* v, int n, float a) {
 // The one-token long-context kernels (attn_wide.hip): fp32 cache scores
 // (with the QK-norm, RoPE and KV store when rope is set), softmax once per row
 // and the wide P.V; -1 (nothing launched) when the shape does not take them.
+// wm (or NULL): the weight groups that warm-up workgroups of the P.V launch
+// read into the caches on the CUs its chain workgroups leave idle.
 int32_t attn_wide_f32(void* s, int32_t lmax, const float* q, const float* kc, const float* vc, float* out,
                       float* scores, const int32_t* pos0p, int32_t n_q, int32_t n_kv, int32_t hd, int32_t max_seq,
-                      float scale, const ScRope* rope);
+                      float scale, const ScRope* rope, const DpufWarm* wm);
 // The int8 cache's softmax once per row + wide P.V after its scores kernel;
-// -1 (nothing launched) when the shape does not take them.
+// -1 (nothing launched) when the shape does not take them.  wm (or NULL):
+// weights that warm-up workgroups of the P.V launch read into the caches.
 int32_t attn_wide_q8(void* s, int32_t lmax, const int32_t* pos0, int32_t n_q, int32_t n_kv, int32_t hd,
-                     int32_t max_seq, float* scores, float* out, DpufKvQ8 c8);
+                     int32_t max_seq, float* scores, float* out, DpufKvQ8 c8, const DpufWarm* wm);
+
+// Warm-up workgroup i (of wm.n_wg; grid position L, so XCD L % 8): the
+// units of its XCD are (job j, round lg, the k-th workgroup of job j on that
+// XCD), job by job; it takes a share of at most WARM_MAXU of them, puts their
+// group addresses and sizes in LDS, and reads the groups with 16-byte loads,
+// WARM_DEPTH in flight per lane.  Called by every thread of the workgroup.
+#define WARM_MAXU 48
+#define WARM_DEPTH 32  // loads in flight per lane (16 and 64 measured slower)
+DEV void warm_read(const DpufWarm& wm, int i, int L, int tid, int nthr) {
+    __shared__ const uint8_t* gtab[WARM_MAXU];
+    __shared__ int gqt[WARM_MAXU];
+    const int x = L & 7, r = i >> 3, per_x = wm.n_wg >> 3;
+    if (per_x <= 0 || wm.n_jobs <= 0) return;
+    int U = 0;
+    for (int j = 0; j < wm.n_jobs; j++) {
+        const DpufWarmJob& J = wm.j[j];
+        const int c = (x - J.wb) & 7;
+        if ((J.group_bytes >> 4) < nthr) return;  // one wrap per step below
+        U += (J.nwg > c ? (J.nwg - c + 7) >> 3 : 0) * J.nr;
+    }
+    if (U <= 0) return;
+    const int tp = (U + per_x - 1) / per_x, u0 = r * tp;
+    int nu = U - u0 < tp ? U - u0 : tp;
+    if (nu > WARM_MAXU) nu = WARM_MAXU;
+    if (nu <= 0) return;
+    if (tid < nu) {
+        int u = u0 + tid;
+        const uint8_t* gp = nullptr;
+        int gq = 0;
+        for (int j = 0; j < wm.n_jobs; j++) {
+            const DpufWarmJob& J = wm.j[j];
+            const int c = (x - J.wb) & 7, cnt = J.nwg > c ? (J.nwg - c + 7) >> 3 : 0;
+            if (u < cnt * J.nr) {
+                const int lg = J.r0 + u / cnt, k = u - (u / cnt) * cnt;
+                const int g = c + 8 * k + lg * J.nwg;
+                if (g < J.n_groups) gp = J.p + (size_t)g * J.group_bytes;
+                gq = J.group_bytes >> 4;
+                break;
+            }
+            u -= cnt * J.nr;
+        }
+        gtab[tid] = gp;
+        gqt[tid] = gq > 0 ? gq : nthr;
+    }
+    __syncthreads();
+    int t = 0, o = tid;
+    uint32_t acc = 0;
+    while (t < nu) {
+        uint4 v[WARM_DEPTH];
+#pragma unroll
+        for (int k = 0; k < WARM_DEPTH; k++) {
+            v[k] = make_uint4(0u, 0u, 0u, 0u);
+            if (t < nu) {
+                const uint8_t* gp = gtab[t];
+                const int gq = gqt[t];
+                if (gp) v[k] = ((const uint4*)gp)[o];
+                o += nthr;  // nthr <= gq: at most one wrap
+                const bool wr = o >= gq;
+                o = wr ? o - gq : o;
+                t += wr ? 1 : 0;
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < WARM_DEPTH; k++) acc ^= v[k].x ^ v[k].w;
+    }
+    if (acc == 0x9E3779B9u) *wm.sink = (int32_t)acc;
+}
 
 #endif

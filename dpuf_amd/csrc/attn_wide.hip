@@ -630,7 +630,7 @@ DEV float pvd_chunk(float (*Vt)[64 / G][PVD_LD], float (*Pt)[G][PVD_LD], int h, 
 template <int HD, int G, bool Q8>
 __global__ __launch_bounds__(192) void k_attn_pvd(const float* __restrict__ P, const float* __restrict__ vc,
                                                   const int32_t* __restrict__ pos0p, int n_kv, int max_seq,
-                                                  float* __restrict__ out, DpufKvQ8 c8) {
+                                                  float* __restrict__ out, DpufKvQ8 c8, DpufWarm warm) {
     using S = PvdShape<G, Q8>;
     constexpr int DW = S::DW;
     static_assert(G == 2 || G == 4, "every 16-lane row of the chain wave holds one head");
@@ -638,11 +638,16 @@ __global__ __launch_bounds__(192) void k_attn_pvd(const float* __restrict__ P, c
     __shared__ __align__(16) float Pt[3][G][PVD_LD];
     const int L = *pos0p + 1, nck = (L + PVD_CK - 1) / PVD_CK, nfull = L / PVD_CK;
     if ((int)blockIdx.y >= HD / DW) {
-        // warm-up workgroups (after the chain workgroups in dispatch order):
-        // the V rows past the chunks the producers load at their start go
-        // into the Infinity Cache, so the producers' later loads hit there
-        // instead of each of the few chain CUs pulling its slice from HBM
+        // warm-up workgroups (after the chain workgroups in dispatch order)
         const int wi = ((int)blockIdx.y - HD / DW) * n_kv + (int)blockIdx.x;
+        if (warm.n_wg > 0) {
+            // the weight groups of the GEMVs after this launch
+            warm_read(warm, wi, (int)(blockIdx.y * gridDim.x + blockIdx.x), threadIdx.x, blockDim.x);
+            return;
+        }
+        // else the V rows past the chunks the producers load at their start
+        // go into the Infinity Cache, so the producers' later loads hit there
+        // instead of each of the few chain CUs pulling its slice from HBM
         const int nw = ((int)gridDim.y - HD / DW) * n_kv;
         constexpr int RB = Q8 ? HD : HD * 4;  // bytes per V row
         const uint8_t* base = Q8 ? (const uint8_t*)c8.vq : (const uint8_t*)vc;
@@ -758,21 +763,28 @@ static void smx_launch(void* s, int seg, float* scores, const int32_t* pos0p, in
 // (gm: its group instance, 2, 4 or 8).
 template <int HD, bool Q8>
 static void pv_wide_launch(void* s, int G, int gm, const float* scores, const float* vc, const int32_t* pos0p, int n_q,
-                           int n_kv, int max_seq, float* out, DpufKvQ8 c8) {
-    // k_attn_pvd: HD / DW chain workgroups per kv head, then (unless the
-    // softmax launch warmed V into the L2s) warm-up workgroups up to about
-    // one per CU
+                           int n_kv, int max_seq, float* out, DpufKvQ8 c8, const DpufWarm* wm) {
+    // k_attn_pvd: HD / DW chain workgroups per kv head, then warm-up
+    // workgroups up to about one per CU: of the GEMV weights in wm, or (when
+    // the softmax launch did not warm V into the L2s) of V
     if (G == 4 || G == 2) {
-        const int ns = HD / (64 / G);
-        const int nwarm = PVD_SMX_WARM && n_kv % 8 == 0 && dpuf_hip_cu_count() - n_q >= 8
-                              ? 0
-                              : (dpuf_hip_cu_count() / n_kv > ns ? dpuf_hip_cu_count() / n_kv : ns) - ns;
+        const int ns = HD / (64 / G), n_cu = dpuf_hip_cu_count();
+        DpufWarm warm;
+        memset(&warm, 0, sizeof warm);
+        int rows = 0;
+        if (wm && wm->sink && wm->n_jobs > 0 && n_cu > n_kv * ns + 8) {
+            warm = *wm;
+            warm.n_wg = (n_cu - n_kv * ns) & ~7;
+            rows = (warm.n_wg + n_kv - 1) / n_kv;
+        } else if (!(PVD_SMX_WARM && n_kv % 8 == 0 && n_cu - n_q >= 8)) {
+            rows = (n_cu / n_kv > ns ? n_cu / n_kv : ns) - ns;
+        }
         if (G == 4)
-            hipLaunchKernelGGL((k_attn_pvd<HD, 4, Q8>), dim3(n_kv, ns + nwarm), dim3(192), 0, ST(s), scores, vc, pos0p,
-                               n_kv, max_seq, out, c8);
+            hipLaunchKernelGGL((k_attn_pvd<HD, 4, Q8>), dim3(n_kv, ns + rows), dim3(192), 0, ST(s), scores, vc, pos0p,
+                               n_kv, max_seq, out, c8, warm);
         else
-            hipLaunchKernelGGL((k_attn_pvd<HD, 2, Q8>), dim3(n_kv, ns + nwarm), dim3(192), 0, ST(s), scores, vc, pos0p,
-                               n_kv, max_seq, out, c8);
+            hipLaunchKernelGGL((k_attn_pvd<HD, 2, Q8>), dim3(n_kv, ns + rows), dim3(192), 0, ST(s), scores, vc, pos0p,
+                               n_kv, max_seq, out, c8, warm);
     }
     else if (gm == 2)
         hipLaunchKernelGGL((k_attn_pvw<HD, 2, Q8>), dim3(n_kv, HD / 4), dim3(192), 0, ST(s), scores, vc, pos0p, n_q,
@@ -787,7 +799,7 @@ static void pv_wide_launch(void* s, int G, int gm, const float* scores, const fl
 
 int32_t attn_wide_f32(void* s, int32_t lmax, const float* q, const float* kc, const float* vc, float* out,
                       float* scores, const int32_t* pos0p, int32_t n_q, int32_t n_kv, int32_t hd, int32_t max_seq,
-                      float scale, const ScRope* rope) {
+                      float scale, const ScRope* rope, const DpufWarm* wm) {
     if (n_kv <= 0 || n_q % n_kv || (hd != 64 && hd != 128 && hd != 256)) return -1;
     if (lmax > max_seq) lmax = max_seq;
     const int G = n_q / n_kv;
@@ -817,7 +829,7 @@ int32_t attn_wide_f32(void* s, int32_t lmax, const float* q, const float* kc, co
 #define WIDE_LAUNCH(HDV)                                                                                          \
     if (gm == 2) SC1_LAUNCH(HDV, 2) else if (gm == 4) SC1_LAUNCH(HDV, 4) else SC1_LAUNCH(HDV, 8)                  \
     smx_launch(s, seg, scores, pos0p, max_seq, n_q, n_kv, G, vc, HDV * 4);                                         \
-    pv_wide_launch<HDV, false>(s, G, gm, scores, vc, pos0p, n_q, n_kv, max_seq, out, DpufKvQ8{});
+    pv_wide_launch<HDV, false>(s, G, gm, scores, vc, pos0p, n_q, n_kv, max_seq, out, DpufKvQ8{}, wm);
             if (hd == 64) {
                 WIDE_LAUNCH(64)
             } else if (hd == 128) {
@@ -836,7 +848,7 @@ int32_t attn_wide_f32(void* s, int32_t lmax, const float* q, const float* kc, co
 }
 
 int32_t attn_wide_q8(void* s, int32_t lmax, const int32_t* pos0, int32_t n_q, int32_t n_kv, int32_t hd,
-                     int32_t max_seq, float* scores, float* out, DpufKvQ8 c8) {
+                     int32_t max_seq, float* scores, float* out, DpufKvQ8 c8, const DpufWarm* wm) {
     if (n_kv <= 0 || n_q % n_kv || (hd != 64 && hd != 128 && hd != 256)) return -1;
     if (lmax > max_seq) lmax = max_seq;
     const int G = n_q / n_kv;
@@ -852,9 +864,12 @@ int32_t attn_wide_q8(void* s, int32_t lmax, const int32_t* pos0, int32_t n_q, in
         if (seg) {
             const int gm = G <= 2 ? 2 : G <= 4 ? 4 : 8;
             smx_launch(s, seg, scores, pos0, max_seq, n_q, n_kv, G, c8.vq, hd);
-            if (hd == 64) pv_wide_launch<64, true>(s, G, gm, scores, nullptr, pos0, n_q, n_kv, max_seq, out, c8);
-            else if (hd == 128) pv_wide_launch<128, true>(s, G, gm, scores, nullptr, pos0, n_q, n_kv, max_seq, out, c8);
-            else pv_wide_launch<256, true>(s, G, gm, scores, nullptr, pos0, n_q, n_kv, max_seq, out, c8);
+            if (hd == 64)
+                pv_wide_launch<64, true>(s, G, gm, scores, nullptr, pos0, n_q, n_kv, max_seq, out, c8, wm);
+            else if (hd == 128)
+                pv_wide_launch<128, true>(s, G, gm, scores, nullptr, pos0, n_q, n_kv, max_seq, out, c8, wm);
+            else
+                pv_wide_launch<256, true>(s, G, gm, scores, nullptr, pos0, n_q, n_kv, max_seq, out, c8, wm);
             LAUNCHED("k_attn_q8_sc/k_attn_smx/wide P.V<q8>");
             return 0;
         }

@@ -867,6 +867,24 @@ static DpufWarm attn_warm(Engine* e, const LayerJobs* lj, const LayerJobs* ln) {
     return w;
 }
 
+/* What the P.V launch of a long-context one-token step warms on the CUs its
+ * chain workgroups leave idle (about 17 us at 4 096 keys): the same groups,
+ * with the O groups on the XCDs of the workgroups that read them (that O
+ * launch preps its own input in producer workgroups ahead of its GEMV
+ * workgroups), and two gate/up rounds instead of one.  Measured at 4 096
+ * keys: one gate/up round 3.14 -> 3.08 ms/token, two 3.05, three 3.19, four
+ * 3.32 (the P.V launch then outlasts its chains); the down projection as
+ * well, 3.84. */
+static DpufWarm attn_warm_fed_o(Engine* e, const LayerJobs* lj, const LayerJobs* ln) {
+    DpufWarm w;
+    memset(&w, 0, sizeof w);
+    if (dpuf_hip_warm_add(&w, 1, &lj->o, 0, 1)) w.j[0].wb += dpuf_hip_fed_producers(e->qd, &lj->o);
+    dpuf_hip_warm_add(&w, 2, lj->gu, 0, 2);
+    if (ln) dpuf_hip_warm_add(&w, 3, ln->qkv, 0, 1);
+    w.sink = e->d_ids + DPUF_AMD_MAX_BATCH + 8;
+    return w;
+}
+
 /* Attention of a multi-session step at layer l (ms_n = M tokens, one per
  * session): the first ms_short tokens (fp32 cache, short context) in one
  * fused decode launch over their sessions' caches; every other token alone,
@@ -896,13 +914,13 @@ static void enqueue_ms_attention(Engine* e, int32_t l, int32_t M, float eps, flo
             const DpufKvQ8 c8 = slot_q8(e, e->ms_slot[m], l);
             dpuf_hip_qk_rope_kv(s, 1, q, k, v, qn, kn, eps, e->d_cos, e->d_sin, NULL, NULL, pp, e->nq, e->nkv, e->hd,
                                 e->max_seq, &c8);
-            dpuf_hip_attn_q8(s, 1, keys, q, c8, ao, e->scores, pp, e->nq, e->nkv, e->hd, e->max_seq, scale);
+            dpuf_hip_attn_q8(s, 1, keys, q, c8, ao, e->scores, pp, e->nq, e->nkv, e->hd, e->max_seq, scale, NULL);
             continue;
         }
         float* kc = slot_k(e, e->ms_slot[m]) + lo;
         float* vc = slot_v(e, e->ms_slot[m]) + lo;
         if (dpuf_hip_attn_decode_rope(s, keys, q, k, v, qn, kn, eps, e->d_cos, e->d_sin, kc, vc, ao, e->scores, pp,
-                                      e->nq, e->nkv, e->hd, e->max_seq, scale) == 0)
+                                      e->nq, e->nkv, e->hd, e->max_seq, scale, NULL) == 0)
             continue;
         dpuf_hip_qk_rope_kv(s, 1, q, k, v, qn, kn, eps, e->d_cos, e->d_sin, kc, vc, pp, e->nq, e->nkv, e->hd,
                             e->max_seq, NULL);
@@ -976,8 +994,9 @@ static void enqueue_layers(Engine* e, int32_t M, int32_t keep_tiles) {
                 const DpufKvQ8 c8 = slot_q8(e, e->active, l);
                 dpuf_hip_qk_rope_kv(s, M, e->q, e->k, e->v, e->d_norm[4 * l + 1], e->d_norm[4 * l + 2], eps,
                                     e->d_cos, e->d_sin, NULL, NULL, e->d_pos0, e->nq, e->nkv, e->hd, e->max_seq, &c8);
+                const DpufWarm wq = attn_warm_fed_o(e, &lj, ln);
                 dpuf_hip_attn_q8(s, M, e->capturing ? e->cap_lmax : e->host_pos0 + M, e->q, c8, e->ao, e->scores,
-                                 e->d_pos0, e->nq, e->nkv, e->hd, e->max_seq, scale);
+                                 e->d_pos0, e->nq, e->nkv, e->hd, e->max_seq, scale, M == 1 ? &wq : NULL);
                 if (M > 1) dpuf_hip_prep(s, M, e->qd, e->ao, W[W_O].sign, e->prep[0]);
                 o_prep = M == 1;
                 fused = 1;
@@ -992,12 +1011,14 @@ static void enqueue_layers(Engine* e, int32_t M, int32_t keep_tiles) {
                  * it can; otherwise it is a launch of its own */
                 int32_t prepped = 0;
                 /* one token: QK-norm, RoPE and the KV store inside the scores
-                 * launch when the wide kernels apply */
+                 * launch when the wide kernels apply; their P.V launch warms
+                 * the caches for the GEMVs after it */
+                const DpufWarm wd = attn_warm_fed_o(e, &lj, ln);
                 const int rope_done =
                     M == 1 && dpuf_hip_attn_decode_rope(s, lmax, e->q, e->k, e->v, e->d_norm[4 * l + 1],
                                                         e->d_norm[4 * l + 2], eps, e->d_cos, e->d_sin, kc, vc, e->ao,
                                                         e->scores, e->d_pos0, e->nq, e->nkv, e->hd, e->max_seq,
-                                                        scale) == 0;
+                                                        scale, &wd) == 0;
                 if (!rope_done) {
                     dpuf_hip_qk_rope_kv(s, M, e->q, e->k, e->v, e->d_norm[4 * l + 1], e->d_norm[4 * l + 2], eps,
                                         e->d_cos, e->d_sin, kc, vc, e->d_pos0, e->nq, e->nkv, e->hd, e->max_seq, NULL);

@@ -671,23 +671,40 @@ static MvKernel mv_fed_kernel(int mode, int nl) {
 // Only for a plan of one group per workgroup with the activations held
 // (every workgroup resident at once, weights issued before the wait);
 // returns -1 without launching otherwise.
-int32_t dpuf_hip_swiglu_gemv(void* s, int32_t I, const float* gate, const float* up, float dz, const uint8_t* sign,
-                             const DpufGemvJob* job, int32_t* flags, const int32_t* serial) {
+// The plan of a producer-fed launch of job over I activations: kernel,
+// threads, producers, GEMV workgroups, LDS bytes; false when it does not apply.
+static bool fed_plan(int32_t I, const DpufGemvJob* job, MvKernel& kf, int& threads, int& np, int& nwg, size_t& lds) {
     const int mode = job->w.mode;
-    if ((mode != 12 && mode != 13 && mode != 14) || job->w.cols != I || I <= 0 || I % 64 || !flags || !serial)
-        return -1;
+    if ((mode != 12 && mode != 13 && mode != 14) || job->w.cols != I || I <= 0 || I % 64) return false;
     const int n_blk = I >> 5, S = (n_blk + 7) >> 3;
-    if (S > (MV_HOIST48 ? 4 : 3) * (16 - MV_NC)) return -1;  // activations loaded per round: no such mode
+    if (S > (MV_HOIST48 ? 4 : 3) * (16 - MV_NC)) return false;  // activations loaded per round: no such mode
     const int ng = job->g1 - job->g0 > 0 ? job->g1 - job->g0 : 0;
     MvKernel k, k1;
     int nw, most, wb[4] = {0, 0, 0, 0};
-    if (mv_plan(1, &ng, I, mode, k, k1, nw, wb, most) == 0 || most != 1) return -1;
-    const int threads = nw * 64, np = (I / 4 + threads - 1) / threads;
-    if (np > 64) return -1;
+    if (mv_plan(1, &ng, I, mode, k, k1, nw, wb, most) == 0 || most != 1) return false;
+    threads = nw * 64;
+    np = (I / 4 + threads - 1) / threads;
+    if (np > 64) return false;
     const int nl = S <= 16 - MV_NC ? 1 : S <= 2 * (16 - MV_NC) ? 2 : S <= 3 * (16 - MV_NC) ? 3 : 4;
-    MvKernel kf = mv_fed_kernel(mode, nl);
-    const size_t lds = (size_t)8 * (n_blk + 2) * 8;
-    if (ng > mv_capacity(kf, threads, lds)) return -1;  // every GEMV workgroup resident at once
+    kf = mv_fed_kernel(mode, nl);
+    lds = (size_t)8 * (n_blk + 2) * 8;
+    nwg = wb[1];
+    return ng <= mv_capacity(kf, threads, lds);  // every GEMV workgroup resident at once
+}
+
+int32_t dpuf_hip_fed_producers(int32_t I, const DpufGemvJob* job) {
+    MvKernel kf;
+    int threads, np, nwg;
+    size_t lds;
+    return fed_plan(I, job, kf, threads, np, nwg, lds) ? np : 0;
+}
+
+int32_t dpuf_hip_swiglu_gemv(void* s, int32_t I, const float* gate, const float* up, float dz, const uint8_t* sign,
+                             const DpufGemvJob* job, int32_t* flags, const int32_t* serial) {
+    MvKernel kf;
+    int threads, np, nwg;
+    size_t lds;
+    if (!flags || !serial || !fed_plan(I, job, kf, threads, np, nwg, lds)) return -1;
     if (!g_err_word) {
         note(hipErrorInvalidValue, "dpuf_hip_swiglu_gemv: no device error word bound");
         return -1;
@@ -703,8 +720,8 @@ int32_t dpuf_hip_swiglu_gemv(void* s, int32_t I, const float* gate, const float*
     A.j[0].rows = job->w.rows;
     A.j[0].x = job->p;
     A.j[0].x.h = NULL;
-    A.wb[0] = wb[0];
-    A.wb[1] = wb[1];
+    A.wb[0] = 0;
+    A.wb[1] = nwg;
     A.err = g_err_word;
     A.nbuf = 1;
     A.nc = 0;
@@ -716,7 +733,7 @@ int32_t dpuf_hip_swiglu_gemv(void* s, int32_t I, const float* gate, const float*
     A.psign = sign;
     A.pflag = flags;
     A.pep = serial;
-    hipLaunchKernelGGL(kf, dim3(np + wb[1]), dim3(threads), lds, ST(s), A);
+    hipLaunchKernelGGL(kf, dim3(np + nwg), dim3(threads), lds, ST(s), A);
     LAUNCHED("k_mv");
     return 0;
 }

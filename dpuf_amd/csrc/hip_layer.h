@@ -174,6 +174,10 @@ void dpuf_hip_gemv_zero(void* s, int32_t M, const DpufGemvJob* job, int32_t r0, 
  * jobs (one mode) as the GEMV will be launched; returns 0 when they do not
  * fit (wm unchanged). */
 int32_t dpuf_hip_warm_add(DpufWarm* wm, int32_t n_jobs, const DpufGemvJob* jobs, int32_t r0, int32_t nr);
+/* Producer workgroups ahead of the GEMV workgroups in dpuf_hip_swiglu_gemv's
+ * launch of job over I activations (0 when that launch does not apply):
+ * what a warm-up plan of the job adds to its workgroup base. */
+int32_t dpuf_hip_fed_producers(int32_t I, const DpufGemvJob* job);
 /* Caps the workgroups of an M == 1 GEMV or K-split GEMM launch (<= 0:
  * device capacity only). */
 void dpuf_hip_set_gemv_max_wg(int32_t n);
@@ -201,15 +205,19 @@ int32_t dpuf_hip_attn_split(void* s, int32_t M, int32_t lmax, const float* q, co
 /* One-token decode past the fused kernel's range (the split path's wide
  * kernels) with the QK-norm, RoPE and KV store of the token (raw q, k, v)
  * done inside the scores launch; -1 with nothing launched when that path
- * does not apply (then qk_rope_kv + attn_split). */
+ * does not apply (then qk_rope_kv + attn_split).  warm (or NULL): weight
+ * groups that workgroups of the P.V launch read into the caches on the CUs
+ * its chains leave idle (groups of 2 and 4). */
 int32_t dpuf_hip_attn_decode_rope(void* s, int32_t lmax, float* q, const float* k, const float* v, const float* qn,
                                   const float* kn, float eps, const float* cos_tab, const float* sin_tab, float* kc,
                                   float* vc, float* out, float* scores, const int32_t* pos0p, int32_t n_q,
-                                  int32_t n_kv, int32_t hd, int32_t max_seq, float scale);
+                                  int32_t n_kv, int32_t hd, int32_t max_seq, float scale, const DpufWarm* warm);
 /* Attention over the int8 KV cache (kv_type 1) for M tokens at positions
- * pos0 .. pos0 + M - 1 of one layer; lmax bounds the keys any replay reaches. */
+ * pos0 .. pos0 + M - 1 of one layer; lmax bounds the keys any replay reaches.
+ * warm (or NULL): as for dpuf_hip_attn_decode_rope, on the one-token path. */
 void dpuf_hip_attn_q8(void* s, int32_t M, int32_t lmax, const float* q, DpufKvQ8 c8, float* out, float* scores,
-                      const int32_t* pos0, int32_t n_q, int32_t n_kv, int32_t hd, int32_t max_seq, float scale);
+                      const int32_t* pos0, int32_t n_q, int32_t n_kv, int32_t hd, int32_t max_seq, float scale,
+                      const DpufWarm* warm);
 /* n rows of fp32 K and V (device) quantised into rows row0 .. of the int8
  * cache, as the KV store does; and n values from element off dequantised. */
 void dpuf_hip_q8_rows(void* s, const float* k, const float* v, int32_t n, int32_t hd, DpufKvQ8 c8, size_t row0);
