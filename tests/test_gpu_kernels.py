@@ -33,8 +33,9 @@ def _same_bits(a, b):
 @pytest.mark.parametrize("rows,cols", SHAPES + SHAPES_8B)
 @pytest.mark.parametrize("m", [1, 7])
 def test_matmul_f32_bit_exact(eng, orc, rows, cols, m):
-    if cols >= 4096 and m > 1:
-        pytest.skip("covered at M=1 for the large shapes")
+    """M = 1 through the one-row GEMV; M = 7 through the few-token GEMMs
+    (at the 8B shapes: fragment pairs for 12288 rows, the K-split kernels for
+    the others)."""
     blob, d = _mat(rows, cols, 11 + rows)
     x = _x(m, cols, rows + cols)
     # a block with amax <= 1e-4 exercises the zero-scale path
