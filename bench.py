@@ -165,6 +165,8 @@ def main():
     ap.add_argument("--graph", type=int, default=1,
                     help="1: one-token steps replay HIP graphs (the default) and the device-argmax entry is timed "
                          "too; 0: every kernel is enqueued (per-kernel traces)")
+    ap.add_argument("--warm-seconds", type=float, default=0.0,
+                    help="with --roofline-only: seconds of device copies before the timed launches")
     ap.add_argument("--roofline-only", action="store_true",
                     help="only the dominant-kernel roofline measurement (for the matching rocprofv3 run)")
     args = ap.parse_args()
@@ -223,6 +225,15 @@ def main():
                 "bytes_per_launch": by.value, "us_per_launch": round(ms * 1e3, 3), "launches": iters}
 
     if args.roofline_only:
+        # right after engine creation the GPU is still at idle clocks;
+        # --warm-seconds of device copies (another kernel, so a profiler's
+        # statistics of the GEMV cover only the timed launches) bring it
+        # closer to the clocks the default run's roofline leg sees after the
+        # decode legs.  Kernel-time runs use it; counter runs leave it at 0,
+        # so that the only copies are the calibration's.
+        t_end = time.time() + args.warm_seconds
+        while time.time() < t_end:
+            assert eng.dpuf_amd_copy_bench(COPY_CAL_BYTES, 256) > 0, eng.dpuf_amd_last_error()
         rl = roofline()
         eng.dpuf_engine_destroy(h)
         # a device-to-device copy of known size: the reference for scaling the
