@@ -33,9 +33,10 @@
 // operations, sp = ws * xs and the fma, with the chains in registers across
 // the block loop, so the block order is the reference's.
 //
-// A workgroup of 4 waves computes 64 GM_RF rows x 16 TT tokens; wave w owns
-// GM_RF 16-row fragments and all the tokens as TT 16-token tiles (GM_RF TT
-// MFMAs per block).  Activations arrive as fp16 (DpufPrep.h, written by the
+// A workgroup of NW = 4 or 8 waves computes 16 NW GM_RF rows x 16 TT tokens;
+// wave w owns GM_RF 16-row fragments and all the tokens as TT 16-token tiles
+// (GM_RF TT MFMAs per block).  With 8 waves twice the rows share a staged
+// token tile: half the activation staging per MFMA.  Activations arrive as fp16 (DpufPrep.h, written by the
 // prep kernels) and are staged in LDS, GM_SB blocks per stage, double-
 // buffered, one barrier per stage; a token's 64 bytes per block are four
 // 16-byte chunks stored XOR-swizzled by token so a fragment read is free of
@@ -49,6 +50,10 @@
 #define GM_RF 1  // 16-row fragments per wave (workgroup = 64 GM_RF rows)
 #define GM_TT 4  // 16-token tiles per workgroup
 #define GM_XCD 1  // XCD-grouped workgroup order
+// Launches of at least this many rows (the fused gate + up projection) take
+// 8-wave workgroups: pp512 at the 8B shape 21.2 -> 20.85 ms; Q/K/V, O and down
+// with them as well, 21.1 ms; down as well, 20.8 ms.
+#define GM_NW8_ROWS 16384
 
 #define GM_RSRC3 0x00020000  // buffer descriptor word 3 (gfx9 family): 32-bit raw data
 
@@ -105,16 +110,19 @@ DEV gm_h8 gm_unpack_a_asym(uint32_t w, uint32_t h) {
 // Modes 13 / 14 hold a 64-block's even half (its D tiles, token scales and
 // sums, row scales) across the odd one: 2 waves per SIMD keep that in
 // registers instead of spilling at the 128 VGPRs of 4.
-template <int TT, int RF, int MODE>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MODE == 12 ? 4 : 2))) void k_gemm_mfma(
+template <int TT, int RF, int MODE, int NW>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(MODE == 12 ? 4 : 2))) void k_gemm_mfma(
     GmArgs A) {
     constexpr int NT = 16 * TT;  // tokens per workgroup
+    constexpr int NTH = 64 * NW;  // threads per workgroup
+    constexpr int GPW = 2 * RF * NW;  // 8-row groups per workgroup
     constexpr bool ASYM = MODE != 12;
     static_assert(GM_SB % 2 == 0, "a stage holds whole 64-blocks");
+    static_assert(NW == 4 || NW == 8, "4 or 8 waves");
     __shared__ __align__(16) uint8_t bq[2][GM_SB][NT][64];  // f16 activations [stage][block][token][k]
     __shared__ __align__(16) float bs[2][GM_SB][16][TT];    // block scales [stage][block][token % 16][token / 16]
     __shared__ __align__(16) int32_t bm[ASYM ? 2 : 1][GM_SB][16][TT];  // 8 * block sums (modes 13 / 14)
-    __shared__ __align__(16) uint32_t bw[2][GM_SB][32 * RF];  // weight scales [stage][block][group * 4 + word]
+    __shared__ __align__(16) uint32_t bw[2][GM_SB][4 * GPW];  // weight scales [stage][block][group * 4 + word]
     // Workgroups go to the 8 XCDs round-robin by linear id L.  L = xcd +
     // 8 j with j = gy r + ty puts row tile 8 r + xcd of every token tile ty on
     // one XCD, dispatched back to back, so the gy workgroups that read the
@@ -130,7 +138,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MODE == 12 
         const int zi = rt - A.tb[A.n_jobs];
         if (zi < A.zt) {
             const int r = A.z0 + 64 * zi + (threadIdx.x & 63);
-            for (int t = threadIdx.x >> 6; t < 16 * TT; t += 4) {
+            for (int t = threadIdx.x >> 6; t < 16 * TT; t += NW) {
                 const int m = ty * 16 * TT + t;
                 if (m < A.M && r < A.z1) A.zo[(size_t)m * A.zld + r] = 0.0f;
             }
@@ -146,7 +154,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MODE == 12 
     const uint16_t* const Jh = ji == 0 ? A.j[0].h : ji == 1 ? A.j[1].h : A.j[2].h;
     const float* const Js = ji == 0 ? A.j[0].s : ji == 1 ? A.j[1].s : A.j[2].s;
     const int32_t* const Jm = ji == 0 ? A.j[0].m : ji == 1 ? A.j[1].m : A.j[2].m;
-    const int gb = J.g0 + (rt - A.tb[ji]) * 8 * RF;  // first group of the workgroup
+    const int gb = J.g0 + (rt - A.tb[ji]) * GPW;  // first group of the workgroup
     const int m0 = ty * NT;
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, i16 = l & 15, kc = l >> 4;
     const int K = A.K, M = A.M, n_blk = K >> 5;
@@ -171,12 +179,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MODE == 12 
         // mode 14: the lane's high-bit word (chunk kc's bits are in word kc / 2)
         oh[f] = (uint32_t)((size_t)(ga - gw0) * gstride + (size_t)n_blk * 144 + (i16 & 7) * 8 + (kc >> 1) * 4);
     }
-    // Weight scales go through LDS with the activations: a stage's 8 RF
+    // Weight scales go through LDS with the activations: a stage's GPW
     // groups x GM_SB blocks x 8 fp16 scales are WD dwords, dword d = (tid +
-    // 256 k) % WD (group d / (4 GM_SB), block (d / 4) % GM_SB, word d % 4),
+    // NTH k) % WD (group d / (4 GM_SB), block (d / 4) % GM_SB, word d % 4),
     // addressed from the workgroup's first group; threads past WD repeat a
     // dword.  Blocks past the end read bytes that are never used.
-    constexpr int WD = 32 * RF * GM_SB, WPT = (WD + 255) / 256;
+    constexpr int WD = 4 * GPW * GM_SB, WPT = (WD + NTH - 1) / NTH;
     const __amdgpu_buffer_rsrc_t rg = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(J.g + (size_t)gb * gstride), 0,
         (int)((size_t)(J.g1 - gb) * gstride < 0xFFFFFFFFu ? (size_t)(J.g1 - gb) * gstride : 0xFFFFFFFFu), GM_RSRC3);
@@ -184,27 +192,27 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MODE == 12 
     int wgi[WPT];               // their LDS word index in a stage buffer
 #pragma unroll
     for (int k = 0; k < WPT; k++) {
-        const int wd = (tid + 256 * k) % WD, g = wd / (4 * GM_SB), b = (wd >> 2) % GM_SB, w4 = wd & 3;
+        const int wd = (tid + NTH * k) % WD, g = wd / (4 * GM_SB), b = (wd >> 2) % GM_SB, w4 = wd & 3;
         og[k] = (uint32_t)((size_t)(min(gb + g, J.g1 - 1) - gb) * gstride + b * 16 + w4 * 4);
-        wgi[k] = b * 32 * RF + g * 4 + w4;
+        wgi[k] = b * 4 * GPW + g * 4 + w4;
     }
     // staging: a stage holds NT tokens x GM_SB blocks of 64 fp16 bytes, four
-    // 16-byte chunks each.  Chunk c = tid + 256 k of the stage is chunk c & 3
+    // 16-byte chunks each.  Chunk c = tid + NTH k of the stage is chunk c & 3
     // of pair c / 4 = (token (c / 4) % NT, block (c / 4) / NT), so the 64
     // lanes of a load read 16 tokens' 64 contiguous bytes.  Scale i = tid +
-    // 256 k is pair i.  Loads are unconditional, at token and block clamped
+    // NTH k is pair i.  Loads are unconditional, at token and block clamped
     // into range: a token past M only feeds output columns that are never
     // stored, a block past the end is never computed, and a load without a
     // branch around it keeps the compiler's wait counts exact.
-    constexpr int CPT = NT * GM_SB * 4 / 256, SPT = (NT * GM_SB + 255) / 256;
-    static_assert(CPT >= 1 && NT * GM_SB * 4 % 256 == 0, "whole chunks per thread");
+    constexpr int CPT = NT * GM_SB * 4 / NTH, SPT = (NT * GM_SB + NTH - 1) / NTH;
+    static_assert(CPT >= 1 && NT * GM_SB * 4 % NTH == 0, "whole chunks per thread");
     const int n_st = (n_blk + GM_SB - 1) / GM_SB;
     gm_u4 sq[CPT];  // a native vector: a struct copy would keep the array in scratch
     float ss[SPT];
     int32_t sm[SPT];
     // byte offsets of the token rows (M K < 2^30 is checked at launch); with
-    // NT = 64 a chunk's block (k) and a scale's block (the wave, + 4 k) are
-    // uniform and go into the scalar offset
+    // NT = 64 a chunk's block (wave / 4 + NW k / 4) and a scale's block (the
+    // wave, + NW k) are uniform and go into the scalar offset
     const __amdgpu_buffer_rsrc_t rh = __builtin_amdgcn_make_buffer_rsrc((void*)Jh, 0, M * K * 2, GM_RSRC3);
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)Js, 0, M * n_blk * 4, GM_RSRC3);
     const __amdgpu_buffer_rsrc_t rm =
@@ -212,13 +220,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MODE == 12 
     uint32_t ho[CPT], so[SPT];
 #pragma unroll
     for (int k = 0; k < CPT; k++) {
-        const int pr = (tid >> 2) + 64 * k, m = min(m0 + pr % NT, M - 1);
+        const int pr = (tid >> 2) + (NTH / 4) * k, m = min(m0 + pr % NT, M - 1);
         const int sbt = NT == 64 ? 0 : pr / NT;
         ho[k] = (uint32_t)(2 * (m * K + 32 * sbt + 8 * (tid & 3)));
     }
 #pragma unroll
     for (int k = 0; k < SPT; k++) {
-        const int i = min(tid + 256 * k, NT * GM_SB - 1), m = min(m0 + i % NT, M - 1);
+        const int i = min(tid + NTH * k, NT * GM_SB - 1), m = min(m0 + i % NT, M - 1);
         const int sbt = NT == 64 ? 0 : i / NT;
         so[k] = (uint32_t)(4 * (m * n_blk + sbt));
     }
@@ -227,13 +235,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MODE == 12 
     auto stage_load = [&](int st) {
 #pragma unroll
         for (int k = 0; k < CPT; k++) {
-            const int sbt = NT == 64 ? k : 0;
+            const int sbt = NT == 64 ? (wu >> 2) + k * (NW / 4) : 0;
             const int b = NT == 64 ? min(st * GM_SB + sbt, n_blk - 1) : st * GM_SB;
             sq[k] = __builtin_bit_cast(gm_u4, __builtin_amdgcn_raw_buffer_load_b128(rh, ho[k], b * 64, 0));
         }
 #pragma unroll
         for (int k = 0; k < SPT; k++) {
-            const int b = NT == 64 ? min(st * GM_SB + wu + 4 * k, n_blk - 1) : st * GM_SB;
+            const int b = NT == 64 ? min(st * GM_SB + wu + NW * k, n_blk - 1) : st * GM_SB;
             ss[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, so[k], b * 4, 0));
             if (ASYM) sm[k] = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(rm, so[k], b * 4, 0);
         }
@@ -243,13 +251,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MODE == 12 
     auto stage_store = [&](int buf) {
 #pragma unroll
         for (int k = 0; k < CPT; k++) {
-            const int c = tid + 256 * k, pr = c >> 2, tk = pr % NT, sbt = pr / NT, qu = c & 3;
+            const int c = tid + NTH * k, pr = c >> 2, tk = pr % NT, sbt = pr / NT, qu = c & 3;
             *(gm_u4*)&bq[buf][sbt][tk][16 * (qu ^ ((tk >> 1) & 3))] = sq[k];
         }
 #pragma unroll
         for (int k = 0; k < SPT; k++) {
-            const int i = tid + 256 * k, tk = i % NT, sbt = i / NT;
-            if (NT * GM_SB % 256 == 0 || i < NT * GM_SB) {
+            const int i = tid + NTH * k, tk = i % NT, sbt = i / NT;
+            if (NT * GM_SB % NTH == 0 || i < NT * GM_SB) {
                 bs[buf][sbt][tk & 15][tk >> 4] = ss[k];
                 if (ASYM) bm[ASYM ? buf : 0][sbt][tk & 15][tk >> 4] = sm[k];
             }
@@ -887,6 +895,12 @@ void dpuf_hip_gm_launch(void* s, int32_t M, int32_t n_jobs, const DpufGemvJob* j
         GmArgs G;
         memset(&G, 0, sizeof G);
         int t = 0;
+        // 8-wave workgroups (128 rows sharing one staged token tile) for the
+        // launches with the most rows, 4-wave ones otherwise
+        int rows_all = 0;
+        for (int i = 0; i < n_jobs; i++) rows_all += jobs[i].g1 > jobs[i].g0 ? 8 * (jobs[i].g1 - jobs[i].g0) : 0;
+        const int nw = jobs[0].w.mode == 12 && M > 16 && rows_all >= GM_NW8_ROWS ? 8 : 4;
+        const int gpw = 2 * GM_RF * nw;
         G.n_jobs = n_jobs;
         G.K = jobs[0].w.cols;
         G.M = M;
@@ -910,7 +924,7 @@ void dpuf_hip_gm_launch(void* s, int32_t M, int32_t n_jobs, const DpufGemvJob* j
             G.j[i].ldo = jobs[i].ldo;
             G.tb[i] = t;
             const int ng = jobs[i].g1 - jobs[i].g0;
-            t += ng > 0 ? (ng + 8 * GM_RF - 1) / (8 * GM_RF) : 0;
+            t += ng > 0 ? (ng + gpw - 1) / gpw : 0;
         }
         G.tb[n_jobs] = t;
         if (zo && z1 > z0) {
@@ -975,11 +989,13 @@ void dpuf_hip_gm_launch(void* s, int32_t M, int32_t n_jobs, const DpufGemvJob* j
         // modes 13 / 14 take this kernel at every M (the K-split kernels
         // are mode 12 only)
         if (mode == 13)
-            hipLaunchKernelGGL((k_gemm_mfma<GM_TT, GM_RF, 13>), grid, dim3(256), 0, ST(s), G);
+            hipLaunchKernelGGL((k_gemm_mfma<GM_TT, GM_RF, 13, 4>), grid, dim3(256), 0, ST(s), G);
         else if (mode == 14)
-            hipLaunchKernelGGL((k_gemm_mfma<GM_TT, GM_RF, 14>), grid, dim3(256), 0, ST(s), G);
+            hipLaunchKernelGGL((k_gemm_mfma<GM_TT, GM_RF, 14, 4>), grid, dim3(256), 0, ST(s), G);
+        else if (nw == 8)
+            hipLaunchKernelGGL((k_gemm_mfma<GM_TT, GM_RF, 12, 8>), grid, dim3(512), 0, ST(s), G);
         else
-            hipLaunchKernelGGL((k_gemm_mfma<GM_TT, GM_RF, 12>), grid, dim3(256), 0, ST(s), G);
+            hipLaunchKernelGGL((k_gemm_mfma<GM_TT, GM_RF, 12, 4>), grid, dim3(256), 0, ST(s), G);
         LAUNCHED("k_gemm_mfma");
     }
 }

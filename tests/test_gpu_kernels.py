@@ -155,10 +155,13 @@ def test_matmul_few_token_workgroup_caps(eng, orc, cap):
     assert _same_bits(out_g, out_o), f"max abs diff {np.nanmax(np.abs(out_g - out_o))}"
 
 
-@pytest.mark.parametrize("rows,cols,m", [(200, 320, 65), (200, 320, 130), (1000, 1024, 130), (72, 64, 200)])
+@pytest.mark.parametrize("rows,cols,m", [(200, 320, 65), (200, 320, 130), (1000, 1024, 130), (72, 64, 200),
+                                         (16400, 320, 130), (16384, 4096, 40)])
 def test_matmul_token_tiles_bit_exact(eng, orc, rows, cols, m):
-    """M > 64: several 64-token tiles of the slab GEMM (the last one ragged),
-    partial 64-row tiles, and 10-block rows (a partial last LDS stage)."""
+    """M > 16: several 64-token tiles of the slab GEMM (the last one ragged),
+    partial 64-row tiles, and 10-block rows (a partial last LDS stage); at
+    16384 rows and more the 8-wave workgroups (128 rows, the last tile
+    partial at 16400)."""
     blob, d = _mat(rows, cols, 31 + rows)
     x = _x(m, cols, 3 * rows + cols)
     x[m - 1, 32:64] = 1e-6  # a zero-scale block in the last tile
