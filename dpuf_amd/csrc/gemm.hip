@@ -50,10 +50,13 @@
 #define GM_RF 1  // 16-row fragments per wave (workgroup = 64 GM_RF rows)
 #define GM_TT 4  // 16-token tiles per workgroup
 #define GM_XCD 1  // XCD-grouped workgroup order
-// Launches of at least this many rows (the fused gate + up projection) take
-// 8-wave workgroups: pp512 at the 8B shape 21.2 -> 20.85 ms; Q/K/V, O and down
-// with them as well, 21.1 ms; down as well, 20.8 ms.
+// Launches of at least this many rows (the fused gate + up projection) and
+// more than GM_NW8_MINM tokens take 8-wave workgroups: pp512 at the 8B shape
+// 21.2 -> 20.85 ms, pp256 13.2 -> 13.0 ms, pp128 10.2 -> 10.5 ms (half the
+// workgroups of the 4-wave grid leave CUs idle), pp32 and pp64 unchanged;
+// Q/K/V, O and down on 8 waves as well, pp512 21.1 ms; down as well, 20.8 ms.
 #define GM_NW8_ROWS 16384
+#define GM_NW8_MINM 128
 
 #define GM_RSRC3 0x00020000  // buffer descriptor word 3 (gfx9 family): 32-bit raw data
 
@@ -899,7 +902,7 @@ void dpuf_hip_gm_launch(void* s, int32_t M, int32_t n_jobs, const DpufGemvJob* j
         // launches with the most rows, 4-wave ones otherwise
         int rows_all = 0;
         for (int i = 0; i < n_jobs; i++) rows_all += jobs[i].g1 > jobs[i].g0 ? 8 * (jobs[i].g1 - jobs[i].g0) : 0;
-        const int nw = jobs[0].w.mode == 12 && M > 16 && rows_all >= GM_NW8_ROWS ? 8 : 4;
+        const int nw = jobs[0].w.mode == 12 && M > GM_NW8_MINM && rows_all >= GM_NW8_ROWS ? 8 : 4;
         const int gpw = 2 * GM_RF * nw;
         G.n_jobs = n_jobs;
         G.K = jobs[0].w.cols;

@@ -160,8 +160,8 @@ def test_matmul_few_token_workgroup_caps(eng, orc, cap):
 def test_matmul_token_tiles_bit_exact(eng, orc, rows, cols, m):
     """M > 16: several 64-token tiles of the slab GEMM (the last one ragged),
     partial 64-row tiles, and 10-block rows (a partial last LDS stage); at
-    16384 rows and more the 8-wave workgroups (128 rows, the last tile
-    partial at 16400)."""
+    16384 rows and more and M > 128 the 8-wave workgroups (128 rows, the last
+    tile partial at 16400 rows)."""
     blob, d = _mat(rows, cols, 31 + rows)
     x = _x(m, cols, 3 * rows + cols)
     x[m - 1, 32:64] = 1e-6  # a zero-scale block in the last tile
