@@ -345,6 +345,33 @@ def test_prefill_m512_8b_width_pruned(eng, orc, monkeypatch):
 
 
 @pytest.mark.timeout(600)
+def test_prefill_chunks_8b_width(eng, orc, monkeypatch):
+    """Prefill in two chunks at the Qwen3-8B width (two layers): 200 tokens
+    (the fused gate+up GEMM on 8-wave workgroups, a ragged last 64-token
+    tile), per-layer residuals of every row and the last row's logits
+    bit-identical; then 56 tokens at position 200 (4-wave workgroups) with
+    every row's logits bit-identical; then 2 decode steps."""
+    monkeypatch.delenv("DPUF_PREFILL_KEEP_TILES", raising=False)
+    monkeypatch.delenv("DPUF_GEN_KEEP_TILES", raising=False)
+    shape = dict(M.QWEN3_8B, num_layers=2, vocab_size=4096, tie_word_embeddings=1)
+    m = M.Model.build(shape, max_seq_len=272, seed=93)
+    p = Pair(eng, orc, m)
+    p.capture(200)
+    ids = np.random.default_rng(94).integers(0, 4096, 256).astype(np.int32)
+    log("8B-width prefill chunks of 200 and 56 tokens")
+    lg, lo = p.forward(ids[:200], 0)
+    assert bits_equal(lg, lo), maxdiff(lg, lo)
+    cg, co = p.captured(200)
+    assert bits_equal(cg, co), maxdiff(cg, co)
+    p.capture(0)
+    lg, lo = p.forward(ids[200:], 200, only_last=0)
+    assert lg.shape == (56, 4096)
+    assert bits_equal(lg, lo), maxdiff(lg, lo)
+    greedy(p, lg, lo, 256, 2, "after 200 + 56")
+    p.close()
+
+
+@pytest.mark.timeout(600)
 def test_lm_head_zone_a_151936(eng, orc, monkeypatch):
     """The LM head at its real size (151936 x 4096, 9496 tiles) with no
     layers, hidden states fed through embeds_in: 150 seeded steps, about 70 %
