@@ -536,6 +536,16 @@ typedef uint32_t gm_u4 __attribute__((ext_vector_type(4)));
 
 // Lane t of one row: columns 4t .. 4t + 3 of the 64-block t / 16 (COH: see
 // row_prep64).
+// One element of the SwiGLU with dead zone (reference swiglu_range_avx2,
+// 8-wide path, dpuf_engine.c:976-989), then the down input's sign bit.
+DEV float swiglu1(float g, float u, float dz, uint32_t neg) {
+    const float ng = fmaxf(-40.0f, fminf(0.0f - g, 40.0f));
+    const float silu = g / (1.0f + exp_poly(ng));
+    float rr = silu * u;
+    if (dz > 0.0f && !(fabsf(rr) >= dz)) rr = 0.0f;
+    return neg ? -rr : rr;
+}
+
 template <bool COH = false>
 DEV void swiglu_prep_lane(int I, const float* __restrict__ gate, const float* __restrict__ up, float dz,
                           const uint8_t* __restrict__ sign, int8_t* q, float* s, int32_t* m, uint16_t* h, int t) {
@@ -546,13 +556,7 @@ DEV void swiglu_prep_lane(int I, const float* __restrict__ gate, const float* __
     const float g[4] = {g4.x, g4.y, g4.z, g4.w}, u[4] = {u4.x, u4.y, u4.z, u4.w};
     float v[4];
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
-        const float ng = fmaxf(-40.0f, fminf(0.0f - g[k], 40.0f));
-        const float silu = g[k] / (1.0f + exp_poly(ng));
-        float rr = silu * u[k];
-        if (dz > 0.0f && !(fabsf(rr) >= dz)) rr = 0.0f;
-        v[k] = ((sb >> k) & 1u) ? -rr : rr;
-    }
+    for (int k = 0; k < 4; k++) v[k] = swiglu1(g[k], u[k], dz, (sb >> k) & 1u);
     row_prep64<COH>(v, r, blk, q, s, m, h);
 }
 

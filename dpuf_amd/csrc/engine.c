@@ -1054,12 +1054,17 @@ static void enqueue_layers(Engine* e, int32_t M, int32_t keep_tiles) {
             e->hcur = ho;
             tm_end(e, tm6);
         }
-        /* (7) gate + up in one launch */
+        /* (7) gate + up in one launch; with many rows and one shared input
+         * the launch also runs (8), SwiGLU + prep of the down input, into
+         * prep[1] (free: gate and up read prep[0]) */
+        int swi = 0;
         {
             const DpufGemvJob* js = jgu;
             double b = gemv_bytes(&W[W_GATE], 0, n_tiles_of(&W[W_GATE]), M) + gemv_bytes(&W[W_UP], 0, n_tiles_of(&W[W_UP]), M);
             const int tm7 = tm_begin(e, K_GU, b);
-            dpuf_hip_gemv(s, M, 2, js, NULL, 0.0f);
+            if (M > 1 && js[0].p.h == e->prep[0].h && js[1].p.h == e->prep[0].h)
+                swi = dpuf_hip_gemm_swiglu(s, M, js, e->deadzone, W[W_DOWN].sign, e->prep[1]) == 0;
+            if (!swi) dpuf_hip_gemv(s, M, 2, js, NULL, 0.0f);
             tm_end(e, tm7);
         }
         /* (8) SwiGLU + dead zone + prep of the down input, (9) down
@@ -1070,7 +1075,8 @@ static void enqueue_layers(Engine* e, int32_t M, int32_t keep_tiles) {
         {
             int32_t nt = n_tiles_of(&W[W_DOWN]);
             int32_t kt = (keep_tiles > 0 && keep_tiles < nt) ? keep_tiles : nt;
-            const DpufGemvJob j = lj.down;
+            DpufGemvJob j = lj.down;
+            if (swi) j.p = e->prep[1];
             int fused = 0;
             if (M == 1 && kt == nt) {
                 const int tm9 = tm_begin(e, K_DOWN, gemv_bytes(&W[W_DOWN], 0, kt, M));
@@ -1079,9 +1085,11 @@ static void enqueue_layers(Engine* e, int32_t M, int32_t keep_tiles) {
                 tm_end(e, tm9);
             }
             if (!fused) {
-                const int tm8 = tm_begin(e, K_PREP, 0);
-                dpuf_hip_swiglu_prep(s, M, I, e->gate, e->up, e->deadzone, W[W_DOWN].sign, e->prep[0]);
-                tm_end(e, tm8);
+                if (!swi) {
+                    const int tm8 = tm_begin(e, K_PREP, 0);
+                    dpuf_hip_swiglu_prep(s, M, I, e->gate, e->up, e->deadzone, W[W_DOWN].sign, e->prep[0]);
+                    tm_end(e, tm8);
+                }
                 const int tm9 = tm_begin(e, K_DOWN, gemv_bytes(&W[W_DOWN], 0, kt, M));
                 if (kt < nt)
                     dpuf_hip_gemv_zero(s, M, &j, kt * 16, W[W_DOWN].rows);

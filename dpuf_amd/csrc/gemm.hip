@@ -82,6 +82,13 @@ struct GmArgs {
     float* zo;
     int zld, z0, z1, zt;
     int32_t* err;  // device error word: set when a bounded wait of k_gemm_sk runs out
+    // gate + up with the SwiGLU (k_gemm_mfma<..., true>): the prep of the
+    // down projection's input [M][swI] goes to swo, with the down input's
+    // sign bits swsign and dead zone swdz
+    DpufPrep swo;
+    const uint8_t* swsign;
+    float swdz;
+    int swI;
 };
 
 
@@ -113,7 +120,7 @@ DEV gm_h8 gm_unpack_a_asym(uint32_t w, uint32_t h) {
 // Modes 13 / 14 hold a 64-block's even half (its D tiles, token scales and
 // sums, row scales) across the odd one: 2 waves per SIMD keep that in
 // registers instead of spilling at the 128 VGPRs of 4.
-template <int TT, int RF, int MODE, int NW>
+template <int TT, int RF, int MODE, int NW, bool SWI = false>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(MODE == 12 ? 4 : 2))) void k_gemm_mfma(
     GmArgs A) {
     constexpr int NT = 16 * TT;  // tokens per workgroup
@@ -122,6 +129,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(MODE ==
     constexpr bool ASYM = MODE != 12;
     static_assert(GM_SB % 2 == 0, "a stage holds whole 64-blocks");
     static_assert(NW == 4 || NW == 8, "4 or 8 waves");
+    static_assert(!SWI || (NW == 8 && RF == 1 && TT == 4 && MODE == 12), "the SwiGLU pairing: 4 + 4 waves");
     __shared__ __align__(16) uint8_t bq[2][GM_SB][NT][64];  // f16 activations [stage][block][token][k]
     __shared__ __align__(16) float bs[2][GM_SB][16][TT];    // block scales [stage][block][token % 16][token / 16]
     __shared__ __align__(16) int32_t bm[ASYM ? 2 : 1][GM_SB][16][TT];  // 8 * block sums (modes 13 / 14)
@@ -148,18 +156,28 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(MODE ==
         }
         return;
     }
+    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, i16 = l & 15, kc = l >> 4;
+    const int wu = __builtin_amdgcn_readfirstlane(w);
+    // SWI: waves 0-3 compute job 0 (gate), waves 4-7 job 1 (up), the same 64
+    // rows (8 groups) of each, and the activations are the jobs' shared input
     int ji = 0;
-    if (A.n_jobs > 1 && rt >= A.tb[1]) ji = 1;
-    if (A.n_jobs > 2 && rt >= A.tb[2]) ji = 2;
+    if (SWI) {
+        ji = wu >> 2;
+    } else {
+        if (A.n_jobs > 1 && rt >= A.tb[1]) ji = 1;
+        if (A.n_jobs > 2 && rt >= A.tb[2]) ji = 2;
+    }
     // the job's fields picked from the kernel arguments by uniform selects,
     // so they stay in scalar registers through the loop
     const GmJob& J = ji == 0 ? A.j[0] : ji == 1 ? A.j[1] : A.j[2];
     const uint16_t* const Jh = ji == 0 ? A.j[0].h : ji == 1 ? A.j[1].h : A.j[2].h;
     const float* const Js = ji == 0 ? A.j[0].s : ji == 1 ? A.j[1].s : A.j[2].s;
     const int32_t* const Jm = ji == 0 ? A.j[0].m : ji == 1 ? A.j[1].m : A.j[2].m;
-    const int gb = J.g0 + (rt - A.tb[ji]) * GPW;  // first group of the workgroup
+    // first group of the workgroup (SWI: of the wave's job), and the wave's
+    // place among the waves of that job
+    const int gb = SWI ? J.g0 + rt * (GPW / 2) : J.g0 + (rt - A.tb[ji]) * GPW;
+    const int wl = SWI ? (wu & 3) : wu;
     const int m0 = ty * NT;
-    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, i16 = l & 15, kc = l >> 4;
     const int K = A.K, M = A.M, n_blk = K >> 5;
     const size_t gstride = (size_t)n_blk * (MODE == 14 ? 208 : 144);
 
@@ -169,15 +187,14 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(MODE ==
     // descriptor's range reads 0 instead of faulting).  Weights of the
     // wave's RF fragments (groups clamped into the job) are addressed from
     // the wave's first group.
-    const int wu = __builtin_amdgcn_readfirstlane(w);
-    const int gw0 = min(gb + 2 * RF * wu, J.g1 - 1);
+    const int gw0 = min(gb + 2 * RF * wl, J.g1 - 1);
     const size_t wbytes = (size_t)(J.g1 - gw0) * gstride;
     const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(J.g + (size_t)gw0 * gstride), 0, (int)(wbytes < 0xFFFFFFFFu ? wbytes : 0xFFFFFFFFu), GM_RSRC3);
     uint32_t on[RF], oh[RF];
 #pragma unroll
     for (int f = 0; f < RF; f++) {
-        const int ga = min(gb + 2 * RF * wu + 2 * f + (i16 >> 3), J.g1 - 1);
+        const int ga = min(gb + 2 * RF * wl + 2 * f + (i16 >> 3), J.g1 - 1);
         on[f] = (uint32_t)((size_t)(ga - gw0) * gstride + (size_t)n_blk * 16 + (i16 & 7) * 16 + kc * 4);
         // mode 14: the lane's high-bit word (chunk kc's bits are in word kc / 2)
         oh[f] = (uint32_t)((size_t)(ga - gw0) * gstride + (size_t)n_blk * 144 + (i16 & 7) * 8 + (kc >> 1) * 4);
@@ -187,16 +204,24 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(MODE ==
     // NTH k) % WD (group d / (4 GM_SB), block (d / 4) % GM_SB, word d % 4),
     // addressed from the workgroup's first group; threads past WD repeat a
     // dword.  Blocks past the end read bytes that are never used.
+    // SWI: groups 0-7 of a stage are job 0's, 8-15 job 1's; with one dword
+    // per thread (d = tid % 256) a wave's dwords are all of one job.
     constexpr int WD = 4 * GPW * GM_SB, WPT = (WD + NTH - 1) / NTH;
+    static_assert(!SWI || (WPT == 1 && WD == 256), "one job per wave's scale dwords");
+    const int jg = SWI ? (wu & 3) >> 1 : ji;
+    const GmJob& JG = jg == 0 ? A.j[0] : jg == 1 ? A.j[1] : A.j[2];
+    const int gbg = SWI ? JG.g0 + rt * (GPW / 2) : gb;
     const __amdgpu_buffer_rsrc_t rg = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(J.g + (size_t)gb * gstride), 0,
-        (int)((size_t)(J.g1 - gb) * gstride < 0xFFFFFFFFu ? (size_t)(J.g1 - gb) * gstride : 0xFFFFFFFFu), GM_RSRC3);
+        (void*)(JG.g + (size_t)gbg * gstride), 0,
+        (int)((size_t)(JG.g1 - gbg) * gstride < 0xFFFFFFFFu ? (size_t)(JG.g1 - gbg) * gstride : 0xFFFFFFFFu),
+        GM_RSRC3);
     uint32_t og[WPT], sw[WPT];  // load offsets; the thread's scale dwords of the stage in flight
     int wgi[WPT];               // their LDS word index in a stage buffer
 #pragma unroll
     for (int k = 0; k < WPT; k++) {
         const int wd = (tid + NTH * k) % WD, g = wd / (4 * GM_SB), b = (wd >> 2) % GM_SB, w4 = wd & 3;
-        og[k] = (uint32_t)((size_t)(min(gb + g, J.g1 - 1) - gb) * gstride + b * 16 + w4 * 4);
+        const int gj = SWI ? (g & (GPW / 2 - 1)) : g;  // the group within its job's rows
+        og[k] = (uint32_t)((size_t)(min(gbg + gj, JG.g1 - 1) - gbg) * gstride + b * 16 + w4 * 4);
         wgi[k] = b * 4 * GPW + g * 4 + w4;
     }
     // staging: a stage holds NT tokens x GM_SB blocks of 64 fp16 bytes, four
@@ -431,6 +456,55 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(MODE ==
     }
     if (st < n_st) compute(st, 0, wn[0], wh[0]);
 
+    if constexpr (SWI) {
+        // SwiGLU + prep of the down input for the workgroup's 64 columns
+        // (one 64-block, blk) of the M tokens m0 .. m0 + 63.  Lane l of wave
+        // w holds acc[0][t][v] for column c = 16 (w & 3) + 4 (l / 16) + v and
+        // token 16 t + l % 16; x[w & 3][t][v][l] in the LDS of the stage
+        // buffers (free once every wave is past its last block) exchanges
+        // them: the up waves write theirs, the gate waves replace them by
+        // swiglu1(gate, up) (swiglu_prep_lane's arithmetic), then each 16-lane
+        // row preps one token's block as swiglu_prep_lane does.
+        float* x = (float*)&bq[0][0][0][0];
+        static_assert(sizeof(bq) >= 4 * TT * 4 * 64 * sizeof(float), "the exchange fits the stage buffers");
+        auto xi = [&](int ww, int t, int v, int ln) { return ((ww * TT + t) * 4 + v) * 64 + ln; };
+        const int blk = (gb * 8) >> 6;  // gb: the wave's first group; a block is 8 groups
+        __syncthreads();
+        if (wu >= 4) {
+#pragma unroll
+            for (int t = 0; t < TT; t++)
+#pragma unroll
+                for (int v = 0; v < 4; v++) x[xi(wl, t, v, l)] = acc[0][t][v];
+        }
+        __syncthreads();
+        if (wu < 4) {
+            const uint8_t* sg = A.swsign ? A.swsign + 8 * blk : nullptr;
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int c = 16 * wl + 4 * kc + v;
+                const uint32_t neg = sg ? (sg[c >> 3] >> (c & 7)) & 1u : 0u;
+#pragma unroll
+                for (int t = 0; t < TT; t++) x[xi(wl, t, v, l)] = swiglu1(acc[0][t][v], x[xi(wl, t, v, l)], A.swdz, neg);
+            }
+        }
+        __syncthreads();
+        const int R = tid >> 4, r = tid & 15, I = A.swI, nbI = I >> 5;
+#pragma unroll
+        for (int pass = 0; pass < NT / 32; pass++) {
+            const int tok = R + 32 * pass, mt = m0 + tok;
+            if (mt < M) {  // uniform over the 16-lane row
+                float v4[4];
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const int c = 4 * r + k;
+                    v4[k] = x[xi(c >> 4, tok >> 4, c & 3, 16 * ((c >> 2) & 3) + (tok & 15))];
+                }
+                row_prep64(v4, r, blk, A.swo.q + (size_t)mt * I, A.swo.s + (size_t)mt * nbI,
+                           A.swo.m + (size_t)mt * nbI, A.swo.h ? A.swo.h + (size_t)mt * I : nullptr);
+            }
+        }
+        return;
+    }
     // rows 16 RF w + 16f + 4kc + v of the workgroup, token m0 + 16t + i16
 #pragma unroll
     for (int f = 0; f < RF; f++) {
@@ -890,6 +964,55 @@ static int gm_capacity(GmKernel k, int threads) {
     return cap;
 }
 
+
+// Gate and up of M > GM_NW8_MINM tokens with the SwiGLU + dead zone + prep of
+// the down input in the same launch (k_gemm_mfma<..., true>): a workgroup's
+// waves 0-3 compute 64 rows of gate, waves 4-7 the same 64 rows of up, from
+// the activations both share, and the workgroup preps those 64 columns of
+// every token into out.  -1 (nothing launched) when the shapes do not allow
+// it: mode 12, one shared input, every row of equal gate / up matrices with
+// 64 | rows, fp16 activations, and out distinct from the input.
+int32_t dpuf_hip_gemm_swiglu(void* s, int32_t M, const DpufGemvJob* jobs, float dz, const uint8_t* sign,
+                             DpufPrep out) {
+    const DpufGemvJob& a = jobs[0];
+    const DpufGemvJob& b = jobs[1];
+    const int I = a.w.rows;
+    if (M <= GM_NW8_MINM || a.w.mode != 12 || b.w.mode != 12 || a.w.cols != b.w.cols || b.w.rows != I || I % 64 ||
+        2 * I < GM_NW8_ROWS || a.g0 != 0 || b.g0 != 0 || a.g1 != I / 8 || b.g1 != I / 8 || !a.p.h || a.p.h != b.p.h ||
+        a.p.s != b.p.s || !out.q || !out.s || !out.m || !out.h || out.h == a.p.h || out.q == a.p.q)
+        return -1;
+    if ((long long)M * a.w.cols >= (1ll << 30) || (long long)M * I >= (1ll << 30)) return -1;
+    GmArgs G;
+    memset(&G, 0, sizeof G);
+    G.n_jobs = 2;
+    G.K = a.w.cols;
+    G.M = M;
+    for (int i = 0; i < 2; i++) {
+        G.j[i].g = jobs[i].w.g;
+        G.j[i].g0 = 0;
+        G.j[i].g1 = jobs[i].g1;
+        G.j[i].rows = jobs[i].w.rows;
+        G.j[i].h = jobs[i].p.h;
+        G.j[i].s = jobs[i].p.s;
+        G.j[i].m = jobs[i].p.m;
+        G.j[i].out = jobs[i].out;
+        G.j[i].ldo = jobs[i].ldo;
+    }
+    const int tiles = I / 64;
+    G.tb[0] = 0;
+    G.tb[1] = tiles;
+    G.tb[2] = tiles;
+    G.swo = out;
+    G.swsign = sign;
+    G.swdz = dz;
+    G.swI = I;
+    const int gx = (tiles + 7) & ~7;
+    G.gy = (M + 16 * GM_TT - 1) / (16 * GM_TT);
+    const dim3 grid = GM_XCD ? dim3(gx * G.gy) : dim3(gx, G.gy);
+    hipLaunchKernelGGL((k_gemm_mfma<GM_TT, GM_RF, 12, 8, true>), grid, dim3(512), 0, ST(s), G);
+    LAUNCHED("k_gemm_mfma");
+    return 0;
+}
 
 // The M > 1 GEMM; rows [z0, z1) of zo are zeroed by the same launch.
 void dpuf_hip_gm_launch(void* s, int32_t M, int32_t n_jobs, const DpufGemvJob* jobs, float* zo, int32_t zld, int32_t z0,

@@ -178,6 +178,12 @@ int32_t dpuf_hip_warm_add(DpufWarm* wm, int32_t n_jobs, const DpufGemvJob* jobs,
  * launch of job over I activations (0 when that launch does not apply):
  * what a warm-up plan of the job adds to its workgroup base. */
 int32_t dpuf_hip_fed_producers(int32_t I, const DpufGemvJob* job);
+/* gate and up (jobs[0], jobs[1]) of M tokens and the SwiGLU + dead zone dz +
+ * prep (sign bits of the down input) of their result into out, in one
+ * launch; -1 with nothing launched when the shapes do not take it (then
+ * dpuf_hip_gemv + dpuf_hip_swiglu_prep).  out must not be the jobs' input. */
+int32_t dpuf_hip_gemm_swiglu(void* s, int32_t M, const DpufGemvJob* jobs, float dz, const uint8_t* sign,
+                             DpufPrep out);
 /* Caps the workgroups of an M == 1 GEMV or K-split GEMM launch (<= 0:
  * device capacity only). */
 void dpuf_hip_set_gemv_max_wg(int32_t n);
