@@ -1054,7 +1054,7 @@ static void enqueue_layers(Engine* e, int32_t M, int32_t keep_tiles) {
             e->hcur = ho;
             tm_end(e, tm6);
         }
-        /* (7) gate + up in one launch; with many rows and one shared input
+        /* (7) gate + up in one launch; above 16 rows, with one shared input,
          * the launch also runs (8), SwiGLU + prep of the down input, into
          * prep[1] (free: gate and up read prep[0]) */
         int swi = 0;

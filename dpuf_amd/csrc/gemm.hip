@@ -965,19 +965,21 @@ static int gm_capacity(GmKernel k, int threads) {
 }
 
 
-// Gate and up of M > GM_NW8_MINM tokens with the SwiGLU + dead zone + prep of
-// the down input in the same launch (k_gemm_mfma<..., true>): a workgroup's
+// Gate and up of M > 16 tokens with the SwiGLU + dead zone + prep of the down
+// input in the same launch (k_gemm_mfma<..., true>): a workgroup's
 // waves 0-3 compute 64 rows of gate, waves 4-7 the same 64 rows of up, from
 // the activations both share, and the workgroup preps those 64 columns of
 // every token into out.  -1 (nothing launched) when the shapes do not allow
 // it: mode 12, one shared input, every row of equal gate / up matrices with
-// 64 | rows, fp16 activations, and out distinct from the input.
+// 64 | rows, fp16 activations, and out distinct from the input.  Unlike the
+// plain gate+up launch it pays at every M > 16 (pp32 8.7 -> 8.6 ms, pp64 9.3
+// -> 9.1, pp128 10.2 either way, pp512 20.7 -> 19.8 at the 8B shape).
 int32_t dpuf_hip_gemm_swiglu(void* s, int32_t M, const DpufGemvJob* jobs, float dz, const uint8_t* sign,
                              DpufPrep out) {
     const DpufGemvJob& a = jobs[0];
     const DpufGemvJob& b = jobs[1];
     const int I = a.w.rows;
-    if (M <= GM_NW8_MINM || a.w.mode != 12 || b.w.mode != 12 || a.w.cols != b.w.cols || b.w.rows != I || I % 64 ||
+    if (M <= 16 || a.w.mode != 12 || b.w.mode != 12 || a.w.cols != b.w.cols || b.w.rows != I || I % 64 ||
         2 * I < GM_NW8_ROWS || a.g0 != 0 || b.g0 != 0 || a.g1 != I / 8 || b.g1 != I / 8 || !a.p.h || a.p.h != b.p.h ||
         a.p.s != b.p.s || !out.q || !out.s || !out.m || !out.h || out.h == a.p.h || out.q == a.p.q)
         return -1;
