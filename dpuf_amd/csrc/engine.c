@@ -1054,16 +1054,17 @@ static void enqueue_layers(Engine* e, int32_t M, int32_t keep_tiles) {
             e->hcur = ho;
             tm_end(e, tm6);
         }
-        /* (7) gate + up in one launch; above 16 rows, with one shared input,
-         * the launch also runs (8), SwiGLU + prep of the down input, into
-         * prep[1] (free: gate and up read prep[0]) */
+        /* (7) gate + up in one launch; with 2 .. 8 or more than 16 rows and
+         * one shared input, the launch also runs (8), SwiGLU + prep of the
+         * down input, into prep[1] (free: gate and up read prep[0]) */
         int swi = 0;
         {
             const DpufGemvJob* js = jgu;
             double b = gemv_bytes(&W[W_GATE], 0, n_tiles_of(&W[W_GATE]), M) + gemv_bytes(&W[W_UP], 0, n_tiles_of(&W[W_UP]), M);
             const int tm7 = tm_begin(e, K_GU, b);
             if (M > 1 && js[0].p.h == e->prep[0].h && js[1].p.h == e->prep[0].h)
-                swi = dpuf_hip_gemm_swiglu(s, M, js, e->deadzone, W[W_DOWN].sign, e->prep[1]) == 0;
+                swi = (M > 8 ? dpuf_hip_gemm_swiglu : dpuf_hip_mvt_swiglu)(s, M, js, e->deadzone, W[W_DOWN].sign,
+                                                                         e->prep[1]) == 0;
             if (!swi) dpuf_hip_gemv(s, M, 2, js, NULL, 0.0f);
             tm_end(e, tm7);
         }

@@ -77,6 +77,13 @@ struct MtArgs {
     int n_jobs;
     int wb[4];  // prefix sums of the workgroups given to each job
     int K, M;
+    // k_mvt<8, 1, 2, true>: a unit pairs 16 rows of gate (j[0]) with the same
+    // rows of up (j[1]); the SwiGLU + prep of the down input [M][swI] goes to
+    // swo (sign bits swsign, dead zone swdz)
+    DpufPrep swo;
+    const uint8_t* swsign;
+    float swdz;
+    int swI;
 };
 
 // LDS bytes of a workgroup: the staged activations of NT tokens (40 bytes
@@ -87,9 +94,10 @@ static constexpr size_t mt_lds(int n_blk, int nt, int p) {
     return (size_t)(n_blk + 4) * ((nt + (p == 2)) * 32 + nt * 8 + MT_FW * 32 * p);
 }
 
-template <int NT, int R, int P>
+template <int NT, int R, int P, bool SWI = false>
 __global__ __launch_bounds__(64 * MT_FW) void k_mvt(MtArgs A) {
     static_assert(P == 1 || NT == 8, "fragment pairs share the lanes of 8 staged tokens");
+    static_assert(!SWI || (NT == 8 && R == 1 && P == 2), "the SwiGLU pairing: gate and up fragments, one wave each");
     constexpr int NV = 4 / R;            // D components per wave
     constexpr int FPW = MT_FW / R;       // units per workgroup round
     constexpr int PF = R == 1 || P == 2 ? 8 : 12;  // quads of nibbles in flight (even)
@@ -107,7 +115,8 @@ __global__ __launch_bounds__(64 * MT_FW) void k_mvt(MtArgs A) {
     // fragment's row 4c + ((k + rho) & 3), so D components 0 .. NV - 1 are
     // the fragment's rows 4c + rho + k, the ones this wave chains
     const int fs = w / R, rho = (w % R) * NV;
-    const int nun = (J.g1 - J.g0 + NG - 1) / NG;  // units of the job
+    // units of the job (SWI: 16 rows of gate and up, two groups of each)
+    const int nun = SWI ? (J.g1 - J.g0) / 2 : (J.g1 - J.g0 + NG - 1) / NG;
     const int lb = bid - A.wb[ji], nwg = A.wb[ji + 1] - A.wb[ji];
     const uint32_t gstride = (uint32_t)n_blk * 144u;
 
@@ -121,27 +130,41 @@ __global__ __launch_bounds__(64 * MT_FW) void k_mvt(MtArgs A) {
     // a unit's nibble loads: lane row i16 is row ri of fragment x (group
     // gf + 2 x + ri / 8, clamped into the job: a missing group repeats the
     // job's last, never stored), from one descriptor at group gf
-    __amdgpu_buffer_rsrc_t rsc;
+    __amdgpu_buffer_rsrc_t rsc, rsb;  // SWI: rsc the gate groups of the unit, rsb the up groups
     uint32_t won[P];
     int ngr = NG;
     auto frag_setup = [&](int u) {
-        const int gf = J.g0 + NG * u;
         const int ri = (i16 & 12) + ((i16 + rho) & 3);
-        ngr = J.g1 - gf < NG ? J.g1 - gf : NG;
-        rsc = __builtin_amdgcn_make_buffer_rsrc((void*)(J.g + (size_t)gf * gstride), 0, (int)(ngr * gstride),
-                                                MT_RSRC3);
+        if constexpr (SWI) {
+            const int gf = J.g0 + 2 * u;
+            ngr = NG;
+            rsc = __builtin_amdgcn_make_buffer_rsrc((void*)(A.j[0].g + (size_t)gf * gstride), 0, (int)(2 * gstride),
+                                                    MT_RSRC3);
+            rsb = __builtin_amdgcn_make_buffer_rsrc((void*)(A.j[1].g + (size_t)gf * gstride), 0, (int)(2 * gstride),
+                                                    MT_RSRC3);
 #pragma unroll
-        for (int x = 0; x < P; x++) {
-            const int ga = min(gf + 2 * x + (ri >> 3), J.g1 - 1);
-            won[x] = (uint32_t)(ga - gf) * gstride + (uint32_t)n_blk * 16u + (uint32_t)(ri & 7) * 16u +
-                     (uint32_t)kc * 128u;
+            for (int x = 0; x < P; x++)
+                won[x] = (uint32_t)(ri >> 3) * gstride + (uint32_t)n_blk * 16u + (uint32_t)(ri & 7) * 16u +
+                         (uint32_t)kc * 128u;
+        } else {
+            const int gf = J.g0 + NG * u;
+            ngr = J.g1 - gf < NG ? J.g1 - gf : NG;
+            rsc = __builtin_amdgcn_make_buffer_rsrc((void*)(J.g + (size_t)gf * gstride), 0, (int)(ngr * gstride),
+                                                    MT_RSRC3);
+#pragma unroll
+            for (int x = 0; x < P; x++) {
+                const int ga = min(gf + 2 * x + (ri >> 3), J.g1 - 1);
+                won[x] = (uint32_t)(ga - gf) * gstride + (uint32_t)n_blk * 16u + (uint32_t)(ri & 7) * 16u +
+                         (uint32_t)kc * 128u;
+            }
         }
     };
     u32x4 wr[P][PF];
     auto quad_load = [&](int p, int qd) {
 #pragma unroll
         for (int x = 0; x < P; x++)
-            wr[x][p] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsc, won[x], qd * 512, 0));
+            wr[x][p] = __builtin_bit_cast(
+                u32x4, __builtin_amdgcn_raw_buffer_load_b128(SWI && x ? rsb : rsc, won[x], qd * 512, 0));
     };
     // the unit's row scales for this wave's LDS area: entry e = group
     // e / n_blk, block e % n_blk (NG n_blk <= 128 NG entries, 2 NG per lane),
@@ -151,9 +174,18 @@ __global__ __launch_bounds__(64 * MT_FW) void k_mvt(MtArgs A) {
     auto scales_load = [&]() {
 #pragma unroll
         for (int k = 0; k < 2 * NG; k++) {
-            const int e = min(l + 64 * k, NG * n_blk - 1), gi = min(e / n_blk, ngr - 1);
-            st[k] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                  rsc, (uint32_t)gi * gstride + (uint32_t)(e % n_blk) * 16u, 0, 0));
+            if constexpr (SWI) {
+                // 64 | n_blk: entry l + 64 k lies in group (64 k) / n_blk for
+                // every lane, so each load's descriptor is uniform
+                const int gi = (64 * k) / n_blk, e = (64 * k) % n_blk + l;
+                st[k] = __builtin_bit_cast(
+                    u32x4, __builtin_amdgcn_raw_buffer_load_b128(gi >= 2 ? rsb : rsc,
+                                                                  (uint32_t)(gi & 1) * gstride + (uint32_t)e * 16u, 0, 0));
+            } else {
+                const int e = min(l + 64 * k, NG * n_blk - 1), gi = min(e / n_blk, ngr - 1);
+                st[k] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                      rsc, (uint32_t)gi * gstride + (uint32_t)(e % n_blk) * 16u, 0, 0));
+            }
         }
     };
     auto scales_store = [&]() {
@@ -338,6 +370,36 @@ __global__ __launch_bounds__(64 * MT_FW) void k_mvt(MtArgs A) {
                 quad_step(std::false_type{}, p, q0 + p, sqt + q0 * 4 * NTS * 32, smt + 4 * q0, sxt + 4 * q0,
                           wst + q0 * 64);
         }
+        if constexpr (SWI) {
+            // lane i16 < 8: gate of token tok, rows 16 f + 4 kc + k; lane
+            // i16 + 8 (row_ror 8): up of the same.  The workgroup's 4 units of
+            // a round are the 64 columns of block f / 4 of the down input:
+            // swiglu1 into LDS, then a 16-lane row per token preps the block
+            // as swiglu_prep_lane does.
+            float* yl = (float*)(smem + mt_lds(n_blk, NT, P));  // [NT][68]
+            const int b64 = f >> 2;
+            const uint8_t* sg = A.swsign ? A.swsign + 8 * b64 : nullptr;
+#pragma unroll
+            for (int k = 0; k < NV; k++) {
+                const float up = DPP_F(acc[k], 0x128);
+                const int c = 16 * (f & 3) + 4 * kc + k;
+                const uint32_t neg = sg ? (sg[c >> 3] >> (c & 7)) & 1u : 0u;
+                if (i16 < 8) yl[tok * 68 + c] = swiglu1(acc[k], up, A.swdz, neg);
+            }
+            __syncthreads();
+            if (tid < 16 * NT) {
+                const int t = tid >> 4, r = tid & 15, I = A.swI, nbI = I >> 5;
+                if (t < M) {  // uniform over the 16-lane row
+                    float v4[4];
+#pragma unroll
+                    for (int k = 0; k < 4; k++) v4[k] = yl[t * 68 + 4 * r + k];
+                    row_prep64(v4, r, b64, A.swo.q + (size_t)t * I, A.swo.s + (size_t)t * nbI,
+                               A.swo.m + (size_t)t * nbI, A.swo.h ? A.swo.h + (size_t)t * I : nullptr);
+                }
+            }
+            __syncthreads();
+            continue;
+        }
         // token tok of fragment fx, rows 4 (kc & 1) + rho + k of group
         // gf + 2 fx + kc / 2
         const int grp = J.g0 + NG * f + 2 * fx + (kc >> 1);
@@ -433,6 +495,54 @@ int32_t dpuf_hip_mvt_launch(void* s, int32_t M, int32_t n_jobs, const DpufGemvJo
         wgs += nun[i] > 0 ? (nw < need ? nw : need) : 0;
         A.wb[i + 1] = wgs;
     }
+    hipLaunchKernelGGL(k, dim3(wgs), dim3(64 * MT_FW), lds, ST(s), A);
+    LAUNCHED("k_mvt");
+    return 0;
+}
+
+// gate and up of 2 .. 8 tokens with the SwiGLU + prep of the down input in
+// the same launch: a unit is 16 rows of gate and the same 16 of up, a
+// workgroup round the 4 units of one 64-block of the down input.
+int32_t dpuf_hip_mvt_swiglu(void* s, int32_t M, const DpufGemvJob* jobs, float dz, const uint8_t* sign,
+                            DpufPrep out) {
+    const DpufGemvJob& a = jobs[0];
+    const DpufGemvJob& b = jobs[1];
+    const int K = a.w.cols, I = a.w.rows, n_blk = K >> 5;
+    if (M < 2 || M > 8 || a.w.mode != 12 || b.w.mode != 12 || b.w.cols != K || b.w.rows != I || K <= 0 ||
+        K % 2048 || n_blk > 128 || I <= 0 || I % 64 || a.g0 != 0 || b.g0 != 0 || a.g1 != I / 8 || b.g1 != I / 8 ||
+        !a.p.q || !a.p.s || !a.p.m || a.p.q != b.p.q || a.p.s != b.p.s || a.p.m != b.p.m || !out.q || !out.s ||
+        !out.m || out.q == a.p.q)
+        return -1;
+    // one wave per unit (the pairing's layout): taken where the plain launch
+    // would also run one wave per unit pair, i.e. units > 2 per CU
+    const int nun = I / 16;
+    if (nun <= 2 * dpuf_hip_cu_count()) return -1;
+    MtKernel k = k_mvt<8, 1, 2, true>;
+    const size_t lds = mt_lds(n_blk, 8, 2) + 8 * 68 * sizeof(float);
+    int cap = mt_capacity(k, lds);
+    if (dpuf_hip_mv_max_wg() > 0 && cap > dpuf_hip_mv_max_wg()) cap = dpuf_hip_mv_max_wg();
+    MtArgs A;
+    memset(&A, 0, sizeof A);
+    A.n_jobs = 1;
+    A.K = K;
+    A.M = M;
+    for (int i = 0; i < 2; i++) {
+        A.j[i].g = jobs[i].w.g;
+        A.j[i].g0 = 0;
+        A.j[i].g1 = I / 8;
+        A.j[i].rows = I;
+        A.j[i].q = a.p.q;
+        A.j[i].s = a.p.s;
+        A.j[i].m = a.p.m;
+    }
+    A.swo = out;
+    A.swsign = sign;
+    A.swdz = dz;
+    A.swI = I;
+    const int need = nun / MT_FW;  // every workgroup takes whole rounds of MT_FW units
+    const int wgs = cap < need ? cap : need;
+    A.wb[0] = 0;
+    A.wb[1] = wgs;
     hipLaunchKernelGGL(k, dim3(wgs), dim3(64 * MT_FW), lds, ST(s), A);
     LAUNCHED("k_mvt");
     return 0;

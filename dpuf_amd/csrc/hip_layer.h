@@ -184,6 +184,11 @@ int32_t dpuf_hip_fed_producers(int32_t I, const DpufGemvJob* job);
  * dpuf_hip_gemv + dpuf_hip_swiglu_prep).  out must not be the jobs' input. */
 int32_t dpuf_hip_gemm_swiglu(void* s, int32_t M, const DpufGemvJob* jobs, float dz, const uint8_t* sign,
                              DpufPrep out);
+/* The same for 2 .. 8 tokens on the few-token kernel (gate and up as the
+ * two fragments of its pairs); -1 with nothing launched when the shapes do
+ * not take it. */
+int32_t dpuf_hip_mvt_swiglu(void* s, int32_t M, const DpufGemvJob* jobs, float dz, const uint8_t* sign,
+                            DpufPrep out);
 /* Caps the workgroups of an M == 1 GEMV or K-split GEMM launch (<= 0:
  * device capacity only). */
 void dpuf_hip_set_gemv_max_wg(int32_t n);
