@@ -261,6 +261,11 @@ __global__ __launch_bounds__(64 * MT_FW) void k_mvt(MtArgs A) {
     const float* sxt = sx + tok * nbp;
     for (; f < nun; f += nwg * FPW) {
         if (f != lb * FPW + fs) frag_start(f);
+        // SWI: the down input's sign bits of this lane's 4 columns
+        // 16 (f & 3) + 4 kc + k of block f / 4, loaded ahead of the K walk
+        uint32_t sgn = 0;
+        if constexpr (SWI)
+            if (A.swsign) sgn = (uint32_t)(A.swsign[8 * (f >> 2) + 2 * (f & 3) + (kc >> 1)] >> (4 * (kc & 1))) & 0xFu;
         scales_store();
         // this lane's scales in the wave's copy: group 2 fx + kc / 2
         // (clamped), rows 4 (kc & 1) + rho .. of each block's 8
@@ -378,13 +383,11 @@ __global__ __launch_bounds__(64 * MT_FW) void k_mvt(MtArgs A) {
             // as swiglu_prep_lane does.
             float* yl = (float*)(smem + mt_lds(n_blk, NT, P));  // [NT][68]
             const int b64 = f >> 2;
-            const uint8_t* sg = A.swsign ? A.swsign + 8 * b64 : nullptr;
 #pragma unroll
             for (int k = 0; k < NV; k++) {
                 const float up = DPP_F(acc[k], 0x128);
                 const int c = 16 * (f & 3) + 4 * kc + k;
-                const uint32_t neg = sg ? (sg[c >> 3] >> (c & 7)) & 1u : 0u;
-                if (i16 < 8) yl[tok * 68 + c] = swiglu1(acc[k], up, A.swdz, neg);
+                if (i16 < 8) yl[tok * 68 + c] = swiglu1(acc[k], up, A.swdz, (sgn >> k) & 1u);
             }
             __syncthreads();
             if (tid < 16 * NT) {
