@@ -530,8 +530,10 @@ def test_few_row_steps_8b_width(eng, orc):
     """Steps of 2..16 rows at the Qwen3-8B width (hidden 4096, FFN 12288,
     two layers), whose Q/K/V and gate/up projections take the few-token
     GEMM: prefill chunks of 12 (16 staged tokens) and 5 rows (fragment
-    pairs) with per-layer residuals, then three sessions decoded together
-    for 3 steps; every row bit-identical to the oracle."""
+    pairs) with per-layer residuals, slot prompts of 3, 8, 5 and 2 rows
+    (gate, up and the SwiGLU + down-input prep in one launch at 2..8 rows),
+    then four sessions decoded together for 3 steps; every row
+    bit-identical to the oracle."""
     shape = dict(M.QWEN3_8B, num_layers=2, vocab_size=4096, tie_word_embeddings=1)
     m = M.Model.build(shape, max_seq_len=64, seed=161)
     p = Pair(eng, orc, m)
@@ -549,19 +551,19 @@ def test_few_row_steps_8b_width(eng, orc):
     cg, co = p.captured(5)
     assert bits_equal(cg, co), maxdiff(cg, co)
     p.capture(0)
-    slots = np.array([1, 4, 6], np.int32)
+    slots = np.array([1, 4, 6, 7], np.int32)
     toks, pos = [], []
-    for s, n in zip(slots, (3, 7, 5)):
+    for s, n in zip(slots, (3, 8, 5, 2)):
         p.set_slot(int(s))
         lg, lo = p.forward(rng.integers(0, 4096, n).astype(np.int32), 0)
         assert bits_equal(lg, lo)
         toks.append(int(np.argmax(lo[0])))
         pos.append(n)
     for step in range(3):
-        log(f"8B-width three-session step {step}")
-        lg = np.zeros((3, 4096), np.float32)
-        got = np.full(3, -1, np.int32)
-        rc = eng.dpuf_amd_engine_forward_slots(p.g, 3, M.ptr(slots), M.ptr(np.array(toks, np.int32)),
+        log(f"8B-width four-session step {step}")
+        lg = np.zeros((len(slots), 4096), np.float32)
+        got = np.full(len(slots), -1, np.int32)
+        rc = eng.dpuf_amd_engine_forward_slots(p.g, len(slots), M.ptr(slots), M.ptr(np.array(toks, np.int32)),
                                               M.ptr(np.array(pos, np.int32)), M.ptr(lg), M.ptr(got))
         assert rc == 0, rc
         for i, s in enumerate(slots):
