@@ -578,6 +578,28 @@ def test_few_row_steps_8b_width(eng, orc):
     p.close()
 
 
+def test_few_row_swiglu_capped_workgroups_8b_width(eng, orc):
+    """Gate, up and the SwiGLU + down-input prep in one few-token launch with
+    its workgroups capped at 40 of the 192 it would take, so each walks 4 or
+    5 of the down input's 64-blocks and reuses its LDS tile across rounds:
+    prompts of 8 and 2 rows at the Qwen3-8B width (one layer), every row's
+    logits bit-identical to the oracle."""
+    shape = dict(M.QWEN3_8B, num_layers=1, vocab_size=4096, tie_word_embeddings=1)
+    m = M.Model.build(shape, max_seq_len=32, seed=171)
+    p = Pair(eng, orc, m)
+    rng = np.random.default_rng(172)
+    eng.dpuf_amd_set_gemv_max_workgroups(40)
+    try:
+        for s, n in ((2, 8), (3, 2)):
+            log(f"capped few-token SwiGLU launch: {n}-row prompt in slot {s}")
+            p.set_slot(s)
+            lg, lo = p.forward(rng.integers(0, 4096, n).astype(np.int32), 0, only_last=0)
+            assert bits_equal(lg, lo), (n, maxdiff(lg, lo))
+    finally:
+        eng.dpuf_amd_set_gemv_max_workgroups(0)
+        p.close()
+
+
 def test_multi_session_8b_attention_geometry(eng, orc):
     """dpuf_amd_engine_forward_slots with groups of 4 and head_dim 128 (two
     decode-attention workgroups per KV head, the second of which stores no
